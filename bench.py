@@ -1,0 +1,197 @@
+#!/usr/bin/env python3
+"""Benchmark of the gfx950 quantized matvec path on one MI355X.
+
+Headline workload: Q4_K decode matvec, 14336 rows x 4096 cols (the Llama-3-8B
+FFN gate/up shape), batch 1.  One step = one rlq_matmul: quantize the fp32
+activation to Q8_K on the GPU and run the Q4_K x Q8_K matvec.  Weights are
+N(0, 0.02) fp32 quantized by this library's own Q4_K encoder on the GPU;
+activations are N(0, 1) fp32; both are resident in HBM before timing.
+
+Cache honesty: 33 MB of weights fit in the 256 MB MALL, so the timed loop
+rotates over ROTATE distinct weight copies (>= 330 MB per sweep).
+
+value     = algorithmic bytes per step (W + fp32 x + fp32 y) * steps / time
+roofline  = the matvec step's algorithmic bytes / its mean duration, each
+            step bracketed by HIP events on the stream it runs on
+cpu_baseline = the CPU oracle (a C restatement of the reference's scalar
+            Rust path) on the same weights, 1 thread, repeated for ~10 s.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--extra]
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+INT8_PEAK_TOPS = 5000.0
+ROTATE = 10
+
+
+def load():
+    import importlib
+
+    return importlib.import_module("rust-llama_amd")
+
+
+def gpu_weights(rlq, ctx, dtype, rows, cols, seed, copies):
+    """N(0, 0.02) fp32 generated and quantized on the GPU; returns handles
+    and the host bytes of copy 0."""
+    torch = rlq.torch
+    g = torch.Generator(device="cuda")
+    handles, host0 = [], None
+    for c in range(copies):
+        g.manual_seed(seed + 1000 * c)
+        xw = torch.randn((rows, cols), generator=g, device="cuda", dtype=torch.float32) * 0.02
+        packed = ctx.quantize(dtype, xw)
+        ctx.sync()
+        del xw
+        handles.append(rlq.Weights(ctx, dtype, packed, rows, cols))
+        if c == 0:
+            host0 = packed.cpu().numpy()
+        del packed
+    return handles, host0
+
+
+def algorithmic_bytes(rlq, dtype, rows, cols, batch):
+    return rlq.row_bytes(dtype, cols) * rows + 4 * cols * batch + 4 * rows * batch
+
+
+def time_steps(rlq, ctx, handles, x, y, steps, warmup):
+    """Per-step events (mean step duration) and a back-to-back loop (throughput)."""
+    torch = rlq.torch
+    n = len(handles)
+    for i in range(warmup):
+        ctx.matmul(handles[i % n], x, y)
+    ctx.sync()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    for i in range(steps):
+        ev[i][0].record()
+        ctx.matmul(handles[i % n], x, y)
+        ev[i][1].record()
+    ctx.sync()
+    per_step_ms = float(np.mean([a.elapsed_time(b) for a, b in ev]))
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    for i in range(steps):
+        ctx.matmul(handles[i % n], x, y)
+    end.record()
+    torch.cuda.synchronize()
+    ctx.sync()
+    loop_ms = start.elapsed_time(end) / steps
+    return per_step_ms, loop_ms
+
+
+def cpu_baseline(dtype, w_host, rows, cols, x_host, budget_s=10.0):
+    """Oracle matvec (reference scalar path restated in C), 1 thread."""
+    import oracle
+
+    t0 = time.perf_counter()
+    reps = 0
+    while True:
+        oracle.matvec(int(dtype), w_host, rows, cols, x_host, threads=1)
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s:
+            break
+    per = el / reps
+    gbs = (w_host.size + 4 * cols + 4 * rows) / per / 1e9
+    return {"value": round(gbs, 4), "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"{reps} full {rows}x{cols} matvecs in {el:.1f} s ({per * 1e3:.1f} ms each), "
+                      "oracle/rlq_oracle.c built with gcc -O2 -ffp-contract=off"}
+
+
+def run_config(rlq, ctx, dtype, rows, cols, batch, seed, steps, warmup, copies):
+    torch = rlq.torch
+    handles, host0 = gpu_weights(rlq, ctx, dtype, rows, cols, seed, copies)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed + 7)
+    x = torch.randn((batch, cols), generator=g, device="cuda", dtype=torch.float32)
+    y = torch.empty((batch, rows), device="cuda", dtype=torch.float32)
+    per_step_ms, loop_ms = time_steps(rlq, ctx, handles, x, y, steps, warmup)
+    nbytes = algorithmic_bytes(rlq, dtype, rows, cols, batch)
+    out = {"rows": rows, "cols": cols, "batch": batch, "dtype": int(dtype), "bytes_per_step": nbytes,
+           "ms_per_step": loop_ms, "event_ms_per_step": per_step_ms,
+           "gbs": nbytes / (loop_ms * 1e-3) / 1e9, "event_gbs": nbytes / (per_step_ms * 1e-3) / 1e9,
+           "rotated_copies": copies}
+    return out, handles, host0, x
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--extra", action="store_true", help="also time the other decode configs")
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one MI355X: this build has no multi-GPU path (run with --gpus 1)",
+              file=sys.stderr)
+        sys.exit(2)
+
+    rlq = load()
+    torch = rlq.torch
+    DT = rlq.DType
+    torch.cuda.set_device(0)
+    ctx = rlq.Context(0)
+
+    rows, cols = 14336, 4096
+    head, handles, host0, x = run_config(rlq, ctx, DT.Q4_K, rows, cols, 1, 0x51A7E002, args.steps, args.warmup,
+                                         ROTATE)
+    roof_gbs = head["event_gbs"]
+    result = {
+        "metric": "Q4_K matvec GB/s (14336x4096, B=1)",
+        "value": round(head["gbs"], 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(head["ms_per_step"], 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic: N(0,0.02) fp32 weights quantized to Q4_K on the GPU; N(0,1) fp32 activations",
+        "config": {"workload": "Q4_K x Q8_K decode matvec 14336x4096, batch 1 (quantize + matvec per step)",
+                   "rows": rows, "cols": cols, "batch": 1, "rotated_weight_copies": ROTATE,
+                   "bytes_per_step": head["bytes_per_step"]},
+        "roofline": {"bound": "hbm", "achieved": round(roof_gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(roof_gbs / HBM_PEAK_GBS, 4), "traffic": None},
+    }
+    if not args.no_cpu:
+        xh = x.cpu().numpy().reshape(-1)
+        result["cpu_baseline"] = cpu_baseline(DT.Q4_K, host0, rows, cols, xh)
+    for h in handles:
+        h.close()
+    if args.extra:
+        extra = {}
+        for name, (t, r, c, b, copies) in {
+            "q4k_14336x4096_b4": (DT.Q4_K, 14336, 4096, 4, ROTATE),
+            "q4k_14336x4096_b8": (DT.Q4_K, 14336, 4096, 8, ROTATE),
+            "q6k_128256x4096_b1": (DT.Q6_K, 128256, 4096, 1, 1),
+            "q6k_128256x4096_b8": (DT.Q6_K, 128256, 4096, 8, 1),
+            "q8_0_4864x896_b1": (DT.Q8_0, 4864, 896, 1, 64),
+            "q8_0_151936x896_b1": (DT.Q8_0, 151936, 896, 1, 3),
+        }.items():
+            o, hs, _, _ = run_config(rlq, ctx, t, r, c, b, 0x51A7E000 + len(extra), max(20, args.steps // 2),
+                                     args.warmup, copies)
+            for h in hs:
+                h.close()
+            o["frac_hbm"] = o["event_gbs"] / HBM_PEAK_GBS
+            extra[name] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in o.items()}
+            torch.cuda.empty_cache()
+        result["extra"] = extra
+    ctx.close()
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,173 @@
+/*
+ * rlq.h - C ABI of the gfx950 (MI355X) quantized matrix-product library.
+ *
+ * Drop-in for rust-llama's `llama-quant` scalar matvec path (crate
+ * crates/quant; public surface crates/quant/src/lib.rs:36-41) and its two
+ * callers, model-runtime `Matrix::multiply` (crates/model-runtime/src/math.rs:144-169)
+ * and the GGML MUL_MAT op (crates/tensor/src/cpu_extra.rs:756-873).  Weight
+ * formats Q8_0 (id 8), Q4_K (12) and Q6_K (14); activations are quantized to
+ * Q8_0 / Q8_K (15) on the GPU, exactly as the reference's quantizers.
+ *
+ * Conventions
+ *   - Plain pointers and sizes.  Sizes are u64 (the reference's usize).
+ *   - Every function returns an rlq_status and, when `err` is non-null, fills
+ *     it.  Codes 1..17 are the reference's QuantError variants in declaration
+ *     order (crates/quant/src/lib.rs:45-63) with the same payloads; 18..20 are
+ *     this library's own.
+ *   - Validate before mutate: on any error, no output buffer is written
+ *     (crates/quant/src/matvec.rs:31-56, encode.rs:37-100).
+ *   - Host functions (`rlq_matvec`, `rlq_quantize_into`, ...) take host
+ *     pointers, run on the GPU of the process-wide default context and return
+ *     when the result is in the caller's buffer (the reference is synchronous).
+ *   - Device functions take device pointers and enqueue on `stream` (a
+ *     hipStream_t passed as void*; NULL = the context's own stream).  Shape
+ *     and length errors are returned at once; data errors found on the GPU
+ *     (non-finite input, unrepresentable scale) suppress the outputs of the
+ *     failing call and are reported by the next rlq_sync().
+ *   - A context or weights handle must not be used by two threads at once.
+ *   - Weights and activations are little-endian GGUF bytes, rows of `cols`
+ *     elements, rows contiguous (ne[0] innermost; math.rs:15-16).
+ */
+#ifndef RLQ_H
+#define RLQ_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* GGML numeric type ids on the path (crates/quant/src/lib.rs:132-169).  Any
+ * id of that enum is accepted where a dtype is taken; ids outside the path
+ * return RLQ_UNIMPLEMENTED after the reference's own checks. */
+enum rlq_dtype { RLQ_Q8_0 = 8, RLQ_Q4_K = 12, RLQ_Q6_K = 14, RLQ_Q8_K = 15 };
+
+typedef enum rlq_status {
+    RLQ_OK = 0,
+    RLQ_INVALID_TYPE = 1,               /* dtype = id */
+    RLQ_UNSUPPORTED_MATVEC = 2,         /* dtype */
+    RLQ_INVALID_VECTOR_LENGTH = 3,      /* a = expected, b = actual */
+    RLQ_INVALID_MATRIX_SHAPE = 4,       /* a = rows, b = cols */
+    RLQ_NON_MULTIPLE = 5,               /* a = elements, b = block_size */
+    RLQ_SIZE_OVERFLOW = 6,
+    RLQ_INVALID_LENGTH = 7,             /* a = expected, b = actual */
+    RLQ_ALLOCATION_FAILED = 8,
+    RLQ_UNSUPPORTED_QUANTIZATION = 9,   /* dtype */
+    RLQ_UNSUPPORTED_WEIGHTED_QUANTIZATION = 10,
+    RLQ_IMPORTANCE_WEIGHTS_REQUIRED = 11,
+    RLQ_INVALID_IMPORTANCE_LENGTH = 12,
+    RLQ_INVALID_IMPORTANCE_WEIGHT = 13,
+    RLQ_UNSUPPORTED_INTEGER_CONVERSION = 14,
+    RLQ_INTEGER_OUT_OF_RANGE = 15,
+    RLQ_NON_FINITE_INPUT = 16,          /* a = index (within the column), b = column */
+    RLQ_UNREPRESENTABLE_SCALE = 17,     /* a = block (within the column), b = column */
+    RLQ_DEVICE_ERROR = 18,              /* a = hipError_t */
+    RLQ_UNIMPLEMENTED = 19,             /* dtype: known to the reference, not on this path */
+    RLQ_INVALID_ARGUMENT = 20           /* null pointer or handle */
+} rlq_status;
+
+typedef struct rlq_error {
+    int32_t code;
+    uint32_t dtype;
+    uint64_t a;
+    uint64_t b;
+} rlq_error;
+
+typedef struct rlq_context rlq_context;
+typedef struct rlq_weights rlq_weights;
+
+/* ---- metadata (no GPU work) -------------------------------------------- */
+
+/* Static text for a status code. */
+const char *rlq_status_string(int32_t code);
+
+/* DType::row_bytes (crates/quant/src/lib.rs:274-285). */
+int32_t rlq_row_bytes(uint32_t dtype, uint64_t elements, uint64_t *out, rlq_error *err);
+
+/* matvec_activation_dtype (crates/quant/src/matvec.rs:7-18). */
+int32_t rlq_matvec_activation_dtype(uint32_t weights_type, uint32_t *out, rlq_error *err);
+
+/* ---- host drop-ins (synchronous, default context) ------------------------ */
+
+/* quantize_into (crates/quant/src/encode.rs:37-100): Q8_0 / Q8_K activation
+ * quantizers and the Q4_K / Q6_K / Q8_0 weight encoders
+ * (crates/quant/src/encode_k.rs:11-33, 430-561), run on the GPU. */
+int32_t rlq_quantize_into(uint32_t dtype, const float *values, uint64_t n, uint8_t *out, uint64_t out_len,
+                          rlq_error *err);
+
+/* dequantize_into (crates/quant/src/lib.rs:299-308; decode.rs). */
+int32_t rlq_dequantize_into(uint32_t dtype, const uint8_t *bytes, uint64_t len, float *out, uint64_t n,
+                            rlq_error *err);
+
+/* dot_packed (crates/quant/src/matvec.rs:90-103). */
+int32_t rlq_dot_packed(uint32_t weights_type, const uint8_t *weights, uint64_t weights_len,
+                       const uint8_t *activation, uint64_t activation_len, uint64_t elements, float *out,
+                       rlq_error *err);
+
+/* matvec (crates/quant/src/matvec.rs:24-87): y[rows] = W[rows x cols] . x[cols].
+ * Uploads the weights on every call; use rlq_weights_create + rlq_matmul to
+ * keep them resident. */
+int32_t rlq_matvec(uint32_t weights_type, const uint8_t *weights, uint64_t weights_len, uint64_t rows,
+                   uint64_t cols, const float *input, uint64_t input_len, float *output, rlq_error *err);
+
+/* ---- device API -------------------------------------------------------- */
+
+/* One context per device; it owns a stream, scratch memory and the device
+ * error word.  device = -1 takes the current HIP device. */
+int32_t rlq_context_create(int32_t device, rlq_context **out, rlq_error *err);
+void rlq_context_destroy(rlq_context *ctx);
+/* The hipStream_t the context uses when a call passes stream = NULL. */
+void *rlq_context_stream(rlq_context *ctx);
+
+/* Matrix::from_quantized (crates/model-runtime/src/math.rs:35-70): checks the
+ * dtype capability, shape and byte length, then keeps a device copy of the
+ * weights in the kernels' layout (Q4_K as stored; Q6_K and Q8_0 split into
+ * 16-byte-aligned planes).  `bytes_on_device` != 0 when `bytes` is a device
+ * pointer.  Returns after the copy is complete. */
+int32_t rlq_weights_create(rlq_context *ctx, uint32_t dtype, const void *bytes, uint64_t len, uint64_t rows,
+                           uint64_t cols, int32_t bytes_on_device, rlq_weights **out, rlq_error *err);
+void rlq_weights_destroy(rlq_weights *w);
+/* rows, cols, dtype of a weights handle (any output pointer may be null). */
+void rlq_weights_shape(const rlq_weights *w, uint64_t *rows, uint64_t *cols, uint32_t *dtype);
+
+/* MUL_MAT (crates/tensor/src/cpu_extra.rs:756-873) with an F32 right-hand
+ * side, and Matrix::multiply for batch = 1: each of the `batch` input rows
+ * x[b*cols ..] is quantized to the weights' activation type on the GPU, then
+ * y[b*rows + r] = dot_packed(weights row r, activation b).  x and y are
+ * device pointers. */
+int32_t rlq_matmul(rlq_context *ctx, const rlq_weights *w, const float *x, uint64_t batch, float *y,
+                   void *stream, rlq_error *err);
+
+/* rlq_matmul followed by the greedy sampler's choice per column
+ * (crates/llama-behavior/src/sampling.rs:607-613: the first strict maximum),
+ * fused into the matvec epilogue: argmax[b] = index of the largest y[b*rows+r]. */
+int32_t rlq_matmul_argmax(rlq_context *ctx, const rlq_weights *w, const float *x, uint64_t batch, float *y,
+                          uint32_t *argmax, void *stream, rlq_error *err);
+
+/* Device quantize_into (crates/quant/src/encode.rs:37-100): the activation
+ * quantizers (Q8_0, Q8_K) and the weight encoders (Q8_0, Q4_K, Q6_K), GGUF
+ * bytes of `batch` rows of `cols` values each.  x and out are device
+ * pointers.  For the K encoders a NonFiniteInput index counts over all
+ * batch*cols values and UnrepresentableScale over all blocks (b = 0). */
+int32_t rlq_quantize_device(rlq_context *ctx, uint32_t dtype, const float *x, uint64_t cols, uint64_t batch,
+                            uint8_t *out, void *stream, rlq_error *err);
+
+/* Wait for `stream` (NULL = the context's), then report and clear the first
+ * data error the GPU recorded since the previous rlq_sync. */
+int32_t rlq_sync(rlq_context *ctx, void *stream, rlq_error *err);
+
+/* Exact integer part of every (row, block) dot of the weights against one
+ * activation row x (device f32, cols values), quantized on the GPU as
+ * rlq_matmul does: isum[r*nb + k] and imin[r*nb + k] for block k, as the
+ * integers of crates/quant/src/matvec_extra.rs:252-283 (the eight lanes
+ * added; imin is the Q4_K mins sum, 0 otherwise) and matvec.rs:124-127.
+ * isum and imin are device pointers of rows*nb i32. */
+int32_t rlq_block_sums(rlq_context *ctx, const rlq_weights *w, const float *x, int32_t *isum, int32_t *imin,
+                       void *stream, rlq_error *err);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* RLQ_H */

@@ -1,0 +1,176 @@
+"""ctypes binding of the CPU oracle (librlq_oracle.so).
+
+TEST INFRASTRUCTURE ONLY: the checker for the HIP path.  Only the tests, the
+smoke check and the CPU-baseline leg of bench.py import this module; the
+product package never does.
+
+The library restates rust-llama's scalar `llama-quant` path in C
+(crates/quant/src/{lib,matvec,matvec_extra,activation,encode,encode_k,decode}.rs);
+see rlq_oracle.h for the per-function citations.  `make -C oracle` builds it.
+"""
+import ctypes
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "librlq_oracle.so")
+
+Q8_0, Q4_K, Q6_K, Q8_K = 8, 12, 14, 15
+BLOCK = {Q8_0: 32, Q4_K: 256, Q6_K: 256, Q8_K: 256}
+TYPE_SIZE = {Q8_0: 34, Q4_K: 144, Q6_K: 210, Q8_K: 292}
+
+# Status codes in the order of the reference's QuantError (lib.rs:45-63).
+ERROR_NAMES = {
+    0: "Ok", 1: "InvalidType", 2: "UnsupportedMatVec", 3: "InvalidVectorLength",
+    4: "InvalidMatrixShape", 5: "NonMultiple", 6: "SizeOverflow", 7: "InvalidLength",
+    8: "AllocationFailed", 9: "UnsupportedQuantization", 10: "UnsupportedWeightedQuantization",
+    11: "ImportanceWeightsRequired", 12: "InvalidImportanceLength", 13: "InvalidImportanceWeight",
+    14: "UnsupportedIntegerConversion", 15: "IntegerOutOfRange", 16: "NonFiniteInput",
+    17: "UnrepresentableScale", 18: "DeviceError", 19: "Unimplemented", 20: "InvalidArgument",
+}
+
+
+class OracleError(Exception):
+    def __init__(self, code, dtype, a, b):
+        self.code, self.dtype, self.a, self.b = code, dtype, a, b
+        super().__init__(f"{ERROR_NAMES.get(code, code)}(dtype={dtype}, a={a}, b={b})")
+
+    @property
+    def name(self):
+        return ERROR_NAMES.get(self.code, str(self.code))
+
+
+class _Err(ctypes.Structure):
+    _fields_ = [("code", ctypes.c_int32), ("dtype", ctypes.c_uint32),
+                ("a", ctypes.c_uint64), ("b", ctypes.c_uint64)]
+
+
+def _load():
+    if not os.path.exists(LIB_PATH):
+        raise RuntimeError(f"{LIB_PATH} is not built: run `make -C oracle`")
+    lib = ctypes.CDLL(LIB_PATH)
+    P, U64, U32, I = ctypes.c_void_p, ctypes.c_uint64, ctypes.c_uint32, ctypes.c_int
+    E = ctypes.POINTER(_Err)
+    lib.oracle_f16_to_f32.argtypes, lib.oracle_f16_to_f32.restype = [ctypes.c_uint16], ctypes.c_float
+    lib.oracle_f32_to_f16.argtypes, lib.oracle_f32_to_f16.restype = [ctypes.c_float], ctypes.c_uint16
+    lib.oracle_row_bytes.argtypes = [U32, U64, ctypes.POINTER(U64), E]
+    lib.oracle_matvec_activation_dtype.argtypes = [U32, ctypes.POINTER(U32), E]
+    lib.oracle_quantize_into.argtypes = [U32, P, U64, P, U64, E]
+    lib.oracle_dequantize_into.argtypes = [U32, P, U64, P, U64, E]
+    lib.oracle_dot_packed.argtypes = [U32, P, U64, P, U64, U64, ctypes.POINTER(ctypes.c_float), E]
+    lib.oracle_matvec.argtypes = [U32, P, U64, U64, U64, P, U64, P, I, E]
+    lib.oracle_matmul.argtypes = [U32, P, U64, U64, U64, P, U64, P, I, E]
+    lib.oracle_block_sums.argtypes = [U32, P, P, U64, P, P]
+    lib.oracle_block_sums.restype = None
+    lib.oracle_argmax.argtypes, lib.oracle_argmax.restype = [P, U64], U64
+    for f in ("oracle_row_bytes", "oracle_matvec_activation_dtype", "oracle_quantize_into",
+              "oracle_dequantize_into", "oracle_dot_packed", "oracle_matvec", "oracle_matmul"):
+        getattr(lib, f).restype = ctypes.c_int
+    return lib
+
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        _lib = _load()
+    return _lib
+
+
+def _ptr(a):
+    return a.ctypes.data_as(ctypes.c_void_p) if a is not None and a.size else None
+
+
+def _check(rc, err):
+    if rc != 0:
+        raise OracleError(err.code, err.dtype, err.a, err.b)
+
+
+def f16_to_f32(bits):
+    return lib().oracle_f16_to_f32(int(bits))
+
+
+def f32_to_f16(value):
+    return lib().oracle_f32_to_f16(float(value))
+
+
+def row_bytes(dtype, elements):
+    out, err = ctypes.c_uint64(), _Err()
+    _check(lib().oracle_row_bytes(dtype, elements, ctypes.byref(out), ctypes.byref(err)), err)
+    return out.value
+
+
+def matvec_activation_dtype(dtype):
+    out, err = ctypes.c_uint32(), _Err()
+    _check(lib().oracle_matvec_activation_dtype(dtype, ctypes.byref(out), ctypes.byref(err)), err)
+    return out.value
+
+
+def quantize_into(dtype, x, out):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    err = _Err()
+    _check(lib().oracle_quantize_into(dtype, _ptr(x), x.size, _ptr(out), out.size, ctypes.byref(err)), err)
+    return out
+
+
+def quantize(dtype, x):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.zeros(row_bytes(dtype, x.size), dtype=np.uint8)
+    return quantize_into(dtype, x, out)
+
+
+def dequantize(dtype, b, n):
+    b = np.ascontiguousarray(b, dtype=np.uint8)
+    out = np.zeros(n, dtype=np.float32)
+    err = _Err()
+    _check(lib().oracle_dequantize_into(dtype, _ptr(b), b.size, _ptr(out), n, ctypes.byref(err)), err)
+    return out
+
+
+def dot_packed(dtype, w, act, elements):
+    w = np.ascontiguousarray(w, dtype=np.uint8)
+    act = np.ascontiguousarray(act, dtype=np.uint8)
+    out, err = ctypes.c_float(), _Err()
+    _check(lib().oracle_dot_packed(dtype, _ptr(w), w.size, _ptr(act), act.size, elements,
+                                   ctypes.byref(out), ctypes.byref(err)), err)
+    return np.float32(out.value)
+
+
+def matvec(dtype, w, rows, cols, x, threads=1):
+    w = np.ascontiguousarray(w, dtype=np.uint8)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.zeros(rows, dtype=np.float32) if rows < (1 << 40) else None
+    err = _Err()
+    rc = lib().oracle_matvec(dtype, _ptr(w), w.size, rows, cols, _ptr(x), x.size,
+                             _ptr(y) if y is not None else ctypes.c_void_p(1), threads,
+                             ctypes.byref(err))
+    _check(rc, err)
+    return y
+
+
+def matmul(dtype, w, rows, cols, x, threads=1):
+    """x is [batch, cols] f32; returns [batch, rows] f32 (GGML MUL_MAT order)."""
+    w = np.ascontiguousarray(w, dtype=np.uint8)
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1, cols)
+    y = np.zeros((x.shape[0], rows), dtype=np.float32)
+    err = _Err()
+    _check(lib().oracle_matmul(dtype, _ptr(w), w.size, rows, cols, _ptr(x), x.shape[0], _ptr(y),
+                               threads, ctypes.byref(err)), err)
+    return y
+
+
+def block_sums(dtype, w_row, act_row, nblocks):
+    w_row = np.ascontiguousarray(w_row, dtype=np.uint8)
+    act_row = np.ascontiguousarray(act_row, dtype=np.uint8)
+    isum = np.zeros(nblocks, dtype=np.int32)
+    imin = np.zeros(nblocks, dtype=np.int32)
+    lib().oracle_block_sums(dtype, _ptr(w_row), _ptr(act_row), nblocks, _ptr(isum), _ptr(imin))
+    return isum, imin
+
+
+def argmax(x):
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    return int(lib().oracle_argmax(_ptr(x), x.size))

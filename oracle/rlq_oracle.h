@@ -1,0 +1,116 @@
+/*
+ * rlq_oracle.h - CPU restatement of rust-llama's scalar quantized-matvec path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This library is the checker for the HIP
+ * implementation: only the tests, the smoke check and the CPU-baseline leg of
+ * the benchmark load it.  The product library never links or calls it.
+ *
+ * It restates, in plain C with the reference's arithmetic order, the Rust
+ * crate `llama-quant` (crates/quant/src) for the dtypes on the path:
+ *   Q8_0 (id 8) and Q4_K (12) / Q6_K (14) weights, Q8_0 and Q8_K (15)
+ *   activations.  Each function cites the reference lines it follows.
+ * Build with `make -C oracle` (gcc -O2 -ffp-contract=off -fno-fast-math), so
+ * that no multiply-add is fused and every f32 operation rounds as Rust's does.
+ *
+ * Status codes follow the order of the reference's `QuantError` enum
+ * (crates/quant/src/lib.rs:45-63); 18..20 are this build's additions.
+ */
+#ifndef RLQ_ORACLE_H
+#define RLQ_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+    ORC_OK = 0,
+    ORC_INVALID_TYPE = 1,                 /* dtype = id */
+    ORC_UNSUPPORTED_MATVEC = 2,           /* dtype */
+    ORC_INVALID_VECTOR_LENGTH = 3,        /* a = expected, b = actual */
+    ORC_INVALID_MATRIX_SHAPE = 4,         /* a = rows, b = cols */
+    ORC_NON_MULTIPLE = 5,                 /* a = elements, b = block_size */
+    ORC_SIZE_OVERFLOW = 6,
+    ORC_INVALID_LENGTH = 7,               /* a = expected, b = actual */
+    ORC_ALLOCATION_FAILED = 8,
+    ORC_UNSUPPORTED_QUANTIZATION = 9,     /* dtype */
+    ORC_UNSUPPORTED_WEIGHTED_QUANTIZATION = 10,
+    ORC_IMPORTANCE_WEIGHTS_REQUIRED = 11,
+    ORC_INVALID_IMPORTANCE_LENGTH = 12,
+    ORC_INVALID_IMPORTANCE_WEIGHT = 13,
+    ORC_UNSUPPORTED_INTEGER_CONVERSION = 14,
+    ORC_INTEGER_OUT_OF_RANGE = 15,
+    ORC_NON_FINITE_INPUT = 16,            /* a = index */
+    ORC_UNREPRESENTABLE_SCALE = 17,       /* a = block */
+    ORC_DEVICE_ERROR = 18,                /* not produced by the oracle */
+    ORC_UNIMPLEMENTED = 19,               /* dtype exists upstream, not restated here */
+    ORC_INVALID_ARGUMENT = 20             /* null pointer */
+};
+
+typedef struct oracle_error {
+    int32_t code;
+    uint32_t dtype;
+    uint64_t a;
+    uint64_t b;
+} oracle_error;
+
+/* lib.rs:323-337 and lib.rs:340-373 */
+float oracle_f16_to_f32(uint16_t bits);
+uint16_t oracle_f32_to_f16(float value);
+
+/* lib.rs:210-285: 0 if id is not a known dtype */
+int oracle_dtype_known(uint32_t id);
+uint64_t oracle_block_size(uint32_t dtype);
+uint64_t oracle_type_size(uint32_t dtype);
+int oracle_row_bytes(uint32_t dtype, uint64_t elements, uint64_t *out, oracle_error *err);
+
+/* matvec.rs:7-18 */
+int oracle_matvec_activation_dtype(uint32_t wtype, uint32_t *out, oracle_error *err);
+
+/* encode.rs:37-100 (Q8_0, Q8_K) and encode_k.rs:11-33 (Q4_K, Q6_K).
+ * Validation precedes any write to `out`. */
+int oracle_quantize_into(uint32_t dtype, const float *x, uint64_t n, uint8_t *out,
+                         uint64_t out_len, oracle_error *err);
+
+/* lib.rs:299-308 with decode.rs:17-23, 42-43, 44-49, 216-258 */
+int oracle_dequantize_into(uint32_t dtype, const uint8_t *bytes, uint64_t len, float *out,
+                           uint64_t n, oracle_error *err);
+
+/* matvec.rs:90-103 */
+int oracle_dot_packed(uint32_t wtype, const uint8_t *w, uint64_t w_len, const uint8_t *act,
+                      uint64_t act_len, uint64_t elements, float *out, oracle_error *err);
+
+/* matvec.rs:24-87.  `threads` > 1 splits rows over pthreads; each row's dot is
+ * the same scalar loop, so the output is identical for every thread count.
+ * `y` (rows floats) is written only on success. */
+int oracle_matvec(uint32_t wtype, const uint8_t *w, uint64_t w_len, uint64_t rows,
+                  uint64_t cols, const float *x, uint64_t x_len, float *y, int threads,
+                  oracle_error *err);
+
+/* crates/tensor/src/cpu_extra.rs:756-873 (MUL_MAT, 2-D case): each of the
+ * `batch` input rows x[b*cols ..] is quantized separately (:820), then
+ * y[b*rows + r] = dot_packed(row r, activation b) (:860). */
+int oracle_matmul(uint32_t wtype, const uint8_t *w, uint64_t w_len, uint64_t rows,
+                  uint64_t cols, const float *x, uint64_t batch, float *y, int threads,
+                  oracle_error *err);
+
+/* Exact per-block integer sums of one packed row against one packed
+ * activation row (no validation; nblocks blocks of the weight type):
+ *   Q4_K: isum = sum_j sc(j)*q(j)*q8(j) (the 8 lanes of matvec_extra.rs:256-266
+ *         added together), imin = sum_s (bsum[2s]+bsum[2s+1])*min_s (:258)
+ *   Q6_K: isum = sum_j sc(j/16)*(q6(j)-32)*q8(j) (:272-281), imin = 0
+ *   Q8_0: isum = sum_j xq(j)*yq(j) per 32-block (matvec.rs:124-127), imin = 0 */
+void oracle_block_sums(uint32_t wtype, const uint8_t *w_row, const uint8_t *act_row,
+                       uint64_t nblocks, int32_t *isum, int32_t *imin);
+
+/* Greedy sampler, crates/llama-behavior/src/sampling.rs:607-613: index of the
+ * first strict maximum (n >= 1). */
+uint64_t oracle_argmax(const float *x, uint64_t n);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

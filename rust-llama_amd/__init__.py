@@ -1,0 +1,355 @@
+"""rust-llama_amd: MI355X (gfx950) drop-in for rust-llama's quantized matvec path.
+
+Python mirror of the reference crate `llama-quant` (crates/quant/src/lib.rs:36-41)
+over the C ABI in include/rlq.h (librlq.so).  Names, argument meaning and error
+behaviour follow the Rust API:
+
+    matvec(DType, weights, rows, cols, input) -> f32[rows]      matvec.rs:24-87
+    dot_packed(DType, weights, activation, elements) -> f32     matvec.rs:90-103
+    matvec_activation_dtype(DType) -> DType                      matvec.rs:7-18
+    quantize(DType, values) / quantize_into(DType, values, out)  encode.rs:10-100
+    dequantize(DType, bytes, elements) / dequantize_into         lib.rs:288-308
+    DType, QuantError                                            lib.rs:45-169
+
+Errors raise QuantError with the reference variant's name and payload.
+Every computation runs on the GPU through librlq.so; there is no CPU path, and
+importing this package fails if the library has not been built
+(`python rust-llama_amd/build.py`).
+
+The device API (Context, Weights) keeps weights resident in HBM and takes
+torch tensors on the GPU; torch supplies device memory and streams only.
+"""
+import ctypes
+import enum
+import os
+
+import numpy as np
+
+try:  # load torch's HIP runtime first so librlq.so binds to the same one
+    import torch
+except ImportError:  # pragma: no cover - the host API still works without torch
+    torch = None
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "librlq.so")
+
+
+class DType(enum.IntEnum):
+    """GGML numeric type ids (crates/quant/src/lib.rs:132-169)."""
+    F32 = 0
+    F16 = 1
+    Q4_0 = 2
+    Q4_1 = 3
+    Q5_0 = 6
+    Q5_1 = 7
+    Q8_0 = 8
+    Q8_1 = 9
+    Q2_K = 10
+    Q3_K = 11
+    Q4_K = 12
+    Q5_K = 13
+    Q6_K = 14
+    Q8_K = 15
+    IQ2_XXS = 16
+    IQ2_XS = 17
+    IQ3_XXS = 18
+    IQ1_S = 19
+    IQ4_NL = 20
+    IQ3_S = 21
+    IQ2_S = 22
+    IQ4_XS = 23
+    I8 = 24
+    I16 = 25
+    I32 = 26
+    I64 = 27
+    F64 = 28
+    IQ1_M = 29
+    BF16 = 30
+    TQ1_0 = 34
+    TQ2_0 = 35
+    MXFP4 = 39
+    NVFP4 = 40
+    Q1_0 = 41
+    Q2_0 = 42
+    F8_E4M3 = 43
+
+
+# Status codes: QuantError variants in declaration order (lib.rs:45-63), then
+# this library's own.
+ERROR_NAMES = {
+    1: "InvalidType", 2: "UnsupportedMatVec", 3: "InvalidVectorLength", 4: "InvalidMatrixShape",
+    5: "NonMultiple", 6: "SizeOverflow", 7: "InvalidLength", 8: "AllocationFailed",
+    9: "UnsupportedQuantization", 10: "UnsupportedWeightedQuantization",
+    11: "ImportanceWeightsRequired", 12: "InvalidImportanceLength", 13: "InvalidImportanceWeight",
+    14: "UnsupportedIntegerConversion", 15: "IntegerOutOfRange", 16: "NonFiniteInput",
+    17: "UnrepresentableScale", 18: "DeviceError", 19: "Unimplemented", 20: "InvalidArgument",
+}
+
+
+class QuantError(Exception):
+    """A QuantError variant: `name`, numeric `code`, `dtype` and the payload
+    fields of the variant (index, block, expected/actual, rows/cols...)."""
+
+    def __init__(self, code, dtype, a, b, message):
+        self.code, self.dtype, self.a, self.b = code, dtype, a, b
+        self.name = ERROR_NAMES.get(code, str(code))
+        super().__init__(f"{self.name}: {message} (dtype={dtype}, a={a}, b={b})")
+
+    @property
+    def index(self):  # NonFiniteInput{index}
+        return self.a
+
+    @property
+    def block(self):  # UnrepresentableScale{block}
+        return self.a
+
+    @property
+    def expected(self):  # InvalidVectorLength / InvalidLength
+        return self.a
+
+    @property
+    def actual(self):
+        return self.b
+
+
+class _Err(ctypes.Structure):
+    _fields_ = [("code", ctypes.c_int32), ("dtype", ctypes.c_uint32), ("a", ctypes.c_uint64),
+                ("b", ctypes.c_uint64)]
+
+
+# Every entry point of include/rlq.h with its ctypes signature.
+_P, _U64, _U32, _I32 = ctypes.c_void_p, ctypes.c_uint64, ctypes.c_uint32, ctypes.c_int32
+_E = ctypes.POINTER(_Err)
+SIGNATURES = {
+    "rlq_status_string": ([_I32], ctypes.c_char_p),
+    "rlq_row_bytes": ([_U32, _U64, ctypes.POINTER(_U64), _E], _I32),
+    "rlq_matvec_activation_dtype": ([_U32, ctypes.POINTER(_U32), _E], _I32),
+    "rlq_quantize_into": ([_U32, _P, _U64, _P, _U64, _E], _I32),
+    "rlq_dequantize_into": ([_U32, _P, _U64, _P, _U64, _E], _I32),
+    "rlq_dot_packed": ([_U32, _P, _U64, _P, _U64, _U64, ctypes.POINTER(ctypes.c_float), _E], _I32),
+    "rlq_matvec": ([_U32, _P, _U64, _U64, _U64, _P, _U64, _P, _E], _I32),
+    "rlq_context_create": ([_I32, ctypes.POINTER(_P), _E], _I32),
+    "rlq_context_destroy": ([_P], None),
+    "rlq_context_stream": ([_P], _P),
+    "rlq_weights_create": ([_P, _U32, _P, _U64, _U64, _U64, _I32, ctypes.POINTER(_P), _E], _I32),
+    "rlq_weights_destroy": ([_P], None),
+    "rlq_weights_shape": ([_P, ctypes.POINTER(_U64), ctypes.POINTER(_U64), ctypes.POINTER(_U32)], None),
+    "rlq_matmul": ([_P, _P, _P, _U64, _P, _P, _E], _I32),
+    "rlq_matmul_argmax": ([_P, _P, _P, _U64, _P, _P, _P, _E], _I32),
+    "rlq_quantize_device": ([_P, _U32, _P, _U64, _U64, _P, _P, _E], _I32),
+    "rlq_sync": ([_P, _P, _E], _I32),
+    "rlq_block_sums": ([_P, _P, _P, _P, _P, _P, _E], _I32),
+}
+
+
+def _load():
+    if not os.path.exists(LIB_PATH):
+        raise ImportError(f"{LIB_PATH} is missing: build it with `python rust-llama_amd/build.py`")
+    lib = ctypes.CDLL(LIB_PATH)
+    for name, (args, res) in SIGNATURES.items():
+        f = getattr(lib, name)
+        f.argtypes, f.restype = args, res
+    return lib
+
+
+_lib = _load()
+
+
+def lib():
+    return _lib
+
+
+def _check(rc, err):
+    if rc != 0:
+        msg = _lib.rlq_status_string(err.code).decode()
+        raise QuantError(err.code, err.dtype, err.a, err.b, msg)
+
+
+def _u8(a):
+    a = np.ascontiguousarray(a)
+    if a.dtype != np.uint8:
+        a = a.view(np.uint8).reshape(-1) if a.dtype.itemsize == 1 else np.frombuffer(a.tobytes(), np.uint8)
+    return a.reshape(-1)
+
+
+def _f32(a):
+    return np.ascontiguousarray(a, dtype=np.float32).reshape(-1)
+
+
+def _ptr(a):
+    return a.ctypes.data_as(ctypes.c_void_p) if a.size else None
+
+
+# ---- metadata --------------------------------------------------------------
+
+def row_bytes(dtype, elements):
+    """DType::row_bytes (lib.rs:274-285)."""
+    out, err = ctypes.c_uint64(), _Err()
+    _check(_lib.rlq_row_bytes(int(dtype), int(elements), ctypes.byref(out), ctypes.byref(err)), err)
+    return out.value
+
+
+def matvec_activation_dtype(weights_type):
+    out, err = ctypes.c_uint32(), _Err()
+    _check(_lib.rlq_matvec_activation_dtype(int(weights_type), ctypes.byref(out), ctypes.byref(err)), err)
+    return DType(out.value)
+
+
+# ---- host drop-ins (synchronous) -----------------------------------------------
+
+def quantize_into(dtype, values, out):
+    values = _f32(values)
+    if not (isinstance(out, np.ndarray) and out.dtype == np.uint8 and out.flags.c_contiguous):
+        raise TypeError("out must be a contiguous uint8 numpy array")
+    err = _Err()
+    _check(_lib.rlq_quantize_into(int(dtype), _ptr(values), values.size, _ptr(out), out.size,
+                                  ctypes.byref(err)), err)
+    return out
+
+
+def quantize(dtype, values):
+    values = _f32(values)
+    out = np.zeros(row_bytes(dtype, values.size), dtype=np.uint8)
+    return quantize_into(dtype, values, out)
+
+
+def dequantize_into(dtype, data, out):
+    data = _u8(data)
+    if not (isinstance(out, np.ndarray) and out.dtype == np.float32 and out.flags.c_contiguous):
+        raise TypeError("out must be a contiguous float32 numpy array")
+    err = _Err()
+    _check(_lib.rlq_dequantize_into(int(dtype), _ptr(data), data.size, _ptr(out), out.size,
+                                    ctypes.byref(err)), err)
+    return out
+
+
+def dequantize(dtype, data, elements):
+    return dequantize_into(dtype, data, np.zeros(int(elements), dtype=np.float32))
+
+
+def dot_packed(weights_type, weights, activation, elements):
+    weights, activation = _u8(weights), _u8(activation)
+    out, err = ctypes.c_float(), _Err()
+    _check(_lib.rlq_dot_packed(int(weights_type), _ptr(weights), weights.size, _ptr(activation),
+                               activation.size, int(elements), ctypes.byref(out), ctypes.byref(err)), err)
+    return np.float32(out.value)
+
+
+def matvec(weights_type, weights, rows, cols, input):
+    weights, input = _u8(weights), _f32(input)
+    out = np.zeros(int(rows) if int(rows) < (1 << 34) else 0, dtype=np.float32)
+    err = _Err()
+    outp = _ptr(out) if out.size else ctypes.c_void_p(16)  # never written unless shapes validate
+    _check(_lib.rlq_matvec(int(weights_type), _ptr(weights), weights.size, int(rows), int(cols),
+                           _ptr(input), input.size, outp, ctypes.byref(err)), err)
+    return out
+
+
+# ---- device API -------------------------------------------------------------
+
+def _dev_ptr(t, dtype):
+    if torch is None or not isinstance(t, torch.Tensor) or not t.is_cuda:
+        raise TypeError("expected a torch tensor on the GPU")
+    if t.dtype != dtype or not t.is_contiguous():
+        raise TypeError(f"expected a contiguous {dtype} tensor")
+    return ctypes.c_void_p(t.data_ptr())
+
+
+def _stream_ptr(stream):
+    if stream is None:
+        return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    return ctypes.c_void_p(stream if isinstance(stream, int) else stream.cuda_stream)
+
+
+class Context:
+    """rlq_context: device scratch, the context's own stream and the device
+    error word.  Kernels run on torch's current stream unless one is given."""
+
+    def __init__(self, device=-1):
+        if device >= 0 and torch is not None:
+            torch.cuda.set_device(device)
+        h, err = ctypes.c_void_p(), _Err()
+        _check(_lib.rlq_context_create(int(device), ctypes.byref(h), ctypes.byref(err)), err)
+        self._h = h
+
+    def close(self):
+        if getattr(self, "_h", None):
+            _lib.rlq_context_destroy(self._h)
+            self._h = None
+
+    __del__ = close
+
+    def matmul(self, w, x, y=None, stream=None):
+        """MUL_MAT / Matrix::multiply: x [batch, cols] f32 -> y [batch, rows] f32."""
+        x2 = x.reshape(-1, w.cols)
+        if y is None:
+            y = torch.empty((x2.shape[0], w.rows), dtype=torch.float32, device=x.device)
+        err = _Err()
+        _check(_lib.rlq_matmul(self._h, w._h, _dev_ptr(x2, torch.float32), x2.shape[0],
+                               _dev_ptr(y, torch.float32), _stream_ptr(stream), ctypes.byref(err)), err)
+        return y
+
+    def matmul_argmax(self, w, x, y=None, argmax=None, stream=None):
+        """matmul followed by the greedy sampler's index per column."""
+        x2 = x.reshape(-1, w.cols)
+        batch = x2.shape[0]
+        if y is None:
+            y = torch.empty((batch, w.rows), dtype=torch.float32, device=x.device)
+        if argmax is None:
+            argmax = torch.empty(batch, dtype=torch.int32, device=x.device)
+        err = _Err()
+        _check(_lib.rlq_matmul_argmax(self._h, w._h, _dev_ptr(x2, torch.float32), batch,
+                                      _dev_ptr(y, torch.float32), _dev_ptr(argmax, torch.int32),
+                                      _stream_ptr(stream), ctypes.byref(err)), err)
+        return y, argmax
+
+    def quantize(self, dtype, x, stream=None):
+        """GPU quantize_into for Q8_0 / Q8_K: x [batch, cols] -> GGUF bytes."""
+        x2 = x.reshape(x.shape[0] if x.dim() > 1 else 1, -1)
+        cols = x2.shape[1]
+        out = torch.empty(x2.shape[0] * row_bytes(dtype, cols), dtype=torch.uint8, device=x.device)
+        err = _Err()
+        _check(_lib.rlq_quantize_device(self._h, int(dtype), _dev_ptr(x2, torch.float32), cols, x2.shape[0],
+                                        _dev_ptr(out, torch.uint8), _stream_ptr(stream), ctypes.byref(err)), err)
+        return out
+
+    def sync(self, stream=None):
+        """Wait for the stream; raise the first data error recorded on the GPU."""
+        err = _Err()
+        _check(_lib.rlq_sync(self._h, _stream_ptr(stream), ctypes.byref(err)), err)
+
+    def block_sums(self, w, x, stream=None):
+        """Exact per-(row, block) integer sums of w against x (one column)."""
+        nb = w.cols // (32 if w.dtype == DType.Q8_0 else 256)
+        isum = torch.empty((w.rows, nb), dtype=torch.int32, device=x.device)
+        imin = torch.empty((w.rows, nb), dtype=torch.int32, device=x.device)
+        err = _Err()
+        _check(_lib.rlq_block_sums(self._h, w._h, _dev_ptr(x.reshape(-1), torch.float32),
+                                   _dev_ptr(isum, torch.int32), _dev_ptr(imin, torch.int32),
+                                   _stream_ptr(stream), ctypes.byref(err)), err)
+        return isum, imin
+
+
+class Weights:
+    """rlq_weights (Matrix::from_quantized, math.rs:35-70): GGUF bytes kept in
+    HBM in the kernels' layout.  `data` is a numpy uint8 array (host) or a
+    torch uint8 tensor on the GPU."""
+
+    def __init__(self, ctx, dtype, data, rows, cols):
+        err, h = _Err(), ctypes.c_void_p()
+        if torch is not None and isinstance(data, torch.Tensor):
+            ptr, n, on_dev = _dev_ptr(data.reshape(-1), torch.uint8), data.numel(), 1
+        else:
+            arr = _u8(data)
+            ptr, n, on_dev, self._keep = _ptr(arr), arr.size, 0, arr
+        _check(_lib.rlq_weights_create(ctx._h, int(dtype), ptr, n, int(rows), int(cols), on_dev,
+                                       ctypes.byref(h), ctypes.byref(err)), err)
+        self._h, self.ctx, self.dtype, self.rows, self.cols = h, ctx, DType(dtype), int(rows), int(cols)
+        self._keep = None
+
+    def close(self):
+        if getattr(self, "_h", None):
+            _lib.rlq_weights_destroy(self._h)
+            self._h = None
+
+    __del__ = close

@@ -1,0 +1,60 @@
+"""Build librlq.so (the gfx950 kernels + C ABI) in-tree with hipcc.
+
+    python rust-llama_amd/build.py
+
+Each .hip source compiles to an object under rust-llama_amd/_build/ in
+parallel, then hipcc links rust-llama_amd/librlq.so.  Flags:
+  --offload-arch=gfx950       MI355X only
+  -ffp-contract=off           f32 rounds step by step, as the reference's Rust
+  -Xclang -target-feature -Xclang -packed-fp32-ops
+                              no packed-f32 instructions are generated
+"""
+import concurrent.futures
+import os
+import subprocess
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(HERE)
+SOURCES = ["api.hip", "matvec.hip", "quantize.hip"]
+LIB = os.path.join(HERE, "librlq.so")
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+
+FLAGS = [
+    "--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-ffp-contract=off",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wall", "-Wno-unused-function",
+    "-I" + os.path.join(ROOT, "include"), "-I" + os.path.join(HERE, "csrc"),
+]
+
+
+def _run(cmd):
+    p = subprocess.run(cmd, capture_output=True, text=True)
+    # hipcc's host pass does not know the packed-fp32 feature; that warning is harmless
+    noise = ("unknown target feature", "packed-fp32-ops", "warning generated", "warnings generated")
+    msg = "\n".join(l for l in (p.stdout + p.stderr).splitlines() if l.strip() and not any(n in l for n in noise))
+    return p.returncode, msg
+
+
+def build(verbose=False):
+    out_dir = os.path.join(HERE, "_build")
+    os.makedirs(out_dir, exist_ok=True)
+    objs = [os.path.join(out_dir, s.replace(".hip", ".o")) for s in SOURCES]
+    cmds = [[HIPCC, *FLAGS, "-c", os.path.join(HERE, "csrc", s), "-o", o] for s, o in zip(SOURCES, objs)]
+    with concurrent.futures.ThreadPoolExecutor(len(cmds)) as ex:
+        results = list(ex.map(_run, cmds))
+    for (rc, msg), s in zip(results, SOURCES):
+        if msg and (verbose or rc):
+            print(f"[{s}]\n{msg}", file=sys.stderr)
+        if rc:
+            raise RuntimeError(f"hipcc failed on {s}")
+    tmp = LIB + ".tmp"
+    rc, msg = _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp, *objs])
+    if rc:
+        raise RuntimeError(f"link failed:\n{msg}")
+    os.replace(tmp, LIB)
+    return LIB
+
+
+if __name__ == "__main__":
+    print(build(verbose=True))

@@ -1,0 +1,616 @@
+// api.hip - the C ABI (include/rlq.h) over the gfx950 kernels.
+//
+// Validation order follows the reference function each entry point replaces
+// (cited per function).  Data checks that need the input values (finite scan,
+// scale preflight) run on the GPU inside the quantizer kernels and land in a
+// device error word; nothing is copied to the caller when it is set.
+#include "rlq.h"
+
+#include <mutex>
+#include <new>
+
+#include "rlq_device.hpp"
+#include "rlq_internal.hpp"
+
+using namespace rlq;
+
+namespace {
+
+// ---- dtype tables (crates/quant/src/lib.rs:171-285) ----------------------
+
+bool dtype_known(uint32_t id) {
+    switch (id) {
+        case 0: case 1: case 2: case 3: case 6: case 7: case 8: case 9: case 10: case 11: case 12: case 13:
+        case 14: case 15: case 16: case 17: case 18: case 19: case 20: case 21: case 22: case 23: case 24:
+        case 25: case 26: case 27: case 28: case 29: case 30: case 34: case 35: case 39: case 40: case 41:
+        case 42: case 43:
+            return true;
+        default:
+            return false;
+    }
+}
+
+uint64_t block_size(uint32_t t) {
+    switch (t) {
+        case 0: case 1: case 30: case 28: case 24: case 25: case 26: case 27: case 43: return 1;
+        case 2: case 3: case 6: case 7: case 8: case 9: case 20: case 39: return 32;
+        case 40: case 42: return 64;
+        case 41: return 128;
+        default: return 256;
+    }
+}
+
+uint64_t type_size(uint32_t t) {
+    switch (t) {
+        case 0: case 26: return 4;
+        case 1: case 30: case 25: return 2;
+        case 28: case 27: return 8;
+        case 24: case 43: return 1;
+        case 2: case 20: case 41: case 42: return 18;
+        case 3: return 20;
+        case 6: return 22;
+        case 7: return 24;
+        case 8: return 34;
+        case 9: case 40: return 36;
+        case 10: return 84;
+        case 11: return 110;
+        case 12: return 144;
+        case 13: return 176;
+        case 14: return 210;
+        case 15: return 292;
+        case 16: case 35: return 66;
+        case 17: return 74;
+        case 18: return 98;
+        case 19: return 50;
+        case 21: return 110;
+        case 22: return 82;
+        case 23: return 136;
+        case 29: return 56;
+        case 34: return 54;
+        case 39: return 17;
+        default: return 0;
+    }
+}
+
+int32_t fail(rlq_error* err, int32_t code, uint32_t dtype = 0, uint64_t a = 0, uint64_t b = 0) {
+    if (err) *err = rlq_error{code, dtype, a, b};
+    return code;
+}
+int32_t ok(rlq_error* err) { return fail(err, RLQ_OK); }
+
+int32_t hip_fail(rlq_error* err, hipError_t e) { return fail(err, RLQ_DEVICE_ERROR, 0, (uint64_t)e); }
+
+#define HIP_TRY(expr)                                  \
+    do {                                               \
+        hipError_t e_ = (expr);                        \
+        if (e_ != hipSuccess) return hip_fail(err, e_); \
+    } while (0)
+
+// DType::row_bytes
+int32_t row_bytes(uint32_t t, uint64_t elements, uint64_t* out, rlq_error* err) {
+    if (!dtype_known(t)) return fail(err, RLQ_INVALID_TYPE, t);
+    const uint64_t bs = block_size(t);
+    if (elements % bs != 0) return fail(err, RLQ_NON_MULTIPLE, t, elements, bs);
+    uint64_t r;
+    if (__builtin_mul_overflow(elements / bs, type_size(t), &r)) return fail(err, RLQ_SIZE_OVERFLOW, t);
+    *out = r;
+    return ok(err);
+}
+
+// lib.rs:310-319
+int32_t validate(uint32_t t, uint64_t bytes, uint64_t elements, rlq_error* err) {
+    uint64_t expected;
+    const int32_t rc = row_bytes(t, elements, &expected, err);
+    if (rc) return rc;
+    if (bytes != expected) return fail(err, RLQ_INVALID_LENGTH, t, expected, bytes);
+    return ok(err);
+}
+
+// matvec.rs:7-18
+int32_t activation_dtype(uint32_t w, uint32_t* out, rlq_error* err) {
+    if (!dtype_known(w)) return fail(err, RLQ_INVALID_TYPE, w);
+    switch (w) {
+        case 41: case 42: case 2: case 6: case 8: case 39: case 40: case 20: *out = 8; break;
+        case 3: case 7: *out = 9; break;
+        case 10: case 11: case 12: case 13: case 14: case 16: case 17: case 22: case 18: case 21: case 19: case 29:
+        case 23: case 34: case 35:
+            *out = 15;
+            break;
+        case 0: case 1: case 43: *out = 0; break;
+        case 30: *out = 30; break;
+        default: return fail(err, RLQ_UNSUPPORTED_MATVEC, w);
+    }
+    return ok(err);
+}
+
+bool path_weight(uint32_t t) { return t == kQ8_0 || t == kQ4_K || t == kQ6_K; }
+
+// ---- device buffers ---------------------------------------------------------
+
+struct DevBuf {
+    void* p = nullptr;
+    size_t n = 0;
+};
+
+}  // namespace
+
+struct rlq_context {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    unsigned long long* err_words = nullptr;  // [0] device API (sticky), [1] host API (per call)
+    unsigned long long* host_err = nullptr;   // pinned readback
+    DevBuf planes, keys, stage_in, stage_w, stage_out;
+};
+
+struct rlq_weights {
+    rlq_context* ctx;
+    uint32_t dtype;
+    uint64_t rows, cols;
+    uint8_t* dev;
+    uint64_t bytes;
+};
+
+namespace {
+
+// Grow-only scratch.  Growing waits for the whole device first (callers may
+// pass their own streams), so no kernel still reads the old buffer when it is
+// freed.
+hipError_t ensure(rlq_context* ctx, DevBuf& b, size_t need) {
+    (void)ctx;
+    if (b.n >= need) return hipSuccess;
+    hipError_t e = hipDeviceSynchronize();
+    if (e != hipSuccess) return e;
+    if (b.p) (void)hipFree(b.p);
+    b.p = nullptr;
+    b.n = 0;
+    size_t n = need < 4096 ? 4096 : need;
+    e = hipMalloc(&b.p, n);
+    if (e != hipSuccess) return e;
+    b.n = n;
+    return hipSuccess;
+}
+
+struct DeviceGuard {
+    int prev = -1;
+    explicit DeviceGuard(int dev) {
+        if (hipGetDevice(&prev) == hipSuccess && prev != dev) (void)hipSetDevice(dev);
+        else prev = -1;
+    }
+    ~DeviceGuard() {
+        if (prev >= 0) (void)hipSetDevice(prev);
+    }
+};
+
+hipStream_t pick(rlq_context* ctx, void* stream) { return stream ? (hipStream_t)stream : ctx->stream; }
+
+// Decode an error key (see rlq_device.hpp) into an rlq_error.
+int32_t key_to_error(unsigned long long key, uint32_t dtype, rlq_error* err) {
+    if (key == ~0ull) return ok(err);
+    const uint64_t column = key >> 41, kind = (key >> 40) & 1, index = key & ((1ull << 40) - 1);
+    return fail(err, kind == (uint64_t)kKindNonFinite ? RLQ_NON_FINITE_INPUT : RLQ_UNREPRESENTABLE_SCALE, dtype,
+                index, column);
+}
+
+// Read and clear error word `slot` after the stream drains.
+int32_t take_error(rlq_context* ctx, int slot, hipStream_t s, uint32_t dtype, rlq_error* err) {
+    HIP_TRY(hipMemcpyAsync(ctx->host_err, ctx->err_words + slot, 8, hipMemcpyDeviceToHost, s));
+    HIP_TRY(hipStreamSynchronize(s));
+    const unsigned long long key = *ctx->host_err;
+    if (key != ~0ull) {
+        HIP_TRY(launch_fill_u64(ctx->err_words + slot, 1, ~0ull, s));
+        HIP_TRY(hipStreamSynchronize(s));
+    }
+    return key_to_error(key, dtype, err);
+}
+
+std::mutex g_default_mu;
+rlq_context* g_default = nullptr;
+
+int32_t default_context(rlq_context** out, rlq_error* err) {
+    if (!g_default) {
+        const int32_t rc = rlq_context_create(-1, &g_default, err);
+        if (rc) return rc;
+    }
+    *out = g_default;
+    return ok(err);
+}
+
+// Quantize `batch` activation rows into planes on `s`, errors into `slot`.
+hipError_t quantize_planes(rlq_context* ctx, uint32_t at, const float* x, uint64_t cols, uint64_t batch,
+                           ActPlanes* planes, int slot, hipStream_t s) {
+    hipError_t e = ensure(ctx, ctx->planes, act_planes_bytes(at, cols, batch));
+    if (e != hipSuccess) return e;
+    *planes = act_planes_carve(ctx->planes.p, at, cols, batch);
+    return at == kQ8_K ? launch_quantize_q8k(x, cols, batch, planes, nullptr, ctx->err_words + slot, s)
+                       : launch_quantize_q8_0(x, cols, batch, planes, nullptr, ctx->err_words + slot, s);
+}
+
+// Upload GGUF weights (host or device bytes) into a fresh device buffer in
+// the kernels' layout.
+hipError_t upload_weights(rlq_context* ctx, uint32_t t, const void* bytes, uint64_t len, uint64_t rows, uint64_t cols,
+                          bool on_device, uint8_t** dev, hipStream_t s) {
+    hipError_t e = hipMalloc((void**)dev, len ? len : 1);
+    if (e != hipSuccess) return e;
+    const uint8_t* src = (const uint8_t*)bytes;
+    if (t == kQ4_K) {
+        e = hipMemcpyAsync(*dev, src, len, on_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice, s);
+    } else {
+        if (!on_device) {
+            e = ensure(ctx, ctx->stage_w, len);
+            if (e == hipSuccess) e = hipMemcpyAsync(ctx->stage_w.p, src, len, hipMemcpyHostToDevice, s);
+            src = (const uint8_t*)ctx->stage_w.p;
+        }
+        if (e == hipSuccess) e = launch_repack(t, src, rows, cols, *dev, s);
+    }
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    if (e != hipSuccess) {
+        (void)hipFree(*dev);
+        *dev = nullptr;
+    }
+    return e;
+}
+
+}  // namespace
+
+// ===========================================================================
+// C ABI
+// ===========================================================================
+
+extern "C" {
+
+const char* rlq_status_string(int32_t code) {
+    switch (code) {
+        case RLQ_OK: return "ok";
+        case RLQ_INVALID_TYPE: return "GGML type is unknown or reserved";
+        case RLQ_UNSUPPORTED_MATVEC: return "no matrix-vector weight dot for this type";
+        case RLQ_INVALID_VECTOR_LENGTH: return "wrong vector length";
+        case RLQ_INVALID_MATRIX_SHAPE: return "matrix dimensions must be positive";
+        case RLQ_NON_MULTIPLE: return "row length is not a multiple of the block size";
+        case RLQ_SIZE_OVERFLOW: return "tensor byte length exceeds addressable memory";
+        case RLQ_INVALID_LENGTH: return "wrong byte length";
+        case RLQ_ALLOCATION_FAILED: return "unable to allocate tensor output";
+        case RLQ_UNSUPPORTED_QUANTIZATION: return "encoder not available for this type";
+        case RLQ_UNSUPPORTED_WEIGHTED_QUANTIZATION: return "importance-weighted encoder not available";
+        case RLQ_IMPORTANCE_WEIGHTS_REQUIRED: return "the type requires importance weights";
+        case RLQ_INVALID_IMPORTANCE_LENGTH: return "wrong importance weight count";
+        case RLQ_INVALID_IMPORTANCE_WEIGHT: return "importance weight must be finite and nonnegative";
+        case RLQ_UNSUPPORTED_INTEGER_CONVERSION: return "integer assignment not defined for this type";
+        case RLQ_INTEGER_OUT_OF_RANGE: return "element outside the integer range";
+        case RLQ_NON_FINITE_INPUT: return "non-finite quantizer input";
+        case RLQ_UNREPRESENTABLE_SCALE: return "quantizer scale is not representable";
+        case RLQ_DEVICE_ERROR: return "HIP runtime error";
+        case RLQ_UNIMPLEMENTED: return "type is outside the Q8_0/Q4_K/Q6_K path";
+        case RLQ_INVALID_ARGUMENT: return "null pointer or handle";
+        default: return "unknown status";
+    }
+}
+
+int32_t rlq_row_bytes(uint32_t dtype, uint64_t elements, uint64_t* out, rlq_error* err) {
+    uint64_t r = 0;
+    const int32_t rc = row_bytes(dtype, elements, &r, err);
+    if (rc == RLQ_OK && out) *out = r;
+    return rc;
+}
+
+int32_t rlq_matvec_activation_dtype(uint32_t w, uint32_t* out, rlq_error* err) {
+    uint32_t a = 0;
+    const int32_t rc = activation_dtype(w, &a, err);
+    if (rc == RLQ_OK && out) *out = a;
+    return rc;
+}
+
+// ---- context ----------------------------------------------------------------
+
+int32_t rlq_context_create(int32_t device, rlq_context** out, rlq_error* err) {
+    if (!out) return fail(err, RLQ_INVALID_ARGUMENT);
+    if (device < 0) HIP_TRY(hipGetDevice(&device));
+    DeviceGuard g(device);
+    rlq_context* ctx = new (std::nothrow) rlq_context;
+    if (!ctx) return fail(err, RLQ_ALLOCATION_FAILED);
+    ctx->device = device;
+    hipError_t e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
+    if (e == hipSuccess) e = hipMalloc((void**)&ctx->err_words, 2 * sizeof(unsigned long long));
+    if (e == hipSuccess) e = hipHostMalloc((void**)&ctx->host_err, sizeof(unsigned long long), hipHostMallocDefault);
+    if (e == hipSuccess) e = launch_fill_u64(ctx->err_words, 2, ~0ull, ctx->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) {
+        rlq_context_destroy(ctx);
+        return hip_fail(err, e);
+    }
+    *out = ctx;
+    return ok(err);
+}
+
+void rlq_context_destroy(rlq_context* ctx) {
+    if (!ctx) return;
+    DeviceGuard g(ctx->device);
+    if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
+    for (DevBuf* b : {&ctx->planes, &ctx->keys, &ctx->stage_in, &ctx->stage_w, &ctx->stage_out})
+        if (b->p) (void)hipFree(b->p);
+    if (ctx->err_words) (void)hipFree(ctx->err_words);
+    if (ctx->host_err) (void)hipHostFree(ctx->host_err);
+    if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
+    if (ctx == g_default) g_default = nullptr;
+    delete ctx;
+}
+
+void* rlq_context_stream(rlq_context* ctx) { return ctx ? (void*)ctx->stream : nullptr; }
+
+// ---- weights ------------------------------------------------------------------
+
+// Matrix::from_quantized (crates/model-runtime/src/math.rs:35-70)
+int32_t rlq_weights_create(rlq_context* ctx, uint32_t dtype, const void* bytes, uint64_t len, uint64_t rows,
+                           uint64_t cols, int32_t bytes_on_device, rlq_weights** out, rlq_error* err) {
+    if (!ctx || !out) return fail(err, RLQ_INVALID_ARGUMENT);
+    uint32_t at;
+    int32_t rc = activation_dtype(dtype, &at, err);
+    if (rc) return rc;
+    if (!path_weight(dtype)) return fail(err, RLQ_UNIMPLEMENTED, dtype);
+    if (rows == 0 || cols == 0) return fail(err, RLQ_INVALID_MATRIX_SHAPE, dtype, rows, cols);
+    uint64_t rb, expected;
+    rc = row_bytes(dtype, cols, &rb, err);
+    if (rc) return rc;
+    if (__builtin_mul_overflow(rb, rows, &expected)) return fail(err, RLQ_SIZE_OVERFLOW, dtype);
+    if (len != expected) return fail(err, RLQ_INVALID_LENGTH, dtype, expected, len);
+    if (!bytes) return fail(err, RLQ_INVALID_ARGUMENT, dtype);
+    DeviceGuard g(ctx->device);
+    rlq_weights* w = new (std::nothrow) rlq_weights{ctx, dtype, rows, cols, nullptr, len};
+    if (!w) return fail(err, RLQ_ALLOCATION_FAILED);
+    const hipError_t e = upload_weights(ctx, dtype, bytes, len, rows, cols, bytes_on_device != 0, &w->dev, ctx->stream);
+    if (e != hipSuccess) {
+        delete w;
+        return e == hipErrorOutOfMemory ? fail(err, RLQ_ALLOCATION_FAILED, dtype) : hip_fail(err, e);
+    }
+    *out = w;
+    return ok(err);
+}
+
+void rlq_weights_destroy(rlq_weights* w) {
+    if (!w) return;
+    DeviceGuard g(w->ctx->device);
+    (void)hipStreamSynchronize(w->ctx->stream);
+    if (w->dev) (void)hipFree(w->dev);
+    delete w;
+}
+
+void rlq_weights_shape(const rlq_weights* w, uint64_t* rows, uint64_t* cols, uint32_t* dtype) {
+    if (!w) return;
+    if (rows) *rows = w->rows;
+    if (cols) *cols = w->cols;
+    if (dtype) *dtype = w->dtype;
+}
+
+// ---- device matmul --------------------------------------------------------------
+
+static int32_t matmul_impl(rlq_context* ctx, const rlq_weights* w, const float* x, uint64_t batch, float* y,
+                           uint32_t* argmax, void* stream, rlq_error* err) {
+    if (!ctx || !w || !x || !y) return fail(err, RLQ_INVALID_ARGUMENT);
+    if (batch == 0) return ok(err);
+    DeviceGuard g(ctx->device);
+    const hipStream_t s = pick(ctx, stream);
+    uint32_t at = 0;
+    (void)activation_dtype(w->dtype, &at, nullptr);
+    ActPlanes planes;
+    HIP_TRY(quantize_planes(ctx, at, x, w->cols, batch, &planes, 0, s));
+    unsigned long long* keys = nullptr;
+    if (argmax) {
+        HIP_TRY(ensure(ctx, ctx->keys, batch * sizeof(unsigned long long)));
+        keys = (unsigned long long*)ctx->keys.p;
+        HIP_TRY(launch_fill_u64(keys, batch, 0ull, s));
+    }
+    HIP_TRY(launch_matvec(w->dtype, w->dev, w->rows, w->cols, &planes, batch, y, w->rows, keys, s));
+    if (argmax) HIP_TRY(launch_argmax_finish(keys, batch, y, w->rows, argmax, s));
+    return ok(err);
+}
+
+int32_t rlq_matmul(rlq_context* ctx, const rlq_weights* w, const float* x, uint64_t batch, float* y, void* stream,
+                   rlq_error* err) {
+    return matmul_impl(ctx, w, x, batch, y, nullptr, stream, err);
+}
+
+int32_t rlq_matmul_argmax(rlq_context* ctx, const rlq_weights* w, const float* x, uint64_t batch, float* y,
+                          uint32_t* argmax, void* stream, rlq_error* err) {
+    if (!argmax) return fail(err, RLQ_INVALID_ARGUMENT);
+    return matmul_impl(ctx, w, x, batch, y, argmax, stream, err);
+}
+
+int32_t rlq_quantize_device(rlq_context* ctx, uint32_t dtype, const float* x, uint64_t cols, uint64_t batch,
+                            uint8_t* out, void* stream, rlq_error* err) {
+    if (!ctx) return fail(err, RLQ_INVALID_ARGUMENT);
+    if (!dtype_known(dtype)) return fail(err, RLQ_INVALID_TYPE, dtype);
+    if (dtype != kQ8_K && dtype != kQ8_0 && dtype != kQ4_K && dtype != kQ6_K) return fail(err, RLQ_UNIMPLEMENTED, dtype);
+    uint64_t rb, n;
+    int32_t rc = row_bytes(dtype, cols, &rb, err);
+    if (rc) return rc;
+    if (__builtin_mul_overflow(cols, batch, &n)) return fail(err, RLQ_SIZE_OVERFLOW, dtype);
+    if (n == 0) return ok(err);
+    if (!x || !out) return fail(err, RLQ_INVALID_ARGUMENT, dtype);
+    DeviceGuard g(ctx->device);
+    const hipStream_t s = pick(ctx, stream);
+    unsigned long long* ew = ctx->err_words;
+    if (dtype == kQ8_K) HIP_TRY(launch_quantize_q8k(x, cols, batch, nullptr, out, ew, s));
+    else if (dtype == kQ8_0) HIP_TRY(launch_quantize_q8_0(x, cols, batch, nullptr, out, ew, s));
+    else {
+        // the K encoders see the rows as one run of blocks (rows are whole blocks)
+        HIP_TRY(launch_finite_scan(x, n, ew, s));
+        HIP_TRY(dtype == kQ4_K ? launch_encode_q4k(x, n, out, ew, s) : launch_encode_q6k(x, n, out, ew, s));
+    }
+    return ok(err);
+}
+
+int32_t rlq_sync(rlq_context* ctx, void* stream, rlq_error* err) {
+    if (!ctx) return fail(err, RLQ_INVALID_ARGUMENT);
+    DeviceGuard g(ctx->device);
+    const hipStream_t s = pick(ctx, stream);
+    HIP_TRY(hipStreamSynchronize(s));
+    return take_error(ctx, 0, s, 0, err);
+}
+
+int32_t rlq_block_sums(rlq_context* ctx, const rlq_weights* w, const float* x, int32_t* isum, int32_t* imin,
+                       void* stream, rlq_error* err) {
+    if (!ctx || !w || !x || !isum || !imin) return fail(err, RLQ_INVALID_ARGUMENT);
+    DeviceGuard g(ctx->device);
+    const hipStream_t s = pick(ctx, stream);
+    uint32_t at = 0;
+    (void)activation_dtype(w->dtype, &at, nullptr);
+    ActPlanes planes;
+    HIP_TRY(quantize_planes(ctx, at, x, w->cols, 1, &planes, 0, s));
+    HIP_TRY(launch_block_sums(w->dtype, w->dev, w->rows, w->cols, &planes, isum, imin, s));
+    return ok(err);
+}
+
+// ---- host drop-ins ----------------------------------------------------------------
+
+// quantize_into (crates/quant/src/encode.rs:37-100; encode_k.rs:11-33)
+int32_t rlq_quantize_into(uint32_t dtype, const float* values, uint64_t n, uint8_t* out, uint64_t out_len,
+                          rlq_error* err) {
+    int32_t rc = validate(dtype, out_len, n, err);
+    if (rc) return rc;
+    // supported() (encode.rs:102-113)
+    if (dtype == 16 || dtype == 17 || dtype == 19) return fail(err, RLQ_IMPORTANCE_WEIGHTS_REQUIRED, dtype);
+    if (dtype == 24 || dtype == 25 || dtype == 26 || dtype == 27) return fail(err, RLQ_UNSUPPORTED_QUANTIZATION, dtype);
+    if (dtype != kQ8_0 && dtype != kQ8_K && dtype != kQ4_K && dtype != kQ6_K) return fail(err, RLQ_UNIMPLEMENTED, dtype);
+    if (n == 0) return ok(err);
+    if (!values || !out) return fail(err, RLQ_INVALID_ARGUMENT, dtype);
+    std::lock_guard<std::mutex> lock(g_default_mu);
+    rlq_context* ctx;
+    rc = default_context(&ctx, err);
+    if (rc) return rc;
+    DeviceGuard g(ctx->device);
+    const hipStream_t s = ctx->stream;
+    HIP_TRY(ensure(ctx, ctx->stage_in, n * sizeof(float)));
+    HIP_TRY(ensure(ctx, ctx->stage_out, out_len));
+    float* xd = (float*)ctx->stage_in.p;
+    uint8_t* od = (uint8_t*)ctx->stage_out.p;
+    unsigned long long* ew = ctx->err_words + 1;
+    HIP_TRY(hipMemcpyAsync(xd, values, n * sizeof(float), hipMemcpyHostToDevice, s));
+    if (dtype == kQ8_K) HIP_TRY(launch_quantize_q8k(xd, n, 1, nullptr, od, ew, s));
+    else if (dtype == kQ8_0) HIP_TRY(launch_quantize_q8_0(xd, n, 1, nullptr, od, ew, s));
+    else {
+        HIP_TRY(launch_finite_scan(xd, n, ew, s));
+        HIP_TRY(dtype == kQ4_K ? launch_encode_q4k(xd, n, od, ew, s) : launch_encode_q6k(xd, n, od, ew, s));
+    }
+    rc = take_error(ctx, 1, s, dtype, err);
+    if (rc) {
+        if (err) err->b = 0;
+        return rc;
+    }
+    HIP_TRY(hipMemcpyAsync(out, od, out_len, hipMemcpyDeviceToHost, s));
+    HIP_TRY(hipStreamSynchronize(s));
+    return ok(err);
+}
+
+// dequantize_into (crates/quant/src/lib.rs:299-308)
+int32_t rlq_dequantize_into(uint32_t dtype, const uint8_t* bytes, uint64_t len, float* out, uint64_t n,
+                            rlq_error* err) {
+    int32_t rc = validate(dtype, len, n, err);
+    if (rc) return rc;
+    if (dtype != kQ8_0 && dtype != kQ8_K && dtype != kQ4_K && dtype != kQ6_K) return fail(err, RLQ_UNIMPLEMENTED, dtype);
+    if (n == 0) return ok(err);
+    if (!bytes || !out) return fail(err, RLQ_INVALID_ARGUMENT, dtype);
+    std::lock_guard<std::mutex> lock(g_default_mu);
+    rlq_context* ctx;
+    rc = default_context(&ctx, err);
+    if (rc) return rc;
+    DeviceGuard g(ctx->device);
+    const hipStream_t s = ctx->stream;
+    HIP_TRY(ensure(ctx, ctx->stage_w, len));
+    HIP_TRY(ensure(ctx, ctx->stage_out, n * sizeof(float)));
+    HIP_TRY(hipMemcpyAsync(ctx->stage_w.p, bytes, len, hipMemcpyHostToDevice, s));
+    HIP_TRY(launch_dequantize(dtype, (const uint8_t*)ctx->stage_w.p, n, (float*)ctx->stage_out.p, s));
+    HIP_TRY(hipMemcpyAsync(out, ctx->stage_out.p, n * sizeof(float), hipMemcpyDeviceToHost, s));
+    HIP_TRY(hipStreamSynchronize(s));
+    return ok(err);
+}
+
+// dot_packed (crates/quant/src/matvec.rs:90-103)
+int32_t rlq_dot_packed(uint32_t wtype, const uint8_t* weights, uint64_t weights_len, const uint8_t* activation,
+                       uint64_t activation_len, uint64_t elements, float* out, rlq_error* err) {
+    uint32_t at;
+    int32_t rc = activation_dtype(wtype, &at, err);
+    if (rc) return rc;
+    if (block_size(wtype) == 1) return fail(err, RLQ_UNSUPPORTED_MATVEC, wtype);
+    if (!path_weight(wtype)) return fail(err, RLQ_UNIMPLEMENTED, wtype);
+    rc = validate(wtype, weights_len, elements, err);
+    if (rc) return rc;
+    rc = validate(at, activation_len, elements, err);
+    if (rc) return rc;
+    if (!out) return fail(err, RLQ_INVALID_ARGUMENT, wtype);
+    if (elements == 0) {  // no blocks: the reference's sums stay 0.0
+        *out = 0.0f;
+        return ok(err);
+    }
+    if (!weights || !activation) return fail(err, RLQ_INVALID_ARGUMENT, wtype);
+    std::lock_guard<std::mutex> lock(g_default_mu);
+    rlq_context* ctx;
+    rc = default_context(&ctx, err);
+    if (rc) return rc;
+    DeviceGuard g(ctx->device);
+    const hipStream_t s = ctx->stream;
+    uint8_t* wd = nullptr;
+    hipError_t e = upload_weights(ctx, wtype, weights, weights_len, 1, elements, false, &wd, s);
+    if (e != hipSuccess) return hip_fail(err, e);
+    e = ensure(ctx, ctx->stage_in, activation_len);
+    if (e == hipSuccess) e = ensure(ctx, ctx->planes, act_planes_bytes(at, elements, 1));
+    if (e == hipSuccess) e = ensure(ctx, ctx->stage_out, sizeof(float));
+    ActPlanes planes{};
+    if (e == hipSuccess) {
+        planes = act_planes_carve(ctx->planes.p, at, elements, 1);
+        e = hipMemcpyAsync(ctx->stage_in.p, activation, activation_len, hipMemcpyHostToDevice, s);
+    }
+    if (e == hipSuccess) e = launch_act_from_gguf(at, (const uint8_t*)ctx->stage_in.p, elements, 1, &planes, s);
+    if (e == hipSuccess)
+        e = launch_matvec(wtype, wd, 1, elements, &planes, 1, (float*)ctx->stage_out.p, 1, nullptr, s);
+    if (e == hipSuccess) e = hipMemcpyAsync(out, ctx->stage_out.p, sizeof(float), hipMemcpyDeviceToHost, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    (void)hipFree(wd);
+    return e == hipSuccess ? ok(err) : hip_fail(err, e);
+}
+
+// matvec (crates/quant/src/matvec.rs:24-87)
+int32_t rlq_matvec(uint32_t wtype, const uint8_t* weights, uint64_t weights_len, uint64_t rows, uint64_t cols,
+                   const float* input, uint64_t input_len, float* output, rlq_error* err) {
+    uint32_t at;
+    int32_t rc = activation_dtype(wtype, &at, err);
+    if (rc) return rc;
+    if (!path_weight(wtype)) return fail(err, RLQ_UNIMPLEMENTED, wtype);
+    if (rows == 0 || cols == 0) return fail(err, RLQ_INVALID_MATRIX_SHAPE, wtype, rows, cols);
+    if (input_len != cols) return fail(err, RLQ_INVALID_VECTOR_LENGTH, wtype, cols, input_len);
+    uint64_t rb, expected;
+    rc = row_bytes(wtype, cols, &rb, err);
+    if (rc) return rc;
+    if (__builtin_mul_overflow(rb, rows, &expected)) return fail(err, RLQ_SIZE_OVERFLOW, wtype);
+    if (weights_len != expected) return fail(err, RLQ_INVALID_LENGTH, wtype, expected, weights_len);
+    if (!weights || !input || !output) return fail(err, RLQ_INVALID_ARGUMENT, wtype);
+    std::lock_guard<std::mutex> lock(g_default_mu);
+    rlq_context* ctx;
+    rc = default_context(&ctx, err);
+    if (rc) return rc;
+    DeviceGuard g(ctx->device);
+    const hipStream_t s = ctx->stream;
+    uint8_t* wd = nullptr;
+    hipError_t e = upload_weights(ctx, wtype, weights, weights_len, rows, cols, false, &wd, s);
+    if (e != hipSuccess) return e == hipErrorOutOfMemory ? fail(err, RLQ_ALLOCATION_FAILED, wtype) : hip_fail(err, e);
+    ActPlanes planes{};
+    e = ensure(ctx, ctx->stage_in, cols * sizeof(float));
+    if (e == hipSuccess) e = ensure(ctx, ctx->stage_out, rows * sizeof(float));
+    if (e == hipSuccess) e = hipMemcpyAsync(ctx->stage_in.p, input, cols * sizeof(float), hipMemcpyHostToDevice, s);
+    if (e == hipSuccess) e = quantize_planes(ctx, at, (const float*)ctx->stage_in.p, cols, 1, &planes, 1, s);
+    if (e == hipSuccess)
+        e = launch_matvec(wtype, wd, rows, cols, &planes, 1, (float*)ctx->stage_out.p, rows, nullptr, s);
+    if (e != hipSuccess) {
+        (void)hipFree(wd);
+        return hip_fail(err, e);
+    }
+    rc = take_error(ctx, 1, s, at, err);
+    (void)hipFree(wd);
+    if (rc) {
+        if (err) err->b = 0;
+        return rc;
+    }
+    HIP_TRY(hipMemcpyAsync(output, ctx->stage_out.p, rows * sizeof(float), hipMemcpyDeviceToHost, s));
+    HIP_TRY(hipStreamSynchronize(s));
+    return ok(err);
+}
+
+}  // extern "C"

@@ -1,0 +1,174 @@
+// rlq_device.hpp - device helpers shared by the gfx950 kernels.
+//
+// Everything here is compiled with -ffp-contract=off: f32 expressions round
+// operation by operation, as the reference's Rust source does, and fused
+// multiply-adds appear only where a kernel asks for one explicitly.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace rlq {
+
+constexpr int kWave = 64;
+
+// ---- f16 <-> f32 --------------------------------------------------------
+
+// Hardware conversion: exact for every non-NaN half (f16 denormals are kept
+// by the default gfx9 FP mode).
+__device__ __forceinline__ float half_to_float(uint32_t bits) {
+    return (float)__builtin_bit_cast(_Float16, (uint16_t)(bits & 0xffffu));
+}
+
+// Binary32 -> binary16 with ties-to-even and signed canonical NaNs, bit for bit
+// as crates/quant/src/lib.rs:340-373 (f32_to_f16).  Used by the encoders,
+// where the stored bits must equal the reference's.
+__device__ __forceinline__ uint32_t float_to_half_bits(float value) {
+    const uint32_t bits = __float_as_uint(value);
+    const uint32_t sign = (bits >> 16) & 0x8000u;
+    const int32_t exp = (int32_t)((bits >> 23) & 255u);
+    const uint32_t frac = bits & 0x7fffffu;
+    if (exp == 255) return sign | (frac == 0 ? 0x7c00u : 0x7e00u);
+    const int32_t e = exp - 127;
+    if (e > 15) return sign | 0x7c00u;
+    if (e >= -14) {
+        uint32_t mant = frac >> 13;
+        const uint32_t rest = frac & 8191u;
+        if (rest > 4096u || (rest == 4096u && (mant & 1u) != 0)) mant += 1;
+        return (sign | ((((uint32_t)(e + 15)) << 10) + mant)) & 0xffffu;
+    }
+    if (e < -25) return sign;
+    const uint32_t mant = frac | 0x800000u;
+    const uint32_t shift = (uint32_t)(-e - 1);
+    uint32_t rounded = mant >> shift;
+    const uint32_t rest = mant & ((1u << shift) - 1u);
+    const uint32_t half = 1u << (shift - 1u);
+    if (rest > half || (rest == half && (rounded & 1u) != 0)) rounded += 1;
+    return (sign | rounded) & 0xffffu;
+}
+
+// Binary16 -> binary32 bit for bit as lib.rs:323-337 (NaNs quieted).  The
+// encoders read back the half they stored through this.
+__device__ __forceinline__ float half_bits_to_float_exact(uint32_t h) {
+    const uint32_t sign = (h & 0x8000u) << 16;
+    const uint32_t exp = (h >> 10) & 31u;
+    const uint32_t fraction = h & 1023u;
+    uint32_t result;
+    if (exp == 0 && fraction == 0) {
+        result = sign;
+    } else if (exp == 0) {
+        const uint32_t shift = (uint32_t)__builtin_clz(fraction) - 21u;
+        result = sign | ((113u - shift) << 23) | (((fraction << shift) & 1023u) << 13);
+    } else if (exp == 31) {
+        result = sign | 0x7f800000u | (fraction << 13) | (fraction != 0 ? 0x00400000u : 0u);
+    } else {
+        result = sign | ((exp + 112u) << 23) | (fraction << 13);
+    }
+    return __uint_as_float(result);
+}
+
+__device__ __forceinline__ bool finite(float v) { return __builtin_isfinite(v); }
+
+// ---- integer dot ---------------------------------------------------------
+
+// v_dot4_i32_i8: acc + sum of four signed byte products.
+__device__ __forceinline__ int32_t dot4(uint32_t a, uint32_t b, int32_t acc) {
+    return __builtin_amdgcn_sdot4((int)a, (int)b, acc, false);
+}
+
+// ---- cross-lane reductions (wave64) -------------------------------------
+
+// DPP control codes (GFX9 encoding).
+constexpr int kQuadXor1 = 0xB1;        // quad_perm [1,0,3,2]
+constexpr int kQuadXor2 = 0x4E;        // quad_perm [2,3,0,1]
+constexpr int kRowHalfMirror = 0x141;  // lane i <-> 7-i within each 8 lanes
+constexpr int kRowRor8 = 0x128;        // rotate right by 8 within each 16 lanes
+
+template <int Ctrl>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), Ctrl, 0xf, 0xf, false));
+}
+template <int Ctrl>
+__device__ __forceinline__ int32_t dpp_i(int32_t v) {
+    return __builtin_amdgcn_update_dpp(0, v, Ctrl, 0xf, 0xf, false);
+}
+
+// Sum over each aligned group of 8 lanes; every lane of the group gets it.
+__device__ __forceinline__ int32_t group8_sum(int32_t v) {
+    v += dpp_i<kQuadXor1>(v);
+    v += dpp_i<kQuadXor2>(v);
+    v += dpp_i<kRowHalfMirror>(v);
+    return v;
+}
+
+// Sum over all 64 lanes; every lane gets it.
+__device__ __forceinline__ float wave_sum(float v) {
+    v += dpp_f<kQuadXor1>(v);
+    v += dpp_f<kQuadXor2>(v);
+    v += dpp_f<kRowHalfMirror>(v);
+    v += dpp_f<kRowRor8>(v);
+    v += __shfl_xor(v, 16, 64);
+    v += __shfl_xor(v, 32, 64);
+    return v;
+}
+
+__device__ __forceinline__ int32_t wave_sum_i(int32_t v) {
+    v += dpp_i<kQuadXor1>(v);
+    v += dpp_i<kQuadXor2>(v);
+    v += dpp_i<kRowHalfMirror>(v);
+    v += dpp_i<kRowRor8>(v);
+    v += __shfl_xor(v, 16, 64);
+    v += __shfl_xor(v, 32, 64);
+    return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+    for (int m = 1; m < 64; m <<= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
+    return v;
+}
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
+    for (int m = 1; m < 64; m <<= 1) {
+        const uint32_t o = (uint32_t)__shfl_xor((int)v, m, 64);
+        v = o < v ? o : v;
+    }
+    return v;
+}
+__device__ __forceinline__ uint64_t wave_min_u64(uint64_t v) {
+    for (int m = 1; m < 64; m <<= 1) {
+        const uint64_t o = __shfl_xor(v, m, 64);
+        v = o < v ? o : v;
+    }
+    return v;
+}
+
+// ---- loads ---------------------------------------------------------------
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// 16-byte global load that streams past the caches (weights are read once).
+__device__ __forceinline__ uint4 load_stream16(const void* p) {
+    const u32x4 v = __builtin_nontemporal_load((const u32x4*)p);
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+// ---- device error word ---------------------------------------------------
+//
+// One u64 per context, UINT64_MAX when clear.  The first data error in the
+// reference's reporting order wins an atomicMin:
+//   key = column << 41 | kind << 40 | index
+// kind 0 = NonFiniteInput{index}, kind 1 = UnrepresentableScale{block}.  In
+// the reference every check of one activation row runs before the next row
+// is quantized (crates/tensor/src/cpu_extra.rs:815-822), and within one row
+// the finite scan precedes the scale preflight (encode.rs:70-77).
+constexpr int kKindNonFinite = 0;
+constexpr int kKindScale = 1;
+
+__device__ __forceinline__ uint64_t error_key(uint64_t column, int kind, uint64_t index) {
+    return (column << 41) | ((uint64_t)kind << 40) | (index & ((1ull << 40) - 1));
+}
+
+__device__ __forceinline__ void report_error(unsigned long long* word, uint64_t key) {
+    atomicMin(word, (unsigned long long)key);
+}
+
+}  // namespace rlq

@@ -1,0 +1,75 @@
+// rlq_internal.hpp - host-side launchers shared between the library's
+// translation units.  Not part of the C ABI (include/rlq.h is).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace rlq {
+
+enum DTypeId : uint32_t { kQ8_0 = 8, kQ4_K = 12, kQ6_K = 14, kQ8_K = 15 };
+
+// Activations of `batch` columns in structure-of-arrays form on the device:
+//   q    int8  [batch][cols]
+//   d    f32   [batch][cols / block]   (Q8_K: the f32 d; Q8_0: f32 of the
+//                                       stored f16 d)
+//   bsum int16 [batch][cols / 16]      (Q8_K only: the Q8_K bsums)
+//   bad  u8    [batch][cols / block]   nonzero marks a block whose column
+//                                      failed validation; the matvec then
+//                                      writes nothing (validate-before-mutate)
+struct ActPlanes {
+    int8_t* q;
+    float* d;
+    int16_t* bsum;
+    uint8_t* bad;
+};
+
+// Bytes one ActPlanes needs for `batch` columns of `cols` elements.
+size_t act_planes_bytes(uint32_t act_type, uint64_t cols, uint64_t batch);
+ActPlanes act_planes_carve(void* base, uint32_t act_type, uint64_t cols, uint64_t batch);
+
+// ---- quantize.hip ----
+// Activation quantizers (matvec.rs:56, cpu_extra.rs:820).  Exactly one of
+// `planes` / `gguf` may be null.  Data errors go to `err_word`.
+hipError_t launch_quantize_q8k(const float* x, uint64_t cols, uint64_t batch, const ActPlanes* planes,
+                               uint8_t* gguf, unsigned long long* err_word, hipStream_t s);
+hipError_t launch_quantize_q8_0(const float* x, uint64_t cols, uint64_t batch, const ActPlanes* planes,
+                                uint8_t* gguf, unsigned long long* err_word, hipStream_t s);
+// Weight encoders (encode_k.rs:430-561), GGUF bytes out, n % 256 == 0.
+hipError_t launch_encode_q4k(const float* x, uint64_t n, uint8_t* out, unsigned long long* err_word,
+                             hipStream_t s);
+hipError_t launch_encode_q6k(const float* x, uint64_t n, uint8_t* out, unsigned long long* err_word,
+                             hipStream_t s);
+// GGUF activation bytes (Q8_K / Q8_0) -> planes, for pre-quantized inputs.
+hipError_t launch_act_from_gguf(uint32_t act_type, const uint8_t* gguf, uint64_t cols, uint64_t batch,
+                                const ActPlanes* planes, hipStream_t s);
+// Finite scan over n values: NonFiniteInput{first index} into err_word.
+hipError_t launch_finite_scan(const float* x, uint64_t n, unsigned long long* err_word, hipStream_t s);
+// Decoders (decode.rs), GGUF bytes in.
+hipError_t launch_dequantize(uint32_t dtype, const uint8_t* b, uint64_t n, float* y, hipStream_t s);
+// GGUF -> device layout.  Q4_K keeps the GGUF layout (plain copy).
+hipError_t launch_repack(uint32_t dtype, const uint8_t* gguf, uint64_t rows, uint64_t cols, uint8_t* dev,
+                         hipStream_t s);
+hipError_t launch_fill_u64(unsigned long long* p, uint64_t n, unsigned long long v, hipStream_t s);
+
+// ---- matvec.hip ----
+// y[b*ldy + r] = dot(row r, activation column b) for b < batch <= 8.
+// `argmax_key` (may be null) receives, per column, the packed greedy-argmax
+// key of y (see matvec.hip).  Rows are skipped entirely when any activation
+// block carries the NaN error mark.
+hipError_t launch_matvec(uint32_t wtype, const uint8_t* w, uint64_t rows, uint64_t cols, const ActPlanes* act,
+                         uint64_t batch, float* y, uint64_t ldy, unsigned long long* argmax_key,
+                         hipStream_t s);
+// Exact per-(row, block) integer sums of the weights against activation
+// column 0 (the debug view of the dot's integer part).
+hipError_t launch_block_sums(uint32_t wtype, const uint8_t* w, uint64_t rows, uint64_t cols,
+                             const ActPlanes* act, int32_t* isum, int32_t* imin, hipStream_t s);
+// Decode argmax keys into u32 indices.
+hipError_t launch_argmax_finish(const unsigned long long* keys, uint64_t batch, const float* y, uint64_t ldy,
+                                uint32_t* out, hipStream_t s);
+
+// Device layout byte count of a rows x cols matrix (equal to the GGUF size).
+uint64_t device_bytes(uint32_t dtype, uint64_t rows, uint64_t cols);
+
+}  // namespace rlq

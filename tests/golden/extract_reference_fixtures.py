@@ -1,0 +1,128 @@
+#!/usr/bin/env python3
+"""Copy the reference's golden records for Q8_0 / Q4_K / Q6_K / Q8_K into tests/golden/.
+
+Run once, in a container where the reference checkout is mounted:
+
+    python tests/golden/extract_reference_fixtures.py [/root/reference]
+
+The reference's quant crate pins its scalar path with little-endian binary
+fixtures produced from the original ggml C code (crates/quant/README.md:45-57).
+This script reads those DATA files only (never code) and keeps the records whose
+dtype is on the quantized-matvec path: 8 (Q8_0), 12 (Q4_K), 14 (Q6_K) and
+15 (Q8_K).  Each output file keeps the source's record layout and magic, with
+the record count rewritten, so a reader of the original format reads it too.
+`manifest.json` records, per output, the source file, its SHA-256, the source
+record indices kept and the SHA-256 of the output.
+
+Record layouts (all integers u32 LE, floats f32 LE), as read by the reference's
+tests:
+  GGQX  crates/quant/tests/matvec_extended.rs:50-86
+        dtype rows cols wsize asize | w[wsize] x[cols] act[asize] generic[rows] native[rows]
+  GGQM  crates/quant/tests/matvec.rs:26-47
+        dtype rows cols size | w[size] x[cols] generic[rows] native[rows]
+  GGQ8  crates/quant/tests/matvec_extended.rs:109-123
+        elements bytes | x[elements] q8k[bytes]
+  GGQE  crates/quant/tests/reference.rs:56-75, encoders_extended.rs:27-44
+        dtype n size | x[n] expected[size]
+  GGQD  crates/quant/tests/reference.rs:20-38
+        dtype n size | bytes[size] expected[n]
+"""
+import hashlib
+import json
+import os
+import struct
+import sys
+
+KEEP = {8, 12, 14, 15}
+SRC_DIR = "crates/quant/tests/fixtures"
+
+
+class Reader:
+    def __init__(self, data):
+        self.data = data
+        self.pos = 0
+
+    def take(self, n):
+        out = self.data[self.pos:self.pos + n]
+        if len(out) != n:
+            raise ValueError("truncated fixture")
+        self.pos += n
+        return out
+
+    def word(self):
+        return struct.unpack("<I", self.take(4))[0]
+
+
+def split_records(kind, data):
+    """Yield (dtype, raw_record_bytes) for every record of a fixture file."""
+    r = Reader(data)
+    magic = r.take(8)
+    count = r.word()
+    records = []
+    for _ in range(count):
+        start = r.pos
+        if kind == "GGQX":
+            dtype, rows, cols, wsize, asize = (r.word() for _ in range(5))
+            r.take(wsize + cols * 4 + asize + rows * 8)
+        elif kind == "GGQM":
+            dtype, rows, cols, size = (r.word() for _ in range(4))
+            r.take(size + cols * 4 + rows * 8)
+        elif kind == "GGQ8":
+            dtype = 15
+            elements, size = r.word(), r.word()
+            r.take(elements * 4 + size)
+        elif kind == "GGQE":
+            dtype, n, size = (r.word() for _ in range(3))
+            r.take(n * 4 + size)
+        elif kind == "GGQD":
+            dtype, n, size = (r.word() for _ in range(3))
+            r.take(size + n * 4)
+        else:
+            raise ValueError(kind)
+        records.append((dtype, data[start:r.pos]))
+    if r.pos != len(data):
+        raise ValueError("trailing bytes in fixture")
+    return magic, records
+
+
+FILES = [
+    ("matvec-extended-reference.bin", "GGQX", "matvec-extended-q4k-q6k.bin"),
+    ("matvec-reference.bin", "GGQM", "matvec-q8_0.bin"),
+    ("q8k-reference.bin", "GGQ8", "q8k.bin"),
+    ("quant-reference.bin", "GGQE", "quant-q8_0-q4k-q6k-q8k.bin"),
+    ("encoder-extended-reference.bin", "GGQE", "encoder-extended-q8_0-q4k-q6k.bin"),
+    ("dequant-reference.bin", "GGQD", "dequant-q8_0-q4k-q6k-q8k.bin"),
+]
+
+
+def main():
+    root = sys.argv[1] if len(sys.argv) > 1 else "/root/reference"
+    here = os.path.dirname(os.path.abspath(__file__))
+    manifest = {"source_root": "rust-llama " + SRC_DIR, "kept_dtypes": sorted(KEEP), "files": {}}
+    for src, kind, dst in FILES:
+        data = open(os.path.join(root, SRC_DIR, src), "rb").read()
+        magic, records = split_records(kind, data)
+        kept = [(i, d, raw) for i, (d, raw) in enumerate(records) if d in KEEP]
+        out = magic + struct.pack("<I", len(kept)) + b"".join(raw for _, _, raw in kept)
+        with open(os.path.join(here, dst), "wb") as f:
+            f.write(out)
+        per_type = {}
+        for _, d, _ in kept:
+            per_type[str(d)] = per_type.get(str(d), 0) + 1
+        manifest["files"][dst] = {
+            "source": f"{SRC_DIR}/{src}",
+            "source_sha256": hashlib.sha256(data).hexdigest(),
+            "source_records": len(records),
+            "kept_source_indices": [i for i, _, _ in kept],
+            "kept_per_dtype": per_type,
+            "sha256": hashlib.sha256(out).hexdigest(),
+            "bytes": len(out),
+        }
+        print(f"{dst}: {len(kept)} of {len(records)} records, {len(out)} bytes, {per_type}")
+    with open(os.path.join(here, "manifest.json"), "w") as f:
+        json.dump(manifest, f, indent=1)
+        f.write("\n")
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,275 @@
+"""GPU parity: the HIP path (librlq.so through its C ABI) against the golden
+records and the CPU oracle.
+
+Bars:
+  - bytes the reference pins bit-exactly (quantizer and encoder outputs,
+    decoders) are compared bit-exactly;
+  - per-block integer dot sums are compared bit-exactly (rlq_block_sums);
+  - f32 outputs: relative L2 error <= 1e-5 against the oracle / golden C
+    output, plus a per-element bound of 2e-5 * (1 + |e|) where the reference's
+    own tests use that bound (matvec.rs:55).
+Every test prints its case before touching the GPU.
+"""
+import numpy as np
+import pytest
+
+import oracle as O
+from golden import fixtures as F
+from rlq_loader import load
+
+pytestmark = pytest.mark.gpu
+
+rlq = load()
+torch = rlq.torch
+DT = rlq.DType
+
+REL_L2 = 1e-5
+
+
+def say(*a):
+    print("[case]", *a, flush=True)
+
+
+def rel_l2(got, want):
+    got, want = np.asarray(got, np.float64), np.asarray(want, np.float64)
+    den = np.linalg.norm(want)
+    return np.linalg.norm(got - want) / (den if den > 0 else 1.0)
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    c = rlq.Context(0)
+    yield c
+    c.close()
+
+
+def randn(seed, n, scale=1.0):
+    return (np.random.default_rng(seed).standard_normal(n) * scale).astype(np.float32)
+
+
+# ------------------------------------------------------------ golden records
+
+def test_q8k_quantizer_golden_bitwise():
+    for i, (x, expected) in enumerate(F.q8k()):
+        say("q8k record", i, x.size)
+        assert np.array_equal(rlq.quantize(DT.Q8_K, x), expected), i
+    for i, r in enumerate(F.matvec_extended()):
+        say("GGQX activation", i)
+        assert np.array_equal(rlq.quantize(DT.Q8_K, r.x), r.activation), i
+
+
+def test_encoders_golden_bitwise():
+    for i, (t, x, expected) in enumerate(F.encoders()):
+        say("encoder record", i, t, x.size)
+        got = rlq.quantize(t, x)
+        assert np.array_equal(got, expected), (i, t, np.nonzero(got != expected)[0][:8])
+
+
+def test_decoders_golden_bitwise():
+    for t, n, b, expected in F.dequant():
+        say("decoder", t, n)
+        y = rlq.dequantize(t, b, n)
+        same = (y.view(np.uint32) == expected.view(np.uint32)) | (np.isnan(y) & np.isnan(expected))
+        assert same.all(), t
+
+
+def test_matvec_golden_q4k_q6k():
+    for i, r in enumerate(F.matvec_extended()):
+        say("GGQX matvec", i, r.dtype, r.rows, r.cols)
+        y = rlq.matvec(r.dtype, r.weights, r.rows, r.cols, r.x)
+        assert rel_l2(y, r.generic) <= REL_L2, i
+        assert np.all(np.abs(y - r.generic) <= 2e-5 * (1 + np.abs(r.generic))), i
+        stride = r.weights.size // r.rows
+        for row in range(r.rows):
+            d = rlq.dot_packed(r.dtype, r.weights[row * stride:(row + 1) * stride], r.activation, r.cols)
+            assert abs(d - r.generic[row]) <= 2e-5 * (1 + abs(r.generic[row])), (i, row)
+
+
+def test_matvec_golden_q8_0():
+    for i, r in enumerate(F.matvec_q8_0()):
+        say("GGQM matvec", i, r.rows, r.cols)
+        y = rlq.matvec(r.dtype, r.weights, r.rows, r.cols, r.x)
+        assert rel_l2(y, r.generic) <= REL_L2, i
+        assert np.all(np.abs(y - r.native) <= 2e-5 * (1 + np.abs(r.native))), i
+
+
+# ------------------------------------------------------------ exact integer parts
+
+def _weights(t, rows, cols, seed):
+    return rlq.quantize(t, randn(seed, rows * cols, 0.02))
+
+
+@pytest.mark.parametrize("t,rows,cols", [(DT.Q4_K, 300, 4096), (DT.Q6_K, 300, 4096), (DT.Q8_0, 300, 896),
+                                         (DT.Q4_K, 7, 768), (DT.Q6_K, 5, 2304)])
+def test_block_sums_bit_exact(ctx, t, rows, cols):
+    say("block sums", t, rows, cols)
+    w = _weights(t, rows, cols, 100 + rows)
+    x = randn(200 + rows, cols)
+    W = rlq.Weights(ctx, t, w, rows, cols)
+    isum, imin = ctx.block_sums(W, torch.from_numpy(x).cuda())
+    torch.cuda.synchronize()
+    at = O.matvec_activation_dtype(int(t))
+    act = O.quantize(at, x)
+    nb = cols // O.BLOCK[int(t)]
+    stride = w.size // rows
+    want_i = np.zeros((rows, nb), np.int32)
+    want_m = np.zeros((rows, nb), np.int32)
+    for r in range(rows):
+        want_i[r], want_m[r] = O.block_sums(int(t), w[r * stride:(r + 1) * stride], act, nb)
+    assert np.array_equal(isum.cpu().numpy(), want_i)
+    assert np.array_equal(imin.cpu().numpy(), want_m)
+
+
+def test_block_sums_golden_records(ctx):
+    for i, r in enumerate(F.matvec_extended()):
+        say("GGQX block sums", i)
+        W = rlq.Weights(ctx, r.dtype, r.weights, r.rows, r.cols)
+        isum, imin = ctx.block_sums(W, torch.from_numpy(r.x).cuda())
+        nb = r.cols // 256
+        stride = r.weights.size // r.rows
+        for row in range(r.rows):
+            wi, wm = O.block_sums(r.dtype, r.weights[row * stride:(row + 1) * stride], r.activation, nb)
+            assert np.array_equal(isum[row].cpu().numpy(), wi), (i, row)
+            assert np.array_equal(imin[row].cpu().numpy(), wm), (i, row)
+
+
+# ------------------------------------------------------------ batched device API
+
+@pytest.mark.parametrize("t,rows,cols", [(DT.Q4_K, 2000, 4096), (DT.Q6_K, 1500, 4096), (DT.Q8_0, 2000, 896),
+                                         (DT.Q4_K, 333, 14336)])
+@pytest.mark.parametrize("batch", [1, 2, 3, 4, 5, 8, 11])
+def test_matmul_batches_against_oracle(ctx, t, rows, cols, batch):
+    say("matmul", t, rows, cols, batch)
+    w = _weights(t, rows, cols, 7 + rows)
+    x = randn(11 + batch, batch * cols).reshape(batch, cols)
+    W = rlq.Weights(ctx, t, w, rows, cols)
+    y = ctx.matmul(W, torch.from_numpy(x).cuda())
+    ctx.sync()
+    want = O.matmul(int(t), w, rows, cols, x, threads=8)
+    got = y.cpu().numpy()
+    for b in range(batch):
+        assert rel_l2(got[b], want[b]) <= REL_L2, b
+
+
+# ------------------------------------------------------------ the benchmark shapes
+
+def test_q4k_14336x4096_encoder_and_matvec(ctx):
+    rows, cols = 14336, 4096
+    say("Q4_K full shape", rows, cols)
+    xw = randn(0x51A7E002, rows * cols, 0.02)
+    w = rlq.quantize(DT.Q4_K, xw)
+    stride = w.size // rows
+    for r in (0, 1, 5000, rows - 1):  # GPU encoder == oracle encoder, bit for bit
+        assert np.array_equal(w[r * stride:(r + 1) * stride], O.quantize(O.Q4_K, xw[r * cols:(r + 1) * cols])), r
+    W = rlq.Weights(ctx, DT.Q4_K, w, rows, cols)
+    for batch in (1, 4, 8):
+        x = randn(batch, batch * cols).reshape(batch, cols)
+        y = ctx.matmul(W, torch.from_numpy(x).cuda())
+        ctx.sync()
+        want = O.matmul(O.Q4_K, w, rows, cols, x, threads=16)
+        for b in range(batch):
+            assert rel_l2(y[b].cpu().numpy(), want[b]) <= REL_L2, (batch, b)
+
+
+def test_q6k_lm_head_128256x4096_argmax(ctx):
+    rows, cols = 128256, 4096
+    say("Q6_K lm_head", rows, cols)
+    xw = randn(0x51A7E004, rows * cols, 0.02)
+    w = rlq.quantize(DT.Q6_K, xw)
+    stride = w.size // rows
+    for r in (0, 77777, rows - 1):
+        assert np.array_equal(w[r * stride:(r + 1) * stride], O.quantize(O.Q6_K, xw[r * cols:(r + 1) * cols])), r
+    del xw
+    W = rlq.Weights(ctx, DT.Q6_K, w, rows, cols)
+    for batch in (1, 8):
+        x = randn(40 + batch, batch * cols).reshape(batch, cols)
+        y, am = ctx.matmul_argmax(W, torch.from_numpy(x).cuda())
+        ctx.sync()
+        got = y.cpu().numpy()
+        want = O.matmul(O.Q6_K, w, rows, cols, x, threads=16)
+        for b in range(batch):
+            assert rel_l2(got[b], want[b]) <= REL_L2, (batch, b)
+            i = int(am[b])
+            assert i == O.argmax(got[b]), b  # fused argmax == greedy choice on the same logits
+            assert want[b][i] >= want[b].max() - 1e-5 * abs(want[b].max()), b
+
+
+def test_q8_0_qwen_lm_head_151936x896(ctx):
+    rows, cols = 151936, 896
+    say("Q8_0 lm_head", rows, cols)
+    xw = randn(0x51A7E005, rows * cols, 0.02)
+    w = rlq.quantize(DT.Q8_0, xw)
+    assert np.array_equal(w[:952 * 3], O.quantize(O.Q8_0, xw[:896 * 3]))
+    W = rlq.Weights(ctx, DT.Q8_0, w, rows, cols)
+    x = randn(5, cols)
+    y, am = ctx.matmul_argmax(W, torch.from_numpy(x).cuda())
+    ctx.sync()
+    want = O.matvec(O.Q8_0, w, rows, cols, x, threads=16)
+    assert rel_l2(y[0].cpu().numpy(), want) <= REL_L2
+    assert int(am[0]) == O.argmax(y[0].cpu().numpy())
+
+
+# ------------------------------------------------------------ errors and edges
+
+def test_host_errors_leave_output_untouched():
+    say("host errors")
+    w = _weights(DT.Q4_K, 4, 512, 3)
+    x = np.ones(512, np.float32)
+    x[300] = np.inf
+    with pytest.raises(rlq.QuantError) as e:
+        rlq.matvec(DT.Q4_K, w, 4, 512, x)
+    assert (e.value.name, e.value.index) == ("NonFiniteInput", 300)
+    x = np.ones(512, np.float32)
+    x[256:] = np.frombuffer(np.uint32(1).tobytes(), np.float32)[0]
+    with pytest.raises(rlq.QuantError) as e:
+        rlq.matvec(DT.Q4_K, w, 4, 512, x)
+    assert (e.value.name, e.value.block) == ("UnrepresentableScale", 1)
+    out = np.full(584, 0xA5, np.uint8)
+    with pytest.raises(rlq.QuantError):
+        rlq.quantize_into(DT.Q8_K, x, out)
+    assert (out == 0xA5).all()
+    rlq.quantize_into(DT.Q8_K, np.full(512, -0.0, np.float32), out)
+    assert (out == 0).all()
+    x = np.ones(64, np.float32)
+    x[40] = np.nan
+    with pytest.raises(rlq.QuantError) as e:
+        rlq.quantize(DT.Q8_0, x)
+    assert (e.value.name, e.value.index) == ("NonFiniteInput", 40)
+    with pytest.raises(rlq.QuantError) as e:
+        rlq.quantize(DT.Q8_0, np.full(64, 3e38, np.float32))
+    assert (e.value.name, e.value.block) == ("UnrepresentableScale", 0)
+    xk = randn(9, 512)
+    xk[17] = np.nan
+    for t in (DT.Q4_K, DT.Q6_K):
+        with pytest.raises(rlq.QuantError) as e:
+            rlq.quantize(t, xk)
+        assert (e.value.name, e.value.index) == ("NonFiniteInput", 17)
+
+
+def test_device_errors_suppress_outputs_and_report_first_column(ctx):
+    say("device errors")
+    rows, cols = 64, 512
+    W = rlq.Weights(ctx, DT.Q4_K, _weights(DT.Q4_K, rows, cols, 4), rows, cols)
+    x = torch.ones((3, cols), dtype=torch.float32, device="cuda")
+    x[2, 7] = float("nan")
+    x[1, 256:] = 1e-45  # unrepresentable scale in column 1, block 1
+    y = torch.full((3, rows), 123.0, device="cuda")
+    ctx.matmul(W, x, y)
+    with pytest.raises(rlq.QuantError) as e:
+        ctx.sync()
+    assert (e.value.name, e.value.block, e.value.b) == ("UnrepresentableScale", 1, 1)
+    assert bool((y == 123.0).all())
+    ctx.sync()  # the error word was cleared
+    x = torch.zeros((2, cols), dtype=torch.float32, device="cuda")
+    ctx.matmul(W, x, y[:2])
+    ctx.sync()
+    assert bool((y[:2] == 0).all())
+
+
+def test_zero_weights_give_zero(ctx):
+    say("zero weights")
+    for t, cols in ((DT.Q4_K, 1024), (DT.Q6_K, 1024), (DT.Q8_0, 96)):
+        W = rlq.Weights(ctx, t, np.zeros(rlq.row_bytes(t, cols) * 9, np.uint8), 9, cols)
+        y = ctx.matmul(W, torch.from_numpy(randn(1, 2 * cols).reshape(2, cols)).cuda())
+        ctx.sync()
+        assert bool((y == 0).all())
