@@ -20,7 +20,7 @@
  *     pointers, run on the GPU of the process-wide default context and return
  *     when the result is in the caller's buffer (the reference is synchronous).
  *   - Device functions take device pointers and enqueue on `stream` (a
- *     hipStream_t passed as void*; NULL = the context's own stream).  Shape
+ *     hipStream_t passed as void*; NULL = the HIP null stream, as in HIP).  Shape
  *     and length errors are returned at once; data errors found on the GPU
  *     (non-finite input, unrepresentable scale) suppress the outputs of the
  *     failing call and are reported by the next rlq_sync().
@@ -113,20 +113,25 @@ int32_t rlq_matvec(uint32_t weights_type, const uint8_t *weights, uint64_t weigh
 
 /* ---- device API -------------------------------------------------------- */
 
-/* One context per device; it owns a stream, scratch memory and the device
- * error word.  device = -1 takes the current HIP device. */
+/* One context per device; it owns a stream for the host drop-ins, scratch
+ * memory and the device error word.  device = -1 takes the current HIP
+ * device.  Device calls on one context share its scratch: queue them on one
+ * stream (or order them) so that they do not overlap. */
 int32_t rlq_context_create(int32_t device, rlq_context **out, rlq_error *err);
 void rlq_context_destroy(rlq_context *ctx);
-/* The hipStream_t the context uses when a call passes stream = NULL. */
+/* The context's own (non-blocking) hipStream_t, which the host drop-ins use. */
 void *rlq_context_stream(rlq_context *ctx);
 
 /* Matrix::from_quantized (crates/model-runtime/src/math.rs:35-70): checks the
  * dtype capability, shape and byte length, then keeps a device copy of the
  * weights in the kernels' layout (Q4_K as stored; Q6_K and Q8_0 split into
  * 16-byte-aligned planes).  `bytes_on_device` != 0 when `bytes` is a device
- * pointer.  Returns after the copy is complete. */
+ * pointer; the device is then synchronized first, so work that produced the
+ * bytes on any stream is complete.  Returns after the copy is complete. */
 int32_t rlq_weights_create(rlq_context *ctx, uint32_t dtype, const void *bytes, uint64_t len, uint64_t rows,
                            uint64_t cols, int32_t bytes_on_device, rlq_weights **out, rlq_error *err);
+/* Frees the device copy; it does not use the creating context, so weights may
+ * be destroyed after their context. */
 void rlq_weights_destroy(rlq_weights *w);
 /* rows, cols, dtype of a weights handle (any output pointer may be null). */
 void rlq_weights_shape(const rlq_weights *w, uint64_t *rows, uint64_t *cols, uint32_t *dtype);
@@ -153,7 +158,7 @@ int32_t rlq_matmul_argmax(rlq_context *ctx, const rlq_weights *w, const float *x
 int32_t rlq_quantize_device(rlq_context *ctx, uint32_t dtype, const float *x, uint64_t cols, uint64_t batch,
                             uint8_t *out, void *stream, rlq_error *err);
 
-/* Wait for `stream` (NULL = the context's), then report and clear the first
+/* Wait for `stream` (NULL = the null stream), then report and clear the first
  * data error the GPU recorded since the previous rlq_sync. */
 int32_t rlq_sync(rlq_context *ctx, void *stream, rlq_error *err);
 

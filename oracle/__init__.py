@@ -64,6 +64,7 @@ def _load():
     lib.oracle_block_sums.argtypes = [U32, P, P, U64, P, P]
     lib.oracle_block_sums.restype = None
     lib.oracle_argmax.argtypes, lib.oracle_argmax.restype = [P, U64], U64
+    lib.oracle_abs_terms.argtypes, lib.oracle_abs_terms.restype = [U32, P, P, U64], ctypes.c_double
     for f in ("oracle_row_bytes", "oracle_matvec_activation_dtype", "oracle_quantize_into",
               "oracle_dequantize_into", "oracle_dot_packed", "oracle_matvec", "oracle_matmul"):
         getattr(lib, f).restype = ctypes.c_int
@@ -169,6 +170,25 @@ def block_sums(dtype, w_row, act_row, nblocks):
     imin = np.zeros(nblocks, dtype=np.int32)
     lib().oracle_block_sums(dtype, _ptr(w_row), _ptr(act_row), nblocks, _ptr(isum), _ptr(imin))
     return isum, imin
+
+
+def abs_terms(dtype, w_row, act_row, nblocks):
+    """Sum of |term| over every f32 term of one row's dot (tolerance helper)."""
+    w_row = np.ascontiguousarray(w_row, dtype=np.uint8)
+    act_row = np.ascontiguousarray(act_row, dtype=np.uint8)
+    return float(lib().oracle_abs_terms(dtype, _ptr(w_row), _ptr(act_row), nblocks))
+
+
+def order_tolerance(dtype, w, rows, act, nblocks):
+    """Per-row bound on the difference between two f32 summation orders of
+    the same dot: 2 * (n + 8) * 2^-24 * abs_terms, where n = nblocks * 2 + 16
+    bounds the additions any one term passes through in either order (the
+    reference's eight serial lanes, a blocked GPU partial sum and its
+    reduction tree) and 8 covers the rounding of each term itself."""
+    stride = w.size // rows
+    n = 2 * nblocks + 16
+    return np.array([2.0 * (n + 8) * 2.0 ** -24 * abs_terms(dtype, w[r * stride:(r + 1) * stride], act, nblocks)
+                     for r in range(rows)])
 
 
 def argmax(x):

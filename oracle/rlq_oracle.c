@@ -777,6 +777,49 @@ void oracle_block_sums(uint32_t t, const uint8_t *w, const uint8_t *a, uint64_t 
     }
 }
 
+/* Tolerance helper, not a restatement: the sum of the absolute values of every
+ * f32 term one row's dot adds, in f64.  Q4_K: |d_w d_a| sum_j |sc q q8| +
+ * |dmin_w d_a| sum_s min_s |bsum[2s]+bsum[2s+1]|; Q6_K: |d_w d_a| sum_j
+ * |sc (q6-32) q8|; Q8_0: |dx dy| sum_j |xq yq|.  Any partition of these
+ * products into f32 partial sums has absolute terms bounded by this value. */
+double oracle_abs_terms(uint32_t t, const uint8_t *w, const uint8_t *a, uint64_t nb) {
+    double total = 0.0;
+    for (uint64_t b = 0; b < nb; ++b) {
+        if (t == T_Q8_0) {
+            const uint8_t *xb = w + b * 34, *yb = a + b * 34;
+            double s = 0.0;
+            for (int j = 0; j < 32; ++j) s += fabs((double)((int8_t)xb[2 + j] * (int8_t)yb[2 + j]));
+            total += fabs((double)half_at(xb, 0) * (double)half_at(yb, 0)) * s;
+        } else if (t == T_Q4_K) {
+            const uint8_t *xb = w + b * 144, *yb = a + b * 292;
+            double s = 0.0, m = 0.0;
+            for (int sub = 0; sub < 8; ++sub) {
+                int32_t scale, mn;
+                scale_min_k(xb + 4, sub, &scale, &mn);
+                m += (double)mn * fabs((double)(bsum_at(yb, 2 * sub) + bsum_at(yb, 2 * sub + 1)));
+                for (int l = 0; l < 32; ++l) {
+                    int32_t q = (xb[16 + sub / 2 * 32 + l] >> (4 * (sub % 2))) & 15;
+                    s += fabs((double)(scale * q * q8k_at(yb, sub * 32 + l)));
+                }
+            }
+            const double da = fabs((double)f32le(yb, 0));
+            total += fabs((double)half_at(xb, 0)) * da * s + fabs((double)half_at(xb, 2)) * da * m;
+        } else {
+            const uint8_t *xb = w + b * 210, *yb = a + b * 292;
+            double s = 0.0;
+            for (int j = 0; j < 256; ++j) {
+                int group = j / 128, side = (j % 128) / 32, pos = j % 32;
+                int32_t low = (xb[group * 64 + (side % 2) * 32 + pos] >> (4 * (side / 2))) & 15;
+                int32_t high = (xb[128 + group * 32 + pos] >> (2 * side)) & 3;
+                int32_t q = (low | (high << 4)) - 32;
+                s += fabs((double)((int8_t)xb[192 + j / 16] * q * q8k_at(yb, j)));
+            }
+            total += fabs((double)half_at(xb, 208) * (double)f32le(yb, 0)) * s;
+        }
+    }
+    return total;
+}
+
 int oracle_dot_packed(uint32_t t, const uint8_t *w, uint64_t w_len, const uint8_t *act,
                       uint64_t act_len, uint64_t elements, float *out, oracle_error *err) {
     uint32_t at;

@@ -105,6 +105,13 @@ int oracle_matmul(uint32_t wtype, const uint8_t *w, uint64_t w_len, uint64_t row
 void oracle_block_sums(uint32_t wtype, const uint8_t *w_row, const uint8_t *act_row,
                        uint64_t nblocks, int32_t *isum, int32_t *imin);
 
+/* Tolerance helper (not a restatement): sum over the row's blocks of the
+ * absolute values of every integer product times its f32 scale, in f64.  It
+ * bounds the f32 rounding of any summation order of the same terms:
+ * |computed - exact| <= n * 2^-24 * abs_terms for n additions per term. */
+double oracle_abs_terms(uint32_t wtype, const uint8_t *w_row, const uint8_t *act_row,
+                        uint64_t nblocks);
+
 /* Greedy sampler, crates/llama-behavior/src/sampling.rs:607-613: index of the
  * first strict maximum (n >= 1). */
 uint64_t oracle_argmax(const float *x, uint64_t n);

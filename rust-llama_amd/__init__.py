@@ -19,6 +19,7 @@ importing this package fails if the library has not been built
 The device API (Context, Weights) keeps weights resident in HBM and takes
 torch tensors on the GPU; torch supplies device memory and streams only.
 """
+import atexit
 import ctypes
 import enum
 import os
@@ -154,6 +155,19 @@ def _load():
 
 _lib = _load()
 
+# Handles still alive when the interpreter exits are left to the process
+# teardown: HIP calls from finalizers after torch has shut its runtime down are
+# not safe.
+_exiting = False
+
+
+def _at_exit():
+    global _exiting
+    _exiting = True
+
+
+atexit.register(_at_exit)
+
 
 def lib():
     return _lib
@@ -274,7 +288,8 @@ class Context:
 
     def close(self):
         if getattr(self, "_h", None):
-            _lib.rlq_context_destroy(self._h)
+            if not _exiting:
+                _lib.rlq_context_destroy(self._h)
             self._h = None
 
     __del__ = close
@@ -349,7 +364,8 @@ class Weights:
 
     def close(self):
         if getattr(self, "_h", None):
-            _lib.rlq_weights_destroy(self._h)
+            if not _exiting:
+                _lib.rlq_weights_destroy(self._h)
             self._h = None
 
     __del__ = close

@@ -143,7 +143,7 @@ struct rlq_context {
 };
 
 struct rlq_weights {
-    rlq_context* ctx;
+    int device;  // the creating context's device; the handle may outlive that context
     uint32_t dtype;
     uint64_t rows, cols;
     uint8_t* dev;
@@ -181,7 +181,11 @@ struct DeviceGuard {
     }
 };
 
-hipStream_t pick(rlq_context* ctx, void* stream) { return stream ? (hipStream_t)stream : ctx->stream; }
+// Device calls run on the caller's stream; NULL is HIP's null stream.
+hipStream_t pick(rlq_context* ctx, void* stream) {
+    (void)ctx;
+    return (hipStream_t)stream;
+}
 
 // Decode an error key (see rlq_device.hpp) into an rlq_error.
 int32_t key_to_error(unsigned long long key, uint32_t dtype, rlq_error* err) {
@@ -232,6 +236,14 @@ hipError_t upload_weights(rlq_context* ctx, uint32_t t, const void* bytes, uint6
     hipError_t e = hipMalloc((void**)dev, len ? len : 1);
     if (e != hipSuccess) return e;
     const uint8_t* src = (const uint8_t*)bytes;
+    if (on_device) {  // the bytes may still be in flight on another stream
+        e = hipDeviceSynchronize();
+        if (e != hipSuccess) {
+            (void)hipFree(*dev);
+            *dev = nullptr;
+            return e;
+        }
+    }
     if (t == kQ4_K) {
         e = hipMemcpyAsync(*dev, src, len, on_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice, s);
     } else {
@@ -354,7 +366,7 @@ int32_t rlq_weights_create(rlq_context* ctx, uint32_t dtype, const void* bytes, 
     if (len != expected) return fail(err, RLQ_INVALID_LENGTH, dtype, expected, len);
     if (!bytes) return fail(err, RLQ_INVALID_ARGUMENT, dtype);
     DeviceGuard g(ctx->device);
-    rlq_weights* w = new (std::nothrow) rlq_weights{ctx, dtype, rows, cols, nullptr, len};
+    rlq_weights* w = new (std::nothrow) rlq_weights{ctx->device, dtype, rows, cols, nullptr, len};
     if (!w) return fail(err, RLQ_ALLOCATION_FAILED);
     const hipError_t e = upload_weights(ctx, dtype, bytes, len, rows, cols, bytes_on_device != 0, &w->dev, ctx->stream);
     if (e != hipSuccess) {
@@ -367,8 +379,8 @@ int32_t rlq_weights_create(rlq_context* ctx, uint32_t dtype, const void* bytes, 
 
 void rlq_weights_destroy(rlq_weights* w) {
     if (!w) return;
-    DeviceGuard g(w->ctx->device);
-    (void)hipStreamSynchronize(w->ctx->stream);
+    DeviceGuard g(w->device);
+    // hipFree waits for every queued use of the buffer on the device.
     if (w->dev) (void)hipFree(w->dev);
     delete w;
 }

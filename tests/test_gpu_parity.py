@@ -36,6 +36,15 @@ def rel_l2(got, want):
     return np.linalg.norm(got - want) / (den if den > 0 else 1.0)
 
 
+def elem_tol(t, w, rows, act, cols, want):
+    """Per-element bound: the reference tests' 2e-5 * (1 + |e|) (matvec.rs:55)
+    widened by the f32 summation-order bound of each row (the GPU adds the
+    same exact integer block sums in another order; records built for
+    cancellation need the latter)."""
+    nb = cols // O.BLOCK[int(t)]
+    return 2e-5 * (1 + np.abs(np.asarray(want, np.float64))) + O.order_tolerance(int(t), w, rows, act, nb)
+
+
 @pytest.fixture(scope="module")
 def ctx():
     c = rlq.Context(0)
@@ -78,11 +87,12 @@ def test_matvec_golden_q4k_q6k():
         say("GGQX matvec", i, r.dtype, r.rows, r.cols)
         y = rlq.matvec(r.dtype, r.weights, r.rows, r.cols, r.x)
         assert rel_l2(y, r.generic) <= REL_L2, i
-        assert np.all(np.abs(y - r.generic) <= 2e-5 * (1 + np.abs(r.generic))), i
+        tol = elem_tol(r.dtype, r.weights, r.rows, r.activation, r.cols, r.generic)
+        assert np.all(np.abs(y - r.generic) <= tol), (i, np.abs(y - r.generic) - tol)
         stride = r.weights.size // r.rows
         for row in range(r.rows):
             d = rlq.dot_packed(r.dtype, r.weights[row * stride:(row + 1) * stride], r.activation, r.cols)
-            assert abs(d - r.generic[row]) <= 2e-5 * (1 + abs(r.generic[row])), (i, row)
+            assert abs(d - r.generic[row]) <= tol[row], (i, row)
 
 
 def test_matvec_golden_q8_0():
@@ -90,7 +100,8 @@ def test_matvec_golden_q8_0():
         say("GGQM matvec", i, r.rows, r.cols)
         y = rlq.matvec(r.dtype, r.weights, r.rows, r.cols, r.x)
         assert rel_l2(y, r.generic) <= REL_L2, i
-        assert np.all(np.abs(y - r.native) <= 2e-5 * (1 + np.abs(r.native))), i
+        tol = elem_tol(r.dtype, r.weights, r.rows, O.quantize(O.Q8_0, r.x), r.cols, r.native)
+        assert np.all(np.abs(y - r.native) <= tol), i
 
 
 # ------------------------------------------------------------ exact integer parts
@@ -273,3 +284,30 @@ def test_zero_weights_give_zero(ctx):
         y = ctx.matmul(W, torch.from_numpy(randn(1, 2 * cols).reshape(2, cols)).cuda())
         ctx.sync()
         assert bool((y == 0).all())
+
+
+# ------------------------------------------------------------ streams and lifetimes
+
+@pytest.mark.parametrize("t", [DT.Q4_K, DT.Q6_K, DT.Q8_0, DT.Q8_K])
+def test_device_quantize_is_ordered_after_torch_producer(ctx, t):
+    """Calls with stream=None run on torch's current stream, so a quantize
+    queued right after the kernel that writes its input sees the final
+    values (no host synchronisation in between)."""
+    rows, cols = 2048, 4096
+    say("ordered quantize", t, rows, cols)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(77)
+    xw = torch.randn((rows, cols), generator=g, device="cuda", dtype=torch.float32) * 0.02
+    packed = ctx.quantize(t, xw)
+    ctx.sync()
+    host_x = xw.cpu().numpy().reshape(-1)
+    want = O.quantize(int(t), host_x)
+    assert np.array_equal(packed.cpu().numpy(), want)
+
+
+def test_weights_outlive_their_context():
+    say("weights after context")
+    c = rlq.Context(0)
+    W = rlq.Weights(c, DT.Q4_K, _weights(DT.Q4_K, 8, 256, 5), 8, 256)
+    c.close()
+    W.close()

@@ -400,3 +400,63 @@ def test_q8k_records_catch_wrong_rounding_and_tie_break():
             q2 = np.minimum(np.rint((inv2 * xb).astype(np.float32)), 127).astype(np.int8)
             diff_tie += not np.array_equal(q2.view(np.uint8), e[4:260])
     assert diff_round > 0 and diff_tie > 0
+
+
+# ---------------------------------------------------------------- order tolerance
+
+def _exact_f64(t, w_row, act, nb):
+    """The dot with exact integer block sums and f32 block scales, summed in
+    f64 (no f32 rounding after the scales)."""
+    isum, imin = O.block_sums(t, w_row, act, nb)
+    ws, as_ = w_row.reshape(nb, -1), act.reshape(nb, -1)
+    tot = 0.0
+    for k in range(nb):
+        if t == O.Q8_0:
+            d = np.float32(np.float32(ws[k, :2].view(np.float16)[0]) * np.float32(as_[k, :2].view(np.float16)[0]))
+            tot += float(d) * int(isum[k])
+        else:
+            ya = np.float32(as_[k, :4].view(np.float32)[0])
+            off = 0 if t == O.Q4_K else 208
+            d = np.float32(np.float32(ws[k, off:off + 2].view(np.float16)[0]) * ya)
+            dm = np.float32(np.float32(ws[k, 2:4].view(np.float16)[0]) * ya) if t == O.Q4_K else np.float32(0)
+            tot += float(d) * int(isum[k]) - float(dm) * int(imin[k])
+    return tot
+
+
+def test_order_tolerance_bounds_the_reference_rounding():
+    """The reference's own f32 result (golden generic C output) lies within
+    half of order_tolerance of the exact value, for every golden row,
+    including the records built for cancellation; and the bound is never
+    below the exact magnitude's rounding."""
+    for r in F.matvec_extended():
+        nb = r.cols // 256
+        tol = O.order_tolerance(r.dtype, r.weights, r.rows, r.activation, nb)
+        stride = r.weights.size // r.rows
+        for row in range(r.rows):
+            exact = _exact_f64(r.dtype, r.weights[row * stride:(row + 1) * stride], r.activation, nb)
+            assert abs(float(r.generic[row]) - exact) <= tol[row] / 2, (r.dtype, r.cols, row)
+            assert tol[row] >= 2 * 2.0 ** -24 * abs(exact)
+    for r in F.matvec_q8_0():
+        nb = r.cols // 32
+        act = O.quantize(O.Q8_0, r.x)
+        tol = O.order_tolerance(r.dtype, r.weights, r.rows, act, nb)
+        stride = r.weights.size // r.rows
+        for row in range(r.rows):
+            exact = _exact_f64(r.dtype, r.weights[row * stride:(row + 1) * stride], act, nb)
+            assert abs(float(r.generic[row]) - exact) <= tol[row] / 2, (r.cols, row)
+
+
+def test_order_tolerance_rejects_a_dropped_block():
+    """Dropping one block's term moves a random row's dot far outside the
+    order tolerance: the bound is tight enough to catch a lost block."""
+    rng = np.random.default_rng(31)
+    for t in (O.Q4_K, O.Q6_K, O.Q8_0):
+        nb = 16 if t != O.Q8_0 else 28
+        n = nb * O.BLOCK[t]
+        w = O.quantize(t, (rng.standard_normal(n) * 0.02).astype(np.float32))
+        act = O.quantize(O.matvec_activation_dtype(t), rng.standard_normal(n).astype(np.float32))
+        full = _exact_f64(t, w, act, nb)
+        bs = O.row_bytes(t, O.BLOCK[t])
+        dropped = _exact_f64(t, w[:-bs], act[:-O.row_bytes(O.matvec_activation_dtype(t), O.BLOCK[t])], nb - 1)
+        tol = O.order_tolerance(t, w, 1, act, nb)[0]
+        assert abs(full - dropped) > 20 * tol, t
