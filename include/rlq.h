@@ -140,7 +140,8 @@ void rlq_weights_shape(const rlq_weights *w, uint64_t *rows, uint64_t *cols, uin
  * side, and Matrix::multiply for batch = 1: each of the `batch` input rows
  * x[b*cols ..] is quantized to the weights' activation type on the GPU, then
  * y[b*rows + r] = dot_packed(weights row r, activation b).  x and y are
- * device pointers. */
+ * device pointers (x 16-byte aligned).  Up to 8 columns share one pass over
+ * the weights. */
 int32_t rlq_matmul(rlq_context *ctx, const rlq_weights *w, const float *x, uint64_t batch, float *y,
                    void *stream, rlq_error *err);
 
@@ -162,14 +163,16 @@ int32_t rlq_quantize_device(rlq_context *ctx, uint32_t dtype, const float *x, ui
  * data error the GPU recorded since the previous rlq_sync. */
 int32_t rlq_sync(rlq_context *ctx, void *stream, rlq_error *err);
 
-/* Exact integer part of every (row, block) dot of the weights against one
- * activation row x (device f32, cols values), quantized on the GPU as
- * rlq_matmul does: isum[r*nb + k] and imin[r*nb + k] for block k, as the
- * integers of crates/quant/src/matvec_extra.rs:252-283 (the eight lanes
- * added; imin is the Q4_K mins sum, 0 otherwise) and matvec.rs:124-127.
- * isum and imin are device pointers of rows*nb i32. */
-int32_t rlq_block_sums(rlq_context *ctx, const rlq_weights *w, const float *x, int32_t *isum, int32_t *imin,
-                       void *stream, rlq_error *err);
+/* Exact integer part of every (row, block) dot of the weights against
+ * activation column 0 of x (device f32, `batch` columns of cols values, 1 <=
+ * batch <= 8), computed inside the kernel rlq_matmul runs for that batch size
+ * (the columns are quantized on the GPU as rlq_matmul does):
+ * isum[r*nb + k] and imin[r*nb + k] for block k are the integers of
+ * crates/quant/src/matvec_extra.rs:252-283 (the eight lanes added; imin is
+ * the Q4_K mins sum, 0 otherwise) and matvec.rs:124-127.  isum and imin are
+ * device pointers of rows*nb i32. */
+int32_t rlq_block_sums(rlq_context *ctx, const rlq_weights *w, const float *x, uint64_t batch, int32_t *isum,
+                       int32_t *imin, void *stream, rlq_error *err);
 
 #ifdef __cplusplus
 }

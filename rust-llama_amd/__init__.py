@@ -139,7 +139,7 @@ SIGNATURES = {
     "rlq_matmul_argmax": ([_P, _P, _P, _U64, _P, _P, _P, _E], _I32),
     "rlq_quantize_device": ([_P, _U32, _P, _U64, _U64, _P, _P, _E], _I32),
     "rlq_sync": ([_P, _P, _E], _I32),
-    "rlq_block_sums": ([_P, _P, _P, _P, _P, _P, _E], _I32),
+    "rlq_block_sums": ([_P, _P, _P, _U64, _P, _P, _P, _E], _I32),
 }
 
 
@@ -334,12 +334,15 @@ class Context:
         _check(_lib.rlq_sync(self._h, _stream_ptr(stream), ctypes.byref(err)), err)
 
     def block_sums(self, w, x, stream=None):
-        """Exact per-(row, block) integer sums of w against x (one column)."""
+        """Exact per-(row, block) integer sums of w against column 0 of x
+        ([batch, cols] or [cols], batch <= 8), from the kernel that matmul
+        uses for that batch size."""
+        x2 = x.reshape(-1, w.cols)
         nb = w.cols // (32 if w.dtype == DType.Q8_0 else 256)
         isum = torch.empty((w.rows, nb), dtype=torch.int32, device=x.device)
         imin = torch.empty((w.rows, nb), dtype=torch.int32, device=x.device)
         err = _Err()
-        _check(_lib.rlq_block_sums(self._h, w._h, _dev_ptr(x.reshape(-1), torch.float32),
+        _check(_lib.rlq_block_sums(self._h, w._h, _dev_ptr(x2, torch.float32), x2.shape[0],
                                    _dev_ptr(isum, torch.int32), _dev_ptr(imin, torch.int32),
                                    _stream_ptr(stream), ctypes.byref(err)), err)
         return isum, imin

@@ -11,6 +11,7 @@
 
 #include "rlq_device.hpp"
 #include "rlq_internal.hpp"
+#include "rlq_layout.hpp"
 
 using namespace rlq;
 
@@ -219,42 +220,26 @@ int32_t default_context(rlq_context** out, rlq_error* err) {
     return ok(err);
 }
 
-// Quantize `batch` activation rows into planes on `s`, errors into `slot`.
-hipError_t quantize_planes(rlq_context* ctx, uint32_t at, const float* x, uint64_t cols, uint64_t batch,
-                           ActPlanes* planes, int slot, hipStream_t s) {
-    hipError_t e = ensure(ctx, ctx->planes, act_planes_bytes(at, cols, batch));
-    if (e != hipSuccess) return e;
-    *planes = act_planes_carve(ctx->planes.p, at, cols, batch);
-    return at == kQ8_K ? launch_quantize_q8k(x, cols, batch, planes, nullptr, ctx->err_words + slot, s)
-                       : launch_quantize_q8_0(x, cols, batch, planes, nullptr, ctx->err_words + slot, s);
-}
-
 // Upload GGUF weights (host or device bytes) into a fresh device buffer in
-// the kernels' layout.
-hipError_t upload_weights(rlq_context* ctx, uint32_t t, const void* bytes, uint64_t len, uint64_t rows, uint64_t cols,
-                          bool on_device, uint8_t** dev, hipStream_t s) {
-    hipError_t e = hipMalloc((void**)dev, len ? len : 1);
+// the tiled layout (rlq_layout.hpp).  Host bytes go through a temporary
+// device copy that is freed before returning.
+hipError_t upload_weights(uint32_t t, const void* bytes, uint64_t len, uint64_t rows, uint64_t cols, bool on_device,
+                          uint8_t** dev, hipStream_t s) {
+    *dev = nullptr;
+    hipError_t e = hipMalloc((void**)dev, layout_bytes(t, rows, cols));
     if (e != hipSuccess) return e;
     const uint8_t* src = (const uint8_t*)bytes;
-    if (on_device) {  // the bytes may still be in flight on another stream
-        e = hipDeviceSynchronize();
-        if (e != hipSuccess) {
-            (void)hipFree(*dev);
-            *dev = nullptr;
-            return e;
-        }
-    }
-    if (t == kQ4_K) {
-        e = hipMemcpyAsync(*dev, src, len, on_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice, s);
+    void* tmp = nullptr;
+    if (on_device) {
+        e = hipDeviceSynchronize();  // the bytes may still be in flight on another stream
     } else {
-        if (!on_device) {
-            e = ensure(ctx, ctx->stage_w, len);
-            if (e == hipSuccess) e = hipMemcpyAsync(ctx->stage_w.p, src, len, hipMemcpyHostToDevice, s);
-            src = (const uint8_t*)ctx->stage_w.p;
-        }
-        if (e == hipSuccess) e = launch_repack(t, src, rows, cols, *dev, s);
+        e = hipMalloc(&tmp, len);
+        if (e == hipSuccess) e = hipMemcpyAsync(tmp, src, len, hipMemcpyHostToDevice, s);
+        src = (const uint8_t*)tmp;
     }
+    if (e == hipSuccess) e = launch_repack(t, src, rows, cols, *dev, s);
     if (e == hipSuccess) e = hipStreamSynchronize(s);
+    if (tmp) (void)hipFree(tmp);
     if (e != hipSuccess) {
         (void)hipFree(*dev);
         *dev = nullptr;
@@ -368,7 +353,7 @@ int32_t rlq_weights_create(rlq_context* ctx, uint32_t dtype, const void* bytes, 
     DeviceGuard g(ctx->device);
     rlq_weights* w = new (std::nothrow) rlq_weights{ctx->device, dtype, rows, cols, nullptr, len};
     if (!w) return fail(err, RLQ_ALLOCATION_FAILED);
-    const hipError_t e = upload_weights(ctx, dtype, bytes, len, rows, cols, bytes_on_device != 0, &w->dev, ctx->stream);
+    const hipError_t e = upload_weights(dtype, bytes, len, rows, cols, bytes_on_device != 0, &w->dev, ctx->stream);
     if (e != hipSuccess) {
         delete w;
         return e == hipErrorOutOfMemory ? fail(err, RLQ_ALLOCATION_FAILED, dtype) : hip_fail(err, e);
@@ -397,20 +382,18 @@ void rlq_weights_shape(const rlq_weights* w, uint64_t* rows, uint64_t* cols, uin
 static int32_t matmul_impl(rlq_context* ctx, const rlq_weights* w, const float* x, uint64_t batch, float* y,
                            uint32_t* argmax, void* stream, rlq_error* err) {
     if (!ctx || !w || !x || !y) return fail(err, RLQ_INVALID_ARGUMENT);
+    if (((uintptr_t)x & 15) || ((uintptr_t)y & 3)) return fail(err, RLQ_INVALID_ARGUMENT, w->dtype);
     if (batch == 0) return ok(err);
     DeviceGuard g(ctx->device);
     const hipStream_t s = pick(ctx, stream);
-    uint32_t at = 0;
-    (void)activation_dtype(w->dtype, &at, nullptr);
-    ActPlanes planes;
-    HIP_TRY(quantize_planes(ctx, at, x, w->cols, batch, &planes, 0, s));
     unsigned long long* keys = nullptr;
     if (argmax) {
         HIP_TRY(ensure(ctx, ctx->keys, batch * sizeof(unsigned long long)));
         keys = (unsigned long long*)ctx->keys.p;
         HIP_TRY(launch_fill_u64(keys, batch, 0ull, s));
     }
-    HIP_TRY(launch_matvec(w->dtype, w->dev, w->rows, w->cols, &planes, batch, y, w->rows, keys, s));
+    HIP_TRY(launch_matvec(w->dtype, w->dev, w->rows, w->cols, x, nullptr, batch, y, w->rows, keys, ctx->err_words, nullptr,
+                          nullptr, s));
     if (argmax) HIP_TRY(launch_argmax_finish(keys, batch, y, w->rows, argmax, s));
     return ok(err);
 }
@@ -458,16 +441,16 @@ int32_t rlq_sync(rlq_context* ctx, void* stream, rlq_error* err) {
     return take_error(ctx, 0, s, 0, err);
 }
 
-int32_t rlq_block_sums(rlq_context* ctx, const rlq_weights* w, const float* x, int32_t* isum, int32_t* imin,
-                       void* stream, rlq_error* err) {
+int32_t rlq_block_sums(rlq_context* ctx, const rlq_weights* w, const float* x, uint64_t batch, int32_t* isum,
+                       int32_t* imin, void* stream, rlq_error* err) {
     if (!ctx || !w || !x || !isum || !imin) return fail(err, RLQ_INVALID_ARGUMENT);
+    if ((uintptr_t)x & 15) return fail(err, RLQ_INVALID_ARGUMENT, w->dtype);
+    if (batch == 0 || batch > 8) return fail(err, RLQ_INVALID_ARGUMENT, w->dtype);
     DeviceGuard g(ctx->device);
     const hipStream_t s = pick(ctx, stream);
-    uint32_t at = 0;
-    (void)activation_dtype(w->dtype, &at, nullptr);
-    ActPlanes planes;
-    HIP_TRY(quantize_planes(ctx, at, x, w->cols, 1, &planes, 0, s));
-    HIP_TRY(launch_block_sums(w->dtype, w->dev, w->rows, w->cols, &planes, isum, imin, s));
+    HIP_TRY(ensure(ctx, ctx->stage_out, batch * w->rows * sizeof(float)));
+    HIP_TRY(launch_matvec(w->dtype, w->dev, w->rows, w->cols, x, nullptr, batch, (float*)ctx->stage_out.p, w->rows,
+                          nullptr, ctx->err_words, isum, imin, s));
     return ok(err);
 }
 
@@ -560,7 +543,7 @@ int32_t rlq_dot_packed(uint32_t wtype, const uint8_t* weights, uint64_t weights_
     DeviceGuard g(ctx->device);
     const hipStream_t s = ctx->stream;
     uint8_t* wd = nullptr;
-    hipError_t e = upload_weights(ctx, wtype, weights, weights_len, 1, elements, false, &wd, s);
+    hipError_t e = upload_weights(wtype, weights, weights_len, 1, elements, false, &wd, s);
     if (e != hipSuccess) return hip_fail(err, e);
     e = ensure(ctx, ctx->stage_in, activation_len);
     if (e == hipSuccess) e = ensure(ctx, ctx->planes, act_planes_bytes(at, elements, 1));
@@ -572,7 +555,8 @@ int32_t rlq_dot_packed(uint32_t wtype, const uint8_t* weights, uint64_t weights_
     }
     if (e == hipSuccess) e = launch_act_from_gguf(at, (const uint8_t*)ctx->stage_in.p, elements, 1, &planes, s);
     if (e == hipSuccess)
-        e = launch_matvec(wtype, wd, 1, elements, &planes, 1, (float*)ctx->stage_out.p, 1, nullptr, s);
+        e = launch_matvec(wtype, wd, 1, elements, nullptr, &planes, 1, (float*)ctx->stage_out.p, 1, nullptr,
+                          ctx->err_words + 1, nullptr, nullptr, s);
     if (e == hipSuccess) e = hipMemcpyAsync(out, ctx->stage_out.p, sizeof(float), hipMemcpyDeviceToHost, s);
     if (e == hipSuccess) e = hipStreamSynchronize(s);
     (void)hipFree(wd);
@@ -601,15 +585,14 @@ int32_t rlq_matvec(uint32_t wtype, const uint8_t* weights, uint64_t weights_len,
     DeviceGuard g(ctx->device);
     const hipStream_t s = ctx->stream;
     uint8_t* wd = nullptr;
-    hipError_t e = upload_weights(ctx, wtype, weights, weights_len, rows, cols, false, &wd, s);
+    hipError_t e = upload_weights(wtype, weights, weights_len, rows, cols, false, &wd, s);
     if (e != hipSuccess) return e == hipErrorOutOfMemory ? fail(err, RLQ_ALLOCATION_FAILED, wtype) : hip_fail(err, e);
-    ActPlanes planes{};
     e = ensure(ctx, ctx->stage_in, cols * sizeof(float));
     if (e == hipSuccess) e = ensure(ctx, ctx->stage_out, rows * sizeof(float));
     if (e == hipSuccess) e = hipMemcpyAsync(ctx->stage_in.p, input, cols * sizeof(float), hipMemcpyHostToDevice, s);
-    if (e == hipSuccess) e = quantize_planes(ctx, at, (const float*)ctx->stage_in.p, cols, 1, &planes, 1, s);
     if (e == hipSuccess)
-        e = launch_matvec(wtype, wd, rows, cols, &planes, 1, (float*)ctx->stage_out.p, rows, nullptr, s);
+        e = launch_matvec(wtype, wd, rows, cols, (const float*)ctx->stage_in.p, nullptr, 1, (float*)ctx->stage_out.p,
+                          rows, nullptr, ctx->err_words + 1, nullptr, nullptr, s);
     if (e != hipSuccess) {
         (void)hipFree(wd);
         return hip_fail(err, e);

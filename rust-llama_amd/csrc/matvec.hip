@@ -1,153 +1,87 @@
-// matvec.hip - HBM-bound decode matvec for Q4_K / Q6_K / Q8_0 weights on gfx950.
+// matvec.hip - decode matvec (batch 1..8) for Q4_K / Q6_K / Q8_0 weights on gfx950.
 //
 // Contract (paths relative to the rust-llama repository):
-//   y[b][r] = dot_packed(row r, activation column b)
+//   y[b][r] = dot_packed(row r, activation column b), the activation being
+//   column b of x quantized to Q8_K (Q4_K, Q6_K) or Q8_0 (Q8_0 weights)
 //     Q8_0  crates/quant/src/matvec.rs:115-160  (Q8_0 branch :124-128)
-//     Q4_K  crates/quant/src/matvec_extra.rs:252-271, 286-293
+//     Q4_K  crates/quant/src/matvec_extra.rs:212-271, 286-293
 //     Q6_K  crates/quant/src/matvec_extra.rs:272-283, 286-293
-// Integer products are exact (v_dot4_i32_i8); each lane scales its exact
-// integer partial by the block's f32 d, as the reference scales each of its
-// eight integer lanes (matvec_extra.rs:286-288).  The f32 summation order
-// differs from the reference's eight serial lanes; results agree to ~1e-7
-// relative.
+//   quantizers crates/quant/src/activation.rs:4-51 (Q8_K),
+//              crates/quant/src/encode.rs:115-126, 151-192 (Q8_0)
 //
-// Work mapping: a wave owns R consecutive rows.  Eight lanes own one weight
-// block (lane c = 0..7 holds one 16-byte slice of it), so one wave instruction
-// reads eight consecutive blocks (1152 B for Q4_K).  All weight loads of a
-// pass are issued before the activation is staged into LDS, so HBM latency
-// overlaps the staging.  Activations (all batch columns) live in LDS.
+// Design.  One kernel per weight format, for any batch of up to 8 columns.
+//  - Weights are read in the tiled device layout (rlq_layout.hpp): a wave owns
+//    16-row tiles and streams each tile's chunks with 16-byte loads issued D
+//    chunks ahead of use, so HBM reads overlap the arithmetic.
+//  - The prologue of every workgroup quantizes all batch columns of x into LDS
+//    (the fused activation quantizer), after the first weight loads are in
+//    flight.  A data error (non-finite input, unrepresentable scale) is
+//    reported to the error word and the workgroup writes nothing.
+//  - Integer products run on v_mfma_i32_16x16x64_i8 with the weights as the
+//    B operand (16 rows = 16 columns of the product) and the activations as
+//    the A operand.  The A rows are (batch column, sub-block) pairs and every
+//    A row is zero outside the K range of its sub-block, so each output is
+//    the exact integer dot of one sub-block for one column; the K-quant
+//    sub-block scales are applied to those integers on the VALU.  The MFMA
+//    work is the same for every batch size.
+//  - Lane l of a wave owns weight row n = l % 16 and output columns that
+//    depend on l / 16; every (row, column) sum lives in one lane, so no cross
+//    lane reduction is needed.
+//
+// F32 order.  Per (row, column) the lane adds one f32 term per block (Q8_0:
+// exactly the reference's `sum += isum as f32 * (dx * dy)` in block order, so
+// Q8_0 results equal the reference bit for bit).  Q4_K / Q6_K add
+// d * isum - dmin * imin per block from the exact block integers, where the
+// reference keeps eight lane accumulators; the difference is f32 rounding of
+// the same exact integers.
 #include "rlq_device.hpp"
 #include "rlq_internal.hpp"
+#include "rlq_layout.hpp"
 
 namespace rlq {
 
-constexpr int kWaves = 4;  // waves per workgroup
-constexpr int kThreads = kWaves * kWave;
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+typedef short i16x2 __attribute__((ext_vector_type(2)));
 
-// ---- Q4_K lane decode ----------------------------------------------------
-
-// 6-bit scale and min of sub-block j from the packed 12 bytes held as three
-// little-endian words (matvec_extra.rs:212-221).
-__device__ __forceinline__ void q4k_scale_min(uint32_t w1, uint32_t w2, uint32_t w3, int j, int32_t& sc,
-                                              int32_t& mn) {
-    if (j < 4) {
-        sc = (int32_t)__builtin_amdgcn_ubfe(w1, 8 * j, 6);
-        mn = (int32_t)__builtin_amdgcn_ubfe(w2, 8 * j, 6);
-    } else {
-        const int k = 8 * (j - 4);
-        sc = (int32_t)(__builtin_amdgcn_ubfe(w3, k, 4) | (__builtin_amdgcn_ubfe(w1, k + 6, 2) << 4));
-        mn = (int32_t)(__builtin_amdgcn_ubfe(w3, k + 4, 4) | (__builtin_amdgcn_ubfe(w2, k + 6, 2) << 4));
-    }
+__device__ __forceinline__ i32x4 mfma_i8(i32x4 a, i32x4 b) {
+    const i32x4 z = {0, 0, 0, 0};
+    return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, z, 0, 0, 0);
 }
 
-// Lane c of a Q4_K block holds qs bytes 16c..16c+15: group g = c/2, half h =
-// c%2.  Low nibbles are elements 64g + 16h + i (sub-block 2g), high nibbles
-// elements 64g + 32 + 16h + i (sub-block 2g+1), i = 0..15.
-struct Q4KLane {
-    uint32_t lo[4], hi[4];
-    int32_t sc_lo, sc_hi, mn;  // mn: min of the sub-block whose bsum this lane adds
-    float dw, dmw;
-};
-
-__device__ __forceinline__ Q4KLane q4k_lane(uint4 hdr, uint4 qs, int c) {
-    Q4KLane L;
-    const int g = c >> 1, h = c & 1;
-    int32_t mn_lo, mn_hi;
-    q4k_scale_min(hdr.y, hdr.z, hdr.w, 2 * g, L.sc_lo, mn_lo);
-    q4k_scale_min(hdr.y, hdr.z, hdr.w, 2 * g + 1, L.sc_hi, mn_hi);
-    L.mn = h ? mn_hi : mn_lo;
-    const uint32_t v[4] = {qs.x, qs.y, qs.z, qs.w};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        L.lo[i] = v[i] & 0x0f0f0f0fu;
-        L.hi[i] = (v[i] >> 4) & 0x0f0f0f0fu;
-    }
-    L.dw = half_to_float(hdr.x);
-    L.dmw = half_to_float(hdr.x >> 16);
-    return L;
+__device__ __forceinline__ i32x4 lo_nibbles(uint4 v) {
+    return i32x4{(int)(v.x & 0x0f0f0f0fu), (int)(v.y & 0x0f0f0f0fu), (int)(v.z & 0x0f0f0f0fu),
+                 (int)(v.w & 0x0f0f0f0fu)};
+}
+__device__ __forceinline__ i32x4 hi_nibbles(uint4 v) {
+    return i32x4{(int)((v.x >> 4) & 0x0f0f0f0fu), (int)((v.y >> 4) & 0x0f0f0f0fu), (int)((v.z >> 4) & 0x0f0f0f0fu),
+                 (int)((v.w >> 4) & 0x0f0f0f0fu)};
 }
 
-// Exact integer partials of one lane against one activation block:
-//   I = sc_lo * sum(lo . q8) + sc_hi * sum(hi . q8)
-//   M = min_s * (bsum[2s] + bsum[2s+1]) for s = 2g + h  (matvec_extra.rs:258)
-__device__ __forceinline__ void q4k_ints(const Q4KLane& L, const int8_t* a_blk, const int32_t* bs32_blk, int c,
-                                         int32_t& I, int32_t& M) {
-    const int g = c >> 1, h = c & 1;
-    const uint4 alo = *(const uint4*)(a_blk + 64 * g + 16 * h);
-    const uint4 ahi = *(const uint4*)(a_blk + 64 * g + 32 + 16 * h);
-    int32_t ilo = dot4(L.lo[0], alo.x, 0);
-    ilo = dot4(L.lo[1], alo.y, ilo);
-    ilo = dot4(L.lo[2], alo.z, ilo);
-    ilo = dot4(L.lo[3], alo.w, ilo);
-    int32_t ihi = dot4(L.hi[0], ahi.x, 0);
-    ihi = dot4(L.hi[1], ahi.y, ihi);
-    ihi = dot4(L.hi[2], ahi.z, ihi);
-    ihi = dot4(L.hi[3], ahi.w, ihi);
-    I = L.sc_lo * ilo + L.sc_hi * ihi;
-    M = L.mn * bs32_blk[2 * g + h];
+__device__ __forceinline__ int32_t dot2(uint32_t a, uint32_t b, int32_t c) {
+    return __builtin_amdgcn_sdot2(__builtin_bit_cast(i16x2, a), __builtin_bit_cast(i16x2, b), c, false);
 }
 
-// ---- Q6_K lane decode ----------------------------------------------------
+__device__ __forceinline__ uint32_t ubyte(uint32_t w, int k) { return __builtin_amdgcn_ubfe(w, 8 * k, 8); }
+__device__ __forceinline__ int32_t sbyte(uint32_t w, int k) { return __builtin_amdgcn_sbfe((int)w, 8 * k, 8); }
 
-// Lane c of a Q6_K block: g = c/4, s0 = (c/2)%2, p0 = 16(c%2).  It holds
-// ql bytes 16c..16c+15 and qh bytes 32g + p0 .. +15, i.e. the 6-bit values of
-// elements ja = 128g + 32 s0 + p0 + i (low nibble) and jb = ja + 64 (high
-// nibble), i = 0..15 (matvec_extra.rs:273-279).  Both 16-element runs sit
-// inside one scale group: sa = ja/16, sb = sa + 4.
-struct Q6KLane {
-    uint32_t qa[4], qb[4];  // unsigned 6-bit values, four per word
-    int32_t sca, scb;
-    float dw;
-};
+// ---- 16-lane row reductions (DPP; every lane of the row gets the result) ----
+constexpr int kRowMirror = 0x140;  // lane i <-> 15 - i within each 16 lanes
 
-__device__ __forceinline__ Q6KLane q6k_lane(uint4 ql, uint4 qh, uint4 sc, uint32_t d16, int c) {
-    Q6KLane L;
-    const int g = c >> 2, s0 = (c >> 1) & 1;
-    const uint32_t l[4] = {ql.x, ql.y, ql.z, ql.w}, hh[4] = {qh.x, qh.y, qh.z, qh.w};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        L.qa[i] = (l[i] & 0x0f0f0f0fu) | (((hh[i] >> (2 * s0)) & 0x03030303u) << 4);
-        L.qb[i] = ((l[i] >> 4) & 0x0f0f0f0fu) | (((hh[i] >> (2 * s0 + 4)) & 0x03030303u) << 4);
-    }
-    // sa = 8g + 2 s0 + (c&1) is byte (2 s0 + (c&1)) of scale word 2g; sb = sa + 4
-    // is the same byte of word 2g + 1.
-    const int sh = 8 * (2 * s0 + (c & 1));
-    L.sca = (int32_t)(int8_t)((g ? sc.z : sc.x) >> sh);
-    L.scb = (int32_t)(int8_t)((g ? sc.w : sc.y) >> sh);
-    L.dw = half_to_float(d16);
-    return L;
+__device__ __forceinline__ float row16_max(float v) {
+    v = fmaxf(v, dpp_f<kQuadXor1>(v));
+    v = fmaxf(v, dpp_f<kQuadXor2>(v));
+    v = fmaxf(v, dpp_f<kRowHalfMirror>(v));
+    return fmaxf(v, dpp_f<kRowMirror>(v));
+}
+__device__ __forceinline__ uint32_t umin_(uint32_t a, uint32_t b) { return a < b ? a : b; }
+__device__ __forceinline__ uint32_t row16_umin(uint32_t v) {
+    v = umin_(v, (uint32_t)dpp_i<kQuadXor1>((int32_t)v));
+    v = umin_(v, (uint32_t)dpp_i<kQuadXor2>((int32_t)v));
+    v = umin_(v, (uint32_t)dpp_i<kRowHalfMirror>((int32_t)v));
+    return umin_(v, (uint32_t)dpp_i<kRowMirror>((int32_t)v));
 }
 
-// I = sc_a * sum((qa - 32) q8) + sc_b * sum((qb - 32) q8).  The -32 offset is
-// applied through the 16-element activation sums: sum(q q8) - 32 bsum.
-__device__ __forceinline__ int32_t q6k_ints(const Q6KLane& L, const int8_t* a_blk, const int32_t* bs16_blk, int c) {
-    const int g = c >> 2, s0 = (c >> 1) & 1, p0 = 16 * (c & 1);
-    const int ja = 128 * g + 32 * s0 + p0;
-    const uint4 aa = *(const uint4*)(a_blk + ja);
-    const uint4 ab = *(const uint4*)(a_blk + ja + 64);
-    int32_t ia = dot4(L.qa[0], aa.x, 0);
-    ia = dot4(L.qa[1], aa.y, ia);
-    ia = dot4(L.qa[2], aa.z, ia);
-    ia = dot4(L.qa[3], aa.w, ia);
-    int32_t ib = dot4(L.qb[0], ab.x, 0);
-    ib = dot4(L.qb[1], ab.y, ib);
-    ib = dot4(L.qb[2], ab.z, ib);
-    ib = dot4(L.qb[3], ab.w, ib);
-    const int sa = ja >> 4;
-    return L.sca * (ia - 32 * bs16_blk[sa]) + L.scb * (ib - 32 * bs16_blk[sa + 4]);
-}
-
-// ---- Q8_0 lane ---------------------------------------------------------
-// Two lanes per 32-element block, lane half k holds elements 16k..16k+15.
-__device__ __forceinline__ int32_t q8_0_ints(uint4 w, const int8_t* a16) {
-    const uint4 a = *(const uint4*)a16;
-    int32_t s = dot4(w.x, a.x, 0);
-    s = dot4(w.y, a.y, s);
-    s = dot4(w.z, a.z, s);
-    return dot4(w.w, a.w, s);
-}
-
-// ---- greedy argmax key -----------------------------------------------------
+// ---- greedy argmax key -------------------------------------------------------
 // Largest value wins, then the lowest row (sampling.rs:607-613 keeps the first
 // strict maximum).  -0.0 is folded onto +0.0 because they compare equal; NaN
 // maps to 0 and never wins (the finish step handles a NaN at row 0).
@@ -158,430 +92,814 @@ __device__ __forceinline__ unsigned long long argmax_key(float v, uint64_t row) 
     return ((unsigned long long)b << 32) | (0xffffffffull - (row & 0xffffffffull));
 }
 
-// ---- activation staging into LDS -------------------------------------------
-// LDS layout: q8 [B][K] | d [B][nb] f32 | sums [B][S] i32, where S is nb*8
-// (Q4_K: 32-element sums bsum[2s]+bsum[2s+1]) or K/16 (Q6_K: the bsums).
-// Returns true when no staged block carries the error mark.
-template <int B>
-__device__ __forceinline__ bool stage_q8k(const ActPlanes& act, uint64_t K, uint32_t nb, bool pair_sums, int8_t* s_q,
-                                          float* s_d, int32_t* s_sum) {
-    const uint32_t tid = threadIdx.x;
-    const uint64_t qwords = (uint64_t)B * K / 16;
-    for (uint64_t i = tid; i < qwords; i += kThreads) ((uint4*)s_q)[i] = ((const uint4*)act.q)[i];
-    int bad = 0;
-    for (uint32_t i = tid; i < B * nb; i += kThreads) {
-        s_d[i] = act.d[i];
-        bad |= act.bad[i];
-    }
-    if (pair_sums) {
-        for (uint32_t i = tid; i < B * nb * 8; i += kThreads)
-            s_sum[i] = (int32_t)act.bsum[2 * i] + (int32_t)act.bsum[2 * i + 1];
-    } else {
-        for (uint32_t i = tid; i < B * nb * 16; i += kThreads) s_sum[i] = act.bsum[i];
-    }
-    return __syncthreads_or(bad) == 0;
-}
-
-template <int B>
-__device__ __forceinline__ bool stage_q8_0(const ActPlanes& act, uint64_t K, uint32_t nb, int8_t* s_q, float* s_d) {
-    const uint32_t tid = threadIdx.x;
-    const uint64_t qwords = (uint64_t)B * K / 16;
-    for (uint64_t i = tid; i < qwords; i += kThreads) ((uint4*)s_q)[i] = ((const uint4*)act.q)[i];
-    int bad = 0;
-    for (uint32_t i = tid; i < B * nb; i += kThreads) {
-        s_d[i] = act.d[i];
-        bad |= act.bad[i];
-    }
-    return __syncthreads_or(bad) == 0;
-}
-
-// Per-row epilogue: reduce each column's lane partials, store, update argmax.
-template <int B>
-__device__ __forceinline__ void finish_row(float (&acc)[B], uint64_t row, uint64_t rows, float* y, uint64_t ldy,
-                                           unsigned long long (&best)[B]) {
+// Max over the 16 lanes of each row (lane & 15), result in every lane.
+__device__ __forceinline__ unsigned long long row16_max_u64(unsigned long long v) {
 #pragma unroll
-    for (int b = 0; b < B; ++b) {
-        const float v = wave_sum(acc[b]);
-        if (row < rows) {
-            if ((threadIdx.x & 63) == b) y[(uint64_t)b * ldy + row] = v;
-            const unsigned long long k = argmax_key(v, row);
-            best[b] = k > best[b] ? k : best[b];
+    for (int m = 1; m < 16; m <<= 1) {
+        const unsigned long long o = __shfl_xor(v, m, 64);
+        v = o > v ? o : v;
+    }
+    return v;
+}
+
+// ---------------------------------------------------------------------------
+// Kernel arguments and the LDS image of the quantized activations
+// ---------------------------------------------------------------------------
+struct MvArgs {
+    const uint8_t* w;                 // weights, device layout
+    uint32_t rows, nb;                // rows; GGUF blocks per row
+    uint32_t ntiles, nchunks;         // 16-row tiles; chunks per tile
+    uint32_t batch;                   // columns in this launch, 1..8
+    uint32_t cols;
+    const float* x;                   // f32 activations [batch][cols], or null
+    ActPlanes pre;                    // pre-quantized activations when x is null
+    float* y;                         // y[b * ldy + row]
+    uint64_t ldy;
+    unsigned long long* argmax_key;   // [batch] or null
+    unsigned long long* err_word;
+    uint32_t err_column0;             // column index of this launch's column 0
+    int32_t* dbg_isum;                // [rows][nb] exact integers vs column 0, or null
+    int32_t* dbg_imin;
+};
+
+// LDS: q8 [batch][S] | d f32 [nb][8] | (Q4_K) bsums i16 [nb][8][16] | 256
+// zero bytes.  S = cols + 16 is an odd multiple of 16, so the A-operand reads
+// of the eight columns fall in distinct banks.  Lanes whose MFMA A operand is
+// all zero read the zero bytes instead of taking a branch.
+struct LdsMap {
+    uint32_t S, d_off, bs_off, zero_off, total;
+};
+
+__host__ __device__ inline LdsMap lds_map(uint32_t t, uint32_t cols, uint32_t batch) {
+    LdsMap m;
+    const uint32_t nb = cols / (t == kQ8_0 ? 32 : 256);
+    m.S = cols + 16;
+    m.d_off = (m.S * batch + 15u) & ~15u;
+    m.bs_off = m.d_off + nb * 32;
+    m.zero_off = m.bs_off + (t == kQ4_K ? nb * 256 : 0);
+    m.total = m.zero_off + 256;
+    return m;
+}
+
+// Q4_K bsums of one (block, column) are stored in the order [kq][4]: K
+// quarter kq = 2g + h finds the 16-value groups it multiplies (half h of
+// sub-blocks 2g, 2g+1, 2g+4, 2g+5) in one 8-byte word.  Slot of group
+// grp = 2 * sub + half:
+__device__ __forceinline__ uint32_t bs_slot(uint32_t grp) {
+    const uint32_t sub = grp >> 1, half = grp & 1;
+    return (2 * ((sub >> 1) & 1) + half) * 4 + (sub & 1) + 2 * (sub >> 2);
+}
+
+// ---------------------------------------------------------------------------
+// Prologue: activations into LDS
+// ---------------------------------------------------------------------------
+
+// The activations are quantized in 16-value units (one Q8_K bsum group, half
+// a Q8_0 block): unit u of the launch is column u / (cols/16), values
+// 16 * (u % (cols/16)) ..; wave w takes units 64 (w + k W) + lane.
+__device__ __forceinline__ void load_unit(const MvArgs& a, uint32_t u, float (&v)[16]) {
+    const uint32_t upc = a.cols / 16;
+    const float4* src = (const float4*)(a.x + (uint64_t)(u / upc) * a.cols + (u % upc) * 16);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const float4 f = src[k];
+        v[4 * k] = f.x, v[4 * k + 1] = f.y, v[4 * k + 2] = f.z, v[4 * k + 3] = f.w;
+    }
+}
+
+// This lane's first unit, loaded before the weight prefetch: loads retire in
+// order, so the quantizer's wait for x does not also wait for the weights.
+__device__ __forceinline__ void prefetch_unit(const MvArgs& a, uint32_t wave, float (&v)[16]) {
+#pragma unroll
+    for (int k = 0; k < 16; ++k) v[k] = 0.0f;
+    const uint32_t u = wave * 64 + (threadIdx.x & 63);
+    if (a.x && u < (a.cols / 16) * a.batch) load_unit(a, u, v);
+}
+
+// Q8_K (activation.rs:4-51) of all batch columns.  A 16-lane row quantizes
+// one 256-value block, 16 values per lane (one bsum group per lane).
+// Returns false in every thread when any block of any column is invalid.
+template <int W, bool BSUMS>
+__device__ __forceinline__ bool stage_q8k(const MvArgs& a, uint8_t* lds, const LdsMap& L, uint32_t wave, const float (&v0)[16]) {
+    const uint32_t K = a.cols, upc = K / 16, units = upc * a.batch;
+    const uint32_t lane = threadIdx.x & 63, r16 = lane & 15;
+    int bad = 0;
+    for (uint32_t base = wave * 64; base < units; base += W * 64) {
+        const uint32_t u = base + lane;
+        if (u >= units) continue;  // whole 16-lane rows drop out together (units % 16 == 0)
+        const uint32_t b = u / upc, e0 = (u % upc) * 16, blk = e0 / 256, in_blk = e0 % 256;
+        float v[16];
+        if (base == wave * 64) {
+#pragma unroll
+            for (int k = 0; k < 16; ++k) v[k] = v0[k];
+        } else {
+            load_unit(a, u, v);
+        }
+        // NonFiniteInput: first index of the block
+        uint32_t nf = 0xffffffffu;
+#pragma unroll
+        for (int k = 15; k >= 0; --k)
+            if (!finite(v[k])) nf = in_blk + k;
+        nf = row16_umin(nf);
+        const bool nonfinite = nf != 0xffffffffu;
+        // inverse_scale: the first value of largest magnitude (strict `>`)
+        float am = 0.0f;
+        uint32_t ai = 0, sg = 0;
+#pragma unroll
+        for (int k = 0; k < 16; ++k)
+            if (fabsf(v[k]) > am) {
+                am = fabsf(v[k]);
+                ai = in_blk + k;
+                sg = __float_as_uint(v[k]) >> 31;
+            }
+        const float amax = row16_max(nonfinite ? 0.0f : am);
+        const uint32_t key = row16_umin((am == amax && amax > 0.0f) ? (ai << 1 | sg) : 0xffffffffu);
+        float inverse = 0.0f;
+        if (amax > 0.0f && !nonfinite) inverse = -127.0f / ((key & 1u) ? -amax : amax);
+        // preflight_q8k: the scale and its reciprocal must be finite
+        const bool scale_bad = !nonfinite && (!finite(inverse) || (inverse != 0.0f && !finite(1.0f / inverse)));
+        const bool invalid = nonfinite || scale_bad;
+        if (invalid) {
+            bad = 1;
+            if (r16 == 0)
+                report_error(a.err_word, nonfinite ? error_key(a.err_column0 + b, kKindNonFinite, blk * 256ull + nf)
+                                                   : error_key(a.err_column0 + b, kKindScale, blk));
+        }
+        // encode_q8k: q = min(rint(inverse * x), 127), bsum of 16, d = 1 / inverse
+        uint32_t qw[4] = {0, 0, 0, 0};
+        if (inverse != 0.0f && !invalid) {
+#pragma unroll
+            for (int k = 0; k < 16; ++k) {
+                int32_t q = (int32_t)__builtin_rintf(inverse * v[k]);
+                q = q < 127 ? q : 127;
+                qw[k / 4] |= ((uint32_t)q & 0xffu) << (8 * (k % 4));
+            }
+        }
+        *(uint4*)(lds + b * L.S + e0) = make_uint4(qw[0], qw[1], qw[2], qw[3]);
+        if (r16 == 0) *(float*)(lds + L.d_off + (blk * 8 + b) * 4) = (inverse != 0.0f && !invalid) ? 1.0f / inverse : 0.0f;
+        if (BSUMS) {  // bsums[g] = sum of the 16 q of group g (activation.rs:43-47)
+            int32_t s = dot4(qw[0], 0x01010101u, 0);
+            s = dot4(qw[1], 0x01010101u, s);
+            s = dot4(qw[2], 0x01010101u, s);
+            s = dot4(qw[3], 0x01010101u, s);
+            *(int16_t*)(lds + L.bs_off + (blk * 8 + b) * 32 + bs_slot(r16) * 2) = (int16_t)s;
+        }
+    }
+    return __syncthreads_or(bad) == 0;
+}
+
+// Q8_0 (encode.rs:115-126, 151-192) of all batch columns: two lanes per
+// 32-value block.
+template <int W>
+__device__ __forceinline__ bool stage_q8_0(const MvArgs& a, uint8_t* lds, const LdsMap& L, uint32_t wave, const float (&v0)[16]) {
+    const uint32_t K = a.cols, upc = K / 16, units = upc * a.batch;
+    const uint32_t lane = threadIdx.x & 63;
+    int bad = 0;
+    for (uint32_t base = wave * 64; base < units; base += W * 64) {
+        const uint32_t u = base + lane;
+        if (u >= units) continue;  // lane pairs drop out together (units is even)
+        const uint32_t b = u / upc, e0 = (u % upc) * 16, blk = e0 / 32, half = (e0 / 16) & 1u;
+        float v[16];
+        if (base == wave * 64) {
+#pragma unroll
+            for (int k = 0; k < 16; ++k) v[k] = v0[k];
+        } else {
+            load_unit(a, u, v);
+        }
+        uint32_t nf = 0xffffffffu;
+#pragma unroll
+        for (int k = 15; k >= 0; --k)
+            if (!finite(v[k])) nf = half * 16 + k;
+        nf = umin_(nf, (uint32_t)dpp_i<kQuadXor1>((int32_t)nf));
+        const bool nonfinite = nf != 0xffffffffu;
+        // scales(): amax = fold(0, max(a, |v|)); d = amax / 127
+        float am = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 16; ++k) am = fmaxf(am, fabsf(v[k]));
+        am = fmaxf(am, dpp_f<kQuadXor1>(am));
+        const float d = nonfinite ? 0.0f : am / 127.0f;
+        const uint32_t dh = float_to_half_bits(d);
+        // preflight (encode.rs:80-90): d, 1/d and the stored half must be finite
+        const bool scale_bad =
+            !nonfinite && (!finite(d) || (d != 0.0f && !finite(1.0f / d)) || (dh & 0x7c00u) == 0x7c00u);
+        const bool invalid = nonfinite || scale_bad;
+        if (invalid) {
+            bad = 1;
+            if (half == 0)
+                report_error(a.err_word, nonfinite ? error_key(a.err_column0 + b, kKindNonFinite, blk * 32ull + nf)
+                                                   : error_key(a.err_column0 + b, kKindScale, blk));
+        }
+        const float inv = d != 0.0f ? 1.0f / d : 0.0f;
+        uint32_t qw[4] = {0, 0, 0, 0};
+        if (!invalid) {
+#pragma unroll
+            for (int k = 0; k < 16; ++k) {
+                // `(x * inv).round() as i8`: half away from zero, saturating
+                float r = __builtin_roundf(v[k] * inv);
+                r = r > 127.0f ? 127.0f : (r < -128.0f ? -128.0f : r);
+                qw[k / 4] |= ((uint32_t)(int32_t)r & 0xffu) << (8 * (k % 4));
+            }
+        }
+        *(uint4*)(lds + b * L.S + e0) = make_uint4(qw[0], qw[1], qw[2], qw[3]);
+        if (half == 0) *(float*)(lds + L.d_off + (blk * 8 + b) * 4) = half_bits_to_float_exact(dh);
+    }
+    return __syncthreads_or(bad) == 0;
+}
+
+// Pre-quantized activations (planes in global memory) into LDS.
+template <int W>
+__device__ __forceinline__ bool stage_planes(const MvArgs& a, uint8_t* lds, const LdsMap& L, uint32_t wtype) {
+    const uint32_t K = a.cols, bs = wtype == kQ8_0 ? 32 : 256, nb = K / bs;
+    const uint32_t tid = threadIdx.x, nt = W * 64;
+    for (uint32_t i = tid; i < a.batch * (K / 16); i += nt) {
+        const uint32_t b = i / (K / 16), e = (i % (K / 16)) * 16;
+        *(uint4*)(lds + b * L.S + e) = *(const uint4*)(a.pre.q + (uint64_t)b * K + e);
+    }
+    int bad = 0;
+    for (uint32_t i = tid; i < a.batch * nb; i += nt) {
+        const uint32_t b = i / nb, blk = i % nb;
+        *(float*)(lds + L.d_off + (blk * 8 + b) * 4) = a.pre.d[i];
+        bad |= a.pre.bad[i];
+    }
+    if (wtype == kQ4_K) {
+        for (uint32_t i = tid; i < a.batch * (K / 16); i += nt) {
+            const uint32_t b = i / (K / 16), g = i % (K / 16);
+            *(int16_t*)(lds + L.bs_off + ((g / 16) * 8 + b) * 32 + bs_slot(g % 16) * 2) = a.pre.bsum[i];
+        }
+    }
+    return __syncthreads_or(bad) == 0;
+}
+
+// ---------------------------------------------------------------------------
+// Per-tile epilogue shared by the three kernels: store y and fold the argmax.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void store_out(const MvArgs& a, uint32_t row, uint32_t b, float v,
+                                          unsigned long long& best) {
+    if (row < a.rows && b < a.batch) {
+        a.y[(uint64_t)b * a.ldy + row] = v;
+        const unsigned long long k = argmax_key(v, row);
+        best = k > best ? k : best;
+    }
+}
+
+__device__ __forceinline__ void publish_argmax(const MvArgs& a, uint32_t b, unsigned long long best) {
+    if (!a.argmax_key) return;
+    best = row16_max_u64(best);
+    if ((threadIdx.x & 15) == 0 && b < a.batch && best) atomicMax(a.argmax_key + b, best);
+}
+
+// ---------------------------------------------------------------------------
+// Software pipeline over a wave's steps: buf[i] holds the loads of step
+// s0 + i, issued D steps before use.  The steady-state loop issues exactly one
+// step's loads per step, so every path through it has the same loads in
+// flight and the compiler's wait counts let D - 1 steps stay outstanding; the
+// drain loop (at most two passes) issues only what remains.
+// ---------------------------------------------------------------------------
+template <int D, typename Step, typename Issue, typename Compute>
+__device__ __forceinline__ void pipeline(uint32_t steps, Step (&buf)[D], Issue& issue, Compute& compute) {
+    uint32_t s0 = 0;
+    for (; s0 + 2 * D <= steps; s0 += D) {
+#pragma unroll
+        for (int i = 0; i < D; ++i) {
+            const Step cur = buf[i];
+            issue(buf[i]);
+            compute(cur);
+        }
+    }
+    for (; s0 < steps; s0 += D) {
+#pragma unroll
+        for (int i = 0; i < D; ++i) {
+            if (s0 + i >= steps) break;
+            const Step cur = buf[i];
+            if (s0 + i + D < steps) issue(buf[i]);
+            compute(cur);
         }
     }
 }
 
-template <int B>
-__device__ __forceinline__ void publish_argmax(const unsigned long long (&best)[B], unsigned long long* key) {
-    if (!key) return;
-    if ((threadIdx.x & 63) == 0) {
-#pragma unroll
-        for (int b = 0; b < B; ++b)
-            if (best[b]) atomicMax(key + b, best[b]);
-    }
+// ---------------------------------------------------------------------------
+// Q4_K
+// ---------------------------------------------------------------------------
+struct Q4Step {
+    uint4 w0, w1, h;
+};
+
+// Common kernel prologue: wave indices, the first x unit, the weight prefetch
+// of steps 0..D-1 (clamped to the last tile, so it never leaves the buffer),
+// and the activation staging.  `ld_tile`/`ld_chunk` track the next step to
+// load: tile gw + k*tw, chunk c.
+#define RLQ_MV_PROLOGUE(WT, CHUNKS)                                                                   \
+    extern __shared__ __align__(16) uint8_t lds[];                                                    \
+    const LdsMap L = lds_map(WT, a.cols, a.batch);                                                   \
+    const uint32_t lane = threadIdx.x & 63, n = lane & 15, kq = lane >> 4;                            \
+    /* wave-uniform indices in scalar registers: loop control stays on the SALU */                    \
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);                           \
+    const uint32_t gw = blockIdx.x * W + wave, tw = gridDim.x * W;                                    \
+    const uint32_t nch = (CHUNKS);                                                                    \
+    const uint32_t steps = gw < a.ntiles ? ((a.ntiles - 1 - gw) / tw + 1) * nch : 0;                  \
+    if (threadIdx.x < 16) *(uint4*)(lds + L.zero_off + threadIdx.x * 16) = make_uint4(0, 0, 0, 0);   \
+    float xv[16];                                                                                     \
+    prefetch_unit(a, wave, xv);                                                                       \
+    uint32_t ld_tile = gw < a.ntiles ? gw : a.ntiles - 1, ld_chunk = 0;                               \
+    auto next_load = [&]() {                                                                          \
+        if (++ld_chunk == nch) {                                                                      \
+            ld_chunk = 0;                                                                             \
+            if (ld_tile + tw < a.ntiles) ld_tile += tw;                                               \
+        }                                                                                             \
+    };
+
+__device__ __forceinline__ int32_t mad24(int32_t a, int32_t b, int32_t c) { return __mul24(a, b) + c; }
+
+// Scales and mins of sub-blocks j and j + 1 (j even) of a Q4_K block from its
+// 12 packed bytes w1..w3 (matvec_extra.rs:212-221): for j < 4 the low six
+// bits of bytes j, j+4; for j >= 4 four bits of byte j+4 and the top two bits
+// of bytes j-4 / j.  As words: sc[0..3] = w1 & 0x3f.., mn[0..3] = w2 & 0x3f..,
+// sc[4..7] = (w3 & 0x0f..) | ((w1 >> 2) & 0x30..), mn[4..7] =
+// ((w3 >> 4) & 0x0f..) | ((w2 >> 2) & 0x30..), one value per byte.
+struct Q4Scales {
+    uint32_t scA, scB, mnA, mnB;
+};
+__device__ __forceinline__ Q4Scales q4k_scales(uint4 h) {
+    Q4Scales q;
+    q.scA = h.y & 0x3f3f3f3fu;
+    q.scB = (h.w & 0x0f0f0f0fu) | ((h.y >> 2) & 0x30303030u);
+    q.mnA = h.z & 0x3f3f3f3fu;
+    q.mnB = ((h.w >> 4) & 0x0f0f0f0fu) | ((h.z >> 2) & 0x30303030u);
+    return q;
 }
 
-// ---------------------------------------------------------------------------
-// Q4_K: R rows per wave, IT block-octets per pass.
-// ---------------------------------------------------------------------------
-template <int B, int R, int IT>
-__global__ __launch_bounds__(kThreads) void q4k_matvec_kernel(const uint8_t* __restrict__ W, uint64_t rows,
-                                                              uint32_t nb, ActPlanes act, float* __restrict__ y,
-                                                              uint64_t ldy, unsigned long long* argmax_key_out) {
-    extern __shared__ __align__(16) uint8_t smem[];
-    const uint64_t K = (uint64_t)nb * 256;
-    int8_t* s_q = (int8_t*)smem;
-    float* s_d = (float*)(smem + B * K);
-    int32_t* s_sum = (int32_t*)(s_d + B * nb);
+// Decode kernels with DBG also store the exact per-(row, block) integers of
+// column 0 (isum: the scaled sub-block dots; imin: the mins term).
 
-    const int lane = threadIdx.x & 63, c = lane & 7, bi = lane >> 3;
-    const uint64_t row0 = ((uint64_t)blockIdx.x * kWaves + (threadIdx.x >> 6)) * R;
-    const uint32_t per_pass = 8 * IT;
-    const uint32_t passes = (nb + per_pass - 1) / per_pass;
-
-    uint4 wh[R][IT], wq[R][IT];
-    auto issue = [&](uint32_t pass) {
-#pragma unroll
-        for (int r = 0; r < R; ++r)
-#pragma unroll
-            for (int it = 0; it < IT; ++it) {
-                const uint32_t blk = pass * per_pass + it * 8 + bi;
-                const uint64_t row = row0 + r;
-                if (row < rows && blk < nb) {
-                    const uint8_t* base = W + (row * nb + blk) * 144;
-                    wh[r][it] = load_stream16(base);
-                    wq[r][it] = load_stream16(base + 16 + 16 * c);
-                } else {
-                    wh[r][it] = make_uint4(0, 0, 0, 0);
-                    wq[r][it] = make_uint4(0, 0, 0, 0);
-                }
-            }
+// Q4_K, batches of three to eight columns: MFMA.
+template <int W, int D, bool DBG>
+__global__ __launch_bounds__(W * 64) void q4k_mv_kernel(MvArgs a) {
+    RLQ_MV_PROLOGUE(kQ4_K, a.nb)
+    const uint32_t nb = a.nb;
+    Q4Step buf[D];
+    auto issue = [&](Q4Step& st) {
+        const uint8_t* base = a.w + ((uint64_t)ld_tile * nb + ld_chunk) * kQ4KChunk;
+        st.w0 = load_stream16(base + lane * 16);
+        st.w1 = load_stream16(base + 1024 + lane * 16);
+        st.h = load_stream16(base + 2048 + n * 16);
+        next_load();
     };
-    issue(0);
-    if (!stage_q8k<B>(act, K, nb, true, s_q, s_d, s_sum)) return;
+#pragma unroll
+    for (int i = 0; i < D; ++i) issue(buf[i]);
 
-    float acc[R][B];
-#pragma unroll
-    for (int r = 0; r < R; ++r)
-#pragma unroll
-        for (int b = 0; b < B; ++b) acc[r][b] = 0.0f;
+    const bool ok = a.x ? stage_q8k<W, true>(a, lds, L, wave, xv) : stage_planes<W>(a, lds, L, kQ4_K);
+    if (!ok) return;
 
-    for (uint32_t pass = 0; pass < passes; ++pass) {
-        if (pass) issue(pass);
-#pragma unroll
-        for (int r = 0; r < R; ++r)
-#pragma unroll
-            for (int it = 0; it < IT; ++it) {
-                const uint32_t blk = pass * per_pass + it * 8 + bi;
-                if (blk >= nb) continue;
-                const Q4KLane L = q4k_lane(wh[r][it], wq[r][it], c);
-#pragma unroll
-                for (int b = 0; b < B; ++b) {
-                    int32_t I, M;
-                    q4k_ints(L, s_q + b * K + blk * 256, s_sum + (b * nb + blk) * 8, c, I, M);
-                    const float da = s_d[b * nb + blk];
-                    const float d = L.dw * da, dmin = L.dmw * da;
-                    acc[r][b] += d * (float)I - dmin * (float)M;
-                }
+    // A operand: lane row r = n holds column r / 2, sub-block parity r % 2; it
+    // is nonzero only in the K quarters (kq / 2 == r % 2) of that sub-block.
+    const uint32_t ab = n >> 1, which = n & 1;
+    const bool a_live = which == (kq >> 1) && ab < a.batch;
+    const uint8_t* a_ptr = a_live ? lds + ab * L.S + 64 * which + 16 * (kq & 1) : lds + L.zero_off;
+    const uint32_t a_step = a_live ? 256 : 0;
+    const uint32_t b0 = 2 * kq;  // this lane's output columns b0, b0 + 1
+
+    float acc0 = 0.0f, acc1 = 0.0f;
+    unsigned long long best0 = 0, best1 = 0;
+    uint32_t tile = gw, blk = 0;
+    auto compute = [&](const Q4Step& cur) {
+        const Q4Scales q = q4k_scales(cur.h);
+        const uint8_t* p = a_ptr + blk * a_step;
+        const i32x4 al0 = *(const i32x4*)(p), ah0 = *(const i32x4*)(p + 32);
+        const i32x4 al1 = *(const i32x4*)(p + 128), ah1 = *(const i32x4*)(p + 160);
+        // sub-blocks: dl0 {0, 2}, dh0 {1, 3}, dl1 {4, 6}, dh1 {5, 7}; element
+        // 2j + w of each is column b0 + j, sub-block parity w
+        const i32x4 dl0 = mfma_i8(al0, lo_nibbles(cur.w0));
+        const i32x4 dh0 = mfma_i8(ah0, hi_nibbles(cur.w0));
+        const i32x4 dl1 = mfma_i8(al1, lo_nibbles(cur.w1));
+        const i32x4 dh1 = mfma_i8(ah1, hi_nibbles(cur.w1));
+        const int32_t c0 = ubyte(q.scA, 0), c1 = ubyte(q.scA, 1), c2 = ubyte(q.scA, 2), c3 = ubyte(q.scA, 3);
+        const int32_t c4 = ubyte(q.scB, 0), c5 = ubyte(q.scB, 1), c6 = ubyte(q.scB, 2), c7 = ubyte(q.scB, 3);
+        // |dot| <= 32*15*127 and scales <= 63: 24-bit products are exact
+        int32_t I0 = mad24(c0, dl0[0], mad24(c2, dl0[1], mad24(c1, dh0[0], __mul24(c3, dh0[1]))));
+        I0 = mad24(c4, dl1[0], mad24(c6, dl1[1], mad24(c5, dh1[0], mad24(c7, dh1[1], I0))));
+        int32_t I1 = mad24(c0, dl0[2], mad24(c2, dl0[3], mad24(c1, dh0[2], __mul24(c3, dh0[3]))));
+        I1 = mad24(c4, dl1[2], mad24(c6, dl1[3], mad24(c5, dh1[2], mad24(c7, dh1[3], I1))));
+        // mins: sum_s min_s * (bsum[2s] + bsum[2s+1])  (matvec_extra.rs:258)
+        const uint32_t m01 = __builtin_amdgcn_perm(0u, q.mnA, 0x0c010c00u);
+        const uint32_t m23 = __builtin_amdgcn_perm(0u, q.mnA, 0x0c030c02u);
+        const uint32_t m45 = __builtin_amdgcn_perm(0u, q.mnB, 0x0c010c00u);
+        const uint32_t m67 = __builtin_amdgcn_perm(0u, q.mnB, 0x0c030c02u);
+        const uint4* bs = (const uint4*)(lds + L.bs_off + (blk * 8 + b0) * 32);
+        const uint4 bA0 = bs[0], bA1 = bs[1], bB0 = bs[2], bB1 = bs[3];
+        const int32_t M0 = dot2(m67, bA1.w, dot2(m23, bA1.z, dot2(m67, bA1.y, dot2(m23, bA1.x,
+                           dot2(m45, bA0.w, dot2(m01, bA0.z, dot2(m45, bA0.y, dot2(m01, bA0.x, 0))))))));
+        const int32_t M1 = dot2(m67, bB1.w, dot2(m23, bB1.z, dot2(m67, bB1.y, dot2(m23, bB1.x,
+                           dot2(m45, bB0.w, dot2(m01, bB0.z, dot2(m45, bB0.y, dot2(m01, bB0.x, 0))))))));
+
+        const float2 da = *(const float2*)(lds + L.d_off + (blk * 8 + b0) * 4);
+        const float dw = half_to_float(cur.h.x), dmw = half_to_float(cur.h.x >> 16);
+        acc0 += (dw * da.x) * (float)I0 - (dmw * da.x) * (float)M0;
+        acc1 += (dw * da.y) * (float)I1 - (dmw * da.y) * (float)M1;
+
+        if (DBG && kq == 0) {
+            const uint32_t row = tile * kTileRows + n;
+            if (row < a.rows) {
+                a.dbg_isum[(uint64_t)row * nb + blk] = I0;
+                a.dbg_imin[(uint64_t)row * nb + blk] = M0;
             }
-    }
+        }
+        if (++blk == nb) {
+            const uint32_t row = tile * kTileRows + n;
+            store_out(a, row, b0, acc0, best0);
+            store_out(a, row, b0 + 1, acc1, best1);
+            acc0 = acc1 = 0.0f;
+            blk = 0;
+            tile += tw;
+        }
+    };
+    pipeline<D>(steps, buf, issue, compute);
+    publish_argmax(a, b0, best0);
+    publish_argmax(a, b0 + 1, best1);
+}
+
+// Q4_K, one or two columns: v_dot4_i32_i8 on the VALU.  Lane (n, kq), kq =
+// 2g + h, multiplies half h of sub-blocks 2g, 2g+1 (qs bytes of w0) and
+// 2g+4, 2g+5 (w1) of row n; its integer partials and its share of the mins
+// (the bsums of exactly those 16-value groups) are scaled per block, and the
+// four K quarters of a row are added once per tile.
+template <int W, int D, int B, bool DBG>
+__global__ __launch_bounds__(W * 64) void q4k_mv_small_kernel(MvArgs a) {
+    RLQ_MV_PROLOGUE(kQ4_K, a.nb)
+    const uint32_t nb = a.nb;
+    Q4Step buf[D];
+    auto issue = [&](Q4Step& st) {
+        const uint8_t* base = a.w + ((uint64_t)ld_tile * nb + ld_chunk) * kQ4KChunk;
+        st.w0 = load_stream16(base + lane * 16);
+        st.w1 = load_stream16(base + 1024 + lane * 16);
+        st.h = load_stream16(base + 2048 + n * 16);
+        next_load();
+    };
+#pragma unroll
+    for (int i = 0; i < D; ++i) issue(buf[i]);
+
+    const bool ok = a.x ? stage_q8k<W, true>(a, lds, L, wave, xv) : stage_planes<W>(a, lds, L, kQ4_K);
+    if (!ok) return;
+
+    const uint32_t g = kq >> 1, h = kq & 1;
+    // activation of (sub-block 2g, half h) and its neighbours: +32 (2g+1),
+    // +128 (2g+4), +160 (2g+5)
+    const uint8_t* a_row = lds + 64 * g + 16 * h;
+    const uint8_t* bs_row = lds + L.bs_off + kq * 8;
+
+    float acc[B];
+#pragma unroll
+    for (int b = 0; b < B; ++b) acc[b] = 0.0f;
     unsigned long long best[B];
 #pragma unroll
     for (int b = 0; b < B; ++b) best[b] = 0;
+    uint32_t tile = gw, blk = 0;
+    auto compute = [&](const Q4Step& cur) {
+        const Q4Scales q = q4k_scales(cur.h);
+        const int32_t s0 = __builtin_amdgcn_ubfe(q.scA, 16 * g, 8), s1 = __builtin_amdgcn_ubfe(q.scA, 16 * g + 8, 8);
+        const int32_t s4 = __builtin_amdgcn_ubfe(q.scB, 16 * g, 8), s5 = __builtin_amdgcn_ubfe(q.scB, 16 * g + 8, 8);
+        const int32_t m0 = __builtin_amdgcn_ubfe(q.mnA, 16 * g, 8), m1 = __builtin_amdgcn_ubfe(q.mnA, 16 * g + 8, 8);
+        const int32_t m4 = __builtin_amdgcn_ubfe(q.mnB, 16 * g, 8), m5 = __builtin_amdgcn_ubfe(q.mnB, 16 * g + 8, 8);
+        const uint32_t l0[4] = {cur.w0.x & 0x0f0f0f0fu, cur.w0.y & 0x0f0f0f0fu, cur.w0.z & 0x0f0f0f0fu,
+                                cur.w0.w & 0x0f0f0f0fu};
+        const uint32_t h0[4] = {(cur.w0.x >> 4) & 0x0f0f0f0fu, (cur.w0.y >> 4) & 0x0f0f0f0fu,
+                                (cur.w0.z >> 4) & 0x0f0f0f0fu, (cur.w0.w >> 4) & 0x0f0f0f0fu};
+        const uint32_t l1[4] = {cur.w1.x & 0x0f0f0f0fu, cur.w1.y & 0x0f0f0f0fu, cur.w1.z & 0x0f0f0f0fu,
+                                cur.w1.w & 0x0f0f0f0fu};
+        const uint32_t h1[4] = {(cur.w1.x >> 4) & 0x0f0f0f0fu, (cur.w1.y >> 4) & 0x0f0f0f0fu,
+                                (cur.w1.z >> 4) & 0x0f0f0f0fu, (cur.w1.w >> 4) & 0x0f0f0f0fu};
+        const float dw = half_to_float(cur.h.x), dmw = half_to_float(cur.h.x >> 16);
 #pragma unroll
-    for (int r = 0; r < R; ++r) finish_row<B>(acc[r], row0 + r, rows, y, ldy, best);
-    publish_argmax<B>(best, argmax_key_out);
-}
-
-// ---------------------------------------------------------------------------
-// Q6_K (planar device layout): R rows per wave, IT block-octets per pass.
-// ---------------------------------------------------------------------------
-template <int B, int R, int IT>
-__global__ __launch_bounds__(kThreads) void q6k_matvec_kernel(const uint8_t* __restrict__ W, uint64_t rows,
-                                                              uint32_t nb, ActPlanes act, float* __restrict__ y,
-                                                              uint64_t ldy, unsigned long long* argmax_key_out) {
-    extern __shared__ __align__(16) uint8_t smem[];
-    const uint64_t K = (uint64_t)nb * 256;
-    int8_t* s_q = (int8_t*)smem;
-    float* s_d = (float*)(smem + B * K);
-    int32_t* s_sum = (int32_t*)(s_d + B * nb);
-
-    const uint64_t nq = rows * nb;
-    const uint8_t* P_ql = W;
-    const uint8_t* P_qh = W + nq * 128;
-    const uint8_t* P_sc = W + nq * 192;
-    const uint16_t* P_d = (const uint16_t*)(W + nq * 208);
-
-    const int lane = threadIdx.x & 63, c = lane & 7, bi = lane >> 3;
-    const int qh_chunk = 2 * (c >> 2) + (c & 1);
-    const uint64_t row0 = ((uint64_t)blockIdx.x * kWaves + (threadIdx.x >> 6)) * R;
-    const uint32_t per_pass = 8 * IT;
-    const uint32_t passes = (nb + per_pass - 1) / per_pass;
-
-    uint4 wl[R][IT], wqh[R][IT], wsc[R][IT];
-    uint32_t wd[R][IT];
-    auto issue = [&](uint32_t pass) {
-#pragma unroll
-        for (int r = 0; r < R; ++r)
-#pragma unroll
-            for (int it = 0; it < IT; ++it) {
-                const uint32_t blk = pass * per_pass + it * 8 + bi;
-                const uint64_t row = row0 + r;
-                if (row < rows && blk < nb) {
-                    const uint64_t q = row * nb + blk;
-                    wl[r][it] = load_stream16(P_ql + q * 128 + 16 * c);
-                    wqh[r][it] = load_stream16(P_qh + q * 64 + 16 * qh_chunk);
-                    wsc[r][it] = load_stream16(P_sc + q * 16);
-                    wd[r][it] = __builtin_nontemporal_load(P_d + q);
-                } else {
-                    wl[r][it] = wqh[r][it] = wsc[r][it] = make_uint4(0, 0, 0, 0);
-                    wd[r][it] = 0;
+        for (int b = 0; b < B; ++b) {
+            const uint8_t* p = a_row + b * L.S + blk * 256;
+            const uint4 x0 = *(const uint4*)(p), x1 = *(const uint4*)(p + 32);
+            const uint4 x4 = *(const uint4*)(p + 128), x5 = *(const uint4*)(p + 160);
+            const int32_t i0 = dot4(l0[3], x0.w, dot4(l0[2], x0.z, dot4(l0[1], x0.y, dot4(l0[0], x0.x, 0))));
+            const int32_t i1 = dot4(h0[3], x1.w, dot4(h0[2], x1.z, dot4(h0[1], x1.y, dot4(h0[0], x1.x, 0))));
+            const int32_t i4 = dot4(l1[3], x4.w, dot4(l1[2], x4.z, dot4(l1[1], x4.y, dot4(l1[0], x4.x, 0))));
+            const int32_t i5 = dot4(h1[3], x5.w, dot4(h1[2], x5.z, dot4(h1[1], x5.y, dot4(h1[0], x5.x, 0))));
+            int32_t I = mad24(s0, i0, mad24(s1, i1, mad24(s4, i4, __mul24(s5, i5))));
+            // this quarter's share of the mins: its four 16-value groups
+            const uint2 bw = *(const uint2*)(bs_row + (blk * 8 + b) * 32);
+            int32_t M = mad24(m0, (int16_t)bw.x, mad24(m1, (int32_t)bw.x >> 16,
+                              mad24(m4, (int16_t)bw.y, __mul24(m5, (int32_t)bw.y >> 16))));
+            const float da = *(const float*)(lds + L.d_off + (blk * 8 + b) * 4);
+            acc[b] += (dw * da) * (float)I - (dmw * da) * (float)M;
+            if (DBG && b == 0) {  // exact block integers: add the four quarters
+                I += __shfl_xor(I, 16, 64);
+                I += __shfl_xor(I, 32, 64);
+                M += __shfl_xor(M, 16, 64);
+                M += __shfl_xor(M, 32, 64);
+                const uint32_t row = tile * kTileRows + n;
+                if (kq == 0 && row < a.rows) {
+                    a.dbg_isum[(uint64_t)row * nb + blk] = I;
+                    a.dbg_imin[(uint64_t)row * nb + blk] = M;
                 }
             }
+        }
+        if (++blk == nb) {
+            const uint32_t row = tile * kTileRows + n;
+#pragma unroll
+            for (int b = 0; b < B; ++b) {
+                float v = acc[b];
+                v += __shfl_xor(v, 16, 64);
+                v += __shfl_xor(v, 32, 64);
+                if (kq == 0) store_out(a, row, b, v, best[b]);
+                acc[b] = 0.0f;
+            }
+            blk = 0;
+            tile += tw;
+        }
     };
-    issue(0);
-    if (!stage_q8k<B>(act, K, nb, false, s_q, s_d, s_sum)) return;
-
-    float acc[R][B];
+    pipeline<D>(steps, buf, issue, compute);
 #pragma unroll
-    for (int r = 0; r < R; ++r)
-#pragma unroll
-        for (int b = 0; b < B; ++b) acc[r][b] = 0.0f;
-
-    for (uint32_t pass = 0; pass < passes; ++pass) {
-        if (pass) issue(pass);
-#pragma unroll
-        for (int r = 0; r < R; ++r)
-#pragma unroll
-            for (int it = 0; it < IT; ++it) {
-                const uint32_t blk = pass * per_pass + it * 8 + bi;
-                if (blk >= nb) continue;
-                const Q6KLane L = q6k_lane(wl[r][it], wqh[r][it], wsc[r][it], wd[r][it], c);
-#pragma unroll
-                for (int b = 0; b < B; ++b) {
-                    const int32_t I = q6k_ints(L, s_q + b * K + blk * 256, s_sum + (b * nb + blk) * 16, c);
-                    const float d = L.dw * s_d[b * nb + blk];
-                    acc[r][b] += d * (float)I;
-                }
-            }
-    }
-    unsigned long long best[B];
-#pragma unroll
-    for (int b = 0; b < B; ++b) best[b] = 0;
-#pragma unroll
-    for (int r = 0; r < R; ++r) finish_row<B>(acc[r], row0 + r, rows, y, ldy, best);
-    publish_argmax<B>(best, argmax_key_out);
+    for (int b = 0; b < B; ++b) publish_argmax(a, b, best[b]);
 }
 
 // ---------------------------------------------------------------------------
-// Q8_0 (planar device layout: qs [q][32] | d [q] f16): two lanes per block,
-// 32 blocks per wave instruction, IT instructions per pass.
+// Q6_K
 // ---------------------------------------------------------------------------
-template <int B, int R, int IT>
-__global__ __launch_bounds__(kThreads) void q8_0_matvec_kernel(const uint8_t* __restrict__ W, uint64_t rows,
-                                                               uint32_t nb, ActPlanes act, float* __restrict__ y,
-                                                               uint64_t ldy, unsigned long long* argmax_key_out) {
-    extern __shared__ __align__(16) uint8_t smem[];
-    const uint64_t K = (uint64_t)nb * 32;
-    int8_t* s_q = (int8_t*)smem;
-    float* s_d = (float*)(smem + ((B * K + 15) & ~(uint64_t)15));
+struct Q6Step {
+    uint4 l0, l1, h0, h1, sc;
+    uint32_t d;
+};
 
-    const uint64_t nq = rows * nb;
-    const uint16_t* P_d = (const uint16_t*)(W + nq * 32);
-    const int lane = threadIdx.x & 63, half = lane & 1, bi = lane >> 1;
-    const uint64_t row0 = ((uint64_t)blockIdx.x * kWaves + (threadIdx.x >> 6)) * R;
-    const uint32_t per_pass = 32 * IT;
-    const uint32_t passes = (nb + per_pass - 1) / per_pass;
+// Signed 6-bit values q - 32 of 16 elements as int8: low nibbles from ql and
+// two bits from qh moved to bits 4..5, then +0x60 ^ 0x80 per byte maps
+// q in 0..63 to q - 32 without carries between bytes.
+__device__ __forceinline__ uint32_t q6_lo(uint32_t ql, uint32_t qh, uint32_t lsh) {
+    return ((ql & 0x0f0f0f0fu) + ((qh << lsh) & 0x30303030u) + 0x60606060u) ^ 0x80808080u;
+}
+__device__ __forceinline__ uint32_t q6_hi(uint32_t ql, uint32_t qh, uint32_t rsh) {
+    return (((ql >> 4) & 0x0f0f0f0fu) + ((qh >> rsh) & 0x30303030u) + 0x60606060u) ^ 0x80808080u;
+}
 
-    uint4 wq[R][IT];
-    uint32_t wd[R][IT];
-    auto issue = [&](uint32_t pass) {
-#pragma unroll
-        for (int r = 0; r < R; ++r)
-#pragma unroll
-            for (int it = 0; it < IT; ++it) {
-                const uint32_t blk = pass * per_pass + it * 32 + bi;
-                const uint64_t row = row0 + r;
-                if (row < rows && blk < nb) {
-                    const uint64_t q = row * nb + blk;
-                    wq[r][it] = load_stream16(W + q * 32 + 16 * half);
-                    wd[r][it] = __builtin_nontemporal_load(P_d + q);
-                } else {
-                    wq[r][it] = make_uint4(0, 0, 0, 0);
-                    wd[r][it] = 0;
-                }
-            }
+template <int W, int D, bool DBG>
+__global__ __launch_bounds__(W * 64) void q6k_mv_kernel(MvArgs a) {
+    RLQ_MV_PROLOGUE(kQ6_K, a.nb)
+    const uint32_t nb = a.nb;
+    Q6Step buf[D];
+    auto issue = [&](Q6Step& st) {
+        const uint8_t* base = a.w + ((uint64_t)ld_tile * nb + ld_chunk) * kQ6KChunk;
+        st.l0 = load_stream16(base + lane * 16);
+        st.l1 = load_stream16(base + 1024 + lane * 16);
+        st.h0 = load_stream16(base + 2048 + n * 64 + 32 * (kq >> 1));
+        st.h1 = load_stream16(base + 2048 + n * 64 + 32 * (kq >> 1) + 16);
+        st.sc = load_stream16(base + 3072 + n * 16);
+        st.d = __builtin_nontemporal_load((const uint16_t*)(base + 3328 + n * 2));
+        next_load();
     };
-    issue(0);
-    if (!stage_q8_0<B>(act, K, nb, s_q, s_d)) return;
+#pragma unroll
+    for (int i = 0; i < D; ++i) issue(buf[i]);
 
-    float acc[R][B];
-#pragma unroll
-    for (int r = 0; r < R; ++r)
-#pragma unroll
-        for (int b = 0; b < B; ++b) acc[r][b] = 0.0f;
+    const bool ok = a.x ? stage_q8k<W, false>(a, lds, L, wave, xv) : stage_planes<W>(a, lds, L, kQ6_K);
+    if (!ok) return;
 
-    for (uint32_t pass = 0; pass < passes; ++pass) {
-        if (pass) issue(pass);
+    // This lane's weights: ql bytes 32kq.. (g = kq/2, s1 = kq%2) give the
+    // elements of 16-element scale groups 8g + 2s1 + h (low nibbles) and
+    // 8g + 2s1 + 4 + h (high nibbles), h = 0, 1.
+    const uint32_t s1 = kq & 1, lsh = 4 - 2 * s1, rsh = 2 * s1;
+    // A operand: lane row r = n holds column r / 4 (+4 for the second column
+    // group) and is nonzero in K quarter kq == r % 4 only.
+    const uint32_t abl = n >> 2, which = n & 3;
+    const uint32_t a_grp = 8 * (which >> 1) + 2 * (which & 1);
+    const uint8_t* a_row = lds + abl * L.S + 16 * a_grp;
+    const bool two_groups = a.batch > 4;
+    const bool a_live0 = which == kq && abl < a.batch;
+    const bool a_live1 = which == kq && abl + 4 < a.batch;
+    const uint8_t* a_ptr0 = a_live0 ? a_row : lds + L.zero_off;
+    const uint8_t* a_ptr1 = a_live1 ? a_row + 4 * L.S : lds + L.zero_off;
+    const uint32_t a_step0 = a_live0 ? 256 : 0, a_step1 = a_live1 ? 256 : 0;
+
+    float acc0 = 0.0f, acc1 = 0.0f;
+    unsigned long long best0 = 0, best1 = 0;
+    uint32_t tile = gw, blk = 0;
+    auto compute = [&](const Q6Step& cur) {
+        // operands (high, h): scale groups {0,2,8,10} + 4*high + h
+        const i32x4 w00 = {(int)q6_lo(cur.l0.x, cur.h0.x, lsh), (int)q6_lo(cur.l0.y, cur.h0.y, lsh),
+                           (int)q6_lo(cur.l0.z, cur.h0.z, lsh), (int)q6_lo(cur.l0.w, cur.h0.w, lsh)};
+        const i32x4 w01 = {(int)q6_lo(cur.l1.x, cur.h1.x, lsh), (int)q6_lo(cur.l1.y, cur.h1.y, lsh),
+                           (int)q6_lo(cur.l1.z, cur.h1.z, lsh), (int)q6_lo(cur.l1.w, cur.h1.w, lsh)};
+        const i32x4 w10 = {(int)q6_hi(cur.l0.x, cur.h0.x, rsh), (int)q6_hi(cur.l0.y, cur.h0.y, rsh),
+                           (int)q6_hi(cur.l0.z, cur.h0.z, rsh), (int)q6_hi(cur.l0.w, cur.h0.w, rsh)};
+        const i32x4 w11 = {(int)q6_hi(cur.l1.x, cur.h1.x, rsh), (int)q6_hi(cur.l1.y, cur.h1.y, rsh),
+                           (int)q6_hi(cur.l1.z, cur.h1.z, rsh), (int)q6_hi(cur.l1.w, cur.h1.w, rsh)};
+        const float dw = half_to_float(cur.d);
+        // integer dot of one column group: output element i of operand (high, h)
+        // is scale group {0,2,8,10}[i] + 4 high + h
+        auto group = [&](const uint8_t* p) {
+            const i32x4 a00 = *(const i32x4*)(p), a01 = *(const i32x4*)(p + 16);
+            const i32x4 a10 = *(const i32x4*)(p + 64), a11 = *(const i32x4*)(p + 80);
+            const i32x4 d00 = mfma_i8(a00, w00), d01 = mfma_i8(a01, w01);
+            const i32x4 d10 = mfma_i8(a10, w10), d11 = mfma_i8(a11, w11);
+            int32_t I = sbyte(cur.sc.x, 0) * d00[0] + sbyte(cur.sc.x, 2) * d00[1] + sbyte(cur.sc.z, 0) * d00[2] +
+                        sbyte(cur.sc.z, 2) * d00[3];
+            I += sbyte(cur.sc.x, 1) * d01[0] + sbyte(cur.sc.x, 3) * d01[1] + sbyte(cur.sc.z, 1) * d01[2] +
+                 sbyte(cur.sc.z, 3) * d01[3];
+            I += sbyte(cur.sc.y, 0) * d10[0] + sbyte(cur.sc.y, 2) * d10[1] + sbyte(cur.sc.w, 0) * d10[2] +
+                 sbyte(cur.sc.w, 2) * d10[3];
+            I += sbyte(cur.sc.y, 1) * d11[0] + sbyte(cur.sc.y, 3) * d11[1] + sbyte(cur.sc.w, 1) * d11[2] +
+                 sbyte(cur.sc.w, 3) * d11[3];
+            return I;
+        };
+        const int32_t I0 = group(a_ptr0 + blk * a_step0);
+        acc0 += (dw * *(const float*)(lds + L.d_off + (blk * 8 + kq) * 4)) * (float)I0;
+        if (DBG && kq == 0) {
+            const uint32_t row = tile * kTileRows + n;
+            if (row < a.rows) {
+                a.dbg_isum[(uint64_t)row * nb + blk] = I0;
+                a.dbg_imin[(uint64_t)row * nb + blk] = 0;
+            }
+        }
+        if (two_groups) {
+            const int32_t I1 = group(a_ptr1 + blk * a_step1);
+            acc1 += (dw * *(const float*)(lds + L.d_off + (blk * 8 + kq + 4) * 4)) * (float)I1;
+        }
+        if (++blk == nb) {
+            const uint32_t row = tile * kTileRows + n;
+            store_out(a, row, kq, acc0, best0);
+            store_out(a, row, kq + 4, acc1, best1);
+            acc0 = acc1 = 0.0f;
+            blk = 0;
+            tile += tw;
+        }
+    };
+    pipeline<D>(steps, buf, issue, compute);
+    publish_argmax(a, kq, best0);
+    publish_argmax(a, kq + 4, best1);
+}
+
+// ---------------------------------------------------------------------------
+// Q8_0: one step is a pair of 32-element blocks
+// ---------------------------------------------------------------------------
+struct Q8Step {
+    uint4 q;
+    uint32_t d;
+};
+
+template <int W, int D, bool DBG>
+__global__ __launch_bounds__(W * 64) void q8_0_mv_kernel(MvArgs a) {
+    RLQ_MV_PROLOGUE(kQ8_0, a.nchunks)
+    const uint32_t nb = a.nb, np = a.nchunks;
+    Q8Step buf[D];
+    auto issue = [&](Q8Step& st) {
+        const uint8_t* base = a.w + ((uint64_t)ld_tile * np + ld_chunk) * kQ80Chunk;
+        st.q = load_stream16(base + lane * 16);
+        st.d = __builtin_nontemporal_load((const uint32_t*)(base + 1024 + n * 4));
+        next_load();
+    };
 #pragma unroll
-        for (int r = 0; r < R; ++r)
-#pragma unroll
-            for (int it = 0; it < IT; ++it) {
-                const uint32_t blk = pass * per_pass + it * 32 + bi;
-                if (blk >= nb) continue;
-                const float dx = half_to_float(wd[r][it]);
-#pragma unroll
-                for (int b = 0; b < B; ++b) {
-                    const int32_t I = q8_0_ints(wq[r][it], s_q + b * K + blk * 32 + 16 * half);
-                    acc[r][b] += (float)I * (dx * s_d[b * nb + blk]);
+    for (int i = 0; i < D; ++i) issue(buf[i]);
+
+    const bool ok = a.x ? stage_q8_0<W>(a, lds, L, wave, xv) : stage_planes<W>(a, lds, L, kQ8_0);
+    if (!ok) return;
+
+    // A operand: lane row r = n holds column r / 2 and block 2p + r % 2; it is
+    // nonzero in the K quarters (kq / 2 == r % 2) of that block.
+    const uint32_t ab = n >> 1, which = n & 1;
+    const bool a_live = which == (kq >> 1) && ab < a.batch;
+    const uint8_t* a_ptr = a_live ? lds + ab * L.S + 32 * which + 16 * (kq & 1) : lds + L.zero_off;
+    const uint32_t a_step = a_live ? 64 : 0;
+    const uint32_t b0 = 2 * kq;
+
+    float acc0 = 0.0f, acc1 = 0.0f;
+    unsigned long long best0 = 0, best1 = 0;
+    uint32_t tile = gw, p = 0;
+    auto compute = [&](const Q8Step& cur) {
+        const bool second = 2 * p + 1 < nb;  // false only for the odd last block of a row
+        i32x4 av = *(const i32x4*)(a_ptr + p * a_step);
+        if (!second && which) av = i32x4{0, 0, 0, 0};
+        const i32x4 dot = mfma_i8(av, i32x4{(int)cur.q.x, (int)cur.q.y, (int)cur.q.z, (int)cur.q.w});
+        // sum += isum as f32 * (dx * dy), block 2p then 2p + 1 (matvec.rs:124-128)
+        const float dx0 = half_to_float(cur.d), dx1 = half_to_float(cur.d >> 16);
+        const float2 dy0 = *(const float2*)(lds + L.d_off + (2 * p * 8 + b0) * 4);
+        acc0 += (float)dot[0] * (dx0 * dy0.x);
+        acc1 += (float)dot[2] * (dx0 * dy0.y);
+        if (second) {
+            const float2 dy1 = *(const float2*)(lds + L.d_off + ((2 * p + 1) * 8 + b0) * 4);
+            acc0 += (float)dot[1] * (dx1 * dy1.x);
+            acc1 += (float)dot[3] * (dx1 * dy1.y);
+        }
+        if (DBG && kq == 0) {
+            const uint32_t row = tile * kTileRows + n;
+            if (row < a.rows) {
+                a.dbg_isum[(uint64_t)row * nb + 2 * p] = dot[0];
+                a.dbg_imin[(uint64_t)row * nb + 2 * p] = 0;
+                if (second) {
+                    a.dbg_isum[(uint64_t)row * nb + 2 * p + 1] = dot[1];
+                    a.dbg_imin[(uint64_t)row * nb + 2 * p + 1] = 0;
                 }
             }
-    }
-    unsigned long long best[B];
-#pragma unroll
-    for (int b = 0; b < B; ++b) best[b] = 0;
-#pragma unroll
-    for (int r = 0; r < R; ++r) finish_row<B>(acc[r], row0 + r, rows, y, ldy, best);
-    publish_argmax<B>(best, argmax_key_out);
+        }
+        if (++p == np) {
+            const uint32_t row = tile * kTileRows + n;
+            store_out(a, row, b0, acc0, best0);
+            store_out(a, row, b0 + 1, acc1, best1);
+            acc0 = acc1 = 0.0f;
+            p = 0;
+            tile += tw;
+        }
+    };
+    pipeline<D>(steps, buf, issue, compute);
+    publish_argmax(a, b0, best0);
+    publish_argmax(a, b0 + 1, best1);
 }
+#undef RLQ_MV_PROLOGUE
 
 // ---------------------------------------------------------------------------
 // host dispatch
 // ---------------------------------------------------------------------------
-static size_t matvec_lds(uint32_t wtype, uint64_t B, uint64_t K) {
-    if (wtype == kQ8_0) return ((B * K + 15) & ~(uint64_t)15) + B * (K / 32) * 4;
-    const uint64_t nb = K / 256;
-    return B * K + B * nb * 4 + B * (wtype == kQ4_K ? nb * 8 : nb * 16) * 4;
+constexpr int kMvWaves = 4;
+constexpr size_t kMaxLds = 160 * 1024;
+
+static int device_cus() {
+    static int cus = 0;
+    if (!cus) {
+        int dev = 0, v = 0;
+        if (hipGetDevice(&dev) == hipSuccess &&
+            hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0)
+            cus = v;
+        else
+            cus = 256;
+    }
+    return cus;
 }
 
-constexpr size_t kMaxLds = 64 * 1024;
-
-template <int B>
-static hipError_t launch_b(uint32_t wtype, const uint8_t* w, uint64_t rows, uint64_t cols, const ActPlanes& act,
-                           float* y, uint64_t ldy, unsigned long long* key, hipStream_t s) {
-    const size_t lds = matvec_lds(wtype, B, cols);
-    if (wtype == kQ4_K) {
-        constexpr int R = B == 1 ? 4 : (B <= 4 ? 2 : 1);
-        const uint64_t grid = (rows + kWaves * R - 1) / (kWaves * R);
-        hipLaunchKernelGGL((q4k_matvec_kernel<B, R, 2>), dim3((unsigned)grid), dim3(kThreads), lds, s, w, rows,
-                           (uint32_t)(cols / 256), act, y, ldy, key);
-    } else if (wtype == kQ6_K) {
-        constexpr int R = B == 1 ? 2 : 1;
-        const uint64_t grid = (rows + kWaves * R - 1) / (kWaves * R);
-        hipLaunchKernelGGL((q6k_matvec_kernel<B, R, 2>), dim3((unsigned)grid), dim3(kThreads), lds, s, w, rows,
-                           (uint32_t)(cols / 256), act, y, ldy, key);
-    } else {
-        constexpr int R = B == 1 ? 4 : (B <= 4 ? 2 : 1);
-        const uint64_t grid = (rows + kWaves * R - 1) / (kWaves * R);
-        hipLaunchKernelGGL((q8_0_matvec_kernel<B, R, 1>), dim3((unsigned)grid), dim3(kThreads), lds, s, w, rows,
-                           (uint32_t)(cols / 32), act, y, ldy, key);
+template <typename K>
+static hipError_t launch_one(K kernel, const MvArgs& a, size_t lds, hipStream_t s) {
+    static size_t lds_set = 64 * 1024;  // above 64 KB the kernel must opt in
+    if (lds > lds_set) {
+        const hipError_t e =
+            hipFuncSetAttribute((const void*)kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return e;
+        lds_set = lds;
     }
+    const uint32_t want = (a.ntiles + kMvWaves - 1) / kMvWaves;
+    const uint32_t cap = 2u * (uint32_t)device_cus();
+    const uint32_t grid = want < cap ? want : cap;
+    hipLaunchKernelGGL(kernel, dim3(grid), dim3(kMvWaves * 64), lds, s, a);
     return hipGetLastError();
 }
 
-static ActPlanes offset_planes(const ActPlanes& a, uint32_t wtype, uint64_t cols, uint64_t b0) {
-    ActPlanes o;
-    const uint64_t bs = wtype == kQ8_0 ? 32 : 256;
-    o.q = a.q + b0 * cols;
-    o.d = a.d + b0 * (cols / bs);
-    o.bsum = a.bsum ? a.bsum + b0 * (cols / 16) : nullptr;
-    o.bad = a.bad + b0 * (cols / bs);
-    return o;
-}
-
-hipError_t launch_matvec(uint32_t wtype, const uint8_t* w, uint64_t rows, uint64_t cols, const ActPlanes* act,
-                         uint64_t batch, float* y, uint64_t ldy, unsigned long long* argmax_key, hipStream_t s) {
-    // Columns are processed in groups small enough for the LDS staging.
+hipError_t launch_matvec(uint32_t wtype, const uint8_t* w, uint64_t rows, uint64_t cols, const float* x,
+                         const ActPlanes* pre, uint64_t batch, float* y, uint64_t ldy,
+                         unsigned long long* argmax_key, unsigned long long* err_word, int32_t* dbg_isum,
+                         int32_t* dbg_imin, hipStream_t s) {
+    const uint32_t bs = wtype == kQ8_0 ? 32 : 256;
+    if (rows == 0 || cols == 0 || cols % bs != 0 || rows > 0xffffffffull - kTileRows || cols > (1u << 30))
+        return hipErrorInvalidValue;
+    if (dbg_isum && batch > 8) return hipErrorInvalidValue;
     uint64_t b0 = 0;
     while (b0 < batch) {
-        uint64_t nbat = batch - b0 < 8 ? batch - b0 : 8;
-        while (nbat > 1 && matvec_lds(wtype, nbat, cols) > kMaxLds) --nbat;
-        if (matvec_lds(wtype, nbat, cols) > kMaxLds) return hipErrorInvalidValue;
-        const ActPlanes a = offset_planes(*act, wtype, cols, b0);
-        float* yb = y + b0 * ldy;
-        unsigned long long* kb = argmax_key ? argmax_key + b0 : nullptr;
+        uint32_t nbat = (uint32_t)(batch - b0 < 8 ? batch - b0 : 8);
+        while (nbat > 1 && lds_map(wtype, (uint32_t)cols, nbat).total > kMaxLds) --nbat;
+        const size_t lds = lds_map(wtype, (uint32_t)cols, nbat).total;
+        if (lds > kMaxLds) return hipErrorInvalidValue;
+        MvArgs a{};
+        a.w = w;
+        a.rows = (uint32_t)rows;
+        a.nb = (uint32_t)(cols / bs);
+        a.ntiles = (uint32_t)layout_tiles(rows);
+        a.nchunks = (uint32_t)layout_chunks_per_tile(wtype, cols);
+        a.batch = nbat;
+        a.cols = (uint32_t)cols;
+        a.x = x ? x + b0 * cols : nullptr;
+        if (pre) {
+            a.pre.q = pre->q + b0 * cols;
+            a.pre.d = pre->d + b0 * (cols / bs);
+            a.pre.bsum = pre->bsum ? pre->bsum + b0 * (cols / 16) : nullptr;
+            a.pre.bad = pre->bad + b0 * (cols / bs);
+        }
+        a.y = y + b0 * ldy;
+        a.ldy = ldy;
+        a.argmax_key = argmax_key ? argmax_key + b0 : nullptr;
+        a.err_word = err_word;
+        a.err_column0 = (uint32_t)b0;
+        a.dbg_isum = b0 == 0 ? dbg_isum : nullptr;  // column 0 only
+        a.dbg_imin = b0 == 0 ? dbg_imin : nullptr;
         hipError_t e;
-        switch (nbat) {
-            case 1: e = launch_b<1>(wtype, w, rows, cols, a, yb, ldy, kb, s); break;
-            case 2: e = launch_b<2>(wtype, w, rows, cols, a, yb, ldy, kb, s); break;
-            case 3: e = launch_b<3>(wtype, w, rows, cols, a, yb, ldy, kb, s); break;
-            case 4: e = launch_b<4>(wtype, w, rows, cols, a, yb, ldy, kb, s); break;
-            case 5: e = launch_b<5>(wtype, w, rows, cols, a, yb, ldy, kb, s); break;
-            case 6: e = launch_b<6>(wtype, w, rows, cols, a, yb, ldy, kb, s); break;
-            case 7: e = launch_b<7>(wtype, w, rows, cols, a, yb, ldy, kb, s); break;
-            default: e = launch_b<8>(wtype, w, rows, cols, a, yb, ldy, kb, s); break;
+        constexpr int W = kMvWaves;
+        const bool dbg = a.dbg_isum != nullptr;
+        if (wtype == kQ4_K) {
+            if (nbat == 1)
+                e = dbg ? launch_one(q4k_mv_small_kernel<W, 8, 1, true>, a, lds, s)
+                        : launch_one(q4k_mv_small_kernel<W, 8, 1, false>, a, lds, s);
+            else if (nbat == 2)
+                e = dbg ? launch_one(q4k_mv_small_kernel<W, 8, 2, true>, a, lds, s)
+                        : launch_one(q4k_mv_small_kernel<W, 8, 2, false>, a, lds, s);
+            else
+                e = dbg ? launch_one(q4k_mv_kernel<W, 8, true>, a, lds, s)
+                        : launch_one(q4k_mv_kernel<W, 8, false>, a, lds, s);
+        } else if (wtype == kQ6_K) {
+            e = dbg ? launch_one(q6k_mv_kernel<W, 4, true>, a, lds, s)
+                    : launch_one(q6k_mv_kernel<W, 4, false>, a, lds, s);
+        } else {
+            e = dbg ? launch_one(q8_0_mv_kernel<W, 8, true>, a, lds, s)
+                    : launch_one(q8_0_mv_kernel<W, 8, false>, a, lds, s);
         }
         if (e != hipSuccess) return e;
         b0 += nbat;
     }
     return hipSuccess;
-}
-
-// ---------------------------------------------------------------------------
-// Exact per-(row, block) integer sums against activation column 0, through
-// the same lane decoders as the matvec kernels.  One wave per row, eight
-// blocks (Q8_0: 32) per step.
-// ---------------------------------------------------------------------------
-__global__ __launch_bounds__(64) void block_sums_kernel(uint32_t wtype, const uint8_t* __restrict__ W, uint64_t rows,
-                                                        uint32_t nb, ActPlanes act, int32_t* isum, int32_t* imin) {
-    const uint64_t row = blockIdx.x;
-    const int lane = threadIdx.x;
-    if (wtype == kQ8_0) {
-        const int half = lane & 1;
-        for (uint32_t base = 0; base < nb; base += 32) {
-            const uint32_t blk = base + (lane >> 1);
-            int32_t I = 0;
-            if (blk < nb) {
-                const uint4 w = *(const uint4*)(W + (row * nb + blk) * 32 + 16 * half);
-                I = q8_0_ints(w, act.q + blk * 32 + 16 * half);
-            }
-            I += __shfl_xor(I, 1, 64);
-            if (blk < nb && half == 0) {
-                isum[row * nb + blk] = I;
-                imin[row * nb + blk] = 0;
-            }
-        }
-        return;
-    }
-    const int c = lane & 7, bi = lane >> 3;
-    const uint64_t nq = rows * nb;
-    for (uint32_t base = 0; base < nb; base += 8) {
-        const uint32_t blk = base + bi;
-        int32_t I = 0, M = 0;
-        if (blk < nb) {
-            const uint64_t q = row * nb + blk;
-            if (wtype == kQ4_K) {
-                const uint8_t* b = W + q * 144;
-                const Q4KLane L = q4k_lane(*(const uint4*)b, *(const uint4*)(b + 16 + 16 * c), c);
-                int32_t bs32[8];
-#pragma unroll
-                for (int s = 0; s < 8; ++s) bs32[s] = (int32_t)act.bsum[blk * 16 + 2 * s] + act.bsum[blk * 16 + 2 * s + 1];
-                q4k_ints(L, act.q + blk * 256, bs32, c, I, M);
-            } else {
-                const int qh_chunk = 2 * (c >> 2) + (c & 1);
-                const Q6KLane L = q6k_lane(*(const uint4*)(W + q * 128 + 16 * c),
-                                           *(const uint4*)(W + nq * 128 + q * 64 + 16 * qh_chunk),
-                                           *(const uint4*)(W + nq * 192 + q * 16),
-                                           ((const uint16_t*)(W + nq * 208))[q], c);
-                int32_t bs16[16];
-#pragma unroll
-                for (int s = 0; s < 16; ++s) bs16[s] = act.bsum[blk * 16 + s];
-                I = q6k_ints(L, act.q + blk * 256, bs16, c);
-            }
-        }
-        I = group8_sum(I);
-        M = group8_sum(M);
-        if (blk < nb && c == 0) {
-            isum[row * nb + blk] = I;
-            imin[row * nb + blk] = M;
-        }
-    }
-}
-
-hipError_t launch_block_sums(uint32_t wtype, const uint8_t* w, uint64_t rows, uint64_t cols, const ActPlanes* act,
-                             int32_t* isum, int32_t* imin, hipStream_t s) {
-    const uint32_t nb = (uint32_t)(cols / (wtype == kQ8_0 ? 32 : 256));
-    hipLaunchKernelGGL(block_sums_kernel, dim3((unsigned)rows), dim3(64), 0, s, wtype, w, rows, nb, *act, isum, imin);
-    return hipGetLastError();
 }
 
 // ---------------------------------------------------------------------------

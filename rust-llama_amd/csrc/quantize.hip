@@ -11,6 +11,7 @@
 // (HIP's default for f32).
 #include "rlq_device.hpp"
 #include "rlq_internal.hpp"
+#include "rlq_layout.hpp"
 
 namespace rlq {
 
@@ -666,62 +667,34 @@ hipError_t launch_dequantize(uint32_t t, const uint8_t* b, uint64_t n, float* y,
 }
 
 // ---------------------------------------------------------------------------
-// GGUF -> device layout
-//   Q4_K : unchanged (144-byte blocks are 16-byte aligned when rows are)
-//   Q6_K : four planes over the whole matrix, block index q = row*nb + blk:
-//          ql [q][128] | qh [q][64] | scales [q][16] | d [q] (f16)
-//   Q8_0 : qs [q][32] | d [q] (f16)
-// Every plane offset is a multiple of 16 bytes.
+// GGUF -> tiled device layout (rlq_layout.hpp).  One thread per source byte;
+// the destination is zeroed first, which fills the padding rows of the last
+// tile and the missing odd Q8_0 block.
 // ---------------------------------------------------------------------------
-uint64_t device_bytes(uint32_t t, uint64_t rows, uint64_t cols) {
-    if (t == kQ4_K) return rows * (cols / 256) * 144;
-    if (t == kQ6_K) return rows * (cols / 256) * 210;
-    return rows * (cols / 32) * 34;
+__global__ __launch_bounds__(256) void fill_zero16_kernel(uint4* __restrict__ p, uint64_t n16) {
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += (uint64_t)gridDim.x * blockDim.x)
+        p[i] = make_uint4(0, 0, 0, 0);
 }
 
-__global__ __launch_bounds__(256) void repack_q6k_kernel(const uint8_t* __restrict__ src, uint64_t nblocks,
-                                                         uint8_t* __restrict__ dst) {
-    // one thread per 2-byte unit of a block: 105 units per block
-    const uint64_t total = nblocks * 105;
-    for (uint64_t u = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; u < total;
-         u += (uint64_t)gridDim.x * blockDim.x) {
-        const uint64_t q = u / 105;
-        const int k = (int)(u % 105) * 2;
-        const uint8_t* b = src + q * 210;
-        uint8_t* dstp;
-        if (k < 128) dstp = dst + q * 128 + k;
-        else if (k < 192) dstp = dst + nblocks * 128 + q * 64 + (k - 128);
-        else if (k < 208) dstp = dst + nblocks * 192 + q * 16 + (k - 192);
-        else dstp = dst + nblocks * 208 + q * 2;
-        dstp[0] = b[k];
-        dstp[1] = b[k + 1];
-    }
-}
-
-__global__ __launch_bounds__(256) void repack_q8_0_kernel(const uint8_t* __restrict__ src, uint64_t nblocks,
-                                                          uint8_t* __restrict__ dst) {
-    const uint64_t total = nblocks * 17;
-    for (uint64_t u = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; u < total;
-         u += (uint64_t)gridDim.x * blockDim.x) {
-        const uint64_t q = u / 17;
-        const int k = (int)(u % 17) * 2;
-        const uint8_t* b = src + q * 34;
-        uint8_t* dstp = k == 0 ? dst + nblocks * 32 + q * 2 : dst + q * 32 + (k - 2);
-        dstp[0] = b[k];
-        dstp[1] = b[k + 1];
+__global__ __launch_bounds__(256) void repack_tiled_kernel(uint32_t t, const uint8_t* __restrict__ src, uint64_t rows,
+                                                           uint64_t nb, uint32_t ts, uint8_t* __restrict__ dst) {
+    const uint64_t per_row = nb * ts, total = rows * per_row;
+    for (uint64_t e = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
+         e += (uint64_t)gridDim.x * blockDim.x) {
+        const uint64_t row = e / per_row, rem = e % per_row, blk = rem / ts;
+        const uint32_t byte = (uint32_t)(rem % ts);
+        dst[layout_offset(t, row, blk, byte, nb)] = src[e];
     }
 }
 
 hipError_t launch_repack(uint32_t t, const uint8_t* gguf, uint64_t rows, uint64_t cols, uint8_t* dev,
                          hipStream_t s) {
-    const uint64_t bytes = device_bytes(t, rows, cols);
-    if (t == kQ4_K) return hipMemcpyAsync(dev, gguf, bytes, hipMemcpyDeviceToDevice, s);
-    const uint64_t nblocks = rows * (cols / (t == kQ6_K ? 256 : 32));
-    const uint64_t units = nblocks * (t == kQ6_K ? 105 : 17);
-    const uint64_t grid = (units + 255) / 256;
-    const unsigned g = (unsigned)(grid < 65536 ? grid : 65536);
-    if (t == kQ6_K) hipLaunchKernelGGL(repack_q6k_kernel, dim3(g), dim3(256), 0, s, gguf, nblocks, dev);
-    else hipLaunchKernelGGL(repack_q8_0_kernel, dim3(g), dim3(256), 0, s, gguf, nblocks, dev);
+    const uint64_t n16 = layout_bytes(t, rows, cols) / 16;
+    hipLaunchKernelGGL(fill_zero16_kernel, dim3(2048), dim3(256), 0, s, (uint4*)dev, n16);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const uint32_t bs = t == kQ8_0 ? 32 : 256, ts = t == kQ8_0 ? 34 : (t == kQ4_K ? 144 : 210);
+    hipLaunchKernelGGL(repack_tiled_kernel, dim3(8192), dim3(256), 0, s, t, gguf, rows, cols / bs, ts, dev);
     return hipGetLastError();
 }
 

@@ -48,28 +48,27 @@ hipError_t launch_act_from_gguf(uint32_t act_type, const uint8_t* gguf, uint64_t
 hipError_t launch_finite_scan(const float* x, uint64_t n, unsigned long long* err_word, hipStream_t s);
 // Decoders (decode.rs), GGUF bytes in.
 hipError_t launch_dequantize(uint32_t dtype, const uint8_t* b, uint64_t n, float* y, hipStream_t s);
-// GGUF -> device layout.  Q4_K keeps the GGUF layout (plain copy).
+// GGUF -> tiled device layout (rlq_layout.hpp); `dev` holds layout_bytes().
 hipError_t launch_repack(uint32_t dtype, const uint8_t* gguf, uint64_t rows, uint64_t cols, uint8_t* dev,
                          hipStream_t s);
 hipError_t launch_fill_u64(unsigned long long* p, uint64_t n, unsigned long long v, hipStream_t s);
 
 // ---- matvec.hip ----
-// y[b*ldy + r] = dot(row r, activation column b) for b < batch <= 8.
-// `argmax_key` (may be null) receives, per column, the packed greedy-argmax
-// key of y (see matvec.hip).  Rows are skipped entirely when any activation
-// block carries the NaN error mark.
-hipError_t launch_matvec(uint32_t wtype, const uint8_t* w, uint64_t rows, uint64_t cols, const ActPlanes* act,
-                         uint64_t batch, float* y, uint64_t ldy, unsigned long long* argmax_key,
-                         hipStream_t s);
-// Exact per-(row, block) integer sums of the weights against activation
-// column 0 (the debug view of the dot's integer part).
-hipError_t launch_block_sums(uint32_t wtype, const uint8_t* w, uint64_t rows, uint64_t cols,
-                             const ActPlanes* act, int32_t* isum, int32_t* imin, hipStream_t s);
+// y[b*ldy + r] = dot(row r, activation column b) for every b < batch, in
+// launches of up to 8 columns.  The activations are quantized in the kernel
+// prologue from f32 `x` ([batch][cols]) or taken from `pre` when x is null.
+// A data error in the activations goes to `err_word` (column index in the
+// key) and suppresses every output of the launch that found it.
+// `argmax_key` (may be null) receives per column the packed greedy-argmax key
+// (see matvec.hip).  With `dbg_isum`/`dbg_imin` (batch <= 8) the kernel that
+// serves this batch size also stores the exact per-(row, block) integers of
+// column 0's dot.
+hipError_t launch_matvec(uint32_t wtype, const uint8_t* w, uint64_t rows, uint64_t cols, const float* x,
+                         const ActPlanes* pre, uint64_t batch, float* y, uint64_t ldy,
+                         unsigned long long* argmax_key, unsigned long long* err_word, int32_t* dbg_isum,
+                         int32_t* dbg_imin, hipStream_t s);
 // Decode argmax keys into u32 indices.
 hipError_t launch_argmax_finish(const unsigned long long* keys, uint64_t batch, const float* y, uint64_t ldy,
                                 uint32_t* out, hipStream_t s);
-
-// Device layout byte count of a rows x cols matrix (equal to the GGUF size).
-uint64_t device_bytes(uint32_t dtype, uint64_t rows, uint64_t cols);
 
 }  // namespace rlq

@@ -1,0 +1,81 @@
+// rlq_layout.hpp - device layout of weights kept in HBM.
+//
+// Rows are grouped into tiles of 16 (the N dimension of one
+// v_mfma_i32_16x16x64_i8); the last tile is zero-padded.  For every
+// (tile, block) the sixteen rows' GGUF blocks are rearranged into one
+// contiguous chunk whose 16-byte pieces sit in the order the 64 lanes of a
+// wave load them, so each load instruction of the decode kernels reads 1 KB
+// (or 256 B for per-row headers) of consecutive bytes.  Lane l of a wave
+// works on row n = l % 16 and K quarter kq = l / 16 of the chunk.
+//
+// Q4_K, chunk of 2304 B per (tile, block):
+//   [P*1024 + l*16, +16)  qs bytes 32g + 16h .. +15 of row n, where P = 0, 1,
+//                         g = 2P + kq/2, h = kq%2 (low nibbles: sub-block 2g,
+//                         high nibbles: sub-block 2g+1, positions 16h..16h+15)
+//   [2048 + n*16, +16)    d, dmin, scales[12] of row n (GGUF bytes 0..15)
+// Q6_K, chunk of 3360 B per (tile, block):
+//   [h*1024 + l*16, +16)  ql bytes 32kq + 16h .. +15 of row n
+//   [2048 + n*64, +64)    qh[64] of row n
+//   [3072 + n*16, +16)    scales[16] of row n
+//   [3328 + n*2, +2)      d of row n
+// Q8_0, chunk of 1088 B per (tile, block pair p):
+//   [l*16, +16)           qs bytes 16(kq%2) .. +15 of block 2p + kq/2, row n
+//   [1024 + n*4, +4)      d of blocks 2p and 2p+1 of row n (a missing
+//                         block 2p+1, when the row has an odd block count,
+//                         is all zero)
+#pragma once
+
+#include <stdint.h>
+
+namespace rlq {
+
+constexpr uint32_t kTileRows = 16;
+constexpr uint32_t kQ4KChunk = 2304;
+constexpr uint32_t kQ6KChunk = 3360;
+constexpr uint32_t kQ80Chunk = 1088;
+
+__host__ __device__ inline uint64_t layout_tiles(uint64_t rows) { return (rows + kTileRows - 1) / kTileRows; }
+
+// Chunks per tile (blocks, or block pairs for Q8_0) and chunk size.
+__host__ __device__ inline uint64_t layout_chunks_per_tile(uint32_t t, uint64_t cols) {
+    return t == 8 ? (cols / 32 + 1) / 2 : cols / 256;
+}
+__host__ __device__ inline uint64_t layout_chunk_bytes(uint32_t t) {
+    return t == 12 ? kQ4KChunk : (t == 14 ? kQ6KChunk : kQ80Chunk);
+}
+__host__ __device__ inline uint64_t layout_bytes(uint32_t t, uint64_t rows, uint64_t cols) {
+    return layout_tiles(rows) * layout_chunks_per_tile(t, cols) * layout_chunk_bytes(t);
+}
+
+// Offset in the device layout of byte `byte` of GGUF block `blk` of row `row`
+// (nb = GGUF blocks per row).
+__host__ __device__ inline uint64_t layout_offset(uint32_t t, uint64_t row, uint64_t blk, uint32_t byte,
+                                                  uint64_t nb) {
+    const uint64_t tile = row / kTileRows;
+    const uint32_t n = (uint32_t)(row % kTileRows);
+    if (t == 12) {
+        const uint64_t base = (tile * nb + blk) * kQ4KChunk;
+        if (byte < 16) return base + 2048 + n * 16 + byte;
+        const uint32_t q = byte - 16, g = q / 32, j = q % 32, h = j / 16, i = j % 16;
+        const uint32_t P = g / 2, kq = 2 * (g % 2) + h;
+        return base + P * 1024 + (16 * kq + n) * 16 + i;
+    }
+    if (t == 14) {
+        const uint64_t base = (tile * nb + blk) * kQ6KChunk;
+        if (byte < 128) {
+            const uint32_t kq = byte / 32, w = byte % 32, h = w / 16, i = w % 16;
+            return base + h * 1024 + (16 * kq + n) * 16 + i;
+        }
+        if (byte < 192) return base + 2048 + n * 64 + (byte - 128);
+        if (byte < 208) return base + 3072 + n * 16 + (byte - 192);
+        return base + 3328 + n * 2 + (byte - 208);
+    }
+    const uint64_t np = (nb + 1) / 2, p = blk / 2;
+    const uint32_t which = (uint32_t)(blk % 2);
+    const uint64_t base = (tile * np + p) * kQ80Chunk;
+    if (byte < 2) return base + 1024 + n * 4 + 2 * which + byte;
+    const uint32_t j = byte - 2, kq = 2 * which + j / 16, i = j % 16;
+    return base + (16 * kq + n) * 16 + i;
+}
+
+}  // namespace rlq

@@ -102,6 +102,8 @@ def test_matvec_golden_q8_0():
         assert rel_l2(y, r.generic) <= REL_L2, i
         tol = elem_tol(r.dtype, r.weights, r.rows, O.quantize(O.Q8_0, r.x), r.cols, r.native)
         assert np.all(np.abs(y - r.native) <= tol), i
+        # Q8_0 adds the block terms in the reference's order: bit-exact
+        assert np.array_equal(y.view(np.uint32), r.generic.view(np.uint32)), i
 
 
 # ------------------------------------------------------------ exact integer parts
@@ -110,17 +112,22 @@ def _weights(t, rows, cols, seed):
     return rlq.quantize(t, randn(seed, rows * cols, 0.02))
 
 
-@pytest.mark.parametrize("t,rows,cols", [(DT.Q4_K, 300, 4096), (DT.Q6_K, 300, 4096), (DT.Q8_0, 300, 896),
-                                         (DT.Q4_K, 7, 768), (DT.Q6_K, 5, 2304)])
-def test_block_sums_bit_exact(ctx, t, rows, cols):
-    say("block sums", t, rows, cols)
+@pytest.mark.parametrize("t,rows,cols,batch", [
+    (DT.Q4_K, 300, 4096, 1), (DT.Q4_K, 300, 4096, 2), (DT.Q4_K, 300, 4096, 3), (DT.Q4_K, 300, 4096, 8),
+    (DT.Q6_K, 300, 4096, 1), (DT.Q6_K, 300, 4096, 5), (DT.Q8_0, 300, 896, 1), (DT.Q8_0, 300, 896, 8),
+    (DT.Q8_0, 21, 96, 3), (DT.Q4_K, 7, 768, 1), (DT.Q4_K, 7, 768, 4), (DT.Q6_K, 5, 2304, 1)])
+def test_block_sums_bit_exact(ctx, t, rows, cols, batch):
+    """Exact per-block integers of column 0 inside every kernel variant (the
+    batch size picks the kernel: Q4_K 1-2 VALU dot4, 3-8 MFMA; Q6_K 5-8 two
+    column groups; Q8_0 with an odd block count)."""
+    say("block sums", t, rows, cols, batch)
     w = _weights(t, rows, cols, 100 + rows)
-    x = randn(200 + rows, cols)
+    x = randn(200 + rows, batch * cols).reshape(batch, cols)
     W = rlq.Weights(ctx, t, w, rows, cols)
     isum, imin = ctx.block_sums(W, torch.from_numpy(x).cuda())
     torch.cuda.synchronize()
     at = O.matvec_activation_dtype(int(t))
-    act = O.quantize(at, x)
+    act = O.quantize(at, x[0])
     nb = cols // O.BLOCK[int(t)]
     stride = w.size // rows
     want_i = np.zeros((rows, nb), np.int32)
@@ -160,6 +167,8 @@ def test_matmul_batches_against_oracle(ctx, t, rows, cols, batch):
     got = y.cpu().numpy()
     for b in range(batch):
         assert rel_l2(got[b], want[b]) <= REL_L2, b
+    if t == DT.Q8_0:  # block terms added in the reference's order: bit-exact
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
 
 
 # ------------------------------------------------------------ the benchmark shapes
