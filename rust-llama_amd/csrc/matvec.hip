@@ -57,6 +57,14 @@ __device__ __forceinline__ i32x4 hi_nibbles(uint4 v) {
                  (int)((v.w >> 4) & 0x0f0f0f0fu)};
 }
 
+// High nibbles of 16 bytes with two 64-bit shifts: bits shifted across the
+// word boundary land in the masked-off high nibble of byte 3.
+__device__ __forceinline__ void hi_nibbles64(uint4 v, uint32_t (&o)[4]) {
+    const uint64_t a = ((((uint64_t)v.y << 32) | v.x) >> 4) & 0x0f0f0f0f0f0f0f0full;
+    const uint64_t b = ((((uint64_t)v.w << 32) | v.z) >> 4) & 0x0f0f0f0f0f0f0f0full;
+    o[0] = (uint32_t)a, o[1] = (uint32_t)(a >> 32), o[2] = (uint32_t)b, o[3] = (uint32_t)(b >> 32);
+}
+
 __device__ __forceinline__ int32_t dot2(uint32_t a, uint32_t b, int32_t c) {
     return __builtin_amdgcn_sdot2(__builtin_bit_cast(i16x2, a), __builtin_bit_cast(i16x2, b), c, false);
 }
@@ -176,9 +184,103 @@ __device__ __forceinline__ void prefetch_unit(const MvArgs& a, uint32_t wave, fl
     if (a.x && u < (a.cols / 16) * a.batch) load_unit(a, u, v);
 }
 
-// Q8_K (activation.rs:4-51) of all batch columns.  A 16-lane row quantizes
-// one 256-value block, 16 values per lane (one bsum group per lane).
-// Returns false in every thread when any block of any column is invalid.
+__device__ __forceinline__ float row16_min(float v) {
+    v = fminf(v, dpp_f<kQuadXor1>(v));
+    v = fminf(v, dpp_f<kQuadXor2>(v));
+    v = fminf(v, dpp_f<kRowHalfMirror>(v));
+    return fminf(v, dpp_f<kRowMirror>(v));
+}
+
+// One Q8_K block (activation.rs:4-51) quantized by the 16 lanes of a DPP row;
+// lane r16 holds values 16 r16 .. 16 r16 + 15 of the block.  Every branch
+// below is uniform over the row.
+//  - Non-finite input: an FMA chain with 0 turns any inf/NaN into NaN; only
+//    then is the first non-finite index searched (NonFiniteInput{index}).
+//  - inverse_scale keeps the FIRST value of largest |x|.  With the row's max
+//    and min, the sign of that value is known unless both +amax and -amax
+//    occur; only then is the first such index searched.
+//  - q = round_ties_even(inverse * x): the product is rounded to f32 first,
+//    then adding 1.5 * 2^23 rounds it to an integer (ties to even) that sits
+//    in the low mantissa bits, whose low byte is q as int8.  |inverse * x| <=
+//    127 (1 + 2^-23)^2 < 127.5, so q <= 127 and the reference's min(127) never
+//    applies.
+struct Q8KRow {
+    uint32_t q[4];
+    float d;
+    int32_t bsum;     // sum of this lane's 16 q
+    int kind;         // -1 valid, kKindNonFinite, kKindScale
+    uint32_t index;   // NonFiniteInput index within the block
+};
+
+__device__ __forceinline__ Q8KRow q8k_row16(const float (&v)[16], uint32_t r16) {
+    Q8KRow o;
+    o.q[0] = o.q[1] = o.q[2] = o.q[3] = 0;
+    o.d = 0.0f;
+    o.bsum = 0;
+    o.kind = -1;
+    o.index = 0;
+    float t = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) t = __builtin_fmaf(v[k], 0.0f, t);
+    if (row16_umin(t == t ? 1u : 0u) == 0) {
+        uint32_t nf = 0xffffffffu;
+#pragma unroll
+        for (int k = 15; k >= 0; --k)
+            if (!finite(v[k])) nf = 16 * r16 + k;
+        o.kind = kKindNonFinite;
+        o.index = row16_umin(nf);
+        return o;
+    }
+    float mx = __builtin_fmaxf(v[0], v[1]), mn = __builtin_fminf(v[0], v[1]);
+#pragma unroll
+    for (int k = 2; k < 16; k += 2) {
+        mx = fmaxf(mx, fmaxf(v[k], v[k + 1]));
+        mn = fminf(mn, fminf(v[k], v[k + 1]));
+    }
+    mx = row16_max(mx);
+    mn = row16_min(mn);
+    float maximum;
+    if (mx > -mn) {
+        maximum = mx;
+    } else if (-mn > mx) {
+        maximum = mn;
+    } else if (mx == 0.0f) {
+        return o;  // all zero: canonical zero block
+    } else {      // +amax and -amax both occur: the first one wins
+        uint32_t key = 0xffffffffu;
+#pragma unroll
+        for (int k = 15; k >= 0; --k)
+            if (fabsf(v[k]) == mx) key = (16 * r16 + k) << 1 | (__float_as_uint(v[k]) >> 31);
+        maximum = (row16_umin(key) & 1u) ? mn : mx;
+    }
+    const float inverse = -127.0f / maximum;
+    if (!finite(inverse) || !finite(1.0f / inverse)) {
+        o.kind = kKindScale;
+        return o;
+    }
+    uint32_t b[16];
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+        const float r = inverse * v[k];
+        b[k] = __float_as_uint(r + 12582912.0f);
+    }
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+        const uint32_t lo = __builtin_amdgcn_perm(b[4 * w + 1], b[4 * w], 0x0c0c0400u);
+        const uint32_t hi = __builtin_amdgcn_perm(b[4 * w + 3], b[4 * w + 2], 0x04000c0cu);
+        o.q[w] = lo | hi;
+    }
+    int32_t sum = dot4(o.q[0], 0x01010101u, 0);
+    sum = dot4(o.q[1], 0x01010101u, sum);
+    sum = dot4(o.q[2], 0x01010101u, sum);
+    o.bsum = dot4(o.q[3], 0x01010101u, sum);
+    o.d = 1.0f / inverse;
+    return o;
+}
+
+// Q8_K of all batch columns into LDS.  A 16-lane row quantizes one 256-value
+// block, 16 values per lane (one bsum group per lane).  Returns false in
+// every thread when any block of any column is invalid.
 template <int W, bool BSUMS>
 __device__ __forceinline__ bool stage_q8k(const MvArgs& a, uint8_t* lds, const LdsMap& L, uint32_t wave, const float (&v0)[16]) {
     const uint32_t K = a.cols, upc = K / 16, units = upc * a.batch;
@@ -187,7 +289,7 @@ __device__ __forceinline__ bool stage_q8k(const MvArgs& a, uint8_t* lds, const L
     for (uint32_t base = wave * 64; base < units; base += W * 64) {
         const uint32_t u = base + lane;
         if (u >= units) continue;  // whole 16-lane rows drop out together (units % 16 == 0)
-        const uint32_t b = u / upc, e0 = (u % upc) * 16, blk = e0 / 256, in_blk = e0 % 256;
+        const uint32_t b = u / upc, e0 = (u % upc) * 16, blk = e0 / 256;
         float v[16];
         if (base == wave * 64) {
 #pragma unroll
@@ -195,61 +297,21 @@ __device__ __forceinline__ bool stage_q8k(const MvArgs& a, uint8_t* lds, const L
         } else {
             load_unit(a, u, v);
         }
-        // NonFiniteInput: first index of the block
-        uint32_t nf = 0xffffffffu;
-#pragma unroll
-        for (int k = 15; k >= 0; --k)
-            if (!finite(v[k])) nf = in_blk + k;
-        nf = row16_umin(nf);
-        const bool nonfinite = nf != 0xffffffffu;
-        // inverse_scale: the first value of largest magnitude (strict `>`)
-        float am = 0.0f;
-        uint32_t ai = 0, sg = 0;
-#pragma unroll
-        for (int k = 0; k < 16; ++k)
-            if (fabsf(v[k]) > am) {
-                am = fabsf(v[k]);
-                ai = in_blk + k;
-                sg = __float_as_uint(v[k]) >> 31;
-            }
-        const float amax = row16_max(nonfinite ? 0.0f : am);
-        const uint32_t key = row16_umin((am == amax && amax > 0.0f) ? (ai << 1 | sg) : 0xffffffffu);
-        float inverse = 0.0f;
-        if (amax > 0.0f && !nonfinite) inverse = -127.0f / ((key & 1u) ? -amax : amax);
-        // preflight_q8k: the scale and its reciprocal must be finite
-        const bool scale_bad = !nonfinite && (!finite(inverse) || (inverse != 0.0f && !finite(1.0f / inverse)));
-        const bool invalid = nonfinite || scale_bad;
-        if (invalid) {
+        const Q8KRow o = q8k_row16(v, r16);
+        if (o.kind >= 0) {
             bad = 1;
             if (r16 == 0)
-                report_error(a.err_word, nonfinite ? error_key(a.err_column0 + b, kKindNonFinite, blk * 256ull + nf)
-                                                   : error_key(a.err_column0 + b, kKindScale, blk));
+                report_error(a.err_word, o.kind == kKindNonFinite
+                                             ? error_key(a.err_column0 + b, kKindNonFinite, blk * 256ull + o.index)
+                                             : error_key(a.err_column0 + b, kKindScale, blk));
         }
-        // encode_q8k: q = min(rint(inverse * x), 127), bsum of 16, d = 1 / inverse
-        uint32_t qw[4] = {0, 0, 0, 0};
-        if (inverse != 0.0f && !invalid) {
-#pragma unroll
-            for (int k = 0; k < 16; ++k) {
-                int32_t q = (int32_t)__builtin_rintf(inverse * v[k]);
-                q = q < 127 ? q : 127;
-                qw[k / 4] |= ((uint32_t)q & 0xffu) << (8 * (k % 4));
-            }
-        }
-        *(uint4*)(lds + b * L.S + e0) = make_uint4(qw[0], qw[1], qw[2], qw[3]);
-        if (r16 == 0) *(float*)(lds + L.d_off + (blk * 8 + b) * 4) = (inverse != 0.0f && !invalid) ? 1.0f / inverse : 0.0f;
-        if (BSUMS) {  // bsums[g] = sum of the 16 q of group g (activation.rs:43-47)
-            int32_t s = dot4(qw[0], 0x01010101u, 0);
-            s = dot4(qw[1], 0x01010101u, s);
-            s = dot4(qw[2], 0x01010101u, s);
-            s = dot4(qw[3], 0x01010101u, s);
-            *(int16_t*)(lds + L.bs_off + (blk * 8 + b) * 32 + bs_slot(r16) * 2) = (int16_t)s;
-        }
+        *(uint4*)(lds + b * L.S + e0) = make_uint4(o.q[0], o.q[1], o.q[2], o.q[3]);
+        if (r16 == 0) *(float*)(lds + L.d_off + (blk * 8 + b) * 4) = o.d;
+        if (BSUMS) *(int16_t*)(lds + L.bs_off + (blk * 8 + b) * 32 + bs_slot(r16) * 2) = (int16_t)o.bsum;
     }
     return __syncthreads_or(bad) == 0;
 }
 
-// Q8_0 (encode.rs:115-126, 151-192) of all batch columns: two lanes per
-// 32-value block.
 template <int W>
 __device__ __forceinline__ bool stage_q8_0(const MvArgs& a, uint8_t* lds, const LdsMap& L, uint32_t wave, const float (&v0)[16]) {
     const uint32_t K = a.cols, upc = K / 16, units = upc * a.batch;
@@ -517,22 +579,66 @@ __global__ __launch_bounds__(W * 64) void q4k_mv_kernel(MvArgs a) {
     publish_argmax(a, b0 + 1, best1);
 }
 
-// Q4_K, one or two columns: v_dot4_i32_i8 on the VALU.  Lane (n, kq), kq =
-// 2g + h, multiplies half h of sub-blocks 2g, 2g+1 (qs bytes of w0) and
-// 2g+4, 2g+5 (w1) of row n; its integer partials and its share of the mins
-// (the bsums of exactly those 16-value groups) are scaled per block, and the
-// four K quarters of a row are added once per tile.
-template <int W, int D, int B, bool DBG>
+// Q4_K, one or two columns: v_dot4_i32_i8 on the VALU.
+//
+// A workgroup of W waves works on TS = W / KS tiles at a time; the KS waves of
+// a tile take its blocks kp, kp + KS, ... (kp = the wave's K part), so a tile's
+// bytes stream through KS waves and every SIMD holds several waves.  Lane
+// (n, kq), kq = 2g + h, multiplies half h of sub-blocks 2g, 2g+1 (qs bytes of
+// w0) and 2g+4, 2g+5 (w1) of row n; its integer partials and its share of the
+// mins (the bsums of exactly those 16-value groups) are scaled per block.  At
+// the end of a tile the wave adds its four K quarters and parks the row sums
+// in LDS; after the last tile the workgroup adds the KS parts in order.
+template <int W, int KS>
+struct SmallGeom {
+    static constexpr int TS = W / KS;
+};
+
+// LDS bytes of the small kernel: the activations plus the parked partials
+// [tmax][TS][KS][16][B] f32, tmax = tiles per (workgroup, tile slot).
+__host__ __device__ inline uint32_t small_part_off(uint32_t cols, uint32_t batch) {
+    return (lds_map(kQ4_K, cols, batch).total + 15u) & ~15u;
+}
+__host__ __device__ inline uint32_t small_lds_bytes(uint32_t cols, uint32_t batch, uint32_t tmax, uint32_t ts,
+                                                    uint32_t ks) {
+    return small_part_off(cols, batch) + tmax * ts * ks * 16u * batch * 4u;
+}
+
+template <int W, int KS, int D, int B, bool DBG>
 __global__ __launch_bounds__(W * 64) void q4k_mv_small_kernel(MvArgs a) {
-    RLQ_MV_PROLOGUE(kQ4_K, a.nb)
-    const uint32_t nb = a.nb;
+    constexpr int TS = SmallGeom<W, KS>::TS;
+    extern __shared__ __align__(16) uint8_t lds[];
+    const LdsMap L = lds_map(kQ4_K, a.cols, a.batch);
+    float* part = (float*)(lds + small_part_off(a.cols, a.batch));
+    const uint32_t lane = threadIdx.x & 63, n = lane & 15, kq = lane >> 4;
+    // wave-uniform indices in scalar registers: loop control stays on the SALU
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t ts = wave / KS, kp = wave % KS;
+    const uint32_t nb = a.nb, ntiles = a.ntiles;
+    const uint32_t tstride = gridDim.x * TS, t0 = blockIdx.x * TS + ts;
+    const uint32_t tmax = (ntiles + tstride - 1) / tstride;
+    const uint32_t my_tiles = t0 < ntiles ? (ntiles - 1 - t0) / tstride + 1 : 0;
+    const uint32_t bpt = kp < nb ? (nb - 1 - kp) / KS + 1 : 0;  // blocks of each tile this wave takes
+    const uint32_t steps = my_tiles * bpt;
+
+    if (threadIdx.x < 16) *(uint4*)(lds + L.zero_off + threadIdx.x * 16) = make_uint4(0, 0, 0, 0);
+    float xv[16];
+    prefetch_unit(a, wave, xv);
+
+    // loads run D steps ahead; past the wave's last step they repeat a valid chunk
+    const uint32_t kp0 = kp < nb ? kp : nb - 1;
+    uint32_t ld_tile = t0 < ntiles ? t0 : ntiles - 1, ld_blk = kp0;
     Q4Step buf[D];
     auto issue = [&](Q4Step& st) {
-        const uint8_t* base = a.w + ((uint64_t)ld_tile * nb + ld_chunk) * kQ4KChunk;
+        const uint8_t* base = a.w + ((uint64_t)ld_tile * nb + ld_blk) * kQ4KChunk;
         st.w0 = load_stream16(base + lane * 16);
         st.w1 = load_stream16(base + 1024 + lane * 16);
         st.h = load_stream16(base + 2048 + n * 16);
-        next_load();
+        ld_blk += KS;
+        if (ld_blk >= nb) {
+            ld_blk = kp0;
+            if (ld_tile + tstride < ntiles) ld_tile += tstride;
+        }
     };
 #pragma unroll
     for (int i = 0; i < D; ++i) issue(buf[i]);
@@ -549,10 +655,7 @@ __global__ __launch_bounds__(W * 64) void q4k_mv_small_kernel(MvArgs a) {
     float acc[B];
 #pragma unroll
     for (int b = 0; b < B; ++b) acc[b] = 0.0f;
-    unsigned long long best[B];
-#pragma unroll
-    for (int b = 0; b < B; ++b) best[b] = 0;
-    uint32_t tile = gw, blk = 0;
+    uint32_t ti = 0, tile = t0, blk = kp, j = 0;
     auto compute = [&](const Q4Step& cur) {
         const Q4Scales q = q4k_scales(cur.h);
         const int32_t s0 = __builtin_amdgcn_ubfe(q.scA, 16 * g, 8), s1 = __builtin_amdgcn_ubfe(q.scA, 16 * g + 8, 8);
@@ -561,12 +664,11 @@ __global__ __launch_bounds__(W * 64) void q4k_mv_small_kernel(MvArgs a) {
         const int32_t m4 = __builtin_amdgcn_ubfe(q.mnB, 16 * g, 8), m5 = __builtin_amdgcn_ubfe(q.mnB, 16 * g + 8, 8);
         const uint32_t l0[4] = {cur.w0.x & 0x0f0f0f0fu, cur.w0.y & 0x0f0f0f0fu, cur.w0.z & 0x0f0f0f0fu,
                                 cur.w0.w & 0x0f0f0f0fu};
-        const uint32_t h0[4] = {(cur.w0.x >> 4) & 0x0f0f0f0fu, (cur.w0.y >> 4) & 0x0f0f0f0fu,
-                                (cur.w0.z >> 4) & 0x0f0f0f0fu, (cur.w0.w >> 4) & 0x0f0f0f0fu};
+        uint32_t h0[4], h1[4];
+        hi_nibbles64(cur.w0, h0);
         const uint32_t l1[4] = {cur.w1.x & 0x0f0f0f0fu, cur.w1.y & 0x0f0f0f0fu, cur.w1.z & 0x0f0f0f0fu,
                                 cur.w1.w & 0x0f0f0f0fu};
-        const uint32_t h1[4] = {(cur.w1.x >> 4) & 0x0f0f0f0fu, (cur.w1.y >> 4) & 0x0f0f0f0fu,
-                                (cur.w1.z >> 4) & 0x0f0f0f0fu, (cur.w1.w >> 4) & 0x0f0f0f0fu};
+        hi_nibbles64(cur.w1, h1);
         const float dw = half_to_float(cur.h.x), dmw = half_to_float(cur.h.x >> 16);
 #pragma unroll
         for (int b = 0; b < B; ++b) {
@@ -596,23 +698,50 @@ __global__ __launch_bounds__(W * 64) void q4k_mv_small_kernel(MvArgs a) {
                 }
             }
         }
-        if (++blk == nb) {
-            const uint32_t row = tile * kTileRows + n;
+        blk += KS;
+        if (++j == bpt) {  // this wave's share of the tile is done: park the row sums
 #pragma unroll
             for (int b = 0; b < B; ++b) {
                 float v = acc[b];
                 v += __shfl_xor(v, 16, 64);
                 v += __shfl_xor(v, 32, 64);
-                if (kq == 0) store_out(a, row, b, v, best[b]);
+                if (kq == 0) part[(((ti * TS + ts) * KS + kp) * 16 + n) * B + b] = v;
                 acc[b] = 0.0f;
             }
-            blk = 0;
-            tile += tw;
+            j = 0;
+            blk = kp;
+            ++ti;
+            tile += tstride;
         }
     };
     pipeline<D>(steps, buf, issue, compute);
+    __syncthreads();
+
+    // add the K parts of every parked (tile, row) in order and store
 #pragma unroll
-    for (int b = 0; b < B; ++b) publish_argmax(a, b, best[b]);
+    for (int b = 0; b < B; ++b) {
+        unsigned long long best = 0;
+        for (uint32_t it = threadIdx.x; it < tmax * TS * 16; it += W * 64) {
+            const uint32_t r = it % 16, slot = it / 16, tsl = slot % TS, til = slot / TS;
+            const uint32_t t = blockIdx.x * TS + tsl + til * tstride;
+            const uint32_t row = t * kTileRows + r;
+            if (t < ntiles && row < a.rows && (uint32_t)b < a.batch) {
+                float v = 0.0f;
+#pragma unroll
+                for (int k = 0; k < KS; ++k)  // waves with no block of the tile (nb < KS) parked nothing
+                    if ((uint32_t)k < nb) v += part[((slot * KS + k) * 16 + r) * B + b];
+                store_out(a, row, b, v, best);
+            }
+        }
+        if (a.argmax_key) {
+#pragma unroll
+            for (int m = 1; m < 64; m <<= 1) {
+                const unsigned long long o = __shfl_xor(best, m, 64);
+                best = o > best ? o : best;
+            }
+            if (lane == 0 && best && (uint32_t)b < a.batch) atomicMax(a.argmax_key + b, best);
+        }
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -840,6 +969,30 @@ static hipError_t launch_one(K kernel, const MvArgs& a, size_t lds, hipStream_t 
     return hipGetLastError();
 }
 
+// Small-batch Q4_K kernel: W waves per workgroup, K of each tile split over
+// KS waves, about kSmallWgPerCu workgroups per CU.
+constexpr int kSmallW = 8, kSmallKS = 8, kSmallD = 2, kSmallWgPerCu = 2;
+
+template <int W, int KS, int D, int B, bool DBG>
+static hipError_t launch_small(const MvArgs& a, hipStream_t s) {
+    constexpr int TS = W / KS;
+    const uint32_t want = (a.ntiles + TS - 1) / TS;
+    const uint32_t cap = (uint32_t)kSmallWgPerCu * (uint32_t)device_cus();
+    const uint32_t grid = want < cap ? want : cap;
+    const uint32_t tstride = grid * TS, tmax = (a.ntiles + tstride - 1) / tstride;
+    const size_t lds = small_lds_bytes(a.cols, a.batch, tmax, TS, KS);
+    if (lds > kMaxLds) return hipErrorInvalidValue;
+    static size_t lds_set = 64 * 1024;
+    if (lds > lds_set) {
+        const hipError_t e = hipFuncSetAttribute((const void*)q4k_mv_small_kernel<W, KS, D, B, DBG>,
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        if (e != hipSuccess) return e;
+        lds_set = lds;
+    }
+    hipLaunchKernelGGL((q4k_mv_small_kernel<W, KS, D, B, DBG>), dim3(grid), dim3(W * 64), lds, s, a);
+    return hipGetLastError();
+}
+
 hipError_t launch_matvec(uint32_t wtype, const uint8_t* w, uint64_t rows, uint64_t cols, const float* x,
                          const ActPlanes* pre, uint64_t batch, float* y, uint64_t ldy,
                          unsigned long long* argmax_key, unsigned long long* err_word, int32_t* dbg_isum,
@@ -881,11 +1034,11 @@ hipError_t launch_matvec(uint32_t wtype, const uint8_t* w, uint64_t rows, uint64
         const bool dbg = a.dbg_isum != nullptr;
         if (wtype == kQ4_K) {
             if (nbat == 1)
-                e = dbg ? launch_one(q4k_mv_small_kernel<W, 8, 1, true>, a, lds, s)
-                        : launch_one(q4k_mv_small_kernel<W, 8, 1, false>, a, lds, s);
+                e = dbg ? launch_small<kSmallW, kSmallKS, kSmallD, 1, true>(a, s)
+                        : launch_small<kSmallW, kSmallKS, kSmallD, 1, false>(a, s);
             else if (nbat == 2)
-                e = dbg ? launch_one(q4k_mv_small_kernel<W, 8, 2, true>, a, lds, s)
-                        : launch_one(q4k_mv_small_kernel<W, 8, 2, false>, a, lds, s);
+                e = dbg ? launch_small<kSmallW, kSmallKS, kSmallD, 2, true>(a, s)
+                        : launch_small<kSmallW, kSmallKS, kSmallD, 2, false>(a, s);
             else
                 e = dbg ? launch_one(q4k_mv_kernel<W, 8, true>, a, lds, s)
                         : launch_one(q4k_mv_kernel<W, 8, false>, a, lds, s);

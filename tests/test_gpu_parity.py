@@ -320,3 +320,38 @@ def test_weights_outlive_their_context():
     W = rlq.Weights(c, DT.Q4_K, _weights(DT.Q4_K, 8, 256, 5), 8, 256)
     c.close()
     W.close()
+
+
+@pytest.mark.parametrize("t,batch", [(DT.Q4_K, 1), (DT.Q4_K, 3), (DT.Q6_K, 1)])
+def test_fused_quantizer_on_golden_q8k_inputs(ctx, t, batch):
+    """The matvec kernels quantize x to Q8_K themselves.  Fed the golden Q8_K
+    inputs (zeros, signed zeros, +/- ties, F32 max, tiny scales), the exact
+    block integers must equal those of the golden activation bytes, and the
+    f32 outputs those of the oracle for every row whose sum of absolute terms
+    stays below F32 max / 2.  (Rows built from x near F32 max can overflow in
+    some summation orders and not in others: the reference's eight lane sums
+    and separate mins sum, or the GPU's per-block terms.)"""
+    for i, (x, expected) in enumerate(F.q8k()):
+        cols, rows = x.size, 32
+        say("fused q8k golden", t, batch, i, cols)
+        w = _weights(t, rows, cols, 500 + i)
+        W = rlq.Weights(ctx, t, w, rows, cols)
+        xb = np.tile(x, (batch, 1))
+        isum, imin = ctx.block_sums(W, torch.from_numpy(xb).cuda())
+        torch.cuda.synchronize()
+        stride = w.size // rows
+        nb = cols // 256
+        for r in range(rows):
+            wi, wm = O.block_sums(int(t), w[r * stride:(r + 1) * stride], expected, nb)
+            assert np.array_equal(isum[r].cpu().numpy(), wi), (i, r)
+            assert np.array_equal(imin[r].cpu().numpy(), wm), (i, r)
+        y = ctx.matmul(W, torch.from_numpy(xb).cuda())
+        ctx.sync()
+        want = O.matvec(int(t), w, rows, cols, x)
+        got = y[0].cpu().numpy()
+        in_range = np.array([O.abs_terms(int(t), w[r * stride:(r + 1) * stride], expected, nb)
+                             < np.finfo(np.float32).max / 2 for r in range(rows)])
+        assert np.isfinite(want[in_range]).all() and np.isfinite(got[in_range]).all(), i
+        if in_range.any():
+            tol = elem_tol(t, w, rows, expected, cols, want)[in_range]
+            assert np.all(np.abs(got[in_range].astype(np.float64) - want[in_range]) <= tol), i
