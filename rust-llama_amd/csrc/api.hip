@@ -126,6 +126,10 @@ int32_t activation_dtype(uint32_t w, uint32_t* out, rlq_error* err) {
 
 bool path_weight(uint32_t t) { return t == kQ8_0 || t == kQ4_K || t == kQ6_K; }
 
+// Batches up to this size run the decode kernels (one pass over the weights
+// per 8 columns); larger Q4_K batches run the prefill GEMM.
+constexpr uint64_t kDecodeMaxBatch = 8;
+
 // ---- device buffers ---------------------------------------------------------
 
 struct DevBuf {
@@ -392,8 +396,15 @@ static int32_t matmul_impl(rlq_context* ctx, const rlq_weights* w, const float* 
         keys = (unsigned long long*)ctx->keys.p;
         HIP_TRY(launch_fill_u64(keys, batch, 0ull, s));
     }
-    HIP_TRY(launch_matvec(w->dtype, w->dev, w->rows, w->cols, x, nullptr, batch, y, w->rows, keys, ctx->err_words, nullptr,
-                          nullptr, s));
+    if (w->dtype == kQ4_K && batch > kDecodeMaxBatch) {  // prefill: one int8-MFMA GEMM
+        HIP_TRY(ensure(ctx, ctx->planes, gemm_planes_bytes(batch, w->cols)));
+        HIP_TRY(launch_gemm_q4k(w->dev, w->rows, w->cols, x, batch, y, w->rows, ctx->planes.p, ctx->err_words, nullptr,
+                                nullptr, s));
+        if (keys) HIP_TRY(launch_argmax_rows(y, batch, w->rows, keys, s));
+    } else {
+        HIP_TRY(launch_matvec(w->dtype, w->dev, w->rows, w->cols, x, nullptr, batch, y, w->rows, keys, ctx->err_words,
+                              nullptr, nullptr, s));
+    }
     if (argmax) HIP_TRY(launch_argmax_finish(keys, batch, y, w->rows, argmax, s));
     return ok(err);
 }
@@ -445,12 +456,20 @@ int32_t rlq_block_sums(rlq_context* ctx, const rlq_weights* w, const float* x, u
                        int32_t* imin, void* stream, rlq_error* err) {
     if (!ctx || !w || !x || !isum || !imin) return fail(err, RLQ_INVALID_ARGUMENT);
     if ((uintptr_t)x & 15) return fail(err, RLQ_INVALID_ARGUMENT, w->dtype);
-    if (batch == 0 || batch > 8) return fail(err, RLQ_INVALID_ARGUMENT, w->dtype);
+    if (batch == 0) return fail(err, RLQ_INVALID_ARGUMENT, w->dtype);
     DeviceGuard g(ctx->device);
     const hipStream_t s = pick(ctx, stream);
     HIP_TRY(ensure(ctx, ctx->stage_out, batch * w->rows * sizeof(float)));
-    HIP_TRY(launch_matvec(w->dtype, w->dev, w->rows, w->cols, x, nullptr, batch, (float*)ctx->stage_out.p, w->rows,
-                          nullptr, ctx->err_words, isum, imin, s));
+    float* y = (float*)ctx->stage_out.p;
+    if (w->dtype == kQ4_K && batch > kDecodeMaxBatch) {
+        HIP_TRY(ensure(ctx, ctx->planes, gemm_planes_bytes(batch, w->cols)));
+        HIP_TRY(launch_gemm_q4k(w->dev, w->rows, w->cols, x, batch, y, w->rows, ctx->planes.p, ctx->err_words, isum,
+                                imin, s));
+    } else {
+        if (batch > kDecodeMaxBatch) return fail(err, RLQ_INVALID_ARGUMENT, w->dtype);
+        HIP_TRY(launch_matvec(w->dtype, w->dev, w->rows, w->cols, x, nullptr, batch, y, w->rows, nullptr,
+                              ctx->err_words, isum, imin, s));
+    }
     return ok(err);
 }
 

@@ -67,6 +67,19 @@ hipError_t launch_matvec(uint32_t wtype, const uint8_t* w, uint64_t rows, uint64
                          const ActPlanes* pre, uint64_t batch, float* y, uint64_t ldy,
                          unsigned long long* argmax_key, unsigned long long* err_word, int32_t* dbg_isum,
                          int32_t* dbg_imin, hipStream_t s);
+// ---- gemm.hip ----
+// Prefill GEMM for Q4_K weights: y[m*ldy + r] = dot(row r, token m) for
+// m < M (M > 8 in practice).  Quantizes x [M][cols] to Q8_K planes in
+// `scratch` (gemm_planes_bytes) first; a data error in any token suppresses
+// every output.  `dbg_isum`/`dbg_imin` (may be null) receive token 0's exact
+// per-(row, block) integers.
+size_t gemm_planes_bytes(uint64_t M, uint64_t K);
+hipError_t launch_gemm_q4k(const uint8_t* w, uint64_t rows, uint64_t cols, const float* x, uint64_t M, float* y,
+                           uint64_t ldy, void* scratch, unsigned long long* err_word, int32_t* dbg_isum,
+                           int32_t* dbg_imin, hipStream_t s);
+
+// Argmax keys of the stored rows y[b*rows ..] (keys zeroed beforehand).
+hipError_t launch_argmax_rows(const float* y, uint64_t batch, uint64_t rows, unsigned long long* keys, hipStream_t s);
 // Decode argmax keys into u32 indices.
 hipError_t launch_argmax_finish(const unsigned long long* keys, uint64_t batch, const float* y, uint64_t ldy,
                                 uint32_t* out, hipStream_t s);

@@ -355,3 +355,84 @@ def test_fused_quantizer_on_golden_q8k_inputs(ctx, t, batch):
         if in_range.any():
             tol = elem_tol(t, w, rows, expected, cols, want)[in_range]
             assert np.all(np.abs(got[in_range].astype(np.float64) - want[in_range]) <= tol), i
+
+
+# ------------------------------------------------------------ prefill GEMM (Q4_K, batch > 8)
+
+@pytest.mark.parametrize("rows,cols,batch", [(300, 4096, 16), (300, 4096, 200), (70, 768, 129), (64, 256, 9)])
+def test_gemm_block_sums_bit_exact(ctx, rows, cols, batch):
+    """Token 0's exact per-block integers inside the prefill GEMM (two-plane
+    MFMA sums and base-128 mins digits), on partial row and token tiles."""
+    say("gemm block sums", rows, cols, batch)
+    w = _weights(DT.Q4_K, rows, cols, 900 + rows)
+    x = randn(901 + batch, batch * cols).reshape(batch, cols)
+    W = rlq.Weights(ctx, DT.Q4_K, w, rows, cols)
+    isum, imin = ctx.block_sums(W, torch.from_numpy(x).cuda())
+    torch.cuda.synchronize()
+    act = O.quantize(O.Q8_K, x[0])
+    nb = cols // 256
+    stride = w.size // rows
+    for r in range(rows):
+        wi, wm = O.block_sums(O.Q4_K, w[r * stride:(r + 1) * stride], act, nb)
+        assert np.array_equal(isum[r].cpu().numpy(), wi), r
+        assert np.array_equal(imin[r].cpu().numpy(), wm), r
+
+
+@pytest.mark.parametrize("rows,cols,batch", [(333, 4096, 64), (1000, 2048, 129), (96, 14336, 17)])
+def test_gemm_against_oracle(ctx, rows, cols, batch):
+    say("gemm", rows, cols, batch)
+    w = _weights(DT.Q4_K, rows, cols, 77 + rows)
+    x = randn(78 + batch, batch * cols).reshape(batch, cols)
+    W = rlq.Weights(ctx, DT.Q4_K, w, rows, cols)
+    y = ctx.matmul(W, torch.from_numpy(x).cuda())
+    ctx.sync()
+    want = O.matmul(O.Q4_K, w, rows, cols, x, threads=16)
+    got = y.cpu().numpy()
+    for b in range(batch):
+        assert rel_l2(got[b], want[b]) <= REL_L2, b
+
+
+def test_gemm_prefill_shape_512x14336x4096(ctx):
+    """The prefill benchmark shape: every token against the oracle on a
+    sample of rows, and the full output's per-token relative L2 on 64
+    tokens."""
+    rows, cols, batch = 14336, 4096, 512
+    say("gemm prefill shape", rows, cols, batch)
+    xw = randn(0x51A7E003, rows * cols, 0.02)
+    w = rlq.quantize(DT.Q4_K, xw)
+    del xw
+    x = randn(0x51A7E003 + 7, batch * cols).reshape(batch, cols)
+    W = rlq.Weights(ctx, DT.Q4_K, w, rows, cols)
+    y = ctx.matmul(W, torch.from_numpy(x).cuda())
+    ctx.sync()
+    got = y.cpu().numpy()
+    stride = w.size // rows
+    sample = np.arange(0, rows, 97)
+    ws = np.concatenate([w[r * stride:(r + 1) * stride] for r in sample])
+    want = O.matmul(O.Q4_K, ws, sample.size, cols, x, threads=16)
+    for b in range(batch):
+        assert rel_l2(got[b, sample], want[b]) <= REL_L2, b
+    want_full = O.matmul(O.Q4_K, w, rows, cols, x[:64:9], threads=16)
+    for k, b in enumerate(range(0, 64, 9)):
+        assert rel_l2(got[b], want_full[k]) <= REL_L2, b
+
+
+def test_gemm_argmax_and_errors(ctx):
+    rows, cols, batch = 1000, 1024, 24
+    say("gemm argmax and errors", rows, cols, batch)
+    w = _weights(DT.Q4_K, rows, cols, 41)
+    W = rlq.Weights(ctx, DT.Q4_K, w, rows, cols)
+    x = randn(42, batch * cols).reshape(batch, cols)
+    y, am = ctx.matmul_argmax(W, torch.from_numpy(x).cuda())
+    ctx.sync()
+    got = y.cpu().numpy()
+    for b in range(batch):
+        assert int(am[b]) == O.argmax(got[b]), b
+    xt = torch.from_numpy(x).cuda()
+    xt[13, 500] = float("inf")
+    y2 = torch.full((batch, rows), 7.0, device="cuda")
+    ctx.matmul(W, xt, y2)
+    with pytest.raises(rlq.QuantError) as e:
+        ctx.sync()
+    assert (e.value.name, e.value.index, e.value.b) == ("NonFiniteInput", 500, 13)
+    assert bool((y2 == 7.0).all())
