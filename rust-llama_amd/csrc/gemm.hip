@@ -99,9 +99,15 @@ struct GemmArgs {
     int32_t* dbg_imin;
 };
 
-constexpr int kGemmWaves = 4;
-constexpr int kGemmTM = 32 * kGemmWaves;  // tokens per workgroup: 32 per wave
-constexpr int kGemmTN = 64;               // weight rows per workgroup: two 32-row MFMA column tiles
+// Workgroup: 8 waves over 128 tokens x 128 weight rows; wave (tg, rg) = (w % 4,
+// w / 4) computes tokens 32 tg .. +31 against rows 64 rg .. +63 (two 32-row
+// MFMA column tiles).  The two int8 planes of the workgroup's 128 rows are
+// double-buffered in LDS: while the MFMAs of block b read one buffer, the
+// waves dequantize block b+1 (loaded into registers one block ahead) into the
+// other, and one barrier per block separates the two.
+constexpr int kGemmWaves = 8;
+constexpr int kGemmTM = 128;  // tokens per workgroup
+constexpr int kGemmTN = 128;  // weight rows per workgroup (eight 16-row tiles)
 
 __device__ __forceinline__ i32x16 mfma32(i32x4 a, i32x4 b, i32x16 c) {
     return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0);
@@ -119,14 +125,63 @@ __device__ __forceinline__ uint32_t bytes_times(uint32_t w, uint32_t s) {
     return __builtin_bit_cast(uint32_t, p);
 }
 
+// One LDS buffer: planes [plane][row tile of 32][sub-block][k half][row][16 B],
+// in the B-operand lane order of v_mfma_i32_32x32x32_i8, plus the rows' mins
+// and d, dmin and the tokens' activation scales of the block.
+struct GemmStage {
+    uint8_t planes[2][4][8][2][32][16];
+    uint32_t mins[4][32][2];
+    float dw[kGemmTN], dmw[kGemmTN], da[kGemmTM];
+};
+
+// Raw Q4_K chunk of one 16-row tile (lane roles of the decode layout).
+struct RawTile {
+    uint4 w0, w1, h;
+};
+
+__device__ __forceinline__ void dequant_tile(GemmStage& st, const RawTile& r, bool live, uint32_t tile_in_wg,
+                                             uint32_t lane) {
+    const uint32_t sn = lane & 15, skq = lane >> 4, sg = skq >> 1, sh = skq & 1;
+    const uint32_t row = 16 * tile_in_wg + sn, rt = row >> 5, rn = row & 31;
+    const uint32_t scA = live ? r.h.y & 0x3f3f3f3fu : 0;
+    const uint32_t scB = live ? (r.h.w & 0x0f0f0f0fu) | ((r.h.y >> 2) & 0x30303030u) : 0;
+#pragma unroll
+    for (int P = 0; P < 2; ++P) {
+        const uint4 wv = P ? r.w1 : r.w0;
+        const uint32_t scw = P ? scB : scA;
+        const uint32_t s_lo = 4 * P + 2 * sg, s_hi = s_lo + 1;
+        const uint32_t c_lo = __builtin_amdgcn_ubfe(scw, 16 * sg, 8), c_hi = __builtin_amdgcn_ubfe(scw, 16 * sg + 8, 8);
+        const uint32_t lo[4] = {wv.x & 0x0f0f0f0fu, wv.y & 0x0f0f0f0fu, wv.z & 0x0f0f0f0fu, wv.w & 0x0f0f0f0fu};
+        const uint32_t hi[4] = {(wv.x >> 4) & 0x0f0f0f0fu, (wv.y >> 4) & 0x0f0f0f0fu, (wv.z >> 4) & 0x0f0f0f0fu,
+                                (wv.w >> 4) & 0x0f0f0f0fu};
+        *(uint4*)st.planes[0][rt][s_lo][sh][rn] = make_uint4(
+            bytes_times(lo[0], c_lo >> 3), bytes_times(lo[1], c_lo >> 3), bytes_times(lo[2], c_lo >> 3),
+            bytes_times(lo[3], c_lo >> 3));
+        *(uint4*)st.planes[1][rt][s_lo][sh][rn] = make_uint4(
+            bytes_times(lo[0], c_lo & 7), bytes_times(lo[1], c_lo & 7), bytes_times(lo[2], c_lo & 7),
+            bytes_times(lo[3], c_lo & 7));
+        *(uint4*)st.planes[0][rt][s_hi][sh][rn] = make_uint4(
+            bytes_times(hi[0], c_hi >> 3), bytes_times(hi[1], c_hi >> 3), bytes_times(hi[2], c_hi >> 3),
+            bytes_times(hi[3], c_hi >> 3));
+        *(uint4*)st.planes[1][rt][s_hi][sh][rn] = make_uint4(
+            bytes_times(hi[0], c_hi & 7), bytes_times(hi[1], c_hi & 7), bytes_times(hi[2], c_hi & 7),
+            bytes_times(hi[3], c_hi & 7));
+    }
+    if (skq == 0) {
+        st.mins[rt][rn][0] = live ? r.h.z & 0x3f3f3f3fu : 0;
+        st.mins[rt][rn][1] = live ? ((r.h.w >> 4) & 0x0f0f0f0fu) | ((r.h.z >> 2) & 0x30303030u) : 0;
+        st.dw[row] = live ? half_to_float(r.h.x) : 0.0f;
+        st.dmw[row] = live ? half_to_float(r.h.x >> 16) : 0.0f;
+    }
+}
+
+template <bool DBG>
 __global__ __launch_bounds__(kGemmWaves * 64) void q4k_gemm_kernel(GemmArgs g) {
-    // B operands of the two planes in the lane order of v_mfma_i32_32x32x32_i8:
-    // [plane][col tile][sub-block][k half][row n][16 bytes]
-    __shared__ __align__(16) uint8_t planes[2][2][8][2][32][16];
-    __shared__ __align__(16) uint32_t mins[2][32][2];  // [col tile][row][mn 0..3 | mn 4..7]
-    __shared__ float dws[kGemmTN], dmws[kGemmTN], das[kGemmTM];
+    extern __shared__ __align__(16) uint8_t smem[];
+    GemmStage* stage = (GemmStage*)smem;  // [2]
 
     const uint32_t lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t tg = wave & 3, rg = wave >> 2;
     const uint32_t n0 = blockIdx.x * kGemmTN, m0 = blockIdx.y * kGemmTM;
     const uint32_t nb = g.nb;
 
@@ -139,11 +194,36 @@ __global__ __launch_bounds__(kGemmWaves * 64) void q4k_gemm_kernel(GemmArgs g) {
     // l % 32, k half l / 32; output element i = token 8(i/4) + 4(l/32) + i%4 of
     // the wave's 32, weight row l % 32 of the column tile.
     const uint32_t ln = lane & 31, kh = lane >> 5;
-    const uint32_t tok = m0 + 32 * wave + ln;  // this lane's A row (< Mp)
-    // staging role: wave t dequantizes 16-row tile t of the workgroup's 64 rows
-    const uint32_t sn = lane & 15, skq = lane >> 4, sg = skq >> 1, sh = skq & 1;
-    const uint32_t srow = 16 * wave + sn, sc_tile = srow >> 5, sc_n = srow & 31;
+    const uint32_t tok = m0 + 32 * tg + ln;  // this lane's A row (< Mp)
+    // staging: wave w loads and dequantizes 16-row tile w of the workgroup
     const uint32_t tile16 = n0 / 16 + wave;
+    const bool tile_live = tile16 < g.ntiles16;
+    const uint8_t* wbase = g.w + (uint64_t)(tile_live ? tile16 : 0) * nb * kQ4KChunk;
+    auto load_raw = [&](uint32_t b) {
+        RawTile r;
+        const uint8_t* base = wbase + (uint64_t)b * kQ4KChunk;
+        r.w0 = load_stream16(base + lane * 16);
+        r.w1 = load_stream16(base + 1024 + lane * 16);
+        r.h = load_stream16(base + 2048 + (lane & 15) * 16);
+        return r;
+    };
+    const int8_t* arow = g.q8 + (uint64_t)tok * g.K + 16 * kh;
+    const int8_t* mrow = g.bsd + (uint64_t)tok * nb * 16 + 8 * kh;
+    auto load_a = [&](uint32_t b, i32x4 (&A)[8], long& Am) {
+#pragma unroll
+        for (int s = 0; s < 8; ++s) A[s] = *(const i32x4*)(arow + b * 256 + 32 * s);
+        Am = *(const long*)(mrow + b * 16);
+    };
+
+    // prologue: block 0 staged, block 1 in flight
+    RawTile raw = load_raw(0);
+    i32x4 A[8];
+    long Am;
+    load_a(0, A, Am);
+    dequant_tile(stage[0], raw, tile_live, wave, lane);
+    for (uint32_t t = threadIdx.x; t < kGemmTM; t += kGemmWaves * 64) stage[0].da[t] = g.da[(uint64_t)(m0 + t) * nb];
+    if (nb > 1) raw = load_raw(1);
+    __syncthreads();
 
     float acc[2][16];
 #pragma unroll
@@ -152,93 +232,32 @@ __global__ __launch_bounds__(kGemmWaves * 64) void q4k_gemm_kernel(GemmArgs g) {
         for (int i = 0; i < 16; ++i) acc[c][i] = 0.0f;
 
     for (uint32_t b = 0; b < nb; ++b) {
-        // ---- stage: two int8 planes, the mins and d, dmin of the 64 rows
-        if (tile16 < g.ntiles16) {
-            const uint8_t* base = g.w + ((uint64_t)tile16 * nb + b) * kQ4KChunk;
-            const uint4 w0 = load_stream16(base + lane * 16);
-            const uint4 w1 = load_stream16(base + 1024 + lane * 16);
-            const uint4 h = load_stream16(base + 2048 + sn * 16);
-            const uint32_t scA = h.y & 0x3f3f3f3fu;
-            const uint32_t scB = (h.w & 0x0f0f0f0fu) | ((h.y >> 2) & 0x30303030u);
-            const uint32_t mnA = h.z & 0x3f3f3f3fu;
-            const uint32_t mnB = ((h.w >> 4) & 0x0f0f0f0fu) | ((h.z >> 2) & 0x30303030u);
-            // this lane: sub-blocks 2g, 2g+1 (w0, g = sg) and 2g'... (w1, g' = 2 + sg), half sh
+        const GemmStage& cur = stage[b & 1];
 #pragma unroll
-            for (int P = 0; P < 2; ++P) {
-                const uint4 wv = P ? w1 : w0;
-                const uint32_t scw = P ? scB : scA;
-                const uint32_t s_lo = 4 * P + 2 * sg, s_hi = s_lo + 1;
-                const uint32_t c_lo = __builtin_amdgcn_ubfe(scw, 16 * sg, 8);
-                const uint32_t c_hi = __builtin_amdgcn_ubfe(scw, 16 * sg + 8, 8);
-                const uint32_t lo[4] = {wv.x & 0x0f0f0f0fu, wv.y & 0x0f0f0f0fu, wv.z & 0x0f0f0f0fu,
-                                        wv.w & 0x0f0f0f0fu};
-                const uint32_t hi[4] = {(wv.x >> 4) & 0x0f0f0f0fu, (wv.y >> 4) & 0x0f0f0f0fu,
-                                        (wv.z >> 4) & 0x0f0f0f0fu, (wv.w >> 4) & 0x0f0f0f0fu};
-                *(uint4*)planes[0][sc_tile][s_lo][sh][sc_n] =
-                    make_uint4(bytes_times(lo[0], c_lo >> 3), bytes_times(lo[1], c_lo >> 3),
-                               bytes_times(lo[2], c_lo >> 3), bytes_times(lo[3], c_lo >> 3));
-                *(uint4*)planes[1][sc_tile][s_lo][sh][sc_n] =
-                    make_uint4(bytes_times(lo[0], c_lo & 7), bytes_times(lo[1], c_lo & 7),
-                               bytes_times(lo[2], c_lo & 7), bytes_times(lo[3], c_lo & 7));
-                *(uint4*)planes[0][sc_tile][s_hi][sh][sc_n] =
-                    make_uint4(bytes_times(hi[0], c_hi >> 3), bytes_times(hi[1], c_hi >> 3),
-                               bytes_times(hi[2], c_hi >> 3), bytes_times(hi[3], c_hi >> 3));
-                *(uint4*)planes[1][sc_tile][s_hi][sh][sc_n] =
-                    make_uint4(bytes_times(hi[0], c_hi & 7), bytes_times(hi[1], c_hi & 7),
-                               bytes_times(hi[2], c_hi & 7), bytes_times(hi[3], c_hi & 7));
-            }
-            if (skq == 0) {
-                mins[sc_tile][sc_n][0] = mnA;
-                mins[sc_tile][sc_n][1] = mnB;
-                dws[srow] = half_to_float(h.x);
-                dmws[srow] = half_to_float(h.x >> 16);
-            }
-        } else {  // rows past the matrix: zero planes
-#pragma unroll
-            for (int P = 0; P < 2; ++P)
-#pragma unroll
-                for (int q = 0; q < 2; ++q) {
-                    const uint32_t s_ = 4 * P + 2 * sg + q;
-                    *(uint4*)planes[0][sc_tile][s_][sh][sc_n] = make_uint4(0, 0, 0, 0);
-                    *(uint4*)planes[1][sc_tile][s_][sh][sc_n] = make_uint4(0, 0, 0, 0);
-                }
-            if (skq == 0) {
-                mins[sc_tile][sc_n][0] = mins[sc_tile][sc_n][1] = 0;
-                dws[srow] = dmws[srow] = 0.0f;
-            }
-        }
-        for (uint32_t t = threadIdx.x; t < kGemmTM; t += kGemmWaves * 64) das[t] = g.da[(uint64_t)(m0 + t) * nb + b];
-        __syncthreads();
-
-        // ---- this wave's 32 tokens x 64 rows
-        i32x4 A[8];
-        const int8_t* ap = g.q8 + (uint64_t)tok * g.K + b * 256 + 16 * kh;
-#pragma unroll
-        for (int s = 0; s < 8; ++s) A[s] = *(const i32x4*)(ap + 32 * s);
-        const long Am = *(const long*)(g.bsd + ((uint64_t)tok * nb + b) * 16 + 8 * kh);
-#pragma unroll
-        for (int c = 0; c < 2; ++c) {
+        for (int c = 0; c < 2; ++c) {  // one 32-row column tile at a time
+            const uint32_t rt = 2 * rg + c;
             i32x16 ca, cb;
 #pragma unroll
             for (int i = 0; i < 16; ++i) ca[i] = cb[i] = 0;
 #pragma unroll
             for (int s = 0; s < 8; ++s) {
-                ca = mfma32(A[s], *(const i32x4*)planes[0][c][s][kh][ln], ca);
-                cb = mfma32(A[s], *(const i32x4*)planes[1][c][s][kh][ln], cb);
+                ca = mfma32(A[s], *(const i32x4*)cur.planes[0][rt][s][kh][ln], ca);
+                cb = mfma32(A[s], *(const i32x4*)cur.planes[1][rt][s][kh][ln], cb);
             }
-            const long mn = *(const long*)mins[c][ln];
+            const long mn = *(const long*)cur.mins[rt][ln];
             const i32x16 clo = mfma32k16(Am, kh == 0 ? mn : 0);
             const i32x16 chi = mfma32k16(Am, kh == 1 ? mn : 0);
-            const float dw = dws[32 * c + ln], dmw = dmws[32 * c + ln];
+            const uint32_t wrow = 32 * rt + ln;
+            const float dw = cur.dw[wrow], dmw = cur.dmw[wrow];
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
-                const uint32_t ti = 32 * wave + 8 * (i / 4) + 4 * kh + (i % 4);
-                const float dai = das[ti];
+                const uint32_t ti = 32 * tg + 8 * (i / 4) + 4 * kh + (i % 4);
+                const float dai = cur.da[ti];
                 const int32_t I = 8 * ca[i] + cb[i];
                 const int32_t Mn = clo[i] + 128 * chi[i];
                 acc[c][i] += (dw * dai) * (float)I - (dmw * dai) * (float)Mn;
-                if (g.dbg_isum && m0 + ti == 0) {
-                    const uint32_t row = n0 + 32 * c + ln;
+                if (DBG && m0 + ti == 0) {
+                    const uint32_t row = n0 + wrow;
                     if (row < g.rows) {
                         g.dbg_isum[(uint64_t)row * nb + b] = I;
                         g.dbg_imin[(uint64_t)row * nb + b] = Mn;
@@ -246,15 +265,25 @@ __global__ __launch_bounds__(kGemmWaves * 64) void q4k_gemm_kernel(GemmArgs g) {
                 }
             }
         }
+        // next block's activations: in flight during the staging and barrier
+        if (b + 1 < nb) load_a(b + 1, A, Am);
+
+        if (b + 1 < nb) {  // stage block b+1 into the other buffer
+            GemmStage& nxt = stage[(b + 1) & 1];
+            dequant_tile(nxt, raw, tile_live, wave, lane);
+            for (uint32_t t = threadIdx.x; t < kGemmTM; t += kGemmWaves * 64)
+                nxt.da[t] = g.da[(uint64_t)(m0 + t) * nb + b + 1];
+            if (b + 2 < nb) raw = load_raw(b + 2);
+        }
         __syncthreads();
     }
 
 #pragma unroll
     for (int c = 0; c < 2; ++c) {
-        const uint32_t row = n0 + 32 * c + ln;
+        const uint32_t row = n0 + 32 * (2 * rg + c) + ln;
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-            const uint32_t m = m0 + 32 * wave + 8 * (i / 4) + 4 * kh + (i % 4);
+            const uint32_t m = m0 + 32 * tg + 8 * (i / 4) + 4 * kh + (i % 4);
             if (m < g.M && row < g.rows) g.y[(uint64_t)m * g.ldy + row] = acc[c][i];
         }
     }
@@ -303,8 +332,20 @@ hipError_t launch_gemm_q4k(const uint8_t* w, uint64_t rows, uint64_t cols, const
     g.ldy = ldy;
     g.dbg_isum = dbg_isum;
     g.dbg_imin = dbg_imin;
+    static bool lds_set = false;
+    const size_t lds = 2 * sizeof(GemmStage);
+    if (!lds_set) {
+        e = hipFuncSetAttribute((const void*)q4k_gemm_kernel<false>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                (int)lds);
+        if (e == hipSuccess)
+            e = hipFuncSetAttribute((const void*)q4k_gemm_kernel<true>, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                    (int)lds);
+        if (e != hipSuccess) return e;
+        lds_set = true;
+    }
     const dim3 grid((unsigned)((rows + kGemmTN - 1) / kGemmTN), (unsigned)(Mp / kGemmTM));
-    hipLaunchKernelGGL(q4k_gemm_kernel, grid, dim3(kGemmWaves * 64), 0, s, g);
+    if (dbg_isum) hipLaunchKernelGGL(q4k_gemm_kernel<true>, grid, dim3(kGemmWaves * 64), lds, s, g);
+    else hipLaunchKernelGGL(q4k_gemm_kernel<false>, grid, dim3(kGemmWaves * 64), lds, s, g);
     return hipGetLastError();
 }
 
