@@ -1,5 +1,5 @@
 // gemm.hip - prefill GEMM for Q4_K weights on gfx950: y[m][n] = dot(row n, token m)
-// for many tokens at once, on int8 MFMA.
+// for many tokens at once, on fp16 MFMA with exact integer operands.
 //
 // Contract: the GGML MUL_MAT semantics of crates/tensor/src/cpu_extra.rs:756-873
 // -- every token (column) is quantized to Q8_K on its own (:820) and every
@@ -9,16 +9,22 @@
 // crates/model-runtime/src/context.rs:452); this kernel computes the same
 // exact per-block integers for all M tokens in one pass over the weights.
 //
-// Integer decomposition.  Per (token m, row n, block):
-//   I  = sum_s sc_s * sum_{j in s} q_j x_j        (sc: 6-bit sub-block scale)
-//   Mn = sum_s mn_s * bsum32_s(m)                 (mn: 6-bit sub-block min)
-//   y += d_n * da_m * I - dmin_n * da_m * Mn      (f32, block by block)
-// sc * q does not fit int8, so sc = 8a + b (a, b <= 7) and the weights are
-// dequantized to two int8 planes a*q and b*q (each <= 105): I = 8 C_a + C_b
-// with C_a, C_b accumulated over the whole block by v_mfma_i32_32x32x32_i8.
-// The mins term runs on v_mfma_i32_32x32x16_i8 with bsum32 split into base-128
-// digits (lo in 0..127, hi in -32..31): Mn = C_lo + 128 C_hi.  Every integer is
-// exact; only the f32 accumulation order differs from the reference's.
+// Integer decomposition.  Per (token m, row n, block of 256):
+//   I  = sum_j (sc_s(j) * q_j) * x_j        sc: 6-bit sub-block scale, q: 4 bits
+//   Mn = sum_s mn_s * bsum32_s(m)           mn: 6-bit sub-block min
+//   y += da_m * (d_n * I - dmin_n * Mn)     f32, block by block
+// Both sums run on v_mfma_f32_32x32x16_f16 with integer-valued operands: the
+// weight operand is sc*q <= 945 and the activation operand q8 in [-127, 127],
+// both exact in f16; products are exact in f32, and every partial sum of a
+// chain is an integer bounded by sum_j |sc q x|.  While that bound stays below
+// 2^24 the f32 accumulation is exact in any order.  The activation quantizer
+// flags a token whose block has sum |x| > 17753 (945 * 17753 < 2^24); a token
+// tile with such a token folds every half block (128 values: 128*945*127 <
+// 2^24) instead of every block.  The mins use bsum16 (|.| <= 2032) against
+// mn (<= 63): always exact.  So I and Mn equal the reference's i32 sums, and
+// float(I) (the f32 of an exact integer, or the f32 sum of two exact halves)
+// is the reference's `sumi as f32`; only the f32 order of the per-block terms
+// differs from the reference's.
 #include "rlq_device.hpp"
 #include "rlq_internal.hpp"
 #include "rlq_layout.hpp"
@@ -26,27 +32,80 @@
 
 namespace rlq {
 
-typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
-typedef int32_t i32x16 __attribute__((ext_vector_type(16)));
-typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 // ---------------------------------------------------------------------------
-// Activations: f32 x [M][K] -> Q8_K planes for the GEMM
-//   q8  int8 [Mp][K]          (Mp = M rounded up to the token tile)
-//   da  f32  [Mp][nb]
-//   bsd int8 [Mp][nb][16]     lo digits of bsum32_s in 0..7, hi digits in 8..15
-//   bad u32  [Mp]             1 when a block of the token is invalid
-// Tokens >= M are written as zeros.  One workgroup of 256 lanes per token:
-// a 16-lane DPP row quantizes one 256-value block (q8k_row16).
+// Tiling
+//
+// Workgroup: 4 waves (one per SIMD) over 128 tokens x 256 weight rows (16
+// layout tiles of 16 rows).  Wave w owns rows 64w .. 64w+63 as two 32-row MFMA
+// column tiles r and all 128 tokens as four 32-token tiles T: eight 32x32
+// accumulator tiles.  Every weight value is dequantized once per workgroup.
+//
+// K is walked in groups of 64 values (4 k-steps of 16).  A group's operands
+// are one LDS stage, filled by global_load_lds_dwordx4 (global -> LDS without
+// VGPRs) three stages ahead in a ring of four; per-block data (weight block
+// headers, activation bsums and scales) sit in a ring of three regions.
+//
+// The f32 accumulators (AGPRs) hold one fold unit: a block, or a half block
+// for flagged tiles.  After each unit the VALU folds them into y (VGPRs).
 // ---------------------------------------------------------------------------
+constexpr uint32_t kGemmTM = 128;          // tokens per workgroup
+constexpr uint32_t kGemmTN = 256;          // weight rows per workgroup
+constexpr uint32_t kGemmThreads = 256;
+constexpr uint32_t kUnsafeAbsSum = 17753;  // floor((2^24 - 1) / 945)
+
+// Activation image, written by gemm_act_kernel.  Per token tile of 128: nb*4
+// groups, then nb block records.
+//   group (b, g): [k-step 4][k half 2][token 128][8 halves]      16 KB
+//   record b:     bsum16 [k half 2][token 128][8 halves]          4 KB
+//                 da [token 128] f32                             512 B
+// Group g, k-step s, k half h, slot t holds the value at block position
+// 64g + 32(s/2) + 16h + 8(s%2) + kPerm[t], kPerm = {0,2,1,3,4,6,5,7}: the
+// order in which the weight dequantizer below produces sc*q.
+constexpr uint32_t kActGroupBytes = 16384;
+constexpr uint32_t kActRecordBytes = 4608;
+constexpr uint32_t kActRecordDa = 4096;
+constexpr uint64_t kActTileBlockBytes = 4 * kActGroupBytes + kActRecordBytes;
+
+__device__ __forceinline__ uint64_t act_group_offset(uint32_t nb, uint32_t b, uint32_t g) {
+    return ((uint64_t)b * 4 + g) * kActGroupBytes;
+}
+__device__ __forceinline__ uint64_t act_record_offset(uint32_t nb, uint32_t b) {
+    return (uint64_t)nb * 4 * kActGroupBytes + (uint64_t)b * kActRecordBytes;
+}
+
+// LDS
+constexpr uint32_t kSlots = 4, kSlotBytes = 24576, kSlotW = 16384;  // [A 16 KB][W 16 tiles x 512 B]
+constexpr uint32_t kRegions = 3, kRegionBytes = 8704;               // [headers 4 KB][record 4.5 KB]
+constexpr uint32_t kRegBS = 4096, kRegDA = kRegBS + kActRecordDa;
+constexpr uint32_t kGemmLds = kSlots * kSlotBytes + kRegions * kRegionBytes;
+
+// ---------------------------------------------------------------------------
+// Activations: f32 x [M][K] -> the image above, plus tokflag[m] = bit 0 data
+// error, bit 1 "some block has sum |q8| > kUnsafeAbsSum".  Tokens >= M are
+// zeros.  One workgroup of 256 lanes per token: a 16-lane DPP row quantizes
+// one 256-value block (q8k_row16), lane r16 holding positions 16 r16 .. +15.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ int32_t row16_sum_i(int32_t v) {
+    v += dpp_i<kQuadXor1>(v);
+    v += dpp_i<kQuadXor2>(v);
+    v += dpp_i<kRowHalfMirror>(v);
+    v += dpp_i<kRowRor8>(v);
+    return v;
+}
+
 __global__ __launch_bounds__(256) void gemm_act_kernel(const float* __restrict__ x, uint32_t M, uint32_t K,
-                                                       int8_t* __restrict__ q8, float* __restrict__ da,
-                                                       int8_t* __restrict__ bsd, uint32_t* __restrict__ bad,
+                                                       uint8_t* __restrict__ img, uint32_t* __restrict__ tokflag,
                                                        unsigned long long* err_word, uint32_t err_column0) {
     const uint32_t m = blockIdx.x, lane = threadIdx.x & 63, r16 = lane & 15;
     const uint32_t nb = K / 256, upr = K / 16;  // 16-value units per token
-    int any_bad = 0;
-    for (uint32_t u = threadIdx.x; u < upr; u += 256) {  // upr % 16 == 0: rows of 16 stay whole
+    const uint32_t tok = m % kGemmTM;
+    uint8_t* tile = img + (uint64_t)(m / kGemmTM) * nb * kActTileBlockBytes;
+    int any_bad = 0, any_unsafe = 0;
+    for (uint32_t u = threadIdx.x; u < upr; u += 256) {  // u % 16 == r16: rows of 16 stay whole
         const uint32_t blk = u / 16;
         float v[16];
         if (m < M) {
@@ -68,18 +127,31 @@ __global__ __launch_bounds__(256) void gemm_act_kernel(const float* __restrict__
                                            ? error_key(err_column0 + m, kKindNonFinite, blk * 256ull + o.index)
                                            : error_key(err_column0 + m, kKindScale, blk));
         }
-        *(uint4*)(q8 + (uint64_t)m * K + u * 16) = make_uint4(o.q[0], o.q[1], o.q[2], o.q[3]);
-        if (r16 == 0) da[(uint64_t)m * nb + blk] = o.d;
-        // bsum32 of sub-block s = bsum[2s] + bsum[2s+1], as base-128 digits
-        const int32_t s32 = o.bsum + dpp_i<kQuadXor1>(o.bsum);
-        if ((r16 & 1) == 0) {
-            int8_t* dst = bsd + ((uint64_t)m * nb + blk) * 16 + (r16 >> 1);
-            dst[0] = (int8_t)(s32 & 127);
-            dst[8] = (int8_t)(s32 >> 7);
+        int32_t q[16];
+#pragma unroll
+        for (int t = 0; t < 16; ++t) q[t] = (int32_t)(int8_t)(o.q[t / 4] >> (8 * (t % 4)));
+        // positions 16 r16 + t: group r16/4, k-steps 2((r16/2)%2) + t/8, k half r16%2
+        uint8_t* ag = tile + act_group_offset(nb, blk, r16 / 4);
+        const uint32_t s0 = 2 * ((r16 >> 1) & 1), hh = r16 & 1;
+        constexpr int kPerm[8] = {0, 2, 1, 3, 4, 6, 5, 7};
+#pragma unroll
+        for (int so = 0; so < 2; ++so) {
+            f16x8 h;
+#pragma unroll
+            for (int t = 0; t < 8; ++t) h[t] = (_Float16)q[8 * so + kPerm[t]];
+            *(f16x8*)(ag + ((s0 + so) * 2 + hh) * 2048 + tok * 16) = h;
         }
+        uint8_t* rec = tile + act_record_offset(nb, blk);
+        *(_Float16*)(rec + (r16 / 8) * 2048 + tok * 16 + (r16 % 8) * 2) = (_Float16)o.bsum;
+        if (r16 == 0) *(float*)(rec + kActRecordDa + tok * 4) = o.d;
+        int32_t sa = 0;
+#pragma unroll
+        for (int t = 0; t < 16; ++t) sa += q[t] < 0 ? -q[t] : q[t];
+        if ((uint32_t)row16_sum_i(sa) > kUnsafeAbsSum) any_unsafe = 1;
     }
     const int token_bad = __syncthreads_or(any_bad);
-    if (threadIdx.x == 0) bad[m] = token_bad ? 1u : 0u;
+    const int token_unsafe = __syncthreads_or(any_unsafe);
+    if (threadIdx.x == 0) tokflag[m] = (token_bad ? 1u : 0u) | (token_unsafe ? 2u : 0u);
 }
 
 // ---------------------------------------------------------------------------
@@ -88,212 +160,355 @@ __global__ __launch_bounds__(256) void gemm_act_kernel(const float* __restrict__
 struct GemmArgs {
     const uint8_t* w;  // Q4_K, tiled device layout (rlq_layout.hpp)
     uint32_t rows, nb, ntiles16;
-    const int8_t* q8;
-    const float* da;
-    const int8_t* bsd;
-    const uint32_t* bad;
-    uint32_t M, Mp, K;
-    float* y;  // y[m * ldy + n]
+    const uint8_t* img;  // activation image
+    const uint32_t* tokflag;
+    uint32_t M, NT, MT;  // tokens; workgroup tiles along rows and tokens
+    float* y;            // y[m * ldy + n]
     uint64_t ldy;
     int32_t* dbg_isum;  // exact integers of token 0, or null
     int32_t* dbg_imin;
 };
 
-// Workgroup: 8 waves over 128 tokens x 128 weight rows; wave (tg, rg) = (w % 4,
-// w / 4) computes tokens 32 tg .. +31 against rows 64 rg .. +63 (two 32-row
-// MFMA column tiles).  The two int8 planes of the workgroup's 128 rows are
-// double-buffered in LDS: while the MFMAs of block b read one buffer, the
-// waves dequantize block b+1 (loaded into registers one block ahead) into the
-// other, and one barrier per block separates the two.
-constexpr int kGemmWaves = 8;
-constexpr int kGemmTM = 128;  // tokens per workgroup
-constexpr int kGemmTN = 128;  // weight rows per workgroup (eight 16-row tiles)
-
-__device__ __forceinline__ i32x16 mfma32(i32x4 a, i32x4 b, i32x16 c) {
-    return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0);
-}
-__device__ __forceinline__ i32x16 mfma32k16(long a, long b) {
-    i32x16 z;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) z[i] = 0;
-    return __builtin_amdgcn_mfma_i32_32x32x16_i8(a, b, z, 0, 0, 0);
+__device__ __forceinline__ f32x16 mfma16(f16x8 a, f16x8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
 
-// bytes * s for four unsigned bytes <= 15 and s <= 7: no product leaves its byte
-__device__ __forceinline__ uint32_t bytes_times(uint32_t w, uint32_t s) {
-    const u16x2 p = __builtin_bit_cast(u16x2, w) * (u16x2){(unsigned short)s, (unsigned short)s};
-    return __builtin_bit_cast(uint32_t, p);
+// global -> LDS, 16 bytes per lane: lane l's 16 bytes at sbase + voff go to
+// LDS address lds + 16 l (lds and sbase wave-uniform).  Issued as inline asm:
+// the compiler would otherwise treat the LDS write as aliasing every later LDS
+// read and wait for all outstanding loads before each; the stage barriers
+// below order these loads instead.
+__device__ __forceinline__ void g2l(const void* sbase, uint32_t voff, uint32_t lds) {
+    asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "{m0}"(lds));
 }
 
-// One LDS buffer: planes [plane][row tile of 32][sub-block][k half][row][16 B],
-// in the B-operand lane order of v_mfma_i32_32x32x32_i8, plus the rows' mins
-// and d, dmin and the tokens' activation scales of the block.
-struct GemmStage {
-    uint8_t planes[2][4][8][2][32][16];
-    uint32_t mins[4][32][2];
-    float dw[kGemmTN], dmw[kGemmTN], da[kGemmTM];
+// Wait until at most N of this wave's vector-memory operations are pending and
+// its LDS operations are done, then barrier: the LDS-DMA loads of the stage
+// about to be read (all but the newest N) have landed for every wave.
+template <int N>
+__device__ __forceinline__ void stage_barrier() {
+    asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" ::"n"(N) : "memory");
+}
+
+__device__ __forceinline__ f16x2 as_h2(uint32_t v) { return __builtin_bit_cast(f16x2, v); }
+
+// Byte K (< 64) of w as the f16 pair (w_K, w_K): bits 0x64kk are 1024 + w_K.
+template <int K>
+__device__ __forceinline__ f16x2 byte_pair(uint32_t w) {
+    const uint32_t sel = (uint32_t)K | 4u << 8 | (uint32_t)K << 16 | 4u << 24;
+    return as_h2(__builtin_amdgcn_perm(0x64646464u, w, sel)) - (f16x2){(_Float16)1024.0f, (_Float16)1024.0f};
+}
+
+// Q4_K block header (16 bytes: d, dmin, 12 scale bytes) -> 6-bit scales and
+// mins, four per word (get_scale_min_k4, crates/quant/src/decode.rs:216-235).
+struct Q4Words {
+    uint32_t scA, scB, mnA, mnB;  // sub-blocks 0-3 and 4-7
+};
+__device__ __forceinline__ Q4Words q4_words(uint4 h) {
+    Q4Words q;
+    q.scA = h.y & 0x3f3f3f3fu;
+    q.scB = (h.w & 0x0f0f0f0fu) | ((h.y >> 2) & 0x30303030u);
+    q.mnA = h.z & 0x3f3f3f3fu;
+    q.mnB = ((h.w >> 4) & 0x0f0f0f0fu) | ((h.z >> 2) & 0x30303030u);
+    return q;
+}
+
+// Scale pairs of one group's two sub-blocks: low nibbles (sub-block 2g) are
+// dequantized from 1024 + q as (1024 + q) sc - 1024 sc, high nibbles (2g + 1)
+// from 1024 + 16 q as (1024 + 16 q) (sc / 16) - 64 sc; each v_pk_fma_f16 is
+// exact (the exact result q*sc <= 945 is an f16).
+struct GroupScales {
+    f16x2 lo, lo_neg, hi, hi_neg;
+};
+template <int G>
+__device__ __forceinline__ GroupScales group_scales(const Q4Words& q) {
+    const uint32_t w = G < 2 ? q.scA : q.scB;
+    const f16x2 a = byte_pair<2 * (G % 2)>(w), b = byte_pair<2 * (G % 2) + 1>(w);
+    GroupScales s;
+    s.lo = a;
+    s.lo_neg = a * (f16x2){(_Float16)-1024.0f, (_Float16)-1024.0f};
+    s.hi = b * (f16x2){(_Float16)0.0625f, (_Float16)0.0625f};
+    s.hi_neg = b * (f16x2){(_Float16)-64.0f, (_Float16)-64.0f};
+    return s;
+}
+
+// B operand of k-step S of a group for one lane: its 16-byte piece holds
+// block positions 64g + 16h + i (low nibble) and 64g + 32 + 16h + i (high
+// nibble), i = 0..15.  S = 0, 1: low nibbles of bytes 8S .. 8S+7; S = 2, 3:
+// high nibbles of bytes 8(S-2) .. ; slot order kPerm.
+template <int S>
+__device__ __forceinline__ f16x8 dequant(const uint4& pc, const GroupScales& sc) {
+    const uint32_t w0 = (S & 1) ? pc.z : pc.x, w1 = (S & 1) ? pc.w : pc.y;
+    constexpr uint32_t mask = S < 2 ? 0x000f000fu : 0x00f000f0u;
+    const f16x2 scale = S < 2 ? sc.lo : sc.hi, neg = S < 2 ? sc.lo_neg : sc.hi_neg;
+    const uint32_t x0 = (w0 & mask) | 0x64006400u, x1 = ((w0 >> 8) & mask) | 0x64006400u;
+    const uint32_t x2 = (w1 & mask) | 0x64006400u, x3 = ((w1 >> 8) & mask) | 0x64006400u;
+    const f16x2 r0 = __builtin_elementwise_fma(as_h2(x0), scale, neg);
+    const f16x2 r1 = __builtin_elementwise_fma(as_h2(x1), scale, neg);
+    const f16x2 r2 = __builtin_elementwise_fma(as_h2(x2), scale, neg);
+    const f16x2 r3 = __builtin_elementwise_fma(as_h2(x3), scale, neg);
+    f16x8 v;
+    v[0] = r0[0], v[1] = r0[1], v[2] = r1[0], v[3] = r1[1];
+    v[4] = r2[0], v[5] = r2[1], v[6] = r3[0], v[7] = r3[1];
+    return v;
+}
+
+// Per-row data of the block being folded: f32 d and dmin and the mins operand
+// (lane half h: mn_{4h} .. mn_{4h+3}, each twice, against bsum16 8h .. 8h+7).
+struct FoldRow {
+    float d, dmin;
+    f16x8 mins;
+};
+__device__ __forceinline__ FoldRow fold_row(uint4 hdr, uint32_t kh) {
+    const Q4Words q = q4_words(hdr);
+    const uint32_t w = kh ? q.mnB : q.mnA;
+    FoldRow f;
+    f.d = half_to_float(hdr.x);
+    f.dmin = half_to_float(hdr.x >> 16);
+    const f16x2 p0 = byte_pair<0>(w), p1 = byte_pair<1>(w), p2 = byte_pair<2>(w), p3 = byte_pair<3>(w);
+    f.mins[0] = p0[0], f.mins[1] = p0[1], f.mins[2] = p1[0], f.mins[3] = p1[1];
+    f.mins[4] = p2[0], f.mins[5] = p2[1], f.mins[6] = p3[0], f.mins[7] = p3[1];
+    return f;
+}
+
+// Everything one workgroup needs, fixed for the launch.
+struct GemmCtx {
+    uint8_t* smem;
+    uint32_t lds;  // LDS address of smem
+    uint32_t nb, rows, nt, mt, wave, lane, ln, kh;
+    const uint8_t* act_tile;  // activation image of token tile mt
+    const uint8_t* w_first;   // first weight layout tile of the workgroup
+    uint32_t w_lane[2];       // this lane's offsets (from w_first) of its weight-piece loads
+    uint32_t h_lane;          // ... and of its header load
+    int32_t* dbg_isum;
+    int32_t* dbg_imin;
 };
 
-// Raw Q4_K chunk of one 16-row tile (lane roles of the decode layout).
-struct RawTile {
-    uint4 w0, w1, h;
-};
+__device__ __forceinline__ const uint8_t* region_ptr(const GemmCtx& c, uint32_t block) {
+    return c.smem + kSlots * kSlotBytes + (block % kRegions) * kRegionBytes;
+}
 
-__device__ __forceinline__ void dequant_tile(GemmStage& st, const RawTile& r, bool live, uint32_t tile_in_wg,
-                                             uint32_t lane) {
-    const uint32_t sn = lane & 15, skq = lane >> 4, sg = skq >> 1, sh = skq & 1;
-    const uint32_t row = 16 * tile_in_wg + sn, rt = row >> 5, rn = row & 31;
-    const uint32_t scA = live ? r.h.y & 0x3f3f3f3fu : 0;
-    const uint32_t scB = live ? (r.h.w & 0x0f0f0f0fu) | ((r.h.y >> 2) & 0x30303030u) : 0;
+// Issue the LDS-DMA loads of stage s = 4 b + G (clamped past the last block).
+// Every wave issues 6 loads per stage, plus 3 when G == 0: the stage barriers'
+// vmcnt counts depend on it.
+template <int G>
+__device__ __forceinline__ void issue_stage(const GemmCtx& c, uint32_t s) {
+    const uint32_t bu = s / 4, b = bu < c.nb ? bu : c.nb - 1;
+    const uint32_t slot = c.lds + (s % kSlots) * kSlotBytes;
+    const uint8_t* ag = c.act_tile + act_group_offset(c.nb, b, G) + c.wave * 4 * 1024;
 #pragma unroll
-    for (int P = 0; P < 2; ++P) {
-        const uint4 wv = P ? r.w1 : r.w0;
-        const uint32_t scw = P ? scB : scA;
-        const uint32_t s_lo = 4 * P + 2 * sg, s_hi = s_lo + 1;
-        const uint32_t c_lo = __builtin_amdgcn_ubfe(scw, 16 * sg, 8), c_hi = __builtin_amdgcn_ubfe(scw, 16 * sg + 8, 8);
-        const uint32_t lo[4] = {wv.x & 0x0f0f0f0fu, wv.y & 0x0f0f0f0fu, wv.z & 0x0f0f0f0fu, wv.w & 0x0f0f0f0fu};
-        const uint32_t hi[4] = {(wv.x >> 4) & 0x0f0f0f0fu, (wv.y >> 4) & 0x0f0f0f0fu, (wv.z >> 4) & 0x0f0f0f0fu,
-                                (wv.w >> 4) & 0x0f0f0f0fu};
-        *(uint4*)st.planes[0][rt][s_lo][sh][rn] = make_uint4(
-            bytes_times(lo[0], c_lo >> 3), bytes_times(lo[1], c_lo >> 3), bytes_times(lo[2], c_lo >> 3),
-            bytes_times(lo[3], c_lo >> 3));
-        *(uint4*)st.planes[1][rt][s_lo][sh][rn] = make_uint4(
-            bytes_times(lo[0], c_lo & 7), bytes_times(lo[1], c_lo & 7), bytes_times(lo[2], c_lo & 7),
-            bytes_times(lo[3], c_lo & 7));
-        *(uint4*)st.planes[0][rt][s_hi][sh][rn] = make_uint4(
-            bytes_times(hi[0], c_hi >> 3), bytes_times(hi[1], c_hi >> 3), bytes_times(hi[2], c_hi >> 3),
-            bytes_times(hi[3], c_hi >> 3));
-        *(uint4*)st.planes[1][rt][s_hi][sh][rn] = make_uint4(
-            bytes_times(hi[0], c_hi & 7), bytes_times(hi[1], c_hi & 7), bytes_times(hi[2], c_hi & 7),
-            bytes_times(hi[3], c_hi & 7));
+    for (int j = 0; j < 4; ++j) g2l(ag + j * 1024, c.lane * 16, slot + (c.wave * 4 + j) * 1024);
+    // layout tile t: the qs bytes of group G of its 16 rows are the 512 bytes at
+    // (G/2) * 1024 + (G%2) * 512 of the block's chunk
+    const uint8_t* wb = c.w_first + (uint64_t)b * kQ4KChunk + (G / 2) * 1024 + (G % 2) * 512;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) g2l(wb, c.w_lane[j], slot + kSlotW + (c.wave * 2 + j) * 1024);
+    if (G == 0) {
+        const uint32_t reg = c.lds + kSlots * kSlotBytes + (bu % kRegions) * kRegionBytes;
+        g2l(c.w_first + (uint64_t)b * kQ4KChunk, c.h_lane, reg + c.wave * 1024);
+        const uint8_t* rec = c.act_tile + act_record_offset(c.nb, b) + c.wave * 1152;
+        g2l(rec, c.lane * 16, reg + kRegBS + c.wave * 1152);
+        if (c.lane < 8) g2l(rec + 1024, c.lane * 16, reg + kRegBS + c.wave * 1152 + 1024);
     }
-    if (skq == 0) {
-        st.mins[rt][rn][0] = live ? r.h.z & 0x3f3f3f3fu : 0;
-        st.mins[rt][rn][1] = live ? ((r.h.w >> 4) & 0x0f0f0f0fu) | ((r.h.z >> 2) & 0x30303030u) : 0;
-        st.dw[row] = live ? half_to_float(r.h.x) : 0.0f;
-        st.dmw[row] = live ? half_to_float(r.h.x >> 16) : 0.0f;
+}
+
+// Accumulator tile X = 2T + r of a finished fold unit into y.  MINS: the unit
+// ends a block (its mins term is due).  DBG stores token 0's integers (ADD:
+// the unit is a second half; its integer adds to the first half's).
+template <int X, bool MINS, bool DBG, bool ADD>
+__device__ __forceinline__ void fold_tile(const GemmCtx& c, const f32x16 (&h)[2][4], float (&y)[2][4][16],
+                                          const FoldRow (&fr)[2], const uint8_t* reg, uint32_t b) {
+    constexpr int r = X % 2, T = X / 2;
+    f32x16 mn = {};
+    if (MINS) {
+        const f16x8 bs = *(const f16x8*)(reg + kRegBS + c.kh * 2048 + (32 * T + c.ln) * 16);
+        mn = mfma16(bs, fr[r].mins, (f32x16){});
     }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const float4 da = *(const float4*)(reg + kRegDA + (32 * T + 8 * q + 4 * c.kh) * 4);
+        const float dav[4] = {da.x, da.y, da.z, da.w};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int i = 4 * q + k;
+            float t = fr[r].d * h[r][T][i];
+            if (MINS) t = __builtin_fmaf(-fr[r].dmin, mn[i], t);
+            y[r][T][i] = __builtin_fmaf(dav[k], t, y[r][T][i]);
+        }
+    }
+    if (DBG && T == 0) {
+        const uint32_t row = c.nt * kGemmTN + 64 * c.wave + 32 * r + c.ln;
+        if (c.mt == 0 && c.kh == 0 && row < c.rows) {
+            int32_t* p = c.dbg_isum + (uint64_t)row * c.nb + b;
+            *p = (ADD ? *p : 0) + (int32_t)h[r][T][0];
+            if (MINS) c.dbg_imin[(uint64_t)row * c.nb + b] = (int32_t)mn[0];
+        }
+    }
+}
+
+#define RLQ_SWITCH4(v, F)     \
+    switch (v) {              \
+        case 0: F(0); break;  \
+        case 1: F(1); break;  \
+        case 2: F(2); break;  \
+        default: F(3); break; \
+    }
+
+// One block: 4 groups of 4 k-steps into h, folded into y after the block
+// (SPLIT: after each half block).
+template <bool SPLIT, bool DBG>
+__device__ __forceinline__ void gemm_block(const GemmCtx& c, uint32_t b, f32x16 (&h)[2][4], float (&y)[2][4][16]) {
+    const uint8_t* reg = region_ptr(c, b);
+    Q4Words qw[2];
+#pragma unroll
+    for (int G = 0; G < 4; ++G) {
+        const uint32_t s = b * 4 + G;
+        // stage s has landed for every wave; slot (s - 1) % 4 is free again
+        if (DBG) stage_barrier<0>();
+        else if (G < 2) stage_barrier<12>();
+        else stage_barrier<15>();
+        if (G == 0) {  // the block's region arrived with its first stage
+#pragma unroll
+            for (int r = 0; r < 2; ++r) {
+                const uint32_t tl = 4 * c.wave + 2 * r + (c.ln >> 4);
+                qw[r] = q4_words(*(const uint4*)(reg + tl * 256 + (c.ln & 15) * 16));
+            }
+        }
+#define RLQ_ISSUE(k) issue_stage<((k) + 3) % 4>(c, s + 3)
+        RLQ_SWITCH4(G, RLQ_ISSUE)
+#undef RLQ_ISSUE
+        const uint8_t* slot = c.smem + (s % kSlots) * kSlotBytes;
+        GroupScales sc[2];
+        uint4 pc[2];
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+#define RLQ_SC(k) sc[r] = group_scales<k>(qw[r])
+            RLQ_SWITCH4(G, RLQ_SC)
+#undef RLQ_SC
+            const uint32_t tl = 4 * c.wave + 2 * r + (c.ln >> 4);
+            pc[r] = *(const uint4*)(slot + kSlotW + tl * 512 + c.kh * 256 + (c.ln & 15) * 16);
+        }
+#pragma unroll
+        for (int S = 0; S < 4; ++S) {
+            f16x8 a[4];
+#pragma unroll
+            for (int T = 0; T < 4; ++T)
+                a[T] = *(const f16x8*)(slot + S * 4096 + c.kh * 2048 + (32 * T + c.ln) * 16);
+            f16x8 bq[2];
+#pragma unroll
+            for (int r = 0; r < 2; ++r) {
+#define RLQ_DQ(k) bq[r] = dequant<k>(pc[r], sc[r])
+                RLQ_SWITCH4(S, RLQ_DQ)
+#undef RLQ_DQ
+            }
+            const bool fresh = S == 0 && (G == 0 || (SPLIT && G == 2));
+#pragma unroll
+            for (int r = 0; r < 2; ++r)
+#pragma unroll
+                for (int T = 0; T < 4; ++T) h[r][T] = mfma16(a[T], bq[r], fresh ? (f32x16){} : h[r][T]);
+        }
+        if ((G == 1 && SPLIT) || G == 3) {
+            FoldRow fr[2];
+#pragma unroll
+            for (int r = 0; r < 2; ++r) {
+                const uint32_t tl = 4 * c.wave + 2 * r + (c.ln >> 4);
+                fr[r] = fold_row(*(const uint4*)(reg + tl * 256 + (c.ln & 15) * 16), c.kh);
+            }
+#define RLQ_FOLD(XX)                                                                                       \
+    {                                                                                                      \
+        if (G == 1) fold_tile<XX, false, DBG, false>(c, h, y, fr, reg, b);                                 \
+        else if (SPLIT) fold_tile<XX, true, DBG, true>(c, h, y, fr, reg, b);                               \
+        else fold_tile<XX, true, DBG, false>(c, h, y, fr, reg, b);                                         \
+    }
+            RLQ_FOLD(0) RLQ_FOLD(1) RLQ_FOLD(2) RLQ_FOLD(3) RLQ_FOLD(4) RLQ_FOLD(5) RLQ_FOLD(6) RLQ_FOLD(7)
+#undef RLQ_FOLD
+        }
+    }
+}
+
+template <bool SPLIT, bool DBG>
+__device__ __forceinline__ void gemm_tile(const GemmCtx& c, float (&y)[2][4][16]) {
+    f32x16 h[2][4];
+    // prologue: stages 0, 1, 2 in flight
+    issue_stage<0>(c, 0);
+    issue_stage<1>(c, 1);
+    issue_stage<2>(c, 2);
+    for (uint32_t b = 0; b < c.nb; ++b) gemm_block<SPLIT, DBG>(c, b, h, y);
+    // LDS-DMA loads past the end may still be in flight: they must land before
+    // the workgroup's LDS can go to another workgroup
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
 template <bool DBG>
-__global__ __launch_bounds__(kGemmWaves * 64) void q4k_gemm_kernel(GemmArgs g) {
+__global__ __launch_bounds__(kGemmThreads) void q4k_gemm_kernel(GemmArgs g) {
     extern __shared__ __align__(16) uint8_t smem[];
-    GemmStage* stage = (GemmStage*)smem;  // [2]
-
     const uint32_t lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const uint32_t tg = wave & 3, rg = wave >> 2;
-    const uint32_t n0 = blockIdx.x * kGemmTN, m0 = blockIdx.y * kGemmTM;
-    const uint32_t nb = g.nb;
+    // XCD-aware order: workgroups i, i + 8, ... share an XCD (and its L2); give
+    // each XCD a contiguous run of tiles, token tile major
+    const uint32_t G = g.NT * g.MT;
+    uint32_t id = blockIdx.x;
+    if (G % 8 == 0) id = (id % 8) * (G / 8) + id / 8;
+    GemmCtx c;
+    c.smem = smem;
+    c.nb = g.nb;
+    c.rows = g.rows;
+    c.nt = id % g.NT;
+    c.mt = id / g.NT;
+    c.wave = wave;
+    c.lane = lane;
+    c.ln = lane & 31;
+    c.kh = lane >> 5;
+    c.act_tile = g.img + (uint64_t)c.mt * g.nb * kActTileBlockBytes;
+    c.dbg_isum = g.dbg_isum;
+    c.dbg_imin = g.dbg_imin;
+    c.lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)smem;
+    // weight loads: tiles past the last one read the last one (rows >= g.rows are never stored)
+    const uint32_t t0 = c.nt * 16, tmax = g.ntiles16 - 1, tstride = g.nb * kQ4KChunk;
+    c.w_first = g.w + (uint64_t)t0 * tstride;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const uint32_t t = t0 + 2 * (wave * 2 + j) + (lane >> 5);
+        c.w_lane[j] = ((t < tmax ? t : tmax) - t0) * tstride + (lane & 31) * 16;
+    }
+    const uint32_t th = t0 + 4 * wave + (lane >> 4);
+    c.h_lane = ((th < tmax ? th : tmax) - t0) * tstride + 2048 + (lane & 15) * 16;
 
     // a data error in any token: this call writes nothing
-    int any_bad = 0;
-    for (uint32_t i = threadIdx.x; i < g.M; i += kGemmWaves * 64) any_bad |= g.bad[i] != 0;
-    if (__syncthreads_or(any_bad)) return;
+    int bad = 0;
+    for (uint32_t i = threadIdx.x; i < g.M; i += kGemmThreads) bad |= (int)(g.tokflag[i] & 1u);
+    const int unsafe = (int)((g.tokflag[c.mt * kGemmTM + (threadIdx.x & 127)] >> 1) & 1u);
+    if (__syncthreads_or(bad)) return;
+    const bool split = __syncthreads_or(unsafe) != 0;
 
-    // MFMA lane roles: A (tokens) row l % 32, k half l / 32; B (weights) column
-    // l % 32, k half l / 32; output element i = token 8(i/4) + 4(l/32) + i%4 of
-    // the wave's 32, weight row l % 32 of the column tile.
-    const uint32_t ln = lane & 31, kh = lane >> 5;
-    const uint32_t tok = m0 + 32 * tg + ln;  // this lane's A row (< Mp)
-    // staging: wave w loads and dequantizes 16-row tile w of the workgroup
-    const uint32_t tile16 = n0 / 16 + wave;
-    const bool tile_live = tile16 < g.ntiles16;
-    const uint8_t* wbase = g.w + (uint64_t)(tile_live ? tile16 : 0) * nb * kQ4KChunk;
-    auto load_raw = [&](uint32_t b) {
-        RawTile r;
-        const uint8_t* base = wbase + (uint64_t)b * kQ4KChunk;
-        r.w0 = load_stream16(base + lane * 16);
-        r.w1 = load_stream16(base + 1024 + lane * 16);
-        r.h = load_stream16(base + 2048 + (lane & 15) * 16);
-        return r;
-    };
-    const int8_t* arow = g.q8 + (uint64_t)tok * g.K + 16 * kh;
-    const int8_t* mrow = g.bsd + (uint64_t)tok * nb * 16 + 8 * kh;
-    auto load_a = [&](uint32_t b, i32x4 (&A)[8], long& Am) {
+    float y[2][4][16];
 #pragma unroll
-        for (int s = 0; s < 8; ++s) A[s] = *(const i32x4*)(arow + b * 256 + 32 * s);
-        Am = *(const long*)(mrow + b * 16);
-    };
+    for (int r = 0; r < 2; ++r)
+#pragma unroll
+        for (int T = 0; T < 4; ++T)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) y[r][T][i] = 0.0f;
+    if (split) gemm_tile<true, DBG>(c, y);
+    else gemm_tile<false, DBG>(c, y);
 
-    // prologue: block 0 staged, block 1 in flight
-    RawTile raw = load_raw(0);
-    i32x4 A[8];
-    long Am;
-    load_a(0, A, Am);
-    dequant_tile(stage[0], raw, tile_live, wave, lane);
-    for (uint32_t t = threadIdx.x; t < kGemmTM; t += kGemmWaves * 64) stage[0].da[t] = g.da[(uint64_t)(m0 + t) * nb];
-    if (nb > 1) raw = load_raw(1);
-    __syncthreads();
-
-    float acc[2][16];
 #pragma unroll
-    for (int c = 0; c < 2; ++c)
+    for (int r = 0; r < 2; ++r) {
+        const uint32_t row = c.nt * kGemmTN + 64 * wave + 32 * r + c.ln;
 #pragma unroll
-        for (int i = 0; i < 16; ++i) acc[c][i] = 0.0f;
-
-    for (uint32_t b = 0; b < nb; ++b) {
-        const GemmStage& cur = stage[b & 1];
-#pragma unroll
-        for (int c = 0; c < 2; ++c) {  // one 32-row column tile at a time
-            const uint32_t rt = 2 * rg + c;
-            i32x16 ca, cb;
-#pragma unroll
-            for (int i = 0; i < 16; ++i) ca[i] = cb[i] = 0;
-#pragma unroll
-            for (int s = 0; s < 8; ++s) {
-                ca = mfma32(A[s], *(const i32x4*)cur.planes[0][rt][s][kh][ln], ca);
-                cb = mfma32(A[s], *(const i32x4*)cur.planes[1][rt][s][kh][ln], cb);
-            }
-            const long mn = *(const long*)cur.mins[rt][ln];
-            const i32x16 clo = mfma32k16(Am, kh == 0 ? mn : 0);
-            const i32x16 chi = mfma32k16(Am, kh == 1 ? mn : 0);
-            const uint32_t wrow = 32 * rt + ln;
-            const float dw = cur.dw[wrow], dmw = cur.dmw[wrow];
+        for (int T = 0; T < 4; ++T)
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
-                const uint32_t ti = 32 * tg + 8 * (i / 4) + 4 * kh + (i % 4);
-                const float dai = cur.da[ti];
-                const int32_t I = 8 * ca[i] + cb[i];
-                const int32_t Mn = clo[i] + 128 * chi[i];
-                acc[c][i] += (dw * dai) * (float)I - (dmw * dai) * (float)Mn;
-                if (DBG && m0 + ti == 0) {
-                    const uint32_t row = n0 + wrow;
-                    if (row < g.rows) {
-                        g.dbg_isum[(uint64_t)row * nb + b] = I;
-                        g.dbg_imin[(uint64_t)row * nb + b] = Mn;
-                    }
-                }
+                const uint32_t m = c.mt * kGemmTM + 32 * T + 8 * (i / 4) + 4 * c.kh + (i % 4);
+                if (m < g.M && row < g.rows) g.y[(uint64_t)m * g.ldy + row] = y[r][T][i];
             }
-        }
-        // next block's activations: in flight during the staging and barrier
-        if (b + 1 < nb) load_a(b + 1, A, Am);
-
-        if (b + 1 < nb) {  // stage block b+1 into the other buffer
-            GemmStage& nxt = stage[(b + 1) & 1];
-            dequant_tile(nxt, raw, tile_live, wave, lane);
-            for (uint32_t t = threadIdx.x; t < kGemmTM; t += kGemmWaves * 64)
-                nxt.da[t] = g.da[(uint64_t)(m0 + t) * nb + b + 1];
-            if (b + 2 < nb) raw = load_raw(b + 2);
-        }
-        __syncthreads();
-    }
-
-#pragma unroll
-    for (int c = 0; c < 2; ++c) {
-        const uint32_t row = n0 + 32 * (2 * rg + c) + ln;
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const uint32_t m = m0 + 32 * tg + 8 * (i / 4) + 4 * kh + (i % 4);
-            if (m < g.M && row < g.rows) g.y[(uint64_t)m * g.ldy + row] = acc[c][i];
-        }
     }
 }
 
 // ---------------------------------------------------------------------------
+static uint64_t gemm_padded_tokens(uint64_t M) { return (M + kGemmTM - 1) / kGemmTM * kGemmTM; }
+
 size_t gemm_planes_bytes(uint64_t M, uint64_t K) {
-    const uint64_t Mp = (M + kGemmTM - 1) / kGemmTM * kGemmTM, nb = K / 256;
-    auto al = [](uint64_t v) { return (v + 255) & ~(uint64_t)255; };
-    return al(Mp * K) + al(Mp * nb * 4) + al(Mp * nb * 16) + al(Mp * 4);
+    const uint64_t Mp = gemm_padded_tokens(M), nb = K / 256;
+    return Mp / kGemmTM * nb * kActTileBlockBytes + Mp * 4;
 }
 
 hipError_t launch_gemm_q4k(const uint8_t* w, uint64_t rows, uint64_t cols, const float* x, uint64_t M, float* y,
@@ -302,18 +517,13 @@ hipError_t launch_gemm_q4k(const uint8_t* w, uint64_t rows, uint64_t cols, const
     if (rows == 0 || cols == 0 || cols % 256 || M == 0 || rows > 0xffffffffull || cols > (1u << 30) ||
         M > (1u << 24))
         return hipErrorInvalidValue;
-    const uint64_t Mp = (M + kGemmTM - 1) / kGemmTM * kGemmTM, nb = cols / 256;
-    auto al = [](uint64_t v) { return (v + 255) & ~(uint64_t)255; };
-    uint8_t* p = (uint8_t*)scratch;
-    int8_t* q8 = (int8_t*)p;
-    p += al(Mp * cols);
-    float* da = (float*)p;
-    p += al(Mp * nb * 4);
-    int8_t* bsd = (int8_t*)p;
-    p += al(Mp * nb * 16);
-    uint32_t* bad = (uint32_t*)p;
-    hipLaunchKernelGGL(gemm_act_kernel, dim3((unsigned)Mp), dim3(256), 0, s, x, (uint32_t)M, (uint32_t)cols, q8, da,
-                       bsd, bad, err_word, 0u);
+    const uint64_t Mp = gemm_padded_tokens(M), nb = cols / 256, MT = Mp / kGemmTM;
+    const uint64_t NT = (rows + kGemmTN - 1) / kGemmTN;
+    if (MT * NT > 0x7fffffffull) return hipErrorInvalidValue;
+    uint8_t* img = (uint8_t*)scratch;
+    uint32_t* tokflag = (uint32_t*)(img + MT * nb * kActTileBlockBytes);
+    hipLaunchKernelGGL(gemm_act_kernel, dim3((unsigned)Mp), dim3(256), 0, s, x, (uint32_t)M, (uint32_t)cols, img,
+                       tokflag, err_word, 0u);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     GemmArgs g{};
@@ -321,31 +531,28 @@ hipError_t launch_gemm_q4k(const uint8_t* w, uint64_t rows, uint64_t cols, const
     g.rows = (uint32_t)rows;
     g.nb = (uint32_t)nb;
     g.ntiles16 = (uint32_t)layout_tiles(rows);
-    g.q8 = q8;
-    g.da = da;
-    g.bsd = bsd;
-    g.bad = bad;
+    g.img = img;
+    g.tokflag = tokflag;
     g.M = (uint32_t)M;
-    g.Mp = (uint32_t)Mp;
-    g.K = (uint32_t)cols;
+    g.NT = (uint32_t)NT;
+    g.MT = (uint32_t)MT;
     g.y = y;
     g.ldy = ldy;
     g.dbg_isum = dbg_isum;
     g.dbg_imin = dbg_imin;
     static bool lds_set = false;
-    const size_t lds = 2 * sizeof(GemmStage);
     if (!lds_set) {
         e = hipFuncSetAttribute((const void*)q4k_gemm_kernel<false>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                (int)lds);
+                                (int)kGemmLds);
         if (e == hipSuccess)
             e = hipFuncSetAttribute((const void*)q4k_gemm_kernel<true>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                    (int)lds);
+                                    (int)kGemmLds);
         if (e != hipSuccess) return e;
         lds_set = true;
     }
-    const dim3 grid((unsigned)((rows + kGemmTN - 1) / kGemmTN), (unsigned)(Mp / kGemmTM));
-    if (dbg_isum) hipLaunchKernelGGL(q4k_gemm_kernel<true>, grid, dim3(kGemmWaves * 64), lds, s, g);
-    else hipLaunchKernelGGL(q4k_gemm_kernel<false>, grid, dim3(kGemmWaves * 64), lds, s, g);
+    const dim3 grid((unsigned)(MT * NT));
+    if (dbg_isum) hipLaunchKernelGGL(q4k_gemm_kernel<true>, grid, dim3(kGemmThreads), kGemmLds, s, g);
+    else hipLaunchKernelGGL(q4k_gemm_kernel<false>, grid, dim3(kGemmThreads), kGemmLds, s, g);
     return hipGetLastError();
 }
 

@@ -378,6 +378,42 @@ def test_gemm_block_sums_bit_exact(ctx, rows, cols, batch):
         assert np.array_equal(imin[r].cpu().numpy(), wm), r
 
 
+@pytest.mark.parametrize("level,split", [(69 / 127, False), (70 / 127, True), (1.0, True)])
+def test_gemm_exact_at_the_f32_bound(ctx, level, split):
+    """The GEMM sums sc*q*q8 in f32 chains, exact while every partial sum
+    stays below 2^24.  Weights of all +1 encode to sc = 63, q = 15 (sc*q =
+    945, the largest); token 0's blocks hold one 1.0 and 255 values `level`,
+    all of one sign (no cancellation): sum |q8| = 127 + 255 round(127 level).
+    69/127 gives 17722 <= 17753, one chain per block with |sum| = 945 * 17722
+    = 16747290 < 2^24; 70/127 and 1.0 exceed 17753, the token's tile folds
+    half blocks (1.0: a full-block chain would pass odd partial sums above
+    2^24).  The other tokens are random, so the flag decides for a mixed tile."""
+    rows, cols, batch = 48, 512, 16
+    say("gemm exact at the f32 bound", level, split)
+    w = O.quantize(O.Q4_K, np.ones(rows * cols, np.float32))
+    x = randn(903, batch * cols).reshape(batch, cols)
+    x[0] = np.float32(level)
+    x[0, ::256] = 1.0
+    act = O.quantize(O.Q8_K, x[0])
+    q8 = np.concatenate([act[b * 292 + 4:b * 292 + 260].view(np.int8) for b in range(cols // 256)])
+    assert (int(np.abs(q8.astype(np.int64)).reshape(-1, 256).sum(axis=1).max()) > 17753) == split
+    W = rlq.Weights(ctx, DT.Q4_K, w, rows, cols)
+    isum, imin = ctx.block_sums(W, torch.from_numpy(x).cuda())
+    torch.cuda.synchronize()
+    stride = w.size // rows
+    for r in range(rows):
+        wi, wm = O.block_sums(O.Q4_K, w[r * stride:(r + 1) * stride], act, cols // 256)
+        assert np.array_equal(isum[r].cpu().numpy(), wi), r
+        assert np.array_equal(imin[r].cpu().numpy(), wm), r
+    assert abs(int(isum[0, 0])) > 16_000_000  # the construction reaches the bound
+    y = ctx.matmul(W, torch.from_numpy(x).cuda())
+    ctx.sync()
+    want = O.matmul(O.Q4_K, w, rows, cols, x, threads=16)
+    got = y.cpu().numpy()
+    for b in range(batch):
+        assert rel_l2(got[b], want[b]) <= REL_L2, b
+
+
 @pytest.mark.parametrize("rows,cols,batch", [(333, 4096, 64), (1000, 2048, 129), (96, 14336, 17)])
 def test_gemm_against_oracle(ctx, rows, cols, batch):
     say("gemm", rows, cols, batch)
