@@ -18,9 +18,9 @@
 // both exact in f16; products are exact in f32, and every partial sum of a
 // chain is an integer bounded by sum_j |sc q x|.  While that bound stays below
 // 2^24 the f32 accumulation is exact in any order.  The activation quantizer
-// flags a token whose block has sum |x| > 17753 (945 * 17753 < 2^24); a token
-// tile with such a token folds every half block (128 values: 128*945*127 <
-// 2^24) instead of every block.  The mins use bsum16 (|.| <= 2032) against
+// flags a (token, block) with sum |x| > 17753 (945 * 17753 < 2^24); a token
+// tile folds such a block in two halves (128 values: 128*945*127 < 2^24)
+// instead of once.  The mins use bsum16 (|.| <= 2032) against
 // mn (<= 63): always exact.  So I and Mn equal the reference's i32 sums, and
 // float(I) (the f32 of an exact integer, or the f32 sum of two exact halves)
 // is the reference's `sumi as f32`; only the f32 order of the per-block terms
@@ -39,55 +39,53 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 // ---------------------------------------------------------------------------
 // Tiling
 //
-// Workgroup: 4 waves (one per SIMD) over 128 tokens x 256 weight rows (16
-// layout tiles of 16 rows).  Wave w owns rows 64w .. 64w+63 as two 32-row MFMA
-// column tiles r and all 128 tokens as four 32-token tiles T: eight 32x32
-// accumulator tiles.  Every weight value is dequantized once per workgroup.
+// Workgroup: 4 waves over 128 tokens x 128 weight rows (8 layout tiles of 16
+// rows); two workgroups share a CU, so each SIMD runs two independent waves
+// and one wave's VALU work (dequantization, the per-block fold) overlaps the
+// other's MFMAs.  Wave w owns rows 32w .. 32w+31 (one MFMA column tile) and
+// the 128 tokens as four 32-token tiles T: each dequantized weight operand
+// feeds four MFMAs.  Accumulators and f32 outputs y live in VGPRs.
 //
 // K is walked in groups of 64 values (4 k-steps of 16).  A group's operands
 // are one LDS stage, filled by global_load_lds_dwordx4 (global -> LDS without
-// VGPRs) three stages ahead in a ring of four; per-block data (weight block
-// headers, activation bsums and scales) sit in a ring of three regions.
-//
-// The f32 accumulators (AGPRs) hold one fold unit: a block, or a half block
-// for flagged tiles.  After each unit the VALU folds them into y (VGPRs).
+// VGPRs) two stages ahead in a ring of three; per-block data (weight block
+// headers, the activation record) sit in a ring of two regions.
 // ---------------------------------------------------------------------------
 constexpr uint32_t kGemmTM = 128;          // tokens per workgroup
-constexpr uint32_t kGemmTN = 256;          // weight rows per workgroup
+constexpr uint32_t kGemmTN = 128;          // weight rows per workgroup
 constexpr uint32_t kGemmThreads = 256;
 constexpr uint32_t kUnsafeAbsSum = 17753;  // floor((2^24 - 1) / 945)
 
 // Activation image, written by gemm_act_kernel.  Per token tile of 128: nb*4
 // groups, then nb block records.
-//   group (b, g): [k-step 4][k half 2][token 128][8 halves]      16 KB
-//   record b:     bsum16 [k half 2][token 128][8 halves]          4 KB
-//                 da [token 128] f32                             512 B
+//   group (b, g): [k-step 4][k half 2][token 128][8 halves]  16 KB
+//   record b:     bsum16 [k half 2][token 128][8 halves]      4 KB
+//                 da [token 128] f32                         512 B
+//                 flags [token 128] u8                       128 B
 // Group g, k-step s, k half h, slot t holds the value at block position
 // 64g + 32(s/2) + 16h + 8(s%2) + kPerm[t], kPerm = {0,2,1,3,4,6,5,7}: the
-// order in which the weight dequantizer below produces sc*q.
+// order in which the weight dequantizer below produces sc*q.  flags: bit 0 a
+// data error in the token's block, bit 1 sum |q8| > kUnsafeAbsSum.
 constexpr uint32_t kActGroupBytes = 16384;
-constexpr uint32_t kActRecordBytes = 4608;
-constexpr uint32_t kActRecordDa = 4096;
+constexpr uint32_t kRecDa = 4096, kRecFlags = 4608, kActRecordBytes = 4736;
 constexpr uint64_t kActTileBlockBytes = 4 * kActGroupBytes + kActRecordBytes;
 
-__device__ __forceinline__ uint64_t act_group_offset(uint32_t nb, uint32_t b, uint32_t g) {
+__device__ __forceinline__ uint64_t act_group_offset(uint32_t b, uint32_t g) {
     return ((uint64_t)b * 4 + g) * kActGroupBytes;
 }
 __device__ __forceinline__ uint64_t act_record_offset(uint32_t nb, uint32_t b) {
     return (uint64_t)nb * 4 * kActGroupBytes + (uint64_t)b * kActRecordBytes;
 }
 
-// LDS
-constexpr uint32_t kSlots = 4, kSlotBytes = 24576, kSlotW = 16384;  // [A 16 KB][W 16 tiles x 512 B]
-constexpr uint32_t kRegions = 3, kRegionBytes = 8704;               // [headers 4 KB][record 4.5 KB]
-constexpr uint32_t kRegBS = 4096, kRegDA = kRegBS + kActRecordDa;
+// LDS per workgroup: stages [A 16 KB][W 8 tiles x 512 B], regions [headers 2 KB][record]
+constexpr uint32_t kSlots = 3, kSlotBytes = 20480, kSlotW = 16384;
+constexpr uint32_t kRegions = 2, kRegRec = 2048, kRegionBytes = kRegRec + kActRecordBytes;
 constexpr uint32_t kGemmLds = kSlots * kSlotBytes + kRegions * kRegionBytes;
 
 // ---------------------------------------------------------------------------
-// Activations: f32 x [M][K] -> the image above, plus tokflag[m] = bit 0 data
-// error, bit 1 "some block has sum |q8| > kUnsafeAbsSum".  Tokens >= M are
-// zeros.  One workgroup of 256 lanes per token: a 16-lane DPP row quantizes
-// one 256-value block (q8k_row16), lane r16 holding positions 16 r16 .. +15.
+// Activations: f32 x [M][K] -> the image above.  Tokens >= M are zeros.  One
+// workgroup per (token tile, block); each 16-lane DPP row quantizes one
+// token's block (q8k_row16), lane r16 holding positions 16 r16 .. +15.
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ int32_t row16_sum_i(int32_t v) {
     v += dpp_i<kQuadXor1>(v);
@@ -98,60 +96,56 @@ __device__ __forceinline__ int32_t row16_sum_i(int32_t v) {
 }
 
 __global__ __launch_bounds__(256) void gemm_act_kernel(const float* __restrict__ x, uint32_t M, uint32_t K,
-                                                       uint8_t* __restrict__ img, uint32_t* __restrict__ tokflag,
-                                                       unsigned long long* err_word, uint32_t err_column0) {
-    const uint32_t m = blockIdx.x, lane = threadIdx.x & 63, r16 = lane & 15;
-    const uint32_t nb = K / 256, upr = K / 16;  // 16-value units per token
-    const uint32_t tok = m % kGemmTM;
-    uint8_t* tile = img + (uint64_t)(m / kGemmTM) * nb * kActTileBlockBytes;
-    int any_bad = 0, any_unsafe = 0;
-    for (uint32_t u = threadIdx.x; u < upr; u += 256) {  // u % 16 == r16: rows of 16 stay whole
-        const uint32_t blk = u / 16;
-        float v[16];
-        if (m < M) {
-            const float4* src = (const float4*)(x + (uint64_t)m * K + u * 16);
+                                                       uint8_t* __restrict__ img, unsigned long long* err_word,
+                                                       uint32_t err_column0) {
+    // workgroup: 16 tokens of one (token tile, block); 16-lane row `row` = one token
+    const uint32_t nb = K / 256, chunks = kGemmTM / 16;
+    const uint32_t chunk = blockIdx.x % chunks, b = (blockIdx.x / chunks) % nb, mt = blockIdx.x / chunks / nb;
+    const uint32_t r16 = threadIdx.x & 15, tok = chunk * 16 + (threadIdx.x >> 4);
+    const uint32_t m = mt * kGemmTM + tok;
+    uint8_t* tile = img + (uint64_t)mt * nb * kActTileBlockBytes;
+    float v[16];
+    if (m < M) {
+        const float4* src = (const float4*)(x + (uint64_t)m * K + b * 256 + r16 * 16);
 #pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                const float4 f = src[k];
-                v[4 * k] = f.x, v[4 * k + 1] = f.y, v[4 * k + 2] = f.z, v[4 * k + 3] = f.w;
-            }
-        } else {
-#pragma unroll
-            for (int k = 0; k < 16; ++k) v[k] = 0.0f;
+        for (int k = 0; k < 4; ++k) {
+            const float4 f = src[k];
+            v[4 * k] = f.x, v[4 * k + 1] = f.y, v[4 * k + 2] = f.z, v[4 * k + 3] = f.w;
         }
-        const Q8KRow o = q8k_row16(v, r16);
-        if (o.kind >= 0) {
-            any_bad = 1;
-            if (r16 == 0)
-                report_error(err_word, o.kind == kKindNonFinite
-                                           ? error_key(err_column0 + m, kKindNonFinite, blk * 256ull + o.index)
-                                           : error_key(err_column0 + m, kKindScale, blk));
-        }
-        int32_t q[16];
+    } else {
 #pragma unroll
-        for (int t = 0; t < 16; ++t) q[t] = (int32_t)(int8_t)(o.q[t / 4] >> (8 * (t % 4)));
-        // positions 16 r16 + t: group r16/4, k-steps 2((r16/2)%2) + t/8, k half r16%2
-        uint8_t* ag = tile + act_group_offset(nb, blk, r16 / 4);
-        const uint32_t s0 = 2 * ((r16 >> 1) & 1), hh = r16 & 1;
-        constexpr int kPerm[8] = {0, 2, 1, 3, 4, 6, 5, 7};
-#pragma unroll
-        for (int so = 0; so < 2; ++so) {
-            f16x8 h;
-#pragma unroll
-            for (int t = 0; t < 8; ++t) h[t] = (_Float16)q[8 * so + kPerm[t]];
-            *(f16x8*)(ag + ((s0 + so) * 2 + hh) * 2048 + tok * 16) = h;
-        }
-        uint8_t* rec = tile + act_record_offset(nb, blk);
-        *(_Float16*)(rec + (r16 / 8) * 2048 + tok * 16 + (r16 % 8) * 2) = (_Float16)o.bsum;
-        if (r16 == 0) *(float*)(rec + kActRecordDa + tok * 4) = o.d;
-        int32_t sa = 0;
-#pragma unroll
-        for (int t = 0; t < 16; ++t) sa += q[t] < 0 ? -q[t] : q[t];
-        if ((uint32_t)row16_sum_i(sa) > kUnsafeAbsSum) any_unsafe = 1;
+        for (int k = 0; k < 16; ++k) v[k] = 0.0f;
     }
-    const int token_bad = __syncthreads_or(any_bad);
-    const int token_unsafe = __syncthreads_or(any_unsafe);
-    if (threadIdx.x == 0) tokflag[m] = (token_bad ? 1u : 0u) | (token_unsafe ? 2u : 0u);
+    const Q8KRow o = q8k_row16(v, r16);
+    if (o.kind >= 0 && r16 == 0)
+        report_error(err_word, o.kind == kKindNonFinite
+                                   ? error_key(err_column0 + m, kKindNonFinite, b * 256ull + o.index)
+                                   : error_key(err_column0 + m, kKindScale, b));
+    int32_t q[16];
+#pragma unroll
+    for (int t = 0; t < 16; ++t) q[t] = (int32_t)(int8_t)(o.q[t / 4] >> (8 * (t % 4)));
+    // positions 16 r16 + t: group r16/4, k-steps 2((r16/2)%2) + t/8, k half r16%2
+    uint8_t* ag = tile + act_group_offset(b, r16 / 4);
+    const uint32_t s0 = 2 * ((r16 >> 1) & 1), hh = r16 & 1;
+    constexpr int kPerm[8] = {0, 2, 1, 3, 4, 6, 5, 7};
+#pragma unroll
+    for (int so = 0; so < 2; ++so) {
+        f16x8 h;
+#pragma unroll
+        for (int t = 0; t < 8; ++t) h[t] = (_Float16)q[8 * so + kPerm[t]];
+        *(f16x8*)(ag + ((s0 + so) * 2 + hh) * 2048 + tok * 16) = h;
+    }
+    uint8_t* rec = tile + act_record_offset(nb, b);
+    *(_Float16*)(rec + (r16 / 8) * 2048 + tok * 16 + (r16 % 8) * 2) = (_Float16)o.bsum;
+    int32_t sa = 0;
+#pragma unroll
+    for (int t = 0; t < 16; ++t) sa += q[t] < 0 ? -q[t] : q[t];
+    sa = row16_sum_i(sa);
+    const int32_t bad = row16_sum_i(o.kind >= 0 ? 1 : 0);
+    if (r16 == 0) {
+        *(float*)(rec + kRecDa + tok * 4) = o.d;
+        rec[kRecFlags + tok] = (uint8_t)((bad ? 1u : 0u) | ((uint32_t)sa > kUnsafeAbsSum ? 2u : 0u));
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -161,7 +155,6 @@ struct GemmArgs {
     const uint8_t* w;  // Q4_K, tiled device layout (rlq_layout.hpp)
     uint32_t rows, nb, ntiles16;
     const uint8_t* img;  // activation image
-    const uint32_t* tokflag;
     uint32_t M, NT, MT;  // tokens; workgroup tiles along rows and tokens
     float* y;            // y[m * ldy + n]
     uint64_t ldy;
@@ -232,27 +225,6 @@ __device__ __forceinline__ GroupScales group_scales(const Q4Words& q) {
     return s;
 }
 
-// B operand of k-step S of a group for one lane: its 16-byte piece holds
-// block positions 64g + 16h + i (low nibble) and 64g + 32 + 16h + i (high
-// nibble), i = 0..15.  S = 0, 1: low nibbles of bytes 8S .. 8S+7; S = 2, 3:
-// high nibbles of bytes 8(S-2) .. ; slot order kPerm.
-template <int S>
-__device__ __forceinline__ f16x8 dequant(const uint4& pc, const GroupScales& sc) {
-    const uint32_t w0 = (S & 1) ? pc.z : pc.x, w1 = (S & 1) ? pc.w : pc.y;
-    constexpr uint32_t mask = S < 2 ? 0x000f000fu : 0x00f000f0u;
-    const f16x2 scale = S < 2 ? sc.lo : sc.hi, neg = S < 2 ? sc.lo_neg : sc.hi_neg;
-    const uint32_t x0 = (w0 & mask) | 0x64006400u, x1 = ((w0 >> 8) & mask) | 0x64006400u;
-    const uint32_t x2 = (w1 & mask) | 0x64006400u, x3 = ((w1 >> 8) & mask) | 0x64006400u;
-    const f16x2 r0 = __builtin_elementwise_fma(as_h2(x0), scale, neg);
-    const f16x2 r1 = __builtin_elementwise_fma(as_h2(x1), scale, neg);
-    const f16x2 r2 = __builtin_elementwise_fma(as_h2(x2), scale, neg);
-    const f16x2 r3 = __builtin_elementwise_fma(as_h2(x3), scale, neg);
-    f16x8 v;
-    v[0] = r0[0], v[1] = r0[1], v[2] = r1[0], v[3] = r1[1];
-    v[4] = r2[0], v[5] = r2[1], v[6] = r3[0], v[7] = r3[1];
-    return v;
-}
-
 // Per-row data of the block being folded: f32 d and dmin and the mins operand
 // (lane half h: mn_{4h} .. mn_{4h+3}, each twice, against bsum16 8h .. 8h+7).
 struct FoldRow {
@@ -278,7 +250,7 @@ struct GemmCtx {
     uint32_t nb, rows, nt, mt, wave, lane, ln, kh;
     const uint8_t* act_tile;  // activation image of token tile mt
     const uint8_t* w_first;   // first weight layout tile of the workgroup
-    uint32_t w_lane[2];       // this lane's offsets (from w_first) of its weight-piece loads
+    uint32_t w_lane;          // this lane's offset (from w_first) of its weight-piece load
     uint32_t h_lane;          // ... and of its header load
     int32_t* dbg_isum;
     int32_t* dbg_imin;
@@ -289,61 +261,99 @@ __device__ __forceinline__ const uint8_t* region_ptr(const GemmCtx& c, uint32_t 
 }
 
 // Issue the LDS-DMA loads of stage s = 4 b + G (clamped past the last block).
-// Every wave issues 6 loads per stage, plus 3 when G == 0: the stage barriers'
-// vmcnt counts depend on it.
+// Every wave issues 5 loads per stage, plus 3 when G == 0: the stage
+// barriers' vmcnt counts depend on it.
 template <int G>
 __device__ __forceinline__ void issue_stage(const GemmCtx& c, uint32_t s) {
     const uint32_t bu = s / 4, b = bu < c.nb ? bu : c.nb - 1;
     const uint32_t slot = c.lds + (s % kSlots) * kSlotBytes;
-    const uint8_t* ag = c.act_tile + act_group_offset(c.nb, b, G) + c.wave * 4 * 1024;
+    const uint8_t* ag = c.act_tile + act_group_offset(b, G) + c.wave * 4096;
 #pragma unroll
     for (int j = 0; j < 4; ++j) g2l(ag + j * 1024, c.lane * 16, slot + (c.wave * 4 + j) * 1024);
     // layout tile t: the qs bytes of group G of its 16 rows are the 512 bytes at
-    // (G/2) * 1024 + (G%2) * 512 of the block's chunk
+    // (G/2) * 1024 + (G%2) * 512 of the block's chunk; wave w loads tiles 2w, 2w+1
     const uint8_t* wb = c.w_first + (uint64_t)b * kQ4KChunk + (G / 2) * 1024 + (G % 2) * 512;
-#pragma unroll
-    for (int j = 0; j < 2; ++j) g2l(wb, c.w_lane[j], slot + kSlotW + (c.wave * 2 + j) * 1024);
+    g2l(wb, c.w_lane, slot + kSlotW + c.wave * 1024);
     if (G == 0) {
         const uint32_t reg = c.lds + kSlots * kSlotBytes + (bu % kRegions) * kRegionBytes;
-        g2l(c.w_first + (uint64_t)b * kQ4KChunk, c.h_lane, reg + c.wave * 1024);
-        const uint8_t* rec = c.act_tile + act_record_offset(c.nb, b) + c.wave * 1152;
-        g2l(rec, c.lane * 16, reg + kRegBS + c.wave * 1152);
-        if (c.lane < 8) g2l(rec + 1024, c.lane * 16, reg + kRegBS + c.wave * 1152 + 1024);
+        if (c.lane < 32) g2l(c.w_first + (uint64_t)b * kQ4KChunk, c.h_lane, reg + c.wave * 512);
+        // the record: 1184 bytes (74 lanes) per wave
+        const uint8_t* rec = c.act_tile + act_record_offset(c.nb, b) + c.wave * 1184;
+        g2l(rec, c.lane * 16, reg + kRegRec + c.wave * 1184);
+        if (c.lane < 10) g2l(rec + 1024, c.lane * 16, reg + kRegRec + c.wave * 1184 + 1024);
     }
 }
 
-// Accumulator tile X = 2T + r of a finished fold unit into y.  MINS: the unit
-// ends a block (its mins term is due).  DBG stores token 0's integers (ADD:
-// the unit is a second half; its integer adds to the first half's).
-template <int X, bool MINS, bool DBG, bool ADD>
-__device__ __forceinline__ void fold_tile(const GemmCtx& c, const f32x16 (&h)[2][4], float (&y)[2][4][16],
-                                          const FoldRow (&fr)[2], const uint8_t* reg, uint32_t b) {
-    constexpr int r = X % 2, T = X / 2;
+// v_and_or_b32 (VOP3 takes no literal: the mask comes in an SGPR, the bias in a VGPR)
+__device__ __forceinline__ uint32_t and_or(uint32_t v, uint32_t mask, uint32_t bias) {
+    uint32_t d;
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(d) : "v"(v), "s"(mask), "v"(bias));
+    return d;
+}
+
+// B operand of k-step S of a group for one lane: its 16-byte piece holds
+// block positions 64g + 16h + i (low nibble) and 64g + 32 + 16h + i (high
+// nibble), i = 0..15.  S = 0, 1: low nibbles of bytes 8S .. 8S+7; S = 2, 3:
+// high nibbles of bytes 8(S-2) .. ; slot order kPerm.  sh: the piece's words
+// shifted right by 8.
+template <int S>
+__device__ __forceinline__ f16x8 dequant_q4(const uint4& pc, const uint4& sh, const GroupScales& sc, uint32_t bias) {
+    const uint32_t w0 = (S & 1) ? pc.z : pc.x, w1 = (S & 1) ? pc.w : pc.y;
+    const uint32_t v0 = (S & 1) ? sh.z : sh.x, v1 = (S & 1) ? sh.w : sh.y;
+    const uint32_t mask = S < 2 ? 0x000f000fu : 0x00f000f0u;
+    const f16x2 scale = S < 2 ? sc.lo : sc.hi, neg = S < 2 ? sc.lo_neg : sc.hi_neg;
+    const f16x2 r0 = __builtin_elementwise_fma(as_h2(and_or(w0, mask, bias)), scale, neg);
+    const f16x2 r1 = __builtin_elementwise_fma(as_h2(and_or(v0, mask, bias)), scale, neg);
+    const f16x2 r2 = __builtin_elementwise_fma(as_h2(and_or(w1, mask, bias)), scale, neg);
+    const f16x2 r3 = __builtin_elementwise_fma(as_h2(and_or(v1, mask, bias)), scale, neg);
+    f16x8 v;
+    v[0] = r0[0], v[1] = r0[1], v[2] = r1[0], v[3] = r1[1];
+    v[4] = r2[0], v[5] = r2[1], v[6] = r3[0], v[7] = r3[1];
+    return v;
+}
+
+// Accumulator tile T of a finished fold unit into y.  MINS: the unit ends a
+// block (its mins term is due).  DBG stores token 0's integers (add: the unit
+// is a second half; its integer adds to the first half's).
+template <int T, bool MINS, bool DBG>
+__device__ __forceinline__ void fold_tile(const GemmCtx& c, const f32x16 (&h)[4], float (&y)[4][16],
+                                          const FoldRow& fr, const uint8_t* reg, uint32_t b, bool add) {
     f32x16 mn = {};
     if (MINS) {
-        const f16x8 bs = *(const f16x8*)(reg + kRegBS + c.kh * 2048 + (32 * T + c.ln) * 16);
-        mn = mfma16(bs, fr[r].mins, (f32x16){});
+        const f16x8 bs = *(const f16x8*)(reg + kRegRec + c.kh * 2048 + (32 * T + c.ln) * 16);
+        mn = mfma16(bs, fr.mins, (f32x16){});
     }
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-        const float4 da = *(const float4*)(reg + kRegDA + (32 * T + 8 * q + 4 * c.kh) * 4);
+        const float4 da = *(const float4*)(reg + kRegRec + kRecDa + (32 * T + 8 * q + 4 * c.kh) * 4);
         const float dav[4] = {da.x, da.y, da.z, da.w};
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
             const int i = 4 * q + k;
-            float t = fr[r].d * h[r][T][i];
-            if (MINS) t = __builtin_fmaf(-fr[r].dmin, mn[i], t);
-            y[r][T][i] = __builtin_fmaf(dav[k], t, y[r][T][i]);
+            float t = fr.d * h[T][i];
+            if (MINS) t = __builtin_fmaf(-fr.dmin, mn[i], t);
+            y[T][i] = __builtin_fmaf(dav[k], t, y[T][i]);
         }
     }
     if (DBG && T == 0) {
-        const uint32_t row = c.nt * kGemmTN + 64 * c.wave + 32 * r + c.ln;
+        const uint32_t row = c.nt * kGemmTN + 32 * c.wave + c.ln;
         if (c.mt == 0 && c.kh == 0 && row < c.rows) {
             int32_t* p = c.dbg_isum + (uint64_t)row * c.nb + b;
-            *p = (ADD ? *p : 0) + (int32_t)h[r][T][0];
+            *p = (add ? *p : 0) + (int32_t)h[T][0];
             if (MINS) c.dbg_imin[(uint64_t)row * c.nb + b] = (int32_t)mn[0];
         }
     }
+}
+
+template <bool MINS, bool DBG>
+__device__ __forceinline__ void fold_all(const GemmCtx& c, const f32x16 (&h)[4], float (&y)[4][16],
+                                         const uint8_t* reg, uint32_t b, bool add) {
+    const uint32_t tl = 2 * c.wave + (c.ln >> 4);
+    const FoldRow fr = fold_row(*(const uint4*)(reg + tl * 256 + (c.ln & 15) * 16), c.kh);
+    fold_tile<0, MINS, DBG>(c, h, y, fr, reg, b, add);
+    fold_tile<1, MINS, DBG>(c, h, y, fr, reg, b, add);
+    fold_tile<2, MINS, DBG>(c, h, y, fr, reg, b, add);
+    fold_tile<3, MINS, DBG>(c, h, y, fr, reg, b, add);
 }
 
 #define RLQ_SWITCH4(v, F)     \
@@ -354,97 +364,78 @@ __device__ __forceinline__ void fold_tile(const GemmCtx& c, const f32x16 (&h)[2]
         default: F(3); break; \
     }
 
-// One block: 4 groups of 4 k-steps into h, folded into y after the block
-// (SPLIT: after each half block).
-template <bool SPLIT, bool DBG>
-__device__ __forceinline__ void gemm_block(const GemmCtx& c, uint32_t b, f32x16 (&h)[2][4], float (&y)[2][4][16]) {
+// One block: 4 groups of 4 k-steps into h, folded into y after the block, or
+// after each half when a token of the tile has the block flagged.
+template <bool DBG>
+__device__ __forceinline__ void gemm_block(const GemmCtx& c, uint32_t b, f32x16 (&h)[4], float (&y)[4][16]) {
     const uint8_t* reg = region_ptr(c, b);
-    Q4Words qw[2];
+    const uint32_t tl = 2 * c.wave + (c.ln >> 4);
+    const uint32_t bias = 0x64006400u;
+    Q4Words qw;
+    bool split = false;
 #pragma unroll
     for (int G = 0; G < 4; ++G) {
         const uint32_t s = b * 4 + G;
-        // stage s has landed for every wave; slot (s - 1) % 4 is free again
+        // stage s has landed for every wave; slot (s - 1) % 3 is free again
         if (DBG) stage_barrier<0>();
-        else if (G < 2) stage_barrier<12>();
-        else stage_barrier<15>();
-        if (G == 0) {  // the block's region arrived with its first stage
-#pragma unroll
-            for (int r = 0; r < 2; ++r) {
-                const uint32_t tl = 4 * c.wave + 2 * r + (c.ln >> 4);
-                qw[r] = q4_words(*(const uint4*)(reg + tl * 256 + (c.ln & 15) * 16));
-            }
-        }
-#define RLQ_ISSUE(k) issue_stage<((k) + 3) % 4>(c, s + 3)
+        else if (G < 3) stage_barrier<5>();
+        else stage_barrier<8>();
+#define RLQ_ISSUE(k) issue_stage<((k) + 2) % 4>(c, s + 2)
         RLQ_SWITCH4(G, RLQ_ISSUE)
 #undef RLQ_ISSUE
-        const uint8_t* slot = c.smem + (s % kSlots) * kSlotBytes;
-        GroupScales sc[2];
-        uint4 pc[2];
-#pragma unroll
-        for (int r = 0; r < 2; ++r) {
-#define RLQ_SC(k) sc[r] = group_scales<k>(qw[r])
-            RLQ_SWITCH4(G, RLQ_SC)
-#undef RLQ_SC
-            const uint32_t tl = 4 * c.wave + 2 * r + (c.ln >> 4);
-            pc[r] = *(const uint4*)(slot + kSlotW + tl * 512 + c.kh * 256 + (c.ln & 15) * 16);
+        if (G == 0) {  // the block's region arrived with its first stage
+            qw = q4_words(*(const uint4*)(reg + tl * 256 + (c.ln & 15) * 16));
+            const uint32_t f0 = reg[kRegRec + kRecFlags + c.lane], f1 = reg[kRegRec + kRecFlags + 64 + c.lane];
+            split = __ballot(((f0 | f1) & 2u) != 0) != 0;  // the same for every wave of the workgroup
         }
+        const uint8_t* slot = c.smem + (s % kSlots) * kSlotBytes;
+        GroupScales sc;
+#define RLQ_SC(k) sc = group_scales<k>(qw)
+        RLQ_SWITCH4(G, RLQ_SC)
+#undef RLQ_SC
+        const uint4 pc = *(const uint4*)(slot + kSlotW + tl * 512 + c.kh * 256 + (c.ln & 15) * 16);
+        const uint4 sh = make_uint4(pc.x >> 8, pc.y >> 8, pc.z >> 8, pc.w >> 8);
+        // software pipeline over the group's 4 k-steps: the A reads of k-step
+        // S+1 are in flight and its B operand is dequantized while the MFMAs
+        // of k-step S run
+        const uint8_t* abase = slot + c.kh * 2048 + c.ln * 16;
+        f16x8 a[2][4], bq[2];
+#pragma unroll
+        for (int T = 0; T < 4; ++T) a[0][T] = *(const f16x8*)(abase + T * 512);
+        bq[0] = dequant_q4<0>(pc, sh, sc, bias);
 #pragma unroll
         for (int S = 0; S < 4; ++S) {
-            f16x8 a[4];
+            if (S < 3) {
 #pragma unroll
-            for (int T = 0; T < 4; ++T)
-                a[T] = *(const f16x8*)(slot + S * 4096 + c.kh * 2048 + (32 * T + c.ln) * 16);
-            f16x8 bq[2];
+                for (int T = 0; T < 4; ++T) a[(S + 1) & 1][T] = *(const f16x8*)(abase + (S + 1) * 4096 + T * 512);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            const bool fresh = S == 0 && G == 0;
 #pragma unroll
-            for (int r = 0; r < 2; ++r) {
-#define RLQ_DQ(k) bq[r] = dequant<k>(pc[r], sc[r])
+            for (int T = 0; T < 4; ++T) h[T] = mfma16(a[S & 1][T], bq[S & 1], fresh ? (f32x16){} : h[T]);
+            if (S < 3) {
+#define RLQ_DQ(k) bq[(S + 1) & 1] = dequant_q4<(k) < 3 ? (k) + 1 : 3>(pc, sh, sc, bias)
                 RLQ_SWITCH4(S, RLQ_DQ)
 #undef RLQ_DQ
             }
-            const bool fresh = S == 0 && (G == 0 || (SPLIT && G == 2));
-#pragma unroll
-            for (int r = 0; r < 2; ++r)
-#pragma unroll
-                for (int T = 0; T < 4; ++T) h[r][T] = mfma16(a[T], bq[r], fresh ? (f32x16){} : h[r][T]);
+            __builtin_amdgcn_sched_barrier(0);
         }
-        if ((G == 1 && SPLIT) || G == 3) {
-            FoldRow fr[2];
+        if (G == 1 && split) {  // first half folded on its own; the second starts from zero
+            fold_all<false, DBG>(c, h, y, reg, b, false);
 #pragma unroll
-            for (int r = 0; r < 2; ++r) {
-                const uint32_t tl = 4 * c.wave + 2 * r + (c.ln >> 4);
-                fr[r] = fold_row(*(const uint4*)(reg + tl * 256 + (c.ln & 15) * 16), c.kh);
-            }
-#define RLQ_FOLD(XX)                                                                                       \
-    {                                                                                                      \
-        if (G == 1) fold_tile<XX, false, DBG, false>(c, h, y, fr, reg, b);                                 \
-        else if (SPLIT) fold_tile<XX, true, DBG, true>(c, h, y, fr, reg, b);                               \
-        else fold_tile<XX, true, DBG, false>(c, h, y, fr, reg, b);                                         \
-    }
-            RLQ_FOLD(0) RLQ_FOLD(1) RLQ_FOLD(2) RLQ_FOLD(3) RLQ_FOLD(4) RLQ_FOLD(5) RLQ_FOLD(6) RLQ_FOLD(7)
-#undef RLQ_FOLD
+            for (int T = 0; T < 4; ++T) h[T] = (f32x16){};
         }
+        if (G == 3) fold_all<true, DBG>(c, h, y, reg, b, split);
     }
-}
-
-template <bool SPLIT, bool DBG>
-__device__ __forceinline__ void gemm_tile(const GemmCtx& c, float (&y)[2][4][16]) {
-    f32x16 h[2][4];
-    // prologue: stages 0, 1, 2 in flight
-    issue_stage<0>(c, 0);
-    issue_stage<1>(c, 1);
-    issue_stage<2>(c, 2);
-    for (uint32_t b = 0; b < c.nb; ++b) gemm_block<SPLIT, DBG>(c, b, h, y);
-    // LDS-DMA loads past the end may still be in flight: they must land before
-    // the workgroup's LDS can go to another workgroup
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 }
 
 template <bool DBG>
-__global__ __launch_bounds__(kGemmThreads) void q4k_gemm_kernel(GemmArgs g) {
+__global__ __launch_bounds__(kGemmThreads, 2) void q4k_gemm_kernel(GemmArgs g) {
     extern __shared__ __align__(16) uint8_t smem[];
     const uint32_t lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     // XCD-aware order: workgroups i, i + 8, ... share an XCD (and its L2); give
-    // each XCD a contiguous run of tiles, token tile major
+    // each XCD a contiguous run of row tiles with all their token tiles, so
+    // the XCD reads its weights from HBM once
     const uint32_t G = g.NT * g.MT;
     uint32_t id = blockIdx.x;
     if (G % 8 == 0) id = (id % 8) * (G / 8) + id / 8;
@@ -452,8 +443,8 @@ __global__ __launch_bounds__(kGemmThreads) void q4k_gemm_kernel(GemmArgs g) {
     c.smem = smem;
     c.nb = g.nb;
     c.rows = g.rows;
-    c.nt = id % g.NT;
-    c.mt = id / g.NT;
+    c.nt = id / g.MT;
+    c.mt = id % g.MT;
     c.wave = wave;
     c.lane = lane;
     c.ln = lane & 31;
@@ -463,52 +454,52 @@ __global__ __launch_bounds__(kGemmThreads) void q4k_gemm_kernel(GemmArgs g) {
     c.dbg_imin = g.dbg_imin;
     c.lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)smem;
     // weight loads: tiles past the last one read the last one (rows >= g.rows are never stored)
-    const uint32_t t0 = c.nt * 16, tmax = g.ntiles16 - 1, tstride = g.nb * kQ4KChunk;
+    const uint32_t t0 = c.nt * (kGemmTN / 16), tmax = g.ntiles16 - 1, tstride = g.nb * kQ4KChunk;
     c.w_first = g.w + (uint64_t)t0 * tstride;
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-        const uint32_t t = t0 + 2 * (wave * 2 + j) + (lane >> 5);
-        c.w_lane[j] = ((t < tmax ? t : tmax) - t0) * tstride + (lane & 31) * 16;
-    }
-    const uint32_t th = t0 + 4 * wave + (lane >> 4);
+    const uint32_t tw = t0 + 2 * wave + (lane >> 5);
+    c.w_lane = ((tw < tmax ? tw : tmax) - t0) * tstride + (lane & 31) * 16;
+    const uint32_t th = t0 + 2 * wave + ((lane >> 4) & 1);
     c.h_lane = ((th < tmax ? th : tmax) - t0) * tstride + 2048 + (lane & 15) * 16;
 
-    // a data error in any token: this call writes nothing
+    // a data error in any token: this call writes nothing (flag bit 0 of every record)
     int bad = 0;
-    for (uint32_t i = threadIdx.x; i < g.M; i += kGemmThreads) bad |= (int)(g.tokflag[i] & 1u);
-    const int unsafe = (int)((g.tokflag[c.mt * kGemmTM + (threadIdx.x & 127)] >> 1) & 1u);
-    if (__syncthreads_or(bad)) return;
-    const bool split = __syncthreads_or(unsafe) != 0;
-
-    float y[2][4][16];
-#pragma unroll
-    for (int r = 0; r < 2; ++r)
-#pragma unroll
-        for (int T = 0; T < 4; ++T)
-#pragma unroll
-            for (int i = 0; i < 16; ++i) y[r][T][i] = 0.0f;
-    if (split) gemm_tile<true, DBG>(c, y);
-    else gemm_tile<false, DBG>(c, y);
-
-#pragma unroll
-    for (int r = 0; r < 2; ++r) {
-        const uint32_t row = c.nt * kGemmTN + 64 * wave + 32 * r + c.ln;
-#pragma unroll
-        for (int T = 0; T < 4; ++T)
-#pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                const uint32_t m = c.mt * kGemmTM + 32 * T + 8 * (i / 4) + 4 * c.kh + (i % 4);
-                if (m < g.M && row < g.rows) g.y[(uint64_t)m * g.ldy + row] = y[r][T][i];
-            }
+    const uint32_t words = g.MT * g.nb * (kGemmTM / 4);
+    for (uint32_t i = threadIdx.x; i < words; i += kGemmThreads) {
+        const uint32_t rec = i / (kGemmTM / 4), part = i % (kGemmTM / 4);
+        const uint8_t* base = g.img + (uint64_t)(rec / g.nb) * g.nb * kActTileBlockBytes +
+                              act_record_offset(g.nb, rec % g.nb) + kRecFlags;
+        bad |= (int)(((const uint32_t*)base)[part] & 0x01010101u);
     }
+    if (__syncthreads_or(bad)) return;
+
+    float y[4][16];
+#pragma unroll
+    for (int T = 0; T < 4; ++T)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) y[T][i] = 0.0f;
+    f32x16 h[4];
+    issue_stage<0>(c, 0);
+    issue_stage<1>(c, 1);
+    for (uint32_t b = 0; b < c.nb; ++b) gemm_block<DBG>(c, b, h, y);
+    // LDS-DMA loads past the end may still be in flight: they must land before
+    // the workgroup's LDS can go to another workgroup
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+
+    const uint32_t row = c.nt * kGemmTN + 32 * wave + c.ln;
+#pragma unroll
+    for (int T = 0; T < 4; ++T)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const uint32_t m = c.mt * kGemmTM + 32 * T + 8 * (i / 4) + 4 * c.kh + (i % 4);
+            if (m < g.M && row < g.rows) g.y[(uint64_t)m * g.ldy + row] = y[T][i];
+        }
 }
 
 // ---------------------------------------------------------------------------
 static uint64_t gemm_padded_tokens(uint64_t M) { return (M + kGemmTM - 1) / kGemmTM * kGemmTM; }
 
 size_t gemm_planes_bytes(uint64_t M, uint64_t K) {
-    const uint64_t Mp = gemm_padded_tokens(M), nb = K / 256;
-    return Mp / kGemmTM * nb * kActTileBlockBytes + Mp * 4;
+    return gemm_padded_tokens(M) / kGemmTM * (K / 256) * kActTileBlockBytes;
 }
 
 hipError_t launch_gemm_q4k(const uint8_t* w, uint64_t rows, uint64_t cols, const float* x, uint64_t M, float* y,
@@ -517,13 +508,12 @@ hipError_t launch_gemm_q4k(const uint8_t* w, uint64_t rows, uint64_t cols, const
     if (rows == 0 || cols == 0 || cols % 256 || M == 0 || rows > 0xffffffffull || cols > (1u << 30) ||
         M > (1u << 24))
         return hipErrorInvalidValue;
-    const uint64_t Mp = gemm_padded_tokens(M), nb = cols / 256, MT = Mp / kGemmTM;
+    const uint64_t nb = cols / 256, MT = gemm_padded_tokens(M) / kGemmTM;
     const uint64_t NT = (rows + kGemmTN - 1) / kGemmTN;
-    if (MT * NT > 0x7fffffffull) return hipErrorInvalidValue;
+    if (MT * NT > 0x7fffffffull || MT * nb * (kGemmTM / 16) > 0x7fffffffull) return hipErrorInvalidValue;
     uint8_t* img = (uint8_t*)scratch;
-    uint32_t* tokflag = (uint32_t*)(img + MT * nb * kActTileBlockBytes);
-    hipLaunchKernelGGL(gemm_act_kernel, dim3((unsigned)Mp), dim3(256), 0, s, x, (uint32_t)M, (uint32_t)cols, img,
-                       tokflag, err_word, 0u);
+    hipLaunchKernelGGL(gemm_act_kernel, dim3((unsigned)(MT * nb * (kGemmTM / 16))), dim3(256), 0, s, x, (uint32_t)M,
+                       (uint32_t)cols, img, err_word, 0u);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     GemmArgs g{};
@@ -532,7 +522,6 @@ hipError_t launch_gemm_q4k(const uint8_t* w, uint64_t rows, uint64_t cols, const
     g.nb = (uint32_t)nb;
     g.ntiles16 = (uint32_t)layout_tiles(rows);
     g.img = img;
-    g.tokflag = tokflag;
     g.M = (uint32_t)M;
     g.NT = (uint32_t)NT;
     g.MT = (uint32_t)MT;
