@@ -4,7 +4,9 @@
 Headline workload: Q4_K decode matvec, 14336 rows x 4096 cols (the Llama-3-8B
 FFN gate/up shape), batch 1.  One step = one rlq_matmul, which is one kernel:
 it quantizes the fp32 activation to Q8_K in its prologue and runs the
-Q4_K x Q8_K matvec.  Weights are N(0, 0.02) fp32 quantized by this library's
+Q4_K x Q8_K matvec.  The metric's second half, the prefill GEMM (M=512 tokens
+against the same weights), is reported in the same line under "prefill": one
+step = one rlq_matmul with batch 512 (Q8_K quantizer kernel + GEMM kernel).  Weights are N(0, 0.02) fp32 quantized by this library's
 own Q4_K encoder on the GPU (bit-exact with the reference's encoder);
 activations are N(0, 1) fp32; both are resident in HBM before timing.
 
@@ -32,7 +34,10 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
+F16_MFMA_PEAK_TFLOPS = 2500.0  # dense f16 MFMA, the instructions the GEMM issues
+INT8_MFMA_PEAK_TOPS = 5000.0   # dense int8 MFMA
 ROTATE = 10
+PREFILL_M = 512
 METRIC = "Q4_K matvec GB/s (14336x4096, B=1) + prefill GEMM TOPS (M=512); tok/s"
 
 
@@ -83,6 +88,27 @@ def time_steps(rlq, ctx, handles, x, y, steps, warmup):
     torch.cuda.synchronize()
     ctx.sync()  # raises if the GPU recorded a data error
     return start.elapsed_time(end) / steps
+
+
+def prefill(rlq, ctx, handles, rows, cols, steps, warmup):
+    """The prefill GEMM over the rotated weight copies: M=512 tokens of N(0,1)."""
+    torch = rlq.torch
+    g = torch.Generator(device="cuda")
+    g.manual_seed(0x51A7E003)
+    x = torch.randn((PREFILL_M, cols), generator=g, device="cuda", dtype=torch.float32)
+    y = torch.empty((PREFILL_M, rows), device="cuda", dtype=torch.float32)
+    ms = time_steps(rlq, ctx, handles, x, y, steps, warmup)
+    ops = 2.0 * PREFILL_M * rows * cols
+    tops = ops / (ms * 1e-3) / 1e12
+    return {
+        "workload": f"Q4_K x Q8_K prefill GEMM, M={PREFILL_M} tokens x K={cols} x N={rows} (Q8_K quantizer "
+                    "kernel + GEMM kernel per step)",
+        "steps": steps, "us_per_step": round(ms * 1e3, 3), "tops": round(tops, 2),
+        "tok_s": round(PREFILL_M / (ms * 1e-3), 1), "ops_per_step": ops,
+        "roofline": {"bound": "mfma", "achieved": round(tops, 2), "peak": F16_MFMA_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(tops / F16_MFMA_PEAK_TFLOPS, 4),
+                     "frac_of_int8_peak": round(tops / INT8_MFMA_PEAK_TOPS, 4), "traffic": None},
+    }
 
 
 def cpu_baseline(dtype, w_host, rows, cols, x_host, budget_s=10.0):
@@ -161,6 +187,7 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(head["gbs"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(head["gbs"] / HBM_PEAK_GBS, 4), "traffic": None},
     }
+    result["prefill"] = prefill(rlq, ctx, handles, rows, cols, max(50, args.steps // 10), max(5, args.warmup // 5))
     if not args.no_cpu:
         xh = x.cpu().numpy().reshape(-1)
         result["cpu_baseline"] = cpu_baseline(DT.Q4_K, host0, rows, cols, xh)
