@@ -396,7 +396,7 @@ static int32_t matmul_impl(rlq_context* ctx, const rlq_weights* w, const float* 
         keys = (unsigned long long*)ctx->keys.p;
         HIP_TRY(launch_fill_u64(keys, batch, 0ull, s));
     }
-    if (w->dtype == kQ4_K && batch > kDecodeMaxBatch) {  // prefill: one int8-MFMA GEMM
+    if (w->dtype == kQ4_K && batch > kDecodeMaxBatch) {  // prefill: the MFMA GEMM
         HIP_TRY(ensure(ctx, ctx->planes, gemm_planes_bytes(batch, w->cols)));
         HIP_TRY(launch_gemm_q4k(w->dev, w->rows, w->cols, x, batch, y, w->rows, ctx->planes.p, ctx->err_words, nullptr,
                                 nullptr, s));

@@ -69,9 +69,9 @@ hipError_t launch_matvec(uint32_t wtype, const uint8_t* w, uint64_t rows, uint64
                          int32_t* dbg_imin, hipStream_t s);
 // ---- gemm.hip ----
 // Prefill GEMM for Q4_K weights: y[m*ldy + r] = dot(row r, token m) for
-// m < M (M > 8 in practice).  Quantizes x [M][cols] to Q8_K planes in
-// `scratch` (gemm_planes_bytes) first; a data error in any token suppresses
-// every output.  `dbg_isum`/`dbg_imin` (may be null) receive token 0's exact
+// m < M (M > 8 in practice).  Quantizes x [M][cols] to Q8_K (as the f16
+// activation image of gemm.hip) in `scratch` (gemm_planes_bytes) first; a
+// data error in any token suppresses every output.  `dbg_isum`/`dbg_imin` (may be null) receive token 0's exact
 // per-(row, block) integers.
 size_t gemm_planes_bytes(uint64_t M, uint64_t K);
 hipError_t launch_gemm_q4k(const uint8_t* w, uint64_t rows, uint64_t cols, const float* x, uint64_t M, float* y,
