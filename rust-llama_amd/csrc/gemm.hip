@@ -260,28 +260,53 @@ __device__ __forceinline__ const uint8_t* region_ptr(const GemmCtx& c, uint32_t 
     return c.smem + kSlots * kSlotBytes + (block % kRegions) * kRegionBytes;
 }
 
-// Issue the LDS-DMA loads of stage s = 4 b + G (clamped past the last block).
+// Issue part P (0..3) of the LDS-DMA loads of stage s = 4 b + G (clamped
+// past the last block); a group issues the next stage's four parts between
+// its k-steps, so a full memory queue stalls the wave while its MFMAs run.
 // Every wave issues 5 loads per stage, plus 3 when G == 0: the stage
 // barriers' vmcnt counts depend on it.
-template <int G>
-__device__ __forceinline__ void issue_stage(const GemmCtx& c, uint32_t s) {
+template <int G, int P>
+__device__ __forceinline__ void issue_part(const GemmCtx& c, uint32_t s) {
     const uint32_t bu = s / 4, b = bu < c.nb ? bu : c.nb - 1;
     const uint32_t slot = c.lds + (s % kSlots) * kSlotBytes;
-    const uint8_t* ag = c.act_tile + act_group_offset(b, G) + c.wave * 4096;
+    if (P < 2) {
+        const uint8_t* ag = c.act_tile + act_group_offset(b, G) + c.wave * 4096;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) g2l(ag + j * 1024, c.lane * 16, slot + (c.wave * 4 + j) * 1024);
-    // layout tile t: the qs bytes of group G of its 16 rows are the 512 bytes at
-    // (G/2) * 1024 + (G%2) * 512 of the block's chunk; wave w loads tiles 2w, 2w+1
-    const uint8_t* wb = c.w_first + (uint64_t)b * kQ4KChunk + (G / 2) * 1024 + (G % 2) * 512;
-    g2l(wb, c.w_lane, slot + kSlotW + c.wave * 1024);
-    if (G == 0) {
-        const uint32_t reg = c.lds + kSlots * kSlotBytes + (bu % kRegions) * kRegionBytes;
-        if (c.lane < 32) g2l(c.w_first + (uint64_t)b * kQ4KChunk, c.h_lane, reg + c.wave * 512);
+        for (int j = 2 * P; j < 2 * P + 2; ++j) g2l(ag + j * 1024, c.lane * 16, slot + (c.wave * 4 + j) * 1024);
+    } else if (P == 2) {
+        // layout tile t: the qs bytes of group G of its 16 rows are the 512 bytes at
+        // (G/2) * 1024 + (G%2) * 512 of the block's chunk; wave w loads tiles 2w, 2w+1
+        const uint8_t* wb = c.w_first + (uint64_t)b * kQ4KChunk + (G / 2) * 1024 + (G % 2) * 512;
+        g2l(wb, c.w_lane, slot + kSlotW + c.wave * 1024);
+        if (G == 0) {
+            const uint32_t reg = c.lds + kSlots * kSlotBytes + (bu % kRegions) * kRegionBytes;
+            if (c.lane < 32) g2l(c.w_first + (uint64_t)b * kQ4KChunk, c.h_lane, reg + c.wave * 512);
+        }
+    } else if (G == 0) {
         // the record: 1184 bytes (74 lanes) per wave
+        const uint32_t reg = c.lds + kSlots * kSlotBytes + (bu % kRegions) * kRegionBytes;
         const uint8_t* rec = c.act_tile + act_record_offset(c.nb, b) + c.wave * 1184;
         g2l(rec, c.lane * 16, reg + kRegRec + c.wave * 1184);
         if (c.lane < 10) g2l(rec + 1024, c.lane * 16, reg + kRegRec + c.wave * 1184 + 1024);
     }
+}
+
+template <int G>
+__device__ __forceinline__ void issue_part_at(const GemmCtx& c, uint32_t s, int P) {
+    switch (P) {  // P is a constant after unrolling
+        case 0: issue_part<G, 0>(c, s); break;
+        case 1: issue_part<G, 1>(c, s); break;
+        case 2: issue_part<G, 2>(c, s); break;
+        default: issue_part<G, 3>(c, s); break;
+    }
+}
+
+template <int G>
+__device__ __forceinline__ void issue_stage(const GemmCtx& c, uint32_t s) {
+    issue_part<G, 0>(c, s);
+    issue_part<G, 1>(c, s);
+    issue_part<G, 2>(c, s);
+    issue_part<G, 3>(c, s);
 }
 
 // v_and_or_b32 (VOP3 takes no literal: the mask comes in an SGPR, the bias in a VGPR)
@@ -380,9 +405,6 @@ __device__ __forceinline__ void gemm_block(const GemmCtx& c, uint32_t b, f32x16 
         if (DBG) stage_barrier<0>();
         else if (G < 3) stage_barrier<5>();
         else stage_barrier<8>();
-#define RLQ_ISSUE(k) issue_stage<((k) + 2) % 4>(c, s + 2)
-        RLQ_SWITCH4(G, RLQ_ISSUE)
-#undef RLQ_ISSUE
         if (G == 0) {  // the block's region arrived with its first stage
             qw = q4_words(*(const uint4*)(reg + tl * 256 + (c.ln & 15) * 16));
             const uint32_t f0 = reg[kRegRec + kRecFlags + c.lane], f1 = reg[kRegRec + kRecFlags + 64 + c.lane];
@@ -413,6 +435,10 @@ __device__ __forceinline__ void gemm_block(const GemmCtx& c, uint32_t b, f32x16 
             const bool fresh = S == 0 && G == 0;
 #pragma unroll
             for (int T = 0; T < 4; ++T) h[T] = mfma16(a[S & 1][T], bq[S & 1], fresh ? (f32x16){} : h[T]);
+            // part S of the stage two ahead (group (G + 2) % 4)
+#define RLQ_ISSUE(k) issue_part_at<((k) + 2) % 4>(c, s + 2, S)
+            RLQ_SWITCH4(G, RLQ_ISSUE)
+#undef RLQ_ISSUE
             if (S < 3) {
 #define RLQ_DQ(k) bq[(S + 1) & 1] = dequant_q4<(k) < 3 ? (k) + 1 : 3>(pc, sh, sc, bias)
                 RLQ_SWITCH4(S, RLQ_DQ)
