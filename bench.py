@@ -20,7 +20,10 @@ roofline  = the same bytes / the kernel's mean duration (the step is one
 cpu_baseline = the CPU oracle (a C restatement of the reference's scalar
             Rust path) on the same weights, 1 thread, repeated for ~10 s.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--extra] [--no-cpu]
+--copy-probe adds one device-to-device copy of 256 MiB before the timed steps:
+the calibration kernel for FETCH_SIZE / WRITE_SIZE counter runs.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--extra] [--no-cpu] [--copy-probe]
 """
 import argparse
 import json
@@ -38,6 +41,13 @@ F16_MFMA_PEAK_TFLOPS = 2500.0  # dense f16 MFMA, the instructions the GEMM issue
 INT8_MFMA_PEAK_TOPS = 5000.0   # dense int8 MFMA
 ROTATE = 10
 PREFILL_M = 512
+# HBM bytes per launch of this build's kernels, measured with rocprofv3 --pmc FETCH_SIZE and
+# WRITE_SIZE (each calibrated against a 256 MiB device copy), recorded in
+# profiles/hbm_traffic_q4k_decode_and_prefill.md: the decode kernel, and the prefill step's
+# two kernels (GEMM + quantizer).
+TRAFFIC_DECODE_BYTES = 33396801
+TRAFFIC_PREFILL_BYTES = 102984548 + 12971772
+COPY_PROBE_BYTES = 256 << 20
 METRIC = "Q4_K matvec GB/s (14336x4096, B=1) + prefill GEMM TOPS (M=512); tok/s"
 
 
@@ -107,7 +117,8 @@ def prefill(rlq, ctx, handles, rows, cols, steps, warmup):
         "tok_s": round(PREFILL_M / (ms * 1e-3), 1), "ops_per_step": ops,
         "roofline": {"bound": "mfma", "achieved": round(tops, 2), "peak": F16_MFMA_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(tops / F16_MFMA_PEAK_TFLOPS, 4),
-                     "frac_of_int8_peak": round(tops / INT8_MFMA_PEAK_TOPS, 4), "traffic": None},
+                     "frac_of_int8_peak": round(tops / INT8_MFMA_PEAK_TOPS, 4),
+                     "traffic": TRAFFIC_PREFILL_BYTES},
     }
 
 
@@ -152,6 +163,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--extra", action="store_true", help="also time the other decode configs")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-probe", action="store_true", help="one 256 MiB device copy (counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one MI355X: every GPU box here has one GPU and this build has no "
@@ -164,6 +176,13 @@ def main():
     torch.cuda.set_device(0)
     ctx = rlq.Context(0)
 
+    if args.copy_probe:
+        src = torch.empty(COPY_PROBE_BYTES, dtype=torch.uint8, device="cuda").fill_(1)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     rows, cols = 14336, 4096
     head, handles, host0, x = run_config(rlq, ctx, DT.Q4_K, rows, cols, 1, 0x51A7E002, args.steps, args.warmup,
                                          ROTATE)
@@ -185,7 +204,7 @@ def main():
                    "rows": rows, "cols": cols, "batch": 1, "rotated_weight_copies": ROTATE,
                    "bytes_per_step": head["bytes_per_step"]},
         "roofline": {"bound": "hbm", "achieved": round(head["gbs"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(head["gbs"] / HBM_PEAK_GBS, 4), "traffic": None},
+                     "frac": round(head["gbs"] / HBM_PEAK_GBS, 4), "traffic": TRAFFIC_DECODE_BYTES},
     }
     result["prefill"] = prefill(rlq, ctx, handles, rows, cols, max(50, args.steps // 10), max(5, args.warmup // 5))
     if not args.no_cpu:
