@@ -13,7 +13,9 @@
  *   - Every function returns an rlq_status and, when `err` is non-null, fills
  *     it.  Codes 1..17 are the reference's QuantError variants in declaration
  *     order (crates/quant/src/lib.rs:45-63) with the same payloads; 18..20 are
- *     this library's own.
+ *     this library's own; 21..23 stand for the model-runtime errors of the
+ *     decode step (crates/model-runtime/src/lib.rs Error: InvalidConfig,
+ *     InvalidToken, InvalidState).
  *   - Validate before mutate: on any error, no output buffer is written
  *     (crates/quant/src/matvec.rs:31-56, encode.rs:37-100).
  *   - Host functions (`rlq_matvec`, `rlq_quantize_into`, ...) take host
@@ -64,7 +66,10 @@ typedef enum rlq_status {
     RLQ_UNREPRESENTABLE_SCALE = 17,     /* a = block (within the column), b = column */
     RLQ_DEVICE_ERROR = 18,              /* a = hipError_t */
     RLQ_UNIMPLEMENTED = 19,             /* dtype: known to the reference, not on this path */
-    RLQ_INVALID_ARGUMENT = 20           /* null pointer or handle */
+    RLQ_INVALID_ARGUMENT = 20,          /* null pointer or handle */
+    RLQ_INVALID_CONFIG = 21,            /* a = check (see rlq_llama_create) */
+    RLQ_INVALID_TOKEN = 22,             /* a = token, b = vocabulary */
+    RLQ_INVALID_STATE = 23              /* a = KV rows held, b = max_context (cache full) */
 } rlq_status;
 
 typedef struct rlq_error {
@@ -124,8 +129,8 @@ void *rlq_context_stream(rlq_context *ctx);
 
 /* Matrix::from_quantized (crates/model-runtime/src/math.rs:35-70): checks the
  * dtype capability, shape and byte length, then keeps a device copy of the
- * weights in the kernels' layout (Q4_K as stored; Q6_K and Q8_0 split into
- * 16-byte-aligned planes).  `bytes_on_device` != 0 when `bytes` is a device
+ * weights in the kernels' tiled layout (16-row tiles; each (tile, block) is
+ * one contiguous chunk in the order the kernels' lanes load it).  `bytes_on_device` != 0 when `bytes` is a device
  * pointer; the device is then synchronized first, so work that produced the
  * bytes on any stream is complete.  Returns after the copy is complete. */
 int32_t rlq_weights_create(rlq_context *ctx, uint32_t dtype, const void *bytes, uint64_t len, uint64_t rows,
@@ -173,6 +178,81 @@ int32_t rlq_sync(rlq_context *ctx, void *stream, rlq_error *err);
  * device pointers of rows*nb i32. */
 int32_t rlq_block_sums(rlq_context *ctx, const rlq_weights *w, const float *x, uint64_t batch, int32_t *isum,
                        int32_t *imin, void *stream, rlq_error *err);
+
+/* ---- dense Llama decode step ------------------------------------------------
+ * LlamaModel of crates/model-runtime/src/llama.rs with quantized matrices,
+ * resident on one GPU with its f32 KV cache.  Every matrix product runs the
+ * decode matvec kernels with the activation quantized to Q8_K (Q8_0 for Q8_0
+ * weights); the attention and the RMSNorm / RoPE / SiLU / residual steps run
+ * on the GPU in the reference's arithmetic order. */
+typedef struct rlq_llama rlq_llama;
+
+/* LlamaConfig (llama.rs:6-17) and the tensor types.  weight_type is that of
+ * the seven layer matrices, output_type that of the output matrix (both Q4_K,
+ * Q6_K or Q8_0), embedding_type that of the token embedding (Q8_0, Q4_K or
+ * Q6_K).  attention_scale 0 means 1/sqrt(head_dim). */
+typedef struct rlq_llama_config {
+    uint64_t vocabulary, width, feed_forward, heads, kv_heads, max_context, n_layers;
+    float rms_epsilon, rope_base, attention_scale;
+    uint32_t weight_type, output_type, embedding_type;
+} rlq_llama_config;
+
+/* LlamaLayer (llama.rs:67-85) without biases: GGUF bytes of the matrices
+ * (rows x cols, rows contiguous: query width x width, key and value
+ * kv_width x width, attention_output width x width, gate and up
+ * feed_forward x width, down width x feed_forward) and f32 norm weights. */
+typedef struct rlq_llama_layer {
+    const float *attention_norm;
+    const void *query, *key, *value, *attention_output;
+    const float *feed_forward_norm;
+    const void *gate, *up, *down;
+} rlq_llama_layer;
+
+/* LlamaWeights: embedding (vocabulary x width), output_norm, output
+ * (vocabulary x width) and n_layers layers.  on_device != 0 when every tensor
+ * pointer is a device pointer (`layers` itself is a host array). */
+typedef struct rlq_llama_tensors {
+    const void *embedding;
+    const float *output_norm;
+    const void *output;
+    const rlq_llama_layer *layers;
+    int32_t on_device;
+} rlq_llama_tensors;
+
+/* LlamaModel::new: LlamaConfig::validate (llama.rs:19-56; RLQ_INVALID_CONFIG
+ * with a = 1 zero or oversized dimension, 2 epsilon, 3 heads/width/kv_heads
+ * grouping, 4 odd head_dim, 5 RoPE base, 6 attention scale, 7 KV size
+ * overflow) and this library's limits (RLQ_UNIMPLEMENTED: a weight type off
+ * the path, width / feed_forward not multiples of 256, kv_width not a
+ * multiple of 16, head_dim not a multiple of 4, or a workgroup's attention
+ * rows beyond 160 KB of LDS), then uploads and tiles the weights.
+ * The tensors may be freed when this returns. */
+int32_t rlq_llama_create(rlq_context *ctx, const rlq_llama_config *cfg, const rlq_llama_tensors *tensors,
+                         rlq_llama **out, rlq_error *err);
+void rlq_llama_destroy(rlq_llama *model);
+/* Drop the KV rows at and above `rows` (0 starts a new sequence). */
+int32_t rlq_llama_truncate(rlq_llama *model, uint64_t rows, rlq_error *err);
+/* KV rows held: the insertion index of the next step. */
+uint64_t rlq_llama_cached(const rlq_llama *model);
+/* LlamaModel::embedding (llama.rs:213-221): the token's decoded embedding row
+ * into hidden (device, width floats). */
+int32_t rlq_llama_embedding(rlq_llama *model, uint32_t token, float *hidden, void *stream, rlq_error *err);
+/* LlamaModel::step (llama.rs:222-248): appends KV row rlq_llama_cached() of
+ * every layer (RoPE at `position`), runs the layers over hidden (device,
+ * width floats, in/out: it receives the last layer's output) and
+ * finish_hidden (:381-392): embedding (width) = RMSNorm(hidden, output_norm),
+ * logits (vocabulary) = output . embedding, argmax (1 u32) = the greedy
+ * choice over the logits.  embedding, logits and argmax are device pointers
+ * and may each be null.  Data errors (a non-finite value) are reported by
+ * rlq_sync; the step's outputs are then unspecified. */
+int32_t rlq_llama_step(rlq_llama *model, float *hidden, uint64_t position, float *embedding, float *logits,
+                       uint32_t *argmax, void *stream, rlq_error *err);
+/* Copies (on `stream`, device to device) the last layer's intermediates of
+ * the latest step: qkv = [query (width) | key (kv_width, before RoPE) | value
+ * (kv_width)], attention (width, the attention output), gate_up = [gate | up]
+ * (2 * feed_forward, before SiLU).  Any output may be null. */
+int32_t rlq_llama_intermediates(const rlq_llama *model, float *qkv, float *attention, float *gate_up,
+                                void *stream, rlq_error *err);
 
 #ifdef __cplusplus
 }

@@ -28,6 +28,7 @@ ERROR_NAMES = {
     11: "ImportanceWeightsRequired", 12: "InvalidImportanceLength", 13: "InvalidImportanceWeight",
     14: "UnsupportedIntegerConversion", 15: "IntegerOutOfRange", 16: "NonFiniteInput",
     17: "UnrepresentableScale", 18: "DeviceError", 19: "Unimplemented", 20: "InvalidArgument",
+    21: "InvalidConfig", 22: "InvalidToken", 23: "InvalidState",
 }
 
 
@@ -65,6 +66,18 @@ def _load():
     lib.oracle_block_sums.restype = None
     lib.oracle_argmax.argtypes, lib.oracle_argmax.restype = [P, U64], U64
     lib.oracle_abs_terms.argtypes, lib.oracle_abs_terms.restype = [U32, P, P, U64], ctypes.c_double
+    F = ctypes.c_float
+    lib.oracle_sse2_exp.argtypes, lib.oracle_sse2_exp.restype = [F], F
+    lib.oracle_silu.argtypes, lib.oracle_silu.restype = [P, U64], None
+    lib.oracle_softmax.argtypes, lib.oracle_softmax.restype = [P, U64], ctypes.c_int
+    lib.oracle_rms_norm.argtypes, lib.oracle_rms_norm.restype = [P, P, U64, F, P], ctypes.c_int
+    lib.oracle_rope.argtypes, lib.oracle_rope.restype = [P, U64, U64, U64, F], None
+    lib.oracle_rope_table.argtypes, lib.oracle_rope_table.restype = [U64, U64, F, P], None
+    lib.oracle_attention.argtypes = [P, P, P, U64, U64, U64, U64, F, P]
+    lib.oracle_attention.restype = ctypes.c_int
+    lib.oracle_llama_embedding.argtypes, lib.oracle_llama_embedding.restype = [P, U32, P], ctypes.c_int
+    lib.oracle_llama_step.argtypes = [P, P, U64, U64, P, P, P, I]
+    lib.oracle_llama_step.restype = ctypes.c_int
     for f in ("oracle_row_bytes", "oracle_matvec_activation_dtype", "oracle_quantize_into",
               "oracle_dequantize_into", "oracle_dot_packed", "oracle_matvec", "oracle_matmul"):
         getattr(lib, f).restype = ctypes.c_int
@@ -194,3 +207,125 @@ def order_tolerance(dtype, w, rows, act, nblocks):
 def argmax(x):
     x = np.ascontiguousarray(x, dtype=np.float32)
     return int(lib().oracle_argmax(_ptr(x), x.size))
+
+
+# ---- dense Llama decode step (rlq_oracle_llama.c) ---------------------------
+
+def _f32c(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def _rc(rc):
+    if rc != 0:
+        raise OracleError(rc, 0, 0, 0)
+
+
+def sse2_exp(x):
+    """cpu_math.rs:94-123, one lane."""
+    return np.float32(lib().oracle_sse2_exp(float(x)))
+
+
+def silu(v):
+    """cpu_math.rs:28-53 (SSE2 policy) on a copy."""
+    v = _f32c(v).copy()
+    lib().oracle_silu(_ptr(v), v.size)
+    return v
+
+
+def softmax(v):
+    """math.rs:293-318 on a copy."""
+    v = _f32c(v).copy()
+    _rc(lib().oracle_softmax(_ptr(v), v.size))
+    return v
+
+
+def rms_norm(x, w, eps):
+    """math.rs:214-228."""
+    x, w = _f32c(x), _f32c(w)
+    out = np.zeros_like(x)
+    _rc(lib().oracle_rms_norm(_ptr(x), _ptr(w), x.size, float(eps), _ptr(out)))
+    return out
+
+
+def rope(v, head_dim, position, base):
+    """math.rs:322-334 on a copy."""
+    v = _f32c(v).copy()
+    lib().oracle_rope(_ptr(v), v.size, int(head_dim), int(position), float(base))
+    return v
+
+
+def rope_table(head_dim, position, base):
+    t = np.zeros(int(head_dim), dtype=np.float32)
+    lib().oracle_rope_table(int(head_dim), int(position), float(base), _ptr(t))
+    return t
+
+
+def attention(q, keys, values, count, heads, kv_heads, head_dim, scale):
+    """math.rs:427-497 with the contiguous padded layout."""
+    q, keys, values = _f32c(q), _f32c(keys), _f32c(values)
+    out = np.zeros(int(heads) * int(head_dim), dtype=np.float32)
+    _rc(lib().oracle_attention(_ptr(q), _ptr(keys), _ptr(values), int(count), int(heads), int(kv_heads),
+                               int(head_dim), float(scale), _ptr(out)))
+    return out
+
+
+LAYER_FIELDS = ("attention_norm", "query", "key", "value", "attention_output", "feed_forward_norm", "gate", "up",
+                "down")
+
+
+class _Layer(ctypes.Structure):
+    _fields_ = [(f, ctypes.c_void_p) for f in LAYER_FIELDS]
+
+
+class _Model(ctypes.Structure):
+    _fields_ = [("vocab", ctypes.c_uint64), ("width", ctypes.c_uint64), ("feed_forward", ctypes.c_uint64),
+                ("heads", ctypes.c_uint64), ("kv_heads", ctypes.c_uint64), ("max_context", ctypes.c_uint64),
+                ("n_layers", ctypes.c_uint64), ("rms_epsilon", ctypes.c_float), ("rope_base", ctypes.c_float),
+                ("attention_scale", ctypes.c_float), ("weight_type", ctypes.c_uint32),
+                ("output_type", ctypes.c_uint32), ("embedding_type", ctypes.c_uint32),
+                ("embedding", ctypes.c_void_p), ("output_norm", ctypes.c_void_p), ("output", ctypes.c_void_p),
+                ("layers", ctypes.POINTER(_Layer))]
+
+
+class LlamaOracle:
+    """LlamaModel (crates/model-runtime/src/llama.rs) restated on the CPU with
+    its own f32 KV cache.  `cfg` has the LlamaConfig fields and the tensor
+    types; `tensors` is the dict of numpy arrays the GPU model takes."""
+
+    def __init__(self, cfg, tensors, threads=8):
+        self.cfg, self.threads = cfg, threads
+        keep = self._keep = []
+
+        def p(a, f32):
+            a = np.ascontiguousarray(a, dtype=np.float32 if f32 else np.uint8)
+            keep.append(a)
+            return a.ctypes.data_as(ctypes.c_void_p)
+
+        n = len(tensors["layers"])
+        self._layers = (_Layer * max(1, n))()
+        for i, L in enumerate(tensors["layers"]):
+            for f in LAYER_FIELDS:
+                setattr(self._layers[i], f, p(L[f], f.endswith("norm")))
+        self._m = _Model(cfg.vocabulary, cfg.width, cfg.feed_forward, cfg.heads, cfg.kv_heads, cfg.max_context, n,
+                         cfg.rms_epsilon, cfg.rope_base, cfg.attention_scale, cfg.weight_type, cfg.output_type,
+                         cfg.embedding_type, p(tensors["embedding"], False), p(tensors["output_norm"], True),
+                         p(tensors["output"], False), self._layers)
+        hd = cfg.width // cfg.heads
+        kvw = cfg.kv_heads * hd
+        self.k_cache = np.zeros((max(1, n), cfg.max_context, kvw), dtype=np.float32)
+        self.v_cache = np.zeros_like(self.k_cache)
+        self.cached = 0
+
+    def embedding(self, token):
+        out = np.zeros(self.cfg.width, dtype=np.float32)
+        _rc(lib().oracle_llama_embedding(ctypes.byref(self._m), int(token), _ptr(out)))
+        return out
+
+    def step(self, hidden, position):
+        """Returns (last layer output, logits); appends one KV row."""
+        h = _f32c(hidden).copy()
+        logits = np.zeros(self.cfg.vocabulary, dtype=np.float32)
+        _rc(lib().oracle_llama_step(ctypes.byref(self._m), _ptr(h), int(position), self.cached,
+                                    _ptr(self.k_cache), _ptr(self.v_cache), _ptr(logits), self.threads))
+        self.cached += 1
+        return h, logits

@@ -46,7 +46,10 @@ enum {
     ORC_UNREPRESENTABLE_SCALE = 17,       /* a = block */
     ORC_DEVICE_ERROR = 18,                /* not produced by the oracle */
     ORC_UNIMPLEMENTED = 19,               /* dtype exists upstream, not restated here */
-    ORC_INVALID_ARGUMENT = 20             /* null pointer */
+    ORC_INVALID_ARGUMENT = 20,            /* null pointer */
+    ORC_INVALID_CONFIG = 21,              /* model-runtime errors of the decode step */
+    ORC_INVALID_TOKEN = 22,
+    ORC_INVALID_STATE = 23
 };
 
 typedef struct oracle_error {
@@ -115,6 +118,55 @@ double oracle_abs_terms(uint32_t wtype, const uint8_t *w_row, const uint8_t *act
 /* Greedy sampler, crates/llama-behavior/src/sampling.rs:607-613: index of the
  * first strict maximum (n >= 1). */
 uint64_t oracle_argmax(const float *x, uint64_t n);
+
+/* ---- dense Llama decode step (rlq_oracle_llama.c) ------------------------ */
+
+/* crates/quant/src/cpu_math.rs:94-123, one lane of the SSE2 exponential. */
+float oracle_sse2_exp(float x);
+/* cpu_math.rs:28-53 (SSE2 policy), in place. */
+void oracle_silu(float *v, uint64_t n);
+/* crates/model-runtime/src/math.rs:293-318 with cpu_math.rs:60-91, in place. */
+int oracle_softmax(float *v, uint64_t n);
+/* math.rs:214-228 */
+int oracle_rms_norm(const float *x, const float *w, uint64_t n, float eps, float *out);
+/* math.rs:322-334, in place over len values of heads of head_dim. */
+void oracle_rope(float *v, uint64_t len, uint64_t head_dim, uint64_t position, float base);
+/* The sin/cos pairs oracle_rope uses at `position`: table[2i] = sin,
+ * table[2i+1] = cos, i < head_dim/2. */
+void oracle_rope_table(uint64_t head_dim, uint64_t position, float base, float *table);
+/* math.rs:427-497, contiguous padded layout (math.rs:365-378). */
+int oracle_attention(const float *q, const float *keys, const float *values, uint64_t count, uint64_t heads,
+                     uint64_t kv_heads, uint64_t head_dim, float scale, float *out);
+
+/* LlamaLayer (crates/model-runtime/src/llama.rs:67-85) without biases: GGUF
+ * bytes of the quantized matrices (rows x cols, rows contiguous) and f32 norm
+ * weights. */
+typedef struct oracle_llama_layer {
+    const float *attention_norm;
+    const uint8_t *query, *key, *value, *attention_output;
+    const float *feed_forward_norm;
+    const uint8_t *gate, *up, *down;
+} oracle_llama_layer;
+
+/* LlamaConfig (llama.rs:6-17) and LlamaWeights.  attention_scale 0 means
+ * 1/sqrt(head_dim). */
+typedef struct oracle_llama_model {
+    uint64_t vocab, width, feed_forward, heads, kv_heads, max_context, n_layers;
+    float rms_epsilon, rope_base, attention_scale;
+    uint32_t weight_type, output_type, embedding_type;
+    const uint8_t *embedding; /* vocab x width */
+    const float *output_norm;
+    const uint8_t *output; /* vocab x width */
+    const oracle_llama_layer *layers;
+} oracle_llama_model;
+
+/* LlamaModel::embedding (llama.rs:213-221). */
+int oracle_llama_embedding(const oracle_llama_model *m, uint32_t token, float *out);
+/* LlamaModel::step (llama.rs:222-392) at the end of a sequential cache of
+ * n_cached rows: hidden (width) in/out, caches [n_layers][max_context][kv_width]
+ * gain row n_cached, logits (vocab) out.  `threads` splits matvec rows. */
+int oracle_llama_step(const oracle_llama_model *m, float *hidden, uint64_t position, uint64_t n_cached,
+                      float *k_cache, float *v_cache, float *logits, int threads);
 
 #ifdef __cplusplus
 }

@@ -18,6 +18,9 @@ importing this package fails if the library has not been built
 
 The device API (Context, Weights) keeps weights resident in HBM and takes
 torch tensors on the GPU; torch supplies device memory and streams only.
+LlamaModel mirrors model-runtime's LlamaModel (crates/model-runtime/src/
+llama.rs): embedding(token) and step(hidden, position) -> (embedding, logits)
+over quantized matrices and a resident f32 KV cache.
 """
 import atexit
 import ctypes
@@ -84,6 +87,7 @@ ERROR_NAMES = {
     11: "ImportanceWeightsRequired", 12: "InvalidImportanceLength", 13: "InvalidImportanceWeight",
     14: "UnsupportedIntegerConversion", 15: "IntegerOutOfRange", 16: "NonFiniteInput",
     17: "UnrepresentableScale", 18: "DeviceError", 19: "Unimplemented", 20: "InvalidArgument",
+    21: "InvalidConfig", 22: "InvalidToken", 23: "InvalidState",
 }
 
 
@@ -140,6 +144,13 @@ SIGNATURES = {
     "rlq_quantize_device": ([_P, _U32, _P, _U64, _U64, _P, _P, _E], _I32),
     "rlq_sync": ([_P, _P, _E], _I32),
     "rlq_block_sums": ([_P, _P, _P, _U64, _P, _P, _P, _E], _I32),
+    "rlq_llama_create": ([_P, _P, _P, ctypes.POINTER(_P), _E], _I32),
+    "rlq_llama_destroy": ([_P], None),
+    "rlq_llama_truncate": ([_P, _U64, _E], _I32),
+    "rlq_llama_cached": ([_P], _U64),
+    "rlq_llama_embedding": ([_P, _U32, _P, _P, _E], _I32),
+    "rlq_llama_step": ([_P, _P, _U64, _P, _P, _P, _P, _E], _I32),
+    "rlq_llama_intermediates": ([_P, _P, _P, _P, _P, _E], _I32),
 }
 
 
@@ -372,3 +383,120 @@ class Weights:
             self._h = None
 
     __del__ = close
+
+
+# ---- dense Llama decode step ----------------------------------------------------
+
+class LlamaConfig(ctypes.Structure):
+    """LlamaConfig (crates/model-runtime/src/llama.rs:6-17) plus the tensor
+    types; attention_scale 0 means 1/sqrt(head_dim)."""
+    _fields_ = [("vocabulary", _U64), ("width", _U64), ("feed_forward", _U64), ("heads", _U64),
+                ("kv_heads", _U64), ("max_context", _U64), ("n_layers", _U64), ("rms_epsilon", ctypes.c_float),
+                ("rope_base", ctypes.c_float), ("attention_scale", ctypes.c_float), ("weight_type", _U32),
+                ("output_type", _U32), ("embedding_type", _U32)]
+
+    @property
+    def head_dim(self):
+        return self.width // self.heads
+
+    @property
+    def kv_width(self):
+        return self.kv_heads * self.head_dim
+
+
+class _LayerT(ctypes.Structure):
+    _fields_ = [("attention_norm", _P), ("query", _P), ("key", _P), ("value", _P), ("attention_output", _P),
+                ("feed_forward_norm", _P), ("gate", _P), ("up", _P), ("down", _P)]
+
+
+class _TensorsT(ctypes.Structure):
+    _fields_ = [("embedding", _P), ("output_norm", _P), ("output", _P), ("layers", ctypes.POINTER(_LayerT)),
+                ("on_device", _I32)]
+
+
+LAYER_FIELDS = ("attention_norm", "query", "key", "value", "attention_output", "feed_forward_norm", "gate", "up",
+                "down")
+
+
+class LlamaModel:
+    """LlamaModel (llama.rs) on the GPU.  `tensors` is a dict with
+    `embedding`, `output_norm`, `output` and `layers` (a list of dicts with
+    LAYER_FIELDS): GGUF bytes of the matrices (rows contiguous) and f32 norm
+    weights, either all numpy arrays or all torch tensors on the GPU.  The
+    model keeps its own tiled copy; the tensors may be dropped afterwards."""
+
+    def __init__(self, ctx, config, tensors):
+        on_dev = torch is not None and isinstance(tensors["embedding"], torch.Tensor)
+        keep = []
+
+        def ptr(a, f32):
+            if on_dev:
+                return _dev_ptr(a.reshape(-1), torch.float32 if f32 else torch.uint8)
+            arr = _f32(a) if f32 else _u8(a)
+            keep.append(arr)
+            return _ptr(arr)
+
+        layers = (_LayerT * max(1, len(tensors["layers"])))()
+        for i, L in enumerate(tensors["layers"]):
+            for f in LAYER_FIELDS:
+                setattr(layers[i], f, ptr(L[f], f.endswith("norm")))
+        t = _TensorsT(ptr(tensors["embedding"], False), ptr(tensors["output_norm"], True),
+                      ptr(tensors["output"], False), layers, 1 if on_dev else 0)
+        h, err = ctypes.c_void_p(), _Err()
+        _check(_lib.rlq_llama_create(ctx._h, ctypes.byref(config), ctypes.byref(t), ctypes.byref(h),
+                                     ctypes.byref(err)), err)
+        self._h, self.ctx, self.config = h, ctx, config
+
+    def close(self):
+        if getattr(self, "_h", None):
+            if not _exiting:
+                _lib.rlq_llama_destroy(self._h)
+            self._h = None
+
+    __del__ = close
+
+    @property
+    def cached(self):
+        """KV rows held: the insertion index of the next step."""
+        return int(_lib.rlq_llama_cached(self._h))
+
+    def truncate(self, rows=0):
+        err = _Err()
+        _check(_lib.rlq_llama_truncate(self._h, int(rows), ctypes.byref(err)), err)
+
+    def embedding(self, token, out=None, stream=None):
+        """LlamaModel::embedding (llama.rs:213-221) -> f32 [width] on the GPU."""
+        if out is None:
+            out = torch.empty(self.config.width, dtype=torch.float32, device="cuda")
+        err = _Err()
+        _check(_lib.rlq_llama_embedding(self._h, int(token), _dev_ptr(out, torch.float32), _stream_ptr(stream),
+                                        ctypes.byref(err)), err)
+        return out
+
+    def step(self, hidden, position, embedding=True, logits=True, argmax=False, stream=None):
+        """LlamaModel::step (llama.rs:222-248): hidden (f32 [width] on the GPU)
+        is updated in place to the last layer's output; returns
+        (embedding, logits, argmax), each None unless asked for."""
+        c = self.config
+        emb = torch.empty(c.width, dtype=torch.float32, device=hidden.device) if embedding else None
+        lg = torch.empty(c.vocabulary, dtype=torch.float32, device=hidden.device) if logits else None
+        am = torch.empty(1, dtype=torch.int32, device=hidden.device) if argmax else None
+        err = _Err()
+        _check(_lib.rlq_llama_step(self._h, _dev_ptr(hidden, torch.float32), int(position),
+                                   _dev_ptr(emb, torch.float32) if emb is not None else None,
+                                   _dev_ptr(lg, torch.float32) if lg is not None else None,
+                                   _dev_ptr(am, torch.int32) if am is not None else None,
+                                   _stream_ptr(stream), ctypes.byref(err)), err)
+        return emb, lg, am
+
+    def intermediates(self, stream=None):
+        """The last layer's [q | k | v] (k before RoPE), attention output and
+        [gate | up] of the latest step, as fresh GPU tensors."""
+        c = self.config
+        qkv = torch.empty(c.width + 2 * c.kv_width, dtype=torch.float32, device="cuda")
+        att = torch.empty(c.width, dtype=torch.float32, device="cuda")
+        gu = torch.empty(2 * c.feed_forward, dtype=torch.float32, device="cuda")
+        err = _Err()
+        _check(_lib.rlq_llama_intermediates(self._h, _dev_ptr(qkv, torch.float32), _dev_ptr(att, torch.float32),
+                                            _dev_ptr(gu, torch.float32), _stream_ptr(stream), ctypes.byref(err)), err)
+        return qkv, att, gu

@@ -16,7 +16,7 @@ import sys
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
-SOURCES = ["api.hip", "gemm.hip", "matvec.hip", "quantize.hip"]
+SOURCES = ["api.hip", "gemm.hip", "llama.hip", "matvec.hip", "quantize.hip"]
 LIB = os.path.join(HERE, "librlq.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 

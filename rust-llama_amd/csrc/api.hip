@@ -6,8 +6,11 @@
 // device error word; nothing is copied to the caller when it is set.
 #include "rlq.h"
 
+#include <math.h>
+
 #include <mutex>
 #include <new>
+#include <vector>
 
 #include "rlq_device.hpp"
 #include "rlq_internal.hpp"
@@ -282,6 +285,9 @@ const char* rlq_status_string(int32_t code) {
         case RLQ_DEVICE_ERROR: return "HIP runtime error";
         case RLQ_UNIMPLEMENTED: return "type is outside the Q8_0/Q4_K/Q6_K path";
         case RLQ_INVALID_ARGUMENT: return "null pointer or handle";
+        case RLQ_INVALID_CONFIG: return "invalid model configuration";
+        case RLQ_INVALID_TOKEN: return "token outside the vocabulary";
+        case RLQ_INVALID_STATE: return "KV cache is full";
         default: return "unknown status";
     }
 }
@@ -450,6 +456,136 @@ int32_t rlq_sync(rlq_context* ctx, void* stream, rlq_error* err) {
     const hipStream_t s = pick(ctx, stream);
     HIP_TRY(hipStreamSynchronize(s));
     return take_error(ctx, 0, s, 0, err);
+}
+
+// ---- dense Llama decode step ---------------------------------------------------
+
+}  // extern "C"
+
+struct rlq_llama {
+    rlq_context* ctx;
+    rlq::LlamaModel m;
+};
+
+namespace {
+
+// LlamaConfig::validate (crates/model-runtime/src/llama.rs:19-56) in its
+// order, then this library's limits.
+int32_t check_llama_config(const rlq_llama_config& c, rlq_error* err) {
+    for (uint64_t v : {c.vocabulary, c.width, c.feed_forward, c.heads, c.kv_heads, c.max_context})
+        if (v == 0 || v > 0xffffffffull) return fail(err, RLQ_INVALID_CONFIG, 0, 1);  // lib.rs:197-206
+    if (!(c.rms_epsilon > 0.0f) || !(c.rms_epsilon <= 3.402823466e38f))
+        return fail(err, RLQ_INVALID_CONFIG, 0, 2);  // lib.rs:207-215
+    if (c.width % c.heads != 0 || c.heads % c.kv_heads != 0) return fail(err, RLQ_INVALID_CONFIG, 0, 3);
+    const uint64_t hd = c.width / c.heads, kvw = c.kv_heads * hd;
+    if (hd % 2 != 0) return fail(err, RLQ_INVALID_CONFIG, 0, 4);
+    if (!(c.rope_base > 0.0f) || !(c.rope_base <= 3.402823466e38f)) return fail(err, RLQ_INVALID_CONFIG, 0, 5);
+    if (c.attention_scale != 0.0f && !(fabsf(c.attention_scale) <= 3.402823466e38f))
+        return fail(err, RLQ_INVALID_CONFIG, 0, 6);
+    uint64_t cache;
+    if (__builtin_mul_overflow(kvw, c.max_context, &cache)) return fail(err, RLQ_INVALID_CONFIG, 0, 7);
+    for (uint32_t t : {c.weight_type, c.output_type, c.embedding_type}) {
+        if (!dtype_known(t)) return fail(err, RLQ_INVALID_TYPE, t);
+        if (!path_weight(t)) return fail(err, RLQ_UNIMPLEMENTED, t);
+    }
+    // whole K-quant blocks along every row; whole 16-row tiles for the fused
+    // Q/K/V and gate/up matrices
+    if (c.width % 256 != 0 || c.feed_forward % 256 != 0 || kvw % 16 != 0)
+        return fail(err, RLQ_UNIMPLEMENTED, c.weight_type, c.width, c.feed_forward);
+    if (hd % 4 != 0) return fail(err, RLQ_UNIMPLEMENTED, 0, hd);  // 16-byte key rows
+    // LDS of the attention workgroups: the G score rows of the softmax, and
+    // the G query heads plus 64 key rows
+    const uint64_t G = c.heads / c.kv_heads, n4 = (c.max_context + 3) / 4 * 4;
+    if ((G * n4 + G * n4 / 4 + 2 * G) * 4 > 160 * 1024 || (G * hd + 64 * (hd + 1)) * 4 > 160 * 1024)
+        return fail(err, RLQ_UNIMPLEMENTED, 0, c.max_context, G);
+    return ok(err);
+}
+
+}  // namespace
+
+extern "C" {
+
+int32_t rlq_llama_create(rlq_context* ctx, const rlq_llama_config* cfg, const rlq_llama_tensors* t, rlq_llama** out,
+                         rlq_error* err) {
+    if (!ctx || !cfg || !t || !out) return fail(err, RLQ_INVALID_ARGUMENT);
+    int32_t rc = check_llama_config(*cfg, err);
+    if (rc) return rc;
+    if (!t->embedding || !t->output_norm || !t->output || (cfg->n_layers && !t->layers))
+        return fail(err, RLQ_INVALID_ARGUMENT);
+    for (uint64_t l = 0; l < cfg->n_layers; ++l) {
+        const rlq_llama_layer& L = t->layers[l];
+        if (!L.attention_norm || !L.query || !L.key || !L.value || !L.attention_output || !L.feed_forward_norm ||
+            !L.gate || !L.up || !L.down)
+            return fail(err, RLQ_INVALID_ARGUMENT, 0, l);
+    }
+    DeviceGuard g(ctx->device);
+    rlq_llama* m = new (std::nothrow) rlq_llama;
+    if (!m) return fail(err, RLQ_ALLOCATION_FAILED);
+    m->ctx = ctx;
+    m->m.device = ctx->device;
+    std::vector<LlamaHostLayer> layers(cfg->n_layers);
+    for (uint64_t l = 0; l < cfg->n_layers; ++l) {
+        const rlq_llama_layer& L = t->layers[l];
+        layers[l] = LlamaHostLayer{L.attention_norm, L.query, L.key, L.value, L.attention_output,
+                                   L.feed_forward_norm, L.gate, L.up, L.down};
+    }
+    const LlamaDims d{cfg->vocabulary, cfg->width, cfg->feed_forward, cfg->heads, cfg->kv_heads, cfg->max_context,
+                      cfg->n_layers, cfg->rms_epsilon, cfg->rope_base, cfg->attention_scale, cfg->weight_type,
+                      cfg->output_type, cfg->embedding_type};
+    const LlamaHostTensors ht{t->embedding, t->output_norm, t->output, layers.data(), t->on_device != 0};
+    hipError_t e = t->on_device ? hipDeviceSynchronize() : hipSuccess;  // device bytes may be in flight
+    if (e == hipSuccess) e = m->m.create(d, ht, ctx->stream);
+    if (e != hipSuccess) {
+        delete m;
+        return e == hipErrorOutOfMemory ? fail(err, RLQ_ALLOCATION_FAILED) : hip_fail(err, e);
+    }
+    *out = m;
+    return ok(err);
+}
+
+void rlq_llama_destroy(rlq_llama* m) {
+    if (!m) return;
+    DeviceGuard g(m->m.device);
+    delete m;
+}
+
+int32_t rlq_llama_truncate(rlq_llama* m, uint64_t rows, rlq_error* err) {
+    if (!m) return fail(err, RLQ_INVALID_ARGUMENT);
+    if (rows < m->m.n_cached) m->m.n_cached = rows;
+    return ok(err);
+}
+
+uint64_t rlq_llama_cached(const rlq_llama* m) { return m ? m->m.n_cached : 0; }
+
+int32_t rlq_llama_embedding(rlq_llama* m, uint32_t token, float* hidden, void* stream, rlq_error* err) {
+    if (!m || !hidden) return fail(err, RLQ_INVALID_ARGUMENT);
+    if (token >= m->m.d.vocab) return fail(err, RLQ_INVALID_TOKEN, 0, token, m->m.d.vocab);  // llama.rs:214-219
+    DeviceGuard g(m->m.device);
+    HIP_TRY(m->m.embedding(token, hidden, (hipStream_t)stream));
+    return ok(err);
+}
+
+int32_t rlq_llama_step(rlq_llama* m, float* hidden, uint64_t position, float* embedding, float* logits,
+                       uint32_t* argmax, void* stream, rlq_error* err) {
+    if (!m || !hidden) return fail(err, RLQ_INVALID_ARGUMENT);
+    if (m->m.n_cached >= m->m.d.max_context) return fail(err, RLQ_INVALID_STATE, 0, m->m.n_cached, m->m.d.max_context);
+    if (position >= m->m.d.max_context) return fail(err, RLQ_INVALID_STATE, 0, position, m->m.d.max_context);
+    DeviceGuard g(m->m.device);
+    HIP_TRY(m->m.step(hidden, position, embedding, logits, argmax, m->ctx->err_words, (hipStream_t)stream));
+    return ok(err);
+}
+
+int32_t rlq_llama_intermediates(const rlq_llama* m, float* qkv, float* attention, float* gate_up, void* stream,
+                                rlq_error* err) {
+    if (!m) return fail(err, RLQ_INVALID_ARGUMENT);
+    DeviceGuard g(m->m.device);
+    const LlamaDims& d = m->m.d;
+    const uint64_t kvw = d.kv_heads * (d.width / d.heads);
+    const hipStream_t s = (hipStream_t)stream;
+    if (qkv) HIP_TRY(hipMemcpyAsync(qkv, m->m.qkv, (d.width + 2 * kvw) * 4, hipMemcpyDeviceToDevice, s));
+    if (attention) HIP_TRY(hipMemcpyAsync(attention, m->m.att, d.width * 4, hipMemcpyDeviceToDevice, s));
+    if (gate_up) HIP_TRY(hipMemcpyAsync(gate_up, m->m.gu, 2 * d.feed_forward * 4, hipMemcpyDeviceToDevice, s));
+    return ok(err);
 }
 
 int32_t rlq_block_sums(rlq_context* ctx, const rlq_weights* w, const float* x, uint64_t batch, int32_t* isum,

@@ -112,14 +112,20 @@ struct MvArgs {
     uint32_t err_column0;             // column index of this launch's column 0
     int32_t* dbg_isum;                // [rows][nb] exact integers vs column 0, or null
     int32_t* dbg_imin;
+    // Input transform applied before quantization (batch 1; MvXform) and the
+    // residual added to every output (y = resid + dot; may alias y), or null.
+    uint32_t xform;
+    float eps;
+    const float* norm_w;
+    const float* resid;
 };
 
 // LDS: q8 [batch][S] | d f32 [nb][8] | (Q4_K) bsums i16 [nb][8][16] | 256
-// zero bytes.  S = cols + 16 is an odd multiple of 16, so the A-operand reads
+// zero bytes | 16 f64 (the RMSNorm reduction of the input transform).  S = cols + 16 is an odd multiple of 16, so the A-operand reads
 // of the eight columns fall in distinct banks.  Lanes whose MFMA A operand is
 // all zero read the zero bytes instead of taking a branch.
 struct LdsMap {
-    uint32_t S, d_off, bs_off, zero_off, total;
+    uint32_t S, d_off, bs_off, zero_off, red_off, total;
 };
 
 __host__ __device__ inline LdsMap lds_map(uint32_t t, uint32_t cols, uint32_t batch) {
@@ -129,7 +135,8 @@ __host__ __device__ inline LdsMap lds_map(uint32_t t, uint32_t cols, uint32_t ba
     m.d_off = (m.S * batch + 15u) & ~15u;
     m.bs_off = m.d_off + nb * 32;
     m.zero_off = m.bs_off + (t == kQ4_K ? nb * 256 : 0);
-    m.total = m.zero_off + 256;
+    m.red_off = m.zero_off + 256;
+    m.total = m.red_off + 128;
     return m;
 }
 
@@ -168,6 +175,56 @@ __device__ __forceinline__ void prefetch_unit(const MvArgs& a, uint32_t wave, fl
     if (a.x && u < (a.cols / 16) * a.batch) load_unit(a, u, v);
 }
 
+// Input transforms of the decode step, applied to the f32 input before it is
+// quantized (batch 1):
+//   kXfRmsNorm   x * scale * norm_w with scale = 1 / sqrt(f32(sum x^2 / K) + eps),
+//                the squares summed in f64 (crates/model-runtime/src/math.rs:214-228)
+//   kXfSiluMul   silu(g) * u over x = [g (K values) | u (K values)]
+//                (crates/model-runtime/src/llama.rs:367-371, SiLU of
+//                crates/quant/src/cpu_math.rs:28-53)
+enum MvXform : uint32_t { kXfNone = 0, kXfRmsNorm = 1, kXfSiluMul = 2 };
+
+__device__ __forceinline__ void load16(const float* p, float (&v)[16]) {
+    const float4* src = (const float4*)p;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const float4 f = src[k];
+        v[4 * k] = f.x, v[4 * k + 1] = f.y, v[4 * k + 2] = f.z, v[4 * k + 3] = f.w;
+    }
+}
+
+// RMSNorm scale of the launch's single input column: every lane adds the
+// squares of its own units in f64, the wave sums are parked in LDS and every
+// thread adds them in wave order, so all threads hold the same value.
+template <int W>
+__device__ __forceinline__ float rms_scale(const MvArgs& a, uint8_t* lds, const LdsMap& L, uint32_t wave,
+                                           const float (&v0)[16]) {
+    const uint32_t units = a.cols / 16, lane = threadIdx.x & 63;
+    double ss = 0.0;
+    for (uint32_t base = wave * 64; base < units; base += W * 64) {
+        const uint32_t u = base + lane;
+        if (u >= units) continue;
+        float v[16];
+        if (base == wave * 64) {
+#pragma unroll
+            for (int k = 0; k < 16; ++k) v[k] = v0[k];
+        } else {
+            load_unit(a, u, v);
+        }
+#pragma unroll
+        for (int k = 0; k < 16; ++k) ss += (double)(v[k] * v[k]);
+    }
+#pragma unroll
+    for (int m = 1; m < 64; m <<= 1) ss += __shfl_xor(ss, m, 64);
+    double* red = (double*)(lds + L.red_off);
+    if (lane == 0) red[wave] = ss;
+    __syncthreads();
+    double total = 0.0;
+#pragma unroll
+    for (int w = 0; w < W; ++w) total += red[w];
+    return 1.0f / sqrtf((float)(total / (double)a.cols) + a.eps);
+}
+
 // Q8_K of all batch columns into LDS.  A 16-lane row quantizes one 256-value
 // block, 16 values per lane (one bsum group per lane).  Returns false in
 // every thread when any block of any column is invalid.
@@ -176,6 +233,14 @@ __device__ __forceinline__ bool stage_q8k(const MvArgs& a, uint8_t* lds, const L
     const uint32_t K = a.cols, upc = K / 16, units = upc * a.batch;
     const uint32_t lane = threadIdx.x & 63, r16 = lane & 15;
     int bad = 0;
+    float scale = 1.0f;
+    if (a.xform == kXfRmsNorm) {
+        scale = rms_scale<W>(a, lds, L, wave, v0);
+        if (!(scale <= 3.402823466e38f) || !(scale > 0.0f)) {  // math.rs:218-220
+            bad = 1;
+            if (threadIdx.x == 0) report_error(a.err_word, error_key(a.err_column0, kKindNonFinite, 0));
+        }
+    }
     for (uint32_t base = wave * 64; base < units; base += W * 64) {
         const uint32_t u = base + lane;
         if (u >= units) continue;  // whole 16-lane rows drop out together (units % 16 == 0)
@@ -186,6 +251,17 @@ __device__ __forceinline__ bool stage_q8k(const MvArgs& a, uint8_t* lds, const L
             for (int k = 0; k < 16; ++k) v[k] = v0[k];
         } else {
             load_unit(a, u, v);
+        }
+        if (a.xform == kXfRmsNorm) {
+            float w[16];
+            load16(a.norm_w + e0, w);
+#pragma unroll
+            for (int k = 0; k < 16; ++k) v[k] = v[k] * scale * w[k];
+        } else if (a.xform == kXfSiluMul) {
+            float up[16];
+            load16(a.x + K + e0, up);
+#pragma unroll
+            for (int k = 0; k < 16; ++k) v[k] = (v[k] / (1.0f + sse2_exp(0.0f - v[k]))) * up[k];
         }
         const Q8KRow o = q8k_row16(v, r16);
         if (o.kind >= 0) {
@@ -288,7 +364,9 @@ __device__ __forceinline__ bool stage_planes(const MvArgs& a, uint8_t* lds, cons
 __device__ __forceinline__ void store_out(const MvArgs& a, uint32_t row, uint32_t b, float v,
                                           unsigned long long& best) {
     if (row < a.rows && b < a.batch) {
-        a.y[(uint64_t)b * a.ldy + row] = v;
+        const uint64_t i = (uint64_t)b * a.ldy + row;
+        if (a.resid) v = a.resid[i] + v;  // math.rs:203-208: hidden += projected
+        a.y[i] = v;
         const unsigned long long k = argmax_key(v, row);
         best = k > best ? k : best;
     }
@@ -887,10 +965,23 @@ hipError_t launch_matvec(uint32_t wtype, const uint8_t* w, uint64_t rows, uint64
                          const ActPlanes* pre, uint64_t batch, float* y, uint64_t ldy,
                          unsigned long long* argmax_key, unsigned long long* err_word, int32_t* dbg_isum,
                          int32_t* dbg_imin, hipStream_t s) {
+    return launch_matvec_ex(wtype, w, rows, cols, x, pre, batch, y, ldy, argmax_key, err_word, dbg_isum, dbg_imin,
+                            MvExtra{}, s);
+}
+
+hipError_t launch_matvec_ex(uint32_t wtype, const uint8_t* w, uint64_t rows, uint64_t cols, const float* x,
+                            const ActPlanes* pre, uint64_t batch, float* y, uint64_t ldy,
+                            unsigned long long* argmax_key, unsigned long long* err_word, int32_t* dbg_isum,
+                            int32_t* dbg_imin, const MvExtra& ex, hipStream_t s) {
     const uint32_t bs = wtype == kQ8_0 ? 32 : 256;
     if (rows == 0 || cols == 0 || cols % bs != 0 || rows > 0xffffffffull - kTileRows || cols > (1u << 30))
         return hipErrorInvalidValue;
     if (dbg_isum && batch > 8) return hipErrorInvalidValue;
+    // the transforms read one f32 column (RMSNorm weights, or [gate | up]) and
+    // exist only in the Q8_K quantizer
+    if (ex.xform != kXfNone && (batch != 1 || !x || wtype == kQ8_0 || ex.xform > kXfSiluMul ||
+                                (ex.xform == kXfRmsNorm && !ex.norm_w)))
+        return hipErrorInvalidValue;
     uint64_t b0 = 0;
     while (b0 < batch) {
         uint32_t nbat = (uint32_t)(batch - b0 < 8 ? batch - b0 : 8);
@@ -919,6 +1010,10 @@ hipError_t launch_matvec(uint32_t wtype, const uint8_t* w, uint64_t rows, uint64
         a.err_column0 = (uint32_t)b0;
         a.dbg_isum = b0 == 0 ? dbg_isum : nullptr;  // column 0 only
         a.dbg_imin = b0 == 0 ? dbg_imin : nullptr;
+        a.xform = ex.xform;
+        a.eps = ex.eps;
+        a.norm_w = ex.norm_w;
+        a.resid = ex.resid ? ex.resid + b0 * ldy : nullptr;
         hipError_t e;
         constexpr int W = kMvWaves;
         const bool dbg = a.dbg_isum != nullptr;

@@ -151,6 +151,30 @@ __device__ __forceinline__ uint4 load_stream16(const void* p) {
     return make_uint4(v.x, v.y, v.z, v.w);
 }
 
+// ---- the reference's SSE2 exponential -------------------------------------
+// One lane of crates/quant/src/cpu_math.rs:94-123 with its exact f32
+// constants and operation order (the file is built without contraction).
+// The source picks one branch per four-lane vector, but both branches give
+// scale*p + scale for every lane with |n| <= 126, so each lane's value
+// depends on that lane alone.
+__device__ __forceinline__ float sse2_exp(float x) {
+    const float z = x * __uint_as_float(0x3fb8aa3bu) + __uint_as_float(0x4b400000u);
+    const float n = z - __uint_as_float(0x4b400000u);
+    const float b = (x - n * __uint_as_float(0x3f317200u)) - n * __uint_as_float(0x35bfbe8eu);
+    const uint32_t exponent = __float_as_uint(z) << 23;
+    const float scale = __uint_as_float(exponent + 0x3f800000u);
+    const float squared = b * b;
+    const float first = __uint_as_float(0x3c072010u) * b + __uint_as_float(0x3d2b9f17u);
+    const float second = __uint_as_float(0x3e2aaf33u) * b + __uint_as_float(0x3efffedbu);
+    const float polynomial = (first * squared + second) * squared + __uint_as_float(0x3f7ffff6u) * b;
+    if (!(fabsf(n) > 126.0f)) return polynomial * scale + scale;
+    const uint32_t shift = n <= 0.0f ? 0x82000000u : 0u;
+    const float high = __uint_as_float(shift + 0x7f000000u);
+    const float low = __uint_as_float(exponent - shift);
+    if (fabsf(n) > 192.0f) return high * high;
+    return (low * polynomial + low) * high;
+}
+
 // ---- device error word ---------------------------------------------------
 //
 // One u64 per context, UINT64_MAX when clear.  The first data error in the

@@ -6,6 +6,8 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include <vector>
+
 namespace rlq {
 
 enum DTypeId : uint32_t { kQ8_0 = 8, kQ4_K = 12, kQ6_K = 14, kQ8_K = 15 };
@@ -67,6 +69,22 @@ hipError_t launch_matvec(uint32_t wtype, const uint8_t* w, uint64_t rows, uint64
                          const ActPlanes* pre, uint64_t batch, float* y, uint64_t ldy,
                          unsigned long long* argmax_key, unsigned long long* err_word, int32_t* dbg_isum,
                          int32_t* dbg_imin, hipStream_t s);
+// Decode-step options of a matvec launch (batch 1 for a transform):
+//   xform   0: quantize x as given; 1: RMSNorm(x) * norm_w with `eps`
+//           (crates/model-runtime/src/math.rs:214-228); 2: x holds
+//           [gate (cols) | up (cols)] and silu(gate) * up is quantized
+//           (crates/model-runtime/src/llama.rs:367-371)
+//   resid   y = resid + dot (math.rs:203-208); may alias y
+struct MvExtra {
+    uint32_t xform = 0;
+    float eps = 0.0f;
+    const float* norm_w = nullptr;
+    const float* resid = nullptr;
+};
+hipError_t launch_matvec_ex(uint32_t wtype, const uint8_t* w, uint64_t rows, uint64_t cols, const float* x,
+                            const ActPlanes* pre, uint64_t batch, float* y, uint64_t ldy,
+                            unsigned long long* argmax_key, unsigned long long* err_word, int32_t* dbg_isum,
+                            int32_t* dbg_imin, const MvExtra& ex, hipStream_t s);
 // ---- gemm.hip ----
 // Prefill GEMM for Q4_K weights: y[m*ldy + r] = dot(row r, token m) for
 // m < M (M > 8 in practice).  Quantizes x [M][cols] to Q8_K (as the f16
@@ -77,6 +95,52 @@ size_t gemm_planes_bytes(uint64_t M, uint64_t K);
 hipError_t launch_gemm_q4k(const uint8_t* w, uint64_t rows, uint64_t cols, const float* x, uint64_t M, float* y,
                            uint64_t ldy, void* scratch, unsigned long long* err_word, int32_t* dbg_isum,
                            int32_t* dbg_imin, hipStream_t s);
+
+// ---- llama.hip ----
+// The dense Llama decode step (crates/model-runtime/src/llama.rs:222-392)
+// over resident weights.  Dimensions are validated by the caller.
+struct LlamaDims {
+    uint64_t vocab, width, feed_forward, heads, kv_heads, max_context, n_layers;
+    float rms_epsilon, rope_base, attention_scale;  // attention_scale 0: 1/sqrt(head_dim)
+    uint32_t weight_type, output_type, embedding_type;
+};
+// GGUF tensors of one layer (rows x cols, rows contiguous) and f32 norms.
+struct LlamaHostLayer {
+    const float* attention_norm;
+    const void *query, *key, *value, *attention_output;
+    const float* feed_forward_norm;
+    const void *gate, *up, *down;
+};
+struct LlamaHostTensors {
+    const void* embedding;  // vocab x width, embedding_type
+    const float* output_norm;
+    const void* output;  // vocab x width, output_type
+    const LlamaHostLayer* layers;
+    bool on_device;
+};
+struct LlamaLayerDev {
+    uint8_t *wqkv = nullptr, *wo = nullptr, *wgu = nullptr, *wdown = nullptr;  // tiled; QKV and gate/up fused
+    float *attn_norm = nullptr, *ffn_norm = nullptr;
+};
+struct LlamaModel {
+    int device = -1;
+    LlamaDims d{};
+    std::vector<LlamaLayerDev> layers;
+    uint8_t *out_w = nullptr, *emb = nullptr;  // tiled output matrix; GGUF embedding rows
+    float *out_norm = nullptr, *k_cache = nullptr, *v_cache = nullptr, *rope_tab = nullptr;
+    float *qkv = nullptr, *scores = nullptr, *att = nullptr, *gu = nullptr, *logits_buf = nullptr;
+    double* part = nullptr;
+    unsigned long long* argmax_keys = nullptr;
+    uint64_t n_cached = 0;  // KV rows held (the insertion index of the next step)
+
+    ~LlamaModel();
+    hipError_t create(const LlamaDims& dims, const LlamaHostTensors& t, hipStream_t s);
+    hipError_t embedding(uint32_t token, float* hidden, hipStream_t s) const;
+    // One step at `position` appending KV row n_cached: hidden (width, device)
+    // in/out; embedding_out (width), logits (vocab) and argmax (1) may be null.
+    hipError_t step(float* hidden, uint64_t position, float* embedding_out, float* logits, uint32_t* argmax,
+                    unsigned long long* err_word, hipStream_t s);
+};
 
 // Argmax keys of the stored rows y[b*rows ..] (keys zeroed beforehand).
 hipError_t launch_argmax_rows(const float* y, uint64_t batch, uint64_t rows, unsigned long long* keys, hipStream_t s);

@@ -1,0 +1,64 @@
+"""Small random-init Llama models for the decode-step tests.
+
+Weights are N(0, 0.02) f32 quantized with the oracle's encoders (Q4_K layer
+matrices and embedding, Q6_K output, as a Q4_K_M-style file), norm weights
+N(1, 0.05); one seed per model.  The shapes are the smallest that keep every
+path of the GPU kernels live: two query heads per KV head, a head dimension of
+64, a context that crosses the 256-column softmax padding.
+"""
+import functools
+import types
+
+import numpy as np
+
+import oracle as O
+
+
+def make_config(n_layers=2, vocabulary=1000, width=256, feed_forward=512, heads=4, kv_heads=2, max_context=300,
+                rms_epsilon=1e-5, rope_base=10000.0, weight_type=O.Q4_K, output_type=O.Q6_K,
+                embedding_type=O.Q4_K):
+    c = types.SimpleNamespace(vocabulary=vocabulary, width=width, feed_forward=feed_forward, heads=heads,
+                              kv_heads=kv_heads, max_context=max_context, n_layers=n_layers,
+                              rms_epsilon=np.float32(rms_epsilon), rope_base=np.float32(rope_base),
+                              attention_scale=np.float32(0.0), weight_type=weight_type, output_type=output_type,
+                              embedding_type=embedding_type)
+    c.head_dim = width // heads
+    c.kv_width = kv_heads * c.head_dim
+    return c
+
+
+def _matrix(rng, dtype, rows, cols, zero=False):
+    if zero:
+        x = np.zeros(rows * cols, np.float32)
+    else:
+        x = rng.normal(0.0, 0.02, rows * cols).astype(np.float32)
+    return O.quantize(dtype, x)
+
+
+@functools.lru_cache(maxsize=8)
+def _tensors(key):
+    (n_layers, vocabulary, width, feed_forward, kv_width, wt, ot, et), seed, zero_layers = key
+    rng = np.random.default_rng(seed)
+    layers = []
+    for _ in range(n_layers):
+        layers.append({
+            "attention_norm": rng.normal(1.0, 0.05, width).astype(np.float32),
+            "query": _matrix(rng, wt, width, width, zero_layers),
+            "key": _matrix(rng, wt, kv_width, width, zero_layers),
+            "value": _matrix(rng, wt, kv_width, width, zero_layers),
+            "attention_output": _matrix(rng, wt, width, width, zero_layers),
+            "feed_forward_norm": rng.normal(1.0, 0.05, width).astype(np.float32),
+            "gate": _matrix(rng, wt, feed_forward, width),
+            "up": _matrix(rng, wt, feed_forward, width),
+            "down": _matrix(rng, wt, width, feed_forward, zero_layers),
+        })
+    # token embeddings of unit scale, as a trained model's
+    emb = O.quantize(et, rng.normal(0.0, 1.0, vocabulary * width).astype(np.float32))
+    return {"embedding": emb, "output_norm": rng.normal(1.0, 0.05, width).astype(np.float32),
+            "output": _matrix(rng, ot, vocabulary, width), "layers": layers}
+
+
+def make_tensors(cfg, seed, zero_layers=False):
+    shape = (cfg.n_layers, cfg.vocabulary, cfg.width, cfg.feed_forward, cfg.kv_width, cfg.weight_type,
+             cfg.output_type, cfg.embedding_type)
+    return _tensors((shape, seed, zero_layers))

@@ -1,0 +1,191 @@
+"""GPU parity of the dense Llama decode step (rlq_llama_*, llama.hip) against
+the CPU oracle (oracle/rlq_oracle_llama.c).
+
+Bars, per part of the step (tests/llama_fixture.py models):
+  - embedding rows and the final RMSNorm: bit-exact;
+  - Q/K/V projections (RMSNorm fused into the quantizer): relative L2 <= 1e-5
+    against the oracle's matvec of its own RMSNorm (the quantized activation
+    is the same bytes; only the f32 combine order of the exact integer block
+    sums differs);
+  - attention, given the GPU's own q/k/v: bit-exact (same RoPE table, the QK
+    sums in the reference's order, the SSE2 softmax, P.V in f64);
+  - the layer output, given the GPU's own attention output and gate/up
+    values: relative L2 <= 1e-5 (the O and down inputs quantize to the same
+    bytes);
+  - gate/up: relative L2 <= 1e-3.  Their input is the RMSNorm of a residual
+    stream that already differs from the oracle's in the last f32 bits (the O
+    projection's combine order), so one Q8_K rounding of its values may land
+    on the other side; one such flip moves the product by about 4e-4;
+  - free-running multi-layer steps: relative L2 <= 2e-3 on the logits for
+    the same reason, and the same greedy token where the oracle's top-two
+    margin exceeds the observed error.
+Every test prints its case before touching the GPU.
+"""
+import numpy as np
+import pytest
+
+import oracle as O
+from llama_fixture import make_config, make_tensors
+from rlq_loader import load
+
+pytestmark = pytest.mark.gpu
+
+rlq = load()
+torch = rlq.torch
+
+
+def say(*a):
+    print("[case]", *a, flush=True)
+
+
+def rel_l2(got, want):
+    got, want = np.asarray(got, np.float64), np.asarray(want, np.float64)
+    den = np.linalg.norm(want)
+    return np.linalg.norm(got - want) / (den if den > 0 else 1.0)
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    c = rlq.Context(0)
+    yield c
+    c.close()
+
+
+def gpu_config(cfg):
+    return rlq.LlamaConfig(cfg.vocabulary, cfg.width, cfg.feed_forward, cfg.heads, cfg.kv_heads, cfg.max_context,
+                           cfg.n_layers, float(cfg.rms_epsilon), float(cfg.rope_base), float(cfg.attention_scale),
+                           cfg.weight_type, cfg.output_type, cfg.embedding_type)
+
+
+def models(ctx, n_layers, seed, **kw):
+    cfg = make_config(n_layers=n_layers, **kw)
+    t = make_tensors(cfg, seed)
+    return cfg, t, rlq.LlamaModel(ctx, gpu_config(cfg), t), O.LlamaOracle(cfg, t)
+
+
+def host(x):
+    return x.detach().cpu().numpy()
+
+
+def test_embedding_rows_exact(ctx):
+    say("llama embedding rows, 0 layers")
+    cfg, t, g, o = models(ctx, 0, 21)
+    for tok in (0, 1, 499, 999):
+        assert np.array_equal(host(g.embedding(tok)), o.embedding(tok)), tok
+    with pytest.raises(rlq.QuantError) as e:
+        g.embedding(cfg.vocabulary)
+    assert e.value.name == "InvalidToken"
+
+
+def test_output_head_without_layers(ctx):
+    """RMSNorm fused into the Q6_K output matvec; the fused greedy argmax."""
+    say("llama step, 0 layers: final norm + output matvec + argmax")
+    cfg, t, g, o = models(ctx, 0, 22)
+    for tok, pos in ((3, 0), (77, 1), (998, 2)):
+        h = g.embedding(tok)
+        emb, logits, am = g.step(h, pos, embedding=True, logits=True, argmax=True)
+        ctx.sync()
+        h_o, logits_o = o.step(o.embedding(tok), pos)
+        assert np.array_equal(host(emb), O.rms_norm(h_o, t["output_norm"], cfg.rms_epsilon))
+        assert rel_l2(host(logits), logits_o) <= 1e-5
+        lg = host(logits)
+        assert int(host(am)[0]) == int(np.argmax(lg))
+
+
+def test_one_layer_parts(ctx):
+    """Each part of one layer against the oracle fed with the GPU's own
+    intermediates, over several steps (the cache grows past 64 rows: two
+    attention chunks)."""
+    say("llama 1 layer, parts, 70 steps")
+    cfg, t, g, o = models(ctx, 1, 23)
+    L = t["layers"][0]
+    W, kvw, hd, F, wt = cfg.width, cfg.kv_width, cfg.head_dim, cfg.feed_forward, cfg.weight_type
+    scale = np.float32(1.0) / np.sqrt(np.float32(hd))
+    kc = np.zeros((cfg.max_context, kvw), np.float32)
+    vc = np.zeros_like(kc)
+    rng = np.random.default_rng(5)
+    worst = {}
+    for step in range(70):
+        tok = int(rng.integers(cfg.vocabulary))
+        h0 = o.embedding(tok)
+        h = torch.from_numpy(h0).cuda()
+        g.step(h, step, embedding=False, logits=False)
+        qkv, att, gu = (host(x) for x in g.intermediates())
+        ctx.sync()
+        # Q/K/V from the exact RMSNorm
+        norm = O.rms_norm(h0, L["attention_norm"], cfg.rms_epsilon)
+        for name, lo, hi, rows in (("query", 0, W, W), ("key", W, W + kvw, kvw), ("value", W + kvw, W + 2 * kvw, kvw)):
+            e = rel_l2(qkv[lo:hi], O.matvec(wt, L[name], rows, W, norm))
+            worst[name] = max(worst.get(name, 0), e)
+            assert e <= 1e-5, (step, name, e)
+        # attention from the GPU's q/k/v: bit-exact
+        q = O.rope(qkv[:W], hd, step, cfg.rope_base)
+        kc[step] = O.rope(qkv[W:W + kvw], hd, step, cfg.rope_base)
+        vc[step] = qkv[W + kvw:]
+        want_att = O.attention(q, kc[:step + 1], vc[:step + 1], step + 1, cfg.heads, cfg.kv_heads, hd, scale)
+        assert np.array_equal(att, want_att), (step, np.max(np.abs(att - want_att)))
+        # the rest of the layer from the GPU's attention output and gate/up
+        hm = h0 + O.matvec(wt, L["attention_output"], W, W, att)
+        n2 = O.rms_norm(hm, L["feed_forward_norm"], cfg.rms_epsilon)
+        want_gu = np.concatenate([O.matvec(wt, L["gate"], F, W, n2), O.matvec(wt, L["up"], F, W, n2)])
+        e = rel_l2(gu, want_gu)
+        worst["gate_up"] = max(worst.get("gate_up", 0), e)
+        assert e <= 1e-3, (step, e)
+        act = O.silu(gu[:F]) * gu[F:]
+        want_h = hm + O.matvec(wt, L["down"], W, F, act)
+        e = rel_l2(host(h), want_h)
+        worst["hidden"] = max(worst.get("hidden", 0), e)
+        assert e <= 1e-5, (step, e)
+    print("worst relative L2 per part:", worst)
+
+
+def test_free_running_steps(ctx):
+    say("llama 2 layers, 12 free-running steps, logits vs oracle")
+    cfg, t, g, o = models(ctx, 2, 24)
+    rng = np.random.default_rng(6)
+    worst = 0.0
+    for step in range(12):
+        tok = int(rng.integers(cfg.vocabulary))
+        h = g.embedding(tok)
+        _, logits, am = g.step(h, step, embedding=False, logits=True, argmax=True)
+        ctx.sync()
+        _, logits_o = o.step(o.embedding(tok), step)
+        lg = host(logits)
+        e = rel_l2(lg, logits_o)
+        worst = max(worst, e)
+        assert e <= 2e-3, (step, e)
+        top = np.sort(logits_o.astype(np.float64))[::-1]
+        margin = top[0] - top[1]
+        if margin > 4 * np.max(np.abs(lg.astype(np.float64) - logits_o)):
+            assert int(host(am)[0]) == O.argmax(logits_o), step
+    print("worst logits relative L2:", worst)
+
+
+def test_cache_limit_and_truncate(ctx):
+    say("llama 1 layer, context 8: cache full, truncate")
+    cfg, t, g, o = models(ctx, 1, 25, max_context=8)
+    h = g.embedding(1)
+    for step in range(8):
+        g.step(h, step, embedding=False, logits=False)
+    assert g.cached == 8
+    with pytest.raises(rlq.QuantError) as e:
+        g.step(h, 8, embedding=False, logits=False)
+    assert e.value.name == "InvalidState"
+    g.truncate(3)
+    assert g.cached == 3
+    g.step(h, 3, embedding=False, logits=False)
+    ctx.sync()
+    assert g.cached == 4
+
+
+@pytest.mark.parametrize("field,value,check", [
+    ("heads", 3, 3), ("kv_heads", 3, 3), ("rms_epsilon", 0.0, 2), ("rope_base", -1.0, 5), ("vocabulary", 0, 1)])
+def test_config_checks(ctx, field, value, check):
+    say("llama config check", field, value)
+    cfg = make_config(n_layers=1)
+    t = make_tensors(cfg, 26)
+    c = gpu_config(cfg)
+    setattr(c, field, value)
+    with pytest.raises(rlq.QuantError) as e:
+        rlq.LlamaModel(ctx, c, t)
+    assert e.value.name == "InvalidConfig" and e.value.a == check
