@@ -23,7 +23,12 @@ cpu_baseline = the CPU oracle (a C restatement of the reference's scalar
 --copy-probe adds one device-to-device copy of 256 MiB before the timed steps:
 the calibration kernel for FETCH_SIZE / WRITE_SIZE counter runs.
 
+"decode_step" (config 5) times whole decode steps of a random-init Llama-3-8B-shape model
+(Q4_K layers, Q6_K output) at a context of ~1000 rows: tok/s and the step's algorithmic bytes
+(every weight byte once + the KV rows read) per second.
+
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--extra] [--no-cpu] [--copy-probe]
+                       [--no-llama] [--llama-steps N] [--llama-cpu]
 """
 import argparse
 import json
@@ -156,6 +161,126 @@ def run_config(rlq, ctx, dtype, rows, cols, batch, seed, steps, warmup, copies):
     return out, handles, host0, x
 
 
+# Llama-3-8B decode-step shape: 32 layers, d_model 4096, 32 query / 8 KV heads of 128, FFN 14336,
+# vocabulary 128256, f32 KV cache of 1024 rows; Q4_K layer matrices and embedding, Q6_K output.
+LLAMA = dict(vocabulary=128256, width=4096, feed_forward=14336, heads=32, kv_heads=8, max_context=1024,
+             n_layers=32, rms_epsilon=1e-5, rope_base=500000.0)
+
+
+def llama_tensors(rlq, ctx, cfg, seed):
+    """Random-init weights on the GPU: matrices N(0, 0.02) and the embedding N(0, 1) in f32, encoded
+    by the library's own Q4_K / Q6_K encoders; norm weights N(1, 0.05)."""
+    torch = rlq.torch
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    DT = rlq.DType
+
+    def mat(dtype, rows, cols, std=0.02):
+        x = torch.randn((rows, cols), generator=g, device="cuda", dtype=torch.float32) * std
+        out = ctx.quantize(dtype, x)
+        del x
+        return out
+
+    def norm(n):
+        return torch.randn(n, generator=g, device="cuda", dtype=torch.float32) * 0.05 + 1.0
+
+    W, F, kvw = cfg.width, cfg.feed_forward, cfg.kv_width
+    layers = []
+    for _ in range(cfg.n_layers):
+        layers.append({"attention_norm": norm(W), "query": mat(DT.Q4_K, W, W), "key": mat(DT.Q4_K, kvw, W),
+                       "value": mat(DT.Q4_K, kvw, W), "attention_output": mat(DT.Q4_K, W, W),
+                       "feed_forward_norm": norm(W), "gate": mat(DT.Q4_K, F, W), "up": mat(DT.Q4_K, F, W),
+                       "down": mat(DT.Q4_K, W, F)})
+    emb = torch.cat([mat(DT.Q4_K, 8016, W, 1.0) for _ in range(cfg.vocabulary // 8016)])
+    t = {"embedding": emb, "output_norm": norm(W), "output": mat(DT.Q6_K, cfg.vocabulary, W), "layers": layers}
+    ctx.sync()
+    return t
+
+
+def decode_step(rlq, ctx, steps, warmup, cpu=False):
+    """Config 5: one decode step of the Llama-3-8B-shape model per token (embedding row, 32 layers,
+    final norm, Q6_K output matvec, greedy argmax), with synthetic tokens; the KV cache is filled
+    to max_context - warmup - steps rows first, so the timed steps see a context of ~1000 rows."""
+    torch = rlq.torch
+    DT = rlq.DType
+    L = LLAMA
+    cfg = rlq.LlamaConfig(L["vocabulary"], L["width"], L["feed_forward"], L["heads"], L["kv_heads"],
+                          L["max_context"], L["n_layers"], L["rms_epsilon"], L["rope_base"], 0.0, DT.Q4_K, DT.Q6_K,
+                          DT.Q4_K)
+    t0 = time.perf_counter()
+    tensors = llama_tensors(rlq, ctx, cfg, 0x51A7E005)
+    gen_s = time.perf_counter() - t0
+    model = rlq.LlamaModel(ctx, cfg, tensors)
+    host_tensors = None
+    if cpu:
+        host_tensors = {"embedding": tensors["embedding"].cpu().numpy(),
+                        "output_norm": tensors["output_norm"].cpu().numpy(),
+                        "output": tensors["output"].cpu().numpy(),
+                        "layers": [{k: v.cpu().numpy() for k, v in l.items()} for l in tensors["layers"]]}
+    del tensors
+    torch.cuda.empty_cache()
+    rng = np.random.default_rng(5)
+    toks = rng.integers(0, cfg.vocabulary, size=cfg.max_context).tolist()
+    h = torch.empty(cfg.width, dtype=torch.float32, device="cuda")
+    am = torch.empty(1, dtype=torch.int32, device="cuda")
+    fill = cfg.max_context - warmup - steps
+    if fill < 0:
+        raise ValueError("warmup + steps exceed the 1024-row context")
+
+    def one(pos):
+        model.embedding(toks[pos], h)
+        model.step(h, pos, embedding=False, logits=False, argmax=True)
+
+    for pos in range(fill + warmup):
+        one(pos)
+    ctx.sync()
+    stream = torch.cuda.current_stream()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record(stream)
+    for pos in range(fill + warmup, fill + warmup + steps):
+        one(pos)
+    end.record(stream)
+    torch.cuda.synchronize()
+    ctx.sync()
+    ms = start.elapsed_time(end) / steps
+    kvw = cfg.kv_heads * (cfg.width // cfg.heads)
+    weights = cfg.n_layers * (rlq.row_bytes(DT.Q4_K, cfg.width) * (2 * cfg.width + 2 * kvw + 2 * cfg.feed_forward)
+                              + rlq.row_bytes(DT.Q4_K, cfg.feed_forward) * cfg.width) \
+        + rlq.row_bytes(DT.Q6_K, cfg.width) * cfg.vocabulary
+    mean_ctx = fill + warmup + (steps + 1) / 2.0
+    kv = 2 * cfg.n_layers * mean_ctx * kvw * 4
+    nbytes = weights + kv
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    out = {"workload": "Llama-3-8B-shape decode step: 32 layers, d 4096, 32/8 heads of 128, FFN 14336, vocab 128256, "
+                       "Q4_K layers + Q6_K output, f32 KV cache; embedding row + 32 layers + final norm + output "
+                       "matvec + greedy argmax per token",
+           "steps": steps, "context_rows": [fill + warmup + 1, fill + warmup + steps],
+           "ms_per_token": round(ms, 4), "tok_s": round(1e3 / ms, 2),
+           "bytes_per_token": int(nbytes), "weight_bytes": int(weights), "kv_bytes_mean": int(kv),
+           "achieved_gbs": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
+           "data": "synthetic random-init weights (N(0,0.02) matrices, N(0,1) embedding, N(1,0.05) norms) and "
+                   "random tokens", "weight_generation_s": round(gen_s, 1)}
+    if cpu:
+        import oracle
+
+        oc = type("C", (), {})()
+        for k, v in L.items():
+            setattr(oc, k, v)
+        oc.attention_scale, oc.weight_type, oc.output_type, oc.embedding_type = 0.0, 12, 14, 12
+        orc = oracle.LlamaOracle(oc, host_tensors, threads=1)
+        x = orc.embedding(toks[0])
+        t1 = time.perf_counter()
+        orc.step(x, 0)
+        el = time.perf_counter() - t1
+        out["cpu_baseline"] = {"value": round(1.0 / el, 4), "unit": "tok/s", "cores": 1, "kind": "port",
+                               "sample": f"one decode step at context 1 (the oracle's scalar restatement, "
+                                         f"1 thread): {el:.2f} s"}
+    model.close()
+    torch.cuda.empty_cache()
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -164,6 +289,9 @@ def main():
     ap.add_argument("--extra", action="store_true", help="also time the other decode configs")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--copy-probe", action="store_true", help="one 256 MiB device copy (counter calibration)")
+    ap.add_argument("--no-llama", action="store_true", help="skip the Llama decode step (config 5)")
+    ap.add_argument("--llama-steps", type=int, default=32)
+    ap.add_argument("--llama-cpu", action="store_true", help="also time one oracle decode step on the host")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one MI355X: every GPU box here has one GPU and this build has no "
@@ -212,6 +340,9 @@ def main():
         result["cpu_baseline"] = cpu_baseline(DT.Q4_K, host0, rows, cols, xh)
     for h in handles:
         h.close()
+    torch.cuda.empty_cache()
+    if not args.no_llama:
+        result["decode_step"] = decode_step(rlq, ctx, args.llama_steps, 8, cpu=args.llama_cpu)
     if args.extra:
         extra = {}
         for name, (t, r, c, b, copies) in {

@@ -492,12 +492,10 @@ int32_t check_llama_config(const rlq_llama_config& c, rlq_error* err) {
     // Q/K/V and gate/up matrices
     if (c.width % 256 != 0 || c.feed_forward % 256 != 0 || kvw % 16 != 0)
         return fail(err, RLQ_UNIMPLEMENTED, c.weight_type, c.width, c.feed_forward);
-    if (hd % 4 != 0) return fail(err, RLQ_UNIMPLEMENTED, 0, hd);  // 16-byte key rows
-    // LDS of the attention workgroups: the G score rows of the softmax, and
-    // the G query heads plus 64 key rows
-    const uint64_t G = c.heads / c.kv_heads, n4 = (c.max_context + 3) / 4 * 4;
-    if ((G * n4 + G * n4 / 4 + 2 * G) * 4 > 160 * 1024 || (G * hd + 64 * (hd + 1)) * 4 > 160 * 1024)
-        return fail(err, RLQ_UNIMPLEMENTED, 0, c.max_context, G);
+    if (hd % 16 != 0 || hd > 256) return fail(err, RLQ_UNIMPLEMENTED, 0, hd);  // 8-dim slices, 16 float4 per thread
+    // LDS of the attention workgroups (their score rows grow with the context)
+    if (llama_attn_lds_bytes(c.heads, c.kv_heads, hd, c.max_context) > 159 * 1024)
+        return fail(err, RLQ_UNIMPLEMENTED, 0, c.max_context, c.heads / c.kv_heads);
     return ok(err);
 }
 

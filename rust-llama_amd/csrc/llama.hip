@@ -8,12 +8,15 @@
 // matvec, which also yields the greedy argmax.
 //
 // Exactness: RMSNorm, RoPE (sin/cos from a host table computed with the
-// same libm calls and operation order as math.rs:322-334), the QK dot (f32
-// products summed in f64 in d order, as the reference), the softmax (SSE2
-// exponential of cpu_math.rs:94-123, f32 pair sums, f64 sum in column order)
-// and SiLU are the reference's operations in the reference's order.  The P.V
-// sums are f64 in 64-token chunks added in order; the matvecs' f32 block
-// combine order is the kernels' own (integer block sums are exact).
+// same libm calls and operation order as math.rs:322-334), the softmax
+// exponentials (SSE2 exponential of cpu_math.rs:94-123) and pair sums, and
+// SiLU are the reference's operations in the reference's order.  The f64 sums
+// of the QK dots and the softmax totals run in parallel orders whose f32
+// results are certified equal to the reference's (or repeated in its order:
+// certified_f32), so scores and probabilities are bit-exact.  The P.V sums
+// add the same f64 terms in another order: an output can differ from the
+// reference's in the last bit.  The matvecs' f32 block combine order is the
+// kernels' own (their integer block sums are exact).
 #include <math.h>
 
 #include <new>
@@ -27,6 +30,41 @@ namespace rlq {
 
 constexpr int kAttnChunk = 64;      // tokens per workgroup of the attention kernels
 constexpr int kAttnThreads = 256;
+constexpr uint32_t kAttnMaxHd = 256;  // head dimension limit: 64 rows of a chunk in 16 float4 per thread
+
+constexpr uint32_t kAttnBatch = 16;   // loads in flight per thread in the P.V prologue
+constexpr uint32_t kPvDims = 8;       // head dimensions per P.V workgroup
+constexpr uint32_t kPvSegs = 8;       // token segments per P.V output
+
+// LDS of attn_pv_kernel, in floats: exponentials [G][rs], pair sums
+// [G][n4/4], max and inverse [G][2], chunk maxima [G][nch], the transposed
+// values [kPvDims][rs] at a 16-byte aligned offset, then the f64 segment sums
+// [kPvSegs][G * kPvDims].  Rows hold n32 =
+// count rounded up to 32 values (8 segments of a multiple of 4) and are
+// padded by 4 floats so the rows a wave reads start in different banks.
+struct AttnPvLds {
+    uint32_t n32, rs, g, stat, cm, v, part, total;
+};
+__host__ __device__ inline AttnPvLds attn_pv_lds(uint32_t G, uint32_t count, uint32_t nch) {
+    AttnPvLds l;
+    const uint32_t n4 = (count + 3) / 4 * 4;
+    l.n32 = (count + 31) / 32 * 32;
+    l.rs = l.n32 + 4;
+    l.g = G * l.rs;
+    l.stat = l.g + G * (n4 / 4);
+    l.cm = l.stat + 2 * G;
+    l.v = (l.cm + G * nch + 3) & ~3u;
+    l.part = (l.v + kPvDims * l.rs + 1) & ~1u;
+    l.total = l.part + 2 * kPvSegs * G * kPvDims;
+    return l;
+}
+
+uint64_t llama_attn_lds_bytes(uint64_t heads, uint64_t kv_heads, uint64_t head_dim, uint64_t max_context) {
+    const uint64_t G = heads / kv_heads, nch = (max_context + kAttnChunk - 1) / kAttnChunk;
+    const uint64_t pv = (uint64_t)attn_pv_lds((uint32_t)G, (uint32_t)max_context, (uint32_t)nch).total * 4;
+    const uint64_t sc = (G * head_dim + kAttnChunk * (head_dim + 1)) * 4;
+    return pv > sc ? pv : sc;
+}
 
 // ---------------------------------------------------------------------------
 // RoPE of one head slice in place in LDS-ready form: out[2p], out[2p+1] from
@@ -37,133 +75,232 @@ __device__ __forceinline__ void rope_pair(const float* in, const float* tab, uin
     out[2 * p + 1] = x * s + y * c;
 }
 
+// The reference adds the f64 terms of its attention sums in one fixed order
+// and rounds the total to f32 (math.rs:467-471, 309-313, 475-488).  These
+// kernels add the same terms in a parallel order.  Two orders of the same n
+// additions differ by at most 2 (n - 1) 2^-53 sum|term|, so when every value
+// that close to `sum` rounds to the same f32 (f32 rounding is monotone, so
+// the two ends decide it), the reference's total rounds to that f32 as well.
+// `f` maps the f64 total to the f32 result (a cast, or the cast of 1/total).
+// Returns false when that cannot be certified; the caller then repeats the
+// sum in the reference's order.
+template <typename F>
+__device__ __forceinline__ bool certified_f32(double sum, double abs_sum, uint32_t n, F f, float* out) {
+    const double eps = (double)n * 2.3e-16 * abs_sum;  // 2^-52 with a margin for the rounding of eps itself
+    *out = f(sum);
+    return f(sum - eps) == f(sum + eps);
+}
+__device__ __forceinline__ float f64_to_f32(double x) { return (float)x; }
+
 // Scores of kv head blockIdx.y's G query heads against tokens
 // [64 * blockIdx.x, +64) of the layer cache (math.rs:462-474):
 // score = f32(sum_d f64(q_d * k_d)) * scale, the sum in d order.  The
 // workgroup whose chunk holds the new row `fresh` applies RoPE to the new key,
 // appends it and the new value to the caches, and uses its own copy of the
-// key.  scores is [heads][row_stride].
-__global__ __launch_bounds__(kAttnThreads) void attn_scores_kernel(const float* __restrict__ qkv,
-                                                                   const float* __restrict__ rope_tab,
-                                                                   float* __restrict__ kc, float* __restrict__ vc,
-                                                                   uint32_t fresh, uint32_t heads, uint32_t kv_heads,
-                                                                   uint32_t hd, float scale, float* __restrict__ scores,
-                                                                   uint32_t row_stride,
-                                                                   unsigned long long* __restrict__ err_word) {
+// key.  scores is [heads][row_stride]; cmax[head][chunk] (stride cstride)
+// receives each chunk's maximum score.
+__global__ __launch_bounds__(kAttnThreads) void attn_scores_kernel(
+    const float* __restrict__ qkv, const float* __restrict__ rope_tab, float* __restrict__ kc, float* __restrict__ vc,
+    uint32_t fresh, uint32_t heads, uint32_t kv_heads, uint32_t hd, float scale, float* __restrict__ scores,
+    uint32_t row_stride, float* __restrict__ cmax, uint32_t cstride, unsigned long long* __restrict__ err_word) {
     extern __shared__ __align__(16) float sm[];
-    const uint32_t G = heads / kv_heads, kvh = blockIdx.y, t0 = blockIdx.x * kAttnChunk;
+    const uint32_t G = heads / kv_heads, kvh = blockIdx.y, c = blockIdx.x, t0 = c * kAttnChunk;
     const uint32_t width = heads * hd, kvw = kv_heads * hd, ks = hd + 1;  // odd row stride: no bank conflicts
     float* q_s = sm;              // [G][hd]
     float* k_s = sm + G * hd;     // [64][hd + 1]
-    const uint32_t tid = threadIdx.x, count = fresh + 1;
+    const uint32_t tid = threadIdx.x, count = fresh + 1, q4 = hd / 4;
+    const uint32_t n_here = count - t0 < (uint32_t)kAttnChunk ? count - t0 : (uint32_t)kAttnChunk;
+    // the chunk's cached keys: every load issued before any is used
+    float4 kr[kAttnMaxHd / 16];
+#pragma unroll
+    for (uint32_t k = 0; k < kAttnMaxHd / 16; ++k) {
+        const uint32_t i = tid + k * kAttnThreads, t = i / q4;
+        kr[k] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (k < hd / 16 && t < n_here && t0 + t != fresh)
+            kr[k] = *(const float4*)(kc + (uint64_t)(t0 + t) * kvw + kvh * hd + 4 * (i % q4));
+    }
     for (uint32_t i = tid; i < G * hd / 2; i += kAttnThreads) {
         const uint32_t h = i / (hd / 2), p = i % (hd / 2);
         rope_pair(qkv + (kvh * G + h) * hd, rope_tab, p, q_s + h * hd);
     }
-    const bool has_fresh = fresh >= t0 && fresh < t0 + kAttnChunk;
-    if (has_fresh) {
+    if (fresh >= t0 && fresh < t0 + kAttnChunk) {
         float* krow = k_s + (fresh - t0) * ks;
         const float* kin = qkv + width + kvh * hd;
         const float* vin = qkv + width + kvw + kvh * hd;
         for (uint32_t p = tid; p < hd / 2; p += kAttnThreads) {
-            float o[2];
-            const float x = kin[2 * p], y = kin[2 * p + 1], s = rope_tab[2 * p], c = rope_tab[2 * p + 1];
-            o[0] = x * c - y * s;
-            o[1] = x * s + y * c;
-            krow[2 * p] = o[0];
-            krow[2 * p + 1] = o[1];
-            kc[(uint64_t)fresh * kvw + kvh * hd + 2 * p] = o[0];
-            kc[(uint64_t)fresh * kvw + kvh * hd + 2 * p + 1] = o[1];
+            const float x = kin[2 * p], y = kin[2 * p + 1], sn = rope_tab[2 * p], cs = rope_tab[2 * p + 1];
+            const float o0 = x * cs - y * sn, o1 = x * sn + y * cs;
+            krow[2 * p] = o0;
+            krow[2 * p + 1] = o1;
+            kc[(uint64_t)fresh * kvw + kvh * hd + 2 * p] = o0;
+            kc[(uint64_t)fresh * kvw + kvh * hd + 2 * p + 1] = o1;
         }
         for (uint32_t d = tid; d < hd; d += kAttnThreads) vc[(uint64_t)fresh * kvw + kvh * hd + d] = vin[d];
     }
-    // cached keys of the chunk, one row per 16-byte-aligned slice
-    const uint32_t n_here = count - t0 < (uint32_t)kAttnChunk ? count - t0 : (uint32_t)kAttnChunk;
-    for (uint32_t i = tid; i < n_here * (hd / 4); i += kAttnThreads) {
-        const uint32_t t = i / (hd / 4), d4 = i % (hd / 4);
-        if (t0 + t == fresh) continue;
-        const float4 v = *(const float4*)(kc + (uint64_t)(t0 + t) * kvw + kvh * hd + 4 * d4);
-        float* dst = k_s + t * ks + 4 * d4;
-        dst[0] = v.x, dst[1] = v.y, dst[2] = v.z, dst[3] = v.w;
+#pragma unroll
+    for (uint32_t k = 0; k < kAttnMaxHd / 16; ++k) {
+        const uint32_t i = tid + k * kAttnThreads, t = i / q4;
+        if (k < hd / 16 && t < n_here && t0 + t != fresh) {
+            float* dst = k_s + t * ks + 4 * (i % q4);
+            dst[0] = kr[k].x, dst[1] = kr[k].y, dst[2] = kr[k].z, dst[3] = kr[k].w;
+        }
     }
     __syncthreads();
+    // pair (h, t) = i: a wave holds one head's 64 tokens
     for (uint32_t i = tid; i < G * kAttnChunk; i += kAttnThreads) {
         const uint32_t h = i / kAttnChunk, t = i % kAttnChunk;
-        if (t >= n_here) continue;
-        const float* q = q_s + h * hd;
-        const float* k = k_s + t * ks;
-        double dot = 0.0;
-        for (uint32_t d = 0; d < hd; ++d) dot += (double)(q[d] * k[d]);
-        const float score = (float)dot * scale;
-        if (!(fabsf(score) <= 3.402823466e38f)) report_error(err_word, error_key(0, kKindNonFinite, t0 + t));
-        scores[(uint64_t)(kvh * G + h) * row_stride + t0 + t] = score;
+        float score = -INFINITY;
+        if (t < n_here) {
+            const float* q = q_s + h * hd;
+            const float* k = k_s + t * ks;
+            // four interleaved partial sums; the f32 total is certified against
+            // the reference's d-order sum, or recomputed in that order
+            double a[4] = {0.0, 0.0, 0.0, 0.0}, b[4] = {0.0, 0.0, 0.0, 0.0};
+            for (uint32_t d = 0; d < hd; d += 4) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const double v = (double)(q[d + j] * k[d + j]);
+                    a[j] += v;
+                    b[j] += fabs(v);
+                }
+            }
+            float dotf;
+            if (!certified_f32((a[0] + a[1]) + (a[2] + a[3]), (b[0] + b[1]) + (b[2] + b[3]), hd, f64_to_f32, &dotf)) {
+                double dot = 0.0;
+                for (uint32_t d = 0; d < hd; ++d) dot += (double)(q[d] * k[d]);
+                dotf = (float)dot;
+            }
+            score = dotf * scale;
+            if (!(fabsf(score) <= 3.402823466e38f)) report_error(err_word, error_key(0, kKindNonFinite, t0 + t));
+            scores[(uint64_t)(kvh * G + h) * row_stride + t0 + t] = score;
+        }
+        float m = score;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+        if (t == 0) cmax[(kvh * G + h) * cstride + c] = m;
     }
 }
 
 // Softmax of the G heads' score rows (math.rs:293-318 with the SSE2 policy of
-// cpu_math.rs:60-91), recomputed by every workgroup of the kv head, then the
-// chunk's part of P.V (math.rs:475-482) as f64 sums over its 64 tokens:
-// part[chunk][head][d].  Columns past `count` are the -inf padding, whose
-// exponentials are exactly 0.
-__global__ __launch_bounds__(kAttnThreads) void attn_pv_kernel(const float* __restrict__ scores,
-                                                               const float* __restrict__ vc, uint32_t count,
-                                                               uint32_t heads, uint32_t kv_heads, uint32_t hd,
-                                                               uint32_t row_stride, double* __restrict__ part) {
+// cpu_math.rs:60-91) and P.V (math.rs:475-482) for 8 of the head dimensions:
+// workgroup (blockIdx.x, blockIdx.y) = (dimensions 8 * blockIdx.x .., kv head).
+// Every workgroup of the kv head recomputes the G rows' softmax from the chunk
+// maxima; the softmax totals are certified against the reference's order
+// (certified_f32).  The P.V sums add the reference's f64 terms in segments:
+// their f32 results can differ from the reference's in the last bit (the
+// certificate fails for about 2 in 10^4 of these 1024-term sums, and a
+// sequential repeat would cost the whole kernel several microseconds).
+// Columns past `count` are the -inf padding, whose exponentials are exactly 0.
+// The loads
+// of the values, the scores and the chunk maxima all go out before the first
+// one is used.
+__global__ __launch_bounds__(kAttnThreads) void attn_pv_kernel(
+    const float* __restrict__ scores, const float* __restrict__ cmax, uint32_t cstride, uint32_t nch,
+    const float* __restrict__ vc, uint32_t count, uint32_t heads, uint32_t kv_heads, uint32_t hd, uint32_t row_stride,
+    float* __restrict__ att) {
     extern __shared__ __align__(16) float sm[];
-    const uint32_t G = heads / kv_heads, kvh = blockIdx.y, c = blockIdx.x, t0 = c * kAttnChunk;
-    const uint32_t n4 = (count + 3) / 4 * 4, ngroups = n4 / 4, kvw = kv_heads * hd;
-    float* e_s = sm;                       // [G][n4] exponentials, then probabilities
-    float* g_s = sm + G * n4;              // [G][ngroups] f32 pair sums
-    float* stat = g_s + G * ngroups;       // [G][2]: max, inverse
-    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    // row maxima, one wave per head
-    for (uint32_t h = wave; h < G; h += kAttnThreads / 64) {
-        const float* row = scores + (uint64_t)(kvh * G + h) * row_stride;
-        float m = -INFINITY;
-        for (uint32_t t = lane; t < count; t += 64) m = fmaxf(m, row[t]);
+    const uint32_t G = heads / kv_heads, kvh = blockIdx.y, d0 = blockIdx.x * kPvDims;
+    const AttnPvLds Lp = attn_pv_lds(G, count, nch);
+    const uint32_t n4 = (count + 3) / 4 * 4, ngroups = n4 / 4, kvw = kv_heads * hd, rs = Lp.rs;
+    float* e_s = sm;                        // [G][rs] exponentials, then probabilities
+    float* g_s = sm + Lp.g;                 // [G][ngroups] f32 pair sums
+    float* stat = sm + Lp.stat;             // [G][2]: max, inverse
+    float* cm_s = sm + Lp.cm;               // [G][nch]
+    float* vt_s = sm + Lp.v;                // [kPvDims][rs] the values, transposed
+    double* sum_s = (double*)(sm + Lp.part);  // [kPvSegs][G * kPvDims]
+    const uint32_t tid = threadIdx.x;
+    const float* vbase = vc + kvh * hd + d0;
+    const uint32_t nload = (G > 2 ? G : 2) * count;  // 2 float4 of values and G scores per token
+    for (uint32_t base = 0; base < nload; base += kAttnBatch * kAttnThreads) {
+        float4 vr[kAttnBatch];
+        float sv[kAttnBatch];
 #pragma unroll
-        for (int o = 1; o < 64; o <<= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
-        if (lane == 0) stat[2 * h] = m;
+        for (uint32_t k = 0; k < kAttnBatch; ++k) {
+            const uint32_t j = base + k * kAttnThreads + tid;
+            vr[k] = j < 2 * count ? *(const float4*)(vbase + (uint64_t)(j / 2) * kvw + 4 * (j % 2))
+                                  : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            sv[k] = j < G * count ? scores[(uint64_t)(kvh * G + j / count) * row_stride + j % count] : 0.0f;
+        }
+        if (base == 0)
+            for (uint32_t i = tid; i < G * nch; i += kAttnThreads) cm_s[i] = cmax[(kvh * G + i / nch) * cstride + i % nch];
+#pragma unroll
+        for (uint32_t k = 0; k < kAttnBatch; ++k) {
+            const uint32_t j = base + k * kAttnThreads + tid;
+            if (j < 2 * count) {
+                float* v = vt_s + 4 * (j % 2) * rs + j / 2;
+                v[0] = vr[k].x, v[rs] = vr[k].y, v[2 * rs] = vr[k].z, v[3 * rs] = vr[k].w;
+            }
+            if (j < G * count) e_s[(j / count) * rs + j % count] = sv[k];  // raw scores for now
+        }
+    }
+    for (uint32_t i = tid; i < kPvDims * (Lp.n32 - count); i += kAttnThreads)  // zero padding of the values
+        vt_s[(i / (Lp.n32 - count)) * rs + count + i % (Lp.n32 - count)] = 0.0f;
+    __syncthreads();
+    if (tid < G) {
+        float m = -INFINITY;
+        for (uint32_t c = 0; c < nch; ++c) m = fmaxf(m, cm_s[tid * nch + c]);
+        stat[2 * tid] = m;
     }
     __syncthreads();
-    for (uint32_t i = tid; i < G * n4; i += kAttnThreads) {
-        const uint32_t h = i / n4, t = i % n4;
+    for (uint32_t h = 0; h < G; ++h) {
         const float m = stat[2 * h];
-        e_s[i] = t < count ? sse2_exp(scores[(uint64_t)(kvh * G + h) * row_stride + t] - m) : 0.0f;
+        for (uint32_t t = tid; t < Lp.n32; t += kAttnThreads)
+            e_s[h * rs + t] = t < count ? sse2_exp(e_s[h * rs + t] - m) : 0.0f;
     }
     __syncthreads();
     for (uint32_t i = tid; i < G * ngroups; i += kAttnThreads) {
-        const uint32_t h = i / ngroups, g = i % ngroups;
-        const float* e = e_s + h * n4 + 4 * g;
+        const float* e = e_s + (i / ngroups) * rs + 4 * (i % ngroups);
         g_s[i] = (e[0] + e[1]) + (e[2] + e[3]);
     }
     __syncthreads();
-    if (tid < G) {  // the f64 sum in column order, as the reference
+    // the row sums (math.rs:309-313): one wave per head, certified against the
+    // reference's column-order f64 sum (the pair sums are >= 0: sum = sum |.|)
+    const uint32_t lane = tid & 63, wave = tid >> 6;
+    for (uint32_t h = wave; h < G; h += kAttnThreads / 64) {
+        const float* gp = g_s + h * ngroups;
         double sum = 0.0;
-        for (uint32_t g = 0; g < ngroups; ++g) sum += (double)g_s[tid * ngroups + g];
-        stat[2 * tid + 1] = (float)(1.0 / sum);
+        for (uint32_t g = lane; g < ngroups; g += 64) sum += (double)gp[g];
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) sum += __shfl_xor(sum, o, 64);
+        if (lane == 0) {
+            float inv;
+            if (!certified_f32(sum, sum, ngroups, [](double x) { return (float)(1.0 / x); }, &inv)) {
+                double seq = 0.0;
+                for (uint32_t g = 0; g < ngroups; ++g) seq += (double)gp[g];
+                inv = (float)(1.0 / seq);
+            }
+            stat[2 * h + 1] = inv;
+        }
     }
     __syncthreads();
-    const uint32_t n_here = count - t0 < (uint32_t)kAttnChunk ? count - t0 : (uint32_t)kAttnChunk;
-    for (uint32_t i = tid; i < G * hd; i += kAttnThreads) {
-        const uint32_t h = i / hd, d = i % hd;
+    for (uint32_t h = 0; h < G; ++h) {  // math.rs:313-315: x *= inverse (the padding stays 0)
         const float inv = stat[2 * h + 1];
-        const float* e = e_s + h * n4 + t0;
-        const float* v = vc + (uint64_t)t0 * kvw + kvh * hd + d;
-        double acc = 0.0;
-        for (uint32_t t = 0; t < n_here; ++t) acc += (double)((e[t] * inv) * v[(uint64_t)t * kvw]);
-        part[((uint64_t)c * heads + kvh * G + h) * hd + d] = acc;
+        for (uint32_t t = tid; t < count; t += kAttnThreads) e_s[h * rs + t] *= inv;
     }
-}
-
-// out[i] = f32 of the chunk parts added in chunk order.
-__global__ __launch_bounds__(256) void attn_reduce_kernel(const double* __restrict__ part, uint32_t nchunks,
-                                                          uint32_t n, float* __restrict__ out) {
-    const uint32_t i = blockIdx.x * 256 + threadIdx.x;
-    if (i >= n) return;
-    double acc = 0.0;
-    for (uint32_t c = 0; c < nchunks; ++c) acc += part[(uint64_t)c * n + i];
-    out[i] = (float)acc;
+    __syncthreads();
+    // P.V: output o = (head, dimension) over kPvSegs token segments of seg
+    // tokens, four interleaved f64 chains per thread; the segment sums are
+    // added in segment order.  The f32 products and the f64 terms are the
+    // reference's; only the order of the f64 additions differs (see above).
+    const uint32_t no = G * kPvDims, seg = Lp.n32 / kPvSegs;
+    for (uint32_t i = tid; i < kPvSegs * no; i += kAttnThreads) {
+        const uint32_t o = i % no, r = i / no;
+        const float* p = e_s + (o / kPvDims) * rs + r * seg;
+        const float* v = vt_s + (o % kPvDims) * rs + r * seg;
+        double a[4] = {0.0, 0.0, 0.0, 0.0};
+        for (uint32_t t = 0; t < seg; t += 4) {
+            const float4 p4 = *(const float4*)(p + t), v4 = *(const float4*)(v + t);
+            a[0] += (double)(p4.x * v4.x), a[1] += (double)(p4.y * v4.y);
+            a[2] += (double)(p4.z * v4.z), a[3] += (double)(p4.w * v4.w);
+        }
+        sum_s[r * no + o] = (a[0] + a[1]) + (a[2] + a[3]);
+    }
+    __syncthreads();
+    for (uint32_t o = tid; o < no; o += kAttnThreads) {
+        double sum = 0.0;
+        for (uint32_t r = 0; r < kPvSegs; ++r) sum += sum_s[r * no + o];
+        att[(kvh * G + o / kPvDims) * hd + d0 + o % kPvDims] = (float)sum;
+    }
 }
 
 // RMSNorm of one row (math.rs:214-228) for the step's embedding output: one
@@ -230,8 +367,8 @@ LlamaModel::~LlamaModel() {
                         (void*)l.ffn_norm})
             if (p) (void)hipFree(p);
     for (void* p : {(void*)out_w, (void*)out_norm, (void*)emb, (void*)k_cache, (void*)v_cache, (void*)rope_tab,
-                    (void*)qkv, (void*)scores, (void*)part, (void*)att, (void*)gu, (void*)argmax_keys,
-                    (void*)logits_buf})
+                    (void*)qkv, (void*)scores, (void*)att, (void*)gu, (void*)argmax_keys,
+                    (void*)logits_buf, (void*)cmax})
         if (p) (void)hipFree(p);
 }
 
@@ -251,19 +388,31 @@ hipError_t LlamaModel::create(const LlamaDims& dims, const LlamaHostTensors& t, 
         }
     }
     const uint64_t row_len = (d.max_context + 255) / 256 * 256, nchunks = (d.max_context + kAttnChunk - 1) / kAttnChunk;
-    // the attention workgroups' LDS grows with the context (the caller checked 160 KB)
-    hipError_t e = hipFuncSetAttribute((const void*)attn_pv_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                       160 * 1024);
-    if (e == hipSuccess)
+    // the attention workgroups' LDS grows with the context (the caller checked
+    // that it fits next to the kernels' few static bytes)
+    // that it fits next to the kernels' few static bytes); the limits only grow,
+    // so models of other shapes in the process keep working
+    static int pv_set = 64 * 1024, scores_set = 64 * 1024;
+    const uint32_t G = (uint32_t)(d.heads / d.kv_heads);
+    const int pv_need = (int)(attn_pv_lds(G, (uint32_t)d.max_context, (uint32_t)nchunks).total * sizeof(float));
+    const int scores_need = (int)((G * hd + kAttnChunk * (hd + 1)) * sizeof(float));
+    hipError_t e = hipSuccess;
+    if (pv_need > pv_set) {
+        e = hipFuncSetAttribute((const void*)attn_pv_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, pv_need);
+        if (e == hipSuccess) pv_set = pv_need;
+    }
+    if (e == hipSuccess && scores_need > scores_set) {
         e = hipFuncSetAttribute((const void*)attn_scores_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                160 * 1024);
+                                scores_need);
+        if (e == hipSuccess) scores_set = scores_need;
+    }
     if (e == hipSuccess) e = hipMalloc((void**)&rope_tab, tab.size() * sizeof(float));
     if (e == hipSuccess) e = hipMemcpy(rope_tab, tab.data(), tab.size() * sizeof(float), hipMemcpyHostToDevice);
     if (e == hipSuccess) e = hipMalloc((void**)&k_cache, d.n_layers * d.max_context * kvw * sizeof(float));
     if (e == hipSuccess) e = hipMalloc((void**)&v_cache, d.n_layers * d.max_context * kvw * sizeof(float));
     if (e == hipSuccess) e = hipMalloc((void**)&qkv, (W + 2 * kvw) * sizeof(float));
     if (e == hipSuccess) e = hipMalloc((void**)&scores, d.heads * row_len * sizeof(float));
-    if (e == hipSuccess) e = hipMalloc((void**)&part, nchunks * W * sizeof(double));
+    if (e == hipSuccess) e = hipMalloc((void**)&cmax, d.heads * nchunks * sizeof(float));
     if (e == hipSuccess) e = hipMalloc((void**)&att, W * sizeof(float));
     if (e == hipSuccess) e = hipMalloc((void**)&gu, 2 * F * sizeof(float));
     if (e == hipSuccess) e = hipMalloc((void**)&argmax_keys, sizeof(unsigned long long));
@@ -331,8 +480,8 @@ hipError_t LlamaModel::step(float* hidden, uint64_t position, float* embedding_o
     const float* tab = rope_tab + position * hd;
     const uint32_t wt = d.weight_type;
     const size_t lds_scores = (H / KVH * hd + kAttnChunk * (hd + 1)) * sizeof(float);
-    const uint64_t n4 = (count + 3) / 4 * 4;
-    const size_t lds_pv = (H / KVH * n4 + H / KVH * (n4 / 4) + 2 * (H / KVH)) * sizeof(float);
+    const size_t lds_pv = attn_pv_lds((uint32_t)(H / KVH), (uint32_t)count, nchunks).total * sizeof(float);
+    const uint32_t cstride = (uint32_t)((d.max_context + kAttnChunk - 1) / kAttnChunk);
     hipError_t e = hipSuccess;
     for (uint64_t l = 0; l < d.n_layers && e == hipSuccess; ++l) {
         const LlamaLayerDev& L = layers[l];
@@ -345,11 +494,10 @@ hipError_t LlamaModel::step(float* hidden, uint64_t position, float* embedding_o
         if (e != hipSuccess) break;
         hipLaunchKernelGGL(attn_scores_kernel, dim3(nchunks, (uint32_t)KVH), dim3(kAttnThreads), lds_scores, s, qkv,
                            tab, kc, vc, (uint32_t)fresh, (uint32_t)H, (uint32_t)KVH, (uint32_t)hd, scale, scores,
-                           (uint32_t)row_stride, err_word);
-        hipLaunchKernelGGL(attn_pv_kernel, dim3(nchunks, (uint32_t)KVH), dim3(kAttnThreads), lds_pv, s, scores, vc,
-                           (uint32_t)count, (uint32_t)H, (uint32_t)KVH, (uint32_t)hd, (uint32_t)row_stride, part);
-        hipLaunchKernelGGL(attn_reduce_kernel, dim3((uint32_t)((W + 255) / 256)), dim3(256), 0, s, part, nchunks,
-                           (uint32_t)W, att);
+                           (uint32_t)row_stride, cmax, cstride, err_word);
+        hipLaunchKernelGGL(attn_pv_kernel, dim3((uint32_t)(hd / kPvDims), (uint32_t)KVH), dim3(kAttnThreads), lds_pv, s,
+                           scores, cmax, cstride, nchunks, vc, (uint32_t)count, (uint32_t)H, (uint32_t)KVH,
+                           (uint32_t)hd, (uint32_t)row_stride, att);
         e = hipGetLastError();
         if (e != hipSuccess) break;
         MvExtra res;

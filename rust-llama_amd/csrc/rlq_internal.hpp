@@ -118,6 +118,8 @@ struct LlamaHostTensors {
     const LlamaHostLayer* layers;
     bool on_device;
 };
+// LDS bytes the attention workgroups need at `max_context` rows.
+uint64_t llama_attn_lds_bytes(uint64_t heads, uint64_t kv_heads, uint64_t head_dim, uint64_t max_context);
 struct LlamaLayerDev {
     uint8_t *wqkv = nullptr, *wo = nullptr, *wgu = nullptr, *wdown = nullptr;  // tiled; QKV and gate/up fused
     float *attn_norm = nullptr, *ffn_norm = nullptr;
@@ -129,7 +131,7 @@ struct LlamaModel {
     uint8_t *out_w = nullptr, *emb = nullptr;  // tiled output matrix; GGUF embedding rows
     float *out_norm = nullptr, *k_cache = nullptr, *v_cache = nullptr, *rope_tab = nullptr;
     float *qkv = nullptr, *scores = nullptr, *att = nullptr, *gu = nullptr, *logits_buf = nullptr;
-    double* part = nullptr;
+    float* cmax = nullptr;  // [heads][chunks of 64 tokens] chunk maxima of the scores
     unsigned long long* argmax_keys = nullptr;
     uint64_t n_cached = 0;  // KV rows held (the insertion index of the next step)
 

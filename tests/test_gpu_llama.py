@@ -7,8 +7,9 @@ Bars, per part of the step (tests/llama_fixture.py models):
     against the oracle's matvec of its own RMSNorm (the quantized activation
     is the same bytes; only the f32 combine order of the exact integer block
     sums differs);
-  - attention, given the GPU's own q/k/v: bit-exact (same RoPE table, the QK
-    sums in the reference's order, the SSE2 softmax, P.V in f64);
+  - attention, given the GPU's own q/k/v: within one f32 ulp per output (the
+    same RoPE table; QK dots and softmax totals certified equal to the
+    reference's f64 order; the P.V f64 sums in another order);
   - the layer output, given the GPU's own attention output and gate/up
     values: relative L2 <= 1e-5 (the O and down inputs quantize to the same
     bytes);
@@ -123,7 +124,11 @@ def test_one_layer_parts(ctx):
         kc[step] = O.rope(qkv[W:W + kvw], hd, step, cfg.rope_base)
         vc[step] = qkv[W + kvw:]
         want_att = O.attention(q, kc[:step + 1], vc[:step + 1], step + 1, cfg.heads, cfg.kv_heads, hd, scale)
-        assert np.array_equal(att, want_att), (step, np.max(np.abs(att - want_att)))
+        # P.V adds the reference's f64 terms in another order: at most the
+        # last f32 bit of an output may differ
+        assert np.all(np.abs(att - want_att) <= np.spacing(np.abs(want_att))), step
+        off = int(np.sum(att != want_att))
+        worst["attention_last_bit"] = worst.get("attention_last_bit", 0) + off
         # the rest of the layer from the GPU's attention output and gate/up
         hm = h0 + O.matvec(wt, L["attention_output"], W, W, att)
         n2 = O.rms_norm(hm, L["feed_forward_norm"], cfg.rms_epsilon)
