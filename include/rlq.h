@@ -249,9 +249,9 @@ int32_t rlq_llama_step(rlq_llama *model, float *hidden, uint64_t position, float
                        uint32_t *argmax, void *stream, rlq_error *err);
 /* Copies (on `stream`, device to device) the last layer's intermediates of
  * the latest step: qkv = [query (width) | key (kv_width, before RoPE) | value
- * (kv_width)], attention (width, the attention output), gate_up = [gate | up]
- * (2 * feed_forward, before SiLU).  Any output may be null. */
-int32_t rlq_llama_intermediates(const rlq_llama *model, float *qkv, float *attention, float *gate_up,
+ * (kv_width)], attention (width, the attention output), ffn = silu(gate) * up
+ * (feed_forward, the down projection's input).  Any output may be null. */
+int32_t rlq_llama_intermediates(const rlq_llama *model, float *qkv, float *attention, float *ffn,
                                 void *stream, rlq_error *err);
 
 #ifdef __cplusplus

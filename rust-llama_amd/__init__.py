@@ -491,11 +491,11 @@ class LlamaModel:
 
     def intermediates(self, stream=None):
         """The last layer's [q | k | v] (k before RoPE), attention output and
-        [gate | up] of the latest step, as fresh GPU tensors."""
+        silu(gate) * up of the latest step, as fresh GPU tensors."""
         c = self.config
         qkv = torch.empty(c.width + 2 * c.kv_width, dtype=torch.float32, device="cuda")
         att = torch.empty(c.width, dtype=torch.float32, device="cuda")
-        gu = torch.empty(2 * c.feed_forward, dtype=torch.float32, device="cuda")
+        gu = torch.empty(c.feed_forward, dtype=torch.float32, device="cuda")
         err = _Err()
         _check(_lib.rlq_llama_intermediates(self._h, _dev_ptr(qkv, torch.float32), _dev_ptr(att, torch.float32),
                                             _dev_ptr(gu, torch.float32), _stream_ptr(stream), ctypes.byref(err)), err)

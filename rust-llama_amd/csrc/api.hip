@@ -573,7 +573,7 @@ int32_t rlq_llama_step(rlq_llama* m, float* hidden, uint64_t position, float* em
     return ok(err);
 }
 
-int32_t rlq_llama_intermediates(const rlq_llama* m, float* qkv, float* attention, float* gate_up, void* stream,
+int32_t rlq_llama_intermediates(const rlq_llama* m, float* qkv, float* attention, float* ffn, void* stream,
                                 rlq_error* err) {
     if (!m) return fail(err, RLQ_INVALID_ARGUMENT);
     DeviceGuard g(m->m.device);
@@ -582,7 +582,7 @@ int32_t rlq_llama_intermediates(const rlq_llama* m, float* qkv, float* attention
     const hipStream_t s = (hipStream_t)stream;
     if (qkv) HIP_TRY(hipMemcpyAsync(qkv, m->m.qkv, (d.width + 2 * kvw) * 4, hipMemcpyDeviceToDevice, s));
     if (attention) HIP_TRY(hipMemcpyAsync(attention, m->m.att, d.width * 4, hipMemcpyDeviceToDevice, s));
-    if (gate_up) HIP_TRY(hipMemcpyAsync(gate_up, m->m.gu, 2 * d.feed_forward * 4, hipMemcpyDeviceToDevice, s));
+    if (ffn) HIP_TRY(hipMemcpyAsync(ffn, m->m.gu, d.feed_forward * 4, hipMemcpyDeviceToDevice, s));
     return ok(err);
 }
 

@@ -35,6 +35,7 @@ constexpr uint32_t kAttnMaxHd = 256;  // head dimension limit: 64 rows of a chun
 constexpr uint32_t kAttnBatch = 16;   // loads in flight per thread in the P.V prologue
 constexpr uint32_t kPvDims = 8;       // head dimensions per P.V workgroup
 constexpr uint32_t kPvSegs = 8;       // token segments per P.V output
+constexpr uint32_t kPvScoreRegs = 4;  // score groups of four per thread held in registers (G * count <= 4096)
 
 // LDS of attn_pv_kernel, in floats: exponentials [G][rs], pair sums
 // [G][n4/4], max and inverse [G][2], chunk maxima [G][nch], the transposed
@@ -202,27 +203,33 @@ __global__ __launch_bounds__(kAttnThreads) void attn_pv_kernel(
     const uint32_t G = heads / kv_heads, kvh = blockIdx.y, d0 = blockIdx.x * kPvDims;
     const AttnPvLds Lp = attn_pv_lds(G, count, nch);
     const uint32_t n4 = (count + 3) / 4 * 4, ngroups = n4 / 4, kvw = kv_heads * hd, rs = Lp.rs;
-    float* e_s = sm;                        // [G][rs] exponentials, then probabilities
+    float* e_s = sm;                        // [G][rs] exponentials
     float* g_s = sm + Lp.g;                 // [G][ngroups] f32 pair sums
     float* stat = sm + Lp.stat;             // [G][2]: max, inverse
     float* cm_s = sm + Lp.cm;               // [G][nch]
     float* vt_s = sm + Lp.v;                // [kPvDims][rs] the values, transposed
     double* sum_s = (double*)(sm + Lp.part);  // [kPvSegs][G * kPvDims]
-    const uint32_t tid = threadIdx.x;
+    const uint32_t tid = threadIdx.x, nq = G * ngroups;  // score groups of four columns
+    // every load of the prologue goes out before the first is used: the
+    // chunk maxima, the first kPvScoreRegs score groups per thread (kept in
+    // registers) and the values (to LDS, transposed)
+    float4 sq[kPvScoreRegs];
+#pragma unroll
+    for (uint32_t k = 0; k < kPvScoreRegs; ++k) {
+        const uint32_t q = k * kAttnThreads + tid;
+        sq[k] = q < nq ? *(const float4*)(scores + (uint64_t)(kvh * G + q / ngroups) * row_stride + 4 * (q % ngroups))
+                       : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+    for (uint32_t i = tid; i < G * nch; i += kAttnThreads) cm_s[i] = cmax[(kvh * G + i / nch) * cstride + i % nch];
     const float* vbase = vc + kvh * hd + d0;
-    const uint32_t nload = (G > 2 ? G : 2) * count;  // 2 float4 of values and G scores per token
-    for (uint32_t base = 0; base < nload; base += kAttnBatch * kAttnThreads) {
+    for (uint32_t base = 0; base < 2 * count; base += kAttnBatch * kAttnThreads) {
         float4 vr[kAttnBatch];
-        float sv[kAttnBatch];
 #pragma unroll
         for (uint32_t k = 0; k < kAttnBatch; ++k) {
             const uint32_t j = base + k * kAttnThreads + tid;
             vr[k] = j < 2 * count ? *(const float4*)(vbase + (uint64_t)(j / 2) * kvw + 4 * (j % 2))
                                   : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            sv[k] = j < G * count ? scores[(uint64_t)(kvh * G + j / count) * row_stride + j % count] : 0.0f;
         }
-        if (base == 0)
-            for (uint32_t i = tid; i < G * nch; i += kAttnThreads) cm_s[i] = cmax[(kvh * G + i / nch) * cstride + i % nch];
 #pragma unroll
         for (uint32_t k = 0; k < kAttnBatch; ++k) {
             const uint32_t j = base + k * kAttnThreads + tid;
@@ -230,11 +237,12 @@ __global__ __launch_bounds__(kAttnThreads) void attn_pv_kernel(
                 float* v = vt_s + 4 * (j % 2) * rs + j / 2;
                 v[0] = vr[k].x, v[rs] = vr[k].y, v[2 * rs] = vr[k].z, v[3 * rs] = vr[k].w;
             }
-            if (j < G * count) e_s[(j / count) * rs + j % count] = sv[k];  // raw scores for now
         }
     }
     for (uint32_t i = tid; i < kPvDims * (Lp.n32 - count); i += kAttnThreads)  // zero padding of the values
         vt_s[(i / (Lp.n32 - count)) * rs + count + i % (Lp.n32 - count)] = 0.0f;
+    for (uint32_t i = tid; i < G * (Lp.n32 - n4); i += kAttnThreads)  // and of the exponentials
+        e_s[(i / (Lp.n32 - n4)) * rs + n4 + i % (Lp.n32 - n4)] = 0.0f;
     __syncthreads();
     if (tid < G) {
         float m = -INFINITY;
@@ -242,16 +250,21 @@ __global__ __launch_bounds__(kAttnThreads) void attn_pv_kernel(
         stat[2 * tid] = m;
     }
     __syncthreads();
-    for (uint32_t h = 0; h < G; ++h) {
+    // exponentials and pair sums of each group of four columns (the groups
+    // past kPvScoreRegs per thread are loaded here)
+    auto group = [&](uint32_t q, float4 x) {
+        const uint32_t h = q / ngroups, t = 4 * (q % ngroups);
         const float m = stat[2 * h];
-        for (uint32_t t = tid; t < Lp.n32; t += kAttnThreads)
-            e_s[h * rs + t] = t < count ? sse2_exp(e_s[h * rs + t] - m) : 0.0f;
-    }
-    __syncthreads();
-    for (uint32_t i = tid; i < G * ngroups; i += kAttnThreads) {
-        const float* e = e_s + (i / ngroups) * rs + 4 * (i % ngroups);
-        g_s[i] = (e[0] + e[1]) + (e[2] + e[3]);
-    }
+        const float e0 = t < count ? sse2_exp(x.x - m) : 0.0f, e1 = t + 1 < count ? sse2_exp(x.y - m) : 0.0f;
+        const float e2 = t + 2 < count ? sse2_exp(x.z - m) : 0.0f, e3 = t + 3 < count ? sse2_exp(x.w - m) : 0.0f;
+        *(float4*)(e_s + h * rs + t) = make_float4(e0, e1, e2, e3);
+        g_s[q] = (e0 + e1) + (e2 + e3);
+    };
+#pragma unroll
+    for (uint32_t k = 0; k < kPvScoreRegs; ++k)
+        if (k * kAttnThreads + tid < nq) group(k * kAttnThreads + tid, sq[k]);
+    for (uint32_t q = kPvScoreRegs * kAttnThreads + tid; q < nq; q += kAttnThreads)
+        group(q, *(const float4*)(scores + (uint64_t)(kvh * G + q / ngroups) * row_stride + 4 * (q % ngroups)));
     __syncthreads();
     // the row sums (math.rs:309-313): one wave per head, certified against the
     // reference's column-order f64 sum (the pair sums are >= 0: sum = sum |.|)
@@ -273,25 +286,22 @@ __global__ __launch_bounds__(kAttnThreads) void attn_pv_kernel(
         }
     }
     __syncthreads();
-    for (uint32_t h = 0; h < G; ++h) {  // math.rs:313-315: x *= inverse (the padding stays 0)
-        const float inv = stat[2 * h + 1];
-        for (uint32_t t = tid; t < count; t += kAttnThreads) e_s[h * rs + t] *= inv;
-    }
-    __syncthreads();
-    // P.V: output o = (head, dimension) over kPvSegs token segments of seg
-    // tokens, four interleaved f64 chains per thread; the segment sums are
-    // added in segment order.  The f32 products and the f64 terms are the
-    // reference's; only the order of the f64 additions differs (see above).
+    // P.V with p = e * inverse (math.rs:313-315, 478-480): output o = (head,
+    // dimension) over kPvSegs token segments of seg tokens, four interleaved
+    // f64 chains per thread; the segment sums are added in segment order.  The
+    // f32 products and f64 terms are the reference's; only the order of the
+    // f64 additions differs (see above).  Padding columns give 0 * 0 terms.
     const uint32_t no = G * kPvDims, seg = Lp.n32 / kPvSegs;
     for (uint32_t i = tid; i < kPvSegs * no; i += kAttnThreads) {
         const uint32_t o = i % no, r = i / no;
-        const float* p = e_s + (o / kPvDims) * rs + r * seg;
+        const float inv = stat[2 * (o / kPvDims) + 1];
+        const float* e = e_s + (o / kPvDims) * rs + r * seg;
         const float* v = vt_s + (o % kPvDims) * rs + r * seg;
         double a[4] = {0.0, 0.0, 0.0, 0.0};
         for (uint32_t t = 0; t < seg; t += 4) {
-            const float4 p4 = *(const float4*)(p + t), v4 = *(const float4*)(v + t);
-            a[0] += (double)(p4.x * v4.x), a[1] += (double)(p4.y * v4.y);
-            a[2] += (double)(p4.z * v4.z), a[3] += (double)(p4.w * v4.w);
+            const float4 e4 = *(const float4*)(e + t), v4 = *(const float4*)(v + t);
+            a[0] += (double)((e4.x * inv) * v4.x), a[1] += (double)((e4.y * inv) * v4.y);
+            a[2] += (double)((e4.z * inv) * v4.z), a[3] += (double)((e4.w * inv) * v4.w);
         }
         sum_s[r * no + o] = (a[0] + a[1]) + (a[2] + a[3]);
     }
@@ -429,6 +439,8 @@ hipError_t LlamaModel::create(const LlamaDims& dims, const LlamaHostTensors& t, 
         if (e != hipSuccess) return e;
     }
     const uint32_t wt = d.weight_type;
+    uint8_t* gu_stage = nullptr;
+    if (e == hipSuccess) e = hipMalloc((void**)&gu_stage, 2 * layout_bytes(wt, F, W));
     auto tiled = [&](const void* src, uint64_t rows, uint64_t cols, uint8_t* dst) {
         return upload_tiled(wt, src, rows, cols, t.on_device, dst, staging, s);
     };
@@ -443,9 +455,19 @@ hipError_t LlamaModel::create(const LlamaDims& dims, const LlamaHostTensors& t, 
         if (e == hipSuccess) e = tiled(hl.value, kvw, W, L.wqkv + bq + bk);
         if (e == hipSuccess) e = hipMalloc((void**)&L.wo, layout_bytes(wt, W, W));
         if (e == hipSuccess) e = tiled(hl.attention_output, W, W, L.wo);
+        // gate and up tiles interleaved (tile 2i = gate tile i, 2i + 1 = up
+        // tile i), so one workgroup holds both halves of silu(gate) * up
         if (e == hipSuccess) e = hipMalloc((void**)&L.wgu, 2 * bg);
-        if (e == hipSuccess) e = tiled(hl.gate, F, W, L.wgu);
-        if (e == hipSuccess) e = tiled(hl.up, F, W, L.wgu + bg);
+        if (e == hipSuccess) e = tiled(hl.gate, F, W, gu_stage);
+        if (e == hipSuccess) e = tiled(hl.up, F, W, gu_stage + bg);
+        if (e == hipSuccess) {
+            const uint64_t tb = bg / (F / kTileRows);  // bytes of one tile
+            e = hipMemcpy2DAsync(L.wgu, 2 * tb, gu_stage, tb, tb, F / kTileRows, hipMemcpyDeviceToDevice, s);
+            if (e == hipSuccess)
+                e = hipMemcpy2DAsync(L.wgu + tb, 2 * tb, gu_stage + bg, tb, tb, F / kTileRows, hipMemcpyDeviceToDevice,
+                                     s);
+            if (e == hipSuccess) e = hipStreamSynchronize(s);  // the stage is reused by the next layer
+        }
         if (e == hipSuccess) e = hipMalloc((void**)&L.wdown, layout_bytes(wt, W, F));
         if (e == hipSuccess) e = tiled(hl.down, W, F, L.wdown);
         if (e == hipSuccess) e = upload_f32(hl.attention_norm, W, t.on_device, &L.attn_norm, s);
@@ -462,6 +484,7 @@ hipError_t LlamaModel::create(const LlamaDims& dims, const LlamaHostTensors& t, 
                            s);
     if (e == hipSuccess) e = hipStreamSynchronize(s);
     if (staging) (void)hipFree(staging);
+    if (gu_stage) (void)hipFree(gu_stage);
     return e;
 }
 
@@ -504,13 +527,13 @@ hipError_t LlamaModel::step(float* hidden, uint64_t position, float* embedding_o
         res.resid = hidden;
         e = launch_matvec_ex(wt, L.wo, W, W, att, nullptr, 1, hidden, W, nullptr, err_word, nullptr, nullptr, res, s);
         if (e != hipSuccess) break;
-        MvExtra norm2;
-        norm2.xform = 1, norm2.eps = d.rms_epsilon, norm2.norm_w = L.ffn_norm;
+        MvExtra norm2;  // gate/up with the FFN norm; the epilogue leaves silu(gate) * up in gu
+        norm2.xform = 1, norm2.eps = d.rms_epsilon, norm2.norm_w = L.ffn_norm, norm2.epilogue = 1;
         e = launch_matvec_ex(wt, L.wgu, 2 * F, W, hidden, nullptr, 1, gu, 2 * F, nullptr, err_word, nullptr, nullptr,
                              norm2, s);
         if (e != hipSuccess) break;
         MvExtra down;
-        down.xform = 2, down.resid = hidden;
+        down.resid = hidden;
         e = launch_matvec_ex(wt, L.wdown, W, F, gu, nullptr, 1, hidden, W, nullptr, err_word, nullptr, nullptr, down,
                              s);
     }

@@ -118,6 +118,9 @@ struct MvArgs {
     float eps;
     const float* norm_w;
     const float* resid;
+    // kEpSiluPair: the rows are gate and up tiles interleaved ([gate tile i,
+    // up tile i] as tiles 2i, 2i + 1) and y[16 i + r] = silu(gate) * up
+    uint32_t epilogue;
 };
 
 // LDS: q8 [batch][S] | d f32 [nb][8] | (Q4_K) bsums i16 [nb][8][16] | 256
@@ -183,6 +186,7 @@ __device__ __forceinline__ void prefetch_unit(const MvArgs& a, uint32_t wave, fl
 //                (crates/model-runtime/src/llama.rs:367-371, SiLU of
 //                crates/quant/src/cpu_math.rs:28-53)
 enum MvXform : uint32_t { kXfNone = 0, kXfRmsNorm = 1, kXfSiluMul = 2 };
+enum MvEpilogue : uint32_t { kEpStore = 0, kEpSiluPair = 1 };
 
 __device__ __forceinline__ void load16(const float* p, float (&v)[16]) {
     const float4* src = (const float4*)p;
@@ -685,6 +689,25 @@ __global__ __launch_bounds__(W * 64) void q4k_mv_small_kernel(MvArgs a) {
     pipeline<D>(steps, buf, issue, compute);
     __syncthreads();
 
+    if (TS == 2 && a.epilogue == kEpSiluPair) {
+        // tile slots (2 til, 2 til + 1) hold gate and up rows of the same 16
+        // outputs (llama.rs:367-371: gate = silu(gate); gate *= up)
+        for (uint32_t it = threadIdx.x; it < tmax * 16; it += W * 64) {
+            const uint32_t r = it % 16, til = it / 16;
+            const uint32_t t = blockIdx.x * TS + til * tstride;  // the gate tile, even
+            if (t + 1 < ntiles) {
+                float g = 0.0f, u = 0.0f;
+#pragma unroll
+                for (int k = 0; k < KS; ++k)
+                    if ((uint32_t)k < nb) {
+                        g += part[((til * TS * KS + k) * 16 + r) * B];
+                        u += part[(((til * TS + 1) * KS + k) * 16 + r) * B];
+                    }
+                a.y[(t / 2) * kTileRows + r] = (g / (1.0f + sse2_exp(0.0f - g))) * u;
+            }
+        }
+        return;
+    }
     // add the K parts of every parked (tile, row) in order and store
 #pragma unroll
     for (int b = 0; b < B; ++b) {
@@ -982,6 +1005,11 @@ hipError_t launch_matvec_ex(uint32_t wtype, const uint8_t* w, uint64_t rows, uin
     if (ex.xform != kXfNone && (batch != 1 || !x || wtype == kQ8_0 || ex.xform > kXfSiluMul ||
                                 (ex.xform == kXfRmsNorm && !ex.norm_w)))
         return hipErrorInvalidValue;
+    // the SiLU pair epilogue: one Q4_K column, whole tile pairs, no argmax or residual
+    if (ex.epilogue != kEpStore &&
+        (ex.epilogue != kEpSiluPair || batch != 1 || wtype != kQ4_K || rows % (2 * kTileRows) != 0 || argmax_key ||
+         ex.resid || dbg_isum))
+        return hipErrorInvalidValue;
     uint64_t b0 = 0;
     while (b0 < batch) {
         uint32_t nbat = (uint32_t)(batch - b0 < 8 ? batch - b0 : 8);
@@ -1014,11 +1042,14 @@ hipError_t launch_matvec_ex(uint32_t wtype, const uint8_t* w, uint64_t rows, uin
         a.eps = ex.eps;
         a.norm_w = ex.norm_w;
         a.resid = ex.resid ? ex.resid + b0 * ldy : nullptr;
+        a.epilogue = ex.epilogue;
         hipError_t e;
         constexpr int W = kMvWaves;
         const bool dbg = a.dbg_isum != nullptr;
         if (wtype == kQ4_K) {
-            if (nbat == 1)
+            if (ex.epilogue == kEpSiluPair)  // two tile slots per workgroup: a gate tile and its up tile
+                e = launch_small<kSmallW, kSmallW / 2, kSmallD, 1, false>(a, s);
+            else if (nbat == 1)
                 e = dbg ? launch_small<kSmallW, kSmallKS, kSmallD, 1, true>(a, s)
                         : launch_small<kSmallW, kSmallKS, kSmallD, 1, false>(a, s);
             else if (nbat == 2)

@@ -75,11 +75,15 @@ hipError_t launch_matvec(uint32_t wtype, const uint8_t* w, uint64_t rows, uint64
 //           [gate (cols) | up (cols)] and silu(gate) * up is quantized
 //           (crates/model-runtime/src/llama.rs:367-371)
 //   resid   y = resid + dot (math.rs:203-208); may alias y
+//   epilogue 0: store y; 1 (Q4_K, batch 1): the rows are gate and up 16-row
+//           tiles interleaved, and y[16 i + r] = silu(gate) * up of tile pair
+//           i (llama.rs:367-371), rows / 2 values
 struct MvExtra {
     uint32_t xform = 0;
     float eps = 0.0f;
     const float* norm_w = nullptr;
     const float* resid = nullptr;
+    uint32_t epilogue = 0;
 };
 hipError_t launch_matvec_ex(uint32_t wtype, const uint8_t* w, uint64_t rows, uint64_t cols, const float* x,
                             const ActPlanes* pre, uint64_t batch, float* y, uint64_t ldy,
