@@ -229,7 +229,10 @@ int oracle_matvec_activation_dtype(uint32_t w, uint32_t *out, oracle_error *err)
 }
 
 /* The weight dtypes whose dot this oracle restates. */
-static int path_weight(uint32_t t) { return t == T_Q8_0 || t == T_Q4_K || t == T_Q6_K; }
+static int path_weight(uint32_t t) {
+    return t == T_Q8_0 || t == T_Q2_K || t == T_Q3_K || t == T_Q4_K || t == T_Q5_K || t == T_Q6_K;
+}
+static int k_weight(uint32_t t) { return t == T_Q2_K || t == T_Q3_K || t == T_Q4_K || t == T_Q5_K || t == T_Q6_K; }
 
 /* ---- Q8_K activation quantizer: activation.rs:4-51 ---------------------- */
 
@@ -466,12 +469,15 @@ static void unpack_scale_min(const uint8_t *p, int sub, uint8_t *sc, uint8_t *mn
     }
 }
 
-/* encode_k.rs:430-507 for Q4_K (nmax 15, rmin -1, 20 steps); out is 144 bytes */
-static int encode_q4k_block(const float *x, uint8_t *out) {
+/* encode_k.rs:430-507: Q4_K (nmax 15, rmin -1, 20 steps; 144 bytes) and Q5_K
+ * (nmax 31, rmin -0.5, 15 steps, high bits at 16..47; 176 bytes) */
+static int encode_q45k_block(int five, const float *x, uint8_t *out) {
+    const int32_t nmax = five ? 31 : 15;
+    const int qpos = five ? 48 : 16;
     int32_t levels[256];
     float scales[8], minima[8];
     float maximum_scale = 0.0f, maximum_minimum = 0.0f;
-    memset(out, 0, 144);
+    memset(out, 0, five ? 176 : 144);
     for (int sub = 0; sub < 8; ++sub) {
         const float *values = x + sub * 32;
         float square_sum = 0.0f;
@@ -481,8 +487,8 @@ static int encode_q4k_block(const float *x, uint8_t *out) {
         float weights[32];
         for (int i = 0; i < 32; ++i) weights[i] = average + fabsf(values[i]);
         float scale, minimum;
-        if (make_affine2(values, 32, 15, weights, levels + sub * 32, -1.0f, 0.1f, 20, 0, &scale,
-                         &minimum))
+        if (make_affine2(values, 32, nmax, weights, levels + sub * 32, five ? -0.5f : -1.0f, 0.1f, five ? 15 : 20,
+                         0, &scale, &minimum))
             return -1;
         scales[sub] = scale;
         minima[sub] = minimum;
@@ -511,16 +517,195 @@ static int encode_q4k_block(const float *x, uint8_t *out) {
             int idx = sub * 32 + j;
             int32_t l;
             if (nearest((x[idx] + minimum) / scale, &l)) return -1;
-            levels[idx] = clampi(l, 0, 15);
+            levels[idx] = clampi(l, 0, nmax);
         }
     }
     for (int group = 0; group < 4; ++group) {
         for (int j = 0; j < 32; ++j) {
             uint8_t low = (uint8_t)levels[group * 64 + j];
             uint8_t high = (uint8_t)levels[group * 64 + j + 32];
-            out[16 + group * 32 + j] = (uint8_t)((low & 15) | ((high & 15) << 4));
+            if (five) {
+                if (low > 15) out[16 + j] |= (uint8_t)(1 << (2 * group));
+                if (high > 15) out[16 + j] |= (uint8_t)(2 << (2 * group));
+            }
+            out[qpos + group * 32 + j] = (uint8_t)((low & 15) | ((high & 15) << 4));
         }
     }
+    return 0;
+}
+static int encode_q4k_block(const float *x, uint8_t *out) { return encode_q45k_block(0, x, out); }
+
+/* encode_k.rs:346-355 */
+static void pack_two_bits(const int32_t *levels, uint8_t *out) {
+    for (int group = 0; group < 2; ++group)
+        for (int j = 0; j < 32; ++j)
+            out[group * 32 + j] = (uint8_t)((uint8_t)levels[group * 128 + j] | ((uint8_t)levels[group * 128 + j + 32] << 2) |
+                                            ((uint8_t)levels[group * 128 + j + 64] << 4) |
+                                            ((uint8_t)levels[group * 128 + j + 96] << 6));
+}
+
+/* encode_k.rs:292-345 (Q2_K: 16 groups of 16, make_affine2 with nmax 3, rmin
+ * -0.5, 15 steps, absolute-error objective; 84 bytes) */
+static int encode_q2k_block(const float *x, uint8_t *out) {
+    int32_t levels[256];
+    float scales[16], minima[16];
+    float maximum_scale = 0.0f, maximum_minimum = 0.0f;
+    memset(out, 0, 84);
+    for (int sub = 0; sub < 16; ++sub) {
+        const float *values = x + sub * 16;
+        float weights[16];
+        for (int i = 0; i < 16; ++i) weights[i] = fabsf(values[i]);
+        float scale, minimum;
+        if (make_affine2(values, 16, 3, weights, levels + sub * 16, -0.5f, 0.1f, 15, 1, &scale, &minimum))
+            return -1;
+        scales[sub] = scale;
+        minima[sub] = minimum;
+        if (scale > maximum_scale) maximum_scale = scale;
+        if (minimum > maximum_minimum) maximum_minimum = minimum;
+    }
+    if (maximum_scale > 0.0f) {
+        const float inverse = 15.0f / maximum_scale;
+        for (int sub = 0; sub < 16; ++sub) {
+            int32_t l;
+            if (nearest(inverse * scales[sub], &l)) return -1;
+            out[sub] = (uint8_t)l;
+        }
+        if (put_half_checked(out, 80, maximum_scale / 15.0f)) return -1;
+    }
+    if (maximum_minimum > 0.0f) {
+        const float inverse = 15.0f / maximum_minimum;
+        for (int sub = 0; sub < 16; ++sub) {
+            int32_t l;
+            if (nearest(inverse * minima[sub], &l)) return -1;
+            out[sub] |= (uint8_t)((uint8_t)l << 4);
+        }
+        if (put_half_checked(out, 82, maximum_minimum / 15.0f)) return -1;
+    }
+    for (int sub = 0; sub < 16; ++sub) {
+        const float scale = half_at(out, 80) * (float)(out[sub] & 15);
+        if (scale == 0.0f) continue;
+        const float minimum = half_at(out, 82) * (float)(out[sub] >> 4);
+        for (int j = 0; j < 16; ++j) {
+            const int idx = sub * 16 + j;
+            int32_t l;
+            if (nearest((x[idx] + minimum) / scale, &l)) return -1;
+            levels[idx] = clampi(l, 0, 3);
+        }
+    }
+    pack_two_bits(levels, out + 16);
+    return 0;
+}
+
+/* encode_k.rs:51-61 */
+static void signed_max(const float *x, int n, float *maximum, float *magnitude) {
+    float mag = 0.0f, mx = 0.0f;
+    for (int i = 0; i < n; ++i)
+        if (fabsf(x[i]) > mag) {
+            mag = fabsf(x[i]);
+            mx = x[i];
+        }
+    *maximum = mx;
+    *magnitude = mag;
+}
+
+/* encode_k.rs:138-185 (make_q3: iterative refinement, weights x^2) */
+static int make_q3(const float *x, int n, int32_t nmax, int32_t *levels, float *scale_out) {
+    float maximum, magnitude;
+    signed_max(x, n, &maximum, &magnitude);
+    if (magnitude < 1e-15f) {
+        for (int i = 0; i < n; ++i) levels[i] = 0;
+        *scale_out = 0.0f;
+        return 0;
+    }
+    const float inverse = -(float)nmax / maximum;
+    float sum_lx = 0.0f, sum_l2 = 0.0f;
+    for (int i = 0; i < n; ++i) {
+        int32_t l;
+        if (nearest(inverse * x[i], &l)) return -1;
+        l = clampi(l, -nmax, nmax - 1);
+        levels[i] = l;
+        const float w = x[i] * x[i];
+        sum_lx += w * x[i] * (float)l;
+        sum_l2 += w * (float)l * (float)l;
+    }
+    if (!is_finite_f(sum_lx) || !is_finite_f(sum_l2)) return -1;
+    for (int it = 0; it < 5; ++it) {
+        int changed = 0;
+        for (int i = 0; i < n; ++i) {
+            const float v = x[i], w = v * v;
+            float lx = sum_lx - w * v * (float)levels[i];
+            if (lx > 0.0f) {
+                float l2 = sum_l2 - w * (float)levels[i] * (float)levels[i];
+                int32_t next;
+                if (nearest(v * l2 / lx, &next)) return -1;
+                next = clampi(next, -nmax, nmax - 1);
+                if (next != levels[i]) {
+                    lx += w * v * (float)next;
+                    l2 += w * (float)next * (float)next;
+                    if (l2 > 0.0f && lx * lx * sum_l2 > sum_lx * sum_lx * l2) {
+                        levels[i] = next;
+                        sum_lx = lx;
+                        sum_l2 = l2;
+                        changed = 1;
+                    }
+                }
+            }
+        }
+        if (!changed) break;
+    }
+    for (int i = 0; i < n; ++i) levels[i] += nmax;
+    const float scale = sum_l2 > 0.0f ? sum_lx / sum_l2 : 0.0f;
+    if (!is_finite_f(scale)) return -1;
+    *scale_out = scale;
+    return 0;
+}
+
+/* encode_k.rs:357-409 (Q3_K: 16 groups of 16, signed 6-bit scales, the high
+ * bit of each 3-bit level in hmask; 110 bytes) */
+static int encode_q3k_block(const float *x, uint8_t *out) {
+    int32_t levels[256];
+    float scales[16];
+    float maximum_scale = 0.0f, maximum_magnitude = 0.0f;
+    memset(out, 0, 110);
+    for (int sub = 0; sub < 16; ++sub) {
+        if (make_q3(x + sub * 16, 16, 4, levels + sub * 16, &scales[sub])) return -1;
+        if (fabsf(scales[sub]) > maximum_magnitude) {
+            maximum_magnitude = fabsf(scales[sub]);
+            maximum_scale = scales[sub];
+        }
+    }
+    if (maximum_scale != 0.0f) {
+        const float inverse = -32.0f / maximum_scale;
+        for (int sub = 0; sub < 16; ++sub) {
+            int32_t l;
+            if (nearest(inverse * scales[sub], &l)) return -1;
+            const uint8_t u = (uint8_t)(clampi(l, -32, 31) + 32);
+            if (sub < 8)
+                out[96 + sub] = u & 15;
+            else
+                out[96 + sub - 8] |= (uint8_t)((u & 15) << 4);
+            out[104 + sub % 4] |= (uint8_t)((u >> 4) << (2 * (sub / 4)));
+        }
+        if (put_half_checked(out, 108, 1.0f / inverse)) return -1;
+    }
+    for (int sub = 0; sub < 16; ++sub) {
+        const uint8_t low = sub < 8 ? (out[96 + sub] & 15) : (out[96 + sub - 8] >> 4);
+        const int32_t sc = (int32_t)(low | (((out[104 + sub % 4] >> (2 * (sub / 4))) & 3) << 4)) - 32;
+        const float scale = half_at(out, 108) * (float)sc;
+        if (scale == 0.0f) continue;
+        for (int j = 0; j < 16; ++j) {
+            const int idx = sub * 16 + j;
+            int32_t l;
+            if (nearest(x[idx] / scale, &l)) return -1;
+            levels[idx] = clampi(l, -4, 3) + 4;
+        }
+    }
+    for (int j = 0; j < 256; ++j)
+        if (levels[j] > 3) {
+            out[j % 32] |= (uint8_t)(1 << (j / 32));
+            levels[j] -= 4;
+        }
+    pack_two_bits(levels, out + 32);
     return 0;
 }
 
@@ -577,19 +762,23 @@ int oracle_quantize_into(uint32_t t, const float *x, uint64_t n, uint8_t *out, u
                          oracle_error *err) {
     int rc = validate(t, out_len, n, err); /* encode.rs:38 */
     if (rc) return rc;
-    if (t != T_Q8_0 && t != T_Q8_K && t != T_Q4_K && t != T_Q6_K)
-        return set_err(err, ORC_UNIMPLEMENTED, t, 0, 0);
+    if (t != T_Q8_0 && t != T_Q8_K && !k_weight(t)) return set_err(err, ORC_UNIMPLEMENTED, t, 0, 0);
     if (n && (!x || !out)) return set_err(err, ORC_INVALID_ARGUMENT, t, 0, 0);
     for (uint64_t i = 0; i < n; ++i) /* encode.rs:70-74, encode_k.rs:13-17 */
         if (!is_finite_f(x[i])) return set_err(err, ORC_NON_FINITE_INPUT, t, i, 0);
     uint64_t bs = oracle_block_size(t), ts = oracle_type_size(t), nb = n / bs;
-    if (t == T_Q4_K || t == T_Q6_K) {
+    if (k_weight(t)) {
         /* encode_k::encode stages the whole row, then quantize_into copies it */
         uint8_t *staged = (uint8_t *)malloc(out_len ? out_len : 1);
         if (!staged) return set_err(err, ORC_ALLOCATION_FAILED, t, 0, 0);
         for (uint64_t b = 0; b < nb; ++b) {
-            int bad = t == T_Q4_K ? encode_q4k_block(x + b * bs, staged + b * ts)
-                                  : encode_q6k_block(x + b * bs, staged + b * ts);
+            const float *xb = x + b * bs;
+            uint8_t *ob = staged + b * ts;
+            int bad = t == T_Q2_K   ? encode_q2k_block(xb, ob)
+                      : t == T_Q3_K ? encode_q3k_block(xb, ob)
+                      : t == T_Q4_K ? encode_q4k_block(xb, ob)
+                      : t == T_Q5_K ? encode_q45k_block(1, xb, ob)
+                                    : encode_q6k_block(xb, ob);
             if (bad) {
                 free(staged);
                 return set_err(err, ORC_UNREPRESENTABLE_SCALE, t, b, 0);
@@ -633,8 +822,7 @@ int oracle_dequantize_into(uint32_t t, const uint8_t *b, uint64_t len, float *y,
                            oracle_error *err) {
     int rc = validate(t, len, n, err);
     if (rc) return rc;
-    if (t != T_Q8_0 && t != T_Q8_K && t != T_Q4_K && t != T_Q6_K)
-        return set_err(err, ORC_UNIMPLEMENTED, t, 0, 0);
+    if (t != T_Q8_0 && t != T_Q8_K && !k_weight(t)) return set_err(err, ORC_UNIMPLEMENTED, t, 0, 0);
     if (n && (!b || !y)) return set_err(err, ORC_INVALID_ARGUMENT, t, 0, 0);
     uint64_t bs = oracle_block_size(t), ts = oracle_type_size(t);
     for (uint64_t blk = 0; blk < n / bs; ++blk) {
@@ -646,7 +834,8 @@ int oracle_dequantize_into(uint32_t t, const uint8_t *b, uint64_t len, float *y,
         } else if (t == T_Q8_K) { /* decode.rs:44-49 */
             float d = f32le(x, 0);
             for (int j = 0; j < 256; ++j) o[j] = d * (float)(int8_t)x[4 + j];
-        } else if (t == T_Q4_K) { /* decode.rs:216-235 */
+        } else if (t == T_Q4_K || t == T_Q5_K) { /* decode.rs:216-235 */
+            const int five = t == T_Q5_K, qbase = five ? 48 : 16;
             float d = half_at(x, 0), mn = half_at(x, 2);
             for (int group = 0; group < 4; ++group) {
                 for (int side = 0; side < 2; ++side) {
@@ -655,11 +844,45 @@ int oracle_dequantize_into(uint32_t t, const uint8_t *b, uint64_t len, float *y,
                     float dl = d * (float)sc;
                     float ml = mn * (float)m;
                     for (int j = 0; j < 32; ++j) {
-                        uint8_t q = (x[16 + group * 32 + j] >> (side * 4)) & 15;
+                        uint8_t q = (x[qbase + group * 32 + j] >> (side * 4)) & 15;
+                        if (five && (x[16 + j] & (1 << (group * 2 + side)))) q += 16;
                         o[group * 64 + side * 32 + j] = dl * (float)q - ml;
                     }
                 }
             }
+        } else if (t == T_Q2_K) { /* decode.rs:159-175 */
+            const float d = half_at(x, 80), mn = half_at(x, 82);
+            for (int group = 0; group < 2; ++group)
+                for (int lane = 0; lane < 4; ++lane)
+                    for (int side = 0; side < 2; ++side) {
+                        const uint8_t sc = x[group * 8 + lane * 2 + side];
+                        const float dl = d * (float)(sc & 15), ml = mn * (float)(sc >> 4);
+                        for (int j = 0; j < 16; ++j)
+                            o[group * 128 + lane * 32 + side * 16 + j] =
+                                dl * (float)((x[16 + group * 32 + side * 16 + j] >> (2 * lane)) & 3) - ml;
+                    }
+        } else if (t == T_Q3_K) { /* decode.rs:177-202 */
+            const float d = half_at(x, 108);
+            const uint8_t *q = x + 32, *packed = x + 96;
+            int32_t sc[16];
+            for (int j = 0; j < 4; ++j) {
+                sc[j] = (packed[j] & 15) | ((packed[8 + j] & 3) << 4);
+                sc[4 + j] = (packed[4 + j] & 15) | (((packed[8 + j] >> 2) & 3) << 4);
+                sc[8 + j] = (packed[j] >> 4) | (((packed[8 + j] >> 4) & 3) << 4);
+                sc[12 + j] = (packed[4 + j] >> 4) | (((packed[8 + j] >> 6) & 3) << 4);
+            }
+            for (int group = 0; group < 2; ++group)
+                for (int lane = 0; lane < 4; ++lane) {
+                    const int mask = 1 << (group * 4 + lane);
+                    for (int side = 0; side < 2; ++side) {
+                        const float dl = d * (float)(sc[group * 8 + lane * 2 + side] - 32);
+                        for (int j = 0; j < 16; ++j) {
+                            const int pos = side * 16 + j;
+                            const int32_t v = ((q[group * 32 + pos] >> (2 * lane)) & 3) - ((x[pos] & mask) ? 0 : 4);
+                            o[group * 128 + lane * 32 + pos] = dl * (float)v;
+                        }
+                    }
+                }
         } else { /* Q6_K, decode.rs:237-258 */
             float d = half_at(x, 208);
             for (int group = 0; group < 2; ++group) {
@@ -700,12 +923,45 @@ static float dot_q8_0(const uint8_t *x, const uint8_t *y, uint64_t nb) {
     return sum;
 }
 
-/* One Q4_K / Q6_K block: the 8 lane integers and (Q4_K) the mins sum. */
+/* matvec_extra.rs:200-210 */
+static void q3_scales(const uint8_t *x, int32_t sc[16]) {
+    const uint8_t *p = x + 96;
+    for (int j = 0; j < 4; ++j) {
+        sc[j] = ((p[j] & 15) | ((p[8 + j] & 3) << 4)) - 32;
+        sc[4 + j] = ((p[4 + j] & 15) | (((p[8 + j] >> 2) & 3) << 4)) - 32;
+        sc[8 + j] = ((p[j] >> 4) | (((p[8 + j] >> 4) & 3) << 4)) - 32;
+        sc[12 + j] = ((p[4 + j] >> 4) | (((p[8 + j] >> 6) & 3) << 4)) - 32;
+    }
+}
+
+/* One Q3_K / Q4_K / Q5_K / Q6_K block: the 8 lane integers and (Q4_K, Q5_K)
+ * the mins sum; Q2_K: lane 0 holds the whole integer sum (matvec_extra.rs:174-197
+ * keeps one accumulator) and mins its mins sum. */
 static void k_block_ints(uint32_t t, const uint8_t *xb, const uint8_t *yb, int32_t ints[8],
                          int32_t *mins_out) {
     for (int l = 0; l < 8; ++l) ints[l] = 0;
     *mins_out = 0;
-    if (t == T_Q4_K) { /* matvec_extra.rs:252-267 */
+    if (t == T_Q2_K) { /* matvec_extra.rs:181-192 */
+        int32_t mins = 0, isum = 0;
+        for (int j = 0; j < 16; ++j) mins += bsum_at(yb, j) * (xb[j] >> 4);
+        for (int j = 0; j < 256; ++j) {
+            int group = j / 128, lane = (j % 128) / 32, pos = j % 32;
+            int32_t q = (xb[16 + group * 32 + pos] >> (2 * lane)) & 3;
+            isum += (xb[j / 16] & 15) * q * q8k_at(yb, j);
+        }
+        ints[0] = isum;
+        *mins_out = mins;
+    } else if (t == T_Q3_K) { /* matvec_extra.rs:234-248 */
+        int32_t sc[16];
+        q3_scales(xb, sc);
+        for (int j = 0; j < 256; ++j) {
+            int group = j / 128, lane = (j % 128) / 32, pos = j % 32;
+            int32_t low = (xb[32 + group * 32 + pos] >> (2 * lane)) & 3;
+            int32_t q = low - ((xb[pos] & (1 << (group * 4 + lane))) == 0 ? 4 : 0);
+            ints[j % 8] += sc[j / 16] * q * q8k_at(yb, j);
+        }
+    } else if (t == T_Q4_K || t == T_Q5_K) { /* matvec_extra.rs:250-270 */
+        const int five = t == T_Q5_K, qpos = five ? 48 : 16;
         int32_t mins = 0;
         for (int sub = 0; sub < 8; ++sub) {
             int32_t scale, mn;
@@ -713,7 +969,8 @@ static void k_block_ints(uint32_t t, const uint8_t *xb, const uint8_t *yb, int32
             mins += (bsum_at(yb, 2 * sub) + bsum_at(yb, 2 * sub + 1)) * mn;
             for (int l = 0; l < 32; ++l) {
                 int j = sub * 32 + l;
-                int32_t q = (xb[16 + sub / 2 * 32 + l] >> (4 * (sub % 2))) & 15;
+                int32_t q = (xb[qpos + sub / 2 * 32 + l] >> (4 * (sub % 2))) & 15;
+                if (five && (xb[16 + l] & (1 << sub))) q += 16;
                 ints[j % 8] += scale * q * q8k_at(yb, j);
             }
         }
@@ -739,10 +996,12 @@ static float dot_k_lanes(uint32_t t, const uint8_t *x, const uint8_t *y, uint64_
         int32_t ints[8], mins;
         float d;
         k_block_ints(t, xb, yb, ints, &mins);
-        if (t == T_Q4_K) {
+        if (t == T_Q4_K || t == T_Q5_K) {
             d = half_at(xb, 0) * f32le(yb, 0);
             float dmin = half_at(xb, 2) * f32le(yb, 0);
             sum -= dmin * (float)mins;
+        } else if (t == T_Q3_K) {
+            d = half_at(xb, 108) * f32le(yb, 0);
         } else {
             d = half_at(xb, 208) * f32le(yb, 0);
         }
@@ -752,9 +1011,23 @@ static float dot_k_lanes(uint32_t t, const uint8_t *x, const uint8_t *y, uint64_
     return sum;
 }
 
+/* matvec_extra.rs:174-198 */
+static float dot_q2k(const uint8_t *x, const uint8_t *y, uint64_t nb) {
+    float sum = 0.0f;
+    for (uint64_t b = 0; b < nb; ++b) {
+        const uint8_t *xb = x + b * 84, *yb = y + b * 292;
+        int32_t ints[8], mins;
+        k_block_ints(T_Q2_K, xb, yb, ints, &mins);
+        const float d = f32le(yb, 0) * half_at(xb, 80);
+        const float mn = f32le(yb, 0) * half_at(xb, 82);
+        sum += d * (float)ints[0] - mn * (float)mins;
+    }
+    return sum;
+}
+
 static float dot_unchecked(uint32_t t, const uint8_t *x, const uint8_t *y, uint64_t elements) {
     uint64_t nb = elements / oracle_block_size(t);
-    return t == T_Q8_0 ? dot_q8_0(x, y, nb) : dot_k_lanes(t, x, y, nb);
+    return t == T_Q8_0 ? dot_q8_0(x, y, nb) : t == T_Q2_K ? dot_q2k(x, y, nb) : dot_k_lanes(t, x, y, nb);
 }
 
 void oracle_block_sums(uint32_t t, const uint8_t *w, const uint8_t *a, uint64_t nb,
@@ -804,6 +1077,44 @@ double oracle_abs_terms(uint32_t t, const uint8_t *w, const uint8_t *a, uint64_t
             }
             const double da = fabs((double)f32le(yb, 0));
             total += fabs((double)half_at(xb, 0)) * da * s + fabs((double)half_at(xb, 2)) * da * m;
+        } else if (t == T_Q2_K || t == T_Q3_K || t == T_Q5_K) {
+            /* per element |scale * q * q8| (Q2_K, Q5_K) or |sc * q * q8| (Q3_K),
+             * and the mins terms of Q2_K / Q5_K */
+            const uint8_t *xb = w + b * oracle_type_size(t), *yb = a + b * 292;
+            double s = 0.0, m = 0.0, dw, dm = 0.0;
+            if (t == T_Q2_K) {
+                for (int j = 0; j < 16; ++j) m += (double)(xb[j] >> 4) * fabs((double)bsum_at(yb, j));
+                for (int j = 0; j < 256; ++j) {
+                    int group = j / 128, lane = (j % 128) / 32, pos = j % 32;
+                    int32_t q = (xb[16 + group * 32 + pos] >> (2 * lane)) & 3;
+                    s += fabs((double)((xb[j / 16] & 15) * q * q8k_at(yb, j)));
+                }
+                dw = half_at(xb, 80), dm = half_at(xb, 82);
+            } else if (t == T_Q3_K) {
+                int32_t sc[16];
+                q3_scales(xb, sc);
+                for (int j = 0; j < 256; ++j) {
+                    int group = j / 128, lane = (j % 128) / 32, pos = j % 32;
+                    int32_t q = ((xb[32 + group * 32 + pos] >> (2 * lane)) & 3) -
+                                ((xb[pos] & (1 << (group * 4 + lane))) == 0 ? 4 : 0);
+                    s += fabs((double)(sc[j / 16] * q * q8k_at(yb, j)));
+                }
+                dw = half_at(xb, 108);
+            } else {
+                for (int sub = 0; sub < 8; ++sub) {
+                    int32_t scale, mn;
+                    scale_min_k(xb + 4, sub, &scale, &mn);
+                    m += (double)mn * fabs((double)(bsum_at(yb, 2 * sub) + bsum_at(yb, 2 * sub + 1)));
+                    for (int l = 0; l < 32; ++l) {
+                        int32_t q = (xb[48 + sub / 2 * 32 + l] >> (4 * (sub % 2))) & 15;
+                        if (xb[16 + l] & (1 << sub)) q += 16;
+                        s += fabs((double)(scale * q * q8k_at(yb, sub * 32 + l)));
+                    }
+                }
+                dw = half_at(xb, 0), dm = half_at(xb, 2);
+            }
+            const double da = fabs((double)f32le(yb, 0));
+            total += fabs(dw) * da * s + fabs(dm) * da * m;
         } else {
             const uint8_t *xb = w + b * 210, *yb = a + b * 292;
             double s = 0.0;

@@ -1,5 +1,6 @@
 #!/usr/bin/env python3
-"""Copy the reference's golden records for Q8_0 / Q4_K / Q6_K / Q8_K into tests/golden/.
+"""Copy the reference's golden records for Q8_0 / Q4_K / Q6_K / Q8_K (and the
+other K formats Q2_K / Q3_K / Q5_K) into tests/golden/.
 
 Run once, in a container where the reference checkout is mounted:
 
@@ -9,7 +10,7 @@ The reference's quant crate pins its scalar path with little-endian binary
 fixtures produced from the original ggml C code (crates/quant/README.md:45-57).
 This script reads those DATA files only (never code) and keeps the records whose
 dtype is on the quantized-matvec path: 8 (Q8_0), 12 (Q4_K), 14 (Q6_K) and
-15 (Q8_K).  Each output file keeps the source's record layout and magic, with
+15 (Q8_K), then, in files of their own, 10 (Q2_K), 11 (Q3_K) and 13 (Q5_K).  Each output file keeps the source's record layout and magic, with
 the record count rewritten, so a reader of the original format reads it too.
 `manifest.json` records, per output, the source file, its SHA-256, the source
 record indices kept and the SHA-256 of the output.
@@ -34,6 +35,7 @@ import struct
 import sys
 
 KEEP = {8, 12, 14, 15}
+KEEP_K = {10, 11, 13}
 SRC_DIR = "crates/quant/tests/fixtures"
 
 
@@ -86,23 +88,27 @@ def split_records(kind, data):
 
 
 FILES = [
-    ("matvec-extended-reference.bin", "GGQX", "matvec-extended-q4k-q6k.bin"),
-    ("matvec-reference.bin", "GGQM", "matvec-q8_0.bin"),
-    ("q8k-reference.bin", "GGQ8", "q8k.bin"),
-    ("quant-reference.bin", "GGQE", "quant-q8_0-q4k-q6k-q8k.bin"),
-    ("encoder-extended-reference.bin", "GGQE", "encoder-extended-q8_0-q4k-q6k.bin"),
-    ("dequant-reference.bin", "GGQD", "dequant-q8_0-q4k-q6k-q8k.bin"),
+    ("matvec-extended-reference.bin", "GGQX", "matvec-extended-q4k-q6k.bin", KEEP),
+    ("matvec-reference.bin", "GGQM", "matvec-q8_0.bin", KEEP),
+    ("q8k-reference.bin", "GGQ8", "q8k.bin", KEEP),
+    ("quant-reference.bin", "GGQE", "quant-q8_0-q4k-q6k-q8k.bin", KEEP),
+    ("encoder-extended-reference.bin", "GGQE", "encoder-extended-q8_0-q4k-q6k.bin", KEEP),
+    ("dequant-reference.bin", "GGQD", "dequant-q8_0-q4k-q6k-q8k.bin", KEEP),
+    # the other K formats on the same dot: Q2_K (10), Q3_K (11), Q5_K (13)
+    ("matvec-extended-reference.bin", "GGQX", "matvec-extended-q2k-q3k-q5k.bin", KEEP_K),
+    ("encoder-extended-reference.bin", "GGQE", "encoder-extended-q2k-q3k-q5k.bin", KEEP_K),
+    ("dequant-reference.bin", "GGQD", "dequant-q2k-q3k-q5k.bin", KEEP_K),
 ]
 
 
 def main():
     root = sys.argv[1] if len(sys.argv) > 1 else "/root/reference"
     here = os.path.dirname(os.path.abspath(__file__))
-    manifest = {"source_root": "rust-llama " + SRC_DIR, "kept_dtypes": sorted(KEEP), "files": {}}
-    for src, kind, dst in FILES:
+    manifest = {"source_root": "rust-llama " + SRC_DIR, "kept_dtypes": sorted(KEEP | KEEP_K), "files": {}}
+    for src, kind, dst, keep in FILES:
         data = open(os.path.join(root, SRC_DIR, src), "rb").read()
         magic, records = split_records(kind, data)
-        kept = [(i, d, raw) for i, (d, raw) in enumerate(records) if d in KEEP]
+        kept = [(i, d, raw) for i, (d, raw) in enumerate(records) if d in keep]
         out = magic + struct.pack("<I", len(kept)) + b"".join(raw for _, _, raw in kept)
         with open(os.path.join(here, dst), "wb") as f:
             f.write(out)

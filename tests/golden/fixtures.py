@@ -53,9 +53,10 @@ class MatvecRecord:
     native: np.ndarray      # original GGML graph output
 
 
-def matvec_extended():
-    """GGQX: 24 Q4_K + 24 Q6_K records (matvec_extended.rs:50-103)."""
-    r = _Reader("matvec-extended-q4k-q6k.bin", b"GGQX0001")
+def matvec_extended(name="matvec-extended-q4k-q6k.bin"):
+    """GGQX: 24 Q4_K + 24 Q6_K records (matvec_extended.rs:50-103), or with
+    name="matvec-extended-q2k-q3k-q5k.bin" 24 each of Q2_K, Q3_K, Q5_K."""
+    r = _Reader(name, b"GGQX0001")
     out = []
     for _ in range(r.count):
         dtype, rows, cols, wsize, asize = (r.word() for _ in range(5))
@@ -91,12 +92,13 @@ def q8k():
     return out
 
 
-def encoders():
+def encoders(names=("quant-q8_0-q4k-q6k-q8k.bin", "encoder-extended-q8_0-q4k-q6k.bin")):
     """GGQE records: (dtype, x, expected bytes) from quant-reference (Q8_0) and
     encoder-extended-reference (Q4_K, Q6_K) (reference.rs:56-81,
-    encoders_extended.rs:27-63)."""
+    encoders_extended.rs:27-63); names=("encoder-extended-q2k-q3k-q5k.bin",)
+    gives the Q2_K, Q3_K and Q5_K records."""
     out = []
-    for name in ("quant-q8_0-q4k-q6k-q8k.bin", "encoder-extended-q8_0-q4k-q6k.bin"):
+    for name in names:
         r = _Reader(name, b"GGQE0001")
         for _ in range(r.count):
             dtype, n, size = r.word(), r.word(), r.word()
@@ -105,9 +107,10 @@ def encoders():
     return out
 
 
-def dequant():
-    """GGQD records: (dtype, n, packed bytes, expected f32) (reference.rs:20-55)."""
-    r = _Reader("dequant-q8_0-q4k-q6k-q8k.bin", b"GGQD0001")
+def dequant(name="dequant-q8_0-q4k-q6k-q8k.bin"):
+    """GGQD records: (dtype, n, packed bytes, expected f32) (reference.rs:20-55);
+    name="dequant-q2k-q3k-q5k.bin" for Q2_K, Q3_K, Q5_K."""
+    r = _Reader(name, b"GGQD0001")
     out = []
     for _ in range(r.count):
         dtype, n, size = r.word(), r.word(), r.word()

@@ -85,6 +85,70 @@ def test_decoders_bitwise():
         assert same.all(), t
 
 
+K_OTHER = "matvec-extended-q2k-q3k-q5k.bin"
+
+
+def test_matvec_extended_q2k_q3k_q5k_bitwise():
+    recs = F.matvec_extended(K_OTHER)
+    assert len(recs) == 72
+    assert sorted({r.dtype for r in recs}) == [O.Q2_K, O.Q3_K, O.Q5_K]
+    for i, r in enumerate(recs):
+        act = O.quantize(O.Q8_K, r.x)
+        assert np.array_equal(act, r.activation), f"record {i}: activation bytes"
+        y = O.matvec(r.dtype, r.weights, r.rows, r.cols, r.x)
+        assert np.array_equal(bits(y), bits(r.generic)), f"record {i} dtype {r.dtype}: generic C"
+        assert np.array_equal(bits(y), bits(r.native)), f"record {i} dtype {r.dtype}: GGML graph"
+
+
+def test_encoders_q2k_q3k_q5k_bitwise():
+    recs = F.encoders(("encoder-extended-q2k-q3k-q5k.bin",))
+    counts = {}
+    for i, (t, x, expected) in enumerate(recs):
+        got = O.quantize(t, x)
+        assert np.array_equal(got, expected), f"record {i} dtype {t}"
+        counts[t] = counts.get(t, 0) + 1
+    assert counts == {O.Q2_K: 52, O.Q3_K: 52, O.Q5_K: 52}
+
+
+def test_decoders_q2k_q3k_q5k_bitwise():
+    recs = F.dequant("dequant-q2k-q3k-q5k.bin")
+    assert sorted(r[0] for r in recs) == [O.Q2_K, O.Q3_K, O.Q5_K]
+    for t, n, b, expected in recs:
+        y = O.dequantize(t, b, n)
+        same = (bits(y) == bits(expected)) | (np.isnan(y) & np.isnan(expected))
+        assert same.all(), t
+
+
+@pytest.mark.parametrize("t", [O.Q2_K, O.Q3_K, O.Q5_K])
+def test_other_k_dot_equals_f64_of_decoded_operands_and_block_sums(t):
+    """The dot of encoded random rows against quantized activations equals
+    the f64 dot of the decoded operands up to f32 rounding, and the block
+    integers rebuild it (Q2_K, Q5_K: d*isum - dmin*imin; Q3_K: d*isum)."""
+    rng = np.random.default_rng(17)
+    nb = 3
+    n = 256 * nb
+    w = O.quantize(t, rng.standard_normal(n).astype(np.float32) * 0.05)
+    x = rng.standard_normal(n).astype(np.float32)
+    act = O.quantize(O.Q8_K, x)
+    got = float(O.dot_packed(t, w, act, n))
+    wf = O.dequantize(t, w, n).astype(np.float64)
+    af = O.dequantize(O.Q8_K, act, n).astype(np.float64)
+    assert abs(got - float(np.dot(wf, af))) <= 1e-5 * float(np.dot(np.abs(wf), np.abs(af)))
+    isum, imin = O.block_sums(t, w, act, nb)
+    ws, as_ = w.reshape(nb, -1), act.reshape(nb, -1)
+    tot = 0.0
+    for k in range(nb):
+        da = np.float64(as_[k, :4].view(np.float32)[0])
+        if t == O.Q2_K:
+            d, dm = (np.float64(v) for v in ws[k, 80:84].view(np.float16))
+        elif t == O.Q3_K:
+            d, dm = np.float64(ws[k, 108:110].view(np.float16)[0]), 0.0
+        else:
+            d, dm = (np.float64(v) for v in ws[k, 0:4].view(np.float16))
+        tot += d * da * isum[k] - dm * da * imin[k]
+    assert abs(got - tot) <= 1e-5 * float(np.dot(np.abs(wf), np.abs(af)))
+
+
 # ---------------------------------------------------------------- error paths
 
 def test_q8k_preflight_and_canonical_zero_blocks():
