@@ -127,7 +127,9 @@ int32_t activation_dtype(uint32_t w, uint32_t* out, rlq_error* err) {
     return ok(err);
 }
 
-bool path_weight(uint32_t t) { return t == kQ8_0 || t == kQ4_K || t == kQ6_K; }
+bool path_weight(uint32_t t) {
+    return t == kQ8_0 || t == kQ2_K || t == kQ3_K || t == kQ4_K || t == kQ5_K || t == kQ6_K;
+}
 
 // Batches up to this size run the decode kernels (one pass over the weights
 // per 8 columns); larger Q4_K batches run the prefill GEMM.
@@ -283,7 +285,7 @@ const char* rlq_status_string(int32_t code) {
         case RLQ_NON_FINITE_INPUT: return "non-finite quantizer input";
         case RLQ_UNREPRESENTABLE_SCALE: return "quantizer scale is not representable";
         case RLQ_DEVICE_ERROR: return "HIP runtime error";
-        case RLQ_UNIMPLEMENTED: return "type is outside the Q8_0/Q4_K/Q6_K path";
+        case RLQ_UNIMPLEMENTED: return "type or operation is outside the Q8_0/Q2_K..Q6_K path";
         case RLQ_INVALID_ARGUMENT: return "null pointer or handle";
         case RLQ_INVALID_CONFIG: return "invalid model configuration";
         case RLQ_INVALID_TOKEN: return "token outside the vocabulary";
@@ -653,7 +655,7 @@ int32_t rlq_dequantize_into(uint32_t dtype, const uint8_t* bytes, uint64_t len, 
                             rlq_error* err) {
     int32_t rc = validate(dtype, len, n, err);
     if (rc) return rc;
-    if (dtype != kQ8_0 && dtype != kQ8_K && dtype != kQ4_K && dtype != kQ6_K) return fail(err, RLQ_UNIMPLEMENTED, dtype);
+    if (dtype != kQ8_K && !path_weight(dtype)) return fail(err, RLQ_UNIMPLEMENTED, dtype);
     if (n == 0) return ok(err);
     if (!bytes || !out) return fail(err, RLQ_INVALID_ARGUMENT, dtype);
     std::lock_guard<std::mutex> lock(g_default_mu);

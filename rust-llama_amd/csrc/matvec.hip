@@ -1,10 +1,13 @@
-// matvec.hip - decode matvec (batch 1..8) for Q4_K / Q6_K / Q8_0 weights on gfx950.
+// matvec.hip - decode matvec (batch 1..8) for Q2_K..Q6_K / Q8_0 weights on gfx950.
 //
 // Contract (paths relative to the rust-llama repository):
 //   y[b][r] = dot_packed(row r, activation column b), the activation being
-//   column b of x quantized to Q8_K (Q4_K, Q6_K) or Q8_0 (Q8_0 weights)
+//   column b of x quantized to Q8_K (K formats) or Q8_0 (Q8_0 weights)
 //     Q8_0  crates/quant/src/matvec.rs:115-160  (Q8_0 branch :124-128)
+//     Q2_K  crates/quant/src/matvec_extra.rs:174-198
+//     Q3_K  crates/quant/src/matvec_extra.rs:200-210, 234-248, 286-293
 //     Q4_K  crates/quant/src/matvec_extra.rs:212-271, 286-293
+//     Q5_K  crates/quant/src/matvec_extra.rs:250-271 (the Q4_K branch plus qh)
 //     Q6_K  crates/quant/src/matvec_extra.rs:272-283, 286-293
 //   quantizers crates/quant/src/activation.rs:4-51 (Q8_K),
 //              crates/quant/src/encode.rs:115-126, 151-192 (Q8_0)
@@ -33,7 +36,9 @@
 // Q8_0 results equal the reference bit for bit).  Q4_K / Q6_K add
 // d * isum - dmin * imin per block from the exact block integers, where the
 // reference keeps eight lane accumulators; the difference is f32 rounding of
-// the same exact integers.
+// the same exact integers.  Q2_K adds d * isum - dmin * imin per block in
+// block order in one lane, which is the reference's own sequence: Q2_K
+// results equal the reference bit for bit.
 #include "rlq_device.hpp"
 #include "rlq_internal.hpp"
 #include "rlq_layout.hpp"
@@ -123,7 +128,7 @@ struct MvArgs {
     uint32_t epilogue;
 };
 
-// LDS: q8 [batch][S] | d f32 [nb][8] | (Q4_K) bsums i16 [nb][8][16] | 256
+// LDS: q8 [batch][S] | d f32 [nb][8] | (Q2_K, Q4_K, Q5_K) bsums i16 [nb][8][16] | 256
 // zero bytes | 16 f64 (the RMSNorm reduction of the input transform).  S = cols + 16 is an odd multiple of 16, so the A-operand reads
 // of the eight columns fall in distinct banks.  Lanes whose MFMA A operand is
 // all zero read the zero bytes instead of taking a branch.
@@ -137,19 +142,23 @@ __host__ __device__ inline LdsMap lds_map(uint32_t t, uint32_t cols, uint32_t ba
     m.S = cols + 16;
     m.d_off = (m.S * batch + 15u) & ~15u;
     m.bs_off = m.d_off + nb * 32;
-    m.zero_off = m.bs_off + (t == kQ4_K ? nb * 256 : 0);
+    m.zero_off = m.bs_off + (t == kQ4_K || t == kQ5_K || t == kQ2_K ? nb * 256 : 0);
     m.red_off = m.zero_off + 256;
     m.total = m.red_off + 128;
     return m;
 }
 
-// Q4_K bsums of one (block, column) are stored in the order [kq][4]: K
-// quarter kq = 2g + h finds the 16-value groups it multiplies (half h of
+// Q4_K / Q5_K bsums of one (block, column) are stored in the order [kq][4]:
+// K quarter kq = 2g + h finds the 16-value groups it multiplies (half h of
 // sub-blocks 2g, 2g+1, 2g+4, 2g+5) in one 8-byte word.  Slot of group
-// grp = 2 * sub + half:
+// grp = 2 * sub + half.  Q2_K keeps the natural order (slot = group).
 __device__ __forceinline__ uint32_t bs_slot(uint32_t grp) {
     const uint32_t sub = grp >> 1, half = grp & 1;
     return (2 * ((sub >> 1) & 1) + half) * 4 + (sub & 1) + 2 * (sub >> 2);
+}
+enum BsumOrder { kBsNone = 0, kBsQuarters = 1, kBsNatural = 2 };
+__host__ __device__ constexpr int bsum_order(uint32_t t) {
+    return t == kQ4_K || t == kQ5_K ? kBsQuarters : (t == kQ2_K ? kBsNatural : kBsNone);
 }
 
 // ---------------------------------------------------------------------------
@@ -232,7 +241,7 @@ __device__ __forceinline__ float rms_scale(const MvArgs& a, uint8_t* lds, const 
 // Q8_K of all batch columns into LDS.  A 16-lane row quantizes one 256-value
 // block, 16 values per lane (one bsum group per lane).  Returns false in
 // every thread when any block of any column is invalid.
-template <int W, bool BSUMS>
+template <int W, int BSUMS>
 __device__ __forceinline__ bool stage_q8k(const MvArgs& a, uint8_t* lds, const LdsMap& L, uint32_t wave, const float (&v0)[16]) {
     const uint32_t K = a.cols, upc = K / 16, units = upc * a.batch;
     const uint32_t lane = threadIdx.x & 63, r16 = lane & 15;
@@ -277,7 +286,9 @@ __device__ __forceinline__ bool stage_q8k(const MvArgs& a, uint8_t* lds, const L
         }
         *(uint4*)(lds + b * L.S + e0) = make_uint4(o.q[0], o.q[1], o.q[2], o.q[3]);
         if (r16 == 0) *(float*)(lds + L.d_off + (blk * 8 + b) * 4) = o.d;
-        if (BSUMS) *(int16_t*)(lds + L.bs_off + (blk * 8 + b) * 32 + bs_slot(r16) * 2) = (int16_t)o.bsum;
+        if (BSUMS != kBsNone)
+            *(int16_t*)(lds + L.bs_off + (blk * 8 + b) * 32 + (BSUMS == kBsQuarters ? bs_slot(r16) : r16) * 2) =
+                (int16_t)o.bsum;
     }
     return __syncthreads_or(bad) == 0;
 }
@@ -353,10 +364,12 @@ __device__ __forceinline__ bool stage_planes(const MvArgs& a, uint8_t* lds, cons
         *(float*)(lds + L.d_off + (blk * 8 + b) * 4) = a.pre.d[i];
         bad |= a.pre.bad[i];
     }
-    if (wtype == kQ4_K) {
+    const int order = bsum_order(wtype);
+    if (order != kBsNone) {
         for (uint32_t i = tid; i < a.batch * (K / 16); i += nt) {
             const uint32_t b = i / (K / 16), g = i % (K / 16);
-            *(int16_t*)(lds + L.bs_off + ((g / 16) * 8 + b) * 32 + bs_slot(g % 16) * 2) = a.pre.bsum[i];
+            const uint32_t slot = order == kBsQuarters ? bs_slot(g % 16) : g % 16;
+            *(int16_t*)(lds + L.bs_off + ((g / 16) * 8 + b) * 32 + slot * 2) = a.pre.bsum[i];
         }
     }
     return __syncthreads_or(bad) == 0;
@@ -412,11 +425,53 @@ __device__ __forceinline__ void pipeline(uint32_t steps, Step (&buf)[D], Issue& 
 }
 
 // ---------------------------------------------------------------------------
-// Q4_K
+// Q4_K and Q5_K (the same kernels; Q5_K adds the fifth bit from qh)
 // ---------------------------------------------------------------------------
+template <uint32_t T>
 struct Q4Step {
     uint4 w0, w1, h;
 };
+template <>
+struct Q4Step<kQ5_K> {
+    uint4 w0, w1, h, qh;
+};
+
+// Chunk geometry of the two formats (rlq_layout.hpp).
+template <uint32_t T>
+struct Q45 {
+    static constexpr uint32_t chunk = T == kQ5_K ? kQ5KChunk : kQ4KChunk;
+    static constexpr uint32_t head = T == kQ5_K ? 2560 : 2048;
+};
+
+template <uint32_t T>
+__device__ __forceinline__ void q45_issue(Q4Step<T>& st, const uint8_t* base, uint32_t lane, uint32_t n,
+                                          uint32_t kq) {
+    st.w0 = load_stream16(base + lane * 16);
+    st.w1 = load_stream16(base + 1024 + lane * 16);
+    st.h = load_stream16(base + Q45<T>::head + n * 16);
+    if constexpr (T == kQ5_K) st.qh = load_stream16(base + 2048 + n * 32 + 16 * (kq & 1));
+}
+
+// Q5_K fifth bits of this lane's four nibble sets, as 0x10 per byte: qh byte
+// 16h + i holds bit `sub` of element 32 sub + 16h + i; the lane's sets are
+// sub-blocks 2g (w0 low), 2g+1 (w0 high), 2g+4 (w1 low), 2g+5 (w1 high),
+// g = kq / 2 (matvec_extra.rs:257-262 with the Q5_K qh term).
+struct Q5High {
+    uint32_t l0[4], h0[4], l1[4], h1[4];
+};
+__device__ __forceinline__ Q5High q5_high(uint4 qh, uint32_t kq) {
+    const uint32_t sh = 2 * (kq >> 1);
+    const uint32_t q[4] = {qh.x >> sh, qh.y >> sh, qh.z >> sh, qh.w >> sh};
+    Q5High o;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        o.l0[i] = (q[i] << 4) & 0x10101010u;
+        o.h0[i] = (q[i] << 3) & 0x10101010u;
+        o.l1[i] = q[i] & 0x10101010u;
+        o.h1[i] = (q[i] >> 1) & 0x10101010u;
+    }
+    return o;
+}
 
 // Common kernel prologue: wave indices, the first x unit, the weight prefetch
 // of steps 0..D-1 (clamped to the last tile, so it never leaves the buffer),
@@ -465,23 +520,20 @@ __device__ __forceinline__ Q4Scales q4k_scales(uint4 h) {
 // Decode kernels with DBG also store the exact per-(row, block) integers of
 // column 0 (isum: the scaled sub-block dots; imin: the mins term).
 
-// Q4_K, batches of three to eight columns: MFMA.
-template <int W, int D, bool DBG>
+// Q4_K / Q5_K, batches of three to eight columns: MFMA.
+template <uint32_t T, int W, int D, bool DBG>
 __global__ __launch_bounds__(W * 64) void q4k_mv_kernel(MvArgs a) {
-    RLQ_MV_PROLOGUE(kQ4_K, a.nb)
+    RLQ_MV_PROLOGUE(T, a.nb)
     const uint32_t nb = a.nb;
-    Q4Step buf[D];
-    auto issue = [&](Q4Step& st) {
-        const uint8_t* base = a.w + ((uint64_t)ld_tile * nb + ld_chunk) * kQ4KChunk;
-        st.w0 = load_stream16(base + lane * 16);
-        st.w1 = load_stream16(base + 1024 + lane * 16);
-        st.h = load_stream16(base + 2048 + n * 16);
+    Q4Step<T> buf[D];
+    auto issue = [&](Q4Step<T>& st) {
+        q45_issue<T>(st, a.w + ((uint64_t)ld_tile * nb + ld_chunk) * Q45<T>::chunk, lane, n, kq);
         next_load();
     };
 #pragma unroll
     for (int i = 0; i < D; ++i) issue(buf[i]);
 
-    const bool ok = a.x ? stage_q8k<W, true>(a, lds, L, wave, xv) : stage_planes<W>(a, lds, L, kQ4_K);
+    const bool ok = a.x ? stage_q8k<W, kBsQuarters>(a, lds, L, wave, xv) : stage_planes<W>(a, lds, L, T);
     if (!ok) return;
 
     // A operand: lane row r = n holds column r / 2, sub-block parity r % 2; it
@@ -495,20 +547,32 @@ __global__ __launch_bounds__(W * 64) void q4k_mv_kernel(MvArgs a) {
     float acc0 = 0.0f, acc1 = 0.0f;
     unsigned long long best0 = 0, best1 = 0;
     uint32_t tile = gw, blk = 0;
-    auto compute = [&](const Q4Step& cur) {
+    auto compute = [&](const Q4Step<T>& cur) {
         const Q4Scales q = q4k_scales(cur.h);
         const uint8_t* p = a_ptr + blk * a_step;
         const i32x4 al0 = *(const i32x4*)(p), ah0 = *(const i32x4*)(p + 32);
         const i32x4 al1 = *(const i32x4*)(p + 128), ah1 = *(const i32x4*)(p + 160);
+        i32x4 wl0 = lo_nibbles(cur.w0), wh0 = hi_nibbles(cur.w0);
+        i32x4 wl1 = lo_nibbles(cur.w1), wh1 = hi_nibbles(cur.w1);
+        if constexpr (T == kQ5_K) {
+            const Q5High hb = q5_high(cur.qh, kq);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                wl0[i] |= (int)hb.l0[i];
+                wh0[i] |= (int)hb.h0[i];
+                wl1[i] |= (int)hb.l1[i];
+                wh1[i] |= (int)hb.h1[i];
+            }
+        }
         // sub-blocks: dl0 {0, 2}, dh0 {1, 3}, dl1 {4, 6}, dh1 {5, 7}; element
         // 2j + w of each is column b0 + j, sub-block parity w
-        const i32x4 dl0 = mfma_i8(al0, lo_nibbles(cur.w0));
-        const i32x4 dh0 = mfma_i8(ah0, hi_nibbles(cur.w0));
-        const i32x4 dl1 = mfma_i8(al1, lo_nibbles(cur.w1));
-        const i32x4 dh1 = mfma_i8(ah1, hi_nibbles(cur.w1));
+        const i32x4 dl0 = mfma_i8(al0, wl0);
+        const i32x4 dh0 = mfma_i8(ah0, wh0);
+        const i32x4 dl1 = mfma_i8(al1, wl1);
+        const i32x4 dh1 = mfma_i8(ah1, wh1);
         const int32_t c0 = ubyte(q.scA, 0), c1 = ubyte(q.scA, 1), c2 = ubyte(q.scA, 2), c3 = ubyte(q.scA, 3);
         const int32_t c4 = ubyte(q.scB, 0), c5 = ubyte(q.scB, 1), c6 = ubyte(q.scB, 2), c7 = ubyte(q.scB, 3);
-        // |dot| <= 32*15*127 and scales <= 63: 24-bit products are exact
+        // |dot| <= 32*31*128 and scales <= 63: 24-bit operands, exact products
         int32_t I0 = mad24(c0, dl0[0], mad24(c2, dl0[1], mad24(c1, dh0[0], __mul24(c3, dh0[1]))));
         I0 = mad24(c4, dl1[0], mad24(c6, dl1[1], mad24(c5, dh1[0], mad24(c7, dh1[1], I0))));
         int32_t I1 = mad24(c0, dl0[2], mad24(c2, dl0[3], mad24(c1, dh0[2], __mul24(c3, dh0[3]))));
@@ -576,11 +640,11 @@ __host__ __device__ inline uint32_t small_lds_bytes(uint32_t cols, uint32_t batc
     return small_part_off(cols, batch) + tmax * ts * ks * 16u * batch * 4u;
 }
 
-template <int W, int KS, int D, int B, bool DBG>
+template <uint32_t T, int W, int KS, int D, int B, bool DBG>
 __global__ __launch_bounds__(W * 64) void q4k_mv_small_kernel(MvArgs a) {
     constexpr int TS = SmallGeom<W, KS>::TS;
     extern __shared__ __align__(16) uint8_t lds[];
-    const LdsMap L = lds_map(kQ4_K, a.cols, a.batch);
+    const LdsMap L = lds_map(T, a.cols, a.batch);
     float* part = (float*)(lds + small_part_off(a.cols, a.batch));
     const uint32_t lane = threadIdx.x & 63, n = lane & 15, kq = lane >> 4;
     // wave-uniform indices in scalar registers: loop control stays on the SALU
@@ -600,12 +664,9 @@ __global__ __launch_bounds__(W * 64) void q4k_mv_small_kernel(MvArgs a) {
     // loads run D steps ahead; past the wave's last step they repeat a valid chunk
     const uint32_t kp0 = kp < nb ? kp : nb - 1;
     uint32_t ld_tile = t0 < ntiles ? t0 : ntiles - 1, ld_blk = kp0;
-    Q4Step buf[D];
-    auto issue = [&](Q4Step& st) {
-        const uint8_t* base = a.w + ((uint64_t)ld_tile * nb + ld_blk) * kQ4KChunk;
-        st.w0 = load_stream16(base + lane * 16);
-        st.w1 = load_stream16(base + 1024 + lane * 16);
-        st.h = load_stream16(base + 2048 + n * 16);
+    Q4Step<T> buf[D];
+    auto issue = [&](Q4Step<T>& st) {
+        q45_issue<T>(st, a.w + ((uint64_t)ld_tile * nb + ld_blk) * Q45<T>::chunk, lane, n, kq);
         ld_blk += KS;
         if (ld_blk >= nb) {
             ld_blk = kp0;
@@ -615,7 +676,7 @@ __global__ __launch_bounds__(W * 64) void q4k_mv_small_kernel(MvArgs a) {
 #pragma unroll
     for (int i = 0; i < D; ++i) issue(buf[i]);
 
-    const bool ok = a.x ? stage_q8k<W, true>(a, lds, L, wave, xv) : stage_planes<W>(a, lds, L, kQ4_K);
+    const bool ok = a.x ? stage_q8k<W, kBsQuarters>(a, lds, L, wave, xv) : stage_planes<W>(a, lds, L, T);
     if (!ok) return;
 
     const uint32_t g = kq >> 1, h = kq & 1;
@@ -628,19 +689,29 @@ __global__ __launch_bounds__(W * 64) void q4k_mv_small_kernel(MvArgs a) {
 #pragma unroll
     for (int b = 0; b < B; ++b) acc[b] = 0.0f;
     uint32_t ti = 0, tile = t0, blk = kp, j = 0;
-    auto compute = [&](const Q4Step& cur) {
+    auto compute = [&](const Q4Step<T>& cur) {
         const Q4Scales q = q4k_scales(cur.h);
         const int32_t s0 = __builtin_amdgcn_ubfe(q.scA, 16 * g, 8), s1 = __builtin_amdgcn_ubfe(q.scA, 16 * g + 8, 8);
         const int32_t s4 = __builtin_amdgcn_ubfe(q.scB, 16 * g, 8), s5 = __builtin_amdgcn_ubfe(q.scB, 16 * g + 8, 8);
         const int32_t m0 = __builtin_amdgcn_ubfe(q.mnA, 16 * g, 8), m1 = __builtin_amdgcn_ubfe(q.mnA, 16 * g + 8, 8);
         const int32_t m4 = __builtin_amdgcn_ubfe(q.mnB, 16 * g, 8), m5 = __builtin_amdgcn_ubfe(q.mnB, 16 * g + 8, 8);
-        const uint32_t l0[4] = {cur.w0.x & 0x0f0f0f0fu, cur.w0.y & 0x0f0f0f0fu, cur.w0.z & 0x0f0f0f0fu,
-                                cur.w0.w & 0x0f0f0f0fu};
+        uint32_t l0[4] = {cur.w0.x & 0x0f0f0f0fu, cur.w0.y & 0x0f0f0f0fu, cur.w0.z & 0x0f0f0f0fu,
+                          cur.w0.w & 0x0f0f0f0fu};
         uint32_t h0[4], h1[4];
         hi_nibbles64(cur.w0, h0);
-        const uint32_t l1[4] = {cur.w1.x & 0x0f0f0f0fu, cur.w1.y & 0x0f0f0f0fu, cur.w1.z & 0x0f0f0f0fu,
-                                cur.w1.w & 0x0f0f0f0fu};
+        uint32_t l1[4] = {cur.w1.x & 0x0f0f0f0fu, cur.w1.y & 0x0f0f0f0fu, cur.w1.z & 0x0f0f0f0fu,
+                          cur.w1.w & 0x0f0f0f0fu};
         hi_nibbles64(cur.w1, h1);
+        if constexpr (T == kQ5_K) {
+            const Q5High hb = q5_high(cur.qh, kq);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                l0[i] |= hb.l0[i];
+                h0[i] |= hb.h0[i];
+                l1[i] |= hb.l1[i];
+                h1[i] |= hb.h1[i];
+            }
+        }
         const float dw = half_to_float(cur.h.x), dmw = half_to_float(cur.h.x >> 16);
 #pragma unroll
         for (int b = 0; b < B; ++b) {
@@ -771,7 +842,7 @@ __global__ __launch_bounds__(W * 64) void q6k_mv_kernel(MvArgs a) {
 #pragma unroll
     for (int i = 0; i < D; ++i) issue(buf[i]);
 
-    const bool ok = a.x ? stage_q8k<W, false>(a, lds, L, wave, xv) : stage_planes<W>(a, lds, L, kQ6_K);
+    const bool ok = a.x ? stage_q8k<W, kBsNone>(a, lds, L, wave, xv) : stage_planes<W>(a, lds, L, kQ6_K);
     if (!ok) return;
 
     // This lane's weights: ql bytes 32kq.. (g = kq/2, s1 = kq%2) give the
@@ -833,6 +904,187 @@ __global__ __launch_bounds__(W * 64) void q6k_mv_kernel(MvArgs a) {
         if (two_groups) {
             const int32_t I1 = group(a_ptr1 + blk * a_step1);
             acc1 += (dw * *(const float*)(lds + L.d_off + (blk * 8 + kq + 4) * 4)) * (float)I1;
+        }
+        if (++blk == nb) {
+            const uint32_t row = tile * kTileRows + n;
+            store_out(a, row, kq, acc0, best0);
+            store_out(a, row, kq + 4, acc1, best1);
+            acc0 = acc1 = 0.0f;
+            blk = 0;
+            tile += tw;
+        }
+    };
+    pipeline<D>(steps, buf, issue, compute);
+    publish_argmax(a, kq, best0);
+    publish_argmax(a, kq + 4, best1);
+}
+
+// ---------------------------------------------------------------------------
+// Q2_K and Q3_K: 16-element scale groups, two bits (+ a high-mask bit) per value
+// ---------------------------------------------------------------------------
+// Lane (n, kq) loads qs bytes 16kq .. +15 of row n: qs byte 32G + p (G = kq/2,
+// p = 16(kq%2) + i) holds element 128G + 32s + p in bits 2s..2s+1, s = 0..3.
+// MFMA s therefore gives this lane's B operand the 16 values of scale group
+// sg(kq, s) = 8G + 2s + kq%2 (elements 16 sg ..).  A row r = n holds column
+// r / 4 (+4 for the second column group) and is nonzero in K quarter r % 4
+// only, with the activations of sg(r % 4, s): output element t of MFMA s in
+// lane (n, kq) is the integer dot of weight row n with column kq over scale
+// group sg(t, s), so every lane holds whole block integers for its column.
+template <uint32_t T>
+struct K16Step;
+template <>
+struct K16Step<kQ3_K> {
+    uint4 q, hm;
+    uint3 sc;
+    uint32_t d;
+};
+template <>
+struct K16Step<kQ2_K> {
+    uint4 q, sc;
+    uint32_t dd;
+};
+
+// The sixteen Q3_K scales as signed bytes, sc[4k..4k+3] in word k
+// (matvec_extra.rs:200-210): low nibbles from bytes 0..7, two high bits from
+// bytes 8..11; q - 32 per byte without carries (+0x60, ^0x80).
+__device__ __forceinline__ void q3_scale_words(uint3 p, uint32_t (&c)[4]) {
+    c[0] = (p.x & 0x0f0f0f0fu) | ((p.z << 4) & 0x30303030u);
+    c[1] = (p.y & 0x0f0f0f0fu) | ((p.z << 2) & 0x30303030u);
+    c[2] = ((p.x >> 4) & 0x0f0f0f0fu) | (p.z & 0x30303030u);
+    c[3] = ((p.y >> 4) & 0x0f0f0f0fu) | ((p.z >> 2) & 0x30303030u);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) c[k] = (c[k] + 0x60606060u) ^ 0x80808080u;
+}
+
+// Q2_K mins of one column: the sum over the 16 groups of min * bsum
+// (matvec_extra.rs:183-185); bs = the column's 16 bsums of the block in LDS.
+__device__ __forceinline__ int32_t q2_mins(uint4 sc, const uint8_t* bs) {
+    const uint4 b0 = ((const uint4*)bs)[0], b1 = ((const uint4*)bs)[1];
+    const uint32_t m[4] = {(sc.x >> 4) & 0x0f0f0f0fu, (sc.y >> 4) & 0x0f0f0f0fu, (sc.z >> 4) & 0x0f0f0f0fu,
+                           (sc.w >> 4) & 0x0f0f0f0fu};
+    const uint32_t bw[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+    int32_t M = 0;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        M = dot2(__builtin_amdgcn_perm(0u, m[k], 0x0c010c00u), bw[2 * k], M);
+        M = dot2(__builtin_amdgcn_perm(0u, m[k], 0x0c030c02u), bw[2 * k + 1], M);
+    }
+    return M;
+}
+
+template <uint32_t T, int W, int D, bool DBG>
+__global__ __launch_bounds__(W * 64) void k16_mv_kernel(MvArgs a) {
+    constexpr uint32_t kChunk = T == kQ3_K ? kQ3KChunk : kQ2KChunk;
+    RLQ_MV_PROLOGUE(T, a.nb)
+    const uint32_t nb = a.nb;
+    K16Step<T> buf[D];
+    auto issue = [&](K16Step<T>& st) {
+        const uint8_t* base = a.w + ((uint64_t)ld_tile * nb + ld_chunk) * kChunk;
+        st.q = load_stream16(base + lane * 16);
+        if constexpr (T == kQ3_K) {
+            st.hm = load_stream16(base + 1024 + n * 32 + 16 * (kq & 1));
+            const uint32_t* sp = (const uint32_t*)(base + 1536 + n * 12);
+            st.sc = make_uint3(__builtin_nontemporal_load(sp), __builtin_nontemporal_load(sp + 1),
+                               __builtin_nontemporal_load(sp + 2));
+            st.d = __builtin_nontemporal_load((const uint16_t*)(base + 1728 + n * 2));
+        } else {
+            st.sc = load_stream16(base + 1024 + n * 16);
+            st.dd = __builtin_nontemporal_load((const uint32_t*)(base + 1280 + n * 4));
+        }
+        next_load();
+    };
+#pragma unroll
+    for (int i = 0; i < D; ++i) issue(buf[i]);
+
+    const bool ok = a.x ? stage_q8k<W, bsum_order(T)>(a, lds, L, wave, xv) : stage_planes<W>(a, lds, L, T);
+    if (!ok) return;
+
+    const uint32_t abl = n >> 2, which = n & 3;
+    const uint8_t* a_row = lds + abl * L.S + 128 * (which >> 1) + 16 * (which & 1);
+    const bool two_groups = a.batch > 4;
+    const bool a_live0 = which == kq && abl < a.batch;
+    const bool a_live1 = which == kq && abl + 4 < a.batch;
+    const uint8_t* a_ptr0 = a_live0 ? a_row : lds + L.zero_off;
+    const uint8_t* a_ptr1 = a_live1 ? a_row + 4 * L.S : lds + L.zero_off;
+    const uint32_t a_step0 = a_live0 ? 256 : 0, a_step1 = a_live1 ? 256 : 0;
+    const uint32_t hsh = 4 * (kq >> 1);  // Q3_K: hmask bit 4G + s
+
+    float acc0 = 0.0f, acc1 = 0.0f;
+    unsigned long long best0 = 0, best1 = 0;
+    uint32_t tile = gw, blk = 0;
+    auto compute = [&](const K16Step<T>& cur) {
+        // B operands of the four MFMAs and the sixteen scales as bytes
+        i32x4 wv[4];
+        uint32_t c[4];
+        if constexpr (T == kQ3_K) {
+            const uint32_t q[4] = {cur.q.x, cur.q.y, cur.q.z, cur.q.w};
+            const uint32_t hm[4] = {cur.hm.x >> hsh, cur.hm.y >> hsh, cur.hm.z >> hsh, cur.hm.w >> hsh};
+#pragma unroll
+            for (int sft = 0; sft < 4; ++sft)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    // low | hbit << 2 in 0..7, minus 4 per byte (+0x7c, ^0x80):
+                    // q = low - (hbit ? 0 : 4)  (matvec_extra.rs:240-244)
+                    const uint32_t hb = sft < 3 ? hm[i] << (2 - sft) : hm[i] >> 1;
+                    const uint32_t v = ((q[i] >> (2 * sft)) & 0x03030303u) | (hb & 0x04040404u);
+                    wv[sft][i] = (int)((v + 0x7c7c7c7cu) ^ 0x80808080u);
+                }
+            q3_scale_words(cur.sc, c);
+        } else {
+            const uint32_t q[4] = {cur.q.x, cur.q.y, cur.q.z, cur.q.w};
+#pragma unroll
+            for (int sft = 0; sft < 4; ++sft)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) wv[sft][i] = (int)((q[i] >> (2 * sft)) & 0x03030303u);
+            c[0] = cur.sc.x & 0x0f0f0f0fu, c[1] = cur.sc.y & 0x0f0f0f0fu;
+            c[2] = cur.sc.z & 0x0f0f0f0fu, c[3] = cur.sc.w & 0x0f0f0f0fu;
+        }
+        auto scale = [&](uint32_t word, int byte) -> int32_t {
+            return T == kQ3_K ? sbyte(word, byte) : (int32_t)ubyte(word, byte);
+        };
+        // integer dot of one column group: sg(t, s) = 8(t/2) + 2s + t%2 is
+        // byte 2(s%2) + t%2 of scale word 2(t/2) + s/2
+        auto group = [&](const uint8_t* p) {
+            int32_t I = 0;
+#pragma unroll
+            for (int sft = 0; sft < 4; ++sft) {
+                const i32x4 av = *(const i32x4*)(p + 32 * sft);
+                const i32x4 dv = mfma_i8(av, wv[sft]);
+                const int bl = 2 * (sft & 1), wl = sft >> 1;
+                I = mad24(scale(c[wl], bl), dv[0], I);
+                I = mad24(scale(c[wl], bl + 1), dv[1], I);
+                I = mad24(scale(c[2 + wl], bl), dv[2], I);
+                I = mad24(scale(c[2 + wl], bl + 1), dv[3], I);
+            }
+            return I;
+        };
+        const float da0 = *(const float*)(lds + L.d_off + (blk * 8 + kq) * 4);
+        const int32_t I0 = group(a_ptr0 + blk * a_step0);
+        int32_t M0 = 0;
+        if constexpr (T == kQ3_K) {
+            acc0 += (half_to_float(cur.d) * da0) * (float)I0;
+        } else {
+            // sum += d * isum - mn * mins with d = y.d * d_w, mn = y.d * dmin_w
+            // (matvec_extra.rs:193-195), in block order
+            M0 = kq < a.batch ? q2_mins(cur.sc, lds + L.bs_off + (blk * 8 + kq) * 32) : 0;
+            acc0 += (da0 * half_to_float(cur.dd)) * (float)I0 - (da0 * half_to_float(cur.dd >> 16)) * (float)M0;
+        }
+        if (DBG && kq == 0) {
+            const uint32_t row = tile * kTileRows + n;
+            if (row < a.rows) {
+                a.dbg_isum[(uint64_t)row * nb + blk] = I0;
+                a.dbg_imin[(uint64_t)row * nb + blk] = M0;
+            }
+        }
+        if (two_groups) {
+            const float da1 = *(const float*)(lds + L.d_off + (blk * 8 + kq + 4) * 4);
+            const int32_t I1 = group(a_ptr1 + blk * a_step1);
+            if constexpr (T == kQ3_K) {
+                acc1 += (half_to_float(cur.d) * da1) * (float)I1;
+            } else {
+                const int32_t M1 = kq + 4 < a.batch ? q2_mins(cur.sc, lds + L.bs_off + (blk * 8 + kq + 4) * 32) : 0;
+                acc1 += (da1 * half_to_float(cur.dd)) * (float)I1 - (da1 * half_to_float(cur.dd >> 16)) * (float)M1;
+            }
         }
         if (++blk == nb) {
             const uint32_t row = tile * kTileRows + n;
@@ -964,7 +1216,7 @@ static hipError_t launch_one(K kernel, const MvArgs& a, size_t lds, hipStream_t 
 // KS waves, about kSmallWgPerCu workgroups per CU.
 constexpr int kSmallW = 8, kSmallKS = 8, kSmallD = 2, kSmallWgPerCu = 2;
 
-template <int W, int KS, int D, int B, bool DBG>
+template <uint32_t T, int W, int KS, int D, int B, bool DBG>
 static hipError_t launch_small(const MvArgs& a, hipStream_t s) {
     constexpr int TS = W / KS;
     const uint32_t want = (a.ntiles + TS - 1) / TS;
@@ -975,13 +1227,31 @@ static hipError_t launch_small(const MvArgs& a, hipStream_t s) {
     if (lds > kMaxLds) return hipErrorInvalidValue;
     static size_t lds_set = 64 * 1024;
     if (lds > lds_set) {
-        const hipError_t e = hipFuncSetAttribute((const void*)q4k_mv_small_kernel<W, KS, D, B, DBG>,
+        const hipError_t e = hipFuncSetAttribute((const void*)q4k_mv_small_kernel<T, W, KS, D, B, DBG>,
                                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
         if (e != hipSuccess) return e;
         lds_set = lds;
     }
-    hipLaunchKernelGGL((q4k_mv_small_kernel<W, KS, D, B, DBG>), dim3(grid), dim3(W * 64), lds, s, a);
+    hipLaunchKernelGGL((q4k_mv_small_kernel<T, W, KS, D, B, DBG>), dim3(grid), dim3(W * 64), lds, s, a);
     return hipGetLastError();
+}
+
+// Q4_K / Q5_K: the VALU kernel for one or two columns, MFMA above.
+template <uint32_t T>
+static hipError_t launch_q45(const MvArgs& a, uint32_t nbat, bool dbg, uint32_t epilogue, size_t lds, hipStream_t s) {
+    // two tile slots per workgroup (a K split of four): the SiLU pair
+    // epilogue's gate and up tiles, and small matrices of at most 4096
+    // columns and 512 tiles (measured: 6144x4096 runs 1 us faster)
+    if (epilogue == kEpSiluPair || (nbat == 1 && !dbg && a.nb <= 16 && a.ntiles <= 512))
+        return launch_small<T, kSmallW, kSmallW / 2, kSmallD, 1, false>(a, s);
+    if (nbat == 1)
+        return dbg ? launch_small<T, kSmallW, kSmallKS, kSmallD, 1, true>(a, s)
+                   : launch_small<T, kSmallW, kSmallKS, kSmallD, 1, false>(a, s);
+    if (nbat == 2)
+        return dbg ? launch_small<T, kSmallW, kSmallKS, kSmallD, 2, true>(a, s)
+                   : launch_small<T, kSmallW, kSmallKS, kSmallD, 2, false>(a, s);
+    return dbg ? launch_one(q4k_mv_kernel<T, kMvWaves, 8, true>, a, lds, s)
+               : launch_one(q4k_mv_kernel<T, kMvWaves, 8, false>, a, lds, s);
 }
 
 hipError_t launch_matvec(uint32_t wtype, const uint8_t* w, uint64_t rows, uint64_t cols, const float* x,
@@ -1005,10 +1275,10 @@ hipError_t launch_matvec_ex(uint32_t wtype, const uint8_t* w, uint64_t rows, uin
     if (ex.xform != kXfNone && (batch != 1 || !x || wtype == kQ8_0 || ex.xform > kXfSiluMul ||
                                 (ex.xform == kXfRmsNorm && !ex.norm_w)))
         return hipErrorInvalidValue;
-    // the SiLU pair epilogue: one Q4_K column, whole tile pairs, no argmax or residual
+    // the SiLU pair epilogue: one Q4_K / Q5_K column, whole tile pairs, no argmax or residual
     if (ex.epilogue != kEpStore &&
-        (ex.epilogue != kEpSiluPair || batch != 1 || wtype != kQ4_K || rows % (2 * kTileRows) != 0 || argmax_key ||
-         ex.resid || dbg_isum))
+        (ex.epilogue != kEpSiluPair || batch != 1 || (wtype != kQ4_K && wtype != kQ5_K) ||
+         rows % (2 * kTileRows) != 0 || argmax_key || ex.resid || dbg_isum))
         return hipErrorInvalidValue;
     uint64_t b0 = 0;
     while (b0 < batch) {
@@ -1047,20 +1317,15 @@ hipError_t launch_matvec_ex(uint32_t wtype, const uint8_t* w, uint64_t rows, uin
         constexpr int W = kMvWaves;
         const bool dbg = a.dbg_isum != nullptr;
         if (wtype == kQ4_K) {
-            // two tile slots per workgroup (a K split of four): the SiLU pair
-            // epilogue's gate and up tiles, and small matrices of at most 4096
-            // columns and 512 tiles (measured: 6144x4096 runs 1 us faster)
-            if (ex.epilogue == kEpSiluPair || (nbat == 1 && !dbg && a.nb <= 16 && a.ntiles <= 512))
-                e = launch_small<kSmallW, kSmallW / 2, kSmallD, 1, false>(a, s);
-            else if (nbat == 1)
-                e = dbg ? launch_small<kSmallW, kSmallKS, kSmallD, 1, true>(a, s)
-                        : launch_small<kSmallW, kSmallKS, kSmallD, 1, false>(a, s);
-            else if (nbat == 2)
-                e = dbg ? launch_small<kSmallW, kSmallKS, kSmallD, 2, true>(a, s)
-                        : launch_small<kSmallW, kSmallKS, kSmallD, 2, false>(a, s);
-            else
-                e = dbg ? launch_one(q4k_mv_kernel<W, 8, true>, a, lds, s)
-                        : launch_one(q4k_mv_kernel<W, 8, false>, a, lds, s);
+            e = launch_q45<kQ4_K>(a, nbat, dbg, ex.epilogue, lds, s);
+        } else if (wtype == kQ5_K) {
+            e = launch_q45<kQ5_K>(a, nbat, dbg, ex.epilogue, lds, s);
+        } else if (wtype == kQ3_K) {
+            e = dbg ? launch_one(k16_mv_kernel<kQ3_K, W, 4, true>, a, lds, s)
+                    : launch_one(k16_mv_kernel<kQ3_K, W, 4, false>, a, lds, s);
+        } else if (wtype == kQ2_K) {
+            e = dbg ? launch_one(k16_mv_kernel<kQ2_K, W, 4, true>, a, lds, s)
+                    : launch_one(k16_mv_kernel<kQ2_K, W, 4, false>, a, lds, s);
         } else if (wtype == kQ6_K) {
             e = dbg ? launch_one(q6k_mv_kernel<W, 4, true>, a, lds, s)
                     : launch_one(q6k_mv_kernel<W, 4, false>, a, lds, s);

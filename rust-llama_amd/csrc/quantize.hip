@@ -629,8 +629,9 @@ __global__ __launch_bounds__(256) void dequantize_kernel(uint32_t t, const uint8
             float d;
             __builtin_memcpy(&d, b, 4);
             v = d * (float)(int8_t)b[4 + i % 256];
-        } else if (t == kQ4_K) {  // decode.rs:216-235
-            const uint8_t* b = src + (i / 256) * 144;
+        } else if (t == kQ4_K || t == kQ5_K) {  // decode.rs:216-235 (Q5_K: + 16 from qh)
+            const bool five = t == kQ5_K;
+            const uint8_t* b = src + (i / 256) * (five ? 176 : 144);
             const int e = (int)(i % 256), group = e / 64, side = (e % 64) / 32, j = e % 32;
             const int sub = group * 2 + side;
             const uint8_t* p = b + 4;
@@ -644,8 +645,24 @@ __global__ __launch_bounds__(256) void dequantize_kernel(uint32_t t, const uint8
             }
             const float dl = half_at(b, 0) * (float)sc;
             const float ml = half_at(b, 2) * (float)m;
-            const uint8_t q = (b[16 + group * 32 + j] >> (side * 4)) & 15;
+            uint8_t q = (b[(five ? 48 : 16) + group * 32 + j] >> (side * 4)) & 15;
+            if (five && ((b[16 + j] >> sub) & 1)) q += 16;
             v = dl * (float)q - ml;
+        } else if (t == kQ2_K) {  // decode.rs:159-175
+            const uint8_t* b = src + (i / 256) * 84;
+            const int e = (int)(i % 256), group = e / 128, lane = (e % 128) / 32, pos = e % 32;
+            const uint8_t sc = b[group * 8 + lane * 2 + pos / 16];
+            const float dl = half_at(b, 80) * (float)(sc & 15), ml = half_at(b, 82) * (float)(sc >> 4);
+            v = dl * (float)((b[16 + group * 32 + pos] >> (2 * lane)) & 3) - ml;
+        } else if (t == kQ3_K) {  // decode.rs:177-202
+            const uint8_t* b = src + (i / 256) * 110;
+            const int e = (int)(i % 256), group = e / 128, lane = (e % 128) / 32, pos = e % 32;
+            const int k = group * 8 + lane * 2 + pos / 16, j = k % 4;  // scale index k = 4 * (k / 4) + j
+            const uint8_t* p = b + 96;
+            const int lo = k < 8 ? p[(k / 4) * 4 + j] & 15 : p[(k / 4 - 2) * 4 + j] >> 4;
+            const int sc = lo | (((p[8 + j] >> (2 * (k / 4))) & 3) << 4);
+            const int q = ((b[32 + group * 32 + pos] >> (2 * lane)) & 3) - (((b[pos] >> (group * 4 + lane)) & 1) ? 0 : 4);
+            v = half_at(b, 108) * (float)(sc - 32) * (float)q;
         } else {  // Q6_K, decode.rs:237-258
             const uint8_t* b = src + (i / 256) * 210;
             const int e = (int)(i % 256), group = e / 128, side = (e % 128) / 32, j = e % 32;
@@ -693,7 +710,8 @@ hipError_t launch_repack(uint32_t t, const uint8_t* gguf, uint64_t rows, uint64_
     hipLaunchKernelGGL(fill_zero16_kernel, dim3(2048), dim3(256), 0, s, (uint4*)dev, n16);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    const uint32_t bs = t == kQ8_0 ? 32 : 256, ts = t == kQ8_0 ? 34 : (t == kQ4_K ? 144 : 210);
+    const uint32_t bs = t == kQ8_0 ? 32 : 256;
+    const uint32_t ts = t == kQ8_0 ? 34 : t == kQ2_K ? 84 : t == kQ3_K ? 110 : t == kQ4_K ? 144 : t == kQ5_K ? 176 : 210;
     hipLaunchKernelGGL(repack_tiled_kernel, dim3(8192), dim3(256), 0, s, t, gguf, rows, cols / bs, ts, dev);
     return hipGetLastError();
 }

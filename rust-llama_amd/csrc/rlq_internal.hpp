@@ -10,7 +10,7 @@
 
 namespace rlq {
 
-enum DTypeId : uint32_t { kQ8_0 = 8, kQ4_K = 12, kQ6_K = 14, kQ8_K = 15 };
+enum DTypeId : uint32_t { kQ8_0 = 8, kQ2_K = 10, kQ3_K = 11, kQ4_K = 12, kQ5_K = 13, kQ6_K = 14, kQ8_K = 15 };
 
 // Activations of `batch` columns in structure-of-arrays form on the device:
 //   q    int8  [batch][cols]

@@ -18,6 +18,20 @@
 //   [2048 + n*64, +64)    qh[64] of row n
 //   [3072 + n*16, +16)    scales[16] of row n
 //   [3328 + n*2, +2)      d of row n
+// Q5_K, chunk of 2816 B per (tile, block): the Q4_K pieces plus qh
+//   [P*1024 + l*16, +16)  qs bytes 32g + 16h .. +15 of row n (GGUF bytes 48..)
+//                         with the Q4_K mapping of P, g, h
+//   [2048 + n*32, +32)    qh[32] of row n (GGUF bytes 16..47)
+//   [2560 + n*16, +16)    d, dmin, scales[12] of row n (GGUF bytes 0..15)
+// Q3_K, chunk of 1760 B per (tile, block):
+//   [l*16, +16)           qs bytes 16kq .. +15 of row n (GGUF bytes 32..95)
+//   [1024 + n*32, +32)    hmask[32] of row n (GGUF bytes 0..31)
+//   [1536 + n*12, +12)    scales[12] of row n (GGUF bytes 96..107)
+//   [1728 + n*2, +2)      d of row n (GGUF bytes 108..109)
+// Q2_K, chunk of 1344 B per (tile, block):
+//   [l*16, +16)           qs bytes 16kq .. +15 of row n (GGUF bytes 16..79)
+//   [1024 + n*16, +16)    scales[16] of row n (GGUF bytes 0..15)
+//   [1280 + n*4, +4)      d, dmin of row n (GGUF bytes 80..83)
 // Q8_0, chunk of 1088 B per (tile, block pair p):
 //   [l*16, +16)           qs bytes 16(kq%2) .. +15 of block 2p + kq/2, row n
 //   [1024 + n*4, +4)      d of blocks 2p and 2p+1 of row n (a missing
@@ -33,6 +47,9 @@ constexpr uint32_t kTileRows = 16;
 constexpr uint32_t kQ4KChunk = 2304;
 constexpr uint32_t kQ6KChunk = 3360;
 constexpr uint32_t kQ80Chunk = 1088;
+constexpr uint32_t kQ5KChunk = 2816;
+constexpr uint32_t kQ3KChunk = 1760;
+constexpr uint32_t kQ2KChunk = 1344;
 
 __host__ __device__ inline uint64_t layout_tiles(uint64_t rows) { return (rows + kTileRows - 1) / kTileRows; }
 
@@ -41,7 +58,14 @@ __host__ __device__ inline uint64_t layout_chunks_per_tile(uint32_t t, uint64_t 
     return t == 8 ? (cols / 32 + 1) / 2 : cols / 256;
 }
 __host__ __device__ inline uint64_t layout_chunk_bytes(uint32_t t) {
-    return t == 12 ? kQ4KChunk : (t == 14 ? kQ6KChunk : kQ80Chunk);
+    switch (t) {
+        case 10: return kQ2KChunk;
+        case 11: return kQ3KChunk;
+        case 12: return kQ4KChunk;
+        case 13: return kQ5KChunk;
+        case 14: return kQ6KChunk;
+        default: return kQ80Chunk;
+    }
 }
 __host__ __device__ inline uint64_t layout_bytes(uint32_t t, uint64_t rows, uint64_t cols) {
     return layout_tiles(rows) * layout_chunks_per_tile(t, cols) * layout_chunk_bytes(t);
@@ -59,6 +83,33 @@ __host__ __device__ inline uint64_t layout_offset(uint32_t t, uint64_t row, uint
         const uint32_t q = byte - 16, g = q / 32, j = q % 32, h = j / 16, i = j % 16;
         const uint32_t P = g / 2, kq = 2 * (g % 2) + h;
         return base + P * 1024 + (16 * kq + n) * 16 + i;
+    }
+    if (t == 13) {
+        const uint64_t base = (tile * nb + blk) * kQ5KChunk;
+        if (byte < 16) return base + 2560 + n * 16 + byte;
+        if (byte < 48) return base + 2048 + n * 32 + (byte - 16);
+        const uint32_t q = byte - 48, g = q / 32, j = q % 32, h = j / 16, i = j % 16;
+        const uint32_t P = g / 2, kq = 2 * (g % 2) + h;
+        return base + P * 1024 + (16 * kq + n) * 16 + i;
+    }
+    if (t == 11) {
+        const uint64_t base = (tile * nb + blk) * kQ3KChunk;
+        if (byte < 32) return base + 1024 + n * 32 + byte;
+        if (byte < 96) {
+            const uint32_t q = byte - 32;
+            return base + (16 * (q / 16) + n) * 16 + q % 16;
+        }
+        if (byte < 108) return base + 1536 + n * 12 + (byte - 96);
+        return base + 1728 + n * 2 + (byte - 108);
+    }
+    if (t == 10) {
+        const uint64_t base = (tile * nb + blk) * kQ2KChunk;
+        if (byte < 16) return base + 1024 + n * 16 + byte;
+        if (byte < 80) {
+            const uint32_t q = byte - 16;
+            return base + (16 * (q / 16) + n) * 16 + q % 16;
+        }
+        return base + 1280 + n * 4 + (byte - 80);
     }
     if (t == 14) {
         const uint64_t base = (tile * nb + blk) * kQ6KChunk;
