@@ -5,8 +5,9 @@
  * crates/quant; public surface crates/quant/src/lib.rs:36-41) and its two
  * callers, model-runtime `Matrix::multiply` (crates/model-runtime/src/math.rs:144-169)
  * and the GGML MUL_MAT op (crates/tensor/src/cpu_extra.rs:756-873).  Weight
- * formats Q8_0 (id 8), Q4_K (12) and Q6_K (14); activations are quantized to
- * Q8_0 / Q8_K (15) on the GPU, exactly as the reference's quantizers.
+ * formats Q8_0 (id 8) and the K formats Q2_K (10), Q3_K (11), Q4_K (12),
+ * Q5_K (13), Q6_K (14); activations are quantized to Q8_0 / Q8_K (15) on the
+ * GPU, exactly as the reference's quantizers.
  *
  * Conventions
  *   - Plain pointers and sizes.  Sizes are u64 (the reference's usize).
@@ -43,7 +44,9 @@ extern "C" {
 /* GGML numeric type ids on the path (crates/quant/src/lib.rs:132-169).  Any
  * id of that enum is accepted where a dtype is taken; ids outside the path
  * return RLQ_UNIMPLEMENTED after the reference's own checks. */
-enum rlq_dtype { RLQ_Q8_0 = 8, RLQ_Q4_K = 12, RLQ_Q6_K = 14, RLQ_Q8_K = 15 };
+enum rlq_dtype {
+    RLQ_Q8_0 = 8, RLQ_Q2_K = 10, RLQ_Q3_K = 11, RLQ_Q4_K = 12, RLQ_Q5_K = 13, RLQ_Q6_K = 14, RLQ_Q8_K = 15
+};
 
 typedef enum rlq_status {
     RLQ_OK = 0,
@@ -97,11 +100,13 @@ int32_t rlq_matvec_activation_dtype(uint32_t weights_type, uint32_t *out, rlq_er
 
 /* quantize_into (crates/quant/src/encode.rs:37-100): Q8_0 / Q8_K activation
  * quantizers and the Q4_K / Q6_K / Q8_0 weight encoders
- * (crates/quant/src/encode_k.rs:11-33, 430-561), run on the GPU. */
+ * (crates/quant/src/encode_k.rs:11-33, 430-561), run on the GPU.  The Q2_K,
+ * Q3_K and Q5_K encoders return RLQ_UNIMPLEMENTED (weights arrive encoded). */
 int32_t rlq_quantize_into(uint32_t dtype, const float *values, uint64_t n, uint8_t *out, uint64_t out_len,
                           rlq_error *err);
 
-/* dequantize_into (crates/quant/src/lib.rs:299-308; decode.rs). */
+/* dequantize_into (crates/quant/src/lib.rs:299-308; decode.rs): Q8_0, Q8_K
+ * and Q2_K..Q6_K. */
 int32_t rlq_dequantize_into(uint32_t dtype, const uint8_t *bytes, uint64_t len, float *out, uint64_t n,
                             rlq_error *err);
 
@@ -173,9 +178,9 @@ int32_t rlq_sync(rlq_context *ctx, void *stream, rlq_error *err);
  * batch <= 8), computed inside the kernel rlq_matmul runs for that batch size
  * (the columns are quantized on the GPU as rlq_matmul does):
  * isum[r*nb + k] and imin[r*nb + k] for block k are the integers of
- * crates/quant/src/matvec_extra.rs:252-283 (the eight lanes added; imin is
- * the Q4_K mins sum, 0 otherwise) and matvec.rs:124-127.  isum and imin are
- * device pointers of rows*nb i32. */
+ * crates/quant/src/matvec_extra.rs:174-283 (the eight lanes added; imin is
+ * the mins sum of Q2_K, Q4_K and Q5_K, 0 otherwise) and matvec.rs:124-127.
+ * isum and imin are device pointers of rows*nb i32. */
 int32_t rlq_block_sums(rlq_context *ctx, const rlq_weights *w, const float *x, uint64_t batch, int32_t *isum,
                        int32_t *imin, void *stream, rlq_error *err);
 

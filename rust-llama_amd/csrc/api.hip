@@ -584,7 +584,7 @@ int32_t rlq_llama_intermediates(const rlq_llama* m, float* qkv, float* attention
     const hipStream_t s = (hipStream_t)stream;
     if (qkv) HIP_TRY(hipMemcpyAsync(qkv, m->m.qkv, (d.width + 2 * kvw) * 4, hipMemcpyDeviceToDevice, s));
     if (attention) HIP_TRY(hipMemcpyAsync(attention, m->m.att, d.width * 4, hipMemcpyDeviceToDevice, s));
-    if (ffn) HIP_TRY(hipMemcpyAsync(ffn, m->m.gu, d.feed_forward * 4, hipMemcpyDeviceToDevice, s));
+    if (ffn) HIP_TRY(m->m.ffn_activation(ffn, s));
     return ok(err);
 }
 

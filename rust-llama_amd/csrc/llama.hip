@@ -317,6 +317,23 @@ __global__ __launch_bounds__(kAttnThreads) void attn_pv_kernel(
 
 // RMSNorm of one row (math.rs:214-228) for the step's embedding output: one
 // workgroup, the squares summed in f64 by one thread in index order.
+// silu(g) * u of [g | u] (llama.rs:367-371), for the inspection of a step
+// whose down projection combined them in its quantizer.
+__global__ __launch_bounds__(256) void silu_mul_kernel(const float* __restrict__ gu, uint32_t n,
+                                                       float* __restrict__ out) {
+    for (uint32_t i = blockIdx.x * 256 + threadIdx.x; i < n; i += gridDim.x * 256) {
+        const float g = gu[i];
+        out[i] = (g / (1.0f + sse2_exp(0.0f - g))) * gu[n + i];
+    }
+}
+
+hipError_t LlamaModel::ffn_activation(float* out, hipStream_t s) const {
+    const uint32_t F = (uint32_t)d.feed_forward;
+    if (fused_ffn()) return hipMemcpyAsync(out, gu, F * sizeof(float), hipMemcpyDeviceToDevice, s);
+    hipLaunchKernelGGL(silu_mul_kernel, dim3((F + 255) / 256), dim3(256), 0, s, gu, F, out);
+    return hipGetLastError();
+}
+
 __global__ __launch_bounds__(256) void rms_norm_row_kernel(const float* __restrict__ x, const float* __restrict__ w,
                                                            uint32_t n, float eps, float* __restrict__ out,
                                                            unsigned long long* __restrict__ err_word) {
@@ -339,11 +356,23 @@ __global__ __launch_bounds__(256) void rms_norm_row_kernel(const float* __restri
 
 namespace {
 
+uint64_t gguf_row_bytes(uint32_t t, uint64_t cols) {
+    switch (t) {
+        case kQ8_0: return cols / 32 * 34;
+        case kQ2_K: return cols / 256 * 84;
+        case kQ3_K: return cols / 256 * 110;
+        case kQ4_K: return cols / 256 * 144;
+        case kQ5_K: return cols / 256 * 176;
+        case kQ6_K: return cols / 256 * 210;
+        default: return 0;
+    }
+}
+
 hipError_t upload_tiled(uint32_t t, const void* gguf, uint64_t rows, uint64_t cols, bool on_device, uint8_t* dst,
                         void* staging, hipStream_t s) {
     const uint8_t* src = (const uint8_t*)gguf;
     if (!on_device) {
-        const uint64_t len = rows * (cols / (t == kQ8_0 ? 32 : 256)) * (t == kQ8_0 ? 34 : (t == kQ4_K ? 144 : 210));
+        const uint64_t len = rows * gguf_row_bytes(t, cols);
         const hipError_t e = hipMemcpyAsync(staging, src, len, hipMemcpyHostToDevice, s);
         if (e != hipSuccess) return e;
         src = (const uint8_t*)staging;
@@ -358,15 +387,6 @@ hipError_t upload_f32(const float* src, uint64_t n, bool on_device, float** dst,
     if (e != hipSuccess) return e;
     return hipMemcpyAsync(*dst, src, n * sizeof(float), on_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice,
                           s);
-}
-
-uint64_t gguf_row_bytes(uint32_t t, uint64_t cols) {
-    switch (t) {
-        case kQ8_0: return cols / 32 * 34;
-        case kQ4_K: return cols / 256 * 144;
-        case kQ6_K: return cols / 256 * 210;
-        default: return 0;
-    }
 }
 
 }  // namespace
@@ -442,7 +462,7 @@ hipError_t LlamaModel::create(const LlamaDims& dims, const LlamaHostTensors& t, 
     }
     const uint32_t wt = d.weight_type;
     uint8_t* gu_stage = nullptr;
-    if (e == hipSuccess) e = hipMalloc((void**)&gu_stage, 2 * layout_bytes(wt, F, W));
+    if (e == hipSuccess && fused_ffn()) e = hipMalloc((void**)&gu_stage, 2 * layout_bytes(wt, F, W));
     auto tiled = [&](const void* src, uint64_t rows, uint64_t cols, uint8_t* dst) {
         return upload_tiled(wt, src, rows, cols, t.on_device, dst, staging, s);
     };
@@ -457,12 +477,19 @@ hipError_t LlamaModel::create(const LlamaDims& dims, const LlamaHostTensors& t, 
         if (e == hipSuccess) e = tiled(hl.value, kvw, W, L.wqkv + bq + bk);
         if (e == hipSuccess) e = hipMalloc((void**)&L.wo, layout_bytes(wt, W, W));
         if (e == hipSuccess) e = tiled(hl.attention_output, W, W, L.wo);
-        // gate and up tiles interleaved (tile 2i = gate tile i, 2i + 1 = up
-        // tile i), so one workgroup holds both halves of silu(gate) * up
+        // Q4_K / Q5_K: gate and up tiles interleaved (tile 2i = gate tile i,
+        // 2i + 1 = up tile i), so one workgroup holds both halves of
+        // silu(gate) * up; other types: [gate; up], whose product [g | u]
+        // the down projection's quantizer combines
         if (e == hipSuccess) e = hipMalloc((void**)&L.wgu, 2 * bg);
-        if (e == hipSuccess) e = tiled(hl.gate, F, W, gu_stage);
-        if (e == hipSuccess) e = tiled(hl.up, F, W, gu_stage + bg);
-        if (e == hipSuccess) {
+        if (e == hipSuccess && !fused_ffn()) {
+            e = tiled(hl.gate, F, W, L.wgu);
+            if (e == hipSuccess) e = tiled(hl.up, F, W, L.wgu + bg);
+        } else if (e == hipSuccess) {
+            e = tiled(hl.gate, F, W, gu_stage);
+            if (e == hipSuccess) e = tiled(hl.up, F, W, gu_stage + bg);
+        }
+        if (e == hipSuccess && fused_ffn()) {
             const uint64_t tb = bg / (F / kTileRows);  // bytes of one tile
             e = hipMemcpy2DAsync(L.wgu, 2 * tb, gu_stage, tb, tb, F / kTileRows, hipMemcpyDeviceToDevice, s);
             if (e == hipSuccess)
@@ -529,13 +556,16 @@ hipError_t LlamaModel::step(float* hidden, uint64_t position, float* embedding_o
         res.resid = hidden;
         e = launch_matvec_ex(wt, L.wo, W, W, att, nullptr, 1, hidden, W, nullptr, err_word, nullptr, nullptr, res, s);
         if (e != hipSuccess) break;
-        MvExtra norm2;  // gate/up with the FFN norm; the epilogue leaves silu(gate) * up in gu
-        norm2.xform = 1, norm2.eps = d.rms_epsilon, norm2.norm_w = L.ffn_norm, norm2.epilogue = 1;
+        // gate/up with the FFN norm: the fused epilogue leaves silu(gate) * up
+        // in gu, the plain one [gate | up] for the down projection to combine
+        MvExtra norm2;
+        norm2.xform = 1, norm2.eps = d.rms_epsilon, norm2.norm_w = L.ffn_norm, norm2.epilogue = fused_ffn() ? 1 : 0;
         e = launch_matvec_ex(wt, L.wgu, 2 * F, W, hidden, nullptr, 1, gu, 2 * F, nullptr, err_word, nullptr, nullptr,
                              norm2, s);
         if (e != hipSuccess) break;
         MvExtra down;
         down.resid = hidden;
+        if (!fused_ffn()) down.xform = 2;
         e = launch_matvec_ex(wt, L.wdown, W, F, gu, nullptr, 1, hidden, W, nullptr, err_word, nullptr, nullptr, down,
                              s);
     }

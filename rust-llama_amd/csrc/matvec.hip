@@ -238,6 +238,22 @@ __device__ __forceinline__ float rms_scale(const MvArgs& a, uint8_t* lds, const 
     return 1.0f / sqrtf((float)(total / (double)a.cols) + a.eps);
 }
 
+// The input transform of the decode step, applied to the 16 values of unit u
+// (element e0 of the launch's single column) before they are quantized.
+__device__ __forceinline__ void apply_xform(const MvArgs& a, uint32_t e0, float scale, float (&v)[16]) {
+    if (a.xform == kXfRmsNorm) {
+        float w[16];
+        load16(a.norm_w + e0, w);
+#pragma unroll
+        for (int k = 0; k < 16; ++k) v[k] = v[k] * scale * w[k];
+    } else if (a.xform == kXfSiluMul) {
+        float up[16];
+        load16(a.x + a.cols + e0, up);
+#pragma unroll
+        for (int k = 0; k < 16; ++k) v[k] = (v[k] / (1.0f + sse2_exp(0.0f - v[k]))) * up[k];
+    }
+}
+
 // Q8_K of all batch columns into LDS.  A 16-lane row quantizes one 256-value
 // block, 16 values per lane (one bsum group per lane).  Returns false in
 // every thread when any block of any column is invalid.
@@ -265,17 +281,7 @@ __device__ __forceinline__ bool stage_q8k(const MvArgs& a, uint8_t* lds, const L
         } else {
             load_unit(a, u, v);
         }
-        if (a.xform == kXfRmsNorm) {
-            float w[16];
-            load16(a.norm_w + e0, w);
-#pragma unroll
-            for (int k = 0; k < 16; ++k) v[k] = v[k] * scale * w[k];
-        } else if (a.xform == kXfSiluMul) {
-            float up[16];
-            load16(a.x + K + e0, up);
-#pragma unroll
-            for (int k = 0; k < 16; ++k) v[k] = (v[k] / (1.0f + sse2_exp(0.0f - v[k]))) * up[k];
-        }
+        apply_xform(a, e0, scale, v);
         const Q8KRow o = q8k_row16(v, r16);
         if (o.kind >= 0) {
             bad = 1;
@@ -298,6 +304,14 @@ __device__ __forceinline__ bool stage_q8_0(const MvArgs& a, uint8_t* lds, const 
     const uint32_t K = a.cols, upc = K / 16, units = upc * a.batch;
     const uint32_t lane = threadIdx.x & 63;
     int bad = 0;
+    float scale = 1.0f;
+    if (a.xform == kXfRmsNorm) {
+        scale = rms_scale<W>(a, lds, L, wave, v0);
+        if (!(scale <= 3.402823466e38f) || !(scale > 0.0f)) {  // math.rs:218-220
+            bad = 1;
+            if (threadIdx.x == 0) report_error(a.err_word, error_key(a.err_column0, kKindNonFinite, 0));
+        }
+    }
     for (uint32_t base = wave * 64; base < units; base += W * 64) {
         const uint32_t u = base + lane;
         if (u >= units) continue;  // lane pairs drop out together (units is even)
@@ -309,6 +323,7 @@ __device__ __forceinline__ bool stage_q8_0(const MvArgs& a, uint8_t* lds, const 
         } else {
             load_unit(a, u, v);
         }
+        apply_xform(a, e0, scale, v);
         uint32_t nf = 0xffffffffu;
 #pragma unroll
         for (int k = 15; k >= 0; --k)
@@ -1270,10 +1285,9 @@ hipError_t launch_matvec_ex(uint32_t wtype, const uint8_t* w, uint64_t rows, uin
     if (rows == 0 || cols == 0 || cols % bs != 0 || rows > 0xffffffffull - kTileRows || cols > (1u << 30))
         return hipErrorInvalidValue;
     if (dbg_isum && batch > 8) return hipErrorInvalidValue;
-    // the transforms read one f32 column (RMSNorm weights, or [gate | up]) and
-    // exist only in the Q8_K quantizer
-    if (ex.xform != kXfNone && (batch != 1 || !x || wtype == kQ8_0 || ex.xform > kXfSiluMul ||
-                                (ex.xform == kXfRmsNorm && !ex.norm_w)))
+    // the transforms read one f32 column (RMSNorm weights, or [gate | up])
+    if (ex.xform != kXfNone &&
+        (batch != 1 || !x || ex.xform > kXfSiluMul || (ex.xform == kXfRmsNorm && !ex.norm_w)))
         return hipErrorInvalidValue;
     // the SiLU pair epilogue: one Q4_K / Q5_K column, whole tile pairs, no argmax or residual
     if (ex.epilogue != kEpStore &&

@@ -142,6 +142,10 @@ struct LlamaModel {
     ~LlamaModel();
     hipError_t create(const LlamaDims& dims, const LlamaHostTensors& t, hipStream_t s);
     hipError_t embedding(uint32_t token, float* hidden, hipStream_t s) const;
+    // Q4_K / Q5_K layers: silu(gate) * up in the gate/up matvec epilogue
+    bool fused_ffn() const { return d.weight_type == kQ4_K || d.weight_type == kQ5_K; }
+    // silu(gate) * up of the last step (feed_forward floats, device)
+    hipError_t ffn_activation(float* out, hipStream_t s) const;
     // One step at `position` appending KV row n_cached: hidden (width, device)
     // in/out; embedding_out (width), logits (vocab) and argmax (1) may be null.
     hipError_t step(float* hidden, uint64_t position, float* embedding_out, float* logits, uint32_t* argmax,

@@ -68,9 +68,10 @@ def host(x):
     return x.detach().cpu().numpy()
 
 
-def test_embedding_rows_exact(ctx):
-    say("llama embedding rows, 0 layers")
-    cfg, t, g, o = models(ctx, 0, 21)
+@pytest.mark.parametrize("et", [O.Q4_K, O.Q8_0, O.Q2_K, O.Q3_K, O.Q5_K, O.Q6_K])
+def test_embedding_rows_exact(ctx, et):
+    say("llama embedding rows, 0 layers, embedding type", et)
+    cfg, t, g, o = models(ctx, 0, 21, embedding_type=et)
     for tok in (0, 1, 499, 999):
         assert np.array_equal(host(g.embedding(tok)), o.embedding(tok)), tok
     with pytest.raises(rlq.QuantError) as e:
@@ -78,10 +79,12 @@ def test_embedding_rows_exact(ctx):
     assert e.value.name == "InvalidToken"
 
 
-def test_output_head_without_layers(ctx):
-    """RMSNorm fused into the Q6_K output matvec; the fused greedy argmax."""
-    say("llama step, 0 layers: final norm + output matvec + argmax")
-    cfg, t, g, o = models(ctx, 0, 22)
+@pytest.mark.parametrize("ot", [O.Q6_K, O.Q8_0, O.Q4_K, O.Q5_K])
+def test_output_head_without_layers(ctx, ot):
+    """RMSNorm fused into the output matvec's quantizer (Q8_K, or Q8_0 for
+    Q8_0 weights); the fused greedy argmax."""
+    say("llama step, 0 layers: final norm + output matvec + argmax, output type", ot)
+    cfg, t, g, o = models(ctx, 0, 22, output_type=ot)
     for tok, pos in ((3, 0), (77, 1), (998, 2)):
         h = g.embedding(tok)
         emb, logits, am = g.step(h, pos, embedding=True, logits=True, argmax=True)
@@ -93,14 +96,17 @@ def test_output_head_without_layers(ctx):
         assert int(host(am)[0]) == int(np.argmax(lg))
 
 
-def test_one_layer_parts(ctx):
+@pytest.mark.parametrize("wt", [O.Q4_K, O.Q5_K, O.Q6_K, O.Q8_0, O.Q3_K, O.Q2_K])
+def test_one_layer_parts(ctx, wt):
     """Each part of one layer against the oracle fed with the GPU's own
     intermediates, over several steps (the cache grows past 64 rows: two
-    attention chunks)."""
-    say("llama 1 layer, parts, 70 steps")
-    cfg, t, g, o = models(ctx, 1, 23)
+    attention chunks).  Q4_K / Q5_K layers run silu(gate) * up in the gate/up
+    epilogue, the other types in the down projection's quantizer; Q8_0
+    layers quantize their activations to Q8_0."""
+    say("llama 1 layer, parts, 70 steps, layer type", wt)
+    cfg, t, g, o = models(ctx, 1, 23, weight_type=wt)
     L = t["layers"][0]
-    W, kvw, hd, F, wt = cfg.width, cfg.kv_width, cfg.head_dim, cfg.feed_forward, cfg.weight_type
+    W, kvw, hd, F = cfg.width, cfg.kv_width, cfg.head_dim, cfg.feed_forward
     scale = np.float32(1.0) / np.sqrt(np.float32(hd))
     kc = np.zeros((cfg.max_context, kvw), np.float32)
     vc = np.zeros_like(kc)
@@ -143,9 +149,10 @@ def test_one_layer_parts(ctx):
     print("worst relative L2 per part:", worst)
 
 
-def test_free_running_steps(ctx):
-    say("llama 2 layers, 12 free-running steps, logits vs oracle")
-    cfg, t, g, o = models(ctx, 2, 24)
+@pytest.mark.parametrize("wt,ot", [(O.Q4_K, O.Q6_K), (O.Q6_K, O.Q8_0)])
+def test_free_running_steps(ctx, wt, ot):
+    say("llama 2 layers, 12 free-running steps, logits vs oracle, types", wt, ot)
+    cfg, t, g, o = models(ctx, 2, 24, weight_type=wt, output_type=ot)
     rng = np.random.default_rng(6)
     worst = 0.0
     for step in range(12):
