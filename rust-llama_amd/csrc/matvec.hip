@@ -987,6 +987,107 @@ __device__ __forceinline__ int32_t q2_mins(uint4 sc, const uint8_t* bs) {
     return M;
 }
 
+// Loads of one chunk (rlq_layout.hpp): this lane's qs piece, the row's high
+// mask half (Q3_K), scales and super-scales.
+template <uint32_t T>
+__device__ __forceinline__ void k16_issue(K16Step<T>& st, const uint8_t* base, uint32_t lane, uint32_t n,
+                                          uint32_t kq) {
+    st.q = load_stream16(base + lane * 16);
+    if constexpr (T == kQ3_K) {
+        st.hm = load_stream16(base + 1024 + n * 32 + 16 * (kq & 1));
+        const uint32_t* sp = (const uint32_t*)(base + 1536 + n * 12);
+        st.sc = make_uint3(__builtin_nontemporal_load(sp), __builtin_nontemporal_load(sp + 1),
+                           __builtin_nontemporal_load(sp + 2));
+        st.d = __builtin_nontemporal_load((const uint16_t*)(base + 1728 + n * 2));
+    } else {
+        st.sc = load_stream16(base + 1024 + n * 16);
+        st.dd = __builtin_nontemporal_load((const uint32_t*)(base + 1280 + n * 4));
+    }
+}
+
+// The B operands of the four MFMAs of one chunk and the sixteen scales as
+// bytes (hsh = 4 * (kq / 2), the lane's high-mask bit offset).
+template <uint32_t T>
+struct K16Ops {
+    i32x4 wv[4];
+    uint32_t c[4];
+};
+template <uint32_t T>
+__device__ __forceinline__ K16Ops<T> k16_ops(const K16Step<T>& cur, uint32_t hsh) {
+    K16Ops<T> o;
+    const uint32_t q[4] = {cur.q.x, cur.q.y, cur.q.z, cur.q.w};
+    if constexpr (T == kQ3_K) {
+        const uint32_t hm[4] = {cur.hm.x >> hsh, cur.hm.y >> hsh, cur.hm.z >> hsh, cur.hm.w >> hsh};
+#pragma unroll
+        for (int sft = 0; sft < 4; ++sft)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                // low | hbit << 2 in 0..7, minus 4 per byte (+0x7c, ^0x80):
+                // q = low - (hbit ? 0 : 4)  (matvec_extra.rs:240-244)
+                const uint32_t hb = sft < 3 ? hm[i] << (2 - sft) : hm[i] >> 1;
+                const uint32_t v = ((q[i] >> (2 * sft)) & 0x03030303u) | (hb & 0x04040404u);
+                o.wv[sft][i] = (int)((v + 0x7c7c7c7cu) ^ 0x80808080u);
+            }
+        q3_scale_words(cur.sc, o.c);
+    } else {
+#pragma unroll
+        for (int sft = 0; sft < 4; ++sft)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) o.wv[sft][i] = (int)((q[i] >> (2 * sft)) & 0x03030303u);
+        o.c[0] = cur.sc.x & 0x0f0f0f0fu, o.c[1] = cur.sc.y & 0x0f0f0f0fu;
+        o.c[2] = cur.sc.z & 0x0f0f0f0fu, o.c[3] = cur.sc.w & 0x0f0f0f0fu;
+    }
+    return o;
+}
+
+// Integer dot of one column group (A rows from p): sg(t, s) = 8(t/2) + 2s +
+// t%2 is byte 2(s%2) + t%2 of scale word 2(t/2) + s/2.
+template <uint32_t T>
+__device__ __forceinline__ int32_t k16_isum(const K16Ops<T>& o, const uint8_t* p) {
+    auto scale = [&](uint32_t word, int byte) -> int32_t {
+        return T == kQ3_K ? sbyte(word, byte) : (int32_t)ubyte(word, byte);
+    };
+    int32_t I = 0;
+#pragma unroll
+    for (int sft = 0; sft < 4; ++sft) {
+        const i32x4 av = *(const i32x4*)(p + 32 * sft);
+        const i32x4 dv = mfma_i8(av, o.wv[sft]);
+        const int bl = 2 * (sft & 1), wl = sft >> 1;
+        I = mad24(scale(o.c[wl], bl), dv[0], I);
+        I = mad24(scale(o.c[wl], bl + 1), dv[1], I);
+        I = mad24(scale(o.c[2 + wl], bl), dv[2], I);
+        I = mad24(scale(o.c[2 + wl], bl + 1), dv[3], I);
+    }
+    return I;
+}
+
+// The f32 term one block adds for column `col` (da = its activation scale):
+// Q3_K d * isum with d = f16(d) * y.d; Q2_K d * isum - mn * mins with
+// d = y.d * f16(d), mn = y.d * f16(dmin) (matvec_extra.rs:193-195, 246).
+template <uint32_t T>
+__device__ __forceinline__ float k16_term(const K16Step<T>& cur, float da, int32_t I, int32_t M) {
+    if constexpr (T == kQ3_K) {
+        return (half_to_float(cur.d) * da) * (float)I;
+    } else {
+        return (da * half_to_float(cur.dd)) * (float)I - (da * half_to_float(cur.dd >> 16)) * (float)M;
+    }
+}
+
+// A-operand setup shared by the two kernels: A row r = n holds column r / 4
+// (+4 for the second group), nonzero in K quarter r % 4 only.
+struct K16A {
+    const uint8_t *p0, *p1;
+    uint32_t step0, step1;
+};
+__device__ __forceinline__ K16A k16_a(const uint8_t* lds, const LdsMap& L, uint32_t batch, uint32_t n, uint32_t kq) {
+    const uint32_t abl = n >> 2, which = n & 3;
+    const uint8_t* a_row = lds + abl * L.S + 128 * (which >> 1) + 16 * (which & 1);
+    const bool live0 = which == kq && abl < batch, live1 = which == kq && abl + 4 < batch;
+    return K16A{live0 ? a_row : lds + L.zero_off, live1 ? a_row + 4 * L.S : lds + L.zero_off, live0 ? 256u : 0u,
+                live1 ? 256u : 0u};
+}
+
+// One wave per tile: every lane adds its column's block terms in block order.
 template <uint32_t T, int W, int D, bool DBG>
 __global__ __launch_bounds__(W * 64) void k16_mv_kernel(MvArgs a) {
     constexpr uint32_t kChunk = T == kQ3_K ? kQ3KChunk : kQ2KChunk;
@@ -994,18 +1095,7 @@ __global__ __launch_bounds__(W * 64) void k16_mv_kernel(MvArgs a) {
     const uint32_t nb = a.nb;
     K16Step<T> buf[D];
     auto issue = [&](K16Step<T>& st) {
-        const uint8_t* base = a.w + ((uint64_t)ld_tile * nb + ld_chunk) * kChunk;
-        st.q = load_stream16(base + lane * 16);
-        if constexpr (T == kQ3_K) {
-            st.hm = load_stream16(base + 1024 + n * 32 + 16 * (kq & 1));
-            const uint32_t* sp = (const uint32_t*)(base + 1536 + n * 12);
-            st.sc = make_uint3(__builtin_nontemporal_load(sp), __builtin_nontemporal_load(sp + 1),
-                               __builtin_nontemporal_load(sp + 2));
-            st.d = __builtin_nontemporal_load((const uint16_t*)(base + 1728 + n * 2));
-        } else {
-            st.sc = load_stream16(base + 1024 + n * 16);
-            st.dd = __builtin_nontemporal_load((const uint32_t*)(base + 1280 + n * 4));
-        }
+        k16_issue<T>(st, a.w + ((uint64_t)ld_tile * nb + ld_chunk) * kChunk, lane, n, kq);
         next_load();
     };
 #pragma unroll
@@ -1014,76 +1104,20 @@ __global__ __launch_bounds__(W * 64) void k16_mv_kernel(MvArgs a) {
     const bool ok = a.x ? stage_q8k<W, bsum_order(T)>(a, lds, L, wave, xv) : stage_planes<W>(a, lds, L, T);
     if (!ok) return;
 
-    const uint32_t abl = n >> 2, which = n & 3;
-    const uint8_t* a_row = lds + abl * L.S + 128 * (which >> 1) + 16 * (which & 1);
+    const K16A A = k16_a(lds, L, a.batch, n, kq);
     const bool two_groups = a.batch > 4;
-    const bool a_live0 = which == kq && abl < a.batch;
-    const bool a_live1 = which == kq && abl + 4 < a.batch;
-    const uint8_t* a_ptr0 = a_live0 ? a_row : lds + L.zero_off;
-    const uint8_t* a_ptr1 = a_live1 ? a_row + 4 * L.S : lds + L.zero_off;
-    const uint32_t a_step0 = a_live0 ? 256 : 0, a_step1 = a_live1 ? 256 : 0;
-    const uint32_t hsh = 4 * (kq >> 1);  // Q3_K: hmask bit 4G + s
+    const uint32_t hsh = 4 * (kq >> 1);
 
     float acc0 = 0.0f, acc1 = 0.0f;
     unsigned long long best0 = 0, best1 = 0;
     uint32_t tile = gw, blk = 0;
     auto compute = [&](const K16Step<T>& cur) {
-        // B operands of the four MFMAs and the sixteen scales as bytes
-        i32x4 wv[4];
-        uint32_t c[4];
-        if constexpr (T == kQ3_K) {
-            const uint32_t q[4] = {cur.q.x, cur.q.y, cur.q.z, cur.q.w};
-            const uint32_t hm[4] = {cur.hm.x >> hsh, cur.hm.y >> hsh, cur.hm.z >> hsh, cur.hm.w >> hsh};
-#pragma unroll
-            for (int sft = 0; sft < 4; ++sft)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    // low | hbit << 2 in 0..7, minus 4 per byte (+0x7c, ^0x80):
-                    // q = low - (hbit ? 0 : 4)  (matvec_extra.rs:240-244)
-                    const uint32_t hb = sft < 3 ? hm[i] << (2 - sft) : hm[i] >> 1;
-                    const uint32_t v = ((q[i] >> (2 * sft)) & 0x03030303u) | (hb & 0x04040404u);
-                    wv[sft][i] = (int)((v + 0x7c7c7c7cu) ^ 0x80808080u);
-                }
-            q3_scale_words(cur.sc, c);
-        } else {
-            const uint32_t q[4] = {cur.q.x, cur.q.y, cur.q.z, cur.q.w};
-#pragma unroll
-            for (int sft = 0; sft < 4; ++sft)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) wv[sft][i] = (int)((q[i] >> (2 * sft)) & 0x03030303u);
-            c[0] = cur.sc.x & 0x0f0f0f0fu, c[1] = cur.sc.y & 0x0f0f0f0fu;
-            c[2] = cur.sc.z & 0x0f0f0f0fu, c[3] = cur.sc.w & 0x0f0f0f0fu;
-        }
-        auto scale = [&](uint32_t word, int byte) -> int32_t {
-            return T == kQ3_K ? sbyte(word, byte) : (int32_t)ubyte(word, byte);
-        };
-        // integer dot of one column group: sg(t, s) = 8(t/2) + 2s + t%2 is
-        // byte 2(s%2) + t%2 of scale word 2(t/2) + s/2
-        auto group = [&](const uint8_t* p) {
-            int32_t I = 0;
-#pragma unroll
-            for (int sft = 0; sft < 4; ++sft) {
-                const i32x4 av = *(const i32x4*)(p + 32 * sft);
-                const i32x4 dv = mfma_i8(av, wv[sft]);
-                const int bl = 2 * (sft & 1), wl = sft >> 1;
-                I = mad24(scale(c[wl], bl), dv[0], I);
-                I = mad24(scale(c[wl], bl + 1), dv[1], I);
-                I = mad24(scale(c[2 + wl], bl), dv[2], I);
-                I = mad24(scale(c[2 + wl], bl + 1), dv[3], I);
-            }
-            return I;
-        };
+        const K16Ops<T> o = k16_ops<T>(cur, hsh);
         const float da0 = *(const float*)(lds + L.d_off + (blk * 8 + kq) * 4);
-        const int32_t I0 = group(a_ptr0 + blk * a_step0);
+        const int32_t I0 = k16_isum<T>(o, A.p0 + blk * A.step0);
         int32_t M0 = 0;
-        if constexpr (T == kQ3_K) {
-            acc0 += (half_to_float(cur.d) * da0) * (float)I0;
-        } else {
-            // sum += d * isum - mn * mins with d = y.d * d_w, mn = y.d * dmin_w
-            // (matvec_extra.rs:193-195), in block order
-            M0 = kq < a.batch ? q2_mins(cur.sc, lds + L.bs_off + (blk * 8 + kq) * 32) : 0;
-            acc0 += (da0 * half_to_float(cur.dd)) * (float)I0 - (da0 * half_to_float(cur.dd >> 16)) * (float)M0;
-        }
+        if constexpr (T == kQ2_K) M0 = kq < a.batch ? q2_mins(cur.sc, lds + L.bs_off + (blk * 8 + kq) * 32) : 0;
+        acc0 += k16_term<T>(cur, da0, I0, M0);
         if (DBG && kq == 0) {
             const uint32_t row = tile * kTileRows + n;
             if (row < a.rows) {
@@ -1093,13 +1127,11 @@ __global__ __launch_bounds__(W * 64) void k16_mv_kernel(MvArgs a) {
         }
         if (two_groups) {
             const float da1 = *(const float*)(lds + L.d_off + (blk * 8 + kq + 4) * 4);
-            const int32_t I1 = group(a_ptr1 + blk * a_step1);
-            if constexpr (T == kQ3_K) {
-                acc1 += (half_to_float(cur.d) * da1) * (float)I1;
-            } else {
-                const int32_t M1 = kq + 4 < a.batch ? q2_mins(cur.sc, lds + L.bs_off + (blk * 8 + kq + 4) * 32) : 0;
-                acc1 += (da1 * half_to_float(cur.dd)) * (float)I1 - (da1 * half_to_float(cur.dd >> 16)) * (float)M1;
-            }
+            const int32_t I1 = k16_isum<T>(o, A.p1 + blk * A.step1);
+            int32_t M1 = 0;
+            if constexpr (T == kQ2_K)
+                M1 = kq + 4 < a.batch ? q2_mins(cur.sc, lds + L.bs_off + (blk * 8 + kq + 4) * 32) : 0;
+            acc1 += k16_term<T>(cur, da1, I1, M1);
         }
         if (++blk == nb) {
             const uint32_t row = tile * kTileRows + n;
@@ -1113,6 +1145,121 @@ __global__ __launch_bounds__(W * 64) void k16_mv_kernel(MvArgs a) {
     pipeline<D>(steps, buf, issue, compute);
     publish_argmax(a, kq, best0);
     publish_argmax(a, kq + 4, best1);
+}
+
+// K split over KS waves per tile (TS = W / KS tile slots per workgroup), for
+// matrices with too few tiles to fill the chip one wave per tile.  Each wave
+// takes blocks kp, kp + KS, ... of its slot's tiles and parks every block's
+// f32 term per (row, column) in LDS; after the last tile the workgroup adds
+// each row's terms in block order from 0, which is the reference's own
+// sequence for Q2_K.  LDS: the activation image, then the terms
+// [tmax * TS][nb][16][batch] f32.
+__host__ __device__ inline uint32_t k16_part_off(uint32_t t, uint32_t cols, uint32_t batch) {
+    return (lds_map(t, cols, batch).total + 15u) & ~15u;
+}
+
+template <uint32_t T, int W, int KS, int D, bool DBG>
+__global__ __launch_bounds__(W * 64) void k16_mv_split_kernel(MvArgs a) {
+    constexpr int TS = W / KS;
+    constexpr uint32_t kChunk = T == kQ3_K ? kQ3KChunk : kQ2KChunk;
+    extern __shared__ __align__(16) uint8_t lds[];
+    const LdsMap L = lds_map(T, a.cols, a.batch);
+    float* part = (float*)(lds + k16_part_off(T, a.cols, a.batch));
+    const uint32_t lane = threadIdx.x & 63, n = lane & 15, kq = lane >> 4;
+    // wave-uniform indices in scalar registers: loop control stays on the SALU
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t ts = wave / KS, kp = wave % KS;
+    const uint32_t nb = a.nb, ntiles = a.ntiles, batch = a.batch;
+    const uint32_t tstride = gridDim.x * TS, t0 = blockIdx.x * TS + ts;
+    const uint32_t tmax = (ntiles + tstride - 1) / tstride;
+    const uint32_t my_tiles = t0 < ntiles ? (ntiles - 1 - t0) / tstride + 1 : 0;
+    const uint32_t bpt = kp < nb ? (nb - 1 - kp) / KS + 1 : 0;  // blocks of each tile this wave takes
+    const uint32_t steps = my_tiles * bpt;
+
+    if (threadIdx.x < 16) *(uint4*)(lds + L.zero_off + threadIdx.x * 16) = make_uint4(0, 0, 0, 0);
+    float xv[16];
+    prefetch_unit(a, wave, xv);
+
+    // loads run D steps ahead; past the wave's last step they repeat a valid chunk
+    const uint32_t kp0 = kp < nb ? kp : nb - 1;
+    uint32_t ld_tile = t0 < ntiles ? t0 : ntiles - 1, ld_blk = kp0;
+    K16Step<T> buf[D];
+    auto issue = [&](K16Step<T>& st) {
+        k16_issue<T>(st, a.w + ((uint64_t)ld_tile * nb + ld_blk) * kChunk, lane, n, kq);
+        ld_blk += KS;
+        if (ld_blk >= nb) {
+            ld_blk = kp0;
+            if (ld_tile + tstride < ntiles) ld_tile += tstride;
+        }
+    };
+#pragma unroll
+    for (int i = 0; i < D; ++i) issue(buf[i]);
+
+    const bool ok = a.x ? stage_q8k<W, bsum_order(T)>(a, lds, L, wave, xv) : stage_planes<W>(a, lds, L, T);
+    if (!ok) return;
+
+    const K16A A = k16_a(lds, L, batch, n, kq);
+    const bool two_groups = batch > 4;
+    const uint32_t hsh = 4 * (kq >> 1);
+    uint32_t ti = 0, tile = t0, blk = kp, j = 0;
+    auto compute = [&](const K16Step<T>& cur) {
+        const K16Ops<T> o = k16_ops<T>(cur, hsh);
+        float* pt = part + ((uint64_t)((ti * TS + ts) * nb + blk) * 16 + n) * batch;
+        const int32_t I0 = k16_isum<T>(o, A.p0 + blk * A.step0);
+        int32_t M0 = 0;
+        if (kq < batch) {
+            if constexpr (T == kQ2_K) M0 = q2_mins(cur.sc, lds + L.bs_off + (blk * 8 + kq) * 32);
+            pt[kq] = k16_term<T>(cur, *(const float*)(lds + L.d_off + (blk * 8 + kq) * 4), I0, M0);
+        }
+        if (DBG && kq == 0) {
+            const uint32_t row = tile * kTileRows + n;
+            if (row < a.rows) {
+                a.dbg_isum[(uint64_t)row * nb + blk] = I0;
+                a.dbg_imin[(uint64_t)row * nb + blk] = M0;
+            }
+        }
+        if (two_groups) {
+            const int32_t I1 = k16_isum<T>(o, A.p1 + blk * A.step1);
+            if (kq + 4 < batch) {
+                int32_t M1 = 0;
+                if constexpr (T == kQ2_K) M1 = q2_mins(cur.sc, lds + L.bs_off + (blk * 8 + kq + 4) * 32);
+                pt[kq + 4] = k16_term<T>(cur, *(const float*)(lds + L.d_off + (blk * 8 + kq + 4) * 4), I1, M1);
+            }
+        }
+        blk += KS;
+        if (++j == bpt) {
+            j = 0;
+            blk = kp;
+            ++ti;
+            tile += tstride;
+        }
+    };
+    pipeline<D>(steps, buf, issue, compute);
+    __syncthreads();
+
+    // every parked (tile, row, column): its block terms added in block order
+    for (uint32_t b = 0; b < batch; ++b) {
+        unsigned long long best = 0;
+        for (uint32_t it = threadIdx.x; it < tmax * TS * 16; it += W * 64) {
+            const uint32_t r = it % 16, slot = it / 16, tsl = slot % TS, til = slot / TS;
+            const uint32_t t = blockIdx.x * TS + tsl + til * tstride;
+            const uint32_t row = t * kTileRows + r;
+            if (t < ntiles && row < a.rows) {
+                const float* pr = part + ((uint64_t)slot * nb * 16 + r) * batch + b;
+                float v = 0.0f;
+                for (uint32_t k = 0; k < nb; ++k) v += pr[(uint64_t)k * 16 * batch];
+                store_out(a, row, b, v, best);
+            }
+        }
+        if (a.argmax_key) {
+#pragma unroll
+            for (int m = 1; m < 64; m <<= 1) {
+                const unsigned long long o = __shfl_xor(best, m, 64);
+                best = o > best ? o : best;
+            }
+            if (lane == 0 && best) atomicMax(a.argmax_key + b, best);
+        }
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -1269,6 +1416,40 @@ static hipError_t launch_q45(const MvArgs& a, uint32_t nbat, bool dbg, uint32_t 
                : launch_one(q4k_mv_kernel<T, kMvWaves, 8, false>, a, lds, s);
 }
 
+// Q2_K / Q3_K: up to four columns the K-split kernel, while its parked terms
+// fit LDS next to the activations (matrices of up to about 2^17 rows at 4096
+// columns); one wave per tile otherwise (measured at 14336x4096: batch 1
+// 9.4 us split vs 11.3 us, batch 8 22.8 us vs 20.7 us).
+constexpr int kK16W = 8, kK16KS = 8, kK16D = 2;
+
+template <uint32_t T, bool DBG>
+static hipError_t launch_k16_split(const MvArgs& a, size_t lds, uint32_t grid, hipStream_t s) {
+    static size_t lds_set = 64 * 1024;
+    auto kernel = k16_mv_split_kernel<T, kK16W, kK16KS, kK16D, DBG>;
+    if (lds > lds_set) {
+        const hipError_t e = hipFuncSetAttribute((const void*)kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                 (int)lds);
+        if (e != hipSuccess) return e;
+        lds_set = lds;
+    }
+    hipLaunchKernelGGL(kernel, dim3(grid), dim3(kK16W * 64), lds, s, a);
+    return hipGetLastError();
+}
+
+template <uint32_t T>
+static hipError_t launch_k16(const MvArgs& a, bool dbg, size_t lds_plain, hipStream_t s) {
+    constexpr int TS = kK16W / kK16KS;
+    const uint32_t want = (a.ntiles + TS - 1) / TS;
+    const uint32_t cap = (uint32_t)kSmallWgPerCu * (uint32_t)device_cus();
+    const uint32_t grid = want < cap ? want : cap;
+    const uint64_t tstride = (uint64_t)grid * TS, tmax = (a.ntiles + tstride - 1) / tstride;
+    const uint64_t lds = k16_part_off(T, a.cols, a.batch) + tmax * TS * a.nb * 16ull * a.batch * 4ull;
+    if (a.batch <= 4 && lds <= kMaxLds)
+        return dbg ? launch_k16_split<T, true>(a, lds, grid, s) : launch_k16_split<T, false>(a, lds, grid, s);
+    return dbg ? launch_one(k16_mv_kernel<T, kMvWaves, 4, true>, a, lds_plain, s)
+               : launch_one(k16_mv_kernel<T, kMvWaves, 4, false>, a, lds_plain, s);
+}
+
 hipError_t launch_matvec(uint32_t wtype, const uint8_t* w, uint64_t rows, uint64_t cols, const float* x,
                          const ActPlanes* pre, uint64_t batch, float* y, uint64_t ldy,
                          unsigned long long* argmax_key, unsigned long long* err_word, int32_t* dbg_isum,
@@ -1335,11 +1516,9 @@ hipError_t launch_matvec_ex(uint32_t wtype, const uint8_t* w, uint64_t rows, uin
         } else if (wtype == kQ5_K) {
             e = launch_q45<kQ5_K>(a, nbat, dbg, ex.epilogue, lds, s);
         } else if (wtype == kQ3_K) {
-            e = dbg ? launch_one(k16_mv_kernel<kQ3_K, W, 4, true>, a, lds, s)
-                    : launch_one(k16_mv_kernel<kQ3_K, W, 4, false>, a, lds, s);
+            e = launch_k16<kQ3_K>(a, dbg, lds, s);
         } else if (wtype == kQ2_K) {
-            e = dbg ? launch_one(k16_mv_kernel<kQ2_K, W, 4, true>, a, lds, s)
-                    : launch_one(k16_mv_kernel<kQ2_K, W, 4, false>, a, lds, s);
+            e = launch_k16<kQ2_K>(a, dbg, lds, s);
         } else if (wtype == kQ6_K) {
             e = dbg ? launch_one(q6k_mv_kernel<W, 4, true>, a, lds, s)
                     : launch_one(q6k_mv_kernel<W, 4, false>, a, lds, s);
