@@ -16,7 +16,8 @@
  *     order (crates/quant/src/lib.rs:45-63) with the same payloads; 18..20 are
  *     this library's own; 21..23 stand for the model-runtime errors of the
  *     decode step (crates/model-runtime/src/lib.rs Error: InvalidConfig,
- *     InvalidToken, InvalidState).
+ *     InvalidToken, InvalidState); 24..26 for the tensor crate's errors of
+ *     MUL_MAT / MUL_MAT_ID (Shape, Bounds, Unsupported).
  *   - Validate before mutate: on any error, no output buffer is written
  *     (crates/quant/src/matvec.rs:31-56, encode.rs:37-100).
  *   - Host functions (`rlq_matvec`, `rlq_quantize_into`, ...) take host
@@ -72,7 +73,12 @@ typedef enum rlq_status {
     RLQ_INVALID_ARGUMENT = 20,          /* null pointer or handle */
     RLQ_INVALID_CONFIG = 21,            /* a = check (see rlq_llama_create) */
     RLQ_INVALID_TOKEN = 22,             /* a = token, b = vocabulary */
-    RLQ_INVALID_STATE = 23              /* a = KV rows held, b = max_context (cache full) */
+    RLQ_INVALID_STATE = 23,             /* a = KV rows held, b = max_context (cache full) */
+    /* TensorError variants of the GGML ops (crates/tensor/src/lib.rs:35-50) */
+    RLQ_TENSOR_SHAPE = 24,              /* Shape: incompatible MUL_MAT / MUL_MAT_ID dimensions */
+    RLQ_TENSOR_BOUNDS = 25,             /* Bounds: an expert id outside [-1, experts); a = its index */
+    RLQ_TENSOR_UNSUPPORTED = 26         /* Unsupported: a right-hand side neither F32 nor the
+                                           activation type; dtype = that type */
 } rlq_status;
 
 typedef struct rlq_error {
@@ -140,11 +146,23 @@ void *rlq_context_stream(rlq_context *ctx);
  * bytes on any stream is complete.  Returns after the copy is complete. */
 int32_t rlq_weights_create(rlq_context *ctx, uint32_t dtype, const void *bytes, uint64_t len, uint64_t rows,
                            uint64_t cols, int32_t bytes_on_device, rlq_weights **out, rlq_error *err);
+/* A stack of n2 x n3 matrices of rows x cols, a GGML weight tensor
+ * [cols, rows, n2, n3] (MUL_MAT broadcast sources, MUL_MAT_ID experts with
+ * n3 = 1): `bytes` holds the matrices' GGUF rows contiguously, matrix
+ * (i2, i3) at offset (i3 * n2 + i2) * rows * row_bytes (the reference's
+ * `contiguous()` layout, crates/tensor/src/cpu_extra.rs:788-790).  Each
+ * matrix is kept in the tiled layout.  rlq_weights_create is the n2 = n3 = 1
+ * case; rlq_matmul uses matrix (0, 0). */
+int32_t rlq_weights_create_stacked(rlq_context *ctx, uint32_t dtype, const void *bytes, uint64_t len,
+                                   uint64_t rows, uint64_t cols, uint64_t n2, uint64_t n3, int32_t bytes_on_device,
+                                   rlq_weights **out, rlq_error *err);
 /* Frees the device copy; it does not use the creating context, so weights may
  * be destroyed after their context. */
 void rlq_weights_destroy(rlq_weights *w);
 /* rows, cols, dtype of a weights handle (any output pointer may be null). */
 void rlq_weights_shape(const rlq_weights *w, uint64_t *rows, uint64_t *cols, uint32_t *dtype);
+/* n2, n3 of a weights handle (1, 1 for rlq_weights_create). */
+void rlq_weights_stack(const rlq_weights *w, uint64_t *n2, uint64_t *n3);
 
 /* MUL_MAT (crates/tensor/src/cpu_extra.rs:756-873) with an F32 right-hand
  * side, and Matrix::multiply for batch = 1: each of the `batch` input rows
@@ -160,6 +178,35 @@ int32_t rlq_matmul(rlq_context *ctx, const rlq_weights *w, const float *x, uint6
  * fused into the matvec epilogue: argmax[b] = index of the largest y[b*rows+r]. */
 int32_t rlq_matmul_argmax(rlq_context *ctx, const rlq_weights *w, const float *x, uint64_t batch, float *y,
                           uint32_t *argmax, void *stream, rlq_error *err);
+
+/* GGML MUL_MAT with batch broadcast (crates/tensor/src/cpu_extra.rs:756-873)
+ * over stacked weights W [cols, rows, w.n2, w.n3] and a right-hand side
+ * X [cols, ncols, n2, n3] (n2 % w.n2 == 0, n3 % w.n3 == 0):
+ *   y[((i3 * n2 + i2) * ncols + c) * rows + r] =
+ *       dot_packed(row r of W(i2 / (n2 / w.n2), i3 / (n3 / w.n3)), column c of X(i2, i3)).
+ * x_dtype is 0 (F32: every column is quantized to the weights' activation
+ * type, once) or that activation type itself (Q8_0 / Q8_K bytes, used as
+ * given).  x (16-byte aligned) and y are device pointers; rows of X are
+ * contiguous, column after column.  Errors, in the reference's order:
+ * RLQ_TENSOR_SHAPE (a = n2, b = n3), RLQ_TENSOR_UNSUPPORTED (x_dtype), then
+ * the quantizer's data errors at rlq_sync (b = the column's index
+ * (i3 * n2 + i2) * ncols + c).  A call with a data error writes no output. */
+int32_t rlq_mul_mat(rlq_context *ctx, const rlq_weights *w, uint32_t x_dtype, const void *x, uint64_t ncols,
+                    uint64_t n2, uint64_t n3, float *y, void *stream, rlq_error *err);
+
+/* GGML MUL_MAT_ID (crates/tensor/src/cpu_index.rs:169-236): experts W[e],
+ * e < w.n2 (w.n3 = 1), right-hand side X [cols, ncols, tokens] (x_dtype as
+ * for rlq_mul_mat), expert ids [slots, tokens] (i32, device, slots %
+ * ncols == 0):
+ *   y[(t * slots + s) * rows + r] = dot_packed(row r of W[ids[t * slots + s]],
+ *                                              column s % ncols of X(t)),
+ * and 0 where the id is -1.  Every column of X is quantized once before the
+ * expert products.  Errors: RLQ_TENSOR_SHAPE, RLQ_TENSOR_UNSUPPORTED at
+ * once; at rlq_sync RLQ_TENSOR_BOUNDS (an id < -1 or >= w.n2; a = its index
+ * t * slots + s) before any quantizer data error.  A call with an error
+ * writes no output. */
+int32_t rlq_mul_mat_id(rlq_context *ctx, const rlq_weights *w, uint32_t x_dtype, const void *x, uint64_t ncols,
+                       uint64_t tokens, const int32_t *ids, uint64_t slots, float *y, void *stream, rlq_error *err);
 
 /* Device quantize_into (crates/quant/src/encode.rs:37-100): the activation
  * quantizers (Q8_0, Q8_K) and the weight encoders (Q8_0, Q4_K, Q6_K), GGUF

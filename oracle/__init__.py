@@ -29,7 +29,10 @@ ERROR_NAMES = {
     14: "UnsupportedIntegerConversion", 15: "IntegerOutOfRange", 16: "NonFiniteInput",
     17: "UnrepresentableScale", 18: "DeviceError", 19: "Unimplemented", 20: "InvalidArgument",
     21: "InvalidConfig", 22: "InvalidToken", 23: "InvalidState",
+    24: "Shape", 25: "Bounds", 26: "Unsupported",
 }
+F32 = 0
+SHAPE, BOUNDS, UNSUPPORTED = 24, 25, 26
 
 
 class OracleError(Exception):
@@ -173,6 +176,88 @@ def matmul(dtype, w, rows, cols, x, threads=1):
     err = _Err()
     _check(lib().oracle_matmul(dtype, _ptr(w), w.size, rows, cols, _ptr(x), x.shape[0], _ptr(y),
                                threads, ctypes.byref(err)), err)
+    return y
+
+
+# ---- GGML MUL_MAT with broadcast and MUL_MAT_ID over quantized weights ------------
+# Loops over the C dot above; the error payloads add the failing column
+# (b) to the reference's QuantError, as the device API reports it.
+
+def _rhs_rows(at, x_dtype, x, cols, n):
+    """The n right-hand rows as activation bytes: packed rows as given, or
+    each f32 row quantized in order (cpu_extra.rs:815-822, cpu_index.rs:209-214)."""
+    arb = row_bytes(at, cols)
+    if x_dtype == at:
+        return np.ascontiguousarray(x, dtype=np.uint8).reshape(n, arb)
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(n, cols)
+    out = np.zeros((n, arb), np.uint8)
+    for c in range(n):
+        try:
+            out[c] = quantize(at, x[c])
+        except OracleError as e:
+            raise OracleError(e.code, e.dtype, e.a, c) from None
+    return out
+
+
+def mul_mat(wtype, w, rows, cols, wn2, wn3, x_dtype, x, ncols, n2, n3):
+    """crates/tensor/src/cpu_extra.rs:756-873 for quantized weights: w holds
+    wn3 x wn2 matrices of rows x cols (GGUF rows, contiguous), x the right-hand
+    side [n3][n2][ncols][cols] (f32, or rows of the activation type).
+    Returns y [n3][n2][ncols][rows] f32: y[i3,i2,c,r] = dot_packed(row r of
+    matrix (i2 / (n2/wn2), i3 / (n3/wn3)), column (i3, i2, c))."""
+    at = matvec_activation_dtype(wtype)                                    # :758
+    if cols == 0 or wn2 == 0 or wn3 == 0 or n2 % wn2 or n3 % wn3:          # :759-769
+        raise OracleError(SHAPE, wtype, n2, n3)
+    if x_dtype not in (F32, at):                                           # :779-784
+        raise OracleError(UNSUPPORTED, x_dtype, 0, 0)
+    n = ncols * n2 * n3
+    y = np.zeros((n3, n2, ncols, rows), np.float32)
+    if n == 0:
+        return y
+    right = _rhs_rows(at, x_dtype, x, cols, n)
+    rb = row_bytes(wtype, cols)
+    w = np.ascontiguousarray(w, dtype=np.uint8).reshape(wn3, wn2, rows, rb)
+    r2, r3 = n2 // wn2, n3 // wn3
+    for i3 in range(n3):                                                   # :811-869
+        for i2 in range(n2):
+            mat = w[i3 // r3, i2 // r2]
+            for c in range(ncols):
+                col = right[(i3 * n2 + i2) * ncols + c]
+                for r in range(rows):
+                    y[i3, i2, c, r] = dot_packed(wtype, mat[r], col, cols)
+    return y
+
+
+def mul_mat_id(wtype, w, rows, cols, experts, x_dtype, x, ncols, tokens, ids):
+    """crates/tensor/src/cpu_index.rs:169-236 for quantized experts: w holds
+    `experts` matrices of rows x cols, x [tokens][ncols][cols], ids
+    [tokens][slots] int32.  Returns y [tokens][slots][rows] f32 with
+    y[t,s] = expert ids[t,s] . column (t, s % ncols), zero for id -1."""
+    ids = np.ascontiguousarray(ids, dtype=np.int32).reshape(tokens, -1) if tokens else np.zeros((0, 0), np.int32)
+    slots = ids.shape[1]
+    at = matvec_activation_dtype(wtype)                                    # :173
+    if cols == 0 or experts == 0 or ncols == 0 or slots % ncols:           # :179-194
+        raise OracleError(SHAPE, wtype, slots, ncols)
+    if x_dtype not in (F32, at):                                           # :195-199
+        raise OracleError(UNSUPPORTED, x_dtype, 0, 0)
+    flat = ids.reshape(-1)
+    bad = np.nonzero((flat < -1) | (flat >= experts))[0]                   # :200-205
+    if bad.size:
+        raise OracleError(BOUNDS, wtype, int(bad[0]), 0)
+    y = np.zeros((tokens, slots, rows), np.float32)                       # :206-209
+    if y.size == 0:
+        return y
+    right = _rhs_rows(at, x_dtype, x, cols, tokens * ncols)               # :210-216
+    rb = row_bytes(wtype, cols)
+    w = np.ascontiguousarray(w, dtype=np.uint8).reshape(experts, rows, rb)
+    for t in range(tokens):                                                # :219-233
+        for s_ in range(slots):
+            e = int(ids[t, s_])
+            if e == -1:
+                continue
+            col = right[t * ncols + s_ % ncols]
+            for r in range(rows):
+                y[t, s_, r] = dot_packed(wtype, w[e, r], col, cols)
     return y
 
 

@@ -88,6 +88,7 @@ ERROR_NAMES = {
     14: "UnsupportedIntegerConversion", 15: "IntegerOutOfRange", 16: "NonFiniteInput",
     17: "UnrepresentableScale", 18: "DeviceError", 19: "Unimplemented", 20: "InvalidArgument",
     21: "InvalidConfig", 22: "InvalidToken", 23: "InvalidState",
+    24: "Shape", 25: "Bounds", 26: "Unsupported",
 }
 
 
@@ -137,8 +138,13 @@ SIGNATURES = {
     "rlq_context_destroy": ([_P], None),
     "rlq_context_stream": ([_P], _P),
     "rlq_weights_create": ([_P, _U32, _P, _U64, _U64, _U64, _I32, ctypes.POINTER(_P), _E], _I32),
+    "rlq_weights_create_stacked": ([_P, _U32, _P, _U64, _U64, _U64, _U64, _U64, _I32, ctypes.POINTER(_P), _E],
+                                   _I32),
     "rlq_weights_destroy": ([_P], None),
     "rlq_weights_shape": ([_P, ctypes.POINTER(_U64), ctypes.POINTER(_U64), ctypes.POINTER(_U32)], None),
+    "rlq_weights_stack": ([_P, ctypes.POINTER(_U64), ctypes.POINTER(_U64)], None),
+    "rlq_mul_mat": ([_P, _P, _U32, _P, _U64, _U64, _U64, _P, _P, _E], _I32),
+    "rlq_mul_mat_id": ([_P, _P, _U32, _P, _U64, _U64, _P, _U64, _P, _P, _E], _I32),
     "rlq_matmul": ([_P, _P, _P, _U64, _P, _P, _E], _I32),
     "rlq_matmul_argmax": ([_P, _P, _P, _U64, _P, _P, _P, _E], _I32),
     "rlq_quantize_device": ([_P, _U32, _P, _U64, _U64, _P, _P, _E], _I32),
@@ -339,6 +345,37 @@ class Context:
                                         _dev_ptr(out, torch.uint8), _stream_ptr(stream), ctypes.byref(err)), err)
         return out
 
+    def mul_mat(self, w, x, x_dtype=DType.F32, y=None, stream=None):
+        """GGML MUL_MAT with broadcast (cpu_extra.rs:756-873): w stacked
+        [w.n3][w.n2] matrices; x [n3, n2, ncols, cols] f32, or uint8 rows of the
+        activation type when x_dtype is it -> y [n3, n2, ncols, rows] f32."""
+        x_dtype = DType(x_dtype)
+        if x.dim() != 4:
+            raise ValueError("x must be [n3, n2, ncols, cols] (f32) or [n3, n2, ncols, row bytes] (uint8)")
+        n3, n2, ncols = x.shape[:3]
+        if y is None:
+            y = torch.empty((n3, n2, ncols, w.rows), dtype=torch.float32, device=x.device)
+        xp = _dev_ptr(x, x.dtype)  # the library checks x_dtype against the weights
+        err = _Err()
+        _check(_lib.rlq_mul_mat(self._h, w._h, int(x_dtype), xp, ncols, n2, n3, _dev_ptr(y, torch.float32),
+                                _stream_ptr(stream), ctypes.byref(err)), err)
+        return y
+
+    def mul_mat_id(self, w, x, ids, x_dtype=DType.F32, y=None, stream=None):
+        """GGML MUL_MAT_ID (cpu_index.rs:169-236): experts w [w.n2 matrices],
+        x [tokens, ncols, cols] f32 (or activation bytes), ids [tokens, slots]
+        int32 on the GPU -> y [tokens, slots, rows] f32 (0 where ids is -1)."""
+        x_dtype = DType(x_dtype)
+        tokens, ncols = x.shape[:2]
+        slots = ids.shape[1]
+        if y is None:
+            y = torch.empty((tokens, slots, w.rows), dtype=torch.float32, device=x.device)
+        xp = _dev_ptr(x, x.dtype)
+        err = _Err()
+        _check(_lib.rlq_mul_mat_id(self._h, w._h, int(x_dtype), xp, ncols, tokens, _dev_ptr(ids, torch.int32),
+                                   slots, _dev_ptr(y, torch.float32), _stream_ptr(stream), ctypes.byref(err)), err)
+        return y
+
     def sync(self, stream=None):
         """Wait for the stream; raise the first data error recorded on the GPU."""
         err = _Err()
@@ -364,16 +401,17 @@ class Weights:
     HBM in the kernels' layout.  `data` is a numpy uint8 array (host) or a
     torch uint8 tensor on the GPU."""
 
-    def __init__(self, ctx, dtype, data, rows, cols):
+    def __init__(self, ctx, dtype, data, rows, cols, n2=1, n3=1):
         err, h = _Err(), ctypes.c_void_p()
         if torch is not None and isinstance(data, torch.Tensor):
             ptr, n, on_dev = _dev_ptr(data.reshape(-1), torch.uint8), data.numel(), 1
         else:
             arr = _u8(data)
             ptr, n, on_dev, self._keep = _ptr(arr), arr.size, 0, arr
-        _check(_lib.rlq_weights_create(ctx._h, int(dtype), ptr, n, int(rows), int(cols), on_dev,
-                                       ctypes.byref(h), ctypes.byref(err)), err)
+        _check(_lib.rlq_weights_create_stacked(ctx._h, int(dtype), ptr, n, int(rows), int(cols), int(n2), int(n3),
+                                               on_dev, ctypes.byref(h), ctypes.byref(err)), err)
         self._h, self.ctx, self.dtype, self.rows, self.cols = h, ctx, DType(dtype), int(rows), int(cols)
+        self.n2, self.n3 = int(n2), int(n3)
         self._keep = None
 
     def close(self):

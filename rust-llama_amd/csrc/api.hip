@@ -149,7 +149,7 @@ struct rlq_context {
     hipStream_t stream = nullptr;
     unsigned long long* err_words = nullptr;  // [0] device API (sticky), [1] host API (per call)
     unsigned long long* host_err = nullptr;   // pinned readback
-    DevBuf planes, keys, stage_in, stage_w, stage_out;
+    DevBuf planes, keys, stage_in, stage_w, stage_out, gate;
 };
 
 struct rlq_weights {
@@ -157,7 +157,9 @@ struct rlq_weights {
     uint32_t dtype;
     uint64_t rows, cols;
     uint8_t* dev;
-    uint64_t bytes;
+    uint64_t bytes;                  // GGUF bytes of all matrices
+    uint64_t n2 = 1, n3 = 1;         // stacked matrices (GGML ne[2], ne[3])
+    uint64_t mat_bytes = 0;          // device bytes of one tiled matrix
 };
 
 namespace {
@@ -200,9 +202,10 @@ hipStream_t pick(rlq_context* ctx, void* stream) {
 // Decode an error key (see rlq_device.hpp) into an rlq_error.
 int32_t key_to_error(unsigned long long key, uint32_t dtype, rlq_error* err) {
     if (key == ~0ull) return ok(err);
-    const uint64_t column = key >> 41, kind = (key >> 40) & 1, index = key & ((1ull << 40) - 1);
+    const uint64_t field = key >> 41, kind = (key >> 40) & 1, index = key & ((1ull << 40) - 1);
+    if (field == 0) return fail(err, RLQ_TENSOR_BOUNDS, dtype, index);
     return fail(err, kind == (uint64_t)kKindNonFinite ? RLQ_NON_FINITE_INPUT : RLQ_UNREPRESENTABLE_SCALE, dtype,
-                index, column);
+                index, field - 1);
 }
 
 // Read and clear error word `slot` after the stream drains.
@@ -233,9 +236,10 @@ int32_t default_context(rlq_context** out, rlq_error* err) {
 // the tiled layout (rlq_layout.hpp).  Host bytes go through a temporary
 // device copy that is freed before returning.
 hipError_t upload_weights(uint32_t t, const void* bytes, uint64_t len, uint64_t rows, uint64_t cols, bool on_device,
-                          uint8_t** dev, hipStream_t s) {
+                          uint8_t** dev, hipStream_t s, uint64_t mats = 1) {
     *dev = nullptr;
-    hipError_t e = hipMalloc((void**)dev, layout_bytes(t, rows, cols));
+    const uint64_t mb = layout_bytes(t, rows, cols);
+    hipError_t e = hipMalloc((void**)dev, mb * mats);
     if (e != hipSuccess) return e;
     const uint8_t* src = (const uint8_t*)bytes;
     void* tmp = nullptr;
@@ -246,7 +250,8 @@ hipError_t upload_weights(uint32_t t, const void* bytes, uint64_t len, uint64_t 
         if (e == hipSuccess) e = hipMemcpyAsync(tmp, src, len, hipMemcpyHostToDevice, s);
         src = (const uint8_t*)tmp;
     }
-    if (e == hipSuccess) e = launch_repack(t, src, rows, cols, *dev, s);
+    for (uint64_t m = 0; m < mats && e == hipSuccess; ++m)
+        e = launch_repack(t, src + m * (len / mats), rows, cols, *dev + m * mb, s);
     if (e == hipSuccess) e = hipStreamSynchronize(s);
     if (tmp) (void)hipFree(tmp);
     if (e != hipSuccess) {
@@ -290,6 +295,9 @@ const char* rlq_status_string(int32_t code) {
         case RLQ_INVALID_CONFIG: return "invalid model configuration";
         case RLQ_INVALID_TOKEN: return "token outside the vocabulary";
         case RLQ_INVALID_STATE: return "KV cache is full";
+        case RLQ_TENSOR_SHAPE: return "MUL_MAT / MUL_MAT_ID dimensions are incompatible";
+        case RLQ_TENSOR_BOUNDS: return "expert id outside the expert tensor";
+        case RLQ_TENSOR_UNSUPPORTED: return "right-hand side must be F32 or the activation type";
         default: return "unknown status";
     }
 }
@@ -334,7 +342,7 @@ void rlq_context_destroy(rlq_context* ctx) {
     if (!ctx) return;
     DeviceGuard g(ctx->device);
     if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
-    for (DevBuf* b : {&ctx->planes, &ctx->keys, &ctx->stage_in, &ctx->stage_w, &ctx->stage_out})
+    for (DevBuf* b : {&ctx->planes, &ctx->keys, &ctx->stage_in, &ctx->stage_w, &ctx->stage_out, &ctx->gate})
         if (b->p) (void)hipFree(b->p);
     if (ctx->err_words) (void)hipFree(ctx->err_words);
     if (ctx->host_err) (void)hipHostFree(ctx->host_err);
@@ -347,31 +355,43 @@ void* rlq_context_stream(rlq_context* ctx) { return ctx ? (void*)ctx->stream : n
 
 // ---- weights ------------------------------------------------------------------
 
-// Matrix::from_quantized (crates/model-runtime/src/math.rs:35-70)
-int32_t rlq_weights_create(rlq_context* ctx, uint32_t dtype, const void* bytes, uint64_t len, uint64_t rows,
-                           uint64_t cols, int32_t bytes_on_device, rlq_weights** out, rlq_error* err) {
+// Matrix::from_quantized (crates/model-runtime/src/math.rs:35-70), for a
+// stack of n2 x n3 matrices
+int32_t rlq_weights_create_stacked(rlq_context* ctx, uint32_t dtype, const void* bytes, uint64_t len, uint64_t rows,
+                                   uint64_t cols, uint64_t n2, uint64_t n3, int32_t bytes_on_device,
+                                   rlq_weights** out, rlq_error* err) {
     if (!ctx || !out) return fail(err, RLQ_INVALID_ARGUMENT);
     uint32_t at;
     int32_t rc = activation_dtype(dtype, &at, err);
     if (rc) return rc;
     if (!path_weight(dtype)) return fail(err, RLQ_UNIMPLEMENTED, dtype);
     if (rows == 0 || cols == 0) return fail(err, RLQ_INVALID_MATRIX_SHAPE, dtype, rows, cols);
-    uint64_t rb, expected;
+    if (n2 == 0 || n3 == 0) return fail(err, RLQ_TENSOR_SHAPE, dtype, n2, n3);
+    uint64_t rb, expected, mats;
     rc = row_bytes(dtype, cols, &rb, err);
     if (rc) return rc;
-    if (__builtin_mul_overflow(rb, rows, &expected)) return fail(err, RLQ_SIZE_OVERFLOW, dtype);
+    if (__builtin_mul_overflow(rb, rows, &expected) || __builtin_mul_overflow(n2, n3, &mats) ||
+        __builtin_mul_overflow(expected, mats, &expected))
+        return fail(err, RLQ_SIZE_OVERFLOW, dtype);
     if (len != expected) return fail(err, RLQ_INVALID_LENGTH, dtype, expected, len);
     if (!bytes) return fail(err, RLQ_INVALID_ARGUMENT, dtype);
     DeviceGuard g(ctx->device);
     rlq_weights* w = new (std::nothrow) rlq_weights{ctx->device, dtype, rows, cols, nullptr, len};
     if (!w) return fail(err, RLQ_ALLOCATION_FAILED);
-    const hipError_t e = upload_weights(dtype, bytes, len, rows, cols, bytes_on_device != 0, &w->dev, ctx->stream);
+    w->n2 = n2, w->n3 = n3, w->mat_bytes = layout_bytes(dtype, rows, cols);
+    const hipError_t e =
+        upload_weights(dtype, bytes, len, rows, cols, bytes_on_device != 0, &w->dev, ctx->stream, mats);
     if (e != hipSuccess) {
         delete w;
         return e == hipErrorOutOfMemory ? fail(err, RLQ_ALLOCATION_FAILED, dtype) : hip_fail(err, e);
     }
     *out = w;
     return ok(err);
+}
+
+int32_t rlq_weights_create(rlq_context* ctx, uint32_t dtype, const void* bytes, uint64_t len, uint64_t rows,
+                           uint64_t cols, int32_t bytes_on_device, rlq_weights** out, rlq_error* err) {
+    return rlq_weights_create_stacked(ctx, dtype, bytes, len, rows, cols, 1, 1, bytes_on_device, out, err);
 }
 
 void rlq_weights_destroy(rlq_weights* w) {
@@ -387,6 +407,130 @@ void rlq_weights_shape(const rlq_weights* w, uint64_t* rows, uint64_t* cols, uin
     if (rows) *rows = w->rows;
     if (cols) *cols = w->cols;
     if (dtype) *dtype = w->dtype;
+}
+
+void rlq_weights_stack(const rlq_weights* w, uint64_t* n2, uint64_t* n3) {
+    if (!w) return;
+    if (n2) *n2 = w->n2;
+    if (n3) *n3 = w->n3;
+}
+
+// ---- GGML MUL_MAT with broadcast, MUL_MAT_ID ---------------------------------------
+
+namespace {
+
+// Every right-hand column quantized once (F32) or taken as given (packed
+// activation bytes) into the context's planes; then the gate kernel.
+int32_t mm_stage(rlq_context* ctx, const rlq_weights* w, uint32_t at, uint32_t x_dtype, const void* x,
+                 uint64_t columns, const int32_t* ids, uint64_t pairs, float* y, hipStream_t s, ActPlanes* planes,
+                 uint32_t** gate, rlq_error* err) {
+    const uint64_t K = w->cols, nb = K / block_size(at);
+    HIP_TRY(ensure(ctx, ctx->planes, act_planes_bytes(at, K, columns)));
+    HIP_TRY(ensure(ctx, ctx->gate, sizeof(uint32_t)));
+    *planes = act_planes_carve(ctx->planes.p, at, K, columns);
+    *gate = (uint32_t*)ctx->gate.p;
+    if (x_dtype == 0) {
+        if (at == kQ8_K) HIP_TRY(launch_quantize_q8k((const float*)x, K, columns, planes, nullptr, ctx->err_words, s));
+        else HIP_TRY(launch_quantize_q8_0((const float*)x, K, columns, planes, nullptr, ctx->err_words, s));
+    } else {
+        HIP_TRY(launch_act_from_gguf(at, (const uint8_t*)x, K, columns, planes, s));
+    }
+    HIP_TRY(launch_mm_prepare(ids, pairs, (uint32_t)w->n2, planes->bad, columns * nb, y, w->rows, *gate,
+                              ctx->err_words, s));
+    return ok(err);
+}
+
+// Common argument checks: (x_dtype, x alignment, column count).
+int32_t mm_check_rhs(const rlq_weights* w, uint32_t at, uint32_t x_dtype, const void* x, const float* y,
+                     uint64_t columns, rlq_error* err) {
+    if (x_dtype != 0 && x_dtype != at) return fail(err, RLQ_TENSOR_UNSUPPORTED, x_dtype);
+    if (!x || !y) return fail(err, RLQ_INVALID_ARGUMENT, w->dtype);
+    if ((x_dtype == 0 && ((uintptr_t)x & 15)) || ((uintptr_t)y & 3)) return fail(err, RLQ_INVALID_ARGUMENT, w->dtype);
+    // one quantizer launch covers every column (grid rows), and error keys
+    // carry the column
+    if (columns > 65535) return fail(err, RLQ_UNIMPLEMENTED, w->dtype, columns, 65535);
+    return ok(err);
+}
+
+}  // namespace
+
+// MUL_MAT (crates/tensor/src/cpu_extra.rs:756-873)
+int32_t rlq_mul_mat(rlq_context* ctx, const rlq_weights* w, uint32_t x_dtype, const void* x, uint64_t ncols,
+                    uint64_t n2, uint64_t n3, float* y, void* stream, rlq_error* err) {
+    if (!ctx || !w) return fail(err, RLQ_INVALID_ARGUMENT);
+    uint32_t at;
+    int32_t rc = activation_dtype(w->dtype, &at, err);
+    if (rc) return rc;
+    if (n2 % w->n2 != 0 || n3 % w->n3 != 0) return fail(err, RLQ_TENSOR_SHAPE, w->dtype, n2, n3);  // :759-769
+    uint64_t columns;
+    if (__builtin_mul_overflow(ncols, n2, &columns) || __builtin_mul_overflow(columns, n3, &columns))
+        return fail(err, RLQ_SIZE_OVERFLOW, w->dtype);
+    if (x_dtype != 0 && x_dtype != at) return fail(err, RLQ_TENSOR_UNSUPPORTED, x_dtype);  // :779-784
+    if (columns == 0) return ok(err);
+    rc = mm_check_rhs(w, at, x_dtype, x, y, columns, err);
+    if (rc) return rc;
+    DeviceGuard g(ctx->device);
+    const hipStream_t s = pick(ctx, stream);
+    ActPlanes planes;
+    uint32_t* gate;
+    rc = mm_stage(ctx, w, at, x_dtype, x, columns, nullptr, 0, y, s, &planes, &gate, err);
+    if (rc) return rc;
+    const uint64_t K = w->cols, nb = K / block_size(at), r2 = n2 / w->n2, r3 = n3 / w->n3;
+    for (uint64_t i3 = 0; i3 < n3; ++i3)
+        for (uint64_t i2 = 0; i2 < n2; ++i2) {
+            const uint64_t slice = i3 * n2 + i2, c0 = slice * ncols;
+            const uint64_t m = (i3 / r3) * w->n2 + i2 / r2;  // the broadcast source matrix
+            ActPlanes p = planes;
+            p.q += c0 * K;
+            p.d += c0 * nb;
+            p.bad += c0 * nb;
+            if (p.bsum) p.bsum += c0 * (K / 16);
+            MvExtra ex;
+            ex.gate = gate;
+            ex.column_base = c0;
+            HIP_TRY(launch_matvec_ex(w->dtype, w->dev + m * w->mat_bytes, w->rows, K, nullptr, &p, ncols,
+                                     y + c0 * w->rows, w->rows, nullptr, ctx->err_words, nullptr, nullptr, ex, s));
+        }
+    return ok(err);
+}
+
+// MUL_MAT_ID (crates/tensor/src/cpu_index.rs:169-236)
+int32_t rlq_mul_mat_id(rlq_context* ctx, const rlq_weights* w, uint32_t x_dtype, const void* x, uint64_t ncols,
+                       uint64_t tokens, const int32_t* ids, uint64_t slots, float* y, void* stream,
+                       rlq_error* err) {
+    if (!ctx || !w) return fail(err, RLQ_INVALID_ARGUMENT);
+    uint32_t at;
+    int32_t rc = activation_dtype(w->dtype, &at, err);
+    if (rc) return rc;
+    if (w->n3 != 1 || ncols == 0 || slots % ncols != 0)  // :179-194
+        return fail(err, RLQ_TENSOR_SHAPE, w->dtype, slots, ncols);
+    if (x_dtype != 0 && x_dtype != at) return fail(err, RLQ_TENSOR_UNSUPPORTED, x_dtype);  // :195-199
+    uint64_t pairs, columns;
+    if (__builtin_mul_overflow(tokens, slots, &pairs) || __builtin_mul_overflow(tokens, ncols, &columns))
+        return fail(err, RLQ_SIZE_OVERFLOW, w->dtype);
+    if (pairs == 0) return ok(err);  // :205-208: an empty output
+    if (!ids) return fail(err, RLQ_INVALID_ARGUMENT, w->dtype);
+    if (w->n2 > 0x7fffffffull) return fail(err, RLQ_UNIMPLEMENTED, w->dtype, w->n2);
+    rc = mm_check_rhs(w, at, x_dtype, x, y, columns, err);
+    if (rc) return rc;
+    if (pairs > 0xffffffffull) return fail(err, RLQ_UNIMPLEMENTED, w->dtype, pairs);
+    DeviceGuard g(ctx->device);
+    const hipStream_t s = pick(ctx, stream);
+    ActPlanes planes;
+    uint32_t* gate;
+    rc = mm_stage(ctx, w, at, x_dtype, x, columns, ids, pairs, y, s, &planes, &gate, err);
+    if (rc) return rc;
+    MvExtra ex;
+    ex.gate = gate;
+    ex.ids = ids;
+    ex.id_pairs = pairs;
+    ex.id_slots = (uint32_t)slots;
+    ex.id_cols = (uint32_t)ncols;
+    ex.id_experts = (uint32_t)w->n2;
+    ex.expert_bytes = w->mat_bytes;
+    HIP_TRY(launch_matvec_ex(w->dtype, w->dev, w->rows, w->cols, nullptr, &planes, 1, y, w->rows, nullptr,
+                             ctx->err_words, nullptr, nullptr, ex, s));
+    return ok(err);
 }
 
 // ---- device matmul --------------------------------------------------------------

@@ -126,7 +126,38 @@ struct MvArgs {
     // kEpSiluPair: the rows are gate and up tiles interleaved ([gate tile i,
     // up tile i] as tiles 2i, 2i + 1) and y[16 i + r] = silu(gate) * up
     uint32_t epilogue;
+    // When non-null and nonzero, every workgroup exits before touching
+    // anything: the call was refused on the device (MUL_MAT / MUL_MAT_ID).
+    const uint32_t* gate;
+    // MUL_MAT_ID: workgroup row blockIdx.y is (token, slot) pair id_base +
+    // blockIdx.y: expert ids[pair] (of id_experts, expert_bytes apart), the
+    // pre-quantized column token * id_cols + slot % id_cols, output rows at
+    // y + pair * ldy.  Null ids: one matrix, one grid row.
+    const int32_t* ids;
+    uint32_t id_base, id_slots, id_cols, id_experts;
+    uint64_t expert_bytes;
 };
+
+// Kernel entry: false when the workgroup has nothing to do (a refused call,
+// an expert slot with id -1, whose outputs the prepare kernel zeroed).
+__device__ __forceinline__ bool mv_enter(MvArgs& a) {
+    if (a.gate && *a.gate) return false;
+    if (!a.ids) return true;
+    const uint32_t pair = a.id_base + blockIdx.y;
+    const int32_t id = a.ids[pair];
+    if (id < 0 || (uint32_t)id >= a.id_experts) return false;
+    const uint32_t token = pair / a.id_slots, slot = pair % a.id_slots;
+    const uint64_t col = (uint64_t)token * a.id_cols + slot % a.id_cols;
+    const uint32_t nb = a.nb;
+    a.w += (uint64_t)id * a.expert_bytes;
+    a.pre.q += col * a.cols;
+    a.pre.d += col * nb;
+    a.pre.bad += col * nb;
+    if (a.pre.bsum) a.pre.bsum += col * (a.cols / 16);
+    a.y += (uint64_t)pair * a.ldy;
+    a.err_column0 = (uint32_t)col;
+    return true;
+}
 
 // LDS: q8 [batch][S] | d f32 [nb][8] | (Q2_K, Q4_K, Q5_K) bsums i16 [nb][8][16] | 256
 // zero bytes | 16 f64 (the RMSNorm reduction of the input transform).  S = cols + 16 is an odd multiple of 16, so the A-operand reads
@@ -493,6 +524,7 @@ __device__ __forceinline__ Q5High q5_high(uint4 qh, uint32_t kq) {
 // and the activation staging.  `ld_tile`/`ld_chunk` track the next step to
 // load: tile gw + k*tw, chunk c.
 #define RLQ_MV_PROLOGUE(WT, CHUNKS)                                                                   \
+    if (!mv_enter(a)) return;                                                                         \
     extern __shared__ __align__(16) uint8_t lds[];                                                    \
     const LdsMap L = lds_map(WT, a.cols, a.batch);                                                   \
     const uint32_t lane = threadIdx.x & 63, n = lane & 15, kq = lane >> 4;                            \
@@ -658,6 +690,7 @@ __host__ __device__ inline uint32_t small_lds_bytes(uint32_t cols, uint32_t batc
 template <uint32_t T, int W, int KS, int D, int B, bool DBG>
 __global__ __launch_bounds__(W * 64) void q4k_mv_small_kernel(MvArgs a) {
     constexpr int TS = SmallGeom<W, KS>::TS;
+    if (!mv_enter(a)) return;
     extern __shared__ __align__(16) uint8_t lds[];
     const LdsMap L = lds_map(T, a.cols, a.batch);
     float* part = (float*)(lds + small_part_off(a.cols, a.batch));
@@ -1162,6 +1195,7 @@ template <uint32_t T, int W, int KS, int D, bool DBG>
 __global__ __launch_bounds__(W * 64) void k16_mv_split_kernel(MvArgs a) {
     constexpr int TS = W / KS;
     constexpr uint32_t kChunk = T == kQ3_K ? kQ3KChunk : kQ2KChunk;
+    if (!mv_enter(a)) return;
     extern __shared__ __align__(16) uint8_t lds[];
     const LdsMap L = lds_map(T, a.cols, a.batch);
     float* part = (float*)(lds + k16_part_off(T, a.cols, a.batch));
@@ -1358,8 +1392,16 @@ static int device_cus() {
     return cus;
 }
 
+// Grid rows (MUL_MAT_ID pairs of this launch, else 1) and the workgroups per
+// row: the device's budget of `cap` workgroups is shared by the rows.
+static uint32_t grid_rows(const MvArgs& a, uint32_t pairs) { return a.ids ? pairs : 1u; }
+static uint32_t grid_cols(uint32_t want, uint32_t cap, uint32_t rows) {
+    const uint32_t per = cap / rows > 0 ? cap / rows : 1u;
+    return want < per ? want : per;
+}
+
 template <typename K>
-static hipError_t launch_one(K kernel, const MvArgs& a, size_t lds, hipStream_t s) {
+static hipError_t launch_one(K kernel, const MvArgs& a, size_t lds, hipStream_t s, uint32_t pairs) {
     static size_t lds_set = 64 * 1024;  // above 64 KB the kernel must opt in
     if (lds > lds_set) {
         const hipError_t e =
@@ -1368,9 +1410,9 @@ static hipError_t launch_one(K kernel, const MvArgs& a, size_t lds, hipStream_t 
         lds_set = lds;
     }
     const uint32_t want = (a.ntiles + kMvWaves - 1) / kMvWaves;
-    const uint32_t cap = 2u * (uint32_t)device_cus();
-    const uint32_t grid = want < cap ? want : cap;
-    hipLaunchKernelGGL(kernel, dim3(grid), dim3(kMvWaves * 64), lds, s, a);
+    const uint32_t gy = grid_rows(a, pairs);
+    const uint32_t grid = grid_cols(want, 2u * (uint32_t)device_cus(), gy);
+    hipLaunchKernelGGL(kernel, dim3(grid, gy), dim3(kMvWaves * 64), lds, s, a);
     return hipGetLastError();
 }
 
@@ -1379,11 +1421,16 @@ static hipError_t launch_one(K kernel, const MvArgs& a, size_t lds, hipStream_t 
 constexpr int kSmallW = 8, kSmallKS = 8, kSmallD = 2, kSmallWgPerCu = 2;
 
 template <uint32_t T, int W, int KS, int D, int B, bool DBG>
-static hipError_t launch_small(const MvArgs& a, hipStream_t s) {
+static hipError_t launch_small(const MvArgs& a, hipStream_t s, uint32_t pairs) {
     constexpr int TS = W / KS;
     const uint32_t want = (a.ntiles + TS - 1) / TS;
-    const uint32_t cap = (uint32_t)kSmallWgPerCu * (uint32_t)device_cus();
-    const uint32_t grid = want < cap ? want : cap;
+    const uint32_t gy = grid_rows(a, pairs);
+    uint32_t grid = grid_cols(want, (uint32_t)kSmallWgPerCu * (uint32_t)device_cus(), gy);
+    // enough workgroups that every one parks at most `room` tiles' partials
+    const size_t off = small_part_off(a.cols, a.batch), per_tile = (size_t)TS * KS * 16u * a.batch * 4u;
+    if (off >= kMaxLds || (kMaxLds - off) / per_tile == 0) return hipErrorInvalidValue;
+    const uint64_t room = (kMaxLds - off) / per_tile, need = (a.ntiles + room * TS - 1) / (room * TS);
+    if (grid < need) grid = (uint32_t)need;
     const uint32_t tstride = grid * TS, tmax = (a.ntiles + tstride - 1) / tstride;
     const size_t lds = small_lds_bytes(a.cols, a.batch, tmax, TS, KS);
     if (lds > kMaxLds) return hipErrorInvalidValue;
@@ -1394,26 +1441,27 @@ static hipError_t launch_small(const MvArgs& a, hipStream_t s) {
         if (e != hipSuccess) return e;
         lds_set = lds;
     }
-    hipLaunchKernelGGL((q4k_mv_small_kernel<T, W, KS, D, B, DBG>), dim3(grid), dim3(W * 64), lds, s, a);
+    hipLaunchKernelGGL((q4k_mv_small_kernel<T, W, KS, D, B, DBG>), dim3(grid, gy), dim3(W * 64), lds, s, a);
     return hipGetLastError();
 }
 
 // Q4_K / Q5_K: the VALU kernel for one or two columns, MFMA above.
 template <uint32_t T>
-static hipError_t launch_q45(const MvArgs& a, uint32_t nbat, bool dbg, uint32_t epilogue, size_t lds, hipStream_t s) {
+static hipError_t launch_q45(const MvArgs& a, uint32_t nbat, bool dbg, uint32_t epilogue, size_t lds, hipStream_t s,
+                             uint32_t pairs) {
     // two tile slots per workgroup (a K split of four): the SiLU pair
     // epilogue's gate and up tiles, and small matrices of at most 4096
     // columns and 512 tiles (measured: 6144x4096 runs 1 us faster)
     if (epilogue == kEpSiluPair || (nbat == 1 && !dbg && a.nb <= 16 && a.ntiles <= 512))
-        return launch_small<T, kSmallW, kSmallW / 2, kSmallD, 1, false>(a, s);
+        return launch_small<T, kSmallW, kSmallW / 2, kSmallD, 1, false>(a, s, pairs);
     if (nbat == 1)
-        return dbg ? launch_small<T, kSmallW, kSmallKS, kSmallD, 1, true>(a, s)
-                   : launch_small<T, kSmallW, kSmallKS, kSmallD, 1, false>(a, s);
+        return dbg ? launch_small<T, kSmallW, kSmallKS, kSmallD, 1, true>(a, s, pairs)
+                   : launch_small<T, kSmallW, kSmallKS, kSmallD, 1, false>(a, s, pairs);
     if (nbat == 2)
-        return dbg ? launch_small<T, kSmallW, kSmallKS, kSmallD, 2, true>(a, s)
-                   : launch_small<T, kSmallW, kSmallKS, kSmallD, 2, false>(a, s);
-    return dbg ? launch_one(q4k_mv_kernel<T, kMvWaves, 8, true>, a, lds, s)
-               : launch_one(q4k_mv_kernel<T, kMvWaves, 8, false>, a, lds, s);
+        return dbg ? launch_small<T, kSmallW, kSmallKS, kSmallD, 2, true>(a, s, pairs)
+                   : launch_small<T, kSmallW, kSmallKS, kSmallD, 2, false>(a, s, pairs);
+    return dbg ? launch_one(q4k_mv_kernel<T, kMvWaves, 8, true>, a, lds, s, pairs)
+               : launch_one(q4k_mv_kernel<T, kMvWaves, 8, false>, a, lds, s, pairs);
 }
 
 // Q2_K / Q3_K: up to four columns the K-split kernel, while its parked terms
@@ -1423,7 +1471,7 @@ static hipError_t launch_q45(const MvArgs& a, uint32_t nbat, bool dbg, uint32_t 
 constexpr int kK16W = 8, kK16KS = 8, kK16D = 2;
 
 template <uint32_t T, bool DBG>
-static hipError_t launch_k16_split(const MvArgs& a, size_t lds, uint32_t grid, hipStream_t s) {
+static hipError_t launch_k16_split(const MvArgs& a, size_t lds, uint32_t grid, uint32_t gy, hipStream_t s) {
     static size_t lds_set = 64 * 1024;
     auto kernel = k16_mv_split_kernel<T, kK16W, kK16KS, kK16D, DBG>;
     if (lds > lds_set) {
@@ -1432,22 +1480,22 @@ static hipError_t launch_k16_split(const MvArgs& a, size_t lds, uint32_t grid, h
         if (e != hipSuccess) return e;
         lds_set = lds;
     }
-    hipLaunchKernelGGL(kernel, dim3(grid), dim3(kK16W * 64), lds, s, a);
+    hipLaunchKernelGGL(kernel, dim3(grid, gy), dim3(kK16W * 64), lds, s, a);
     return hipGetLastError();
 }
 
 template <uint32_t T>
-static hipError_t launch_k16(const MvArgs& a, bool dbg, size_t lds_plain, hipStream_t s) {
+static hipError_t launch_k16(const MvArgs& a, bool dbg, size_t lds_plain, hipStream_t s, uint32_t pairs) {
     constexpr int TS = kK16W / kK16KS;
     const uint32_t want = (a.ntiles + TS - 1) / TS;
-    const uint32_t cap = (uint32_t)kSmallWgPerCu * (uint32_t)device_cus();
-    const uint32_t grid = want < cap ? want : cap;
+    const uint32_t gy = grid_rows(a, pairs);
+    const uint32_t grid = grid_cols(want, (uint32_t)kSmallWgPerCu * (uint32_t)device_cus(), gy);
     const uint64_t tstride = (uint64_t)grid * TS, tmax = (a.ntiles + tstride - 1) / tstride;
     const uint64_t lds = k16_part_off(T, a.cols, a.batch) + tmax * TS * a.nb * 16ull * a.batch * 4ull;
     if (a.batch <= 4 && lds <= kMaxLds)
-        return dbg ? launch_k16_split<T, true>(a, lds, grid, s) : launch_k16_split<T, false>(a, lds, grid, s);
-    return dbg ? launch_one(k16_mv_kernel<T, kMvWaves, 4, true>, a, lds_plain, s)
-               : launch_one(k16_mv_kernel<T, kMvWaves, 4, false>, a, lds_plain, s);
+        return dbg ? launch_k16_split<T, true>(a, lds, grid, gy, s) : launch_k16_split<T, false>(a, lds, grid, gy, s);
+    return dbg ? launch_one(k16_mv_kernel<T, kMvWaves, 4, true>, a, lds_plain, s, pairs)
+               : launch_one(k16_mv_kernel<T, kMvWaves, 4, false>, a, lds_plain, s, pairs);
 }
 
 hipError_t launch_matvec(uint32_t wtype, const uint8_t* w, uint64_t rows, uint64_t cols, const float* x,
@@ -1475,6 +1523,10 @@ hipError_t launch_matvec_ex(uint32_t wtype, const uint8_t* w, uint64_t rows, uin
         (ex.epilogue != kEpSiluPair || batch != 1 || (wtype != kQ4_K && wtype != kQ5_K) ||
          rows % (2 * kTileRows) != 0 || argmax_key || ex.resid || dbg_isum))
         return hipErrorInvalidValue;
+    // expert pairs: one pre-quantized column each, plain stores
+    if (ex.ids && (batch != 1 || x || !pre || argmax_key || dbg_isum || ex.resid || ex.xform != kXfNone ||
+                   ex.epilogue != kEpStore || ex.id_pairs == 0 || ex.id_slots == 0 || ex.id_cols == 0))
+        return hipErrorInvalidValue;
     uint64_t b0 = 0;
     while (b0 < batch) {
         uint32_t nbat = (uint32_t)(batch - b0 < 8 ? batch - b0 : 8);
@@ -1500,7 +1552,7 @@ hipError_t launch_matvec_ex(uint32_t wtype, const uint8_t* w, uint64_t rows, uin
         a.ldy = ldy;
         a.argmax_key = argmax_key ? argmax_key + b0 : nullptr;
         a.err_word = err_word;
-        a.err_column0 = (uint32_t)b0;
+        a.err_column0 = (uint32_t)(ex.column_base + b0);
         a.dbg_isum = b0 == 0 ? dbg_isum : nullptr;  // column 0 only
         a.dbg_imin = b0 == 0 ? dbg_imin : nullptr;
         a.xform = ex.xform;
@@ -1508,31 +1560,89 @@ hipError_t launch_matvec_ex(uint32_t wtype, const uint8_t* w, uint64_t rows, uin
         a.norm_w = ex.norm_w;
         a.resid = ex.resid ? ex.resid + b0 * ldy : nullptr;
         a.epilogue = ex.epilogue;
-        hipError_t e;
+        a.gate = ex.gate;
+        a.ids = ex.ids;
+        a.id_slots = ex.id_slots;
+        a.id_cols = ex.id_cols;
+        a.id_experts = ex.id_experts;
+        a.expert_bytes = ex.expert_bytes;
         constexpr int W = kMvWaves;
         const bool dbg = a.dbg_isum != nullptr;
-        if (wtype == kQ4_K) {
-            e = launch_q45<kQ4_K>(a, nbat, dbg, ex.epilogue, lds, s);
-        } else if (wtype == kQ5_K) {
-            e = launch_q45<kQ5_K>(a, nbat, dbg, ex.epilogue, lds, s);
-        } else if (wtype == kQ3_K) {
-            e = launch_k16<kQ3_K>(a, dbg, lds, s);
-        } else if (wtype == kQ2_K) {
-            e = launch_k16<kQ2_K>(a, dbg, lds, s);
-        } else if (wtype == kQ6_K) {
-            e = dbg ? launch_one(q6k_mv_kernel<W, 4, true>, a, lds, s)
-                    : launch_one(q6k_mv_kernel<W, 4, false>, a, lds, s);
-        } else {
-            e = dbg ? launch_one(q8_0_mv_kernel<W, 8, true>, a, lds, s)
-                    : launch_one(q8_0_mv_kernel<W, 8, false>, a, lds, s);
+        auto dispatch = [&](uint32_t pairs) -> hipError_t {
+            switch (wtype) {
+                case kQ4_K: return launch_q45<kQ4_K>(a, nbat, dbg, ex.epilogue, lds, s, pairs);
+                case kQ5_K: return launch_q45<kQ5_K>(a, nbat, dbg, ex.epilogue, lds, s, pairs);
+                case kQ3_K: return launch_k16<kQ3_K>(a, dbg, lds, s, pairs);
+                case kQ2_K: return launch_k16<kQ2_K>(a, dbg, lds, s, pairs);
+                case kQ6_K:
+                    return dbg ? launch_one(q6k_mv_kernel<W, 4, true>, a, lds, s, pairs)
+                               : launch_one(q6k_mv_kernel<W, 4, false>, a, lds, s, pairs);
+                default:
+                    return dbg ? launch_one(q8_0_mv_kernel<W, 8, true>, a, lds, s, pairs)
+                               : launch_one(q8_0_mv_kernel<W, 8, false>, a, lds, s, pairs);
+            }
+        };
+        if (!a.ids) {
+            const hipError_t e = dispatch(1);
+            if (e != hipSuccess) return e;
+        } else {  // grid rows are pairs, at most 65535 per launch
+            for (uint64_t p0 = 0; p0 < ex.id_pairs; p0 += 65535) {
+                a.id_base = (uint32_t)p0;
+                const hipError_t e = dispatch((uint32_t)(ex.id_pairs - p0 < 65535 ? ex.id_pairs - p0 : 65535));
+                if (e != hipSuccess) return e;
+            }
         }
-        if (e != hipSuccess) return e;
         b0 += nbat;
     }
     return hipSuccess;
 }
 
 // ---------------------------------------------------------------------------
+// ---------------------------------------------------------------------------
+// MUL_MAT / MUL_MAT_ID prepare (one workgroup): the reference checks every
+// expert id before it quantizes anything (crates/tensor/src/cpu_index.rs:
+// 197-202) and writes no output when any check or any column's quantization
+// fails.  The gate is 1 when an id is outside [-1, experts) (the first one is
+// reported as TensorError::Bounds) or any pre-quantized block is bad;
+// otherwise the outputs of the pairs with id -1 are zeroed (the reference's
+// `zeros` output, cpu_index.rs:204) and the gate is 0.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void mm_prepare_kernel(const int32_t* __restrict__ ids, uint64_t pairs,
+                                                         int32_t experts, const uint8_t* __restrict__ bad,
+                                                         uint64_t nbad, float* __restrict__ y, uint64_t rows,
+                                                         uint32_t* gate, unsigned long long* err_word) {
+    __shared__ unsigned long long first_s;
+    __shared__ int flag_s;
+    if (threadIdx.x == 0) first_s = ~0ull, flag_s = 0;
+    __syncthreads();
+    unsigned long long first = ~0ull;
+    for (uint64_t i = threadIdx.x; i < pairs; i += 256) {
+        const int32_t id = ids[i];
+        if ((id < -1 || id >= experts) && i < first) first = i;
+    }
+    int any_bad = 0;
+    for (uint64_t i = threadIdx.x; i < nbad; i += 256) any_bad |= bad[i];
+    if (first != ~0ull) atomicMin(&first_s, first);
+    if (any_bad) atomicOr(&flag_s, 1);
+    __syncthreads();
+    const bool refused = first_s != ~0ull || flag_s != 0;
+    if (threadIdx.x == 0) {
+        *gate = refused ? 1u : 0u;
+        if (first_s != ~0ull) report_error(err_word, bounds_key(first_s));
+    }
+    if (refused || !ids) return;
+    for (uint64_t p = 0; p < pairs; ++p)
+        if (ids[p] == -1)
+            for (uint64_t r = threadIdx.x; r < rows; r += 256) y[p * rows + r] = 0.0f;
+}
+
+hipError_t launch_mm_prepare(const int32_t* ids, uint64_t pairs, uint32_t experts, const uint8_t* bad, uint64_t nbad,
+                             float* y, uint64_t rows, uint32_t* gate, unsigned long long* err_word, hipStream_t s) {
+    hipLaunchKernelGGL(mm_prepare_kernel, dim3(1), dim3(256), 0, s, ids, ids ? pairs : 0, (int32_t)experts, bad, nbad,
+                       y, rows, gate, err_word);
+    return hipGetLastError();
+}
+
 __global__ void argmax_finish_kernel(const unsigned long long* keys, uint64_t batch, const float* y, uint64_t ldy,
                                      uint32_t* out) {
     const uint64_t b = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;

@@ -179,17 +179,21 @@ __device__ __forceinline__ float sse2_exp(float x) {
 //
 // One u64 per context, UINT64_MAX when clear.  The first data error in the
 // reference's reporting order wins an atomicMin:
-//   key = column << 41 | kind << 40 | index
+//   key = (column + 1) << 41 | kind << 40 | index
 // kind 0 = NonFiniteInput{index}, kind 1 = UnrepresentableScale{block}.  In
 // the reference every check of one activation row runs before the next row
 // is quantized (crates/tensor/src/cpu_extra.rs:815-822), and within one row
-// the finite scan precedes the scale preflight (encode.rs:70-77).
+// the finite scan precedes the scale preflight (encode.rs:70-77).  Keys with
+// a column field of 0 are call-level errors found before any row is
+// quantized: MUL_MAT_ID's expert-id check (TensorError::Bounds,
+// crates/tensor/src/cpu_index.rs:197-202), key = index of the first bad id.
 constexpr int kKindNonFinite = 0;
 constexpr int kKindScale = 1;
 
 __device__ __forceinline__ uint64_t error_key(uint64_t column, int kind, uint64_t index) {
-    return (column << 41) | ((uint64_t)kind << 40) | (index & ((1ull << 40) - 1));
+    return ((column + 1) << 41) | ((uint64_t)kind << 40) | (index & ((1ull << 40) - 1));
 }
+__device__ __forceinline__ uint64_t bounds_key(uint64_t index) { return index & ((1ull << 40) - 1); }
 
 __device__ __forceinline__ void report_error(unsigned long long* word, uint64_t key) {
     atomicMin(word, (unsigned long long)key);

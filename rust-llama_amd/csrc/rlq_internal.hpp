@@ -84,7 +84,21 @@ struct MvExtra {
     const float* norm_w = nullptr;
     const float* resid = nullptr;
     uint32_t epilogue = 0;
+    uint64_t column_base = 0;          // error-report index of this launch's column 0
+    const uint32_t* gate = nullptr;    // device word: nonzero refuses the launch
+    // MUL_MAT_ID: id_pairs (token, slot) pairs, expert ids[pair] of
+    // id_experts matrices expert_bytes apart, column token * id_cols +
+    // slot % id_cols of the pre-quantized planes, y + pair * ldy
+    const int32_t* ids = nullptr;
+    uint64_t id_pairs = 0;
+    uint32_t id_slots = 0, id_cols = 0, id_experts = 0;
+    uint64_t expert_bytes = 0;
 };
+// The MUL_MAT / MUL_MAT_ID gate (one workgroup, before the products): checks
+// the ids (ids may be null) and the `bad` bytes of the pre-quantized planes,
+// zeroes the outputs of pairs with id -1, writes *gate.
+hipError_t launch_mm_prepare(const int32_t* ids, uint64_t pairs, uint32_t experts, const uint8_t* bad, uint64_t nbad,
+                             float* y, uint64_t rows, uint32_t* gate, unsigned long long* err_word, hipStream_t s);
 hipError_t launch_matvec_ex(uint32_t wtype, const uint8_t* w, uint64_t rows, uint64_t cols, const float* x,
                             const ActPlanes* pre, uint64_t batch, float* y, uint64_t ldy,
                             unsigned long long* argmax_key, unsigned long long* err_word, int32_t* dbg_isum,

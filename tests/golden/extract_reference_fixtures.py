@@ -27,6 +27,11 @@ tests:
         dtype n size | x[n] expected[size]
   GGQD  crates/quant/tests/reference.rs:20-38
         dtype n size | bytes[size] expected[n]
+  GGTR0002  crates/tensor/tests/extended.rs:30-42, 185-204 and indexing.rs:28-41, 90-110
+        name tag flag | ni ints[i64] | nf floats | nt tensors | expected tensor
+        with tensor = dtype shape[4 x u64] (strides[4 x u64], inputs only) nbytes[u64] bytes
+        (strings are u32 length + UTF-8).  Kept: the GGML MUL_MAT and MUL_MAT_ID
+        graphs whose weight (first input) type is on the path.
 """
 import hashlib
 import json
@@ -36,7 +41,9 @@ import sys
 
 KEEP = {8, 12, 14, 15}
 KEEP_K = {10, 11, 13}
+KEEP_MM = {8, 10, 11, 12, 13, 14}
 SRC_DIR = "crates/quant/tests/fixtures"
+TENSOR_DIR = "crates/tensor/tests/fixtures"
 
 
 class Reader:
@@ -53,6 +60,20 @@ class Reader:
 
     def word(self):
         return struct.unpack("<I", self.take(4))[0]
+
+    def u64(self):
+        return struct.unpack("<Q", self.take(8))[0]
+
+    def string(self):
+        return self.take(self.word()).decode()
+
+    def ggtr_tensor(self, strided):
+        dtype = self.word()
+        self.take(32)  # shape
+        if strided:
+            self.take(32)
+        self.take(self.u64())
+        return dtype
 
 
 def split_records(kind, data):
@@ -79,6 +100,16 @@ def split_records(kind, data):
         elif kind == "GGQD":
             dtype, n, size = (r.word() for _ in range(3))
             r.take(size + n * 4)
+        elif kind == "GGTR0002":
+            r.string()
+            tag = r.string()
+            r.word()
+            r.take(8 * r.word())
+            r.take(4 * r.word())
+            nt = r.word()
+            types = [r.ggtr_tensor(True) for _ in range(nt)]
+            r.ggtr_tensor(False)
+            dtype = types[0] if tag in ("mul_mat", "mul_mat_id") else -1
         else:
             raise ValueError(kind)
         records.append((dtype, data[start:r.pos]))
@@ -98,6 +129,9 @@ FILES = [
     ("matvec-extended-reference.bin", "GGQX", "matvec-extended-q2k-q3k-q5k.bin", KEEP_K),
     ("encoder-extended-reference.bin", "GGQE", "encoder-extended-q2k-q3k-q5k.bin", KEEP_K),
     ("dequant-reference.bin", "GGQD", "dequant-q2k-q3k-q5k.bin", KEEP_K),
+    # GGML MUL_MAT with ne2/ne3 broadcast and MUL_MAT_ID with expert ids
+    (TENSOR_DIR + "/cpu-extended-reference.bin", "GGTR0002", "mul-mat-broadcast.bin", KEEP_MM),
+    (TENSOR_DIR + "/cpu-indexing-gnu-reference.bin", "GGTR0002", "mul-mat-id.bin", KEEP_MM),
 ]
 
 
@@ -106,7 +140,9 @@ def main():
     here = os.path.dirname(os.path.abspath(__file__))
     manifest = {"source_root": "rust-llama " + SRC_DIR, "kept_dtypes": sorted(KEEP | KEEP_K), "files": {}}
     for src, kind, dst, keep in FILES:
-        data = open(os.path.join(root, SRC_DIR, src), "rb").read()
+        if "/" not in src:
+            src = f"{SRC_DIR}/{src}"
+        data = open(os.path.join(root, src), "rb").read()
         magic, records = split_records(kind, data)
         kept = [(i, d, raw) for i, (d, raw) in enumerate(records) if d in keep]
         out = magic + struct.pack("<I", len(kept)) + b"".join(raw for _, _, raw in kept)
@@ -116,7 +152,7 @@ def main():
         for _, d, _ in kept:
             per_type[str(d)] = per_type.get(str(d), 0) + 1
         manifest["files"][dst] = {
-            "source": f"{SRC_DIR}/{src}",
+            "source": src,
             "source_sha256": hashlib.sha256(data).hexdigest(),
             "source_records": len(records),
             "kept_source_indices": [i for i, _, _ in kept],

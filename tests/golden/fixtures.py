@@ -118,3 +118,75 @@ def dequant(name="dequant-q8_0-q4k-q6k-q8k.bin"):
         out.append((dtype, n, b, r.floats(n)))
     r.done()
     return out
+
+
+# ---- GGML graph records (crates/tensor/tests/{extended,indexing}.rs) ------------
+
+# bytes per element / block and elements per block of the types in these records
+_GG_TYPES = {0: (4, 1), 26: (4, 1), 8: (34, 32), 10: (84, 256), 11: (110, 256), 12: (144, 256), 13: (176, 256),
+             14: (210, 256), 15: (292, 256)}
+
+
+@dataclass
+class GgTensor:
+    dtype: int
+    shape: tuple      # ne[0..3]
+    strides: tuple    # nb[0..3] in bytes (contiguous for expected outputs)
+    data: bytes
+
+    def contiguous(self):
+        """Rows of ne[0] elements, row (i1, i2, i3) at offset i1 nb1 + i2 nb2 +
+        i3 nb3 of the record, packed one after another (the reference's
+        Tensor::contiguous)."""
+        ts, bs = _GG_TYPES[self.dtype]
+        rb = self.shape[0] // bs * ts
+        out = bytearray()
+        for i3 in range(self.shape[3]):
+            for i2 in range(self.shape[2]):
+                for i1 in range(self.shape[1]):
+                    o = i1 * self.strides[1] + i2 * self.strides[2] + i3 * self.strides[3]
+                    out += self.data[o:o + rb]
+        return np.frombuffer(bytes(out), np.uint8).copy()
+
+
+@dataclass
+class GgCase:
+    name: str
+    tag: str
+    inputs: list
+    expected: GgTensor
+
+
+def ggml_cases(name):
+    """GGTR0002 records: mul-mat-broadcast.bin (MUL_MAT: weights, rhs) and
+    mul-mat-id.bin (MUL_MAT_ID: experts, rhs, ids), expected f32 output."""
+    r = _Reader(name, b"GGTR0002")
+
+    def u64():
+        return struct.unpack("<Q", r.take(8))[0]
+
+    def string():
+        return r.take(r.word()).decode()
+
+    def tensor(strided):
+        dtype = r.word()
+        shape = tuple(u64() for _ in range(4))
+        strides = tuple(u64() for _ in range(4)) if strided else None
+        data = r.take(u64())
+        if strides is None:
+            ts, bs = _GG_TYPES[dtype]
+            rb = shape[0] // bs * ts
+            strides = (ts, rb, rb * shape[1], rb * shape[1] * shape[2])
+        return GgTensor(dtype, shape, strides, data)
+
+    out = []
+    for _ in range(r.count):
+        nm, tag = string(), string()
+        r.word()
+        r.take(8 * r.word())
+        r.take(4 * r.word())
+        nt = r.word()
+        inputs = [tensor(True) for _ in range(nt)]
+        out.append(GgCase(nm, tag, inputs, tensor(False)))
+    r.done()
+    return out
