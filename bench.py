@@ -187,6 +187,47 @@ def run_config(rlq, ctx, dtype, rows, cols, batch, seed, steps, warmup, copies):
     return out, handles, host0, x
 
 
+def moe_decode(rlq, ctx, steps, warmup):
+    """MUL_MAT_ID at a Mixtral-8x7B FFN shape: 8 Q4_K experts of 14336x4096,
+    one token routed to 2 of them per step (one activation column shared by
+    both slots); the expert pair rotates over 4 disjoint pairs, so the 264 MB
+    of experts cannot sit in the 256 MB MALL.  One step = the column's Q8_K
+    quantizer, the id check, and one launch over both (token, slot) pairs."""
+    torch = rlq.torch
+    DT = rlq.DType
+    experts, rows, cols, slots = 8, 14336, 4096, 2
+    g = torch.Generator(device="cuda")
+    g.manual_seed(0x51A7E00E)
+    xw = torch.randn((experts * rows, cols), generator=g, device="cuda", dtype=torch.float32) * 0.02
+    packed = ctx.quantize(DT.Q4_K, xw)
+    ctx.sync()
+    del xw
+    W = rlq.Weights(ctx, DT.Q4_K, packed, rows, cols, experts)
+    del packed
+    x = torch.randn((1, 1, cols), generator=g, device="cuda", dtype=torch.float32)
+    ids = [torch.tensor([[2 * i, 2 * i + 1]], dtype=torch.int32, device="cuda") for i in range(4)]
+    y = torch.empty((1, slots, rows), device="cuda", dtype=torch.float32)
+    for i in range(warmup):
+        ctx.mul_mat_id(W, x, ids[i % 4], y=y)
+    ctx.sync()
+    stream = torch.cuda.current_stream()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record(stream)
+    for i in range(steps):
+        ctx.mul_mat_id(W, x, ids[i % 4], y=y)
+    end.record(stream)
+    torch.cuda.synchronize()
+    ctx.sync()
+    ms = start.elapsed_time(end) / steps
+    nbytes = slots * rlq.row_bytes(DT.Q4_K, cols) * rows + 4 * cols + 4 * slots * rows + 8
+    W.close()
+    return {"workload": "MUL_MAT_ID Q4_K, 8 experts of 14336x4096, 1 token, top-2 (quantizer + id check + one "
+                        "grouped matvec launch per step)",
+            "steps": steps, "us_per_step": round(ms * 1e3, 3), "bytes_per_step": nbytes,
+            "gbs": round(nbytes / (ms * 1e-3) / 1e9, 2), "frac_hbm": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+
+
 # Llama-3-8B decode-step shape: 32 layers, d_model 4096, 32 query / 8 KV heads of 128, FFN 14336,
 # vocabulary 128256, f32 KV cache of 1024 rows; Q4_K layer matrices and embedding, Q6_K output.
 LLAMA = dict(vocabulary=128256, width=4096, feed_forward=14336, heads=32, kv_heads=8, max_context=1024,
@@ -391,6 +432,8 @@ def main():
                 h.close()
             extra[name] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in o.items()}
             torch.cuda.empty_cache()
+        extra["moe_q4k_8x14336x4096_top2"] = moe_decode(rlq, ctx, max(200, args.steps // 4), args.warmup)
+        torch.cuda.empty_cache()
         result["extra"] = extra
     ctx.close()
     print(json.dumps(result), flush=True)
