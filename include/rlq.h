@@ -17,7 +17,8 @@
  *     this library's own; 21..23 stand for the model-runtime errors of the
  *     decode step (crates/model-runtime/src/lib.rs Error: InvalidConfig,
  *     InvalidToken, InvalidState); 24..26 for the tensor crate's errors of
- *     MUL_MAT / MUL_MAT_ID (Shape, Bounds, Unsupported).
+ *     MUL_MAT / MUL_MAT_ID (Shape, Bounds, Unsupported); 27..30 for the GGUF
+ *     crate's (Io, Invalid, Limit, Unsupported).
  *   - Validate before mutate: on any error, no output buffer is written
  *     (crates/quant/src/matvec.rs:31-56, encode.rs:37-100).
  *   - Host functions (`rlq_matvec`, `rlq_quantize_into`, ...) take host
@@ -77,8 +78,14 @@ typedef enum rlq_status {
     /* TensorError variants of the GGML ops (crates/tensor/src/lib.rs:35-50) */
     RLQ_TENSOR_SHAPE = 24,              /* Shape: incompatible MUL_MAT / MUL_MAT_ID dimensions */
     RLQ_TENSOR_BOUNDS = 25,             /* Bounds: an expert id outside [-1, experts); a = its index */
-    RLQ_TENSOR_UNSUPPORTED = 26         /* Unsupported: a right-hand side neither F32 nor the
+    RLQ_TENSOR_UNSUPPORTED = 26,        /* Unsupported: a right-hand side neither F32 nor the
                                            activation type; dtype = that type */
+    /* llama_gguf::Error variants (crates/gguf/src/lib.rs:26-32); a = the header
+       byte position of the failed check (IO: a = errno, b = the position) */
+    RLQ_GGUF_IO = 27,
+    RLQ_GGUF_INVALID = 28,
+    RLQ_GGUF_LIMIT = 29,
+    RLQ_GGUF_UNSUPPORTED = 30
 } rlq_status;
 
 typedef struct rlq_error {
@@ -305,6 +312,84 @@ int32_t rlq_llama_step(rlq_llama *model, float *hidden, uint64_t position, float
  * (feed_forward, the down projection's input).  Any output may be null. */
 int32_t rlq_llama_intermediates(const rlq_llama *model, float *qkv, float *attention, float *ffn,
                                 void *stream, rlq_error *err);
+
+/* ---- GGUF files (crates/gguf) ---------------------------------------------------
+ * Host-only: no device is used.  The reader follows RawGguf (crates/gguf/src/
+ * raw.rs:85-300) with Limits::default(): GGUF v2/v3 of either byte order,
+ * metadata in file order, tensor descriptors whose payloads follow each other
+ * padded to the alignment, tensor payloads read on demand.  Keys, strings and
+ * tensor names are byte strings (lengths given); lookups compare their
+ * C-string prefixes, first match in file order (the native getters). */
+typedef struct rlq_gguf rlq_gguf;
+
+/* RawGguf::open (raw.rs:66-80): header, then every tensor's payload bounds
+ * checked against the file length. */
+int32_t rlq_gguf_open(const char *path, rlq_gguf **out, rlq_error *err);
+/* RawGguf::read_header (raw.rs:80-84) over a memory image (copied): header
+ * only, payload bounds unchecked. */
+int32_t rlq_gguf_read_header_memory(const uint8_t *bytes, uint64_t len, rlq_gguf **out, rlq_error *err);
+void rlq_gguf_close(rlq_gguf *g);
+void rlq_gguf_header(const rlq_gguf *g, uint32_t *version, uint32_t *alignment, uint64_t *data_offset,
+                     uint64_t *n_kv, uint64_t *n_tensors, int32_t *big_endian);
+/* Metadata entry i in file order: key bytes, GGUF value type (0..12), the
+ * array element type, and count (array elements; string bytes; 1). */
+int32_t rlq_gguf_kv_at(const rlq_gguf *g, uint64_t i, const uint8_t **key, uint64_t *key_len, uint32_t *type,
+                       uint32_t *element_type, uint64_t *count, rlq_error *err);
+/* Scalar value (j = 0) or element j of a scalar array: its bits, zero-extended
+ * to 64 (bool as 0/1, as the reader normalizes it). */
+int32_t rlq_gguf_kv_scalar(const rlq_gguf *g, uint64_t i, uint64_t j, uint64_t *bits, rlq_error *err);
+/* String value (j = 0) or element j of a string array. */
+int32_t rlq_gguf_kv_string(const rlq_gguf *g, uint64_t i, uint64_t j, const uint8_t **s, uint64_t *len,
+                           rlq_error *err);
+/* First entry whose key's C-string prefix equals key's (raw.rs:320-326), or -1. */
+int64_t rlq_gguf_find_kv(const rlq_gguf *g, const uint8_t *key, uint64_t len);
+/* Tensor descriptor i: name bytes, stored rank, dims (padded with 1 to 4),
+ * type, offset within the data section and stored bytes. */
+int32_t rlq_gguf_tensor_at(const rlq_gguf *g, uint64_t i, const uint8_t **name, uint64_t *name_len, uint32_t *n_dims,
+                           uint64_t *dims, uint32_t *dtype, uint64_t *offset, uint64_t *bytes, rlq_error *err);
+int64_t rlq_gguf_find_tensor(const rlq_gguf *g, const uint8_t *name, uint64_t len);
+/* read_tensor (lib.rs:322-350): the stored bytes of tensor i; out_len must
+ * equal its byte count. */
+int32_t rlq_gguf_read_tensor(rlq_gguf *g, uint64_t i, void *out, uint64_t out_len, rlq_error *err);
+/* write_native_header (raw.rs:346-390): the header as gguf_get_meta_data
+ * writes it (the file's version and alignment, C-string tensor names,
+ * trailing unit dimensions dropped, padding to the data offset).  *len gets
+ * the size; out may be null to query it. */
+int32_t rlq_gguf_native_header(const rlq_gguf *g, uint8_t *out, uint64_t cap, uint64_t *len, rlq_error *err);
+
+/* One metadata entry to write.  type 0..12 (GGUF value types).  Scalars:
+ * data holds the value's 1/2/4/8 little-endian bytes.  Strings (8): data
+ * holds count bytes.  Arrays (9): element_type and count elements; scalar
+ * elements packed in data, string elements concatenated in data with their
+ * byte lengths in lengths. */
+typedef struct rlq_gguf_kv {
+    const uint8_t *key;
+    uint64_t key_len;
+    uint32_t type, element_type;
+    uint64_t count;
+    const void *data;
+    const uint64_t *lengths;
+} rlq_gguf_kv;
+/* One tensor to write: dims[0] contiguous (GGML order), data = its stored
+ * bytes (row_bytes(dims[0]) x dims[1] x ...). */
+typedef struct rlq_gguf_tensor {
+    const uint8_t *name;
+    uint64_t name_len;
+    uint32_t n_dims;
+    uint64_t dims[4];
+    uint32_t dtype;
+    const void *data;
+} rlq_gguf_tensor;
+/* write_raw_header (writer.rs:476-486): a GGUF v3 little-endian header in the
+ * given order, validated before any byte is produced (writer.rs:227-350),
+ * padded to the data offset; *file_bytes = the whole file's size. */
+int32_t rlq_gguf_write_header(const rlq_gguf_kv *kv, uint64_t n_kv, const rlq_gguf_tensor *tensors,
+                              uint64_t n_tensors, uint8_t *out, uint64_t cap, uint64_t *len, uint64_t *file_bytes,
+                              rlq_error *err);
+/* write_ordered (writer.rs:550-583): header, then each payload padded with
+ * zeros to the alignment. */
+int32_t rlq_gguf_write(const char *path, const rlq_gguf_kv *kv, uint64_t n_kv, const rlq_gguf_tensor *tensors,
+                       uint64_t n_tensors, rlq_error *err);
 
 #ifdef __cplusplus
 }

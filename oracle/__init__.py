@@ -30,6 +30,7 @@ ERROR_NAMES = {
     17: "UnrepresentableScale", 18: "DeviceError", 19: "Unimplemented", 20: "InvalidArgument",
     21: "InvalidConfig", 22: "InvalidToken", 23: "InvalidState",
     24: "Shape", 25: "Bounds", 26: "Unsupported",
+    27: "GgufIo", 28: "GgufInvalid", 29: "GgufLimit", 30: "GgufUnsupported",
 }
 F32 = 0
 SHAPE, BOUNDS, UNSUPPORTED = 24, 25, 26

@@ -89,6 +89,7 @@ ERROR_NAMES = {
     17: "UnrepresentableScale", 18: "DeviceError", 19: "Unimplemented", 20: "InvalidArgument",
     21: "InvalidConfig", 22: "InvalidToken", 23: "InvalidState",
     24: "Shape", 25: "Bounds", 26: "Unsupported",
+    27: "GgufIo", 28: "GgufInvalid", 29: "GgufLimit", 30: "GgufUnsupported",
 }
 
 
@@ -150,6 +151,23 @@ SIGNATURES = {
     "rlq_quantize_device": ([_P, _U32, _P, _U64, _U64, _P, _P, _E], _I32),
     "rlq_sync": ([_P, _P, _E], _I32),
     "rlq_block_sums": ([_P, _P, _P, _U64, _P, _P, _P, _E], _I32),
+    "rlq_gguf_open": ([ctypes.c_char_p, ctypes.POINTER(_P), _E], _I32),
+    "rlq_gguf_read_header_memory": ([_P, _U64, ctypes.POINTER(_P), _E], _I32),
+    "rlq_gguf_close": ([_P], None),
+    "rlq_gguf_header": ([_P, ctypes.POINTER(_U32), ctypes.POINTER(_U32), ctypes.POINTER(_U64), ctypes.POINTER(_U64),
+                         ctypes.POINTER(_U64), ctypes.POINTER(_I32)], None),
+    "rlq_gguf_kv_at": ([_P, _U64, ctypes.POINTER(_P), ctypes.POINTER(_U64), ctypes.POINTER(_U32),
+                        ctypes.POINTER(_U32), ctypes.POINTER(_U64), _E], _I32),
+    "rlq_gguf_kv_scalar": ([_P, _U64, _U64, ctypes.POINTER(_U64), _E], _I32),
+    "rlq_gguf_kv_string": ([_P, _U64, _U64, ctypes.POINTER(_P), ctypes.POINTER(_U64), _E], _I32),
+    "rlq_gguf_find_kv": ([_P, _P, _U64], ctypes.c_int64),
+    "rlq_gguf_tensor_at": ([_P, _U64, ctypes.POINTER(_P), ctypes.POINTER(_U64), ctypes.POINTER(_U32), _P,
+                            ctypes.POINTER(_U32), ctypes.POINTER(_U64), ctypes.POINTER(_U64), _E], _I32),
+    "rlq_gguf_find_tensor": ([_P, _P, _U64], ctypes.c_int64),
+    "rlq_gguf_read_tensor": ([_P, _U64, _P, _U64, _E], _I32),
+    "rlq_gguf_native_header": ([_P, _P, _U64, ctypes.POINTER(_U64), _E], _I32),
+    "rlq_gguf_write_header": ([_P, _U64, _P, _U64, _P, _U64, ctypes.POINTER(_U64), ctypes.POINTER(_U64), _E], _I32),
+    "rlq_gguf_write": ([ctypes.c_char_p, _P, _U64, _P, _U64, _E], _I32),
     "rlq_llama_create": ([_P, _P, _P, ctypes.POINTER(_P), _E], _I32),
     "rlq_llama_destroy": ([_P], None),
     "rlq_llama_truncate": ([_P, _U64, _E], _I32),
@@ -538,3 +556,177 @@ class LlamaModel:
         _check(_lib.rlq_llama_intermediates(self._h, _dev_ptr(qkv, torch.float32), _dev_ptr(att, torch.float32),
                                             _dev_ptr(gu, torch.float32), _stream_ptr(stream), ctypes.byref(err)), err)
         return qkv, att, gu
+
+
+# ---- GGUF files (host only) -------------------------------------------------------
+
+GGUF_SCALAR_BYTES = {0: 1, 1: 1, 2: 2, 3: 2, 4: 4, 5: 4, 6: 4, 7: 1, 10: 8, 11: 8, 12: 8}
+
+
+class GgufFile:
+    """rlq_gguf: RawGguf (crates/gguf/src/raw.rs) over a file (open) or a
+    memory image (from_bytes, header only).  Keys, strings and names are bytes."""
+
+    def __init__(self, handle):
+        self._h = handle
+        v, a, nk, nt = _U32(), _U32(), _U64(), _U64()
+        d, big = _U64(), _I32()
+        _lib.rlq_gguf_header(self._h, ctypes.byref(v), ctypes.byref(a), ctypes.byref(d), ctypes.byref(nk),
+                             ctypes.byref(nt), ctypes.byref(big))
+        self.version, self.alignment, self.data_offset = v.value, a.value, d.value
+        self.n_kv, self.n_tensors, self.big_endian = nk.value, nt.value, bool(big.value)
+
+    @classmethod
+    def open(cls, path):
+        h, err = ctypes.c_void_p(), _Err()
+        _check(_lib.rlq_gguf_open(os.fsencode(path), ctypes.byref(h), ctypes.byref(err)), err)
+        return cls(h)
+
+    @classmethod
+    def from_bytes(cls, data):
+        buf = _u8(np.frombuffer(bytes(data), np.uint8))
+        h, err = ctypes.c_void_p(), _Err()
+        _check(_lib.rlq_gguf_read_header_memory(_ptr(buf), buf.size, ctypes.byref(h), ctypes.byref(err)), err)
+        return cls(h)
+
+    def close(self):
+        if getattr(self, "_h", None):
+            if not _exiting:
+                _lib.rlq_gguf_close(self._h)
+            self._h = None
+
+    __del__ = close
+
+    def kv(self, i):
+        """(key, type, value): value is an int (scalar bits), bytes (string),
+        or (element_type, [int | bytes]) for arrays."""
+        k, kl, ty, el, n, err = ctypes.c_void_p(), _U64(), _U32(), _U32(), _U64(), _Err()
+        _check(_lib.rlq_gguf_kv_at(self._h, i, ctypes.byref(k), ctypes.byref(kl), ctypes.byref(ty), ctypes.byref(el),
+                                   ctypes.byref(n), ctypes.byref(err)), err)
+        key = ctypes.string_at(k.value, kl.value) if kl.value else b""
+        if ty.value == 8:
+            return key, 8, self._string(i, 0)
+        if ty.value == 9:
+            items = [self._string(i, j) if el.value == 8 else self._scalar(i, j) for j in range(n.value)]
+            return key, 9, (el.value, items)
+        return key, ty.value, self._scalar(i, 0)
+
+    def _scalar(self, i, j):
+        b, err = _U64(), _Err()
+        _check(_lib.rlq_gguf_kv_scalar(self._h, i, j, ctypes.byref(b), ctypes.byref(err)), err)
+        return b.value
+
+    def _string(self, i, j):
+        p, n, err = ctypes.c_void_p(), _U64(), _Err()
+        _check(_lib.rlq_gguf_kv_string(self._h, i, j, ctypes.byref(p), ctypes.byref(n), ctypes.byref(err)), err)
+        return ctypes.string_at(p.value, n.value) if n.value else b""
+
+    def find_kv(self, key):
+        key = bytes(key)
+        r = _lib.rlq_gguf_find_kv(self._h, ctypes.c_char_p(key), len(key))
+        return None if r < 0 else r
+
+    def tensor(self, i):
+        """(name, dims (stored rank), dtype, offset, bytes)."""
+        nm, nl, nd, dt, off, nb, err = ctypes.c_void_p(), _U64(), _U32(), _U32(), _U64(), _U64(), _Err()
+        dims = (_U64 * 4)()
+        _check(_lib.rlq_gguf_tensor_at(self._h, i, ctypes.byref(nm), ctypes.byref(nl), ctypes.byref(nd), dims,
+                                       ctypes.byref(dt), ctypes.byref(off), ctypes.byref(nb), ctypes.byref(err)), err)
+        name = ctypes.string_at(nm.value, nl.value) if nl.value else b""
+        return name, list(dims)[:nd.value], dt.value, off.value, nb.value
+
+    def find_tensor(self, name):
+        name = bytes(name)
+        r = _lib.rlq_gguf_find_tensor(self._h, ctypes.c_char_p(name), len(name))
+        return None if r < 0 else r
+
+    def read_tensor(self, i):
+        nb = self.tensor(i)[4]
+        out = np.zeros(nb, np.uint8)
+        err = _Err()
+        _check(_lib.rlq_gguf_read_tensor(self._h, i, _ptr(out) if nb else None, nb, ctypes.byref(err)), err)
+        return out
+
+    def native_header(self):
+        n, err = _U64(), _Err()
+        _check(_lib.rlq_gguf_native_header(self._h, None, 0, ctypes.byref(n), ctypes.byref(err)), err)
+        out = np.zeros(n.value, np.uint8)
+        _check(_lib.rlq_gguf_native_header(self._h, _ptr(out), n.value, ctypes.byref(n), ctypes.byref(err)), err)
+        return out.tobytes()
+
+
+class _GgufKv(ctypes.Structure):
+    _fields_ = [("key", _P), ("key_len", _U64), ("type", _U32), ("element_type", _U32), ("count", _U64),
+                ("data", _P), ("lengths", _P)]
+
+
+class _GgufTensor(ctypes.Structure):
+    _fields_ = [("name", _P), ("name_len", _U64), ("n_dims", _U32), ("dims", _U64 * 4), ("dtype", _U32),
+                ("data", _P)]
+
+
+def _gguf_structs(kvs, tensors):
+    """kvs: [(key bytes, type, value)] with value as for GgufFile.kv;
+    tensors: [(name bytes, dims, dtype, payload uint8 array or None)]."""
+    keep = []
+    ks = (_GgufKv * max(1, len(kvs)))()
+    for i, (key, ty, val) in enumerate(kvs):
+        key = bytes(key)
+        keep.append(key)
+        k = ks[i]
+        k.key, k.key_len, k.type = ctypes.cast(ctypes.c_char_p(key), _P), len(key), ty
+        if ty == 8:
+            buf = bytes(val)
+            keep.append(buf)
+            k.count, k.data = len(buf), ctypes.cast(ctypes.c_char_p(buf), _P)
+        elif ty == 9:
+            el, items = val
+            k.element_type, k.count = el, len(items)
+            if el == 8:
+                buf = b"".join(bytes(x) for x in items)
+                lens = (_U64 * max(1, len(items)))(*[len(x) for x in items])
+                keep += [buf, lens]
+                k.data, k.lengths = ctypes.cast(ctypes.c_char_p(buf), _P), ctypes.cast(lens, _P)
+            else:
+                w = GGUF_SCALAR_BYTES.get(el, 1)
+                buf = b"".join(int(x).to_bytes(w, "little") for x in items)
+                keep.append(buf)
+                k.data = ctypes.cast(ctypes.c_char_p(buf), _P)
+        else:
+            buf = int(val).to_bytes(GGUF_SCALAR_BYTES.get(ty, 8), "little")
+            keep.append(buf)
+            k.count, k.data = 1, ctypes.cast(ctypes.c_char_p(buf), _P)
+    ts = (_GgufTensor * max(1, len(tensors)))()
+    for i, (name, dims, dtype, data) in enumerate(tensors):
+        name = bytes(name)
+        keep.append(name)
+        t = ts[i]
+        t.name, t.name_len, t.n_dims, t.dtype = ctypes.cast(ctypes.c_char_p(name), _P), len(name), len(dims), dtype
+        for d, v in enumerate(dims):
+            t.dims[d] = v
+        if data is not None:
+            arr = _u8(data)
+            keep.append(arr)
+            t.data = _ptr(arr)
+    return ks, ts, keep
+
+
+def gguf_header(kvs, tensors):
+    """write_raw_header: (header bytes padded to the data offset, file bytes)."""
+    ks, ts, keep = _gguf_structs(kvs, tensors)
+    n, fb, err = _U64(), _U64(), _Err()
+    _check(_lib.rlq_gguf_write_header(ks, len(kvs), ts, len(tensors), None, 0, ctypes.byref(n), ctypes.byref(fb),
+                                      ctypes.byref(err)), err)
+    out = np.zeros(n.value, np.uint8)
+    _check(_lib.rlq_gguf_write_header(ks, len(kvs), ts, len(tensors), _ptr(out), n.value, ctypes.byref(n),
+                                      ctypes.byref(fb), ctypes.byref(err)), err)
+    del keep
+    return out.tobytes(), fb.value
+
+
+def gguf_write(path, kvs, tensors):
+    """write_ordered: a GGUF v3 file of the given metadata and tensors."""
+    ks, ts, keep = _gguf_structs(kvs, tensors)
+    err = _Err()
+    _check(_lib.rlq_gguf_write(os.fsencode(path), ks, len(kvs), ts, len(tensors), ctypes.byref(err)), err)
+    del keep

@@ -17,6 +17,8 @@ import sys
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 SOURCES = ["api.hip", "gemm.hip", "llama.hip", "matvec.hip", "quantize.hip"]
+HOST_SOURCES = ["gguf.cpp"]  # host-only C++ (no device code), built with g++
+CXX = os.environ.get("CXX", "g++")
 LIB = os.path.join(HERE, "librlq.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
@@ -41,9 +43,15 @@ def build(verbose=False):
     os.makedirs(out_dir, exist_ok=True)
     objs = [os.path.join(out_dir, s.replace(".hip", ".o")) for s in SOURCES]
     cmds = [[HIPCC, *FLAGS, "-c", os.path.join(HERE, "csrc", s), "-o", o] for s, o in zip(SOURCES, objs)]
+    host_objs = [os.path.join(out_dir, s.replace(".cpp", ".o")) for s in HOST_SOURCES]
+    cmds += [[CXX, "-O2", "-std=c++17", "-fPIC", "-Wall", "-I" + os.path.join(ROOT, "include"),
+              "-I" + os.path.join(HERE, "csrc"), "-c", os.path.join(HERE, "csrc", s), "-o", o]
+             for s, o in zip(HOST_SOURCES, host_objs)]
+    srcs = SOURCES + HOST_SOURCES
+    objs = objs + host_objs
     with concurrent.futures.ThreadPoolExecutor(len(cmds)) as ex:
         results = list(ex.map(_run, cmds))
-    for (rc, msg), s in zip(results, SOURCES):
+    for (rc, msg), s in zip(results, srcs):
         if msg and (verbose or rc):
             print(f"[{s}]\n{msg}", file=sys.stderr)
         if rc:

@@ -32,6 +32,10 @@ tests:
         with tensor = dtype shape[4 x u64] (strides[4 x u64], inputs only) nbytes[u64] bytes
         (strings are u32 length + UTF-8).  Kept: the GGML MUL_MAT and MUL_MAT_ID
         graphs whose weight (first input) type is on the path.
+Copied whole (GGUF reader corpus and a real file; crates/gguf/tests/raw_native.rs:286-300):
+  fixtures/gguf-bytes/{reader,booleans}-data.bin and -reference.tsv (1093 + 512
+  header cases with the original C getters' observations) and
+  fixtures/inference/ggml-vocab-llama-spm.gguf (a vocabulary-only Llama GGUF).
 """
 import hashlib
 import json
@@ -135,6 +139,15 @@ FILES = [
 ]
 
 
+COPIES = [
+    ("fixtures/gguf-bytes/reader-data.bin", "gguf-reader-data.bin"),
+    ("fixtures/gguf-bytes/reader-reference.tsv", "gguf-reader-reference.tsv"),
+    ("fixtures/gguf-bytes/booleans-data.bin", "gguf-booleans-data.bin"),
+    ("fixtures/gguf-bytes/booleans-reference.tsv", "gguf-booleans-reference.tsv"),
+    ("fixtures/inference/ggml-vocab-llama-spm.gguf", "ggml-vocab-llama-spm.gguf"),
+]
+
+
 def main():
     root = sys.argv[1] if len(sys.argv) > 1 else "/root/reference"
     here = os.path.dirname(os.path.abspath(__file__))
@@ -161,6 +174,13 @@ def main():
             "bytes": len(out),
         }
         print(f"{dst}: {len(kept)} of {len(records)} records, {len(out)} bytes, {per_type}")
+    for src, dst in COPIES:
+        data = open(os.path.join(root, src), "rb").read()
+        with open(os.path.join(here, dst), "wb") as f:
+            f.write(data)
+        manifest["files"][dst] = {"source": src, "source_sha256": hashlib.sha256(data).hexdigest(),
+                                  "sha256": hashlib.sha256(data).hexdigest(), "bytes": len(data), "copied": True}
+        print(f"{dst}: copied, {len(data)} bytes")
     with open(os.path.join(here, "manifest.json"), "w") as f:
         json.dump(manifest, f, indent=1)
         f.write("\n")
