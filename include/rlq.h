@@ -265,6 +265,10 @@ typedef struct rlq_llama_layer {
     const void *query, *key, *value, *attention_output;
     const float *feed_forward_norm;
     const void *gate, *up, *down;
+    /* types of query, key, value, attention_output, gate, up, down (a GGUF
+     * file types every tensor on its own: Q4_K_M keeps some attn_v and
+     * ffn_down in Q6_K); 0 = rlq_llama_config.weight_type */
+    uint32_t types[7];
 } rlq_llama_layer;
 
 /* LlamaWeights: embedding (vocabulary x width), output_norm, output
@@ -290,6 +294,32 @@ int32_t rlq_llama_create(rlq_context *ctx, const rlq_llama_config *cfg, const rl
                          rlq_llama **out, rlq_error *err);
 void rlq_llama_destroy(rlq_llama *model);
 /* Drop the KV rows at and above `rows` (0 starts a new sequence). */
+/* The inference crate's llama loader (crates/inference/src/loader.rs:242-410)
+ * over a GGUF file: hparams from the llama.* metadata (exact UINT32 / finite
+ * FLOAT32 values), the vocabulary size from tokenizer.ggml.tokens, max_context
+ * = min(llama.context_length, context_length), every tensor checked against
+ * its GGML shape and typed on its own (per-matrix types), output.weight
+ * optional (absent: the token embedding projects).  Failures: the GGUF
+ * reader's codes; RLQ_GGUF_INVALID / RLQ_GGUF_UNSUPPORTED (the loader's
+ * Error::Invalid / Unsupported) with a = the check: 1 context_length 0,
+ * 2 architecture, 3 general.type, 4 nextn layers, 5 Hadamard transforms,
+ * 6 tokenizer.ggml.tokens, 7-13 embedding_length, head_count, width % heads,
+ * head_count_kv, block_count (1..512), feed_forward_length, context_length,
+ * 14 rope.dimension_count, 15 key/value_length, 16 sliding window / experts,
+ * 17 causal, 18-20 RoPE scaling, 21 qk_norm, 22-24 rms epsilon, freq_base,
+ * attention.scale, 30-32 token_embd / output_norm / output, 40-48 the layer
+ * tensors (q, k, v, output, gate, up, down, attn_norm, ffn_norm),
+ * 50 rope_freqs, 51 a tensor the model does not use (b = its index);
+ * RLQ_UNIMPLEMENTED for a matrix type off the path, a non-F32 norm (dtype =
+ * the type, a = the check) or biases (a = 49); then rlq_llama_create's own
+ * checks. */
+int32_t rlq_llama_create_from_gguf(rlq_context *ctx, const char *path, uint64_t context_length, rlq_llama **out,
+                                   rlq_error *err);
+
+/* The configuration a model was created with (a GGUF-loaded one: as the
+ * loader derived it; weight_type = the type of layer 0's query). */
+void rlq_llama_config_of(const rlq_llama *model, rlq_llama_config *out);
+
 int32_t rlq_llama_truncate(rlq_llama *model, uint64_t rows, rlq_error *err);
 /* KV rows held: the insertion index of the next step. */
 uint64_t rlq_llama_cached(const rlq_llama *model);

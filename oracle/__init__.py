@@ -359,8 +359,19 @@ LAYER_FIELDS = ("attention_norm", "query", "key", "value", "attention_output", "
                 "down")
 
 
+# the seven matrices in the order of a layer's per-matrix type array
+MATRIX_FIELDS = ("query", "key", "value", "attention_output", "gate", "up", "down")
+
+
 class _Layer(ctypes.Structure):
-    _fields_ = [(f, ctypes.c_void_p) for f in LAYER_FIELDS]
+    _fields_ = [(f, ctypes.c_void_p) for f in LAYER_FIELDS] + [("types", ctypes.c_uint32 * 7)]
+
+
+def layer_types(L):
+    """A layer dict's optional per-matrix types ({name: type}), 0 = the
+    model's weight_type."""
+    t = L.get("types", {})
+    return [int(t.get(f, 0)) for f in MATRIX_FIELDS]
 
 
 class _Model(ctypes.Structure):
@@ -392,6 +403,8 @@ class LlamaOracle:
         for i, L in enumerate(tensors["layers"]):
             for f in LAYER_FIELDS:
                 setattr(self._layers[i], f, p(L[f], f.endswith("norm")))
+            for k, ty in enumerate(layer_types(L)):
+                self._layers[i].types[k] = ty
         self._m = _Model(cfg.vocabulary, cfg.width, cfg.feed_forward, cfg.heads, cfg.kv_heads, cfg.max_context, n,
                          cfg.rms_epsilon, cfg.rope_base, cfg.attention_scale, cfg.weight_type, cfg.output_type,
                          cfg.embedding_type, p(tensors["embedding"], False), p(tensors["output_norm"], True),

@@ -146,6 +146,9 @@ typedef struct oracle_llama_layer {
     const uint8_t *query, *key, *value, *attention_output;
     const float *feed_forward_norm;
     const uint8_t *gate, *up, *down;
+    /* types of query, key, value, attention_output, gate, up, down; 0 = the
+     * model's weight_type (a GGUF file types every tensor on its own) */
+    uint32_t types[7];
 } oracle_llama_layer;
 
 /* LlamaConfig (llama.rs:6-17) and LlamaWeights.  attention_scale 0 means

@@ -204,6 +204,10 @@ int oracle_attention(const float *q, const float *keys, const float *values, uin
 
 /* Matrix::multiply (math.rs:144-169) for a quantized matrix: finite input,
  * llama_quant::matvec, finite output. */
+static uint32_t layer_type(const oracle_llama_model *m, const oracle_llama_layer *L, int k) {
+    return L->types[k] ? L->types[k] : m->weight_type;
+}
+
 static int multiply(uint32_t t, const uint8_t *w, uint64_t rows, uint64_t cols, const float *x, float *y,
                     int threads) {
     if (!all_finite(x, cols)) return ORC_NON_FINITE_INPUT;
@@ -246,25 +250,25 @@ int oracle_llama_step(const oracle_llama_model *m, float *hidden, uint64_t posit
         const oracle_llama_layer *L = &m->layers[l];
         float *kc = k_cache + l * m->max_context * kvw, *vc = v_cache + l * m->max_context * kvw;
         rc = oracle_rms_norm(hidden, L->attention_norm, W, m->rms_epsilon, norm);
-        if (rc == ORC_OK) rc = multiply(m->weight_type, L->query, W, W, norm, q, threads);
-        if (rc == ORC_OK) rc = multiply(m->weight_type, L->key, kvw, W, norm, k, threads);
-        if (rc == ORC_OK) rc = multiply(m->weight_type, L->value, kvw, W, norm, v, threads);
+        if (rc == ORC_OK) rc = multiply(layer_type(m, L, 0), L->query, W, W, norm, q, threads);
+        if (rc == ORC_OK) rc = multiply(layer_type(m, L, 1), L->key, kvw, W, norm, k, threads);
+        if (rc == ORC_OK) rc = multiply(layer_type(m, L, 2), L->value, kvw, W, norm, v, threads);
         if (rc != ORC_OK) break;
         oracle_rope(q, W, hd, position, m->rope_base);
         oracle_rope(k, kvw, hd, position, m->rope_base);
         memcpy(kc + n_cached * kvw, k, kvw * sizeof(float));
         memcpy(vc + n_cached * kvw, v, kvw * sizeof(float));
         rc = oracle_attention(q, kc, vc, n_cached + 1, H, KVH, hd, scale, att);
-        if (rc == ORC_OK) rc = multiply(m->weight_type, L->attention_output, W, W, att, proj, threads);
+        if (rc == ORC_OK) rc = multiply(layer_type(m, L, 3), L->attention_output, W, W, att, proj, threads);
         if (rc != ORC_OK) break;
         for (uint64_t i = 0; i < W; ++i) hidden[i] += proj[i];
         rc = oracle_rms_norm(hidden, L->feed_forward_norm, W, m->rms_epsilon, norm);
-        if (rc == ORC_OK) rc = multiply(m->weight_type, L->gate, F, W, norm, gate, threads);
-        if (rc == ORC_OK) rc = multiply(m->weight_type, L->up, F, W, norm, up, threads);
+        if (rc == ORC_OK) rc = multiply(layer_type(m, L, 4), L->gate, F, W, norm, gate, threads);
+        if (rc == ORC_OK) rc = multiply(layer_type(m, L, 5), L->up, F, W, norm, up, threads);
         if (rc != ORC_OK) break;
         oracle_silu(gate, F);
         for (uint64_t i = 0; i < F; ++i) gate[i] *= up[i];
-        rc = multiply(m->weight_type, L->down, W, F, gate, proj, threads);
+        rc = multiply(layer_type(m, L, 6), L->down, W, F, gate, proj, threads);
         if (rc != ORC_OK) break;
         for (uint64_t i = 0; i < W; ++i) hidden[i] += proj[i];
         if (!all_finite(hidden, W)) rc = ORC_NON_FINITE_INPUT;

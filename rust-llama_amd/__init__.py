@@ -169,6 +169,8 @@ SIGNATURES = {
     "rlq_gguf_write_header": ([_P, _U64, _P, _U64, _P, _U64, ctypes.POINTER(_U64), ctypes.POINTER(_U64), _E], _I32),
     "rlq_gguf_write": ([ctypes.c_char_p, _P, _U64, _P, _U64, _E], _I32),
     "rlq_llama_create": ([_P, _P, _P, ctypes.POINTER(_P), _E], _I32),
+    "rlq_llama_create_from_gguf": ([_P, ctypes.c_char_p, _U64, ctypes.POINTER(_P), _E], _I32),
+    "rlq_llama_config_of": ([_P, _P], None),
     "rlq_llama_destroy": ([_P], None),
     "rlq_llama_truncate": ([_P, _U64, _E], _I32),
     "rlq_llama_cached": ([_P], _U64),
@@ -462,7 +464,11 @@ class LlamaConfig(ctypes.Structure):
 
 class _LayerT(ctypes.Structure):
     _fields_ = [("attention_norm", _P), ("query", _P), ("key", _P), ("value", _P), ("attention_output", _P),
-                ("feed_forward_norm", _P), ("gate", _P), ("up", _P), ("down", _P)]
+                ("feed_forward_norm", _P), ("gate", _P), ("up", _P), ("down", _P), ("types", _U32 * 7)]
+
+
+# the seven matrices in the order of rlq_llama_layer.types
+MATRIX_FIELDS = ("query", "key", "value", "attention_output", "gate", "up", "down")
 
 
 class _TensorsT(ctypes.Structure):
@@ -477,9 +483,22 @@ LAYER_FIELDS = ("attention_norm", "query", "key", "value", "attention_output", "
 class LlamaModel:
     """LlamaModel (llama.rs) on the GPU.  `tensors` is a dict with
     `embedding`, `output_norm`, `output` and `layers` (a list of dicts with
-    LAYER_FIELDS): GGUF bytes of the matrices (rows contiguous) and f32 norm
-    weights, either all numpy arrays or all torch tensors on the GPU.  The
-    model keeps its own tiled copy; the tensors may be dropped afterwards."""
+    LAYER_FIELDS and optionally `types`, {matrix name: dtype} for matrices
+    not of config.weight_type): GGUF bytes of the matrices (rows contiguous)
+    and f32 norm weights, either all numpy arrays or all torch tensors on the
+    GPU.  The model keeps its own tiled copy; the tensors may be dropped
+    afterwards.  LlamaModel.from_gguf loads a GGUF file instead."""
+
+    @classmethod
+    def from_gguf(cls, ctx, path, context_length):
+        """rlq_llama_create_from_gguf: the inference crate's llama loader."""
+        self = cls.__new__(cls)
+        h, err = ctypes.c_void_p(), _Err()
+        _check(_lib.rlq_llama_create_from_gguf(ctx._h, os.fsencode(path), int(context_length), ctypes.byref(h),
+                                               ctypes.byref(err)), err)
+        self._h, self.ctx, self.config = h, ctx, LlamaConfig()
+        _lib.rlq_llama_config_of(h, ctypes.byref(self.config))
+        return self
 
     def __init__(self, ctx, config, tensors):
         on_dev = torch is not None and isinstance(tensors["embedding"], torch.Tensor)
@@ -496,6 +515,9 @@ class LlamaModel:
         for i, L in enumerate(tensors["layers"]):
             for f in LAYER_FIELDS:
                 setattr(layers[i], f, ptr(L[f], f.endswith("norm")))
+            types = L.get("types", {})
+            for k, f in enumerate(MATRIX_FIELDS):
+                layers[i].types[k] = int(types.get(f, 0))
         t = _TensorsT(ptr(tensors["embedding"], False), ptr(tensors["output_norm"], True),
                       ptr(tensors["output"], False), layers, 1 if on_dev else 0)
         h, err = ctypes.c_void_p(), _Err()

@@ -7,9 +7,11 @@
 #include "rlq.h"
 
 #include <math.h>
+#include <string.h>
 
 #include <mutex>
 #include <new>
+#include <string>
 #include <vector>
 
 #include "rlq_device.hpp"
@@ -606,6 +608,11 @@ int32_t rlq_llama_create(rlq_context* ctx, const rlq_llama_config* cfg, const rl
         if (!L.attention_norm || !L.query || !L.key || !L.value || !L.attention_output || !L.feed_forward_norm ||
             !L.gate || !L.up || !L.down)
             return fail(err, RLQ_INVALID_ARGUMENT, 0, l);
+        for (int k = 0; k < 7; ++k) {  // per-matrix types: on the path
+            const uint32_t ty = L.types[k] ? L.types[k] : cfg->weight_type;
+            if (!dtype_known(ty)) return fail(err, RLQ_INVALID_TYPE, ty, l, k);
+            if (!path_weight(ty)) return fail(err, RLQ_UNIMPLEMENTED, ty, l, k);
+        }
     }
     DeviceGuard g(ctx->device);
     rlq_llama* m = new (std::nothrow) rlq_llama;
@@ -616,7 +623,8 @@ int32_t rlq_llama_create(rlq_context* ctx, const rlq_llama_config* cfg, const rl
     for (uint64_t l = 0; l < cfg->n_layers; ++l) {
         const rlq_llama_layer& L = t->layers[l];
         layers[l] = LlamaHostLayer{L.attention_norm, L.query, L.key, L.value, L.attention_output,
-                                   L.feed_forward_norm, L.gate, L.up, L.down};
+                                   L.feed_forward_norm, L.gate, L.up, L.down, {}};
+        for (int k = 0; k < 7; ++k) layers[l].types[k] = L.types[k] ? L.types[k] : cfg->weight_type;
     }
     const LlamaDims d{cfg->vocabulary, cfg->width, cfg->feed_forward, cfg->heads, cfg->kv_heads, cfg->max_context,
                       cfg->n_layers, cfg->rms_epsilon, cfg->rope_base, cfg->attention_scale, cfg->weight_type,
@@ -630,6 +638,253 @@ int32_t rlq_llama_create(rlq_context* ctx, const rlq_llama_config* cfg, const rl
     }
     *out = m;
     return ok(err);
+}
+
+// ---- LlamaModel from a GGUF file (crates/inference/src/loader.rs:242-410) ----------
+
+namespace {
+
+struct GgufReader {
+    rlq_gguf* g = nullptr;
+    ~GgufReader() { rlq_gguf_close(g); }
+    int64_t find(const char* key) const { return rlq_gguf_find_kv(g, (const uint8_t*)key, strlen(key)); }
+    uint32_t type(int64_t i) const {
+        uint32_t t = 0;
+        rlq_gguf_kv_at(g, (uint64_t)i, nullptr, nullptr, &t, nullptr, nullptr, nullptr);
+        return t;
+    }
+    uint64_t bits(int64_t i) const {
+        uint64_t b = 0;
+        rlq_gguf_kv_scalar(g, (uint64_t)i, 0, &b, nullptr);
+        return b;
+    }
+    std::string str(int64_t i) const {
+        const uint8_t* p = nullptr;
+        uint64_t n = 0;
+        if (rlq_gguf_kv_string(g, (uint64_t)i, 0, &p, &n, nullptr) != RLQ_OK) return std::string();
+        return std::string((const char*)p, n);
+    }
+};
+
+// Loader check failures: a = the check number of rlq_llama_create_from_gguf.
+constexpr int32_t kInvalid = RLQ_GGUF_INVALID, kUnsupported = RLQ_GGUF_UNSUPPORTED;
+
+}  // namespace
+
+int32_t rlq_llama_create_from_gguf(rlq_context* ctx, const char* path, uint64_t context_length, rlq_llama** out,
+                                   rlq_error* err) {
+    if (!ctx || !path || !out) return fail(err, RLQ_INVALID_ARGUMENT);
+    if (context_length == 0) return fail(err, kInvalid, 0, 1);  // validate_options
+    GgufReader r;
+    int32_t rc = rlq_gguf_open(path, &r.g, err);
+    if (rc) return rc;
+    // loader.rs:12-30: hparams are exact UINT32 / finite FLOAT32 values
+    auto uint = [&](const char* key, int64_t dflt, uint64_t check, uint64_t* v) -> int32_t {
+        const int64_t i = r.find(key);
+        if (i < 0) {
+            if (dflt < 0) return fail(err, kInvalid, 0, check);
+            *v = (uint64_t)dflt;
+            return RLQ_OK;
+        }
+        if (r.type(i) != 4) return fail(err, kInvalid, 0, check);
+        *v = r.bits(i);
+        return RLQ_OK;
+    };
+    auto real = [&](const char* key, float dflt, uint64_t check, float* v) -> int32_t {
+        const int64_t i = r.find(key);
+        if (i < 0) {
+            *v = dflt;
+            return RLQ_OK;
+        }
+        if (r.type(i) != 6) return fail(err, kInvalid, 0, check);
+        const uint32_t b = (uint32_t)r.bits(i);
+        memcpy(v, &b, 4);
+        if (!(fabsf(*v) <= 3.402823466e38f)) return fail(err, kInvalid, 0, check);
+        return RLQ_OK;
+    };
+#define RLQ_TRY(x)                 \
+    do {                           \
+        const int32_t rc_ = (x);   \
+        if (rc_) return rc_;       \
+    } while (0)
+    // architecture and shared metadata (loader.rs:75-89, 244-280)
+    const int64_t ia = r.find("general.architecture");
+    if (ia < 0 || r.type(ia) != 8) return fail(err, kInvalid, 0, 2);
+    if (r.str(ia) != "llama") return fail(err, kUnsupported, 0, 2);
+    const int64_t it = r.find("general.type");
+    if (it >= 0 && r.type(it) != 8) return fail(err, kInvalid, 0, 3);
+    if (it >= 0 && r.str(it) != "model") return fail(err, kUnsupported, 0, 3);
+    uint64_t nextn = 0;
+    RLQ_TRY(uint("llama.nextn_predict_layers", 0, 4, &nextn));
+    if (nextn != 0) return fail(err, kUnsupported, 0, 4);
+    if (r.find("prism.hadamard.version") >= 0) return fail(err, kUnsupported, 0, 5);
+    // the vocabulary: the tokenizer's token list
+    const int64_t itok = r.find("tokenizer.ggml.tokens");
+    uint32_t tok_type = 0, tok_elem = 0;
+    uint64_t vocab = 0;
+    if (itok >= 0) rlq_gguf_kv_at(r.g, (uint64_t)itok, nullptr, nullptr, &tok_type, &tok_elem, &vocab, nullptr);
+    if (itok < 0 || tok_type != 9 || tok_elem != 8 || vocab == 0) return fail(err, kInvalid, 0, 6);
+    // hparams (loader.rs:282-331)
+    uint64_t width, heads, kv_heads, layers, ff, train_context, v;
+    RLQ_TRY(uint("llama.embedding_length", -1, 7, &width));
+    RLQ_TRY(uint("llama.attention.head_count", -1, 8, &heads));
+    if (width == 0 || heads == 0 || width % heads != 0) return fail(err, kInvalid, 0, 9);
+    const uint64_t hd = width / heads;
+    RLQ_TRY(uint("llama.attention.head_count_kv", (int64_t)heads, 10, &kv_heads));
+    RLQ_TRY(uint("llama.block_count", -1, 11, &layers));
+    if (layers == 0 || layers > 512) return fail(err, kInvalid, 0, 11);
+    RLQ_TRY(uint("llama.feed_forward_length", -1, 12, &ff));
+    RLQ_TRY(uint("llama.context_length", -1, 13, &train_context));
+    RLQ_TRY(uint("llama.rope.dimension_count", (int64_t)hd, 14, &v));
+    if (v != hd) return fail(err, kUnsupported, 0, 14);
+    for (const char* key : {"llama.attention.key_length", "llama.attention.value_length"}) {
+        RLQ_TRY(uint(key, (int64_t)hd, 15, &v));
+        if (v != hd) return fail(err, kUnsupported, 0, 15);
+    }
+    for (const char* key : {"llama.attention.sliding_window", "llama.expert_count", "llama.expert_used_count"}) {
+        RLQ_TRY(uint(key, 0, 16, &v));
+        if (v != 0) return fail(err, kUnsupported, 0, 16);
+    }
+    const int64_t ic = r.find("llama.attention.causal");  // require_causal (loader.rs:31-45)
+    if (ic >= 0 && r.type(ic) != 7) return fail(err, kInvalid, 0, 17);
+    if (ic >= 0 && r.bits(ic) != 1) return fail(err, kUnsupported, 0, 17);
+    // require_unscaled_rope (loader.rs:46-74)
+    const int64_t is = r.find("llama.rope.scaling.type");
+    if (is >= 0 && r.type(is) != 8) return fail(err, kInvalid, 0, 18);
+    const std::string kind = is >= 0 ? r.str(is) : std::string("linear");
+    if (kind != "none" && kind != "linear") return fail(err, kUnsupported, 0, 18);
+    float factor = 0.0f, gain = 1.0f;
+    RLQ_TRY(real(r.find("llama.rope.scaling.factor") >= 0 ? "llama.rope.scaling.factor" : "llama.rope.scale_linear",
+                 0.0f, 19, &factor));
+    if (kind != "none" && factor != 0.0f && factor != 1.0f) return fail(err, kUnsupported, 0, 19);
+    RLQ_TRY(real("llama.rope.scaling.attn_factor", 1.0f, 20, &gain));
+    if (gain != 1.0f) return fail(err, kUnsupported, 0, 20);
+    for (const char* key : {"llama.attention.qk_norm", "llama.attention.qk_norm_rms"}) {
+        const int64_t i = r.find(key);
+        if (i >= 0 && !(r.type(i) == 7 && r.bits(i) == 0)) return fail(err, kUnsupported, 0, 21);
+    }
+    float eps, rope_base, scale;
+    RLQ_TRY(real("llama.attention.layer_norm_rms_epsilon", 1e-5f, 22, &eps));
+    RLQ_TRY(real("llama.rope.freq_base", 10000.0f, 23, &rope_base));
+    RLQ_TRY(real("llama.attention.scale", 0.0f, 24, &scale));
+    const uint64_t kvw = kv_heads * hd;  // kv_heads == 0 and heads % kv_heads: check_llama_config
+    // tensors (loader.rs:96-160, 338-409): GGML shapes, trailing axes of one
+    uint64_t n_tensors = 0;
+    rlq_gguf_header(r.g, nullptr, nullptr, nullptr, nullptr, &n_tensors, nullptr);
+    std::vector<uint8_t> used(n_tensors, 0);
+    struct Got {
+        int64_t i;
+        uint32_t dtype;
+        uint64_t bytes;
+    };
+    auto tensor = [&](const std::string& name, uint64_t d0, uint64_t d1, bool optional, bool vector, uint64_t check,
+                      Got* got) -> int32_t {
+        got->i = rlq_gguf_find_tensor(r.g, (const uint8_t*)name.data(), name.size());
+        if (got->i < 0) return optional ? RLQ_OK : fail(err, kInvalid, 0, check);
+        uint32_t nd;
+        uint64_t dims[4], off;
+        rlq_gguf_tensor_at(r.g, (uint64_t)got->i, nullptr, nullptr, &nd, dims, &got->dtype, &off, &got->bytes, nullptr);
+        const uint64_t want[4] = {d0, vector ? 1 : d1, 1, 1};
+        for (int k = 0; k < 4; ++k)
+            if (dims[k] != want[k]) return fail(err, kInvalid, 0, check);
+        if (vector ? got->dtype != 0 : !path_weight(got->dtype)) return fail(err, RLQ_UNIMPLEMENTED, got->dtype, check);
+        used[(size_t)got->i] = 1;
+        return RLQ_OK;
+    };
+    Got emb, onorm, outw;
+    RLQ_TRY(tensor("token_embd.weight", width, vocab, false, false, 30, &emb));
+    RLQ_TRY(tensor("output_norm.weight", width, 0, false, true, 31, &onorm));
+    RLQ_TRY(tensor("output.weight", width, vocab, true, false, 32, &outw));
+    static const char* const kNames[7] = {"attn_q.weight", "attn_k.weight", "attn_v.weight", "attn_output.weight",
+                                          "ffn_gate.weight", "ffn_up.weight", "ffn_down.weight"};
+    std::vector<Got> mats(layers * 7), norms(layers * 2);
+    for (uint64_t l = 0; l < layers; ++l) {
+        const std::string b = "blk." + std::to_string(l) + ".";
+        const uint64_t shapes[7][2] = {{width, width}, {width, kvw}, {width, kvw}, {width, width},
+                                       {width, ff},    {width, ff},  {ff, width}};
+        for (int k = 0; k < 7; ++k)
+            RLQ_TRY(tensor(b + kNames[k], shapes[k][0], shapes[k][1], false, false, 40 + k, &mats[l * 7 + k]));
+        RLQ_TRY(tensor(b + "attn_norm.weight", width, 0, false, true, 47, &norms[l * 2]));
+        RLQ_TRY(tensor(b + "ffn_norm.weight", width, 0, false, true, 48, &norms[l * 2 + 1]));
+        // biases: the reference adds them (loader.rs:364-388); this step has none
+        for (const char* bias : {"attn_q.bias", "attn_k.bias", "attn_v.bias", "attn_output.bias", "ffn_gate.bias",
+                                 "ffn_up.bias", "ffn_down.bias"}) {
+            const std::string nm = b + bias;
+            if (rlq_gguf_find_tensor(r.g, (const uint8_t*)nm.data(), nm.size()) >= 0)
+                return fail(err, RLQ_UNIMPLEMENTED, 0, 49);
+        }
+    }
+    std::vector<uint8_t> host;  // every payload this model reads
+    std::vector<uint64_t> at(n_tensors, 0);
+    uint64_t total = 0;
+    for (uint64_t i = 0; i < n_tensors; ++i)
+        if (used[i]) {
+            uint64_t nb;
+            rlq_gguf_tensor_at(r.g, i, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, &nb, nullptr);
+            at[i] = total;
+            total += (nb + 255) & ~255ull;
+        }
+    const int64_t irf = rlq_gguf_find_tensor(r.g, (const uint8_t*)"rope_freqs.weight", 17);
+    if (irf >= 0) {  // loader.rs:395-402: all-one frequency factors only
+        uint32_t nd, dt;
+        uint64_t dims[4], off, nb;
+        rlq_gguf_tensor_at(r.g, (uint64_t)irf, nullptr, nullptr, &nd, dims, &dt, &off, &nb, nullptr);
+        if (dt != 0) return fail(err, RLQ_UNIMPLEMENTED, dt, 50);
+        std::vector<float> f(nb / 4);
+        rc = rlq_gguf_read_tensor(r.g, (uint64_t)irf, f.data(), nb, err);
+        if (rc) return rc;
+        if (dims[0] * dims[1] * dims[2] * dims[3] != hd / 2) return fail(err, kUnsupported, 0, 50);
+        for (float x : f)
+            if (x != 1.0f) return fail(err, kUnsupported, 0, 50);
+        used[(size_t)irf] = 1;
+    }
+    for (uint64_t i = 0; i < n_tensors; ++i)
+        if (!used[i]) return fail(err, kUnsupported, 0, 51, i);  // unimplemented tensors
+    try {
+        host.resize(total);
+    } catch (const std::bad_alloc&) {
+        return fail(err, RLQ_ALLOCATION_FAILED);
+    }
+    for (uint64_t i = 0; i < n_tensors; ++i)
+        if (used[i] && (int64_t)i != irf) {
+            uint64_t nb;
+            rlq_gguf_tensor_at(r.g, i, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, &nb, nullptr);
+            rc = rlq_gguf_read_tensor(r.g, i, host.data() + at[i], nb, err);
+            if (rc) return rc;
+        }
+    auto ptr = [&](const Got& g) -> const void* { return host.data() + at[(size_t)g.i]; };
+    std::vector<rlq_llama_layer> ls(layers);
+    for (uint64_t l = 0; l < layers; ++l) {
+        const Got* m = &mats[l * 7];
+        ls[l] = rlq_llama_layer{(const float*)ptr(norms[l * 2]), ptr(m[0]), ptr(m[1]), ptr(m[2]), ptr(m[3]),
+                                (const float*)ptr(norms[l * 2 + 1]), ptr(m[4]), ptr(m[5]), ptr(m[6]), {}};
+        for (int k = 0; k < 7; ++k) ls[l].types[k] = m[k].dtype;
+    }
+    const bool tied = outw.i < 0;  // no output.weight: the embedding matrix projects (loader.rs:345-355)
+    rlq_llama_config cfg{vocab,
+                         width,
+                         ff,
+                         heads,
+                         kv_heads,
+                         train_context < context_length ? train_context : context_length,
+                         layers,
+                         eps,
+                         rope_base,
+                         scale,
+                         mats[0].dtype,
+                         tied ? emb.dtype : outw.dtype,
+                         emb.dtype};
+    rlq_llama_tensors tensors{ptr(emb), (const float*)ptr(onorm), tied ? ptr(emb) : ptr(outw), ls.data(), 0};
+#undef RLQ_TRY
+    return rlq_llama_create(ctx, &cfg, &tensors, out, err);
+}
+
+void rlq_llama_config_of(const rlq_llama* m, rlq_llama_config* out) {
+    if (!m || !out) return;
+    const LlamaDims& d = m->m.d;
+    *out = rlq_llama_config{d.vocab,        d.width,     d.feed_forward,    d.heads,       d.kv_heads,
+                            d.max_context,  d.n_layers,  d.rms_epsilon,     d.rope_base,   d.attention_scale,
+                            d.weight_type,  d.output_type, d.embedding_type};
 }
 
 void rlq_llama_destroy(rlq_llama* m) {

@@ -329,7 +329,8 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const float* __restrict__
 
 hipError_t LlamaModel::ffn_activation(float* out, hipStream_t s) const {
     const uint32_t F = (uint32_t)d.feed_forward;
-    if (fused_ffn()) return hipMemcpyAsync(out, gu, F * sizeof(float), hipMemcpyDeviceToDevice, s);
+    if (layers.empty() || layers.back().gu_mode() == 0)  // the last layer's
+        return hipMemcpyAsync(out, gu, F * sizeof(float), hipMemcpyDeviceToDevice, s);
     hipLaunchKernelGGL(silu_mul_kernel, dim3((F + 255) / 256), dim3(256), 0, s, gu, F, out);
     return hipGetLastError();
 }
@@ -450,46 +451,61 @@ hipError_t LlamaModel::create(const LlamaDims& dims, const LlamaHostTensors& t, 
     if (e == hipSuccess) e = hipMalloc((void**)&argmax_keys, sizeof(unsigned long long));
     if (e == hipSuccess) e = hipMalloc((void**)&logits_buf, d.vocab * sizeof(float));
     if (e != hipSuccess) return e;
-    // staging for host GGUF bytes: the largest tensor
+    // staging for host GGUF bytes: the largest tensor; the gate/up stage of
+    // the interleaving copy
+    uint64_t big = gguf_row_bytes(d.output_type, W) * d.vocab, stage_gu = 0;
+    for (uint64_t l = 0; l < d.n_layers; ++l) {
+        const uint32_t* ty = t.layers[l].types;
+        for (int k = 0; k < 7; ++k) {
+            const uint64_t rows = k < 4 ? (k == 1 || k == 2 ? kvw : W) : (k == 6 ? W : F), cols = k == 6 ? F : W;
+            const uint64_t b = gguf_row_bytes(ty[k], cols) * rows;
+            big = big > b ? big : b;
+        }
+        if (ty[4] == ty[5] && (ty[4] == kQ4_K || ty[4] == kQ5_K)) {
+            const uint64_t b = 2 * layout_bytes(ty[4], F, W);
+            stage_gu = stage_gu > b ? stage_gu : b;
+        }
+    }
     void* staging = nullptr;
     if (!t.on_device) {
-        uint64_t big = gguf_row_bytes(d.weight_type, W) * F;
-        big = big > gguf_row_bytes(d.weight_type, F) * W ? big : gguf_row_bytes(d.weight_type, F) * W;
-        const uint64_t o = gguf_row_bytes(d.output_type, W) * d.vocab;
-        big = big > o ? big : o;
         e = hipMalloc(&staging, big);
         if (e != hipSuccess) return e;
     }
-    const uint32_t wt = d.weight_type;
     uint8_t* gu_stage = nullptr;
-    if (e == hipSuccess && fused_ffn()) e = hipMalloc((void**)&gu_stage, 2 * layout_bytes(wt, F, W));
-    auto tiled = [&](const void* src, uint64_t rows, uint64_t cols, uint8_t* dst) {
-        return upload_tiled(wt, src, rows, cols, t.on_device, dst, staging, s);
+    if (e == hipSuccess && stage_gu) e = hipMalloc((void**)&gu_stage, stage_gu);
+    auto tiled = [&](uint32_t ty, const void* src, uint64_t rows, uint64_t cols, uint8_t* dst) {
+        return upload_tiled(ty, src, rows, cols, t.on_device, dst, staging, s);
     };
     for (uint64_t l = 0; l < d.n_layers && e == hipSuccess; ++l) {
         const LlamaHostLayer& hl = t.layers[l];
         LlamaLayerDev& L = layers[l];
-        // Q, K, V (and gate, up) share one tiled buffer: rows are whole tiles
-        const uint64_t bq = layout_bytes(wt, W, W), bk = layout_bytes(wt, kvw, W), bg = layout_bytes(wt, F, W);
-        e = hipMalloc((void**)&L.wqkv, bq + 2 * bk);
-        if (e == hipSuccess) e = tiled(hl.query, W, W, L.wqkv);
-        if (e == hipSuccess) e = tiled(hl.key, kvw, W, L.wqkv + bq);
-        if (e == hipSuccess) e = tiled(hl.value, kvw, W, L.wqkv + bq + bk);
-        if (e == hipSuccess) e = hipMalloc((void**)&L.wo, layout_bytes(wt, W, W));
-        if (e == hipSuccess) e = tiled(hl.attention_output, W, W, L.wo);
-        // Q4_K / Q5_K: gate and up tiles interleaved (tile 2i = gate tile i,
-        // 2i + 1 = up tile i), so one workgroup holds both halves of
-        // silu(gate) * up; other types: [gate; up], whose product [g | u]
-        // the down projection's quantizer combines
-        if (e == hipSuccess) e = hipMalloc((void**)&L.wgu, 2 * bg);
-        if (e == hipSuccess && !fused_ffn()) {
-            e = tiled(hl.gate, F, W, L.wgu);
-            if (e == hipSuccess) e = tiled(hl.up, F, W, L.wgu + bg);
+        L.tq = hl.types[0], L.tk = hl.types[1], L.tv = hl.types[2], L.to = hl.types[3];
+        L.tg = hl.types[4], L.tu = hl.types[5], L.td = hl.types[6];
+        // Q, K, V back to back in one buffer: rows are whole tiles, so with one
+        // type the three are one tiled matrix of W + 2 kvw rows
+        const uint64_t bq = layout_bytes(L.tq, W, W), bk = layout_bytes(L.tk, kvw, W), bv = layout_bytes(L.tv, kvw, W);
+        L.off_k = bq, L.off_v = bq + bk;
+        e = hipMalloc((void**)&L.wqkv, bq + bk + bv);
+        if (e == hipSuccess) e = tiled(L.tq, hl.query, W, W, L.wqkv);
+        if (e == hipSuccess) e = tiled(L.tk, hl.key, kvw, W, L.wqkv + L.off_k);
+        if (e == hipSuccess) e = tiled(L.tv, hl.value, kvw, W, L.wqkv + L.off_v);
+        if (e == hipSuccess) e = hipMalloc((void**)&L.wo, layout_bytes(L.to, W, W));
+        if (e == hipSuccess) e = tiled(L.to, hl.attention_output, W, W, L.wo);
+        // gu_mode 0 (Q4_K / Q5_K): gate and up tiles interleaved (tile 2i =
+        // gate tile i, 2i + 1 = up tile i), so one workgroup holds both halves
+        // of silu(gate) * up; otherwise [gate; up], whose product [g | u] the
+        // down projection's quantizer combines
+        const uint64_t bg = layout_bytes(L.tg, F, W), bu = layout_bytes(L.tu, F, W);
+        L.off_up = bg;
+        if (e == hipSuccess) e = hipMalloc((void**)&L.wgu, bg + bu);
+        if (e == hipSuccess && L.gu_mode() != 0) {
+            e = tiled(L.tg, hl.gate, F, W, L.wgu);
+            if (e == hipSuccess) e = tiled(L.tu, hl.up, F, W, L.wgu + L.off_up);
         } else if (e == hipSuccess) {
-            e = tiled(hl.gate, F, W, gu_stage);
-            if (e == hipSuccess) e = tiled(hl.up, F, W, gu_stage + bg);
+            e = tiled(L.tg, hl.gate, F, W, gu_stage);
+            if (e == hipSuccess) e = tiled(L.tu, hl.up, F, W, gu_stage + bg);
         }
-        if (e == hipSuccess && fused_ffn()) {
+        if (e == hipSuccess && L.gu_mode() == 0) {
             const uint64_t tb = bg / (F / kTileRows);  // bytes of one tile
             e = hipMemcpy2DAsync(L.wgu, 2 * tb, gu_stage, tb, tb, F / kTileRows, hipMemcpyDeviceToDevice, s);
             if (e == hipSuccess)
@@ -497,8 +513,8 @@ hipError_t LlamaModel::create(const LlamaDims& dims, const LlamaHostTensors& t, 
                                      s);
             if (e == hipSuccess) e = hipStreamSynchronize(s);  // the stage is reused by the next layer
         }
-        if (e == hipSuccess) e = hipMalloc((void**)&L.wdown, layout_bytes(wt, W, F));
-        if (e == hipSuccess) e = tiled(hl.down, W, F, L.wdown);
+        if (e == hipSuccess) e = hipMalloc((void**)&L.wdown, layout_bytes(L.td, W, F));
+        if (e == hipSuccess) e = tiled(L.td, hl.down, W, F, L.wdown);
         if (e == hipSuccess) e = upload_f32(hl.attention_norm, W, t.on_device, &L.attn_norm, s);
         if (e == hipSuccess) e = upload_f32(hl.feed_forward_norm, W, t.on_device, &L.ffn_norm, s);
     }
@@ -530,7 +546,6 @@ hipError_t LlamaModel::step(float* hidden, uint64_t position, float* embedding_o
     const uint32_t nchunks = (uint32_t)((count + kAttnChunk - 1) / kAttnChunk);
     const float scale = d.attention_scale != 0.0f ? d.attention_scale : 1.0f / sqrtf((float)hd);
     const float* tab = rope_tab + position * hd;
-    const uint32_t wt = d.weight_type;
     const size_t lds_scores = (H / KVH * hd + kAttnChunk * (hd + 4)) * sizeof(float);
     const size_t lds_pv = attn_pv_lds((uint32_t)(H / KVH), (uint32_t)count, nchunks).total * sizeof(float);
     const uint32_t cstride = (uint32_t)((d.max_context + kAttnChunk - 1) / kAttnChunk);
@@ -541,8 +556,19 @@ hipError_t LlamaModel::step(float* hidden, uint64_t position, float* embedding_o
         float* vc = v_cache + l * d.max_context * kvw;
         MvExtra norm1;
         norm1.xform = 1, norm1.eps = d.rms_epsilon, norm1.norm_w = L.attn_norm;
-        e = launch_matvec_ex(wt, L.wqkv, W + 2 * kvw, W, hidden, nullptr, 1, qkv, W + 2 * kvw, nullptr, err_word,
-                             nullptr, nullptr, norm1, s);
+        if (L.fused_qkv()) {
+            e = launch_matvec_ex(L.tq, L.wqkv, W + 2 * kvw, W, hidden, nullptr, 1, qkv, W + 2 * kvw, nullptr, err_word,
+                                 nullptr, nullptr, norm1, s);
+        } else {  // one launch per type (each quantizes the same normalized input)
+            e = launch_matvec_ex(L.tq, L.wqkv, W, W, hidden, nullptr, 1, qkv, W, nullptr, err_word, nullptr, nullptr,
+                                 norm1, s);
+            if (e == hipSuccess)
+                e = launch_matvec_ex(L.tk, L.wqkv + L.off_k, kvw, W, hidden, nullptr, 1, qkv + W, kvw, nullptr,
+                                     err_word, nullptr, nullptr, norm1, s);
+            if (e == hipSuccess)
+                e = launch_matvec_ex(L.tv, L.wqkv + L.off_v, kvw, W, hidden, nullptr, 1, qkv + W + kvw, kvw, nullptr,
+                                     err_word, nullptr, nullptr, norm1, s);
+        }
         if (e != hipSuccess) break;
         hipLaunchKernelGGL(attn_scores_kernel, dim3(nchunks, (uint32_t)KVH), dim3(kAttnThreads), lds_scores, s, qkv,
                            tab, kc, vc, (uint32_t)fresh, (uint32_t)H, (uint32_t)KVH, (uint32_t)hd, scale, scores,
@@ -554,19 +580,27 @@ hipError_t LlamaModel::step(float* hidden, uint64_t position, float* embedding_o
         if (e != hipSuccess) break;
         MvExtra res;
         res.resid = hidden;
-        e = launch_matvec_ex(wt, L.wo, W, W, att, nullptr, 1, hidden, W, nullptr, err_word, nullptr, nullptr, res, s);
+        e = launch_matvec_ex(L.to, L.wo, W, W, att, nullptr, 1, hidden, W, nullptr, err_word, nullptr, nullptr, res, s);
         if (e != hipSuccess) break;
         // gate/up with the FFN norm: the fused epilogue leaves silu(gate) * up
         // in gu, the plain one [gate | up] for the down projection to combine
         MvExtra norm2;
-        norm2.xform = 1, norm2.eps = d.rms_epsilon, norm2.norm_w = L.ffn_norm, norm2.epilogue = fused_ffn() ? 1 : 0;
-        e = launch_matvec_ex(wt, L.wgu, 2 * F, W, hidden, nullptr, 1, gu, 2 * F, nullptr, err_word, nullptr, nullptr,
-                             norm2, s);
+        norm2.xform = 1, norm2.eps = d.rms_epsilon, norm2.norm_w = L.ffn_norm, norm2.epilogue = L.gu_mode() == 0 ? 1 : 0;
+        if (L.gu_mode() != 2) {
+            e = launch_matvec_ex(L.tg, L.wgu, 2 * F, W, hidden, nullptr, 1, gu, 2 * F, nullptr, err_word, nullptr,
+                                 nullptr, norm2, s);
+        } else {
+            e = launch_matvec_ex(L.tg, L.wgu, F, W, hidden, nullptr, 1, gu, F, nullptr, err_word, nullptr, nullptr,
+                                 norm2, s);
+            if (e == hipSuccess)
+                e = launch_matvec_ex(L.tu, L.wgu + L.off_up, F, W, hidden, nullptr, 1, gu + F, F, nullptr, err_word,
+                                     nullptr, nullptr, norm2, s);
+        }
         if (e != hipSuccess) break;
         MvExtra down;
         down.resid = hidden;
-        if (!fused_ffn()) down.xform = 2;
-        e = launch_matvec_ex(wt, L.wdown, W, F, gu, nullptr, 1, hidden, W, nullptr, err_word, nullptr, nullptr, down,
+        if (L.gu_mode() != 0) down.xform = 2;
+        e = launch_matvec_ex(L.td, L.wdown, W, F, gu, nullptr, 1, hidden, W, nullptr, err_word, nullptr, nullptr, down,
                              s);
     }
     if (e != hipSuccess) return e;

@@ -128,6 +128,7 @@ struct LlamaHostLayer {
     const void *query, *key, *value, *attention_output;
     const float* feed_forward_norm;
     const void *gate, *up, *down;
+    uint32_t types[7];  // query, key, value, attention_output, gate, up, down (resolved, nonzero)
 };
 struct LlamaHostTensors {
     const void* embedding;  // vocab x width, embedding_type
@@ -139,8 +140,17 @@ struct LlamaHostTensors {
 // LDS bytes the attention workgroups need at `max_context` rows.
 uint64_t llama_attn_lds_bytes(uint64_t heads, uint64_t kv_heads, uint64_t head_dim, uint64_t max_context);
 struct LlamaLayerDev {
-    uint8_t *wqkv = nullptr, *wo = nullptr, *wgu = nullptr, *wdown = nullptr;  // tiled; QKV and gate/up fused
+    // tiled matrices: Q, K, V back to back in wqkv; gate and up in wgu
+    // (tiles interleaved when the epilogue fuses silu(gate) * up)
+    uint8_t *wqkv = nullptr, *wo = nullptr, *wgu = nullptr, *wdown = nullptr;
     float *attn_norm = nullptr, *ffn_norm = nullptr;
+    uint32_t tq = 0, tk = 0, tv = 0, to = 0, tg = 0, tu = 0, td = 0;
+    uint64_t off_k = 0, off_v = 0, off_up = 0;  // byte offsets of K, V in wqkv and of up in wgu
+    bool fused_qkv() const { return tq == tk && tk == tv; }
+    // gate/up: 0 = one launch, silu(gate) * up in its epilogue (Q4_K, Q5_K);
+    // 1 = one launch over [gate; up], combined in the down projection's
+    // quantizer; 2 = two launches (different types), combined the same way
+    int gu_mode() const { return tg != tu ? 2 : (tg == kQ4_K || tg == kQ5_K ? 0 : 1); }
 };
 struct LlamaModel {
     int device = -1;
@@ -156,9 +166,7 @@ struct LlamaModel {
     ~LlamaModel();
     hipError_t create(const LlamaDims& dims, const LlamaHostTensors& t, hipStream_t s);
     hipError_t embedding(uint32_t token, float* hidden, hipStream_t s) const;
-    // Q4_K / Q5_K layers: silu(gate) * up in the gate/up matvec epilogue
-    bool fused_ffn() const { return d.weight_type == kQ4_K || d.weight_type == kQ5_K; }
-    // silu(gate) * up of the last step (feed_forward floats, device)
+    // silu(gate) * up of the last step's last layer (feed_forward floats, device)
     hipError_t ffn_activation(float* out, hipStream_t s) const;
     // One step at `position` appending KV row n_cached: hidden (width, device)
     // in/out; embedding_out (width), logits (vocab) and argmax (1) may be null.

@@ -26,7 +26,7 @@ import numpy as np
 import pytest
 
 import oracle as O
-from llama_fixture import make_config, make_tensors
+from llama_fixture import gguf_contents, make_config, make_tensors, matrix_type
 from rlq_loader import load
 
 pytestmark = pytest.mark.gpu
@@ -58,9 +58,9 @@ def gpu_config(cfg):
                            cfg.weight_type, cfg.output_type, cfg.embedding_type)
 
 
-def models(ctx, n_layers, seed, **kw):
+def models(ctx, n_layers, seed, mixed=False, **kw):
     cfg = make_config(n_layers=n_layers, **kw)
-    t = make_tensors(cfg, seed)
+    t = make_tensors(cfg, seed, mixed=mixed)
     return cfg, t, rlq.LlamaModel(ctx, gpu_config(cfg), t), O.LlamaOracle(cfg, t)
 
 
@@ -96,15 +96,17 @@ def test_output_head_without_layers(ctx, ot):
         assert int(host(am)[0]) == int(np.argmax(lg))
 
 
-@pytest.mark.parametrize("wt", [O.Q4_K, O.Q5_K, O.Q6_K, O.Q8_0, O.Q3_K, O.Q2_K])
-def test_one_layer_parts(ctx, wt):
+@pytest.mark.parametrize("wt,mixed", [(O.Q4_K, False), (O.Q5_K, False), (O.Q6_K, False), (O.Q8_0, False),
+                                      (O.Q3_K, False), (O.Q2_K, False), (O.Q4_K, True)])
+def test_one_layer_parts(ctx, wt, mixed):
     """Each part of one layer against the oracle fed with the GPU's own
     intermediates, over several steps (the cache grows past 64 rows: two
     attention chunks).  Q4_K / Q5_K layers run silu(gate) * up in the gate/up
     epilogue, the other types in the down projection's quantizer; Q8_0
-    layers quantize their activations to Q8_0."""
-    say("llama 1 layer, parts, 70 steps, layer type", wt)
-    cfg, t, g, o = models(ctx, 1, 23, weight_type=wt)
+    layers quantize their activations to Q8_0.  mixed: V and down in Q6_K
+    (a Q4_K_M layer), so Q/K/V run as three launches."""
+    say("llama 1 layer, parts, 70 steps, layer type", wt, "mixed" if mixed else "")
+    cfg, t, g, o = models(ctx, 1, 23, mixed=mixed, weight_type=wt)
     L = t["layers"][0]
     W, kvw, hd, F = cfg.width, cfg.kv_width, cfg.head_dim, cfg.feed_forward
     scale = np.float32(1.0) / np.sqrt(np.float32(hd))
@@ -122,7 +124,7 @@ def test_one_layer_parts(ctx, wt):
         # Q/K/V from the exact RMSNorm
         norm = O.rms_norm(h0, L["attention_norm"], cfg.rms_epsilon)
         for name, lo, hi, rows in (("query", 0, W, W), ("key", W, W + kvw, kvw), ("value", W + kvw, W + 2 * kvw, kvw)):
-            e = rel_l2(qkv[lo:hi], O.matvec(wt, L[name], rows, W, norm))
+            e = rel_l2(qkv[lo:hi], O.matvec(matrix_type(cfg, L, name), L[name], rows, W, norm))
             worst[name] = max(worst.get(name, 0), e)
             assert e <= 1e-5, (step, name, e)
         # attention from the GPU's q/k/v: bit-exact
@@ -136,13 +138,14 @@ def test_one_layer_parts(ctx, wt):
         off = int(np.sum(att != want_att))
         worst["attention_last_bit"] = worst.get("attention_last_bit", 0) + off
         # the rest of the layer from the GPU's attention output and silu(gate) * up
-        hm = h0 + O.matvec(wt, L["attention_output"], W, W, att)
+        mt = lambda name: matrix_type(cfg, L, name)  # noqa: E731
+        hm = h0 + O.matvec(mt("attention_output"), L["attention_output"], W, W, att)
         n2 = O.rms_norm(hm, L["feed_forward_norm"], cfg.rms_epsilon)
-        want_ffn = O.silu(O.matvec(wt, L["gate"], F, W, n2)) * O.matvec(wt, L["up"], F, W, n2)
+        want_ffn = O.silu(O.matvec(mt("gate"), L["gate"], F, W, n2)) * O.matvec(mt("up"), L["up"], F, W, n2)
         e = rel_l2(gu, want_ffn)
         worst["silu_gate_up"] = max(worst.get("silu_gate_up", 0), e)
         assert e <= 1e-3, (step, e)
-        want_h = hm + O.matvec(wt, L["down"], W, F, gu)
+        want_h = hm + O.matvec(mt("down"), L["down"], W, F, gu)
         e = rel_l2(host(h), want_h)
         worst["hidden"] = max(worst.get("hidden", 0), e)
         assert e <= 1e-5, (step, e)
@@ -200,3 +203,73 @@ def test_config_checks(ctx, field, value, check):
     with pytest.raises(rlq.QuantError) as e:
         rlq.LlamaModel(ctx, c, t)
     assert e.value.name == "InvalidConfig" and e.value.a == check
+
+
+# ------------------------------------------------------------ models from GGUF files
+
+@pytest.mark.parametrize("tied", [False, True])
+def test_gguf_model_equals_direct_creation(ctx, tmp_path, tied):
+    """A model written with the library's GGUF writer and loaded by
+    rlq_llama_create_from_gguf (mixed per-matrix types; tied: no
+    output.weight, the embedding projects) runs the same kernels on the same
+    bytes as the model created from the tensors: identical logits, and the
+    oracle's within the free-running bar."""
+    say("llama GGUF round trip, 2 layers, mixed types, tied output" if tied else "llama GGUF round trip, 2 layers")
+    cfg = make_config(n_layers=2, output_type=O.Q4_K if tied else O.Q6_K)
+    t = make_tensors(cfg, 27, mixed=True)
+    if tied:
+        t = dict(t, output=t["embedding"])
+    kvs, tensors = gguf_contents(cfg, t, tied=tied)
+    path = str(tmp_path / "model.gguf")
+    rlq.gguf_write(path, kvs, tensors)
+    g = rlq.LlamaModel.from_gguf(ctx, path, 4096)
+    c = g.config
+    assert (c.vocabulary, c.width, c.feed_forward, c.heads, c.kv_heads, c.max_context, c.n_layers) == \
+        (cfg.vocabulary, cfg.width, cfg.feed_forward, cfg.heads, cfg.kv_heads, cfg.max_context, cfg.n_layers)
+    assert (c.weight_type, c.output_type, c.embedding_type) == (cfg.weight_type, cfg.output_type, cfg.embedding_type)
+    assert (c.rms_epsilon, c.rope_base, c.attention_scale) == (cfg.rms_epsilon, cfg.rope_base, 0.0)
+    d = rlq.LlamaModel(ctx, gpu_config(cfg), t)
+    o = O.LlamaOracle(cfg, t)
+    rng = np.random.default_rng(9)
+    for step in range(8):
+        tok = int(rng.integers(cfg.vocabulary))
+        assert np.array_equal(host(g.embedding(tok)), host(d.embedding(tok)))
+        _, lg, ag = g.step(g.embedding(tok), step, embedding=False, logits=True, argmax=True)
+        _, ld, ad = d.step(d.embedding(tok), step, embedding=False, logits=True, argmax=True)
+        ctx.sync()
+        assert np.array_equal(host(lg), host(ld)) and int(host(ag)[0]) == int(host(ad)[0]), step
+        _, lo = o.step(o.embedding(tok), step)
+        assert rel_l2(host(lg), lo) <= 2e-3, step
+
+
+def test_gguf_loader_checks(ctx, tmp_path):
+    """The reference loader's checks (loader.rs:242-410), with the check
+    number in the error payload."""
+    cfg = make_config(n_layers=1)
+    t = make_tensors(cfg, 28)
+    path = str(tmp_path / "bad.gguf")
+    W = cfg.width
+    cases = [
+        (dict(drop=[b"llama.embedding_length"]), "GgufInvalid", 7),
+        (dict(extra_kv=[(b"llama.expert_count", 4, 8)]), "GgufUnsupported", 16),
+        (dict(drop=[b"general.architecture"], extra_kv=[(b"general.architecture", 8, b"gpt2")]), "GgufUnsupported", 2),
+        (dict(extra_kv=[(b"llama.rope.scaling.type", 8, b"yarn")]), "GgufUnsupported", 18),
+        (dict(drop=[b"llama.context_length"], extra_kv=[(b"llama.context_length", 10, 300)]), "GgufInvalid", 13),
+        (dict(extra_tensors=[(b"blk.0.attn_q.bias", [W], 0, np.zeros(4 * W, np.uint8))]), "Unimplemented", 49),
+        (dict(extra_tensors=[(b"vision.weight", [4], 0, np.zeros(16, np.uint8))]), "GgufUnsupported", 51),
+        (dict(drop=[b"blk.0.ffn_down.weight"]), "GgufInvalid", 46),
+    ]
+    for kw, name, check in cases:
+        say("GGUF loader check", name, check)
+        kvs, tensors = gguf_contents(cfg, t, **kw)
+        rlq.gguf_write(path, kvs, tensors)
+        with pytest.raises(rlq.QuantError) as e:
+            rlq.LlamaModel.from_gguf(ctx, path, 4096)
+        assert (e.value.name, e.value.a) == (name, check), (kw, e.value)
+    kvs, tensors = gguf_contents(cfg, t)
+    rlq.gguf_write(path, kvs, tensors)
+    with pytest.raises(rlq.QuantError) as e:
+        rlq.LlamaModel.from_gguf(ctx, path, 0)
+    assert (e.value.name, e.value.a) == ("GgufInvalid", 1)
+    m = rlq.LlamaModel.from_gguf(ctx, path, 100)  # min(context_length, the file's)
+    assert m.config.max_context == 100
