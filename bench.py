@@ -266,8 +266,13 @@ def llama_tensors(rlq, ctx, cfg, seed):
 
 def decode_step(rlq, ctx, steps, warmup, cpu=False):
     """Config 5: one decode step of the Llama-3-8B-shape model per token (embedding row, 32 layers,
-    final norm, Q6_K output matvec, greedy argmax), with synthetic tokens; the KV cache is filled
-    to max_context - warmup - steps rows first, so the timed steps see a context of ~1000 rows."""
+    final norm, Q6_K output matvec, greedy argmax), with synthetic tokens.  The random-init model is
+    written as a GGUF file by the library's GGUF writer and loaded by its llama GGUF loader
+    (rlq_llama_create_from_gguf); the KV cache is filled to max_context - warmup - steps rows
+    first, so the timed steps see a context of ~1000 rows."""
+    import shutil
+    import tempfile
+
     torch = rlq.torch
     DT = rlq.DType
     L = LLAMA
@@ -277,15 +282,26 @@ def decode_step(rlq, ctx, steps, warmup, cpu=False):
     t0 = time.perf_counter()
     tensors = llama_tensors(rlq, ctx, cfg, 0x51A7E005)
     gen_s = time.perf_counter() - t0
-    model = rlq.LlamaModel(ctx, cfg, tensors)
-    host_tensors = None
-    if cpu:
-        host_tensors = {"embedding": tensors["embedding"].cpu().numpy(),
-                        "output_norm": tensors["output_norm"].cpu().numpy(),
-                        "output": tensors["output"].cpu().numpy(),
-                        "layers": [{k: v.cpu().numpy() for k, v in l.items()} for l in tensors["layers"]]}
+    host_tensors = {"embedding": tensors["embedding"].cpu().numpy(),
+                    "output_norm": tensors["output_norm"].cpu().numpy(),
+                    "output": tensors["output"].cpu().numpy(),
+                    "layers": [{k: v.cpu().numpy() for k, v in l.items()} for l in tensors["layers"]]}
     del tensors
     torch.cuda.empty_cache()
+    tmp = tempfile.mkdtemp(prefix="rlq-llama-")
+    try:
+        path = os.path.join(tmp, "llama3-8b-shape-q4k.gguf")
+        t0 = time.perf_counter()
+        rlq.write_llama_gguf(path, cfg, host_tensors)
+        write_s = time.perf_counter() - t0
+        file_bytes = os.path.getsize(path)
+        t0 = time.perf_counter()
+        model = rlq.LlamaModel.from_gguf(ctx, path, cfg.max_context)
+        load_s = time.perf_counter() - t0
+    finally:
+        shutil.rmtree(tmp, ignore_errors=True)
+    if not cpu:
+        host_tensors = None
     rng = np.random.default_rng(5)
     toks = rng.integers(0, cfg.vocabulary, size=cfg.max_context).tolist()
     h = torch.empty(cfg.width, dtype=torch.float32, device="cuda")
@@ -327,7 +343,10 @@ def decode_step(rlq, ctx, steps, warmup, cpu=False):
            "bytes_per_token": int(nbytes), "weight_bytes": int(weights), "kv_bytes_mean": int(kv),
            "achieved_gbs": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
            "data": "synthetic random-init weights (N(0,0.02) matrices, N(0,1) embedding, N(1,0.05) norms) and "
-                   "random tokens", "weight_generation_s": round(gen_s, 1)}
+                   "random tokens", "weight_generation_s": round(gen_s, 1),
+           "gguf": {"file_bytes": file_bytes, "write_s": round(write_s, 2), "load_s": round(load_s, 2),
+                    "how": "written by rlq_gguf_write (the library's GGUF v3 writer), loaded by "
+                           "rlq_llama_create_from_gguf"}}
     if cpu:
         import oracle
 

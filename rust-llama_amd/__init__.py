@@ -752,3 +752,56 @@ def gguf_write(path, kvs, tensors):
     err = _Err()
     _check(_lib.rlq_gguf_write(os.fsencode(path), ks, len(kvs), ts, len(tensors), ctypes.byref(err)), err)
     del keep
+
+
+# GGUF tensor names of a llama layer's tensors (crates/inference/src/loader.rs:356-394)
+LLAMA_GGUF_NAMES = {"query": "attn_q", "key": "attn_k", "value": "attn_v", "attention_output": "attn_output",
+                    "gate": "ffn_gate", "up": "ffn_up", "down": "ffn_down", "attention_norm": "attn_norm",
+                    "feed_forward_norm": "ffn_norm"}
+
+
+def llama_gguf_contents(config, tensors, tied=False, tokens=None):
+    """The metadata and tensors of a llama GGUF file holding a model, in the
+    keys, names and GGML shapes the reference's loader reads
+    (crates/inference/src/loader.rs:282-394), for gguf_write.  `config` has
+    the LlamaConfig fields, `tensors` the LlamaModel dict (numpy arrays; a
+    layer's optional `types` maps matrix names to their types).  tied: no
+    output.weight (the embedding projects).  tokens: the vocabulary strings
+    (default <t0>, <t1>, ...)."""
+    f32 = lambda x: int(np.float32(x).view(np.uint32))  # noqa: E731
+    V, W, F = int(config.vocabulary), int(config.width), int(config.feed_forward)
+    hd = W // int(config.heads)
+    kvw = int(config.kv_heads) * hd
+    toks = tokens if tokens is not None else [b"<t%d>" % i for i in range(V)]
+    kvs = [(b"general.architecture", 8, b"llama"), (b"general.name", 8, b"random-init"),
+           (b"llama.block_count", 4, len(tensors["layers"])), (b"llama.context_length", 4, int(config.max_context)),
+           (b"llama.embedding_length", 4, W), (b"llama.feed_forward_length", 4, F),
+           (b"llama.attention.head_count", 4, int(config.heads)),
+           (b"llama.attention.head_count_kv", 4, int(config.kv_heads)),
+           (b"llama.attention.layer_norm_rms_epsilon", 6, f32(config.rms_epsilon)),
+           (b"llama.rope.freq_base", 6, f32(config.rope_base)), (b"llama.rope.dimension_count", 4, hd),
+           (b"tokenizer.ggml.model", 8, b"llama"), (b"tokenizer.ggml.tokens", 9, (8, toks))]
+    if float(config.attention_scale) != 0.0:
+        kvs.append((b"llama.attention.scale", 6, f32(config.attention_scale)))
+    as_u8 = lambda a: np.ascontiguousarray(a).reshape(-1).view(np.uint8)  # noqa: E731
+    out = [(b"token_embd.weight", [W, V], int(config.embedding_type), as_u8(tensors["embedding"])),
+           (b"output_norm.weight", [W], 0, as_u8(np.asarray(tensors["output_norm"], np.float32)))]
+    if not tied:
+        out.append((b"output.weight", [W, V], int(config.output_type), as_u8(tensors["output"])))
+    shapes = {"query": [W, W], "key": [W, kvw], "value": [W, kvw], "attention_output": [W, W], "gate": [W, F],
+              "up": [W, F], "down": [F, W]}
+    for i, L in enumerate(tensors["layers"]):
+        types = L.get("types", {})
+        for name, g in LLAMA_GGUF_NAMES.items():
+            nm = b"blk.%d.%s.weight" % (i, g.encode())
+            if name.endswith("norm"):
+                out.append((nm, [W], 0, as_u8(np.asarray(L[name], np.float32))))
+            else:
+                out.append((nm, shapes[name], int(types.get(name, config.weight_type)), as_u8(L[name])))
+    return kvs, out
+
+
+def write_llama_gguf(path, config, tensors, tied=False, tokens=None):
+    """A llama GGUF v3 file of the model (gguf_write of llama_gguf_contents)."""
+    kvs, ts = llama_gguf_contents(config, tensors, tied, tokens)
+    gguf_write(path, kvs, ts)

@@ -77,40 +77,12 @@ def matrix_type(cfg, layer, name):
     return layer.get("types", {}).get(name, cfg.weight_type)
 
 
-GGUF_NAMES = {"query": "attn_q", "key": "attn_k", "value": "attn_v", "attention_output": "attn_output",
-              "gate": "ffn_gate", "up": "ffn_up", "down": "ffn_down", "attention_norm": "attn_norm",
-              "feed_forward_norm": "ffn_norm"}
-
-
 def gguf_contents(cfg, t, tied=False, extra_kv=(), extra_tensors=(), drop=()):
-    """The metadata and tensors of a llama GGUF file holding this model, in
-    the names and GGML shapes of the reference's loader
-    (crates/inference/src/loader.rs:282-394): (kvs, tensors) for the
-    library's GGUF writer.  tied: no output.weight (the embedding projects;
-    the model's output matrix must then be the embedding)."""
-    f32 = lambda x: int(np.float32(x).view(np.uint32))  # noqa: E731
-    kvs = [(b"general.architecture", 8, b"llama"), (b"general.name", 8, b"random-init"),
-           (b"llama.block_count", 4, cfg.n_layers), (b"llama.context_length", 4, cfg.max_context),
-           (b"llama.embedding_length", 4, cfg.width), (b"llama.feed_forward_length", 4, cfg.feed_forward),
-           (b"llama.attention.head_count", 4, cfg.heads), (b"llama.attention.head_count_kv", 4, cfg.kv_heads),
-           (b"llama.attention.layer_norm_rms_epsilon", 6, f32(cfg.rms_epsilon)),
-           (b"llama.rope.freq_base", 6, f32(cfg.rope_base)), (b"llama.rope.dimension_count", 4, cfg.head_dim),
-           (b"tokenizer.ggml.model", 8, b"llama"),
-           (b"tokenizer.ggml.tokens", 9, (8, [b"t%d" % i for i in range(cfg.vocabulary)]))]
+    """The metadata and tensors of a llama GGUF file holding this model (the
+    library's llama_gguf_contents), with keys or tensors dropped or added."""
+    from rlq_loader import load
+
+    kvs, tensors = load().llama_gguf_contents(cfg, t, tied=tied)
     kvs = [kv for kv in kvs if kv[0] not in drop] + list(extra_kv)
-    W, F, kvw = cfg.width, cfg.feed_forward, cfg.kv_width
-    tensors = [(b"token_embd.weight", [W, cfg.vocabulary], cfg.embedding_type, t["embedding"]),
-               (b"output_norm.weight", [W], 0, t["output_norm"].view(np.uint8))]
-    if not tied:
-        tensors.append((b"output.weight", [W, cfg.vocabulary], cfg.output_type, t["output"]))
-    shapes = {"query": [W, W], "key": [W, kvw], "value": [W, kvw], "attention_output": [W, W], "gate": [W, F],
-              "up": [W, F], "down": [F, W]}
-    for i, L in enumerate(t["layers"]):
-        for name, g in GGUF_NAMES.items():
-            nm = b"blk.%d.%s.weight" % (i, g.encode())
-            if name.endswith("norm"):
-                tensors.append((nm, [W], 0, L[name].view(np.uint8)))
-            else:
-                tensors.append((nm, shapes[name], matrix_type(cfg, L, name), L[name]))
     tensors = [x for x in tensors if x[0] not in drop] + list(extra_tensors)
     return kvs, tensors
