@@ -325,7 +325,7 @@ class Context:
 
     def close(self):
         if getattr(self, "_h", None):
-            if not _exiting:
+            if _exiting is False:  # None once module teardown has cleared the globals
                 _lib.rlq_context_destroy(self._h)
             self._h = None
 
@@ -436,7 +436,7 @@ class Weights:
 
     def close(self):
         if getattr(self, "_h", None):
-            if not _exiting:
+            if _exiting is False:  # None once module teardown has cleared the globals
                 _lib.rlq_weights_destroy(self._h)
             self._h = None
 
@@ -527,7 +527,7 @@ class LlamaModel:
 
     def close(self):
         if getattr(self, "_h", None):
-            if not _exiting:
+            if _exiting is False:  # None once module teardown has cleared the globals
                 _lib.rlq_llama_destroy(self._h)
             self._h = None
 
@@ -613,7 +613,7 @@ class GgufFile:
 
     def close(self):
         if getattr(self, "_h", None):
-            if not _exiting:
+            if _exiting is False:  # None once module teardown has cleared the globals
                 _lib.rlq_gguf_close(self._h)
             self._h = None
 

@@ -567,6 +567,60 @@ __device__ __forceinline__ Q4Scales q4k_scales(uint4 h) {
 // Decode kernels with DBG also store the exact per-(row, block) integers of
 // column 0 (isum: the scaled sub-block dots; imin: the mins term).
 
+// Exact integers of one chunk for this lane's row n and columns b0, b0 + 1:
+// the scaled sub-block dots I and the mins sums M (matvec_extra.rs:252-262).
+// The A operand: lane row r holds column r / 2, sub-block parity r % 2, and is
+// nonzero only in the K quarters (kq / 2 == r % 2) of that sub-block; p is
+// this lane's A row at the chunk's block, bs the columns' bsums of the block.
+struct Q45Ints {
+    int32_t I0, I1, M0, M1;
+};
+template <uint32_t T>
+__device__ __forceinline__ Q45Ints q45_mfma_ints(const Q4Step<T>& cur, const uint8_t* p, const uint8_t* bs_blk_b0,
+                                                 uint32_t kq) {
+    const Q4Scales q = q4k_scales(cur.h);
+    const i32x4 al0 = *(const i32x4*)(p), ah0 = *(const i32x4*)(p + 32);
+    const i32x4 al1 = *(const i32x4*)(p + 128), ah1 = *(const i32x4*)(p + 160);
+    i32x4 wl0 = lo_nibbles(cur.w0), wh0 = hi_nibbles(cur.w0);
+    i32x4 wl1 = lo_nibbles(cur.w1), wh1 = hi_nibbles(cur.w1);
+    if constexpr (T == kQ5_K) {
+        const Q5High hb = q5_high(cur.qh, kq);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            wl0[i] |= (int)hb.l0[i];
+            wh0[i] |= (int)hb.h0[i];
+            wl1[i] |= (int)hb.l1[i];
+            wh1[i] |= (int)hb.h1[i];
+        }
+    }
+    // sub-blocks: dl0 {0, 2}, dh0 {1, 3}, dl1 {4, 6}, dh1 {5, 7}; element
+    // 2j + w of each is column b0 + j, sub-block parity w
+    const i32x4 dl0 = mfma_i8(al0, wl0);
+    const i32x4 dh0 = mfma_i8(ah0, wh0);
+    const i32x4 dl1 = mfma_i8(al1, wl1);
+    const i32x4 dh1 = mfma_i8(ah1, wh1);
+    const int32_t c0 = ubyte(q.scA, 0), c1 = ubyte(q.scA, 1), c2 = ubyte(q.scA, 2), c3 = ubyte(q.scA, 3);
+    const int32_t c4 = ubyte(q.scB, 0), c5 = ubyte(q.scB, 1), c6 = ubyte(q.scB, 2), c7 = ubyte(q.scB, 3);
+    Q45Ints o;
+    // |dot| <= 32*31*128 and scales <= 63: 24-bit operands, exact products
+    o.I0 = mad24(c0, dl0[0], mad24(c2, dl0[1], mad24(c1, dh0[0], __mul24(c3, dh0[1]))));
+    o.I0 = mad24(c4, dl1[0], mad24(c6, dl1[1], mad24(c5, dh1[0], mad24(c7, dh1[1], o.I0))));
+    o.I1 = mad24(c0, dl0[2], mad24(c2, dl0[3], mad24(c1, dh0[2], __mul24(c3, dh0[3]))));
+    o.I1 = mad24(c4, dl1[2], mad24(c6, dl1[3], mad24(c5, dh1[2], mad24(c7, dh1[3], o.I1))));
+    // mins: sum_s min_s * (bsum[2s] + bsum[2s+1])  (matvec_extra.rs:258)
+    const uint32_t m01 = __builtin_amdgcn_perm(0u, q.mnA, 0x0c010c00u);
+    const uint32_t m23 = __builtin_amdgcn_perm(0u, q.mnA, 0x0c030c02u);
+    const uint32_t m45 = __builtin_amdgcn_perm(0u, q.mnB, 0x0c010c00u);
+    const uint32_t m67 = __builtin_amdgcn_perm(0u, q.mnB, 0x0c030c02u);
+    const uint4* bs = (const uint4*)bs_blk_b0;
+    const uint4 bA0 = bs[0], bA1 = bs[1], bB0 = bs[2], bB1 = bs[3];
+    o.M0 = dot2(m67, bA1.w, dot2(m23, bA1.z, dot2(m67, bA1.y, dot2(m23, bA1.x,
+           dot2(m45, bA0.w, dot2(m01, bA0.z, dot2(m45, bA0.y, dot2(m01, bA0.x, 0))))))));
+    o.M1 = dot2(m67, bB1.w, dot2(m23, bB1.z, dot2(m67, bB1.y, dot2(m23, bB1.x,
+           dot2(m45, bB0.w, dot2(m01, bB0.z, dot2(m45, bB0.y, dot2(m01, bB0.x, 0))))))));
+    return o;
+}
+
 // Q4_K / Q5_K, batches of three to eight columns: MFMA.
 template <uint32_t T, int W, int D, bool DBG>
 __global__ __launch_bounds__(W * 64) void q4k_mv_kernel(MvArgs a) {
@@ -595,57 +649,17 @@ __global__ __launch_bounds__(W * 64) void q4k_mv_kernel(MvArgs a) {
     unsigned long long best0 = 0, best1 = 0;
     uint32_t tile = gw, blk = 0;
     auto compute = [&](const Q4Step<T>& cur) {
-        const Q4Scales q = q4k_scales(cur.h);
-        const uint8_t* p = a_ptr + blk * a_step;
-        const i32x4 al0 = *(const i32x4*)(p), ah0 = *(const i32x4*)(p + 32);
-        const i32x4 al1 = *(const i32x4*)(p + 128), ah1 = *(const i32x4*)(p + 160);
-        i32x4 wl0 = lo_nibbles(cur.w0), wh0 = hi_nibbles(cur.w0);
-        i32x4 wl1 = lo_nibbles(cur.w1), wh1 = hi_nibbles(cur.w1);
-        if constexpr (T == kQ5_K) {
-            const Q5High hb = q5_high(cur.qh, kq);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                wl0[i] |= (int)hb.l0[i];
-                wh0[i] |= (int)hb.h0[i];
-                wl1[i] |= (int)hb.l1[i];
-                wh1[i] |= (int)hb.h1[i];
-            }
-        }
-        // sub-blocks: dl0 {0, 2}, dh0 {1, 3}, dl1 {4, 6}, dh1 {5, 7}; element
-        // 2j + w of each is column b0 + j, sub-block parity w
-        const i32x4 dl0 = mfma_i8(al0, wl0);
-        const i32x4 dh0 = mfma_i8(ah0, wh0);
-        const i32x4 dl1 = mfma_i8(al1, wl1);
-        const i32x4 dh1 = mfma_i8(ah1, wh1);
-        const int32_t c0 = ubyte(q.scA, 0), c1 = ubyte(q.scA, 1), c2 = ubyte(q.scA, 2), c3 = ubyte(q.scA, 3);
-        const int32_t c4 = ubyte(q.scB, 0), c5 = ubyte(q.scB, 1), c6 = ubyte(q.scB, 2), c7 = ubyte(q.scB, 3);
-        // |dot| <= 32*31*128 and scales <= 63: 24-bit operands, exact products
-        int32_t I0 = mad24(c0, dl0[0], mad24(c2, dl0[1], mad24(c1, dh0[0], __mul24(c3, dh0[1]))));
-        I0 = mad24(c4, dl1[0], mad24(c6, dl1[1], mad24(c5, dh1[0], mad24(c7, dh1[1], I0))));
-        int32_t I1 = mad24(c0, dl0[2], mad24(c2, dl0[3], mad24(c1, dh0[2], __mul24(c3, dh0[3]))));
-        I1 = mad24(c4, dl1[2], mad24(c6, dl1[3], mad24(c5, dh1[2], mad24(c7, dh1[3], I1))));
-        // mins: sum_s min_s * (bsum[2s] + bsum[2s+1])  (matvec_extra.rs:258)
-        const uint32_t m01 = __builtin_amdgcn_perm(0u, q.mnA, 0x0c010c00u);
-        const uint32_t m23 = __builtin_amdgcn_perm(0u, q.mnA, 0x0c030c02u);
-        const uint32_t m45 = __builtin_amdgcn_perm(0u, q.mnB, 0x0c010c00u);
-        const uint32_t m67 = __builtin_amdgcn_perm(0u, q.mnB, 0x0c030c02u);
-        const uint4* bs = (const uint4*)(lds + L.bs_off + (blk * 8 + b0) * 32);
-        const uint4 bA0 = bs[0], bA1 = bs[1], bB0 = bs[2], bB1 = bs[3];
-        const int32_t M0 = dot2(m67, bA1.w, dot2(m23, bA1.z, dot2(m67, bA1.y, dot2(m23, bA1.x,
-                           dot2(m45, bA0.w, dot2(m01, bA0.z, dot2(m45, bA0.y, dot2(m01, bA0.x, 0))))))));
-        const int32_t M1 = dot2(m67, bB1.w, dot2(m23, bB1.z, dot2(m67, bB1.y, dot2(m23, bB1.x,
-                           dot2(m45, bB0.w, dot2(m01, bB0.z, dot2(m45, bB0.y, dot2(m01, bB0.x, 0))))))));
-
+        const Q45Ints o = q45_mfma_ints<T>(cur, a_ptr + blk * a_step, lds + L.bs_off + (blk * 8 + b0) * 32, kq);
         const float2 da = *(const float2*)(lds + L.d_off + (blk * 8 + b0) * 4);
         const float dw = half_to_float(cur.h.x), dmw = half_to_float(cur.h.x >> 16);
-        acc0 += (dw * da.x) * (float)I0 - (dmw * da.x) * (float)M0;
-        acc1 += (dw * da.y) * (float)I1 - (dmw * da.y) * (float)M1;
+        acc0 += (dw * da.x) * (float)o.I0 - (dmw * da.x) * (float)o.M0;
+        acc1 += (dw * da.y) * (float)o.I1 - (dmw * da.y) * (float)o.M1;
 
         if (DBG && kq == 0) {
             const uint32_t row = tile * kTileRows + n;
             if (row < a.rows) {
-                a.dbg_isum[(uint64_t)row * nb + blk] = I0;
-                a.dbg_imin[(uint64_t)row * nb + blk] = M0;
+                a.dbg_isum[(uint64_t)row * nb + blk] = o.I0;
+                a.dbg_imin[(uint64_t)row * nb + blk] = o.M0;
             }
         }
         if (++blk == nb) {
@@ -1420,8 +1434,12 @@ static hipError_t launch_one(K kernel, const MvArgs& a, size_t lds, hipStream_t 
 // KS waves, about kSmallWgPerCu workgroups per CU.
 constexpr int kSmallW = 8, kSmallKS = 8, kSmallD = 2, kSmallWgPerCu = 2;
 
-template <uint32_t T, int W, int KS, int D, int B, bool DBG>
-static hipError_t launch_small(const MvArgs& a, hipStream_t s, uint32_t pairs) {
+// K-split kernels with parked partials: the grid and the LDS of
+// [tmax][TS][KS][16][batch] partials.  lds_set is the kernel's own record of
+// the dynamic LDS limit it has been given.
+template <int W, int KS>
+static hipError_t launch_parked(void (*kernel)(MvArgs), size_t& lds_set, const MvArgs& a, hipStream_t s,
+                                uint32_t pairs) {
     constexpr int TS = W / KS;
     const uint32_t want = (a.ntiles + TS - 1) / TS;
     const uint32_t gy = grid_rows(a, pairs);
@@ -1434,15 +1452,20 @@ static hipError_t launch_small(const MvArgs& a, hipStream_t s, uint32_t pairs) {
     const uint32_t tstride = grid * TS, tmax = (a.ntiles + tstride - 1) / tstride;
     const size_t lds = small_lds_bytes(a.cols, a.batch, tmax, TS, KS);
     if (lds > kMaxLds) return hipErrorInvalidValue;
-    static size_t lds_set = 64 * 1024;
     if (lds > lds_set) {
-        const hipError_t e = hipFuncSetAttribute((const void*)q4k_mv_small_kernel<T, W, KS, D, B, DBG>,
-                                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+        const hipError_t e = hipFuncSetAttribute((const void*)kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                 (int)lds);
         if (e != hipSuccess) return e;
         lds_set = lds;
     }
-    hipLaunchKernelGGL((q4k_mv_small_kernel<T, W, KS, D, B, DBG>), dim3(grid, gy), dim3(W * 64), lds, s, a);
+    hipLaunchKernelGGL(kernel, dim3(grid, gy), dim3(W * 64), lds, s, a);
     return hipGetLastError();
+}
+
+template <uint32_t T, int W, int KS, int D, int B, bool DBG>
+static hipError_t launch_small(const MvArgs& a, hipStream_t s, uint32_t pairs) {
+    static size_t lds_set = 64 * 1024;
+    return launch_parked<W, KS>(q4k_mv_small_kernel<T, W, KS, D, B, DBG>, lds_set, a, s, pairs);
 }
 
 // Q4_K / Q5_K: the VALU kernel for one or two columns, MFMA above.
