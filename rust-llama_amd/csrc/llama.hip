@@ -28,42 +28,57 @@
 
 namespace rlq {
 
-constexpr int kAttnChunk = 64;      // tokens per workgroup of the attention kernels
+constexpr int kAttnChunk = 16;      // tokens per workgroup of the scores kernel
 constexpr int kAttnThreads = 256;
-constexpr uint32_t kAttnMaxHd = 256;  // head dimension limit: 64 rows of a chunk in 16 float4 per thread
+constexpr uint32_t kAttnMaxHd = 256;  // head dimension limit
+constexpr uint32_t kScKeyRegs = kAttnMaxHd * kAttnChunk / 4 / kAttnThreads;  // float4 of a chunk's keys per thread
+constexpr uint32_t kScKeyPad = 16;  // floats after each key row in LDS
 
-constexpr uint32_t kAttnBatch = 16;   // loads in flight per thread in the P.V prologue
-constexpr uint32_t kPvDims = 8;       // head dimensions per P.V workgroup
-constexpr uint32_t kPvSegs = 8;       // token segments per P.V output
-constexpr uint32_t kPvScoreRegs = 4;  // score groups of four per thread held in registers (G * count <= 4096)
+constexpr uint32_t kAttnBatch = 16;   // value loads in flight per thread in the P.V prologue
+constexpr uint32_t kPvDims = 4;       // head dimensions per P.V workgroup: one float4 of each value row
+constexpr uint32_t kPvThreads = 512;
+constexpr uint32_t kPvWaves = kPvThreads / 64;
+constexpr uint32_t kPvScoreRegs = 4;  // score groups of four per thread held in registers (G * count <= 8192)
 
-// LDS of attn_pv_kernel, in floats: exponentials [G][rs], pair sums
-// [G][n4/4], max and inverse [G][2], chunk maxima [G][nch], the transposed
-// values [kPvDims][rs] at a 16-byte aligned offset, then the f64 segment sums
-// [kPvSegs][G * kPvDims].  Rows hold n32 =
-// count rounded up to 32 values (8 segments of a multiple of 4) and are
-// padded by 4 floats so the rows a wave reads start in different banks.
+// The value cache of a layer is slice-major: [kv_heads * hd / 4][max_context]
+// float4, slice kvh * hd / 4 + d / 4 holding dimensions d .. d + 3 of kv head
+// kvh for every token, so a P.V workgroup reads one contiguous run.
+__host__ __device__ inline uint64_t v_cache_index(uint32_t kvh, uint32_t hd, uint32_t d, uint64_t token,
+                                                  uint64_t max_context) {
+    return ((uint64_t)(kvh * (hd / 4) + d / 4) * max_context + token) * 4 + d % 4;
+}
+
+// P.V waves per head: the waves of a workgroup split G heads' columns.
+__host__ __device__ inline uint32_t pv_waves_per_head(uint32_t G) { return G < kPvWaves ? kPvWaves / G : 1u; }
+
+// LDS of attn_pv_kernel, in floats: exponentials [G][n64], pair sums
+// [G][n4/4], max and inverse [G][2], chunk maxima [G][nch], the values [n64]
+// float4 at a 16-byte aligned offset, then the f64 wave partials
+// [G][waves per head][4].  n64 = count rounded up to 64 (one column per lane
+// of a wave); the columns past count are zero.
 struct AttnPvLds {
-    uint32_t n32, rs, g, stat, cm, v, part, total;
+    uint32_t n64, g, stat, cm, v, part, total;
 };
 __host__ __device__ inline AttnPvLds attn_pv_lds(uint32_t G, uint32_t count, uint32_t nch) {
     AttnPvLds l;
     const uint32_t n4 = (count + 3) / 4 * 4;
-    l.n32 = (count + 31) / 32 * 32;
-    l.rs = l.n32 + 4;
-    l.g = G * l.rs;
+    l.n64 = (count + 63) / 64 * 64;
+    l.g = G * l.n64;
     l.stat = l.g + G * (n4 / 4);
     l.cm = l.stat + 2 * G;
     l.v = (l.cm + G * nch + 3) & ~3u;
-    l.part = (l.v + kPvDims * l.rs + 1) & ~1u;
-    l.total = l.part + 2 * kPvSegs * G * kPvDims;
+    l.part = l.v + 4 * l.n64;
+    l.total = l.part + 2 * 4 * G * pv_waves_per_head(G);
     return l;
+}
+__host__ __device__ inline uint32_t attn_scores_lds(uint32_t G, uint32_t hd) {
+    return (G * hd + kAttnChunk * (hd + kScKeyPad)) * 4;
 }
 
 uint64_t llama_attn_lds_bytes(uint64_t heads, uint64_t kv_heads, uint64_t head_dim, uint64_t max_context) {
     const uint64_t G = heads / kv_heads, nch = (max_context + kAttnChunk - 1) / kAttnChunk;
     const uint64_t pv = (uint64_t)attn_pv_lds((uint32_t)G, (uint32_t)max_context, (uint32_t)nch).total * 4;
-    const uint64_t sc = (G * head_dim + kAttnChunk * (head_dim + 4)) * 4;
+    const uint64_t sc = attn_scores_lds((uint32_t)G, (uint32_t)head_dim);
     return pv > sc ? pv : sc;
 }
 
@@ -94,32 +109,35 @@ __device__ __forceinline__ bool certified_f32(double sum, double abs_sum, uint32
 __device__ __forceinline__ float f64_to_f32(double x) { return (float)x; }
 
 // Scores of kv head blockIdx.y's G query heads against tokens
-// [64 * blockIdx.x, +64) of the layer cache (math.rs:462-474):
+// [16 * blockIdx.x, +16) of the layer cache (math.rs:462-474):
 // score = f32(sum_d f64(q_d * k_d)) * scale, the sum in d order.  The
 // workgroup whose chunk holds the new row `fresh` applies RoPE to the new key,
 // appends it and the new value to the caches, and uses its own copy of the
 // key.  scores is [heads][row_stride]; cmax[head][chunk] (stride cstride)
-// receives each chunk's maximum score.
+// receives each chunk's maximum score.  Four lanes share a (head, token) dot:
+// quarter j takes the float4s j, j + 4, ... of the row, and a wave holds one
+// head's 16 tokens.
 __global__ __launch_bounds__(kAttnThreads) void attn_scores_kernel(
     const float* __restrict__ qkv, const float* __restrict__ rope_tab, float* __restrict__ kc, float* __restrict__ vc,
-    uint32_t fresh, uint32_t heads, uint32_t kv_heads, uint32_t hd, float scale, float* __restrict__ scores,
-    uint32_t row_stride, float* __restrict__ cmax, uint32_t cstride, unsigned long long* __restrict__ err_word) {
+    uint32_t max_context, uint32_t fresh, uint32_t heads, uint32_t kv_heads, uint32_t hd, float scale,
+    float* __restrict__ scores, uint32_t row_stride, float* __restrict__ cmax, uint32_t cstride,
+    unsigned long long* __restrict__ err_word) {
     extern __shared__ __align__(16) float sm[];
     const uint32_t G = heads / kv_heads, kvh = blockIdx.y, c = blockIdx.x, t0 = c * kAttnChunk;
-    // key rows at a stride of hd + 4 floats: the eight lanes of one 128-byte
-    // LDS pass read eight different 16-byte bank groups
-    const uint32_t width = heads * hd, kvw = kv_heads * hd, ks = hd + 4;
+    // key rows at a stride of hd + 16 floats: the two rows one eight-lane LDS
+    // pass reads (four quarters each) start 16 banks apart
+    const uint32_t width = heads * hd, kvw = kv_heads * hd, ks = hd + kScKeyPad;
     float* q_s = sm;              // [G][hd]
-    float* k_s = sm + G * hd;     // [64][hd + 4]
+    float* k_s = sm + G * hd;     // [16][hd + 16]
     const uint32_t tid = threadIdx.x, count = fresh + 1, q4 = hd / 4;
     const uint32_t n_here = count - t0 < (uint32_t)kAttnChunk ? count - t0 : (uint32_t)kAttnChunk;
     // the chunk's cached keys: every load issued before any is used
-    float4 kr[kAttnMaxHd / 16];
+    float4 kr[kScKeyRegs];
 #pragma unroll
-    for (uint32_t k = 0; k < kAttnMaxHd / 16; ++k) {
+    for (uint32_t k = 0; k < kScKeyRegs; ++k) {
         const uint32_t i = tid + k * kAttnThreads, t = i / q4;
         kr[k] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        if (k < hd / 16 && t < n_here && t0 + t != fresh)
+        if (t < n_here && t0 + t != fresh)
             kr[k] = *(const float4*)(kc + (uint64_t)(t0 + t) * kvw + kvh * hd + 4 * (i % q4));
     }
     for (uint32_t i = tid; i < G * hd / 2; i += kAttnThreads) {
@@ -138,118 +156,128 @@ __global__ __launch_bounds__(kAttnThreads) void attn_scores_kernel(
             kc[(uint64_t)fresh * kvw + kvh * hd + 2 * p] = o0;
             kc[(uint64_t)fresh * kvw + kvh * hd + 2 * p + 1] = o1;
         }
-        for (uint32_t d = tid; d < hd; d += kAttnThreads) vc[(uint64_t)fresh * kvw + kvh * hd + d] = vin[d];
+        for (uint32_t d = tid; d < hd; d += kAttnThreads) vc[v_cache_index(kvh, hd, d, fresh, max_context)] = vin[d];
     }
 #pragma unroll
-    for (uint32_t k = 0; k < kAttnMaxHd / 16; ++k) {
+    for (uint32_t k = 0; k < kScKeyRegs; ++k) {
         const uint32_t i = tid + k * kAttnThreads, t = i / q4;
-        if (k < hd / 16 && t < n_here && t0 + t != fresh) {
-            *(float4*)(k_s + t * ks + 4 * (i % q4)) = kr[k];
-        }
+        if (t < n_here && t0 + t != fresh) *(float4*)(k_s + t * ks + 4 * (i % q4)) = kr[k];
     }
     __syncthreads();
-    // pair (h, t) = i: a wave holds one head's 64 tokens
-    for (uint32_t i = tid; i < G * kAttnChunk; i += kAttnThreads) {
+    // pair (h, t) = i takes lanes 4i .. 4i + 3; the trip count is uniform per
+    // wave (G * 16 pairs, 16 per wave), so every lane reaches the shuffles
+    const uint32_t quarter = tid & 3;
+    for (uint32_t i = tid >> 2; i < G * kAttnChunk; i += kAttnThreads / 4) {
         const uint32_t h = i / kAttnChunk, t = i % kAttnChunk;
-        float score = -INFINITY;
-        if (t < n_here) {
-            const float* q = q_s + h * hd;
-            const float* k = k_s + t * ks;
-            // four interleaved partial sums; the f32 total is certified against
-            // the reference's d-order sum, or recomputed in that order.  The
-            // magnitudes are summed in f32 (relative error < 2^-16 for hd <= 256,
-            // covered by the factor 1.01).
-            double a[4] = {0.0, 0.0, 0.0, 0.0};
-            float b = 0.0f;
-            for (uint32_t d = 0; d < hd; d += 4) {
-                const float4 q4 = *(const float4*)(q + d), k4 = *(const float4*)(k + d);
-                const float x0 = q4.x * k4.x, x1 = q4.y * k4.y, x2 = q4.z * k4.z, x3 = q4.w * k4.w;
+        const bool live = t < n_here;
+        const float* q = q_s + h * hd;
+        const float* k = k_s + t * ks;
+        // four interleaved partial sums per lane, then the four lanes'; the
+        // f32 total is certified against the reference's d-order sum, or
+        // recomputed in that order.  The magnitudes are summed in f32
+        // (relative error < 2^-16 for hd <= 256, covered by the factor 1.01).
+        double a[4] = {0.0, 0.0, 0.0, 0.0};
+        float b = 0.0f;
+        if (live) {
+            for (uint32_t d = 4 * quarter; d < hd; d += 16) {
+                const float4 q4v = *(const float4*)(q + d), k4 = *(const float4*)(k + d);
+                const float x0 = q4v.x * k4.x, x1 = q4v.y * k4.y, x2 = q4v.z * k4.z, x3 = q4v.w * k4.w;
                 a[0] += (double)x0, a[1] += (double)x1, a[2] += (double)x2, a[3] += (double)x3;
                 b += (fabsf(x0) + fabsf(x1)) + (fabsf(x2) + fabsf(x3));
             }
+        }
+        double part = (a[0] + a[1]) + (a[2] + a[3]);
+        part += __shfl_xor(part, 1, 64);
+        part += __shfl_xor(part, 2, 64);
+        b += __shfl_xor(b, 1, 64);
+        b += __shfl_xor(b, 2, 64);
+        float score = -INFINITY;
+        if (live) {
             float dotf;
-            if (!certified_f32((a[0] + a[1]) + (a[2] + a[3]), 1.01 * (double)b, hd, f64_to_f32, &dotf)) {
+            if (!certified_f32(part, 1.01 * (double)b, hd, f64_to_f32, &dotf)) {
                 double dot = 0.0;
                 for (uint32_t d = 0; d < hd; ++d) dot += (double)(q[d] * k[d]);
                 dotf = (float)dot;
             }
             score = dotf * scale;
-            if (!(fabsf(score) <= 3.402823466e38f)) report_error(err_word, error_key(0, kKindNonFinite, t0 + t));
-            scores[(uint64_t)(kvh * G + h) * row_stride + t0 + t] = score;
+            if (quarter == 0) {
+                if (!(fabsf(score) <= 3.402823466e38f)) report_error(err_word, error_key(0, kKindNonFinite, t0 + t));
+                scores[(uint64_t)(kvh * G + h) * row_stride + t0 + t] = score;
+            }
         }
         float m = score;
 #pragma unroll
-        for (int o = 1; o < 64; o <<= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
-        if (t == 0) cmax[(kvh * G + h) * cstride + c] = m;
+        for (int o = 4; o < 64; o <<= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+        if ((tid & 63) == 0) cmax[(kvh * G + h) * cstride + c] = m;
     }
 }
 
 // Softmax of the G heads' score rows (math.rs:293-318 with the SSE2 policy of
-// cpu_math.rs:60-91) and P.V (math.rs:475-482) for 8 of the head dimensions:
-// workgroup (blockIdx.x, blockIdx.y) = (dimensions 8 * blockIdx.x .., kv head).
+// cpu_math.rs:60-91) and P.V (math.rs:475-482) for 4 of the head dimensions:
+// workgroup (blockIdx.x, blockIdx.y) = (dimensions 4 * blockIdx.x .., kv head).
 // Every workgroup of the kv head recomputes the G rows' softmax from the chunk
 // maxima; the softmax totals are certified against the reference's order
-// (certified_f32).  The P.V sums add the reference's f64 terms in segments:
-// their f32 results can differ from the reference's in the last bit (the
-// certificate fails for about 2 in 10^4 of these 1024-term sums, and a
-// sequential repeat would cost the whole kernel several microseconds).
-// Columns past `count` are the -inf padding, whose exponentials are exactly 0.
-// The loads
-// of the values, the scores and the chunk maxima all go out before the first
-// one is used.
-__global__ __launch_bounds__(kAttnThreads) void attn_pv_kernel(
+// (certified_f32).  The P.V sums add the reference's f64 terms in another
+// order (lane r of a head's wave takes every 64th column from r, then the
+// 64 lanes are added in a fixed tree): their f32 results can differ from the
+// reference's in the last bit (the certificate fails for about 2 in 10^4 of
+// these 1024-term sums, and a sequential repeat would cost the whole kernel
+// several microseconds).  With more waves than heads, a head's columns are
+// split over pv_waves_per_head waves whose partials are added in wave order.
+// Columns past `count` have exponential and value 0.
+// The loads of the values, the scores and the chunk maxima all go out before
+// the first one is used.
+__global__ __launch_bounds__(kPvThreads) void attn_pv_kernel(
     const float* __restrict__ scores, const float* __restrict__ cmax, uint32_t cstride, uint32_t nch,
-    const float* __restrict__ vc, uint32_t count, uint32_t heads, uint32_t kv_heads, uint32_t hd, uint32_t row_stride,
-    float* __restrict__ att) {
+    const float* __restrict__ vc, uint32_t max_context, uint32_t count, uint32_t heads, uint32_t kv_heads, uint32_t hd,
+    uint32_t row_stride, float* __restrict__ att) {
     extern __shared__ __align__(16) float sm[];
     const uint32_t G = heads / kv_heads, kvh = blockIdx.y, d0 = blockIdx.x * kPvDims;
     const AttnPvLds Lp = attn_pv_lds(G, count, nch);
-    const uint32_t n4 = (count + 3) / 4 * 4, ngroups = n4 / 4, kvw = kv_heads * hd, rs = Lp.rs;
-    float* e_s = sm;                        // [G][rs] exponentials
+    const uint32_t n4 = (count + 3) / 4 * 4, ngroups = n4 / 4, n64 = Lp.n64;
+    float* e_s = sm;                        // [G][n64] exponentials
     float* g_s = sm + Lp.g;                 // [G][ngroups] f32 pair sums
     float* stat = sm + Lp.stat;             // [G][2]: max, inverse
     float* cm_s = sm + Lp.cm;               // [G][nch]
-    float* vt_s = sm + Lp.v;                // [kPvDims][rs] the values, transposed
-    double* sum_s = (double*)(sm + Lp.part);  // [kPvSegs][G * kPvDims]
-    const uint32_t tid = threadIdx.x, nq = G * ngroups;  // score groups of four columns
+    float4* v_s = (float4*)(sm + Lp.v);     // [n64] the values of dimensions d0 .. d0 + 3
+    double* part = (double*)(sm + Lp.part);  // [G][wph][4]
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nq = G * ngroups;
     // every load of the prologue goes out before the first is used: the
     // chunk maxima, the first kPvScoreRegs score groups per thread (kept in
-    // registers) and the values (to LDS, transposed)
+    // registers) and the values (to LDS)
     float4 sq[kPvScoreRegs];
 #pragma unroll
     for (uint32_t k = 0; k < kPvScoreRegs; ++k) {
-        const uint32_t q = k * kAttnThreads + tid;
+        const uint32_t q = k * kPvThreads + tid;
         sq[k] = q < nq ? *(const float4*)(scores + (uint64_t)(kvh * G + q / ngroups) * row_stride + 4 * (q % ngroups))
                        : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     }
-    for (uint32_t i = tid; i < G * nch; i += kAttnThreads) cm_s[i] = cmax[(kvh * G + i / nch) * cstride + i % nch];
-    const float* vbase = vc + kvh * hd + d0;
-    for (uint32_t base = 0; base < 2 * count; base += kAttnBatch * kAttnThreads) {
+    for (uint32_t i = tid; i < G * nch; i += kPvThreads) cm_s[i] = cmax[(kvh * G + i / nch) * cstride + i % nch];
+    const float4* vsrc = (const float4*)(vc + v_cache_index(kvh, hd, d0, 0, max_context));
+    for (uint32_t base = 0; base < count; base += kAttnBatch * kPvThreads) {
         float4 vr[kAttnBatch];
 #pragma unroll
         for (uint32_t k = 0; k < kAttnBatch; ++k) {
-            const uint32_t j = base + k * kAttnThreads + tid;
-            vr[k] = j < 2 * count ? *(const float4*)(vbase + (uint64_t)(j / 2) * kvw + 4 * (j % 2))
-                                  : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            const uint32_t j = base + k * kPvThreads + tid;
+            vr[k] = j < count ? vsrc[j] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         }
 #pragma unroll
         for (uint32_t k = 0; k < kAttnBatch; ++k) {
-            const uint32_t j = base + k * kAttnThreads + tid;
-            if (j < 2 * count) {
-                float* v = vt_s + 4 * (j % 2) * rs + j / 2;
-                v[0] = vr[k].x, v[rs] = vr[k].y, v[2 * rs] = vr[k].z, v[3 * rs] = vr[k].w;
-            }
+            const uint32_t j = base + k * kPvThreads + tid;
+            if (j < count) v_s[j] = vr[k];
         }
     }
-    for (uint32_t i = tid; i < kPvDims * (Lp.n32 - count); i += kAttnThreads)  // zero padding of the values
-        vt_s[(i / (Lp.n32 - count)) * rs + count + i % (Lp.n32 - count)] = 0.0f;
-    for (uint32_t i = tid; i < G * (Lp.n32 - n4); i += kAttnThreads)  // and of the exponentials
-        e_s[(i / (Lp.n32 - n4)) * rs + n4 + i % (Lp.n32 - n4)] = 0.0f;
+    for (uint32_t j = count + tid; j < n64; j += kPvThreads) v_s[j] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    for (uint32_t i = tid; i < G * (n64 - n4); i += kPvThreads)  // zero exponentials past the last group
+        e_s[(i / (n64 - n4)) * n64 + n4 + i % (n64 - n4)] = 0.0f;
     __syncthreads();
-    if (tid < G) {
+    // the row maxima: one wave per head over its chunk maxima
+    for (uint32_t h = wave; h < G; h += kPvWaves) {
         float m = -INFINITY;
-        for (uint32_t c = 0; c < nch; ++c) m = fmaxf(m, cm_s[tid * nch + c]);
-        stat[2 * tid] = m;
+        for (uint32_t c = lane; c < nch; c += 64) m = fmaxf(m, cm_s[h * nch + c]);
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+        if (lane == 0) stat[2 * h] = m;
     }
     __syncthreads();
     // exponentials and pair sums of each group of four columns (the groups
@@ -259,19 +287,18 @@ __global__ __launch_bounds__(kAttnThreads) void attn_pv_kernel(
         const float m = stat[2 * h];
         const float e0 = t < count ? sse2_exp(x.x - m) : 0.0f, e1 = t + 1 < count ? sse2_exp(x.y - m) : 0.0f;
         const float e2 = t + 2 < count ? sse2_exp(x.z - m) : 0.0f, e3 = t + 3 < count ? sse2_exp(x.w - m) : 0.0f;
-        *(float4*)(e_s + h * rs + t) = make_float4(e0, e1, e2, e3);
+        *(float4*)(e_s + h * n64 + t) = make_float4(e0, e1, e2, e3);
         g_s[q] = (e0 + e1) + (e2 + e3);
     };
 #pragma unroll
     for (uint32_t k = 0; k < kPvScoreRegs; ++k)
-        if (k * kAttnThreads + tid < nq) group(k * kAttnThreads + tid, sq[k]);
-    for (uint32_t q = kPvScoreRegs * kAttnThreads + tid; q < nq; q += kAttnThreads)
+        if (k * kPvThreads + tid < nq) group(k * kPvThreads + tid, sq[k]);
+    for (uint32_t q = kPvScoreRegs * kPvThreads + tid; q < nq; q += kPvThreads)
         group(q, *(const float4*)(scores + (uint64_t)(kvh * G + q / ngroups) * row_stride + 4 * (q % ngroups)));
     __syncthreads();
     // the row sums (math.rs:309-313): one wave per head, certified against the
     // reference's column-order f64 sum (the pair sums are >= 0: sum = sum |.|)
-    const uint32_t lane = tid & 63, wave = tid >> 6;
-    for (uint32_t h = wave; h < G; h += kAttnThreads / 64) {
+    for (uint32_t h = wave; h < G; h += kPvWaves) {
         const float* gp = g_s + h * ngroups;
         double sum = 0.0;
         for (uint32_t g = lane; g < ngroups; g += 64) sum += (double)gp[g];
@@ -288,30 +315,42 @@ __global__ __launch_bounds__(kAttnThreads) void attn_pv_kernel(
         }
     }
     __syncthreads();
-    // P.V with p = e * inverse (math.rs:313-315, 478-480): output o = (head,
-    // dimension) over kPvSegs token segments of seg tokens, four interleaved
-    // f64 chains per thread; the segment sums are added in segment order.  The
-    // f32 products and f64 terms are the reference's; only the order of the
-    // f64 additions differs (see above).  Padding columns give 0 * 0 terms.
-    const uint32_t no = G * kPvDims, seg = Lp.n32 / kPvSegs;
-    for (uint32_t i = tid; i < kPvSegs * no; i += kAttnThreads) {
-        const uint32_t o = i % no, r = i / no;
-        const float inv = stat[2 * (o / kPvDims) + 1];
-        const float* e = e_s + (o / kPvDims) * rs + r * seg;
-        const float* v = vt_s + (o % kPvDims) * rs + r * seg;
-        double a[4] = {0.0, 0.0, 0.0, 0.0};
-        for (uint32_t t = 0; t < seg; t += 4) {
-            const float4 e4 = *(const float4*)(e + t), v4 = *(const float4*)(v + t);
-            a[0] += (double)((e4.x * inv) * v4.x), a[1] += (double)((e4.y * inv) * v4.y);
-            a[2] += (double)((e4.z * inv) * v4.z), a[3] += (double)((e4.w * inv) * v4.w);
+    // P.V with p = e * inverse (math.rs:313-315, 478-480): wph waves per
+    // head, lane r of part w over columns 64 w + r, 64 (w + wph) + r, ...,
+    // one f64 chain per dimension.  The f32 products and f64 terms are the
+    // reference's; only the order of the f64 additions differs (see above).
+    // Padding columns give 0 * 0 terms.
+    const uint32_t wph = pv_waves_per_head(G), hstep = kPvWaves / wph;
+    if (wave < hstep * wph) {
+        for (uint32_t h = wave / wph; h < G; h += hstep) {
+            const uint32_t w = wave % wph;
+            const float inv = stat[2 * h + 1];
+            const float* e = e_s + h * n64;
+            double a0 = 0.0, a1 = 0.0, a2 = 0.0, a3 = 0.0;
+            for (uint32_t t = 64 * w + lane; t < n64; t += 64 * wph) {
+                const float p = e[t] * inv;
+                const float4 v = v_s[t];
+                a0 += (double)(p * v.x), a1 += (double)(p * v.y), a2 += (double)(p * v.z), a3 += (double)(p * v.w);
+            }
+#pragma unroll
+            for (int o = 1; o < 64; o <<= 1) {
+                a0 += __shfl_xor(a0, o, 64);
+                a1 += __shfl_xor(a1, o, 64);
+                a2 += __shfl_xor(a2, o, 64);
+                a3 += __shfl_xor(a3, o, 64);
+            }
+            if (lane == 0) {
+                double* pp = part + (h * wph + w) * 4;
+                pp[0] = a0, pp[1] = a1, pp[2] = a2, pp[3] = a3;
+            }
         }
-        sum_s[r * no + o] = (a[0] + a[1]) + (a[2] + a[3]);
     }
     __syncthreads();
-    for (uint32_t o = tid; o < no; o += kAttnThreads) {
+    for (uint32_t o = tid; o < G * 4; o += kPvThreads) {
+        const uint32_t h = o / 4, j = o % 4;
         double sum = 0.0;
-        for (uint32_t r = 0; r < kPvSegs; ++r) sum += sum_s[r * no + o];
-        att[(kvh * G + o / kPvDims) * hd + d0 + o % kPvDims] = (float)sum;
+        for (uint32_t w = 0; w < wph; ++w) sum += part[(h * wph + w) * 4 + j];
+        att[(kvh * G + h) * hd + d0 + j] = (float)sum;
     }
 }
 
@@ -422,13 +461,12 @@ hipError_t LlamaModel::create(const LlamaDims& dims, const LlamaHostTensors& t, 
     }
     const uint64_t row_len = (d.max_context + 255) / 256 * 256, nchunks = (d.max_context + kAttnChunk - 1) / kAttnChunk;
     // the attention workgroups' LDS grows with the context (the caller checked
-    // that it fits next to the kernels' few static bytes)
     // that it fits next to the kernels' few static bytes); the limits only grow,
     // so models of other shapes in the process keep working
     static int pv_set = 64 * 1024, scores_set = 64 * 1024;
     const uint32_t G = (uint32_t)(d.heads / d.kv_heads);
     const int pv_need = (int)(attn_pv_lds(G, (uint32_t)d.max_context, (uint32_t)nchunks).total * sizeof(float));
-    const int scores_need = (int)((G * hd + kAttnChunk * (hd + 4)) * sizeof(float));
+    const int scores_need = (int)attn_scores_lds(G, (uint32_t)hd);
     hipError_t e = hipSuccess;
     if (pv_need > pv_set) {
         e = hipFuncSetAttribute((const void*)attn_pv_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, pv_need);
@@ -546,7 +584,7 @@ hipError_t LlamaModel::step(float* hidden, uint64_t position, float* embedding_o
     const uint32_t nchunks = (uint32_t)((count + kAttnChunk - 1) / kAttnChunk);
     const float scale = d.attention_scale != 0.0f ? d.attention_scale : 1.0f / sqrtf((float)hd);
     const float* tab = rope_tab + position * hd;
-    const size_t lds_scores = (H / KVH * hd + kAttnChunk * (hd + 4)) * sizeof(float);
+    const size_t lds_scores = attn_scores_lds((uint32_t)(H / KVH), (uint32_t)hd);
     const size_t lds_pv = attn_pv_lds((uint32_t)(H / KVH), (uint32_t)count, nchunks).total * sizeof(float);
     const uint32_t cstride = (uint32_t)((d.max_context + kAttnChunk - 1) / kAttnChunk);
     hipError_t e = hipSuccess;
@@ -571,11 +609,11 @@ hipError_t LlamaModel::step(float* hidden, uint64_t position, float* embedding_o
         }
         if (e != hipSuccess) break;
         hipLaunchKernelGGL(attn_scores_kernel, dim3(nchunks, (uint32_t)KVH), dim3(kAttnThreads), lds_scores, s, qkv,
-                           tab, kc, vc, (uint32_t)fresh, (uint32_t)H, (uint32_t)KVH, (uint32_t)hd, scale, scores,
+                           tab, kc, vc, (uint32_t)d.max_context, (uint32_t)fresh, (uint32_t)H, (uint32_t)KVH, (uint32_t)hd, scale, scores,
                            (uint32_t)row_stride, cmax, cstride, err_word);
-        hipLaunchKernelGGL(attn_pv_kernel, dim3((uint32_t)(hd / kPvDims), (uint32_t)KVH), dim3(kAttnThreads), lds_pv, s,
-                           scores, cmax, cstride, nchunks, vc, (uint32_t)count, (uint32_t)H, (uint32_t)KVH,
-                           (uint32_t)hd, (uint32_t)row_stride, att);
+        hipLaunchKernelGGL(attn_pv_kernel, dim3((uint32_t)(hd / kPvDims), (uint32_t)KVH), dim3(kPvThreads), lds_pv, s,
+                           scores, cmax, cstride, nchunks, vc, (uint32_t)d.max_context, (uint32_t)count, (uint32_t)H,
+                           (uint32_t)KVH, (uint32_t)hd, (uint32_t)row_stride, att);
         e = hipGetLastError();
         if (e != hipSuccess) break;
         MvExtra res;
