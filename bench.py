@@ -130,6 +130,64 @@ def time_steps(rlq, ctx, handles, x, y, steps, warmup):
     return start.elapsed_time(end) / steps
 
 
+def call_distribution(rlq, ctx, handles, x, y, calls):
+    """Median and p90 of single rlq_matmul calls, each bracketed by its own
+    pair of HIP events on the launch stream (weights rotated as in the timed
+    loop); the events' own cost is included."""
+    torch = rlq.torch
+    n = len(handles)
+    stream = torch.cuda.current_stream()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(calls)]
+    torch.cuda.synchronize()
+    for i, (a, b) in enumerate(ev):
+        a.record(stream)
+        ctx.matmul(handles[i % n], x, y)
+        b.record(stream)
+    torch.cuda.synchronize()
+    ctx.sync()
+    us = np.sort(np.array([a.elapsed_time(b) * 1e3 for a, b in ev]))
+    return {"calls": calls, "median_us": round(float(np.median(us)), 3),
+            "p90_us": round(float(us[int(0.9 * (calls - 1))]), 3)}
+
+
+def practical_peaks(torch, reps=20):
+    """Measured ceilings beside the spec peaks: a 1 GiB device-to-device copy
+    (bytes read + written per second), and torch's (hipBLASLt) dense f16 and
+    int8 GEMMs at 8192^3."""
+    out = {}
+
+    def timed(fn):
+        fn()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(reps):
+            fn()
+        b.record()
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) / reps * 1e-3
+
+    src = torch.empty(1 << 30, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    out["copy_gbs"] = round(2 * src.numel() / timed(lambda: dst.copy_(src)) / 1e9, 1)
+    del src, dst
+    n = 8192
+    a = torch.randn((n, n), device="cuda", dtype=torch.float16)
+    b = torch.randn((n, n), device="cuda", dtype=torch.float16)
+    out["f16_gemm_tflops"] = round(2 * n ** 3 / timed(lambda: torch.mm(a, b)) / 1e12, 1)
+    del a, b
+    try:
+        a8 = torch.randint(-127, 127, (n, n), device="cuda", dtype=torch.int8)
+        b8 = torch.randint(-127, 127, (n, n), device="cuda", dtype=torch.int8)
+        out["int8_gemm_tops"] = round(2 * n ** 3 / timed(lambda: torch._int_mm(a8, b8)) / 1e12, 1)
+        del a8, b8
+    except (RuntimeError, AttributeError) as e:
+        out["int8_gemm_tops"] = None
+        out["int8_note"] = str(e).splitlines()[0][:120]
+    torch.cuda.empty_cache()
+    return out
+
+
 def prefill(rlq, ctx, handles, rows, cols, steps, warmup):
     """The prefill GEMM over the rotated weight copies: M=512 tokens of N(0,1)."""
     torch = rlq.torch
@@ -152,23 +210,34 @@ def prefill(rlq, ctx, handles, rows, cols, steps, warmup):
     }
 
 
-def cpu_baseline(dtype, w_host, rows, cols, x_host, budget_s=10.0):
-    """Oracle matvec (the reference's scalar path restated in C), 1 thread."""
+def cpu_baseline(dtype, w_host, rows, cols, x_host, budget_s=10.0, all_cores_s=5.0):
+    """Oracle matvec (the reference's scalar path restated in C): 1 thread (the
+    reference never threads a matvec), then row-parallel over the host cores
+    this job may use (at most 16) as a second figure."""
     import oracle
 
-    t0 = time.perf_counter()
-    reps = 0
-    while True:
-        oracle.matvec(int(dtype), w_host, rows, cols, x_host, threads=1)
-        reps += 1
-        el = time.perf_counter() - t0
-        if el >= budget_s:
-            break
+    def timed(threads, budget):
+        t0 = time.perf_counter()
+        reps = 0
+        while True:
+            oracle.matvec(int(dtype), w_host, rows, cols, x_host, threads=threads)
+            reps += 1
+            el = time.perf_counter() - t0
+            if el >= budget:
+                return reps, el
+
+    nbytes = w_host.size + 4 * cols + 4 * rows
+    reps, el = timed(1, budget_s)
     per = el / reps
-    gbs = (w_host.size + 4 * cols + 4 * rows) / per / 1e9
-    return {"value": round(gbs, 4), "unit": "GB/s", "cores": 1, "kind": "port",
-            "sample": f"{reps} full {rows}x{cols} Q4_K matvecs of the benchmark's weights in {el:.1f} s "
-                      f"({per * 1e3:.1f} ms each), oracle/rlq_oracle.c built with gcc -O2 -ffp-contract=off"}
+    out = {"value": round(nbytes / per / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
+           "sample": f"{reps} full {rows}x{cols} Q4_K matvecs of the benchmark's weights in {el:.1f} s "
+                     f"({per * 1e3:.1f} ms each), oracle/rlq_oracle.c built with gcc -O2 -ffp-contract=off"}
+    cores = max(1, min(16, os.cpu_count() or 1))
+    if cores > 1:
+        reps, el = timed(cores, all_cores_s)
+        out["all_cores"] = {"value": round(nbytes / (el / reps) / 1e9, 4), "unit": "GB/s", "cores": cores,
+                            "sample": f"{reps} matvecs in {el:.1f} s, rows split over {cores} threads"}
+    return out
 
 
 def run_config(rlq, ctx, dtype, rows, cols, batch, seed, steps, warmup, copies):
@@ -420,7 +489,10 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(head["gbs"], 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(head["gbs"] / HBM_PEAK_GBS, 4), "traffic": TRAFFIC_DECODE_BYTES},
     }
+    result["single_call"] = call_distribution(rlq, ctx, handles, x,
+                                           torch.empty((1, rows), device="cuda", dtype=torch.float32), 200)
     result["prefill"] = prefill(rlq, ctx, handles, rows, cols, max(50, args.steps // 10), max(5, args.warmup // 5))
+    result["practical_peaks"] = practical_peaks(torch)
     if not args.no_cpu:
         xh = x.cpu().numpy().reshape(-1)
         result["cpu_baseline"] = cpu_baseline(DT.Q4_K, host0, rows, cols, xh)
