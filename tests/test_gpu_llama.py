@@ -152,6 +152,38 @@ def test_one_layer_parts(ctx, wt, mixed):
     print("worst relative L2 per part:", worst)
 
 
+@pytest.mark.parametrize("heads,kv_heads,width", [(4, 4, 256), (8, 1, 256), (16, 4, 256), (1, 1, 256),
+                                                  (32, 1, 512), (12, 4, 768)])
+def test_attention_head_shapes(ctx, heads, kv_heads, width):
+    """The attention kernels over head layouts the 8B shape does not use:
+    MHA (one query head per KV head), 8 and 32 query heads per KV head (more
+    heads than P.V waves), 3 per KV head (waves left idle), and head
+    dimensions 16 (the smallest: quarters of one float4) and 256 (the
+    largest).  70 steps cross five 16-token score chunks and the 64-column
+    P.V boundary; the attention output is checked against the oracle fed
+    with the GPU's own q/k/v."""
+    say("llama attention heads", heads, "kv heads", kv_heads, "width", width, "70 steps")
+    cfg, t, g, o = models(ctx, 1, 31, width=width, heads=heads, kv_heads=kv_heads, max_context=80)
+    W, kvw, hd = cfg.width, cfg.kv_width, cfg.head_dim
+    scale = np.float32(1.0) / np.sqrt(np.float32(hd))
+    kc = np.zeros((cfg.max_context, kvw), np.float32)
+    vc = np.zeros_like(kc)
+    rng = np.random.default_rng(9)
+    last_bit = 0
+    for step in range(70):
+        h = torch.from_numpy(o.embedding(int(rng.integers(cfg.vocabulary)))).cuda()
+        g.step(h, step, embedding=False, logits=False)
+        qkv, att, _ = (host(x) for x in g.intermediates())
+        ctx.sync()
+        q = O.rope(qkv[:W], hd, step, cfg.rope_base)
+        kc[step] = O.rope(qkv[W:W + kvw], hd, step, cfg.rope_base)
+        vc[step] = qkv[W + kvw:]
+        want = O.attention(q, kc[:step + 1], vc[:step + 1], step + 1, cfg.heads, cfg.kv_heads, hd, scale)
+        assert np.all(np.abs(att - want) <= np.spacing(np.abs(want))), step
+        last_bit += int(np.sum(att != want))
+    print("outputs differing in the last bit:", last_bit, "of", 70 * W)
+
+
 @pytest.mark.parametrize("wt,ot", [(O.Q4_K, O.Q6_K), (O.Q6_K, O.Q8_0)])
 def test_free_running_steps(ctx, wt, ot):
     say("llama 2 layers, 12 free-running steps, logits vs oracle, types", wt, ot)
