@@ -651,16 +651,22 @@ hipError_t LlamaModel::step(float* hidden, uint64_t position, float* embedding_o
     if (logits || argmax) {
         MvExtra norm3;
         norm3.xform = 1, norm3.eps = d.rms_epsilon, norm3.norm_w = out_norm;
-        if (argmax) {
-            e = launch_fill_u64(argmax_keys, 1, 0ull, s);
-            if (e != hipSuccess) return e;
+        if (argmax) {  // the keys start at 0: left so by the last step's finish, or cleared here
+            if (!keys_zero) {
+                e = launch_fill_u64(argmax_keys, 1, 0ull, s);
+                if (e != hipSuccess) return e;
+            }
+            keys_zero = false;
         }
         // logits land in the caller's buffer, or in the model's own when only
         // the argmax is wanted
         float* y = logits ? logits : logits_buf;
         e = launch_matvec_ex(d.output_type, out_w, d.vocab, W, hidden, nullptr, 1, y, d.vocab,
                              argmax ? argmax_keys : nullptr, err_word, nullptr, nullptr, norm3, s);
-        if (e == hipSuccess && argmax) e = launch_argmax_finish(argmax_keys, 1, y, d.vocab, argmax, s);
+        if (e == hipSuccess && argmax) {
+            e = launch_argmax_finish(argmax_keys, 1, y, d.vocab, argmax, s, true);
+            keys_zero = e == hipSuccess;
+        }
         if (e != hipSuccess) return e;
     }
     ++n_cached;

@@ -1666,12 +1666,13 @@ hipError_t launch_mm_prepare(const int32_t* ids, uint64_t pairs, uint32_t expert
     return hipGetLastError();
 }
 
-__global__ void argmax_finish_kernel(const unsigned long long* keys, uint64_t batch, const float* y, uint64_t ldy,
-                                     uint32_t* out) {
+__global__ void argmax_finish_kernel(unsigned long long* keys, uint64_t batch, const float* y, uint64_t ldy,
+                                     uint32_t* out, bool reset) {
     const uint64_t b = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (b >= batch) return;
     const float y0 = y[b * ldy];
     const unsigned long long k = keys[b];
+    if (reset) keys[b] = 0ull;
     // A NaN first logit is never replaced by the reference's strict `>` scan.
     out[b] = (y0 != y0 || k == 0) ? 0u : (uint32_t)(0xffffffffull - (k & 0xffffffffull));
 }
@@ -1701,10 +1702,10 @@ hipError_t launch_argmax_rows(const float* y, uint64_t batch, uint64_t rows, uns
     return hipGetLastError();
 }
 
-hipError_t launch_argmax_finish(const unsigned long long* keys, uint64_t batch, const float* y, uint64_t ldy,
-                                uint32_t* out, hipStream_t s) {
+hipError_t launch_argmax_finish(unsigned long long* keys, uint64_t batch, const float* y, uint64_t ldy, uint32_t* out,
+                                hipStream_t s, bool reset) {
     hipLaunchKernelGGL(argmax_finish_kernel, dim3((unsigned)((batch + 63) / 64)), dim3(64), 0, s, keys, batch, y, ldy,
-                       out);
+                       out, reset);
     return hipGetLastError();
 }
 

@@ -159,8 +159,9 @@ struct LlamaModel {
     uint8_t *out_w = nullptr, *emb = nullptr;  // tiled output matrix; GGUF embedding rows
     float *out_norm = nullptr, *k_cache = nullptr, *v_cache = nullptr, *rope_tab = nullptr;
     float *qkv = nullptr, *scores = nullptr, *att = nullptr, *gu = nullptr, *logits_buf = nullptr;
-    float* cmax = nullptr;  // [heads][chunks of 64 tokens] chunk maxima of the scores
+    float* cmax = nullptr;  // [heads][chunks of 16 tokens] chunk maxima of the scores
     unsigned long long* argmax_keys = nullptr;
+    bool keys_zero = false;  // argmax_keys is 0 in stream order (the last step's finish reset it)
     uint64_t n_cached = 0;  // KV rows held (the insertion index of the next step)
 
     ~LlamaModel();
@@ -176,8 +177,8 @@ struct LlamaModel {
 
 // Argmax keys of the stored rows y[b*rows ..] (keys zeroed beforehand).
 hipError_t launch_argmax_rows(const float* y, uint64_t batch, uint64_t rows, unsigned long long* keys, hipStream_t s);
-// Decode argmax keys into u32 indices.
-hipError_t launch_argmax_finish(const unsigned long long* keys, uint64_t batch, const float* y, uint64_t ldy,
-                                uint32_t* out, hipStream_t s);
+// Decode argmax keys into u32 indices; reset: then set the keys back to 0.
+hipError_t launch_argmax_finish(unsigned long long* keys, uint64_t batch, const float* y, uint64_t ldy, uint32_t* out,
+                                hipStream_t s, bool reset = false);
 
 }  // namespace rlq
