@@ -169,19 +169,21 @@ def test_matmul_batches_against_oracle(ctx, t, batch):
 
 
 @pytest.mark.parametrize("t", K_OTHER)
-def test_encoded_weights_against_oracle(ctx, t):
+@pytest.mark.parametrize("batch", [2, 1])
+def test_encoded_weights_against_oracle(ctx, t, batch):
     """Weights from the oracle's encoders (the reference's encode_k.rs), a
-    shape with 17 blocks per row and a partial last tile."""
+    shape with 17 blocks per row and a partial last tile (batch 1: the
+    16-wave K split that rows of more than 16 blocks take)."""
     rows, cols = 77, 17 * 256
-    say("encoded weights matvec", t, rows, cols)
+    say("encoded weights matvec", t, rows, cols, "batch", batch)
     w = encoded(t, rows, cols, 31)
-    x = randn(32, 2 * cols).reshape(2, cols)
+    x = randn(32, 2 * cols).reshape(2, cols)[:batch]
     W = rlq.Weights(ctx, t, w, rows, cols)
-    y = ctx.matmul(W, torch.from_numpy(x).cuda())
+    y = ctx.matmul(W, torch.from_numpy(np.ascontiguousarray(x)).cuda())
     ctx.sync()
     want = O.matmul(int(t), w, rows, cols, x, threads=8)
     got = y.cpu().numpy()
-    for b in range(2):
+    for b in range(batch):
         act = O.quantize(O.Q8_K, x[b])
         assert rel_l2(got[b], want[b]) <= REL_L2
         assert np.all(np.abs(got[b] - want[b]) <= elem_tol(t, w, rows, act, cols, want[b]))
