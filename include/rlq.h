@@ -287,8 +287,9 @@ typedef struct rlq_llama_tensors {
  * grouping, 4 odd head_dim, 5 RoPE base, 6 attention scale, 7 KV size
  * overflow) and this library's limits (RLQ_UNIMPLEMENTED: a weight type off
  * the path, width / feed_forward not multiples of 256, kv_width not a
- * multiple of 16, head_dim not a multiple of 16 or above 256, or a workgroup's attention
- * rows beyond 159 KB of LDS), then uploads and tiles the weights.
+ * multiple of 16, head_dim not a multiple of 16 or above 256, or a score workgroup's
+ * G query heads' rows beyond 159 KB of LDS: only for hundreds of query heads per KV
+ * head; the context length is not limited by LDS), then uploads and tiles the weights.
  * The tensors may be freed when this returns. */
 int32_t rlq_llama_create(rlq_context *ctx, const rlq_llama_config *cfg, const rlq_llama_tensors *tensors,
                          rlq_llama **out, rlq_error *err);

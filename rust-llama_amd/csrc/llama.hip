@@ -34,11 +34,10 @@ constexpr uint32_t kAttnMaxHd = 256;  // head dimension limit
 constexpr uint32_t kScKeyRegs = kAttnMaxHd * kAttnChunk / 4 / kAttnThreads;  // float4 of a chunk's keys per thread
 constexpr uint32_t kScKeyPad = 16;  // floats after each key row in LDS
 
-constexpr uint32_t kAttnBatch = 16;   // value loads in flight per thread in the P.V prologue
 constexpr uint32_t kPvDims = 4;       // head dimensions per P.V workgroup: one float4 of each value row
 constexpr uint32_t kPvThreads = 512;
 constexpr uint32_t kPvWaves = kPvThreads / 64;
-constexpr uint32_t kPvScoreRegs = 4;  // score groups of four per thread held in registers (G * count <= 8192)
+constexpr uint32_t kPvRegGroups = 4;  // column groups of four per lane whose values and exponentials stay in registers
 
 // The value cache of a layer is slice-major: [kv_heads * hd / 4][max_context]
 // float4, slice kvh * hd / 4 + d / 4 holding dimensions d .. d + 3 of kv head
@@ -51,24 +50,18 @@ __host__ __device__ inline uint64_t v_cache_index(uint32_t kvh, uint32_t hd, uin
 // P.V waves per head: the waves of a workgroup split G heads' columns.
 __host__ __device__ inline uint32_t pv_waves_per_head(uint32_t G) { return G < kPvWaves ? kPvWaves / G : 1u; }
 
-// LDS of attn_pv_kernel, in floats: exponentials [G][n64], pair sums
-// [G][n4/4], max and inverse [G][2], chunk maxima [G][nch], the values [n64]
-// float4 at a 16-byte aligned offset, then the f64 wave partials
-// [G][waves per head][4].  n64 = count rounded up to 64 (one column per lane
-// of a wave); the columns past count are zero.
+// LDS of attn_pv_kernel, in floats: max and inverse [G][2], then the f64
+// partial row sums [G][waves per head] and P.V partials [G][waves per head][4].
+// It does not grow with the context: the scores and values stream from HBM.
 struct AttnPvLds {
-    uint32_t n64, g, stat, cm, v, part, total;
+    uint32_t rsum, part, total;
 };
-__host__ __device__ inline AttnPvLds attn_pv_lds(uint32_t G, uint32_t count, uint32_t nch) {
+__host__ __device__ inline AttnPvLds attn_pv_lds(uint32_t G) {
     AttnPvLds l;
-    const uint32_t n4 = (count + 3) / 4 * 4;
-    l.n64 = (count + 63) / 64 * 64;
-    l.g = G * l.n64;
-    l.stat = l.g + G * (n4 / 4);
-    l.cm = l.stat + 2 * G;
-    l.v = (l.cm + G * nch + 3) & ~3u;
-    l.part = l.v + 4 * l.n64;
-    l.total = l.part + 2 * 4 * G * pv_waves_per_head(G);
+    const uint32_t wph = pv_waves_per_head(G);
+    l.rsum = (2 * G + 1) & ~1u;
+    l.part = l.rsum + 2 * G * wph;
+    l.total = l.part + 2 * 4 * G * wph;
     return l;
 }
 __host__ __device__ inline uint32_t attn_scores_lds(uint32_t G, uint32_t hd) {
@@ -76,8 +69,9 @@ __host__ __device__ inline uint32_t attn_scores_lds(uint32_t G, uint32_t hd) {
 }
 
 uint64_t llama_attn_lds_bytes(uint64_t heads, uint64_t kv_heads, uint64_t head_dim, uint64_t max_context) {
-    const uint64_t G = heads / kv_heads, nch = (max_context + kAttnChunk - 1) / kAttnChunk;
-    const uint64_t pv = (uint64_t)attn_pv_lds((uint32_t)G, (uint32_t)max_context, (uint32_t)nch).total * 4;
+    const uint64_t G = heads / kv_heads;
+    (void)max_context;
+    const uint64_t pv = (uint64_t)attn_pv_lds((uint32_t)G).total * 4;
     const uint64_t sc = attn_scores_lds((uint32_t)G, (uint32_t)head_dim);
     return pv > sc ? pv : sc;
 }
@@ -215,122 +209,147 @@ __global__ __launch_bounds__(kAttnThreads) void attn_scores_kernel(
 // Softmax of the G heads' score rows (math.rs:293-318 with the SSE2 policy of
 // cpu_math.rs:60-91) and P.V (math.rs:475-482) for 4 of the head dimensions:
 // workgroup (blockIdx.x, blockIdx.y) = (dimensions 4 * blockIdx.x .., kv head).
-// Every workgroup of the kv head recomputes the G rows' softmax from the chunk
-// maxima; the softmax totals are certified against the reference's order
-// (certified_f32).  The P.V sums add the reference's f64 terms in another
-// order (lane r of a head's wave takes every 64th column from r, then the
-// 64 lanes are added in a fixed tree): their f32 results can differ from the
-// reference's in the last bit (the certificate fails for about 2 in 10^4 of
-// these 1024-term sums, and a sequential repeat would cost the whole kernel
-// several microseconds).  With more waves than heads, a head's columns are
-// split over pv_waves_per_head waves whose partials are added in wave order.
-// Columns past `count` have exponential and value 0.
-// The loads of the values, the scores and the chunk maxima all go out before
-// the first one is used.
+// Every workgroup of the kv head computes the G rows' softmax from the chunk
+// maxima.  The columns go in groups of four (the reference's SSE2 vectors);
+// lane r of part w of a head's wph waves takes groups 64 w + r, + 64 wph, ...
+// Its first kPvRegGroups groups' values are loaded when the kernel starts and
+// their exponentials kept from the row sums; later groups are reloaded and
+// their exponentials recomputed (the same f32 function of the same inputs),
+// so the LDS does not grow with the context.  The softmax totals are
+// certified against the reference's order (certified_f32).  The P.V sums add
+// the reference's f64 terms in another order (per lane, then the 64 lanes in
+// a fixed tree, then the head's waves in order): their f32 results can differ
+// from the reference's in the last bit (the certificate fails for about 2 in
+// 10^4 of these 1024-term sums, and a sequential repeat would cost the whole
+// kernel several microseconds).  Columns past `count` have exponential 0.
+__device__ __forceinline__ void exp_group(float4 x, uint32_t t, uint32_t count, float m, float (&e)[4]) {
+    e[0] = t < count ? sse2_exp(x.x - m) : 0.0f;
+    e[1] = t + 1 < count ? sse2_exp(x.y - m) : 0.0f;
+    e[2] = t + 2 < count ? sse2_exp(x.z - m) : 0.0f;
+    e[3] = t + 3 < count ? sse2_exp(x.w - m) : 0.0f;
+}
+
 __global__ __launch_bounds__(kPvThreads) void attn_pv_kernel(
     const float* __restrict__ scores, const float* __restrict__ cmax, uint32_t cstride, uint32_t nch,
     const float* __restrict__ vc, uint32_t max_context, uint32_t count, uint32_t heads, uint32_t kv_heads, uint32_t hd,
     uint32_t row_stride, float* __restrict__ att) {
     extern __shared__ __align__(16) float sm[];
     const uint32_t G = heads / kv_heads, kvh = blockIdx.y, d0 = blockIdx.x * kPvDims;
-    const AttnPvLds Lp = attn_pv_lds(G, count, nch);
-    const uint32_t n4 = (count + 3) / 4 * 4, ngroups = n4 / 4, n64 = Lp.n64;
-    float* e_s = sm;                        // [G][n64] exponentials
-    float* g_s = sm + Lp.g;                 // [G][ngroups] f32 pair sums
-    float* stat = sm + Lp.stat;             // [G][2]: max, inverse
-    float* cm_s = sm + Lp.cm;               // [G][nch]
-    float4* v_s = (float4*)(sm + Lp.v);     // [n64] the values of dimensions d0 .. d0 + 3
-    double* part = (double*)(sm + Lp.part);  // [G][wph][4]
-    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, nq = G * ngroups;
-    // every load of the prologue goes out before the first is used: the
-    // chunk maxima, the first kPvScoreRegs score groups per thread (kept in
-    // registers) and the values (to LDS)
-    float4 sq[kPvScoreRegs];
-#pragma unroll
-    for (uint32_t k = 0; k < kPvScoreRegs; ++k) {
-        const uint32_t q = k * kPvThreads + tid;
-        sq[k] = q < nq ? *(const float4*)(scores + (uint64_t)(kvh * G + q / ngroups) * row_stride + 4 * (q % ngroups))
-                       : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    }
-    for (uint32_t i = tid; i < G * nch; i += kPvThreads) cm_s[i] = cmax[(kvh * G + i / nch) * cstride + i % nch];
+    const AttnPvLds Lp = attn_pv_lds(G);
+    float* stat = sm;                          // [G][2]: max, inverse
+    double* rsum = (double*)(sm + Lp.rsum);    // [G][wph]
+    double* part = (double*)(sm + Lp.part);    // [G][wph][4]
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t ngroups = (count + 3) / 4;
+    const uint32_t wph = pv_waves_per_head(G), hstep = kPvWaves / wph;
+    const bool active = wave < hstep * wph;  // wave-uniform
+    const uint32_t w = wave % wph, h0 = wave / wph, gstride = 64 * wph, g0 = 64 * w + lane;
     const float4* vsrc = (const float4*)(vc + v_cache_index(kvh, hd, d0, 0, max_context));
-    for (uint32_t base = 0; base < count; base += kAttnBatch * kPvThreads) {
-        float4 vr[kAttnBatch];
+    // the values of this lane's first groups (shared by every head of the kv head)
+    float4 vr[kPvRegGroups][4];
 #pragma unroll
-        for (uint32_t k = 0; k < kAttnBatch; ++k) {
-            const uint32_t j = base + k * kPvThreads + tid;
-            vr[k] = j < count ? vsrc[j] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        }
+    for (uint32_t k = 0; k < kPvRegGroups; ++k)
 #pragma unroll
-        for (uint32_t k = 0; k < kAttnBatch; ++k) {
-            const uint32_t j = base + k * kPvThreads + tid;
-            if (j < count) v_s[j] = vr[k];
+        for (uint32_t j = 0; j < 4; ++j) {
+            const uint32_t t = 4 * (g0 + k * gstride) + j;
+            vr[k][j] = active && t < count ? vsrc[t] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         }
-    }
-    for (uint32_t j = count + tid; j < n64; j += kPvThreads) v_s[j] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    for (uint32_t i = tid; i < G * (n64 - n4); i += kPvThreads)  // zero exponentials past the last group
-        e_s[(i / (n64 - n4)) * n64 + n4 + i % (n64 - n4)] = 0.0f;
-    __syncthreads();
     // the row maxima: one wave per head over its chunk maxima
     for (uint32_t h = wave; h < G; h += kPvWaves) {
         float m = -INFINITY;
-        for (uint32_t c = lane; c < nch; c += 64) m = fmaxf(m, cm_s[h * nch + c]);
+        for (uint32_t c = lane; c < nch; c += 64) m = fmaxf(m, cmax[(kvh * G + h) * cstride + c]);
 #pragma unroll
         for (int o = 1; o < 64; o <<= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
         if (lane == 0) stat[2 * h] = m;
     }
     __syncthreads();
-    // exponentials and pair sums of each group of four columns (the groups
-    // past kPvScoreRegs per thread are loaded here)
-    auto group = [&](uint32_t q, float4 x) {
-        const uint32_t h = q / ngroups, t = 4 * (q % ngroups);
-        const float m = stat[2 * h];
-        const float e0 = t < count ? sse2_exp(x.x - m) : 0.0f, e1 = t + 1 < count ? sse2_exp(x.y - m) : 0.0f;
-        const float e2 = t + 2 < count ? sse2_exp(x.z - m) : 0.0f, e3 = t + 3 < count ? sse2_exp(x.w - m) : 0.0f;
-        *(float4*)(e_s + h * n64 + t) = make_float4(e0, e1, e2, e3);
-        g_s[q] = (e0 + e1) + (e2 + e3);
-    };
+    // exponentials and f32 pair sums of each group (math.rs:303-313), the
+    // lane's pair sums added in f64; the first head's first groups keep
+    // their exponentials for P.V
+    float er[kPvRegGroups][4];
+    if (active) {
+        for (uint32_t h = h0; h < G; h += hstep) {
+            const float m = stat[2 * h];
+            const float* srow = scores + (uint64_t)(kvh * G + h) * row_stride;
+            double sum = 0.0;
 #pragma unroll
-    for (uint32_t k = 0; k < kPvScoreRegs; ++k)
-        if (k * kPvThreads + tid < nq) group(k * kPvThreads + tid, sq[k]);
-    for (uint32_t q = kPvScoreRegs * kPvThreads + tid; q < nq; q += kPvThreads)
-        group(q, *(const float4*)(scores + (uint64_t)(kvh * G + q / ngroups) * row_stride + 4 * (q % ngroups)));
-    __syncthreads();
-    // the row sums (math.rs:309-313): one wave per head, certified against the
-    // reference's column-order f64 sum (the pair sums are >= 0: sum = sum |.|)
-    for (uint32_t h = wave; h < G; h += kPvWaves) {
-        const float* gp = g_s + h * ngroups;
-        double sum = 0.0;
-        for (uint32_t g = lane; g < ngroups; g += 64) sum += (double)gp[g];
+            for (uint32_t k = 0; k < kPvRegGroups; ++k) {
+                const uint32_t g = g0 + k * gstride;
+                float e[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+                if (g < ngroups) exp_group(*(const float4*)(srow + 4 * g), 4 * g, count, m, e);
+                if (h == h0) {
 #pragma unroll
-        for (int o = 1; o < 64; o <<= 1) sum += __shfl_xor(sum, o, 64);
-        if (lane == 0) {
-            float inv;
-            if (!certified_f32(sum, sum, ngroups, [](double x) { return (float)(1.0 / x); }, &inv)) {
-                double seq = 0.0;
-                for (uint32_t g = 0; g < ngroups; ++g) seq += (double)gp[g];
-                inv = (float)(1.0 / seq);
+                    for (uint32_t j = 0; j < 4; ++j) er[k][j] = e[j];
+                }
+                sum += (double)((e[0] + e[1]) + (e[2] + e[3]));
             }
-            stat[2 * h + 1] = inv;
+            for (uint32_t g = g0 + kPvRegGroups * gstride; g < ngroups; g += gstride) {
+                float e[4];
+                exp_group(*(const float4*)(srow + 4 * g), 4 * g, count, m, e);
+                sum += (double)((e[0] + e[1]) + (e[2] + e[3]));
+            }
+#pragma unroll
+            for (int o = 1; o < 64; o <<= 1) sum += __shfl_xor(sum, o, 64);
+            if (lane == 0) rsum[h * wph + w] = sum;
         }
     }
     __syncthreads();
-    // P.V with p = e * inverse (math.rs:313-315, 478-480): wph waves per
-    // head, lane r of part w over columns 64 w + r, 64 (w + wph) + r, ...,
-    // one f64 chain per dimension.  The f32 products and f64 terms are the
-    // reference's; only the order of the f64 additions differs (see above).
-    // Padding columns give 0 * 0 terms.
-    const uint32_t wph = pv_waves_per_head(G), hstep = kPvWaves / wph;
-    if (wave < hstep * wph) {
-        for (uint32_t h = wave / wph; h < G; h += hstep) {
-            const uint32_t w = wave % wph;
-            const float inv = stat[2 * h + 1];
-            const float* e = e_s + h * n64;
+    // the row totals, certified against the reference's column-order f64 sum
+    // (the pair sums are >= 0: sum = sum |.|), else repeated in that order
+    for (uint32_t h = tid; h < G; h += kPvThreads) {
+        double sum = 0.0;
+        for (uint32_t v = 0; v < wph; ++v) sum += rsum[h * wph + v];
+        float inv;
+        if (!certified_f32(sum, sum, ngroups, [](double x) { return (float)(1.0 / x); }, &inv)) {
+            const float m = stat[2 * h];
+            const float* srow = scores + (uint64_t)(kvh * G + h) * row_stride;
+            double seq = 0.0;
+            for (uint32_t g = 0; g < ngroups; ++g) {
+                float e[4];
+                exp_group(*(const float4*)(srow + 4 * g), 4 * g, count, m, e);
+                seq += (double)((e[0] + e[1]) + (e[2] + e[3]));
+            }
+            inv = (float)(1.0 / seq);
+        }
+        stat[2 * h + 1] = inv;
+    }
+    __syncthreads();
+    // P.V with p = e * inverse (math.rs:313-315, 478-480), one f64 chain per
+    // dimension.  The f32 products and f64 terms are the reference's; only
+    // the order of the f64 additions differs (see above).
+    if (active) {
+        for (uint32_t h = h0; h < G; h += hstep) {
+            const float m = stat[2 * h], inv = stat[2 * h + 1];
+            const float* srow = scores + (uint64_t)(kvh * G + h) * row_stride;
             double a0 = 0.0, a1 = 0.0, a2 = 0.0, a3 = 0.0;
-            for (uint32_t t = 64 * w + lane; t < n64; t += 64 * wph) {
-                const float p = e[t] * inv;
-                const float4 v = v_s[t];
-                a0 += (double)(p * v.x), a1 += (double)(p * v.y), a2 += (double)(p * v.z), a3 += (double)(p * v.w);
+            auto add = [&](const float (&e)[4], const float4 (&v)[4]) {
+#pragma unroll
+                for (uint32_t j = 0; j < 4; ++j) {
+                    const float p = e[j] * inv;
+                    a0 += (double)(p * v[j].x), a1 += (double)(p * v[j].y);
+                    a2 += (double)(p * v[j].z), a3 += (double)(p * v[j].w);
+                }
+            };
+#pragma unroll
+            for (uint32_t k = 0; k < kPvRegGroups; ++k) {
+                const uint32_t g = g0 + k * gstride;
+                float e[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+                if (h == h0) {
+#pragma unroll
+                    for (uint32_t j = 0; j < 4; ++j) e[j] = er[k][j];
+                } else if (g < ngroups) {
+                    exp_group(*(const float4*)(srow + 4 * g), 4 * g, count, m, e);
+                }
+                add(e, vr[k]);
+            }
+            for (uint32_t g = g0 + kPvRegGroups * gstride; g < ngroups; g += gstride) {
+                float e[4];
+                exp_group(*(const float4*)(srow + 4 * g), 4 * g, count, m, e);
+                float4 v[4];
+#pragma unroll
+                for (uint32_t j = 0; j < 4; ++j)
+                    v[j] = 4 * g + j < count ? vsrc[4 * g + j] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                add(e, v);
             }
 #pragma unroll
             for (int o = 1; o < 64; o <<= 1) {
@@ -349,7 +368,7 @@ __global__ __launch_bounds__(kPvThreads) void attn_pv_kernel(
     for (uint32_t o = tid; o < G * 4; o += kPvThreads) {
         const uint32_t h = o / 4, j = o % 4;
         double sum = 0.0;
-        for (uint32_t w = 0; w < wph; ++w) sum += part[(h * wph + w) * 4 + j];
+        for (uint32_t v = 0; v < wph; ++v) sum += part[(h * wph + v) * 4 + j];
         att[(kvh * G + h) * hd + d0 + j] = (float)sum;
     }
 }
@@ -465,7 +484,7 @@ hipError_t LlamaModel::create(const LlamaDims& dims, const LlamaHostTensors& t, 
     // so models of other shapes in the process keep working
     static int pv_set = 64 * 1024, scores_set = 64 * 1024;
     const uint32_t G = (uint32_t)(d.heads / d.kv_heads);
-    const int pv_need = (int)(attn_pv_lds(G, (uint32_t)d.max_context, (uint32_t)nchunks).total * sizeof(float));
+    const int pv_need = (int)(attn_pv_lds(G).total * sizeof(float));
     const int scores_need = (int)attn_scores_lds(G, (uint32_t)hd);
     hipError_t e = hipSuccess;
     if (pv_need > pv_set) {
@@ -585,7 +604,7 @@ hipError_t LlamaModel::step(float* hidden, uint64_t position, float* embedding_o
     const float scale = d.attention_scale != 0.0f ? d.attention_scale : 1.0f / sqrtf((float)hd);
     const float* tab = rope_tab + position * hd;
     const size_t lds_scores = attn_scores_lds((uint32_t)(H / KVH), (uint32_t)hd);
-    const size_t lds_pv = attn_pv_lds((uint32_t)(H / KVH), (uint32_t)count, nchunks).total * sizeof(float);
+    const size_t lds_pv = attn_pv_lds((uint32_t)(H / KVH)).total * sizeof(float);
     const uint32_t cstride = (uint32_t)((d.max_context + kAttnChunk - 1) / kAttnChunk);
     hipError_t e = hipSuccess;
     for (uint64_t l = 0; l < d.n_layers && e == hipSuccess; ++l) {

@@ -184,6 +184,37 @@ def test_attention_head_shapes(ctx, heads, kv_heads, width):
     print("outputs differing in the last bit:", last_bit, "of", 70 * W)
 
 
+def test_attention_long_context(ctx):
+    """2,600 rows of cache with four query heads per KV head: each P.V lane
+    keeps its first 4 column groups (2,048 columns over the workgroup) in
+    registers and reloads the rest, and the workgroup's LDS no longer grows
+    with the context.  Checked against the oracle at the register boundary
+    and at the end."""
+    say("llama attention, context 2600, 4 heads / 1 kv head")
+    cfg, t, g, o = models(ctx, 1, 33, heads=4, kv_heads=1, max_context=2600)
+    W, kvw, hd = cfg.width, cfg.kv_width, cfg.head_dim
+    scale = np.float32(1.0) / np.sqrt(np.float32(hd))
+    kc = np.zeros((cfg.max_context, kvw), np.float32)
+    vc = np.zeros_like(kc)
+    rng = np.random.default_rng(13)
+    toks = rng.integers(cfg.vocabulary, size=cfg.max_context)
+    checked = 0
+    for step in range(cfg.max_context):
+        h = torch.from_numpy(o.embedding(int(toks[step]))).cuda()
+        g.step(h, step, embedding=False, logits=False)
+        qkv, att, _ = (host(x) for x in g.intermediates())
+        kc[step] = O.rope(qkv[W:W + kvw], hd, step, cfg.rope_base)
+        vc[step] = qkv[W + kvw:]
+        if step in (2046, 2047, 2048, 2049, 2050, 2599):
+            ctx.sync()
+            q = O.rope(qkv[:W], hd, step, cfg.rope_base)
+            want = O.attention(q, kc[:step + 1], vc[:step + 1], step + 1, cfg.heads, cfg.kv_heads, hd, scale)
+            assert np.all(np.abs(att - want) <= np.spacing(np.abs(want))), step
+            checked += 1
+    ctx.sync()
+    assert checked == 6
+
+
 @pytest.mark.parametrize("wt,ot", [(O.Q4_K, O.Q6_K), (O.Q6_K, O.Q8_0)])
 def test_free_running_steps(ctx, wt, ot):
     say("llama 2 layers, 12 free-running steps, logits vs oracle, types", wt, ot)
