@@ -295,8 +295,9 @@ __global__ __launch_bounds__(kPvThreads) void attn_pv_kernel(
     }
     __syncthreads();
     // the row totals, certified against the reference's column-order f64 sum
-    // (the pair sums are >= 0: sum = sum |.|), else repeated in that order
-    for (uint32_t h = tid; h < G; h += kPvThreads) {
+    // (the pair sums are >= 0: sum = sum |.|), else repeated in that order by
+    // the head's wave: 64 pair sums per load, added lane by lane
+    for (uint32_t h = wave; h < G; h += kPvWaves) {
         double sum = 0.0;
         for (uint32_t v = 0; v < wph; ++v) sum += rsum[h * wph + v];
         float inv;
@@ -304,14 +305,19 @@ __global__ __launch_bounds__(kPvThreads) void attn_pv_kernel(
             const float m = stat[2 * h];
             const float* srow = scores + (uint64_t)(kvh * G + h) * row_stride;
             double seq = 0.0;
-            for (uint32_t g = 0; g < ngroups; ++g) {
-                float e[4];
-                exp_group(*(const float4*)(srow + 4 * g), 4 * g, count, m, e);
-                seq += (double)((e[0] + e[1]) + (e[2] + e[3]));
+            for (uint32_t base = 0; base < ngroups; base += 64) {
+                float ps = 0.0f;
+                if (base + lane < ngroups) {
+                    float e[4];
+                    exp_group(*(const float4*)(srow + 4 * (base + lane)), 4 * (base + lane), count, m, e);
+                    ps = (e[0] + e[1]) + (e[2] + e[3]);
+                }
+                const uint32_t n = ngroups - base < 64 ? ngroups - base : 64;
+                for (uint32_t l = 0; l < n; ++l) seq += (double)__shfl(ps, (int)l, 64);
             }
             inv = (float)(1.0 / seq);
         }
-        stat[2 * h + 1] = inv;
+        if (lane == 0) stat[2 * h + 1] = inv;
     }
     __syncthreads();
     // P.V with p = e * inverse (math.rs:313-315, 478-480), one f64 chain per
