@@ -586,9 +586,10 @@ int32_t check_llama_config(const rlq_llama_config& c, rlq_error* err) {
     if (c.width % 256 != 0 || c.feed_forward % 256 != 0 || kvw % 16 != 0)
         return fail(err, RLQ_UNIMPLEMENTED, c.weight_type, c.width, c.feed_forward);
     if (hd % 16 != 0 || hd > 256) return fail(err, RLQ_UNIMPLEMENTED, 0, hd);  // dots in quarters of whole float4s
-    // LDS of the attention workgroups (their score rows grow with the context)
-    if (llama_attn_lds_bytes(c.heads, c.kv_heads, hd, c.max_context) > 159 * 1024)
-        return fail(err, RLQ_UNIMPLEMENTED, 0, c.max_context, c.heads / c.kv_heads);
+    // LDS of the attention workgroups (the G query heads of a KV head; it
+    // does not grow with the context)
+    if (llama_attn_lds_bytes(c.heads, c.kv_heads, hd) > 159 * 1024)
+        return fail(err, RLQ_UNIMPLEMENTED, 0, c.heads / c.kv_heads, hd);
     return ok(err);
 }
 

@@ -68,9 +68,8 @@ __host__ __device__ inline uint32_t attn_scores_lds(uint32_t G, uint32_t hd) {
     return (G * hd + kAttnChunk * (hd + kScKeyPad)) * 4;
 }
 
-uint64_t llama_attn_lds_bytes(uint64_t heads, uint64_t kv_heads, uint64_t head_dim, uint64_t max_context) {
+uint64_t llama_attn_lds_bytes(uint64_t heads, uint64_t kv_heads, uint64_t head_dim) {
     const uint64_t G = heads / kv_heads;
-    (void)max_context;
     const uint64_t pv = (uint64_t)attn_pv_lds((uint32_t)G).total * 4;
     const uint64_t sc = attn_scores_lds((uint32_t)G, (uint32_t)head_dim);
     return pv > sc ? pv : sc;

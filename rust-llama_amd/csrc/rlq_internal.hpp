@@ -137,8 +137,8 @@ struct LlamaHostTensors {
     const LlamaHostLayer* layers;
     bool on_device;
 };
-// LDS bytes the attention workgroups need at `max_context` rows.
-uint64_t llama_attn_lds_bytes(uint64_t heads, uint64_t kv_heads, uint64_t head_dim, uint64_t max_context);
+// LDS bytes the attention workgroups need (independent of the context).
+uint64_t llama_attn_lds_bytes(uint64_t heads, uint64_t kv_heads, uint64_t head_dim);
 struct LlamaLayerDev {
     // tiled matrices: Q, K, V back to back in wqkv; gate and up in wgu
     // (tiles interleaved when the epilogue fuses silu(gate) * up)
