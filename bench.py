@@ -260,8 +260,9 @@ def moe_decode(rlq, ctx, steps, warmup):
     """MUL_MAT_ID at a Mixtral-8x7B FFN shape: 8 Q4_K experts of 14336x4096,
     one token routed to 2 of them per step (one activation column shared by
     both slots); the expert pair rotates over 4 disjoint pairs, so the 264 MB
-    of experts cannot sit in the 256 MB MALL.  One step = the column's Q8_K
-    quantizer, the id check, and one launch over both (token, slot) pairs."""
+    of experts cannot sit in the 256 MB MALL.  One step = one launch over both
+    (token, slot) pairs, each workgroup checking the ids and quantizing the
+    column to Q8_K in its prologue."""
     torch = rlq.torch
     DT = rlq.DType
     experts, rows, cols, slots = 8, 14336, 4096, 2
@@ -291,8 +292,8 @@ def moe_decode(rlq, ctx, steps, warmup):
     ms = start.elapsed_time(end) / steps
     nbytes = slots * rlq.row_bytes(DT.Q4_K, cols) * rows + 4 * cols + 4 * slots * rows + 8
     W.close()
-    return {"workload": "MUL_MAT_ID Q4_K, 8 experts of 14336x4096, 1 token, top-2 (quantizer + id check + one "
-                        "grouped matvec launch per step)",
+    return {"workload": "MUL_MAT_ID Q4_K, 8 experts of 14336x4096, 1 token, top-2 (one launch per step: id "
+                        "check, Q8_K quantizer and both experts' matvecs)",
             "steps": steps, "us_per_step": round(ms * 1e3, 3), "bytes_per_step": nbytes,
             "gbs": round(nbytes / (ms * 1e-3) / 1e9, 2), "frac_hbm": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
 

@@ -463,18 +463,28 @@ int32_t rlq_mul_mat_id(rlq_context* ctx, const rlq_weights* w, uint32_t x_dtype,
     if (pairs > 0xffffffffull) return fail(err, RLQ_UNIMPLEMENTED, w->dtype, pairs);
     DeviceGuard g(ctx->device);
     const hipStream_t s = pick(ctx, stream);
-    ActPlanes planes;
-    uint32_t* gate;
-    rc = mm_stage(ctx, w, at, x_dtype, x, columns, ids, pairs, y, s, &planes, &gate, err);
-    if (rc) return rc;
     MvExtra ex;
-    ex.gate = gate;
     ex.ids = ids;
     ex.id_pairs = pairs;
     ex.id_slots = (uint32_t)slots;
     ex.id_cols = (uint32_t)ncols;
     ex.id_experts = (uint32_t)w->n2;
     ex.expert_bytes = w->mat_bytes;
+    // one token with one f32 column (MoE decode) over Q4_K / Q5_K experts:
+    // a single launch checks the ids and quantizes the column in every
+    // workgroup; otherwise the column planes, the gate and the product
+    if (tokens == 1 && ncols == 1 && x_dtype == 0 && (w->dtype == kQ4_K || w->dtype == kQ5_K) &&
+        ((uintptr_t)x & 15) == 0) {
+        ex.id_inline = true;
+        HIP_TRY(launch_matvec_ex(w->dtype, w->dev, w->rows, w->cols, (const float*)x, nullptr, 1, y, w->rows,
+                                 nullptr, ctx->err_words, nullptr, nullptr, ex, s));
+        return ok(err);
+    }
+    ActPlanes planes;
+    uint32_t* gate;
+    rc = mm_stage(ctx, w, at, x_dtype, x, columns, ids, pairs, y, s, &planes, &gate, err);
+    if (rc) return rc;
+    ex.gate = gate;
     HIP_TRY(launch_matvec_ex(w->dtype, w->dev, w->rows, w->cols, nullptr, &planes, 1, y, w->rows, nullptr,
                              ctx->err_words, nullptr, nullptr, ex, s));
     return ok(err);

@@ -136,13 +136,42 @@ struct MvArgs {
     const int32_t* ids;
     uint32_t id_base, id_slots, id_cols, id_experts;
     uint64_t expert_bytes;
+    // ids checked in the kernel (id_total pairs), x the one shared f32
+    // column; zero_pair: this workgroup's pair has id -1 (set by mv_enter)
+    uint32_t id_inline, id_total, zero_pair;
 };
 
 // Kernel entry: false when the workgroup has nothing to do (a refused call,
-// an expert slot with id -1, whose outputs the prepare kernel zeroed).
+// an expert slot with id -1, whose outputs the prepare kernel zeroed).  With
+// id_inline every workgroup checks every id first (the reference checks them
+// all before it quantizes anything, crates/tensor/src/cpu_index.rs:197-202):
+// one out of [-1, experts) refuses the call, the first is reported as
+// TensorError::Bounds; a -1 pair goes on (to quantize the shared column and
+// refuse with the others if it is bad) and then writes zeros.
 __device__ __forceinline__ bool mv_enter(MvArgs& a) {
     if (a.gate && *a.gate) return false;
     if (!a.ids) return true;
+    if (a.id_inline) {
+        int bad = 0;
+        for (uint32_t i = threadIdx.x; i < a.id_total; i += blockDim.x) {
+            const int32_t id = a.ids[i];
+            bad |= id < -1 || id >= (int32_t)a.id_experts;
+        }
+        if (__syncthreads_or(bad)) {
+            if (a.id_base == 0 && blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) {
+                uint32_t first = 0;
+                while (first < a.id_total && a.ids[first] >= -1 && a.ids[first] < (int32_t)a.id_experts) ++first;
+                report_error(a.err_word, bounds_key(first));
+            }
+            return false;
+        }
+        const uint32_t pair = a.id_base + blockIdx.y;
+        const int32_t id = a.ids[pair];
+        a.zero_pair = id < 0;
+        if (id >= 0) a.w += (uint64_t)id * a.expert_bytes;
+        a.y += (uint64_t)pair * a.ldy;
+        return true;
+    }
     const uint32_t pair = a.id_base + blockIdx.y;
     const int32_t id = a.ids[pair];
     if (id < 0 || (uint32_t)id >= a.id_experts) return false;
@@ -740,6 +769,14 @@ __global__ __launch_bounds__(W * 64) void q4k_mv_small_kernel(MvArgs a) {
 
     const bool ok = a.x ? stage_q8k<W, kBsQuarters>(a, lds, L, wave, xv) : stage_planes<W>(a, lds, L, T);
     if (!ok) return;
+    if (a.zero_pair) {  // MUL_MAT_ID slot with id -1 (cpu_index.rs:204): this workgroup's rows are 0
+        for (uint32_t it = threadIdx.x; it < tmax * TS * 16; it += W * 64) {
+            const uint32_t r = it % 16, slot = it / 16;
+            const uint32_t t = blockIdx.x * TS + slot % TS + (slot / TS) * tstride, row = t * kTileRows + r;
+            if (t < ntiles && row < a.rows) a.y[row] = 0.0f;
+        }
+        return;
+    }
 
     const uint32_t g = kq >> 1, h = kq & 1;
     // activation of (sub-block 2g, half h) and its neighbours: +32 (2g+1),
@@ -1550,9 +1587,13 @@ hipError_t launch_matvec_ex(uint32_t wtype, const uint8_t* w, uint64_t rows, uin
         (ex.epilogue != kEpSiluPair || batch != 1 || (wtype != kQ4_K && wtype != kQ5_K) ||
          rows % (2 * kTileRows) != 0 || argmax_key || ex.resid || dbg_isum))
         return hipErrorInvalidValue;
-    // expert pairs: one pre-quantized column each, plain stores
-    if (ex.ids && (batch != 1 || x || !pre || argmax_key || dbg_isum || ex.resid || ex.xform != kXfNone ||
-                   ex.epilogue != kEpStore || ex.id_pairs == 0 || ex.id_slots == 0 || ex.id_cols == 0))
+    // expert pairs: one pre-quantized column each, plain stores; or, checked
+    // in the kernel, one shared f32 column and the VALU Q4_K / Q5_K kernel
+    if (ex.ids && (batch != 1 || argmax_key || dbg_isum || ex.resid || ex.xform != kXfNone ||
+                   ex.epilogue != kEpStore || ex.id_pairs == 0 || ex.id_pairs > 0xffffffffull || ex.id_slots == 0 ||
+                   ex.id_cols == 0 || (ex.id_inline ? (!x || pre || ex.id_cols != 1 || ex.gate ||
+                                                        (wtype != kQ4_K && wtype != kQ5_K))
+                                                     : (x || !pre))))
         return hipErrorInvalidValue;
     uint64_t b0 = 0;
     while (b0 < batch) {
@@ -1593,6 +1634,8 @@ hipError_t launch_matvec_ex(uint32_t wtype, const uint8_t* w, uint64_t rows, uin
         a.id_cols = ex.id_cols;
         a.id_experts = ex.id_experts;
         a.expert_bytes = ex.expert_bytes;
+        a.id_inline = ex.ids && ex.id_inline ? 1u : 0u;
+        a.id_total = (uint32_t)ex.id_pairs;
         constexpr int W = kMvWaves;
         const bool dbg = a.dbg_isum != nullptr;
         auto dispatch = [&](uint32_t pairs) -> hipError_t {

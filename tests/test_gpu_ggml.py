@@ -160,6 +160,49 @@ def test_mul_mat_id_decode_shape(ctx, t):
         check_rows(t, mats, rows, cols, acts, y.cpu().numpy(), want, (t, ncols))
 
 
+@pytest.mark.parametrize("t", [O.Q4_K, O.Q5_K])
+@pytest.mark.parametrize("rows,cols", [(300, 2048), (40, 4352)])
+def test_mul_mat_id_one_token_single_launch(ctx, t, rows, cols):
+    """One token with one f32 column shared by its slots (MoE decode): one
+    launch checks the ids and quantizes the column in every workgroup.  Its
+    outputs equal the planes path's bit for bit (the same column given as
+    Q8_K bytes), meet the oracle's bars, and refusals write nothing."""
+    experts, slots = 6, 3
+    say("MUL_MAT_ID one token", t, rows, cols, experts, slots)
+    w = random_w(t, rows, cols, experts, 70 + t)
+    W = rlq.Weights(ctx, t, w, rows, cols, experts)
+    rng = np.random.default_rng(71)
+    x = rng.standard_normal((1, 1, cols)).astype(np.float32)
+    xq = O.quantize(O.Q8_K, x.reshape(-1))
+    mb = rows * O.row_bytes(t, cols)
+    for ids in ([[4, 0, -1]], [[2, 2, 5]], [[-1, -1, -1]]):
+        ids = np.array(ids, np.int32)
+        y = ctx.mul_mat_id(W, torch.from_numpy(x).cuda(), torch.from_numpy(ids).cuda())
+        yq = ctx.mul_mat_id(W, torch.from_numpy(xq).cuda().reshape(1, 1, -1), torch.from_numpy(ids).cuda(),
+                            x_dtype=DT.Q8_K)
+        ctx.sync()
+        got = y.cpu().numpy()
+        assert np.array_equal(bits(got), bits(yq.cpu().numpy())), ids
+        want = O.mul_mat_id(t, w, rows, cols, experts, O.F32, x, 1, 1, ids)
+        mats = [None if i < 0 else w[i * mb:(i + 1) * mb] for i in ids[0]]
+        check_rows(t, mats, rows, cols, [xq] * slots, got, want, (t, ids.tolist()))
+    # an id out of range: Bounds at its flat index, before the bad column
+    xb = x.copy()
+    xb[0, 0, 100] = np.nan
+    y = torch.full((1, slots, rows), 7.0, device="cuda")
+    ctx.mul_mat_id(W, torch.from_numpy(xb).cuda(), torch.tensor([[0, 6, -1]], dtype=torch.int32, device="cuda"), y=y)
+    with pytest.raises(rlq.QuantError) as e:
+        ctx.sync()
+    assert (e.value.name, e.value.a) == ("Bounds", 1)
+    assert bool((y == 7.0).all())
+    # valid ids and a non-finite value: refused, nothing written (the -1 slot included)
+    ctx.mul_mat_id(W, torch.from_numpy(xb).cuda(), torch.tensor([[0, 5, -1]], dtype=torch.int32, device="cuda"), y=y)
+    with pytest.raises(rlq.QuantError) as e:
+        ctx.sync()
+    assert (e.value.name, e.value.index, e.value.b) == ("NonFiniteInput", 100, 0)
+    assert bool((y == 7.0).all())
+
+
 def test_mul_mat_id_many_pairs_packed_rhs(ctx):
     """64 tokens x 2 slots of 16 Q4_K experts with Q8_K activation bytes as
     the right-hand side (used as given)."""
