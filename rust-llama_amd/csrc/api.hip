@@ -470,11 +470,10 @@ int32_t rlq_mul_mat_id(rlq_context* ctx, const rlq_weights* w, uint32_t x_dtype,
     ex.id_cols = (uint32_t)ncols;
     ex.id_experts = (uint32_t)w->n2;
     ex.expert_bytes = w->mat_bytes;
-    // one token with one f32 column (MoE decode) over Q4_K / Q5_K experts:
-    // a single launch checks the ids and quantizes the column in every
-    // workgroup; otherwise the column planes, the gate and the product
-    if (tokens == 1 && ncols == 1 && x_dtype == 0 && (w->dtype == kQ4_K || w->dtype == kQ5_K) &&
-        ((uintptr_t)x & 15) == 0) {
+    // one token with one f32 column (MoE decode): a single launch checks the
+    // ids and quantizes the column in every workgroup; otherwise the column
+    // planes, the gate and the product
+    if (tokens == 1 && ncols == 1 && x_dtype == 0 && ((uintptr_t)x & 15) == 0) {
         ex.id_inline = true;
         HIP_TRY(launch_matvec_ex(w->dtype, w->dev, w->rows, w->cols, (const float*)x, nullptr, 1, y, w->rows,
                                  nullptr, ctx->err_words, nullptr, nullptr, ex, s));

@@ -470,6 +470,24 @@ __device__ __forceinline__ void publish_argmax(const MvArgs& a, uint32_t b, unsi
     if ((threadIdx.x & 15) == 0 && b < a.batch && best) atomicMax(a.argmax_key + b, best);
 }
 
+// MUL_MAT_ID slot with id -1 (cpu_index.rs:204), once the call is known to
+// stand: the rows this workgroup would have computed are 0.  One wave per
+// tile (tiles gw, gw + tw, ...), or tile slots of the K-split kernels.
+__device__ __forceinline__ void zero_wave_tiles(const MvArgs& a, uint32_t gw, uint32_t tw, uint32_t n, uint32_t kq) {
+    for (uint32_t t = gw; t < a.ntiles; t += tw) {
+        const uint32_t row = t * kTileRows + n;
+        if (kq == 0 && row < a.rows) a.y[row] = 0.0f;
+    }
+}
+template <int W, int TS>
+__device__ __forceinline__ void zero_slot_tiles(const MvArgs& a, uint32_t tmax, uint32_t tstride) {
+    for (uint32_t it = threadIdx.x; it < tmax * TS * 16; it += W * 64) {
+        const uint32_t r = it % 16, slot = it / 16;
+        const uint32_t t = blockIdx.x * TS + slot % TS + (slot / TS) * tstride, row = t * kTileRows + r;
+        if (t < a.ntiles && row < a.rows) a.y[row] = 0.0f;
+    }
+}
+
 // ---------------------------------------------------------------------------
 // Software pipeline over a wave's steps: buf[i] holds the loads of step
 // s0 + i, issued D steps before use.  The steady-state loop issues exactly one
@@ -665,6 +683,7 @@ __global__ __launch_bounds__(W * 64) void q4k_mv_kernel(MvArgs a) {
 
     const bool ok = a.x ? stage_q8k<W, kBsQuarters>(a, lds, L, wave, xv) : stage_planes<W>(a, lds, L, T);
     if (!ok) return;
+    if (a.zero_pair) return zero_wave_tiles(a, gw, tw, n, kq);
 
     // A operand: lane row r = n holds column r / 2, sub-block parity r % 2; it
     // is nonzero only in the K quarters (kq / 2 == r % 2) of that sub-block.
@@ -769,14 +788,7 @@ __global__ __launch_bounds__(W * 64) void q4k_mv_small_kernel(MvArgs a) {
 
     const bool ok = a.x ? stage_q8k<W, kBsQuarters>(a, lds, L, wave, xv) : stage_planes<W>(a, lds, L, T);
     if (!ok) return;
-    if (a.zero_pair) {  // MUL_MAT_ID slot with id -1 (cpu_index.rs:204): this workgroup's rows are 0
-        for (uint32_t it = threadIdx.x; it < tmax * TS * 16; it += W * 64) {
-            const uint32_t r = it % 16, slot = it / 16;
-            const uint32_t t = blockIdx.x * TS + slot % TS + (slot / TS) * tstride, row = t * kTileRows + r;
-            if (t < ntiles && row < a.rows) a.y[row] = 0.0f;
-        }
-        return;
-    }
+    if (a.zero_pair) return zero_slot_tiles<W, TS>(a, tmax, tstride);
 
     const uint32_t g = kq >> 1, h = kq & 1;
     // activation of (sub-block 2g, half h) and its neighbours: +32 (2g+1),
@@ -943,6 +955,7 @@ __global__ __launch_bounds__(W * 64) void q6k_mv_kernel(MvArgs a) {
 
     const bool ok = a.x ? stage_q8k<W, kBsNone>(a, lds, L, wave, xv) : stage_planes<W>(a, lds, L, kQ6_K);
     if (!ok) return;
+    if (a.zero_pair) return zero_wave_tiles(a, gw, tw, n, kq);
 
     // This lane's weights: ql bytes 32kq.. (g = kq/2, s1 = kq%2) give the
     // elements of 16-element scale groups 8g + 2s1 + h (low nibbles) and
@@ -1187,6 +1200,7 @@ __global__ __launch_bounds__(W * 64) void k16_mv_kernel(MvArgs a) {
 
     const bool ok = a.x ? stage_q8k<W, bsum_order(T)>(a, lds, L, wave, xv) : stage_planes<W>(a, lds, L, T);
     if (!ok) return;
+    if (a.zero_pair) return zero_wave_tiles(a, gw, tw, n, kq);
 
     const K16A A = k16_a(lds, L, a.batch, n, kq);
     const bool two_groups = a.batch > 4;
@@ -1282,6 +1296,7 @@ __global__ __launch_bounds__(W * 64) void k16_mv_split_kernel(MvArgs a) {
 
     const bool ok = a.x ? stage_q8k<W, bsum_order(T)>(a, lds, L, wave, xv) : stage_planes<W>(a, lds, L, T);
     if (!ok) return;
+    if (a.zero_pair) return zero_slot_tiles<W, TS>(a, tmax, tstride);
 
     const K16A A = k16_a(lds, L, batch, n, kq);
     const bool two_groups = batch > 4;
@@ -1371,6 +1386,7 @@ __global__ __launch_bounds__(W * 64) void q8_0_mv_kernel(MvArgs a) {
 
     const bool ok = a.x ? stage_q8_0<W>(a, lds, L, wave, xv) : stage_planes<W>(a, lds, L, kQ8_0);
     if (!ok) return;
+    if (a.zero_pair) return zero_wave_tiles(a, gw, tw, n, kq);
 
     // A operand: lane row r = n holds column r / 2 and block 2p + r % 2; it is
     // nonzero in the K quarters (kq / 2 == r % 2) of that block.
@@ -1588,11 +1604,10 @@ hipError_t launch_matvec_ex(uint32_t wtype, const uint8_t* w, uint64_t rows, uin
          rows % (2 * kTileRows) != 0 || argmax_key || ex.resid || dbg_isum))
         return hipErrorInvalidValue;
     // expert pairs: one pre-quantized column each, plain stores; or, checked
-    // in the kernel, one shared f32 column and the VALU Q4_K / Q5_K kernel
+    // in the kernel, one shared f32 column
     if (ex.ids && (batch != 1 || argmax_key || dbg_isum || ex.resid || ex.xform != kXfNone ||
                    ex.epilogue != kEpStore || ex.id_pairs == 0 || ex.id_pairs > 0xffffffffull || ex.id_slots == 0 ||
-                   ex.id_cols == 0 || (ex.id_inline ? (!x || pre || ex.id_cols != 1 || ex.gate ||
-                                                        (wtype != kQ4_K && wtype != kQ5_K))
+                   ex.id_cols == 0 || (ex.id_inline ? (!x || pre || ex.id_cols != 1 || ex.gate)
                                                      : (x || !pre))))
         return hipErrorInvalidValue;
     uint64_t b0 = 0;

@@ -94,9 +94,9 @@ struct MvExtra {
     uint32_t id_slots = 0, id_cols = 0, id_experts = 0;
     uint64_t expert_bytes = 0;
     // MUL_MAT_ID of one f32 column shared by every pair (one token, one
-    // column; Q4_K / Q5_K): each workgroup checks every id, quantizes the
-    // column and zeroes its rows of a -1 pair itself, with no gate, planes or
-    // prepare launch
+    // column): each workgroup checks every id, quantizes the column and
+    // zeroes its rows of a -1 pair itself, with no gate, planes or prepare
+    // launch
     bool id_inline = false;
 };
 // The MUL_MAT / MUL_MAT_ID gate (one workgroup, before the products): checks

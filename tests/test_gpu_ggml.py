@@ -160,26 +160,27 @@ def test_mul_mat_id_decode_shape(ctx, t):
         check_rows(t, mats, rows, cols, acts, y.cpu().numpy(), want, (t, ncols))
 
 
-@pytest.mark.parametrize("t", [O.Q4_K, O.Q5_K])
+@pytest.mark.parametrize("t", [O.Q4_K, O.Q5_K, O.Q6_K, O.Q3_K, O.Q2_K, O.Q8_0])
 @pytest.mark.parametrize("rows,cols", [(300, 2048), (40, 4352)])
 def test_mul_mat_id_one_token_single_launch(ctx, t, rows, cols):
     """One token with one f32 column shared by its slots (MoE decode): one
     launch checks the ids and quantizes the column in every workgroup.  Its
     outputs equal the planes path's bit for bit (the same column given as
-    Q8_K bytes), meet the oracle's bars, and refusals write nothing."""
+    activation bytes), meet the oracle's bars, and refusals write nothing."""
     experts, slots = 6, 3
     say("MUL_MAT_ID one token", t, rows, cols, experts, slots)
     w = random_w(t, rows, cols, experts, 70 + t)
     W = rlq.Weights(ctx, t, w, rows, cols, experts)
     rng = np.random.default_rng(71)
     x = rng.standard_normal((1, 1, cols)).astype(np.float32)
-    xq = O.quantize(O.Q8_K, x.reshape(-1))
+    at = O.matvec_activation_dtype(t)
+    xq = O.quantize(at, x.reshape(-1))
     mb = rows * O.row_bytes(t, cols)
     for ids in ([[4, 0, -1]], [[2, 2, 5]], [[-1, -1, -1]]):
         ids = np.array(ids, np.int32)
         y = ctx.mul_mat_id(W, torch.from_numpy(x).cuda(), torch.from_numpy(ids).cuda())
         yq = ctx.mul_mat_id(W, torch.from_numpy(xq).cuda().reshape(1, 1, -1), torch.from_numpy(ids).cuda(),
-                            x_dtype=DT.Q8_K)
+                            x_dtype=DT(at))
         ctx.sync()
         got = y.cpu().numpy()
         assert np.array_equal(bits(got), bits(yq.cpu().numpy())), ids
