@@ -97,6 +97,9 @@ struct rlq_context {
     unsigned long long* err_words = nullptr;  // [0] device API (sticky), [1] host API (per call)
     unsigned long long* host_err = nullptr;   // pinned readback
     DevBuf planes, keys, stage_in, stage_w, stage_out, gate;
+    // leading argmax keys that are 0 in stream order: the last greedy-token
+    // kernel set its keys back to 0, so the next call clears only the rest
+    uint64_t keys_zero = 0;
 };
 
 struct rlq_weights {
@@ -500,9 +503,13 @@ static int32_t matmul_impl(rlq_context* ctx, const rlq_weights* w, const float* 
     const hipStream_t s = pick(ctx, stream);
     unsigned long long* keys = nullptr;
     if (argmax) {
+        const void* before = ctx->keys.p;
         HIP_TRY(ensure(ctx, ctx->keys, batch * sizeof(unsigned long long)));
+        if (ctx->keys.p != before) ctx->keys_zero = 0;  // a new buffer
         keys = (unsigned long long*)ctx->keys.p;
-        HIP_TRY(launch_fill_u64(keys, batch, 0ull, s));
+        if (ctx->keys_zero < batch)
+            HIP_TRY(launch_fill_u64(keys + ctx->keys_zero, batch - ctx->keys_zero, 0ull, s));
+        ctx->keys_zero = 0;  // the product below sets keys [0, batch)
     }
     if (w->dtype == kQ4_K && batch > kDecodeMaxBatch) {  // prefill: the MFMA GEMM
         HIP_TRY(ensure(ctx, ctx->planes, gemm_planes_bytes(batch, w->cols)));
@@ -513,7 +520,10 @@ static int32_t matmul_impl(rlq_context* ctx, const rlq_weights* w, const float* 
         HIP_TRY(launch_matvec(w->dtype, w->dev, w->rows, w->cols, x, nullptr, batch, y, w->rows, keys, ctx->err_words,
                               nullptr, nullptr, s));
     }
-    if (argmax) HIP_TRY(launch_argmax_finish(keys, batch, y, w->rows, argmax, s));
+    if (argmax) {
+        HIP_TRY(launch_argmax_finish(keys, batch, y, w->rows, argmax, s, true));
+        ctx->keys_zero = batch;
+    }
     return ok(err);
 }
 

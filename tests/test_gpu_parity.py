@@ -229,6 +229,23 @@ def test_q8_0_qwen_lm_head_151936x896(ctx):
     assert int(am[0]) == O.argmax(y[0].cpu().numpy())
 
 
+def test_argmax_keys_across_calls(ctx):
+    """The greedy-token kernel sets the argmax keys back to 0, and a call
+    clears only keys past those: batches 3, 1, 5, 2, 12 (the prefill GEMM)
+    and 1 in a row, each argmax the first maximum of its own logits."""
+    rows, cols = 1000, 2048
+    w = _weights(DT.Q4_K, rows, cols, 77)
+    W = rlq.Weights(ctx, DT.Q4_K, w, rows, cols)
+    for i, batch in enumerate((3, 1, 5, 2, 12, 1)):
+        say("argmax keys across calls, batch", batch)
+        x = randn(300 + i, batch * cols).reshape(batch, cols)
+        y, am = ctx.matmul_argmax(W, torch.from_numpy(x).cuda())
+        ctx.sync()
+        got = y.cpu().numpy()
+        for b in range(batch):
+            assert int(am[b]) == O.argmax(got[b]), (batch, b)
+
+
 # ------------------------------------------------------------ errors and edges
 
 def test_host_errors_leave_output_untouched():
