@@ -421,6 +421,11 @@ int32_t rlq_mul_mat(rlq_context* ctx, const rlq_weights* w, uint32_t x_dtype, co
     if (rc) return rc;
     DeviceGuard g(ctx->device);
     const hipStream_t s = pick(ctx, stream);
+    if (columns == 1 && x_dtype == 0) {  // one f32 column: one launch that quantizes it in every workgroup
+        HIP_TRY(launch_matvec_ex(w->dtype, w->dev, w->rows, w->cols, (const float*)x, nullptr, 1, y, w->rows,
+                                 nullptr, ctx->err_words, nullptr, nullptr, MvExtra{}, s));
+        return ok(err);
+    }
     ActPlanes planes;
     uint32_t* gate;
     rc = mm_stage(ctx, w, at, x_dtype, x, columns, nullptr, 0, y, s, &planes, &gate, err);

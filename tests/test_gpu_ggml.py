@@ -253,6 +253,35 @@ def test_mul_mat_broadcast_shapes(ctx, t, xd):
     check_rows(t, mats, rows, cols, acts, y.cpu().numpy(), want, (t, xd))
 
 
+@pytest.mark.parametrize("t", [O.Q4_K, O.Q5_K, O.Q6_K, O.Q3_K, O.Q2_K, O.Q8_0])
+def test_mul_mat_one_column_single_launch(ctx, t):
+    """MUL_MAT of one f32 column (a decode step's GGML graph): one launch
+    that quantizes the column in every workgroup.  Bitwise equal to the
+    planes path (the column given as activation bytes), the oracle's bars,
+    and a non-finite value refuses the call."""
+    rows, cols = 300, 2304 if t == O.Q8_0 else 2048
+    say("MUL_MAT one column", t, rows, cols)
+    w = random_w(t, rows, cols, 1, 90 + t)
+    W = rlq.Weights(ctx, t, w, rows, cols)
+    x = np.random.default_rng(91).standard_normal((1, 1, 1, cols)).astype(np.float32)
+    at = O.matvec_activation_dtype(t)
+    xq = O.quantize(at, x.reshape(-1))
+    y = ctx.mul_mat(W, torch.from_numpy(x).cuda())
+    yq = ctx.mul_mat(W, torch.from_numpy(xq).cuda().reshape(1, 1, 1, -1), x_dtype=DT(at))
+    ctx.sync()
+    got = y.cpu().numpy()
+    assert np.array_equal(bits(got), bits(yq.cpu().numpy()))
+    want = O.mul_mat(t, w, rows, cols, 1, 1, O.F32, x, 1, 1, 1)
+    check_rows(t, [w], rows, cols, [xq], got, want, t)
+    x[0, 0, 0, 33] = np.inf
+    y = torch.full((1, 1, 1, rows), 7.0, device="cuda")
+    ctx.mul_mat(W, torch.from_numpy(x).cuda(), y=y)
+    with pytest.raises(rlq.QuantError) as e:
+        ctx.sync()
+    assert (e.value.name, e.value.index, e.value.b) == ("NonFiniteInput", 33, 0)
+    assert bool((y == 7.0).all())
+
+
 # ------------------------------------------------------------ errors
 
 def test_errors_refuse_the_whole_call(ctx):
