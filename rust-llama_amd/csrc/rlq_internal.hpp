@@ -167,6 +167,7 @@ struct LlamaModel {
     float* cmax = nullptr;  // [heads][chunks of 16 tokens] chunk maxima of the scores
     unsigned long long* argmax_keys = nullptr;
     bool keys_zero = false;  // argmax_keys is 0 in stream order (the last step's finish reset it)
+    bool repeat_all = false;  // attention sums always repeated in the reference's order
     uint64_t n_cached = 0;  // KV rows held (the insertion index of the next step)
 
     ~LlamaModel();

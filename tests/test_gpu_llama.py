@@ -184,6 +184,38 @@ def test_attention_head_shapes(ctx, heads, kv_heads, width):
     print("outputs differing in the last bit:", last_bit, "of", 70 * W)
 
 
+def test_attention_repeats_equal_certified_sums(ctx, monkeypatch):
+    """The repeats in the reference's order, which run when a certificate
+    fails (rare), forced for every QK dot and softmax total with
+    RLQ_ATTN_REPEAT_ALL=1: the attention output is bitwise the certified
+    kernels' (both are the reference's f32 values) and the oracle's."""
+    say("llama attention, every sum repeated in the reference's order, 70 steps")
+    cfg, t, g, o = models(ctx, 1, 35, heads=8, kv_heads=2, max_context=80)
+    monkeypatch.setenv("RLQ_ATTN_REPEAT_ALL", "1")
+    g2 = rlq.LlamaModel(ctx, gpu_config(cfg), t)
+    monkeypatch.delenv("RLQ_ATTN_REPEAT_ALL")
+    W, kvw, hd = cfg.width, cfg.kv_width, cfg.head_dim
+    scale = np.float32(1.0) / np.sqrt(np.float32(hd))
+    kc = np.zeros((cfg.max_context, kvw), np.float32)
+    vc = np.zeros_like(kc)
+    rng = np.random.default_rng(17)
+    for step in range(70):
+        h0 = o.embedding(int(rng.integers(cfg.vocabulary)))
+        g.step(torch.from_numpy(h0).cuda(), step, embedding=False, logits=False)
+        qkv, att, _ = (host(x) for x in g.intermediates())
+        g2.step(torch.from_numpy(h0).cuda(), step, embedding=False, logits=False)
+        qkv2, att2, _ = (host(x) for x in g2.intermediates())
+        ctx.sync()
+        assert np.array_equal(qkv.view(np.uint32), qkv2.view(np.uint32)), step
+        assert np.array_equal(att.view(np.uint32), att2.view(np.uint32)), step
+        q = O.rope(qkv[:W], hd, step, cfg.rope_base)
+        kc[step] = O.rope(qkv[W:W + kvw], hd, step, cfg.rope_base)
+        vc[step] = qkv[W + kvw:]
+        want = O.attention(q, kc[:step + 1], vc[:step + 1], step + 1, cfg.heads, cfg.kv_heads, hd, scale)
+        assert np.all(np.abs(att2 - want) <= np.spacing(np.abs(want))), step
+    g2.close()
+
+
 def test_attention_long_context(ctx):
     """2,600 rows of cache with four query heads per KV head: each P.V lane
     keeps its first 4 column groups (2,048 columns over the workgroup) in
