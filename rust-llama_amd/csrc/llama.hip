@@ -38,7 +38,7 @@ constexpr uint32_t kScKeyPad = 16;  // floats after each key row in LDS
 constexpr uint32_t kPvDims = 4;       // head dimensions per P.V workgroup: one float4 of each value row
 constexpr uint32_t kPvThreads = 512;
 constexpr uint32_t kPvWaves = kPvThreads / 64;
-constexpr uint32_t kPvRegGroups = 4;  // column groups of four per lane whose values and exponentials stay in registers
+constexpr uint32_t kPvRegGroups = 2;  // column groups of four per lane whose values and exponentials stay in registers
 
 // The value cache of a layer is slice-major: [kv_heads * hd / 4][max_context]
 // float4, slice kvh * hd / 4 + d / 4 holding dimensions d .. d + 3 of kv head
