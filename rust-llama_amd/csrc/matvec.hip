@@ -871,19 +871,19 @@ __global__ __launch_bounds__(W * 64) void q4k_mv_small_kernel(MvArgs a) {
     pipeline<D>(steps, buf, issue, compute);
     __syncthreads();
 
-    if (TS == 2 && a.epilogue == kEpSiluPair) {
-        // tile slots (2 til, 2 til + 1) hold gate and up rows of the same 16
+    if (TS % 2 == 0 && a.epilogue == kEpSiluPair) {
+        // tile slots (2 q, 2 q + 1) hold gate and up rows of the same 16
         // outputs (llama.rs:367-371: gate = silu(gate); gate *= up)
-        for (uint32_t it = threadIdx.x; it < tmax * 16; it += W * 64) {
-            const uint32_t r = it % 16, til = it / 16;
-            const uint32_t t = blockIdx.x * TS + til * tstride;  // the gate tile, even
+        for (uint32_t it = threadIdx.x; it < tmax * (TS / 2) * 16; it += W * 64) {
+            const uint32_t r = it % 16, q = (it / 16) % (TS / 2), til = it / 16 / (TS / 2);
+            const uint32_t t = blockIdx.x * TS + 2 * q + til * tstride;  // the gate tile, even
             if (t + 1 < ntiles) {
                 float g = 0.0f, u = 0.0f;
 #pragma unroll
                 for (int k = 0; k < KS; ++k)
                     if ((uint32_t)k < nb) {
-                        g += part[((til * TS * KS + k) * 16 + r) * B];
-                        u += part[(((til * TS + 1) * KS + k) * 16 + r) * B];
+                        g += part[(((til * TS + 2 * q) * KS + k) * 16 + r) * B];
+                        u += part[(((til * TS + 2 * q + 1) * KS + k) * 16 + r) * B];
                     }
                 a.y[(t / 2) * kTileRows + r] = (g / (1.0f + sse2_exp(0.0f - g))) * u;
             }
@@ -1525,10 +1525,13 @@ static hipError_t launch_small(const MvArgs& a, hipStream_t s, uint32_t pairs) {
 template <uint32_t T>
 static hipError_t launch_q45(const MvArgs& a, uint32_t nbat, bool dbg, uint32_t epilogue, size_t lds, hipStream_t s,
                              uint32_t pairs) {
-    // two tile slots per workgroup (a K split of four): the SiLU pair
-    // epilogue's gate and up tiles, and small matrices of at most 4096
-    // columns and 512 tiles (measured: 6144x4096 runs 1 us faster)
-    if (epilogue == kEpSiluPair || (nbat == 1 && !dbg && a.nb <= 16 && a.ntiles <= 512))
+    // the SiLU pair epilogue: four tile slots per workgroup (two gate/up
+    // pairs, a K split of two; 28672x4096 measured 14.6 us against 15.3 us
+    // with one pair and a split of four)
+    if (epilogue == kEpSiluPair) return launch_small<T, kSmallW, kSmallW / 4, kSmallD, 1, false>(a, s, pairs);
+    // two tile slots per workgroup (a K split of four): small matrices of at
+    // most 4096 columns and 512 tiles (measured: 6144x4096 runs 1 us faster)
+    if (nbat == 1 && !dbg && a.nb <= 16 && a.ntiles <= 512)
         return launch_small<T, kSmallW, kSmallW / 2, kSmallD, 1, false>(a, s, pairs);
     // more than 16 blocks per row (4096x14336, the down projection): 16 waves
     // per workgroup, K split 16 ways (measured 10.4 us vs 10.7 us with 8)
