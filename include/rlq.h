@@ -208,7 +208,8 @@ int32_t rlq_mul_mat(rlq_context *ctx, const rlq_weights *w, uint32_t x_dtype, co
  *   y[(t * slots + s) * rows + r] = dot_packed(row r of W[ids[t * slots + s]],
  *                                              column s % ncols of X(t)),
  * and 0 where the id is -1.  Every column of X is quantized once before the
- * expert products.  Errors: RLQ_TENSOR_SHAPE, RLQ_TENSOR_UNSUPPORTED at
+ * expert products (one token with one F32 column: inside the one product
+ * launch, by every workgroup).  Errors: RLQ_TENSOR_SHAPE, RLQ_TENSOR_UNSUPPORTED at
  * once; at rlq_sync RLQ_TENSOR_BOUNDS (an id < -1 or >= w.n2; a = its index
  * t * slots + s) before any quantizer data error.  A call with an error
  * writes no output. */
