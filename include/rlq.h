@@ -85,8 +85,23 @@ typedef enum rlq_status {
     RLQ_GGUF_IO = 27,
     RLQ_GGUF_INVALID = 28,
     RLQ_GGUF_LIMIT = 29,
-    RLQ_GGUF_UNSUPPORTED = 30
+    RLQ_GGUF_UNSUPPORTED = 30,
+    /* model-runtime Error::NonFinite (crates/model-runtime/src/lib.rs:51):
+       a = the check (rlq_nonfinite_check), b = the Llama layer (n_layers for
+       the final norm and the output matrix; 0 for rlq_multiply) */
+    RLQ_NON_FINITE = 31
 } rlq_status;
+
+/* The reference's NonFinite checks, by the name it reports. */
+enum rlq_nonfinite_check {
+    RLQ_CHECK_RMS_SCALE = 1,         /* "RMS normalization scale" (math.rs:218-220) */
+    RLQ_CHECK_RMS_OUTPUT = 2,        /* "RMS normalization output" (math.rs:227) */
+    RLQ_CHECK_MATRIX_INPUT = 3,      /* "matrix input" (math.rs:152) */
+    RLQ_CHECK_MATRIX_OUTPUT = 4,     /* "matrix output" (math.rs:167) */
+    RLQ_CHECK_ATTENTION_SCORE = 5,   /* "attention score" (math.rs:476-478) */
+    RLQ_CHECK_ATTENTION_OUTPUT = 6,  /* "attention output" (math.rs:494) */
+    RLQ_CHECK_LAYER_OUTPUT = 7       /* "Llama layer output" (llama.rs:378) */
+};
 
 typedef struct rlq_error {
     int32_t code;
@@ -180,6 +195,17 @@ void rlq_weights_stack(const rlq_weights *w, uint64_t *n2, uint64_t *n3);
 int32_t rlq_matmul(rlq_context *ctx, const rlq_weights *w, const float *x, uint64_t batch, float *y,
                    void *stream, rlq_error *err);
 
+/* Matrix::multiply (crates/model-runtime/src/math.rs:144-169) of one input
+ * vector x (device, cols floats, 16-byte aligned) into y (device, rows
+ * floats): finite(input), llama_quant::matvec, finite(output).  Data errors at
+ * rlq_sync, in the reference's order: RLQ_NON_FINITE (a =
+ * RLQ_CHECK_MATRIX_INPUT) for a non-finite input; the quantizer's
+ * RLQ_UNREPRESENTABLE_SCALE (a = block; the reference wraps this QuantError
+ * in Error::Shape with its text); RLQ_NON_FINITE (a =
+ * RLQ_CHECK_MATRIX_OUTPUT) for a non-finite output.  With an input error no
+ * output is written; with an output error y holds the outputs. */
+int32_t rlq_multiply(rlq_context *ctx, const rlq_weights *w, const float *x, float *y, void *stream, rlq_error *err);
+
 /* rlq_matmul followed by the greedy sampler's choice per column
  * (crates/llama-behavior/src/sampling.rs:607-613: the first strict maximum),
  * fused into the matvec epilogue: argmax[b] = index of the largest y[b*rows+r]. */
@@ -238,6 +264,19 @@ int32_t rlq_sync(rlq_context *ctx, void *stream, rlq_error *err);
  * isum and imin are device pointers of rows*nb i32. */
 int32_t rlq_block_sums(rlq_context *ctx, const rlq_weights *w, const float *x, uint64_t batch, int32_t *isum,
                        int32_t *imin, void *stream, rlq_error *err);
+
+/* rlq_block_sums that also hands out the launch's outputs and reaches the
+ * decode step's fused gate/up kernel (test surface; no reference
+ * counterpart).  y (device, may be null): the outputs of the same launch,
+ * batch*rows floats as rlq_matmul writes them.  flags RLQ_SUMS_SILU_PAIR:
+ * the kernel rlq_llama_step runs for a Q4_K / Q5_K gate/up product
+ * (batch 1; rows a multiple of 32 whose 16-row tiles alternate gate and up:
+ * tile 2i holds gate rows 16i.., tile 2i+1 up rows 16i..), with the integers
+ * of every row of w and y = silu(gate) * up, rows/2 floats
+ * (crates/model-runtime/src/llama.rs:367-371). */
+#define RLQ_SUMS_SILU_PAIR 1u
+int32_t rlq_block_sums_ex(rlq_context *ctx, const rlq_weights *w, const float *x, uint64_t batch, uint32_t flags,
+                          int32_t *isum, int32_t *imin, float *y, void *stream, rlq_error *err);
 
 /* ---- dense Llama decode step ------------------------------------------------
  * LlamaModel of crates/model-runtime/src/llama.rs with quantized matrices,
@@ -334,16 +373,31 @@ int32_t rlq_llama_embedding(rlq_llama *model, uint32_t token, float *hidden, voi
  * finish_hidden (:381-392): embedding (width) = RMSNorm(hidden, output_norm),
  * logits (vocabulary) = output . embedding, argmax (1 u32) = the greedy
  * choice over the logits.  embedding, logits and argmax are device pointers
- * and may each be null.  Data errors (a non-finite value) are reported by
- * rlq_sync; the step's outputs are then unspecified. */
+ * and may each be null.  Data errors are reported by rlq_sync as the
+ * reference's sequential step would report its first: RLQ_NON_FINITE with
+ * the check (a) and the layer (b; n_layers for the final norm and output),
+ * or RLQ_UNREPRESENTABLE_SCALE (a = block, b = layer) from an activation
+ * quantizer; the step's outputs are then unspecified. */
 int32_t rlq_llama_step(rlq_llama *model, float *hidden, uint64_t position, float *embedding, float *logits,
                        uint32_t *argmax, void *stream, rlq_error *err);
 /* Copies (on `stream`, device to device) the last layer's intermediates of
  * the latest step: qkv = [query (width) | key (kv_width, before RoPE) | value
- * (kv_width)], attention (width, the attention output), ffn = silu(gate) * up
- * (feed_forward, the down projection's input).  Any output may be null. */
-int32_t rlq_llama_intermediates(const rlq_llama *model, float *qkv, float *attention, float *ffn,
+ * (kv_width)], attention (width, the attention output), ffn_input (width, the
+ * residual stream after attention: hidden + attention_output . attention,
+ * the FFN RMSNorm's input), ffn = silu(gate) * up (feed_forward, the down
+ * projection's input).  Any output may be null. */
+int32_t rlq_llama_intermediates(const rlq_llama *model, float *qkv, float *attention, float *ffn_input, float *ffn,
                                 void *stream, rlq_error *err);
+
+/* Test surface (no reference counterpart): while `parts` (device, n_layers
+ * x (4 width + 2 kv_width + feed_forward) floats) is non-null, every
+ * rlq_llama_step also copies each layer's intermediates there, layer l at
+ * l * (4 width + 2 kv_width + feed_forward): [query | key (before RoPE) |
+ * value] (width + 2 kv_width), the attention output (width), the residual
+ * stream after attention (width), silu(gate) * up (feed_forward) and the
+ * layer output (width), so a checker can feed every part of every layer its
+ * own input.  NULL stops the copies. */
+int32_t rlq_llama_trace(rlq_llama *model, float *parts, rlq_error *err);
 
 /* ---- GGUF files (crates/gguf) ---------------------------------------------------
  * Host-only: no device is used.  The reader follows RawGguf (crates/gguf/src/

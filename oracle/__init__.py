@@ -31,6 +31,7 @@ ERROR_NAMES = {
     21: "InvalidConfig", 22: "InvalidToken", 23: "InvalidState",
     24: "Shape", 25: "Bounds", 26: "Unsupported",
     27: "GgufIo", 28: "GgufInvalid", 29: "GgufLimit", 30: "GgufUnsupported",
+    31: "NonFinite",
 }
 F32 = 0
 SHAPE, BOUNDS, UNSUPPORTED = 24, 25, 26
@@ -80,8 +81,12 @@ def _load():
     lib.oracle_attention.argtypes = [P, P, P, U64, U64, U64, U64, F, P]
     lib.oracle_attention.restype = ctypes.c_int
     lib.oracle_llama_embedding.argtypes, lib.oracle_llama_embedding.restype = [P, U32, P], ctypes.c_int
-    lib.oracle_llama_step.argtypes = [P, P, U64, U64, P, P, P, I]
+    lib.oracle_llama_step.argtypes = [P, P, U64, U64, P, P, P, I, E]
     lib.oracle_llama_step.restype = ctypes.c_int
+    lib.oracle_llama_run_layer.argtypes = [P, U64, P, U64, U64, P, P, I, E]
+    lib.oracle_llama_run_layer.restype = ctypes.c_int
+    lib.oracle_llama_finish.argtypes = [P, P, P, P, I, E]
+    lib.oracle_llama_finish.restype = ctypes.c_int
     for f in ("oracle_row_bytes", "oracle_matvec_activation_dtype", "oracle_quantize_into",
               "oracle_dequantize_into", "oracle_dot_packed", "oracle_matvec", "oracle_matmul"):
         getattr(lib, f).restype = ctypes.c_int
@@ -424,7 +429,38 @@ class LlamaOracle:
         """Returns (last layer output, logits); appends one KV row."""
         h = _f32c(hidden).copy()
         logits = np.zeros(self.cfg.vocabulary, dtype=np.float32)
-        _rc(lib().oracle_llama_step(ctypes.byref(self._m), _ptr(h), int(position), self.cached,
-                                    _ptr(self.k_cache), _ptr(self.v_cache), _ptr(logits), self.threads))
+        err = _Err()
+        rc = lib().oracle_llama_step(ctypes.byref(self._m), _ptr(h), int(position), self.cached,
+                                     _ptr(self.k_cache), _ptr(self.v_cache), _ptr(logits), self.threads,
+                                     ctypes.byref(err))
         self.cached += 1
+        if rc != 0:  # NonFinite: a = the check, b = the layer; a quantizer's QuantError: b = the layer
+            raise OracleError(rc, err.dtype, err.a, err.b)
         return h, logits
+
+    def layer(self, index, hidden, position):
+        """Layer `index` alone over a copy of hidden at `position`, writing
+        that layer's KV row `cached` (advance() moves to the next row once
+        every layer of a step has run)."""
+        h = _f32c(hidden).copy()
+        err = _Err()
+        rc = lib().oracle_llama_run_layer(ctypes.byref(self._m), int(index), _ptr(h), int(position), self.cached,
+                                      _ptr(self.k_cache), _ptr(self.v_cache), self.threads, ctypes.byref(err))
+        if rc != 0:
+            raise OracleError(rc, err.dtype, err.a, err.b)
+        return h
+
+    def advance(self):
+        self.cached += 1
+
+    def finish(self, hidden):
+        """finish_hidden of a last-layer output: (embedding, logits)."""
+        h = _f32c(hidden)
+        emb = np.zeros(self.cfg.width, dtype=np.float32)
+        logits = np.zeros(self.cfg.vocabulary, dtype=np.float32)
+        err = _Err()
+        rc = lib().oracle_llama_finish(ctypes.byref(self._m), _ptr(h), _ptr(emb), _ptr(logits), self.threads,
+                                       ctypes.byref(err))
+        if rc != 0:
+            raise OracleError(rc, err.dtype, err.a, err.b)
+        return emb, logits

@@ -49,7 +49,8 @@ enum {
     ORC_INVALID_ARGUMENT = 20,            /* null pointer */
     ORC_INVALID_CONFIG = 21,              /* model-runtime errors of the decode step */
     ORC_INVALID_TOKEN = 22,
-    ORC_INVALID_STATE = 23
+    ORC_INVALID_STATE = 23,
+    ORC_NON_FINITE = 31                   /* model-runtime Error::NonFinite: a = check, b = layer */
 };
 
 typedef struct oracle_error {
@@ -169,7 +170,13 @@ int oracle_llama_embedding(const oracle_llama_model *m, uint32_t token, float *o
  * n_cached rows: hidden (width) in/out, caches [n_layers][max_context][kv_width]
  * gain row n_cached, logits (vocab) out.  `threads` splits matvec rows. */
 int oracle_llama_step(const oracle_llama_model *m, float *hidden, uint64_t position, uint64_t n_cached,
-                      float *k_cache, float *v_cache, float *logits, int threads);
+                      float *k_cache, float *v_cache, float *logits, int threads, oracle_error *err);
+/* One layer of the step (layer l over hidden, KV row n_cached of layer l),
+ * and finish_hidden alone (embedding may be null). */
+int oracle_llama_run_layer(const oracle_llama_model *m, uint64_t l, float *hidden, uint64_t position, uint64_t n_cached,
+                           float *k_cache, float *v_cache, int threads, oracle_error *err);
+int oracle_llama_finish(const oracle_llama_model *m, const float *hidden, float *embedding, float *logits,
+                        int threads, oracle_error *err);
 
 #ifdef __cplusplus
 }

@@ -90,7 +90,13 @@ ERROR_NAMES = {
     21: "InvalidConfig", 22: "InvalidToken", 23: "InvalidState",
     24: "Shape", 25: "Bounds", 26: "Unsupported",
     27: "GgufIo", 28: "GgufInvalid", 29: "GgufLimit", 30: "GgufUnsupported",
+    31: "NonFinite",
 }
+
+# NonFinite checks (QuantError.a of a NonFinite error): the names the
+# reference's model-runtime reports
+NONFINITE_CHECKS = {1: "RMS normalization scale", 2: "RMS normalization output", 3: "matrix input",
+                    4: "matrix output", 5: "attention score", 6: "attention output", 7: "Llama layer output"}
 
 
 class QuantError(Exception):
@@ -147,10 +153,12 @@ SIGNATURES = {
     "rlq_mul_mat": ([_P, _P, _U32, _P, _U64, _U64, _U64, _P, _P, _E], _I32),
     "rlq_mul_mat_id": ([_P, _P, _U32, _P, _U64, _U64, _P, _U64, _P, _P, _E], _I32),
     "rlq_matmul": ([_P, _P, _P, _U64, _P, _P, _E], _I32),
+    "rlq_multiply": ([_P, _P, _P, _P, _P, _E], _I32),
     "rlq_matmul_argmax": ([_P, _P, _P, _U64, _P, _P, _P, _E], _I32),
     "rlq_quantize_device": ([_P, _U32, _P, _U64, _U64, _P, _P, _E], _I32),
     "rlq_sync": ([_P, _P, _E], _I32),
     "rlq_block_sums": ([_P, _P, _P, _U64, _P, _P, _P, _E], _I32),
+    "rlq_block_sums_ex": ([_P, _P, _P, _U64, _U32, _P, _P, _P, _P, _E], _I32),
     "rlq_gguf_open": ([ctypes.c_char_p, ctypes.POINTER(_P), _E], _I32),
     "rlq_gguf_read_header_memory": ([_P, _U64, ctypes.POINTER(_P), _E], _I32),
     "rlq_gguf_close": ([_P], None),
@@ -176,7 +184,8 @@ SIGNATURES = {
     "rlq_llama_cached": ([_P], _U64),
     "rlq_llama_embedding": ([_P, _U32, _P, _P, _E], _I32),
     "rlq_llama_step": ([_P, _P, _U64, _P, _P, _P, _P, _E], _I32),
-    "rlq_llama_intermediates": ([_P, _P, _P, _P, _P, _E], _I32),
+    "rlq_llama_intermediates": ([_P, _P, _P, _P, _P, _P, _E], _I32),
+    "rlq_llama_trace": ([_P, _P, _E], _I32),
 }
 
 
@@ -341,6 +350,17 @@ class Context:
                                _dev_ptr(y, torch.float32), _stream_ptr(stream), ctypes.byref(err)), err)
         return y
 
+    def multiply(self, w, x, y=None, stream=None):
+        """Matrix::multiply (math.rs:144-169): one input vector x [cols] ->
+        y [rows], with the reference's finite checks of the input and the
+        output (NonFinite errors at sync)."""
+        if y is None:
+            y = torch.empty(w.rows, dtype=torch.float32, device=x.device)
+        err = _Err()
+        _check(_lib.rlq_multiply(self._h, w._h, _dev_ptr(x, torch.float32), _dev_ptr(y, torch.float32),
+                                 _stream_ptr(stream), ctypes.byref(err)), err)
+        return y
+
     def matmul_argmax(self, w, x, y=None, argmax=None, stream=None):
         """matmul followed by the greedy sampler's index per column."""
         x2 = x.reshape(-1, w.cols)
@@ -414,6 +434,25 @@ class Context:
                                    _dev_ptr(isum, torch.int32), _dev_ptr(imin, torch.int32),
                                    _stream_ptr(stream), ctypes.byref(err)), err)
         return isum, imin
+
+    SUMS_SILU_PAIR = 1
+
+    def block_sums_ex(self, w, x, flags=0, stream=None):
+        """block_sums plus the same launch's outputs: (isum, imin, y).  With
+        flags=SUMS_SILU_PAIR the decode step's gate/up kernel runs over w (Q4_K
+        / Q5_K rows whose 16-row tiles alternate gate and up) and y holds
+        silu(gate) * up, rows / 2 values; otherwise y is [batch, rows]."""
+        x2 = x.reshape(-1, w.cols)
+        nb = w.cols // (32 if w.dtype == DType.Q8_0 else 256)
+        isum = torch.empty((w.rows, nb), dtype=torch.int32, device=x.device)
+        imin = torch.empty((w.rows, nb), dtype=torch.int32, device=x.device)
+        n = w.rows // 2 if flags & self.SUMS_SILU_PAIR else x2.shape[0] * w.rows
+        y = torch.empty(n, dtype=torch.float32, device=x.device)
+        err = _Err()
+        _check(_lib.rlq_block_sums_ex(self._h, w._h, _dev_ptr(x2, torch.float32), x2.shape[0], int(flags),
+                                      _dev_ptr(isum, torch.int32), _dev_ptr(imin, torch.int32),
+                                      _dev_ptr(y, torch.float32), _stream_ptr(stream), ctypes.byref(err)), err)
+        return isum, imin, y
 
 
 class Weights:
@@ -567,17 +606,42 @@ class LlamaModel:
                                    _stream_ptr(stream), ctypes.byref(err)), err)
         return emb, lg, am
 
+    @property
+    def trace_stride(self):
+        c = self.config
+        return 4 * c.width + 2 * c.kv_width + c.feed_forward
+
+    def trace(self, parts):
+        """rlq_llama_trace: with a GPU tensor [n_layers, trace_stride] f32,
+        every later step also copies each layer's intermediates there
+        (split_trace() names them); None stops it."""
+        self._trace = parts  # kept alive while the library writes to it
+        err = _Err()
+        _check(_lib.rlq_llama_trace(self._h, _dev_ptr(parts, torch.float32) if parts is not None else None,
+                                    ctypes.byref(err)), err)
+
+    def split_trace(self, row):
+        """One layer's row of the trace as (qkv, attention, ffn_input, ffn, output)."""
+        c = self.config
+        a = c.width + 2 * c.kv_width
+        cuts = (a, a + c.width, a + 2 * c.width, a + 2 * c.width + c.feed_forward)
+        return row[:cuts[0]], row[cuts[0]:cuts[1]], row[cuts[1]:cuts[2]], row[cuts[2]:cuts[3]], row[cuts[3]:]
+
     def intermediates(self, stream=None):
-        """The last layer's [q | k | v] (k before RoPE), attention output and
-        silu(gate) * up of the latest step, as fresh GPU tensors."""
+        """The last layer's [q | k | v] (k before RoPE), attention output,
+        silu(gate) * up and the residual stream after attention (the FFN
+        norm's input) of the latest step, as fresh GPU tensors:
+        (qkv, attention, ffn, ffn_input)."""
         c = self.config
         qkv = torch.empty(c.width + 2 * c.kv_width, dtype=torch.float32, device="cuda")
         att = torch.empty(c.width, dtype=torch.float32, device="cuda")
+        mid = torch.empty(c.width, dtype=torch.float32, device="cuda")
         gu = torch.empty(c.feed_forward, dtype=torch.float32, device="cuda")
         err = _Err()
         _check(_lib.rlq_llama_intermediates(self._h, _dev_ptr(qkv, torch.float32), _dev_ptr(att, torch.float32),
-                                            _dev_ptr(gu, torch.float32), _stream_ptr(stream), ctypes.byref(err)), err)
-        return qkv, att, gu
+                                            _dev_ptr(mid, torch.float32), _dev_ptr(gu, torch.float32),
+                                            _stream_ptr(stream), ctypes.byref(err)), err)
+        return qkv, att, gu, mid
 
 
 # ---- GGUF files (host only) -------------------------------------------------------

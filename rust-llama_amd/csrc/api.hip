@@ -11,6 +11,7 @@
 
 #include <mutex>
 #include <new>
+#include <stdexcept>
 #include <string>
 #include <vector>
 
@@ -116,10 +117,14 @@ namespace {
 
 // Grow-only scratch.  Growing waits for the whole device first (callers may
 // pass their own streams), so no kernel still reads the old buffer when it is
-// freed.
-hipError_t ensure(rlq_context* ctx, DevBuf& b, size_t need) {
+// freed.  *grown (may be null) tells whether the buffer was replaced: its
+// contents are then undefined, even when the allocator hands back the old
+// address.
+hipError_t ensure(rlq_context* ctx, DevBuf& b, size_t need, bool* grown = nullptr) {
     (void)ctx;
+    if (grown) *grown = false;
     if (b.n >= need) return hipSuccess;
+    if (grown) *grown = true;
     hipError_t e = hipDeviceSynchronize();
     if (e != hipSuccess) return e;
     if (b.p) (void)hipFree(b.p);
@@ -149,10 +154,32 @@ hipStream_t pick(rlq_context* ctx, void* stream) {
     return (hipStream_t)stream;
 }
 
+// A model stage (rlq_device.hpp ModelStage) as the reference reports it: the
+// QuantError of an activation quantizer (0), or the NonFinite check (rlq.h
+// rlq_nonfinite_check).
+uint32_t stage_check(uint32_t stage) {
+    switch (stage) {
+        case kStAttnNormScale: case kStFfnNormScale: return RLQ_CHECK_RMS_SCALE;
+        case kStAttnNormOut: case kStFfnNormOut: return RLQ_CHECK_RMS_OUTPUT;
+        case kStOIn: case kStDownIn: return RLQ_CHECK_MATRIX_INPUT;
+        case kStQkvOut: case kStOOut: case kStGuOut: case kStDownOut: return RLQ_CHECK_MATRIX_OUTPUT;
+        case kStScore: return RLQ_CHECK_ATTENTION_SCORE;
+        case kStAttnOut: return RLQ_CHECK_ATTENTION_OUTPUT;
+        case kStLayerOut: return RLQ_CHECK_LAYER_OUTPUT;
+        default: return 0;  // kStQkvQuant, kStOQuant, kStGuQuant, kStDownQuant
+    }
+}
+
 // Decode an error key (see rlq_device.hpp) into an rlq_error.
 int32_t key_to_error(unsigned long long key, uint32_t dtype, rlq_error* err) {
     if (key == ~0ull) return ok(err);
     const uint64_t field = key >> 41, kind = (key >> 40) & 1, index = key & ((1ull << 40) - 1);
+    if (field == kModelField) {  // model-runtime checks: layer, stage, index
+        const uint64_t layer = (key >> 25) & 0xffff, stage = (key >> 20) & 31, idx = key & 0xfffff;
+        const uint32_t check = stage_check((uint32_t)stage);
+        if (check == 0) return fail(err, RLQ_UNREPRESENTABLE_SCALE, dtype, idx, layer);
+        return fail(err, RLQ_NON_FINITE, dtype, check, layer);
+    }
     if (field == 0) return fail(err, RLQ_TENSOR_BOUNDS, dtype, index);
     return fail(err, kind == (uint64_t)kKindNonFinite ? RLQ_NON_FINITE_INPUT : RLQ_UNREPRESENTABLE_SCALE, dtype,
                 index, field - 1);
@@ -172,6 +199,8 @@ int32_t take_error(rlq_context* ctx, int slot, hipStream_t s, uint32_t dtype, rl
 
 std::mutex g_default_mu;
 rlq_context* g_default = nullptr;
+
+
 
 int32_t default_context(rlq_context** out, rlq_error* err) {
     if (!g_default) {
@@ -248,6 +277,11 @@ const char* rlq_status_string(int32_t code) {
         case RLQ_TENSOR_SHAPE: return "MUL_MAT / MUL_MAT_ID dimensions are incompatible";
         case RLQ_TENSOR_BOUNDS: return "expert id outside the expert tensor";
         case RLQ_TENSOR_UNSUPPORTED: return "right-hand side must be F32 or the activation type";
+        case RLQ_GGUF_IO: return "GGUF file could not be read or written";
+        case RLQ_GGUF_INVALID: return "GGUF file is malformed";
+        case RLQ_GGUF_LIMIT: return "GGUF file exceeds a reader limit";
+        case RLQ_GGUF_UNSUPPORTED: return "GGUF content is not supported";
+        case RLQ_NON_FINITE: return "non-finite value";
         default: return "unknown status";
     }
 }
@@ -508,9 +542,9 @@ static int32_t matmul_impl(rlq_context* ctx, const rlq_weights* w, const float* 
     const hipStream_t s = pick(ctx, stream);
     unsigned long long* keys = nullptr;
     if (argmax) {
-        const void* before = ctx->keys.p;
-        HIP_TRY(ensure(ctx, ctx->keys, batch * sizeof(unsigned long long)));
-        if (ctx->keys.p != before) ctx->keys_zero = 0;  // a new buffer
+        bool grown = false;
+        HIP_TRY(ensure(ctx, ctx->keys, batch * sizeof(unsigned long long), &grown));
+        if (grown) ctx->keys_zero = 0;  // a new buffer holds nothing known
         keys = (unsigned long long*)ctx->keys.p;
         if (ctx->keys_zero < batch)
             HIP_TRY(launch_fill_u64(keys + ctx->keys_zero, batch - ctx->keys_zero, 0ull, s));
@@ -537,11 +571,26 @@ int32_t rlq_matmul(rlq_context* ctx, const rlq_weights* w, const float* x, uint6
     return matmul_impl(ctx, w, x, batch, y, nullptr, stream, err);
 }
 
+// Matrix::multiply (crates/model-runtime/src/math.rs:144-169): the input's
+// finite scan is the quantizer's own (the first non-finite value refuses the
+// call), then the product, then the finite scan of the outputs.
+int32_t rlq_multiply(rlq_context* ctx, const rlq_weights* w, const float* x, float* y, void* stream, rlq_error* err) {
+    if (!ctx || !w || !x || !y) return fail(err, RLQ_INVALID_ARGUMENT);
+    if (((uintptr_t)x & 15) || ((uintptr_t)y & 3)) return fail(err, RLQ_INVALID_ARGUMENT, w->dtype);
+    DeviceGuard g(ctx->device);
+    MvExtra ex;
+    ex.chk = mv_chk(0, kStOIn, kStOQuant, kStOOut, 0);  // matrix input, the quantizer, matrix output
+    HIP_TRY(launch_matvec_ex(w->dtype, w->dev, w->rows, w->cols, x, nullptr, 1, y, w->rows, nullptr, ctx->err_words,
+                             nullptr, nullptr, ex, pick(ctx, stream)));
+    return ok(err);
+}
+
 int32_t rlq_matmul_argmax(rlq_context* ctx, const rlq_weights* w, const float* x, uint64_t batch, float* y,
                           uint32_t* argmax, void* stream, rlq_error* err) {
     if (!argmax) return fail(err, RLQ_INVALID_ARGUMENT);
     return matmul_impl(ctx, w, x, batch, y, argmax, stream, err);
 }
+
 
 int32_t rlq_quantize_device(rlq_context* ctx, uint32_t dtype, const float* x, uint64_t cols, uint64_t batch,
                             uint8_t* out, void* stream, rlq_error* err) {
@@ -601,6 +650,8 @@ int32_t check_llama_config(const rlq_llama_config& c, rlq_error* err) {
         return fail(err, RLQ_INVALID_CONFIG, 0, 6);
     uint64_t cache;
     if (__builtin_mul_overflow(kvw, c.max_context, &cache)) return fail(err, RLQ_INVALID_CONFIG, 0, 7);
+    // the device error keys carry the layer in 16 bits
+    if (c.n_layers > 0xffff) return fail(err, RLQ_UNIMPLEMENTED, 0, c.n_layers, 0xffff);
     for (uint32_t t : {c.weight_type, c.output_type, c.embedding_type}) {
         if (!dtype_known(t)) return fail(err, RLQ_INVALID_TYPE, t);
         if (!path_weight(t)) return fail(err, RLQ_UNIMPLEMENTED, t);
@@ -644,7 +695,13 @@ int32_t rlq_llama_create(rlq_context* ctx, const rlq_llama_config* cfg, const rl
     if (!m) return fail(err, RLQ_ALLOCATION_FAILED);
     m->ctx = ctx;
     m->m.device = ctx->device;
-    std::vector<LlamaHostLayer> layers(cfg->n_layers);
+    std::vector<LlamaHostLayer> layers;
+    try {
+        layers.resize(cfg->n_layers);
+    } catch (const std::exception&) {  // bad_alloc, length_error: no abort across the C ABI
+        delete m;
+        return fail(err, RLQ_ALLOCATION_FAILED);
+    }
     for (uint64_t l = 0; l < cfg->n_layers; ++l) {
         const rlq_llama_layer& L = t->layers[l];
         layers[l] = LlamaHostLayer{L.attention_norm, L.query, L.key, L.value, L.attention_output,
@@ -944,8 +1001,8 @@ int32_t rlq_llama_step(rlq_llama* m, float* hidden, uint64_t position, float* em
     return ok(err);
 }
 
-int32_t rlq_llama_intermediates(const rlq_llama* m, float* qkv, float* attention, float* ffn, void* stream,
-                                rlq_error* err) {
+int32_t rlq_llama_intermediates(const rlq_llama* m, float* qkv, float* attention, float* ffn_input, float* ffn,
+                                void* stream, rlq_error* err) {
     if (!m) return fail(err, RLQ_INVALID_ARGUMENT);
     DeviceGuard g(m->m.device);
     const LlamaDims& d = m->m.d;
@@ -953,29 +1010,49 @@ int32_t rlq_llama_intermediates(const rlq_llama* m, float* qkv, float* attention
     const hipStream_t s = (hipStream_t)stream;
     if (qkv) HIP_TRY(hipMemcpyAsync(qkv, m->m.qkv, (d.width + 2 * kvw) * 4, hipMemcpyDeviceToDevice, s));
     if (attention) HIP_TRY(hipMemcpyAsync(attention, m->m.att, d.width * 4, hipMemcpyDeviceToDevice, s));
+    if (ffn_input) HIP_TRY(hipMemcpyAsync(ffn_input, m->m.mid, d.width * 4, hipMemcpyDeviceToDevice, s));
     if (ffn) HIP_TRY(m->m.ffn_activation(ffn, s));
     return ok(err);
 }
 
-int32_t rlq_block_sums(rlq_context* ctx, const rlq_weights* w, const float* x, uint64_t batch, int32_t* isum,
-                       int32_t* imin, void* stream, rlq_error* err) {
+int32_t rlq_llama_trace(rlq_llama* m, float* layer_outputs, rlq_error* err) {
+    if (!m) return fail(err, RLQ_INVALID_ARGUMENT);
+    m->m.trace = layer_outputs;
+    return ok(err);
+}
+
+int32_t rlq_block_sums_ex(rlq_context* ctx, const rlq_weights* w, const float* x, uint64_t batch, uint32_t flags,
+                          int32_t* isum, int32_t* imin, float* y, void* stream, rlq_error* err) {
     if (!ctx || !w || !x || !isum || !imin) return fail(err, RLQ_INVALID_ARGUMENT);
-    if ((uintptr_t)x & 15) return fail(err, RLQ_INVALID_ARGUMENT, w->dtype);
-    if (batch == 0) return fail(err, RLQ_INVALID_ARGUMENT, w->dtype);
+    if (((uintptr_t)x & 15) || ((uintptr_t)y & 3)) return fail(err, RLQ_INVALID_ARGUMENT, w->dtype);
+    if (batch == 0 || (flags & ~RLQ_SUMS_SILU_PAIR)) return fail(err, RLQ_INVALID_ARGUMENT, w->dtype);
+    const bool pair = (flags & RLQ_SUMS_SILU_PAIR) != 0;
+    // the SiLU-pair epilogue: one column of Q4_K / Q5_K rows in whole gate/up tile pairs
+    if (pair && (batch != 1 || (w->dtype != kQ4_K && w->dtype != kQ5_K) || w->rows % (2 * kTileRows) != 0))
+        return fail(err, RLQ_INVALID_ARGUMENT, w->dtype, batch, w->rows);
     DeviceGuard g(ctx->device);
     const hipStream_t s = pick(ctx, stream);
-    HIP_TRY(ensure(ctx, ctx->stage_out, batch * w->rows * sizeof(float)));
-    float* y = (float*)ctx->stage_out.p;
+    if (!y) {
+        HIP_TRY(ensure(ctx, ctx->stage_out, batch * w->rows * sizeof(float)));
+        y = (float*)ctx->stage_out.p;
+    }
     if (w->dtype == kQ4_K && batch > kDecodeMaxBatch) {
         HIP_TRY(ensure(ctx, ctx->planes, gemm_planes_bytes(batch, w->cols)));
         HIP_TRY(launch_gemm_q4k(w->dev, w->rows, w->cols, x, batch, y, w->rows, ctx->planes.p, ctx->err_words, isum,
                                 imin, s));
     } else {
         if (batch > kDecodeMaxBatch) return fail(err, RLQ_INVALID_ARGUMENT, w->dtype);
-        HIP_TRY(launch_matvec(w->dtype, w->dev, w->rows, w->cols, x, nullptr, batch, y, w->rows, nullptr,
-                              ctx->err_words, isum, imin, s));
+        MvExtra ex;
+        ex.epilogue = pair ? 1u : 0u;
+        HIP_TRY(launch_matvec_ex(w->dtype, w->dev, w->rows, w->cols, x, nullptr, batch, y, w->rows, nullptr,
+                                 ctx->err_words, isum, imin, ex, s));
     }
     return ok(err);
+}
+
+int32_t rlq_block_sums(rlq_context* ctx, const rlq_weights* w, const float* x, uint64_t batch, int32_t* isum,
+                       int32_t* imin, void* stream, rlq_error* err) {
+    return rlq_block_sums_ex(ctx, w, x, batch, 0, isum, imin, nullptr, stream, err);
 }
 
 // ---- host drop-ins ----------------------------------------------------------------

@@ -21,6 +21,7 @@
 #include <stdlib.h>
 
 #include <new>
+#include <stdexcept>
 #include <vector>
 
 #include "rlq_device.hpp"
@@ -115,7 +116,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_scores_kernel(
     const float* __restrict__ qkv, const float* __restrict__ rope_tab, float* __restrict__ kc, float* __restrict__ vc,
     uint32_t max_context, uint32_t fresh, uint32_t heads, uint32_t kv_heads, uint32_t hd, float scale,
     float* __restrict__ scores, uint32_t row_stride, float* __restrict__ cmax, uint32_t cstride,
-    unsigned long long* __restrict__ err_word, uint32_t repeat_all) {
+    unsigned long long* __restrict__ err_word, uint32_t layer, uint32_t repeat_all) {
     extern __shared__ __align__(16) float sm[];
     const uint32_t G = heads / kv_heads, kvh = blockIdx.y, c = blockIdx.x, t0 = c * kAttnChunk;
     // key rows at a stride of hd + 16 floats: the two rows one eight-lane LDS
@@ -195,7 +196,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_scores_kernel(
             }
             score = dotf * scale;
             if (quarter == 0) {
-                if (!(fabsf(score) <= 3.402823466e38f)) report_error(err_word, error_key(0, kKindNonFinite, t0 + t));
+                if (!(fabsf(score) <= 3.402823466e38f)) report_error(err_word, model_key(layer, kStScore, t0 + t));
                 scores[(uint64_t)(kvh * G + h) * row_stride + t0 + t] = score;
             }
         }
@@ -232,7 +233,8 @@ __device__ __forceinline__ void exp_group(float4 x, uint32_t t, uint32_t count, 
 __global__ __launch_bounds__(kPvThreads) void attn_pv_kernel(
     const float* __restrict__ scores, const float* __restrict__ cmax, uint32_t cstride, uint32_t nch,
     const float* __restrict__ vc, uint32_t max_context, uint32_t count, uint32_t heads, uint32_t kv_heads, uint32_t hd,
-    uint32_t row_stride, float* __restrict__ att, uint32_t repeat_all) {
+    uint32_t row_stride, float* __restrict__ att, unsigned long long* __restrict__ err_word, uint32_t layer,
+    uint32_t repeat_all) {
     extern __shared__ __align__(16) float sm[];
     const uint32_t G = heads / kv_heads, kvh = blockIdx.y, d0 = blockIdx.x * kPvDims;
     const AttnPvLds Lp = attn_pv_lds(G);
@@ -375,7 +377,9 @@ __global__ __launch_bounds__(kPvThreads) void attn_pv_kernel(
         const uint32_t h = o / 4, j = o % 4;
         double sum = 0.0;
         for (uint32_t v = 0; v < wph; ++v) sum += part[(h * wph + v) * 4 + j];
-        att[(kvh * G + h) * hd + d0 + j] = (float)sum;
+        const float r = (float)sum;
+        if (!finite(r)) report_error(err_word, model_key(layer, kStAttnOut, 0));  // math.rs:494
+        att[(kvh * G + h) * hd + d0 + j] = r;
     }
 }
 
@@ -391,28 +395,37 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const float* __restrict__
     }
 }
 
-hipError_t LlamaModel::ffn_activation(float* out, hipStream_t s) const {
+hipError_t LlamaModel::ffn_activation_of(const LlamaLayerDev& L, float* out, hipStream_t s) const {
     const uint32_t F = (uint32_t)d.feed_forward;
-    if (layers.empty() || layers.back().gu_mode() == 0)  // the last layer's
-        return hipMemcpyAsync(out, gu, F * sizeof(float), hipMemcpyDeviceToDevice, s);
+    if (L.gu_mode() == 0) return hipMemcpyAsync(out, gu, F * sizeof(float), hipMemcpyDeviceToDevice, s);
     hipLaunchKernelGGL(silu_mul_kernel, dim3((F + 255) / 256), dim3(256), 0, s, gu, F, out);
     return hipGetLastError();
 }
 
+hipError_t LlamaModel::ffn_activation(float* out, hipStream_t s) const {
+    if (layers.empty()) return hipSuccess;  // no layer: nothing to copy
+    return ffn_activation_of(layers.back(), out, s);  // the last layer's
+}
+
 __global__ __launch_bounds__(256) void rms_norm_row_kernel(const float* __restrict__ x, const float* __restrict__ w,
                                                            uint32_t n, float eps, float* __restrict__ out,
-                                                           unsigned long long* __restrict__ err_word) {
+                                                           unsigned long long* __restrict__ err_word, uint32_t layer) {
     __shared__ float scale_s;
     if (threadIdx.x == 0) {
         double sum = 0.0;
         for (uint32_t i = 0; i < n; ++i) sum += (double)(x[i] * x[i]);
         const float scale = 1.0f / sqrtf((float)(sum / (double)n) + eps);
-        if (!(scale <= 3.402823466e38f) || !(scale > 0.0f)) report_error(err_word, error_key(0, kKindNonFinite, 0));
+        if (!(scale <= 3.402823466e38f) || !(scale > 0.0f))  // math.rs:218-220
+            report_error(err_word, model_key(layer, kStAttnNormScale, 0));
         scale_s = scale;
     }
     __syncthreads();
     const float scale = scale_s;
-    for (uint32_t i = threadIdx.x; i < n; i += 256) out[i] = x[i] * scale * w[i];
+    for (uint32_t i = threadIdx.x; i < n; i += 256) {
+        const float v = x[i] * scale * w[i];
+        if (!finite(v)) report_error(err_word, model_key(layer, kStAttnNormOut, 0));  // math.rs:227
+        out[i] = v;
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -464,7 +477,7 @@ LlamaModel::~LlamaModel() {
                         (void*)l.ffn_norm})
             if (p) (void)hipFree(p);
     for (void* p : {(void*)out_w, (void*)out_norm, (void*)emb, (void*)k_cache, (void*)v_cache, (void*)rope_tab,
-                    (void*)qkv, (void*)scores, (void*)att, (void*)gu, (void*)argmax_keys,
+                    (void*)qkv, (void*)scores, (void*)att, (void*)mid, (void*)gu, (void*)argmax_keys,
                     (void*)logits_buf, (void*)cmax})
         if (p) (void)hipFree(p);
 }
@@ -476,9 +489,18 @@ hipError_t LlamaModel::create(const LlamaDims& dims, const LlamaHostTensors& t, 
     repeat_all = rep && rep[0] == '1';
     d = dims;
     const uint64_t W = d.width, F = d.feed_forward, hd = W / d.heads, kvw = d.kv_heads * hd;
-    layers.assign(d.n_layers, LlamaLayerDev{});
+    // host memory: the layer records and the RoPE table (max_context x hd
+    // floats); a failed reservation is an allocation error, not an abort
+    std::vector<float> tab;
+    try {
+        layers.assign(d.n_layers, LlamaLayerDev{});
+        tab.resize(d.max_context * hd);
+    } catch (const std::bad_alloc&) {
+        return hipErrorOutOfMemory;
+    } catch (const std::length_error&) {
+        return hipErrorOutOfMemory;
+    }
     // the rope table: the reference's theta sequence and libm sin/cos per position
-    std::vector<float> tab(d.max_context * hd);
     const float theta_scale = powf(d.rope_base, -2.0f / (float)hd);
     for (uint64_t p = 0; p < d.max_context; ++p) {
         float theta = (float)p;
@@ -508,12 +530,17 @@ hipError_t LlamaModel::create(const LlamaDims& dims, const LlamaHostTensors& t, 
     }
     if (e == hipSuccess) e = hipMalloc((void**)&rope_tab, tab.size() * sizeof(float));
     if (e == hipSuccess) e = hipMemcpy(rope_tab, tab.data(), tab.size() * sizeof(float), hipMemcpyHostToDevice);
-    if (e == hipSuccess) e = hipMalloc((void**)&k_cache, d.n_layers * d.max_context * kvw * sizeof(float));
-    if (e == hipSuccess) e = hipMalloc((void**)&v_cache, d.n_layers * d.max_context * kvw * sizeof(float));
+    uint64_t cache_bytes = 0;  // per cache: n_layers x max_context x kv_width floats
+    if (__builtin_mul_overflow(d.max_context * kvw, (uint64_t)sizeof(float), &cache_bytes) ||
+        __builtin_mul_overflow(cache_bytes, d.n_layers, &cache_bytes))
+        return hipErrorOutOfMemory;
+    if (e == hipSuccess) e = hipMalloc((void**)&k_cache, cache_bytes);
+    if (e == hipSuccess) e = hipMalloc((void**)&v_cache, cache_bytes);
     if (e == hipSuccess) e = hipMalloc((void**)&qkv, (W + 2 * kvw) * sizeof(float));
     if (e == hipSuccess) e = hipMalloc((void**)&scores, d.heads * row_len * sizeof(float));
     if (e == hipSuccess) e = hipMalloc((void**)&cmax, d.heads * nchunks * sizeof(float));
     if (e == hipSuccess) e = hipMalloc((void**)&att, W * sizeof(float));
+    if (e == hipSuccess) e = hipMalloc((void**)&mid, W * sizeof(float));
     if (e == hipSuccess) e = hipMalloc((void**)&gu, 2 * F * sizeof(float));
     if (e == hipSuccess) e = hipMalloc((void**)&argmax_keys, sizeof(unsigned long long));
     if (e == hipSuccess) e = hipMalloc((void**)&logits_buf, d.vocab * sizeof(float));
@@ -621,8 +648,10 @@ hipError_t LlamaModel::step(float* hidden, uint64_t position, float* embedding_o
         const LlamaLayerDev& L = layers[l];
         float* kc = k_cache + l * d.max_context * kvw;
         float* vc = v_cache + l * d.max_context * kvw;
+        const uint32_t lay = (uint32_t)l;
         MvExtra norm1;
         norm1.xform = 1, norm1.eps = d.rms_epsilon, norm1.norm_w = L.attn_norm;
+        norm1.chk = mv_chk(kStAttnNormScale, kStAttnNormOut, kStQkvQuant, kStQkvOut, 0), norm1.chk_layer = lay;
         if (L.fused_qkv()) {
             e = launch_matvec_ex(L.tq, L.wqkv, W + 2 * kvw, W, hidden, nullptr, 1, qkv, W + 2 * kvw, nullptr, err_word,
                                  nullptr, nullptr, norm1, s);
@@ -639,48 +668,68 @@ hipError_t LlamaModel::step(float* hidden, uint64_t position, float* embedding_o
         if (e != hipSuccess) break;
         hipLaunchKernelGGL(attn_scores_kernel, dim3(nchunks, (uint32_t)KVH), dim3(kAttnThreads), lds_scores, s, qkv,
                            tab, kc, vc, (uint32_t)d.max_context, (uint32_t)fresh, (uint32_t)H, (uint32_t)KVH,
-                           (uint32_t)hd, scale, scores, (uint32_t)row_stride, cmax, cstride, err_word,
+                           (uint32_t)hd, scale, scores, (uint32_t)row_stride, cmax, cstride, err_word, lay,
                            repeat_all ? 1u : 0u);
         hipLaunchKernelGGL(attn_pv_kernel, dim3((uint32_t)(hd / kPvDims), (uint32_t)KVH), dim3(kPvThreads), lds_pv, s,
                            scores, cmax, cstride, nchunks, vc, (uint32_t)d.max_context, (uint32_t)count, (uint32_t)H,
-                           (uint32_t)KVH, (uint32_t)hd, (uint32_t)row_stride, att, repeat_all ? 1u : 0u);
+                           (uint32_t)KVH, (uint32_t)hd, (uint32_t)row_stride, att, err_word, lay,
+                           repeat_all ? 1u : 0u);
         e = hipGetLastError();
         if (e != hipSuccess) break;
+        // the residual stream after attention goes to `mid` (the FFN norm's
+        // input); the down projection adds its output to it into hidden
         MvExtra res;
         res.resid = hidden;
-        e = launch_matvec_ex(L.to, L.wo, W, W, att, nullptr, 1, hidden, W, nullptr, err_word, nullptr, nullptr, res, s);
+        res.chk = mv_chk(0, kStOIn, kStOQuant, kStOOut, 0), res.chk_layer = lay;
+        e = launch_matvec_ex(L.to, L.wo, W, W, att, nullptr, 1, mid, W, nullptr, err_word, nullptr, nullptr, res, s);
         if (e != hipSuccess) break;
         // gate/up with the FFN norm: the fused epilogue leaves silu(gate) * up
         // in gu, the plain one [gate | up] for the down projection to combine
         MvExtra norm2;
         norm2.xform = 1, norm2.eps = d.rms_epsilon, norm2.norm_w = L.ffn_norm, norm2.epilogue = L.gu_mode() == 0 ? 1 : 0;
+        norm2.chk = mv_chk(kStFfnNormScale, kStFfnNormOut, kStGuQuant, kStGuOut, 0), norm2.chk_layer = lay;
         if (L.gu_mode() != 2) {
-            e = launch_matvec_ex(L.tg, L.wgu, 2 * F, W, hidden, nullptr, 1, gu, 2 * F, nullptr, err_word, nullptr,
+            e = launch_matvec_ex(L.tg, L.wgu, 2 * F, W, mid, nullptr, 1, gu, 2 * F, nullptr, err_word, nullptr,
                                  nullptr, norm2, s);
         } else {
-            e = launch_matvec_ex(L.tg, L.wgu, F, W, hidden, nullptr, 1, gu, F, nullptr, err_word, nullptr, nullptr,
+            e = launch_matvec_ex(L.tg, L.wgu, F, W, mid, nullptr, 1, gu, F, nullptr, err_word, nullptr, nullptr,
                                  norm2, s);
             if (e == hipSuccess)
-                e = launch_matvec_ex(L.tu, L.wgu + L.off_up, F, W, hidden, nullptr, 1, gu + F, F, nullptr, err_word,
+                e = launch_matvec_ex(L.tu, L.wgu + L.off_up, F, W, mid, nullptr, 1, gu + F, F, nullptr, err_word,
                                      nullptr, nullptr, norm2, s);
         }
         if (e != hipSuccess) break;
         MvExtra down;
-        down.resid = hidden;
+        down.resid = mid;
+        down.chk = mv_chk(0, kStDownIn, kStDownQuant, kStDownOut, kStLayerOut), down.chk_layer = lay;
         if (L.gu_mode() != 0) down.xform = 2;
         e = launch_matvec_ex(L.td, L.wdown, W, F, gu, nullptr, 1, hidden, W, nullptr, err_word, nullptr, nullptr, down,
                              s);
+        if (e == hipSuccess && trace) {  // the checker's copy of every layer's parts
+            float* tr = trace + l * trace_stride();
+            e = hipMemcpyAsync(tr, qkv, (W + 2 * kvw) * sizeof(float), hipMemcpyDeviceToDevice, s);
+            tr += W + 2 * kvw;
+            if (e == hipSuccess) e = hipMemcpyAsync(tr, att, W * sizeof(float), hipMemcpyDeviceToDevice, s);
+            if (e == hipSuccess) e = hipMemcpyAsync(tr + W, mid, W * sizeof(float), hipMemcpyDeviceToDevice, s);
+            if (e == hipSuccess) e = ffn_activation_of(L, tr + 2 * W, s);
+            if (e == hipSuccess)
+                e = hipMemcpyAsync(tr + 2 * W + F, hidden, W * sizeof(float), hipMemcpyDeviceToDevice, s);
+        }
     }
     if (e != hipSuccess) return e;
     if (embedding_out) {
         hipLaunchKernelGGL(rms_norm_row_kernel, dim3(1), dim3(256), 0, s, hidden, out_norm, (uint32_t)W,
-                           d.rms_epsilon, embedding_out, err_word);
+                           d.rms_epsilon, embedding_out, err_word, (uint32_t)d.n_layers);
         e = hipGetLastError();
         if (e != hipSuccess) return e;
     }
     if (logits || argmax) {
         MvExtra norm3;
         norm3.xform = 1, norm3.eps = d.rms_epsilon, norm3.norm_w = out_norm;
+        // finish_hidden (llama.rs:381-392): checks numbered as a layer's first
+        // four, with layer = n_layers
+        norm3.chk = mv_chk(kStAttnNormScale, kStAttnNormOut, kStQkvQuant, kStQkvOut, 0);
+        norm3.chk_layer = (uint32_t)d.n_layers;
         if (argmax) {  // the keys start at 0: left so by the last step's finish, or cleared here
             if (!keys_zero) {
                 e = launch_fill_u64(argmax_keys, 1, 0ull, s);

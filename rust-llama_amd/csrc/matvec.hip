@@ -139,7 +139,33 @@ struct MvArgs {
     // ids checked in the kernel (id_total pairs), x the one shared f32
     // column; zero_pair: this workgroup's pair has id -1 (set by mv_enter)
     uint32_t id_inline, id_total, zero_pair;
+    // Model-runtime checks (Matrix::multiply, the decode step): a nonzero chk
+    // packs five 5-bit ModelStage ids (MvChk order; 0 = that check is off)
+    // and every data error becomes a model_key of layer chk_layer; chk 0
+    // keeps the quantizers' own QuantError keys
+    uint32_t chk, chk_layer;
 };
+
+// the fields of chk, in the order of mv_chk's arguments
+enum MvChk : int { kChkScale = 0, kChkIn = 1, kChkQuant = 2, kChkOut = 3, kChkResid = 4 };
+__device__ __forceinline__ uint32_t chk_stage(const MvArgs& a, int f) { return (a.chk >> (5 * f)) & 31u; }
+
+// Keys of the quantizer's data errors: QuantError keys of column
+// err_column0 + b, or the model stages of the input check and the scale.
+__device__ __forceinline__ uint64_t quant_nonfinite_key(const MvArgs& a, uint32_t b, uint64_t index) {
+    return a.chk ? model_key(a.chk_layer, chk_stage(a, kChkIn), 0) : error_key(a.err_column0 + b, kKindNonFinite, index);
+}
+__device__ __forceinline__ uint64_t quant_scale_key(const MvArgs& a, uint32_t b, uint64_t block) {
+    return a.chk ? model_key(a.chk_layer, chk_stage(a, kChkQuant), block) : error_key(a.err_column0 + b, kKindScale, block);
+}
+__device__ __forceinline__ uint64_t rms_scale_key(const MvArgs& a) {
+    return a.chk ? model_key(a.chk_layer, chk_stage(a, kChkScale), 0) : error_key(a.err_column0, kKindNonFinite, 0);
+}
+// finite(&output, ...) of a model check stage (math.rs:181-187)
+__device__ __forceinline__ void check_finite(const MvArgs& a, int f, float v) {
+    const uint32_t st = chk_stage(a, f);
+    if (st && !finite(v)) report_error(a.err_word, model_key(a.chk_layer, st, 0));
+}
 
 // Kernel entry: false when the workgroup has nothing to do (a refused call,
 // an expert slot with id -1, whose outputs the prepare kernel zeroed).  With
@@ -268,7 +294,13 @@ __device__ __forceinline__ void load16(const float* p, float (&v)[16]) {
 
 // RMSNorm scale of the launch's single input column: every lane adds the
 // squares of its own units in f64, the wave sums are parked in LDS and every
-// thread adds them in wave order, so all threads hold the same value.
+// thread adds them in wave order, so all threads hold the same value.  The
+// reference adds the squares one after another (math.rs:216); two orders of
+// the same n nonnegative f64 terms differ by at most 2 (n - 1) 2^-53 of their
+// sum, so when both ends of that interval give the same f32 mean, the
+// reference's mean is that f32 too.  Otherwise (rare: an interval that
+// straddles an f32 rounding boundary) thread 0 repeats the sum in the
+// reference's order.
 template <int W>
 __device__ __forceinline__ float rms_scale(const MvArgs& a, uint8_t* lds, const LdsMap& L, uint32_t wave,
                                            const float (&v0)[16]) {
@@ -295,7 +327,18 @@ __device__ __forceinline__ float rms_scale(const MvArgs& a, uint8_t* lds, const 
     double total = 0.0;
 #pragma unroll
     for (int w = 0; w < W; ++w) total += red[w];
-    return 1.0f / sqrtf((float)(total / (double)a.cols) + a.eps);
+    const double n = (double)a.cols, err = n * 2.3e-16 * total;  // 2^-52 n sum, with a margin
+    if ((float)((total - err) / n) != (float)((total + err) / n)) {  // every thread takes the same branch
+        __syncthreads();  // every thread has read red[]
+        if (threadIdx.x == 0) {
+            double seq = 0.0;
+            for (uint32_t i = 0; i < a.cols; ++i) seq += (double)(a.x[i] * a.x[i]);
+            red[0] = seq;
+        }
+        __syncthreads();
+        total = red[0];
+    }
+    return 1.0f / sqrtf((float)(total / n) + a.eps);
 }
 
 // The input transform of the decode step, applied to the 16 values of unit u
@@ -327,7 +370,7 @@ __device__ __forceinline__ bool stage_q8k(const MvArgs& a, uint8_t* lds, const L
         scale = rms_scale<W>(a, lds, L, wave, v0);
         if (!(scale <= 3.402823466e38f) || !(scale > 0.0f)) {  // math.rs:218-220
             bad = 1;
-            if (threadIdx.x == 0) report_error(a.err_word, error_key(a.err_column0, kKindNonFinite, 0));
+            if (threadIdx.x == 0) report_error(a.err_word, rms_scale_key(a));
         }
     }
     for (uint32_t base = wave * 64; base < units; base += W * 64) {
@@ -346,9 +389,8 @@ __device__ __forceinline__ bool stage_q8k(const MvArgs& a, uint8_t* lds, const L
         if (o.kind >= 0) {
             bad = 1;
             if (r16 == 0)
-                report_error(a.err_word, o.kind == kKindNonFinite
-                                             ? error_key(a.err_column0 + b, kKindNonFinite, blk * 256ull + o.index)
-                                             : error_key(a.err_column0 + b, kKindScale, blk));
+                report_error(a.err_word, o.kind == kKindNonFinite ? quant_nonfinite_key(a, b, blk * 256ull + o.index)
+                                                                  : quant_scale_key(a, b, blk));
         }
         *(uint4*)(lds + b * L.S + e0) = make_uint4(o.q[0], o.q[1], o.q[2], o.q[3]);
         if (r16 == 0) *(float*)(lds + L.d_off + (blk * 8 + b) * 4) = o.d;
@@ -369,7 +411,7 @@ __device__ __forceinline__ bool stage_q8_0(const MvArgs& a, uint8_t* lds, const 
         scale = rms_scale<W>(a, lds, L, wave, v0);
         if (!(scale <= 3.402823466e38f) || !(scale > 0.0f)) {  // math.rs:218-220
             bad = 1;
-            if (threadIdx.x == 0) report_error(a.err_word, error_key(a.err_column0, kKindNonFinite, 0));
+            if (threadIdx.x == 0) report_error(a.err_word, rms_scale_key(a));
         }
     }
     for (uint32_t base = wave * 64; base < units; base += W * 64) {
@@ -404,8 +446,8 @@ __device__ __forceinline__ bool stage_q8_0(const MvArgs& a, uint8_t* lds, const 
         if (invalid) {
             bad = 1;
             if (half == 0)
-                report_error(a.err_word, nonfinite ? error_key(a.err_column0 + b, kKindNonFinite, blk * 32ull + nf)
-                                                   : error_key(a.err_column0 + b, kKindScale, blk));
+                report_error(a.err_word, nonfinite ? quant_nonfinite_key(a, b, blk * 32ull + nf)
+                                                   : quant_scale_key(a, b, blk));
         }
         const float inv = d != 0.0f ? 1.0f / d : 0.0f;
         uint32_t qw[4] = {0, 0, 0, 0};
@@ -457,7 +499,9 @@ __device__ __forceinline__ void store_out(const MvArgs& a, uint32_t row, uint32_
                                           unsigned long long& best) {
     if (row < a.rows && b < a.batch) {
         const uint64_t i = (uint64_t)b * a.ldy + row;
+        if (a.chk) check_finite(a, kChkOut, v);
         if (a.resid) v = a.resid[i] + v;  // math.rs:203-208: hidden += projected
+        if (a.chk) check_finite(a, kChkResid, v);
         a.y[i] = v;
         const unsigned long long k = argmax_key(v, row);
         best = k > best ? k : best;
@@ -885,6 +929,10 @@ __global__ __launch_bounds__(W * 64) void q4k_mv_small_kernel(MvArgs a) {
                         g += part[(((til * TS + 2 * q) * KS + k) * 16 + r) * B];
                         u += part[(((til * TS + 2 * q + 1) * KS + k) * 16 + r) * B];
                     }
+                if (a.chk) {  // the gate and up outputs themselves (math.rs:167)
+                    check_finite(a, kChkOut, g);
+                    check_finite(a, kChkOut, u);
+                }
                 a.y[(t / 2) * kTileRows + r] = (g / (1.0f + sse2_exp(0.0f - g))) * u;
             }
         }
@@ -1528,15 +1576,21 @@ static hipError_t launch_q45(const MvArgs& a, uint32_t nbat, bool dbg, uint32_t 
     // the SiLU pair epilogue: four tile slots per workgroup (two gate/up
     // pairs, a K split of two; 28672x4096 measured 14.6 us against 15.3 us
     // with one pair and a split of four)
-    if (epilogue == kEpSiluPair) return launch_small<T, kSmallW, kSmallW / 4, kSmallD, 1, false>(a, s, pairs);
+    // (each variant has a DBG twin that also stores the block integers, so
+    // rlq_block_sums checks the very kernel rlq_matmul runs)
+    if (epilogue == kEpSiluPair)
+        return dbg ? launch_small<T, kSmallW, kSmallW / 4, kSmallD, 1, true>(a, s, pairs)
+                   : launch_small<T, kSmallW, kSmallW / 4, kSmallD, 1, false>(a, s, pairs);
     // two tile slots per workgroup (a K split of four): small matrices of at
     // most 4096 columns and 512 tiles (measured: 6144x4096 runs 1 us faster)
-    if (nbat == 1 && !dbg && a.nb <= 16 && a.ntiles <= 512)
-        return launch_small<T, kSmallW, kSmallW / 2, kSmallD, 1, false>(a, s, pairs);
+    if (nbat == 1 && a.nb <= 16 && a.ntiles <= 512)
+        return dbg ? launch_small<T, kSmallW, kSmallW / 2, kSmallD, 1, true>(a, s, pairs)
+                   : launch_small<T, kSmallW, kSmallW / 2, kSmallD, 1, false>(a, s, pairs);
     // more than 16 blocks per row (4096x14336, the down projection): 16 waves
     // per workgroup, K split 16 ways (measured 10.4 us vs 10.7 us with 8)
-    if (nbat == 1 && !dbg && a.nb > 16)
-        return launch_small<T, 2 * kSmallW, 2 * kSmallKS, kSmallD, 1, false>(a, s, pairs);
+    if (nbat == 1 && a.nb > 16)
+        return dbg ? launch_small<T, 2 * kSmallW, 2 * kSmallKS, kSmallD, 1, true>(a, s, pairs)
+                   : launch_small<T, 2 * kSmallW, 2 * kSmallKS, kSmallD, 1, false>(a, s, pairs);
     if (nbat == 1)
         return dbg ? launch_small<T, kSmallW, kSmallKS, kSmallD, 1, true>(a, s, pairs)
                    : launch_small<T, kSmallW, kSmallKS, kSmallD, 1, false>(a, s, pairs);
@@ -1604,7 +1658,7 @@ hipError_t launch_matvec_ex(uint32_t wtype, const uint8_t* w, uint64_t rows, uin
     // the SiLU pair epilogue: one Q4_K / Q5_K column, whole tile pairs, no argmax or residual
     if (ex.epilogue != kEpStore &&
         (ex.epilogue != kEpSiluPair || batch != 1 || (wtype != kQ4_K && wtype != kQ5_K) ||
-         rows % (2 * kTileRows) != 0 || argmax_key || ex.resid || dbg_isum))
+         rows % (2 * kTileRows) != 0 || argmax_key || ex.resid))
         return hipErrorInvalidValue;
     // expert pairs: one pre-quantized column each, plain stores; or, checked
     // in the kernel, one shared f32 column
@@ -1654,6 +1708,8 @@ hipError_t launch_matvec_ex(uint32_t wtype, const uint8_t* w, uint64_t rows, uin
         a.expert_bytes = ex.expert_bytes;
         a.id_inline = ex.ids && ex.id_inline ? 1u : 0u;
         a.id_total = (uint32_t)ex.id_pairs;
+        a.chk = ex.chk;
+        a.chk_layer = ex.chk_layer;
         constexpr int W = kMvWaves;
         const bool dbg = a.dbg_isum != nullptr;
         auto dispatch = [&](uint32_t pairs) -> hipError_t {

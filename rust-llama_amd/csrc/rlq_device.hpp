@@ -199,4 +199,36 @@ __device__ __forceinline__ void report_error(unsigned long long* word, uint64_t 
     atomicMin(word, (unsigned long long)key);
 }
 
+// Model-runtime errors (crates/model-runtime: Matrix::multiply and the Llama
+// decode step) use the column field's largest value, so they sort after every
+// quantizer key of a plain call:
+//   key = 0x7fffff << 41 | layer << 25 | stage << 20 | index
+// The stage numbers the step's checks in the reference's order within a
+// layer (ModelStage), so the smallest key is the first check the reference's
+// sequential step would fail: an earlier layer first, then an earlier stage.
+constexpr uint64_t kModelField = 0x7fffffull;
+enum ModelStage : uint32_t {
+    kStAttnNormScale = 1,   // math.rs:218-220 "RMS normalization scale"
+    kStAttnNormOut = 2,     // math.rs:227 "RMS normalization output" (the Q/K/V quantizer's input)
+    kStQkvQuant = 3,        // the Q/K/V activation's QuantError (UnrepresentableScale)
+    kStQkvOut = 4,          // math.rs:167 "matrix output"
+    kStScore = 5,           // math.rs:476-478 "attention score"
+    kStAttnOut = 6,         // math.rs:494 "attention output"
+    kStOIn = 7,             // math.rs:152 "matrix input"
+    kStOQuant = 8,
+    kStOOut = 9,
+    kStFfnNormScale = 10,
+    kStFfnNormOut = 11,
+    kStGuQuant = 12,
+    kStGuOut = 13,
+    kStDownIn = 14,         // silu(gate) * up, the down projection's input
+    kStDownQuant = 15,
+    kStDownOut = 16,
+    kStLayerOut = 17,       // llama.rs:378 "Llama layer output"
+};
+__device__ __forceinline__ uint64_t model_key(uint32_t layer, uint32_t stage, uint64_t index) {
+    return (kModelField << 41) | ((uint64_t)(layer & 0xffffu) << 25) | ((uint64_t)(stage & 31u) << 20) |
+           (index < 0xfffffull ? index : 0xfffffull);
+}
+
 }  // namespace rlq

@@ -98,7 +98,14 @@ struct MvExtra {
     // zeroes its rows of a -1 pair itself, with no gate, planes or prepare
     // launch
     bool id_inline = false;
+    // Model-runtime checks: five 5-bit ModelStage ids (RMS scale, quantizer
+    // input, quantizer scale, output, output after the residual add; 0 =
+    // off) and the layer of the error keys.  0: QuantError keys.
+    uint32_t chk = 0, chk_layer = 0;
 };
+constexpr uint32_t mv_chk(uint32_t scale, uint32_t in, uint32_t quant, uint32_t out, uint32_t resid) {
+    return scale | in << 5 | quant << 10 | out << 15 | resid << 20;
+}
 // The MUL_MAT / MUL_MAT_ID gate (one workgroup, before the products): checks
 // the ids (ids may be null) and the `bad` bytes of the pre-quantized planes,
 // zeroes the outputs of pairs with id -1, writes *gate.
@@ -164,6 +171,15 @@ struct LlamaModel {
     uint8_t *out_w = nullptr, *emb = nullptr;  // tiled output matrix; GGUF embedding rows
     float *out_norm = nullptr, *k_cache = nullptr, *v_cache = nullptr, *rope_tab = nullptr;
     float *qkv = nullptr, *scores = nullptr, *att = nullptr, *gu = nullptr, *logits_buf = nullptr;
+    float* mid = nullptr;  // the residual stream after attention (the FFN norm's input)
+    // caller's device buffer: each step copies layer l's parts to trace + l *
+    // trace_stride(): [q | k | v] (k before RoPE), the attention output, the
+    // residual after attention, silu(gate) * up, the layer output
+    float* trace = nullptr;
+    uint64_t trace_stride() const {
+        const uint64_t kvw = d.kv_heads * (d.width / d.heads);
+        return 4 * d.width + 2 * kvw + d.feed_forward;
+    }
     float* cmax = nullptr;  // [heads][chunks of 16 tokens] chunk maxima of the scores
     unsigned long long* argmax_keys = nullptr;
     bool keys_zero = false;  // argmax_keys is 0 in stream order (the last step's finish reset it)
@@ -175,6 +191,7 @@ struct LlamaModel {
     hipError_t embedding(uint32_t token, float* hidden, hipStream_t s) const;
     // silu(gate) * up of the last step's last layer (feed_forward floats, device)
     hipError_t ffn_activation(float* out, hipStream_t s) const;
+    hipError_t ffn_activation_of(const LlamaLayerDev& L, float* out, hipStream_t s) const;
     // One step at `position` appending KV row n_cached: hidden (width, device)
     // in/out; embedding_out (width), logits (vocab) and argmax (1) may be null.
     hipError_t step(float* hidden, uint64_t position, float* embedding_out, float* logits, uint32_t* argmax,

@@ -86,3 +86,41 @@ def gguf_contents(cfg, t, tied=False, extra_kv=(), extra_tensors=(), drop=()):
     kvs = [kv for kv in kvs if kv[0] not in drop] + list(extra_kv)
     tensors = [x for x in tensors if x[0] not in drop] + list(extra_tensors)
     return kvs, tensors
+
+
+# Llama-3-8B decode-step shape: 32 layers, d_model 4096, 32 query / 8 KV heads of 128, FFN 14336,
+# vocabulary 128256; Q4_K layer matrices and embedding, Q6_K output.
+LLAMA3_8B = dict(vocabulary=128256, width=4096, feed_forward=14336, heads=32, kv_heads=8, rope_base=500000.0)
+
+
+def gpu_tensors(rlq, ctx, cfg, seed):
+    """Random-init tensors of `cfg` made on the GPU: matrices N(0, 0.02) and
+    the embedding N(0, 1) in f32, encoded by the library's Q4_K / Q6_K
+    encoders (bit-exact with the oracle's); norm weights N(1, 0.05).  The
+    8B-shape weights (4.7 GB) are too many for the oracle's CPU encoders.
+    Returns (device tensors, host copies)."""
+    torch = rlq.torch
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+
+    def mat(dtype, rows, cols, std=0.02):
+        parts, step = [], max(1, (1 << 26) // cols)
+        for r0 in range(0, rows, step):
+            x = torch.randn((min(step, rows - r0), cols), generator=g, device="cuda", dtype=torch.float32) * std
+            parts.append(ctx.quantize(dtype, x))
+        return torch.cat(parts) if len(parts) > 1 else parts[0]
+
+    def norm(n):
+        return torch.randn(n, generator=g, device="cuda", dtype=torch.float32) * 0.05 + 1.0
+
+    W, F, kvw = cfg.width, cfg.feed_forward, cfg.kv_width
+    wt, ot, et = cfg.weight_type, cfg.output_type, cfg.embedding_type
+    layers = [{"attention_norm": norm(W), "query": mat(wt, W, W), "key": mat(wt, kvw, W), "value": mat(wt, kvw, W),
+               "attention_output": mat(wt, W, W), "feed_forward_norm": norm(W), "gate": mat(wt, F, W),
+               "up": mat(wt, F, W), "down": mat(wt, W, F)} for _ in range(cfg.n_layers)]
+    dev = {"embedding": mat(et, cfg.vocabulary, W, 1.0), "output_norm": norm(W), "output": mat(ot, cfg.vocabulary, W),
+           "layers": layers}
+    ctx.sync()
+    host = {k: v.cpu().numpy() for k, v in dev.items() if k != "layers"}
+    host["layers"] = [{k: v.cpu().numpy() for k, v in L.items()} for L in layers]
+    return dev, host

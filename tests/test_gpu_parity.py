@@ -138,6 +138,90 @@ def test_block_sums_bit_exact(ctx, t, rows, cols, batch):
     assert np.array_equal(imin.cpu().numpy(), want_m)
 
 
+def _q5k_blocks(rows, cols, seed):
+    """GGUF Q5_K bytes of rows x cols: random quants and scales, f16 d and
+    dmin drawn from [2^-14, 2^-6] (there is no Q5_K encoder on the path)."""
+    rng = np.random.default_rng(seed)
+    nblk = rows * (cols // 256)
+    b = rng.integers(0, 256, (nblk, 176), dtype=np.uint8)
+    for off in (0, 2):
+        b[:, off:off + 2] = rng.uniform(2.0 ** -14, 2.0 ** -6, nblk).astype(np.float16).view(np.uint8).reshape(nblk, 2)
+    return b.reshape(-1)
+
+
+def _packed(t, rows, cols, seed):
+    return _q5k_blocks(rows, cols, seed) if t == DT.Q5_K else _weights(t, rows, cols, seed)
+
+
+def _oracle_sums(t, w, rows, act, nb):
+    stride = w.size // rows
+    want_i = np.zeros((rows, nb), np.int32)
+    want_m = np.zeros((rows, nb), np.int32)
+    for r in range(rows):
+        want_i[r], want_m[r] = O.block_sums(int(t), w[r * stride:(r + 1) * stride], act, nb)
+    return want_i, want_m
+
+
+@pytest.mark.parametrize("t,rows,cols,variant", [
+    (DT.Q4_K, 4096, 4096, "two tile slots, K split 4 (<= 512 tiles): the O projection"),
+    (DT.Q4_K, 6144, 4096, "two tile slots, K split 4: the fused Q/K/V projection"),
+    (DT.Q4_K, 14336, 4096, "one tile slot, K split 8 (> 512 tiles): the headline matvec"),
+    (DT.Q4_K, 4096, 14336, "16 waves, K split 16 (> 16 blocks): the down projection"),
+    (DT.Q5_K, 4096, 4096, "Q5_K, K split 4"),
+    (DT.Q5_K, 4096, 14336, "Q5_K, 16 waves, K split 16")])
+def test_block_sums_every_decode_variant(ctx, t, rows, cols, variant):
+    """rlq_block_sums runs the very kernel variant rlq_matmul picks for a
+    shape (the batch-1 variants are chosen by tile and block counts): the
+    integers of every (row, block) bitwise, and the same launch's f32
+    outputs against the oracle."""
+    say("block sums, batch 1,", t, rows, cols, variant)
+    w = _packed(t, rows, cols, 300 + rows + cols)
+    x = randn(400 + rows, cols)
+    W = rlq.Weights(ctx, t, w, rows, cols)
+    isum, imin, y = ctx.block_sums_ex(W, torch.from_numpy(x).cuda())
+    ctx.sync()
+    nb = cols // 256
+    want_i, want_m = _oracle_sums(t, w, rows, O.quantize(O.Q8_K, x), nb)
+    assert np.array_equal(isum.cpu().numpy(), want_i)
+    assert np.array_equal(imin.cpu().numpy(), want_m)
+    assert rel_l2(y.cpu().numpy(), O.matvec(int(t), w, rows, cols, x, threads=16)) <= REL_L2
+
+
+def _interleave_tiles(g, u, rows, row_bytes):
+    """[gate tile 0, up tile 0, gate tile 1, ...] of two GGUF matrices of
+    `rows` rows (a multiple of 16): the decode step's gate/up layout."""
+    gt = g.reshape(rows // 16, 16 * row_bytes)
+    ut = u.reshape(rows // 16, 16 * row_bytes)
+    return np.stack([gt, ut], axis=1).reshape(-1)
+
+
+@pytest.mark.parametrize("t,ff,cols", [(DT.Q4_K, 14336, 4096), (DT.Q4_K, 512, 4096), (DT.Q5_K, 14336, 4096),
+                                       (DT.Q4_K, 1024, 2048)])
+def test_silu_pair_kernel_integers_and_outputs(ctx, t, ff, cols):
+    """The decode step's gate/up kernel (two gate/up tile pairs per
+    workgroup, K split over two waves per tile, silu(gate) * up in the
+    epilogue): integers of every gate and up row bitwise, and silu(gate) * up
+    within 1e-5 of the oracle's (llama.rs:367-371)."""
+    say("SiLU-pair gate/up kernel", t, ff, cols)
+    rb = rlq.row_bytes(t, cols)
+    g = _packed(t, ff, cols, 500 + ff)
+    u = _packed(t, ff, cols, 600 + ff)
+    W = rlq.Weights(ctx, t, _interleave_tiles(g, u, ff, rb), 2 * ff, cols)
+    x = randn(700 + ff, cols)
+    isum, imin, y = ctx.block_sums_ex(W, torch.from_numpy(x).cuda(), flags=ctx.SUMS_SILU_PAIR)
+    ctx.sync()
+    nb = cols // 256
+    act = O.quantize(O.Q8_K, x)
+    gi, gm = _oracle_sums(t, g, ff, act, nb)
+    ui, um = _oracle_sums(t, u, ff, act, nb)
+    wi = np.stack([gi.reshape(ff // 16, 16, nb), ui.reshape(ff // 16, 16, nb)], axis=1).reshape(2 * ff, nb)
+    wm = np.stack([gm.reshape(ff // 16, 16, nb), um.reshape(ff // 16, 16, nb)], axis=1).reshape(2 * ff, nb)
+    assert np.array_equal(isum.cpu().numpy(), wi)
+    assert np.array_equal(imin.cpu().numpy(), wm)
+    want = O.silu(O.matvec(int(t), g, ff, cols, x, threads=16)) * O.matvec(int(t), u, ff, cols, x, threads=16)
+    assert rel_l2(y.cpu().numpy(), want) <= REL_L2
+
+
 def test_block_sums_golden_records(ctx):
     for i, r in enumerate(F.matvec_extended()):
         say("GGQX block sums", i)
@@ -303,6 +387,51 @@ def test_device_errors_suppress_outputs_and_report_first_column(ctx):
     assert bool((y[:2] == 0).all())
 
 
+from test_oracle_llama import huge_q4k  # noqa: E402
+
+
+def test_multiply_finite_checks(ctx):
+    """Matrix::multiply (math.rs:144-169): finite(input) as NonFinite
+    "matrix input" before anything is written, the quantizer's
+    UnrepresentableScale, and finite(output) as NonFinite "matrix output"
+    (an f32 overflow forced by extreme weights and input; the oracle's own
+    product overflows the same way); a finite product equals rlq_matmul's
+    bitwise."""
+    rows, cols = 64, 1024
+    say("Matrix::multiply finite checks", rows, cols)
+    W = rlq.Weights(ctx, DT.Q4_K, _weights(DT.Q4_K, rows, cols, 12), rows, cols)
+    x = torch.from_numpy(randn(13, cols)).cuda()
+    y = ctx.multiply(W, x)
+    ctx.sync()
+    assert torch.equal(y.view(torch.int32), ctx.matmul(W, x)[0].view(torch.int32))
+    bad = x.clone()
+    bad[700] = float("inf")
+    y.fill_(7.0)
+    ctx.multiply(W, bad, y)
+    with pytest.raises(rlq.QuantError) as e:
+        ctx.sync()
+    assert (e.value.name, e.value.a, e.value.b) == ("NonFinite", 3, 0)
+    assert bool((y == 7.0).all())
+    tiny = x.clone()
+    tiny[512:768] = 1e-45
+    ctx.multiply(W, tiny, y)
+    with pytest.raises(rlq.QuantError) as e:
+        ctx.sync()
+    assert (e.value.name, e.value.block) == ("UnrepresentableScale", 2)
+    assert bool((y == 7.0).all())
+    Wh = rlq.Weights(ctx, DT.Q4_K, huge_q4k(rows, cols), rows, cols)
+    big = np.full(cols, 1e36, np.float32)
+    want = O.matvec(O.Q4_K, huge_q4k(rows, cols), rows, cols, big)
+    assert not np.all(np.isfinite(want))  # the reference's multiply fails its output check here
+    y = ctx.multiply(Wh, torch.from_numpy(big).cuda())
+    with pytest.raises(rlq.QuantError) as e:
+        ctx.sync()
+    assert (e.value.name, e.value.a, e.value.b) == ("NonFinite", 4, 0)
+    assert not bool(torch.isfinite(y).all())
+    ctx.matmul(Wh, torch.from_numpy(big).cuda())  # llama_quant::matvec has no output check
+    ctx.sync()
+
+
 def test_zero_weights_give_zero(ctx):
     say("zero weights")
     for t, cols in ((DT.Q4_K, 1024), (DT.Q6_K, 1024), (DT.Q8_0, 96)):
@@ -367,7 +496,7 @@ def test_fused_quantizer_on_golden_q8k_inputs(ctx, t, batch):
         want = O.matvec(int(t), w, rows, cols, x)
         got = y[0].cpu().numpy()
         in_range = np.array([O.abs_terms(int(t), w[r * stride:(r + 1) * stride], expected, nb)
-                             < np.finfo(np.float32).max / 2 for r in range(rows)])
+                             < float(np.finfo(np.float32).max) / 2 for r in range(rows)])  # compared in f64
         assert np.isfinite(want[in_range]).all() and np.isfinite(got[in_range]).all(), i
         if in_range.any():
             tol = elem_tol(t, w, rows, expected, cols, want)[in_range]

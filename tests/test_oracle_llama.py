@@ -239,3 +239,71 @@ def test_one_layer_step_by_parts():
     assert np.array_equal(h, want)
     n3 = O.rms_norm(want, t["output_norm"], cfg.rms_epsilon)
     assert np.array_equal(logits, O.matvec(cfg.output_type, t["output"], cfg.vocabulary, W, n3))
+
+
+def huge_q4k(rows, cols):
+    """Q4_K bytes whose dots overflow f32 against a large input: f16 d =
+    65504, every sub-block scale 63 and min 0 (matvec_extra.rs:212-221),
+    every quant 15."""
+    blk = np.zeros(144, np.uint8)
+    blk[0:2] = np.array([0x7BFF], np.uint16).view(np.uint8)
+    blk[4:8], blk[8:12], blk[12:16] = 0xFF, 0x00, 0x0F
+    blk[16:] = 0xFF
+    return np.tile(blk, rows * cols // 256)
+
+
+def nonfinite_cases():
+    """(model config, tensors, input hidden or None for the embedding of
+    token 3, expected (check, layer)) of the decode step's NonFinite checks:
+    logits that overflow ("matrix output" in finish_hidden, layer =
+    n_layers = 0); FFN-norm weights of 1e36, whose gate and up stay finite
+    but silu(gate) * up overflows ("matrix input" of the down projection,
+    layer 0); a NaN hidden state (the first RMSNorm's "scale", layer 0)."""
+    cfg0 = make_config(n_layers=0, output_type=O.Q4_K)
+    t0 = dict(make_tensors(cfg0, 29))
+    t0["output"] = huge_q4k(cfg0.vocabulary, cfg0.width)
+    t0["output_norm"] = np.full(cfg0.width, 1e30, np.float32)
+    cfg1 = make_config(n_layers=1)
+    t1 = make_tensors(cfg1, 30)
+    L = dict(t1["layers"][0])
+    L["feed_forward_norm"] = np.full(cfg1.width, 1e36, np.float32)
+    t1 = dict(t1, layers=[L])
+    return [(cfg0, t0, None, (4, 0)), (cfg1, t1, None, (3, 0)),
+            (cfg1, t1, np.full(cfg1.width, np.nan, np.float32), (1, 0))]
+
+
+@pytest.mark.parametrize("case", range(3))
+def test_step_nonfinite_checks(case):
+    """The reference's first failing check and its layer (llama.rs:250-392,
+    math.rs:144-228): the overflow and NaN constructions fail where f32
+    arithmetic says they must (the product, the f32 square, checked here
+    with numpy), and the step reports that check."""
+    cfg, t, h, (check, layer) = nonfinite_cases()[case]
+    o = O.LlamaOracle(cfg, t)
+    x = o.embedding(3) if h is None else h
+    if case == 0:  # the final norm is finite, the logits are not
+        n = O.rms_norm(x, t["output_norm"], cfg.rms_epsilon)
+        assert np.all(np.isfinite(n))
+        assert not np.all(np.isfinite(O.matvec(O.Q4_K, t["output"], cfg.vocabulary, cfg.width, n)))
+    with pytest.raises(O.OracleError) as e:
+        o.step(x, 0)
+    assert (e.value.name, e.value.a, e.value.b) == ("NonFinite", check, layer)
+
+
+def test_layer_by_layer_equals_the_step():
+    """The checker's per-layer entry points restate the same step: every
+    layer run on its own, then finish_hidden, give the step's last-layer
+    output and logits bit for bit over several positions (KV rows shared)."""
+    cfg = make_config(n_layers=3)
+    t = make_tensors(cfg, 41)
+    a, b = O.LlamaOracle(cfg, t), O.LlamaOracle(cfg, t)
+    for pos, tok in enumerate((5, 17, 999, 0)):
+        h_step, lg_step = a.step(a.embedding(tok), pos)
+        h = b.embedding(tok)
+        for li in range(cfg.n_layers):
+            h = b.layer(li, h, pos)
+        b.advance()
+        emb, lg = b.finish(h)
+        assert np.array_equal(h.view(np.uint32), h_step.view(np.uint32)), pos
+        assert np.array_equal(lg.view(np.uint32), lg_step.view(np.uint32)), pos
+        assert np.array_equal(emb, O.rms_norm(h, t["output_norm"], cfg.rms_epsilon)), pos
