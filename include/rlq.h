@@ -89,7 +89,8 @@ typedef enum rlq_status {
     /* model-runtime Error::NonFinite (crates/model-runtime/src/lib.rs:51):
        a = the check (rlq_nonfinite_check), b = the Llama layer (n_layers for
        the final norm and the output matrix; 0 for rlq_multiply) */
-    RLQ_NON_FINITE = 31
+    RLQ_NON_FINITE = 31,
+    RLQ_SCRATCH_LIMIT = 32              /* rlq_matmul_noalloc: a = bytes needed, b = the scratch size */
 } rlq_status;
 
 /* The reference's NonFinite checks, by the name it reports. */
@@ -211,6 +212,20 @@ int32_t rlq_multiply(rlq_context *ctx, const rlq_weights *w, const float *x, flo
  * fused into the matvec epilogue: argmax[b] = index of the largest y[b*rows+r]. */
 int32_t rlq_matmul_argmax(rlq_context *ctx, const rlq_weights *w, const float *x, uint64_t batch, float *y,
                           uint32_t *argmax, void *stream, rlq_error *err);
+
+/* No counterpart in the reference: for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  rlq_matmul (argmax null) or rlq_matmul_argmax (argmax
+ * non-null) on the same kernels, with the same results, that allocates and
+ * frees nothing: the argmax keys and the prefill GEMM's activation image
+ * (batches above 8 of Q4_K weights) live in a static 32 MiB device array
+ * that each GPU holds until the process ends.  A call whose workspace
+ * exceeds it returns RLQ_SCRATCH_LIMIT (a = bytes needed, b = 33554432); for
+ * 4096 columns that is a batch of about 3,700.  Every call on one GPU, from
+ * any context, shares that GPU's array: calls that overlap on one GPU (other
+ * streams, other threads) race and must be ordered by the caller. */
+int32_t rlq_matmul_noalloc(rlq_context *ctx, const rlq_weights *w, const float *x, uint64_t batch, float *y,
+                           uint32_t *argmax, void *stream, rlq_error *err);
 
 /* GGML MUL_MAT with batch broadcast (crates/tensor/src/cpu_extra.rs:756-873)
  * over stacked weights W [cols, rows, w.n2, w.n3] and a right-hand side

@@ -31,7 +31,7 @@ ERROR_NAMES = {
     21: "InvalidConfig", 22: "InvalidToken", 23: "InvalidState",
     24: "Shape", 25: "Bounds", 26: "Unsupported",
     27: "GgufIo", 28: "GgufInvalid", 29: "GgufLimit", 30: "GgufUnsupported",
-    31: "NonFinite",
+    31: "NonFinite", 32: "ScratchLimit",
 }
 F32 = 0
 SHAPE, BOUNDS, UNSUPPORTED = 24, 25, 26

@@ -90,7 +90,7 @@ ERROR_NAMES = {
     21: "InvalidConfig", 22: "InvalidToken", 23: "InvalidState",
     24: "Shape", 25: "Bounds", 26: "Unsupported",
     27: "GgufIo", 28: "GgufInvalid", 29: "GgufLimit", 30: "GgufUnsupported",
-    31: "NonFinite",
+    31: "NonFinite", 32: "ScratchLimit",
 }
 
 # NonFinite checks (QuantError.a of a NonFinite error): the names the
@@ -154,6 +154,7 @@ SIGNATURES = {
     "rlq_mul_mat_id": ([_P, _P, _U32, _P, _U64, _U64, _P, _U64, _P, _P, _E], _I32),
     "rlq_matmul": ([_P, _P, _P, _U64, _P, _P, _E], _I32),
     "rlq_multiply": ([_P, _P, _P, _P, _P, _E], _I32),
+    "rlq_matmul_noalloc": ([_P, _P, _P, _U64, _P, _P, _P, _E], _I32),
     "rlq_matmul_argmax": ([_P, _P, _P, _U64, _P, _P, _P, _E], _I32),
     "rlq_quantize_device": ([_P, _U32, _P, _U64, _U64, _P, _P, _E], _I32),
     "rlq_sync": ([_P, _P, _E], _I32),
@@ -373,6 +374,18 @@ class Context:
         _check(_lib.rlq_matmul_argmax(self._h, w._h, _dev_ptr(x2, torch.float32), batch,
                                       _dev_ptr(y, torch.float32), _dev_ptr(argmax, torch.int32),
                                       _stream_ptr(stream), ctypes.byref(err)), err)
+        return y, argmax
+
+    def matmul_noalloc(self, w, x, y, argmax=None, stream=None):
+        """rlq_matmul_noalloc: matmul (argmax None) or matmul_argmax into the
+        caller's y [batch, rows] (and argmax [batch] int32), with the
+        library's static device scratch instead of any allocation."""
+        x2 = x.reshape(-1, w.cols)
+        err = _Err()
+        _check(_lib.rlq_matmul_noalloc(self._h, w._h, _dev_ptr(x2, torch.float32), x2.shape[0],
+                                       _dev_ptr(y, torch.float32),
+                                       _dev_ptr(argmax, torch.int32) if argmax is not None else None,
+                                       _stream_ptr(stream), ctypes.byref(err)), err)
         return y, argmax
 
     def quantize(self, dtype, x, stream=None):

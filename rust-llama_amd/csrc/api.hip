@@ -94,6 +94,7 @@ struct DevBuf {
 
 struct rlq_context {
     int device = 0;
+    uint8_t* scratch = nullptr;  // this device's copy of the static `scratch` array (rlq_matmul_noalloc)
     hipStream_t stream = nullptr;
     unsigned long long* err_words = nullptr;  // [0] device API (sticky), [1] host API (per call)
     unsigned long long* host_err = nullptr;   // pinned readback
@@ -200,7 +201,38 @@ int32_t take_error(rlq_context* ctx, int slot, hipStream_t s, uint32_t dtype, rl
 std::mutex g_default_mu;
 rlq_context* g_default = nullptr;
 
+}  // namespace
 
+// ---- static scratch of rlq_matmul_noalloc ----------------------------------
+// Device memory that rlq_matmul_noalloc uses instead of allocating: the
+// argmax keys (8 bytes per column, padded to 256) and then the prefill
+// GEMM's activation image (gemm_planes_bytes).  Each device holds its own
+// copy for the life of the process.  Host code never passes the array's name
+// to a kernel (on the host it is only a handle): every use goes through the
+// device address hipGetSymbolAddress returns, taken once per device at
+// context creation with that device current.
+constexpr size_t kScratchBytes = size_t(32) << 20;
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+namespace {
+
+constexpr int kScratchDevices = 256;
+std::mutex g_scratch_mu;
+uint8_t* g_scratch_addr[kScratchDevices];
+
+// The calling thread's current device must be `device`.
+hipError_t scratch_address(int device, uint8_t** out) {
+    if (device < 0 || device >= kScratchDevices) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_addr[device]) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return e;
+        g_scratch_addr[device] = (uint8_t*)p;
+    }
+    *out = g_scratch_addr[device];
+    return hipSuccess;
+}
 
 int32_t default_context(rlq_context** out, rlq_error* err) {
     if (!g_default) {
@@ -282,6 +314,7 @@ const char* rlq_status_string(int32_t code) {
         case RLQ_GGUF_LIMIT: return "GGUF file exceeds a reader limit";
         case RLQ_GGUF_UNSUPPORTED: return "GGUF content is not supported";
         case RLQ_NON_FINITE: return "non-finite value";
+        case RLQ_SCRATCH_LIMIT: return "workspace exceeds the library's static scratch";
         default: return "unknown status";
     }
 }
@@ -309,7 +342,8 @@ int32_t rlq_context_create(int32_t device, rlq_context** out, rlq_error* err) {
     rlq_context* ctx = new (std::nothrow) rlq_context;
     if (!ctx) return fail(err, RLQ_ALLOCATION_FAILED);
     ctx->device = device;
-    hipError_t e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
+    hipError_t e = scratch_address(device, &ctx->scratch);
+    if (e == hipSuccess) e = hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking);
     if (e == hipSuccess) e = hipMalloc((void**)&ctx->err_words, 2 * sizeof(unsigned long long));
     if (e == hipSuccess) e = hipHostMalloc((void**)&ctx->host_err, sizeof(unsigned long long), hipHostMallocDefault);
     if (e == hipSuccess) e = launch_fill_u64(ctx->err_words, 2, ~0ull, ctx->stream);
@@ -591,6 +625,36 @@ int32_t rlq_matmul_argmax(rlq_context* ctx, const rlq_weights* w, const float* x
     return matmul_impl(ctx, w, x, batch, y, argmax, stream, err);
 }
 
+// rlq_matmul / rlq_matmul_argmax on the same kernels, with every buffer
+// beyond the inputs and outputs taken from this device's static scratch:
+// nothing is allocated or freed.  The keys are cleared by a fill kernel
+// (never a memset, so the call may be captured in a graph).
+int32_t rlq_matmul_noalloc(rlq_context* ctx, const rlq_weights* w, const float* x, uint64_t batch, float* y,
+                           uint32_t* argmax, void* stream, rlq_error* err) {
+    if (!ctx || !w || !x || !y) return fail(err, RLQ_INVALID_ARGUMENT);
+    if (((uintptr_t)x & 15) || ((uintptr_t)y & 3)) return fail(err, RLQ_INVALID_ARGUMENT, w->dtype);
+    if (batch == 0) return ok(err);
+    if (batch > kScratchBytes) return fail(err, RLQ_SCRATCH_LIMIT, w->dtype, ~0ull, kScratchBytes);
+    const bool gemm = w->dtype == kQ4_K && batch > kDecodeMaxBatch;
+    const uint64_t keys_bytes = argmax ? (batch * 8 + 255) / 256 * 256 : 0;
+    const uint64_t need = keys_bytes + (gemm ? gemm_planes_bytes(batch, w->cols) : 0);
+    if (need > kScratchBytes) return fail(err, RLQ_SCRATCH_LIMIT, w->dtype, need, kScratchBytes);
+    if (!ctx->scratch) return fail(err, RLQ_INVALID_ARGUMENT, w->dtype);
+    DeviceGuard g(ctx->device);
+    const hipStream_t s = pick(ctx, stream);
+    unsigned long long* keys = argmax ? (unsigned long long*)ctx->scratch : nullptr;
+    if (keys) HIP_TRY(launch_fill_u64(keys, batch, 0ull, s));
+    if (gemm) {
+        HIP_TRY(launch_gemm_q4k(w->dev, w->rows, w->cols, x, batch, y, w->rows, ctx->scratch + keys_bytes,
+                                ctx->err_words, nullptr, nullptr, s));
+        if (keys) HIP_TRY(launch_argmax_rows(y, batch, w->rows, keys, s));
+    } else {
+        HIP_TRY(launch_matvec(w->dtype, w->dev, w->rows, w->cols, x, nullptr, batch, y, w->rows, keys, ctx->err_words,
+                              nullptr, nullptr, s));
+    }
+    if (keys) HIP_TRY(launch_argmax_finish(keys, batch, y, w->rows, argmax, s, true));
+    return ok(err);
+}
 
 int32_t rlq_quantize_device(rlq_context* ctx, uint32_t dtype, const float* x, uint64_t cols, uint64_t batch,
                             uint8_t* out, void* stream, rlq_error* err) {
