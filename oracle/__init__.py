@@ -14,7 +14,7 @@ import os
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "librlq_oracle.so")
+LIB_PATH = os.environ.get("RLQ_ORACLE_LIB") or os.path.join(HERE, "librlq_oracle.so")
 
 Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, Q8_K = 8, 10, 11, 12, 13, 14, 15
 BLOCK = {Q8_0: 32, Q2_K: 256, Q3_K: 256, Q4_K: 256, Q5_K: 256, Q6_K: 256, Q8_K: 256}

@@ -35,7 +35,9 @@ except ImportError:  # pragma: no cover - the host API still works without torch
     torch = None
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "librlq.so")
+# RLQ_LIB_PATH selects another build of the library (the host-sanitizer build
+# of `build.py --sanitize`, for CPU test runs)
+LIB_PATH = os.environ.get("RLQ_LIB_PATH") or os.path.join(HERE, "librlq.so")
 
 
 class DType(enum.IntEnum):

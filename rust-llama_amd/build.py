@@ -38,13 +38,26 @@ def _run(cmd):
     return p.returncode, msg
 
 
-def build(verbose=False):
-    out_dir = os.path.join(HERE, "_build")
+# Host-side AddressSanitizer + UndefinedBehaviorSanitizer build (CPU test
+# runs only): every flag reaches the host pass alone, the GPU code is built as
+# usual; gguf.cpp is built by the same clang so one sanitizer runtime serves
+# the process (libclang_rt.asan, preloaded by the oracle Makefile's
+# `sanitize` target).
+SAN_HOST = ["-Xarch_host", "-fsanitize=address", "-Xarch_host", "-fsanitize=undefined",
+            "-Xarch_host", "-fno-omit-frame-pointer", "-Xarch_host", "-fno-sanitize-recover=undefined"]
+CLANGXX = "/opt/rocm/llvm/bin/clang++"
+
+
+def build(verbose=False, sanitize=False):
+    out_dir = os.path.join(HERE, "_asan" if sanitize else "_build")
     os.makedirs(out_dir, exist_ok=True)
     objs = [os.path.join(out_dir, s.replace(".hip", ".o")) for s in SOURCES]
-    cmds = [[HIPCC, *FLAGS, "-c", os.path.join(HERE, "csrc", s), "-o", o] for s, o in zip(SOURCES, objs)]
+    extra = SAN_HOST if sanitize else []
+    cmds = [[HIPCC, *FLAGS, *extra, "-c", os.path.join(HERE, "csrc", s), "-o", o] for s, o in zip(SOURCES, objs)]
     host_objs = [os.path.join(out_dir, s.replace(".cpp", ".o")) for s in HOST_SOURCES]
-    cmds += [[CXX, "-O2", "-std=c++17", "-fPIC", "-Wall", "-I" + os.path.join(ROOT, "include"),
+    host_cxx, host_san = (CLANGXX, ["-fsanitize=address,undefined", "-fno-omit-frame-pointer",
+                                    "-fno-sanitize-recover=undefined"]) if sanitize else (CXX, [])
+    cmds += [[host_cxx, "-O2", "-std=c++17", "-fPIC", "-Wall", *host_san, "-I" + os.path.join(ROOT, "include"),
               "-I" + os.path.join(HERE, "csrc"), "-c", os.path.join(HERE, "csrc", s), "-o", o]
              for s, o in zip(HOST_SOURCES, host_objs)]
     srcs = SOURCES + HOST_SOURCES
@@ -56,13 +69,15 @@ def build(verbose=False):
             print(f"[{s}]\n{msg}", file=sys.stderr)
         if rc:
             raise RuntimeError(f"hipcc failed on {s}")
-    tmp = LIB + ".tmp"
-    rc, msg = _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp, *objs])
+    lib = os.path.join(out_dir, "librlq.so") if sanitize else LIB
+    tmp = lib + ".tmp"
+    link = ["-shared-libsan", *SAN_HOST] if sanitize else []
+    rc, msg = _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", *link, "-o", tmp, *objs])
     if rc:
         raise RuntimeError(f"link failed:\n{msg}")
-    os.replace(tmp, LIB)
-    return LIB
+    os.replace(tmp, lib)
+    return lib
 
 
 if __name__ == "__main__":
-    print(build(verbose=True))
+    print(build(verbose=True, sanitize="--sanitize" in sys.argv[1:]))
