@@ -15,20 +15,32 @@ rotates over ROTATE distinct weight copies (>= 330 MB per sweep).
 
 value     = algorithmic bytes per step (W + fp32 x + fp32 y) / mean step time,
             the K timed steps bracketed by HIP events on the stream they run on
-roofline  = the same bytes / the kernel's mean duration (the step is one
-            kernel), against MI355X's 8 TB/s HBM peak
+roofline  = the same bytes / the mean step time; the step is one kernel, so
+            this is that kernel's mean duration launched back to back (the
+            rocprofv3 kernel trace of the same command agrees), against
+            MI355X's 8 TB/s HBM peak
 cpu_baseline = the CPU oracle (a C restatement of the reference's scalar
             Rust path) on the same weights, 1 thread, repeated for ~10 s.
 
 --copy-probe adds one device-to-device copy of 256 MiB before the timed steps:
 the calibration kernel for FETCH_SIZE / WRITE_SIZE counter runs.
 
+"configs" times every other BASELINE configuration the same way, each with its own roofline:
+Q8_0 4864x896 (batch 1), Q4_K 14336x4096 at batches 4 and 8, the Q6_K 128256x4096 output
+projection at batches 1 and 8 with the fused greedy argmax, and the Qwen-vocabulary output
+projection 151936x896 as Q8_0 (Q6_K has no encoding at K=896) with the argmax.  Matrices that fit
+the 256 MB MALL rotate over copies so that a sweep touches >= 300 MB.
+
+"prefill" prices the GEMM against the int8 MFMA peak (5.0 POP/s), the figure the target is
+quoted on.
+
 "decode_step" (config 5) times whole decode steps of a random-init Llama-3-8B-shape model
 (Q4_K layers, Q6_K output) at a context of ~1000 rows: tok/s and the step's algorithmic bytes
-(every weight byte once + the KV rows read) per second.
+(every weight byte once + the KV rows read) per second, with one oracle step on one host thread
+as its CPU baseline.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--extra] [--no-cpu] [--copy-probe]
-                       [--no-llama] [--llama-steps N] [--llama-cpu]
+                       [--no-llama] [--no-configs] [--llama-steps N] [--no-llama-cpu]
 """
 import argparse
 import json
@@ -110,20 +122,28 @@ def algorithmic_bytes(rlq, dtype, rows, cols, batch):
     return rlq.row_bytes(dtype, cols) * rows + 4 * cols * batch + 4 * rows * batch
 
 
-def time_steps(rlq, ctx, handles, x, y, steps, warmup):
-    """Mean step time (ms) of `steps` back-to-back rlq_matmul calls, bracketed
-    by HIP events on the stream they are launched on (torch's current one)."""
+def time_steps(rlq, ctx, handles, x, y, steps, warmup, argmax=None):
+    """Mean step time (ms) of `steps` back-to-back rlq_matmul calls (or
+    rlq_matmul_argmax when `argmax` is given), bracketed by HIP events on the
+    stream they are launched on (torch's current one)."""
     torch = rlq.torch
     n = len(handles)
+
+    def call(i):
+        if argmax is None:
+            ctx.matmul(handles[i % n], x, y)
+        else:
+            ctx.matmul_argmax(handles[i % n], x, y, argmax)
+
     for i in range(warmup):
-        ctx.matmul(handles[i % n], x, y)
+        call(i)
     ctx.sync()
     stream = torch.cuda.current_stream()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     start.record(stream)
     for i in range(steps):
-        ctx.matmul(handles[i % n], x, y)
+        call(i)
     end.record(stream)
     torch.cuda.synchronize()
     ctx.sync()  # raises if the GPU recorded a data error
@@ -203,9 +223,9 @@ def prefill(rlq, ctx, handles, rows, cols, steps, warmup):
                     "kernel + GEMM kernel per step)",
         "steps": steps, "us_per_step": round(ms * 1e3, 3), "tops": round(tops, 2),
         "tok_s": round(PREFILL_M / (ms * 1e-3), 1), "ops_per_step": ops,
-        "roofline": {"bound": "mfma", "achieved": round(tops, 2), "peak": F16_MFMA_PEAK_TFLOPS,
-                     "unit": "TFLOP/s", "frac": round(tops / F16_MFMA_PEAK_TFLOPS, 4),
-                     "frac_of_int8_peak": round(tops / INT8_MFMA_PEAK_TOPS, 4),
+        "roofline": {"bound": "mfma", "achieved": round(tops, 2), "peak": INT8_MFMA_PEAK_TOPS,
+                     "unit": "TOP/s", "frac": round(tops / INT8_MFMA_PEAK_TOPS, 4),
+                     "frac_of_f16_peak": round(tops / F16_MFMA_PEAK_TFLOPS, 4),
                      "traffic": TRAFFIC_PREFILL_BYTES},
     }
 
@@ -240,7 +260,7 @@ def cpu_baseline(dtype, w_host, rows, cols, x_host, budget_s=10.0, all_cores_s=5
     return out
 
 
-def run_config(rlq, ctx, dtype, rows, cols, batch, seed, steps, warmup, copies):
+def run_config(rlq, ctx, dtype, rows, cols, batch, seed, steps, warmup, copies, argmax=False):
     torch = rlq.torch
     make = gpu_random_blocks if int(dtype) in RANDOM_BLOCK else gpu_weights
     handles, host0 = make(rlq, ctx, dtype, rows, cols, seed, copies)
@@ -248,12 +268,44 @@ def run_config(rlq, ctx, dtype, rows, cols, batch, seed, steps, warmup, copies):
     g.manual_seed(seed + 7)
     x = torch.randn((batch, cols), generator=g, device="cuda", dtype=torch.float32)
     y = torch.empty((batch, rows), device="cuda", dtype=torch.float32)
-    ms = time_steps(rlq, ctx, handles, x, y, steps, warmup)
-    nbytes = algorithmic_bytes(rlq, dtype, rows, cols, batch)
+    am = torch.empty(batch, device="cuda", dtype=torch.int32) if argmax else None
+    ms = time_steps(rlq, ctx, handles, x, y, steps, warmup, argmax=am)
+    nbytes = algorithmic_bytes(rlq, dtype, rows, cols, batch) + (4 * batch if argmax else 0)
     out = {"rows": rows, "cols": cols, "batch": batch, "dtype": rlq.DType(dtype).name, "bytes_per_step": nbytes,
            "us_per_step": ms * 1e3, "gbs": nbytes / (ms * 1e-3) / 1e9, "rotated_copies": copies}
     out["frac_hbm"] = out["gbs"] / HBM_PEAK_GBS
     return out, handles, host0, x
+
+
+# The other BASELINE configurations (name: dtype, rows, cols, batch, rotated copies, fused argmax,
+# workload).  Copies bring each timed sweep to >= 300 MB where one matrix fits the MALL.
+CONFIGS = {
+    "q8_0_4864x896_b1": ("Q8_0", 4864, 896, 1, 64, False,
+                         "Q8_0 x Q8_0 decode matvec 4864x896 (Qwen2.5-0.5B FFN up), batch 1"),
+    "q4k_14336x4096_b4": ("Q4_K", 14336, 4096, 4, ROTATE, False, "Q4_K x Q8_K decode matvec 14336x4096, batch 4"),
+    "q4k_14336x4096_b8": ("Q4_K", 14336, 4096, 8, ROTATE, False, "Q4_K x Q8_K decode matvec 14336x4096, batch 8"),
+    "q6k_128256x4096_b1_argmax": ("Q6_K", 128256, 4096, 1, 1, True,
+                                  "Q6_K output projection 128256x4096, batch 1, fused greedy argmax"),
+    "q6k_128256x4096_b8_argmax": ("Q6_K", 128256, 4096, 8, 1, True,
+                                  "Q6_K output projection 128256x4096, batch 8, fused greedy argmax"),
+    "q8_0_151936x896_b1_argmax": ("Q8_0", 151936, 896, 1, 3, True,
+                                  "Qwen-vocabulary output projection 151936x896 as Q8_0 (Q6_K cannot encode "
+                                  "K=896), batch 1, fused greedy argmax"),
+}
+
+
+def config_legs(rlq, ctx, steps, warmup):
+    legs = {}
+    for i, (name, (dt, r, c, b, copies, am, workload)) in enumerate(CONFIGS.items()):
+        o, hs, _, _ = run_config(rlq, ctx, rlq.DType[dt], r, c, b, 0x51A7E010 + i, steps, warmup, copies, argmax=am)
+        for h in hs:
+            h.close()
+        rlq.torch.cuda.empty_cache()
+        legs[name] = {"workload": workload, "us_per_step": round(o["us_per_step"], 3),
+                      "bytes_per_step": o["bytes_per_step"], "rotated_copies": copies,
+                      "roofline": {"bound": "hbm", "achieved": round(o["gbs"], 2), "peak": HBM_PEAK_GBS,
+                                   "unit": "GB/s", "frac": round(o["gbs"] / HBM_PEAK_GBS, 4)}}
+    return legs
 
 
 def moe_decode(rlq, ctx, steps, warmup):
@@ -447,7 +499,8 @@ def main():
     ap.add_argument("--copy-probe", action="store_true", help="one 256 MiB device copy (counter calibration)")
     ap.add_argument("--no-llama", action="store_true", help="skip the Llama decode step (config 5)")
     ap.add_argument("--llama-steps", type=int, default=32)
-    ap.add_argument("--llama-cpu", action="store_true", help="also time one oracle decode step on the host")
+    ap.add_argument("--no-llama-cpu", action="store_true", help="skip the oracle decode step on the host")
+    ap.add_argument("--no-configs", action="store_true", help="skip the other BASELINE configurations")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one MI355X: every GPU box here has one GPU and this build has no "
@@ -505,17 +558,13 @@ def main():
     for h in handles:
         h.close()
     torch.cuda.empty_cache()
+    if not args.no_configs:
+        result["configs"] = config_legs(rlq, ctx, max(200, args.steps // 4), args.warmup)
     if not args.no_llama:
-        result["decode_step"] = decode_step(rlq, ctx, args.llama_steps, 8, cpu=args.llama_cpu)
+        result["decode_step"] = decode_step(rlq, ctx, args.llama_steps, 8, cpu=not (args.no_llama_cpu or args.no_cpu))
     if args.extra:
         extra = {}
         for name, (t, r, c, b, copies) in {
-            "q4k_14336x4096_b4": (DT.Q4_K, 14336, 4096, 4, ROTATE),
-            "q4k_14336x4096_b8": (DT.Q4_K, 14336, 4096, 8, ROTATE),
-            "q6k_128256x4096_b1": (DT.Q6_K, 128256, 4096, 1, 1),
-            "q6k_128256x4096_b8": (DT.Q6_K, 128256, 4096, 8, 1),
-            "q8_0_4864x896_b1": (DT.Q8_0, 4864, 896, 1, 64),
-            "q8_0_151936x896_b1": (DT.Q8_0, 151936, 896, 1, 3),
             "q5k_14336x4096_b1": (DT.Q5_K, 14336, 4096, 1, ROTATE),
             "q5k_14336x4096_b8": (DT.Q5_K, 14336, 4096, 8, ROTATE),
             "q3k_14336x4096_b1": (DT.Q3_K, 14336, 4096, 1, ROTATE),
