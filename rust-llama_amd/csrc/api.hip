@@ -98,10 +98,10 @@ struct rlq_context {
     hipStream_t stream = nullptr;
     unsigned long long* err_words = nullptr;  // [0] device API (sticky), [1] host API (per call)
     unsigned long long* host_err = nullptr;   // pinned readback
+    // keys: the decode launches' argmax state (kArgmaxStateBytes; its counter
+    // set to 0 when the buffer is made, and left at 0 by every launch), then
+    // the prefill path's per-column keys
     DevBuf planes, keys, stage_in, stage_w, stage_out, gate;
-    // leading argmax keys that are 0 in stream order: the last greedy-token
-    // kernel set its keys back to 0, so the next call clears only the rest
-    uint64_t keys_zero = 0;
 };
 
 struct rlq_weights {
@@ -204,8 +204,9 @@ rlq_context* g_default = nullptr;
 }  // namespace
 
 // ---- static scratch of rlq_matmul_noalloc ----------------------------------
-// Device memory that rlq_matmul_noalloc uses instead of allocating: the
-// argmax keys (8 bytes per column, padded to 256) and then the prefill
+// Device memory that rlq_matmul_noalloc uses instead of allocating: with an
+// argmax, the decode launches' argmax state (kArgmaxStateBytes) and, on the
+// prefill path, 8 bytes of keys per column (padded to 256); then the prefill
 // GEMM's activation image (gemm_planes_bytes).  Each device holds its own
 // copy for the life of the process.  Host code never passes the array's name
 // to a kernel (on the host it is only a handle): every use goes through the
@@ -574,28 +575,26 @@ static int32_t matmul_impl(rlq_context* ctx, const rlq_weights* w, const float* 
     if (batch == 0) return ok(err);
     DeviceGuard g(ctx->device);
     const hipStream_t s = pick(ctx, stream);
-    unsigned long long* keys = nullptr;
+    const bool gemm = w->dtype == kQ4_K && batch > kDecodeMaxBatch;
     if (argmax) {
         bool grown = false;
-        HIP_TRY(ensure(ctx, ctx->keys, batch * sizeof(unsigned long long), &grown));
-        if (grown) ctx->keys_zero = 0;  // a new buffer holds nothing known
-        keys = (unsigned long long*)ctx->keys.p;
-        if (ctx->keys_zero < batch)
-            HIP_TRY(launch_fill_u64(keys + ctx->keys_zero, batch - ctx->keys_zero, 0ull, s));
-        ctx->keys_zero = 0;  // the product below sets keys [0, batch)
+        HIP_TRY(ensure(ctx, ctx->keys, kArgmaxStateBytes + (gemm ? batch * sizeof(unsigned long long) : 0), &grown));
+        if (grown) HIP_TRY(launch_fill_u64((unsigned long long*)ctx->keys.p, 1, 0ull, s));  // the arrival counter
     }
-    if (w->dtype == kQ4_K && batch > kDecodeMaxBatch) {  // prefill: the MFMA GEMM
+    if (gemm) {  // prefill: the MFMA GEMM, then the argmax over the stored rows
         HIP_TRY(ensure(ctx, ctx->planes, gemm_planes_bytes(batch, w->cols)));
         HIP_TRY(launch_gemm_q4k(w->dev, w->rows, w->cols, x, batch, y, w->rows, ctx->planes.p, ctx->err_words, nullptr,
                                 nullptr, s));
-        if (keys) HIP_TRY(launch_argmax_rows(y, batch, w->rows, keys, s));
-    } else {
-        HIP_TRY(launch_matvec(w->dtype, w->dev, w->rows, w->cols, x, nullptr, batch, y, w->rows, keys, ctx->err_words,
-                              nullptr, nullptr, s));
-    }
-    if (argmax) {
-        HIP_TRY(launch_argmax_finish(keys, batch, y, w->rows, argmax, s, true));
-        ctx->keys_zero = batch;
+        if (argmax) {
+            unsigned long long* keys = (unsigned long long*)((uint8_t*)ctx->keys.p + kArgmaxStateBytes);
+            HIP_TRY(launch_fill_u64(keys, batch, 0ull, s));
+            HIP_TRY(launch_argmax_rows(y, batch, w->rows, keys, s));
+            HIP_TRY(launch_argmax_finish(keys, batch, y, w->rows, argmax, s));
+        }
+    } else {  // decode: the argmax is finished inside each launch
+        const MvArgmax am = argmax_state(ctx->keys.p, argmax);
+        HIP_TRY(launch_matvec(w->dtype, w->dev, w->rows, w->cols, x, nullptr, batch, y, w->rows,
+                              argmax ? &am : nullptr, ctx->err_words, nullptr, nullptr, s));
     }
     return ok(err);
 }
@@ -636,23 +635,29 @@ int32_t rlq_matmul_noalloc(rlq_context* ctx, const rlq_weights* w, const float* 
     if (batch == 0) return ok(err);
     if (batch > kScratchBytes) return fail(err, RLQ_SCRATCH_LIMIT, w->dtype, ~0ull, kScratchBytes);
     const bool gemm = w->dtype == kQ4_K && batch > kDecodeMaxBatch;
-    const uint64_t keys_bytes = argmax ? (batch * 8 + 255) / 256 * 256 : 0;
-    const uint64_t need = keys_bytes + (gemm ? gemm_planes_bytes(batch, w->cols) : 0);
+    const uint64_t state_bytes = argmax ? kArgmaxStateBytes : 0;
+    const uint64_t keys_bytes = argmax && gemm ? (batch * 8 + 255) / 256 * 256 : 0;
+    const uint64_t need = state_bytes + keys_bytes + (gemm ? gemm_planes_bytes(batch, w->cols) : 0);
     if (need > kScratchBytes) return fail(err, RLQ_SCRATCH_LIMIT, w->dtype, need, kScratchBytes);
     if (!ctx->scratch) return fail(err, RLQ_INVALID_ARGUMENT, w->dtype);
     DeviceGuard g(ctx->device);
     const hipStream_t s = pick(ctx, stream);
-    unsigned long long* keys = argmax ? (unsigned long long*)ctx->scratch : nullptr;
-    if (keys) HIP_TRY(launch_fill_u64(keys, batch, 0ull, s));
+    // the scratch keeps the last call's contents: what must start at 0 is cleared
+    if (argmax) HIP_TRY(launch_fill_u64((unsigned long long*)ctx->scratch, 1, 0ull, s));  // the arrival counter
     if (gemm) {
-        HIP_TRY(launch_gemm_q4k(w->dev, w->rows, w->cols, x, batch, y, w->rows, ctx->scratch + keys_bytes,
+        HIP_TRY(launch_gemm_q4k(w->dev, w->rows, w->cols, x, batch, y, w->rows, ctx->scratch + state_bytes + keys_bytes,
                                 ctx->err_words, nullptr, nullptr, s));
-        if (keys) HIP_TRY(launch_argmax_rows(y, batch, w->rows, keys, s));
+        if (argmax) {
+            unsigned long long* keys = (unsigned long long*)(ctx->scratch + state_bytes);
+            HIP_TRY(launch_fill_u64(keys, batch, 0ull, s));
+            HIP_TRY(launch_argmax_rows(y, batch, w->rows, keys, s));
+            HIP_TRY(launch_argmax_finish(keys, batch, y, w->rows, argmax, s));
+        }
     } else {
-        HIP_TRY(launch_matvec(w->dtype, w->dev, w->rows, w->cols, x, nullptr, batch, y, w->rows, keys, ctx->err_words,
-                              nullptr, nullptr, s));
+        const MvArgmax am = argmax_state(ctx->scratch, argmax);
+        HIP_TRY(launch_matvec(w->dtype, w->dev, w->rows, w->cols, x, nullptr, batch, y, w->rows,
+                              argmax ? &am : nullptr, ctx->err_words, nullptr, nullptr, s));
     }
-    if (keys) HIP_TRY(launch_argmax_finish(keys, batch, y, w->rows, argmax, s, true));
     return ok(err);
 }
 

@@ -477,7 +477,7 @@ LlamaModel::~LlamaModel() {
                         (void*)l.ffn_norm})
             if (p) (void)hipFree(p);
     for (void* p : {(void*)out_w, (void*)out_norm, (void*)emb, (void*)k_cache, (void*)v_cache, (void*)rope_tab,
-                    (void*)qkv, (void*)scores, (void*)att, (void*)mid, (void*)gu, (void*)argmax_keys,
+                    (void*)qkv, (void*)scores, (void*)att, (void*)mid, (void*)gu, am_state,
                     (void*)logits_buf, (void*)cmax})
         if (p) (void)hipFree(p);
 }
@@ -542,7 +542,8 @@ hipError_t LlamaModel::create(const LlamaDims& dims, const LlamaHostTensors& t, 
     if (e == hipSuccess) e = hipMalloc((void**)&att, W * sizeof(float));
     if (e == hipSuccess) e = hipMalloc((void**)&mid, W * sizeof(float));
     if (e == hipSuccess) e = hipMalloc((void**)&gu, 2 * F * sizeof(float));
-    if (e == hipSuccess) e = hipMalloc((void**)&argmax_keys, sizeof(unsigned long long));
+    if (e == hipSuccess) e = hipMalloc(&am_state, kArgmaxStateBytes);
+    if (e == hipSuccess) e = launch_fill_u64((unsigned long long*)am_state, 1, 0ull, s);  // the arrival counter
     if (e == hipSuccess) e = hipMalloc((void**)&logits_buf, d.vocab * sizeof(float));
     if (e != hipSuccess) return e;
     // staging for host GGUF bytes: the largest tensor; the gate/up stage of
@@ -730,22 +731,12 @@ hipError_t LlamaModel::step(float* hidden, uint64_t position, float* embedding_o
         // four, with layer = n_layers
         norm3.chk = mv_chk(kStAttnNormScale, kStAttnNormOut, kStQkvQuant, kStQkvOut, 0);
         norm3.chk_layer = (uint32_t)d.n_layers;
-        if (argmax) {  // the keys start at 0: left so by the last step's finish, or cleared here
-            if (!keys_zero) {
-                e = launch_fill_u64(argmax_keys, 1, 0ull, s);
-                if (e != hipSuccess) return e;
-            }
-            keys_zero = false;
-        }
         // logits land in the caller's buffer, or in the model's own when only
-        // the argmax is wanted
+        // the argmax is wanted; the greedy token is finished inside the launch
         float* y = logits ? logits : logits_buf;
-        e = launch_matvec_ex(d.output_type, out_w, d.vocab, W, hidden, nullptr, 1, y, d.vocab,
-                             argmax ? argmax_keys : nullptr, err_word, nullptr, nullptr, norm3, s);
-        if (e == hipSuccess && argmax) {
-            e = launch_argmax_finish(argmax_keys, 1, y, d.vocab, argmax, s, true);
-            keys_zero = e == hipSuccess;
-        }
+        const MvArgmax am = argmax_state(am_state, argmax);
+        e = launch_matvec_ex(d.output_type, out_w, d.vocab, W, hidden, nullptr, 1, y, d.vocab, argmax ? &am : nullptr,
+                             err_word, nullptr, nullptr, norm3, s);
         if (e != hipSuccess) return e;
     }
     ++n_cached;

@@ -80,10 +80,12 @@ __device__ __forceinline__ int32_t sbyte(uint32_t w, int k) { return __builtin_a
 
 // ---- greedy argmax key -------------------------------------------------------
 // Largest value wins, then the lowest row (sampling.rs:607-613 keeps the first
-// strict maximum).  -0.0 is folded onto +0.0 because they compare equal; NaN
-// maps to 0 and never wins (the finish step handles a NaN at row 0).
+// strict maximum).  -0.0 is folded onto +0.0 because they compare equal.  A
+// NaN never wins a strict `>` and maps to 0, except at row 0: the reference's
+// scan starts from row 0 and nothing compares greater than a NaN, so a NaN
+// there is the answer; its key is the largest (it decodes to row 0).
 __device__ __forceinline__ unsigned long long argmax_key(float v, uint64_t row) {
-    if (v != v) return 0ull;
+    if (v != v) return row == 0 ? ~0ull : 0ull;
     uint32_t b = __float_as_uint(v == 0.0f ? 0.0f : v);
     b = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
     return ((unsigned long long)b << 32) | (0xffffffffull - (row & 0xffffffffull));
@@ -112,7 +114,14 @@ struct MvArgs {
     ActPlanes pre;                    // pre-quantized activations when x is null
     float* y;                         // y[b * ldy + row]
     uint64_t ldy;
-    unsigned long long* argmax_key;   // [batch] or null
+    // Greedy argmax of every column (crates/llama-behavior/src/sampling.rs:
+    // 607-618), finished inside the launch (finish_argmax): am_slots
+    // [gridDim.x][batch] per-workgroup keys, am_count the launch's arrival
+    // counter (0 before and after every launch), am_out [batch] token ids; null
+    // am_out: no argmax
+    unsigned long long* am_slots;
+    unsigned int* am_count;
+    uint32_t* am_out;
     unsigned long long* err_word;
     uint32_t err_column0;             // column index of this launch's column 0
     int32_t* dbg_isum;                // [rows][nb] exact integers vs column 0, or null
@@ -219,7 +228,7 @@ __device__ __forceinline__ bool mv_enter(MvArgs& a) {
 // of the eight columns fall in distinct banks.  Lanes whose MFMA A operand is
 // all zero read the zero bytes instead of taking a branch.
 struct LdsMap {
-    uint32_t S, d_off, bs_off, zero_off, red_off, total;
+    uint32_t S, d_off, bs_off, zero_off, red_off, am_off, total;
 };
 
 __host__ __device__ inline LdsMap lds_map(uint32_t t, uint32_t cols, uint32_t batch) {
@@ -230,7 +239,8 @@ __host__ __device__ inline LdsMap lds_map(uint32_t t, uint32_t cols, uint32_t ba
     m.bs_off = m.d_off + nb * 32;
     m.zero_off = m.bs_off + (t == kQ4_K || t == kQ5_K || t == kQ2_K ? nb * 256 : 0);
     m.red_off = m.zero_off + 256;
-    m.total = m.red_off + 128;
+    m.am_off = m.red_off + 128;  // argmax: 8 u64 keys, then the last-workgroup flag
+    m.total = m.am_off + 80;
     return m;
 }
 
@@ -508,10 +518,59 @@ __device__ __forceinline__ void store_out(const MvArgs& a, uint32_t row, uint32_
     }
 }
 
-__device__ __forceinline__ void publish_argmax(const MvArgs& a, uint32_t b, unsigned long long best) {
-    if (!a.argmax_key) return;
+// The argmax keys of a workgroup: every lane's best key of column b folded
+// (max over its 16-lane row, then an LDS max) into the workgroup's key.
+__device__ __forceinline__ void fold_argmax(const MvArgs& a, uint8_t* lds, const LdsMap& L, uint32_t b,
+                                            unsigned long long best) {
+    if (!a.am_out) return;
     best = row16_max_u64(best);
-    if ((threadIdx.x & 15) == 0 && b < a.batch && best) atomicMax(a.argmax_key + b, best);
+    if ((threadIdx.x & 15) == 0 && b < a.batch && best) atomicMax((unsigned long long*)(lds + L.am_off) + b, best);
+}
+
+// The end of every decode kernel that takes an argmax (every thread of the
+// workgroup calls it, after its last fold).  Each workgroup writes its keys to
+// its own slot with agent-scope atomic exchanges, waits for them, and then
+// counts itself in; the last workgroup to arrive reads every slot, writes the
+// token ids and sets the counter back to 0.  All cross-workgroup data moves
+// through agent-scope atomics (coherent across the device's L2s), so no cache
+// write-back is needed.
+__device__ __forceinline__ void finish_argmax(const MvArgs& a, uint8_t* lds, const LdsMap& L) {
+    if (!a.am_out) return;
+    unsigned long long* keys = (unsigned long long*)(lds + L.am_off);
+    int* last = (int*)(keys + 8);
+    const uint32_t tid = threadIdx.x, nt = blockDim.x, G = gridDim.x;
+    __syncthreads();
+    if (tid < a.batch) {
+        const unsigned long long old = __hip_atomic_exchange(a.am_slots + (uint64_t)blockIdx.x * a.batch + tid,
+                                                             keys[tid], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __asm__ volatile("" : : "v"(old));  // the exchange has been performed before the count below
+    }
+    __syncthreads();
+    if (tid == 0)
+        *last = __hip_atomic_fetch_add(a.am_count, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == G - 1;
+    __syncthreads();
+    if (!*last) return;
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    for (uint32_t b = 0; b < a.batch; ++b) {
+        unsigned long long best = 0;
+        for (uint32_t w = tid; w < G; w += nt) {
+            const unsigned long long k =
+                __hip_atomic_load(a.am_slots + (uint64_t)w * a.batch + b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            best = k > best ? k : best;
+        }
+#pragma unroll
+        for (int m = 1; m < 64; m <<= 1) {
+            const unsigned long long o = __shfl_xor(best, m, 64);
+            best = o > best ? o : best;
+        }
+        if ((tid & 63) == 0 && best) atomicMax(keys + b, best);
+    }
+    __syncthreads();
+    if (tid < a.batch) {
+        const unsigned long long k = keys[tid];
+        a.am_out[tid] = k == 0 ? 0u : (uint32_t)(0xffffffffull - (k & 0xffffffffull));
+    }
+    if (tid == 0) __hip_atomic_store(a.am_count, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // MUL_MAT_ID slot with id -1 (cpu_index.rs:204), once the call is known to
@@ -625,6 +684,7 @@ __device__ __forceinline__ Q5High q5_high(uint4 qh, uint32_t kq) {
     const uint32_t nch = (CHUNKS);                                                                    \
     const uint32_t steps = gw < a.ntiles ? ((a.ntiles - 1 - gw) / tw + 1) * nch : 0;                  \
     if (threadIdx.x < 16) *(uint4*)(lds + L.zero_off + threadIdx.x * 16) = make_uint4(0, 0, 0, 0);   \
+    if (threadIdx.x < 8) ((unsigned long long*)(lds + L.am_off))[threadIdx.x] = 0ull;                 \
     float xv[16];                                                                                     \
     prefetch_unit(a, wave, xv);                                                                       \
     uint32_t ld_tile = gw < a.ntiles ? gw : a.ntiles - 1, ld_chunk = 0;                               \
@@ -726,7 +786,7 @@ __global__ __launch_bounds__(W * 64) void q4k_mv_kernel(MvArgs a) {
     for (int i = 0; i < D; ++i) issue(buf[i]);
 
     const bool ok = a.x ? stage_q8k<W, kBsQuarters>(a, lds, L, wave, xv) : stage_planes<W>(a, lds, L, T);
-    if (!ok) return;
+    if (!ok) return finish_argmax(a, lds, L);
     if (a.zero_pair) return zero_wave_tiles(a, gw, tw, n, kq);
 
     // A operand: lane row r = n holds column r / 2, sub-block parity r % 2; it
@@ -764,8 +824,9 @@ __global__ __launch_bounds__(W * 64) void q4k_mv_kernel(MvArgs a) {
         }
     };
     pipeline<D>(steps, buf, issue, compute);
-    publish_argmax(a, b0, best0);
-    publish_argmax(a, b0 + 1, best1);
+    fold_argmax(a, lds, L, b0, best0);
+    fold_argmax(a, lds, L, b0 + 1, best1);
+    finish_argmax(a, lds, L);
 }
 
 // Q4_K, one or two columns: v_dot4_i32_i8 on the VALU.
@@ -812,6 +873,7 @@ __global__ __launch_bounds__(W * 64) void q4k_mv_small_kernel(MvArgs a) {
     const uint32_t steps = my_tiles * bpt;
 
     if (threadIdx.x < 16) *(uint4*)(lds + L.zero_off + threadIdx.x * 16) = make_uint4(0, 0, 0, 0);
+    if (threadIdx.x < 8) ((unsigned long long*)(lds + L.am_off))[threadIdx.x] = 0ull;
     float xv[16];
     prefetch_unit(a, wave, xv);
 
@@ -831,7 +893,7 @@ __global__ __launch_bounds__(W * 64) void q4k_mv_small_kernel(MvArgs a) {
     for (int i = 0; i < D; ++i) issue(buf[i]);
 
     const bool ok = a.x ? stage_q8k<W, kBsQuarters>(a, lds, L, wave, xv) : stage_planes<W>(a, lds, L, T);
-    if (!ok) return;
+    if (!ok) return finish_argmax(a, lds, L);
     if (a.zero_pair) return zero_slot_tiles<W, TS>(a, tmax, tstride);
 
     const uint32_t g = kq >> 1, h = kq & 1;
@@ -954,15 +1016,16 @@ __global__ __launch_bounds__(W * 64) void q4k_mv_small_kernel(MvArgs a) {
                 store_out(a, row, b, v, best);
             }
         }
-        if (a.argmax_key) {
+        if (a.am_out) {
 #pragma unroll
             for (int m = 1; m < 64; m <<= 1) {
                 const unsigned long long o = __shfl_xor(best, m, 64);
                 best = o > best ? o : best;
             }
-            if (lane == 0 && best && (uint32_t)b < a.batch) atomicMax(a.argmax_key + b, best);
+            if (lane == 0 && best && (uint32_t)b < a.batch) atomicMax((unsigned long long*)(lds + L.am_off) + b, best);
         }
     }
+    finish_argmax(a, lds, L);
 }
 
 // ---------------------------------------------------------------------------
@@ -1002,7 +1065,7 @@ __global__ __launch_bounds__(W * 64) void q6k_mv_kernel(MvArgs a) {
     for (int i = 0; i < D; ++i) issue(buf[i]);
 
     const bool ok = a.x ? stage_q8k<W, kBsNone>(a, lds, L, wave, xv) : stage_planes<W>(a, lds, L, kQ6_K);
-    if (!ok) return;
+    if (!ok) return finish_argmax(a, lds, L);
     if (a.zero_pair) return zero_wave_tiles(a, gw, tw, n, kq);
 
     // This lane's weights: ql bytes 32kq.. (g = kq/2, s1 = kq%2) give the
@@ -1075,8 +1138,9 @@ __global__ __launch_bounds__(W * 64) void q6k_mv_kernel(MvArgs a) {
         }
     };
     pipeline<D>(steps, buf, issue, compute);
-    publish_argmax(a, kq, best0);
-    publish_argmax(a, kq + 4, best1);
+    fold_argmax(a, lds, L, kq, best0);
+    fold_argmax(a, lds, L, kq + 4, best1);
+    finish_argmax(a, lds, L);
 }
 
 // ---------------------------------------------------------------------------
@@ -1247,7 +1311,7 @@ __global__ __launch_bounds__(W * 64) void k16_mv_kernel(MvArgs a) {
     for (int i = 0; i < D; ++i) issue(buf[i]);
 
     const bool ok = a.x ? stage_q8k<W, bsum_order(T)>(a, lds, L, wave, xv) : stage_planes<W>(a, lds, L, T);
-    if (!ok) return;
+    if (!ok) return finish_argmax(a, lds, L);
     if (a.zero_pair) return zero_wave_tiles(a, gw, tw, n, kq);
 
     const K16A A = k16_a(lds, L, a.batch, n, kq);
@@ -1289,8 +1353,9 @@ __global__ __launch_bounds__(W * 64) void k16_mv_kernel(MvArgs a) {
         }
     };
     pipeline<D>(steps, buf, issue, compute);
-    publish_argmax(a, kq, best0);
-    publish_argmax(a, kq + 4, best1);
+    fold_argmax(a, lds, L, kq, best0);
+    fold_argmax(a, lds, L, kq + 4, best1);
+    finish_argmax(a, lds, L);
 }
 
 // K split over KS waves per tile (TS = W / KS tile slots per workgroup), for
@@ -1324,6 +1389,7 @@ __global__ __launch_bounds__(W * 64) void k16_mv_split_kernel(MvArgs a) {
     const uint32_t steps = my_tiles * bpt;
 
     if (threadIdx.x < 16) *(uint4*)(lds + L.zero_off + threadIdx.x * 16) = make_uint4(0, 0, 0, 0);
+    if (threadIdx.x < 8) ((unsigned long long*)(lds + L.am_off))[threadIdx.x] = 0ull;
     float xv[16];
     prefetch_unit(a, wave, xv);
 
@@ -1343,7 +1409,7 @@ __global__ __launch_bounds__(W * 64) void k16_mv_split_kernel(MvArgs a) {
     for (int i = 0; i < D; ++i) issue(buf[i]);
 
     const bool ok = a.x ? stage_q8k<W, bsum_order(T)>(a, lds, L, wave, xv) : stage_planes<W>(a, lds, L, T);
-    if (!ok) return;
+    if (!ok) return finish_argmax(a, lds, L);
     if (a.zero_pair) return zero_slot_tiles<W, TS>(a, tmax, tstride);
 
     const K16A A = k16_a(lds, L, batch, n, kq);
@@ -1399,15 +1465,16 @@ __global__ __launch_bounds__(W * 64) void k16_mv_split_kernel(MvArgs a) {
                 store_out(a, row, b, v, best);
             }
         }
-        if (a.argmax_key) {
+        if (a.am_out) {
 #pragma unroll
             for (int m = 1; m < 64; m <<= 1) {
                 const unsigned long long o = __shfl_xor(best, m, 64);
                 best = o > best ? o : best;
             }
-            if (lane == 0 && best) atomicMax(a.argmax_key + b, best);
+            if (lane == 0 && best) atomicMax((unsigned long long*)(lds + L.am_off) + b, best);
         }
     }
+    finish_argmax(a, lds, L);
 }
 
 // ---------------------------------------------------------------------------
@@ -1433,7 +1500,7 @@ __global__ __launch_bounds__(W * 64) void q8_0_mv_kernel(MvArgs a) {
     for (int i = 0; i < D; ++i) issue(buf[i]);
 
     const bool ok = a.x ? stage_q8_0<W>(a, lds, L, wave, xv) : stage_planes<W>(a, lds, L, kQ8_0);
-    if (!ok) return;
+    if (!ok) return finish_argmax(a, lds, L);
     if (a.zero_pair) return zero_wave_tiles(a, gw, tw, n, kq);
 
     // A operand: lane row r = n holds column r / 2 and block 2p + r % 2; it is
@@ -1483,8 +1550,9 @@ __global__ __launch_bounds__(W * 64) void q8_0_mv_kernel(MvArgs a) {
         }
     };
     pipeline<D>(steps, buf, issue, compute);
-    publish_argmax(a, b0, best0);
-    publish_argmax(a, b0 + 1, best1);
+    fold_argmax(a, lds, L, b0, best0);
+    fold_argmax(a, lds, L, b0 + 1, best1);
+    finish_argmax(a, lds, L);
 }
 #undef RLQ_MV_PROLOGUE
 
@@ -1527,6 +1595,7 @@ static hipError_t launch_one(K kernel, const MvArgs& a, size_t lds, hipStream_t 
     const uint32_t want = (a.ntiles + kMvWaves - 1) / kMvWaves;
     const uint32_t gy = grid_rows(a, pairs);
     const uint32_t grid = grid_cols(want, 2u * (uint32_t)device_cus(), gy);
+    if (a.am_out && grid > kArgmaxMaxGrid) return hipErrorInvalidValue;
     hipLaunchKernelGGL(kernel, dim3(grid, gy), dim3(kMvWaves * 64), lds, s, a);
     return hipGetLastError();
 }
@@ -1552,7 +1621,7 @@ static hipError_t launch_parked(void (*kernel)(MvArgs), size_t& lds_set, const M
     if (grid < need) grid = (uint32_t)need;
     const uint32_t tstride = grid * TS, tmax = (a.ntiles + tstride - 1) / tstride;
     const size_t lds = small_lds_bytes(a.cols, a.batch, tmax, TS, KS);
-    if (lds > kMaxLds) return hipErrorInvalidValue;
+    if (lds > kMaxLds || (a.am_out && grid > kArgmaxMaxGrid)) return hipErrorInvalidValue;
     if (lds > lds_set) {
         const hipError_t e = hipFuncSetAttribute((const void*)kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
                                                  (int)lds);
@@ -1611,6 +1680,7 @@ template <uint32_t T, bool DBG>
 static hipError_t launch_k16_split(const MvArgs& a, size_t lds, uint32_t grid, uint32_t gy, hipStream_t s) {
     static size_t lds_set = 64 * 1024;
     auto kernel = k16_mv_split_kernel<T, kK16W, kK16KS, kK16D, DBG>;
+    if (a.am_out && grid > kArgmaxMaxGrid) return hipErrorInvalidValue;
     if (lds > lds_set) {
         const hipError_t e = hipFuncSetAttribute((const void*)kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
                                                  (int)lds);
@@ -1636,17 +1706,16 @@ static hipError_t launch_k16(const MvArgs& a, bool dbg, size_t lds_plain, hipStr
 }
 
 hipError_t launch_matvec(uint32_t wtype, const uint8_t* w, uint64_t rows, uint64_t cols, const float* x,
-                         const ActPlanes* pre, uint64_t batch, float* y, uint64_t ldy,
-                         unsigned long long* argmax_key, unsigned long long* err_word, int32_t* dbg_isum,
-                         int32_t* dbg_imin, hipStream_t s) {
-    return launch_matvec_ex(wtype, w, rows, cols, x, pre, batch, y, ldy, argmax_key, err_word, dbg_isum, dbg_imin,
-                            MvExtra{}, s);
+                         const ActPlanes* pre, uint64_t batch, float* y, uint64_t ldy, const MvArgmax* am,
+                         unsigned long long* err_word, int32_t* dbg_isum, int32_t* dbg_imin, hipStream_t s) {
+    return launch_matvec_ex(wtype, w, rows, cols, x, pre, batch, y, ldy, am, err_word, dbg_isum, dbg_imin, MvExtra{},
+                            s);
 }
 
 hipError_t launch_matvec_ex(uint32_t wtype, const uint8_t* w, uint64_t rows, uint64_t cols, const float* x,
-                            const ActPlanes* pre, uint64_t batch, float* y, uint64_t ldy,
-                            unsigned long long* argmax_key, unsigned long long* err_word, int32_t* dbg_isum,
-                            int32_t* dbg_imin, const MvExtra& ex, hipStream_t s) {
+                            const ActPlanes* pre, uint64_t batch, float* y, uint64_t ldy, const MvArgmax* am,
+                            unsigned long long* err_word, int32_t* dbg_isum, int32_t* dbg_imin, const MvExtra& ex,
+                            hipStream_t s) {
     const uint32_t bs = wtype == kQ8_0 ? 32 : 256;
     if (rows == 0 || cols == 0 || cols % bs != 0 || rows > 0xffffffffull - kTileRows || cols > (1u << 30))
         return hipErrorInvalidValue;
@@ -1658,11 +1727,11 @@ hipError_t launch_matvec_ex(uint32_t wtype, const uint8_t* w, uint64_t rows, uin
     // the SiLU pair epilogue: one Q4_K / Q5_K column, whole tile pairs, no argmax or residual
     if (ex.epilogue != kEpStore &&
         (ex.epilogue != kEpSiluPair || batch != 1 || (wtype != kQ4_K && wtype != kQ5_K) ||
-         rows % (2 * kTileRows) != 0 || argmax_key || ex.resid))
+         rows % (2 * kTileRows) != 0 || am || ex.resid))
         return hipErrorInvalidValue;
     // expert pairs: one pre-quantized column each, plain stores; or, checked
     // in the kernel, one shared f32 column
-    if (ex.ids && (batch != 1 || argmax_key || dbg_isum || ex.resid || ex.xform != kXfNone ||
+    if (ex.ids && (batch != 1 || am || dbg_isum || ex.resid || ex.xform != kXfNone ||
                    ex.epilogue != kEpStore || ex.id_pairs == 0 || ex.id_pairs > 0xffffffffull || ex.id_slots == 0 ||
                    ex.id_cols == 0 || (ex.id_inline ? (!x || pre || ex.id_cols != 1 || ex.gate)
                                                      : (x || !pre))))
@@ -1690,7 +1759,9 @@ hipError_t launch_matvec_ex(uint32_t wtype, const uint8_t* w, uint64_t rows, uin
         }
         a.y = y + b0 * ldy;
         a.ldy = ldy;
-        a.argmax_key = argmax_key ? argmax_key + b0 : nullptr;
+        a.am_out = am ? am->out + b0 : nullptr;
+        a.am_slots = am ? am->slots : nullptr;
+        a.am_count = am ? am->count : nullptr;
         a.err_word = err_word;
         a.err_column0 = (uint32_t)(ex.column_base + b0);
         a.dbg_isum = b0 == 0 ? dbg_isum : nullptr;  // column 0 only

@@ -56,19 +56,33 @@ hipError_t launch_repack(uint32_t dtype, const uint8_t* gguf, uint64_t rows, uin
 hipError_t launch_fill_u64(unsigned long long* p, uint64_t n, unsigned long long v, hipStream_t s);
 
 // ---- matvec.hip ----
+// The greedy argmax of a decode launch, finished inside the launch (its last
+// workgroup decodes the token ids): per-workgroup key slots, the arrival
+// counter (0 between launches; set to 0 once when the state is allocated)
+// and the caller's token ids.
+struct MvArgmax {
+    unsigned long long* slots;  // [kArgmaxMaxGrid][8]
+    unsigned int* count;
+    uint32_t* out;              // [batch]
+};
+constexpr uint32_t kArgmaxMaxGrid = 4096;  // workgroups of one argmax launch
+constexpr size_t kArgmaxStateBytes = 256 + size_t(kArgmaxMaxGrid) * 8 * 8;
+inline MvArgmax argmax_state(void* base, uint32_t* out) {
+    return MvArgmax{(unsigned long long*)((uint8_t*)base + 256), (unsigned int*)base, out};
+}
+
 // y[b*ldy + r] = dot(row r, activation column b) for every b < batch, in
 // launches of up to 8 columns.  The activations are quantized in the kernel
 // prologue from f32 `x` ([batch][cols]) or taken from `pre` when x is null.
 // A data error in the activations goes to `err_word` (column index in the
 // key) and suppresses every output of the launch that found it.
-// `argmax_key` (may be null) receives per column the packed greedy-argmax key
-// (see matvec.hip).  With `dbg_isum`/`dbg_imin` (batch <= 8) the kernel that
+// `am` (may be null) receives the greedy argmax of every column in am->out.
+// With `dbg_isum`/`dbg_imin` (batch <= 8) the kernel that
 // serves this batch size also stores the exact per-(row, block) integers of
 // column 0's dot.
 hipError_t launch_matvec(uint32_t wtype, const uint8_t* w, uint64_t rows, uint64_t cols, const float* x,
-                         const ActPlanes* pre, uint64_t batch, float* y, uint64_t ldy,
-                         unsigned long long* argmax_key, unsigned long long* err_word, int32_t* dbg_isum,
-                         int32_t* dbg_imin, hipStream_t s);
+                         const ActPlanes* pre, uint64_t batch, float* y, uint64_t ldy, const MvArgmax* am,
+                         unsigned long long* err_word, int32_t* dbg_isum, int32_t* dbg_imin, hipStream_t s);
 // Decode-step options of a matvec launch (batch 1 for a transform):
 //   xform   0: quantize x as given; 1: RMSNorm(x) * norm_w with `eps`
 //           (crates/model-runtime/src/math.rs:214-228); 2: x holds
@@ -112,9 +126,9 @@ constexpr uint32_t mv_chk(uint32_t scale, uint32_t in, uint32_t quant, uint32_t 
 hipError_t launch_mm_prepare(const int32_t* ids, uint64_t pairs, uint32_t experts, const uint8_t* bad, uint64_t nbad,
                              float* y, uint64_t rows, uint32_t* gate, unsigned long long* err_word, hipStream_t s);
 hipError_t launch_matvec_ex(uint32_t wtype, const uint8_t* w, uint64_t rows, uint64_t cols, const float* x,
-                            const ActPlanes* pre, uint64_t batch, float* y, uint64_t ldy,
-                            unsigned long long* argmax_key, unsigned long long* err_word, int32_t* dbg_isum,
-                            int32_t* dbg_imin, const MvExtra& ex, hipStream_t s);
+                            const ActPlanes* pre, uint64_t batch, float* y, uint64_t ldy, const MvArgmax* am,
+                            unsigned long long* err_word, int32_t* dbg_isum, int32_t* dbg_imin, const MvExtra& ex,
+                            hipStream_t s);
 // ---- gemm.hip ----
 // Prefill GEMM for Q4_K weights: y[m*ldy + r] = dot(row r, token m) for
 // m < M (M > 8 in practice).  Quantizes x [M][cols] to Q8_K (as the f16
@@ -181,8 +195,7 @@ struct LlamaModel {
         return 4 * d.width + 2 * kvw + d.feed_forward;
     }
     float* cmax = nullptr;  // [heads][chunks of 16 tokens] chunk maxima of the scores
-    unsigned long long* argmax_keys = nullptr;
-    bool keys_zero = false;  // argmax_keys is 0 in stream order (the last step's finish reset it)
+    void* am_state = nullptr;  // the output matvec's argmax state (kArgmaxStateBytes)
     bool repeat_all = false;  // attention sums always repeated in the reference's order
     uint64_t n_cached = 0;  // KV rows held (the insertion index of the next step)
 

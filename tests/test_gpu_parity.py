@@ -330,6 +330,34 @@ def test_argmax_keys_across_calls(ctx):
             assert int(am[b]) == O.argmax(got[b]), (batch, b)
 
 
+@pytest.mark.parametrize("t,rows,cols", [(DT.Q8_0, 9000, 896), (DT.Q6_K, 3000, 2048), (DT.Q4_K, 5000, 4096)])
+def test_argmax_nan_rows(ctx, t, rows, cols):
+    """The greedy scan (sampling.rs:607-618) starts from row 0 and keeps the
+    first strict maximum: a NaN at row 0 is the answer (nothing compares
+    greater), a NaN anywhere else never wins.  NaN logits come from a NaN f16
+    scale in one row's first block.  Batches 1 and 3, over the in-launch
+    argmax of the decode kernels."""
+    say("argmax with NaN logits", t, rows, cols)
+    w = _weights(t, rows, cols, 88)
+    rb = w.size // rows
+    dpos = {DT.Q8_0: 0, DT.Q6_K: 208, DT.Q4_K: 0}[t]  # the f16 d of block 0
+    for nan_row in (0, 1234):
+        wn = w.copy()
+        wn[nan_row * rb + dpos:nan_row * rb + dpos + 2] = np.array([0x7E00], np.uint16).view(np.uint8)
+        W = rlq.Weights(ctx, t, wn, rows, cols)
+        for batch in (1, 3):
+            x = torch.from_numpy(randn(90 + batch, batch * cols).reshape(batch, cols)).cuda()
+            y, am = ctx.matmul_argmax(W, x)
+            ctx.sync()
+            got = y.cpu().numpy()
+            for b in range(batch):
+                assert np.isnan(got[b][nan_row]), (nan_row, b)
+                assert int(am[b]) == O.argmax(got[b]), (nan_row, b)
+                if nan_row == 0:
+                    assert int(am[b]) == 0
+        W.close()
+
+
 # ------------------------------------------------------------ errors and edges
 
 def test_host_errors_leave_output_untouched():
