@@ -1028,6 +1028,194 @@ __global__ __launch_bounds__(W * 64) void q4k_mv_small_kernel(MvArgs a) {
     finish_argmax(a, lds, L);
 }
 
+// Batch-1 Q4_K/Q5_K kernel for a plain f32 column (no ids, no gate, no
+// input transform, no residual).  Each wave quantizes only the blocks it
+// multiplies (blocks kp, kp + KS, ... of every tile it takes) while its first
+// weight chunks are in flight, so a workgroup's Q8_K image costs one barrier
+// and no shared quantization pass.  A tile's K parts are parked in LDS and
+// counted with a workgroup-scope atomic; the wave that brings the count to
+// the tile's part count adds the parts in K order and stores the row
+// (no barrier between tiles).
+__host__ __device__ inline uint32_t b1_lds_bytes(uint32_t cols, uint32_t tmax, uint32_t ts, uint32_t ks) {
+    return small_part_off(cols, 1) + tmax * ts * ks * 16u * 4u + tmax * ts * 4u;
+}
+
+// FULL: the output checks of a model stage (chk) and the in-launch argmax;
+// without them neither is compiled in.
+template <uint32_t T, int W, int KS, int D, bool DBG, bool FULL>
+__global__ __launch_bounds__(W * 64) void q45_mv_b1_kernel(MvArgs a) {
+    constexpr int TS = W / KS;
+    extern __shared__ __align__(16) uint8_t lds[];
+    const LdsMap L = lds_map(T, a.cols, 1);
+    float* part = (float*)(lds + small_part_off(a.cols, 1));
+    const uint32_t lane = threadIdx.x & 63, n = lane & 15, kq = lane >> 4;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t ts = wave / KS, kp = wave % KS;
+    const uint32_t nb = a.nb, ntiles = a.ntiles;
+    const uint32_t tstride = gridDim.x * TS, t0 = blockIdx.x * TS + ts;
+    const uint32_t tmax = (ntiles + tstride - 1) / tstride;
+    const uint32_t my_tiles = t0 < ntiles ? (ntiles - 1 - t0) / tstride + 1 : 0;
+    const uint32_t bpt = kp < nb ? (nb - 1 - kp) / KS + 1 : 0;  // blocks of each tile this wave takes
+    const uint32_t steps = my_tiles * bpt;
+    const uint32_t nk = (uint32_t)KS < nb ? (uint32_t)KS : nb;  // waves of a tile that take blocks
+    uint32_t* cnt = (uint32_t*)(part + tmax * TS * KS * 16);
+    for (uint32_t i = threadIdx.x; i < tmax * TS; i += W * 64) cnt[i] = 0;
+    if (FULL && threadIdx.x < 8) ((unsigned long long*)(lds + L.am_off))[threadIdx.x] = 0ull;
+
+    // the first own block of each 16-lane row, loaded before the weights (the
+    // waves of tile slot 0 cover every block)
+    const uint32_t r16 = lane & 15;
+    float xv[16];
+    if (ts == 0 && kq < bpt) load16(a.x + (kp + KS * kq) * 256 + r16 * 16, xv);
+    const uint32_t kp0 = kp < nb ? kp : nb - 1;
+    uint32_t ld_tile = t0 < ntiles ? t0 : ntiles - 1, ld_blk = kp0;
+    Q4Step<T> buf[D];
+    auto issue = [&](Q4Step<T>& st) {
+        q45_issue<T>(st, a.w + ((uint64_t)ld_tile * nb + ld_blk) * Q45<T>::chunk, lane, n, kq);
+        ld_blk += KS;
+        if (ld_blk >= nb) {
+            ld_blk = kp0;
+            if (ld_tile + tstride < ntiles) ld_tile += tstride;
+        }
+    };
+#pragma unroll
+    for (int i = 0; i < D; ++i) issue(buf[i]);
+
+    // Q8_K of the own blocks (quantize_row_q8_K, 16 lanes per block; at
+    // most four blocks per wave, so every input load precedes the weights')
+    int bad = 0;
+    if (ts == 0 && kq < bpt) {
+        const uint32_t blk = kp + KS * kq;
+        const Q8KRow o = q8k_row16(xv, r16);
+        if (o.kind >= 0) {
+            bad = 1;
+            if (r16 == 0)
+                report_error(a.err_word, o.kind == kKindNonFinite ? quant_nonfinite_key(a, 0, blk * 256ull + o.index)
+                                                                  : quant_scale_key(a, 0, blk));
+        }
+        *(uint4*)(lds + blk * 256 + r16 * 16) = make_uint4(o.q[0], o.q[1], o.q[2], o.q[3]);
+        if (r16 == 0) *(float*)(lds + L.d_off + blk * 32) = o.d;
+        *(int16_t*)(lds + L.bs_off + blk * 256 + bs_slot(r16) * 2) = (int16_t)o.bsum;
+    }
+    // the counters' zeros, every own block and every wave's error flag
+    if (__syncthreads_or(bad)) {
+        if (FULL) finish_argmax(a, lds, L);
+        return;
+    }
+
+    const uint32_t g = kq >> 1, h = kq & 1;
+    // activation of (sub-block 2g, half h) and its neighbours: +32 (2g+1),
+    // +128 (2g+4), +160 (2g+5)
+    const uint8_t* a_row = lds + 64 * g + 16 * h;
+    const uint8_t* bs_row = lds + L.bs_off + kq * 8;
+    // bytes 2g and 2g + 1 of a packed scale word, widened to two i16 lanes
+    const uint32_t psel = (2 * g) | 0x0c00u | (2 * g + 1) << 16 | 0x0c000000u;
+    typedef short s2 __attribute__((ext_vector_type(2)));
+    unsigned long long best = 0;
+    float acc = 0.0f;
+    uint32_t ti = 0, blk = kp, j = 0, tile = t0;
+    auto compute = [&](const Q4Step<T>& cur) {
+        const Q4Scales q = q4k_scales(cur.h);
+        uint32_t l0[4] = {cur.w0.x & 0x0f0f0f0fu, cur.w0.y & 0x0f0f0f0fu, cur.w0.z & 0x0f0f0f0fu,
+                          cur.w0.w & 0x0f0f0f0fu};
+        uint32_t h0[4], h1[4];
+        hi_nibbles64(cur.w0, h0);
+        uint32_t l1[4] = {cur.w1.x & 0x0f0f0f0fu, cur.w1.y & 0x0f0f0f0fu, cur.w1.z & 0x0f0f0f0fu,
+                          cur.w1.w & 0x0f0f0f0fu};
+        hi_nibbles64(cur.w1, h1);
+        if constexpr (T == kQ5_K) {
+            const Q5High hb = q5_high(cur.qh, kq);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                l0[i] |= hb.l0[i];
+                h0[i] |= hb.h0[i];
+                l1[i] |= hb.l1[i];
+                h1[i] |= hb.h1[i];
+            }
+        }
+        const float dw = half_to_float(cur.h.x), dmw = half_to_float(cur.h.x >> 16);
+        const uint8_t* p = a_row + blk * 256;
+        const uint4 x0 = *(const uint4*)(p), x1 = *(const uint4*)(p + 32);
+        const uint4 x4 = *(const uint4*)(p + 128), x5 = *(const uint4*)(p + 160);
+        const int32_t i0 = dot4(l0[3], x0.w, dot4(l0[2], x0.z, dot4(l0[1], x0.y, dot4(l0[0], x0.x, 0))));
+        const int32_t i1 = dot4(h0[3], x1.w, dot4(h0[2], x1.z, dot4(h0[1], x1.y, dot4(h0[0], x1.x, 0))));
+        const int32_t i4 = dot4(l1[3], x4.w, dot4(l1[2], x4.z, dot4(l1[1], x4.y, dot4(l1[0], x4.x, 0))));
+        const int32_t i5 = dot4(h1[3], x5.w, dot4(h1[2], x5.z, dot4(h1[1], x5.y, dot4(h1[0], x5.x, 0))));
+        // this quarter's sub-blocks 2g, 2g+1, 2g+4, 2g+5: scales and mins
+        // (6-bit) and bsums (|b| <= 16 * 128) fit i16, and so do the Q4_K
+        // sub-block sums (|i| <= 15 * 128 * 16): two dot2 per sum (Q5_K sums
+        // reach 31 * 128 * 16 and take the 24-bit multiplies)
+        const uint2 bw = *(const uint2*)(bs_row + blk * 256);
+        const uint32_t S01 = __builtin_amdgcn_perm(0u, q.scA, psel), S45 = __builtin_amdgcn_perm(0u, q.scB, psel);
+        const uint32_t M01 = __builtin_amdgcn_perm(0u, q.mnA, psel), M45 = __builtin_amdgcn_perm(0u, q.mnB, psel);
+        int32_t I;
+        if constexpr (T == kQ5_K) {
+            I = mad24(S01 & 0xffff, i0, mad24(S01 >> 16, i1, mad24(S45 & 0xffff, i4, __mul24(S45 >> 16, i5))));
+        } else {
+            const uint32_t P01 = __builtin_amdgcn_perm((uint32_t)i1, (uint32_t)i0, 0x05040100u);
+            const uint32_t P45 = __builtin_amdgcn_perm((uint32_t)i5, (uint32_t)i4, 0x05040100u);
+            I = __builtin_amdgcn_sdot2(__builtin_bit_cast(s2, S01), __builtin_bit_cast(s2, P01),
+                                       __builtin_amdgcn_sdot2(__builtin_bit_cast(s2, S45), __builtin_bit_cast(s2, P45),
+                                                              0, false),
+                                       false);
+        }
+        int32_t M = __builtin_amdgcn_sdot2(__builtin_bit_cast(s2, M01), __builtin_bit_cast(s2, bw.x),
+                                           __builtin_amdgcn_sdot2(__builtin_bit_cast(s2, M45),
+                                                                  __builtin_bit_cast(s2, bw.y), 0, false),
+                                           false);
+        const float da = *(const float*)(lds + L.d_off + blk * 32);
+        acc += (dw * da) * (float)I - (dmw * da) * (float)M;
+        if (DBG) {  // exact block integers: add the four quarters
+            I += __shfl_xor(I, 16, 64);
+            I += __shfl_xor(I, 32, 64);
+            M += __shfl_xor(M, 16, 64);
+            M += __shfl_xor(M, 32, 64);
+            const uint32_t row = tile * kTileRows + n;
+            if (kq == 0 && row < a.rows) {
+                a.dbg_isum[(uint64_t)row * nb + blk] = I;
+                a.dbg_imin[(uint64_t)row * nb + blk] = M;
+            }
+        }
+        blk += KS;
+        if (++j == bpt) {  // this wave's share of the tile is done: park the row sums
+            float v = acc;
+            v += __shfl_xor(v, 16, 64);
+            v += __shfl_xor(v, 32, 64);
+            const uint32_t slot = ti * TS + ts;
+            if (kq == 0) part[(slot * KS + kp) * 16 + n] = v;
+            // one wave's LDS operations are performed in order: the partial
+            // is in place before the count
+            uint32_t prev = 0;
+            if (lane == 0)
+                prev = __hip_atomic_fetch_add(cnt + slot, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_WORKGROUP);
+            prev = __shfl(prev, 0, 64);
+            const uint32_t row = tile * kTileRows + n;
+            if (prev == nk - 1 && kq == 0 && row < a.rows) {  // the last part: add them in K order
+                float s = 0.0f;
+#pragma unroll
+                for (int k = 0; k < KS; ++k)
+                    if ((uint32_t)k < nk) s += part[(slot * KS + k) * 16 + n];
+                if (FULL && a.chk) check_finite(a, kChkOut, s);
+                a.y[row] = s;
+                if (FULL) {
+                    const unsigned long long key = argmax_key(s, row);
+                    best = key > best ? key : best;
+                }
+            }
+            acc = 0.0f;
+            j = 0;
+            blk = kp;
+            ++ti;
+            tile += tstride;
+        }
+    };
+    pipeline<D>(steps, buf, issue, compute);
+    if (FULL) {
+        fold_argmax(a, lds, L, kq, best);
+        finish_argmax(a, lds, L);
+    }
+}
+
 // ---------------------------------------------------------------------------
 // Q6_K
 // ---------------------------------------------------------------------------
@@ -1638,6 +1826,31 @@ static hipError_t launch_small(const MvArgs& a, hipStream_t s, uint32_t pairs) {
     return launch_parked<W, KS>(q4k_mv_small_kernel<T, W, KS, D, B, DBG>, lds_set, a, s, pairs);
 }
 
+// The batch-1 kernel for a plain column: grid and LDS as launch_parked, plus
+// one arrival counter per (tile, slot).
+template <uint32_t T, int W, int KS, int D, bool DBG, bool FULL>
+static hipError_t launch_b1(const MvArgs& a, hipStream_t s) {
+    constexpr int TS = W / KS;
+    static size_t lds_set = 64 * 1024;
+    auto kernel = q45_mv_b1_kernel<T, W, KS, D, DBG, FULL>;
+    uint32_t grid = grid_cols((a.ntiles + TS - 1) / TS, (uint32_t)kSmallWgPerCu * (uint32_t)device_cus(), 1);
+    const size_t off = small_part_off(a.cols, 1), per_tile = (size_t)TS * KS * 16u * 4u + TS * 4u;
+    if (off >= kMaxLds || (kMaxLds - off) / per_tile == 0) return hipErrorInvalidValue;
+    const uint64_t room = (kMaxLds - off) / per_tile, need = (a.ntiles + room * TS - 1) / (room * TS);
+    if (grid < need) grid = (uint32_t)need;
+    const uint32_t tstride = grid * TS, tmax = (a.ntiles + tstride - 1) / tstride;
+    const size_t lds = b1_lds_bytes(a.cols, tmax, TS, KS);
+    if (lds > kMaxLds || (a.am_out && grid > kArgmaxMaxGrid)) return hipErrorInvalidValue;
+    if (lds > lds_set) {
+        const hipError_t e = hipFuncSetAttribute((const void*)kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                 (int)lds);
+        if (e != hipSuccess) return e;
+        lds_set = lds;
+    }
+    hipLaunchKernelGGL(kernel, dim3(grid), dim3(W * 64), lds, s, a);
+    return hipGetLastError();
+}
+
 // Q4_K / Q5_K: the VALU kernel for one or two columns, MFMA above.
 template <uint32_t T>
 static hipError_t launch_q45(const MvArgs& a, uint32_t nbat, bool dbg, uint32_t epilogue, size_t lds, hipStream_t s,
@@ -1650,6 +1863,28 @@ static hipError_t launch_q45(const MvArgs& a, uint32_t nbat, bool dbg, uint32_t 
     if (epilogue == kEpSiluPair)
         return dbg ? launch_small<T, kSmallW, kSmallW / 4, kSmallD, 1, true>(a, s, pairs)
                    : launch_small<T, kSmallW, kSmallW / 4, kSmallD, 1, false>(a, s, pairs);
+    // one plain f32 column: the batch-1 kernel, whose waves take at most 4
+    // blocks of a tile (measured, Q4_K, us against the shared-quantization
+    // kernel: 14336x4096 8.3 / 9.2 with two tile slots of a K split of 4;
+    // 6144x4096 5.5 / 6.6 likewise; 4096x4096 5.2 / 6.2 with one slot of a
+    // split of 4; 4096x14336 9.6 / 10.6 with a split of 16)
+    if (nbat == 1 && a.x && a.xform == kXfNone && !a.ids && !a.gate && !a.resid && a.nb <= 64) {
+        const bool full = a.chk || a.am_out;
+        if (a.nb > 16)
+            return dbg ? (full ? launch_b1<T, 16, 16, kSmallD, true, true>(a, s)
+                               : launch_b1<T, 16, 16, kSmallD, true, false>(a, s))
+                       : (full ? launch_b1<T, 16, 16, kSmallD, false, true>(a, s)
+                               : launch_b1<T, 16, 16, kSmallD, false, false>(a, s));
+        if (a.ntiles >= 384)
+            return dbg ? (full ? launch_b1<T, 8, 4, kSmallD, true, true>(a, s)
+                               : launch_b1<T, 8, 4, kSmallD, true, false>(a, s))
+                       : (full ? launch_b1<T, 8, 4, kSmallD, false, true>(a, s)
+                               : launch_b1<T, 8, 4, kSmallD, false, false>(a, s));
+        return dbg ? (full ? launch_b1<T, 4, 4, kSmallD, true, true>(a, s)
+                           : launch_b1<T, 4, 4, kSmallD, true, false>(a, s))
+                   : (full ? launch_b1<T, 4, 4, kSmallD, false, true>(a, s)
+                           : launch_b1<T, 4, 4, kSmallD, false, false>(a, s));
+    }
     // two tile slots per workgroup (a K split of four): small matrices of at
     // most 4096 columns and 512 tiles (measured: 6144x4096 runs 1 us faster)
     if (nbat == 1 && a.nb <= 16 && a.ntiles <= 512)

@@ -163,12 +163,14 @@ def _oracle_sums(t, w, rows, act, nb):
 
 
 @pytest.mark.parametrize("t,rows,cols,variant", [
-    (DT.Q4_K, 4096, 4096, "two tile slots, K split 4 (<= 512 tiles): the O projection"),
-    (DT.Q4_K, 6144, 4096, "two tile slots, K split 4: the fused Q/K/V projection"),
-    (DT.Q4_K, 14336, 4096, "one tile slot, K split 8 (> 512 tiles): the headline matvec"),
-    (DT.Q4_K, 4096, 14336, "16 waves, K split 16 (> 16 blocks): the down projection"),
-    (DT.Q5_K, 4096, 4096, "Q5_K, K split 4"),
-    (DT.Q5_K, 4096, 14336, "Q5_K, 16 waves, K split 16")])
+    (DT.Q4_K, 4096, 4096, "batch-1 kernel, one tile slot, K split 4 (< 384 tiles)"),
+    (DT.Q4_K, 6144, 4096, "batch-1 kernel, two tile slots, K split 4 (>= 384 tiles)"),
+    (DT.Q4_K, 14336, 4096, "batch-1 kernel, two tile slots, K split 4: the headline matvec"),
+    (DT.Q4_K, 4096, 14336, "batch-1 kernel, 16 waves, K split 16 (> 16 blocks)"),
+    (DT.Q4_K, 333, 16384, "batch-1 kernel, K split 16 at 64 blocks: 4 blocks per wave, the most it takes"),
+    (DT.Q4_K, 333, 18432, "72 blocks: the shared-quantization kernel, 16 waves, K split 16"),
+    (DT.Q5_K, 4096, 4096, "Q5_K, batch-1 kernel, K split 4"),
+    (DT.Q5_K, 4096, 14336, "Q5_K, batch-1 kernel, K split 16")])
 def test_block_sums_every_decode_variant(ctx, t, rows, cols, variant):
     """rlq_block_sums runs the very kernel variant rlq_matmul picks for a
     shape (the batch-1 variants are chosen by tile and block counts): the
@@ -330,7 +332,8 @@ def test_argmax_keys_across_calls(ctx):
             assert int(am[b]) == O.argmax(got[b]), (batch, b)
 
 
-@pytest.mark.parametrize("t,rows,cols", [(DT.Q8_0, 9000, 896), (DT.Q6_K, 3000, 2048), (DT.Q4_K, 5000, 4096)])
+@pytest.mark.parametrize("t,rows,cols", [(DT.Q8_0, 9000, 896), (DT.Q6_K, 3000, 2048), (DT.Q4_K, 5000, 4096),
+                                         (DT.Q4_K, 9000, 2048)])
 def test_argmax_nan_rows(ctx, t, rows, cols):
     """The greedy scan (sampling.rs:607-618) starts from row 0 and keeps the
     first strict maximum: a NaN at row 0 is the answer (nothing compares
@@ -415,17 +418,48 @@ def test_device_errors_suppress_outputs_and_report_first_column(ctx):
     assert bool((y[:2] == 0).all())
 
 
+def test_device_errors_of_the_batch1_plain_kernel(ctx):
+    """One f32 column over 513 tiles (the batch-1 kernel whose workgroups
+    each quantize their own blocks): the first error is reported and no
+    output is written; a clean call afterwards is exact."""
+    rows, cols = 8208, 1024
+    say("device errors, batch-1 kernel", rows, cols)
+    w = _weights(DT.Q4_K, rows, cols, 5)
+    W = rlq.Weights(ctx, DT.Q4_K, w, rows, cols)
+    y = torch.full((1, rows), 123.0, device="cuda")
+    x = torch.from_numpy(randn(6, cols)).cuda()
+    bad = x.clone()
+    bad[900] = float("nan")
+    bad[300] = float("inf")
+    ctx.matmul(W, bad.view(1, cols), y)
+    with pytest.raises(rlq.QuantError) as e:
+        ctx.sync()
+    assert (e.value.name, e.value.index) == ("NonFiniteInput", 300)
+    assert bool((y == 123.0).all())
+    tiny = x.clone()
+    tiny[768:] = 1e-45
+    ctx.matmul(W, tiny.view(1, cols), y)
+    with pytest.raises(rlq.QuantError) as e:
+        ctx.sync()
+    assert (e.value.name, e.value.block) == ("UnrepresentableScale", 3)
+    assert bool((y == 123.0).all())
+    ctx.matmul(W, x.view(1, cols), y)
+    ctx.sync()
+    assert rel_l2(y.cpu().numpy()[0], O.matvec(O.Q4_K, w, rows, cols, x.cpu().numpy(), threads=16)) <= REL_L2
+
+
 from test_oracle_llama import huge_q4k  # noqa: E402
 
 
-def test_multiply_finite_checks(ctx):
+@pytest.mark.parametrize("rows", [64, 8208])
+def test_multiply_finite_checks(ctx, rows):
     """Matrix::multiply (math.rs:144-169): finite(input) as NonFinite
     "matrix input" before anything is written, the quantizer's
     UnrepresentableScale, and finite(output) as NonFinite "matrix output"
     (an f32 overflow forced by extreme weights and input; the oracle's own
     product overflows the same way); a finite product equals rlq_matmul's
-    bitwise."""
-    rows, cols = 64, 1024
+    bitwise.  8208 rows (513 tiles) run the batch-1 plain-column kernel."""
+    cols = 1024
     say("Matrix::multiply finite checks", rows, cols)
     W = rlq.Weights(ctx, DT.Q4_K, _weights(DT.Q4_K, rows, cols, 12), rows, cols)
     x = torch.from_numpy(randn(13, cols)).cuda()
