@@ -1028,20 +1028,59 @@ __global__ __launch_bounds__(W * 64) void q4k_mv_small_kernel(MvArgs a) {
     finish_argmax(a, lds, L);
 }
 
-// Batch-1 Q4_K/Q5_K kernel for a plain f32 column (no ids, no gate, no
-// input transform, no residual).  Each wave quantizes only the blocks it
-// multiplies (blocks kp, kp + KS, ... of every tile it takes) while its first
-// weight chunks are in flight, so a workgroup's Q8_K image costs one barrier
+// Batch-1 Q4_K/Q5_K kernel for one f32 column (no ids, no gate).  Each wave
+// quantizes only the blocks it multiplies (blocks kp, kp + KS, ... of every
+// tile it takes, at most four) while its first weight chunks are in flight, so
+// a workgroup's Q8_K image costs one barrier (two with the RMSNorm transform)
 // and no shared quantization pass.  A tile's K parts are parked in LDS and
 // counted with a workgroup-scope atomic; the wave that brings the count to
-// the tile's part count adds the parts in K order and stores the row
-// (no barrier between tiles).
+// the tile's part count adds the parts in K order and stores the row (no
+// barrier between tiles).  LDS after the Q8_K image: partials
+// [tmax][TS][KS][16], counters [tmax][TS], residuals [tmax][TS][16].
 __host__ __device__ inline uint32_t b1_lds_bytes(uint32_t cols, uint32_t tmax, uint32_t ts, uint32_t ks) {
-    return small_part_off(cols, 1) + tmax * ts * ks * 16u * 4u + tmax * ts * 4u;
+    return small_part_off(cols, 1) + tmax * ts * ks * 16u * 4u + tmax * ts * 4u + tmax * ts * 16u * 4u;
 }
 
-// FULL: the output checks of a model stage (chk) and the in-launch argmax;
-// without them neither is compiled in.
+// The RMSNorm scale (math.rs:210-221) from the values of the workgroup's own
+// blocks: every element of the column is held by exactly one lane (the waves
+// of tile slot 0 cover every block), its square is added in f64 by that lane,
+// the lane sums meet in LDS and every thread adds the wave sums in wave
+// order.  The certificate of rms_scale decides whether that sum fixes the
+// reference's f32 mean; otherwise thread 0 repeats the sum in the reference's
+// order.  Every workgroup computes the same value.
+template <int W>
+__device__ __forceinline__ float b1_rms_scale(const MvArgs& a, uint8_t* lds, const LdsMap& L, uint32_t wave,
+                                              bool mine, const float (&v)[16]) {
+    double ss = 0.0;
+    if (mine) {
+#pragma unroll
+        for (int k = 0; k < 16; ++k) ss += (double)(v[k] * v[k]);
+    }
+#pragma unroll
+    for (int m = 1; m < 64; m <<= 1) ss += __shfl_xor(ss, m, 64);
+    double* red = (double*)(lds + L.red_off);
+    if ((threadIdx.x & 63) == 0) red[wave] = ss;
+    __syncthreads();
+    double total = 0.0;
+#pragma unroll
+    for (int w = 0; w < W; ++w) total += red[w];
+    const double n = (double)a.cols, err = n * 2.3e-16 * total;
+    if ((float)((total - err) / n) != (float)((total + err) / n)) {  // every thread takes the same branch
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            double seq = 0.0;
+            for (uint32_t i = 0; i < a.cols; ++i) seq += (double)(a.x[i] * a.x[i]);
+            red[0] = seq;
+        }
+        __syncthreads();
+        total = red[0];
+    }
+    return 1.0f / sqrtf((float)(total / n) + a.eps);
+}
+
+// FULL: the decode step's extras (the RMSNorm input transform, the residual
+// add), the output checks of a model stage (chk) and the in-launch argmax;
+// without them none is compiled in.
 template <uint32_t T, int W, int KS, int D, bool DBG, bool FULL>
 __global__ __launch_bounds__(W * 64) void q45_mv_b1_kernel(MvArgs a) {
     constexpr int TS = W / KS;
@@ -1059,14 +1098,25 @@ __global__ __launch_bounds__(W * 64) void q45_mv_b1_kernel(MvArgs a) {
     const uint32_t steps = my_tiles * bpt;
     const uint32_t nk = (uint32_t)KS < nb ? (uint32_t)KS : nb;  // waves of a tile that take blocks
     uint32_t* cnt = (uint32_t*)(part + tmax * TS * KS * 16);
+    float* rs = (float*)(cnt + tmax * TS);
     for (uint32_t i = threadIdx.x; i < tmax * TS; i += W * 64) cnt[i] = 0;
+    const bool rms = FULL && a.xform == kXfRmsNorm;
     if (FULL && threadIdx.x < 8) ((unsigned long long*)(lds + L.am_off))[threadIdx.x] = 0ull;
 
-    // the first own block of each 16-lane row, loaded before the weights (the
-    // waves of tile slot 0 cover every block)
+    // loaded before the weights: the first own block of each 16-lane row
+    // (the waves of tile slot 0 cover every block), its RMSNorm weights and
+    // the residuals of this slot's tiles (at most four, the host checks)
     const uint32_t r16 = lane & 15;
-    float xv[16];
-    if (ts == 0 && kq < bpt) load16(a.x + (kp + KS * kq) * 256 + r16 * 16, xv);
+    const bool mine = ts == 0 && kq < bpt;
+    const uint32_t xblk = kp + KS * kq;
+    float xv[16], nw[16], res = 0.0f;
+    if (mine) load16(a.x + xblk * 256 + r16 * 16, xv);
+    if (rms && mine) load16(a.norm_w + xblk * 256 + r16 * 16, nw);
+    const bool res_lane = FULL && a.resid && kp == 0 && kq < my_tiles;
+    if (res_lane) {
+        const uint32_t row = (t0 + kq * tstride) * kTileRows + n;
+        if (row < a.rows) res = a.resid[row];
+    }
     const uint32_t kp0 = kp < nb ? kp : nb - 1;
     uint32_t ld_tile = t0 < ntiles ? t0 : ntiles - 1, ld_blk = kp0;
     Q4Step<T> buf[D];
@@ -1081,23 +1131,32 @@ __global__ __launch_bounds__(W * 64) void q45_mv_b1_kernel(MvArgs a) {
 #pragma unroll
     for (int i = 0; i < D; ++i) issue(buf[i]);
 
-    // Q8_K of the own blocks (quantize_row_q8_K, 16 lanes per block; at
-    // most four blocks per wave, so every input load precedes the weights')
+    // Q8_K of the own blocks (quantize_row_q8_K, 16 lanes per block)
     int bad = 0;
-    if (ts == 0 && kq < bpt) {
-        const uint32_t blk = kp + KS * kq;
+    if (rms) {
+        const float scale = b1_rms_scale<W>(a, lds, L, wave, mine, xv);
+        if (!(scale <= 3.402823466e38f) || !(scale > 0.0f)) {  // math.rs:218-220
+            bad = 1;
+            if (threadIdx.x == 0) report_error(a.err_word, rms_scale_key(a));
+        }
+#pragma unroll
+        for (int k = 0; k < 16; ++k) xv[k] = xv[k] * scale * nw[k];
+    }
+    if (res_lane) rs[(kq * TS + ts) * 16 + n] = res;
+    if (mine) {
         const Q8KRow o = q8k_row16(xv, r16);
         if (o.kind >= 0) {
             bad = 1;
             if (r16 == 0)
-                report_error(a.err_word, o.kind == kKindNonFinite ? quant_nonfinite_key(a, 0, blk * 256ull + o.index)
-                                                                  : quant_scale_key(a, 0, blk));
+                report_error(a.err_word, o.kind == kKindNonFinite ? quant_nonfinite_key(a, 0, xblk * 256ull + o.index)
+                                                                  : quant_scale_key(a, 0, xblk));
         }
-        *(uint4*)(lds + blk * 256 + r16 * 16) = make_uint4(o.q[0], o.q[1], o.q[2], o.q[3]);
-        if (r16 == 0) *(float*)(lds + L.d_off + blk * 32) = o.d;
-        *(int16_t*)(lds + L.bs_off + blk * 256 + bs_slot(r16) * 2) = (int16_t)o.bsum;
+        *(uint4*)(lds + xblk * 256 + r16 * 16) = make_uint4(o.q[0], o.q[1], o.q[2], o.q[3]);
+        if (r16 == 0) *(float*)(lds + L.d_off + xblk * 32) = o.d;
+        *(int16_t*)(lds + L.bs_off + xblk * 256 + bs_slot(r16) * 2) = (int16_t)o.bsum;
     }
-    // the counters' zeros, every own block and every wave's error flag
+    // the counters' zeros, every own block, the residuals and every wave's
+    // error flag
     if (__syncthreads_or(bad)) {
         if (FULL) finish_argmax(a, lds, L);
         return;
@@ -1114,6 +1173,14 @@ __global__ __launch_bounds__(W * 64) void q45_mv_b1_kernel(MvArgs a) {
     unsigned long long best = 0;
     float acc = 0.0f;
     uint32_t ti = 0, blk = kp, j = 0, tile = t0;
+    // the K parts of slot sl added in K order
+    auto sum_parts = [&](uint32_t sl) {
+        float s = 0.0f;
+#pragma unroll
+        for (int k = 0; k < KS; ++k)
+            if ((uint32_t)k < nk) s += part[(sl * KS + k) * 16 + n];
+        return s;
+    };
     auto compute = [&](const Q4Step<T>& cur) {
         const Q4Scales q = q4k_scales(cur.h);
         uint32_t l0[4] = {cur.w0.x & 0x0f0f0f0fu, cur.w0.y & 0x0f0f0f0fu, cur.w0.z & 0x0f0f0f0fu,
@@ -1185,22 +1252,12 @@ __global__ __launch_bounds__(W * 64) void q45_mv_b1_kernel(MvArgs a) {
             if (kq == 0) part[(slot * KS + kp) * 16 + n] = v;
             // one wave's LDS operations are performed in order: the partial
             // is in place before the count
-            uint32_t prev = 0;
-            if (lane == 0)
-                prev = __hip_atomic_fetch_add(cnt + slot, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_WORKGROUP);
-            prev = __shfl(prev, 0, 64);
-            const uint32_t row = tile * kTileRows + n;
-            if (prev == nk - 1 && kq == 0 && row < a.rows) {  // the last part: add them in K order
-                float s = 0.0f;
-#pragma unroll
-                for (int k = 0; k < KS; ++k)
-                    if ((uint32_t)k < nk) s += part[(slot * KS + k) * 16 + n];
-                if (FULL && a.chk) check_finite(a, kChkOut, s);
-                a.y[row] = s;
-                if (FULL) {
-                    const unsigned long long key = argmax_key(s, row);
-                    best = key > best ? key : best;
-                }
+            if (lane == 0) {
+                const uint32_t prev =
+                    __hip_atomic_fetch_add(cnt + slot, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_WORKGROUP);
+                // the last part: this wave finishes the tile after its last
+                // step (no global store or atomic between the weight loads)
+                if (prev == nk - 1) cnt[slot] = nk + 1 + wave;
             }
             acc = 0.0f;
             j = 0;
@@ -1210,6 +1267,23 @@ __global__ __launch_bounds__(W * 64) void q45_mv_b1_kernel(MvArgs a) {
         }
     };
     pipeline<D>(steps, buf, issue, compute);
+
+    // the tiles this wave completed: add their K parts in order and store
+    for (uint32_t i = 0; i < my_tiles; ++i) {
+        const uint32_t slot = i * TS + ts, row = (t0 + i * tstride) * kTileRows + n;
+        if (cnt[slot] != nk + 1 + wave || kq != 0 || row >= a.rows) continue;  // (the mark is wave-uniform)
+        float s = sum_parts(slot);
+        if (FULL && a.chk) check_finite(a, kChkOut, s);
+        if (FULL && a.resid) {
+            s = rs[slot * 16 + n] + s;  // math.rs:203-208: hidden += projected
+            if (a.chk) check_finite(a, kChkResid, s);
+        }
+        a.y[row] = s;
+        if (FULL) {
+            const unsigned long long key = argmax_key(s, row);
+            best = key > best ? key : best;
+        }
+    }
     if (FULL) {
         fold_argmax(a, lds, L, kq, best);
         finish_argmax(a, lds, L);
@@ -1826,21 +1900,44 @@ static hipError_t launch_small(const MvArgs& a, hipStream_t s, uint32_t pairs) {
     return launch_parked<W, KS>(q4k_mv_small_kernel<T, W, KS, D, B, DBG>, lds_set, a, s, pairs);
 }
 
-// The batch-1 kernel for a plain column: grid and LDS as launch_parked, plus
-// one arrival counter per (tile, slot).
+// The batch-1 kernel: grid as launch_parked (enough workgroups that the
+// parked partials fit in LDS), the LDS of b1_lds_bytes.
+template <int W, int KS>
+static void b1_grid(const MvArgs& a, uint32_t& grid, uint32_t& tmax) {
+    constexpr int TS = W / KS;
+    grid = grid_cols((a.ntiles + TS - 1) / TS, (uint32_t)kSmallWgPerCu * (uint32_t)device_cus(), 1);
+    const size_t off = small_part_off(a.cols, 1), per_tile = (size_t)TS * KS * 16u * 4u + TS * 4u + TS * 64u;
+    const uint64_t room = off < kMaxLds ? (kMaxLds - off) / per_tile : 0;
+    if (room == 0) {
+        grid = tmax = 0;
+        return;
+    }
+    const uint64_t need = (a.ntiles + room * TS - 1) / (room * TS);
+    if (grid < need) grid = (uint32_t)need;
+    tmax = (a.ntiles + grid * TS - 1) / (grid * TS);
+}
+
+// Whether the batch-1 kernel with W waves and a K split of KS takes a call:
+// at most 4 blocks per wave, no SiLU pair, the residual only with at most 4
+// tiles per slot (they are loaded up front).
+template <int W, int KS>
+static bool b1_takes(const MvArgs& a) {
+    if (a.nb > 4u * KS || a.epilogue != kEpStore) return false;
+    uint32_t grid, tmax;
+    b1_grid<W, KS>(a, grid, tmax);
+    return grid > 0 && (!a.resid || tmax <= 4);
+}
+
 template <uint32_t T, int W, int KS, int D, bool DBG, bool FULL>
 static hipError_t launch_b1(const MvArgs& a, hipStream_t s) {
     constexpr int TS = W / KS;
     static size_t lds_set = 64 * 1024;
     auto kernel = q45_mv_b1_kernel<T, W, KS, D, DBG, FULL>;
-    uint32_t grid = grid_cols((a.ntiles + TS - 1) / TS, (uint32_t)kSmallWgPerCu * (uint32_t)device_cus(), 1);
-    const size_t off = small_part_off(a.cols, 1), per_tile = (size_t)TS * KS * 16u * 4u + TS * 4u;
-    if (off >= kMaxLds || (kMaxLds - off) / per_tile == 0) return hipErrorInvalidValue;
-    const uint64_t room = (kMaxLds - off) / per_tile, need = (a.ntiles + room * TS - 1) / (room * TS);
-    if (grid < need) grid = (uint32_t)need;
-    const uint32_t tstride = grid * TS, tmax = (a.ntiles + tstride - 1) / tstride;
+    uint32_t grid, tmax;
+    b1_grid<W, KS>(a, grid, tmax);
     const size_t lds = b1_lds_bytes(a.cols, tmax, TS, KS);
-    if (lds > kMaxLds || (a.am_out && grid > kArgmaxMaxGrid)) return hipErrorInvalidValue;
+    if (grid == 0 || lds > kMaxLds || (a.am_out && grid > kArgmaxMaxGrid) || (a.resid && tmax > 4))
+        return hipErrorInvalidValue;
     if (lds > lds_set) {
         const hipError_t e = hipFuncSetAttribute((const void*)kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
                                                  (int)lds);
@@ -1851,10 +1948,38 @@ static hipError_t launch_b1(const MvArgs& a, hipStream_t s) {
     return hipGetLastError();
 }
 
+template <uint32_t T, int W, int KS>
+static hipError_t launch_b1_any(const MvArgs& a, bool dbg, bool full, hipStream_t s) {
+    return dbg ? (full ? launch_b1<T, W, KS, kSmallD, true, true>(a, s)
+                       : launch_b1<T, W, KS, kSmallD, true, false>(a, s))
+               : (full ? launch_b1<T, W, KS, kSmallD, false, true>(a, s)
+                       : launch_b1<T, W, KS, kSmallD, false, false>(a, s));
+}
+
 // Q4_K / Q5_K: the VALU kernel for one or two columns, MFMA above.
 template <uint32_t T>
 static hipError_t launch_q45(const MvArgs& a, uint32_t nbat, bool dbg, uint32_t epilogue, size_t lds, hipStream_t s,
                              uint32_t pairs) {
+    // one f32 column: the batch-1 kernel (measured, Q4_K, us against the
+    // shared-quantization kernel: 14336x4096 8.3 / 9.2 with two tile slots
+    // of a K split of 4; 6144x4096 5.5 / 6.6 likewise; 4096x4096 5.2 / 6.2
+    // with one slot of a split of 4; 4096x14336 9.6 / 10.6 with a split of
+    // 16).  Its FULL variant takes the decode step's RMSNorm input and
+    // residual, model checks and the argmax (Q/K/V 6144x4096 with RMSNorm
+    // 6.9 / 7.1, O 4096x4096 with the residual 6.0 / 6.3, down 4096x14336
+    // 10.2 / 10.9).  The SiLU pair stays with the kernel below (28672x4096:
+    // 15.2 us in the batch-1 kernel with two slots, 14.6 with four).
+    if (nbat == 1 && a.x && (a.xform == kXfNone || a.xform == kXfRmsNorm) && !a.ids && !a.gate &&
+        epilogue == kEpStore) {
+        const bool full = a.chk || a.am_out || a.resid || a.xform != kXfNone;
+        if (a.nb > 16) {
+            if (b1_takes<16, 16>(a)) return launch_b1_any<T, 16, 16>(a, dbg, full, s);
+        } else if (a.ntiles >= 384) {
+            if (b1_takes<8, 4>(a)) return launch_b1_any<T, 8, 4>(a, dbg, full, s);
+        } else if (b1_takes<4, 4>(a)) {
+            return launch_b1_any<T, 4, 4>(a, dbg, full, s);
+        }
+    }
     // the SiLU pair epilogue: four tile slots per workgroup (two gate/up
     // pairs, a K split of two; 28672x4096 measured 14.6 us against 15.3 us
     // with one pair and a split of four)
@@ -1863,28 +1988,6 @@ static hipError_t launch_q45(const MvArgs& a, uint32_t nbat, bool dbg, uint32_t 
     if (epilogue == kEpSiluPair)
         return dbg ? launch_small<T, kSmallW, kSmallW / 4, kSmallD, 1, true>(a, s, pairs)
                    : launch_small<T, kSmallW, kSmallW / 4, kSmallD, 1, false>(a, s, pairs);
-    // one plain f32 column: the batch-1 kernel, whose waves take at most 4
-    // blocks of a tile (measured, Q4_K, us against the shared-quantization
-    // kernel: 14336x4096 8.3 / 9.2 with two tile slots of a K split of 4;
-    // 6144x4096 5.5 / 6.6 likewise; 4096x4096 5.2 / 6.2 with one slot of a
-    // split of 4; 4096x14336 9.6 / 10.6 with a split of 16)
-    if (nbat == 1 && a.x && a.xform == kXfNone && !a.ids && !a.gate && !a.resid && a.nb <= 64) {
-        const bool full = a.chk || a.am_out;
-        if (a.nb > 16)
-            return dbg ? (full ? launch_b1<T, 16, 16, kSmallD, true, true>(a, s)
-                               : launch_b1<T, 16, 16, kSmallD, true, false>(a, s))
-                       : (full ? launch_b1<T, 16, 16, kSmallD, false, true>(a, s)
-                               : launch_b1<T, 16, 16, kSmallD, false, false>(a, s));
-        if (a.ntiles >= 384)
-            return dbg ? (full ? launch_b1<T, 8, 4, kSmallD, true, true>(a, s)
-                               : launch_b1<T, 8, 4, kSmallD, true, false>(a, s))
-                       : (full ? launch_b1<T, 8, 4, kSmallD, false, true>(a, s)
-                               : launch_b1<T, 8, 4, kSmallD, false, false>(a, s));
-        return dbg ? (full ? launch_b1<T, 4, 4, kSmallD, true, true>(a, s)
-                           : launch_b1<T, 4, 4, kSmallD, true, false>(a, s))
-                   : (full ? launch_b1<T, 4, 4, kSmallD, false, true>(a, s)
-                           : launch_b1<T, 4, 4, kSmallD, false, false>(a, s));
-    }
     // two tile slots per workgroup (a K split of four): small matrices of at
     // most 4096 columns and 512 tiles (measured: 6144x4096 runs 1 us faster)
     if (nbat == 1 && a.nb <= 16 && a.ntiles <= 512)
