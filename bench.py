@@ -124,16 +124,17 @@ def algorithmic_bytes(rlq, dtype, rows, cols, batch):
 
 def time_steps(rlq, ctx, handles, x, y, steps, warmup, argmax=None):
     """Mean step time (ms) of `steps` back-to-back rlq_matmul calls (or
-    rlq_matmul_argmax when `argmax` is given), bracketed by HIP events on the
-    stream they are launched on (torch's current one)."""
+    rlq_matmul_argmax when `argmax` is given) through prepared calls
+    (Context.bind_matmul), bracketed by HIP events on the stream they are
+    launched on (torch's current one)."""
     torch = rlq.torch
     n = len(handles)
+    # prepared calls (tensors, stream and error record resolved once), so the
+    # host issues launches faster than the GPU retires them
+    bound = [ctx.bind_matmul(h, x, y, argmax) for h in handles]
 
     def call(i):
-        if argmax is None:
-            ctx.matmul(handles[i % n], x, y)
-        else:
-            ctx.matmul_argmax(handles[i % n], x, y, argmax)
+        bound[i % n]()
 
     for i in range(warmup):
         call(i)

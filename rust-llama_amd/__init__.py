@@ -378,6 +378,39 @@ class Context:
                                       _stream_ptr(stream), ctypes.byref(err)), err)
         return y, argmax
 
+    def bind_matmul(self, w, x, y, argmax=None, stream=None):
+        """A prepared matmul (or matmul_argmax when argmax is given): the
+        tensors, the stream (torch's current one when None, taken now) and
+        the error record are resolved once, and the returned function of no
+        arguments launches the same call again with only the C call's own
+        cost (for serving loops; it raises like matmul).  The tensors stay
+        referenced by the function."""
+        x2 = x.reshape(-1, w.cols)
+        batch = x2.shape[0]
+        if y.numel() != batch * w.rows:
+            raise ValueError("y must hold batch * rows f32 values")
+        err = _Err()
+        ref = ctypes.byref(err)
+        h, wh = self._h, w._h
+        xp, yp, sp = _dev_ptr(x2, torch.float32), _dev_ptr(y, torch.float32), _stream_ptr(stream)
+        keep = (w, x2, y, argmax)
+        if argmax is None:
+            fn = _lib.rlq_matmul
+
+            def call():
+                rc = fn(h, wh, xp, batch, yp, sp, ref)
+                if rc:
+                    _check(rc, err)
+        else:
+            fn, ap = _lib.rlq_matmul_argmax, _dev_ptr(argmax, torch.int32)
+
+            def call():
+                rc = fn(h, wh, xp, batch, yp, ap, sp, ref)
+                if rc:
+                    _check(rc, err)
+        call.tensors = keep
+        return call
+
     def matmul_noalloc(self, w, x, y, argmax=None, stream=None):
         """rlq_matmul_noalloc: matmul (argmax None) or matmul_argmax into the
         caller's y [batch, rows] (and argmax [batch] int32), with the

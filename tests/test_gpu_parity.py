@@ -494,6 +494,33 @@ def test_multiply_finite_checks(ctx, rows):
     ctx.sync()
 
 
+def test_bound_matmul_is_matmul(ctx):
+    """Context.bind_matmul: the prepared call writes what matmul writes, the
+    argmax form what matmul_argmax writes, every time it runs; a data error
+    raises from the call's sync like matmul's."""
+    rows, cols = 9000, 2048
+    say("prepared matmul calls", rows, cols)
+    W = rlq.Weights(ctx, DT.Q4_K, _weights(DT.Q4_K, rows, cols, 21), rows, cols)
+    x = torch.from_numpy(randn(22, cols)).cuda().view(1, cols)
+    want = ctx.matmul(W, x)
+    want_y, want_am = ctx.matmul_argmax(W, x)
+    y = torch.empty((1, rows), device="cuda")
+    y2, am = torch.empty((1, rows), device="cuda"), torch.empty(1, dtype=torch.int32, device="cuda")
+    call, call_am = ctx.bind_matmul(W, x, y), ctx.bind_matmul(W, x, y2, am)
+    for _ in range(3):
+        y.fill_(0.0)
+        call()
+        call_am()
+        ctx.sync()
+        assert torch.equal(y.view(torch.int32), want.view(torch.int32))
+        assert torch.equal(y2.view(torch.int32), want_y.view(torch.int32)) and int(am[0]) == int(want_am[0])
+    x[0, 5] = float("nan")
+    call()
+    with pytest.raises(rlq.QuantError) as e:
+        ctx.sync()
+    assert (e.value.name, e.value.index) == ("NonFiniteInput", 5)
+
+
 def test_zero_weights_give_zero(ctx):
     say("zero weights")
     for t, cols in ((DT.Q4_K, 1024), (DT.Q6_K, 1024), (DT.Q8_0, 96)):
