@@ -62,8 +62,17 @@ PREFILL_M = 512
 # WRITE_SIZE (each calibrated against a 256 MiB device copy), recorded in
 # profiles/hbm_traffic_q4k_decode_and_prefill.md: the decode kernel, and the prefill step's
 # two kernels (GEMM + quantizer).
-TRAFFIC_DECODE_BYTES = 33396801
-TRAFFIC_PREFILL_BYTES = 102984548 + 12971772
+TRAFFIC_DECODE_BYTES = 33381163
+TRAFFIC_PREFILL_BYTES = 103014901 + 12971701
+# the same measurement for the kernels of the other configurations (per launch)
+TRAFFIC_CONFIG_BYTES = {
+    "q8_0_4864x896_b1": 5054682,
+    "q4k_14336x4096_b4": 34455195,
+    "q4k_14336x4096_b8": 35208775,
+    "q6k_128256x4096_b1_argmax": 434140214,
+    "q6k_128256x4096_b8_argmax": 440090559,
+    "q8_0_151936x896_b1_argmax": 145813761,
+}
 COPY_PROBE_BYTES = 256 << 20
 METRIC = "Q4_K matvec GB/s (14336x4096, B=1) + prefill GEMM TOPS (M=512); tok/s"
 
@@ -305,7 +314,8 @@ def config_legs(rlq, ctx, steps, warmup):
         legs[name] = {"workload": workload, "us_per_step": round(o["us_per_step"], 3),
                       "bytes_per_step": o["bytes_per_step"], "rotated_copies": copies,
                       "roofline": {"bound": "hbm", "achieved": round(o["gbs"], 2), "peak": HBM_PEAK_GBS,
-                                   "unit": "GB/s", "frac": round(o["gbs"] / HBM_PEAK_GBS, 4)}}
+                                   "unit": "GB/s", "frac": round(o["gbs"] / HBM_PEAK_GBS, 4),
+                                   "traffic": TRAFFIC_CONFIG_BYTES.get(name)}}
     return legs
 
 
