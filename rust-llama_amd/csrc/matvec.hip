@@ -772,22 +772,66 @@ __device__ __forceinline__ Q45Ints q45_mfma_ints(const Q4Step<T>& cur, const uin
     return o;
 }
 
-// Q4_K / Q5_K, batches of three to eight columns: MFMA.
-template <uint32_t T, int W, int D, bool DBG>
-__global__ __launch_bounds__(W * 64) void q4k_mv_kernel(MvArgs a) {
-    RLQ_MV_PROLOGUE(T, a.nb)
-    const uint32_t nb = a.nb;
+// Q4_K / Q5_K, three to eight columns, K split over KS waves per tile: the
+// MFMA step q45_mfma_ints, with a workgroup of W waves holding TS = W / KS
+// tile slots and the waves of a slot taking blocks kp, kp + KS, ... of its
+// tile (every SIMD holds several waves, the grid is a few hundred
+// workgroups).  The columns are quantized by the whole workgroup (stage_q8k)
+// while the first weight chunks load.  Lane (n, kq) holds the partial sums of
+// row n, columns 2 kq and 2 kq + 1 of its K part; a tile's parts are parked
+// in LDS [tmax][TS][KS][16][8] and counted with a workgroup-scope atomic, and
+// the wave that completes the count adds them in K order after its last step
+// (so no global store sits between its weight loads).
+__host__ __device__ inline uint32_t ks_part_off(uint32_t T, uint32_t cols, uint32_t batch) {
+    return (lds_map(T, cols, batch).total + 15u) & ~15u;
+}
+__host__ __device__ inline uint32_t ks_lds_bytes(uint32_t T, uint32_t cols, uint32_t batch, uint32_t tmax, uint32_t ts,
+                                                 uint32_t ks) {
+    return ks_part_off(T, cols, batch) + tmax * ts * ks * 16u * 8u * 4u + tmax * ts * 4u;
+}
+
+template <uint32_t T, int W, int KS, int D, bool DBG>
+__global__ __launch_bounds__(W * 64) void q45_mv_ks_kernel(MvArgs a) {
+    constexpr int TS = W / KS;
+    if (!mv_enter(a)) return;
+    extern __shared__ __align__(16) uint8_t lds[];
+    const LdsMap L = lds_map(T, a.cols, a.batch);
+    float* part = (float*)(lds + ks_part_off(T, a.cols, a.batch));
+    const uint32_t lane = threadIdx.x & 63, n = lane & 15, kq = lane >> 4;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t ts = wave / KS, kp = wave % KS;
+    const uint32_t nb = a.nb, ntiles = a.ntiles;
+    const uint32_t tstride = gridDim.x * TS, t0 = blockIdx.x * TS + ts;
+    const uint32_t tmax = (ntiles + tstride - 1) / tstride;
+    const uint32_t my_tiles = t0 < ntiles ? (ntiles - 1 - t0) / tstride + 1 : 0;
+    const uint32_t bpt = kp < nb ? (nb - 1 - kp) / KS + 1 : 0;  // blocks of each tile this wave takes
+    const uint32_t steps = my_tiles * bpt;
+    const uint32_t nk = (uint32_t)KS < nb ? (uint32_t)KS : nb;  // waves of a tile that take blocks
+    uint32_t* cnt = (uint32_t*)(part + tmax * TS * KS * 16 * 8);
+    for (uint32_t i = threadIdx.x; i < tmax * TS; i += W * 64) cnt[i] = 0;
+    if (threadIdx.x < 16) *(uint4*)(lds + L.zero_off + threadIdx.x * 16) = make_uint4(0, 0, 0, 0);
+    if (threadIdx.x < 8) ((unsigned long long*)(lds + L.am_off))[threadIdx.x] = 0ull;
+    float xv[16];
+    prefetch_unit(a, wave, xv);
+
+    const uint32_t kp0 = kp < nb ? kp : nb - 1;
+    uint32_t ld_tile = t0 < ntiles ? t0 : ntiles - 1, ld_blk = kp0;
     Q4Step<T> buf[D];
     auto issue = [&](Q4Step<T>& st) {
-        q45_issue<T>(st, a.w + ((uint64_t)ld_tile * nb + ld_chunk) * Q45<T>::chunk, lane, n, kq);
-        next_load();
+        q45_issue<T>(st, a.w + ((uint64_t)ld_tile * nb + ld_blk) * Q45<T>::chunk, lane, n, kq);
+        ld_blk += KS;
+        if (ld_blk >= nb) {
+            ld_blk = kp0;
+            if (ld_tile + tstride < ntiles) ld_tile += tstride;
+        }
     };
 #pragma unroll
     for (int i = 0; i < D; ++i) issue(buf[i]);
 
+    // the counters' zeros are in place with the activations (one barrier)
     const bool ok = a.x ? stage_q8k<W, kBsQuarters>(a, lds, L, wave, xv) : stage_planes<W>(a, lds, L, T);
     if (!ok) return finish_argmax(a, lds, L);
-    if (a.zero_pair) return zero_wave_tiles(a, gw, tw, n, kq);
+    if (a.zero_pair) return zero_slot_tiles<W, TS>(a, tmax, tstride);
 
     // A operand: lane row r = n holds column r / 2, sub-block parity r % 2; it
     // is nonzero only in the K quarters (kq / 2 == r % 2) of that sub-block.
@@ -798,15 +842,13 @@ __global__ __launch_bounds__(W * 64) void q4k_mv_kernel(MvArgs a) {
     const uint32_t b0 = 2 * kq;  // this lane's output columns b0, b0 + 1
 
     float acc0 = 0.0f, acc1 = 0.0f;
-    unsigned long long best0 = 0, best1 = 0;
-    uint32_t tile = gw, blk = 0;
+    uint32_t ti = 0, blk = kp, j = 0, tile = t0;
     auto compute = [&](const Q4Step<T>& cur) {
         const Q45Ints o = q45_mfma_ints<T>(cur, a_ptr + blk * a_step, lds + L.bs_off + (blk * 8 + b0) * 32, kq);
         const float2 da = *(const float2*)(lds + L.d_off + (blk * 8 + b0) * 4);
         const float dw = half_to_float(cur.h.x), dmw = half_to_float(cur.h.x >> 16);
         acc0 += (dw * da.x) * (float)o.I0 - (dmw * da.x) * (float)o.M0;
         acc1 += (dw * da.y) * (float)o.I1 - (dmw * da.y) * (float)o.M1;
-
         if (DBG && kq == 0) {
             const uint32_t row = tile * kTileRows + n;
             if (row < a.rows) {
@@ -814,16 +856,42 @@ __global__ __launch_bounds__(W * 64) void q4k_mv_kernel(MvArgs a) {
                 a.dbg_imin[(uint64_t)row * nb + blk] = o.M0;
             }
         }
-        if (++blk == nb) {
-            const uint32_t row = tile * kTileRows + n;
-            store_out(a, row, b0, acc0, best0);
-            store_out(a, row, b0 + 1, acc1, best1);
+        blk += KS;
+        if (++j == bpt) {  // this wave's share of the tile is done: park its sums
+            const uint32_t slot = ti * TS + ts;
+            *(float2*)(part + ((slot * KS + kp) * 16 + n) * 8 + b0) = make_float2(acc0, acc1);
+            // one wave's LDS operations are performed in order: the partials
+            // are in place before the count
+            if (lane == 0) {
+                const uint32_t prev =
+                    __hip_atomic_fetch_add(cnt + slot, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_WORKGROUP);
+                if (prev == nk - 1) cnt[slot] = nk + 1 + wave;  // this wave finishes the tile
+            }
             acc0 = acc1 = 0.0f;
-            blk = 0;
-            tile += tw;
+            j = 0;
+            blk = kp;
+            ++ti;
+            tile += tstride;
         }
     };
     pipeline<D>(steps, buf, issue, compute);
+
+    // the tiles this wave completed: add their K parts in order and store
+    unsigned long long best0 = 0, best1 = 0;
+    for (uint32_t i = 0; i < my_tiles; ++i) {
+        const uint32_t slot = i * TS + ts, row = (t0 + i * tstride) * kTileRows + n;
+        if (cnt[slot] != nk + 1 + wave) continue;  // (the mark is wave-uniform)
+        float s0 = 0.0f, s1 = 0.0f;
+#pragma unroll
+        for (int k = 0; k < KS; ++k)
+            if ((uint32_t)k < nk) {
+                const float2 v = *(const float2*)(part + ((slot * KS + k) * 16 + n) * 8 + b0);
+                s0 += v.x;
+                s1 += v.y;
+            }
+        store_out(a, row, b0, s0, best0);
+        store_out(a, row, b0 + 1, s1, best1);
+    }
     fold_argmax(a, lds, L, b0, best0);
     fold_argmax(a, lds, L, b0 + 1, best1);
     finish_argmax(a, lds, L);
@@ -1956,6 +2024,31 @@ static hipError_t launch_b1_any(const MvArgs& a, bool dbg, bool full, hipStream_
                        : launch_b1<T, W, KS, kSmallD, false, false>(a, s));
 }
 
+// The K-split MFMA kernel for 3 to 8 columns: grid as launch_parked.
+template <uint32_t T, int W, int KS, int D, bool DBG>
+static hipError_t launch_ks(const MvArgs& a, hipStream_t s, uint32_t pairs) {
+    constexpr int TS = W / KS;
+    static size_t lds_set = 64 * 1024;
+    auto kernel = q45_mv_ks_kernel<T, W, KS, D, DBG>;
+    const uint32_t gy = grid_rows(a, pairs);
+    uint32_t grid = grid_cols((a.ntiles + TS - 1) / TS, (uint32_t)kSmallWgPerCu * (uint32_t)device_cus(), gy);
+    const size_t off = ks_part_off(T, a.cols, a.batch), per_tile = (size_t)TS * KS * 16u * 8u * 4u + TS * 4u;
+    if (off >= kMaxLds || (kMaxLds - off) / per_tile == 0) return hipErrorInvalidValue;
+    const uint64_t room = (kMaxLds - off) / per_tile, need = (a.ntiles + room * TS - 1) / (room * TS);
+    if (grid < need) grid = (uint32_t)need;
+    const uint32_t tstride = grid * TS, tmax = (a.ntiles + tstride - 1) / tstride;
+    const size_t lds = ks_lds_bytes(T, a.cols, a.batch, tmax, TS, KS);
+    if (lds > kMaxLds || (a.am_out && grid > kArgmaxMaxGrid)) return hipErrorInvalidValue;
+    if (lds > lds_set) {
+        const hipError_t e = hipFuncSetAttribute((const void*)kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                 (int)lds);
+        if (e != hipSuccess) return e;
+        lds_set = lds;
+    }
+    hipLaunchKernelGGL(kernel, dim3(grid, gy), dim3(W * 64), lds, s, a);
+    return hipGetLastError();
+}
+
 // Q4_K / Q5_K: the VALU kernel for one or two columns, MFMA above.
 template <uint32_t T>
 static hipError_t launch_q45(const MvArgs& a, uint32_t nbat, bool dbg, uint32_t epilogue, size_t lds, hipStream_t s,
@@ -2004,8 +2097,7 @@ static hipError_t launch_q45(const MvArgs& a, uint32_t nbat, bool dbg, uint32_t 
     if (nbat == 2)
         return dbg ? launch_small<T, kSmallW, kSmallKS, kSmallD, 2, true>(a, s, pairs)
                    : launch_small<T, kSmallW, kSmallKS, kSmallD, 2, false>(a, s, pairs);
-    return dbg ? launch_one(q4k_mv_kernel<T, kMvWaves, 8, true>, a, lds, s, pairs)
-               : launch_one(q4k_mv_kernel<T, kMvWaves, 8, false>, a, lds, s, pairs);
+    return dbg ? launch_ks<T, 8, 4, 2, true>(a, s, pairs) : launch_ks<T, 8, 4, 2, false>(a, s, pairs);
 }
 
 // Q2_K / Q3_K: up to four columns the K-split kernel, while its parked terms

@@ -418,6 +418,33 @@ def test_device_errors_suppress_outputs_and_report_first_column(ctx):
     assert bool((y[:2] == 0).all())
 
 
+def test_device_errors_of_six_to_eight_columns(ctx):
+    """Six to eight Q4_K / Q5_K columns are quantized once by the planes
+    kernel, then multiplied: the first error (by column, then the
+    reference's order inside it) is reported, no output is written, and a
+    clean call is exact against the oracle."""
+    for t in (DT.Q4_K, DT.Q5_K):
+        rows, cols, batch = 1000, 1024, 7
+        say("device errors, planes path", t, rows, cols, batch)
+        w = _weights(t, rows, cols, 7) if t == DT.Q4_K else _q5k_blocks(rows, cols, 7)
+        W = rlq.Weights(ctx, t, w, rows, cols)
+        x = torch.from_numpy(randn(8, batch * cols).reshape(batch, cols)).cuda()
+        y = torch.full((batch, rows), 123.0, device="cuda")
+        bad = x.clone()
+        bad[5, 600] = float("inf")
+        bad[3, 256:512] = 1e-45
+        ctx.matmul(W, bad, y)
+        with pytest.raises(rlq.QuantError) as e:
+            ctx.sync()
+        assert (e.value.name, e.value.block, e.value.b) == ("UnrepresentableScale", 1, 3)
+        assert bool((y == 123.0).all())
+        ctx.matmul(W, x, y)
+        ctx.sync()
+        got, xs = y.cpu().numpy(), x.cpu().numpy()
+        for b in range(batch):
+            assert rel_l2(got[b], O.matvec(int(t), w, rows, cols, xs[b], threads=16)) <= REL_L2, (t, b)
+
+
 def test_device_errors_of_the_batch1_plain_kernel(ctx):
     """One f32 column over 513 tiles (the batch-1 kernel whose workgroups
     each quantize their own blocks): the first error is reported and no
