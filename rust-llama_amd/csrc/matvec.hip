@@ -1884,6 +1884,128 @@ __global__ __launch_bounds__(W * 64) void q8_0_mv_kernel(MvArgs a) {
     fold_argmax(a, lds, L, b0 + 1, best1);
     finish_argmax(a, lds, L);
 }
+
+// Q8_0 with K split over KS waves per tile (the MFMA step of q8_0_mv_kernel):
+// W waves hold TS = W / KS tile slots and the waves of a slot take chunks
+// (block pairs) kp, kp + KS, ... of its tile, so a matrix of a few hundred
+// tiles still spreads over every CU.  Every block's f32 term
+// isum * (dx * dy) is parked in LDS [tmax][TS][nb][16][8] and the wave that
+// completes a tile's count adds them in block order, the reference's order
+// (matvec.rs:124-128): the outputs stay bit-exact.
+template <int W, int KS, int D, bool DBG>
+__global__ __launch_bounds__(W * 64) void q8_0_mv_ks_kernel(MvArgs a) {
+    constexpr int TS = W / KS;
+    if (!mv_enter(a)) return;
+    extern __shared__ __align__(16) uint8_t lds[];
+    const LdsMap L = lds_map(kQ8_0, a.cols, a.batch);
+    float* part = (float*)(lds + ks_part_off(kQ8_0, a.cols, a.batch));
+    const uint32_t lane = threadIdx.x & 63, n = lane & 15, kq = lane >> 4;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t ts = wave / KS, kp = wave % KS;
+    const uint32_t nb = a.nb, np = a.nchunks, ntiles = a.ntiles;
+    const uint32_t tstride = gridDim.x * TS, t0 = blockIdx.x * TS + ts;
+    const uint32_t tmax = (ntiles + tstride - 1) / tstride;
+    const uint32_t my_tiles = t0 < ntiles ? (ntiles - 1 - t0) / tstride + 1 : 0;
+    const uint32_t cpt = kp < np ? (np - 1 - kp) / KS + 1 : 0;  // chunks of each tile this wave takes
+    const uint32_t steps = my_tiles * cpt;
+    const uint32_t nk = (uint32_t)KS < np ? (uint32_t)KS : np;  // waves of a tile that take chunks
+    uint32_t* cnt = (uint32_t*)(part + tmax * TS * nb * 16 * 8);
+    for (uint32_t i = threadIdx.x; i < tmax * TS; i += W * 64) cnt[i] = 0;
+    if (threadIdx.x < 16) *(uint4*)(lds + L.zero_off + threadIdx.x * 16) = make_uint4(0, 0, 0, 0);
+    if (threadIdx.x < 8) ((unsigned long long*)(lds + L.am_off))[threadIdx.x] = 0ull;
+    float xv[16];
+    prefetch_unit(a, wave, xv);
+
+    const uint32_t kp0 = kp < np ? kp : np - 1;
+    uint32_t ld_tile = t0 < ntiles ? t0 : ntiles - 1, ld_chunk = kp0;
+    Q8Step buf[D];
+    auto issue = [&](Q8Step& st) {
+        const uint8_t* base = a.w + ((uint64_t)ld_tile * np + ld_chunk) * kQ80Chunk;
+        st.q = load_stream16(base + lane * 16);
+        st.d = __builtin_nontemporal_load((const uint32_t*)(base + 1024 + n * 4));
+        ld_chunk += KS;
+        if (ld_chunk >= np) {
+            ld_chunk = kp0;
+            if (ld_tile + tstride < ntiles) ld_tile += tstride;
+        }
+    };
+#pragma unroll
+    for (int i = 0; i < D; ++i) issue(buf[i]);
+
+    const bool ok = a.x ? stage_q8_0<W>(a, lds, L, wave, xv) : stage_planes<W>(a, lds, L, kQ8_0);
+    if (!ok) return finish_argmax(a, lds, L);
+    if (a.zero_pair) return zero_slot_tiles<W, TS>(a, tmax, tstride);
+
+    // A operand: lane row r = n holds column r / 2 and block 2p + r % 2; it is
+    // nonzero in the K quarters (kq / 2 == r % 2) of that block.
+    const uint32_t ab = n >> 1, which = n & 1;
+    const bool a_live = which == (kq >> 1) && ab < a.batch;
+    const uint8_t* a_ptr = a_live ? lds + ab * L.S + 32 * which + 16 * (kq & 1) : lds + L.zero_off;
+    const uint32_t a_step = a_live ? 64 : 0;
+    const uint32_t b0 = 2 * kq;
+
+    uint32_t ti = 0, p = kp, j = 0, tile = t0;
+    auto compute = [&](const Q8Step& cur) {
+        const bool second = 2 * p + 1 < nb;  // false only for the odd last block of a row
+        i32x4 av = *(const i32x4*)(a_ptr + p * a_step);
+        if (!second && which) av = i32x4{0, 0, 0, 0};
+        const i32x4 dot = mfma_i8(av, i32x4{(int)cur.q.x, (int)cur.q.y, (int)cur.q.z, (int)cur.q.w});
+        // the terms isum as f32 * (dx * dy) of blocks 2p and 2p + 1
+        // (matvec.rs:124-128), parked for the in-order sum
+        const float dx0 = half_to_float(cur.d), dx1 = half_to_float(cur.d >> 16);
+        const float2 dy0 = *(const float2*)(lds + L.d_off + (2 * p * 8 + b0) * 4);
+        float* pt = part + (((ti * TS + ts) * nb + 2 * p) * 16 + n) * 8 + b0;
+        *(float2*)pt = make_float2((float)dot[0] * (dx0 * dy0.x), (float)dot[2] * (dx0 * dy0.y));
+        if (second) {
+            const float2 dy1 = *(const float2*)(lds + L.d_off + ((2 * p + 1) * 8 + b0) * 4);
+            *(float2*)(pt + 16 * 8) = make_float2((float)dot[1] * (dx1 * dy1.x), (float)dot[3] * (dx1 * dy1.y));
+        }
+        if (DBG && kq == 0) {
+            const uint32_t row = tile * kTileRows + n;
+            if (row < a.rows) {
+                a.dbg_isum[(uint64_t)row * nb + 2 * p] = dot[0];
+                a.dbg_imin[(uint64_t)row * nb + 2 * p] = 0;
+                if (second) {
+                    a.dbg_isum[(uint64_t)row * nb + 2 * p + 1] = dot[1];
+                    a.dbg_imin[(uint64_t)row * nb + 2 * p + 1] = 0;
+                }
+            }
+        }
+        p += KS;
+        if (++j == cpt) {  // this wave's share of the tile is parked: count it
+            const uint32_t slot = ti * TS + ts;
+            // one wave's LDS operations are performed in order: the terms are
+            // in place before the count
+            if (lane == 0) {
+                const uint32_t prev =
+                    __hip_atomic_fetch_add(cnt + slot, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_WORKGROUP);
+                if (prev == nk - 1) cnt[slot] = nk + 1 + wave;  // this wave finishes the tile
+            }
+            j = 0;
+            p = kp;
+            ++ti;
+            tile += tstride;
+        }
+    };
+    pipeline<D>(steps, buf, issue, compute);
+
+    unsigned long long best0 = 0, best1 = 0;
+    for (uint32_t i = 0; i < my_tiles; ++i) {
+        const uint32_t slot = i * TS + ts, row = (t0 + i * tstride) * kTileRows + n;
+        if (cnt[slot] != nk + 1 + wave) continue;  // (the mark is wave-uniform)
+        float s0 = 0.0f, s1 = 0.0f;
+        for (uint32_t blk = 0; blk < nb; ++blk) {
+            const float2 v = *(const float2*)(part + ((slot * nb + blk) * 16 + n) * 8 + b0);
+            s0 += v.x;
+            s1 += v.y;
+        }
+        store_out(a, row, b0, s0, best0);
+        store_out(a, row, b0 + 1, s1, best1);
+    }
+    fold_argmax(a, lds, L, b0, best0);
+    fold_argmax(a, lds, L, b0 + 1, best1);
+    finish_argmax(a, lds, L);
+}
 #undef RLQ_MV_PROLOGUE
 
 // ---------------------------------------------------------------------------
@@ -2039,6 +2161,38 @@ static hipError_t launch_ks(const MvArgs& a, hipStream_t s, uint32_t pairs) {
     const uint32_t tstride = grid * TS, tmax = (a.ntiles + tstride - 1) / tstride;
     const size_t lds = ks_lds_bytes(T, a.cols, a.batch, tmax, TS, KS);
     if (lds > kMaxLds || (a.am_out && grid > kArgmaxMaxGrid)) return hipErrorInvalidValue;
+    if (lds > lds_set) {
+        const hipError_t e = hipFuncSetAttribute((const void*)kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                 (int)lds);
+        if (e != hipSuccess) return e;
+        lds_set = lds;
+    }
+    hipLaunchKernelGGL(kernel, dim3(grid, gy), dim3(W * 64), lds, s, a);
+    return hipGetLastError();
+}
+
+// The K-split Q8_0 kernel: taken when one workgroup's tile slots hold one
+// tile each (a few hundred tiles) and their parked block terms fit LDS.
+template <int W, int KS>
+static bool q8_0_ks_takes(const MvArgs& a, uint32_t pairs) {
+    constexpr int TS = W / KS;
+    const uint32_t gy = grid_rows(a, pairs);
+    const uint32_t grid = grid_cols((a.ntiles + TS - 1) / TS, (uint32_t)kSmallWgPerCu * (uint32_t)device_cus(), gy);
+    const uint64_t tmax = (a.ntiles + (uint64_t)grid * TS - 1) / ((uint64_t)grid * TS);
+    return tmax == 1 && ks_part_off(kQ8_0, a.cols, a.batch) + (uint64_t)TS * a.nb * 16 * 8 * 4 + TS * 4 <= kMaxLds;
+}
+
+template <int W, int KS, bool DBG>
+static hipError_t launch_q8_0_ks(const MvArgs& a, hipStream_t s, uint32_t pairs) {
+    constexpr int TS = W / KS;
+    static size_t lds_set = 64 * 1024;
+    auto kernel = q8_0_mv_ks_kernel<W, KS, 2, DBG>;
+    const uint32_t gy = grid_rows(a, pairs);
+    const uint32_t grid = grid_cols((a.ntiles + TS - 1) / TS, (uint32_t)kSmallWgPerCu * (uint32_t)device_cus(), gy);
+    const size_t lds = ks_part_off(kQ8_0, a.cols, a.batch) + (size_t)TS * a.nb * 16 * 8 * 4 + TS * 4;
+    if ((a.ntiles + (uint64_t)grid * TS - 1) / ((uint64_t)grid * TS) != 1 || lds > kMaxLds ||
+        (a.am_out && grid > kArgmaxMaxGrid))
+        return hipErrorInvalidValue;
     if (lds > lds_set) {
         const hipError_t e = hipFuncSetAttribute((const void*)kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
                                                  (int)lds);
@@ -2223,6 +2377,8 @@ hipError_t launch_matvec_ex(uint32_t wtype, const uint8_t* w, uint64_t rows, uin
                     return dbg ? launch_one(q6k_mv_kernel<W, 4, true>, a, lds, s, pairs)
                                : launch_one(q6k_mv_kernel<W, 4, false>, a, lds, s, pairs);
                 default:
+                    if (q8_0_ks_takes<8, 4>(a, pairs))
+                        return dbg ? launch_q8_0_ks<8, 4, true>(a, s, pairs) : launch_q8_0_ks<8, 4, false>(a, s, pairs);
                     return dbg ? launch_one(q8_0_mv_kernel<W, 8, true>, a, lds, s, pairs)
                                : launch_one(q8_0_mv_kernel<W, 8, false>, a, lds, s, pairs);
             }
