@@ -247,15 +247,21 @@ __global__ __launch_bounds__(kPvThreads) void attn_pv_kernel(
     const bool active = wave < hstep * wph;  // wave-uniform
     const uint32_t w = wave % wph, h0 = wave / wph, gstride = 64 * wph, g0 = 64 * w + lane;
     const float4* vsrc = (const float4*)(vc + v_cache_index(kvh, hd, d0, 0, max_context));
-    // the values of this lane's first groups (shared by every head of the kv head)
-    float4 vr[kPvRegGroups][4];
+    // the values of this lane's first groups (shared by every head of the kv
+    // head) and the first head's scores of those groups, loaded before the
+    // maxima are known
+    float4 vr[kPvRegGroups][4], sr[kPvRegGroups];
 #pragma unroll
-    for (uint32_t k = 0; k < kPvRegGroups; ++k)
+    for (uint32_t k = 0; k < kPvRegGroups; ++k) {
+        const uint32_t g = g0 + k * gstride;
+        sr[k] = active && h0 < G && g < ngroups ? *(const float4*)(scores + (uint64_t)(kvh * G + h0) * row_stride + 4 * g)
+                                                : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 #pragma unroll
         for (uint32_t j = 0; j < 4; ++j) {
-            const uint32_t t = 4 * (g0 + k * gstride) + j;
+            const uint32_t t = 4 * g + j;
             vr[k][j] = active && t < count ? vsrc[t] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         }
+    }
     // the row maxima: one wave per head over its chunk maxima
     for (uint32_t h = wave; h < G; h += kPvWaves) {
         float m = -INFINITY;
@@ -278,7 +284,7 @@ __global__ __launch_bounds__(kPvThreads) void attn_pv_kernel(
             for (uint32_t k = 0; k < kPvRegGroups; ++k) {
                 const uint32_t g = g0 + k * gstride;
                 float e[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-                if (g < ngroups) exp_group(*(const float4*)(srow + 4 * g), 4 * g, count, m, e);
+                if (g < ngroups) exp_group(h == h0 ? sr[k] : *(const float4*)(srow + 4 * g), 4 * g, count, m, e);
                 if (h == h0) {
 #pragma unroll
                     for (uint32_t j = 0; j < 4; ++j) er[k][j] = e[j];
