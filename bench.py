@@ -183,7 +183,7 @@ def call_distribution(rlq, ctx, handles, x, y, calls):
 def practical_peaks(torch, reps=20):
     """Measured ceilings beside the spec peaks: a 1 GiB device-to-device copy
     (bytes read + written per second), and torch's (hipBLASLt) dense f16 and
-    int8 GEMMs at 8192^3."""
+    int8 GEMMs at 8192^3 and at the prefill shape 512x4096x14336."""
     out = {}
 
     def timed(fn):
@@ -214,6 +214,21 @@ def practical_peaks(torch, reps=20):
     except (RuntimeError, AttributeError) as e:
         out["int8_gemm_tops"] = None
         out["int8_note"] = str(e).splitlines()[0][:120]
+    # the same library GEMMs at the prefill shape (M=512 tokens, K=4096, N=14336):
+    # the ceiling a dense, unquantized product of that shape reaches here
+    m, k, nn = PREFILL_M, 4096, 14336
+    a = torch.randn((m, k), device="cuda", dtype=torch.float16)
+    b = torch.randn((k, nn), device="cuda", dtype=torch.float16)
+    out["f16_gemm_prefill_shape_tflops"] = round(2 * m * k * nn / timed(lambda: torch.mm(a, b)) / 1e12, 1)
+    del a, b
+    try:
+        a8 = torch.randint(-127, 127, (m, k), device="cuda", dtype=torch.int8)
+        b8 = torch.randint(-127, 127, (k, nn), device="cuda", dtype=torch.int8)
+        out["int8_gemm_prefill_shape_tops"] = round(2 * m * k * nn / timed(lambda: torch._int_mm(a8, b8)) / 1e12, 1)
+        del a8, b8
+    except (RuntimeError, AttributeError) as e:
+        out["int8_gemm_prefill_shape_tops"] = None
+        out["int8_prefill_note"] = str(e).splitlines()[0][:120]
     torch.cuda.empty_cache()
     return out
 
