@@ -238,8 +238,8 @@ __host__ __device__ inline LdsMap lds_map(uint32_t t, uint32_t cols, uint32_t ba
     m.d_off = (m.S * batch + 15u) & ~15u;
     m.bs_off = m.d_off + nb * 32;
     m.zero_off = m.bs_off + (t == kQ4_K || t == kQ5_K || t == kQ2_K ? nb * 256 : 0);
-    m.red_off = m.zero_off + 256;
-    m.am_off = m.red_off + 128;  // argmax: 8 u64 keys, then the last-workgroup flag
+    m.red_off = m.zero_off + 256;  // f64 row sums of the RMSNorm: [wave][4], up to 16 waves
+    m.am_off = m.red_off + 512;    // argmax: 8 u64 keys, then the last-workgroup flag
     m.total = m.am_off + 80;
     return m;
 }
@@ -329,14 +329,13 @@ __device__ __forceinline__ float rms_scale(const MvArgs& a, uint8_t* lds, const 
 #pragma unroll
         for (int k = 0; k < 16; ++k) ss += (double)(v[k] * v[k]);
     }
-#pragma unroll
-    for (int m = 1; m < 64; m <<= 1) ss += __shfl_xor(ss, m, 64);
+    ss = row16_sum_f64(ss);
     double* red = (double*)(lds + L.red_off);
-    if (lane == 0) red[wave] = ss;
+    if ((lane & 15) == 0) red[wave * 4 + (lane >> 4)] = ss;
     __syncthreads();
     double total = 0.0;
 #pragma unroll
-    for (int w = 0; w < W; ++w) total += red[w];
+    for (int w = 0; w < 4 * W; ++w) total += red[w];
     const double n = (double)a.cols, err = n * 2.3e-16 * total;  // 2^-52 n sum, with a margin
     if ((float)((total - err) / n) != (float)((total + err) / n)) {  // every thread takes the same branch
         __syncthreads();  // every thread has read red[]
@@ -1124,14 +1123,13 @@ __device__ __forceinline__ float b1_rms_scale(const MvArgs& a, uint8_t* lds, con
 #pragma unroll
         for (int k = 0; k < 16; ++k) ss += (double)(v[k] * v[k]);
     }
-#pragma unroll
-    for (int m = 1; m < 64; m <<= 1) ss += __shfl_xor(ss, m, 64);
+    ss = row16_sum_f64(ss);
     double* red = (double*)(lds + L.red_off);
-    if ((threadIdx.x & 63) == 0) red[wave] = ss;
+    if ((threadIdx.x & 15) == 0) red[wave * 4 + ((threadIdx.x & 63) >> 4)] = ss;
     __syncthreads();
     double total = 0.0;
 #pragma unroll
-    for (int w = 0; w < W; ++w) total += red[w];
+    for (int w = 0; w < 4 * W; ++w) total += red[w];
     const double n = (double)a.cols, err = n * 2.3e-16 * total;
     if ((float)((total - err) / n) != (float)((total + err) / n)) {  // every thread takes the same branch
         __syncthreads();

@@ -101,6 +101,24 @@ __device__ __forceinline__ int32_t group8_sum(int32_t v) {
     return v;
 }
 
+// f64 moved by DPP: the two halves separately.
+template <int Ctrl>
+__device__ __forceinline__ double dpp_d(double v) {
+    const unsigned long long u = (unsigned long long)__double_as_longlong(v);
+    const uint32_t lo = (uint32_t)dpp_i<Ctrl>((int32_t)(uint32_t)u);
+    const uint32_t hi = (uint32_t)dpp_i<Ctrl>((int32_t)(uint32_t)(u >> 32));
+    return __longlong_as_double((long long)(((unsigned long long)hi << 32) | lo));
+}
+// Sum over each aligned row of 16 lanes in a fixed order; every lane of the
+// row gets it (DPP only: no LDS traffic).
+__device__ __forceinline__ double row16_sum_f64(double v) {
+    v += dpp_d<kQuadXor1>(v);
+    v += dpp_d<kQuadXor2>(v);
+    v += dpp_d<kRowHalfMirror>(v);
+    v += dpp_d<kRowRor8>(v);
+    return v;
+}
+
 // Sum over all 64 lanes; every lane gets it.
 __device__ __forceinline__ float wave_sum(float v) {
     v += dpp_f<kQuadXor1>(v);
