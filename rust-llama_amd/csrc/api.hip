@@ -570,9 +570,9 @@ int32_t rlq_mul_mat_id(rlq_context* ctx, const rlq_weights* w, uint32_t x_dtype,
 
 // Q4_K / Q5_K columns from this many per launch on are quantized once by the
 // planes kernel instead of in every workgroup's prologue (14336x4096 batch
-// 8: 14.0 us for both launches against 16.0 us fused; batch 4: 13.1 against
-// 12.8).
-constexpr uint64_t kPlanesMinBatch = 6;
+// 8: 13.1 us for both launches against 16.0 us fused; batch 4: 12.8 either
+// way).
+constexpr uint64_t kPlanesMinBatch = 5;
 
 // The decode launch of `batch` (<= 8) f32 columns: the fused kernels, or the
 // Q8_K planes kernel and then the matvec over the planes.

@@ -501,6 +501,59 @@ __device__ __forceinline__ bool stage_planes(const MvArgs& a, uint8_t* lds, cons
     return __syncthreads_or(bad) == 0;
 }
 
+// The planes of a K-format launch loaded before its weights, when they fit
+// kPlaneRegs uint4 of q8 per thread (batch * cols <= 64 W * 16 kPlaneRegs):
+// every staging load then precedes the weight loads, so its wait does not
+// wait for them (loads retire in order).  One float of d, one flag byte and
+// four bsums per thread.
+constexpr uint32_t kPlaneRegs = 4;
+struct PlanePrefetch {
+    uint4 q[kPlaneRegs];
+    float d;
+    uint32_t bad;
+    uint2 bs;
+};
+__host__ __device__ inline bool planes_fit(uint32_t threads, uint32_t batch, uint32_t cols, uint32_t nb) {
+    return batch * (cols / 16) <= kPlaneRegs * threads && batch * nb <= threads;
+}
+template <int W>
+__device__ __forceinline__ void prefetch_planes(const MvArgs& a, PlanePrefetch& p) {
+    const uint32_t tid = threadIdx.x, K = a.cols, upc = K / 16, units = a.batch * upc;
+#pragma unroll
+    for (uint32_t r = 0; r < kPlaneRegs; ++r) {
+        const uint32_t i = tid + r * W * 64;
+        p.q[r] = i < units ? *(const uint4*)(a.pre.q + (uint64_t)(i / upc) * K + (i % upc) * 16) : make_uint4(0, 0, 0, 0);
+    }
+    p.d = 0.0f;
+    p.bad = 0;
+    if (tid < a.batch * a.nb) {
+        p.d = a.pre.d[tid];
+        p.bad = a.pre.bad[tid];
+    }
+    p.bs = tid < units / 4 ? *(const uint2*)(a.pre.bsum + 4 * tid) : make_uint2(0, 0);
+}
+// stage_planes from the prefetched registers (Q8_K planes, quarter-ordered bsums)
+template <int W>
+__device__ __forceinline__ bool stage_planes_prefetched(const MvArgs& a, uint8_t* lds, const LdsMap& L,
+                                                        const PlanePrefetch& p) {
+    const uint32_t tid = threadIdx.x, K = a.cols, upc = K / 16, units = a.batch * upc, nb = a.nb;
+#pragma unroll
+    for (uint32_t r = 0; r < kPlaneRegs; ++r) {
+        const uint32_t i = tid + r * W * 64;
+        if (i < units) *(uint4*)(lds + (i / upc) * L.S + (i % upc) * 16) = p.q[r];
+    }
+    if (tid < a.batch * nb) *(float*)(lds + L.d_off + ((tid % nb) * 8 + tid / nb) * 4) = p.d;
+    if (tid < units / 4) {
+        const int16_t v[4] = {(int16_t)p.bs.x, (int16_t)(p.bs.x >> 16), (int16_t)p.bs.y, (int16_t)(p.bs.y >> 16)};
+#pragma unroll
+        for (uint32_t k = 0; k < 4; ++k) {
+            const uint32_t i = 4 * tid + k, b = i / upc, g = i % upc;
+            *(int16_t*)(lds + L.bs_off + ((g / 16) * 8 + b) * 32 + bs_slot(g % 16) * 2) = v[k];
+        }
+    }
+    return __syncthreads_or(p.bad != 0) == 0;
+}
+
 // ---------------------------------------------------------------------------
 // Per-tile epilogue shared by the three kernels: store y and fold the argmax.
 // ---------------------------------------------------------------------------
@@ -789,7 +842,8 @@ __host__ __device__ inline uint32_t ks_lds_bytes(uint32_t T, uint32_t cols, uint
     return ks_part_off(T, cols, batch) + tmax * ts * ks * 16u * 8u * 4u + tmax * ts * 4u;
 }
 
-template <uint32_t T, int W, int KS, int D, bool DBG>
+// PL: planes input that fits the prefetch registers (prefetch_planes).
+template <uint32_t T, int W, int KS, int D, bool DBG, bool PL>
 __global__ __launch_bounds__(W * 64) void q45_mv_ks_kernel(MvArgs a) {
     constexpr int TS = W / KS;
     if (!mv_enter(a)) return;
@@ -811,7 +865,9 @@ __global__ __launch_bounds__(W * 64) void q45_mv_ks_kernel(MvArgs a) {
     if (threadIdx.x < 16) *(uint4*)(lds + L.zero_off + threadIdx.x * 16) = make_uint4(0, 0, 0, 0);
     if (threadIdx.x < 8) ((unsigned long long*)(lds + L.am_off))[threadIdx.x] = 0ull;
     float xv[16];
-    prefetch_unit(a, wave, xv);
+    PlanePrefetch pp;
+    if constexpr (PL) prefetch_planes<W>(a, pp);
+    else prefetch_unit(a, wave, xv);
 
     const uint32_t kp0 = kp < nb ? kp : nb - 1;
     uint32_t ld_tile = t0 < ntiles ? t0 : ntiles - 1, ld_blk = kp0;
@@ -828,7 +884,9 @@ __global__ __launch_bounds__(W * 64) void q45_mv_ks_kernel(MvArgs a) {
     for (int i = 0; i < D; ++i) issue(buf[i]);
 
     // the counters' zeros are in place with the activations (one barrier)
-    const bool ok = a.x ? stage_q8k<W, kBsQuarters>(a, lds, L, wave, xv) : stage_planes<W>(a, lds, L, T);
+    bool ok;
+    if constexpr (PL) ok = stage_planes_prefetched<W>(a, lds, L, pp);
+    else ok = a.x ? stage_q8k<W, kBsQuarters>(a, lds, L, wave, xv) : stage_planes<W>(a, lds, L, T);
     if (!ok) return finish_argmax(a, lds, L);
     if (a.zero_pair) return zero_slot_tiles<W, TS>(a, tmax, tstride);
 
@@ -2145,11 +2203,11 @@ static hipError_t launch_b1_any(const MvArgs& a, bool dbg, bool full, hipStream_
 }
 
 // The K-split MFMA kernel for 3 to 8 columns: grid as launch_parked.
-template <uint32_t T, int W, int KS, int D, bool DBG>
-static hipError_t launch_ks(const MvArgs& a, hipStream_t s, uint32_t pairs) {
+template <uint32_t T, int W, int KS, int D, bool DBG, bool PL>
+static hipError_t launch_ks_pl(const MvArgs& a, hipStream_t s, uint32_t pairs) {
     constexpr int TS = W / KS;
     static size_t lds_set = 64 * 1024;
-    auto kernel = q45_mv_ks_kernel<T, W, KS, D, DBG>;
+    auto kernel = q45_mv_ks_kernel<T, W, KS, D, DBG, PL>;
     const uint32_t gy = grid_rows(a, pairs);
     uint32_t grid = grid_cols((a.ntiles + TS - 1) / TS, (uint32_t)kSmallWgPerCu * (uint32_t)device_cus(), gy);
     const size_t off = ks_part_off(T, a.cols, a.batch), per_tile = (size_t)TS * KS * 16u * 8u * 4u + TS * 4u;
@@ -2199,6 +2257,12 @@ static hipError_t launch_q8_0_ks(const MvArgs& a, hipStream_t s, uint32_t pairs)
     }
     hipLaunchKernelGGL(kernel, dim3(grid, gy), dim3(W * 64), lds, s, a);
     return hipGetLastError();
+}
+
+template <uint32_t T, int W, int KS, int D, bool DBG>
+static hipError_t launch_ks(const MvArgs& a, hipStream_t s, uint32_t pairs) {
+    return !a.x && planes_fit(W * 64, a.batch, a.cols, a.nb) ? launch_ks_pl<T, W, KS, D, DBG, true>(a, s, pairs)
+                                                             : launch_ks_pl<T, W, KS, D, DBG, false>(a, s, pairs);
 }
 
 // Q4_K / Q5_K: the VALU kernel for one or two columns, MFMA above.
