@@ -102,31 +102,6 @@ def gpu_weights(rlq, ctx, dtype, rows, cols, seed, copies):
     return handles, host0
 
 
-# GGUF block bytes and the offsets of the f16 super-block scales of the K
-# formats without a device encoder
-RANDOM_BLOCK = {10: (84, (80, 82)), 11: (110, (108,)), 13: (176, (0, 2))}
-
-
-def gpu_random_blocks(rlq, ctx, dtype, rows, cols, seed, copies):
-    """GGUF blocks with random quants and scales and f16 super-scales in
-    [2^-14, 2^-6], generated on the GPU (Q2_K, Q3_K, Q5_K)."""
-    torch = rlq.torch
-    ts, halves = RANDOM_BLOCK[int(dtype)]
-    nblk = rows * (cols // 256)
-    g = torch.Generator(device="cuda")
-    handles = []
-    for c in range(copies):
-        g.manual_seed(seed + 1000 * c)
-        b = torch.randint(0, 256, (nblk, ts), generator=g, device="cuda", dtype=torch.uint8)
-        for off in halves:
-            h = (torch.rand(nblk, generator=g, device="cuda") * (2.0 ** -6 - 2.0 ** -14) + 2.0 ** -14).half()
-            b[:, off:off + 2] = h.view(torch.uint8).view(nblk, 2)
-        torch.cuda.synchronize()
-        handles.append(rlq.Weights(ctx, dtype, b.view(-1), rows, cols))
-        del b
-    return handles, None
-
-
 def algorithmic_bytes(rlq, dtype, rows, cols, batch):
     return rlq.row_bytes(dtype, cols) * rows + 4 * cols * batch + 4 * rows * batch
 
@@ -287,8 +262,7 @@ def cpu_baseline(dtype, w_host, rows, cols, x_host, budget_s=10.0, all_cores_s=5
 
 def run_config(rlq, ctx, dtype, rows, cols, batch, seed, steps, warmup, copies, argmax=False):
     torch = rlq.torch
-    make = gpu_random_blocks if int(dtype) in RANDOM_BLOCK else gpu_weights
-    handles, host0 = make(rlq, ctx, dtype, rows, cols, seed, copies)
+    handles, host0 = gpu_weights(rlq, ctx, dtype, rows, cols, seed, copies)
     g = torch.Generator(device="cuda")
     g.manual_seed(seed + 7)
     x = torch.randn((batch, cols), generator=g, device="cuda", dtype=torch.float32)

@@ -128,9 +128,8 @@ int32_t rlq_matvec_activation_dtype(uint32_t weights_type, uint32_t *out, rlq_er
 /* ---- host drop-ins (synchronous, default context) ------------------------ */
 
 /* quantize_into (crates/quant/src/encode.rs:37-100): Q8_0 / Q8_K activation
- * quantizers and the Q4_K / Q6_K / Q8_0 weight encoders
- * (crates/quant/src/encode_k.rs:11-33, 430-561), run on the GPU.  The Q2_K,
- * Q3_K and Q5_K encoders return RLQ_UNIMPLEMENTED (weights arrive encoded). */
+ * quantizers and the Q8_0 and Q2_K..Q6_K weight encoders
+ * (crates/quant/src/encode_k.rs:11-561), run on the GPU. */
 int32_t rlq_quantize_into(uint32_t dtype, const float *values, uint64_t n, uint8_t *out, uint64_t out_len,
                           rlq_error *err);
 
@@ -258,7 +257,7 @@ int32_t rlq_mul_mat_id(rlq_context *ctx, const rlq_weights *w, uint32_t x_dtype,
                        uint64_t tokens, const int32_t *ids, uint64_t slots, float *y, void *stream, rlq_error *err);
 
 /* Device quantize_into (crates/quant/src/encode.rs:37-100): the activation
- * quantizers (Q8_0, Q8_K) and the weight encoders (Q8_0, Q4_K, Q6_K), GGUF
+ * quantizers (Q8_0, Q8_K) and the weight encoders (Q8_0, Q2_K..Q6_K), GGUF
  * bytes of `batch` rows of `cols` values each.  x and out are device
  * pointers.  For the K encoders a NonFiniteInput index counts over all
  * batch*cols values and UnrepresentableScale over all blocks (b = 0). */

@@ -687,7 +687,7 @@ int32_t rlq_quantize_device(rlq_context* ctx, uint32_t dtype, const float* x, ui
                             uint8_t* out, void* stream, rlq_error* err) {
     if (!ctx) return fail(err, RLQ_INVALID_ARGUMENT);
     if (!dtype_known(dtype)) return fail(err, RLQ_INVALID_TYPE, dtype);
-    if (dtype != kQ8_K && dtype != kQ8_0 && dtype != kQ4_K && dtype != kQ6_K) return fail(err, RLQ_UNIMPLEMENTED, dtype);
+    if (dtype != kQ8_K && !path_weight(dtype)) return fail(err, RLQ_UNIMPLEMENTED, dtype);
     uint64_t rb, n;
     int32_t rc = row_bytes(dtype, cols, &rb, err);
     if (rc) return rc;
@@ -702,7 +702,7 @@ int32_t rlq_quantize_device(rlq_context* ctx, uint32_t dtype, const float* x, ui
     else {
         // the K encoders see the rows as one run of blocks (rows are whole blocks)
         HIP_TRY(launch_finite_scan(x, n, ew, s));
-        HIP_TRY(dtype == kQ4_K ? launch_encode_q4k(x, n, out, ew, s) : launch_encode_q6k(x, n, out, ew, s));
+        HIP_TRY(launch_encode_k(dtype, x, n, out, ew, s));
     }
     return ok(err);
 }
@@ -1155,7 +1155,7 @@ int32_t rlq_quantize_into(uint32_t dtype, const float* values, uint64_t n, uint8
     // supported() (encode.rs:102-113)
     if (dtype == 16 || dtype == 17 || dtype == 19) return fail(err, RLQ_IMPORTANCE_WEIGHTS_REQUIRED, dtype);
     if (dtype == 24 || dtype == 25 || dtype == 26 || dtype == 27) return fail(err, RLQ_UNSUPPORTED_QUANTIZATION, dtype);
-    if (dtype != kQ8_0 && dtype != kQ8_K && dtype != kQ4_K && dtype != kQ6_K) return fail(err, RLQ_UNIMPLEMENTED, dtype);
+    if (dtype != kQ8_K && !path_weight(dtype)) return fail(err, RLQ_UNIMPLEMENTED, dtype);
     if (n == 0) return ok(err);
     if (!values || !out) return fail(err, RLQ_INVALID_ARGUMENT, dtype);
     std::lock_guard<std::mutex> lock(g_default_mu);
@@ -1174,7 +1174,7 @@ int32_t rlq_quantize_into(uint32_t dtype, const float* values, uint64_t n, uint8
     else if (dtype == kQ8_0) HIP_TRY(launch_quantize_q8_0(xd, n, 1, nullptr, od, ew, s));
     else {
         HIP_TRY(launch_finite_scan(xd, n, ew, s));
-        HIP_TRY(dtype == kQ4_K ? launch_encode_q4k(xd, n, od, ew, s) : launch_encode_q6k(xd, n, od, ew, s));
+        HIP_TRY(launch_encode_k(dtype, xd, n, od, ew, s));
     }
     rc = take_error(ctx, 1, s, dtype, err);
     if (rc) {

@@ -4,7 +4,9 @@
 //   Q8_K activation  crates/quant/src/activation.rs:4-51
 //   Q8_0             crates/quant/src/encode.rs:115-126 (scale), 151-192 (block),
 //                    preflight encode.rs:79-90
-//   Q4_K / Q6_K      crates/quant/src/encode_k.rs:37-137, 189-279, 410-561
+//   K encoders       crates/quant/src/encode_k.rs:37-561 (Q2_K 292-355,
+//                    Q3_K 138-185 and 357-409, Q4_K / Q5_K 410-507, Q6_K
+//                    70-137 and 508-561, make_qkx2_quants 189-279)
 //   decoders         crates/quant/src/decode.rs:17-49, 205-258
 // Compiled with -ffp-contract=off, so every f32 expression below rounds step
 // by step as the Rust source does; division and sqrt are correctly rounded
@@ -264,9 +266,14 @@ __device__ __forceinline__ int32_t clampi(int32_t v, int32_t lo, int32_t hi) {
     return v < lo ? lo : (v > hi ? hi : v);
 }
 
-// make_qkx2_quants restatement, encode_k.rs:189-279 (use_mad = false).
+// make_qkx2_quants restatement, encode_k.rs:189-279; MAD selects the
+// weighted absolute error (Q2_K) over the weighted squared error.
 // Returns false on the reference's Err(()).
-template <int N>
+template <bool MAD>
+__device__ __forceinline__ float fit_error(float difference) {
+    return MAD ? fabsf(difference) : difference * difference;
+}
+template <int N, bool MAD>
 __device__ bool make_affine2(const float (&x)[N], int32_t nmax, const float (&weights)[N], int32_t (&levels)[N],
                              float rmin, float rdelta, int steps, float& scale_out, float& min_out) {
     float minimum = x[0], maximum = x[0];
@@ -298,7 +305,7 @@ __device__ bool make_affine2(const float (&x)[N], int32_t nmax, const float (&we
         ok &= nearest(inverse * (x[i] - minimum), l);
         levels[i] = clampi(l, 0, nmax);
         const float difference = scale * (float)levels[i] + minimum - x[i];
-        best_error += weights[i] * (difference * difference);
+        best_error += weights[i] * fit_error<MAD>(difference);
     }
     if (!ok) return false;
     for (int step = 0; step <= steps; ++step) {
@@ -328,9 +335,8 @@ __device__ bool make_affine2(const float (&x)[N], int32_t nmax, const float (&we
             float error = 0.0f;
 #pragma unroll
             for (int i = 0; i < N; ++i) {
-                float difference = candidate_scale * (float)candidate[i] + candidate_minimum - x[i];
-                difference = difference * difference;
-                error += weights[i] * difference;
+                const float difference = candidate_scale * (float)candidate[i] + candidate_minimum - x[i];
+                error += weights[i] * fit_error<MAD>(difference);
             }
             if (error < best_error) {
 #pragma unroll
@@ -347,9 +353,14 @@ __device__ bool make_affine2(const float (&x)[N], int32_t nmax, const float (&we
     return true;
 }
 
-// Q4_K: 8 lanes per super-block (one 32-value sub-block each), 8 blocks a WG.
-__global__ __launch_bounds__(64) void encode_q4k_kernel(const float* __restrict__ x, uint64_t nblocks,
-                                                        uint8_t* __restrict__ out, unsigned long long* err_word) {
+// Q4_K / Q5_K (encode_k.rs:430-507): 8 lanes per super-block (one 32-value
+// sub-block each), 8 blocks a WG.  Q5_K: levels 0..31 (rmin -0.5, 15 steps),
+// the fifth bits in bytes 16..47 and the nibbles from byte 48 (176 bytes).
+template <bool FIVE>
+__global__ __launch_bounds__(64) void encode_q45k_kernel(const float* __restrict__ x, uint64_t nblocks,
+                                                         uint8_t* __restrict__ out, unsigned long long* err_word) {
+    constexpr int32_t kNmax = FIVE ? 31 : 15;
+    constexpr uint32_t kBytes = FIVE ? 176 : 144, kQs = FIVE ? 48 : 16;
     __shared__ uint8_t lv[8][256];
     const uint32_t lane = threadIdx.x, gb = lane >> 3, sub = lane & 7;
     const uint64_t blk = (uint64_t)blockIdx.x * 8 + gb;
@@ -372,7 +383,7 @@ __global__ __launch_bounds__(64) void encode_q4k_kernel(const float* __restrict_
     for (int i = 0; i < 32; ++i) weights[i] = average + fabsf(xs[i]);
     int32_t levels[32];
     float scale = 0.0f, minimum = 0.0f;
-    if (ok) ok &= make_affine2<32>(xs, 15, weights, levels, -1.0f, 0.1f, 20, scale, minimum);
+    if (ok) ok &= make_affine2<32, false>(xs, kNmax, weights, levels, FIVE ? -0.5f : -1.0f, 0.1f, FIVE ? 15 : 20, scale, minimum);
 
     // maximum_scale / maximum_minimum: strict `>` from +0.0 (encode_k.rs:454-459)
     float ms = scale > 0.0f ? scale : 0.0f, mm = minimum > 0.0f ? minimum : 0.0f;
@@ -425,7 +436,7 @@ __global__ __launch_bounds__(64) void encode_q4k_kernel(const float* __restrict_
         for (int i = 0; i < 32; ++i) {
             int32_t l = 0;
             ok &= nearest((xs[i] + minimum2) / scale2, l);
-            levels[i] = clampi(l, 0, 15);
+            levels[i] = clampi(l, 0, kNmax);
         }
     }
 #pragma unroll
@@ -436,7 +447,7 @@ __global__ __launch_bounds__(64) void encode_q4k_kernel(const float* __restrict_
     __syncthreads();
     if (!active) return;
     if (!okw && sub == 0) report_error(err_word, error_key(0, kKindScale, blk));
-    uint8_t* o = out + blk * 144;
+    uint8_t* o = out + blk * kBytes;
     if (sub == 0) {
         o[0] = (uint8_t)(dh & 0xff);
         o[1] = (uint8_t)(dh >> 8);
@@ -450,16 +461,21 @@ __global__ __launch_bounds__(64) void encode_q4k_kernel(const float* __restrict_
     for (int k = 0; k < 16; ++k) {
         const int byte = sub * 16 + k, group = byte / 32, j = byte % 32;
         const uint8_t low = lv[gb][group * 64 + j], high = lv[gb][group * 64 + j + 32];
-        o[16 + byte] = (uint8_t)((low & 15) | ((high & 15) << 4));
+        o[kQs + byte] = (uint8_t)((low & 15) | ((high & 15) << 4));
     }
-}
-
-hipError_t launch_encode_q4k(const float* x, uint64_t n, uint8_t* out, unsigned long long* err_word,
-                             hipStream_t s) {
-    const uint64_t nb = n / 256;
-    if (nb == 0) return hipSuccess;
-    hipLaunchKernelGGL(encode_q4k_kernel, dim3((unsigned)((nb + 7) / 8)), dim3(64), 0, s, x, nb, out, err_word);
-    return hipGetLastError();
+    if constexpr (FIVE) {
+        // fifth-bit bytes sub*4 .. +3: bit 2g of byte j from level 64g + j,
+        // bit 2g + 1 from level 64g + j + 32
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int j = sub * 4 + k;
+            uint32_t h = 0;
+#pragma unroll
+            for (int g = 0; g < 4; ++g)
+                h |= (lv[gb][g * 64 + j] > 15 ? 1u : 0u) << (2 * g) | (lv[gb][g * 64 + j + 32] > 15 ? 2u : 0u) << (2 * g);
+            o[16 + j] = (uint8_t)h;
+        }
+    }
 }
 
 // make_qx with rmse = 1 and no importance weights, encode_k.rs:70-137.
@@ -602,11 +618,253 @@ __global__ __launch_bounds__(64) void encode_q6k_kernel(const float* __restrict_
     }
 }
 
-hipError_t launch_encode_q6k(const float* x, uint64_t n, uint8_t* out, unsigned long long* err_word,
-                             hipStream_t s) {
+// Q2_K (encode_k.rs:292-355): 16 lanes per super-block (one 16-value
+// sub-block each), 4 blocks a WG.  Scales and minima are 4-bit against the
+// f16 d (byte 80) and dmin (byte 82); levels 0..3, two bits each from byte 16.
+__global__ __launch_bounds__(64) void encode_q2k_kernel(const float* __restrict__ x, uint64_t nblocks,
+                                                        uint8_t* __restrict__ out, unsigned long long* err_word) {
+    __shared__ uint8_t lv[4][256];
+    const uint32_t lane = threadIdx.x, gb = lane >> 4, sub = lane & 15;
+    const uint64_t blk = (uint64_t)blockIdx.x * 4 + gb;
+    const bool active = blk < nblocks;
+    float xs[16], weights[16];
+#pragma unroll
+    for (int i = 0; i < 16; i += 4) {
+        float4 v = active ? *(const float4*)(x + blk * 256 + sub * 16 + i) : make_float4(0, 0, 0, 0);
+        xs[i] = v.x, xs[i + 1] = v.y, xs[i + 2] = v.z, xs[i + 3] = v.w;
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) weights[i] = fabsf(xs[i]);
+    int32_t levels[16];
+    float scale = 0.0f, minimum = 0.0f;
+    bool ok = make_affine2<16, true>(xs, 3, weights, levels, -0.5f, 0.1f, 15, scale, minimum);
+
+    // maximum_scale / maximum_minimum: strict `>` from +0.0 (encode_k.rs:313-318)
+    float ms = scale > 0.0f ? scale : 0.0f, mm = minimum > 0.0f ? minimum : 0.0f;
+    for (int k = 1; k < 16; k <<= 1) {
+        const float os = __shfl_xor(ms, k, 16), om = __shfl_xor(mm, k, 16);
+        ms = os > ms ? os : ms;
+        mm = om > mm ? om : mm;
+    }
+    // the scale byte: `nearest(..) as u8`, then `|= (nearest(..) as u8) << 4`
+    uint32_t sbyte = 0, dh = 0, mh = 0;
+    if (ms > 0.0f) {
+        int32_t l = 0;
+        ok &= nearest(15.0f / ms * scale, l);
+        sbyte = (uint8_t)l;
+        dh = float_to_half_bits(ms / 15.0f);
+        ok &= (dh & 0x7c00u) != 0x7c00u;
+    }
+    if (mm > 0.0f) {
+        int32_t l = 0;
+        ok &= nearest(15.0f / mm * minimum, l);
+        sbyte |= (uint8_t)((uint8_t)l << 4);
+        mh = float_to_half_bits(mm / 15.0f);
+        ok &= (mh & 0x7c00u) != 0x7c00u;
+    }
+    const float scale2 = half_bits_to_float_exact(dh) * (float)(sbyte & 15);
+    if (scale2 != 0.0f) {
+        const float minimum2 = half_bits_to_float_exact(mh) * (float)(sbyte >> 4);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            int32_t l = 0;
+            ok &= nearest((xs[i] + minimum2) / scale2, l);
+            levels[i] = clampi(l, 0, 3);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) lv[gb][sub * 16 + i] = (uint8_t)levels[i];
+    int okw = ok ? 1 : 0;
+    for (int k = 1; k < 16; k <<= 1) okw &= __shfl_xor(okw, k, 16);
+    __syncthreads();
+    if (!active) return;
+    if (!okw && sub == 0) report_error(err_word, error_key(0, kKindScale, blk));
+    uint8_t* o = out + blk * 84;
+    o[sub] = (uint8_t)sbyte;
+    // two-bit bytes sub*4 .. +3 (pack_two_bits, encode_k.rs:347-355)
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const int byte = sub * 4 + k, g = byte / 32, j = byte % 32;
+        const uint8_t* L = lv[gb] + g * 128 + j;
+        o[16 + byte] = (uint8_t)(L[0] | (L[32] << 2) | (L[64] << 4) | (L[96] << 6));
+    }
+    if (sub == 0) {
+        o[80] = (uint8_t)(dh & 0xff);
+        o[81] = (uint8_t)(dh >> 8);
+        o[82] = (uint8_t)(mh & 0xff);
+        o[83] = (uint8_t)(mh >> 8);
+    }
+}
+
+// make_q3 (encode_k.rs:138-185): signed levels -nmax .. nmax - 1 fitted to
+// x with weights x^2, then up to five passes of single-level moves that
+// raise (sum w l x)^2 / sum w l^2, then shifted to 0 .. 2 nmax - 1.
+__device__ bool make_q3_levels(const float (&x)[16], int32_t nmax, int32_t (&levels)[16], float& scale_out) {
+    float maximum = 0.0f, magnitude = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+        if (fabsf(x[i]) > magnitude) {
+            magnitude = fabsf(x[i]);
+            maximum = x[i];
+        }
+    if (magnitude < 1e-15f) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) levels[i] = 0;
+        scale_out = 0.0f;
+        return true;
+    }
+    const float inverse = (float)(-nmax) / maximum;
+    float sum_lx = 0.0f, sum_l2 = 0.0f;
+    bool ok = true;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        int32_t l = 0;
+        ok &= nearest(inverse * x[i], l);
+        l = clampi(l, -nmax, nmax - 1);
+        levels[i] = l;
+        const float w = x[i] * x[i];
+        sum_lx += w * x[i] * (float)l;
+        sum_l2 += w * (float)l * (float)l;
+    }
+    if (!ok || !finite(sum_lx) || !finite(sum_l2)) return false;
+    for (int pass = 0; pass < 5; ++pass) {
+        bool changed = false;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const float v = x[i], w = v * v;
+            float lx = sum_lx - w * v * (float)levels[i];
+            if (lx > 0.0f) {
+                float l2 = sum_l2 - w * (float)levels[i] * (float)levels[i];
+                int32_t next = 0;
+                if (!nearest(v * l2 / lx, next)) return false;
+                next = clampi(next, -nmax, nmax - 1);
+                if (next != levels[i]) {
+                    lx += w * v * (float)next;
+                    l2 += w * (float)next * (float)next;
+                    if (l2 > 0.0f && lx * lx * sum_l2 > sum_lx * sum_lx * l2) {
+                        levels[i] = next;
+                        sum_lx = lx;
+                        sum_l2 = l2;
+                        changed = true;
+                    }
+                }
+            }
+        }
+        if (!changed) break;
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) levels[i] += nmax;
+    const float scale = sum_l2 > 0.0f ? sum_lx / sum_l2 : 0.0f;
+    if (!finite(scale)) return false;
+    scale_out = scale;
+    return true;
+}
+
+// Q3_K (encode_k.rs:357-409): 16 lanes per super-block (one 16-value
+// sub-block each), 4 blocks a WG.  Bytes 0..31 hold the third bit of each
+// level (bit j / 32 of byte j % 32), 32..95 the low two bits, 96..107 the
+// signed 6-bit scales (+32), 108 the f16 d.
+__global__ __launch_bounds__(64) void encode_q3k_kernel(const float* __restrict__ x, uint64_t nblocks,
+                                                        uint8_t* __restrict__ out, unsigned long long* err_word) {
+    __shared__ uint8_t lv[4][256];
+    const uint32_t lane = threadIdx.x, gb = lane >> 4, sub = lane & 15, base = lane & ~15u;
+    const uint64_t blk = (uint64_t)blockIdx.x * 4 + gb;
+    const bool active = blk < nblocks;
+    float xs[16];
+#pragma unroll
+    for (int i = 0; i < 16; i += 4) {
+        float4 v = active ? *(const float4*)(x + blk * 256 + sub * 16 + i) : make_float4(0, 0, 0, 0);
+        xs[i] = v.x, xs[i + 1] = v.y, xs[i + 2] = v.z, xs[i + 3] = v.w;
+    }
+    int32_t levels[16];
+    float scale = 0.0f;
+    bool ok = make_q3_levels(xs, 4, levels, scale);
+
+    // first sub-block of largest |scale| (strict `>` from 0, encode_k.rs:367-370)
+    uint64_t key = fabsf(scale) > 0.0f ? (((uint64_t)__float_as_uint(fabsf(scale)) << 32) | (15u - sub)) : 0;
+    for (int k = 1; k < 16; k <<= 1) {
+        const uint64_t o = __shfl_xor(key, k, 16);
+        key = o > key ? o : key;
+    }
+    const int winner = key ? (int)(15u - (uint32_t)(key & 0xffffffffu)) : 0;
+    const float maximum_scale = key ? __shfl(scale, (int)base + winner, 64) : 0.0f;
+
+    // the scale's byte value l + 32 (0 when every scale is 0, d = 0)
+    int32_t u = 0;
+    uint32_t dh = 0;
+    if (maximum_scale != 0.0f) {
+        const float inverse = -32.0f / maximum_scale;
+        int32_t l = 0;
+        ok &= nearest(inverse * scale, l);
+        u = clampi(l, -32, 31) + 32;
+        dh = float_to_half_bits(1.0f / inverse);
+        ok &= (dh & 0x7c00u) != 0x7c00u;
+    }
+    const float scale2 = half_bits_to_float_exact(dh) * (float)(u - 32);
+    if (scale2 != 0.0f) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            int32_t l = 0;
+            ok &= nearest(xs[i] / scale2, l);
+            levels[i] = clampi(l, -4, 3) + 4;
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) lv[gb][sub * 16 + i] = (uint8_t)levels[i];
+    // the scale bytes' inputs from the other lanes of the block
+    const int32_t u_hi = __shfl(u, (int)(base + ((sub + 8) & 15)), 64);
+    int32_t u_top[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) u_top[q] = __shfl(u, (int)(base + (sub & 3) + 4 * q), 64);
+    int okw = ok ? 1 : 0;
+    for (int k = 1; k < 16; k <<= 1) okw &= __shfl_xor(okw, k, 16);
+    __syncthreads();
+    if (!active) return;
+    if (!okw && sub == 0) report_error(err_word, error_key(0, kKindScale, blk));
+    uint8_t* o = out + blk * 110;
+    // third bits: bytes 2 sub, 2 sub + 1
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        const int j = sub * 2 + k;
+        uint32_t h = 0;
+#pragma unroll
+        for (int b = 0; b < 8; ++b) h |= (lv[gb][j + 32 * b] > 3 ? 1u : 0u) << b;
+        o[j] = (uint8_t)h;
+    }
+    // low two bits: bytes 32 + sub*4 .. +3 (pack_two_bits of the levels less 4)
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const int byte = sub * 4 + k, g = byte / 32, j = byte % 32;
+        const uint8_t* L = lv[gb] + g * 128 + j;
+        o[32 + byte] = (uint8_t)((L[0] & 3) | ((L[32] & 3) << 2) | ((L[64] & 3) << 4) | ((L[96] & 3) << 6));
+    }
+    if (sub < 8) {
+        o[96 + sub] = (uint8_t)((u & 15) | ((u_hi & 15) << 4));
+    } else if (sub < 12) {
+        uint32_t t = 0;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) t |= (uint32_t)(u_top[q] >> 4) << (2 * q);
+        o[104 + (sub - 8)] = (uint8_t)t;
+    } else if (sub == 12) {
+        o[108] = (uint8_t)(dh & 0xff);
+        o[109] = (uint8_t)(dh >> 8);
+    }
+}
+
+// All K encoders (encode_k.rs:11-33): n values as one run of n / 256 blocks.
+hipError_t launch_encode_k(uint32_t t, const float* x, uint64_t n, uint8_t* out, unsigned long long* err_word,
+                           hipStream_t s) {
     const uint64_t nb = n / 256;
     if (nb == 0) return hipSuccess;
-    hipLaunchKernelGGL(encode_q6k_kernel, dim3((unsigned)((nb + 3) / 4)), dim3(64), 0, s, x, nb, out, err_word);
+    const dim3 by8((unsigned)((nb + 7) / 8)), by4((unsigned)((nb + 3) / 4));
+    switch (t) {
+        case kQ2_K: hipLaunchKernelGGL(encode_q2k_kernel, by4, dim3(64), 0, s, x, nb, out, err_word); break;
+        case kQ3_K: hipLaunchKernelGGL(encode_q3k_kernel, by4, dim3(64), 0, s, x, nb, out, err_word); break;
+        case kQ4_K: hipLaunchKernelGGL(encode_q45k_kernel<false>, by8, dim3(64), 0, s, x, nb, out, err_word); break;
+        case kQ5_K: hipLaunchKernelGGL(encode_q45k_kernel<true>, by8, dim3(64), 0, s, x, nb, out, err_word); break;
+        case kQ6_K: hipLaunchKernelGGL(encode_q6k_kernel, by4, dim3(64), 0, s, x, nb, out, err_word); break;
+        default: return hipErrorInvalidValue;
+    }
     return hipGetLastError();
 }
 

@@ -38,11 +38,10 @@ hipError_t launch_quantize_q8k(const float* x, uint64_t cols, uint64_t batch, co
                                uint8_t* gguf, unsigned long long* err_word, hipStream_t s);
 hipError_t launch_quantize_q8_0(const float* x, uint64_t cols, uint64_t batch, const ActPlanes* planes,
                                 uint8_t* gguf, unsigned long long* err_word, hipStream_t s);
-// Weight encoders (encode_k.rs:430-561), GGUF bytes out, n % 256 == 0.
-hipError_t launch_encode_q4k(const float* x, uint64_t n, uint8_t* out, unsigned long long* err_word,
-                             hipStream_t s);
-hipError_t launch_encode_q6k(const float* x, uint64_t n, uint8_t* out, unsigned long long* err_word,
-                             hipStream_t s);
+// K weight encoders Q2_K..Q6_K (encode_k.rs:11-561), GGUF bytes out,
+// n % 256 == 0.
+hipError_t launch_encode_k(uint32_t t, const float* x, uint64_t n, uint8_t* out, unsigned long long* err_word,
+                           hipStream_t s);
 // GGUF activation bytes (Q8_K / Q8_0) -> planes, for pre-quantized inputs.
 hipError_t launch_act_from_gguf(uint32_t act_type, const uint8_t* gguf, uint64_t cols, uint64_t batch,
                                 const ActPlanes* planes, hipStream_t s);

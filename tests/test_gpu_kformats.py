@@ -92,6 +92,66 @@ def test_decoders_golden_bitwise():
         assert same.all(), t
 
 
+def test_encoders_golden_bitwise():
+    """The device Q2_K / Q3_K / Q5_K encoders (quantize.hip) reproduce the
+    reference's encoder records (encoders_extended.rs:27-63) byte for byte."""
+    for i, (t, x, expected) in enumerate(F.encoders(("encoder-extended-q2k-q3k-q5k.bin",))):
+        say("encoder record", i, t, x.size)
+        got = rlq.quantize(t, x)
+        assert np.array_equal(got, expected), (i, t, np.nonzero(got != expected)[0][:8])
+
+
+def edge_blocks(seed):
+    """Blocks of 256 values that reach each branch of the encoders: zeros,
+    constants of both signs, one spike, all-negative and all-positive
+    ramps, scales that round to a zero or subnormal f16, tiny and large
+    magnitudes, alternating signs, and Gaussian rows at 0.02 and 1."""
+    rng = np.random.default_rng(seed)
+    g = lambda s: rng.standard_normal(256).astype(np.float32) * np.float32(s)
+    spike = np.zeros(256, np.float32)
+    spike[7] = 1.0
+    half = g(1.0)
+    half[:128] = 0.0
+    alt = np.where(np.arange(256) % 2 == 0, 1e-3, -1e-3).astype(np.float32)
+    blocks = [np.zeros(256, np.float32), np.full(256, 0.5, np.float32), np.full(256, -0.5, np.float32), spike,
+              -np.linspace(0.01, 1.0, 256, dtype=np.float32), np.linspace(0.01, 1.0, 256, dtype=np.float32),
+              g(1e-8), g(1e-6), g(1e-30), np.abs(g(1.0)), -np.abs(g(1.0)), g(1e3), g(3e3), half, alt,
+              g(0.02), g(1.0)]
+    return np.concatenate(blocks + [g(0.02) for _ in range(15)])
+
+
+@pytest.mark.parametrize("t", K_OTHER)
+def test_encoders_against_oracle(ctx, t):
+    """Host and device encoders against the oracle's encoder (encode_k.rs),
+    bit for bit, on edge blocks and 64 Gaussian rows of 4096; then the
+    first UnrepresentableScale block and the first non-finite index."""
+    say("encoder vs oracle", t)
+    x = edge_blocks(70 + int(t))
+    want = O.quantize(int(t), x)
+    assert np.array_equal(rlq.quantize(t, x), want)
+    xr = np.random.default_rng(71).standard_normal(64 * 4096).astype(np.float32) * np.float32(0.02)
+    want_r = O.quantize(int(t), xr)
+    got_r = ctx.quantize(t, torch.from_numpy(xr.reshape(64, 4096)).cuda())
+    ctx.sync()
+    assert np.array_equal(got_r.cpu().numpy(), want_r)
+    # a block whose super-scale overflows f16, after two good blocks and
+    # before another overflowing one: block 2 is reported
+    bad = np.concatenate([x[:512], np.full(256, 1e9, np.float32) * np.sign(x[:256] + 0.5), x[:256] * 1e9])
+    with pytest.raises(O.OracleError) as oe:
+        O.quantize(int(t), bad)
+    with pytest.raises(rlq.QuantError) as e:
+        rlq.quantize(t, bad)
+    assert (e.value.name, e.value.block) == (oe.value.name, 2) == ("UnrepresentableScale", 2)
+    with pytest.raises(rlq.QuantError) as e:
+        ctx.quantize(t, torch.from_numpy(bad.reshape(2, 512)).cuda())
+        ctx.sync()
+    assert (e.value.name, e.value.block) == ("UnrepresentableScale", 2)
+    bad[700] = np.nan  # non-finite values are reported before any scale
+    with pytest.raises(rlq.QuantError) as e:
+        rlq.quantize(t, bad)
+    assert (e.value.name, e.value.index) == ("NonFiniteInput", 700)
+
+
 def test_matvec_golden_records():
     for i, r in enumerate(F.matvec_extended("matvec-extended-q2k-q3k-q5k.bin")):
         say("GGQX matvec", i, r.dtype, r.rows, r.cols)

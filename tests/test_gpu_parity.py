@@ -140,7 +140,8 @@ def test_block_sums_bit_exact(ctx, t, rows, cols, batch):
 
 def _q5k_blocks(rows, cols, seed):
     """GGUF Q5_K bytes of rows x cols: random quants and scales, f16 d and
-    dmin drawn from [2^-14, 2^-6] (there is no Q5_K encoder on the path)."""
+    dmin drawn from [2^-14, 2^-6] (they reach the high bits and sub-block
+    scales that encoded Gaussian rows rarely set)."""
     rng = np.random.default_rng(seed)
     nblk = rows * (cols // 256)
     b = rng.integers(0, 256, (nblk, 176), dtype=np.uint8)
