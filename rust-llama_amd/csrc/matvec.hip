@@ -1205,9 +1205,20 @@ __device__ __forceinline__ float b1_rms_scale(const MvArgs& a, uint8_t* lds, con
 // FULL: the decode step's extras (the RMSNorm input transform, the residual
 // add), the output checks of a model stage (chk) and the in-launch argmax;
 // without them none is compiled in.
-template <uint32_t T, int W, int KS, int D, bool DBG, bool FULL>
+// BAL deals the tiles out in equal shares of bytes per CU (otherwise they
+// are grid-strided over the tile slots): two workgroups of two tile slots per
+// CU, c = grid / 2, ntiles = u c / 2 with u in 6..8.  Workgroup g < c takes
+// tiles 2g and 2g + 1; workgroup c + h the rest of a CU's u half tiles: tile
+// 2c + h (u = 6, 7) or tiles 2c + 2h, 2c + 2h + 1 (u = 8), and for u = 7 rows
+// 8 (h & 1) .. + 7 of tile 3c + h / 2.  In that half tile lane row n loads and
+// computes row (n & 7) | 8 (h & 1), so lane pairs read the same bytes (one
+// fetch), and only the lanes of the own half store.  Every CU then streams
+// the same bytes (with the dispatcher's two workgroups per CU, one of each
+// kind); the row sums are those of the grid-strided deal, bit for bit.
+template <uint32_t T, int W, int KS, int D, bool DBG, bool FULL, bool BAL = false>
 __global__ __launch_bounds__(W * 64) void q45_mv_b1_kernel(MvArgs a) {
     constexpr int TS = W / KS;
+    static_assert(!BAL || TS == 2, "the balanced deal takes two tile slots");
     extern __shared__ __align__(16) uint8_t lds[];
     const LdsMap L = lds_map(T, a.cols, 1);
     float* part = (float*)(lds + small_part_off(a.cols, 1));
@@ -1216,8 +1227,39 @@ __global__ __launch_bounds__(W * 64) void q45_mv_b1_kernel(MvArgs a) {
     const uint32_t ts = wave / KS, kp = wave % KS;
     const uint32_t nb = a.nb, ntiles = a.ntiles;
     const uint32_t tstride = gridDim.x * TS, t0 = blockIdx.x * TS + ts;
-    const uint32_t tmax = (ntiles + tstride - 1) / tstride;
-    const uint32_t my_tiles = t0 < ntiles ? (ntiles - 1 - t0) / tstride + 1 : 0;
+    // the deal: this wave's tile count, the ordinal of its half tile (none:
+    // ~0), which half; tile_of(i) is tile i of its sequence
+    uint32_t tmax, my_tiles, half_ti = ~0u, hsel = 0, bt = 0;
+    if constexpr (BAL) {
+        const uint32_t c = gridDim.x / 2, u = 2 * ntiles / c;
+        tmax = 1;
+        my_tiles = 1;
+        if (blockIdx.x < c) {
+            bt = 2 * blockIdx.x + ts;
+        } else {
+            const uint32_t h = blockIdx.x - c;
+            if (u == 8) {
+                bt = 2 * c + 2 * h + ts;
+            } else if (ts == 0) {
+                bt = 2 * c + h;
+            } else if (u == 7) {
+                bt = 3 * c + h / 2, half_ti = 0, hsel = h & 1;
+            } else {
+                my_tiles = 0;
+            }
+        }
+    } else {
+        tmax = (ntiles + tstride - 1) / tstride;
+        my_tiles = t0 < ntiles ? (ntiles - 1 - t0) / tstride + 1 : 0;
+    }
+    auto tile_of = [&](uint32_t i) -> uint32_t {
+        if constexpr (BAL) return bt;
+        else return t0 + i * tstride;
+    };
+    // whether lane row n is this workgroup's row of tile i; the row a lane
+    // loads in the half tile
+    auto own_row = [&](uint32_t i) { return i != half_ti || (n >> 3) == hsel; };
+    const uint32_t nh = (n & 7) | (hsel << 3);
     const uint32_t bpt = kp < nb ? (nb - 1 - kp) / KS + 1 : 0;  // blocks of each tile this wave takes
     const uint32_t steps = my_tiles * bpt;
     const uint32_t nk = (uint32_t)KS < nb ? (uint32_t)KS : nb;  // waves of a tile that take blocks
@@ -1238,18 +1280,21 @@ __global__ __launch_bounds__(W * 64) void q45_mv_b1_kernel(MvArgs a) {
     if (rms && mine) load16(a.norm_w + xblk * 256 + r16 * 16, nw);
     const bool res_lane = FULL && a.resid && kp == 0 && kq < my_tiles;
     if (res_lane) {
-        const uint32_t row = (t0 + kq * tstride) * kTileRows + n;
+        const uint32_t row = tile_of(kq) * kTileRows + n;
         if (row < a.rows) res = a.resid[row];
     }
     const uint32_t kp0 = kp < nb ? kp : nb - 1;
     uint32_t ld_tile = t0 < ntiles ? t0 : ntiles - 1, ld_blk = kp0;
+    if constexpr (BAL) ld_tile = my_tiles ? bt : 0;
     Q4Step<T> buf[D];
     auto issue = [&](Q4Step<T>& st) {
-        q45_issue<T>(st, a.w + ((uint64_t)ld_tile * nb + ld_blk) * Q45<T>::chunk, lane, n, kq);
+        const uint8_t* base = a.w + ((uint64_t)ld_tile * nb + ld_blk) * Q45<T>::chunk;
+        if (BAL && half_ti == 0) q45_issue<T>(st, base, kq * 16 + nh, nh, kq);  // the half tile
+        else q45_issue<T>(st, base, lane, n, kq);
         ld_blk += KS;
         if (ld_blk >= nb) {
             ld_blk = kp0;
-            if (ld_tile + tstride < ntiles) ld_tile += tstride;
+            if (!BAL && ld_tile + tstride < ntiles) ld_tile += tstride;
         }
     };
 #pragma unroll
@@ -1296,7 +1341,7 @@ __global__ __launch_bounds__(W * 64) void q45_mv_b1_kernel(MvArgs a) {
     typedef short s2 __attribute__((ext_vector_type(2)));
     unsigned long long best = 0;
     float acc = 0.0f;
-    uint32_t ti = 0, blk = kp, j = 0, tile = t0;
+    uint32_t ti = 0, blk = kp, j = 0, tile = tile_of(0);
     // the K parts of slot sl added in K order
     auto sum_parts = [&](uint32_t sl) {
         float s = 0.0f;
@@ -1362,7 +1407,7 @@ __global__ __launch_bounds__(W * 64) void q45_mv_b1_kernel(MvArgs a) {
             M += __shfl_xor(M, 16, 64);
             M += __shfl_xor(M, 32, 64);
             const uint32_t row = tile * kTileRows + n;
-            if (kq == 0 && row < a.rows) {
+            if (kq == 0 && row < a.rows && own_row(ti)) {
                 a.dbg_isum[(uint64_t)row * nb + blk] = I;
                 a.dbg_imin[(uint64_t)row * nb + blk] = M;
             }
@@ -1386,16 +1431,16 @@ __global__ __launch_bounds__(W * 64) void q45_mv_b1_kernel(MvArgs a) {
             acc = 0.0f;
             j = 0;
             blk = kp;
-            ++ti;
-            tile += tstride;
+            tile = tile_of(++ti);
         }
     };
     pipeline<D>(steps, buf, issue, compute);
 
     // the tiles this wave completed: add their K parts in order and store
     for (uint32_t i = 0; i < my_tiles; ++i) {
-        const uint32_t slot = i * TS + ts, row = (t0 + i * tstride) * kTileRows + n;
-        if (cnt[slot] != nk + 1 + wave || kq != 0 || row >= a.rows) continue;  // (the mark is wave-uniform)
+        const uint32_t slot = i * TS + ts, row = tile_of(i) * kTileRows + n;
+        // (the mark is wave-uniform)
+        if (cnt[slot] != nk + 1 + wave || kq != 0 || row >= a.rows || !own_row(i)) continue;
         float s = sum_parts(slot);
         if (FULL && a.chk) check_finite(a, kChkOut, s);
         if (FULL && a.resid) {
@@ -2174,13 +2219,34 @@ static bool b1_takes(const MvArgs& a) {
     return grid > 0 && (!a.resid || tmax <= 4);
 }
 
-template <uint32_t T, int W, int KS, int D, bool DBG, bool FULL>
+// The balanced deal: two workgroups of two tile slots per CU, u = 2 ntiles /
+// CUs in 6..8 (14336 rows: 8.3 us against 8.5 grid-strided).
+static void b1_bal_grid(const MvArgs& a, uint32_t& grid, uint32_t& tmax) {
+    const uint32_t cus = (uint32_t)device_cus();
+    grid = tmax = 0;
+    if (cus == 0 || (2ull * a.ntiles) % cus != 0) return;
+    const uint64_t u = 2ull * a.ntiles / cus;
+    if (u < 6 || u > 8 || (u == 7 && cus % 2 != 0)) return;
+    grid = 2 * cus;
+    tmax = 1;
+}
+
+template <int W, int KS>
+static bool b1_bal_takes(const MvArgs& a) {
+    if (W / KS != 2 || a.nb > 4u * KS || a.epilogue != kEpStore) return false;
+    uint32_t grid, tmax;
+    b1_bal_grid(a, grid, tmax);
+    return grid > 0 && b1_lds_bytes(a.cols, tmax, 2, KS) <= kMaxLds;
+}
+
+template <uint32_t T, int W, int KS, int D, bool DBG, bool FULL, bool BAL = false>
 static hipError_t launch_b1(const MvArgs& a, hipStream_t s) {
     constexpr int TS = W / KS;
     static size_t lds_set = 64 * 1024;
-    auto kernel = q45_mv_b1_kernel<T, W, KS, D, DBG, FULL>;
+    auto kernel = q45_mv_b1_kernel<T, W, KS, D, DBG, FULL, BAL>;
     uint32_t grid, tmax;
-    b1_grid<W, KS>(a, grid, tmax);
+    if constexpr (BAL) b1_bal_grid(a, grid, tmax);
+    else b1_grid<W, KS>(a, grid, tmax);
     const size_t lds = b1_lds_bytes(a.cols, tmax, TS, KS);
     if (grid == 0 || lds > kMaxLds || (a.am_out && grid > kArgmaxMaxGrid) || (a.resid && tmax > 4))
         return hipErrorInvalidValue;
@@ -2194,12 +2260,12 @@ static hipError_t launch_b1(const MvArgs& a, hipStream_t s) {
     return hipGetLastError();
 }
 
-template <uint32_t T, int W, int KS>
+template <uint32_t T, int W, int KS, bool BAL = false>
 static hipError_t launch_b1_any(const MvArgs& a, bool dbg, bool full, hipStream_t s) {
-    return dbg ? (full ? launch_b1<T, W, KS, kSmallD, true, true>(a, s)
-                       : launch_b1<T, W, KS, kSmallD, true, false>(a, s))
-               : (full ? launch_b1<T, W, KS, kSmallD, false, true>(a, s)
-                       : launch_b1<T, W, KS, kSmallD, false, false>(a, s));
+    return dbg ? (full ? launch_b1<T, W, KS, kSmallD, true, true, BAL>(a, s)
+                       : launch_b1<T, W, KS, kSmallD, true, false, BAL>(a, s))
+               : (full ? launch_b1<T, W, KS, kSmallD, false, true, BAL>(a, s)
+                       : launch_b1<T, W, KS, kSmallD, false, false, BAL>(a, s));
 }
 
 // The K-split MFMA kernel for 3 to 8 columns: grid as launch_parked.
@@ -2271,7 +2337,8 @@ static hipError_t launch_q45(const MvArgs& a, uint32_t nbat, bool dbg, uint32_t 
                              uint32_t pairs) {
     // one f32 column: the batch-1 kernel (measured, Q4_K, us against the
     // shared-quantization kernel: 14336x4096 8.3 / 9.2 with two tile slots
-    // of a K split of 4; 6144x4096 5.5 / 6.6 likewise; 4096x4096 5.2 / 6.2
+    // of a K split of 4 in the balanced deal, 8.5 grid-strided; 6144x4096
+    // 5.5 / 6.6 with two slots, grid-strided; 4096x4096 5.2 / 6.2
     // with one slot of a split of 4; 4096x14336 9.6 / 10.6 with a split of
     // 16).  Its FULL variant takes the decode step's RMSNorm input and
     // residual, model checks and the argmax (Q/K/V 6144x4096 with RMSNorm
@@ -2284,6 +2351,7 @@ static hipError_t launch_q45(const MvArgs& a, uint32_t nbat, bool dbg, uint32_t 
         if (a.nb > 16) {
             if (b1_takes<16, 16>(a)) return launch_b1_any<T, 16, 16>(a, dbg, full, s);
         } else if (a.ntiles >= 384) {
+            if (b1_bal_takes<8, 4>(a)) return launch_b1_any<T, 8, 4, true>(a, dbg, full, s);
             if (b1_takes<8, 4>(a)) return launch_b1_any<T, 8, 4>(a, dbg, full, s);
         } else if (b1_takes<4, 4>(a)) {
             return launch_b1_any<T, 4, 4>(a, dbg, full, s);

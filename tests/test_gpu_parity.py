@@ -166,7 +166,11 @@ def _oracle_sums(t, w, rows, act, nb):
 @pytest.mark.parametrize("t,rows,cols,variant", [
     (DT.Q4_K, 4096, 4096, "batch-1 kernel, one tile slot, K split 4 (< 384 tiles)"),
     (DT.Q4_K, 6144, 4096, "batch-1 kernel, two tile slots, K split 4 (>= 384 tiles)"),
-    (DT.Q4_K, 14336, 4096, "batch-1 kernel, two tile slots, K split 4: the headline matvec"),
+    (DT.Q4_K, 12288, 4096, "batch-1 kernel, balanced deal, u = 6: one slot of every second workgroup idle"),
+    (DT.Q4_K, 14336, 4096, "batch-1 kernel, balanced deal, u = 7 (half tiles): the headline matvec"),
+    (DT.Q4_K, 14330, 4096, "balanced deal, u = 7, the last tile partial and dealt out in halves"),
+    (DT.Q4_K, 16384, 4096, "batch-1 kernel, balanced deal, u = 8"),
+    (DT.Q5_K, 14336, 4096, "Q5_K, batch-1 kernel, balanced deal, u = 7"),
     (DT.Q4_K, 4096, 14336, "batch-1 kernel, 16 waves, K split 16 (> 16 blocks)"),
     (DT.Q4_K, 333, 16384, "batch-1 kernel, K split 16 at 64 blocks: 4 blocks per wave, the most it takes"),
     (DT.Q4_K, 333, 18432, "72 blocks: the shared-quantization kernel, 16 waves, K split 16"),
@@ -334,18 +338,19 @@ def test_argmax_keys_across_calls(ctx):
 
 
 @pytest.mark.parametrize("t,rows,cols", [(DT.Q8_0, 9000, 896), (DT.Q6_K, 3000, 2048), (DT.Q4_K, 5000, 4096),
-                                         (DT.Q4_K, 9000, 2048)])
+                                         (DT.Q4_K, 9000, 2048), (DT.Q4_K, 14336, 4096)])
 def test_argmax_nan_rows(ctx, t, rows, cols):
     """The greedy scan (sampling.rs:607-618) starts from row 0 and keeps the
     first strict maximum: a NaN at row 0 is the answer (nothing compares
     greater), a NaN anywhere else never wins.  NaN logits come from a NaN f16
     scale in one row's first block.  Batches 1 and 3, over the in-launch
-    argmax of the decode kernels."""
+    argmax of the decode kernels (at 14336 rows also a NaN in a tile that the
+    batch-1 kernel deals out in halves)."""
     say("argmax with NaN logits", t, rows, cols)
     w = _weights(t, rows, cols, 88)
     rb = w.size // rows
     dpos = {DT.Q8_0: 0, DT.Q6_K: 208, DT.Q4_K: 0}[t]  # the f16 d of block 0
-    for nan_row in (0, 1234):
+    for nan_row in (0, 1234) + ((rows - 300,) if rows > 12288 else ()):
         wn = w.copy()
         wn[nan_row * rb + dpos:nan_row * rb + dpos + 2] = np.array([0x7E00], np.uint16).view(np.uint8)
         W = rlq.Weights(ctx, t, wn, rows, cols)
