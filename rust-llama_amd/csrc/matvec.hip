@@ -153,6 +153,9 @@ struct MvArgs {
     // and every data error becomes a model_key of layer chk_layer; chk 0
     // keeps the quantizers' own QuantError keys
     uint32_t chk, chk_layer;
+    // The batch-1 kernel's balanced deal over this many CUs (0: the tiles
+    // are grid-strided)
+    uint32_t deal_cus;
 };
 
 // the fields of chk, in the order of mv_chk's arguments
@@ -1206,19 +1209,19 @@ __device__ __forceinline__ float b1_rms_scale(const MvArgs& a, uint8_t* lds, con
 // add), the output checks of a model stage (chk) and the in-launch argmax;
 // without them none is compiled in.
 // BAL deals the tiles out in equal shares of bytes per CU (otherwise they
-// are grid-strided over the tile slots): two workgroups of two tile slots per
-// CU, c = grid / 2, ntiles = u c / 2 with u in 6..8.  Workgroup g < c takes
-// tiles 2g and 2g + 1; workgroup c + h the rest of a CU's u half tiles: tile
-// 2c + h (u = 6, 7) or tiles 2c + 2h, 2c + 2h + 1 (u = 8), and for u = 7 rows
-// 8 (h & 1) .. + 7 of tile 3c + h / 2.  In that half tile lane row n loads and
-// computes row (n & 7) | 8 (h & 1), so lane pairs read the same bytes (one
-// fetch), and only the lanes of the own half store.  Every CU then streams
-// the same bytes (with the dispatcher's two workgroups per CU, one of each
-// kind); the row sums are those of the grid-strided deal, bit for bit.
+// are grid-strided over the tile slots).  With C = a.deal_cus CUs, ntiles =
+// u C / 2 (u half tiles a CU, 3 <= u <= 8) and k = grid / C workgroups of TS
+// tile slots per CU, workgroup g = m C + c (m < k) fills slot j = TS m + ts
+// of "CU" c: tile j C + c while j < u / 2, then for odd u rows 8 (c & 1) ..
+// + 7 of tile (u / 2) C + c / 2, and nothing after.  In that half tile lane row n
+// loads and computes row (n & 7) | 8 (c & 1), so lane pairs read the same
+// bytes (one fetch), and only the lanes of the own half store.  With the
+// dispatcher's k workgroups per CU (one of each m) every CU streams the same
+// bytes; the row sums are those of the grid-strided deal, bit for bit.
 template <uint32_t T, int W, int KS, int D, bool DBG, bool FULL, bool BAL = false>
 __global__ __launch_bounds__(W * 64) void q45_mv_b1_kernel(MvArgs a) {
     constexpr int TS = W / KS;
-    static_assert(!BAL || TS == 2, "the balanced deal takes two tile slots");
+    static_assert(!BAL || TS == 2 || TS == 4, "the balanced deal takes two or four tile slots");
     extern __shared__ __align__(16) uint8_t lds[];
     const LdsMap L = lds_map(T, a.cols, 1);
     float* part = (float*)(lds + small_part_off(a.cols, 1));
@@ -1231,23 +1234,14 @@ __global__ __launch_bounds__(W * 64) void q45_mv_b1_kernel(MvArgs a) {
     // ~0), which half; tile_of(i) is tile i of its sequence
     uint32_t tmax, my_tiles, half_ti = ~0u, hsel = 0, bt = 0;
     if constexpr (BAL) {
-        const uint32_t c = gridDim.x / 2, u = 2 * ntiles / c;
+        const uint32_t C = a.deal_cus, q = ntiles / C, cls = blockIdx.x / C, c = blockIdx.x - cls * C;
+        const uint32_t j = TS * cls + ts;
+        const bool odd = ntiles > q * C;
         tmax = 1;
         my_tiles = 1;
-        if (blockIdx.x < c) {
-            bt = 2 * blockIdx.x + ts;
-        } else {
-            const uint32_t h = blockIdx.x - c;
-            if (u == 8) {
-                bt = 2 * c + 2 * h + ts;
-            } else if (ts == 0) {
-                bt = 2 * c + h;
-            } else if (u == 7) {
-                bt = 3 * c + h / 2, half_ti = 0, hsel = h & 1;
-            } else {
-                my_tiles = 0;
-            }
-        }
+        if (j < q) bt = j * C + c;
+        else if (j == q && odd) bt = q * C + c / 2, half_ti = 0, hsel = c & 1;
+        else my_tiles = 0;
     } else {
         tmax = (ntiles + tstride - 1) / tstride;
         my_tiles = t0 < ntiles ? (ntiles - 1 - t0) / tstride + 1 : 0;
@@ -2219,24 +2213,29 @@ static bool b1_takes(const MvArgs& a) {
     return grid > 0 && (!a.resid || tmax <= 4);
 }
 
-// The balanced deal: two workgroups of two tile slots per CU, u = 2 ntiles /
-// CUs in 6..8 (14336 rows: 8.3 us against 8.5 grid-strided).
-static void b1_bal_grid(const MvArgs& a, uint32_t& grid, uint32_t& tmax) {
+// The balanced deal: u = 2 ntiles / CUs half tiles a CU, 3 <= u <= 8 (0:
+// the tiles do not divide so), in workgroups of TS tile slots (the CU's
+// (u + 1) / 2 slots, rounded up to whole workgroups).
+static uint32_t b1_bal_units(const MvArgs& a) {
     const uint32_t cus = (uint32_t)device_cus();
-    grid = tmax = 0;
-    if (cus == 0 || (2ull * a.ntiles) % cus != 0) return;
+    if (cus == 0 || (2ull * a.ntiles) % cus != 0) return 0;
     const uint64_t u = 2ull * a.ntiles / cus;
-    if (u < 6 || u > 8 || (u == 7 && cus % 2 != 0)) return;
-    grid = 2 * cus;
-    tmax = 1;
+    return u < 3 || u > 8 || (u % 2 == 1 && cus % 2 != 0) ? 0 : (uint32_t)u;
+}
+template <int TS>
+static void b1_bal_grid(const MvArgs& a, uint32_t& grid, uint32_t& tmax) {
+    const uint32_t u = b1_bal_units(a);
+    grid = u ? ((u + 1) / 2 + TS - 1) / TS * (uint32_t)device_cus() : 0;
+    tmax = u ? 1 : 0;
 }
 
 template <int W, int KS>
 static bool b1_bal_takes(const MvArgs& a) {
-    if (W / KS != 2 || a.nb > 4u * KS || a.epilogue != kEpStore) return false;
+    constexpr int TS = W / KS;
+    if ((TS != 2 && TS != 4) || a.nb > 4u * KS || a.epilogue != kEpStore) return false;
     uint32_t grid, tmax;
-    b1_bal_grid(a, grid, tmax);
-    return grid > 0 && b1_lds_bytes(a.cols, tmax, 2, KS) <= kMaxLds;
+    b1_bal_grid<TS>(a, grid, tmax);
+    return grid > 0 && b1_lds_bytes(a.cols, tmax, TS, KS) <= kMaxLds;
 }
 
 template <uint32_t T, int W, int KS, int D, bool DBG, bool FULL, bool BAL = false>
@@ -2245,7 +2244,7 @@ static hipError_t launch_b1(const MvArgs& a, hipStream_t s) {
     static size_t lds_set = 64 * 1024;
     auto kernel = q45_mv_b1_kernel<T, W, KS, D, DBG, FULL, BAL>;
     uint32_t grid, tmax;
-    if constexpr (BAL) b1_bal_grid(a, grid, tmax);
+    if constexpr (BAL) b1_bal_grid<TS>(a, grid, tmax);
     else b1_grid<W, KS>(a, grid, tmax);
     const size_t lds = b1_lds_bytes(a.cols, tmax, TS, KS);
     if (grid == 0 || lds > kMaxLds || (a.am_out && grid > kArgmaxMaxGrid) || (a.resid && tmax > 4))
@@ -2256,7 +2255,9 @@ static hipError_t launch_b1(const MvArgs& a, hipStream_t s) {
         if (e != hipSuccess) return e;
         lds_set = lds;
     }
-    hipLaunchKernelGGL(kernel, dim3(grid), dim3(W * 64), lds, s, a);
+    MvArgs b = a;
+    b.deal_cus = BAL ? (uint32_t)device_cus() : 0;
+    hipLaunchKernelGGL(kernel, dim3(grid), dim3(W * 64), lds, s, b);
     return hipGetLastError();
 }
 
@@ -2336,9 +2337,8 @@ template <uint32_t T>
 static hipError_t launch_q45(const MvArgs& a, uint32_t nbat, bool dbg, uint32_t epilogue, size_t lds, hipStream_t s,
                              uint32_t pairs) {
     // one f32 column: the batch-1 kernel (measured, Q4_K, us against the
-    // shared-quantization kernel: 14336x4096 8.3 / 9.2 with two tile slots
-    // of a K split of 4 in the balanced deal, 8.5 grid-strided; 6144x4096
-    // 5.5 / 6.6 with two slots, grid-strided; 4096x4096 5.2 / 6.2
+    // shared-quantization kernel: 14336x4096 7.9 / 9.2 in the balanced deal
+    // below; 6144x4096 5.5 / 6.6; 4096x4096 5.2 / 6.2
     // with one slot of a split of 4; 4096x14336 9.6 / 10.6 with a split of
     // 16).  Its FULL variant takes the decode step's RMSNorm input and
     // residual, model checks and the argmax (Q/K/V 6144x4096 with RMSNorm
@@ -2351,7 +2351,13 @@ static hipError_t launch_q45(const MvArgs& a, uint32_t nbat, bool dbg, uint32_t 
         if (a.nb > 16) {
             if (b1_takes<16, 16>(a)) return launch_b1_any<T, 16, 16>(a, dbg, full, s);
         } else if (a.ntiles >= 384) {
-            if (b1_bal_takes<8, 4>(a)) return launch_b1_any<T, 8, 4, true>(a, dbg, full, s);
+            // the balanced deal: one workgroup per CU, its tile slots the
+            // CU's (14336x4096: 7.9 us with four slots of 16 waves, 8.15 with
+            // two workgroups of two slots, 8.45 grid-strided; 6144x4096 5.5
+            // with two slots, 6.4 with four)
+            const uint32_t u = b1_bal_units(a);
+            if (u >= 5 && b1_bal_takes<16, 4>(a)) return launch_b1_any<T, 16, 4, true>(a, dbg, full, s);
+            if (u >= 3 && u <= 4 && b1_bal_takes<8, 4>(a)) return launch_b1_any<T, 8, 4, true>(a, dbg, full, s);
             if (b1_takes<8, 4>(a)) return launch_b1_any<T, 8, 4>(a, dbg, full, s);
         } else if (b1_takes<4, 4>(a)) {
             return launch_b1_any<T, 4, 4>(a, dbg, full, s);

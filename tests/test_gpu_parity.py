@@ -165,11 +165,14 @@ def _oracle_sums(t, w, rows, act, nb):
 
 @pytest.mark.parametrize("t,rows,cols,variant", [
     (DT.Q4_K, 4096, 4096, "batch-1 kernel, one tile slot, K split 4 (< 384 tiles)"),
-    (DT.Q4_K, 6144, 4096, "batch-1 kernel, two tile slots, K split 4 (>= 384 tiles)"),
-    (DT.Q4_K, 12288, 4096, "batch-1 kernel, balanced deal, u = 6: one slot of every second workgroup idle"),
-    (DT.Q4_K, 14336, 4096, "batch-1 kernel, balanced deal, u = 7 (half tiles): the headline matvec"),
+    (DT.Q4_K, 6144, 4096, "batch-1 kernel, balanced deal, u = 3: one workgroup of two slots per CU, a full and a half tile"),
+    (DT.Q4_K, 8192, 4096, "batch-1 kernel, balanced deal, u = 4: two slots per CU, two full tiles"),
+    (DT.Q4_K, 10240, 4096, "batch-1 kernel, balanced deal, u = 5: four slots per CU, two full tiles, a half, one idle"),
+    (DT.Q4_K, 6400, 4096, "batch-1 kernel, two tile slots, K split 4, grid-strided (400 tiles)"),
+    (DT.Q4_K, 12288, 4096, "batch-1 kernel, balanced deal, u = 6: four slots per CU, one idle"),
+    (DT.Q4_K, 14336, 4096, "batch-1 kernel, balanced deal, u = 7: four slots per CU, the last a half tile: the headline"),
     (DT.Q4_K, 14330, 4096, "balanced deal, u = 7, the last tile partial and dealt out in halves"),
-    (DT.Q4_K, 16384, 4096, "batch-1 kernel, balanced deal, u = 8"),
+    (DT.Q4_K, 16384, 4096, "batch-1 kernel, balanced deal, u = 8: four full tiles per CU"),
     (DT.Q5_K, 14336, 4096, "Q5_K, batch-1 kernel, balanced deal, u = 7"),
     (DT.Q4_K, 4096, 14336, "batch-1 kernel, 16 waves, K split 16 (> 16 blocks)"),
     (DT.Q4_K, 333, 16384, "batch-1 kernel, K split 16 at 64 blocks: 4 blocks per wave, the most it takes"),
