@@ -569,10 +569,10 @@ int32_t rlq_mul_mat_id(rlq_context* ctx, const rlq_weights* w, uint32_t x_dtype,
 // ---- device matmul --------------------------------------------------------------
 
 // Q4_K / Q5_K columns from this many per launch on are quantized once by the
-// planes kernel instead of in every workgroup's prologue (14336x4096 batch
-// 8: 13.1 us for both launches against 16.0 us fused; batch 4: 12.8 either
-// way).
-constexpr uint64_t kPlanesMinBatch = 5;
+// planes kernel instead of in every workgroup's prologue (with one workgroup
+// per CU; 14336x4096 batch 8: 12.6 us for both launches against 12.9 us
+// fused, batch 6: 12.5 against 11.8; 6144x4096 batch 8: 9.8 against 10.9).
+constexpr uint64_t kPlanesMinBatch = 7;
 
 // The decode launch of `batch` (<= 8) f32 columns: the fused kernels, or the
 // Q8_K planes kernel and then the matvec over the planes.

@@ -647,6 +647,35 @@ __device__ __forceinline__ void zero_slot_tiles(const MvArgs& a, uint32_t tmax, 
 }
 
 // ---------------------------------------------------------------------------
+// The balanced deal of the decode kernels: the tiles dealt out in equal
+// shares of bytes per CU (otherwise they are grid-strided over the tile
+// slots).  With C CUs, ntiles = u C / 2 (u half tiles a CU, 3 <= u <= 8) and
+// k = grid / C workgroups of TS tile slots per CU, workgroup g = m C + c
+// (m < k) fills slot j = TS m + ts of "CU" c: tile j C + c while j < u / 2,
+// then for odd u rows 8 (c & 1) .. + 7 of tile (u / 2) C + c / 2, and nothing
+// after.  In that half tile lane row n loads and computes row (n & 7) |
+// 8 (c & 1), so lane pairs read the same bytes (one fetch), and only the
+// lanes of the own half store.  With the dispatcher's k workgroups per CU (one
+// of each m) every CU streams the same bytes; every row's sums are those of
+// the grid-strided deal, bit for bit.
+// ---------------------------------------------------------------------------
+struct TileDeal {
+    uint32_t tile;     // the slot's tile (one per slot)
+    uint32_t count;    // 1, or 0 for an idle slot
+    uint32_t half;     // 1: the tile is a half tile
+    uint32_t hsel;     // its half: rows 8 hsel .. 8 hsel + 7
+};
+template <int TS>
+__device__ __forceinline__ TileDeal balanced_deal(uint32_t C, uint32_t ntiles, uint32_t ts) {
+    const uint32_t q = ntiles / C, cls = blockIdx.x / C, c = blockIdx.x - cls * C, j = TS * cls + ts;
+    TileDeal d{0, 1, 0, 0};
+    if (j < q) d.tile = j * C + c;
+    else if (j == q && ntiles > q * C) d.tile = q * C + c / 2, d.half = 1, d.hsel = c & 1;
+    else d.count = 0;
+    return d;
+}
+
+// ---------------------------------------------------------------------------
 // Software pipeline over a wave's steps: buf[i] holds the loads of step
 // s0 + i, issued D steps before use.  The steady-state loop issues exactly one
 // step's loads per step, so every path through it has the same loads in
@@ -846,9 +875,11 @@ __host__ __device__ inline uint32_t ks_lds_bytes(uint32_t T, uint32_t cols, uint
 }
 
 // PL: planes input that fits the prefetch registers (prefetch_planes).
-template <uint32_t T, int W, int KS, int D, bool DBG, bool PL>
+// BAL: the balanced deal over a.deal_cus CUs (balanced_deal; one matrix).
+template <uint32_t T, int W, int KS, int D, bool DBG, bool PL, bool BAL = false>
 __global__ __launch_bounds__(W * 64) void q45_mv_ks_kernel(MvArgs a) {
     constexpr int TS = W / KS;
+    static_assert(!BAL || TS == 2 || TS == 4, "the balanced deal takes two or four tile slots");
     if (!mv_enter(a)) return;
     extern __shared__ __align__(16) uint8_t lds[];
     const LdsMap L = lds_map(T, a.cols, a.batch);
@@ -858,8 +889,23 @@ __global__ __launch_bounds__(W * 64) void q45_mv_ks_kernel(MvArgs a) {
     const uint32_t ts = wave / KS, kp = wave % KS;
     const uint32_t nb = a.nb, ntiles = a.ntiles;
     const uint32_t tstride = gridDim.x * TS, t0 = blockIdx.x * TS + ts;
-    const uint32_t tmax = (ntiles + tstride - 1) / tstride;
-    const uint32_t my_tiles = t0 < ntiles ? (ntiles - 1 - t0) / tstride + 1 : 0;
+    // this wave's tiles: tile_of(i) for i < my_tiles; half_ti the ordinal of
+    // its half tile (none: ~0) and hsel its half (BAL: balanced_deal)
+    uint32_t tmax, my_tiles, half_ti = ~0u, hsel = 0, bt = 0;
+    if constexpr (BAL) {
+        const TileDeal d = balanced_deal<TS>(a.deal_cus, ntiles, ts);
+        tmax = 1, my_tiles = d.count, bt = d.tile, hsel = d.hsel;
+        if (d.half) half_ti = 0;
+    } else {
+        tmax = (ntiles + tstride - 1) / tstride;
+        my_tiles = t0 < ntiles ? (ntiles - 1 - t0) / tstride + 1 : 0;
+    }
+    auto tile_of = [&](uint32_t i) -> uint32_t {
+        if constexpr (BAL) return bt;
+        else return t0 + i * tstride;
+    };
+    auto own_row = [&](uint32_t i) { return i != half_ti || (n >> 3) == hsel; };
+    const uint32_t nh = (n & 7) | (hsel << 3);
     const uint32_t bpt = kp < nb ? (nb - 1 - kp) / KS + 1 : 0;  // blocks of each tile this wave takes
     const uint32_t steps = my_tiles * bpt;
     const uint32_t nk = (uint32_t)KS < nb ? (uint32_t)KS : nb;  // waves of a tile that take blocks
@@ -874,13 +920,16 @@ __global__ __launch_bounds__(W * 64) void q45_mv_ks_kernel(MvArgs a) {
 
     const uint32_t kp0 = kp < nb ? kp : nb - 1;
     uint32_t ld_tile = t0 < ntiles ? t0 : ntiles - 1, ld_blk = kp0;
+    if constexpr (BAL) ld_tile = my_tiles ? bt : 0;
     Q4Step<T> buf[D];
     auto issue = [&](Q4Step<T>& st) {
-        q45_issue<T>(st, a.w + ((uint64_t)ld_tile * nb + ld_blk) * Q45<T>::chunk, lane, n, kq);
+        const uint8_t* base = a.w + ((uint64_t)ld_tile * nb + ld_blk) * Q45<T>::chunk;
+        if (BAL && half_ti == 0) q45_issue<T>(st, base, kq * 16 + nh, nh, kq);  // the half tile
+        else q45_issue<T>(st, base, lane, n, kq);
         ld_blk += KS;
         if (ld_blk >= nb) {
             ld_blk = kp0;
-            if (ld_tile + tstride < ntiles) ld_tile += tstride;
+            if (!BAL && ld_tile + tstride < ntiles) ld_tile += tstride;
         }
     };
 #pragma unroll
@@ -902,7 +951,7 @@ __global__ __launch_bounds__(W * 64) void q45_mv_ks_kernel(MvArgs a) {
     const uint32_t b0 = 2 * kq;  // this lane's output columns b0, b0 + 1
 
     float acc0 = 0.0f, acc1 = 0.0f;
-    uint32_t ti = 0, blk = kp, j = 0, tile = t0;
+    uint32_t ti = 0, blk = kp, j = 0, tile = tile_of(0);
     auto compute = [&](const Q4Step<T>& cur) {
         const Q45Ints o = q45_mfma_ints<T>(cur, a_ptr + blk * a_step, lds + L.bs_off + (blk * 8 + b0) * 32, kq);
         const float2 da = *(const float2*)(lds + L.d_off + (blk * 8 + b0) * 4);
@@ -911,7 +960,7 @@ __global__ __launch_bounds__(W * 64) void q45_mv_ks_kernel(MvArgs a) {
         acc1 += (dw * da.y) * (float)o.I1 - (dmw * da.y) * (float)o.M1;
         if (DBG && kq == 0) {
             const uint32_t row = tile * kTileRows + n;
-            if (row < a.rows) {
+            if (row < a.rows && own_row(ti)) {
                 a.dbg_isum[(uint64_t)row * nb + blk] = o.I0;
                 a.dbg_imin[(uint64_t)row * nb + blk] = o.M0;
             }
@@ -930,8 +979,7 @@ __global__ __launch_bounds__(W * 64) void q45_mv_ks_kernel(MvArgs a) {
             acc0 = acc1 = 0.0f;
             j = 0;
             blk = kp;
-            ++ti;
-            tile += tstride;
+            tile = tile_of(++ti);
         }
     };
     pipeline<D>(steps, buf, issue, compute);
@@ -939,8 +987,8 @@ __global__ __launch_bounds__(W * 64) void q45_mv_ks_kernel(MvArgs a) {
     // the tiles this wave completed: add their K parts in order and store
     unsigned long long best0 = 0, best1 = 0;
     for (uint32_t i = 0; i < my_tiles; ++i) {
-        const uint32_t slot = i * TS + ts, row = (t0 + i * tstride) * kTileRows + n;
-        if (cnt[slot] != nk + 1 + wave) continue;  // (the mark is wave-uniform)
+        const uint32_t slot = i * TS + ts, row = tile_of(i) * kTileRows + n;
+        if (cnt[slot] != nk + 1 + wave || !own_row(i)) continue;  // (the mark is wave-uniform)
         float s0 = 0.0f, s1 = 0.0f;
 #pragma unroll
         for (int k = 0; k < KS; ++k)
@@ -1208,16 +1256,7 @@ __device__ __forceinline__ float b1_rms_scale(const MvArgs& a, uint8_t* lds, con
 // FULL: the decode step's extras (the RMSNorm input transform, the residual
 // add), the output checks of a model stage (chk) and the in-launch argmax;
 // without them none is compiled in.
-// BAL deals the tiles out in equal shares of bytes per CU (otherwise they
-// are grid-strided over the tile slots).  With C = a.deal_cus CUs, ntiles =
-// u C / 2 (u half tiles a CU, 3 <= u <= 8) and k = grid / C workgroups of TS
-// tile slots per CU, workgroup g = m C + c (m < k) fills slot j = TS m + ts
-// of "CU" c: tile j C + c while j < u / 2, then for odd u rows 8 (c & 1) ..
-// + 7 of tile (u / 2) C + c / 2, and nothing after.  In that half tile lane row n
-// loads and computes row (n & 7) | 8 (c & 1), so lane pairs read the same
-// bytes (one fetch), and only the lanes of the own half store.  With the
-// dispatcher's k workgroups per CU (one of each m) every CU streams the same
-// bytes; the row sums are those of the grid-strided deal, bit for bit.
+// BAL: the balanced deal over a.deal_cus CUs (balanced_deal).
 template <uint32_t T, int W, int KS, int D, bool DBG, bool FULL, bool BAL = false>
 __global__ __launch_bounds__(W * 64) void q45_mv_b1_kernel(MvArgs a) {
     constexpr int TS = W / KS;
@@ -1230,18 +1269,13 @@ __global__ __launch_bounds__(W * 64) void q45_mv_b1_kernel(MvArgs a) {
     const uint32_t ts = wave / KS, kp = wave % KS;
     const uint32_t nb = a.nb, ntiles = a.ntiles;
     const uint32_t tstride = gridDim.x * TS, t0 = blockIdx.x * TS + ts;
-    // the deal: this wave's tile count, the ordinal of its half tile (none:
-    // ~0), which half; tile_of(i) is tile i of its sequence
+    // this wave's tiles: tile_of(i) for i < my_tiles; half_ti the ordinal of
+    // its half tile (none: ~0) and hsel its half
     uint32_t tmax, my_tiles, half_ti = ~0u, hsel = 0, bt = 0;
     if constexpr (BAL) {
-        const uint32_t C = a.deal_cus, q = ntiles / C, cls = blockIdx.x / C, c = blockIdx.x - cls * C;
-        const uint32_t j = TS * cls + ts;
-        const bool odd = ntiles > q * C;
-        tmax = 1;
-        my_tiles = 1;
-        if (j < q) bt = j * C + c;
-        else if (j == q && odd) bt = q * C + c / 2, half_ti = 0, hsel = c & 1;
-        else my_tiles = 0;
+        const TileDeal d = balanced_deal<TS>(a.deal_cus, ntiles, ts);
+        tmax = 1, my_tiles = d.count, bt = d.tile, hsel = d.hsel;
+        if (d.half) half_ti = 0;
     } else {
         tmax = (ntiles + tstride - 1) / tstride;
         my_tiles = t0 < ntiles ? (ntiles - 1 - t0) / tstride + 1 : 0;
@@ -2270,18 +2304,25 @@ static hipError_t launch_b1_any(const MvArgs& a, bool dbg, bool full, hipStream_
 }
 
 // The K-split MFMA kernel for 3 to 8 columns: grid as launch_parked.
-template <uint32_t T, int W, int KS, int D, bool DBG, bool PL>
+template <uint32_t T, int W, int KS, int D, bool DBG, bool PL, bool BAL = false>
 static hipError_t launch_ks_pl(const MvArgs& a, hipStream_t s, uint32_t pairs) {
     constexpr int TS = W / KS;
     static size_t lds_set = 64 * 1024;
-    auto kernel = q45_mv_ks_kernel<T, W, KS, D, DBG, PL>;
+    auto kernel = q45_mv_ks_kernel<T, W, KS, D, DBG, PL, BAL>;
     const uint32_t gy = grid_rows(a, pairs);
-    uint32_t grid = grid_cols((a.ntiles + TS - 1) / TS, (uint32_t)kSmallWgPerCu * (uint32_t)device_cus(), gy);
-    const size_t off = ks_part_off(T, a.cols, a.batch), per_tile = (size_t)TS * KS * 16u * 8u * 4u + TS * 4u;
-    if (off >= kMaxLds || (kMaxLds - off) / per_tile == 0) return hipErrorInvalidValue;
-    const uint64_t room = (kMaxLds - off) / per_tile, need = (a.ntiles + room * TS - 1) / (room * TS);
-    if (grid < need) grid = (uint32_t)need;
-    const uint32_t tstride = grid * TS, tmax = (a.ntiles + tstride - 1) / tstride;
+    uint32_t grid, tmax;
+    if constexpr (BAL) {  // one matrix, one grid row
+        b1_bal_grid<TS>(a, grid, tmax);
+        if (grid == 0 || gy != 1 || a.ids) return hipErrorInvalidValue;
+    } else {
+        grid = grid_cols((a.ntiles + TS - 1) / TS, (uint32_t)kSmallWgPerCu * (uint32_t)device_cus(), gy);
+        const size_t off = ks_part_off(T, a.cols, a.batch), per_tile = (size_t)TS * KS * 16u * 8u * 4u + TS * 4u;
+        if (off >= kMaxLds || (kMaxLds - off) / per_tile == 0) return hipErrorInvalidValue;
+        const uint64_t room = (kMaxLds - off) / per_tile, need = (a.ntiles + room * TS - 1) / (room * TS);
+        if (grid < need) grid = (uint32_t)need;
+        const uint32_t tstride = grid * TS;
+        tmax = (a.ntiles + tstride - 1) / tstride;
+    }
     const size_t lds = ks_lds_bytes(T, a.cols, a.batch, tmax, TS, KS);
     if (lds > kMaxLds || (a.am_out && grid > kArgmaxMaxGrid)) return hipErrorInvalidValue;
     if (lds > lds_set) {
@@ -2290,7 +2331,9 @@ static hipError_t launch_ks_pl(const MvArgs& a, hipStream_t s, uint32_t pairs) {
         if (e != hipSuccess) return e;
         lds_set = lds;
     }
-    hipLaunchKernelGGL(kernel, dim3(grid, gy), dim3(W * 64), lds, s, a);
+    MvArgs b = a;
+    b.deal_cus = BAL ? (uint32_t)device_cus() : 0;
+    hipLaunchKernelGGL(kernel, dim3(grid, gy), dim3(W * 64), lds, s, b);
     return hipGetLastError();
 }
 
@@ -2326,10 +2369,19 @@ static hipError_t launch_q8_0_ks(const MvArgs& a, hipStream_t s, uint32_t pairs)
     return hipGetLastError();
 }
 
-template <uint32_t T, int W, int KS, int D, bool DBG>
+// Whether the balanced deal's LDS (one tile per slot) fits.
+template <uint32_t T, int W, int KS>
+static bool ks_bal_takes(const MvArgs& a) {
+    constexpr int TS = W / KS;
+    uint32_t grid, tmax;
+    b1_bal_grid<TS>(a, grid, tmax);
+    return grid > 0 && ks_lds_bytes(T, a.cols, a.batch, tmax, TS, KS) <= kMaxLds;
+}
+
+template <uint32_t T, int W, int KS, int D, bool DBG, bool BAL = false>
 static hipError_t launch_ks(const MvArgs& a, hipStream_t s, uint32_t pairs) {
-    return !a.x && planes_fit(W * 64, a.batch, a.cols, a.nb) ? launch_ks_pl<T, W, KS, D, DBG, true>(a, s, pairs)
-                                                             : launch_ks_pl<T, W, KS, D, DBG, false>(a, s, pairs);
+    return !a.x && planes_fit(W * 64, a.batch, a.cols, a.nb) ? launch_ks_pl<T, W, KS, D, DBG, true, BAL>(a, s, pairs)
+                                                             : launch_ks_pl<T, W, KS, D, DBG, false, BAL>(a, s, pairs);
 }
 
 // Q4_K / Q5_K: the VALU kernel for one or two columns, MFMA above.
@@ -2385,7 +2437,18 @@ static hipError_t launch_q45(const MvArgs& a, uint32_t nbat, bool dbg, uint32_t 
         return dbg ? launch_small<T, kSmallW, kSmallKS, kSmallD, 1, true>(a, s, pairs)
                    : launch_small<T, kSmallW, kSmallKS, kSmallD, 1, false>(a, s, pairs);
     // two to eight columns: the K-split MFMA kernel (14336x4096 batch 2:
-    // 11.1 us against 11.5 us for the VALU kernel with two columns)
+    // 11.1 us against 11.5 us for the VALU kernel with two columns).  One
+    // matrix takes the balanced deal, one workgroup per CU: four tile slots
+    // of 16 waves from u = 5, two of 8 below (14336x4096 batches 2 / 4 / 8
+    // 10.3 / 11.2 / 12.9 us against 11.3 / 12.9 / 16.1 grid-strided; 6144x4096
+    // 7.6 / 8.6 / 10.9 against 7.8 / 8.9 / 11.0)
+    if (!a.ids && grid_rows(a, pairs) == 1) {
+        const uint32_t u = b1_bal_units(a);
+        if (u >= 5 && ks_bal_takes<T, 16, 4>(a))
+            return dbg ? launch_ks<T, 16, 4, 2, true, true>(a, s, pairs) : launch_ks<T, 16, 4, 2, false, true>(a, s, pairs);
+        if (u >= 3 && ks_bal_takes<T, 8, 4>(a))
+            return dbg ? launch_ks<T, 8, 4, 2, true, true>(a, s, pairs) : launch_ks<T, 8, 4, 2, false, true>(a, s, pairs);
+    }
     return dbg ? launch_ks<T, 8, 4, 2, true>(a, s, pairs) : launch_ks<T, 8, 4, 2, false>(a, s, pairs);
 }
 

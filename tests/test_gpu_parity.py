@@ -197,6 +197,30 @@ def test_block_sums_every_decode_variant(ctx, t, rows, cols, variant):
     assert rel_l2(y.cpu().numpy(), O.matvec(int(t), w, rows, cols, x, threads=16)) <= REL_L2
 
 
+@pytest.mark.parametrize("t,rows,cols,batch", [
+    (DT.Q4_K, 14336, 4096, 2), (DT.Q4_K, 14336, 4096, 5), (DT.Q4_K, 14336, 4096, 8), (DT.Q4_K, 14330, 4096, 3),
+    (DT.Q4_K, 6144, 4096, 4), (DT.Q5_K, 14336, 4096, 6)])
+def test_block_sums_balanced_columns(ctx, t, rows, cols, batch):
+    """Two to eight columns in the balanced deal (one workgroup per CU: four
+    tile slots at 12288..16384 rows, the last a half tile at 14336, two slots
+    at 6144; fused quantization below seven columns, the planes from
+    seven): column 0's integers bitwise, every column's outputs against the
+    oracle."""
+    say("block sums, balanced deal,", t, rows, cols, "batch", batch)
+    w = _packed(t, rows, cols, 900 + rows + batch)
+    x = randn(950 + batch, batch * cols).reshape(batch, cols)
+    W = rlq.Weights(ctx, t, w, rows, cols)
+    isum, imin, y = ctx.block_sums_ex(W, torch.from_numpy(x).cuda())
+    ctx.sync()
+    nb = cols // 256
+    want_i, want_m = _oracle_sums(t, w, rows, O.quantize(O.Q8_K, x[0]), nb)
+    assert np.array_equal(isum.cpu().numpy(), want_i)
+    assert np.array_equal(imin.cpu().numpy(), want_m)
+    got = y.cpu().numpy().reshape(batch, rows)
+    for b in range(batch):
+        assert rel_l2(got[b], O.matvec(int(t), w, rows, cols, x[b], threads=16)) <= REL_L2, b
+
+
 def _interleave_tiles(g, u, rows, row_bytes):
     """[gate tile 0, up tile 0, gate tile 1, ...] of two GGUF matrices of
     `rows` rows (a multiple of 16): the decode step's gate/up layout."""
