@@ -173,6 +173,8 @@ def _oracle_sums(t, w, rows, act, nb):
     (DT.Q4_K, 14336, 4096, "batch-1 kernel, balanced deal, u = 7: four slots per CU, the last a half tile: the headline"),
     (DT.Q4_K, 14330, 4096, "balanced deal, u = 7, the last tile partial and dealt out in halves"),
     (DT.Q4_K, 16384, 4096, "batch-1 kernel, balanced deal, u = 8: four full tiles per CU"),
+    (DT.Q4_K, 14336, 512, "balanced deal, two blocks per row: two of each slot's four K parts idle"),
+    (DT.Q5_K, 14336, 768, "Q5_K, balanced deal, three blocks per row"),
     (DT.Q5_K, 14336, 4096, "Q5_K, batch-1 kernel, balanced deal, u = 7"),
     (DT.Q4_K, 4096, 14336, "batch-1 kernel, 16 waves, K split 16 (> 16 blocks)"),
     (DT.Q4_K, 333, 16384, "batch-1 kernel, K split 16 at 64 blocks: 4 blocks per wave, the most it takes"),
@@ -199,7 +201,8 @@ def test_block_sums_every_decode_variant(ctx, t, rows, cols, variant):
 
 @pytest.mark.parametrize("t,rows,cols,batch", [
     (DT.Q4_K, 14336, 4096, 2), (DT.Q4_K, 14336, 4096, 5), (DT.Q4_K, 14336, 4096, 8), (DT.Q4_K, 14330, 4096, 3),
-    (DT.Q4_K, 6144, 4096, 4), (DT.Q5_K, 14336, 4096, 6)])
+    (DT.Q4_K, 6144, 4096, 4), (DT.Q5_K, 14336, 4096, 6), (DT.Q4_K, 14336, 512, 3), (DT.Q4_K, 12288, 8192, 2),
+    (DT.Q4_K, 14336, 768, 7)])
 def test_block_sums_balanced_columns(ctx, t, rows, cols, batch):
     """Two to eight columns in the balanced deal (one workgroup per CU: four
     tile slots at 12288..16384 rows, the last a half tile at 14336, two slots
