@@ -588,7 +588,10 @@ __device__ __forceinline__ void fold_argmax(const MvArgs& a, uint8_t* lds, const
 // counts itself in; the last workgroup to arrive reads every slot, writes the
 // token ids and sets the counter back to 0.  All cross-workgroup data moves
 // through agent-scope atomics (coherent across the device's L2s), so no cache
-// write-back is needed.
+// write-back is needed.  The two round trips lengthen every workgroup's tail
+// (Q8_0 151936x896: about 4 us of a 31 us launch); sixteen group counters in
+// place of the one measured the same, so the time is the round trips, not
+// contention on the counter.
 __device__ __forceinline__ void finish_argmax(const MvArgs& a, uint8_t* lds, const LdsMap& L) {
     if (!a.am_out) return;
     unsigned long long* keys = (unsigned long long*)(lds + L.am_off);
@@ -2164,8 +2167,11 @@ static uint32_t grid_cols(uint32_t want, uint32_t cap, uint32_t rows) {
     return want < per ? want : per;
 }
 
+// per_cu workgroups of kMvWaves waves per CU at most (Q8_0 151936x896: 25.8
+// us at three, 27.5 at two; Q6_K 128256x4096: 71.5 at two, 75.4 at three).
 template <typename K>
-static hipError_t launch_one(K kernel, const MvArgs& a, size_t lds, hipStream_t s, uint32_t pairs) {
+static hipError_t launch_one(K kernel, const MvArgs& a, size_t lds, hipStream_t s, uint32_t pairs,
+                             uint32_t per_cu = 2) {
     static size_t lds_set = 64 * 1024;  // above 64 KB the kernel must opt in
     if (lds > lds_set) {
         const hipError_t e =
@@ -2175,7 +2181,7 @@ static hipError_t launch_one(K kernel, const MvArgs& a, size_t lds, hipStream_t 
     }
     const uint32_t want = (a.ntiles + kMvWaves - 1) / kMvWaves;
     const uint32_t gy = grid_rows(a, pairs);
-    const uint32_t grid = grid_cols(want, 2u * (uint32_t)device_cus(), gy);
+    const uint32_t grid = grid_cols(want, per_cu * (uint32_t)device_cus(), gy);
     if (a.am_out && grid > kArgmaxMaxGrid) return hipErrorInvalidValue;
     hipLaunchKernelGGL(kernel, dim3(grid, gy), dim3(kMvWaves * 64), lds, s, a);
     return hipGetLastError();
@@ -2577,8 +2583,8 @@ hipError_t launch_matvec_ex(uint32_t wtype, const uint8_t* w, uint64_t rows, uin
                 default:
                     if (q8_0_ks_takes<8, 4>(a, pairs))
                         return dbg ? launch_q8_0_ks<8, 4, true>(a, s, pairs) : launch_q8_0_ks<8, 4, false>(a, s, pairs);
-                    return dbg ? launch_one(q8_0_mv_kernel<W, 8, true>, a, lds, s, pairs)
-                               : launch_one(q8_0_mv_kernel<W, 8, false>, a, lds, s, pairs);
+                    return dbg ? launch_one(q8_0_mv_kernel<W, 8, true>, a, lds, s, pairs, 3)
+                               : launch_one(q8_0_mv_kernel<W, 8, false>, a, lds, s, pairs, 3);
             }
         };
         if (!a.ids) {
