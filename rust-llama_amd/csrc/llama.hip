@@ -182,10 +182,10 @@ __global__ __launch_bounds__(kAttnThreads) void attn_scores_kernel(
             }
         }
         double part = (a[0] + a[1]) + (a[2] + a[3]);
-        part += __shfl_xor(part, 1, 64);
-        part += __shfl_xor(part, 2, 64);
-        b += __shfl_xor(b, 1, 64);
-        b += __shfl_xor(b, 2, 64);
+        part += dpp_d<kQuadXor1>(part);  // the four lanes of the pair, by DPP
+        part += dpp_d<kQuadXor2>(part);
+        b += dpp_f<kQuadXor1>(b);
+        b += dpp_f<kQuadXor2>(b);
         float score = -INFINITY;
         if (live) {
             float dotf;
@@ -201,8 +201,11 @@ __global__ __launch_bounds__(kAttnThreads) void attn_scores_kernel(
             }
         }
         float m = score;
-#pragma unroll
-        for (int o = 4; o < 64; o <<= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+        // the quads hold equal values: the rest of the wave's 16 pairs
+        m = fmaxf(m, dpp_f<kRowHalfMirror>(m));
+        m = fmaxf(m, dpp_f<kRowRor8>(m));
+        m = fmaxf(m, __shfl_xor(m, 16, 64));
+        m = fmaxf(m, __shfl_xor(m, 32, 64));
         if ((tid & 63) == 0) cmax[(kvh * G + h) * cstride + c] = m;
     }
 }
@@ -266,8 +269,7 @@ __global__ __launch_bounds__(kPvThreads) void attn_pv_kernel(
     for (uint32_t h = wave; h < G; h += kPvWaves) {
         float m = -INFINITY;
         for (uint32_t c = lane; c < nch; c += 64) m = fmaxf(m, cmax[(kvh * G + h) * cstride + c]);
-#pragma unroll
-        for (int o = 1; o < 64; o <<= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+        m = wave_max_dpp(m);
         if (lane == 0) stat[2 * h] = m;
     }
     __syncthreads();
@@ -296,8 +298,7 @@ __global__ __launch_bounds__(kPvThreads) void attn_pv_kernel(
                 exp_group(*(const float4*)(srow + 4 * g), 4 * g, count, m, e);
                 sum += (double)((e[0] + e[1]) + (e[2] + e[3]));
             }
-#pragma unroll
-            for (int o = 1; o < 64; o <<= 1) sum += __shfl_xor(sum, o, 64);
+            sum = wave_sum_f64(sum);
             if (lane == 0) rsum[h * wph + w] = sum;
         }
     }
@@ -365,13 +366,10 @@ __global__ __launch_bounds__(kPvThreads) void attn_pv_kernel(
                     v[j] = 4 * g + j < count ? vsrc[4 * g + j] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
                 add(e, v);
             }
-#pragma unroll
-            for (int o = 1; o < 64; o <<= 1) {
-                a0 += __shfl_xor(a0, o, 64);
-                a1 += __shfl_xor(a1, o, 64);
-                a2 += __shfl_xor(a2, o, 64);
-                a3 += __shfl_xor(a3, o, 64);
-            }
+            a0 = wave_sum_f64(a0);
+            a1 = wave_sum_f64(a1);
+            a2 = wave_sum_f64(a2);
+            a3 = wave_sum_f64(a3);
             if (lane == 0) {
                 double* pp = part + (h * wph + w) * 4;
                 pp[0] = a0, pp[1] = a1, pp[2] = a2, pp[3] = a3;

@@ -144,6 +144,23 @@ __device__ __forceinline__ float wave_max(float v) {
     for (int m = 1; m < 64; m <<= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
     return v;
 }
+// Sum over all 64 lanes in a fixed order (the 16-lane rows by DPP, then the
+// rows); every lane gets it.
+__device__ __forceinline__ double wave_sum_f64(double v) {
+    v = row16_sum_f64(v);
+    v += __shfl_xor(v, 16, 64);
+    v += __shfl_xor(v, 32, 64);
+    return v;
+}
+// Maximum over all 64 lanes (DPP inside the rows, then the rows).
+__device__ __forceinline__ float wave_max_dpp(float v) {
+    v = fmaxf(v, dpp_f<kQuadXor1>(v));
+    v = fmaxf(v, dpp_f<kQuadXor2>(v));
+    v = fmaxf(v, dpp_f<kRowHalfMirror>(v));
+    v = fmaxf(v, dpp_f<kRowRor8>(v));
+    v = fmaxf(v, __shfl_xor(v, 16, 64));
+    return fmaxf(v, __shfl_xor(v, 32, 64));
+}
 __device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
     for (int m = 1; m < 64; m <<= 1) {
         const uint32_t o = (uint32_t)__shfl_xor((int)v, m, 64);
