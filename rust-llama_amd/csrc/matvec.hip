@@ -1831,9 +1831,11 @@ __host__ __device__ inline uint32_t k16_part_off(uint32_t t, uint32_t cols, uint
     return (lds_map(t, cols, batch).total + 15u) & ~15u;
 }
 
-template <uint32_t T, int W, int KS, int D, bool DBG>
+// BAL: the balanced deal over a.deal_cus CUs (balanced_deal; one matrix).
+template <uint32_t T, int W, int KS, int D, bool DBG, bool BAL = false>
 __global__ __launch_bounds__(W * 64) void k16_mv_split_kernel(MvArgs a) {
     constexpr int TS = W / KS;
+    static_assert(!BAL || TS == 2 || TS == 4, "the balanced deal takes two or four tile slots");
     constexpr uint32_t kChunk = T == kQ3_K ? kQ3KChunk : kQ2KChunk;
     if (!mv_enter(a)) return;
     extern __shared__ __align__(16) uint8_t lds[];
@@ -1845,8 +1847,23 @@ __global__ __launch_bounds__(W * 64) void k16_mv_split_kernel(MvArgs a) {
     const uint32_t ts = wave / KS, kp = wave % KS;
     const uint32_t nb = a.nb, ntiles = a.ntiles, batch = a.batch;
     const uint32_t tstride = gridDim.x * TS, t0 = blockIdx.x * TS + ts;
-    const uint32_t tmax = (ntiles + tstride - 1) / tstride;
-    const uint32_t my_tiles = t0 < ntiles ? (ntiles - 1 - t0) / tstride + 1 : 0;
+    // this wave's tiles: tile_of(i) for i < my_tiles; half_ti the ordinal of
+    // its half tile (none: ~0) and hsel its half
+    uint32_t tmax, my_tiles, half_ti = ~0u, hsel = 0, bt = 0;
+    if constexpr (BAL) {
+        const TileDeal d = balanced_deal<TS>(a.deal_cus, ntiles, ts);
+        tmax = 1, my_tiles = d.count, bt = d.tile, hsel = d.hsel;
+        if (d.half) half_ti = 0;
+    } else {
+        tmax = (ntiles + tstride - 1) / tstride;
+        my_tiles = t0 < ntiles ? (ntiles - 1 - t0) / tstride + 1 : 0;
+    }
+    auto tile_of = [&](uint32_t i) -> uint32_t {
+        if constexpr (BAL) return bt;
+        else return t0 + i * tstride;
+    };
+    auto own_row = [&](uint32_t i) { return i != half_ti || (n >> 3) == hsel; };
+    const uint32_t nh = (n & 7) | (hsel << 3);
     const uint32_t bpt = kp < nb ? (nb - 1 - kp) / KS + 1 : 0;  // blocks of each tile this wave takes
     const uint32_t steps = my_tiles * bpt;
 
@@ -1858,13 +1875,16 @@ __global__ __launch_bounds__(W * 64) void k16_mv_split_kernel(MvArgs a) {
     // loads run D steps ahead; past the wave's last step they repeat a valid chunk
     const uint32_t kp0 = kp < nb ? kp : nb - 1;
     uint32_t ld_tile = t0 < ntiles ? t0 : ntiles - 1, ld_blk = kp0;
+    if constexpr (BAL) ld_tile = my_tiles ? bt : 0;
     K16Step<T> buf[D];
     auto issue = [&](K16Step<T>& st) {
-        k16_issue<T>(st, a.w + ((uint64_t)ld_tile * nb + ld_blk) * kChunk, lane, n, kq);
+        const uint8_t* base = a.w + ((uint64_t)ld_tile * nb + ld_blk) * kChunk;
+        if (BAL && half_ti == 0) k16_issue<T>(st, base, kq * 16 + nh, nh, kq);  // the half tile
+        else k16_issue<T>(st, base, lane, n, kq);
         ld_blk += KS;
         if (ld_blk >= nb) {
             ld_blk = kp0;
-            if (ld_tile + tstride < ntiles) ld_tile += tstride;
+            if (!BAL && ld_tile + tstride < ntiles) ld_tile += tstride;
         }
     };
 #pragma unroll
@@ -1877,7 +1897,7 @@ __global__ __launch_bounds__(W * 64) void k16_mv_split_kernel(MvArgs a) {
     const K16A A = k16_a(lds, L, batch, n, kq);
     const bool two_groups = batch > 4;
     const uint32_t hsh = 4 * (kq >> 1);
-    uint32_t ti = 0, tile = t0, blk = kp, j = 0;
+    uint32_t ti = 0, tile = tile_of(0), blk = kp, j = 0;
     auto compute = [&](const K16Step<T>& cur) {
         const K16Ops<T> o = k16_ops<T>(cur, hsh);
         float* pt = part + ((uint64_t)((ti * TS + ts) * nb + blk) * 16 + n) * batch;
@@ -1889,7 +1909,7 @@ __global__ __launch_bounds__(W * 64) void k16_mv_split_kernel(MvArgs a) {
         }
         if (DBG && kq == 0) {
             const uint32_t row = tile * kTileRows + n;
-            if (row < a.rows) {
+            if (row < a.rows && own_row(ti)) {
                 a.dbg_isum[(uint64_t)row * nb + blk] = I0;
                 a.dbg_imin[(uint64_t)row * nb + blk] = M0;
             }
@@ -1906,8 +1926,7 @@ __global__ __launch_bounds__(W * 64) void k16_mv_split_kernel(MvArgs a) {
         if (++j == bpt) {
             j = 0;
             blk = kp;
-            ++ti;
-            tile += tstride;
+            tile = tile_of(++ti);
         }
     };
     pipeline<D>(steps, buf, issue, compute);
@@ -1918,9 +1937,15 @@ __global__ __launch_bounds__(W * 64) void k16_mv_split_kernel(MvArgs a) {
         unsigned long long best = 0;
         for (uint32_t it = threadIdx.x; it < tmax * TS * 16; it += W * 64) {
             const uint32_t r = it % 16, slot = it / 16, tsl = slot % TS, til = slot / TS;
-            const uint32_t t = blockIdx.x * TS + tsl + til * tstride;
+            uint32_t t = blockIdx.x * TS + tsl + til * tstride;
+            bool own = true;
+            if constexpr (BAL) {  // the slot's tile in the deal, and its own rows
+                const TileDeal d = balanced_deal<TS>(a.deal_cus, ntiles, tsl);
+                t = d.count ? d.tile : ntiles;
+                own = !d.half || (r >> 3) == d.hsel;
+            }
             const uint32_t row = t * kTileRows + r;
-            if (t < ntiles && row < a.rows) {
+            if (t < ntiles && row < a.rows && own) {
                 const float* pr = part + ((uint64_t)slot * nb * 16 + r) * batch + b;
                 float v = 0.0f;
                 for (uint32_t k = 0; k < nb; ++k) v += pr[(uint64_t)k * 16 * batch];
@@ -2479,8 +2504,39 @@ static hipError_t launch_k16_split(const MvArgs& a, size_t lds, uint32_t grid, u
     return hipGetLastError();
 }
 
+// The K-split kernel in the balanced deal (one matrix): W waves, K split KS,
+// one tile per slot.
+template <uint32_t T, int W, int KS, bool DBG>
+static hipError_t launch_k16_bal(const MvArgs& a, hipStream_t s) {
+    constexpr int TS = W / KS;
+    static size_t lds_set = 64 * 1024;
+    auto kernel = k16_mv_split_kernel<T, W, KS, kK16D, DBG, true>;
+    uint32_t grid, tmax;
+    b1_bal_grid<TS>(a, grid, tmax);
+    const uint64_t lds = k16_part_off(T, a.cols, a.batch) + (uint64_t)tmax * TS * a.nb * 16ull * a.batch * 4ull;
+    if (grid == 0 || a.ids || a.batch > 4 || lds > kMaxLds || (a.am_out && grid > kArgmaxMaxGrid))
+        return hipErrorInvalidValue;
+    if (lds > lds_set) {
+        const hipError_t e = hipFuncSetAttribute((const void*)kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                 (int)lds);
+        if (e != hipSuccess) return e;
+        lds_set = lds;
+    }
+    MvArgs b = a;
+    b.deal_cus = (uint32_t)device_cus();
+    hipLaunchKernelGGL(kernel, dim3(grid), dim3(W * 64), lds, s, b);
+    return hipGetLastError();
+}
+
 template <uint32_t T>
 static hipError_t launch_k16(const MvArgs& a, bool dbg, size_t lds_plain, hipStream_t s, uint32_t pairs) {
+    // one matrix of 10240..16384 rows (on 256 CUs), up to four columns: the
+    // balanced deal, one workgroup of 16 waves per CU, four slots of a K split
+    // of 4 (14336x4096 Q2_K batches 1 / 2 / 4: 8.6 / 9.5 / 11.0 us against
+    // 9.6 / 11.1 / 14.6; Q3_K 9.9 / 10.9 / 12.5 against 11.2 / 12.7 / 16.2)
+    if (a.batch <= 4 && !a.ids && grid_rows(a, pairs) == 1 && b1_bal_units(a) >= 5 &&
+        k16_part_off(T, a.cols, a.batch) + 4ull * a.nb * 16ull * a.batch * 4ull <= kMaxLds)
+        return dbg ? launch_k16_bal<T, 16, 4, true>(a, s) : launch_k16_bal<T, 16, 4, false>(a, s);
     constexpr int TS = kK16W / kK16KS;
     const uint32_t want = (a.ntiles + TS - 1) / TS;
     const uint32_t gy = grid_rows(a, pairs);

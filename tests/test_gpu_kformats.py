@@ -208,6 +208,37 @@ def test_block_sums_bit_exact(ctx, t, rows, cols, batch):
     assert np.array_equal(imin.cpu().numpy(), want_m)
 
 
+@pytest.mark.parametrize("t", (DT.Q2_K, DT.Q3_K))
+@pytest.mark.parametrize("rows,batch", [(14336, 1), (14336, 3), (14330, 2), (12288, 4), (10240, 1)])
+def test_block_sums_balanced_deal(ctx, t, rows, batch):
+    """Q2_K / Q3_K at 10240..16384 rows and up to four columns run the K-split
+    kernel in the balanced deal (one workgroup per CU, four tile slots, the
+    last a half tile at 14336 rows): column 0's integers bitwise, every
+    column's outputs against the oracle (Q2_K bitwise)."""
+    cols = 4096
+    say("block sums, balanced deal", t, rows, cols, batch)
+    w = random_blocks(t, rows, cols, 300 + rows + int(t))
+    x = randn(400 + rows + batch, batch * cols).reshape(batch, cols)
+    W = rlq.Weights(ctx, t, w, rows, cols)
+    isum, imin, y = ctx.block_sums_ex(W, torch.from_numpy(x).cuda())
+    ctx.sync()
+    act = O.quantize(O.Q8_K, x[0])
+    nb = cols // 256
+    stride = w.size // rows
+    want_i = np.zeros((rows, nb), np.int32)
+    want_m = np.zeros((rows, nb), np.int32)
+    for r in range(rows):
+        want_i[r], want_m[r] = O.block_sums(int(t), w[r * stride:(r + 1) * stride], act, nb)
+    assert np.array_equal(isum.cpu().numpy(), want_i)
+    assert np.array_equal(imin.cpu().numpy(), want_m)
+    got = y.cpu().numpy().reshape(batch, rows)
+    want = O.matmul(int(t), w, rows, cols, x, threads=16)
+    for b in range(batch):
+        assert rel_l2(got[b], want[b]) <= REL_L2, b
+    if t == DT.Q2_K:
+        assert np.array_equal(bits(got), bits(want))
+
+
 # ------------------------------------------------------------ batched device API
 
 @pytest.mark.parametrize("t", K_OTHER)
