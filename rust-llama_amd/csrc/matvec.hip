@@ -2192,9 +2192,10 @@ static uint32_t grid_cols(uint32_t want, uint32_t cap, uint32_t rows) {
     return want < per ? want : per;
 }
 
-// per_cu workgroups of kMvWaves waves per CU at most (Q8_0 151936x896: 25.8
-// us at three, 27.5 at two; Q6_K 128256x4096: 71.5 at two, 75.4 at three).
-template <typename K>
+// per_cu workgroups of W waves per CU at most (Q8_0 151936x896 with W = 4:
+// 25.8 us at three, 27.5 at two; Q6_K 128256x4096 with the argmax: one of 8
+// waves 71.8 us, two of 4 72.7-75.4, and at 8 columns 83.3 against 88.4).
+template <int W = kMvWaves, typename K>
 static hipError_t launch_one(K kernel, const MvArgs& a, size_t lds, hipStream_t s, uint32_t pairs,
                              uint32_t per_cu = 2) {
     static size_t lds_set = 64 * 1024;  // above 64 KB the kernel must opt in
@@ -2204,11 +2205,11 @@ static hipError_t launch_one(K kernel, const MvArgs& a, size_t lds, hipStream_t 
         if (e != hipSuccess) return e;
         lds_set = lds;
     }
-    const uint32_t want = (a.ntiles + kMvWaves - 1) / kMvWaves;
+    const uint32_t want = (a.ntiles + W - 1) / W;
     const uint32_t gy = grid_rows(a, pairs);
     const uint32_t grid = grid_cols(want, per_cu * (uint32_t)device_cus(), gy);
     if (a.am_out && grid > kArgmaxMaxGrid) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(kernel, dim3(grid, gy), dim3(kMvWaves * 64), lds, s, a);
+    hipLaunchKernelGGL(kernel, dim3(grid, gy), dim3(W * 64), lds, s, a);
     return hipGetLastError();
 }
 
@@ -2634,8 +2635,8 @@ hipError_t launch_matvec_ex(uint32_t wtype, const uint8_t* w, uint64_t rows, uin
                 case kQ3_K: return launch_k16<kQ3_K>(a, dbg, lds, s, pairs);
                 case kQ2_K: return launch_k16<kQ2_K>(a, dbg, lds, s, pairs);
                 case kQ6_K:
-                    return dbg ? launch_one(q6k_mv_kernel<W, 4, true>, a, lds, s, pairs)
-                               : launch_one(q6k_mv_kernel<W, 4, false>, a, lds, s, pairs);
+                    return dbg ? launch_one<2 * W>(q6k_mv_kernel<2 * W, 4, true>, a, lds, s, pairs, 1)
+                               : launch_one<2 * W>(q6k_mv_kernel<2 * W, 4, false>, a, lds, s, pairs, 1);
                 default:
                     if (q8_0_ks_takes<8, 4>(a, pairs))
                         return dbg ? launch_q8_0_ks<8, 4, true>(a, s, pairs) : launch_q8_0_ks<8, 4, false>(a, s, pairs);
