@@ -2515,7 +2515,7 @@ static hipError_t launch_k16_bal(const MvArgs& a, hipStream_t s) {
     uint32_t grid, tmax;
     b1_bal_grid<TS>(a, grid, tmax);
     const uint64_t lds = k16_part_off(T, a.cols, a.batch) + (uint64_t)tmax * TS * a.nb * 16ull * a.batch * 4ull;
-    if (grid == 0 || a.ids || a.batch > 4 || lds > kMaxLds || (a.am_out && grid > kArgmaxMaxGrid))
+    if (grid == 0 || a.ids || a.batch > 8 || lds > kMaxLds || (a.am_out && grid > kArgmaxMaxGrid))
         return hipErrorInvalidValue;
     if (lds > lds_set) {
         const hipError_t e = hipFuncSetAttribute((const void*)kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -2531,11 +2531,12 @@ static hipError_t launch_k16_bal(const MvArgs& a, hipStream_t s) {
 
 template <uint32_t T>
 static hipError_t launch_k16(const MvArgs& a, bool dbg, size_t lds_plain, hipStream_t s, uint32_t pairs) {
-    // one matrix of 10240..16384 rows (on 256 CUs), up to four columns: the
-    // balanced deal, one workgroup of 16 waves per CU, four slots of a K split
-    // of 4 (14336x4096 Q2_K batches 1 / 2 / 4: 8.6 / 9.5 / 11.0 us against
-    // 9.6 / 11.1 / 14.6; Q3_K 9.9 / 10.9 / 12.5 against 11.2 / 12.7 / 16.2)
-    if (a.batch <= 4 && !a.ids && grid_rows(a, pairs) == 1 && b1_bal_units(a) >= 5 &&
+    // one matrix of 10240..16384 rows (on 256 CUs): the balanced deal, one
+    // workgroup of 16 waves per CU, four slots of a K split of 4 (14336x4096
+    // Q2_K batches 1 / 2 / 4 / 5 / 8: 8.6 / 9.5 / 11.0 / 14.1 / 16.6 us against
+    // 9.6 / 11.1 / 14.6 / 18.1 / 20.6; Q3_K 9.9 / 10.9 / 12.5 / 14.6 / 17.0
+    // against 11.2 / 12.7 / 16.2 / 18.5 / 20.7)
+    if (!a.ids && grid_rows(a, pairs) == 1 && b1_bal_units(a) >= 5 &&
         k16_part_off(T, a.cols, a.batch) + 4ull * a.nb * 16ull * a.batch * 4ull <= kMaxLds)
         return dbg ? launch_k16_bal<T, 16, 4, true>(a, s) : launch_k16_bal<T, 16, 4, false>(a, s);
     constexpr int TS = kK16W / kK16KS;

@@ -209,10 +209,11 @@ def test_block_sums_bit_exact(ctx, t, rows, cols, batch):
 
 
 @pytest.mark.parametrize("t", (DT.Q2_K, DT.Q3_K))
-@pytest.mark.parametrize("rows,batch", [(14336, 1), (14336, 3), (14330, 2), (12288, 4), (10240, 1)])
+@pytest.mark.parametrize("rows,batch", [(14336, 1), (14336, 3), (14330, 2), (12288, 4), (10240, 1), (14336, 5),
+                                        (14336, 8), (16384, 7)])
 def test_block_sums_balanced_deal(ctx, t, rows, batch):
-    """Q2_K / Q3_K at 10240..16384 rows and up to four columns run the K-split
-    kernel in the balanced deal (one workgroup per CU, four tile slots, the
+    """Q2_K / Q3_K at 10240..16384 rows run the K-split kernel in the
+    balanced deal (one workgroup per CU, four tile slots, the
     last a half tile at 14336 rows): column 0's integers bitwise, every
     column's outputs against the oracle (Q2_K bitwise)."""
     cols = 4096
