@@ -230,6 +230,20 @@ def prefill(rlq, ctx, handles, rows, cols, steps, warmup):
     }
 
 
+def host_cpu():
+    """The host CPU the CPU baselines ran on: its model name and logical CPU count."""
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return f"{model}, {os.cpu_count() or 0} logical CPUs visible"
+
+
 def cpu_baseline(dtype, w_host, rows, cols, x_host, budget_s=10.0, all_cores_s=5.0):
     """Oracle matvec (the reference's scalar path restated in C): 1 thread (the
     reference never threads a matvec), then row-parallel over the host cores
@@ -251,7 +265,8 @@ def cpu_baseline(dtype, w_host, rows, cols, x_host, budget_s=10.0, all_cores_s=5
     per = el / reps
     out = {"value": round(nbytes / per / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
            "sample": f"{reps} full {rows}x{cols} Q4_K matvecs of the benchmark's weights in {el:.1f} s "
-                     f"({per * 1e3:.1f} ms each), oracle/rlq_oracle.c built with gcc -O2 -ffp-contract=off"}
+                     f"({per * 1e3:.1f} ms each), oracle/rlq_oracle.c built with gcc -O2 -ffp-contract=off",
+           "host": host_cpu()}
     cores = max(1, min(16, os.cpu_count() or 1))
     if cores > 1:
         reps, el = timed(cores, all_cores_s)
@@ -483,7 +498,7 @@ def decode_step(rlq, ctx, steps, warmup, cpu=False):
         el = time.perf_counter() - t1
         out["cpu_baseline"] = {"value": round(1.0 / el, 4), "unit": "tok/s", "cores": 1, "kind": "port",
                                "sample": f"one decode step at context 1 (the oracle's scalar restatement, "
-                                         f"1 thread): {el:.2f} s"}
+                                         f"1 thread): {el:.2f} s", "host": host_cpu()}
     model.close()
     torch.cuda.empty_cache()
     return out
