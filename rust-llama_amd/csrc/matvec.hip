@@ -609,19 +609,52 @@ __device__ __forceinline__ void finish_argmax(const MvArgs& a, uint8_t* lds, con
     __syncthreads();
     if (!*last) return;
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    for (uint32_t b = 0; b < a.batch; ++b) {
-        unsigned long long best = 0;
-        for (uint32_t w = tid; w < G; w += nt) {
-            const unsigned long long k =
-                __hip_atomic_load(a.am_slots + (uint64_t)w * a.batch + b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            best = k > best ? k : best;
-        }
+    const uint32_t nbat = a.batch;
+    if ((nbat & (nbat - 1)) == 0) {
+        // batch 1, 2, 4 or 8: the G * batch slot keys (slot w * batch + b)
+        // eight per thread at a time, every one of them column tid % batch
+        // (blockDim is a multiple of 64); the eight loads are issued before
+        // any key is compared, so the pass costs one global round trip per
+        // 8 * blockDim keys, not one per key a thread reads (the maximum does
+        // not depend on the order)
+        const uint32_t total = G * nbat;
+        unsigned long long v = 0;
+        if (total <= nt) {  // at most one key per thread
+            if (tid < total) v = __hip_atomic_load(a.am_slots + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        } else {
+            for (uint32_t i0 = tid; i0 < total; i0 += 8 * nt) {
+                unsigned long long k[8];
 #pragma unroll
-        for (int m = 1; m < 64; m <<= 1) {
-            const unsigned long long o = __shfl_xor(best, m, 64);
-            best = o > best ? o : best;
+                for (int u = 0; u < 8; ++u) {
+                    const uint32_t i = i0 + u * nt;
+                    k[u] = i < total ? __hip_atomic_load(a.am_slots + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                                     : 0ull;
+                }
+#pragma unroll
+                for (int u = 0; u < 8; ++u) v = k[u] > v ? k[u] : v;
+            }
         }
-        if ((tid & 63) == 0 && best) atomicMax(keys + b, best);
+        // lanes of one column are those with the same lane % batch
+        for (uint32_t m = nbat; m < 64; m <<= 1) {
+            const unsigned long long o = __shfl_xor(v, m, 64);
+            v = o > v ? o : v;
+        }
+        if ((tid & 63) < nbat && v) atomicMax(keys + (tid & 63), v);
+    } else {
+        for (uint32_t b = 0; b < nbat; ++b) {
+            unsigned long long best = 0;
+            for (uint32_t w = tid; w < G; w += nt) {
+                const unsigned long long k = __hip_atomic_load(a.am_slots + (uint64_t)w * nbat + b, __ATOMIC_RELAXED,
+                                                               __HIP_MEMORY_SCOPE_AGENT);
+                best = k > best ? k : best;
+            }
+#pragma unroll
+            for (int m = 1; m < 64; m <<= 1) {
+                const unsigned long long o = __shfl_xor(best, m, 64);
+                best = o > best ? o : best;
+            }
+            if ((tid & 63) == 0 && best) atomicMax(keys + b, best);
+        }
     }
     __syncthreads();
     if (tid < a.batch) {

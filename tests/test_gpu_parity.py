@@ -322,7 +322,9 @@ def test_q6k_lm_head_128256x4096_argmax(ctx):
         assert np.array_equal(w[r * stride:(r + 1) * stride], O.quantize(O.Q6_K, xw[r * cols:(r + 1) * cols])), r
     del xw
     W = rlq.Weights(ctx, DT.Q6_K, w, rows, cols)
-    for batch in (1, 8):
+    # 256 workgroups of 512 threads: batches 1 and 2 leave the last workgroup
+    # one slot key per thread, 4 and 8 several (loaded eight at a time)
+    for batch in (1, 2, 4, 8):
         x = randn(40 + batch, batch * cols).reshape(batch, cols)
         y, am = ctx.matmul_argmax(W, torch.from_numpy(x).cuda())
         ctx.sync()
@@ -342,12 +344,15 @@ def test_q8_0_qwen_lm_head_151936x896(ctx):
     w = rlq.quantize(DT.Q8_0, xw)
     assert np.array_equal(w[:952 * 3], O.quantize(O.Q8_0, xw[:896 * 3]))
     W = rlq.Weights(ctx, DT.Q8_0, w, rows, cols)
-    x = randn(5, cols)
-    y, am = ctx.matmul_argmax(W, torch.from_numpy(x).cuda())
-    ctx.sync()
-    want = O.matvec(O.Q8_0, w, rows, cols, x, threads=16)
-    assert rel_l2(y[0].cpu().numpy(), want) <= REL_L2
-    assert int(am[0]) == O.argmax(y[0].cpu().numpy())
+    # three workgroups per CU: several slot keys per thread of the last one
+    for batch in (1, 2):
+        x = randn(5 + batch, batch * cols).reshape(batch, cols)
+        y, am = ctx.matmul_argmax(W, torch.from_numpy(x).cuda())
+        ctx.sync()
+        want = O.matmul(O.Q8_0, w, rows, cols, x, threads=16)
+        for b in range(batch):
+            assert rel_l2(y[b].cpu().numpy(), want[b]) <= REL_L2, (batch, b)
+            assert int(am[b]) == O.argmax(y[b].cpu().numpy()), (batch, b)
 
 
 def test_argmax_keys_across_calls(ctx):
