@@ -2360,12 +2360,20 @@ static hipError_t launch_b1(const MvArgs& a, hipStream_t s) {
     return hipGetLastError();
 }
 
+// Chunks in flight per wave: one with 16 waves per CU, two with fewer (the
+// weight chunks a CU has in flight before its activations arrive delay them;
+// 14336x4096 in the balanced deal 7.6 us at one against 7.9 at two, the down
+// projection 4096x14336 10.0 against 10.4; with 8 or 4 waves one is slower:
+// Q/K/V 6144x4096 7.3 against 6.8, O 4096x4096 6.4 against 5.8).
+constexpr int b1_depth(int W) { return W >= 16 ? 1 : kSmallD; }
+
 template <uint32_t T, int W, int KS, bool BAL = false>
 static hipError_t launch_b1_any(const MvArgs& a, bool dbg, bool full, hipStream_t s) {
-    return dbg ? (full ? launch_b1<T, W, KS, kSmallD, true, true, BAL>(a, s)
-                       : launch_b1<T, W, KS, kSmallD, true, false, BAL>(a, s))
-               : (full ? launch_b1<T, W, KS, kSmallD, false, true, BAL>(a, s)
-                       : launch_b1<T, W, KS, kSmallD, false, false, BAL>(a, s));
+    constexpr int D = b1_depth(W);
+    return dbg ? (full ? launch_b1<T, W, KS, D, true, true, BAL>(a, s)
+                       : launch_b1<T, W, KS, D, true, false, BAL>(a, s))
+               : (full ? launch_b1<T, W, KS, D, false, true, BAL>(a, s)
+                       : launch_b1<T, W, KS, D, false, false, BAL>(a, s));
 }
 
 // The K-split MFMA kernel for 3 to 8 columns: grid as launch_parked.
@@ -2509,8 +2517,8 @@ static hipError_t launch_q45(const MvArgs& a, uint32_t nbat, bool dbg, uint32_t 
     // 7.6 / 8.6 / 10.9 against 7.8 / 8.9 / 11.0)
     if (!a.ids && grid_rows(a, pairs) == 1) {
         const uint32_t u = b1_bal_units(a);
-        if (u >= 5 && ks_bal_takes<T, 16, 4>(a))
-            return dbg ? launch_ks<T, 16, 4, 2, true, true>(a, s, pairs) : launch_ks<T, 16, 4, 2, false, true>(a, s, pairs);
+        if (u >= 5 && ks_bal_takes<T, 16, 4>(a))  // one chunk in flight per wave (batch 4: 10.6 us against 11.2 at two)
+            return dbg ? launch_ks<T, 16, 4, 1, true, true>(a, s, pairs) : launch_ks<T, 16, 4, 1, false, true>(a, s, pairs);
         if (u >= 3 && ks_bal_takes<T, 8, 4>(a))
             return dbg ? launch_ks<T, 8, 4, 2, true, true>(a, s, pairs) : launch_ks<T, 8, 4, 2, false, true>(a, s, pairs);
     }
@@ -2677,8 +2685,10 @@ hipError_t launch_matvec_ex(uint32_t wtype, const uint8_t* w, uint64_t rows, uin
                 default:
                     if (q8_0_ks_takes<8, 4>(a, pairs))
                         return dbg ? launch_q8_0_ks<8, 4, true>(a, s, pairs) : launch_q8_0_ks<8, 4, false>(a, s, pairs);
-                    return dbg ? launch_one(q8_0_mv_kernel<W, 8, true>, a, lds, s, pairs, 3)
-                               : launch_one(q8_0_mv_kernel<W, 8, false>, a, lds, s, pairs, 3);
+                    // ten chunks in flight per wave (151936x896 + argmax: 30.3 us
+                    // against 30.9 with eight, 31.8 with six)
+                    return dbg ? launch_one(q8_0_mv_kernel<W, 10, true>, a, lds, s, pairs, 3)
+                               : launch_one(q8_0_mv_kernel<W, 10, false>, a, lds, s, pairs, 3);
             }
         };
         if (!a.ids) {
