@@ -2360,12 +2360,13 @@ static hipError_t launch_b1(const MvArgs& a, hipStream_t s) {
     return hipGetLastError();
 }
 
-// Chunks in flight per wave: one with 16 waves per CU, two with fewer (the
-// weight chunks a CU has in flight before its activations arrive delay them;
-// 14336x4096 in the balanced deal 7.6 us at one against 7.9 at two, the down
-// projection 4096x14336 10.0 against 10.4; with 8 or 4 waves one is slower:
-// Q/K/V 6144x4096 7.3 against 6.8, O 4096x4096 6.4 against 5.8).
-constexpr int b1_depth(int W) { return W >= 16 ? 1 : kSmallD; }
+// Chunks in flight per wave: one with 16 waves per CU, two with 8, three
+// with 4 (the weight chunks a CU has in flight before its activations arrive
+// delay them, and too few starve the stream: 14336x4096 in the balanced deal
+// 7.6 us at one against 7.9 at two, the down projection 4096x14336 10.0
+// against 10.4; Q/K/V 6144x4096 with 8 waves 6.8 at two, 7.3 at one, 6.9 at
+// three; O 4096x4096 with 4 waves 5.65 at three, 5.8 at two, 6.4 at one).
+constexpr int b1_depth(int W) { return W >= 16 ? 1 : W >= 8 ? 2 : 3; }
 
 template <uint32_t T, int W, int KS, bool BAL = false>
 static hipError_t launch_b1_any(const MvArgs& a, bool dbg, bool full, hipStream_t s) {
@@ -2552,7 +2553,9 @@ template <uint32_t T, int W, int KS, bool DBG>
 static hipError_t launch_k16_bal(const MvArgs& a, hipStream_t s) {
     constexpr int TS = W / KS;
     static size_t lds_set = 64 * 1024;
-    auto kernel = k16_mv_split_kernel<T, W, KS, kK16D, DBG, true>;
+    // one chunk in flight per wave with 16 waves (14336x4096 Q3_K 9.73 us
+    // against 9.98 at two, Q2_K 8.45 against 8.53)
+    auto kernel = k16_mv_split_kernel<T, W, KS, W >= 16 ? 1 : kK16D, DBG, true>;
     uint32_t grid, tmax;
     b1_bal_grid<TS>(a, grid, tmax);
     const uint64_t lds = k16_part_off(T, a.cols, a.batch) + (uint64_t)tmax * TS * a.nb * 16ull * a.batch * 4ull;
