@@ -133,7 +133,7 @@ __global__ __launch_bounds__(kAttnThreads) void attn_scores_kernel(
         const uint32_t i = tid + k * kAttnThreads, t = i / q4;
         kr[k] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         if (t < n_here && t0 + t != fresh)
-            kr[k] = *(const float4*)(kc + (uint64_t)(t0 + t) * kvw + kvh * hd + 4 * (i % q4));
+            kr[k] = load_stream_f4(kc + (uint64_t)(t0 + t) * kvw + kvh * hd + 4 * (i % q4));
     }
     for (uint32_t i = tid; i < G * hd / 2; i += kAttnThreads) {
         const uint32_t h = i / (hd / 2), p = i % (hd / 2);

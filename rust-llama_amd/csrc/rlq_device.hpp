@@ -186,6 +186,18 @@ __device__ __forceinline__ uint4 load_stream16(const void* p) {
     return make_uint4(v.x, v.y, v.z, v.w);
 }
 
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// The same for four floats read once per launch: the cached keys of the
+// attention scores.  Llama-3-8B decode step at a context of 1024, ms per token
+// on one box: plain loads 1.7437-1.7441, non-temporal keys 1.7071-1.7085,
+// non-temporal values 1.7333-1.7334, both 1.7355-1.7356 (the values stay
+// plain).
+__device__ __forceinline__ float4 load_stream_f4(const void* p) {
+    const f32x4 v = __builtin_nontemporal_load((const f32x4*)p);
+    return make_float4(v.x, v.y, v.z, v.w);
+}
+
 // ---- the reference's SSE2 exponential -------------------------------------
 // One lane of crates/quant/src/cpu_math.rs:94-123 with its exact f32
 // constants and operation order (the file is built without contraction).
