@@ -63,8 +63,9 @@ constexpr uint32_t kUnsafeAbsSum = 17753;  // floor((2^24 - 1) / 945)
 //                 da [token 128] f32                         512 B
 //                 flags [token 128] u8                       128 B
 // Group g, k-step s, k half h, slot t holds the value at block position
-// 64g + 32(s/2) + 16h + 8(s%2) + kPerm[t], kPerm = {0,2,1,3,4,6,5,7}: the
-// order in which the weight dequantizer below produces sc*q.  flags: bit 0 a
+// 64g + 32(s/2) + q45_pos_of_slot(16h + 8(s%2) + kPerm[t]), kPerm =
+// {0,2,1,3,4,6,5,7}: the order in which the weight dequantizer below produces
+// sc*q from the weights' slots (rlq_layout.hpp).  flags: bit 0 a
 // data error in the token's block, bit 1 sum |q8| > kUnsafeAbsSum.
 constexpr uint32_t kActGroupBytes = 16384;
 constexpr uint32_t kRecDa = 4096, kRecFlags = 4608, kActRecordBytes = 4736;
@@ -121,10 +122,14 @@ __global__ __launch_bounds__(256) void gemm_act_kernel(const float* __restrict__
         report_error(err_word, o.kind == kKindNonFinite
                                    ? error_key(err_column0 + m, kKindNonFinite, b * 256ull + o.index)
                                    : error_key(err_column0 + m, kKindScale, b));
+    // the weights' slot order (q45_slots): slot 16 hh + t holds position
+    // q45_pos_of_slot(16 hh + t) of the sub-block
+    const uint4 sl = q45_slots(o.q, r16 & 1);
+    const uint32_t sw[4] = {sl.x, sl.y, sl.z, sl.w};
     int32_t q[16];
 #pragma unroll
-    for (int t = 0; t < 16; ++t) q[t] = (int32_t)(int8_t)(o.q[t / 4] >> (8 * (t % 4)));
-    // positions 16 r16 + t: group r16/4, k-steps 2((r16/2)%2) + t/8, k half r16%2
+    for (int t = 0; t < 16; ++t) q[t] = (int32_t)(int8_t)(sw[t / 4] >> (8 * (t % 4)));
+    // slots 16 (r16%2) + t of sub-block r16/2: group r16/4, k-steps 2((r16/2)%2) + t/8, k half r16%2
     uint8_t* ag = tile + act_group_offset(b, r16 / 4);
     const uint32_t s0 = 2 * ((r16 >> 1) & 1), hh = r16 & 1;
     constexpr int kPerm[8] = {0, 2, 1, 3, 4, 6, 5, 7};

@@ -404,7 +404,8 @@ __device__ __forceinline__ bool stage_q8k(const MvArgs& a, uint8_t* lds, const L
                 report_error(a.err_word, o.kind == kKindNonFinite ? quant_nonfinite_key(a, b, blk * 256ull + o.index)
                                                                   : quant_scale_key(a, b, blk));
         }
-        *(uint4*)(lds + b * L.S + e0) = make_uint4(o.q[0], o.q[1], o.q[2], o.q[3]);
+        *(uint4*)(lds + b * L.S + e0) =
+            BSUMS == kBsQuarters ? q45_slots(o.q, r16 & 1) : make_uint4(o.q[0], o.q[1], o.q[2], o.q[3]);
         if (r16 == 0) *(float*)(lds + L.d_off + (blk * 8 + b) * 4) = o.d;
         if (BSUMS != kBsNone)
             *(int16_t*)(lds + L.bs_off + (blk * 8 + b) * 32 + (BSUMS == kBsQuarters ? bs_slot(r16) : r16) * 2) =
@@ -483,9 +484,12 @@ template <int W>
 __device__ __forceinline__ bool stage_planes(const MvArgs& a, uint8_t* lds, const LdsMap& L, uint32_t wtype) {
     const uint32_t K = a.cols, bs = wtype == kQ8_0 ? 32 : 256, nb = K / bs;
     const uint32_t tid = threadIdx.x, nt = W * 64;
-    for (uint32_t i = tid; i < a.batch * (K / 16); i += nt) {
+    const bool slots = wtype == kQ4_K || wtype == kQ5_K;
+    for (uint32_t i = tid; i < a.batch * (K / 16); i += nt) {  // lane pairs hold unit pairs (i, i ^ 1)
         const uint32_t b = i / (K / 16), e = (i % (K / 16)) * 16;
-        *(uint4*)(lds + b * L.S + e) = *(const uint4*)(a.pre.q + (uint64_t)b * K + e);
+        const uint4 v = *(const uint4*)(a.pre.q + (uint64_t)b * K + e);
+        const uint32_t q[4] = {v.x, v.y, v.z, v.w};
+        *(uint4*)(lds + b * L.S + e) = slots ? q45_slots(q, i & 1) : v;
     }
     int bad = 0;
     for (uint32_t i = tid; i < a.batch * nb; i += nt) {
@@ -535,7 +539,8 @@ __device__ __forceinline__ void prefetch_planes(const MvArgs& a, PlanePrefetch& 
     }
     p.bs = tid < units / 4 ? *(const uint2*)(a.pre.bsum + 4 * tid) : make_uint2(0, 0);
 }
-// stage_planes from the prefetched registers (Q8_K planes, quarter-ordered bsums)
+// stage_planes from the prefetched registers (Q8_K planes of Q4_K / Q5_K:
+// the slot order and quarter-ordered bsums)
 template <int W>
 __device__ __forceinline__ bool stage_planes_prefetched(const MvArgs& a, uint8_t* lds, const LdsMap& L,
                                                         const PlanePrefetch& p) {
@@ -543,7 +548,9 @@ __device__ __forceinline__ bool stage_planes_prefetched(const MvArgs& a, uint8_t
 #pragma unroll
     for (uint32_t r = 0; r < kPlaneRegs; ++r) {
         const uint32_t i = tid + r * W * 64;
-        if (i < units) *(uint4*)(lds + (i / upc) * L.S + (i % upc) * 16) = p.q[r];
+        const uint32_t q[4] = {p.q[r].x, p.q[r].y, p.q[r].z, p.q[r].w};
+        const uint4 v = q45_slots(q, tid & 1);  // (both lanes of a pair, before the bound)
+        if (i < units) *(uint4*)(lds + (i / upc) * L.S + (i % upc) * 16) = v;
     }
     if (tid < a.batch * nb) *(float*)(lds + L.d_off + ((tid % nb) * 8 + tid / nb) * 4) = p.d;
     if (tid < units / 4) {
@@ -1041,38 +1048,163 @@ __global__ __launch_bounds__(W * 64) void q45_mv_ks_kernel(MvArgs a) {
     finish_argmax(a, lds, L);
 }
 
-// Q4_K, one or two columns: v_dot4_i32_i8 on the VALU.
+// ---------------------------------------------------------------------------
+// The reference's f32 order for one column (matvec_extra.rs:223-294)
+// ---------------------------------------------------------------------------
+// The reference keeps eight f32 accumulators lanes[j % 8] over all blocks of
+// a row: per block, integers[l] = the exact dot over the elements j with
+// j % 8 == l, then (Q4_K / Q5_K) sum -= dmin * mins, then lanes[l] +=
+// d * integers[l]; at the end sum += lanes[0], ..., lanes[7].  The one-column
+// Q4_K / Q5_K kernels reproduce that sequence bit for bit: the weights' slot
+// order (rlq_layout.hpp) puts the four values of one lane class of a
+// sub-block in one 4-byte word, so every v_dot4 yields one (sub-block, class)
+// integer; each block's eight terms d * integers[l] and its mins term
+// dmin * mins are parked in LDS, and the row's sum is then formed in the
+// reference's order (exact_row_sum).
+
+// Sums over lane pairs l, l ^ 32 and l, l ^ 16 (v_permlane32_swap /
+// v_permlane16_swap exchange the two halves, resp. adjacent 16-lane rows, of
+// a value with itself), in every lane.
+__device__ __forceinline__ int32_t sum_xor32(int32_t v) {
+    const auto r = __builtin_amdgcn_permlane32_swap((unsigned)v, (unsigned)v, false, false);
+    return (int32_t)(r[0] + r[1]);
+}
+__device__ __forceinline__ int32_t sum_xor16(int32_t v) {
+    const auto r = __builtin_amdgcn_permlane16_swap((unsigned)v, (unsigned)v, false, false);
+    return (int32_t)(r[0] + r[1]);
+}
+
+// Parked terms per (tile slot, block): [4][16] float2, lane kq of row n
+// holding classes 4 (kq % 2) + 2 (kq / 2) and + 1, then [16] f32 mins terms.
+constexpr uint32_t kParkBlockBytes = 4 * 16 * 8 + 16 * 4;
+__host__ __device__ inline uint32_t park_bytes(uint32_t nb) { return nb * kParkBlockBytes; }
+
+// Exact integers of one Q4_K / Q5_K chunk for lane (n, kq = 2g + h): I[k]
+// the reference's integers[4h + k] of row n (whole: the lanes kq and kq ^ 2
+// hold sub-blocks 2g, 2g+1, 2g+4, 2g+5 and 2(1-g), ... of the same
+// classes), M the whole mins sum (matvec_extra.rs:252-270).  p is this
+// lane's activation row at the block (sub-block 2g, slots 16h ..), bs its
+// bsum word, psel the byte selector of the scale pair (2g, 2g+1).
+struct Q45Lanes {
+    int32_t I[4];
+    int32_t M;
+};
+template <uint32_t T>
+__device__ __forceinline__ Q45Lanes q45_lane_ints(const Q4Step<T>& cur, const uint8_t* p, const uint8_t* bs,
+                                                  uint32_t kq, uint32_t psel) {
+    typedef short s2 __attribute__((ext_vector_type(2)));
+    const Q4Scales q = q4k_scales(cur.h);
+    uint32_t l0[4] = {cur.w0.x & 0x0f0f0f0fu, cur.w0.y & 0x0f0f0f0fu, cur.w0.z & 0x0f0f0f0fu, cur.w0.w & 0x0f0f0f0fu};
+    uint32_t h0[4], h1[4];
+    hi_nibbles64(cur.w0, h0);
+    uint32_t l1[4] = {cur.w1.x & 0x0f0f0f0fu, cur.w1.y & 0x0f0f0f0fu, cur.w1.z & 0x0f0f0f0fu, cur.w1.w & 0x0f0f0f0fu};
+    hi_nibbles64(cur.w1, h1);
+    if constexpr (T == kQ5_K) {
+        const Q5High hb = q5_high(cur.qh, kq);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            l0[i] |= hb.l0[i];
+            h0[i] |= hb.h0[i];
+            l1[i] |= hb.l1[i];
+            h1[i] |= hb.h1[i];
+        }
+    }
+    const uint4 x0 = *(const uint4*)(p), x1 = *(const uint4*)(p + 32);
+    const uint4 x4 = *(const uint4*)(p + 128), x5 = *(const uint4*)(p + 160);
+    const uint32_t a0[4] = {x0.x, x0.y, x0.z, x0.w}, a1[4] = {x1.x, x1.y, x1.z, x1.w};
+    const uint32_t a4[4] = {x4.x, x4.y, x4.z, x4.w}, a5[4] = {x5.x, x5.y, x5.z, x5.w};
+    // scales of sub-blocks (2g, 2g+1) and (2g+4, 2g+5) as i16 pairs
+    const uint32_t S01 = __builtin_amdgcn_perm(0u, q.scA, psel), S45 = __builtin_amdgcn_perm(0u, q.scB, psel);
+    Q45Lanes o;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        // the class's four-value dots of the four sub-blocks: |.| <= 31 * 128 * 4
+        // fits i16, so each pair is scaled by one v_dot2
+        const int32_t i0 = dot4(l0[k], a0[k], 0), i1 = dot4(h0[k], a1[k], 0);
+        const int32_t i4 = dot4(l1[k], a4[k], 0), i5 = dot4(h1[k], a5[k], 0);
+        const uint32_t P01 = __builtin_amdgcn_perm((uint32_t)i1, (uint32_t)i0, 0x05040100u);
+        const uint32_t P45 = __builtin_amdgcn_perm((uint32_t)i5, (uint32_t)i4, 0x05040100u);
+        const int32_t I = __builtin_amdgcn_sdot2(
+            __builtin_bit_cast(s2, S01), __builtin_bit_cast(s2, P01),
+            __builtin_amdgcn_sdot2(__builtin_bit_cast(s2, S45), __builtin_bit_cast(s2, P45), 0, false), false);
+        o.I[k] = sum_xor32(I);
+    }
+    // mins: this quarter's four 16-value groups, then all four quarters
+    const uint32_t M01 = __builtin_amdgcn_perm(0u, q.mnA, psel), M45 = __builtin_amdgcn_perm(0u, q.mnB, psel);
+    const uint2 bw = *(const uint2*)bs;
+    const int32_t M = __builtin_amdgcn_sdot2(
+        __builtin_bit_cast(s2, M01), __builtin_bit_cast(s2, bw.x),
+        __builtin_amdgcn_sdot2(__builtin_bit_cast(s2, M45), __builtin_bit_cast(s2, bw.y), 0, false), false);
+    o.M = sum_xor32(sum_xor16(M));
+    return o;
+}
+
+// Park one block's terms of lane (n, kq): d * integers[l] for its classes
+// (matvec_extra.rs:287-289, the product rounded to f32) and, when mins, the
+// mins term dmin * mins (:268).  pk / pm: the block's parked records.
+__device__ __forceinline__ void park_terms(float2* pk, float* pm, uint32_t lane, uint32_t n, uint32_t kq, float d,
+                                           const int32_t (&I)[4], bool mins, float dmin, int32_t M) {
+    const bool g = (kq >> 1) != 0;
+    pk[lane] = make_float2(d * (float)(g ? I[2] : I[0]), d * (float)(g ? I[3] : I[1]));
+    if (mins && kq == 0) pm[n] = dmin * (float)M;
+}
+
+// The row's f32 in the reference's order from its parked terms (nb blocks;
+// pk, pm the slot's records): lanes[l] over the blocks in order, sum minus
+// the mins terms in order, then sum + lanes[0..7].  Every lane of row n
+// returns it; the four lanes (n, kq) of the row must be active.
+__device__ __forceinline__ float exact_row_sum(const float2* pk, const float* pm, uint32_t nb, uint32_t n,
+                                               uint32_t kq, bool mins) {
+    const float2* p = pk + (2 * (kq & 1) + (kq >> 1)) * 16 + n;  // classes 2 kq, 2 kq + 1
+    float l0 = 0.0f, l1 = 0.0f;
+    for (uint32_t b = 0; b < nb; ++b) {
+        const float2 v = p[b * 64];
+        l0 += v.x;
+        l1 += v.y;
+    }
+    float s = 0.0f;
+    if (mins)
+        for (uint32_t b = 0; b < nb; ++b) s -= pm[b * 16 + n];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        s += __shfl(l0, (int)(n + 16 * j), 64);
+        s += __shfl(l1, (int)(n + 16 * j), 64);
+    }
+    return s;
+}
+
+// Q4_K / Q5_K, one column with a shared Q8_K image: v_dot4_i32_i8 on the
+// VALU (the SiLU-pair epilogue, pre-quantized planes, MUL_MAT_ID pairs).
 //
 // A workgroup of W waves works on TS = W / KS tiles at a time; the KS waves of
 // a tile take its blocks kp, kp + KS, ... (kp = the wave's K part), so a tile's
 // bytes stream through KS waves and every SIMD holds several waves.  Lane
-// (n, kq), kq = 2g + h, multiplies half h of sub-blocks 2g, 2g+1 (qs bytes of
-// w0) and 2g+4, 2g+5 (w1) of row n; its integer partials and its share of the
-// mins (the bsums of exactly those 16-value groups) are scaled per block.  At
-// the end of a tile the wave adds its four K quarters and parks the row sums
-// in LDS; after the last tile the workgroup adds the KS parts in order.
+// (n, kq), kq = 2g + h, multiplies slots 16h .. 16h + 15 (lane classes
+// 4h .. 4h + 3) of sub-blocks 2g, 2g+1 (qs bytes of w0) and 2g+4, 2g+5 (w1)
+// of row n (q45_lane_ints); every block's terms are parked in LDS, and after
+// the last tile the workgroup forms each row's sum in the reference's order
+// (exact_row_sum).
 template <int W, int KS>
 struct SmallGeom {
     static constexpr int TS = W / KS;
 };
 
-// LDS bytes of the small kernel: the activations plus the parked partials
-// [tmax][TS][KS][16][B] f32, tmax = tiles per (workgroup, tile slot).
+// LDS bytes of the small kernel: the activations plus the parked terms
+// [tmax][TS][nb] (park_terms), tmax = tiles per (workgroup, tile slot).
 __host__ __device__ inline uint32_t small_part_off(uint32_t cols, uint32_t batch) {
     return (lds_map(kQ4_K, cols, batch).total + 15u) & ~15u;
 }
-__host__ __device__ inline uint32_t small_lds_bytes(uint32_t cols, uint32_t batch, uint32_t tmax, uint32_t ts,
-                                                    uint32_t ks) {
-    return small_part_off(cols, batch) + tmax * ts * ks * 16u * batch * 4u;
+__host__ __device__ inline uint32_t small_lds_bytes(uint32_t cols, uint32_t tmax, uint32_t ts) {
+    return small_part_off(cols, 1) + tmax * ts * park_bytes(cols / 256);
 }
 
-template <uint32_t T, int W, int KS, int D, int B, bool DBG>
-__global__ __launch_bounds__(W * 64) void q4k_mv_small_kernel(MvArgs a) {
+// (two workgroups of 8 waves per CU: at most 128 VGPRs)
+template <uint32_t T, int W, int KS, int D, bool DBG>
+__global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(4))) void q4k_mv_small_kernel(MvArgs a) {
     constexpr int TS = SmallGeom<W, KS>::TS;
     if (!mv_enter(a)) return;
     extern __shared__ __align__(16) uint8_t lds[];
-    const LdsMap L = lds_map(T, a.cols, a.batch);
-    float* part = (float*)(lds + small_part_off(a.cols, a.batch));
+    const LdsMap L = lds_map(T, a.cols, 1);
     const uint32_t lane = threadIdx.x & 63, n = lane & 15, kq = lane >> 4;
     // wave-uniform indices in scalar registers: loop control stays on the SALU
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -1083,6 +1215,8 @@ __global__ __launch_bounds__(W * 64) void q4k_mv_small_kernel(MvArgs a) {
     const uint32_t my_tiles = t0 < ntiles ? (ntiles - 1 - t0) / tstride + 1 : 0;
     const uint32_t bpt = kp < nb ? (nb - 1 - kp) / KS + 1 : 0;  // blocks of each tile this wave takes
     const uint32_t steps = my_tiles * bpt;
+    float2* park = (float2*)(lds + small_part_off(a.cols, 1));
+    float* parkm = (float*)(park + tmax * TS * nb * 64);
 
     if (threadIdx.x < 16) *(uint4*)(lds + L.zero_off + threadIdx.x * 16) = make_uint4(0, 0, 0, 0);
     if (threadIdx.x < 8) ((unsigned long long*)(lds + L.am_off))[threadIdx.x] = 0ull;
@@ -1109,77 +1243,29 @@ __global__ __launch_bounds__(W * 64) void q4k_mv_small_kernel(MvArgs a) {
     if (a.zero_pair) return zero_slot_tiles<W, TS>(a, tmax, tstride);
 
     const uint32_t g = kq >> 1, h = kq & 1;
-    // activation of (sub-block 2g, half h) and its neighbours: +32 (2g+1),
-    // +128 (2g+4), +160 (2g+5)
+    // activation of (sub-block 2g, slots 16h ..) and its neighbours: +32
+    // (2g+1), +128 (2g+4), +160 (2g+5)
     const uint8_t* a_row = lds + 64 * g + 16 * h;
     const uint8_t* bs_row = lds + L.bs_off + kq * 8;
+    const uint32_t psel = (2 * g) | 0x0c00u | (2 * g + 1) << 16 | 0x0c000000u;
 
-    float acc[B];
-#pragma unroll
-    for (int b = 0; b < B; ++b) acc[b] = 0.0f;
     uint32_t ti = 0, tile = t0, blk = kp, j = 0;
     auto compute = [&](const Q4Step<T>& cur) {
-        const Q4Scales q = q4k_scales(cur.h);
-        const int32_t s0 = __builtin_amdgcn_ubfe(q.scA, 16 * g, 8), s1 = __builtin_amdgcn_ubfe(q.scA, 16 * g + 8, 8);
-        const int32_t s4 = __builtin_amdgcn_ubfe(q.scB, 16 * g, 8), s5 = __builtin_amdgcn_ubfe(q.scB, 16 * g + 8, 8);
-        const int32_t m0 = __builtin_amdgcn_ubfe(q.mnA, 16 * g, 8), m1 = __builtin_amdgcn_ubfe(q.mnA, 16 * g + 8, 8);
-        const int32_t m4 = __builtin_amdgcn_ubfe(q.mnB, 16 * g, 8), m5 = __builtin_amdgcn_ubfe(q.mnB, 16 * g + 8, 8);
-        uint32_t l0[4] = {cur.w0.x & 0x0f0f0f0fu, cur.w0.y & 0x0f0f0f0fu, cur.w0.z & 0x0f0f0f0fu,
-                          cur.w0.w & 0x0f0f0f0fu};
-        uint32_t h0[4], h1[4];
-        hi_nibbles64(cur.w0, h0);
-        uint32_t l1[4] = {cur.w1.x & 0x0f0f0f0fu, cur.w1.y & 0x0f0f0f0fu, cur.w1.z & 0x0f0f0f0fu,
-                          cur.w1.w & 0x0f0f0f0fu};
-        hi_nibbles64(cur.w1, h1);
-        if constexpr (T == kQ5_K) {
-            const Q5High hb = q5_high(cur.qh, kq);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                l0[i] |= hb.l0[i];
-                h0[i] |= hb.h0[i];
-                l1[i] |= hb.l1[i];
-                h1[i] |= hb.h1[i];
-            }
-        }
+        const Q45Lanes o = q45_lane_ints<T>(cur, a_row + blk * 256, bs_row + blk * 256, kq, psel);
         const float dw = half_to_float(cur.h.x), dmw = half_to_float(cur.h.x >> 16);
-#pragma unroll
-        for (int b = 0; b < B; ++b) {
-            const uint8_t* p = a_row + b * L.S + blk * 256;
-            const uint4 x0 = *(const uint4*)(p), x1 = *(const uint4*)(p + 32);
-            const uint4 x4 = *(const uint4*)(p + 128), x5 = *(const uint4*)(p + 160);
-            const int32_t i0 = dot4(l0[3], x0.w, dot4(l0[2], x0.z, dot4(l0[1], x0.y, dot4(l0[0], x0.x, 0))));
-            const int32_t i1 = dot4(h0[3], x1.w, dot4(h0[2], x1.z, dot4(h0[1], x1.y, dot4(h0[0], x1.x, 0))));
-            const int32_t i4 = dot4(l1[3], x4.w, dot4(l1[2], x4.z, dot4(l1[1], x4.y, dot4(l1[0], x4.x, 0))));
-            const int32_t i5 = dot4(h1[3], x5.w, dot4(h1[2], x5.z, dot4(h1[1], x5.y, dot4(h1[0], x5.x, 0))));
-            int32_t I = mad24(s0, i0, mad24(s1, i1, mad24(s4, i4, __mul24(s5, i5))));
-            // this quarter's share of the mins: its four 16-value groups
-            const uint2 bw = *(const uint2*)(bs_row + (blk * 8 + b) * 32);
-            int32_t M = mad24(m0, (int16_t)bw.x, mad24(m1, (int32_t)bw.x >> 16,
-                              mad24(m4, (int16_t)bw.y, __mul24(m5, (int32_t)bw.y >> 16))));
-            const float da = *(const float*)(lds + L.d_off + (blk * 8 + b) * 4);
-            acc[b] += (dw * da) * (float)I - (dmw * da) * (float)M;
-            if (DBG && b == 0) {  // exact block integers: add the four quarters
-                I += __shfl_xor(I, 16, 64);
-                I += __shfl_xor(I, 32, 64);
-                M += __shfl_xor(M, 16, 64);
-                M += __shfl_xor(M, 32, 64);
-                const uint32_t row = tile * kTileRows + n;
-                if (kq == 0 && row < a.rows) {
-                    a.dbg_isum[(uint64_t)row * nb + blk] = I;
-                    a.dbg_imin[(uint64_t)row * nb + blk] = M;
-                }
+        const float da = *(const float*)(lds + L.d_off + blk * 32);
+        const uint32_t rec = (ti * TS + ts) * nb + blk;
+        park_terms(park + rec * 64, parkm + rec * 16, lane, n, kq, dw * da, o.I, true, dmw * da, o.M);
+        if (DBG) {  // exact block integers: the eight classes
+            const int32_t I = sum_xor16(o.I[0] + o.I[1] + o.I[2] + o.I[3]);
+            const uint32_t row = tile * kTileRows + n;
+            if (kq == 0 && row < a.rows) {
+                a.dbg_isum[(uint64_t)row * nb + blk] = I;
+                a.dbg_imin[(uint64_t)row * nb + blk] = o.M;
             }
         }
         blk += KS;
-        if (++j == bpt) {  // this wave's share of the tile is done: park the row sums
-#pragma unroll
-            for (int b = 0; b < B; ++b) {
-                float v = acc[b];
-                v += __shfl_xor(v, 16, 64);
-                v += __shfl_xor(v, 32, 64);
-                if (kq == 0) part[(((ti * TS + ts) * KS + kp) * 16 + n) * B + b] = v;
-                acc[b] = 0.0f;
-            }
+        if (++j == bpt) {
             j = 0;
             blk = kp;
             ++ti;
@@ -1189,53 +1275,41 @@ __global__ __launch_bounds__(W * 64) void q4k_mv_small_kernel(MvArgs a) {
     pipeline<D>(steps, buf, issue, compute);
     __syncthreads();
 
+    // each row's sum in the reference's order, one wave per tile slot (pair)
     if (TS % 2 == 0 && a.epilogue == kEpSiluPair) {
         // tile slots (2 q, 2 q + 1) hold gate and up rows of the same 16
         // outputs (llama.rs:367-371: gate = silu(gate); gate *= up)
-        for (uint32_t it = threadIdx.x; it < tmax * (TS / 2) * 16; it += W * 64) {
-            const uint32_t r = it % 16, q = (it / 16) % (TS / 2), til = it / 16 / (TS / 2);
+        for (uint32_t it = wave; it < tmax * (TS / 2); it += W) {
+            const uint32_t q = it % (TS / 2), til = it / (TS / 2);
             const uint32_t t = blockIdx.x * TS + 2 * q + til * tstride;  // the gate tile, even
-            if (t + 1 < ntiles) {
-                float g = 0.0f, u = 0.0f;
-#pragma unroll
-                for (int k = 0; k < KS; ++k)
-                    if ((uint32_t)k < nb) {
-                        g += part[(((til * TS + 2 * q) * KS + k) * 16 + r) * B];
-                        u += part[(((til * TS + 2 * q + 1) * KS + k) * 16 + r) * B];
-                    }
-                if (a.chk) {  // the gate and up outputs themselves (math.rs:167)
-                    check_finite(a, kChkOut, g);
-                    check_finite(a, kChkOut, u);
-                }
-                a.y[(t / 2) * kTileRows + r] = (g / (1.0f + sse2_exp(0.0f - g))) * u;
+            if (t + 1 >= ntiles) continue;                                // (wave-uniform)
+            const uint32_t sg = (til * TS + 2 * q) * nb;
+            const float gs = exact_row_sum(park + sg * 64, parkm + sg * 16, nb, n, kq, true);
+            const float us = exact_row_sum(park + (sg + nb) * 64, parkm + (sg + nb) * 16, nb, n, kq, true);
+            if (kq != 0) continue;
+            if (a.chk) {  // the gate and up outputs themselves (math.rs:167)
+                check_finite(a, kChkOut, gs);
+                check_finite(a, kChkOut, us);
             }
+            a.y[(t / 2) * kTileRows + n] = (gs / (1.0f + sse2_exp(0.0f - gs))) * us;
         }
         return;
     }
-    // add the K parts of every parked (tile, row) in order and store
+    unsigned long long best = 0;
+    for (uint32_t slot = wave; slot < tmax * TS; slot += W) {
+        const uint32_t t = blockIdx.x * TS + slot % TS + (slot / TS) * tstride;
+        if (t >= ntiles) continue;  // (wave-uniform)
+        const float v = exact_row_sum(park + slot * nb * 64, parkm + slot * nb * 16, nb, n, kq, true);
+        const uint32_t row = t * kTileRows + n;
+        if (kq == 0 && row < a.rows) store_out(a, row, 0, v, best);
+    }
+    if (a.am_out) {
 #pragma unroll
-    for (int b = 0; b < B; ++b) {
-        unsigned long long best = 0;
-        for (uint32_t it = threadIdx.x; it < tmax * TS * 16; it += W * 64) {
-            const uint32_t r = it % 16, slot = it / 16, tsl = slot % TS, til = slot / TS;
-            const uint32_t t = blockIdx.x * TS + tsl + til * tstride;
-            const uint32_t row = t * kTileRows + r;
-            if (t < ntiles && row < a.rows && (uint32_t)b < a.batch) {
-                float v = 0.0f;
-#pragma unroll
-                for (int k = 0; k < KS; ++k)  // waves with no block of the tile (nb < KS) parked nothing
-                    if ((uint32_t)k < nb) v += part[((slot * KS + k) * 16 + r) * B + b];
-                store_out(a, row, b, v, best);
-            }
+        for (int m = 1; m < 64; m <<= 1) {
+            const unsigned long long o = __shfl_xor(best, m, 64);
+            best = o > best ? o : best;
         }
-        if (a.am_out) {
-#pragma unroll
-            for (int m = 1; m < 64; m <<= 1) {
-                const unsigned long long o = __shfl_xor(best, m, 64);
-                best = o > best ? o : best;
-            }
-            if (lane == 0 && best && (uint32_t)b < a.batch) atomicMax((unsigned long long*)(lds + L.am_off) + b, best);
-        }
+        if (lane == 0 && best) atomicMax((unsigned long long*)(lds + L.am_off), best);
     }
     finish_argmax(a, lds, L);
 }
@@ -1244,13 +1318,14 @@ __global__ __launch_bounds__(W * 64) void q4k_mv_small_kernel(MvArgs a) {
 // quantizes only the blocks it multiplies (blocks kp, kp + KS, ... of every
 // tile it takes, at most four) while its first weight chunks are in flight, so
 // a workgroup's Q8_K image costs one barrier (two with the RMSNorm transform)
-// and no shared quantization pass.  A tile's K parts are parked in LDS and
-// counted with a workgroup-scope atomic; the wave that brings the count to
-// the tile's part count adds the parts in K order and stores the row (no
-// barrier between tiles).  LDS after the Q8_K image: partials
-// [tmax][TS][KS][16], counters [tmax][TS], residuals [tmax][TS][16].
-__host__ __device__ inline uint32_t b1_lds_bytes(uint32_t cols, uint32_t tmax, uint32_t ts, uint32_t ks) {
-    return small_part_off(cols, 1) + tmax * ts * ks * 16u * 4u + tmax * ts * 4u + tmax * ts * 16u * 4u;
+// and no shared quantization pass.  Every block's terms are parked in LDS
+// (park_terms) and a tile's K parts are counted with a workgroup-scope
+// atomic; the wave that brings the count to the tile's part count forms each
+// row's sum in the reference's order (exact_row_sum) and stores it (no
+// barrier between tiles).  LDS after the Q8_K image: parked terms
+// [tmax][TS][nb], counters [tmax][TS], residuals [tmax][TS][16].
+__host__ __device__ inline uint32_t b1_lds_bytes(uint32_t cols, uint32_t tmax, uint32_t ts) {
+    return small_part_off(cols, 1) + tmax * ts * (park_bytes(cols / 256) + 4u + 16u * 4u);
 }
 
 // The RMSNorm scale (math.rs:210-221) from the values of the workgroup's own
@@ -1299,7 +1374,6 @@ __global__ __launch_bounds__(W * 64) void q45_mv_b1_kernel(MvArgs a) {
     static_assert(!BAL || TS == 2 || TS == 4, "the balanced deal takes two or four tile slots");
     extern __shared__ __align__(16) uint8_t lds[];
     const LdsMap L = lds_map(T, a.cols, 1);
-    float* part = (float*)(lds + small_part_off(a.cols, 1));
     const uint32_t lane = threadIdx.x & 63, n = lane & 15, kq = lane >> 4;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t ts = wave / KS, kp = wave % KS;
@@ -1327,7 +1401,11 @@ __global__ __launch_bounds__(W * 64) void q45_mv_b1_kernel(MvArgs a) {
     const uint32_t bpt = kp < nb ? (nb - 1 - kp) / KS + 1 : 0;  // blocks of each tile this wave takes
     const uint32_t steps = my_tiles * bpt;
     const uint32_t nk = (uint32_t)KS < nb ? (uint32_t)KS : nb;  // waves of a tile that take blocks
-    uint32_t* cnt = (uint32_t*)(part + tmax * TS * KS * 16);
+    // LDS after the Q8_K image: parked terms [tmax * TS][nb] (park_terms),
+    // counters [tmax * TS], residuals [tmax * TS][16]
+    float2* park = (float2*)(lds + small_part_off(a.cols, 1));
+    float* parkm = (float*)(park + tmax * TS * nb * 64);
+    uint32_t* cnt = (uint32_t*)(parkm + tmax * TS * nb * 16);
     float* rs = (float*)(cnt + tmax * TS);
     for (uint32_t i = threadIdx.x; i < tmax * TS; i += W * 64) cnt[i] = 0;
     const bool rms = FULL && a.xform == kXfRmsNorm;
@@ -1384,7 +1462,7 @@ __global__ __launch_bounds__(W * 64) void q45_mv_b1_kernel(MvArgs a) {
                 report_error(a.err_word, o.kind == kKindNonFinite ? quant_nonfinite_key(a, 0, xblk * 256ull + o.index)
                                                                   : quant_scale_key(a, 0, xblk));
         }
-        *(uint4*)(lds + xblk * 256 + r16 * 16) = make_uint4(o.q[0], o.q[1], o.q[2], o.q[3]);
+        *(uint4*)(lds + xblk * 256 + r16 * 16) = q45_slots(o.q, r16 & 1);
         if (r16 == 0) *(float*)(lds + L.d_off + xblk * 32) = o.d;
         *(int16_t*)(lds + L.bs_off + xblk * 256 + bs_slot(r16) * 2) = (int16_t)o.bsum;
     }
@@ -1396,95 +1474,33 @@ __global__ __launch_bounds__(W * 64) void q45_mv_b1_kernel(MvArgs a) {
     }
 
     const uint32_t g = kq >> 1, h = kq & 1;
-    // activation of (sub-block 2g, half h) and its neighbours: +32 (2g+1),
-    // +128 (2g+4), +160 (2g+5)
+    // activation of (sub-block 2g, slots 16h ..) and its neighbours: +32
+    // (2g+1), +128 (2g+4), +160 (2g+5)
     const uint8_t* a_row = lds + 64 * g + 16 * h;
     const uint8_t* bs_row = lds + L.bs_off + kq * 8;
     // bytes 2g and 2g + 1 of a packed scale word, widened to two i16 lanes
     const uint32_t psel = (2 * g) | 0x0c00u | (2 * g + 1) << 16 | 0x0c000000u;
-    typedef short s2 __attribute__((ext_vector_type(2)));
     unsigned long long best = 0;
-    float acc = 0.0f;
     uint32_t ti = 0, blk = kp, j = 0, tile = tile_of(0);
-    // the K parts of slot sl added in K order
-    auto sum_parts = [&](uint32_t sl) {
-        float s = 0.0f;
-#pragma unroll
-        for (int k = 0; k < KS; ++k)
-            if ((uint32_t)k < nk) s += part[(sl * KS + k) * 16 + n];
-        return s;
-    };
     auto compute = [&](const Q4Step<T>& cur) {
-        const Q4Scales q = q4k_scales(cur.h);
-        uint32_t l0[4] = {cur.w0.x & 0x0f0f0f0fu, cur.w0.y & 0x0f0f0f0fu, cur.w0.z & 0x0f0f0f0fu,
-                          cur.w0.w & 0x0f0f0f0fu};
-        uint32_t h0[4], h1[4];
-        hi_nibbles64(cur.w0, h0);
-        uint32_t l1[4] = {cur.w1.x & 0x0f0f0f0fu, cur.w1.y & 0x0f0f0f0fu, cur.w1.z & 0x0f0f0f0fu,
-                          cur.w1.w & 0x0f0f0f0fu};
-        hi_nibbles64(cur.w1, h1);
-        if constexpr (T == kQ5_K) {
-            const Q5High hb = q5_high(cur.qh, kq);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                l0[i] |= hb.l0[i];
-                h0[i] |= hb.h0[i];
-                l1[i] |= hb.l1[i];
-                h1[i] |= hb.h1[i];
-            }
-        }
+        const Q45Lanes o = q45_lane_ints<T>(cur, a_row + blk * 256, bs_row + blk * 256, kq, psel);
         const float dw = half_to_float(cur.h.x), dmw = half_to_float(cur.h.x >> 16);
-        const uint8_t* p = a_row + blk * 256;
-        const uint4 x0 = *(const uint4*)(p), x1 = *(const uint4*)(p + 32);
-        const uint4 x4 = *(const uint4*)(p + 128), x5 = *(const uint4*)(p + 160);
-        const int32_t i0 = dot4(l0[3], x0.w, dot4(l0[2], x0.z, dot4(l0[1], x0.y, dot4(l0[0], x0.x, 0))));
-        const int32_t i1 = dot4(h0[3], x1.w, dot4(h0[2], x1.z, dot4(h0[1], x1.y, dot4(h0[0], x1.x, 0))));
-        const int32_t i4 = dot4(l1[3], x4.w, dot4(l1[2], x4.z, dot4(l1[1], x4.y, dot4(l1[0], x4.x, 0))));
-        const int32_t i5 = dot4(h1[3], x5.w, dot4(h1[2], x5.z, dot4(h1[1], x5.y, dot4(h1[0], x5.x, 0))));
-        // this quarter's sub-blocks 2g, 2g+1, 2g+4, 2g+5: scales and mins
-        // (6-bit) and bsums (|b| <= 16 * 128) fit i16, and so do the Q4_K
-        // sub-block sums (|i| <= 15 * 128 * 16): two dot2 per sum (Q5_K sums
-        // reach 31 * 128 * 16 and take the 24-bit multiplies)
-        const uint2 bw = *(const uint2*)(bs_row + blk * 256);
-        const uint32_t S01 = __builtin_amdgcn_perm(0u, q.scA, psel), S45 = __builtin_amdgcn_perm(0u, q.scB, psel);
-        const uint32_t M01 = __builtin_amdgcn_perm(0u, q.mnA, psel), M45 = __builtin_amdgcn_perm(0u, q.mnB, psel);
-        int32_t I;
-        if constexpr (T == kQ5_K) {
-            I = mad24(S01 & 0xffff, i0, mad24(S01 >> 16, i1, mad24(S45 & 0xffff, i4, __mul24(S45 >> 16, i5))));
-        } else {
-            const uint32_t P01 = __builtin_amdgcn_perm((uint32_t)i1, (uint32_t)i0, 0x05040100u);
-            const uint32_t P45 = __builtin_amdgcn_perm((uint32_t)i5, (uint32_t)i4, 0x05040100u);
-            I = __builtin_amdgcn_sdot2(__builtin_bit_cast(s2, S01), __builtin_bit_cast(s2, P01),
-                                       __builtin_amdgcn_sdot2(__builtin_bit_cast(s2, S45), __builtin_bit_cast(s2, P45),
-                                                              0, false),
-                                       false);
-        }
-        int32_t M = __builtin_amdgcn_sdot2(__builtin_bit_cast(s2, M01), __builtin_bit_cast(s2, bw.x),
-                                           __builtin_amdgcn_sdot2(__builtin_bit_cast(s2, M45),
-                                                                  __builtin_bit_cast(s2, bw.y), 0, false),
-                                           false);
         const float da = *(const float*)(lds + L.d_off + blk * 32);
-        acc += (dw * da) * (float)I - (dmw * da) * (float)M;
-        if (DBG) {  // exact block integers: add the four quarters
-            I += __shfl_xor(I, 16, 64);
-            I += __shfl_xor(I, 32, 64);
-            M += __shfl_xor(M, 16, 64);
-            M += __shfl_xor(M, 32, 64);
+        const uint32_t rec = (ti * TS + ts) * nb + blk;
+        park_terms(park + rec * 64, parkm + rec * 16, lane, n, kq, dw * da, o.I, true, dmw * da, o.M);
+        if (DBG) {  // exact block integers: the eight classes
+            const int32_t I = sum_xor16(o.I[0] + o.I[1] + o.I[2] + o.I[3]);
             const uint32_t row = tile * kTileRows + n;
             if (kq == 0 && row < a.rows && own_row(ti)) {
                 a.dbg_isum[(uint64_t)row * nb + blk] = I;
-                a.dbg_imin[(uint64_t)row * nb + blk] = M;
+                a.dbg_imin[(uint64_t)row * nb + blk] = o.M;
             }
         }
         blk += KS;
-        if (++j == bpt) {  // this wave's share of the tile is done: park the row sums
-            float v = acc;
-            v += __shfl_xor(v, 16, 64);
-            v += __shfl_xor(v, 32, 64);
+        if (++j == bpt) {  // this wave's share of the tile is parked: count it
             const uint32_t slot = ti * TS + ts;
-            if (kq == 0) part[(slot * KS + kp) * 16 + n] = v;
-            // one wave's LDS operations are performed in order: the partial
-            // is in place before the count
+            // one wave's LDS operations are performed in order: the terms are
+            // in place before the count
             if (lane == 0) {
                 const uint32_t prev =
                     __hip_atomic_fetch_add(cnt + slot, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_WORKGROUP);
@@ -1492,7 +1508,6 @@ __global__ __launch_bounds__(W * 64) void q45_mv_b1_kernel(MvArgs a) {
                 // step (no global store or atomic between the weight loads)
                 if (prev == nk - 1) cnt[slot] = nk + 1 + wave;
             }
-            acc = 0.0f;
             j = 0;
             blk = kp;
             tile = tile_of(++ti);
@@ -1500,12 +1515,14 @@ __global__ __launch_bounds__(W * 64) void q45_mv_b1_kernel(MvArgs a) {
     };
     pipeline<D>(steps, buf, issue, compute);
 
-    // the tiles this wave completed: add their K parts in order and store
+    // the tiles this wave completed: each row's sum in the reference's order
     for (uint32_t i = 0; i < my_tiles; ++i) {
         const uint32_t slot = i * TS + ts, row = tile_of(i) * kTileRows + n;
-        // (the mark is wave-uniform)
-        if (cnt[slot] != nk + 1 + wave || kq != 0 || row >= a.rows || !own_row(i)) continue;
-        float s = sum_parts(slot);
+        // (the mark is wave-uniform; the other conditions hold for the four
+        // lanes of a row alike)
+        if (cnt[slot] != nk + 1 + wave || row >= a.rows || !own_row(i)) continue;
+        float s = exact_row_sum(park + slot * nb * 64, parkm + slot * nb * 16, nb, n, kq, true);
+        if (kq != 0) continue;
         if (FULL && a.chk) check_finite(a, kChkOut, s);
         if (FULL && a.resid) {
             s = rs[slot * 16 + n] + s;  // math.rs:203-208: hidden += projected
@@ -1635,6 +1652,120 @@ __global__ __launch_bounds__(W * 64) void q6k_mv_kernel(MvArgs a) {
     pipeline<D>(steps, buf, issue, compute);
     fold_argmax(a, lds, L, kq, best0);
     fold_argmax(a, lds, L, kq + 4, best1);
+    finish_argmax(a, lds, L);
+}
+
+// Q6_K, one column, in the reference's f32 order (matvec_extra.rs:272-293):
+// eight lane accumulators lanes[j % 8] per row over all blocks, then
+// sum = 0 + lanes[0] + ... + lanes[7].  The weight chunks and lane roles are
+// those of q6k_mv_kernel; the A rows split each scale group's dot by lane
+// class.  A row r holds class c = r % 8 of K quarter r / 8 (first MFMA of a
+// pair) or 2 + r / 8 (second): the activation of that quarter's scale group
+// masked to the elements j with j % 8 == c (bytes c and c + 8 of the
+// group's 16).  Output i of the pair in lane (n, kq) is then the exact dot of
+// weight row n over class 4 (kq % 2) + i of scale group
+// {0, 2, 8, 10}[kq / 2] + off (first) or {8, 10}[kq / 2] + off (second), with
+// off = 0, 1, 4, 5 for the four weight operands; the lanes kq and kq ^ 2
+// hold the other eight groups of the same classes.  A wave takes whole tiles
+// and walks their blocks in order, so the accumulators stay in registers.
+template <int W, int D, bool DBG>
+__global__ __launch_bounds__(W * 64) void q6k_mv_one_kernel(MvArgs a) {
+    RLQ_MV_PROLOGUE(kQ6_K, a.nb)
+    const uint32_t nb = a.nb;
+    Q6Step buf[D];
+    auto issue = [&](Q6Step& st) {
+        const uint8_t* base = a.w + ((uint64_t)ld_tile * nb + ld_chunk) * kQ6KChunk;
+        st.l0 = load_stream16(base + lane * 16);
+        st.l1 = load_stream16(base + 1024 + lane * 16);
+        st.h0 = load_stream16(base + 2048 + n * 64 + 32 * (kq >> 1));
+        st.h1 = load_stream16(base + 2048 + n * 64 + 32 * (kq >> 1) + 16);
+        st.sc = load_stream16(base + 3072 + n * 16);
+        st.d = __builtin_nontemporal_load((const uint16_t*)(base + 3328 + n * 2));
+        next_load();
+    };
+#pragma unroll
+    for (int i = 0; i < D; ++i) issue(buf[i]);
+
+    const bool ok = a.x ? stage_q8k<W, kBsNone>(a, lds, L, wave, xv) : stage_planes<W>(a, lds, L, kQ6_K);
+    if (!ok) return finish_argmax(a, lds, L);
+    if (a.zero_pair) return zero_wave_tiles(a, gw, tw, n, kq);
+
+    const uint32_t s1 = kq & 1, lsh = 4 - 2 * s1, rsh = 2 * s1;
+    // this lane's A operand: K quarter kq of A row n, i.e. scale group
+    // {0, 2, 8, 10}[kq] of the operand, masked to class n % 8; live in the
+    // first MFMA of a pair when kq == n / 8, in the second when kq == 2 + n / 8
+    const uint32_t cls = n & 7, qsel = n >> 3;
+    const bool live0 = kq == qsel, live1 = kq == 2 + qsel;
+    const uint8_t* a_ptr = live0 || live1 ? lds + 16 * (8 * (kq >> 1) + 2 * (kq & 1)) : lds + L.zero_off;
+    const uint32_t a_step = live0 || live1 ? 256 : 0;
+    const uint32_t byte = 0xffu << (8 * (cls & 3));
+    uint32_t m0[4], m1[4];  // the masks of the two MFMAs (zero where not live)
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+        const uint32_t mk = (uint32_t)(w & 1) == (cls >> 2) ? byte : 0u;
+        m0[w] = live0 ? mk : 0u;
+        m1[w] = live1 ? mk : 0u;
+    }
+    const uint32_t g2 = 16 * (kq >> 1);  // bit offset of scale bytes 2 (kq / 2), + 1 in each scale word
+
+    float lanes[4] = {0.0f, 0.0f, 0.0f, 0.0f};  // classes 4 (kq % 2) + i
+    unsigned long long best = 0;
+    uint32_t tile = gw, blk = 0;
+    auto compute = [&](const Q6Step& cur) {
+        const i32x4 w00 = {(int)q6_lo(cur.l0.x, cur.h0.x, lsh), (int)q6_lo(cur.l0.y, cur.h0.y, lsh),
+                           (int)q6_lo(cur.l0.z, cur.h0.z, lsh), (int)q6_lo(cur.l0.w, cur.h0.w, lsh)};
+        const i32x4 w01 = {(int)q6_lo(cur.l1.x, cur.h1.x, lsh), (int)q6_lo(cur.l1.y, cur.h1.y, lsh),
+                           (int)q6_lo(cur.l1.z, cur.h1.z, lsh), (int)q6_lo(cur.l1.w, cur.h1.w, lsh)};
+        const i32x4 w10 = {(int)q6_hi(cur.l0.x, cur.h0.x, rsh), (int)q6_hi(cur.l0.y, cur.h0.y, rsh),
+                           (int)q6_hi(cur.l0.z, cur.h0.z, rsh), (int)q6_hi(cur.l0.w, cur.h0.w, rsh)};
+        const i32x4 w11 = {(int)q6_hi(cur.l1.x, cur.h1.x, rsh), (int)q6_hi(cur.l1.y, cur.h1.y, rsh),
+                           (int)q6_hi(cur.l1.z, cur.h1.z, rsh), (int)q6_hi(cur.l1.w, cur.h1.w, rsh)};
+        const uint8_t* p = a_ptr + blk * a_step;
+        int32_t I[4] = {0, 0, 0, 0};
+        // one weight operand: its scale groups' signed scales sa (first MFMA)
+        // and sb (second); |dot| <= 2 * 32 * 128 and |scale| <= 128 fit the
+        // 24-bit multiplies
+        auto pair = [&](const i32x4& wop, uint32_t aoff, int32_t sa, int32_t sb) {
+            const uint4 x = *(const uint4*)(p + aoff);
+            const i32x4 A0 = {(int)(x.x & m0[0]), (int)(x.y & m0[1]), (int)(x.z & m0[2]), (int)(x.w & m0[3])};
+            const i32x4 A1 = {(int)(x.x & m1[0]), (int)(x.y & m1[1]), (int)(x.z & m1[2]), (int)(x.w & m1[3])};
+            const i32x4 d0 = mfma_i8(A0, wop), d1 = mfma_i8(A1, wop);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) I[i] = mad24(sa, d0[i], mad24(sb, d1[i], I[i]));
+        };
+        pair(w00, 0, __builtin_amdgcn_sbfe((int)cur.sc.x, g2, 8), __builtin_amdgcn_sbfe((int)cur.sc.z, g2, 8));
+        pair(w01, 16, __builtin_amdgcn_sbfe((int)cur.sc.x, g2 + 8, 8), __builtin_amdgcn_sbfe((int)cur.sc.z, g2 + 8, 8));
+        pair(w10, 64, __builtin_amdgcn_sbfe((int)cur.sc.y, g2, 8), __builtin_amdgcn_sbfe((int)cur.sc.w, g2, 8));
+        pair(w11, 80, __builtin_amdgcn_sbfe((int)cur.sc.y, g2 + 8, 8), __builtin_amdgcn_sbfe((int)cur.sc.w, g2 + 8, 8));
+        const float d = half_to_float(cur.d) * *(const float*)(lds + L.d_off + blk * 32);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            I[i] = sum_xor32(I[i]);
+            lanes[i] += d * (float)I[i];  // matvec_extra.rs:287-289
+        }
+        if (DBG) {
+            const int32_t It = sum_xor16(I[0] + I[1] + I[2] + I[3]);
+            const uint32_t row = tile * kTileRows + n;
+            if (kq == 0 && row < a.rows) {
+                a.dbg_isum[(uint64_t)row * nb + blk] = It;
+                a.dbg_imin[(uint64_t)row * nb + blk] = 0;
+            }
+        }
+        if (++blk == nb) {  // sum = 0 + lanes[0] + ... + lanes[7] (:290-292)
+            float sum = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) sum += __shfl(lanes[i], (int)n, 64);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) sum += __shfl(lanes[i], (int)(n + 16), 64);
+            if (kq == 0) store_out(a, tile * kTileRows + n, 0, sum, best);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) lanes[i] = 0.0f;
+            blk = 0;
+            tile += tw;
+        }
+    };
+    pipeline<D>(steps, buf, issue, compute);
+    fold_argmax(a, lds, L, kq, best);
     finish_argmax(a, lds, L);
 }
 
@@ -2250,23 +2381,24 @@ static hipError_t launch_one(K kernel, const MvArgs& a, size_t lds, hipStream_t 
 // KS waves, about kSmallWgPerCu workgroups per CU.
 constexpr int kSmallW = 8, kSmallKS = 8, kSmallD = 2, kSmallWgPerCu = 2;
 
-// K-split kernels with parked partials: the grid and the LDS of
-// [tmax][TS][KS][16][batch] partials.  lds_set is the kernel's own record of
-// the dynamic LDS limit it has been given.
+// The one-column small kernel: the grid and the LDS of its parked terms
+// [tmax][TS][nb].  lds_set is the kernel's own record of the dynamic LDS
+// limit it has been given.
 template <int W, int KS>
 static hipError_t launch_parked(void (*kernel)(MvArgs), size_t& lds_set, const MvArgs& a, hipStream_t s,
                                 uint32_t pairs) {
     constexpr int TS = W / KS;
+    if (a.batch != 1) return hipErrorInvalidValue;
     const uint32_t want = (a.ntiles + TS - 1) / TS;
     const uint32_t gy = grid_rows(a, pairs);
     uint32_t grid = grid_cols(want, (uint32_t)kSmallWgPerCu * (uint32_t)device_cus(), gy);
-    // enough workgroups that every one parks at most `room` tiles' partials
-    const size_t off = small_part_off(a.cols, a.batch), per_tile = (size_t)TS * KS * 16u * a.batch * 4u;
+    // enough workgroups that every one parks at most `room` tiles' terms
+    const size_t off = small_part_off(a.cols, 1), per_tile = (size_t)TS * park_bytes(a.nb);
     if (off >= kMaxLds || (kMaxLds - off) / per_tile == 0) return hipErrorInvalidValue;
     const uint64_t room = (kMaxLds - off) / per_tile, need = (a.ntiles + room * TS - 1) / (room * TS);
     if (grid < need) grid = (uint32_t)need;
     const uint32_t tstride = grid * TS, tmax = (a.ntiles + tstride - 1) / tstride;
-    const size_t lds = small_lds_bytes(a.cols, a.batch, tmax, TS, KS);
+    const size_t lds = small_lds_bytes(a.cols, tmax, TS);
     if (lds > kMaxLds || (a.am_out && grid > kArgmaxMaxGrid)) return hipErrorInvalidValue;
     if (lds > lds_set) {
         const hipError_t e = hipFuncSetAttribute((const void*)kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -2278,10 +2410,10 @@ static hipError_t launch_parked(void (*kernel)(MvArgs), size_t& lds_set, const M
     return hipGetLastError();
 }
 
-template <uint32_t T, int W, int KS, int D, int B, bool DBG>
+template <uint32_t T, int W, int KS, int D, bool DBG>
 static hipError_t launch_small(const MvArgs& a, hipStream_t s, uint32_t pairs) {
     static size_t lds_set = 64 * 1024;
-    return launch_parked<W, KS>(q4k_mv_small_kernel<T, W, KS, D, B, DBG>, lds_set, a, s, pairs);
+    return launch_parked<W, KS>(q4k_mv_small_kernel<T, W, KS, D, DBG>, lds_set, a, s, pairs);
 }
 
 // The batch-1 kernel: grid as launch_parked (enough workgroups that the
@@ -2290,7 +2422,7 @@ template <int W, int KS>
 static void b1_grid(const MvArgs& a, uint32_t& grid, uint32_t& tmax) {
     constexpr int TS = W / KS;
     grid = grid_cols((a.ntiles + TS - 1) / TS, (uint32_t)kSmallWgPerCu * (uint32_t)device_cus(), 1);
-    const size_t off = small_part_off(a.cols, 1), per_tile = (size_t)TS * KS * 16u * 4u + TS * 4u + TS * 64u;
+    const size_t off = small_part_off(a.cols, 1), per_tile = (size_t)TS * (park_bytes(a.nb) + 4u + 64u);
     const uint64_t room = off < kMaxLds ? (kMaxLds - off) / per_tile : 0;
     if (room == 0) {
         grid = tmax = 0;
@@ -2334,7 +2466,7 @@ static bool b1_bal_takes(const MvArgs& a) {
     if ((TS != 2 && TS != 4) || a.nb > 4u * KS || a.epilogue != kEpStore) return false;
     uint32_t grid, tmax;
     b1_bal_grid<TS>(a, grid, tmax);
-    return grid > 0 && b1_lds_bytes(a.cols, tmax, TS, KS) <= kMaxLds;
+    return grid > 0 && b1_lds_bytes(a.cols, tmax, TS) <= kMaxLds;
 }
 
 template <uint32_t T, int W, int KS, int D, bool DBG, bool FULL, bool BAL = false>
@@ -2345,7 +2477,7 @@ static hipError_t launch_b1(const MvArgs& a, hipStream_t s) {
     uint32_t grid, tmax;
     if constexpr (BAL) b1_bal_grid<TS>(a, grid, tmax);
     else b1_grid<W, KS>(a, grid, tmax);
-    const size_t lds = b1_lds_bytes(a.cols, tmax, TS, KS);
+    const size_t lds = b1_lds_bytes(a.cols, tmax, TS);
     if (grid == 0 || lds > kMaxLds || (a.am_out && grid > kArgmaxMaxGrid) || (a.resid && tmax > 4))
         return hipErrorInvalidValue;
     if (lds > lds_set) {
@@ -2495,21 +2627,21 @@ static hipError_t launch_q45(const MvArgs& a, uint32_t nbat, bool dbg, uint32_t 
     // (each variant has a DBG twin that also stores the block integers, so
     // rlq_block_sums checks the very kernel rlq_matmul runs)
     if (epilogue == kEpSiluPair)
-        return dbg ? launch_small<T, kSmallW, kSmallW / 4, kSmallD, 1, true>(a, s, pairs)
-                   : launch_small<T, kSmallW, kSmallW / 4, kSmallD, 1, false>(a, s, pairs);
+        return dbg ? launch_small<T, kSmallW, kSmallW / 4, kSmallD, true>(a, s, pairs)
+                   : launch_small<T, kSmallW, kSmallW / 4, kSmallD, false>(a, s, pairs);
     // two tile slots per workgroup (a K split of four): small matrices of at
     // most 4096 columns and 512 tiles (measured: 6144x4096 runs 1 us faster)
     if (nbat == 1 && a.nb <= 16 && a.ntiles <= 512)
-        return dbg ? launch_small<T, kSmallW, kSmallW / 2, kSmallD, 1, true>(a, s, pairs)
-                   : launch_small<T, kSmallW, kSmallW / 2, kSmallD, 1, false>(a, s, pairs);
+        return dbg ? launch_small<T, kSmallW, kSmallW / 2, kSmallD, true>(a, s, pairs)
+                   : launch_small<T, kSmallW, kSmallW / 2, kSmallD, false>(a, s, pairs);
     // more than 16 blocks per row (4096x14336, the down projection): 16 waves
     // per workgroup, K split 16 ways (measured 10.4 us vs 10.7 us with 8)
     if (nbat == 1 && a.nb > 16)
-        return dbg ? launch_small<T, 2 * kSmallW, 2 * kSmallKS, kSmallD, 1, true>(a, s, pairs)
-                   : launch_small<T, 2 * kSmallW, 2 * kSmallKS, kSmallD, 1, false>(a, s, pairs);
+        return dbg ? launch_small<T, 2 * kSmallW, 2 * kSmallKS, kSmallD, true>(a, s, pairs)
+                   : launch_small<T, 2 * kSmallW, 2 * kSmallKS, kSmallD, false>(a, s, pairs);
     if (nbat == 1)
-        return dbg ? launch_small<T, kSmallW, kSmallKS, kSmallD, 1, true>(a, s, pairs)
-                   : launch_small<T, kSmallW, kSmallKS, kSmallD, 1, false>(a, s, pairs);
+        return dbg ? launch_small<T, kSmallW, kSmallKS, kSmallD, true>(a, s, pairs)
+                   : launch_small<T, kSmallW, kSmallKS, kSmallD, false>(a, s, pairs);
     // two to eight columns: the K-split MFMA kernel (14336x4096 batch 2:
     // 11.1 us against 11.5 us for the VALU kernel with two columns).  One
     // matrix takes the balanced deal, one workgroup per CU: four tile slots
@@ -2682,7 +2814,11 @@ hipError_t launch_matvec_ex(uint32_t wtype, const uint8_t* w, uint64_t rows, uin
                 case kQ6_K:
                     // one workgroup of 8 waves per CU, three chunks in flight per
                     // wave (128256x4096 + argmax, batch 8: 78.5 us against 79.6
-                    // with four and 80.3 with five; batch 1 71.1 with three or four)
+                    // with four and 80.3 with five; batch 1 71.1 with three or four);
+                    // one column in the reference's f32 order
+                    if (nbat == 1)
+                        return dbg ? launch_one<2 * W>(q6k_mv_one_kernel<2 * W, 3, true>, a, lds, s, pairs, 1)
+                                   : launch_one<2 * W>(q6k_mv_one_kernel<2 * W, 3, false>, a, lds, s, pairs, 1);
                     return dbg ? launch_one<2 * W>(q6k_mv_kernel<2 * W, 3, true>, a, lds, s, pairs, 1)
                                : launch_one<2 * W>(q6k_mv_kernel<2 * W, 3, false>, a, lds, s, pairs, 1);
                 default:

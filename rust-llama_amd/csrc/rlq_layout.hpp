@@ -9,9 +9,14 @@
 // works on row n = l % 16 and K quarter kq = l / 16 of the chunk.
 //
 // Q4_K, chunk of 2304 B per (tile, block):
-//   [P*1024 + l*16, +16)  qs bytes 32g + 16h .. +15 of row n, where P = 0, 1,
-//                         g = 2P + kq/2, h = kq%2 (low nibbles: sub-block 2g,
-//                         high nibbles: sub-block 2g+1, positions 16h..16h+15)
+//   [P*1024 + l*16, +16)  qs bytes 32g + q45_pos_of_slot(16h + s), s = 0..15, of
+//                         row n, where P = 0, 1, g = 2P + kq/2, h = kq%2 (low
+//                         nibbles: sub-block 2g, high nibbles: sub-block
+//                         2g+1).  Slot 16h + 4k + i holds position
+//                         4h + k + 8i of the sub-block, so each 4-byte word
+//                         of a lane holds the four values of one lane class
+//                         j % 8 = 4h + k (the reference's eight accumulators,
+//                         matvec_extra.rs:223-294)
 //   [2048 + n*16, +16)    d, dmin, scales[12] of row n (GGUF bytes 0..15)
 // Q6_K, chunk of 3360 B per (tile, block):
 //   [h*1024 + l*16, +16)  ql bytes 32kq + 16h .. +15 of row n
@@ -19,9 +24,10 @@
 //   [3072 + n*16, +16)    scales[16] of row n
 //   [3328 + n*2, +2)      d of row n
 // Q5_K, chunk of 2816 B per (tile, block): the Q4_K pieces plus qh
-//   [P*1024 + l*16, +16)  qs bytes 32g + 16h .. +15 of row n (GGUF bytes 48..)
-//                         with the Q4_K mapping of P, g, h
-//   [2048 + n*32, +32)    qh[32] of row n (GGUF bytes 16..47)
+//   [P*1024 + l*16, +16)  qs bytes of row n (GGUF bytes 48..) with the Q4_K
+//                         mapping of P, g, h and slots
+//   [2048 + n*32, +32)    qh[32] of row n (GGUF bytes 16..47), byte p at slot
+//                         q45_slot_of_pos(p)
 //   [2560 + n*16, +16)    d, dmin, scales[12] of row n (GGUF bytes 0..15)
 // Q3_K, chunk of 1760 B per (tile, block):
 //   [l*16, +16)           qs bytes 16kq .. +15 of row n (GGUF bytes 32..95)
@@ -53,6 +59,15 @@ constexpr uint32_t kQ2KChunk = 1344;
 
 __host__ __device__ inline uint64_t layout_tiles(uint64_t rows) { return (rows + kTileRows - 1) / kTileRows; }
 
+// Q4_K / Q5_K slot order within a 32-value sub-block: slot 16h + 4k + i
+// holds position 4h + k + 8i (h, k, i = the lane half, the word, the byte).
+__host__ __device__ constexpr uint32_t q45_pos_of_slot(uint32_t w) {
+    return 4 * (w >> 4) + ((w >> 2) & 3u) + 8 * (w & 3u);
+}
+__host__ __device__ constexpr uint32_t q45_slot_of_pos(uint32_t p) {
+    return 16 * ((p >> 2) & 1u) + 4 * (p & 3u) + (p >> 3);
+}
+
 // Chunks per tile (blocks, or block pairs for Q8_0) and chunk size.
 __host__ __device__ inline uint64_t layout_chunks_per_tile(uint32_t t, uint64_t cols) {
     return t == 8 ? (cols / 32 + 1) / 2 : cols / 256;
@@ -80,15 +95,15 @@ __host__ __device__ inline uint64_t layout_offset(uint32_t t, uint64_t row, uint
     if (t == 12) {
         const uint64_t base = (tile * nb + blk) * kQ4KChunk;
         if (byte < 16) return base + 2048 + n * 16 + byte;
-        const uint32_t q = byte - 16, g = q / 32, j = q % 32, h = j / 16, i = j % 16;
+        const uint32_t q = byte - 16, g = q / 32, w = q45_slot_of_pos(q % 32), h = w / 16, i = w % 16;
         const uint32_t P = g / 2, kq = 2 * (g % 2) + h;
         return base + P * 1024 + (16 * kq + n) * 16 + i;
     }
     if (t == 13) {
         const uint64_t base = (tile * nb + blk) * kQ5KChunk;
         if (byte < 16) return base + 2560 + n * 16 + byte;
-        if (byte < 48) return base + 2048 + n * 32 + (byte - 16);
-        const uint32_t q = byte - 48, g = q / 32, j = q % 32, h = j / 16, i = j % 16;
+        if (byte < 48) return base + 2048 + n * 32 + q45_slot_of_pos(byte - 16);
+        const uint32_t q = byte - 48, g = q / 32, w = q45_slot_of_pos(q % 32), h = w / 16, i = w % 16;
         const uint32_t P = g / 2, kq = 2 * (g % 2) + h;
         return base + P * 1024 + (16 * kq + n) * 16 + i;
     }

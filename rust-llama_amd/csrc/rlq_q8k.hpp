@@ -117,4 +117,26 @@ __device__ __forceinline__ Q8KRow q8k_row16(const float (&v)[16], uint32_t r16) 
     return o;
 }
 
+// The Q4_K / Q5_K slot order of an activation image (rlq_layout.hpp,
+// q45_pos_of_slot): the two lanes of a quad pair hold the 16 values of one
+// sub-block half each (lane bit 0 = half h'), q their natural bytes.  Slot
+// word k' (k' = 0..7) of the sub-block is (u0[k'], u0[k'+8], u1[k'], u1[k'+8])
+// with u0, u1 the two halves; the lane of half h' returns words 4h'..4h'+3,
+// i.e. slots 16h'..16h'+15, which it stores where its natural bytes would
+// go.  Both lanes of the pair must be active.
+__device__ __forceinline__ uint4 q45_slots(const uint32_t (&q)[4], uint32_t odd) {
+    // (u[k'], u[k'+8]) pairs of this half, two per word
+    const uint32_t Q0 = __builtin_amdgcn_perm(q[2], q[0], 0x05010400u);
+    const uint32_t Q1 = __builtin_amdgcn_perm(q[2], q[0], 0x07030602u);
+    const uint32_t Q2 = __builtin_amdgcn_perm(q[3], q[1], 0x05010400u);
+    const uint32_t Q3 = __builtin_amdgcn_perm(q[3], q[1], 0x07030602u);
+    // the even lane sends its pairs 4..7, the odd lane its pairs 0..3
+    const uint32_t R0 = (uint32_t)dpp_i<kQuadXor1>((int32_t)(odd ? Q0 : Q2));
+    const uint32_t R1 = (uint32_t)dpp_i<kQuadXor1>((int32_t)(odd ? Q1 : Q3));
+    const uint32_t lo0 = odd ? R0 : Q0, hi0 = odd ? Q2 : R0;
+    const uint32_t lo1 = odd ? R1 : Q1, hi1 = odd ? Q3 : R1;
+    return make_uint4(__builtin_amdgcn_perm(hi0, lo0, 0x05040100u), __builtin_amdgcn_perm(hi0, lo0, 0x07060302u),
+                      __builtin_amdgcn_perm(hi1, lo1, 0x05040100u), __builtin_amdgcn_perm(hi1, lo1, 0x07060302u));
+}
+
 }  // namespace rlq

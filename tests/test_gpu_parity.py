@@ -7,7 +7,10 @@ Bars:
   - per-block integer dot sums are compared bit-exactly (rlq_block_sums);
   - f32 outputs: relative L2 error <= 1e-5 against the oracle / golden C
     output, plus a per-element bound of 2e-5 * (1 + |e|) where the reference's
-    own tests use that bound (matvec.rs:55).
+    own tests use that bound (matvec.rs:55);
+  - f32 outputs bit-exact where the kernels follow the reference's f32 order:
+    Q8_0 at every batch size, Q4_K / Q5_K / Q6_K with one column (the
+    reference's eight lane accumulators, matvec_extra.rs:223-294).
 Every test prints its case before touching the GPU.
 """
 import numpy as np
@@ -28,6 +31,15 @@ REL_L2 = 1e-5
 
 def say(*a):
     print("[case]", *a, flush=True)
+
+
+def bits(y):
+    return np.asarray(y, np.float32).view(np.uint32)
+
+
+def exact(t, batch):
+    """Whether a launch of `batch` columns gives the reference's f32 bits."""
+    return t == DT.Q8_0 or (batch == 1 and t in (DT.Q4_K, DT.Q5_K, DT.Q6_K))
 
 
 def rel_l2(got, want):
@@ -89,10 +101,14 @@ def test_matvec_golden_q4k_q6k():
         assert rel_l2(y, r.generic) <= REL_L2, i
         tol = elem_tol(r.dtype, r.weights, r.rows, r.activation, r.cols, r.generic)
         assert np.all(np.abs(y - r.generic) <= tol), (i, np.abs(y - r.generic) - tol)
+        if exact(r.dtype, 1):
+            assert np.array_equal(bits(y), bits(r.generic)), i
         stride = r.weights.size // r.rows
         for row in range(r.rows):
             d = rlq.dot_packed(r.dtype, r.weights[row * stride:(row + 1) * stride], r.activation, r.cols)
             assert abs(d - r.generic[row]) <= tol[row], (i, row)
+            if exact(r.dtype, 1):
+                assert bits(d) == bits(r.generic[row]), (i, row)
 
 
 def test_matvec_golden_q8_0():
@@ -196,7 +212,9 @@ def test_block_sums_every_decode_variant(ctx, t, rows, cols, variant):
     want_i, want_m = _oracle_sums(t, w, rows, O.quantize(O.Q8_K, x), nb)
     assert np.array_equal(isum.cpu().numpy(), want_i)
     assert np.array_equal(imin.cpu().numpy(), want_m)
-    assert rel_l2(y.cpu().numpy(), O.matvec(int(t), w, rows, cols, x, threads=16)) <= REL_L2
+    want = O.matvec(int(t), w, rows, cols, x, threads=16)
+    assert rel_l2(y.cpu().numpy(), want) <= REL_L2
+    assert np.array_equal(bits(y.cpu().numpy()), bits(want))
 
 
 @pytest.mark.parametrize("t,rows,cols,batch", [
@@ -257,6 +275,7 @@ def test_silu_pair_kernel_integers_and_outputs(ctx, t, ff, cols):
     assert np.array_equal(imin.cpu().numpy(), wm)
     want = O.silu(O.matvec(int(t), g, ff, cols, x, threads=16)) * O.matvec(int(t), u, ff, cols, x, threads=16)
     assert rel_l2(y.cpu().numpy(), want) <= REL_L2
+    assert np.array_equal(bits(y.cpu().numpy()), bits(want))
 
 
 def test_block_sums_golden_records(ctx):
@@ -288,8 +307,8 @@ def test_matmul_batches_against_oracle(ctx, t, rows, cols, batch):
     got = y.cpu().numpy()
     for b in range(batch):
         assert rel_l2(got[b], want[b]) <= REL_L2, b
-    if t == DT.Q8_0:  # block terms added in the reference's order: bit-exact
-        assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    if exact(t, batch):  # the reference's f32 order: bit-exact
+        assert np.array_equal(bits(got), bits(want))
 
 
 # ------------------------------------------------------------ the benchmark shapes
@@ -310,6 +329,8 @@ def test_q4k_14336x4096_encoder_and_matvec(ctx):
         want = O.matmul(O.Q4_K, w, rows, cols, x, threads=16)
         for b in range(batch):
             assert rel_l2(y[b].cpu().numpy(), want[b]) <= REL_L2, (batch, b)
+        if exact(DT.Q4_K, batch):
+            assert np.array_equal(bits(y.cpu().numpy()), bits(want)), batch
 
 
 def test_q6k_lm_head_128256x4096_argmax(ctx):
@@ -335,6 +356,9 @@ def test_q6k_lm_head_128256x4096_argmax(ctx):
             i = int(am[b])
             assert i == O.argmax(got[b]), b  # fused argmax == greedy choice on the same logits
             assert want[b][i] >= want[b].max() - 1e-5 * abs(want[b].max()), b
+        if exact(DT.Q6_K, batch):
+            assert np.array_equal(bits(got), bits(want)), batch
+            assert int(am[0]) == O.argmax(want[0])
 
 
 def test_q8_0_qwen_lm_head_151936x896(ctx):

@@ -7,7 +7,9 @@ beyond 64 blocks), and batches 1..8 (one pass of the decode kernels) and 9 or
 
 Bars, as in test_gpu_parity: column 0's per-block integers bitwise (every
 batch for Q4_K, up to 8 columns otherwise), every column's f32 outputs within
-relative L2 1e-5 of the oracle.  Weights: the library's encoder on N(0, 0.02)
+relative L2 1e-5 of the oracle, and bitwise where the kernels keep the
+reference's f32 order (Q8_0 and Q2_K at every batch, Q4_K, Q5_K and Q6_K with
+one column).  Weights: the library's encoder on N(0, 0.02)
 values for Q4_K, Q6_K and Q8_0; random GGUF blocks (random quants and scales,
 finite positive f16 super-scales) for Q2_K, Q3_K and Q5_K, as in
 test_gpu_kformats.  Every case prints itself before touching the GPU.
@@ -24,6 +26,8 @@ DT = rlq.DType
 
 REL_L2 = 1e-5
 DECODE_MAX_BATCH = 8
+EXACT_ALWAYS = (DT.Q8_0, DT.Q2_K)
+EXACT_ONE_COLUMN = (DT.Q4_K, DT.Q5_K, DT.Q6_K)
 # byte offsets of the f16 super-block scales of the random-block formats
 HALVES = {DT.Q2_K: (80, 82), DT.Q3_K: (108,), DT.Q5_K: (0, 2)}
 
@@ -122,6 +126,8 @@ def test_sweep(t, rows, cols, batch):
         want = O.matmul(int(t), w, rows, cols, x, threads=16)
         for b in range(batch):
             assert rel_l2(got[b], want[b]) <= REL_L2, b
+        if t in EXACT_ALWAYS or (batch == 1 and t in EXACT_ONE_COLUMN):  # the reference's f32 order
+            assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
         W.close()
     finally:
         ctx.close()
