@@ -52,18 +52,28 @@ __host__ __device__ inline uint64_t v_cache_index(uint32_t kvh, uint32_t hd, uin
 // P.V waves per head: the waves of a workgroup split G heads' columns.
 __host__ __device__ inline uint32_t pv_waves_per_head(uint32_t G) { return G < kPvWaves ? kPvWaves / G : 1u; }
 
-// LDS of attn_pv_kernel, in floats: max and inverse [G][2], then the f64
-// partial row sums [G][waves per head] and P.V partials [G][waves per head][4].
+// LDS of attn_pv_kernel, in floats: max and inverse [G][2], the f64 partial
+// row sums [G][waves per head], the P.V records [G][waves per head][4]
+// (PvRec), and one 256-term f64 buffer per wave for the sequential repeats.
 // It does not grow with the context: the scores and values stream from HBM.
+struct PvRec {
+    double sum;     // the wave's tree sum of its lanes' segment sums
+    float wsum;     // sum over its lanes r of (lanes per head - 1 - r) |segment sum|
+    float abs_sum;  // sum |term|
+    float min_abs;  // smallest nonzero |term| (infinity: none)
+    float pad;
+};
+constexpr uint32_t kPvRepTerms = 256;
 struct AttnPvLds {
-    uint32_t rsum, part, total;
+    uint32_t rsum, part, rep, total;
 };
 __host__ __device__ inline AttnPvLds attn_pv_lds(uint32_t G) {
     AttnPvLds l;
     const uint32_t wph = pv_waves_per_head(G);
     l.rsum = (2 * G + 1) & ~1u;
     l.part = l.rsum + 2 * G * wph;
-    l.total = l.part + 2 * 4 * G * wph;
+    l.rep = l.part + (uint32_t)(sizeof(PvRec) / 4) * 4 * G * wph;
+    l.total = l.rep + 2 * kPvRepTerms * kPvWaves;
     return l;
 }
 __host__ __device__ inline uint32_t attn_scores_lds(uint32_t G, uint32_t hd) {
@@ -211,26 +221,59 @@ __global__ __launch_bounds__(kAttnThreads) void attn_scores_kernel(
 }
 
 // Softmax of the G heads' score rows (math.rs:293-318 with the SSE2 policy of
-// cpu_math.rs:60-91) and P.V (math.rs:475-482) for 4 of the head dimensions:
+// cpu_math.rs:60-91) and P.V (math.rs:475-488) for 4 of the head dimensions:
 // workgroup (blockIdx.x, blockIdx.y) = (dimensions 4 * blockIdx.x .., kv head).
 // Every workgroup of the kv head computes the G rows' softmax from the chunk
 // maxima.  The columns go in groups of four (the reference's SSE2 vectors);
-// lane r of part w of a head's wph waves takes groups 64 w + r, + 64 wph, ...
-// Its first kPvRegGroups groups' values are loaded when the kernel starts and
-// their exponentials kept from the row sums; later groups are reloaded and
-// their exponentials recomputed (the same f32 function of the same inputs),
-// so the LDS does not grow with the context.  The softmax totals are
-// certified against the reference's order (certified_f32).  The P.V sums add
-// the reference's f64 terms in another order (per lane, then the 64 lanes in
-// a fixed tree, then the head's waves in order): their f32 results can differ
-// from the reference's in the last bit (the certificate fails for about 2 in
-// 10^4 of these 1024-term sums, and a sequential repeat would cost the whole
-// kernel several microseconds).  Columns past `count` have exponential 0.
+// the 64 wph lanes of a head's wph waves take contiguous runs of GL groups in
+// column order (lane r of part w: groups (64 w + r) GL ..).  Its first
+// kPvRegGroups groups' values are loaded when the kernel starts and their
+// exponentials kept from the row sums; later groups are reloaded and their
+// exponentials recomputed (the same f32 function of the same inputs), so the
+// LDS does not grow with the context.  The softmax totals are certified
+// against the reference's order (certified_f32).  Each P.V sum adds the
+// reference's f64 terms f64(p * v) column by column within a lane (the
+// reference's order inside the run) and the lanes' run sums in a fixed tree;
+// its f32 result is certified (pv_certified) or the sum is repeated in the
+// reference's column order.  Columns past `count` have exponential 0 and are
+// not added.
 __device__ __forceinline__ void exp_group(float4 x, uint32_t t, uint32_t count, float m, float (&e)[4]) {
     e[0] = t < count ? sse2_exp(x.x - m) : 0.0f;
     e[1] = t + 1 < count ? sse2_exp(x.y - m) : 0.0f;
     e[2] = t + 2 < count ? sse2_exp(x.z - m) : 0.0f;
     e[3] = t + 3 < count ? sse2_exp(x.w - m) : 0.0f;
+}
+
+// Whether the f32 rounding of a P.V sum added in the kernel's order (sum,
+// from terms with sum |term| = A, smallest nonzero |term| = M, over lanes of
+// runs of at most L columns whose run sums weigh wsum as in PvRec) is the
+// f32 rounding of the reference's sequential sum (math.rs:482-488):
+//  - exactly: every term is an f32 value, a multiple of q = 2^(e(M) - 23);
+//    if A < 2^53 q, every partial sum in any order is a multiple of q below
+//    2^53 q, so every f64 addition is exact and all orders give the exact sum;
+//  - else by an interval: the reference's k-th partial sum rounds by at most
+//    2^-53 of itself, and its prefix P_k lies within |E_r| + A_r of zero (E_r
+//    the sum of the runs before run r, |E_r| <= sum of |runs| before it, A_r
+//    the run's sum |term|), so its sum is within 2^-53 (L sum_r |E_r| + L A)
+//    of the exact one; the kernel's within 2^-53 (L A + 16 A) (the runs
+//    and a tree of at most 13 levels).  When both ends of that interval round
+//    to one f32, so does the reference's sum.
+__device__ __forceinline__ bool pv_certified(double sum, double A, double wsum, float M, double L) {
+    if (!(M < INFINITY)) return true;  // no nonzero term: the sum is +0 in any order
+    int e;
+    frexpf(M, &e);  // M = f 2^e, f in [0.5, 1): q = 2^(e - 1 - 23)
+    if (A * (1.0 + 1e-3) < ldexp(1.0, e - 1 - 23 + 53)) return true;
+    const double B = 1.1102230246251565e-16 * 1.02 * (L * wsum * 1.001 + 2.0 * L * A * 1.001 + 16.0 * A * 1.001);
+    return (float)(sum - B) == (float)(sum + B);
+}
+
+__device__ __forceinline__ float wave_min_dpp(float v) {
+    v = fminf(v, dpp_f<kQuadXor1>(v));
+    v = fminf(v, dpp_f<kQuadXor2>(v));
+    v = fminf(v, dpp_f<kRowHalfMirror>(v));
+    v = fminf(v, dpp_f<kRowRor8>(v));
+    v = fminf(v, __shfl_xor(v, 16, 64));
+    return fminf(v, __shfl_xor(v, 32, 64));
 }
 
 __global__ __launch_bounds__(kPvThreads) void attn_pv_kernel(
@@ -241,14 +284,18 @@ __global__ __launch_bounds__(kPvThreads) void attn_pv_kernel(
     extern __shared__ __align__(16) float sm[];
     const uint32_t G = heads / kv_heads, kvh = blockIdx.y, d0 = blockIdx.x * kPvDims;
     const AttnPvLds Lp = attn_pv_lds(G);
-    float* stat = sm;                          // [G][2]: max, inverse
-    double* rsum = (double*)(sm + Lp.rsum);    // [G][wph]
-    double* part = (double*)(sm + Lp.part);    // [G][wph][4]
+    float* stat = sm;                        // [G][2]: max, inverse
+    double* rsum = (double*)(sm + Lp.rsum);  // [G][wph]
+    PvRec* rec = (PvRec*)(sm + Lp.part);     // [G][wph][4]
+    double* rep = (double*)(sm + Lp.rep);    // [kPvWaves][kPvRepTerms]
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t ngroups = (count + 3) / 4;
     const uint32_t wph = pv_waves_per_head(G), hstep = kPvWaves / wph;
     const bool active = wave < hstep * wph;  // wave-uniform
-    const uint32_t w = wave % wph, h0 = wave / wph, gstride = 64 * wph, g0 = 64 * w + lane;
+    const uint32_t w = wave % wph, h0 = wave / wph;
+    // this lane's run of groups [gb, ge) in column order
+    const uint32_t LP = 64 * wph, li = 64 * w + lane, GL = (ngroups + LP - 1) / LP;
+    const uint32_t gb = li * GL < ngroups ? li * GL : ngroups, ge = gb + GL < ngroups ? gb + GL : ngroups;
     const float4* vsrc = (const float4*)(vc + v_cache_index(kvh, hd, d0, 0, max_context));
     // the values of this lane's first groups (shared by every head of the kv
     // head) and the first head's scores of those groups, loaded before the
@@ -256,13 +303,13 @@ __global__ __launch_bounds__(kPvThreads) void attn_pv_kernel(
     float4 vr[kPvRegGroups][4], sr[kPvRegGroups];
 #pragma unroll
     for (uint32_t k = 0; k < kPvRegGroups; ++k) {
-        const uint32_t g = g0 + k * gstride;
-        sr[k] = active && h0 < G && g < ngroups ? *(const float4*)(scores + (uint64_t)(kvh * G + h0) * row_stride + 4 * g)
-                                                : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        const uint32_t g = gb + k;
+        sr[k] = active && h0 < G && g < ge ? *(const float4*)(scores + (uint64_t)(kvh * G + h0) * row_stride + 4 * g)
+                                           : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 #pragma unroll
         for (uint32_t j = 0; j < 4; ++j) {
             const uint32_t t = 4 * g + j;
-            vr[k][j] = active && t < count ? vsrc[t] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            vr[k][j] = active && g < ge && t < count ? vsrc[t] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         }
     }
     // the row maxima: one wave per head over its chunk maxima
@@ -284,16 +331,16 @@ __global__ __launch_bounds__(kPvThreads) void attn_pv_kernel(
             double sum = 0.0;
 #pragma unroll
             for (uint32_t k = 0; k < kPvRegGroups; ++k) {
-                const uint32_t g = g0 + k * gstride;
+                const uint32_t g = gb + k;
                 float e[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-                if (g < ngroups) exp_group(h == h0 ? sr[k] : *(const float4*)(srow + 4 * g), 4 * g, count, m, e);
+                if (g < ge) exp_group(h == h0 ? sr[k] : *(const float4*)(srow + 4 * g), 4 * g, count, m, e);
                 if (h == h0) {
 #pragma unroll
                     for (uint32_t j = 0; j < 4; ++j) er[k][j] = e[j];
                 }
                 sum += (double)((e[0] + e[1]) + (e[2] + e[3]));
             }
-            for (uint32_t g = g0 + kPvRegGroups * gstride; g < ngroups; g += gstride) {
+            for (uint32_t g = gb + kPvRegGroups; g < ge; ++g) {
                 float e[4];
                 exp_group(*(const float4*)(srow + 4 * g), 4 * g, count, m, e);
                 sum += (double)((e[0] + e[1]) + (e[2] + e[3]));
@@ -330,60 +377,107 @@ __global__ __launch_bounds__(kPvThreads) void attn_pv_kernel(
     }
     __syncthreads();
     // P.V with p = e * inverse (math.rs:313-315, 478-480), one f64 chain per
-    // dimension.  The f32 products and f64 terms are the reference's; only
-    // the order of the f64 additions differs (see above).
+    // dimension over the lane's run in column order, and the certificate's
+    // statistics of the terms
     if (active) {
         for (uint32_t h = h0; h < G; h += hstep) {
             const float m = stat[2 * h], inv = stat[2 * h + 1];
             const float* srow = scores + (uint64_t)(kvh * G + h) * row_stride;
-            double a0 = 0.0, a1 = 0.0, a2 = 0.0, a3 = 0.0;
-            auto add = [&](const float (&e)[4], const float4 (&v)[4]) {
+            double a[4] = {0.0, 0.0, 0.0, 0.0};
+            float as[4] = {0.0f, 0.0f, 0.0f, 0.0f}, mn[4] = {INFINITY, INFINITY, INFINITY, INFINITY};
+            auto add = [&](const float (&e)[4], const float4 (&v)[4], uint32_t t0) {
 #pragma unroll
                 for (uint32_t j = 0; j < 4; ++j) {
+                    if (t0 + j >= count) break;  // the reference adds the `count` columns only
                     const float p = e[j] * inv;
-                    a0 += (double)(p * v[j].x), a1 += (double)(p * v[j].y);
-                    a2 += (double)(p * v[j].z), a3 += (double)(p * v[j].w);
+                    const float t[4] = {p * v[j].x, p * v[j].y, p * v[j].z, p * v[j].w};
+#pragma unroll
+                    for (uint32_t d = 0; d < 4; ++d) {
+                        a[d] += (double)t[d];
+                        as[d] += fabsf(t[d]);
+                        mn[d] = t[d] != 0.0f ? fminf(mn[d], fabsf(t[d])) : mn[d];
+                    }
                 }
             };
 #pragma unroll
             for (uint32_t k = 0; k < kPvRegGroups; ++k) {
-                const uint32_t g = g0 + k * gstride;
-                float e[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+                const uint32_t g = gb + k;
+                if (g >= ge) break;
+                float e[4];
                 if (h == h0) {
 #pragma unroll
                     for (uint32_t j = 0; j < 4; ++j) e[j] = er[k][j];
-                } else if (g < ngroups) {
+                } else {
                     exp_group(*(const float4*)(srow + 4 * g), 4 * g, count, m, e);
                 }
-                add(e, vr[k]);
+                add(e, vr[k], 4 * g);
             }
-            for (uint32_t g = g0 + kPvRegGroups * gstride; g < ngroups; g += gstride) {
+            for (uint32_t g = gb + kPvRegGroups; g < ge; ++g) {
                 float e[4];
                 exp_group(*(const float4*)(srow + 4 * g), 4 * g, count, m, e);
                 float4 v[4];
 #pragma unroll
                 for (uint32_t j = 0; j < 4; ++j)
                     v[j] = 4 * g + j < count ? vsrc[4 * g + j] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-                add(e, v);
+                add(e, v, 4 * g);
             }
-            a0 = wave_sum_f64(a0);
-            a1 = wave_sum_f64(a1);
-            a2 = wave_sum_f64(a2);
-            a3 = wave_sum_f64(a3);
-            if (lane == 0) {
-                double* pp = part + (h * wph + w) * 4;
-                pp[0] = a0, pp[1] = a1, pp[2] = a2, pp[3] = a3;
+            const float wgt = (float)(LP - 1 - li);
+#pragma unroll
+            for (uint32_t d = 0; d < 4; ++d) {
+                const double sum = wave_sum_f64(a[d]);
+                const float ws = wave_sum(wgt * fabsf((float)a[d]));
+                const float ab = wave_sum(as[d]);
+                const float mi = wave_min_dpp(mn[d]);
+                if (lane == 0) rec[(h * wph + w) * 4 + d] = PvRec{sum, ws, ab, mi, 0.0f};
             }
         }
     }
     __syncthreads();
-    for (uint32_t o = tid; o < G * 4; o += kPvThreads) {
+    // each output: certified, or repeated in the reference's column order by
+    // one wave (kPvRepTerms terms per round through its LDS buffer, added by
+    // lane 0)
+    const double L = 4.0 * GL;
+    for (uint32_t o = wave; o < G * 4; o += kPvWaves) {  // (wave-uniform)
         const uint32_t h = o / 4, j = o % 4;
-        double sum = 0.0;
-        for (uint32_t v = 0; v < wph; ++v) sum += part[(h * wph + v) * 4 + j];
-        const float r = (float)sum;
-        if (!finite(r)) report_error(err_word, model_key(layer, kStAttnOut, 0));  // math.rs:494
-        att[(kvh * G + h) * hd + d0 + j] = r;
+        double sum = 0.0, A = 0.0, ws = 0.0;
+        float M = INFINITY;
+        for (uint32_t v = 0; v < wph; ++v) {
+            const PvRec r = rec[(h * wph + v) * 4 + j];
+            sum += r.sum;
+            A += (double)r.abs_sum;
+            ws += (double)r.wsum;
+            M = fminf(M, r.min_abs);
+        }
+        float res = (float)sum;
+        if (repeat_all || !pv_certified(sum, A, ws, M, L)) {
+            const float m = stat[2 * h], inv = stat[2 * h + 1];
+            const float* srow = scores + (uint64_t)(kvh * G + h) * row_stride;
+            const float* vcol = vc + v_cache_index(kvh, hd, d0 + j, 0, max_context);
+            double* buf = rep + wave * kPvRepTerms;
+            double seq = 0.0;
+            for (uint32_t base = 0; base < ngroups; base += kPvRepTerms / 4) {
+                const uint32_t g = base + lane;
+                if (g < ngroups) {
+                    float e[4];
+                    exp_group(*(const float4*)(srow + 4 * g), 4 * g, count, m, e);
+#pragma unroll
+                    for (uint32_t jj = 0; jj < 4; ++jj) {
+                        const uint32_t t = 4 * g + jj;
+                        buf[4 * lane + jj] = t < count ? (double)((e[jj] * inv) * vcol[(uint64_t)t * 4]) : 0.0;
+                    }
+                }
+                // one wave's LDS operations are performed in order
+                if (lane == 0) {
+                    const uint32_t nt = count - 4 * base < kPvRepTerms ? count - 4 * base : kPvRepTerms;
+                    for (uint32_t i = 0; i < nt; ++i) seq += buf[i];
+                }
+            }
+            res = (float)__shfl(seq, 0, 64);
+        }
+        if (lane == 0) {
+            if (!finite(res)) report_error(err_word, model_key(layer, kStAttnOut, 0));  // math.rs:494
+            att[(kvh * G + h) * hd + d0 + j] = res;
+        }
     }
 }
 
