@@ -255,9 +255,28 @@ __device__ __forceinline__ uint32_t bs_slot(uint32_t grp) {
     const uint32_t sub = grp >> 1, half = grp & 1;
     return (2 * ((sub >> 1) & 1) + half) * 4 + (sub & 1) + 2 * (sub >> 2);
 }
-enum BsumOrder { kBsNone = 0, kBsQuarters = 1, kBsNatural = 2 };
+// kBsOne: the one-column Q4_K / Q5_K kernels' image (store_one_unit)
+enum BsumOrder { kBsNone = 0, kBsQuarters = 1, kBsNatural = 2, kBsOne = 3 };
 __host__ __device__ constexpr int bsum_order(uint32_t t) {
     return t == kQ4_K || t == kQ5_K ? kBsQuarters : (t == kQ2_K ? kBsNatural : kBsNone);
+}
+
+// The activation image of the one-column Q4_K / Q5_K kernels (lds_map of
+// four columns' room): every 4-byte word k of the slot-order Q8_K image
+// (q45_slots) in a 16-byte record of its own at 16 k, at word position k % 4,
+// the other 12 bytes zero, so one 16-byte read yields an MFMA A operand that
+// is zero outside one lane class (q45_one_ints); and per block the eight
+// sub-block sums of q8 (i16) at bs_off + 256 blk.  A lane pair (r16, r16 ^ 1)
+// stores the 16 slot bytes v and the bsum of unit r16 of block blk.
+__device__ __forceinline__ void store_one_unit(uint8_t* lds, const LdsMap& L, uint32_t blk, uint32_t r16, uint4 v,
+                                               int32_t bsum) {
+    uint8_t* p = lds + blk * 1024 + r16 * 64;
+    *(uint4*)(p) = make_uint4(v.x, 0u, 0u, 0u);
+    *(uint4*)(p + 16) = make_uint4(0u, v.y, 0u, 0u);
+    *(uint4*)(p + 32) = make_uint4(0u, 0u, v.z, 0u);
+    *(uint4*)(p + 48) = make_uint4(0u, 0u, 0u, v.w);
+    const int32_t sub = bsum + dpp_i<kQuadXor1>(bsum);  // both halves of the sub-block
+    if ((r16 & 1) == 0) *(int16_t*)(lds + L.bs_off + blk * 256 + r16) = (int16_t)sub;
 }
 
 // ---------------------------------------------------------------------------
@@ -404,10 +423,12 @@ __device__ __forceinline__ bool stage_q8k(const MvArgs& a, uint8_t* lds, const L
                 report_error(a.err_word, o.kind == kKindNonFinite ? quant_nonfinite_key(a, b, blk * 256ull + o.index)
                                                                   : quant_scale_key(a, b, blk));
         }
-        *(uint4*)(lds + b * L.S + e0) =
-            BSUMS == kBsQuarters ? q45_slots(o.q, r16 & 1) : make_uint4(o.q[0], o.q[1], o.q[2], o.q[3]);
+        if (BSUMS == kBsOne) store_one_unit(lds, L, blk, r16, q45_slots(o.q, r16 & 1), o.bsum);  // (one column)
+        else
+            *(uint4*)(lds + b * L.S + e0) =
+                BSUMS == kBsQuarters ? q45_slots(o.q, r16 & 1) : make_uint4(o.q[0], o.q[1], o.q[2], o.q[3]);
         if (r16 == 0) *(float*)(lds + L.d_off + (blk * 8 + b) * 4) = o.d;
-        if (BSUMS != kBsNone)
+        if (BSUMS != kBsNone && BSUMS != kBsOne)
             *(int16_t*)(lds + L.bs_off + (blk * 8 + b) * 32 + (BSUMS == kBsQuarters ? bs_slot(r16) : r16) * 2) =
                 (int16_t)o.bsum;
     }
@@ -479,9 +500,11 @@ __device__ __forceinline__ bool stage_q8_0(const MvArgs& a, uint8_t* lds, const 
     return __syncthreads_or(bad) == 0;
 }
 
-// Pre-quantized activations (planes in global memory) into LDS.
+// Pre-quantized activations (planes in global memory) into LDS; one: the
+// one-column Q4_K / Q5_K image (store_one_unit).
 template <int W>
-__device__ __forceinline__ bool stage_planes(const MvArgs& a, uint8_t* lds, const LdsMap& L, uint32_t wtype) {
+__device__ __forceinline__ bool stage_planes(const MvArgs& a, uint8_t* lds, const LdsMap& L, uint32_t wtype,
+                                             bool one = false) {
     const uint32_t K = a.cols, bs = wtype == kQ8_0 ? 32 : 256, nb = K / bs;
     const uint32_t tid = threadIdx.x, nt = W * 64;
     const bool slots = wtype == kQ4_K || wtype == kQ5_K;
@@ -489,7 +512,8 @@ __device__ __forceinline__ bool stage_planes(const MvArgs& a, uint8_t* lds, cons
         const uint32_t b = i / (K / 16), e = (i % (K / 16)) * 16;
         const uint4 v = *(const uint4*)(a.pre.q + (uint64_t)b * K + e);
         const uint32_t q[4] = {v.x, v.y, v.z, v.w};
-        *(uint4*)(lds + b * L.S + e) = slots ? q45_slots(q, i & 1) : v;
+        if (one) store_one_unit(lds, L, e / 256, (e % 256) / 16, q45_slots(q, i & 1), a.pre.bsum[i]);  // (one column)
+        else *(uint4*)(lds + b * L.S + e) = slots ? q45_slots(q, i & 1) : v;
     }
     int bad = 0;
     for (uint32_t i = tid; i < a.batch * nb; i += nt) {
@@ -498,7 +522,7 @@ __device__ __forceinline__ bool stage_planes(const MvArgs& a, uint8_t* lds, cons
         bad |= a.pre.bad[i];
     }
     const int order = bsum_order(wtype);
-    if (order != kBsNone) {
+    if (order != kBsNone && !one) {
         for (uint32_t i = tid; i < a.batch * (K / 16); i += nt) {
             const uint32_t b = i / (K / 16), g = i % (K / 16);
             const uint32_t slot = order == kBsQuarters ? bs_slot(g % 16) : g % 16;
@@ -1055,12 +1079,9 @@ __global__ __launch_bounds__(W * 64) void q45_mv_ks_kernel(MvArgs a) {
 // a row: per block, integers[l] = the exact dot over the elements j with
 // j % 8 == l, then (Q4_K / Q5_K) sum -= dmin * mins, then lanes[l] +=
 // d * integers[l]; at the end sum += lanes[0], ..., lanes[7].  The one-column
-// Q4_K / Q5_K kernels reproduce that sequence bit for bit: the weights' slot
-// order (rlq_layout.hpp) puts the four values of one lane class of a
-// sub-block in one 4-byte word, so every v_dot4 yields one (sub-block, class)
-// integer; each block's eight terms d * integers[l] and its mins term
-// dmin * mins are parked in LDS, and the row's sum is then formed in the
-// reference's order (exact_row_sum).
+// Q4_K / Q5_K kernels reproduce that sequence bit for bit: each block's eight
+// terms d * integers[l] and its mins term dmin * mins are parked in LDS, and
+// the row's sum is then formed in the reference's order (exact_row_sum).
 
 // Sums over lane pairs l, l ^ 32 and l, l ^ 16 (v_permlane32_swap /
 // v_permlane16_swap exchange the two halves, resp. adjacent 16-lane rows, of
@@ -1075,23 +1096,45 @@ __device__ __forceinline__ int32_t sum_xor16(int32_t v) {
 }
 
 // Parked terms per (tile slot, block): [4][16] float2, lane kq of row n
-// holding classes 4 (kq % 2) + 2 (kq / 2) and + 1, then [16] f32 mins terms.
+// holding classes 2 kq and 2 kq + 1, then [16] f32 mins terms.
 constexpr uint32_t kParkBlockBytes = 4 * 16 * 8 + 16 * 4;
 __host__ __device__ inline uint32_t park_bytes(uint32_t nb) { return nb * kParkBlockBytes; }
 
-// Exact integers of one Q4_K / Q5_K chunk for lane (n, kq = 2g + h): I[k]
-// the reference's integers[4h + k] of row n (whole: the lanes kq and kq ^ 2
-// hold sub-blocks 2g, 2g+1, 2g+4, 2g+5 and 2(1-g), ... of the same
-// classes), M the whole mins sum (matvec_extra.rs:252-270).  p is this
-// lane's activation row at the block (sub-block 2g, slots 16h ..), bs its
-// bsum word, psel the byte selector of the scale pair (2g, 2g+1).
-struct Q45Lanes {
-    int32_t I[4];
-    int32_t M;
+// The A operand of lane (r = n, kq) in the one-column MFMA step: A row r
+// stands for lane class c = 2 (r / 4) + (r / 2) % 2 of sub-block parity
+// g = r % 2 (sub-blocks 2g, 2g+1, 2g+4, 2g+5 of the four MFMAs).  The
+// weights' K quarter kq holds sub-blocks 2 (kq / 2), ... at slots
+// 16 (kq % 2) .., whose 4-byte word k holds class 4 (kq % 2) + k
+// (rlq_layout.hpp), so the row is live in quarter kq = 2g + c / 4 only, with
+// word c % 4 of that quarter's activation: one record of the expanded image
+// (store_one_unit).  Output element i of lane (n, kq) is then the exact dot of
+// weight row n over class 2 kq + i / 2 of the MFMA's sub-block of parity i % 2.
+struct OneA {
+    const uint8_t* p;       // this lane's record at block 0 (the zero bytes when not live)
+    uint32_t step, o1, o2, o3;  // per block; sub-blocks 2g+1, 2g+4, 2g+5
+};
+__device__ __forceinline__ OneA one_a_operand(uint8_t* lds, const LdsMap& L, uint32_t n, uint32_t kq) {
+    const uint32_t c = 2 * (n >> 2) + ((n >> 1) & 1), g = n & 1;
+    const bool live = kq == 2 * g + (c >> 2);
+    OneA o;
+    o.p = live ? lds + 4 * (64 * (kq >> 1) + 16 * (kq & 1)) + 16 * (c & 3) : lds + L.zero_off;
+    o.step = live ? 1024u : 0u;
+    o.o1 = live ? 4u * 32u : 0u;
+    o.o2 = live ? 4u * 128u : 0u;
+    o.o3 = live ? 4u * 160u : 0u;
+    return o;
+}
+
+// Exact integers of one Q4_K / Q5_K chunk for lane (n, kq): the reference's
+// integers[2 kq] and integers[2 kq + 1] of row n over all eight sub-blocks,
+// and the whole mins sum (matvec_extra.rs:252-270).  a: the lane's A record
+// at the block (one_a_operand); ss: the block's sub-block sums.
+struct Q45One {
+    int32_t I0, I1, M;
 };
 template <uint32_t T>
-__device__ __forceinline__ Q45Lanes q45_lane_ints(const Q4Step<T>& cur, const uint8_t* p, const uint8_t* bs,
-                                                  uint32_t kq, uint32_t psel) {
+__device__ __forceinline__ Q45One q45_one_ints(const Q4Step<T>& cur, const OneA& A, const uint8_t* a,
+                                               const uint8_t* ss, uint32_t kq) {
     typedef short s2 __attribute__((ext_vector_type(2)));
     const Q4Scales q = q4k_scales(cur.h);
     uint32_t l0[4] = {cur.w0.x & 0x0f0f0f0fu, cur.w0.y & 0x0f0f0f0fu, cur.w0.z & 0x0f0f0f0fu, cur.w0.w & 0x0f0f0f0fu};
@@ -1109,43 +1152,43 @@ __device__ __forceinline__ Q45Lanes q45_lane_ints(const Q4Step<T>& cur, const ui
             h1[i] |= hb.h1[i];
         }
     }
-    const uint4 x0 = *(const uint4*)(p), x1 = *(const uint4*)(p + 32);
-    const uint4 x4 = *(const uint4*)(p + 128), x5 = *(const uint4*)(p + 160);
-    const uint32_t a0[4] = {x0.x, x0.y, x0.z, x0.w}, a1[4] = {x1.x, x1.y, x1.z, x1.w};
-    const uint32_t a4[4] = {x4.x, x4.y, x4.z, x4.w}, a5[4] = {x5.x, x5.y, x5.z, x5.w};
-    // scales of sub-blocks (2g, 2g+1) and (2g+4, 2g+5) as i16 pairs
-    const uint32_t S01 = __builtin_amdgcn_perm(0u, q.scA, psel), S45 = __builtin_amdgcn_perm(0u, q.scB, psel);
-    Q45Lanes o;
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-        // the class's four-value dots of the four sub-blocks: |.| <= 31 * 128 * 4
-        // fits i16, so each pair is scaled by one v_dot2
-        const int32_t i0 = dot4(l0[k], a0[k], 0), i1 = dot4(h0[k], a1[k], 0);
-        const int32_t i4 = dot4(l1[k], a4[k], 0), i5 = dot4(h1[k], a5[k], 0);
-        const uint32_t P01 = __builtin_amdgcn_perm((uint32_t)i1, (uint32_t)i0, 0x05040100u);
-        const uint32_t P45 = __builtin_amdgcn_perm((uint32_t)i5, (uint32_t)i4, 0x05040100u);
-        const int32_t I = __builtin_amdgcn_sdot2(
-            __builtin_bit_cast(s2, S01), __builtin_bit_cast(s2, P01),
-            __builtin_amdgcn_sdot2(__builtin_bit_cast(s2, S45), __builtin_bit_cast(s2, P45), 0, false), false);
-        o.I[k] = sum_xor32(I);
-    }
-    // mins: this quarter's four 16-value groups, then all four quarters
-    const uint32_t M01 = __builtin_amdgcn_perm(0u, q.mnA, psel), M45 = __builtin_amdgcn_perm(0u, q.mnB, psel);
-    const uint2 bw = *(const uint2*)bs;
-    const int32_t M = __builtin_amdgcn_sdot2(
-        __builtin_bit_cast(s2, M01), __builtin_bit_cast(s2, bw.x),
-        __builtin_amdgcn_sdot2(__builtin_bit_cast(s2, M45), __builtin_bit_cast(s2, bw.y), 0, false), false);
-    o.M = sum_xor32(sum_xor16(M));
+    auto vec = [](const uint32_t (&w)[4]) { return i32x4{(int)w[0], (int)w[1], (int)w[2], (int)w[3]}; };
+    const i32x4 dl0 = mfma_i8(*(const i32x4*)(a), vec(l0));
+    const i32x4 dh0 = mfma_i8(*(const i32x4*)(a + A.o1), vec(h0));
+    const i32x4 dl1 = mfma_i8(*(const i32x4*)(a + A.o2), vec(l1));
+    const i32x4 dh1 = mfma_i8(*(const i32x4*)(a + A.o3), vec(h1));
+    // scale pairs of the MFMAs' sub-blocks (0, 2), (1, 3), (4, 6), (5, 7) as
+    // i16 pairs; a class's dots |.| <= 31 * 128 * 4 fit i16 as well
+    const uint32_t s02 = __builtin_amdgcn_perm(0u, q.scA, 0x0c020c00u), s13 = __builtin_amdgcn_perm(0u, q.scA, 0x0c030c01u);
+    const uint32_t s46 = __builtin_amdgcn_perm(0u, q.scB, 0x0c020c00u), s57 = __builtin_amdgcn_perm(0u, q.scB, 0x0c030c01u);
+    auto pk = [](int32_t lo, int32_t hi) { return __builtin_bit_cast(s2, __builtin_amdgcn_perm((uint32_t)hi, (uint32_t)lo, 0x05040100u)); };
+    auto cls = [&](int e) {
+        int32_t I = __builtin_amdgcn_sdot2(__builtin_bit_cast(s2, s02), pk(dl0[2 * e], dl0[2 * e + 1]), 0, false);
+        I = __builtin_amdgcn_sdot2(__builtin_bit_cast(s2, s13), pk(dh0[2 * e], dh0[2 * e + 1]), I, false);
+        I = __builtin_amdgcn_sdot2(__builtin_bit_cast(s2, s46), pk(dl1[2 * e], dl1[2 * e + 1]), I, false);
+        return __builtin_amdgcn_sdot2(__builtin_bit_cast(s2, s57), pk(dh1[2 * e], dh1[2 * e + 1]), I, false);
+    };
+    Q45One o;
+    o.I0 = cls(0);
+    o.I1 = cls(1);
+    // mins: sum_s min_s * (bsum[2s] + bsum[2s+1]) over the block's sub-block sums
+    const uint4 S = *(const uint4*)ss;
+    const uint32_t m01 = __builtin_amdgcn_perm(0u, q.mnA, 0x0c010c00u), m23 = __builtin_amdgcn_perm(0u, q.mnA, 0x0c030c02u);
+    const uint32_t m45 = __builtin_amdgcn_perm(0u, q.mnB, 0x0c010c00u), m67 = __builtin_amdgcn_perm(0u, q.mnB, 0x0c030c02u);
+    int32_t M = __builtin_amdgcn_sdot2(__builtin_bit_cast(s2, m01), __builtin_bit_cast(s2, S.x), 0, false);
+    M = __builtin_amdgcn_sdot2(__builtin_bit_cast(s2, m23), __builtin_bit_cast(s2, S.y), M, false);
+    M = __builtin_amdgcn_sdot2(__builtin_bit_cast(s2, m45), __builtin_bit_cast(s2, S.z), M, false);
+    o.M = __builtin_amdgcn_sdot2(__builtin_bit_cast(s2, m67), __builtin_bit_cast(s2, S.w), M, false);
     return o;
 }
 
-// Park one block's terms of lane (n, kq): d * integers[l] for its classes
-// (matvec_extra.rs:287-289, the product rounded to f32) and, when mins, the
-// mins term dmin * mins (:268).  pk / pm: the block's parked records.
+// Park one block's terms of lane (n, kq): d * integers[2 kq], d *
+// integers[2 kq + 1] (matvec_extra.rs:287-289, each product rounded to f32)
+// and, when mins, the mins term dmin * mins (:268).  pk / pm: the block's
+// parked records.
 __device__ __forceinline__ void park_terms(float2* pk, float* pm, uint32_t lane, uint32_t n, uint32_t kq, float d,
-                                           const int32_t (&I)[4], bool mins, float dmin, int32_t M) {
-    const bool g = (kq >> 1) != 0;
-    pk[lane] = make_float2(d * (float)(g ? I[2] : I[0]), d * (float)(g ? I[3] : I[1]));
+                                           int32_t I0, int32_t I1, bool mins, float dmin, int32_t M) {
+    pk[lane] = make_float2(d * (float)I0, d * (float)I1);
     if (mins && kq == 0) pm[n] = dmin * (float)M;
 }
 
@@ -1155,16 +1198,30 @@ __device__ __forceinline__ void park_terms(float2* pk, float* pm, uint32_t lane,
 // returns it; the four lanes (n, kq) of the row must be active.
 __device__ __forceinline__ float exact_row_sum(const float2* pk, const float* pm, uint32_t nb, uint32_t n,
                                                uint32_t kq, bool mins) {
-    const float2* p = pk + (2 * (kq & 1) + (kq >> 1)) * 16 + n;  // classes 2 kq, 2 kq + 1
-    float l0 = 0.0f, l1 = 0.0f;
-    for (uint32_t b = 0; b < nb; ++b) {
+    const float2* p = pk + kq * 16 + n;  // classes 2 kq, 2 kq + 1
+    float l0 = 0.0f, l1 = 0.0f, s = 0.0f;
+    uint32_t b = 0;
+    for (; b + 8 <= nb; b += 8) {  // eight blocks' loads before their adds
+        float2 v[8];
+        float m[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            v[k] = p[(b + k) * 64];
+            m[k] = mins ? pm[(b + k) * 16 + n] : 0.0f;
+        }
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            l0 += v[k].x;
+            l1 += v[k].y;
+            if (mins) s -= m[k];
+        }
+    }
+    for (; b < nb; ++b) {
         const float2 v = p[b * 64];
         l0 += v.x;
         l1 += v.y;
+        if (mins) s -= pm[b * 16 + n];
     }
-    float s = 0.0f;
-    if (mins)
-        for (uint32_t b = 0; b < nb; ++b) s -= pm[b * 16 + n];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         s += __shfl(l0, (int)(n + 16 * j), 64);
@@ -1173,29 +1230,30 @@ __device__ __forceinline__ float exact_row_sum(const float2* pk, const float* pm
     return s;
 }
 
-// Q4_K / Q5_K, one column with a shared Q8_K image: v_dot4_i32_i8 on the
-// VALU (the SiLU-pair epilogue, pre-quantized planes, MUL_MAT_ID pairs).
+// Q4_K / Q5_K, one column with a shared Q8_K image (the SiLU-pair epilogue,
+// pre-quantized planes, MUL_MAT_ID pairs).
 //
 // A workgroup of W waves works on TS = W / KS tiles at a time; the KS waves of
 // a tile take its blocks kp, kp + KS, ... (kp = the wave's K part), so a tile's
 // bytes stream through KS waves and every SIMD holds several waves.  Lane
-// (n, kq), kq = 2g + h, multiplies slots 16h .. 16h + 15 (lane classes
-// 4h .. 4h + 3) of sub-blocks 2g, 2g+1 (qs bytes of w0) and 2g+4, 2g+5 (w1)
-// of row n (q45_lane_ints); every block's terms are parked in LDS, and after
-// the last tile the workgroup forms each row's sum in the reference's order
+// (n, kq) gets the integers of lane classes 2 kq, 2 kq + 1 of row n from four
+// MFMAs (q45_one_ints); every block's terms are parked in LDS, and after the
+// last tile the workgroup forms each row's sum in the reference's order
 // (exact_row_sum).
 template <int W, int KS>
 struct SmallGeom {
     static constexpr int TS = W / KS;
 };
 
-// LDS bytes of the small kernel: the activations plus the parked terms
-// [tmax][TS][nb] (park_terms), tmax = tiles per (workgroup, tile slot).
-__host__ __device__ inline uint32_t small_part_off(uint32_t cols, uint32_t batch) {
-    return (lds_map(kQ4_K, cols, batch).total + 15u) & ~15u;
+// LDS bytes of the small kernel: the activations (store_one_unit) plus the
+// parked terms [tmax][TS][nb] (park_terms), tmax = tiles per (workgroup,
+// tile slot).
+__host__ __device__ inline LdsMap lds_map_one(uint32_t t, uint32_t cols) { return lds_map(t, cols, 4); }
+__host__ __device__ inline uint32_t one_part_off(uint32_t cols) {
+    return (lds_map_one(kQ4_K, cols).total + 15u) & ~15u;
 }
 __host__ __device__ inline uint32_t small_lds_bytes(uint32_t cols, uint32_t tmax, uint32_t ts) {
-    return small_part_off(cols, 1) + tmax * ts * park_bytes(cols / 256);
+    return one_part_off(cols) + tmax * ts * park_bytes(cols / 256);
 }
 
 // (two workgroups of 8 waves per CU: at most 128 VGPRs)
@@ -1204,7 +1262,7 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(4))) voi
     constexpr int TS = SmallGeom<W, KS>::TS;
     if (!mv_enter(a)) return;
     extern __shared__ __align__(16) uint8_t lds[];
-    const LdsMap L = lds_map(T, a.cols, 1);
+    const LdsMap L = lds_map_one(T, a.cols);
     const uint32_t lane = threadIdx.x & 63, n = lane & 15, kq = lane >> 4;
     // wave-uniform indices in scalar registers: loop control stays on the SALU
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -1215,7 +1273,7 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(4))) voi
     const uint32_t my_tiles = t0 < ntiles ? (ntiles - 1 - t0) / tstride + 1 : 0;
     const uint32_t bpt = kp < nb ? (nb - 1 - kp) / KS + 1 : 0;  // blocks of each tile this wave takes
     const uint32_t steps = my_tiles * bpt;
-    float2* park = (float2*)(lds + small_part_off(a.cols, 1));
+    float2* park = (float2*)(lds + one_part_off(a.cols));
     float* parkm = (float*)(park + tmax * TS * nb * 64);
 
     if (threadIdx.x < 16) *(uint4*)(lds + L.zero_off + threadIdx.x * 16) = make_uint4(0, 0, 0, 0);
@@ -1238,26 +1296,20 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(4))) voi
 #pragma unroll
     for (int i = 0; i < D; ++i) issue(buf[i]);
 
-    const bool ok = a.x ? stage_q8k<W, kBsQuarters>(a, lds, L, wave, xv) : stage_planes<W>(a, lds, L, T);
+    const bool ok = a.x ? stage_q8k<W, kBsOne>(a, lds, L, wave, xv) : stage_planes<W>(a, lds, L, T, true);
     if (!ok) return finish_argmax(a, lds, L);
     if (a.zero_pair) return zero_slot_tiles<W, TS>(a, tmax, tstride);
 
-    const uint32_t g = kq >> 1, h = kq & 1;
-    // activation of (sub-block 2g, slots 16h ..) and its neighbours: +32
-    // (2g+1), +128 (2g+4), +160 (2g+5)
-    const uint8_t* a_row = lds + 64 * g + 16 * h;
-    const uint8_t* bs_row = lds + L.bs_off + kq * 8;
-    const uint32_t psel = (2 * g) | 0x0c00u | (2 * g + 1) << 16 | 0x0c000000u;
-
+    const OneA A = one_a_operand(lds, L, n, kq);
     uint32_t ti = 0, tile = t0, blk = kp, j = 0;
     auto compute = [&](const Q4Step<T>& cur) {
-        const Q45Lanes o = q45_lane_ints<T>(cur, a_row + blk * 256, bs_row + blk * 256, kq, psel);
+        const Q45One o = q45_one_ints<T>(cur, A, A.p + blk * A.step, lds + L.bs_off + blk * 256, kq);
         const float dw = half_to_float(cur.h.x), dmw = half_to_float(cur.h.x >> 16);
         const float da = *(const float*)(lds + L.d_off + blk * 32);
         const uint32_t rec = (ti * TS + ts) * nb + blk;
-        park_terms(park + rec * 64, parkm + rec * 16, lane, n, kq, dw * da, o.I, true, dmw * da, o.M);
+        park_terms(park + rec * 64, parkm + rec * 16, lane, n, kq, dw * da, o.I0, o.I1, true, dmw * da, o.M);
         if (DBG) {  // exact block integers: the eight classes
-            const int32_t I = sum_xor16(o.I[0] + o.I[1] + o.I[2] + o.I[3]);
+            const int32_t I = sum_xor32(sum_xor16(o.I0 + o.I1));
             const uint32_t row = tile * kTileRows + n;
             if (kq == 0 && row < a.rows) {
                 a.dbg_isum[(uint64_t)row * nb + blk] = I;
@@ -1325,7 +1377,7 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(4))) voi
 // barrier between tiles).  LDS after the Q8_K image: parked terms
 // [tmax][TS][nb], counters [tmax][TS], residuals [tmax][TS][16].
 __host__ __device__ inline uint32_t b1_lds_bytes(uint32_t cols, uint32_t tmax, uint32_t ts) {
-    return small_part_off(cols, 1) + tmax * ts * (park_bytes(cols / 256) + 4u + 16u * 4u);
+    return one_part_off(cols) + tmax * ts * (park_bytes(cols / 256) + 4u + 16u * 4u);
 }
 
 // The RMSNorm scale (math.rs:210-221) from the values of the workgroup's own
@@ -1373,7 +1425,7 @@ __global__ __launch_bounds__(W * 64) void q45_mv_b1_kernel(MvArgs a) {
     constexpr int TS = W / KS;
     static_assert(!BAL || TS == 2 || TS == 4, "the balanced deal takes two or four tile slots");
     extern __shared__ __align__(16) uint8_t lds[];
-    const LdsMap L = lds_map(T, a.cols, 1);
+    const LdsMap L = lds_map_one(T, a.cols);
     const uint32_t lane = threadIdx.x & 63, n = lane & 15, kq = lane >> 4;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t ts = wave / KS, kp = wave % KS;
@@ -1403,11 +1455,12 @@ __global__ __launch_bounds__(W * 64) void q45_mv_b1_kernel(MvArgs a) {
     const uint32_t nk = (uint32_t)KS < nb ? (uint32_t)KS : nb;  // waves of a tile that take blocks
     // LDS after the Q8_K image: parked terms [tmax * TS][nb] (park_terms),
     // counters [tmax * TS], residuals [tmax * TS][16]
-    float2* park = (float2*)(lds + small_part_off(a.cols, 1));
+    float2* park = (float2*)(lds + one_part_off(a.cols));
     float* parkm = (float*)(park + tmax * TS * nb * 64);
     uint32_t* cnt = (uint32_t*)(parkm + tmax * TS * nb * 16);
     float* rs = (float*)(cnt + tmax * TS);
     for (uint32_t i = threadIdx.x; i < tmax * TS; i += W * 64) cnt[i] = 0;
+    if (threadIdx.x < 16) *(uint4*)(lds + L.zero_off + threadIdx.x * 16) = make_uint4(0, 0, 0, 0);  // dead A lanes
     const bool rms = FULL && a.xform == kXfRmsNorm;
     if (FULL && threadIdx.x < 8) ((unsigned long long*)(lds + L.am_off))[threadIdx.x] = 0ull;
 
@@ -1462,9 +1515,8 @@ __global__ __launch_bounds__(W * 64) void q45_mv_b1_kernel(MvArgs a) {
                 report_error(a.err_word, o.kind == kKindNonFinite ? quant_nonfinite_key(a, 0, xblk * 256ull + o.index)
                                                                   : quant_scale_key(a, 0, xblk));
         }
-        *(uint4*)(lds + xblk * 256 + r16 * 16) = q45_slots(o.q, r16 & 1);
+        store_one_unit(lds, L, xblk, r16, q45_slots(o.q, r16 & 1), o.bsum);
         if (r16 == 0) *(float*)(lds + L.d_off + xblk * 32) = o.d;
-        *(int16_t*)(lds + L.bs_off + xblk * 256 + bs_slot(r16) * 2) = (int16_t)o.bsum;
     }
     // the counters' zeros, every own block, the residuals and every wave's
     // error flag
@@ -1473,23 +1525,17 @@ __global__ __launch_bounds__(W * 64) void q45_mv_b1_kernel(MvArgs a) {
         return;
     }
 
-    const uint32_t g = kq >> 1, h = kq & 1;
-    // activation of (sub-block 2g, slots 16h ..) and its neighbours: +32
-    // (2g+1), +128 (2g+4), +160 (2g+5)
-    const uint8_t* a_row = lds + 64 * g + 16 * h;
-    const uint8_t* bs_row = lds + L.bs_off + kq * 8;
-    // bytes 2g and 2g + 1 of a packed scale word, widened to two i16 lanes
-    const uint32_t psel = (2 * g) | 0x0c00u | (2 * g + 1) << 16 | 0x0c000000u;
+    const OneA A = one_a_operand(lds, L, n, kq);
     unsigned long long best = 0;
     uint32_t ti = 0, blk = kp, j = 0, tile = tile_of(0);
     auto compute = [&](const Q4Step<T>& cur) {
-        const Q45Lanes o = q45_lane_ints<T>(cur, a_row + blk * 256, bs_row + blk * 256, kq, psel);
+        const Q45One o = q45_one_ints<T>(cur, A, A.p + blk * A.step, lds + L.bs_off + blk * 256, kq);
         const float dw = half_to_float(cur.h.x), dmw = half_to_float(cur.h.x >> 16);
         const float da = *(const float*)(lds + L.d_off + blk * 32);
         const uint32_t rec = (ti * TS + ts) * nb + blk;
-        park_terms(park + rec * 64, parkm + rec * 16, lane, n, kq, dw * da, o.I, true, dmw * da, o.M);
+        park_terms(park + rec * 64, parkm + rec * 16, lane, n, kq, dw * da, o.I0, o.I1, true, dmw * da, o.M);
         if (DBG) {  // exact block integers: the eight classes
-            const int32_t I = sum_xor16(o.I[0] + o.I[1] + o.I[2] + o.I[3]);
+            const int32_t I = sum_xor32(sum_xor16(o.I0 + o.I1));
             const uint32_t row = tile * kTileRows + n;
             if (kq == 0 && row < a.rows && own_row(ti)) {
                 a.dbg_isum[(uint64_t)row * nb + blk] = I;
@@ -2393,7 +2439,7 @@ static hipError_t launch_parked(void (*kernel)(MvArgs), size_t& lds_set, const M
     const uint32_t gy = grid_rows(a, pairs);
     uint32_t grid = grid_cols(want, (uint32_t)kSmallWgPerCu * (uint32_t)device_cus(), gy);
     // enough workgroups that every one parks at most `room` tiles' terms
-    const size_t off = small_part_off(a.cols, 1), per_tile = (size_t)TS * park_bytes(a.nb);
+    const size_t off = one_part_off(a.cols), per_tile = (size_t)TS * park_bytes(a.nb);
     if (off >= kMaxLds || (kMaxLds - off) / per_tile == 0) return hipErrorInvalidValue;
     const uint64_t room = (kMaxLds - off) / per_tile, need = (a.ntiles + room * TS - 1) / (room * TS);
     if (grid < need) grid = (uint32_t)need;
@@ -2422,7 +2468,7 @@ template <int W, int KS>
 static void b1_grid(const MvArgs& a, uint32_t& grid, uint32_t& tmax) {
     constexpr int TS = W / KS;
     grid = grid_cols((a.ntiles + TS - 1) / TS, (uint32_t)kSmallWgPerCu * (uint32_t)device_cus(), 1);
-    const size_t off = small_part_off(a.cols, 1), per_tile = (size_t)TS * (park_bytes(a.nb) + 4u + 64u);
+    const size_t off = one_part_off(a.cols), per_tile = (size_t)TS * (park_bytes(a.nb) + 4u + 64u);
     const uint64_t room = off < kMaxLds ? (kMaxLds - off) / per_tile : 0;
     if (room == 0) {
         grid = tmax = 0;
