@@ -255,28 +255,34 @@ __device__ __forceinline__ uint32_t bs_slot(uint32_t grp) {
     const uint32_t sub = grp >> 1, half = grp & 1;
     return (2 * ((sub >> 1) & 1) + half) * 4 + (sub & 1) + 2 * (sub >> 2);
 }
-// kBsOne: the one-column Q4_K / Q5_K kernels' image (store_one_unit)
-enum BsumOrder { kBsNone = 0, kBsQuarters = 1, kBsNatural = 2, kBsOne = 3 };
+// kBsOne / kBsOneCompact: the one-column Q4_K / Q5_K kernels' image
+// (store_one_unit, expanded or compact)
+enum BsumOrder { kBsNone = 0, kBsQuarters = 1, kBsNatural = 2, kBsOne = 3, kBsOneCompact = 4 };
 __host__ __device__ constexpr int bsum_order(uint32_t t) {
     return t == kQ4_K || t == kQ5_K ? kBsQuarters : (t == kQ2_K ? kBsNatural : kBsNone);
 }
 
-// The activation image of the one-column Q4_K / Q5_K kernels (lds_map of
-// four columns' room): every 4-byte word k of the slot-order Q8_K image
-// (q45_slots) in a 16-byte record of its own at 16 k, at word position k % 4,
-// the other 12 bytes zero, so one 16-byte read yields an MFMA A operand that
-// is zero outside one lane class (q45_one_ints); and per block the eight
-// sub-block sums of q8 (i16) at bs_off + 256 blk.  A lane pair (r16, r16 ^ 1)
+// The activation image of the one-column Q4_K / Q5_K kernels.  Expanded
+// (lds_map of four columns' room): every 4-byte word k of the slot-order
+// Q8_K image (q45_slots) in a 16-byte record of its own at 16 k, at word
+// position k % 4, the other 12 bytes zero, so one 16-byte read yields an MFMA
+// A operand that is zero outside one lane class (q45_one_ints); compact: the
+// slot-order image itself, masked in registers.  Per block, the eight
+// sub-block sums of q8 (i16) at bs_off + 16 blk.  A lane pair (r16, r16 ^ 1)
 // stores the 16 slot bytes v and the bsum of unit r16 of block blk.
 __device__ __forceinline__ void store_one_unit(uint8_t* lds, const LdsMap& L, uint32_t blk, uint32_t r16, uint4 v,
-                                               int32_t bsum) {
-    uint8_t* p = lds + blk * 1024 + r16 * 64;
-    *(uint4*)(p) = make_uint4(v.x, 0u, 0u, 0u);
-    *(uint4*)(p + 16) = make_uint4(0u, v.y, 0u, 0u);
-    *(uint4*)(p + 32) = make_uint4(0u, 0u, v.z, 0u);
-    *(uint4*)(p + 48) = make_uint4(0u, 0u, 0u, v.w);
+                                               int32_t bsum, bool exp) {
+    if (exp) {
+        uint8_t* p = lds + blk * 1024 + r16 * 64;
+        *(uint4*)(p) = make_uint4(v.x, 0u, 0u, 0u);
+        *(uint4*)(p + 16) = make_uint4(0u, v.y, 0u, 0u);
+        *(uint4*)(p + 32) = make_uint4(0u, 0u, v.z, 0u);
+        *(uint4*)(p + 48) = make_uint4(0u, 0u, 0u, v.w);
+    } else {
+        *(uint4*)(lds + blk * 256 + r16 * 16) = v;
+    }
     const int32_t sub = bsum + dpp_i<kQuadXor1>(bsum);  // both halves of the sub-block
-    if ((r16 & 1) == 0) *(int16_t*)(lds + L.bs_off + blk * 256 + r16) = (int16_t)sub;
+    if ((r16 & 1) == 0) *(int16_t*)(lds + L.bs_off + blk * 16 + r16) = (int16_t)sub;
 }
 
 // ---------------------------------------------------------------------------
@@ -423,12 +429,13 @@ __device__ __forceinline__ bool stage_q8k(const MvArgs& a, uint8_t* lds, const L
                 report_error(a.err_word, o.kind == kKindNonFinite ? quant_nonfinite_key(a, b, blk * 256ull + o.index)
                                                                   : quant_scale_key(a, b, blk));
         }
-        if (BSUMS == kBsOne) store_one_unit(lds, L, blk, r16, q45_slots(o.q, r16 & 1), o.bsum);  // (one column)
+        if (BSUMS == kBsOne || BSUMS == kBsOneCompact)  // (one column)
+            store_one_unit(lds, L, blk, r16, q45_slots(o.q, r16 & 1), o.bsum, BSUMS == kBsOne);
         else
             *(uint4*)(lds + b * L.S + e0) =
                 BSUMS == kBsQuarters ? q45_slots(o.q, r16 & 1) : make_uint4(o.q[0], o.q[1], o.q[2], o.q[3]);
         if (r16 == 0) *(float*)(lds + L.d_off + (blk * 8 + b) * 4) = o.d;
-        if (BSUMS != kBsNone && BSUMS != kBsOne)
+        if (BSUMS != kBsNone && BSUMS != kBsOne && BSUMS != kBsOneCompact)
             *(int16_t*)(lds + L.bs_off + (blk * 8 + b) * 32 + (BSUMS == kBsQuarters ? bs_slot(r16) : r16) * 2) =
                 (int16_t)o.bsum;
     }
@@ -501,10 +508,10 @@ __device__ __forceinline__ bool stage_q8_0(const MvArgs& a, uint8_t* lds, const 
 }
 
 // Pre-quantized activations (planes in global memory) into LDS; one: the
-// one-column Q4_K / Q5_K image (store_one_unit).
+// one-column Q4_K / Q5_K image (store_one_unit, expanded when exp).
 template <int W>
 __device__ __forceinline__ bool stage_planes(const MvArgs& a, uint8_t* lds, const LdsMap& L, uint32_t wtype,
-                                             bool one = false) {
+                                             bool one = false, bool exp = false) {
     const uint32_t K = a.cols, bs = wtype == kQ8_0 ? 32 : 256, nb = K / bs;
     const uint32_t tid = threadIdx.x, nt = W * 64;
     const bool slots = wtype == kQ4_K || wtype == kQ5_K;
@@ -512,7 +519,7 @@ __device__ __forceinline__ bool stage_planes(const MvArgs& a, uint8_t* lds, cons
         const uint32_t b = i / (K / 16), e = (i % (K / 16)) * 16;
         const uint4 v = *(const uint4*)(a.pre.q + (uint64_t)b * K + e);
         const uint32_t q[4] = {v.x, v.y, v.z, v.w};
-        if (one) store_one_unit(lds, L, e / 256, (e % 256) / 16, q45_slots(q, i & 1), a.pre.bsum[i]);  // (one column)
+        if (one) store_one_unit(lds, L, e / 256, (e % 256) / 16, q45_slots(q, i & 1), a.pre.bsum[i], exp);
         else *(uint4*)(lds + b * L.S + e) = slots ? q45_slots(q, i & 1) : v;
     }
     int bad = 0;
@@ -1096,7 +1103,8 @@ __device__ __forceinline__ int32_t sum_xor16(int32_t v) {
 }
 
 // Parked terms per (tile slot, block): [4][16] float2, lane kq of row n
-// holding classes 2 kq and 2 kq + 1, then [16] f32 mins terms.
+// holding classes 2 kq and 2 kq + 1, then [16] f32, the block's mins term of
+// row n (the four lanes of a row store the same value).
 constexpr uint32_t kParkBlockBytes = 4 * 16 * 8 + 16 * 4;
 __host__ __device__ inline uint32_t park_bytes(uint32_t nb) { return nb * kParkBlockBytes; }
 
@@ -1110,31 +1118,52 @@ __host__ __device__ inline uint32_t park_bytes(uint32_t nb) { return nb * kParkB
 // (store_one_unit).  Output element i of lane (n, kq) is then the exact dot of
 // weight row n over class 2 kq + i / 2 of the MFMA's sub-block of parity i % 2.
 struct OneA {
-    const uint8_t* p;       // this lane's record at block 0 (the zero bytes when not live)
+    const uint8_t* p;           // this lane's A bytes at block 0 (the zero bytes when not live)
     uint32_t step, o1, o2, o3;  // per block; sub-blocks 2g+1, 2g+4, 2g+5
+    uint32_t m[4];              // compact image: the word mask
 };
-__device__ __forceinline__ OneA one_a_operand(uint8_t* lds, const LdsMap& L, uint32_t n, uint32_t kq) {
+__device__ __forceinline__ OneA one_a_operand(uint8_t* lds, const LdsMap& L, uint32_t n, uint32_t kq, bool exp) {
     const uint32_t c = 2 * (n >> 2) + ((n >> 1) & 1), g = n & 1;
     const bool live = kq == 2 * g + (c >> 2);
+    const uint32_t O = 64 * (kq >> 1) + 16 * (kq & 1), x = exp ? 4u : 1u;
     OneA o;
-    o.p = live ? lds + 4 * (64 * (kq >> 1) + 16 * (kq & 1)) + 16 * (c & 3) : lds + L.zero_off;
-    o.step = live ? 1024u : 0u;
-    o.o1 = live ? 4u * 32u : 0u;
-    o.o2 = live ? 4u * 128u : 0u;
-    o.o3 = live ? 4u * 160u : 0u;
+    o.p = live ? lds + x * O + (exp ? 16 * (c & 3) : 0u) : lds + L.zero_off;
+    o.step = live ? 256u * x : 0u;
+    o.o1 = live ? x * 32u : 0u;
+    o.o2 = live ? x * 128u : 0u;
+    o.o3 = live ? x * 160u : 0u;
+#pragma unroll
+    for (uint32_t w = 0; w < 4; ++w) o.m[w] = live && w == (c & 3) ? ~0u : 0u;
     return o;
+}
+
+// The LDS operands of one chunk: the four A operands (masked in registers for
+// the compact image), the block's sub-block sums and Q8_K scale.  a: the
+// lane's A record at the block (one_a_operand).
+struct OneLoads {
+    i32x4 a0, a1, a2, a3;
+    uint4 S;
+    float da;
+};
+template <bool EXP>
+__device__ __forceinline__ OneLoads one_loads(const OneA& A, const uint8_t* a, const uint8_t* ss, const uint8_t* dp) {
+    auto aop = [&](const uint8_t* q) {
+        const i32x4 v = *(const i32x4*)q;
+        if constexpr (EXP) return v;
+        else return i32x4{v[0] & (int)A.m[0], v[1] & (int)A.m[1], v[2] & (int)A.m[2], v[3] & (int)A.m[3]};
+    };
+    return OneLoads{aop(a), aop(a + A.o1), aop(a + A.o2), aop(a + A.o3), *(const uint4*)ss, *(const float*)dp};
 }
 
 // Exact integers of one Q4_K / Q5_K chunk for lane (n, kq): the reference's
 // integers[2 kq] and integers[2 kq + 1] of row n over all eight sub-blocks,
-// and the whole mins sum (matvec_extra.rs:252-270).  a: the lane's A record
-// at the block (one_a_operand); ss: the block's sub-block sums.
+// and the whole mins sum (matvec_extra.rs:252-270), from the chunk's LDS
+// operands r.
 struct Q45One {
     int32_t I0, I1, M;
 };
 template <uint32_t T>
-__device__ __forceinline__ Q45One q45_one_ints(const Q4Step<T>& cur, const OneA& A, const uint8_t* a,
-                                               const uint8_t* ss, uint32_t kq) {
+__device__ __forceinline__ Q45One q45_one_ints(const Q4Step<T>& cur, const OneLoads& r, uint32_t kq) {
     typedef short s2 __attribute__((ext_vector_type(2)));
     const Q4Scales q = q4k_scales(cur.h);
     uint32_t l0[4] = {cur.w0.x & 0x0f0f0f0fu, cur.w0.y & 0x0f0f0f0fu, cur.w0.z & 0x0f0f0f0fu, cur.w0.w & 0x0f0f0f0fu};
@@ -1153,10 +1182,10 @@ __device__ __forceinline__ Q45One q45_one_ints(const Q4Step<T>& cur, const OneA&
         }
     }
     auto vec = [](const uint32_t (&w)[4]) { return i32x4{(int)w[0], (int)w[1], (int)w[2], (int)w[3]}; };
-    const i32x4 dl0 = mfma_i8(*(const i32x4*)(a), vec(l0));
-    const i32x4 dh0 = mfma_i8(*(const i32x4*)(a + A.o1), vec(h0));
-    const i32x4 dl1 = mfma_i8(*(const i32x4*)(a + A.o2), vec(l1));
-    const i32x4 dh1 = mfma_i8(*(const i32x4*)(a + A.o3), vec(h1));
+    const i32x4 dl0 = mfma_i8(r.a0, vec(l0));
+    const i32x4 dh0 = mfma_i8(r.a1, vec(h0));
+    const i32x4 dl1 = mfma_i8(r.a2, vec(l1));
+    const i32x4 dh1 = mfma_i8(r.a3, vec(h1));
     // scale pairs of the MFMAs' sub-blocks (0, 2), (1, 3), (4, 6), (5, 7) as
     // i16 pairs; a class's dots |.| <= 31 * 128 * 4 fit i16 as well
     const uint32_t s02 = __builtin_amdgcn_perm(0u, q.scA, 0x0c020c00u), s13 = __builtin_amdgcn_perm(0u, q.scA, 0x0c030c01u);
@@ -1172,7 +1201,7 @@ __device__ __forceinline__ Q45One q45_one_ints(const Q4Step<T>& cur, const OneA&
     o.I0 = cls(0);
     o.I1 = cls(1);
     // mins: sum_s min_s * (bsum[2s] + bsum[2s+1]) over the block's sub-block sums
-    const uint4 S = *(const uint4*)ss;
+    const uint4 S = r.S;
     const uint32_t m01 = __builtin_amdgcn_perm(0u, q.mnA, 0x0c010c00u), m23 = __builtin_amdgcn_perm(0u, q.mnA, 0x0c030c02u);
     const uint32_t m45 = __builtin_amdgcn_perm(0u, q.mnB, 0x0c010c00u), m67 = __builtin_amdgcn_perm(0u, q.mnB, 0x0c030c02u);
     int32_t M = __builtin_amdgcn_sdot2(__builtin_bit_cast(s2, m01), __builtin_bit_cast(s2, S.x), 0, false);
@@ -1184,21 +1213,20 @@ __device__ __forceinline__ Q45One q45_one_ints(const Q4Step<T>& cur, const OneA&
 
 // Park one block's terms of lane (n, kq): d * integers[2 kq], d *
 // integers[2 kq + 1] (matvec_extra.rs:287-289, each product rounded to f32)
-// and, when mins, the mins term dmin * mins (:268).  pk / pm: the block's
-// parked records.
-__device__ __forceinline__ void park_terms(float2* pk, float* pm, uint32_t lane, uint32_t n, uint32_t kq, float d,
-                                           int32_t I0, int32_t I1, bool mins, float dmin, int32_t M) {
-    pk[lane] = make_float2(d * (float)I0, d * (float)I1);
-    if (mins && kq == 0) pm[n] = dmin * (float)M;
+// and the mins term dmin * mins (:268).  pk: the slot's records (park_bytes).
+__device__ __forceinline__ void park_terms(uint8_t* pk, uint32_t nb, uint32_t blk, uint32_t lane, float d,
+                                           int32_t I0, int32_t I1, float mn) {
+    ((float2*)pk)[blk * 64 + lane] = make_float2(d * (float)I0, d * (float)I1);
+    ((float*)(pk + nb * 512))[blk * 16 + (lane & 15)] = mn;
 }
 
 // The row's f32 in the reference's order from its parked terms (nb blocks;
-// pk, pm the slot's records): lanes[l] over the blocks in order, sum minus
-// the mins terms in order, then sum + lanes[0..7].  Every lane of row n
-// returns it; the four lanes (n, kq) of the row must be active.
-__device__ __forceinline__ float exact_row_sum(const float2* pk, const float* pm, uint32_t nb, uint32_t n,
-                                               uint32_t kq, bool mins) {
-    const float2* p = pk + kq * 16 + n;  // classes 2 kq, 2 kq + 1
+// pk the slot's records): lanes[l] over the blocks in order, sum minus the
+// mins terms in order, then sum + lanes[0..7].  Lane kq = 0 of row n returns
+// it; the four lanes (n, kq) of every row of the wave must take part.
+__device__ __forceinline__ float exact_row_sum(const uint8_t* pk, uint32_t nb, uint32_t lane) {
+    const float2* p = (const float2*)pk + lane;                    // classes 2 kq, 2 kq + 1 of row n
+    const float* q = (const float*)(pk + nb * 512) + (lane & 15);  // the mins terms
     float l0 = 0.0f, l1 = 0.0f, s = 0.0f;
     uint32_t b = 0;
     for (; b + 8 <= nb; b += 8) {  // eight blocks' loads before their adds
@@ -1207,21 +1235,22 @@ __device__ __forceinline__ float exact_row_sum(const float2* pk, const float* pm
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
             v[k] = p[(b + k) * 64];
-            m[k] = mins ? pm[(b + k) * 16 + n] : 0.0f;
+            m[k] = q[(b + k) * 16];
         }
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
             l0 += v[k].x;
             l1 += v[k].y;
-            if (mins) s -= m[k];
+            s -= m[k];
         }
     }
     for (; b < nb; ++b) {
         const float2 v = p[b * 64];
         l0 += v.x;
         l1 += v.y;
-        if (mins) s -= pm[b * 16 + n];
+        s -= q[b * 16];
     }
+    const uint32_t n = lane & 15;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         s += __shfl(l0, (int)(n + 16 * j), 64);
@@ -1248,21 +1277,36 @@ struct SmallGeom {
 // LDS bytes of the small kernel: the activations (store_one_unit) plus the
 // parked terms [tmax][TS][nb] (park_terms), tmax = tiles per (workgroup,
 // tile slot).
-__host__ __device__ inline LdsMap lds_map_one(uint32_t t, uint32_t cols) { return lds_map(t, cols, 4); }
-__host__ __device__ inline uint32_t one_part_off(uint32_t cols) {
-    return (lds_map_one(kQ4_K, cols).total + 15u) & ~15u;
+// LDS of the one-column kernels: the image (expanded: 4 cols bytes), d f32
+// [nb][8] (column 0 used), the sub-block sums [nb][8] i16, the zero bytes,
+// the RMSNorm reduction and the argmax keys.
+__host__ __device__ inline LdsMap lds_map_one(uint32_t t, uint32_t cols, bool exp) {
+    LdsMap m;
+    const uint32_t nb = cols / 256;
+    m.S = 0;
+    m.d_off = (exp ? 4u : 1u) * cols;
+    m.bs_off = m.d_off + nb * 32;
+    m.zero_off = m.bs_off + nb * 16;
+    m.red_off = m.zero_off + 256;
+    m.am_off = m.red_off + 512;
+    m.total = m.am_off + 80;
+    return m;
 }
-__host__ __device__ inline uint32_t small_lds_bytes(uint32_t cols, uint32_t tmax, uint32_t ts) {
-    return one_part_off(cols) + tmax * ts * park_bytes(cols / 256);
+__host__ __device__ inline uint32_t one_part_off(uint32_t cols, bool exp) {
+    return (lds_map_one(kQ4_K, cols, exp).total + 15u) & ~15u;
+}
+__host__ __device__ inline uint32_t small_lds_bytes(uint32_t cols, uint32_t tmax, uint32_t ts, bool exp) {
+    return one_part_off(cols, exp) + tmax * ts * park_bytes(cols / 256);
 }
 
-// (two workgroups of 8 waves per CU: at most 128 VGPRs)
-template <uint32_t T, int W, int KS, int D, bool DBG>
+// (two workgroups of 8 waves per CU: at most 128 VGPRs).  EXP: the expanded
+// activation image (store_one_unit), else the compact one.
+template <uint32_t T, int W, int KS, int D, bool DBG, bool EXP>
 __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(4))) void q4k_mv_small_kernel(MvArgs a) {
     constexpr int TS = SmallGeom<W, KS>::TS;
     if (!mv_enter(a)) return;
     extern __shared__ __align__(16) uint8_t lds[];
-    const LdsMap L = lds_map_one(T, a.cols);
+    const LdsMap L = lds_map_one(T, a.cols, EXP);
     const uint32_t lane = threadIdx.x & 63, n = lane & 15, kq = lane >> 4;
     // wave-uniform indices in scalar registers: loop control stays on the SALU
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -1273,8 +1317,7 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(4))) voi
     const uint32_t my_tiles = t0 < ntiles ? (ntiles - 1 - t0) / tstride + 1 : 0;
     const uint32_t bpt = kp < nb ? (nb - 1 - kp) / KS + 1 : 0;  // blocks of each tile this wave takes
     const uint32_t steps = my_tiles * bpt;
-    float2* park = (float2*)(lds + one_part_off(a.cols));
-    float* parkm = (float*)(park + tmax * TS * nb * 64);
+    uint8_t* park = lds + one_part_off(a.cols, EXP);
 
     if (threadIdx.x < 16) *(uint4*)(lds + L.zero_off + threadIdx.x * 16) = make_uint4(0, 0, 0, 0);
     if (threadIdx.x < 8) ((unsigned long long*)(lds + L.am_off))[threadIdx.x] = 0ull;
@@ -1296,18 +1339,19 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(4))) voi
 #pragma unroll
     for (int i = 0; i < D; ++i) issue(buf[i]);
 
-    const bool ok = a.x ? stage_q8k<W, kBsOne>(a, lds, L, wave, xv) : stage_planes<W>(a, lds, L, T, true);
+    const bool ok = a.x ? stage_q8k<W, EXP ? kBsOne : kBsOneCompact>(a, lds, L, wave, xv)
+                        : stage_planes<W>(a, lds, L, T, true, EXP);
     if (!ok) return finish_argmax(a, lds, L);
     if (a.zero_pair) return zero_slot_tiles<W, TS>(a, tmax, tstride);
 
-    const OneA A = one_a_operand(lds, L, n, kq);
+    const OneA A = one_a_operand(lds, L, n, kq, EXP);
+    const uint32_t pbytes = park_bytes(nb);
     uint32_t ti = 0, tile = t0, blk = kp, j = 0;
     auto compute = [&](const Q4Step<T>& cur) {
-        const Q45One o = q45_one_ints<T>(cur, A, A.p + blk * A.step, lds + L.bs_off + blk * 256, kq);
+        const OneLoads r = one_loads<EXP>(A, A.p + blk * A.step, lds + L.bs_off + blk * 16, lds + L.d_off + blk * 32);
+        const Q45One o = q45_one_ints<T>(cur, r, kq);
         const float dw = half_to_float(cur.h.x), dmw = half_to_float(cur.h.x >> 16);
-        const float da = *(const float*)(lds + L.d_off + blk * 32);
-        const uint32_t rec = (ti * TS + ts) * nb + blk;
-        park_terms(park + rec * 64, parkm + rec * 16, lane, n, kq, dw * da, o.I0, o.I1, true, dmw * da, o.M);
+        park_terms(park + (ti * TS + ts) * pbytes, nb, blk, lane, dw * r.da, o.I0, o.I1, (dmw * r.da) * (float)o.M);
         if (DBG) {  // exact block integers: the eight classes
             const int32_t I = sum_xor32(sum_xor16(o.I0 + o.I1));
             const uint32_t row = tile * kTileRows + n;
@@ -1335,9 +1379,9 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(4))) voi
             const uint32_t q = it % (TS / 2), til = it / (TS / 2);
             const uint32_t t = blockIdx.x * TS + 2 * q + til * tstride;  // the gate tile, even
             if (t + 1 >= ntiles) continue;                                // (wave-uniform)
-            const uint32_t sg = (til * TS + 2 * q) * nb;
-            const float gs = exact_row_sum(park + sg * 64, parkm + sg * 16, nb, n, kq, true);
-            const float us = exact_row_sum(park + (sg + nb) * 64, parkm + (sg + nb) * 16, nb, n, kq, true);
+            const uint8_t* pg = park + (til * TS + 2 * q) * pbytes;
+            const float gs = exact_row_sum(pg, nb, lane);
+            const float us = exact_row_sum(pg + pbytes, nb, lane);
             if (kq != 0) continue;
             if (a.chk) {  // the gate and up outputs themselves (math.rs:167)
                 check_finite(a, kChkOut, gs);
@@ -1351,7 +1395,7 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(4))) voi
     for (uint32_t slot = wave; slot < tmax * TS; slot += W) {
         const uint32_t t = blockIdx.x * TS + slot % TS + (slot / TS) * tstride;
         if (t >= ntiles) continue;  // (wave-uniform)
-        const float v = exact_row_sum(park + slot * nb * 64, parkm + slot * nb * 16, nb, n, kq, true);
+        const float v = exact_row_sum(park + slot * pbytes, nb, lane);
         const uint32_t row = t * kTileRows + n;
         if (kq == 0 && row < a.rows) store_out(a, row, 0, v, best);
     }
@@ -1377,7 +1421,7 @@ __global__ __launch_bounds__(W * 64) __attribute__((amdgpu_waves_per_eu(4))) voi
 // barrier between tiles).  LDS after the Q8_K image: parked terms
 // [tmax][TS][nb], counters [tmax][TS], residuals [tmax][TS][16].
 __host__ __device__ inline uint32_t b1_lds_bytes(uint32_t cols, uint32_t tmax, uint32_t ts) {
-    return one_part_off(cols) + tmax * ts * (park_bytes(cols / 256) + 4u + 16u * 4u);
+    return one_part_off(cols, true) + tmax * ts * (park_bytes(cols / 256) + 4u + 16u * 4u);
 }
 
 // The RMSNorm scale (math.rs:210-221) from the values of the workgroup's own
@@ -1425,7 +1469,7 @@ __global__ __launch_bounds__(W * 64) void q45_mv_b1_kernel(MvArgs a) {
     constexpr int TS = W / KS;
     static_assert(!BAL || TS == 2 || TS == 4, "the balanced deal takes two or four tile slots");
     extern __shared__ __align__(16) uint8_t lds[];
-    const LdsMap L = lds_map_one(T, a.cols);
+    const LdsMap L = lds_map_one(T, a.cols, true);
     const uint32_t lane = threadIdx.x & 63, n = lane & 15, kq = lane >> 4;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t ts = wave / KS, kp = wave % KS;
@@ -1455,9 +1499,9 @@ __global__ __launch_bounds__(W * 64) void q45_mv_b1_kernel(MvArgs a) {
     const uint32_t nk = (uint32_t)KS < nb ? (uint32_t)KS : nb;  // waves of a tile that take blocks
     // LDS after the Q8_K image: parked terms [tmax * TS][nb] (park_terms),
     // counters [tmax * TS], residuals [tmax * TS][16]
-    float2* park = (float2*)(lds + one_part_off(a.cols));
-    float* parkm = (float*)(park + tmax * TS * nb * 64);
-    uint32_t* cnt = (uint32_t*)(parkm + tmax * TS * nb * 16);
+    uint8_t* park = lds + one_part_off(a.cols, true);
+    const uint32_t pbytes = park_bytes(nb);
+    uint32_t* cnt = (uint32_t*)(park + tmax * TS * pbytes);
     float* rs = (float*)(cnt + tmax * TS);
     for (uint32_t i = threadIdx.x; i < tmax * TS; i += W * 64) cnt[i] = 0;
     if (threadIdx.x < 16) *(uint4*)(lds + L.zero_off + threadIdx.x * 16) = make_uint4(0, 0, 0, 0);  // dead A lanes
@@ -1515,7 +1559,7 @@ __global__ __launch_bounds__(W * 64) void q45_mv_b1_kernel(MvArgs a) {
                 report_error(a.err_word, o.kind == kKindNonFinite ? quant_nonfinite_key(a, 0, xblk * 256ull + o.index)
                                                                   : quant_scale_key(a, 0, xblk));
         }
-        store_one_unit(lds, L, xblk, r16, q45_slots(o.q, r16 & 1), o.bsum);
+        store_one_unit(lds, L, xblk, r16, q45_slots(o.q, r16 & 1), o.bsum, true);
         if (r16 == 0) *(float*)(lds + L.d_off + xblk * 32) = o.d;
     }
     // the counters' zeros, every own block, the residuals and every wave's
@@ -1525,15 +1569,14 @@ __global__ __launch_bounds__(W * 64) void q45_mv_b1_kernel(MvArgs a) {
         return;
     }
 
-    const OneA A = one_a_operand(lds, L, n, kq);
+    const OneA A = one_a_operand(lds, L, n, kq, true);
     unsigned long long best = 0;
     uint32_t ti = 0, blk = kp, j = 0, tile = tile_of(0);
     auto compute = [&](const Q4Step<T>& cur) {
-        const Q45One o = q45_one_ints<T>(cur, A, A.p + blk * A.step, lds + L.bs_off + blk * 256, kq);
+        const OneLoads r = one_loads<true>(A, A.p + blk * A.step, lds + L.bs_off + blk * 16, lds + L.d_off + blk * 32);
+        const Q45One o = q45_one_ints<T>(cur, r, kq);
         const float dw = half_to_float(cur.h.x), dmw = half_to_float(cur.h.x >> 16);
-        const float da = *(const float*)(lds + L.d_off + blk * 32);
-        const uint32_t rec = (ti * TS + ts) * nb + blk;
-        park_terms(park + rec * 64, parkm + rec * 16, lane, n, kq, dw * da, o.I0, o.I1, true, dmw * da, o.M);
+        park_terms(park + (ti * TS + ts) * pbytes, nb, blk, lane, dw * r.da, o.I0, o.I1, (dmw * r.da) * (float)o.M);
         if (DBG) {  // exact block integers: the eight classes
             const int32_t I = sum_xor32(sum_xor16(o.I0 + o.I1));
             const uint32_t row = tile * kTileRows + n;
@@ -1562,13 +1605,13 @@ __global__ __launch_bounds__(W * 64) void q45_mv_b1_kernel(MvArgs a) {
     pipeline<D>(steps, buf, issue, compute);
 
     // the tiles this wave completed: each row's sum in the reference's order
+    // (every lane of the wave takes part; rows past the matrix and the other
+    // half of a half tile are not stored)
     for (uint32_t i = 0; i < my_tiles; ++i) {
         const uint32_t slot = i * TS + ts, row = tile_of(i) * kTileRows + n;
-        // (the mark is wave-uniform; the other conditions hold for the four
-        // lanes of a row alike)
-        if (cnt[slot] != nk + 1 + wave || row >= a.rows || !own_row(i)) continue;
-        float s = exact_row_sum(park + slot * nb * 64, parkm + slot * nb * 16, nb, n, kq, true);
-        if (kq != 0) continue;
+        if (cnt[slot] != nk + 1 + wave) continue;  // (wave-uniform)
+        float s = exact_row_sum(park + slot * pbytes, nb, lane);
+        if (kq != 0 || row >= a.rows || !own_row(i)) continue;
         if (FULL && a.chk) check_finite(a, kChkOut, s);
         if (FULL && a.resid) {
             s = rs[slot * 16 + n] + s;  // math.rs:203-208: hidden += projected
@@ -2432,19 +2475,19 @@ constexpr int kSmallW = 8, kSmallKS = 8, kSmallD = 2, kSmallWgPerCu = 2;
 // limit it has been given.
 template <int W, int KS>
 static hipError_t launch_parked(void (*kernel)(MvArgs), size_t& lds_set, const MvArgs& a, hipStream_t s,
-                                uint32_t pairs) {
+                                uint32_t pairs, bool exp) {
     constexpr int TS = W / KS;
     if (a.batch != 1) return hipErrorInvalidValue;
     const uint32_t want = (a.ntiles + TS - 1) / TS;
     const uint32_t gy = grid_rows(a, pairs);
     uint32_t grid = grid_cols(want, (uint32_t)kSmallWgPerCu * (uint32_t)device_cus(), gy);
     // enough workgroups that every one parks at most `room` tiles' terms
-    const size_t off = one_part_off(a.cols), per_tile = (size_t)TS * park_bytes(a.nb);
+    const size_t off = one_part_off(a.cols, exp), per_tile = (size_t)TS * park_bytes(a.nb);
     if (off >= kMaxLds || (kMaxLds - off) / per_tile == 0) return hipErrorInvalidValue;
     const uint64_t room = (kMaxLds - off) / per_tile, need = (a.ntiles + room * TS - 1) / (room * TS);
     if (grid < need) grid = (uint32_t)need;
     const uint32_t tstride = grid * TS, tmax = (a.ntiles + tstride - 1) / tstride;
-    const size_t lds = small_lds_bytes(a.cols, tmax, TS);
+    const size_t lds = small_lds_bytes(a.cols, tmax, TS, exp);
     if (lds > kMaxLds || (a.am_out && grid > kArgmaxMaxGrid)) return hipErrorInvalidValue;
     if (lds > lds_set) {
         const hipError_t e = hipFuncSetAttribute((const void*)kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
@@ -2456,10 +2499,15 @@ static hipError_t launch_parked(void (*kernel)(MvArgs), size_t& lds_set, const M
     return hipGetLastError();
 }
 
+// The expanded image where one tile's terms per slot fit beside it (K up
+// to about 16K), else the compact one.
 template <uint32_t T, int W, int KS, int D, bool DBG>
 static hipError_t launch_small(const MvArgs& a, hipStream_t s, uint32_t pairs) {
-    static size_t lds_set = 64 * 1024;
-    return launch_parked<W, KS>(q4k_mv_small_kernel<T, W, KS, D, DBG>, lds_set, a, s, pairs);
+    static size_t lds_exp = 64 * 1024, lds_cmp = 64 * 1024;
+    constexpr int TS = W / KS;
+    if (one_part_off(a.cols, true) + (size_t)TS * park_bytes(a.nb) <= kMaxLds)
+        return launch_parked<W, KS>(q4k_mv_small_kernel<T, W, KS, D, DBG, true>, lds_exp, a, s, pairs, true);
+    return launch_parked<W, KS>(q4k_mv_small_kernel<T, W, KS, D, DBG, false>, lds_cmp, a, s, pairs, false);
 }
 
 // The batch-1 kernel: grid as launch_parked (enough workgroups that the
@@ -2468,7 +2516,7 @@ template <int W, int KS>
 static void b1_grid(const MvArgs& a, uint32_t& grid, uint32_t& tmax) {
     constexpr int TS = W / KS;
     grid = grid_cols((a.ntiles + TS - 1) / TS, (uint32_t)kSmallWgPerCu * (uint32_t)device_cus(), 1);
-    const size_t off = one_part_off(a.cols), per_tile = (size_t)TS * (park_bytes(a.nb) + 4u + 64u);
+    const size_t off = one_part_off(a.cols, true), per_tile = (size_t)TS * (park_bytes(a.nb) + 4u + 64u);
     const uint64_t room = off < kMaxLds ? (kMaxLds - off) / per_tile : 0;
     if (room == 0) {
         grid = tmax = 0;
@@ -2675,17 +2723,21 @@ static hipError_t launch_q45(const MvArgs& a, uint32_t nbat, bool dbg, uint32_t 
     if (epilogue == kEpSiluPair)
         return dbg ? launch_small<T, kSmallW, kSmallW / 4, kSmallD, true>(a, s, pairs)
                    : launch_small<T, kSmallW, kSmallW / 4, kSmallD, false>(a, s, pairs);
+    // one column beyond the one-column kernels' LDS (the compact image and
+    // one tile's parked terms: about 46K columns) runs the batched kernel
+    // below, within the f32 tolerance instead of bit for bit
+    const bool one = nbat == 1 && one_part_off(a.cols, false) + (size_t)park_bytes(a.nb) <= kMaxLds;
     // two tile slots per workgroup (a K split of four): small matrices of at
     // most 4096 columns and 512 tiles (measured: 6144x4096 runs 1 us faster)
-    if (nbat == 1 && a.nb <= 16 && a.ntiles <= 512)
+    if (one && a.nb <= 16 && a.ntiles <= 512)
         return dbg ? launch_small<T, kSmallW, kSmallW / 2, kSmallD, true>(a, s, pairs)
                    : launch_small<T, kSmallW, kSmallW / 2, kSmallD, false>(a, s, pairs);
     // more than 16 blocks per row (4096x14336, the down projection): 16 waves
     // per workgroup, K split 16 ways (measured 10.4 us vs 10.7 us with 8)
-    if (nbat == 1 && a.nb > 16)
+    if (one && a.nb > 16)
         return dbg ? launch_small<T, 2 * kSmallW, 2 * kSmallKS, kSmallD, true>(a, s, pairs)
                    : launch_small<T, 2 * kSmallW, 2 * kSmallKS, kSmallD, false>(a, s, pairs);
-    if (nbat == 1)
+    if (one)
         return dbg ? launch_small<T, kSmallW, kSmallKS, kSmallD, true>(a, s, pairs)
                    : launch_small<T, kSmallW, kSmallKS, kSmallD, false>(a, s, pairs);
     // two to eight columns: the K-split MFMA kernel (14336x4096 batch 2:

@@ -195,6 +195,8 @@ def _oracle_sums(t, w, rows, act, nb):
     (DT.Q4_K, 4096, 14336, "batch-1 kernel, 16 waves, K split 16 (> 16 blocks)"),
     (DT.Q4_K, 333, 16384, "batch-1 kernel, K split 16 at 64 blocks: 4 blocks per wave, the most it takes"),
     (DT.Q4_K, 333, 18432, "72 blocks: the shared-quantization kernel, 16 waves, K split 16"),
+    (DT.Q4_K, 333, 28672, "112 blocks (a Llama-70B down projection): the compact activation image"),
+    (DT.Q5_K, 40, 32768, "Q5_K, 128 blocks: the compact activation image"),
     (DT.Q5_K, 4096, 4096, "Q5_K, batch-1 kernel, K split 4"),
     (DT.Q5_K, 4096, 14336, "Q5_K, batch-1 kernel, K split 16")])
 def test_block_sums_every_decode_variant(ctx, t, rows, cols, variant):
@@ -215,6 +217,23 @@ def test_block_sums_every_decode_variant(ctx, t, rows, cols, variant):
     want = O.matvec(int(t), w, rows, cols, x, threads=16)
     assert rel_l2(y.cpu().numpy(), want) <= REL_L2
     assert np.array_equal(bits(y.cpu().numpy()), bits(want))
+
+
+def test_one_column_beyond_the_one_column_kernels(ctx):
+    """One Q4_K column of 65536 values (256 blocks per row): the one-column
+    kernels' compact image and one tile's parked terms exceed the LDS, so the
+    batched kernel runs it: integers bitwise, outputs within the f32 bar."""
+    t, rows, cols = DT.Q4_K, 40, 65536
+    say("one column beyond the one-column kernels", t, rows, cols)
+    w = _packed(t, rows, cols, 77)
+    x = randn(78, cols)
+    W = rlq.Weights(ctx, t, w, rows, cols)
+    isum, imin, y = ctx.block_sums_ex(W, torch.from_numpy(x).cuda())
+    ctx.sync()
+    want_i, want_m = _oracle_sums(t, w, rows, O.quantize(O.Q8_K, x), cols // 256)
+    assert np.array_equal(isum.cpu().numpy(), want_i)
+    assert np.array_equal(imin.cpu().numpy(), want_m)
+    assert rel_l2(y.cpu().numpy(), O.matvec(int(t), w, rows, cols, x, threads=16)) <= REL_L2
 
 
 @pytest.mark.parametrize("t,rows,cols,batch", [
