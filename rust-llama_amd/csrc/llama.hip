@@ -57,10 +57,10 @@ __host__ __device__ inline uint32_t pv_waves_per_head(uint32_t G) { return G < k
 // (PvRec), and one 256-term f64 buffer per wave for the sequential repeats.
 // It does not grow with the context: the scores and values stream from HBM.
 struct PvRec {
-    double sum;     // the wave's tree sum of its lanes' segment sums
-    float wsum;     // sum over its lanes r of (lanes per head - 1 - r) |segment sum|
+    double sum;     // the wave's tree sum of its lanes' f64 sums
+    float wsum;     // sum over its column groups g of (groups - 1 - g) |f32 group sum|
     float abs_sum;  // sum |term|
-    float min_abs;  // smallest nonzero |term| (infinity: none)
+    float min_abs;  // smallest |term| (infinity: none)
     float pad;
 };
 constexpr uint32_t kPvRepTerms = 256;
@@ -225,18 +225,16 @@ __global__ __launch_bounds__(kAttnThreads) void attn_scores_kernel(
 // workgroup (blockIdx.x, blockIdx.y) = (dimensions 4 * blockIdx.x .., kv head).
 // Every workgroup of the kv head computes the G rows' softmax from the chunk
 // maxima.  The columns go in groups of four (the reference's SSE2 vectors);
-// the 64 wph lanes of a head's wph waves take contiguous runs of GL groups in
-// column order (lane r of part w: groups (64 w + r) GL ..).  Its first
-// kPvRegGroups groups' values are loaded when the kernel starts and their
-// exponentials kept from the row sums; later groups are reloaded and their
-// exponentials recomputed (the same f32 function of the same inputs), so the
-// LDS does not grow with the context.  The softmax totals are certified
-// against the reference's order (certified_f32).  Each P.V sum adds the
-// reference's f64 terms f64(p * v) column by column within a lane (the
-// reference's order inside the run) and the lanes' run sums in a fixed tree;
-// its f32 result is certified (pv_certified) or the sum is repeated in the
-// reference's column order.  Columns past `count` have exponential 0 and are
-// not added.
+// lane r of part w of a head's wph waves takes groups 64 w + r, + 64 wph, ...
+// Its first kPvRegGroups groups' values are loaded when the kernel starts and
+// their exponentials kept from the row sums; later groups are reloaded and
+// their exponentials recomputed (the same f32 function of the same inputs),
+// so the LDS does not grow with the context.  The softmax totals are
+// certified against the reference's order (certified_f32).  Each P.V sum adds
+// the reference's f64 terms f64(p * v) in another order (per lane, then the
+// 64 lanes in a fixed tree, then the head's waves in order); its f32 result
+// is certified (pv_certified) or the sum is repeated in the reference's
+// column order.  Columns past `count` have exponential 0 and are not added.
 __device__ __forceinline__ void exp_group(float4 x, uint32_t t, uint32_t count, float m, float (&e)[4]) {
     e[0] = t < count ? sse2_exp(x.x - m) : 0.0f;
     e[1] = t + 1 < count ? sse2_exp(x.y - m) : 0.0f;
@@ -244,26 +242,32 @@ __device__ __forceinline__ void exp_group(float4 x, uint32_t t, uint32_t count, 
     e[3] = t + 3 < count ? sse2_exp(x.w - m) : 0.0f;
 }
 
-// Whether the f32 rounding of a P.V sum added in the kernel's order (sum,
-// from terms with sum |term| = A, smallest nonzero |term| = M, over lanes of
-// runs of at most L columns whose run sums weigh wsum as in PvRec) is the
-// f32 rounding of the reference's sequential sum (math.rs:482-488):
+// Whether the f32 rounding of a P.V sum added in the kernel's order (sum; at
+// most tl columns per lane) is the f32 rounding of the reference's
+// sequential sum (math.rs:482-488).  A = sum |term|, M = min |term| (0 when
+// a term is zero), wsum = sum over the column groups g (four columns, in
+// column order, R of them) of (R - 1 - g) |group sum|, each group sum added
+// in f32 (within 4 2^-24 of its sum |term| of the exact one).
 //  - exactly: every term is an f32 value, a multiple of q = 2^(e(M) - 23);
 //    if A < 2^53 q, every partial sum in any order is a multiple of q below
 //    2^53 q, so every f64 addition is exact and all orders give the exact sum;
 //  - else by an interval: the reference's k-th partial sum rounds by at most
-//    2^-53 of itself, and its prefix P_k lies within |E_r| + A_r of zero (E_r
-//    the sum of the runs before run r, |E_r| <= sum of |runs| before it, A_r
-//    the run's sum |term|), so its sum is within 2^-53 (L sum_r |E_r| + L A)
-//    of the exact one; the kernel's within 2^-53 (L A + 16 A) (the runs
-//    and a tree of at most 13 levels).  When both ends of that interval round
-//    to one f32, so does the reference's sum.
-__device__ __forceinline__ bool pv_certified(double sum, double A, double wsum, float M, double L) {
-    if (!(M < INFINITY)) return true;  // no nonzero term: the sum is +0 in any order
-    int e;
-    frexpf(M, &e);  // M = f 2^e, f in [0.5, 1): q = 2^(e - 1 - 23)
-    if (A * (1.0 + 1e-3) < ldexp(1.0, e - 1 - 23 + 53)) return true;
-    const double B = 1.1102230246251565e-16 * 1.02 * (L * wsum * 1.001 + 2.0 * L * A * 1.001 + 16.0 * A * 1.001);
+//    2^-53 of itself, and its prefix P_k lies within |E_g| + A_g of zero (E_g
+//    the sum of the groups before column k's group g, |E_g| <= the sum of
+//    their |group sums|, A_g the group's sum |term|), so its sum is within
+//    2^-53 (4 wsum + 4 (4 2^-24 R + 1) A) of the exact one; the kernel's within
+//    2^-53 (tl A + 16 A) (each lane's columns, then a tree of at most 13
+//    levels).  When both ends of that interval round to one f32, so does the
+//    reference's sum.
+__device__ __forceinline__ bool pv_certified(double sum, double A, double wsum, float M, double tl, double R) {
+    if (!(M < INFINITY)) return true;  // no term
+    if (M > 0.0f) {
+        int e;
+        frexpf(M, &e);  // M = f 2^e, f in [0.5, 1): q = 2^(e - 1 - 23)
+        if (A * (1.0 + 1e-3) < ldexp(1.0, e - 1 - 23 + 53)) return true;
+    }
+    const double B =
+        1.1102230246251565e-16 * 1.02 * 1.001 * (4.0 * wsum + (4.0 * (4.0 * 5.9604644775390625e-8 * R + 1.0) + tl + 16.0) * A);
     return (float)(sum - B) == (float)(sum + B);
 }
 
@@ -292,10 +296,7 @@ __global__ __launch_bounds__(kPvThreads) void attn_pv_kernel(
     const uint32_t ngroups = (count + 3) / 4;
     const uint32_t wph = pv_waves_per_head(G), hstep = kPvWaves / wph;
     const bool active = wave < hstep * wph;  // wave-uniform
-    const uint32_t w = wave % wph, h0 = wave / wph;
-    // this lane's run of groups [gb, ge) in column order
-    const uint32_t LP = 64 * wph, li = 64 * w + lane, GL = (ngroups + LP - 1) / LP;
-    const uint32_t gb = li * GL < ngroups ? li * GL : ngroups, ge = gb + GL < ngroups ? gb + GL : ngroups;
+    const uint32_t w = wave % wph, h0 = wave / wph, gstride = 64 * wph, g0 = 64 * w + lane;
     const float4* vsrc = (const float4*)(vc + v_cache_index(kvh, hd, d0, 0, max_context));
     // the values of this lane's first groups (shared by every head of the kv
     // head) and the first head's scores of those groups, loaded before the
@@ -303,13 +304,13 @@ __global__ __launch_bounds__(kPvThreads) void attn_pv_kernel(
     float4 vr[kPvRegGroups][4], sr[kPvRegGroups];
 #pragma unroll
     for (uint32_t k = 0; k < kPvRegGroups; ++k) {
-        const uint32_t g = gb + k;
-        sr[k] = active && h0 < G && g < ge ? *(const float4*)(scores + (uint64_t)(kvh * G + h0) * row_stride + 4 * g)
-                                           : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        const uint32_t g = g0 + k * gstride;
+        sr[k] = active && h0 < G && g < ngroups ? *(const float4*)(scores + (uint64_t)(kvh * G + h0) * row_stride + 4 * g)
+                                                : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 #pragma unroll
         for (uint32_t j = 0; j < 4; ++j) {
             const uint32_t t = 4 * g + j;
-            vr[k][j] = active && g < ge && t < count ? vsrc[t] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            vr[k][j] = active && t < count ? vsrc[t] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         }
     }
     // the row maxima: one wave per head over its chunk maxima
@@ -331,16 +332,16 @@ __global__ __launch_bounds__(kPvThreads) void attn_pv_kernel(
             double sum = 0.0;
 #pragma unroll
             for (uint32_t k = 0; k < kPvRegGroups; ++k) {
-                const uint32_t g = gb + k;
+                const uint32_t g = g0 + k * gstride;
                 float e[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-                if (g < ge) exp_group(h == h0 ? sr[k] : *(const float4*)(srow + 4 * g), 4 * g, count, m, e);
+                if (g < ngroups) exp_group(h == h0 ? sr[k] : *(const float4*)(srow + 4 * g), 4 * g, count, m, e);
                 if (h == h0) {
 #pragma unroll
                     for (uint32_t j = 0; j < 4; ++j) er[k][j] = e[j];
                 }
                 sum += (double)((e[0] + e[1]) + (e[2] + e[3]));
             }
-            for (uint32_t g = gb + kPvRegGroups; g < ge; ++g) {
+            for (uint32_t g = g0 + kPvRegGroups * gstride; g < ngroups; g += gstride) {
                 float e[4];
                 exp_group(*(const float4*)(srow + 4 * g), 4 * g, count, m, e);
                 sum += (double)((e[0] + e[1]) + (e[2] + e[3]));
@@ -377,32 +378,39 @@ __global__ __launch_bounds__(kPvThreads) void attn_pv_kernel(
     }
     __syncthreads();
     // P.V with p = e * inverse (math.rs:313-315, 478-480), one f64 chain per
-    // dimension over the lane's run in column order, and the certificate's
-    // statistics of the terms
+    // dimension over the lane's groups, and the certificate's statistics of
+    // the terms (pv_certified)
     if (active) {
         for (uint32_t h = h0; h < G; h += hstep) {
             const float m = stat[2 * h], inv = stat[2 * h + 1];
             const float* srow = scores + (uint64_t)(kvh * G + h) * row_stride;
             double a[4] = {0.0, 0.0, 0.0, 0.0};
-            float as[4] = {0.0f, 0.0f, 0.0f, 0.0f}, mn[4] = {INFINITY, INFINITY, INFINITY, INFINITY};
-            auto add = [&](const float (&e)[4], const float4 (&v)[4], uint32_t t0) {
+            float as[4] = {0.0f, 0.0f, 0.0f, 0.0f}, ws[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+            float mn[4] = {INFINITY, INFINITY, INFINITY, INFINITY};
+            auto add = [&](const float (&e)[4], const float4 (&v)[4], uint32_t g) {
+                const uint32_t nt = count - 4 * g < 4 ? count - 4 * g : 4;  // the reference adds `count` columns
+                float gs[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
                 for (uint32_t j = 0; j < 4; ++j) {
-                    if (t0 + j >= count) break;  // the reference adds the `count` columns only
+                    if (j >= nt) break;
                     const float p = e[j] * inv;
                     const float t[4] = {p * v[j].x, p * v[j].y, p * v[j].z, p * v[j].w};
 #pragma unroll
                     for (uint32_t d = 0; d < 4; ++d) {
                         a[d] += (double)t[d];
+                        gs[d] += t[d];
                         as[d] += fabsf(t[d]);
-                        mn[d] = t[d] != 0.0f ? fminf(mn[d], fabsf(t[d])) : mn[d];
+                        mn[d] = fminf(mn[d], fabsf(t[d]));
                     }
                 }
+                const float wg = (float)(ngroups - 1 - g);
+#pragma unroll
+                for (uint32_t d = 0; d < 4; ++d) ws[d] = __builtin_fmaf(wg, fabsf(gs[d]), ws[d]);
             };
 #pragma unroll
             for (uint32_t k = 0; k < kPvRegGroups; ++k) {
-                const uint32_t g = gb + k;
-                if (g >= ge) break;
+                const uint32_t g = g0 + k * gstride;
+                if (g >= ngroups) break;
                 float e[4];
                 if (h == h0) {
 #pragma unroll
@@ -410,33 +418,32 @@ __global__ __launch_bounds__(kPvThreads) void attn_pv_kernel(
                 } else {
                     exp_group(*(const float4*)(srow + 4 * g), 4 * g, count, m, e);
                 }
-                add(e, vr[k], 4 * g);
+                add(e, vr[k], g);
             }
-            for (uint32_t g = gb + kPvRegGroups; g < ge; ++g) {
+            for (uint32_t g = g0 + kPvRegGroups * gstride; g < ngroups; g += gstride) {
                 float e[4];
                 exp_group(*(const float4*)(srow + 4 * g), 4 * g, count, m, e);
                 float4 v[4];
 #pragma unroll
                 for (uint32_t j = 0; j < 4; ++j)
                     v[j] = 4 * g + j < count ? vsrc[4 * g + j] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-                add(e, v, 4 * g);
+                add(e, v, g);
             }
-            const float wgt = (float)(LP - 1 - li);
 #pragma unroll
             for (uint32_t d = 0; d < 4; ++d) {
                 const double sum = wave_sum_f64(a[d]);
-                const float ws = wave_sum(wgt * fabsf((float)a[d]));
+                const float wsum = wave_sum(ws[d]);
                 const float ab = wave_sum(as[d]);
                 const float mi = wave_min_dpp(mn[d]);
-                if (lane == 0) rec[(h * wph + w) * 4 + d] = PvRec{sum, ws, ab, mi, 0.0f};
+                if (lane == 0) rec[(h * wph + w) * 4 + d] = PvRec{sum, wsum, ab, mi, 0.0f};
             }
         }
     }
     __syncthreads();
     // each output: certified, or repeated in the reference's column order by
-    // one wave (kPvRepTerms terms per round through its LDS buffer, added by
-    // lane 0)
-    const double L = 4.0 * GL;
+    // one wave: its lanes compute kPvRepTerms terms per round into its LDS
+    // buffer, and lane 0 adds them in order, sixteen loads ahead of its adds
+    const double tl = 4.0 * ((ngroups + gstride - 1) / gstride);  // columns per lane
     for (uint32_t o = wave; o < G * 4; o += kPvWaves) {  // (wave-uniform)
         const uint32_t h = o / 4, j = o % 4;
         double sum = 0.0, A = 0.0, ws = 0.0;
@@ -449,7 +456,7 @@ __global__ __launch_bounds__(kPvThreads) void attn_pv_kernel(
             M = fminf(M, r.min_abs);
         }
         float res = (float)sum;
-        if (repeat_all || !pv_certified(sum, A, ws, M, L)) {
+        if (repeat_all || !pv_certified(sum, A, ws, M, tl, (double)ngroups)) {
             const float m = stat[2 * h], inv = stat[2 * h + 1];
             const float* srow = scores + (uint64_t)(kvh * G + h) * row_stride;
             const float* vcol = vc + v_cache_index(kvh, hd, d0 + j, 0, max_context);
@@ -469,7 +476,15 @@ __global__ __launch_bounds__(kPvThreads) void attn_pv_kernel(
                 // one wave's LDS operations are performed in order
                 if (lane == 0) {
                     const uint32_t nt = count - 4 * base < kPvRepTerms ? count - 4 * base : kPvRepTerms;
-                    for (uint32_t i = 0; i < nt; ++i) seq += buf[i];
+                    uint32_t i = 0;
+                    for (; i + 16 <= nt; i += 16) {
+                        double x[16];
+#pragma unroll
+                        for (uint32_t k = 0; k < 16; ++k) x[k] = buf[i + k];
+#pragma unroll
+                        for (uint32_t k = 0; k < 16; ++k) seq += x[k];
+                    }
+                    for (; i < nt; ++i) seq += buf[i];
                 }
             }
             res = (float)__shfl(seq, 0, 64);
