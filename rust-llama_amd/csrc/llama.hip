@@ -53,12 +53,13 @@ __host__ __device__ inline uint64_t v_cache_index(uint32_t kvh, uint32_t hd, uin
 __host__ __device__ inline uint32_t pv_waves_per_head(uint32_t G) { return G < kPvWaves ? kPvWaves / G : 1u; }
 
 // LDS of attn_pv_kernel, in floats: max and inverse [G][2], the f64 partial
-// row sums [G][waves per head], the P.V records [G][waves per head][4]
-// (PvRec), and one 256-term f64 buffer per wave for the sequential repeats.
+// row sums [G][waves per head], the P.V records [G][waves per head][4
+// dimensions][4 lane rows] (PvRec), and one 256-term f64 buffer per wave for
+// the sequential repeats.
 // It does not grow with the context: the scores and values stream from HBM.
 struct PvRec {
-    double sum;     // the wave's tree sum of its lanes' f64 sums
-    float wsum;     // sum over its column groups g of (groups - 1 - g) |f32 group sum|
+    double sum;     // the 16 lanes' tree sum of their f64 sums
+    float wsum;     // sum over their column groups g of (groups - 1 - g) |group sum|
     float abs_sum;  // sum |term|
     float min_abs;  // smallest |term| (infinity: none)
     float pad;
@@ -72,7 +73,7 @@ __host__ __device__ inline AttnPvLds attn_pv_lds(uint32_t G) {
     const uint32_t wph = pv_waves_per_head(G);
     l.rsum = (2 * G + 1) & ~1u;
     l.part = l.rsum + 2 * G * wph;
-    l.rep = l.part + (uint32_t)(sizeof(PvRec) / 4) * 4 * G * wph;
+    l.rep = l.part + (uint32_t)(sizeof(PvRec) / 4) * 16 * G * wph;
     l.total = l.rep + 2 * kPvRepTerms * kPvWaves;
     return l;
 }
@@ -231,8 +232,8 @@ __global__ __launch_bounds__(kAttnThreads) void attn_scores_kernel(
 // their exponentials recomputed (the same f32 function of the same inputs),
 // so the LDS does not grow with the context.  The softmax totals are
 // certified against the reference's order (certified_f32).  Each P.V sum adds
-// the reference's f64 terms f64(p * v) in another order (per lane, then the
-// 64 lanes in a fixed tree, then the head's waves in order); its f32 result
+// the reference's f64 terms f64(p * v) in another order (per lane, then each
+// 16-lane row in a fixed tree, then the head's rows in order); its f32 result
 // is certified (pv_certified) or the sum is repeated in the reference's
 // column order.  Columns past `count` have exponential 0 and are not added.
 __device__ __forceinline__ void exp_group(float4 x, uint32_t t, uint32_t count, float m, float (&e)[4]) {
@@ -246,8 +247,9 @@ __device__ __forceinline__ void exp_group(float4 x, uint32_t t, uint32_t count, 
 // most tl columns per lane) is the f32 rounding of the reference's
 // sequential sum (math.rs:482-488).  A = sum |term|, M = min |term| (0 when
 // a term is zero), wsum = sum over the column groups g (four columns, in
-// column order, R of them) of (R - 1 - g) |group sum|, each group sum added
-// in f32 (within 4 2^-24 of its sum |term| of the exact one).
+// column order, R of them) of (R - 1 - g) |group sum|, each group sum the
+// growth of a lane's f64 sum rounded to f32 (within 2^-23 of itself plus
+// 4 2^-53 A of the exact one).
 //  - exactly: every term is an f32 value, a multiple of q = 2^(e(M) - 23);
 //    if A < 2^53 q, every partial sum in any order is a multiple of q below
 //    2^53 q, so every f64 addition is exact and all orders give the exact sum;
@@ -255,10 +257,10 @@ __device__ __forceinline__ void exp_group(float4 x, uint32_t t, uint32_t count, 
 //    2^-53 of itself, and its prefix P_k lies within |E_g| + A_g of zero (E_g
 //    the sum of the groups before column k's group g, |E_g| <= the sum of
 //    their |group sums|, A_g the group's sum |term|), so its sum is within
-//    2^-53 (4 wsum + 4 (4 2^-24 R + 1) A) of the exact one; the kernel's within
-//    2^-53 (tl A + 16 A) (each lane's columns, then a tree of at most 13
-//    levels).  When both ends of that interval round to one f32, so does the
-//    reference's sum.
+//    2^-53 (4 wsum 1.001 + 4 (4 2^-53 R^2 + 1) A) of the exact one; the kernel's within
+//    2^-53 (tl A + 40 A) (each lane's columns, its 16-lane row in a tree of
+//    4 levels, then at most 32 row sums in order).  When both ends of that
+//    interval round to one f32, so does the reference's sum.
 __device__ __forceinline__ bool pv_certified(double sum, double A, double wsum, float M, double tl, double R) {
     if (!(M < INFINITY)) return true;  // no term
     if (M > 0.0f) {
@@ -267,17 +269,22 @@ __device__ __forceinline__ bool pv_certified(double sum, double A, double wsum, 
         if (A * (1.0 + 1e-3) < ldexp(1.0, e - 1 - 23 + 53)) return true;
     }
     const double B =
-        1.1102230246251565e-16 * 1.02 * 1.001 * (4.0 * wsum + (4.0 * (4.0 * 5.9604644775390625e-8 * R + 1.0) + tl + 16.0) * A);
+        1.1102230246251565e-16 * 1.02 * 1.001 * (4.0 * wsum + (4.0 * (4.0 * 1.1102230246251565e-16 * R * R + 1.0) + tl + 40.0) * A);
     return (float)(sum - B) == (float)(sum + B);
 }
 
-__device__ __forceinline__ float wave_min_dpp(float v) {
+// Sum / minimum over each 16-lane row (DPP only).
+__device__ __forceinline__ float row16_sum_f(float v) {
+    v += dpp_f<kQuadXor1>(v);
+    v += dpp_f<kQuadXor2>(v);
+    v += dpp_f<kRowHalfMirror>(v);
+    return v + dpp_f<kRowRor8>(v);
+}
+__device__ __forceinline__ float row16_min_f(float v) {
     v = fminf(v, dpp_f<kQuadXor1>(v));
     v = fminf(v, dpp_f<kQuadXor2>(v));
     v = fminf(v, dpp_f<kRowHalfMirror>(v));
-    v = fminf(v, dpp_f<kRowRor8>(v));
-    v = fminf(v, __shfl_xor(v, 16, 64));
-    return fminf(v, __shfl_xor(v, 32, 64));
+    return fminf(v, dpp_f<kRowRor8>(v));
 }
 
 __global__ __launch_bounds__(kPvThreads) void attn_pv_kernel(
@@ -389,7 +396,9 @@ __global__ __launch_bounds__(kPvThreads) void attn_pv_kernel(
             float mn[4] = {INFINITY, INFINITY, INFINITY, INFINITY};
             auto add = [&](const float (&e)[4], const float4 (&v)[4], uint32_t g) {
                 const uint32_t nt = count - 4 * g < 4 ? count - 4 * g : 4;  // the reference adds `count` columns
-                float gs[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+                double a0[4];
+#pragma unroll
+                for (uint32_t d = 0; d < 4; ++d) a0[d] = a[d];
 #pragma unroll
                 for (uint32_t j = 0; j < 4; ++j) {
                     if (j >= nt) break;
@@ -398,14 +407,14 @@ __global__ __launch_bounds__(kPvThreads) void attn_pv_kernel(
 #pragma unroll
                     for (uint32_t d = 0; d < 4; ++d) {
                         a[d] += (double)t[d];
-                        gs[d] += t[d];
                         as[d] += fabsf(t[d]);
                         mn[d] = fminf(mn[d], fabsf(t[d]));
                     }
                 }
+                // the group's sum as the lane sum's growth (within 4 2^-53 A of it)
                 const float wg = (float)(ngroups - 1 - g);
 #pragma unroll
-                for (uint32_t d = 0; d < 4; ++d) ws[d] = __builtin_fmaf(wg, fabsf(gs[d]), ws[d]);
+                for (uint32_t d = 0; d < 4; ++d) ws[d] = __builtin_fmaf(wg, fabsf((float)(a[d] - a0[d])), ws[d]);
             };
 #pragma unroll
             for (uint32_t k = 0; k < kPvRegGroups; ++k) {
@@ -429,13 +438,14 @@ __global__ __launch_bounds__(kPvThreads) void attn_pv_kernel(
                     v[j] = 4 * g + j < count ? vsrc[4 * g + j] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
                 add(e, v, g);
             }
+            // per 16-lane row (DPP); the rows meet in the final pass
 #pragma unroll
             for (uint32_t d = 0; d < 4; ++d) {
-                const double sum = wave_sum_f64(a[d]);
-                const float wsum = wave_sum(ws[d]);
-                const float ab = wave_sum(as[d]);
-                const float mi = wave_min_dpp(mn[d]);
-                if (lane == 0) rec[(h * wph + w) * 4 + d] = PvRec{sum, wsum, ab, mi, 0.0f};
+                const double sum = row16_sum_f64(a[d]);
+                const float wsum = row16_sum_f(ws[d]);
+                const float ab = row16_sum_f(as[d]);
+                const float mi = row16_min_f(mn[d]);
+                if ((lane & 15) == 0) rec[((h * wph + w) * 4 + d) * 4 + (lane >> 4)] = PvRec{sum, wsum, ab, mi, 0.0f};
             }
         }
     }
@@ -448,8 +458,8 @@ __global__ __launch_bounds__(kPvThreads) void attn_pv_kernel(
         const uint32_t h = o / 4, j = o % 4;
         double sum = 0.0, A = 0.0, ws = 0.0;
         float M = INFINITY;
-        for (uint32_t v = 0; v < wph; ++v) {
-            const PvRec r = rec[(h * wph + v) * 4 + j];
+        for (uint32_t v = 0; v < 4 * wph; ++v) {  // (wave part, row) in order
+            const PvRec r = rec[((h * wph + v / 4) * 4 + j) * 4 + v % 4];
             sum += r.sum;
             A += (double)r.abs_sum;
             ws += (double)r.wsum;
