@@ -43,6 +43,7 @@ Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--extra] [--no-cpu] 
                        [--no-llama] [--no-configs] [--llama-steps N] [--no-llama-cpu]
 """
 import argparse
+import ctypes
 import json
 import os
 import sys
@@ -155,10 +156,14 @@ def call_distribution(rlq, ctx, handles, x, y, calls):
             "p90_us": round(float(us[int(0.9 * (calls - 1))]), 3)}
 
 
-def practical_peaks(torch, reps=20):
+def practical_peaks(torch, rlq=None, reps=20):
     """Measured ceilings beside the spec peaks: a 1 GiB device-to-device copy
-    (bytes read + written per second), and torch's (hipBLASLt) dense f16 and
-    int8 GEMMs at 8192^3 and at the prefill shape 512x4096x14336."""
+    (bytes read + written per second), torch's (hipBLASLt) dense f16 and int8
+    GEMMs at 8192^3 and at the prefill shape 512x4096x14336, and the library's
+    probes: chained MFMAs from registers (v_mfma_i32_32x32x32_i8 and
+    v_mfma_f32_32x32x16_f16) and a plain read of the headline's weight bytes
+    with the one-column matvec's launch shape and loads, over the same 10
+    rotated copies (rlq_probe_mfma, rlq_probe_stream)."""
     out = {}
 
     def timed(fn):
@@ -204,7 +209,60 @@ def practical_peaks(torch, reps=20):
     except (RuntimeError, AttributeError) as e:
         out["int8_gemm_prefill_shape_tops"] = None
         out["int8_prefill_note"] = str(e).splitlines()[0][:120]
+    if rlq is not None:
+        out.update(probe_peaks(rlq, torch, reps))
     torch.cuda.empty_cache()
+    return out
+
+
+def probe_peaks(rlq, torch, reps):
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    stream = torch.cuda.current_stream()
+    sp = ctypes.c_void_p(stream.cuda_stream)
+    out = {}
+    wgs, iters = 4 * cus, 4000
+    sink = torch.zeros(16 * max(wgs, cus), dtype=torch.int32, device="cuda")
+    for kind, key, per in ((0, "mfma_i8_32x32x32_tops", 2 * 32 * 32 * 32), (1, "mfma_f16_32x32x16_tflops", 2 * 32 * 32 * 16)):
+        def launch():
+            rc = rlq._lib.rlq_probe_mfma(kind, wgs, iters, ctypes.c_void_p(sink.data_ptr()), sp)
+            if rc != 0:
+                raise RuntimeError(f"rlq_probe_mfma: {rc}")
+        launch()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        for _ in range(reps):
+            launch()
+        b.record(stream)
+        torch.cuda.synchronize()
+        s = a.elapsed_time(b) / reps * 1e-3
+        out[key] = round(wgs * 4 * 4 * iters * per / s / 1e12, 1)
+    # the headline's bytes (Q4_K 14336x4096: 33,030,144 B) in 10 rotated copies
+    nbytes, copies = 14336 * 2304, ROTATE
+    bufs = [torch.empty(nbytes, dtype=torch.uint8, device="cuda") for _ in range(copies)]
+
+    def read(i):
+        rc = rlq._lib.rlq_probe_stream(ctypes.c_void_p(bufs[i % copies].data_ptr()), nbytes, cus,
+                                       ctypes.c_void_p(sink.data_ptr()), sp)
+        if rc != 0:
+            raise RuntimeError(f"rlq_probe_stream: {rc}")
+
+    for i in range(50):
+        read(i)
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    n = 2000
+    a.record(stream)
+    for i in range(n):
+        read(i)
+    b.record(stream)
+    torch.cuda.synchronize()
+    us = a.elapsed_time(b) / n * 1e3
+    out["stream_floor"] = {"bytes": nbytes, "us_per_pass": round(us, 3), "gbs": round(nbytes / us / 1e3, 1),
+                           "note": "33,030,144 weight bytes read with the one-column matvec's grid (one workgroup "
+                                   "of 16 waves per CU) and 1 KB non-temporal load runs, 10 rotated copies, "
+                                   "launched back to back"}
+    del bufs
     return out
 
 
@@ -492,13 +550,23 @@ def decode_step(rlq, ctx, steps, warmup, cpu=False):
             setattr(oc, k, v)
         oc.attention_scale, oc.weight_type, oc.output_type, oc.embedding_type = 0.0, 12, 14, 12
         orc = oracle.LlamaOracle(oc, host_tensors, threads=1)
-        x = orc.embedding(toks[0])
+        # the same work as a GPU step: a context of ~1000 rows (the cache
+        # filled with N(0, 1) rows; attention reads every row the step sees)
+        pos = int(round(mean_ctx)) - 1
+        crng = np.random.default_rng(6)
+        orc.k_cache[:, :pos] = crng.standard_normal((orc.k_cache.shape[0], pos, orc.k_cache.shape[2]),
+                                                    dtype=np.float32)
+        orc.v_cache[:, :pos] = crng.standard_normal((orc.v_cache.shape[0], pos, orc.v_cache.shape[2]),
+                                                    dtype=np.float32)
+        orc.cached = pos
+        x = orc.embedding(toks[pos])
         t1 = time.perf_counter()
-        orc.step(x, 0)
+        orc.step(x, pos)
         el = time.perf_counter() - t1
         out["cpu_baseline"] = {"value": round(1.0 / el, 4), "unit": "tok/s", "cores": 1, "kind": "port",
-                               "sample": f"one decode step at context 1 (the oracle's scalar restatement, "
-                                         f"1 thread): {el:.2f} s", "host": host_cpu()}
+                               "sample": f"one decode step at context {pos + 1} (the oracle's scalar restatement, "
+                                         f"1 thread; the KV cache pre-filled with N(0,1) rows): {el:.2f} s",
+                               "host": host_cpu()}
     model.close()
     torch.cuda.empty_cache()
     return out
@@ -566,7 +634,7 @@ def main():
                       "gbs": round(head["bytes_per_step"] / (warm_ms * 1e-3) / 1e9, 2),
                       "note": "the same call on one weight copy (cache-resident); the headline rotates 10 copies"}
     result["prefill"] = prefill(rlq, ctx, handles, rows, cols, max(50, args.steps // 10), max(5, args.warmup // 5))
-    result["practical_peaks"] = practical_peaks(torch)
+    result["practical_peaks"] = practical_peaks(torch, rlq)
     if not args.no_cpu:
         xh = x.cpu().numpy().reshape(-1)
         result["cpu_baseline"] = cpu_baseline(DT.Q4_K, host0, rows, cols, xh)

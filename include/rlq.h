@@ -491,6 +491,21 @@ int32_t rlq_gguf_write_header(const rlq_gguf_kv *kv, uint64_t n_kv, const rlq_gg
 int32_t rlq_gguf_write(const char *path, const rlq_gguf_kv *kv, uint64_t n_kv, const rlq_gguf_tensor *tensors,
                        uint64_t n_tensors, rlq_error *err);
 
+/* ---- measurement probes ------------------------------------------------
+ * No counterpart in the reference: kernels that measure this GPU's practical
+ * ceilings for the benchmark, next to the spec peaks.  Both are asynchronous
+ * on `stream` and write one word per wave to `out` (4 words per workgroup
+ * for rlq_probe_mfma, 16 for rlq_probe_stream) so that no work is dead. */
+/* kind 0: v_mfma_i32_32x32x32_i8, kind 1: v_mfma_f32_32x32x16_f16; each of
+ * the 4 waves of `workgroups` 256-thread workgroups runs 4 independent
+ * accumulator chains of `iters` MFMAs from registers. */
+int32_t rlq_probe_mfma(uint32_t kind, uint32_t workgroups, uint32_t iters, uint32_t *out, void *stream);
+/* A read of `len` device bytes (a multiple of 1024, 16-byte aligned) by
+ * `workgroups` workgroups of 16 waves, each wave instruction a 1 KB run of
+ * 16-byte non-temporal loads: the one-column matvec's launch shape and load
+ * pattern without its arithmetic. */
+int32_t rlq_probe_stream(const void *bytes, uint64_t len, uint32_t workgroups, uint32_t *out, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -189,6 +189,8 @@ SIGNATURES = {
     "rlq_llama_step": ([_P, _P, _U64, _P, _P, _P, _P, _E], _I32),
     "rlq_llama_intermediates": ([_P, _P, _P, _P, _P, _P, _E], _I32),
     "rlq_llama_trace": ([_P, _P, _E], _I32),
+    "rlq_probe_mfma": ([_U32, _U32, _U32, _P, _P], _I32),
+    "rlq_probe_stream": ([_P, _U64, _U32, _P, _P], _I32),
 }
 
 

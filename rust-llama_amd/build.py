@@ -16,7 +16,7 @@ import sys
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
-SOURCES = ["api.hip", "gemm.hip", "llama.hip", "matvec.hip", "quantize.hip"]
+SOURCES = ["api.hip", "gemm.hip", "llama.hip", "matvec.hip", "probe.hip", "quantize.hip"]
 HOST_SOURCES = ["gguf.cpp"]  # host-only C++ (no device code), built with g++
 CXX = os.environ.get("CXX", "g++")
 LIB = os.path.join(HERE, "librlq.so")

@@ -1,0 +1,92 @@
+// probe.hip - measurement probes, the practical ceilings reported next to the
+// MI355X spec peaks (bench.py practical_peaks):
+//  - rlq_probe_mfma: chained MFMAs from registers, no memory traffic:
+//    v_mfma_i32_32x32x32_i8 (the int8 peak the prefill target is quoted on)
+//    and v_mfma_f32_32x32x16_f16 (the instruction the prefill GEMM issues);
+//  - rlq_probe_stream: a plain read of a buffer with the one-column matvec's
+//    launch shape (one workgroup of 16 waves per CU) and load pattern (each
+//    wave instruction a 1 KB run of 16-byte non-temporal loads), XORed and
+//    never written back: the time a pass over the matvec's bytes takes with
+//    no arithmetic.
+#include "rlq_device.hpp"
+#include "rlq.h"
+#include "rlq_internal.hpp"
+
+namespace rlq {
+
+typedef int32_t p_i32x4 __attribute__((ext_vector_type(4)));
+typedef int32_t p_i32x16 __attribute__((ext_vector_type(16)));
+typedef float p_f32x16 __attribute__((ext_vector_type(16)));
+typedef _Float16 p_f16x8 __attribute__((ext_vector_type(8)));
+
+// Four independent accumulator chains per wave, `iters` MFMAs each; every
+// wave stores one word of its accumulators so nothing is left dead.
+template <int KIND>
+__global__ __launch_bounds__(256) void mfma_probe_kernel(uint32_t iters, uint32_t* out) {
+    const uint32_t lane = threadIdx.x & 63, gw = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if constexpr (KIND == 0) {
+        const p_i32x4 a = {(int)(lane * 0x01010101u), 3, 5, 7}, b = {11, (int)lane, 13, 17};
+        p_i32x16 c0 = {}, c1 = {}, c2 = {}, c3 = {};
+        for (uint32_t i = 0; i < iters; ++i) {
+            c0 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c0, 0, 0, 0);
+            c1 = __builtin_amdgcn_mfma_i32_32x32x32_i8(b, a, c1, 0, 0, 0);
+            c2 = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, a, c2, 0, 0, 0);
+            c3 = __builtin_amdgcn_mfma_i32_32x32x32_i8(b, b, c3, 0, 0, 0);
+        }
+        if (lane == 0) out[gw] = (uint32_t)(c0[0] ^ c1[1] ^ c2[2] ^ c3[3]);
+    } else {
+        p_f16x8 a, b;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) a[k] = (_Float16)(lane + k), b[k] = (_Float16)(k - 3);
+        p_f32x16 c0 = {}, c1 = {}, c2 = {}, c3 = {};
+        for (uint32_t i = 0; i < iters; ++i) {
+            c0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c0, 0, 0, 0);
+            c1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(b, a, c1, 0, 0, 0);
+            c2 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, a, c2, 0, 0, 0);
+            c3 = __builtin_amdgcn_mfma_f32_32x32x16_f16(b, b, c3, 0, 0, 0);
+        }
+        if (lane == 0) out[gw] = __float_as_uint(c0[0] + c1[1] + c2[2] + c3[3]);
+    }
+}
+
+// Workgroup g of `grid` reads its equal share of the n16 16-byte units: wave
+// w's 1 KB runs w, w + 16, ... of the share, two runs in flight per wave.
+__global__ __launch_bounds__(1024) void stream_probe_kernel(const uint8_t* p, uint64_t n16, uint32_t* out) {
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint64_t runs = n16 / 64, per = (runs + gridDim.x - 1) / gridDim.x;
+    const uint64_t r0 = (uint64_t)blockIdx.x * per, r1 = r0 + per < runs ? r0 + per : runs;
+    uint32_t x = 0;
+    uint64_t r = r0 + wave;
+    for (; r + 16 < r1; r += 32) {
+        const uint4 v0 = load_stream16(p + (r * 64 + lane) * 16);
+        const uint4 v1 = load_stream16(p + ((r + 16) * 64 + lane) * 16);
+        x ^= v0.x ^ v0.y ^ v0.z ^ v0.w ^ v1.x ^ v1.y ^ v1.z ^ v1.w;
+    }
+    if (r < r1) {
+        const uint4 v = load_stream16(p + (r * 64 + lane) * 16);
+        x ^= v.x ^ v.y ^ v.z ^ v.w;
+    }
+    x ^= (uint32_t)__shfl_xor((int)x, 32, 64);
+    if (lane == 0) out[blockIdx.x * 16 + wave] = x;
+}
+
+}  // namespace rlq
+
+using namespace rlq;
+
+extern "C" int32_t rlq_probe_mfma(uint32_t kind, uint32_t workgroups, uint32_t iters, uint32_t* out, void* stream) {
+    if (kind > 1 || workgroups == 0 || !out) return RLQ_INVALID_ARGUMENT;
+    if (kind == 0)
+        hipLaunchKernelGGL(mfma_probe_kernel<0>, dim3(workgroups), dim3(256), 0, (hipStream_t)stream, iters, out);
+    else
+        hipLaunchKernelGGL(mfma_probe_kernel<1>, dim3(workgroups), dim3(256), 0, (hipStream_t)stream, iters, out);
+    return hipGetLastError() == hipSuccess ? RLQ_OK : RLQ_DEVICE_ERROR;
+}
+
+extern "C" int32_t rlq_probe_stream(const void* bytes, uint64_t len, uint32_t workgroups, uint32_t* out,
+                                    void* stream) {
+    if (!bytes || !out || workgroups == 0 || len % 1024 != 0 || ((uintptr_t)bytes & 15)) return RLQ_INVALID_ARGUMENT;
+    hipLaunchKernelGGL(stream_probe_kernel, dim3(workgroups), dim3(1024), 0, (hipStream_t)stream,
+                       (const uint8_t*)bytes, len / 16, out);
+    return hipGetLastError() == hipSuccess ? RLQ_OK : RLQ_DEVICE_ERROR;
+}

@@ -380,6 +380,28 @@ def test_q6k_lm_head_128256x4096_argmax(ctx):
             assert int(am[0]) == O.argmax(want[0])
 
 
+def test_q8_0_qwen_ffn_up_4864x896(ctx):
+    """The Qwen2.5-0.5B FFN-up shape at batch 1 (the benchmark's Q8_0
+    configuration, 304 tiles): the library's encoder equals the oracle's on
+    sampled rows, and the outputs are bitwise the oracle's (the reference's
+    block-order f32 sum), for N(0, 1) input and a few edge columns."""
+    rows, cols = 4864, 896
+    say("Q8_0 FFN up", rows, cols)
+    xw = randn(0x51A7E001, rows * cols, 0.02)
+    w = rlq.quantize(DT.Q8_0, xw)
+    stride = w.size // rows
+    for r in (0, 1, 2431, rows - 1):
+        assert np.array_equal(w[r * stride:(r + 1) * stride], O.quantize(O.Q8_0, xw[r * cols:(r + 1) * cols])), r
+    W = rlq.Weights(ctx, DT.Q8_0, w, rows, cols)
+    cases = [randn(0x51A7E101, cols), np.zeros(cols, np.float32), np.full(cols, 1e-6, np.float32),
+             (randn(0x51A7E102, cols) * np.float32(1e4)).astype(np.float32)]
+    for k, x in enumerate(cases):
+        y = ctx.matmul(W, torch.from_numpy(x.reshape(1, cols)).cuda())
+        ctx.sync()
+        want = O.matvec(O.Q8_0, w, rows, cols, x, threads=16)
+        assert np.array_equal(bits(y.cpu().numpy()[0]), bits(want)), k
+
+
 def test_q8_0_qwen_lm_head_151936x896(ctx):
     rows, cols = 151936, 896
     say("Q8_0 lm_head", rows, cols)
