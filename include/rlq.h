@@ -191,7 +191,9 @@ void rlq_weights_stack(const rlq_weights *w, uint64_t *n2, uint64_t *n3);
  * x[b*cols ..] is quantized to the weights' activation type on the GPU, then
  * y[b*rows + r] = dot_packed(weights row r, activation b).  x and y are
  * device pointers (x 16-byte aligned).  Up to 8 columns share one pass over
- * the weights. */
+ * the weights.  A call takes at most 8388606 columns (the error keys carry
+ * the column): more return RLQ_UNIMPLEMENTED (a = batch, b = the limit), as
+ * do rlq_matmul_argmax, rlq_matmul_noalloc and rlq_quantize_device. */
 int32_t rlq_matmul(rlq_context *ctx, const rlq_weights *w, const float *x, uint64_t batch, float *y,
                    void *stream, rlq_error *err);
 
@@ -259,7 +261,8 @@ int32_t rlq_mul_mat_id(rlq_context *ctx, const rlq_weights *w, uint32_t x_dtype,
 /* Device quantize_into (crates/quant/src/encode.rs:37-100): the activation
  * quantizers (Q8_0, Q8_K) and the weight encoders (Q8_0, Q2_K..Q6_K), GGUF
  * bytes of `batch` rows of `cols` values each.  x and out are device
- * pointers.  For the K encoders a NonFiniteInput index counts over all
+ * pointers, x 16-byte aligned (RLQ_INVALID_ARGUMENT otherwise).  For the K
+ * encoders a NonFiniteInput index counts over all
  * batch*cols values and UnrepresentableScale over all blocks (b = 0). */
 int32_t rlq_quantize_device(rlq_context *ctx, uint32_t dtype, const float *x, uint64_t cols, uint64_t batch,
                             uint8_t *out, void *stream, rlq_error *err);

@@ -198,6 +198,10 @@ int32_t take_error(rlq_context* ctx, int slot, hipStream_t s, uint32_t dtype, rl
     return key_to_error(key, dtype, err);
 }
 
+// The context of the entry points that take none (rlq_quantize_into and the
+// like), created on first use under g_default_mu.  It is never handed to a
+// caller and never destroyed: it lives until the process ends, and no static
+// destructor or exit handler of this library calls HIP.
 std::mutex g_default_mu;
 rlq_context* g_default = nullptr;
 
@@ -366,7 +370,6 @@ void rlq_context_destroy(rlq_context* ctx) {
     if (ctx->err_words) (void)hipFree(ctx->err_words);
     if (ctx->host_err) (void)hipHostFree(ctx->host_err);
     if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
-    if (ctx == g_default) g_default = nullptr;
     delete ctx;
 }
 
@@ -591,11 +594,16 @@ static hipError_t decode_launch(rlq_context* ctx, const rlq_weights* w, const fl
                             isum, imin, ex, s);
 }
 
+// Columns per call: an error key holds column + 1 in 23 bits below the
+// model runtime's field 0x7fffff (rlq_device.hpp).
+constexpr uint64_t kMaxKeyColumns = (1ull << 23) - 2;
+
 static int32_t matmul_impl(rlq_context* ctx, const rlq_weights* w, const float* x, uint64_t batch, float* y,
                            uint32_t* argmax, void* stream, rlq_error* err) {
     if (!ctx || !w || !x || !y) return fail(err, RLQ_INVALID_ARGUMENT);
     if (((uintptr_t)x & 15) || ((uintptr_t)y & 3)) return fail(err, RLQ_INVALID_ARGUMENT, w->dtype);
     if (batch == 0) return ok(err);
+    if (batch > kMaxKeyColumns) return fail(err, RLQ_UNIMPLEMENTED, w->dtype, batch, kMaxKeyColumns);
     DeviceGuard g(ctx->device);
     const hipStream_t s = pick(ctx, stream);
     const bool gemm = w->dtype == kQ4_K && batch > kDecodeMaxBatch;
@@ -655,7 +663,7 @@ int32_t rlq_matmul_noalloc(rlq_context* ctx, const rlq_weights* w, const float* 
     if (!ctx || !w || !x || !y) return fail(err, RLQ_INVALID_ARGUMENT);
     if (((uintptr_t)x & 15) || ((uintptr_t)y & 3)) return fail(err, RLQ_INVALID_ARGUMENT, w->dtype);
     if (batch == 0) return ok(err);
-    if (batch > kScratchBytes) return fail(err, RLQ_SCRATCH_LIMIT, w->dtype, ~0ull, kScratchBytes);
+    if (batch > kMaxKeyColumns) return fail(err, RLQ_UNIMPLEMENTED, w->dtype, batch, kMaxKeyColumns);
     const bool gemm = w->dtype == kQ4_K && batch > kDecodeMaxBatch;
     const uint64_t state_bytes = argmax ? kArgmaxStateBytes : 0;
     const uint64_t keys_bytes = argmax && gemm ? (batch * 8 + 255) / 256 * 256 : 0;
@@ -693,7 +701,8 @@ int32_t rlq_quantize_device(rlq_context* ctx, uint32_t dtype, const float* x, ui
     if (rc) return rc;
     if (__builtin_mul_overflow(cols, batch, &n)) return fail(err, RLQ_SIZE_OVERFLOW, dtype);
     if (n == 0) return ok(err);
-    if (!x || !out) return fail(err, RLQ_INVALID_ARGUMENT, dtype);
+    if (!x || !out || ((uintptr_t)x & 15)) return fail(err, RLQ_INVALID_ARGUMENT, dtype);
+    if (batch > kMaxKeyColumns) return fail(err, RLQ_UNIMPLEMENTED, dtype, batch, kMaxKeyColumns);
     DeviceGuard g(ctx->device);
     const hipStream_t s = pick(ctx, stream);
     unsigned long long* ew = ctx->err_words;

@@ -560,16 +560,10 @@ hipError_t launch_gemm_q4k(const uint8_t* w, uint64_t rows, uint64_t cols, const
     g.ldy = ldy;
     g.dbg_isum = dbg_isum;
     g.dbg_imin = dbg_imin;
-    static bool lds_set = false;
-    if (!lds_set) {
-        e = hipFuncSetAttribute((const void*)q4k_gemm_kernel<false>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                (int)kGemmLds);
-        if (e == hipSuccess)
-            e = hipFuncSetAttribute((const void*)q4k_gemm_kernel<true>, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                    (int)kGemmLds);
-        if (e != hipSuccess) return e;
-        lds_set = true;
-    }
+    static LdsLimit lds_plain, lds_dbg;
+    e = dbg_isum ? lds_dbg.raise((const void*)q4k_gemm_kernel<true>, kGemmLds)
+                 : lds_plain.raise((const void*)q4k_gemm_kernel<false>, kGemmLds);
+    if (e != hipSuccess) return e;
     const dim3 grid((unsigned)(MT * NT));
     if (dbg_isum) hipLaunchKernelGGL(q4k_gemm_kernel<true>, grid, dim3(kGemmThreads), kGemmLds, s, g);
     else hipLaunchKernelGGL(q4k_gemm_kernel<false>, grid, dim3(kGemmThreads), kGemmLds, s, g);

@@ -634,23 +634,13 @@ hipError_t LlamaModel::create(const LlamaDims& dims, const LlamaHostTensors& t, 
         }
     }
     const uint64_t row_len = (d.max_context + 255) / 256 * 256, nchunks = (d.max_context + kAttnChunk - 1) / kAttnChunk;
-    // the attention workgroups' LDS grows with the context (the caller checked
-    // that it fits next to the kernels' few static bytes); the limits only grow,
-    // so models of other shapes in the process keep working
-    static int pv_set = 64 * 1024, scores_set = 64 * 1024;
+    // the attention workgroups' LDS grows with the group size and head width
+    // (the caller checked that it fits next to the kernels' few static bytes);
+    // the limits only grow, so models of other shapes in the process keep working
+    static LdsLimit pv_limit, scores_limit;
     const uint32_t G = (uint32_t)(d.heads / d.kv_heads);
-    const int pv_need = (int)(attn_pv_lds(G).total * sizeof(float));
-    const int scores_need = (int)attn_scores_lds(G, (uint32_t)hd);
-    hipError_t e = hipSuccess;
-    if (pv_need > pv_set) {
-        e = hipFuncSetAttribute((const void*)attn_pv_kernel, hipFuncAttributeMaxDynamicSharedMemorySize, pv_need);
-        if (e == hipSuccess) pv_set = pv_need;
-    }
-    if (e == hipSuccess && scores_need > scores_set) {
-        e = hipFuncSetAttribute((const void*)attn_scores_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                scores_need);
-        if (e == hipSuccess) scores_set = scores_need;
-    }
+    hipError_t e = pv_limit.raise((const void*)attn_pv_kernel, attn_pv_lds(G).total * sizeof(float));
+    if (e == hipSuccess) e = scores_limit.raise((const void*)attn_scores_kernel, attn_scores_lds(G, (uint32_t)hd));
     if (e == hipSuccess) e = hipMalloc((void**)&rope_tab, tab.size() * sizeof(float));
     if (e == hipSuccess) e = hipMemcpy(rope_tab, tab.data(), tab.size() * sizeof(float), hipMemcpyHostToDevice);
     uint64_t cache_bytes = 0;  // per cache: n_layers x max_context x kv_width floats

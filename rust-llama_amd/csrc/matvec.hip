@@ -630,6 +630,16 @@ __device__ __forceinline__ void fold_argmax(const MvArgs& a, uint8_t* lds, const
 // (Q8_0 151936x896: about 4 us of a 31 us launch); sixteen group counters in
 // place of the one measured the same, so the time is the round trips, not
 // contention on the counter.
+//
+// The ordering of the slot exchanges before the count rests on the hardware,
+// not on a release/acquire pair of the memory model: each exchanging thread
+// waits for its exchange's returned value (an atomic returns once it has been
+// performed at the device-coherent level), then the workgroup barrier, then
+// the count.  A release on the count is what the model asks for, but on
+// gfx950 it writes the workgroup's whole L2 back (buffer_wbl2): measured, the
+// Q8_0 151936x896 argmax launch went from 30.8 to 50.0 us and Q6_K 128256x4096
+// batch 8 from 82.2 to 83.6 us.  The argmax tests over every kernel and
+// batch size guard the assumption.
 __device__ __forceinline__ void finish_argmax(const MvArgs& a, uint8_t* lds, const LdsMap& L) {
     if (!a.am_out) return;
     unsigned long long* keys = (unsigned long long*)(lds + L.am_off);
@@ -2424,17 +2434,15 @@ __global__ __launch_bounds__(W * 64) void q8_0_mv_ks_kernel(MvArgs a) {
 constexpr int kMvWaves = 4;
 constexpr size_t kMaxLds = 160 * 1024;
 
-static int device_cus() {
-    static int cus = 0;
-    if (!cus) {
-        int dev = 0, v = 0;
-        if (hipGetDevice(&dev) == hipSuccess &&
-            hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0)
-            cus = v;
-        else
-            cus = 256;
-    }
-    return cus;
+int device_cus() {
+    static std::atomic<int> cus[kMaxDevices];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 256;
+    int v = cus[dev].load(std::memory_order_relaxed);
+    if (v > 0) return v;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0) v = 256;
+    cus[dev].store(v, std::memory_order_relaxed);  // every thread stores the same count
+    return v;
 }
 
 // Grid rows (MUL_MAT_ID pairs of this launch, else 1) and the workgroups per
@@ -2448,16 +2456,11 @@ static uint32_t grid_cols(uint32_t want, uint32_t cap, uint32_t rows) {
 // per_cu workgroups of W waves per CU at most (Q8_0 151936x896 with W = 4:
 // 25.8 us at three, 27.5 at two; Q6_K 128256x4096 with the argmax: one of 8
 // waves 71.8 us, two of 4 72.7-75.4, and at 8 columns 83.3 against 88.4).
-template <int W = kMvWaves, typename K>
-static hipError_t launch_one(K kernel, const MvArgs& a, size_t lds, hipStream_t s, uint32_t pairs,
-                             uint32_t per_cu = 2) {
-    static size_t lds_set = 64 * 1024;  // above 64 KB the kernel must opt in
-    if (lds > lds_set) {
-        const hipError_t e =
-            hipFuncSetAttribute((const void*)kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-        if (e != hipSuccess) return e;
-        lds_set = lds;
-    }
+// The kernel is a template argument so that each kernel keeps its own limit.
+template <int W, void (*kernel)(MvArgs)>
+static hipError_t launch_one(const MvArgs& a, size_t lds, hipStream_t s, uint32_t pairs, uint32_t per_cu = 2) {
+    static LdsLimit lds_limit;
+    if (const hipError_t e = lds_limit.raise((const void*)kernel, lds); e != hipSuccess) return e;
     const uint32_t want = (a.ntiles + W - 1) / W;
     const uint32_t gy = grid_rows(a, pairs);
     const uint32_t grid = grid_cols(want, per_cu * (uint32_t)device_cus(), gy);
@@ -2471,10 +2474,9 @@ static hipError_t launch_one(K kernel, const MvArgs& a, size_t lds, hipStream_t 
 constexpr int kSmallW = 8, kSmallKS = 8, kSmallD = 2, kSmallWgPerCu = 2;
 
 // The one-column small kernel: the grid and the LDS of its parked terms
-// [tmax][TS][nb].  lds_set is the kernel's own record of the dynamic LDS
-// limit it has been given.
+// [tmax][TS][nb].  lds_limit is the kernel's own dynamic-LDS limit.
 template <int W, int KS>
-static hipError_t launch_parked(void (*kernel)(MvArgs), size_t& lds_set, const MvArgs& a, hipStream_t s,
+static hipError_t launch_parked(void (*kernel)(MvArgs), LdsLimit& lds_limit, const MvArgs& a, hipStream_t s,
                                 uint32_t pairs, bool exp) {
     constexpr int TS = W / KS;
     if (a.batch != 1) return hipErrorInvalidValue;
@@ -2489,12 +2491,7 @@ static hipError_t launch_parked(void (*kernel)(MvArgs), size_t& lds_set, const M
     const uint32_t tstride = grid * TS, tmax = (a.ntiles + tstride - 1) / tstride;
     const size_t lds = small_lds_bytes(a.cols, tmax, TS, exp);
     if (lds > kMaxLds || (a.am_out && grid > kArgmaxMaxGrid)) return hipErrorInvalidValue;
-    if (lds > lds_set) {
-        const hipError_t e = hipFuncSetAttribute((const void*)kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                 (int)lds);
-        if (e != hipSuccess) return e;
-        lds_set = lds;
-    }
+    if (const hipError_t e = lds_limit.raise((const void*)kernel, lds); e != hipSuccess) return e;
     hipLaunchKernelGGL(kernel, dim3(grid, gy), dim3(W * 64), lds, s, a);
     return hipGetLastError();
 }
@@ -2503,7 +2500,7 @@ static hipError_t launch_parked(void (*kernel)(MvArgs), size_t& lds_set, const M
 // to about 16K), else the compact one.
 template <uint32_t T, int W, int KS, int D, bool DBG>
 static hipError_t launch_small(const MvArgs& a, hipStream_t s, uint32_t pairs) {
-    static size_t lds_exp = 64 * 1024, lds_cmp = 64 * 1024;
+    static LdsLimit lds_exp, lds_cmp;
     constexpr int TS = W / KS;
     if (one_part_off(a.cols, true) + (size_t)TS * park_bytes(a.nb) <= kMaxLds)
         return launch_parked<W, KS>(q4k_mv_small_kernel<T, W, KS, D, DBG, true>, lds_exp, a, s, pairs, true);
@@ -2566,7 +2563,7 @@ static bool b1_bal_takes(const MvArgs& a) {
 template <uint32_t T, int W, int KS, int D, bool DBG, bool FULL, bool BAL = false>
 static hipError_t launch_b1(const MvArgs& a, hipStream_t s) {
     constexpr int TS = W / KS;
-    static size_t lds_set = 64 * 1024;
+    static LdsLimit lds_limit;
     auto kernel = q45_mv_b1_kernel<T, W, KS, D, DBG, FULL, BAL>;
     uint32_t grid, tmax;
     if constexpr (BAL) b1_bal_grid<TS>(a, grid, tmax);
@@ -2574,12 +2571,7 @@ static hipError_t launch_b1(const MvArgs& a, hipStream_t s) {
     const size_t lds = b1_lds_bytes(a.cols, tmax, TS);
     if (grid == 0 || lds > kMaxLds || (a.am_out && grid > kArgmaxMaxGrid) || (a.resid && tmax > 4))
         return hipErrorInvalidValue;
-    if (lds > lds_set) {
-        const hipError_t e = hipFuncSetAttribute((const void*)kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                 (int)lds);
-        if (e != hipSuccess) return e;
-        lds_set = lds;
-    }
+    if (const hipError_t e = lds_limit.raise((const void*)kernel, lds); e != hipSuccess) return e;
     MvArgs b = a;
     b.deal_cus = BAL ? (uint32_t)device_cus() : 0;
     hipLaunchKernelGGL(kernel, dim3(grid), dim3(W * 64), lds, s, b);
@@ -2607,7 +2599,7 @@ static hipError_t launch_b1_any(const MvArgs& a, bool dbg, bool full, hipStream_
 template <uint32_t T, int W, int KS, int D, bool DBG, bool PL, bool BAL = false>
 static hipError_t launch_ks_pl(const MvArgs& a, hipStream_t s, uint32_t pairs) {
     constexpr int TS = W / KS;
-    static size_t lds_set = 64 * 1024;
+    static LdsLimit lds_limit;
     auto kernel = q45_mv_ks_kernel<T, W, KS, D, DBG, PL, BAL>;
     const uint32_t gy = grid_rows(a, pairs);
     uint32_t grid, tmax;
@@ -2625,12 +2617,7 @@ static hipError_t launch_ks_pl(const MvArgs& a, hipStream_t s, uint32_t pairs) {
     }
     const size_t lds = ks_lds_bytes(T, a.cols, a.batch, tmax, TS, KS);
     if (lds > kMaxLds || (a.am_out && grid > kArgmaxMaxGrid)) return hipErrorInvalidValue;
-    if (lds > lds_set) {
-        const hipError_t e = hipFuncSetAttribute((const void*)kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                 (int)lds);
-        if (e != hipSuccess) return e;
-        lds_set = lds;
-    }
+    if (const hipError_t e = lds_limit.raise((const void*)kernel, lds); e != hipSuccess) return e;
     MvArgs b = a;
     b.deal_cus = BAL ? (uint32_t)device_cus() : 0;
     hipLaunchKernelGGL(kernel, dim3(grid, gy), dim3(W * 64), lds, s, b);
@@ -2651,7 +2638,7 @@ static bool q8_0_ks_takes(const MvArgs& a, uint32_t pairs) {
 template <int W, int KS, bool DBG>
 static hipError_t launch_q8_0_ks(const MvArgs& a, hipStream_t s, uint32_t pairs) {
     constexpr int TS = W / KS;
-    static size_t lds_set = 64 * 1024;
+    static LdsLimit lds_limit;
     auto kernel = q8_0_mv_ks_kernel<W, KS, 2, DBG>;
     const uint32_t gy = grid_rows(a, pairs);
     const uint32_t grid = grid_cols((a.ntiles + TS - 1) / TS, (uint32_t)kSmallWgPerCu * (uint32_t)device_cus(), gy);
@@ -2659,12 +2646,7 @@ static hipError_t launch_q8_0_ks(const MvArgs& a, hipStream_t s, uint32_t pairs)
     if ((a.ntiles + (uint64_t)grid * TS - 1) / ((uint64_t)grid * TS) != 1 || lds > kMaxLds ||
         (a.am_out && grid > kArgmaxMaxGrid))
         return hipErrorInvalidValue;
-    if (lds > lds_set) {
-        const hipError_t e = hipFuncSetAttribute((const void*)kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                 (int)lds);
-        if (e != hipSuccess) return e;
-        lds_set = lds;
-    }
+    if (const hipError_t e = lds_limit.raise((const void*)kernel, lds); e != hipSuccess) return e;
     hipLaunchKernelGGL(kernel, dim3(grid, gy), dim3(W * 64), lds, s, a);
     return hipGetLastError();
 }
@@ -2764,15 +2746,10 @@ constexpr int kK16W = 8, kK16KS = 8, kK16D = 2;
 
 template <uint32_t T, bool DBG>
 static hipError_t launch_k16_split(const MvArgs& a, size_t lds, uint32_t grid, uint32_t gy, hipStream_t s) {
-    static size_t lds_set = 64 * 1024;
+    static LdsLimit lds_limit;
     auto kernel = k16_mv_split_kernel<T, kK16W, kK16KS, kK16D, DBG>;
     if (a.am_out && grid > kArgmaxMaxGrid) return hipErrorInvalidValue;
-    if (lds > lds_set) {
-        const hipError_t e = hipFuncSetAttribute((const void*)kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                 (int)lds);
-        if (e != hipSuccess) return e;
-        lds_set = lds;
-    }
+    if (const hipError_t e = lds_limit.raise((const void*)kernel, lds); e != hipSuccess) return e;
     hipLaunchKernelGGL(kernel, dim3(grid, gy), dim3(kK16W * 64), lds, s, a);
     return hipGetLastError();
 }
@@ -2782,7 +2759,7 @@ static hipError_t launch_k16_split(const MvArgs& a, size_t lds, uint32_t grid, u
 template <uint32_t T, int W, int KS, bool DBG>
 static hipError_t launch_k16_bal(const MvArgs& a, hipStream_t s) {
     constexpr int TS = W / KS;
-    static size_t lds_set = 64 * 1024;
+    static LdsLimit lds_limit;
     // one chunk in flight per wave with 16 waves (14336x4096 Q3_K 9.73 us
     // against 9.98 at two, Q2_K 8.45 against 8.53)
     auto kernel = k16_mv_split_kernel<T, W, KS, W >= 16 ? 1 : kK16D, DBG, true>;
@@ -2791,12 +2768,7 @@ static hipError_t launch_k16_bal(const MvArgs& a, hipStream_t s) {
     const uint64_t lds = k16_part_off(T, a.cols, a.batch) + (uint64_t)tmax * TS * a.nb * 16ull * a.batch * 4ull;
     if (grid == 0 || a.ids || a.batch > 8 || lds > kMaxLds || (a.am_out && grid > kArgmaxMaxGrid))
         return hipErrorInvalidValue;
-    if (lds > lds_set) {
-        const hipError_t e = hipFuncSetAttribute((const void*)kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                 (int)lds);
-        if (e != hipSuccess) return e;
-        lds_set = lds;
-    }
+    if (const hipError_t e = lds_limit.raise((const void*)kernel, lds); e != hipSuccess) return e;
     MvArgs b = a;
     b.deal_cus = (uint32_t)device_cus();
     hipLaunchKernelGGL(kernel, dim3(grid), dim3(W * 64), lds, s, b);
@@ -2821,8 +2793,8 @@ static hipError_t launch_k16(const MvArgs& a, bool dbg, size_t lds_plain, hipStr
     const uint64_t lds = k16_part_off(T, a.cols, a.batch) + tmax * TS * a.nb * 16ull * a.batch * 4ull;
     if (a.batch <= 4 && lds <= kMaxLds)
         return dbg ? launch_k16_split<T, true>(a, lds, grid, gy, s) : launch_k16_split<T, false>(a, lds, grid, gy, s);
-    return dbg ? launch_one(k16_mv_kernel<T, kMvWaves, 4, true>, a, lds_plain, s, pairs)
-               : launch_one(k16_mv_kernel<T, kMvWaves, 4, false>, a, lds_plain, s, pairs);
+    return dbg ? launch_one<kMvWaves, k16_mv_kernel<T, kMvWaves, 4, true>>(a, lds_plain, s, pairs)
+               : launch_one<kMvWaves, k16_mv_kernel<T, kMvWaves, 4, false>>(a, lds_plain, s, pairs);
 }
 
 hipError_t launch_matvec(uint32_t wtype, const uint8_t* w, uint64_t rows, uint64_t cols, const float* x,
@@ -2915,17 +2887,17 @@ hipError_t launch_matvec_ex(uint32_t wtype, const uint8_t* w, uint64_t rows, uin
                     // with four and 80.3 with five; batch 1 71.1 with three or four);
                     // one column in the reference's f32 order
                     if (nbat == 1)
-                        return dbg ? launch_one<2 * W>(q6k_mv_one_kernel<2 * W, 3, true>, a, lds, s, pairs, 1)
-                                   : launch_one<2 * W>(q6k_mv_one_kernel<2 * W, 3, false>, a, lds, s, pairs, 1);
-                    return dbg ? launch_one<2 * W>(q6k_mv_kernel<2 * W, 3, true>, a, lds, s, pairs, 1)
-                               : launch_one<2 * W>(q6k_mv_kernel<2 * W, 3, false>, a, lds, s, pairs, 1);
+                        return dbg ? launch_one<2 * W, q6k_mv_one_kernel<2 * W, 3, true>>(a, lds, s, pairs, 1)
+                                   : launch_one<2 * W, q6k_mv_one_kernel<2 * W, 3, false>>(a, lds, s, pairs, 1);
+                    return dbg ? launch_one<2 * W, q6k_mv_kernel<2 * W, 3, true>>(a, lds, s, pairs, 1)
+                               : launch_one<2 * W, q6k_mv_kernel<2 * W, 3, false>>(a, lds, s, pairs, 1);
                 default:
                     if (q8_0_ks_takes<8, 4>(a, pairs))
                         return dbg ? launch_q8_0_ks<8, 4, true>(a, s, pairs) : launch_q8_0_ks<8, 4, false>(a, s, pairs);
                     // ten chunks in flight per wave (151936x896 + argmax: 30.3 us
                     // against 30.9 with eight, 31.8 with six)
-                    return dbg ? launch_one(q8_0_mv_kernel<W, 10, true>, a, lds, s, pairs, 3)
-                               : launch_one(q8_0_mv_kernel<W, 10, false>, a, lds, s, pairs, 3);
+                    return dbg ? launch_one<W, q8_0_mv_kernel<W, 10, true>>(a, lds, s, pairs, 3)
+                               : launch_one<W, q8_0_mv_kernel<W, 10, false>>(a, lds, s, pairs, 3);
             }
         };
         if (!a.ids) {

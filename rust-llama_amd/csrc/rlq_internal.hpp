@@ -6,6 +6,8 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include <atomic>
+#include <mutex>
 #include <vector>
 
 namespace rlq {
@@ -215,5 +217,39 @@ hipError_t launch_argmax_rows(const float* y, uint64_t batch, uint64_t rows, uns
 // Decode argmax keys into u32 indices; reset: then set the keys back to 0.
 hipError_t launch_argmax_finish(unsigned long long* keys, uint64_t batch, const float* y, uint64_t ldy, uint32_t* out,
                                 hipStream_t s, bool reset = false);
+
+// ---- per-device launch state (any number of host threads) ----
+constexpr int kMaxDevices = 256;
+
+// The compute units of the calling thread's current device, read once per
+// device (256 if HIP cannot say).
+int device_cus();
+
+// One kernel's dynamic-LDS limit per device: HIP refuses a launch that asks
+// for more than 64 KB unless the kernel's limit was raised first.  The limit
+// only grows, under the lock, and is recorded after HIP has accepted it, so a
+// thread that reads a recorded limit of at least its own size may launch.
+// Objects of this class live in static storage (zero-initialized, no
+// destructor that calls HIP).
+class LdsLimit {
+  public:
+    hipError_t raise(const void* kernel, size_t bytes) {
+        if (bytes <= 64 * 1024) return hipSuccess;
+        int dev = 0;
+        hipError_t e = hipGetDevice(&dev);
+        if (e != hipSuccess) return e;
+        if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+        if (bytes <= set_[dev].load(std::memory_order_acquire)) return hipSuccess;
+        std::lock_guard<std::mutex> lock(mu_);
+        if (bytes <= set_[dev].load(std::memory_order_relaxed)) return hipSuccess;
+        e = hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+        if (e == hipSuccess) set_[dev].store(bytes, std::memory_order_release);
+        return e;
+    }
+
+  private:
+    std::mutex mu_;
+    std::atomic<size_t> set_[kMaxDevices] = {};
+};
 
 }  // namespace rlq

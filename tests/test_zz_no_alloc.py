@@ -46,6 +46,8 @@ def inputs(seed, batch, cols):
     (DT.Q4_K, 1000, 4096, (300, 40), True),     # prefill GEMM: activation image in the scratch
     (DT.Q4_K, 1000, 4096, (300, 40), False),
     (DT.Q4_K, 2000, 2048, (7, 3), True),        # decode kernels: only the argmax keys in the scratch
+    (DT.Q5_K, 1500, 4096, (8, 7), True),        # 7-8 columns: fused quantizer here, planes kernel in rlq_matmul
+    (DT.Q5_K, 1500, 4096, (8, 7), False),
     (DT.Q6_K, 3000, 4096, (8, 1), True),
     (DT.Q8_0, 2000, 896, (5, 2), True)])
 def test_noalloc_equals_allocating_entry_point(ctx, t, rows, cols, batches, with_argmax):
@@ -95,3 +97,32 @@ def test_noalloc_data_errors_and_refusal(ctx):
     ctx.matmul_noalloc(W, x, y)
     ctx.sync()
     assert torch.equal(bits(y), bits(ctx.matmul(W, x)))
+
+
+@pytest.mark.parametrize("t", [DT.Q4_K, DT.Q5_K])
+@pytest.mark.parametrize("batch", [7, 8])
+def test_noalloc_errors_of_seven_and_eight_columns(ctx, t, batch):
+    """At 7-8 Q4_K / Q5_K columns rlq_matmul quantizes every column in the
+    planes kernel first, while rlq_matmul_noalloc quantizes in each decode
+    workgroup's prologue: both must report the same first error (by column,
+    then the reference's order inside it) and leave every output untouched."""
+    W = weights(ctx, t, 768, 4096, 7)
+    for case in ("nan", "scale"):
+        say("matmul_noalloc errors", t, "batch", batch, case)
+        x = inputs(11, batch, 4096)
+        if case == "nan":
+            x[5, 1000] = float("nan")
+            x[6, 10] = float("inf")
+        else:
+            x[4, 512:768] = 1e-45  # column 4, block 2: an unrepresentable scale
+            x[5, 3] = float("nan")
+        got = []
+        for call in (ctx.matmul_noalloc, ctx.matmul):
+            y = torch.full((batch, 768), 5.0, device="cuda")
+            call(W, x, y)
+            with pytest.raises(rlq.QuantError) as e:
+                ctx.sync()
+            got.append((e.value.name, e.value.a, e.value.b))
+            assert bool((y == 5.0).all()), call
+        assert got[0] == got[1]
+        assert got[0] == (("NonFiniteInput", 1000, 5) if case == "nan" else ("UnrepresentableScale", 2, 4))
