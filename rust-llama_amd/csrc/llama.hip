@@ -11,12 +11,12 @@
 // same libm calls and operation order as math.rs:322-334), the softmax
 // exponentials (SSE2 exponential of cpu_math.rs:94-123) and pair sums, and
 // SiLU are the reference's operations in the reference's order.  The f64 sums
-// of the QK dots and the softmax totals run in parallel orders whose f32
-// results are certified equal to the reference's (or repeated in its order:
-// certified_f32), so scores and probabilities are bit-exact.  The P.V sums
-// add the same f64 terms in another order: an output can differ from the
-// reference's in the last bit.  The matvecs' f32 block combine order is the
-// kernels' own (their integer block sums are exact).
+// of the QK dots, the softmax totals and the P.V outputs run in parallel
+// orders whose f32 results are certified equal to the reference's (or
+// repeated in its order: certified_f32, pv_interval, f64_sum_exact), so scores,
+// probabilities and attention outputs are bit-exact.  The one-column
+// matvecs of every weight type but Q3_K combine their exact integer block
+// sums in the reference's f32 order (Q3_K in the kernel's own).
 #include <math.h>
 #include <stdlib.h>
 
@@ -37,9 +37,9 @@ constexpr uint32_t kScKeyRegs = kAttnMaxHd * kAttnChunk / 4 / kAttnThreads;  // 
 constexpr uint32_t kScKeyPad = 16;  // floats after each key row in LDS
 
 constexpr uint32_t kPvDims = 4;       // head dimensions per P.V workgroup: one float4 of each value row
-constexpr uint32_t kPvThreads = 512;
-constexpr uint32_t kPvWaves = kPvThreads / 64;
-constexpr uint32_t kPvRegGroups = 2;  // column groups of four per lane whose values and exponentials stay in registers
+constexpr uint32_t kPvMaxWaves = 8;   // waves per P.V workgroup: one per query head of the kv head
+constexpr uint32_t kPvRegGroups = 4;  // column groups of four per lane whose values and exponentials stay in registers
+constexpr uint32_t kPvRepTerms = 256;  // f64 terms per round of a sequential P.V repeat
 
 // The value cache of a layer is slice-major: [kv_heads * hd / 4][max_context]
 // float4, slice kvh * hd / 4 + d / 4 holding dimensions d .. d + 3 of kv head
@@ -49,41 +49,18 @@ __host__ __device__ inline uint64_t v_cache_index(uint32_t kvh, uint32_t hd, uin
     return ((uint64_t)(kvh * (hd / 4) + d / 4) * max_context + token) * 4 + d % 4;
 }
 
-// P.V waves per head: the waves of a workgroup split G heads' columns.
-__host__ __device__ inline uint32_t pv_waves_per_head(uint32_t G) { return G < kPvWaves ? kPvWaves / G : 1u; }
-
-// LDS of attn_pv_kernel, in floats: max and inverse [G][2], the f64 partial
-// row sums [G][waves per head], the P.V records [G][waves per head][4
-// dimensions][4 lane rows] (PvRec), and one 256-term f64 buffer per wave for
-// the sequential repeats.
-// It does not grow with the context: the scores and values stream from HBM.
-struct PvRec {
-    double sum;     // the 16 lanes' tree sum of their f64 sums
-    float wsum;     // sum over their column groups g of (groups - 1 - g) |group sum|
-    float abs_sum;  // sum |term|
-    float min_abs;  // smallest |term| (infinity: none)
-    float pad;
-};
-constexpr uint32_t kPvRepTerms = 256;
-struct AttnPvLds {
-    uint32_t rsum, part, rep, total;
-};
-__host__ __device__ inline AttnPvLds attn_pv_lds(uint32_t G) {
-    AttnPvLds l;
-    const uint32_t wph = pv_waves_per_head(G);
-    l.rsum = (2 * G + 1) & ~1u;
-    l.part = l.rsum + 2 * G * wph;
-    l.rep = l.part + (uint32_t)(sizeof(PvRec) / 4) * 16 * G * wph;
-    l.total = l.rep + 2 * kPvRepTerms * kPvWaves;
-    return l;
-}
+// P.V waves per workgroup, and its LDS: one kPvRepTerms f64 buffer per wave
+// for the sequential repeats (it does not grow with the context: the scores
+// and values stream from HBM).
+__host__ __device__ inline uint32_t pv_waves(uint32_t G) { return G < kPvMaxWaves ? G : kPvMaxWaves; }
+__host__ __device__ inline uint32_t attn_pv_lds_bytes(uint32_t G) { return pv_waves(G) * kPvRepTerms * 8; }
 __host__ __device__ inline uint32_t attn_scores_lds(uint32_t G, uint32_t hd) {
     return (G * hd + kAttnChunk * (hd + kScKeyPad)) * 4;
 }
 
 uint64_t llama_attn_lds_bytes(uint64_t heads, uint64_t kv_heads, uint64_t head_dim) {
     const uint64_t G = heads / kv_heads;
-    const uint64_t pv = (uint64_t)attn_pv_lds((uint32_t)G).total * 4;
+    const uint64_t pv = attn_pv_lds_bytes((uint32_t)G);
     const uint64_t sc = attn_scores_lds((uint32_t)G, (uint32_t)head_dim);
     return pv > sc ? pv : sc;
 }
@@ -113,6 +90,17 @@ __device__ __forceinline__ bool certified_f32(double sum, double abs_sum, uint32
     return f(sum - eps) == f(sum + eps);
 }
 __device__ __forceinline__ float f64_to_f32(double x) { return (float)x; }
+
+// Whether every order of an f64 sum of f32 terms gives the exact sum: with M
+// the smallest |term| (0 when a term is zero) and A >= sum |term|, every term
+// of magnitude >= M is a multiple of q = ulp(M) (2^-149 for a subnormal M),
+// so when A < 2^53 q every partial sum in any order is a multiple of q below
+// 2^53 q, exactly representable, and every f64 addition is exact.
+__device__ __forceinline__ bool f64_sum_exact(double A, float M) {
+    const uint32_t b = (__float_as_uint(M) >> 23) & 0xffu;  // q = 2^(b - 150), 2^-149 for b = 0
+    const double lim = __longlong_as_double((long long)((uint64_t)((b == 0u ? 1u : b) + 53u + 1023u - 150u) << 52));
+    return M > 0.0f && M < INFINITY && A * (1.0 + 1e-3) < lim;
+}
 
 // Scores of kv head blockIdx.y's G query heads against tokens
 // [16 * blockIdx.x, +16) of the layer cache (math.rs:462-474):
@@ -179,17 +167,19 @@ __global__ __launch_bounds__(kAttnThreads) void attn_scores_kernel(
         const float* q = q_s + h * hd;
         const float* k = k_s + t * ks;
         // four interleaved partial sums per lane, then the four lanes'; the
-        // f32 total is certified against the reference's d-order sum, or
+        // f32 total is certified against the reference's d-order sum (exact
+        // in every order, f64_sum_exact, or by the bound of certified_f32), or
         // recomputed in that order.  The magnitudes are summed in f32
         // (relative error < 2^-16 for hd <= 256, covered by the factor 1.01).
         double a[4] = {0.0, 0.0, 0.0, 0.0};
-        float b = 0.0f;
+        float b = 0.0f, mn = INFINITY;
         if (live) {
             for (uint32_t d = 4 * quarter; d < hd; d += 16) {
                 const float4 q4v = *(const float4*)(q + d), k4 = *(const float4*)(k + d);
                 const float x0 = q4v.x * k4.x, x1 = q4v.y * k4.y, x2 = q4v.z * k4.z, x3 = q4v.w * k4.w;
                 a[0] += (double)x0, a[1] += (double)x1, a[2] += (double)x2, a[3] += (double)x3;
                 b += (fabsf(x0) + fabsf(x1)) + (fabsf(x2) + fabsf(x3));
+                mn = fminf(mn, fminf(fminf(fabsf(x0), fabsf(x1)), fminf(fabsf(x2), fabsf(x3))));
             }
         }
         double part = (a[0] + a[1]) + (a[2] + a[3]);
@@ -197,12 +187,27 @@ __global__ __launch_bounds__(kAttnThreads) void attn_scores_kernel(
         part += dpp_d<kQuadXor2>(part);
         b += dpp_f<kQuadXor1>(b);
         b += dpp_f<kQuadXor2>(b);
+        mn = fminf(mn, dpp_f<kQuadXor1>(mn));
+        mn = fminf(mn, dpp_f<kQuadXor2>(mn));
         float score = -INFINITY;
         if (live) {
             float dotf;
-            if (!certified_f32(part, 1.01 * (double)b, hd, f64_to_f32, &dotf) || repeat_all) {
+            const bool exact = f64_sum_exact(1.01 * (double)b, mn);
+            if (exact) dotf = (float)part;
+            if ((!exact && !certified_f32(part, 1.01 * (double)b, hd, f64_to_f32, &dotf)) || repeat_all) {
+                // sixteen products loaded and formed ahead of their adds
                 double dot = 0.0;
-                for (uint32_t d = 0; d < hd; ++d) dot += (double)(q[d] * k[d]);
+                for (uint32_t d = 0; d < hd; d += 16) {
+                    float x[16];
+#pragma unroll
+                    for (uint32_t u = 0; u < 4; ++u) {
+                        const float4 qa = *(const float4*)(q + d + 4 * u), ka = *(const float4*)(k + d + 4 * u);
+                        x[4 * u] = qa.x * ka.x, x[4 * u + 1] = qa.y * ka.y;
+                        x[4 * u + 2] = qa.z * ka.z, x[4 * u + 3] = qa.w * ka.w;
+                    }
+#pragma unroll
+                    for (uint32_t u = 0; u < 16; ++u) dot += (double)x[u];
+                }
                 dotf = (float)dot;
             }
             score = dotf * scale;
@@ -211,36 +216,35 @@ __global__ __launch_bounds__(kAttnThreads) void attn_scores_kernel(
                 scores[(uint64_t)(kvh * G + h) * row_stride + t0 + t] = score;
             }
         }
-        float m = score;
-        // the quads hold equal values: the rest of the wave's 16 pairs
-        m = fmaxf(m, dpp_f<kRowHalfMirror>(m));
-        m = fmaxf(m, dpp_f<kRowRor8>(m));
-        m = fmaxf(m, __shfl_xor(m, 16, 64));
-        m = fmaxf(m, __shfl_xor(m, 32, 64));
+        // the maximum of the wave's 16 pairs (one head's 16 tokens)
+        const float m = wave_max_dpp(score);
         if ((tid & 63) == 0) cmax[(kvh * G + h) * cstride + c] = m;
     }
 }
 
 // Softmax of the G heads' score rows (math.rs:293-318 with the SSE2 policy of
 // cpu_math.rs:60-91) and P.V (math.rs:475-488) for 4 of the head dimensions:
-// workgroup (blockIdx.x, blockIdx.y) = (dimensions 4 * blockIdx.x .., kv head).
-// Every workgroup of the kv head computes the G rows' softmax from the chunk
-// maxima.  The columns go in groups of four (the reference's SSE2 vectors);
-// lane r of part w of a head's wph waves takes groups 64 w + r, + 64 wph, ...
-// Its first kPvRegGroups groups' values are loaded when the kernel starts and
-// their exponentials kept from the row sums; later groups are reloaded and
-// their exponentials recomputed (the same f32 function of the same inputs),
-// so the LDS does not grow with the context.  The softmax totals are
-// certified against the reference's order (certified_f32).  Each P.V sum adds
-// the reference's f64 terms f64(p * v) in another order (per lane, then each
-// 16-lane row in a fixed tree, then the head's rows in order); its f32 result
-// is certified (pv_certified) or the sum is repeated in the reference's
-// column order.  Columns past `count` have exponential 0 and are not added.
+// workgroup (blockIdx.x, blockIdx.y) = (dimensions 4 * blockIdx.x .., kv head),
+// one wave per query head of the kv head (heads past kPvMaxWaves loop over the
+// waves).  The waves never wait for each other: each one takes its head's
+// maximum from the chunk maxima, the exponentials of every column and their
+// total, and the four P.V sums.  The columns go in groups of four (the
+// reference's SSE2 vectors); lane r takes groups r, r + 64, ...  Its first
+// kPvRegGroups groups' values (shared by the wave's heads) are loaded when the
+// kernel starts and their exponentials kept from the row total; later groups
+// are reloaded and their exponentials recomputed (the same f32 function of the
+// same inputs), so the LDS does not grow with the context.  The softmax total
+// is certified against the reference's order (certified_f32).  Each P.V sum
+// adds the reference's f64 terms f64(p * v) in another order (per lane, then
+// the wave in a fixed tree); its f32 result is certified (pv_interval) or the
+// sum is repeated in the reference's column order.  Columns past `count` have
+// exponential 0 and are not added.
+// (The four exponentials are computed whatever the count and masked after,
+// so no lane branches and their evaluations interleave.)
 __device__ __forceinline__ void exp_group(float4 x, uint32_t t, uint32_t count, float m, float (&e)[4]) {
-    e[0] = t < count ? sse2_exp(x.x - m) : 0.0f;
-    e[1] = t + 1 < count ? sse2_exp(x.y - m) : 0.0f;
-    e[2] = t + 2 < count ? sse2_exp(x.z - m) : 0.0f;
-    e[3] = t + 3 < count ? sse2_exp(x.w - m) : 0.0f;
+    const float v[4] = {sse2_exp(x.x - m), sse2_exp(x.y - m), sse2_exp(x.z - m), sse2_exp(x.w - m)};
+#pragma unroll
+    for (uint32_t j = 0; j < 4; ++j) e[j] = __uint_as_float(__float_as_uint(v[j]) & (t + j < count ? ~0u : 0u));
 }
 
 // Whether the f32 rounding of a P.V sum added in the kernel's order (sum; at
@@ -250,26 +254,24 @@ __device__ __forceinline__ void exp_group(float4 x, uint32_t t, uint32_t count, 
 // column order, R of them) of (R - 1 - g) |group sum|, each group sum the
 // growth of a lane's f64 sum rounded to f32 (within 2^-23 of itself plus
 // 4 2^-53 A of the exact one).
-//  - exactly: every term is an f32 value, a multiple of q = 2^(e(M) - 23);
-//    if A < 2^53 q, every partial sum in any order is a multiple of q below
-//    2^53 q, so every f64 addition is exact and all orders give the exact sum;
-//  - else by an interval: the reference's k-th partial sum rounds by at most
+//  - by an interval (pv_interval): the reference's k-th partial sum rounds by at most
 //    2^-53 of itself, and its prefix P_k lies within |E_g| + A_g of zero (E_g
 //    the sum of the groups before column k's group g, |E_g| <= the sum of
 //    their |group sums|, A_g the group's sum |term|), so its sum is within
 //    2^-53 (4 wsum 1.001 + 4 (4 2^-53 R^2 + 1) A) of the exact one; the kernel's within
-//    2^-53 (tl A + 40 A) (each lane's columns, its 16-lane row in a tree of
-//    4 levels, then at most 32 row sums in order).  When both ends of that
-//    interval round to one f32, so does the reference's sum.
-__device__ __forceinline__ bool pv_certified(double sum, double A, double wsum, float M, double tl, double R) {
-    if (!(M < INFINITY)) return true;  // no term
-    if (M > 0.0f) {
-        int e;
-        frexpf(M, &e);  // M = f 2^e, f in [0.5, 1): q = 2^(e - 1 - 23)
-        if (A * (1.0 + 1e-3) < ldexp(1.0, e - 1 - 23 + 53)) return true;
-    }
-    const double B =
-        1.1102230246251565e-16 * 1.02 * 1.001 * (4.0 * wsum + (4.0 * (4.0 * 1.1102230246251565e-16 * R * R + 1.0) + tl + 40.0) * A);
+//    2^-53 (tl A + 40 A) (each lane's columns, then the wave's tree of six
+//    levels).  When both ends of that interval round to one f32, so does the
+//    reference's sum;
+//  - else exactly (f64_sum_exact of A and M).
+// The interval's coefficient of A: 4 (4 2^-53 R^2 + 1) + tl + 40.
+__device__ __forceinline__ double pv_coef_a(double tl, double R) {
+    return 4.0 * (4.0 * 1.1102230246251565e-16 * R * R + 1.0) + tl + 40.0;
+}
+// The interval test with C = 4 wsum + pv_coef_a A (C computed in f32 per
+// lane and per 16-lane row: relative error below 1e-6, covered by one more
+// factor 1.001).
+__device__ __forceinline__ bool pv_interval(double sum, double C) {
+    const double B = 1.1102230246251565e-16 * 1.02 * 1.001 * 1.001 * C;
     return (float)(sum - B) == (float)(sum + B);
 }
 
@@ -287,87 +289,59 @@ __device__ __forceinline__ float row16_min_f(float v) {
     return fminf(v, dpp_f<kRowRor8>(v));
 }
 
-__global__ __launch_bounds__(kPvThreads) void attn_pv_kernel(
+__global__ __launch_bounds__(kPvMaxWaves * 64) void attn_pv_kernel(
     const float* __restrict__ scores, const float* __restrict__ cmax, uint32_t cstride, uint32_t nch,
     const float* __restrict__ vc, uint32_t max_context, uint32_t count, uint32_t heads, uint32_t kv_heads, uint32_t hd,
     uint32_t row_stride, float* __restrict__ att, unsigned long long* __restrict__ err_word, uint32_t layer,
     uint32_t repeat_all) {
-    extern __shared__ __align__(16) float sm[];
+    extern __shared__ __align__(16) double rep_s[];  // [waves][kPvRepTerms]: the sequential repeats
     const uint32_t G = heads / kv_heads, kvh = blockIdx.y, d0 = blockIdx.x * kPvDims;
-    const AttnPvLds Lp = attn_pv_lds(G);
-    float* stat = sm;                        // [G][2]: max, inverse
-    double* rsum = (double*)(sm + Lp.rsum);  // [G][wph]
-    PvRec* rec = (PvRec*)(sm + Lp.part);     // [G][wph][4]
-    double* rep = (double*)(sm + Lp.rep);    // [kPvWaves][kPvRepTerms]
-    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
     const uint32_t ngroups = (count + 3) / 4;
-    const uint32_t wph = pv_waves_per_head(G), hstep = kPvWaves / wph;
-    const bool active = wave < hstep * wph;  // wave-uniform
-    const uint32_t w = wave % wph, h0 = wave / wph, gstride = 64 * wph, g0 = 64 * w + lane;
     const float4* vsrc = (const float4*)(vc + v_cache_index(kvh, hd, d0, 0, max_context));
-    // the values of this lane's first groups (shared by every head of the kv
-    // head) and the first head's scores of those groups, loaded before the
-    // maxima are known
-    float4 vr[kPvRegGroups][4], sr[kPvRegGroups];
+    double* buf = rep_s + wave * kPvRepTerms;
+    float4 vr[kPvRegGroups][4];
 #pragma unroll
-    for (uint32_t k = 0; k < kPvRegGroups; ++k) {
-        const uint32_t g = g0 + k * gstride;
-        sr[k] = active && h0 < G && g < ngroups ? *(const float4*)(scores + (uint64_t)(kvh * G + h0) * row_stride + 4 * g)
-                                                : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    for (uint32_t k = 0; k < kPvRegGroups; ++k)
 #pragma unroll
         for (uint32_t j = 0; j < 4; ++j) {
-            const uint32_t t = 4 * g + j;
-            vr[k][j] = active && t < count ? vsrc[t] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            const uint32_t t = 4 * (lane + 64 * k) + j;
+            vr[k][j] = t < count ? vsrc[t] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
         }
-    }
-    // the row maxima: one wave per head over its chunk maxima
-    for (uint32_t h = wave; h < G; h += kPvWaves) {
+    const double tl = 4.0 * ((ngroups + 63) / 64);  // columns per lane
+    for (uint32_t h = wave; h < G; h += nw) {        // (wave-uniform)
+        const uint32_t row = kvh * G + h;
+        const float* srow = scores + (uint64_t)row * row_stride;
+        float4 sr[kPvRegGroups];
+#pragma unroll
+        for (uint32_t k = 0; k < kPvRegGroups; ++k) {
+            const uint32_t g = lane + 64 * k;
+            sr[k] = g < ngroups ? *(const float4*)(srow + 4 * g) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        }
         float m = -INFINITY;
-        for (uint32_t c = lane; c < nch; c += 64) m = fmaxf(m, cmax[(kvh * G + h) * cstride + c]);
+        for (uint32_t c = lane; c < nch; c += 64) m = fmaxf(m, cmax[row * cstride + c]);
         m = wave_max_dpp(m);
-        if (lane == 0) stat[2 * h] = m;
-    }
-    __syncthreads();
-    // exponentials and f32 pair sums of each group (math.rs:303-313), the
-    // lane's pair sums added in f64; the first head's first groups keep
-    // their exponentials for P.V
-    float er[kPvRegGroups][4];
-    if (active) {
-        for (uint32_t h = h0; h < G; h += hstep) {
-            const float m = stat[2 * h];
-            const float* srow = scores + (uint64_t)(kvh * G + h) * row_stride;
-            double sum = 0.0;
-#pragma unroll
-            for (uint32_t k = 0; k < kPvRegGroups; ++k) {
-                const uint32_t g = g0 + k * gstride;
-                float e[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-                if (g < ngroups) exp_group(h == h0 ? sr[k] : *(const float4*)(srow + 4 * g), 4 * g, count, m, e);
-                if (h == h0) {
-#pragma unroll
-                    for (uint32_t j = 0; j < 4; ++j) er[k][j] = e[j];
-                }
-                sum += (double)((e[0] + e[1]) + (e[2] + e[3]));
-            }
-            for (uint32_t g = g0 + kPvRegGroups * gstride; g < ngroups; g += gstride) {
-                float e[4];
-                exp_group(*(const float4*)(srow + 4 * g), 4 * g, count, m, e);
-                sum += (double)((e[0] + e[1]) + (e[2] + e[3]));
-            }
-            sum = wave_sum_f64(sum);
-            if (lane == 0) rsum[h * wph + w] = sum;
-        }
-    }
-    __syncthreads();
-    // the row totals, certified against the reference's column-order f64 sum
-    // (the pair sums are >= 0: sum = sum |.|), else repeated in that order by
-    // the head's wave: 64 pair sums per load, added lane by lane
-    for (uint32_t h = wave; h < G; h += kPvWaves) {
+        // exponentials and f32 pair sums of each group (math.rs:303-313), the
+        // lane's pair sums added in f64
+        float er[kPvRegGroups][4];
         double sum = 0.0;
-        for (uint32_t v = 0; v < wph; ++v) sum += rsum[h * wph + v];
+#pragma unroll
+        for (uint32_t k = 0; k < kPvRegGroups; ++k) {
+            const uint32_t g = lane + 64 * k;
+            exp_group(sr[k], 4 * g, count, m, er[k]);  // zero past the row (4 g >= count there)
+            sum += (double)((er[k][0] + er[k][1]) + (er[k][2] + er[k][3]));
+        }
+        for (uint32_t g = lane + 64 * kPvRegGroups; g < ngroups; g += 64) {
+            float e[4];
+            exp_group(*(const float4*)(srow + 4 * g), 4 * g, count, m, e);
+            sum += (double)((e[0] + e[1]) + (e[2] + e[3]));
+        }
+        sum = wave_sum_f64(sum);
+        // the row total, certified against the reference's column-order f64
+        // sum (the pair sums are >= 0: sum = sum |.|), else repeated in that
+        // order: 64 pair sums per load, added lane by lane
         float inv;
         if (!certified_f32(sum, sum, ngroups, [](double x) { return (float)(1.0 / x); }, &inv) || repeat_all) {
-            const float m = stat[2 * h];
-            const float* srow = scores + (uint64_t)(kvh * G + h) * row_stride;
             double seq = 0.0;
             for (uint32_t base = 0; base < ngroups; base += 64) {
                 float ps = 0.0f;
@@ -377,131 +351,121 @@ __global__ __launch_bounds__(kPvThreads) void attn_pv_kernel(
                     ps = (e[0] + e[1]) + (e[2] + e[3]);
                 }
                 const uint32_t n = ngroups - base < 64 ? ngroups - base : 64;
-                for (uint32_t l = 0; l < n; ++l) seq += (double)__shfl(ps, (int)l, 64);
+                for (uint32_t l = 0; l < n; ++l) seq += (double)readlane_f(ps, (int)l);
             }
             inv = (float)(1.0 / seq);
         }
-        if (lane == 0) stat[2 * h + 1] = inv;
-    }
-    __syncthreads();
-    // P.V with p = e * inverse (math.rs:313-315, 478-480), one f64 chain per
-    // dimension over the lane's groups, and the certificate's statistics of
-    // the terms (pv_certified)
-    if (active) {
-        for (uint32_t h = h0; h < G; h += hstep) {
-            const float m = stat[2 * h], inv = stat[2 * h + 1];
-            const float* srow = scores + (uint64_t)(kvh * G + h) * row_stride;
-            double a[4] = {0.0, 0.0, 0.0, 0.0};
-            float as[4] = {0.0f, 0.0f, 0.0f, 0.0f}, ws[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-            float mn[4] = {INFINITY, INFINITY, INFINITY, INFINITY};
-            auto add = [&](const float (&e)[4], const float4 (&v)[4], uint32_t g) {
-                const uint32_t nt = count - 4 * g < 4 ? count - 4 * g : 4;  // the reference adds `count` columns
-                double a0[4];
+        // P.V with p = e * inverse (math.rs:313-315, 478-480), one f64 chain
+        // per dimension over the lane's groups, and the certificate's
+        // statistics of the terms (pv_interval, f64_sum_exact)
+        double a[4] = {0.0, 0.0, 0.0, 0.0};
+        float as[4] = {0.0f, 0.0f, 0.0f, 0.0f}, ws[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        float mn[4] = {INFINITY, INFINITY, INFINITY, INFINITY};
+        // the reference adds `count` columns: a column past it (in the last
+        // group) has e = 0 and v = 0, a +0 term, which leaves the f64 sum (never
+        // -0) and the magnitude sums unchanged and is kept out of the minimum
+        auto add = [&](const float (&e)[4], const float4 (&v)[4], uint32_t g) {
+            double a0[4];
 #pragma unroll
-                for (uint32_t d = 0; d < 4; ++d) a0[d] = a[d];
+            for (uint32_t d = 0; d < 4; ++d) a0[d] = a[d];
 #pragma unroll
-                for (uint32_t j = 0; j < 4; ++j) {
-                    if (j >= nt) break;
-                    const float p = e[j] * inv;
-                    const float t[4] = {p * v[j].x, p * v[j].y, p * v[j].z, p * v[j].w};
+            for (uint32_t j = 0; j < 4; ++j) {
+                const float p = e[j] * inv;
+                const float t[4] = {p * v[j].x, p * v[j].y, p * v[j].z, p * v[j].w};
+                const bool live = 4 * g + j < count;
 #pragma unroll
-                    for (uint32_t d = 0; d < 4; ++d) {
-                        a[d] += (double)t[d];
-                        as[d] += fabsf(t[d]);
-                        mn[d] = fminf(mn[d], fabsf(t[d]));
-                    }
+                for (uint32_t d = 0; d < 4; ++d) {
+                    a[d] += (double)t[d];
+                    as[d] += fabsf(t[d]);
+                    mn[d] = fminf(mn[d], live ? fabsf(t[d]) : INFINITY);
                 }
-                // the group's sum as the lane sum's growth (within 4 2^-53 A of it)
-                const float wg = (float)(ngroups - 1 - g);
-#pragma unroll
-                for (uint32_t d = 0; d < 4; ++d) ws[d] = __builtin_fmaf(wg, fabsf((float)(a[d] - a0[d])), ws[d]);
-            };
-#pragma unroll
-            for (uint32_t k = 0; k < kPvRegGroups; ++k) {
-                const uint32_t g = g0 + k * gstride;
-                if (g >= ngroups) break;
-                float e[4];
-                if (h == h0) {
-#pragma unroll
-                    for (uint32_t j = 0; j < 4; ++j) e[j] = er[k][j];
-                } else {
-                    exp_group(*(const float4*)(srow + 4 * g), 4 * g, count, m, e);
-                }
-                add(e, vr[k], g);
             }
-            for (uint32_t g = g0 + kPvRegGroups * gstride; g < ngroups; g += gstride) {
-                float e[4];
-                exp_group(*(const float4*)(srow + 4 * g), 4 * g, count, m, e);
-                float4 v[4];
+            // the group's sum as the lane sum's growth (within 4 2^-53 A of it)
+            const float wg = (float)(ngroups - 1 - g);
 #pragma unroll
-                for (uint32_t j = 0; j < 4; ++j)
-                    v[j] = 4 * g + j < count ? vsrc[4 * g + j] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-                add(e, v, g);
-            }
-            // per 16-lane row (DPP); the rows meet in the final pass
+            for (uint32_t d = 0; d < 4; ++d) ws[d] = __builtin_fmaf(wg, fabsf((float)(a[d] - a0[d])), ws[d]);
+        };
 #pragma unroll
-            for (uint32_t d = 0; d < 4; ++d) {
-                const double sum = row16_sum_f64(a[d]);
-                const float wsum = row16_sum_f(ws[d]);
-                const float ab = row16_sum_f(as[d]);
-                const float mi = row16_min_f(mn[d]);
-                if ((lane & 15) == 0) rec[((h * wph + w) * 4 + d) * 4 + (lane >> 4)] = PvRec{sum, wsum, ab, mi, 0.0f};
+        for (uint32_t k = 0; k < kPvRegGroups; ++k) {
+            const uint32_t g = lane + 64 * k;
+            if (g >= ngroups) break;
+            add(er[k], vr[k], g);
+        }
+        for (uint32_t g = lane + 64 * kPvRegGroups; g < ngroups; g += 64) {
+            float e[4];
+            exp_group(*(const float4*)(srow + 4 * g), 4 * g, count, m, e);
+            float4 v[4];
+#pragma unroll
+            for (uint32_t j = 0; j < 4; ++j)
+                v[j] = 4 * g + j < count ? vsrc[4 * g + j] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            add(e, v, g);
+        }
+        // each output: the wave's sums (the four outputs' reductions side by
+        // side; every lane gets the same values, so the branches below are
+        // wave-uniform), certified or repeated in the reference's column
+        // order: the lanes compute kPvRepTerms terms per round into the wave's
+        // LDS buffer, and lane 0 adds them in order, sixteen loads ahead of its
+        // adds
+        double s16[4], C16[4];
+        const float ka = (float)pv_coef_a(tl, (double)ngroups);
+#pragma unroll
+        for (uint32_t j = 0; j < 4; ++j) {
+            s16[j] = row16_sum_f64(a[j]);
+            C16[j] = (double)row16_sum_f(4.0f * ws[j] + ka * as[j]);
+        }
+        float out[4];
+        bool cert[4];
+#pragma unroll
+        for (uint32_t j = 0; j < 4; ++j) {
+            const double s = rows_sum_f64(s16[j]);
+            out[j] = (float)s;
+            cert[j] = pv_interval(s, rows_sum_f64(C16[j]));
+            if (!cert[j]) {  // (rare) every order exact?
+                const double A = rows_sum_f64((double)row16_sum_f(as[j]));
+                const float m16 = row16_min_f(mn[j]);
+                cert[j] = f64_sum_exact(A, fminf(fminf(readlane_f(m16, 0), readlane_f(m16, 16)),
+                                                 fminf(readlane_f(m16, 32), readlane_f(m16, 48))));
             }
         }
-    }
-    __syncthreads();
-    // each output: certified, or repeated in the reference's column order by
-    // one wave: its lanes compute kPvRepTerms terms per round into its LDS
-    // buffer, and lane 0 adds them in order, sixteen loads ahead of its adds
-    const double tl = 4.0 * ((ngroups + gstride - 1) / gstride);  // columns per lane
-    for (uint32_t o = wave; o < G * 4; o += kPvWaves) {  // (wave-uniform)
-        const uint32_t h = o / 4, j = o % 4;
-        double sum = 0.0, A = 0.0, ws = 0.0;
-        float M = INFINITY;
-        for (uint32_t v = 0; v < 4 * wph; ++v) {  // (wave part, row) in order
-            const PvRec r = rec[((h * wph + v / 4) * 4 + j) * 4 + v % 4];
-            sum += r.sum;
-            A += (double)r.abs_sum;
-            ws += (double)r.wsum;
-            M = fminf(M, r.min_abs);
-        }
-        float res = (float)sum;
-        if (repeat_all || !pv_certified(sum, A, ws, M, tl, (double)ngroups)) {
-            const float m = stat[2 * h], inv = stat[2 * h + 1];
-            const float* srow = scores + (uint64_t)(kvh * G + h) * row_stride;
-            const float* vcol = vc + v_cache_index(kvh, hd, d0 + j, 0, max_context);
-            double* buf = rep + wave * kPvRepTerms;
-            double seq = 0.0;
-            for (uint32_t base = 0; base < ngroups; base += kPvRepTerms / 4) {
-                const uint32_t g = base + lane;
-                if (g < ngroups) {
-                    float e[4];
-                    exp_group(*(const float4*)(srow + 4 * g), 4 * g, count, m, e);
 #pragma unroll
-                    for (uint32_t jj = 0; jj < 4; ++jj) {
-                        const uint32_t t = 4 * g + jj;
-                        buf[4 * lane + jj] = t < count ? (double)((e[jj] * inv) * vcol[(uint64_t)t * 4]) : 0.0;
+        for (uint32_t j = 0; j < 4; ++j) {
+            if (repeat_all || !cert[j]) {
+                const float* vcol = vc + v_cache_index(kvh, hd, d0 + j, 0, max_context);
+                double seq = 0.0;
+                for (uint32_t base = 0; base < ngroups; base += kPvRepTerms / 4) {
+                    const uint32_t g = base + lane;
+                    if (g < ngroups) {
+                        float e[4];
+                        exp_group(*(const float4*)(srow + 4 * g), 4 * g, count, m, e);
+#pragma unroll
+                        for (uint32_t jj = 0; jj < 4; ++jj) {
+                            const uint32_t t = 4 * g + jj;
+                            buf[4 * lane + jj] = t < count ? (double)((e[jj] * inv) * vcol[(uint64_t)t * 4]) : 0.0;
+                        }
                     }
-                }
-                // one wave's LDS operations are performed in order
-                if (lane == 0) {
-                    const uint32_t nt = count - 4 * base < kPvRepTerms ? count - 4 * base : kPvRepTerms;
-                    uint32_t i = 0;
-                    for (; i + 16 <= nt; i += 16) {
-                        double x[16];
+                    // one wave's LDS operations are performed in order
+                    if (lane == 0) {
+                        const uint32_t nt = count - 4 * base < kPvRepTerms ? count - 4 * base : kPvRepTerms;
+                        uint32_t i = 0;
+                        for (; i + 16 <= nt; i += 16) {
+                            double x[16];
 #pragma unroll
-                        for (uint32_t k = 0; k < 16; ++k) x[k] = buf[i + k];
+                            for (uint32_t k = 0; k < 16; ++k) x[k] = buf[i + k];
 #pragma unroll
-                        for (uint32_t k = 0; k < 16; ++k) seq += x[k];
+                            for (uint32_t k = 0; k < 16; ++k) seq += x[k];
+                        }
+                        for (; i < nt; ++i) seq += buf[i];
                     }
-                    for (; i < nt; ++i) seq += buf[i];
+                    __builtin_amdgcn_wave_barrier();
                 }
+                out[j] = (float)readlane_d(seq, 0);
             }
-            res = (float)__shfl(seq, 0, 64);
         }
         if (lane == 0) {
-            if (!finite(res)) report_error(err_word, model_key(layer, kStAttnOut, 0));  // math.rs:494
-            att[(kvh * G + h) * hd + d0 + j] = res;
+#pragma unroll
+            for (uint32_t j = 0; j < 4; ++j)
+                if (!finite(out[j])) report_error(err_word, model_key(layer, kStAttnOut, 0));  // math.rs:494
+            *(float4*)(att + (uint64_t)row * hd + d0) = make_float4(out[0], out[1], out[2], out[3]);
         }
     }
 }
@@ -639,7 +603,7 @@ hipError_t LlamaModel::create(const LlamaDims& dims, const LlamaHostTensors& t, 
     // the limits only grow, so models of other shapes in the process keep working
     static LdsLimit pv_limit, scores_limit;
     const uint32_t G = (uint32_t)(d.heads / d.kv_heads);
-    hipError_t e = pv_limit.raise((const void*)attn_pv_kernel, attn_pv_lds(G).total * sizeof(float));
+    hipError_t e = pv_limit.raise((const void*)attn_pv_kernel, attn_pv_lds_bytes(G));
     if (e == hipSuccess) e = scores_limit.raise((const void*)attn_scores_kernel, attn_scores_lds(G, (uint32_t)hd));
     if (e == hipSuccess) e = hipMalloc((void**)&rope_tab, tab.size() * sizeof(float));
     if (e == hipSuccess) e = hipMemcpy(rope_tab, tab.data(), tab.size() * sizeof(float), hipMemcpyHostToDevice);
@@ -755,7 +719,7 @@ hipError_t LlamaModel::step(float* hidden, uint64_t position, float* embedding_o
     const float scale = d.attention_scale != 0.0f ? d.attention_scale : 1.0f / sqrtf((float)hd);
     const float* tab = rope_tab + position * hd;
     const size_t lds_scores = attn_scores_lds((uint32_t)(H / KVH), (uint32_t)hd);
-    const size_t lds_pv = attn_pv_lds((uint32_t)(H / KVH)).total * sizeof(float);
+    const size_t lds_pv = attn_pv_lds_bytes((uint32_t)(H / KVH));
     const uint32_t cstride = (uint32_t)((d.max_context + kAttnChunk - 1) / kAttnChunk);
     hipError_t e = hipSuccess;
     for (uint64_t l = 0; l < d.n_layers && e == hipSuccess; ++l) {
@@ -784,7 +748,8 @@ hipError_t LlamaModel::step(float* hidden, uint64_t position, float* embedding_o
                            tab, kc, vc, (uint32_t)d.max_context, (uint32_t)fresh, (uint32_t)H, (uint32_t)KVH,
                            (uint32_t)hd, scale, scores, (uint32_t)row_stride, cmax, cstride, err_word, lay,
                            repeat_all ? 1u : 0u);
-        hipLaunchKernelGGL(attn_pv_kernel, dim3((uint32_t)(hd / kPvDims), (uint32_t)KVH), dim3(kPvThreads), lds_pv, s,
+        hipLaunchKernelGGL(attn_pv_kernel, dim3((uint32_t)(hd / kPvDims), (uint32_t)KVH),
+                           dim3(64 * pv_waves((uint32_t)(H / KVH))), lds_pv, s,
                            scores, cmax, cstride, nchunks, vc, (uint32_t)d.max_context, (uint32_t)count, (uint32_t)H,
                            (uint32_t)KVH, (uint32_t)hd, (uint32_t)row_stride, att, err_word, lay,
                            repeat_all ? 1u : 0u);

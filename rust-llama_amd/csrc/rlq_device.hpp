@@ -119,15 +119,26 @@ __device__ __forceinline__ double row16_sum_f64(double v) {
     return v;
 }
 
-// Sum over all 64 lanes; every lane gets it.
+// The value of lane l (uniform: the wave's scalar read of one lane).
+__device__ __forceinline__ float readlane_f(float v, int l) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
+__device__ __forceinline__ double readlane_d(double v, int l) {
+    const unsigned long long u = (unsigned long long)__double_as_longlong(v);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)u, l);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(u >> 32), l);
+    return __longlong_as_double((long long)(((unsigned long long)hi << 32) | lo));
+}
+
+// Sum over all 64 lanes ((row 0 + row 1) + (row 2 + row 3) of the 16-lane
+// row sums); every lane gets it.  These wave reductions read the rows with
+// scalar lane reads: call them with every lane of the wave active.
 __device__ __forceinline__ float wave_sum(float v) {
     v += dpp_f<kQuadXor1>(v);
     v += dpp_f<kQuadXor2>(v);
     v += dpp_f<kRowHalfMirror>(v);
     v += dpp_f<kRowRor8>(v);
-    v += __shfl_xor(v, 16, 64);
-    v += __shfl_xor(v, 32, 64);
-    return v;
+    return (readlane_f(v, 0) + readlane_f(v, 16)) + (readlane_f(v, 32) + readlane_f(v, 48));
 }
 
 __device__ __forceinline__ int32_t wave_sum_i(int32_t v) {
@@ -144,22 +155,21 @@ __device__ __forceinline__ float wave_max(float v) {
     for (int m = 1; m < 64; m <<= 1) v = fmaxf(v, __shfl_xor(v, m, 64));
     return v;
 }
+// The four 16-lane rows' (row-uniform) values combined as (row 0 + row 1) +
+// (row 2 + row 3).
+__device__ __forceinline__ double rows_sum_f64(double v) {
+    return (readlane_d(v, 0) + readlane_d(v, 16)) + (readlane_d(v, 32) + readlane_d(v, 48));
+}
 // Sum over all 64 lanes in a fixed order (the 16-lane rows by DPP, then the
 // rows); every lane gets it.
-__device__ __forceinline__ double wave_sum_f64(double v) {
-    v = row16_sum_f64(v);
-    v += __shfl_xor(v, 16, 64);
-    v += __shfl_xor(v, 32, 64);
-    return v;
-}
+__device__ __forceinline__ double wave_sum_f64(double v) { return rows_sum_f64(row16_sum_f64(v)); }
 // Maximum over all 64 lanes (DPP inside the rows, then the rows).
 __device__ __forceinline__ float wave_max_dpp(float v) {
     v = fmaxf(v, dpp_f<kQuadXor1>(v));
     v = fmaxf(v, dpp_f<kQuadXor2>(v));
     v = fmaxf(v, dpp_f<kRowHalfMirror>(v));
     v = fmaxf(v, dpp_f<kRowRor8>(v));
-    v = fmaxf(v, __shfl_xor(v, 16, 64));
-    return fmaxf(v, __shfl_xor(v, 32, 64));
+    return fmaxf(fmaxf(readlane_f(v, 0), readlane_f(v, 16)), fmaxf(readlane_f(v, 32), readlane_f(v, 48)));
 }
 __device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
     for (int m = 1; m < 64; m <<= 1) {
@@ -214,12 +224,14 @@ __device__ __forceinline__ float sse2_exp(float x) {
     const float first = __uint_as_float(0x3c072010u) * b + __uint_as_float(0x3d2b9f17u);
     const float second = __uint_as_float(0x3e2aaf33u) * b + __uint_as_float(0x3efffedbu);
     const float polynomial = (first * squared + second) * squared + __uint_as_float(0x3f7ffff6u) * b;
-    if (!(fabsf(n) > 126.0f)) return polynomial * scale + scale;
+    // both branches computed and one selected (no divergent branch, so the
+    // exponentials of a lane interleave)
+    const float plain = polynomial * scale + scale;
     const uint32_t shift = n <= 0.0f ? 0x82000000u : 0u;
     const float high = __uint_as_float(shift + 0x7f000000u);
     const float low = __uint_as_float(exponent - shift);
-    if (fabsf(n) > 192.0f) return high * high;
-    return (low * polynomial + low) * high;
+    const float wide = fabsf(n) > 192.0f ? high * high : (low * polynomial + low) * high;
+    return fabsf(n) > 126.0f ? wide : plain;
 }
 
 // ---- device error word ---------------------------------------------------
