@@ -35,6 +35,7 @@ constexpr int kAttnThreads = 256;
 constexpr uint32_t kAttnMaxHd = 256;  // head dimension limit
 constexpr uint32_t kScKeyRegs = kAttnMaxHd * kAttnChunk / 4 / kAttnThreads;  // float4 of a chunk's keys per thread
 constexpr uint32_t kScKeyPad = 16;  // floats after each key row in LDS
+static_assert(kAttnMaxHd <= kAttnThreads, "the new key row: one element per thread");
 
 constexpr uint32_t kPvDims = 4;       // head dimensions per P.V workgroup: one float4 of each value row
 constexpr uint32_t kPvMaxWaves = 8;   // waves per P.V workgroup: one per query head of the kv head
@@ -134,23 +135,29 @@ __global__ __launch_bounds__(kAttnThreads) void attn_scores_kernel(
         if (t < n_here && t0 + t != fresh)
             kr[k] = load_stream_f4(kc + (uint64_t)(t0 + t) * kvw + kvh * hd + 4 * (i % q4));
     }
+    // the new key's pair and value element of this thread (hd <= the
+    // workgroup's threads), loaded with the cached keys
+    const bool has_fresh = fresh >= t0 && fresh < t0 + kAttnChunk;
+    float fx = 0.0f, fy = 0.0f, fsn = 0.0f, fcs = 0.0f, fv = 0.0f;
+    if (has_fresh) {
+        const float* kin = qkv + width + kvh * hd;
+        if (tid < hd / 2) fx = kin[2 * tid], fy = kin[2 * tid + 1], fsn = rope_tab[2 * tid], fcs = rope_tab[2 * tid + 1];
+        if (tid < hd) fv = qkv[width + kvw + kvh * hd + tid];
+    }
     for (uint32_t i = tid; i < G * hd / 2; i += kAttnThreads) {
         const uint32_t h = i / (hd / 2), p = i % (hd / 2);
         rope_pair(qkv + (kvh * G + h) * hd, rope_tab, p, q_s + h * hd);
     }
-    if (fresh >= t0 && fresh < t0 + kAttnChunk) {
-        float* krow = k_s + (fresh - t0) * ks;
-        const float* kin = qkv + width + kvh * hd;
-        const float* vin = qkv + width + kvw + kvh * hd;
-        for (uint32_t p = tid; p < hd / 2; p += kAttnThreads) {
-            const float x = kin[2 * p], y = kin[2 * p + 1], sn = rope_tab[2 * p], cs = rope_tab[2 * p + 1];
-            const float o0 = x * cs - y * sn, o1 = x * sn + y * cs;
-            krow[2 * p] = o0;
-            krow[2 * p + 1] = o1;
-            kc[(uint64_t)fresh * kvw + kvh * hd + 2 * p] = o0;
-            kc[(uint64_t)fresh * kvw + kvh * hd + 2 * p + 1] = o1;
+    if (has_fresh) {
+        if (tid < hd / 2) {
+            const float o0 = fx * fcs - fy * fsn, o1 = fx * fsn + fy * fcs;
+            float* krow = k_s + (fresh - t0) * ks;
+            krow[2 * tid] = o0;
+            krow[2 * tid + 1] = o1;
+            kc[(uint64_t)fresh * kvw + kvh * hd + 2 * tid] = o0;
+            kc[(uint64_t)fresh * kvw + kvh * hd + 2 * tid + 1] = o1;
         }
-        for (uint32_t d = tid; d < hd; d += kAttnThreads) vc[v_cache_index(kvh, hd, d, fresh, max_context)] = vin[d];
+        if (tid < hd) vc[v_cache_index(kvh, hd, tid, fresh, max_context)] = fv;
     }
 #pragma unroll
     for (uint32_t k = 0; k < kScKeyRegs; ++k) {
@@ -275,6 +282,10 @@ __device__ __forceinline__ bool pv_interval(double sum, double C) {
     return (float)(sum - B) == (float)(sum + B);
 }
 
+__device__ __forceinline__ float f4_at(const float4& v, uint32_t j) {
+    return j == 0 ? v.x : j == 1 ? v.y : j == 2 ? v.z : v.w;
+}
+
 // Sum / minimum over each 16-lane row (DPP only).
 __device__ __forceinline__ float row16_sum_f(float v) {
     v += dpp_f<kQuadXor1>(v);
@@ -360,10 +371,9 @@ __global__ __launch_bounds__(kPvMaxWaves * 64) void attn_pv_kernel(
         // statistics of the terms (pv_interval, f64_sum_exact)
         double a[4] = {0.0, 0.0, 0.0, 0.0};
         float as[4] = {0.0f, 0.0f, 0.0f, 0.0f}, ws[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-        float mn[4] = {INFINITY, INFINITY, INFINITY, INFINITY};
         // the reference adds `count` columns: a column past it (in the last
         // group) has e = 0 and v = 0, a +0 term, which leaves the f64 sum (never
-        // -0) and the magnitude sums unchanged and is kept out of the minimum
+        // -0) and the magnitude sums unchanged
         auto add = [&](const float (&e)[4], const float4 (&v)[4], uint32_t g) {
             double a0[4];
 #pragma unroll
@@ -372,12 +382,10 @@ __global__ __launch_bounds__(kPvMaxWaves * 64) void attn_pv_kernel(
             for (uint32_t j = 0; j < 4; ++j) {
                 const float p = e[j] * inv;
                 const float t[4] = {p * v[j].x, p * v[j].y, p * v[j].z, p * v[j].w};
-                const bool live = 4 * g + j < count;
 #pragma unroll
                 for (uint32_t d = 0; d < 4; ++d) {
                     a[d] += (double)t[d];
                     as[d] += fabsf(t[d]);
-                    mn[d] = fminf(mn[d], live ? fabsf(t[d]) : INFINITY);
                 }
             }
             // the group's sum as the lane sum's growth (within 4 2^-53 A of it)
@@ -420,9 +428,34 @@ __global__ __launch_bounds__(kPvMaxWaves * 64) void attn_pv_kernel(
             const double s = rows_sum_f64(s16[j]);
             out[j] = (float)s;
             cert[j] = pv_interval(s, rows_sum_f64(C16[j]));
-            if (!cert[j]) {  // (rare) every order exact?
+        }
+#pragma unroll
+        for (uint32_t j = 0; j < 4; ++j) {
+            if (!cert[j]) {  // (rare) every order exact?  The smallest |term| of the lane's columns, again
+                float mn = INFINITY;
+                auto low = [&](const float (&e)[4], const float4 (&v)[4], uint32_t g) {
+#pragma unroll
+                    for (uint32_t jj = 0; jj < 4; ++jj) {
+                        const float t = (e[jj] * inv) * f4_at(v[jj], j);
+                        mn = fminf(mn, 4 * g + jj < count ? fabsf(t) : INFINITY);
+                    }
+                };
+#pragma unroll
+                for (uint32_t k = 0; k < kPvRegGroups; ++k) {
+                    const uint32_t g = lane + 64 * k;
+                    if (g < ngroups) low(er[k], vr[k], g);
+                }
+                for (uint32_t g = lane + 64 * kPvRegGroups; g < ngroups; g += 64) {
+                    float e[4];
+                    exp_group(*(const float4*)(srow + 4 * g), 4 * g, count, m, e);
+                    float4 v[4];
+#pragma unroll
+                    for (uint32_t jj = 0; jj < 4; ++jj)
+                        v[jj] = 4 * g + jj < count ? vsrc[4 * g + jj] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                    low(e, v, g);
+                }
                 const double A = rows_sum_f64((double)row16_sum_f(as[j]));
-                const float m16 = row16_min_f(mn[j]);
+                const float m16 = row16_min_f(mn);
                 cert[j] = f64_sum_exact(A, fminf(fminf(readlane_f(m16, 0), readlane_f(m16, 16)),
                                                  fminf(readlane_f(m16, 32), readlane_f(m16, 48))));
             }
