@@ -1230,10 +1230,21 @@ __device__ __forceinline__ void park_terms(uint8_t* pk, uint32_t nb, uint32_t bl
     ((float*)(pk + nb * 512))[blk * 16 + (lane & 15)] = mn;
 }
 
+// Lane n of 16-lane row 0 gets v of lane n + 16 r (r = 1, 2, 3); every lane
+// of the wave must be active.
+__device__ __forceinline__ float row_from(float v, int r) {
+    const unsigned u = __float_as_uint(v);
+    if (r == 1) return __uint_as_float(__builtin_amdgcn_permlane16_swap(u, u, false, false)[1]);
+    if (r == 2) return __uint_as_float(__builtin_amdgcn_permlane32_swap(u, u, false, false)[1]);
+    const unsigned r1 = __builtin_amdgcn_permlane16_swap(u, u, false, false)[1];  // rows 1, 1, 3, 3
+    return __uint_as_float(__builtin_amdgcn_permlane32_swap(r1, r1, false, false)[1]);
+}
+
 // The row's f32 in the reference's order from its parked terms (nb blocks;
 // pk the slot's records): lanes[l] over the blocks in order, sum minus the
 // mins terms in order, then sum + lanes[0..7].  Lane kq = 0 of row n returns
-// it; the four lanes (n, kq) of every row of the wave must take part.
+// it (the other lanes return other sums); every lane of the wave must take
+// part.
 __device__ __forceinline__ float exact_row_sum(const uint8_t* pk, uint32_t nb, uint32_t lane) {
     const float2* p = (const float2*)pk + lane;                    // classes 2 kq, 2 kq + 1 of row n
     const float* q = (const float*)(pk + nb * 512) + (lane & 15);  // the mins terms
@@ -1260,12 +1271,19 @@ __device__ __forceinline__ float exact_row_sum(const uint8_t* pk, uint32_t nb, u
         l1 += v.y;
         s -= q[b * 16];
     }
-    const uint32_t n = lane & 15;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        s += __shfl(l0, (int)(n + 16 * j), 64);
-        s += __shfl(l1, (int)(n + 16 * j), 64);
-    }
+    // lane n of row 0 takes the rows' lanes n + 16 j in order j = 0..3 by lane
+    // swaps (v_permlane16_swap brings row 1 to row 0, v_permlane32_swap rows 2
+    // and 3): the order of the reference's lanes[0..7]
+    const float a1 = row_from(l0, 1), a2 = row_from(l0, 2), a3 = row_from(l0, 3);
+    const float b1 = row_from(l1, 1), b2 = row_from(l1, 2), b3 = row_from(l1, 3);
+    s += l0;
+    s += l1;
+    s += a1;
+    s += b1;
+    s += a2;
+    s += b2;
+    s += a3;
+    s += b3;
     return s;
 }
 
