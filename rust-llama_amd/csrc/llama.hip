@@ -15,8 +15,8 @@
 // orders whose f32 results are certified equal to the reference's (or
 // repeated in its order: certified_f32, pv_interval, f64_sum_exact), so scores,
 // probabilities and attention outputs are bit-exact.  The one-column
-// matvecs of every weight type but Q3_K combine their exact integer block
-// sums in the reference's f32 order (Q3_K in the kernel's own).
+// matvecs of every weight type combine their exact integer block sums in the
+// reference's f32 order.
 #include <math.h>
 #include <stdlib.h>
 

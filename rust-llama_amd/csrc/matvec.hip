@@ -2444,6 +2444,268 @@ __global__ __launch_bounds__(W * 64) void q8_0_mv_ks_kernel(MvArgs a) {
     fold_argmax(a, lds, L, b0 + 1, best1);
     finish_argmax(a, lds, L);
 }
+// Q3_K, one column, in the reference's f32 order (matvec_extra.rs:235-248,
+// 287-292): eight lane accumulators lanes[j % 8] per row over all blocks,
+// integers[l] the sum over the scale groups g of scale_g times the group's
+// dot over the elements j with j % 8 == l, then sum = 0 + lanes[0] + ... +
+// lanes[7].  The chunk loads and B operands are those of the K16 kernels
+// (lane (n, kq), operand s: elements 128 (kq / 2) + 32 s + 16 (kq % 2) + i of
+// row n, scale group 8 (kq / 2) + 2 s + kq % 2); the A rows split each
+// group's dot by lane class as in q6k_mv_one_kernel: A row r holds class
+// c = r % 8 of K quarter r / 8 (first MFMA of a pair) or 2 + r / 8 (second),
+// the activations of that quarter's elements masked to the bytes c and c + 8.
+// Output i of the pair in lane (n, kq) is the dot over class 4 (kq % 2) + i
+// of scale group 2 s + kq / 2 (first) or 8 + 2 s + kq / 2 (second); the lanes
+// kq and kq ^ 2 hold the other eight groups.  A wave takes whole tiles and
+// walks their blocks in order, so the accumulators stay in registers.
+template <int W, int D, bool DBG>
+__global__ __launch_bounds__(W * 64) void q3k_mv_one_kernel(MvArgs a) {
+    RLQ_MV_PROLOGUE(kQ3_K, a.nb)
+    const uint32_t nb = a.nb;
+    K16Step<kQ3_K> buf[D];
+    auto issue = [&](K16Step<kQ3_K>& st) {
+        k16_issue<kQ3_K>(st, a.w + ((uint64_t)ld_tile * nb + ld_chunk) * kQ3KChunk, lane, n, kq);
+        next_load();
+    };
+#pragma unroll
+    for (int i = 0; i < D; ++i) issue(buf[i]);
+
+    const bool ok = a.x ? stage_q8k<W, kBsNone>(a, lds, L, wave, xv) : stage_planes<W>(a, lds, L, kQ3_K);
+    if (!ok) return finish_argmax(a, lds, L);
+    if (a.zero_pair) return zero_wave_tiles(a, gw, tw, n, kq);
+
+    const uint32_t hsh = 4 * (kq >> 1), sb0 = kq >> 1;  // high-mask bits; scale byte of the output groups
+    const uint32_t cls = n & 7, qsel = n >> 3;
+    const bool live0 = kq == qsel, live1 = kq == 2 + qsel;
+    const uint8_t* a_ptr = live0 || live1 ? lds + 128 * (kq >> 1) + 16 * (kq & 1) : lds + L.zero_off;
+    const uint32_t a_step = live0 || live1 ? 256 : 0;
+    const uint32_t byte = 0xffu << (8 * (cls & 3));
+    uint32_t m0[4], m1[4];  // the masks of the two MFMAs (zero where not live)
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+        const uint32_t mk = (uint32_t)(w & 1) == (cls >> 2) ? byte : 0u;
+        m0[w] = live0 ? mk : 0u;
+        m1[w] = live1 ? mk : 0u;
+    }
+
+    float lanes[4] = {0.0f, 0.0f, 0.0f, 0.0f};  // classes 4 (kq % 2) + i
+    unsigned long long best = 0;
+    uint32_t tile = gw, blk = 0;
+    auto compute = [&](const K16Step<kQ3_K>& cur) {
+        const K16Ops<kQ3_K> o = k16_ops<kQ3_K>(cur, hsh);
+        const uint8_t* p = a_ptr + blk * a_step;
+        int32_t I[4] = {0, 0, 0, 0};
+#pragma unroll
+        for (int sft = 0; sft < 4; ++sft) {
+            const uint4 x = *(const uint4*)(p + 32 * sft);
+            const i32x4 A0 = {(int)(x.x & m0[0]), (int)(x.y & m0[1]), (int)(x.z & m0[2]), (int)(x.w & m0[3])};
+            const i32x4 A1 = {(int)(x.x & m1[0]), (int)(x.y & m1[1]), (int)(x.z & m1[2]), (int)(x.w & m1[3])};
+            const i32x4 d0 = mfma_i8(A0, o.wv[sft]), d1 = mfma_i8(A1, o.wv[sft]);
+            // the signed 6-bit scales of groups 2 s + kq / 2 and 8 + 2 s + kq / 2
+            const int32_t sa = sbyte(o.c[sft >> 1], 2 * (sft & 1) + sb0);
+            const int32_t sb = sbyte(o.c[2 + (sft >> 1)], 2 * (sft & 1) + sb0);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) I[i] = mad24(sa, d0[i], mad24(sb, d1[i], I[i]));
+        }
+        const float d = half_to_float(cur.d) * *(const float*)(lds + L.d_off + blk * 32);  // :246
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            I[i] = sum_xor32(I[i]);
+            lanes[i] += d * (float)I[i];  // matvec_extra.rs:287-289
+        }
+        if (DBG) {
+            const int32_t It = sum_xor16(I[0] + I[1] + I[2] + I[3]);
+            const uint32_t row = tile * kTileRows + n;
+            if (kq == 0 && row < a.rows) {
+                a.dbg_isum[(uint64_t)row * nb + blk] = It;
+                a.dbg_imin[(uint64_t)row * nb + blk] = 0;
+            }
+        }
+        if (++blk == nb) {  // sum = 0 + lanes[0] + ... + lanes[7] (:290-292)
+            float sum = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) sum += __shfl(lanes[i], (int)n, 64);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) sum += __shfl(lanes[i], (int)(n + 16), 64);
+            if (kq == 0) store_out(a, tile * kTileRows + n, 0, sum, best);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) lanes[i] = 0.0f;
+            blk = 0;
+            tile += tw;
+        }
+    };
+    pipeline<D>(steps, buf, issue, compute);
+    fold_argmax(a, lds, L, kq, best);
+    finish_argmax(a, lds, L);
+}
+
+// Q3_K, one column, the blocks of each tile split over KS waves: the class
+// dots of q3k_mv_one_kernel, each block's four class terms d * integers[l]
+// (rounded to f32, matvec_extra.rs:287-289) parked in LDS per lane (classes
+// 0..3 in lane kq = 0 of row n, 4..7 in lane kq = 1), and after the last
+// step one wave per tile slot forms each row's sum in the reference's order:
+// lanes[l] over the blocks in order, then sum = 0 + lanes[0] + ... + lanes[7].
+// LDS after the Q8_K image: [tmax][TS][nb][32] float4.  BAL: the balanced
+// deal over a.deal_cus CUs (balanced_deal; one tile per slot, a half tile
+// read by lane pairs and stored by its own half).
+__host__ __device__ inline uint32_t q3_part_off(uint32_t cols) { return (lds_map(kQ3_K, cols, 1).total + 15u) & ~15u; }
+__host__ __device__ inline uint32_t q3_split_lds(uint32_t cols, uint32_t tmax, uint32_t ts) {
+    return q3_part_off(cols) + tmax * ts * (cols / 256) * 512u;
+}
+
+template <int W, int KS, int D, bool DBG, bool BAL = false>
+__global__ __launch_bounds__(W * 64) void q3k_mv_split_kernel(MvArgs a) {
+    constexpr int TS = W / KS;
+    static_assert(!BAL || TS == 2 || TS == 4, "the balanced deal takes two or four tile slots");
+    if (!mv_enter(a)) return;
+    extern __shared__ __align__(16) uint8_t lds[];
+    const LdsMap L = lds_map(kQ3_K, a.cols, a.batch);
+    const uint32_t lane = threadIdx.x & 63, n = lane & 15, kq = lane >> 4;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t ts = wave / KS, kp = wave % KS;
+    const uint32_t nb = a.nb, ntiles = a.ntiles;
+    const uint32_t tstride = gridDim.x * TS, t0 = blockIdx.x * TS + ts;
+    uint32_t tmax, my_tiles, half = 0, hsel = 0, bt = 0;
+    if constexpr (BAL) {
+        const TileDeal dl = balanced_deal<TS>(a.deal_cus, ntiles, ts);
+        tmax = 1, my_tiles = dl.count, bt = dl.tile, half = dl.half, hsel = dl.hsel;
+    } else {
+        tmax = (ntiles + tstride - 1) / tstride;
+        my_tiles = t0 < ntiles ? (ntiles - 1 - t0) / tstride + 1 : 0;
+    }
+    const uint32_t nh = (n & 7) | (hsel << 3);  // the row a lane loads in a half tile
+    const uint32_t bpt = kp < nb ? (nb - 1 - kp) / KS + 1 : 0;  // blocks of each tile this wave takes
+    const uint32_t steps = my_tiles * bpt;
+    float4* park = (float4*)(lds + q3_part_off(a.cols));
+
+    if (threadIdx.x < 16) *(uint4*)(lds + L.zero_off + threadIdx.x * 16) = make_uint4(0, 0, 0, 0);
+    if (threadIdx.x < 8) ((unsigned long long*)(lds + L.am_off))[threadIdx.x] = 0ull;
+    float xv[16];
+    prefetch_unit(a, wave, xv);
+
+    // loads run D steps ahead; past the wave's last step they repeat a valid chunk
+    const uint32_t kp0 = kp < nb ? kp : nb - 1;
+    uint32_t ld_tile = t0 < ntiles ? t0 : ntiles - 1, ld_blk = kp0;
+    if constexpr (BAL) ld_tile = my_tiles ? bt : 0;
+    K16Step<kQ3_K> buf[D];
+    auto issue = [&](K16Step<kQ3_K>& st) {
+        const uint8_t* base = a.w + ((uint64_t)ld_tile * nb + ld_blk) * kQ3KChunk;
+        if (BAL && half) k16_issue<kQ3_K>(st, base, kq * 16 + nh, nh, kq);  // the half tile
+        else k16_issue<kQ3_K>(st, base, lane, n, kq);
+        ld_blk += KS;
+        if (ld_blk >= nb) {
+            ld_blk = kp0;
+            if (!BAL && ld_tile + tstride < ntiles) ld_tile += tstride;
+        }
+    };
+#pragma unroll
+    for (int i = 0; i < D; ++i) issue(buf[i]);
+
+    const bool ok = a.x ? stage_q8k<W, kBsNone>(a, lds, L, wave, xv) : stage_planes<W>(a, lds, L, kQ3_K);
+    if (!ok) return finish_argmax(a, lds, L);
+    if (a.zero_pair) return zero_slot_tiles<W, TS>(a, tmax, tstride);
+
+    // the operands of q3k_mv_one_kernel
+    const uint32_t hsh = 4 * (kq >> 1), sb0 = kq >> 1;
+    const uint32_t cls = n & 7, qsel = n >> 3;
+    const bool live0 = kq == qsel, live1 = kq == 2 + qsel;
+    const uint8_t* a_ptr = live0 || live1 ? lds + 128 * (kq >> 1) + 16 * (kq & 1) : lds + L.zero_off;
+    const uint32_t a_step = live0 || live1 ? 256 : 0;
+    const uint32_t byte = 0xffu << (8 * (cls & 3));
+    uint32_t m0[4], m1[4];
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+        const uint32_t mk = (uint32_t)(w & 1) == (cls >> 2) ? byte : 0u;
+        m0[w] = live0 ? mk : 0u;
+        m1[w] = live1 ? mk : 0u;
+    }
+
+    uint32_t ti = 0, tile = BAL ? bt : t0, blk = kp, j = 0;
+    auto compute = [&](const K16Step<kQ3_K>& cur) {
+        const K16Ops<kQ3_K> o = k16_ops<kQ3_K>(cur, hsh);
+        const uint8_t* p = a_ptr + blk * a_step;
+        int32_t I[4] = {0, 0, 0, 0};
+#pragma unroll
+        for (int sft = 0; sft < 4; ++sft) {
+            const uint4 x = *(const uint4*)(p + 32 * sft);
+            const i32x4 A0 = {(int)(x.x & m0[0]), (int)(x.y & m0[1]), (int)(x.z & m0[2]), (int)(x.w & m0[3])};
+            const i32x4 A1 = {(int)(x.x & m1[0]), (int)(x.y & m1[1]), (int)(x.z & m1[2]), (int)(x.w & m1[3])};
+            const i32x4 d0 = mfma_i8(A0, o.wv[sft]), d1 = mfma_i8(A1, o.wv[sft]);
+            const int32_t sa = sbyte(o.c[sft >> 1], 2 * (sft & 1) + sb0);
+            const int32_t sb = sbyte(o.c[2 + (sft >> 1)], 2 * (sft & 1) + sb0);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) I[i] = mad24(sa, d0[i], mad24(sb, d1[i], I[i]));
+        }
+        const float d = half_to_float(cur.d) * *(const float*)(lds + L.d_off + blk * 32);  // :246
+#pragma unroll
+        for (int i = 0; i < 4; ++i) I[i] = sum_xor32(I[i]);
+        if (kq < 2)
+            park[((ti * TS + ts) * nb + blk) * 32 + lane] =
+                make_float4(d * (float)I[0], d * (float)I[1], d * (float)I[2], d * (float)I[3]);
+        if (DBG) {
+            const int32_t It = sum_xor16(I[0] + I[1] + I[2] + I[3]);
+            const uint32_t row = tile * kTileRows + n;
+            if (kq == 0 && row < a.rows && (!half || (n >> 3) == hsel)) {
+                a.dbg_isum[(uint64_t)row * nb + blk] = It;
+                a.dbg_imin[(uint64_t)row * nb + blk] = 0;
+            }
+        }
+        blk += KS;
+        if (++j == bpt) {
+            j = 0;
+            blk = kp;
+            ++ti;
+            tile += tstride;
+        }
+    };
+    pipeline<D>(steps, buf, issue, compute);
+    __syncthreads();
+
+    // each row's sum in the reference's order, one wave per tile slot (in a
+    // half tile lane pairs hold the same row; the own half stores it)
+    unsigned long long best = 0;
+    for (uint32_t slot = wave; slot < tmax * TS; slot += W) {  // (wave-uniform)
+        uint32_t t = blockIdx.x * TS + slot % TS + (slot / TS) * tstride;
+        bool own = true;
+        if constexpr (BAL) {
+            const TileDeal dl = balanced_deal<TS>(a.deal_cus, ntiles, slot);
+            if (!dl.count) continue;
+            t = dl.tile;
+            own = !dl.half || (n >> 3) == dl.hsel;
+        }
+        if (t >= ntiles) continue;
+        const float4* pk = park + (uint64_t)slot * nb * 32 + (lane & 31);
+        float c0 = 0.0f, c1 = 0.0f, c2 = 0.0f, c3 = 0.0f;
+        uint32_t b = 0;
+        for (; b + 8 <= nb; b += 8) {  // eight blocks' loads before their adds
+            float4 v[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) v[k] = pk[(b + k) * 32];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) c0 += v[k].x, c1 += v[k].y, c2 += v[k].z, c3 += v[k].w;
+        }
+        for (; b < nb; ++b) {
+            const float4 v = pk[b * 32];
+            c0 += v.x, c1 += v.y, c2 += v.z, c3 += v.w;
+        }
+        // classes 4..7 of row n sit in lane n + 16 (row 1 of the wave)
+        const float h0 = row_from(c0, 1), h1 = row_from(c1, 1), h2 = row_from(c2, 1), h3 = row_from(c3, 1);
+        float sum = 0.0f;
+        sum += c0;
+        sum += c1;
+        sum += c2;
+        sum += c3;
+        sum += h0;
+        sum += h1;
+        sum += h2;
+        sum += h3;
+        const uint32_t row = t * kTileRows + n;
+        if (kq == 0 && row < a.rows && own) store_out(a, row, 0, sum, best);
+    }
+    fold_argmax(a, lds, L, 0, best);
+    finish_argmax(a, lds, L);
+}
+
 #undef RLQ_MV_PROLOGUE
 
 // ---------------------------------------------------------------------------
@@ -2756,6 +3018,51 @@ static hipError_t launch_q45(const MvArgs& a, uint32_t nbat, bool dbg, uint32_t 
     return dbg ? launch_ks<T, 8, 4, 2, true>(a, s, pairs) : launch_ks<T, 8, 4, 2, false>(a, s, pairs);
 }
 
+// The split Q3_K kernel: 8 waves, two tile slots of a K split of 4, or, at
+// no more tiles than CUs, 16 waves, one slot of a K split of 16 (4096x14336:
+// 13.2 us against 19.8 with two slots, 13.6 with 8 waves of a split of 8);
+// about kSmallWgPerCu workgroups per CU and enough that the parked terms fit
+// LDS (one workgroup's slots at least: q3_split_fits).
+static bool q3_split_fits(const MvArgs& a, uint32_t ts = 2) {
+    const size_t off = q3_part_off(a.cols), per_tile = (size_t)ts * a.nb * 512u;
+    return off < kMaxLds && (kMaxLds - off) / per_tile > 0;
+}
+// The balanced deal (one matrix of 6144-16384 rows on 256 CUs): one
+// workgroup of 16 waves per CU, four slots of a K split of 4.
+template <bool DBG>
+static hipError_t launch_q3_bal(const MvArgs& a, hipStream_t s) {
+    constexpr int W = 16, KS = 4, TS = W / KS;
+    static LdsLimit lds_limit;
+    auto kernel = q3k_mv_split_kernel<W, KS, 1, DBG, true>;
+    uint32_t grid, tmax;
+    b1_bal_grid<TS>(a, grid, tmax);
+    const size_t lds = q3_split_lds(a.cols, tmax, TS);
+    if (grid == 0 || a.ids || lds > kMaxLds || (a.am_out && grid > kArgmaxMaxGrid)) return hipErrorInvalidValue;
+    if (const hipError_t e = lds_limit.raise((const void*)kernel, lds); e != hipSuccess) return e;
+    MvArgs b = a;
+    b.deal_cus = (uint32_t)device_cus();
+    hipLaunchKernelGGL(kernel, dim3(grid), dim3(W * 64), lds, s, b);
+    return hipGetLastError();
+}
+template <int W, int KS, bool DBG>
+static hipError_t launch_q3_split(const MvArgs& a, hipStream_t s, uint32_t pairs) {
+    constexpr int TS = W / KS;
+    static LdsLimit lds_limit;
+    auto kernel = q3k_mv_split_kernel<W, KS, 2, DBG>;
+    const uint32_t gy = grid_rows(a, pairs);
+    uint32_t grid = grid_cols((a.ntiles + TS - 1) / TS, (uint32_t)kSmallWgPerCu * (uint32_t)device_cus(), gy);
+    const size_t off = q3_part_off(a.cols), per_tile = (size_t)TS * a.nb * 512u;
+    if (!q3_split_fits(a, TS)) return hipErrorInvalidValue;
+    const uint64_t room = (kMaxLds - off) / per_tile, need = (a.ntiles + room * TS - 1) / (room * TS);
+    if (grid < need) grid = (uint32_t)need;
+    const uint32_t tstride = grid * TS, tmax = (a.ntiles + tstride - 1) / tstride;
+    const size_t lds = q3_split_lds(a.cols, tmax, TS);
+    if (lds > kMaxLds || (a.am_out && grid > kArgmaxMaxGrid)) return hipErrorInvalidValue;
+    if (const hipError_t e = lds_limit.raise((const void*)kernel, lds); e != hipSuccess) return e;
+    hipLaunchKernelGGL(kernel, dim3(grid, gy), dim3(W * 64), lds, s, a);
+    return hipGetLastError();
+}
+
 // Q2_K / Q3_K: up to four columns the K-split kernel, while its parked terms
 // fit LDS next to the activations (matrices of up to about 2^17 rows at 4096
 // columns); one wave per tile otherwise (measured at 14336x4096: batch 1
@@ -2795,6 +3102,20 @@ static hipError_t launch_k16_bal(const MvArgs& a, hipStream_t s) {
 
 template <uint32_t T>
 static hipError_t launch_k16(const MvArgs& a, bool dbg, size_t lds_plain, hipStream_t s, uint32_t pairs) {
+    // Q3_K, one column: the reference's f32 order; the blocks of each tile
+    // split over several waves while the parked terms fit LDS, else one wave
+    // per tile (14336x4096: balanced 12.0 us, split 13.0, one wave per tile
+    // 15.3; the kernels in their own order took 10.2)
+    if (T == kQ3_K && a.batch == 1) {
+        if (!a.ids && grid_rows(a, pairs) == 1 && b1_bal_units(a) >= 5 && q3_split_lds(a.cols, 1, 4) <= kMaxLds)
+            return dbg ? launch_q3_bal<true>(a, s) : launch_q3_bal<false>(a, s);
+        if (q3_split_fits(a) && a.ntiles * grid_rows(a, pairs) > (uint32_t)device_cus())
+            return dbg ? launch_q3_split<8, 4, true>(a, s, pairs) : launch_q3_split<8, 4, false>(a, s, pairs);
+        if (q3_split_fits(a, 1))
+            return dbg ? launch_q3_split<16, 16, true>(a, s, pairs) : launch_q3_split<16, 16, false>(a, s, pairs);
+        return dbg ? launch_one<kMvWaves, q3k_mv_one_kernel<kMvWaves, 3, true>>(a, lds_plain, s, pairs)
+                   : launch_one<kMvWaves, q3k_mv_one_kernel<kMvWaves, 3, false>>(a, lds_plain, s, pairs);
+    }
     // one matrix of 10240..16384 rows (on 256 CUs): the balanced deal, one
     // workgroup of 16 waves per CU, four slots of a K split of 4 (14336x4096
     // Q2_K batches 1 / 2 / 4 / 5 / 8: 8.6 / 9.5 / 11.0 / 14.1 / 16.6 us against

@@ -57,7 +57,7 @@ def bits(y):
 
 def exact(t, batch):
     """Whether a launch of `batch` columns gives the reference's f32 bits."""
-    return t == DT.Q2_K or (batch == 1 and t == DT.Q5_K)
+    return t == DT.Q2_K or (batch == 1 and t in (DT.Q3_K, DT.Q5_K))
 
 
 def random_blocks(t, rows, cols, seed):
@@ -221,8 +221,9 @@ def test_block_sums_bit_exact(ctx, t, rows, cols, batch):
 def test_block_sums_balanced_deal(ctx, t, rows, batch):
     """Q2_K / Q3_K at 10240..16384 rows run the K-split kernel in the
     balanced deal (one workgroup per CU, four tile slots, the
-    last a half tile at 14336 rows): column 0's integers bitwise, every
-    column's outputs against the oracle (Q2_K bitwise)."""
+    last a half tile at 14336 rows; Q3_K with one column the one-column
+    kernel): column 0's integers bitwise, every column's outputs against the
+    oracle (Q2_K, and Q3_K with one column, bitwise)."""
     cols = 4096
     say("block sums, balanced deal", t, rows, cols, batch)
     w = random_blocks(t, rows, cols, 300 + rows + int(t))
@@ -245,6 +246,35 @@ def test_block_sums_balanced_deal(ctx, t, rows, batch):
         assert rel_l2(got[b], want[b]) <= REL_L2, b
     if exact(t, batch):
         assert np.array_equal(bits(got), bits(want))
+
+
+@pytest.mark.parametrize("rows,cols", [(300, 4096), (7, 768), (6144, 4096), (8200, 2048), (14336, 4096),
+                                       (33, 49152), (20, 65536)])
+def test_q3k_one_column_every_launch_bitwise(ctx, rows, cols):
+    """Q3_K with one column, each of its launch shapes: one 16-wave tile slot
+    of a K split of 16 (no more tiles than CUs; 3 blocks a row leave most
+    waves without a block, 192 blocks a row fill most of LDS), two 8-wave
+    slots of a split of 4 (more tiles, not the balanced deal), the balanced
+    deal, and one wave per tile where the parked terms of one tile no longer
+    fit LDS (256 blocks a row).  Column 0's integers and every output
+    against the oracle bitwise."""
+    t = DT.Q3_K
+    say("Q3_K one column", rows, cols)
+    w = random_blocks(t, rows, cols, 500 + rows)
+    x = randn(600 + rows, cols).reshape(1, cols)
+    W = rlq.Weights(ctx, t, w, rows, cols)
+    isum, imin, y = ctx.block_sums_ex(W, torch.from_numpy(x).cuda())
+    ctx.sync()
+    act = O.quantize(O.Q8_K, x[0])
+    nb = cols // 256
+    stride = w.size // rows
+    want_i = np.zeros((rows, nb), np.int32)
+    for r in range(rows):
+        want_i[r] = O.block_sums(int(t), w[r * stride:(r + 1) * stride], act, nb)[0]
+    assert np.array_equal(isum.cpu().numpy(), want_i)
+    assert not imin.cpu().numpy().any()
+    want = O.matmul(int(t), w, rows, cols, x, threads=16)
+    assert np.array_equal(bits(y.cpu().numpy().reshape(1, rows)), bits(want))
 
 
 # ------------------------------------------------------------ batched device API

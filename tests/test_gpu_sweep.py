@@ -27,7 +27,7 @@ DT = rlq.DType
 REL_L2 = 1e-5
 DECODE_MAX_BATCH = 8
 EXACT_ALWAYS = (DT.Q8_0, DT.Q2_K)
-EXACT_ONE_COLUMN = (DT.Q4_K, DT.Q5_K, DT.Q6_K)
+EXACT_ONE_COLUMN = (DT.Q3_K, DT.Q4_K, DT.Q5_K, DT.Q6_K)
 # byte offsets of the f16 super-block scales of the random-block formats
 HALVES = {DT.Q2_K: (80, 82), DT.Q3_K: (108,), DT.Q5_K: (0, 2)}
 
