@@ -39,21 +39,22 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 // ---------------------------------------------------------------------------
 // Tiling
 //
-// Workgroup: 4 waves over 128 tokens x 128 weight rows (8 layout tiles of 16
-// rows); two workgroups share a CU, so each SIMD runs two independent waves
-// and one wave's VALU work (dequantization, the per-block fold) overlaps the
-// other's MFMAs.  Wave w owns rows 32w .. 32w+31 (one MFMA column tile) and
-// the 128 tokens as four 32-token tiles T: each dequantized weight operand
-// feeds four MFMAs.  Accumulators and f32 outputs y live in VGPRs.
+// Workgroup: 8 waves over 128 tokens x 256 weight rows (16 layout tiles of 16
+// rows), one workgroup per CU (two waves per SIMD).  Wave w owns rows
+// 32w .. 32w+31 (one MFMA column tile) and the 128 tokens as four 32-token
+// tiles T: each dequantized weight operand feeds four MFMAs.  Accumulators
+// and f32 outputs y live in VGPRs.  (Four waves over 128 rows, two workgroups
+// per CU, two stages ahead: 86-89 us at 512x4096x14336 against 83.6-83.9.)
 //
 // K is walked in groups of 64 values (4 k-steps of 16).  A group's operands
 // are one LDS stage, filled by global_load_lds_dwordx4 (global -> LDS without
-// VGPRs) two stages ahead in a ring of three; per-block data (weight block
+// VGPRs) kAhead stages ahead in a ring of kSlots; per-block data (weight block
 // headers, the activation record) sit in a ring of two regions.
 // ---------------------------------------------------------------------------
-constexpr uint32_t kGemmTM = 128;          // tokens per workgroup
-constexpr uint32_t kGemmTN = 128;          // weight rows per workgroup
-constexpr uint32_t kGemmThreads = 256;
+constexpr uint32_t kGemmWaves = 8;                 // one 32-row MFMA column tile each
+constexpr uint32_t kGemmTM = 128;                  // tokens per workgroup
+constexpr uint32_t kGemmTN = 32 * kGemmWaves;      // weight rows per workgroup
+constexpr uint32_t kGemmThreads = 64 * kGemmWaves;
 constexpr uint32_t kUnsafeAbsSum = 17753;  // floor((2^24 - 1) / 945)
 
 // Activation image, written by gemm_act_kernel.  Per token tile of 128: nb*4
@@ -78,10 +79,26 @@ __device__ __forceinline__ uint64_t act_record_offset(uint32_t nb, uint32_t b) {
     return (uint64_t)nb * 4 * kActGroupBytes + (uint64_t)b * kActRecordBytes;
 }
 
-// LDS per workgroup: stages [A 16 KB][W 8 tiles x 512 B], regions [headers 2 KB][record]
-constexpr uint32_t kSlots = 3, kSlotBytes = 20480, kSlotW = 16384;
-constexpr uint32_t kRegions = 2, kRegRec = 2048, kRegionBytes = kRegRec + kActRecordBytes;
+// LDS per workgroup: a ring of kSlots stages [A 16 KB][W kGemmTN/16 tiles x
+// 512 B], filled kAhead stages ahead; two regions [headers kGemmTN x 16 B][record]
+// (the stage kAhead ahead of a block's last one belongs at most to the next
+// block, so two regions never collide while kAhead <= 4).
+constexpr uint32_t kAhead = 3, kSlots = kAhead + 1;
+constexpr uint32_t kSlotW = kActGroupBytes, kSlotBytes = kSlotW + kGemmTN / 16 * 512;
+constexpr uint32_t kRegions = 2, kRegRec = kGemmTN * 16, kRegionBytes = kRegRec + kActRecordBytes;
 constexpr uint32_t kGemmLds = kSlots * kSlotBytes + kRegions * kRegionBytes;
+static_assert(kAhead >= 1 && kAhead <= 4 && 16 % kGemmWaves == 0 && kActRecordBytes % (16 * kGemmWaves) == 0, "");
+// LDS-DMA loads per wave and stage (A pieces, W pieces), and the extra ones of
+// a block's first stage (headers, record)
+constexpr int kLoadsStage = 16 / kGemmWaves + 1;
+constexpr int kLoadsFirst = 1 + (kActRecordBytes / kGemmWaves + 1023) / 1024;
+// loads a wave may still have pending at the barrier of a stage of group G:
+// those of the kAhead - 1 stages after it
+constexpr int pending_loads(int G) {
+    int n = 0;
+    for (int k = 1; k < (int)kAhead; ++k) n += kLoadsStage + ((G + k) % 4 == 0 ? kLoadsFirst : 0);
+    return n;
+}
 
 // ---------------------------------------------------------------------------
 // Activations: f32 x [M][K] -> the image above.  Tokens >= M are zeros.  One
@@ -266,18 +283,21 @@ __device__ __forceinline__ const uint8_t* region_ptr(const GemmCtx& c, uint32_t 
 }
 
 // Issue part P (0..3) of the LDS-DMA loads of stage s = 4 b + G (clamped
-// past the last block); a group issues the next stage's four parts between
-// its k-steps, so a full memory queue stalls the wave while its MFMAs run.
-// Every wave issues 5 loads per stage, plus 3 when G == 0: the stage
-// barriers' vmcnt counts depend on it.
+// past the last block); a group issues the stage kAhead ahead's four parts
+// between its k-steps, so a full memory queue stalls the wave while its MFMAs
+// run.  Every wave issues kLoadsStage loads per stage, plus kLoadsFirst when
+// G == 0: the stage barriers' vmcnt counts (pending_loads) depend on it.
 template <int G, int P>
 __device__ __forceinline__ void issue_part(const GemmCtx& c, uint32_t s) {
     const uint32_t bu = s / 4, b = bu < c.nb ? bu : c.nb - 1;
     const uint32_t slot = c.lds + (s % kSlots) * kSlotBytes;
     if (P < 2) {
-        const uint8_t* ag = c.act_tile + act_group_offset(b, G) + c.wave * 4096;
+        // wave w loads the 1 KB pieces per * w .. per * w + per - 1 of the 16
+        constexpr uint32_t per = 16 / kGemmWaves;
+        const uint8_t* ag = c.act_tile + act_group_offset(b, G) + c.wave * per * 1024;
 #pragma unroll
-        for (int j = 2 * P; j < 2 * P + 2; ++j) g2l(ag + j * 1024, c.lane * 16, slot + (c.wave * 4 + j) * 1024);
+        for (uint32_t j = P * per / 2; j < (P + 1) * per / 2; ++j)
+            g2l(ag + j * 1024, c.lane * 16, slot + (c.wave * per + j) * 1024);
     } else if (P == 2) {
         // layout tile t: the qs bytes of group G of its 16 rows are the 512 bytes at
         // (G/2) * 1024 + (G%2) * 512 of the block's chunk; wave w loads tiles 2w, 2w+1
@@ -288,11 +308,12 @@ __device__ __forceinline__ void issue_part(const GemmCtx& c, uint32_t s) {
             if (c.lane < 32) g2l(c.w_first + (uint64_t)b * kQ4KChunk, c.h_lane, reg + c.wave * 512);
         }
     } else if (G == 0) {
-        // the record: 1184 bytes (74 lanes) per wave
+        // the record: rb bytes (rl lanes) per wave
+        constexpr uint32_t rb = kActRecordBytes / kGemmWaves, rl = rb / 16;
         const uint32_t reg = c.lds + kSlots * kSlotBytes + (bu % kRegions) * kRegionBytes;
-        const uint8_t* rec = c.act_tile + act_record_offset(c.nb, b) + c.wave * 1184;
-        g2l(rec, c.lane * 16, reg + kRegRec + c.wave * 1184);
-        if (c.lane < 10) g2l(rec + 1024, c.lane * 16, reg + kRegRec + c.wave * 1184 + 1024);
+        const uint8_t* rec = c.act_tile + act_record_offset(c.nb, b) + c.wave * rb;
+        if (rl >= 64 || c.lane < rl) g2l(rec, c.lane * 16, reg + kRegRec + c.wave * rb);
+        if (rl > 64 && c.lane < rl - 64) g2l(rec + 1024, c.lane * 16, reg + kRegRec + c.wave * rb + 1024);
     }
 }
 
@@ -407,9 +428,13 @@ __device__ __forceinline__ void gemm_block(const GemmCtx& c, uint32_t b, f32x16 
     for (int G = 0; G < 4; ++G) {
         const uint32_t s = b * 4 + G;
         // stage s has landed for every wave; slot (s - 1) % 3 is free again
-        if (DBG) stage_barrier<0>();
-        else if (G < 3) stage_barrier<5>();
-        else stage_barrier<8>();
+        if (DBG) {
+            stage_barrier<0>();
+        } else {
+#define RLQ_BAR(k) stage_barrier<pending_loads(k)>()
+            RLQ_SWITCH4(G, RLQ_BAR)
+#undef RLQ_BAR
+        }
         if (G == 0) {  // the block's region arrived with its first stage
             qw = q4_words(*(const uint4*)(reg + tl * 256 + (c.ln & 15) * 16));
             const uint32_t f0 = reg[kRegRec + kRecFlags + c.lane], f1 = reg[kRegRec + kRecFlags + 64 + c.lane];
@@ -440,8 +465,8 @@ __device__ __forceinline__ void gemm_block(const GemmCtx& c, uint32_t b, f32x16 
             const bool fresh = S == 0 && G == 0;
 #pragma unroll
             for (int T = 0; T < 4; ++T) h[T] = mfma16(a[S & 1][T], bq[S & 1], fresh ? (f32x16){} : h[T]);
-            // part S of the stage two ahead (group (G + 2) % 4)
-#define RLQ_ISSUE(k) issue_part_at<((k) + 2) % 4>(c, s + 2, S)
+            // part S of the stage kAhead ahead
+#define RLQ_ISSUE(k) issue_part_at<((k) + kAhead) % 4>(c, s + kAhead, S)
             RLQ_SWITCH4(G, RLQ_ISSUE)
 #undef RLQ_ISSUE
             if (S < 3) {
@@ -461,7 +486,7 @@ __device__ __forceinline__ void gemm_block(const GemmCtx& c, uint32_t b, f32x16 
 }
 
 template <bool DBG>
-__global__ __launch_bounds__(kGemmThreads, 2) void q4k_gemm_kernel(GemmArgs g) {
+__global__ __launch_bounds__(kGemmThreads, 8 / kGemmWaves) void q4k_gemm_kernel(GemmArgs g) {
     extern __shared__ __align__(16) uint8_t smem[];
     const uint32_t lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     // XCD-aware order: workgroups i, i + 8, ... share an XCD (and its L2); give
@@ -510,7 +535,9 @@ __global__ __launch_bounds__(kGemmThreads, 2) void q4k_gemm_kernel(GemmArgs g) {
         for (int i = 0; i < 16; ++i) y[T][i] = 0.0f;
     f32x16 h[4];
     issue_stage<0>(c, 0);
-    issue_stage<1>(c, 1);
+    if (kAhead > 1) issue_stage<1>(c, 1);
+    if (kAhead > 2) issue_stage<2>(c, 2);
+    if (kAhead > 3) issue_stage<3>(c, 3);
     for (uint32_t b = 0; b < c.nb; ++b) gemm_block<DBG>(c, b, h, y);
     // LDS-DMA loads past the end may still be in flight: they must land before
     // the workgroup's LDS can go to another workgroup
