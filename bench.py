@@ -63,16 +63,16 @@ PREFILL_M = 512
 # WRITE_SIZE (each calibrated against a 256 MiB device copy), recorded in
 # profiles/hbm_traffic_q4k_decode_and_prefill.md: the decode kernel, and the prefill step's
 # two kernels (GEMM + quantizer).
-TRAFFIC_DECODE_BYTES = 33345505
-TRAFFIC_PREFILL_BYTES = 103213500 + 12975078
+TRAFFIC_DECODE_BYTES = 33351490
+TRAFFIC_PREFILL_BYTES = 98617131 + 12975038
 # the same measurement for the kernels of the other configurations (per launch)
 TRAFFIC_CONFIG_BYTES = {
-    "q8_0_4864x896_b1": 4951453,
-    "q4k_14336x4096_b4": 34042784,
-    "q4k_14336x4096_b8": 34012096 + 224233,  # the matvec, then the planes kernel
-    "q6k_128256x4096_b1_argmax": 436369070,
-    "q6k_128256x4096_b8_argmax": 440941365,
-    "q8_0_151936x896_b1_argmax": 146145931,
+    "q8_0_4864x896_b1": 4963715,
+    "q4k_14336x4096_b4": 34064124,
+    "q4k_14336x4096_b8": 33980196 + 224233,  # the matvec, then the planes kernel
+    "q6k_128256x4096_b1_argmax": 436357969,
+    "q6k_128256x4096_b8_argmax": 440944786,
+    "q8_0_151936x896_b1_argmax": 146142805,
 }
 COPY_PROBE_BYTES = 256 << 20
 METRIC = "Q4_K matvec GB/s (14336x4096, B=1) + prefill GEMM TOPS (M=512); tok/s"
