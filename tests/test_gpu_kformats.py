@@ -9,8 +9,8 @@ Bars, as for Q4_K / Q6_K:
   - Q2_K: bit-exact.  The reference adds `d * isum - mn * mins` per block into
     one f32 sum (matvec_extra.rs:193-195) and the kernel's lane does the same
     in block order.
-  - Q5_K with one column: bit-exact.  The one-column kernels keep the
-    reference's eight lane accumulators (matvec_extra.rs:223-294).
+  - Q3_K and Q5_K with one column: bit-exact.  The one-column kernels keep
+    the reference's eight lane accumulators (matvec_extra.rs:223-294).
 Weights are the oracle's encoder outputs for small cases and random GGUF
 blocks (every bit of the quants and scales random, finite f16 super-scales)
 for the rest, which reaches sub-block scales and high bits that encoded
@@ -257,7 +257,7 @@ def test_q3k_one_column_every_launch_bitwise(ctx, rows, cols):
     slots of a split of 4 (more tiles, not the balanced deal), the balanced
     deal, and one wave per tile where the parked terms of one tile no longer
     fit LDS (256 blocks a row).  Column 0's integers and every output
-    against the oracle bitwise."""
+    against the oracle bitwise, and the fused argmax against the oracle's."""
     t = DT.Q3_K
     say("Q3_K one column", rows, cols)
     w = random_blocks(t, rows, cols, 500 + rows)
@@ -275,6 +275,10 @@ def test_q3k_one_column_every_launch_bitwise(ctx, rows, cols):
     assert not imin.cpu().numpy().any()
     want = O.matmul(int(t), w, rows, cols, x, threads=16)
     assert np.array_equal(bits(y.cpu().numpy().reshape(1, rows)), bits(want))
+    y2, am = ctx.matmul_argmax(W, torch.from_numpy(x).cuda())
+    ctx.sync()
+    assert np.array_equal(bits(y2.cpu().numpy().reshape(1, rows)), bits(want))
+    assert int(am[0]) == O.argmax(want[0])
 
 
 # ------------------------------------------------------------ batched device API

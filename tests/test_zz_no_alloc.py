@@ -49,7 +49,9 @@ def inputs(seed, batch, cols):
     (DT.Q5_K, 1500, 4096, (8, 7), True),        # 7-8 columns: fused quantizer here, planes kernel in rlq_matmul
     (DT.Q5_K, 1500, 4096, (8, 7), False),
     (DT.Q6_K, 3000, 4096, (8, 1), True),
-    (DT.Q8_0, 2000, 896, (5, 2), True)])
+    (DT.Q8_0, 2000, 896, (5, 2), True),
+    (DT.Q3_K, 2048, 4096, (2, 1), True),        # Q3_K one column: the class-ordered split kernel
+    (DT.Q2_K, 1500, 2048, (1, 3), True)])
 def test_noalloc_equals_allocating_entry_point(ctx, t, rows, cols, batches, with_argmax):
     W = weights(ctx, t, rows, cols, 31 + rows)
     for i, batch in enumerate(batches):
