@@ -161,9 +161,11 @@ def practical_peaks(torch, rlq=None, reps=20):
     (bytes read + written per second), torch's (hipBLASLt) dense f16 and int8
     GEMMs at 8192^3 and at the prefill shape 512x4096x14336, and the library's
     probes: chained MFMAs from registers (v_mfma_i32_32x32x32_i8 and
-    v_mfma_f32_32x32x16_f16) and a plain read of the headline's weight bytes
-    with the one-column matvec's launch shape and loads, over the same 10
-    rotated copies (rlq_probe_mfma, rlq_probe_stream)."""
+    v_mfma_f32_32x32x16_f16), LDS reads in the prefill GEMM's A-operand
+    pattern alone and feeding f16 MFMAs at the GEMM's ratio, and a plain read
+    of the headline's weight bytes with the one-column matvec's launch shape
+    and loads, over the same 10 rotated copies (rlq_probe_mfma,
+    rlq_probe_stream)."""
     out = {}
 
     def timed(fn):
@@ -220,9 +222,15 @@ def probe_peaks(rlq, torch, reps):
     stream = torch.cuda.current_stream()
     sp = ctypes.c_void_p(stream.cuda_stream)
     out = {}
-    wgs, iters = 4 * cus, 4000
-    sink = torch.zeros(16 * max(wgs, cus), dtype=torch.int32, device="cuda")
-    for kind, key, per in ((0, "mfma_i8_32x32x32_tops", 2 * 32 * 32 * 32), (1, "mfma_f16_32x32x16_tflops", 2 * 32 * 32 * 16)):
+    iters = 4000
+    sink = torch.zeros(16 * 4 * cus, dtype=torch.int32, device="cuda")
+    # (kind, key, work per wave step, workgroups): the MFMA chains at four
+    # workgroups per CU; the LDS reads and the GEMM's ratio at two, the
+    # prefill GEMM's occupancy (work per step: 4 MFMAs, or 4 KB read)
+    for kind, key, per, wgs in ((0, "mfma_i8_32x32x32_tops", 4 * 2 * 32 * 32 * 32, 4 * cus),
+                                (1, "mfma_f16_32x32x16_tflops", 4 * 2 * 32 * 32 * 16, 4 * cus),
+                                (2, "lds_read_b128_tbs", 4 * 1024, 2 * cus),
+                                (3, "mfma_f16_with_lds_a_reads_tflops", 4 * 2 * 32 * 32 * 16, 2 * cus)):
         def launch():
             rc = rlq._lib.rlq_probe_mfma(kind, wgs, iters, ctypes.c_void_p(sink.data_ptr()), sp)
             if rc != 0:
@@ -236,7 +244,7 @@ def probe_peaks(rlq, torch, reps):
         b.record(stream)
         torch.cuda.synchronize()
         s = a.elapsed_time(b) / reps * 1e-3
-        out[key] = round(wgs * 4 * 4 * iters * per / s / 1e12, 1)
+        out[key] = round(wgs * 4 * iters * per / s / 1e12, 1)
     # the headline's bytes (Q4_K 14336x4096: 33,030,144 B) in 10 rotated copies
     nbytes, copies = 14336 * 2304, ROTATE
     bufs = [torch.empty(nbytes, dtype=torch.uint8, device="cuda") for _ in range(copies)]

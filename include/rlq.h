@@ -501,7 +501,10 @@ int32_t rlq_gguf_write(const char *path, const rlq_gguf_kv *kv, uint64_t n_kv, c
  * for rlq_probe_mfma, 16 for rlq_probe_stream) so that no work is dead. */
 /* kind 0: v_mfma_i32_32x32x32_i8, kind 1: v_mfma_f32_32x32x16_f16; each of
  * the 4 waves of `workgroups` 256-thread workgroups runs 4 independent
- * accumulator chains of `iters` MFMAs from registers. */
+ * accumulator chains of `iters` MFMAs from registers.  kind 2: `iters` steps
+ * of four 1 KB ds_read_b128 reads per wave (the prefill GEMM's A-operand
+ * pattern, 20 KB of LDS per workgroup); kind 3: the same four reads per step
+ * feeding four v_mfma_f32_32x32x16_f16. */
 int32_t rlq_probe_mfma(uint32_t kind, uint32_t workgroups, uint32_t iters, uint32_t *out, void *stream);
 /* A read of `len` device bytes (a multiple of 1024, 16-byte aligned) by
  * `workgroups` workgroups of 16 waves, each wave instruction a 1 KB run of

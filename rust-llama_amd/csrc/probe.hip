@@ -3,6 +3,9 @@
 //  - rlq_probe_mfma: chained MFMAs from registers, no memory traffic:
 //    v_mfma_i32_32x32x32_i8 (the int8 peak the prefill target is quoted on)
 //    and v_mfma_f32_32x32x16_f16 (the instruction the prefill GEMM issues);
+//    LDS reads alone in the prefill GEMM's A-operand pattern (four 1 KB
+//    ds_read_b128 per step); and the GEMM's inner ratio, four such reads
+//    feeding four f16 MFMAs;
 //  - rlq_probe_stream: a plain read of a buffer with the one-column matvec's
 //    launch shape (one workgroup of 16 waves per CU) and load pattern (each
 //    wave instruction a 1 KB run of 16-byte non-temporal loads), XORed and
@@ -34,7 +37,7 @@ __global__ __launch_bounds__(256) void mfma_probe_kernel(uint32_t iters, uint32_
             c3 = __builtin_amdgcn_mfma_i32_32x32x32_i8(b, b, c3, 0, 0, 0);
         }
         if (lane == 0) out[gw] = (uint32_t)(c0[0] ^ c1[1] ^ c2[2] ^ c3[3]);
-    } else {
+    } else if constexpr (KIND == 1) {
         p_f16x8 a, b;
 #pragma unroll
         for (int k = 0; k < 8; ++k) a[k] = (_Float16)(lane + k), b[k] = (_Float16)(k - 3);
@@ -46,6 +49,36 @@ __global__ __launch_bounds__(256) void mfma_probe_kernel(uint32_t iters, uint32_
             c3 = __builtin_amdgcn_mfma_f32_32x32x16_f16(b, b, c3, 0, 0, 0);
         }
         if (lane == 0) out[gw] = __float_as_uint(c0[0] + c1[1] + c2[2] + c3[3]);
+    } else {
+        // the prefill GEMM's A reads: per step four 16-byte reads per lane at
+        // 512-byte strides, a different 4 KB quarter of a 20 KB region per step
+        __shared__ __align__(16) uint8_t sm[20480];
+        for (uint32_t i = threadIdx.x; i < 20480 / 16; i += 256) ((uint4*)sm)[i] = make_uint4(i, 3 * i, 5 * i, 7 * i);
+        __syncthreads();
+        uint4 x = make_uint4(0, 0, 0, 0);
+        p_f16x8 b;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) b[k] = (_Float16)(k - 3);
+        p_f32x16 c0 = {}, c1 = {}, c2 = {}, c3 = {};
+        for (uint32_t i = 0; i < iters; ++i) {
+            asm volatile("" ::: "memory");  // every step reads LDS again
+            const uint8_t* base = sm + (i & 3) * 4096 + lane * 16;
+            if constexpr (KIND == 2) {
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    const uint4 v = *(const uint4*)(base + t * 512);
+                    x.x ^= v.x, x.y ^= v.y, x.z ^= v.z, x.w ^= v.w;
+                }
+            } else {
+                const p_f16x8 a0 = *(const p_f16x8*)base, a1 = *(const p_f16x8*)(base + 512);
+                const p_f16x8 a2 = *(const p_f16x8*)(base + 1024), a3 = *(const p_f16x8*)(base + 1536);
+                c0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, b, c0, 0, 0, 0);
+                c1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, b, c1, 0, 0, 0);
+                c2 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a2, b, c2, 0, 0, 0);
+                c3 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a3, b, c3, 0, 0, 0);
+            }
+        }
+        if (lane == 0) out[gw] = (x.x ^ x.y ^ x.z ^ x.w) + __float_as_uint(c0[0] + c1[1] + c2[2] + c3[3]);
     }
 }
 
@@ -75,11 +108,14 @@ __global__ __launch_bounds__(1024) void stream_probe_kernel(const uint8_t* p, ui
 using namespace rlq;
 
 extern "C" int32_t rlq_probe_mfma(uint32_t kind, uint32_t workgroups, uint32_t iters, uint32_t* out, void* stream) {
-    if (kind > 1 || workgroups == 0 || !out) return RLQ_INVALID_ARGUMENT;
-    if (kind == 0)
-        hipLaunchKernelGGL(mfma_probe_kernel<0>, dim3(workgroups), dim3(256), 0, (hipStream_t)stream, iters, out);
-    else
-        hipLaunchKernelGGL(mfma_probe_kernel<1>, dim3(workgroups), dim3(256), 0, (hipStream_t)stream, iters, out);
+    if (kind > 3 || workgroups == 0 || !out) return RLQ_INVALID_ARGUMENT;
+    const hipStream_t s = (hipStream_t)stream;
+    switch (kind) {
+        case 0: hipLaunchKernelGGL(mfma_probe_kernel<0>, dim3(workgroups), dim3(256), 0, s, iters, out); break;
+        case 1: hipLaunchKernelGGL(mfma_probe_kernel<1>, dim3(workgroups), dim3(256), 0, s, iters, out); break;
+        case 2: hipLaunchKernelGGL(mfma_probe_kernel<2>, dim3(workgroups), dim3(256), 0, s, iters, out); break;
+        default: hipLaunchKernelGGL(mfma_probe_kernel<3>, dim3(workgroups), dim3(256), 0, s, iters, out); break;
+    }
     return hipGetLastError() == hipSuccess ? RLQ_OK : RLQ_DEVICE_ERROR;
 }
 
