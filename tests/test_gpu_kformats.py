@@ -196,8 +196,9 @@ def test_block_sums_golden_records(ctx):
                                              (300, 4096, 8), (7, 768, 1), (37, 2304, 4)])
 def test_block_sums_bit_exact(ctx, t, rows, cols, batch):
     """Exact per-block integers of column 0 inside every kernel variant (Q5_K:
-    1-2 columns the VALU kernel, 3-8 MFMA; Q2_K / Q3_K: one or two column
-    groups), rows that leave a partial last tile."""
+    the one-column kernel, then the K-split MFMA kernel from 2 columns; Q2_K /
+    Q3_K: the one-column Q3_K kernels, then one or two column groups), rows
+    that leave a partial last tile."""
     say("block sums", t, rows, cols, batch)
     w = random_blocks(t, rows, cols, 100 + rows + int(t))
     x = randn(200 + rows, batch * cols).reshape(batch, cols)
