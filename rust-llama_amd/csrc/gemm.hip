@@ -517,16 +517,33 @@ __global__ __launch_bounds__(kGemmThreads, 8 / kGemmWaves) void q4k_gemm_kernel(
     const uint32_t th = t0 + 2 * wave + ((lane >> 4) & 1);
     c.h_lane = ((th < tmax ? th : tmax) - t0) * tstride + 2048 + (lane & 15) * 16;
 
-    // a data error in any token: this call writes nothing (flag bit 0 of every record)
+    // the first stages' loads go out before the flag scan, so the two wait together
+    issue_stage<0>(c, 0);
+    if (kAhead > 1) issue_stage<1>(c, 1);
+    if (kAhead > 2) issue_stage<2>(c, 2);
+    if (kAhead > 3) issue_stage<3>(c, 3);
+    // a data error in any token: this call writes nothing (flag bit 0 of every
+    // record); eight words per thread in flight at once
     int bad = 0;
     const uint32_t words = g.MT * g.nb * (kGemmTM / 4);
-    for (uint32_t i = threadIdx.x; i < words; i += kGemmThreads) {
-        const uint32_t rec = i / (kGemmTM / 4), part = i % (kGemmTM / 4);
-        const uint8_t* base = g.img + (uint64_t)(rec / g.nb) * g.nb * kActTileBlockBytes +
-                              act_record_offset(g.nb, rec % g.nb) + kRecFlags;
-        bad |= (int)(((const uint32_t*)base)[part] & 0x01010101u);
+    for (uint32_t i0 = threadIdx.x; i0 < words; i0 += 8 * kGemmThreads) {
+        uint32_t f[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {  // past the end: the last word again (no branch between the loads)
+            const uint32_t i = i0 + k * kGemmThreads < words ? i0 + k * kGemmThreads : words - 1;
+            const uint32_t rec = i / (kGemmTM / 4), part = i % (kGemmTM / 4);
+            const uint8_t* base = g.img + (uint64_t)(rec / g.nb) * g.nb * kActTileBlockBytes +
+                                  act_record_offset(g.nb, rec % g.nb) + kRecFlags;
+            f[k] = ((const uint32_t*)base)[part];
+        }
+#pragma unroll
+        for (int k = 0; k < 8; ++k) bad |= (int)(f[k] & 0x01010101u);
     }
-    if (__syncthreads_or(bad)) return;
+    if (__syncthreads_or(bad)) {
+        // the LDS-DMA loads must land before the workgroup's LDS is released
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        return;
+    }
 
     float y[4][16];
 #pragma unroll
@@ -534,10 +551,6 @@ __global__ __launch_bounds__(kGemmThreads, 8 / kGemmWaves) void q4k_gemm_kernel(
 #pragma unroll
         for (int i = 0; i < 16; ++i) y[T][i] = 0.0f;
     f32x16 h[4];
-    issue_stage<0>(c, 0);
-    if (kAhead > 1) issue_stage<1>(c, 1);
-    if (kAhead > 2) issue_stage<2>(c, 2);
-    if (kAhead > 3) issue_stage<3>(c, 3);
     for (uint32_t b = 0; b < c.nb; ++b) gemm_block<DBG>(c, b, h, y);
     // LDS-DMA loads past the end may still be in flight: they must land before
     // the workgroup's LDS can go to another workgroup
