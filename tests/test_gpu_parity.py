@@ -840,3 +840,32 @@ def test_gemm_argmax_and_errors(ctx):
         ctx.sync()
     assert (e.value.name, e.value.index, e.value.b) == ("NonFiniteInput", 500, 13)
     assert bool((y2 == 7.0).all())
+
+
+def test_gemm_many_token_tiles(ctx):
+    """Seventeen and thirty-three token tiles: every token against the oracle
+    at 2100 tokens (a partial last tile), then a non-finite value in the last
+    of 4100 tokens, which every workgroup's scan of the records' flags must
+    reach: the call reports its column and element and writes nothing."""
+    rows, cols = 64, 4096
+    w = _weights(DT.Q4_K, rows, cols, 91)
+    W = rlq.Weights(ctx, DT.Q4_K, w, rows, cols)
+    batch = 2100
+    say("gemm many token tiles", rows, cols, batch)
+    x = randn(92, batch * cols).reshape(batch, cols)
+    y = ctx.matmul(W, torch.from_numpy(x).cuda())
+    ctx.sync()
+    want = O.matmul(O.Q4_K, w, rows, cols, x, threads=16)
+    got = y.cpu().numpy()
+    for b in range(batch):
+        assert rel_l2(got[b], want[b]) <= REL_L2, b
+    batch = 4100
+    say("gemm many token tiles, error in the last token", rows, cols, batch)
+    xt = torch.from_numpy(randn(93, batch * cols).reshape(batch, cols)).cuda()
+    xt[batch - 1, 4095] = float("nan")
+    y2 = torch.full((batch, rows), 7.0, device="cuda")
+    ctx.matmul(W, xt, y2)
+    with pytest.raises(rlq.QuantError) as e:
+        ctx.sync()
+    assert (e.value.name, e.value.index, e.value.b) == ("NonFiniteInput", 4095, batch - 1)
+    assert bool((y2 == 7.0).all())
