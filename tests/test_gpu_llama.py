@@ -224,6 +224,47 @@ def test_attention_repeats_equal_certified_sums(ctx, monkeypatch):
     g2.close()
 
 
+def test_attention_scores_below_the_plain_exponential(ctx):
+    """Scores spread over hundreds (the attention RMSNorm weights times 20,
+    so q and k grow 20-fold): softmax arguments below -87.3 take the
+    exponential's other branch (subnormal results; zero below about -133.5).
+    The attention output is bitwise the oracle's at every step, and the run
+    is checked to reach both ranges."""
+    say("llama attention, attention norm x20 (scores below exp's plain range), 70 steps")
+    cfg = make_config(n_layers=1, heads=8, kv_heads=2, max_context=80)
+    t0 = make_tensors(cfg, 37)
+    L = dict(t0["layers"][0])
+    L["attention_norm"] = (L["attention_norm"] * np.float32(20.0)).astype(np.float32)
+    t = dict(t0, layers=[L])  # (a copy: the fixture's tensors are shared)
+    g, o = rlq.LlamaModel(ctx, gpu_config(cfg), t), O.LlamaOracle(cfg, t)
+    W, kvw, hd = cfg.width, cfg.kv_width, cfg.head_dim
+    scale = np.float32(1.0) / np.sqrt(np.float32(hd))
+    kc = np.zeros((cfg.max_context, kvw), np.float32)
+    vc = np.zeros_like(kc)
+    rng = np.random.default_rng(19)
+    plain = subnormal = zero = 0
+    for step in range(70):
+        h = torch.from_numpy(o.embedding(int(rng.integers(cfg.vocabulary)))).cuda()
+        g.step(h, step, embedding=False, logits=False)
+        qkv, att, _, _ = (host(x) for x in g.intermediates())
+        ctx.sync()
+        q = O.rope(qkv[:W], hd, step, cfg.rope_base)
+        kc[step] = O.rope(qkv[W:W + kvw], hd, step, cfg.rope_base)
+        vc[step] = qkv[W + kvw:]
+        want = O.attention(q, kc[:step + 1], vc[:step + 1], step + 1, cfg.heads, cfg.kv_heads, hd, scale)
+        assert np.array_equal(bits(att), bits(want)), step
+        G = cfg.heads // cfg.kv_heads
+        for hh in range(cfg.heads):
+            kv = hh // G
+            s = kc[:step + 1, kv * hd:(kv + 1) * hd].astype(np.float64) @ q[hh * hd:(hh + 1) * hd] * float(scale)
+            x = s - s.max()
+            plain += int((x > -86.0).sum())
+            subnormal += int(((x < -89.0) & (x > -132.0)).sum())
+            zero += int((x < -135.0).sum())
+    g.close()
+    assert plain > 0 and subnormal > 0 and zero > 0, (plain, subnormal, zero)
+
+
 def test_attention_long_context(ctx):
     """2,600 rows of cache with four query heads per KV head: each P.V lane
     keeps its first 2 column groups (1,024 columns over the workgroup) in

@@ -8,8 +8,8 @@ beyond 64 blocks), and batches 1..8 (one pass of the decode kernels) and 9 or
 Bars, as in test_gpu_parity: column 0's per-block integers bitwise (every
 batch for Q4_K, up to 8 columns otherwise), every column's f32 outputs within
 relative L2 1e-5 of the oracle, and bitwise where the kernels keep the
-reference's f32 order (Q8_0 and Q2_K at every batch, Q4_K, Q5_K and Q6_K with
-one column).  Weights: the library's encoder on N(0, 0.02)
+reference's f32 order (Q8_0 and Q2_K at every batch, Q3_K, Q4_K, Q5_K and
+Q6_K with one column).  Weights: the library's encoder on N(0, 0.02)
 values for Q4_K, Q6_K and Q8_0; random GGUF blocks (random quants and scales,
 finite positive f16 super-scales) for Q2_K, Q3_K and Q5_K, as in
 test_gpu_kformats.  Every case prints itself before touching the GPU.
