@@ -245,6 +245,30 @@ def probe_peaks(rlq, torch, reps):
         torch.cuda.synchronize()
         s = a.elapsed_time(b) / reps * 1e-3
         out[key] = round(wgs * 4 * iters * per / s / 1e12, 1)
+    # MFMA waves and FMA waves on the same SIMDs (one 8-wave workgroup per CU):
+    # each half alone, and together with the MFMA accumulators in VGPRs and in
+    # AGPRs.  overlap = the time the pair saves against running the halves one
+    # after the other, as a fraction of the shorter half (1: fully hidden)
+    co = {}
+    for kind, key in ((4, "mfma_alone_us"), (5, "fma_alone_us"), (6, "together_vgpr_acc_us"),
+                      (7, "mfma_alone_agpr_acc_us"), (8, "together_agpr_acc_us")):
+        def launch():
+            rc = rlq._lib.rlq_probe_mfma(kind, cus, 2000, ctypes.c_void_p(sink.data_ptr()), sp)
+            if rc != 0:
+                raise RuntimeError(f"rlq_probe_mfma: {rc}")
+        launch()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        for _ in range(reps):
+            launch()
+        b.record(stream)
+        torch.cuda.synchronize()
+        co[key] = round(a.elapsed_time(b) / reps * 1e3, 1)
+    for acc, m in (("vgpr", co["mfma_alone_us"]), ("agpr", co["mfma_alone_agpr_acc_us"])):
+        f = co["fma_alone_us"]
+        co[f"overlap_{acc}_acc"] = round((m + f - co[f"together_{acc}_acc_us"]) / min(m, f), 2)
+    out["mfma_fma_coexec"] = co
     # the headline's bytes (Q4_K 14336x4096: 33,030,144 B) in 10 rotated copies
     nbytes, copies = 14336 * 2304, ROTATE
     bufs = [torch.empty(nbytes, dtype=torch.uint8, device="cuda") for _ in range(copies)]

@@ -498,13 +498,18 @@ int32_t rlq_gguf_write(const char *path, const rlq_gguf_kv *kv, uint64_t n_kv, c
  * No counterpart in the reference: kernels that measure this GPU's practical
  * ceilings for the benchmark, next to the spec peaks.  Both are asynchronous
  * on `stream` and write one word per wave to `out` (4 words per workgroup
- * for rlq_probe_mfma, 16 for rlq_probe_stream) so that no work is dead. */
+ * for rlq_probe_mfma kinds 0-3, 8 for kinds 4-8, 16 for rlq_probe_stream) so
+ * that no work is dead. */
 /* kind 0: v_mfma_i32_32x32x32_i8, kind 1: v_mfma_f32_32x32x16_f16; each of
  * the 4 waves of `workgroups` 256-thread workgroups runs 4 independent
  * accumulator chains of `iters` MFMAs from registers.  kind 2: `iters` steps
  * of four 1 KB ds_read_b128 reads per wave (the prefill GEMM's A-operand
  * pattern, 20 KB of LDS per workgroup); kind 3: the same four reads per step
- * feeding four v_mfma_f32_32x32x16_f16. */
+ * feeding four v_mfma_f32_32x32x16_f16.  Kinds 4-8: 512-thread workgroups,
+ * waves 0-3 running four v_mfma_f32_32x32x16_f16 chains of `iters` steps and
+ * waves 4-7 eight f32 FMA chains of 2 * iters steps (two waves per SIMD):
+ * kind 4 the MFMA waves alone, 5 the FMA waves alone, 6 both; 7 and 8 as 4
+ * and 6 with the MFMA accumulators in AGPRs instead of VGPRs. */
 int32_t rlq_probe_mfma(uint32_t kind, uint32_t workgroups, uint32_t iters, uint32_t *out, void *stream);
 /* A read of `len` device bytes (a multiple of 1024, 16-byte aligned) by
  * `workgroups` workgroups of 16 waves, each wave instruction a 1 KB run of

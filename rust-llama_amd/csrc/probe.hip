@@ -5,7 +5,9 @@
 //    and v_mfma_f32_32x32x16_f16 (the instruction the prefill GEMM issues);
 //    LDS reads alone in the prefill GEMM's A-operand pattern (four 1 KB
 //    ds_read_b128 per step); and the GEMM's inner ratio, four such reads
-//    feeding four f16 MFMAs;
+//    feeding four f16 MFMAs; and whether MFMAs of one wave and FMAs of
+//    another overlap on one SIMD, with the MFMA accumulators in VGPRs or in
+//    AGPRs;
 //  - rlq_probe_stream: a plain read of a buffer with the one-column matvec's
 //    launch shape (one workgroup of 16 waves per CU) and load pattern (each
 //    wave instruction a 1 KB run of 16-byte non-temporal loads), XORed and
@@ -82,6 +84,49 @@ __global__ __launch_bounds__(256) void mfma_probe_kernel(uint32_t iters, uint32_
     }
 }
 
+// MFMA and VALU work of different waves on one SIMD: 8 waves per workgroup
+// (two per SIMD), waves 0-3 running four f16 MFMA chains of `iters` steps,
+// waves 4-7 eight f32 FMA chains of 2 * iters steps.  MFMA_HALF / VALU_HALF
+// select the halves that run (the other exits); AG keeps the MFMA
+// accumulators in AGPRs (an inline-asm operand that needs one makes the
+// compiler pick the AGPR form of the MFMAs), else they are VGPRs.
+template <bool MFMA_HALF, bool VALU_HALF, bool AG>
+__global__ __launch_bounds__(512) void coexec_probe_kernel(uint32_t iters, uint32_t* out) {
+    if constexpr (AG) {
+        float z = 0.0f;
+        asm volatile("; %0" : "+a"(z));
+    }
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6, gw = blockIdx.x * 8 + wave;
+    float r = 0.0f;
+    if (wave < 4) {
+        if (!MFMA_HALF) return;
+        p_f16x8 a, b;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) a[k] = (_Float16)(lane + k), b[k] = (_Float16)(k - 3);
+        p_f32x16 c0 = {}, c1 = {}, c2 = {}, c3 = {};
+        for (uint32_t i = 0; i < iters; ++i) {
+            c0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c0, 0, 0, 0);
+            c1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(b, a, c1, 0, 0, 0);
+            c2 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, a, c2, 0, 0, 0);
+            c3 = __builtin_amdgcn_mfma_f32_32x32x16_f16(b, b, c3, 0, 0, 0);
+        }
+        r = c0[0] + c1[1] + c2[2] + c3[3];
+    } else {
+        if (!VALU_HALF) return;
+        float v[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) v[k] = (float)(lane + k);
+        const float m = 1.0000001f, o = 0.5f * (float)lane;
+        for (uint32_t i = 0; i < 2 * iters; ++i) {
+#pragma unroll
+            for (int k = 0; k < 8; ++k) v[k] = __builtin_fmaf(v[k], m, o);
+        }
+#pragma unroll
+        for (int k = 0; k < 8; ++k) r += v[k];
+    }
+    if (lane == 0) out[gw] = __float_as_uint(r);
+}
+
 // Workgroup g of `grid` reads its equal share of the n16 16-byte units: wave
 // w's 1 KB runs w, w + 16, ... of the share, two runs in flight per wave.
 __global__ __launch_bounds__(1024) void stream_probe_kernel(const uint8_t* p, uint64_t n16, uint32_t* out) {
@@ -108,13 +153,19 @@ __global__ __launch_bounds__(1024) void stream_probe_kernel(const uint8_t* p, ui
 using namespace rlq;
 
 extern "C" int32_t rlq_probe_mfma(uint32_t kind, uint32_t workgroups, uint32_t iters, uint32_t* out, void* stream) {
-    if (kind > 3 || workgroups == 0 || !out) return RLQ_INVALID_ARGUMENT;
+    if (kind > 8 || workgroups == 0 || !out) return RLQ_INVALID_ARGUMENT;
     const hipStream_t s = (hipStream_t)stream;
+    const dim3 g(workgroups), b4(256), b8(512);
     switch (kind) {
-        case 0: hipLaunchKernelGGL(mfma_probe_kernel<0>, dim3(workgroups), dim3(256), 0, s, iters, out); break;
-        case 1: hipLaunchKernelGGL(mfma_probe_kernel<1>, dim3(workgroups), dim3(256), 0, s, iters, out); break;
-        case 2: hipLaunchKernelGGL(mfma_probe_kernel<2>, dim3(workgroups), dim3(256), 0, s, iters, out); break;
-        default: hipLaunchKernelGGL(mfma_probe_kernel<3>, dim3(workgroups), dim3(256), 0, s, iters, out); break;
+        case 0: hipLaunchKernelGGL(mfma_probe_kernel<0>, g, b4, 0, s, iters, out); break;
+        case 1: hipLaunchKernelGGL(mfma_probe_kernel<1>, g, b4, 0, s, iters, out); break;
+        case 2: hipLaunchKernelGGL(mfma_probe_kernel<2>, g, b4, 0, s, iters, out); break;
+        case 3: hipLaunchKernelGGL(mfma_probe_kernel<3>, g, b4, 0, s, iters, out); break;
+        case 4: hipLaunchKernelGGL((coexec_probe_kernel<true, false, false>), g, b8, 0, s, iters, out); break;
+        case 5: hipLaunchKernelGGL((coexec_probe_kernel<false, true, false>), g, b8, 0, s, iters, out); break;
+        case 6: hipLaunchKernelGGL((coexec_probe_kernel<true, true, false>), g, b8, 0, s, iters, out); break;
+        case 7: hipLaunchKernelGGL((coexec_probe_kernel<true, false, true>), g, b8, 0, s, iters, out); break;
+        default: hipLaunchKernelGGL((coexec_probe_kernel<true, true, true>), g, b8, 0, s, iters, out); break;
     }
     return hipGetLastError() == hipSuccess ? RLQ_OK : RLQ_DEVICE_ERROR;
 }
