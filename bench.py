@@ -294,6 +294,33 @@ def probe_peaks(rlq, torch, reps):
                            "note": "33,030,144 weight bytes read with the one-column matvec's grid (one workgroup "
                                    "of 16 waves per CU) and 1 KB non-temporal load runs, 10 rotated copies, "
                                    "launched back to back"}
+    # the same bytes read with other launch shapes: waves per workgroup, 1 KB
+    # runs in flight per wave, workgroups per CU, non-temporal or plain loads
+    sweep = {}
+    for waves, runs, per_cu, nt in ((16, 1, 1, 1), (16, 2, 1, 1), (16, 4, 1, 1), (16, 8, 1, 1), (16, 2, 1, 0),
+                                    (8, 2, 2, 1), (8, 4, 2, 1), (8, 4, 4, 1), (4, 4, 4, 1), (4, 8, 4, 1),
+                                    (4, 4, 8, 1)):
+        def read_shape(i):
+            rc = rlq._lib.rlq_probe_stream_shape(ctypes.c_void_p(bufs[i % copies].data_ptr()), nbytes, per_cu * cus,
+                                                 waves, runs, nt, ctypes.c_void_p(sink.data_ptr()), sp)
+            if rc != 0:
+                raise RuntimeError(f"rlq_probe_stream_shape: {rc}")
+
+        for i in range(30):
+            read_shape(i)
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        n = 500
+        a.record(stream)
+        for i in range(n):
+            read_shape(i)
+        b.record(stream)
+        torch.cuda.synchronize()
+        sweep[f"{waves}w_{runs}r_{per_cu}wg_{'nt' if nt else 'plain'}"] = round(a.elapsed_time(b) / n * 1e3, 3)
+    best = min(sweep, key=sweep.get)
+    out["stream_shapes_us"] = {"passes": sweep, "best": best,
+                               "note": "the stream floor's bytes read with other launch shapes (waves per workgroup, "
+                                       "1 KB runs in flight per wave, workgroups per CU, load kind)"}
     del bufs
     return out
 

@@ -498,8 +498,8 @@ int32_t rlq_gguf_write(const char *path, const rlq_gguf_kv *kv, uint64_t n_kv, c
  * No counterpart in the reference: kernels that measure this GPU's practical
  * ceilings for the benchmark, next to the spec peaks.  Both are asynchronous
  * on `stream` and write one word per wave to `out` (4 words per workgroup
- * for rlq_probe_mfma kinds 0-3, 8 for kinds 4-8, 16 for rlq_probe_stream) so
- * that no work is dead. */
+ * for rlq_probe_mfma kinds 0-3, 8 for kinds 4-8, 16 for rlq_probe_stream,
+ * `waves` for rlq_probe_stream_shape) so that no work is dead. */
 /* kind 0: v_mfma_i32_32x32x32_i8, kind 1: v_mfma_f32_32x32x16_f16; each of
  * the 4 waves of `workgroups` 256-thread workgroups runs 4 independent
  * accumulator chains of `iters` MFMAs from registers.  kind 2: `iters` steps
@@ -516,6 +516,12 @@ int32_t rlq_probe_mfma(uint32_t kind, uint32_t workgroups, uint32_t iters, uint3
  * 16-byte non-temporal loads: the one-column matvec's launch shape and load
  * pattern without its arithmetic. */
 int32_t rlq_probe_stream(const void *bytes, uint64_t len, uint32_t workgroups, uint32_t *out, void *stream);
+/* The same read by `workgroups` workgroups of `waves` (4, 8 or 16) waves, each
+ * wave keeping `runs` (1, 2, 4 or 8) 1 KB runs in flight, with non-temporal
+ * loads when `non_temporal` is nonzero, else plain ones; rlq_probe_stream is
+ * (16, 2, non-temporal).  Other values: RLQ_INVALID_ARGUMENT. */
+int32_t rlq_probe_stream_shape(const void *bytes, uint64_t len, uint32_t workgroups, uint32_t waves, uint32_t runs,
+                               uint32_t non_temporal, uint32_t *out, void *stream);
 
 #ifdef __cplusplus
 }

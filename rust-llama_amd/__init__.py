@@ -191,6 +191,7 @@ SIGNATURES = {
     "rlq_llama_trace": ([_P, _P, _E], _I32),
     "rlq_probe_mfma": ([_U32, _U32, _U32, _P, _P], _I32),
     "rlq_probe_stream": ([_P, _U64, _U32, _P, _P], _I32),
+    "rlq_probe_stream_shape": ([_P, _U64, _U32, _U32, _U32, _U32, _P, _P], _I32),
 }
 
 

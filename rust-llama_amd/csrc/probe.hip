@@ -12,7 +12,8 @@
 //    launch shape (one workgroup of 16 waves per CU) and load pattern (each
 //    wave instruction a 1 KB run of 16-byte non-temporal loads), XORed and
 //    never written back: the time a pass over the matvec's bytes takes with
-//    no arithmetic.
+//    no arithmetic; rlq_probe_stream_shape the same read with other
+//    workgroup sizes, runs in flight per wave and load kinds.
 #include "rlq_device.hpp"
 #include "rlq.h"
 #include "rlq_internal.hpp"
@@ -127,25 +128,51 @@ __global__ __launch_bounds__(512) void coexec_probe_kernel(uint32_t iters, uint3
     if (lane == 0) out[gw] = __float_as_uint(r);
 }
 
-// Workgroup g of `grid` reads its equal share of the n16 16-byte units: wave
-// w's 1 KB runs w, w + 16, ... of the share, two runs in flight per wave.
-__global__ __launch_bounds__(1024) void stream_probe_kernel(const uint8_t* p, uint64_t n16, uint32_t* out) {
+// Workgroup g of `grid` (W waves) reads its equal share of the n16 16-byte
+// units in 1 KB runs: wave w takes runs w, w + W, ... of the share, R of them
+// in flight (NT: non-temporal loads), XORed and never written back.
+template <int W, int R, bool NT>
+__global__ __launch_bounds__(W * 64) void stream_probe_kernel(const uint8_t* p, uint64_t n16, uint32_t* out) {
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint64_t runs = n16 / 64, per = (runs + gridDim.x - 1) / gridDim.x;
     const uint64_t r0 = (uint64_t)blockIdx.x * per, r1 = r0 + per < runs ? r0 + per : runs;
     uint32_t x = 0;
     uint64_t r = r0 + wave;
-    for (; r + 16 < r1; r += 32) {
-        const uint4 v0 = load_stream16(p + (r * 64 + lane) * 16);
-        const uint4 v1 = load_stream16(p + ((r + 16) * 64 + lane) * 16);
-        x ^= v0.x ^ v0.y ^ v0.z ^ v0.w ^ v1.x ^ v1.y ^ v1.z ^ v1.w;
+    for (; r + (uint64_t)(R - 1) * W < r1; r += (uint64_t)R * W) {  // the R runs all below r1
+        uint4 v[R];
+#pragma unroll
+        for (int k = 0; k < R; ++k) {
+            const uint8_t* q = p + ((r + (uint64_t)k * W) * 64 + lane) * 16;
+            v[k] = NT ? load_stream16(q) : *(const uint4*)q;
+        }
+        __builtin_amdgcn_sched_barrier(0);  // all R loads issued before the first use
+#pragma unroll
+        for (int k = 0; k < R; ++k) x ^= v[k].x ^ v[k].y ^ v[k].z ^ v[k].w;
     }
-    if (r < r1) {
-        const uint4 v = load_stream16(p + (r * 64 + lane) * 16);
+    for (; r < r1; r += W) {
+        const uint8_t* q = p + (r * 64 + lane) * 16;
+        const uint4 v = NT ? load_stream16(q) : *(const uint4*)q;
         x ^= v.x ^ v.y ^ v.z ^ v.w;
     }
     x ^= (uint32_t)__shfl_xor((int)x, 32, 64);
-    if (lane == 0) out[blockIdx.x * 16 + wave] = x;
+    if (lane == 0) out[blockIdx.x * W + wave] = x;
+}
+
+template <int W, int R, bool NT>
+static void launch_stream(const void* bytes, uint64_t len, uint32_t workgroups, uint32_t* out, hipStream_t s) {
+    hipLaunchKernelGGL((stream_probe_kernel<W, R, NT>), dim3(workgroups), dim3(W * 64), 0, s, (const uint8_t*)bytes,
+                       len / 16, out);
+}
+template <int W, bool NT>
+static bool launch_stream_runs(uint32_t runs, const void* bytes, uint64_t len, uint32_t workgroups, uint32_t* out,
+                               hipStream_t s) {
+    switch (runs) {
+        case 1: launch_stream<W, 1, NT>(bytes, len, workgroups, out, s); return true;
+        case 2: launch_stream<W, 2, NT>(bytes, len, workgroups, out, s); return true;
+        case 4: launch_stream<W, 4, NT>(bytes, len, workgroups, out, s); return true;
+        case 8: launch_stream<W, 8, NT>(bytes, len, workgroups, out, s); return true;
+        default: return false;
+    }
 }
 
 }  // namespace rlq
@@ -170,10 +197,25 @@ extern "C" int32_t rlq_probe_mfma(uint32_t kind, uint32_t workgroups, uint32_t i
     return hipGetLastError() == hipSuccess ? RLQ_OK : RLQ_DEVICE_ERROR;
 }
 
+extern "C" int32_t rlq_probe_stream_shape(const void* bytes, uint64_t len, uint32_t workgroups, uint32_t waves,
+                                          uint32_t runs, uint32_t non_temporal, uint32_t* out, void* stream) {
+    if (!bytes || !out || workgroups == 0 || len % 1024 != 0 || ((uintptr_t)bytes & 15)) return RLQ_INVALID_ARGUMENT;
+    const hipStream_t s = (hipStream_t)stream;
+    bool ok;
+    switch (waves * 2 + (non_temporal ? 1 : 0)) {
+        case 8: ok = launch_stream_runs<4, false>(runs, bytes, len, workgroups, out, s); break;
+        case 9: ok = launch_stream_runs<4, true>(runs, bytes, len, workgroups, out, s); break;
+        case 16: ok = launch_stream_runs<8, false>(runs, bytes, len, workgroups, out, s); break;
+        case 17: ok = launch_stream_runs<8, true>(runs, bytes, len, workgroups, out, s); break;
+        case 32: ok = launch_stream_runs<16, false>(runs, bytes, len, workgroups, out, s); break;
+        case 33: ok = launch_stream_runs<16, true>(runs, bytes, len, workgroups, out, s); break;
+        default: ok = false;
+    }
+    if (!ok) return RLQ_INVALID_ARGUMENT;
+    return hipGetLastError() == hipSuccess ? RLQ_OK : RLQ_DEVICE_ERROR;
+}
+
 extern "C" int32_t rlq_probe_stream(const void* bytes, uint64_t len, uint32_t workgroups, uint32_t* out,
                                     void* stream) {
-    if (!bytes || !out || workgroups == 0 || len % 1024 != 0 || ((uintptr_t)bytes & 15)) return RLQ_INVALID_ARGUMENT;
-    hipLaunchKernelGGL(stream_probe_kernel, dim3(workgroups), dim3(1024), 0, (hipStream_t)stream,
-                       (const uint8_t*)bytes, len / 16, out);
-    return hipGetLastError() == hipSuccess ? RLQ_OK : RLQ_DEVICE_ERROR;
+    return rlq_probe_stream_shape(bytes, len, workgroups, 16, 2, 1, out, stream);
 }
