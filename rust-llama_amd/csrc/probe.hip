@@ -200,6 +200,7 @@ extern "C" int32_t rlq_probe_mfma(uint32_t kind, uint32_t workgroups, uint32_t i
 extern "C" int32_t rlq_probe_stream_shape(const void* bytes, uint64_t len, uint32_t workgroups, uint32_t waves,
                                           uint32_t runs, uint32_t non_temporal, uint32_t* out, void* stream) {
     if (!bytes || !out || workgroups == 0 || len % 1024 != 0 || ((uintptr_t)bytes & 15)) return RLQ_INVALID_ARGUMENT;
+    if (waves != 4 && waves != 8 && waves != 16) return RLQ_INVALID_ARGUMENT;
     const hipStream_t s = (hipStream_t)stream;
     bool ok;
     switch (waves * 2 + (non_temporal ? 1 : 0)) {

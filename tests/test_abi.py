@@ -93,3 +93,21 @@ def test_non_path_types_are_unimplemented_not_silently_wrong():
     with pytest.raises(rlq.QuantError) as g:
         rlq.quantize(rlq.DType.I64, np.zeros(256, np.float32))
     assert g.value.name == "UnsupportedQuantization"
+
+
+def test_probe_arguments_refused_before_any_launch():
+    """The measurement probes check their arguments before any device call:
+    unknown kinds, shapes and runs, a misaligned or ragged buffer, no output
+    (the pointers are never dereferenced on these paths)."""
+    lib = rlq.lib()
+    invalid = 20  # RLQ_INVALID_ARGUMENT
+    assert rlq.ERROR_NAMES[invalid] == "InvalidArgument"
+    fake = ctypes.c_void_p(4096)
+    assert lib.rlq_probe_mfma(9, 1, 1, fake, None) == invalid
+    assert lib.rlq_probe_mfma(0, 0, 1, fake, None) == invalid
+    assert lib.rlq_probe_mfma(0, 1, 1, None, None) == invalid
+    for waves, runs, length, ptr in ((3, 2, 1024, fake), (32, 2, 1024, fake), (2 ** 31 + 4, 2, 1024, fake),
+                                     (16, 3, 1024, fake), (16, 0, 1024, fake), (16, 2, 1000, fake),
+                                     (16, 2, 1024, ctypes.c_void_p(4100))):
+        assert lib.rlq_probe_stream_shape(ptr, length, 1, waves, runs, 1, fake, None) == invalid, (waves, runs)
+    assert lib.rlq_probe_stream(fake, 1000, 1, fake, None) == invalid
