@@ -9,7 +9,8 @@ Bars, as in test_gpu_parity: column 0's per-block integers bitwise (every
 batch for Q4_K, up to 8 columns otherwise), every column's f32 outputs within
 relative L2 1e-5 of the oracle, and bitwise where the kernels keep the
 reference's f32 order (Q8_0 and Q2_K at every batch, Q3_K, Q4_K, Q5_K and
-Q6_K with one column).  Weights: the library's encoder on N(0, 0.02)
+Q6_K with one column).  A second draw of 48 cases takes most row counts at random and
+batches of 13 to 33.  Weights: the library's encoder on N(0, 0.02)
 values for Q4_K, Q6_K and Q8_0; random GGUF blocks (random quants and scales,
 finite positive f16 super-scales) for Q2_K, Q3_K and Q5_K, as in
 test_gpu_kformats.  Every case prints itself before touching the GPU.
@@ -40,23 +41,26 @@ BATCHES = (1, 1, 1, 2, 3, 4, 5, 6, 7, 8, 9, 12)
 MAX_BLOCKS = {"k": 16384 * 16, "q8_0": 16384 * 128}  # bounds the oracle's work per case
 
 
-def _cases(n=96, seed=0x5EED):
+def _cases(n=96, seed=0x5EED, batches=BATCHES, pooled=0.7):
     rng = np.random.default_rng(seed)
     out = []
     for i in range(n):
         t = TYPES[i % len(TYPES)]
-        rows = int(rng.choice(ROW_POOL)) if rng.random() < 0.7 else int(rng.integers(1, 17000))
+        rows = int(rng.choice(ROW_POOL)) if rng.random() < pooled else int(rng.integers(1, 17000))
         if t == DT.Q8_0:
             nb, bs, cap = int(rng.choice(NB_POOL_Q8_0)), 32, MAX_BLOCKS["q8_0"]
         else:
             nb, bs, cap = int(rng.choice(NB_POOL)), 256, MAX_BLOCKS["k"]
         while rows * nb > cap and nb > 1:
             nb //= 2
-        out.append((t, rows, nb * bs, int(rng.choice(BATCHES))))
+        out.append((t, rows, nb * bs, int(rng.choice(batches))))
     return out
 
 
 CASES = _cases()
+# a second draw: row counts mostly at random, batches of 13 to 33 (two to
+# five passes of the decode kernels; Q4_K's GEMM with one ragged token tile)
+CASES_WIDE = _cases(48, seed=0xC0FFEE, batches=(1, 2, 5, 8, 13, 16, 17, 24, 31, 33), pooled=0.3)
 
 
 def say(*a):
@@ -95,8 +99,8 @@ def test_sweep_covers_the_dispatch_boundaries():
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("t,rows,cols,batch", CASES,
-                         ids=[f"{DT(c[0]).name}-{c[1]}x{c[2]}-b{c[3]}" for c in CASES])
+@pytest.mark.parametrize("t,rows,cols,batch", CASES + CASES_WIDE,
+                         ids=[f"{DT(c[0]).name}-{c[1]}x{c[2]}-b{c[3]}" for c in CASES + CASES_WIDE])
 def test_sweep(t, rows, cols, batch):
     say("sweep", DT(t).name, rows, cols, "batch", batch)
     seed = rows * 131 + cols * 7 + batch + int(t)
