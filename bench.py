@@ -67,7 +67,7 @@ TRAFFIC_DECODE_BYTES = 33351490
 TRAFFIC_PREFILL_BYTES = 98617131 + 12975038
 # the same measurement for the kernels of the other configurations (per launch)
 TRAFFIC_CONFIG_BYTES = {
-    "q8_0_4864x896_b1": 4963715,
+    "q8_0_4864x896_b1": 4961661,
     "q4k_14336x4096_b4": 34064124,
     "q4k_14336x4096_b8": 33980196 + 224233,  # the matvec, then the planes kernel
     "q6k_128256x4096_b1_argmax": 436357969,

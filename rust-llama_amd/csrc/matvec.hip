@@ -3231,6 +3231,17 @@ hipError_t launch_matvec_ex(uint32_t wtype, const uint8_t* w, uint64_t rows, uin
                     return dbg ? launch_one<2 * W, q6k_mv_kernel<2 * W, 3, true>>(a, lds, s, pairs, 1)
                                : launch_one<2 * W, q6k_mv_kernel<2 * W, 3, false>>(a, lds, s, pairs, 1);
                 default:
+                    // the K split by block pairs per row (batch 1 / 4 / 8, us, against
+                    // 8 waves of a 4-way split): a 16-way split of 16 waves from 32
+                    // pairs (896x4864 9.0 / 11.2 / 14.3 against 23.5 / 27.9 / 34.6,
+                    // 4096x4096 8.8 / 10.5 / 13.1 against 12.7 / 15.1 / 29.6), an
+                    // 8-way split of 16 waves from 12 (14336x4096 20.5 / 24.2 against
+                    // 24.5 / 29.2 where the 16-way split would need two tiles per slot;
+                    // 4864x896 6.53 against 6.62, 10.5 with the 16-way split)
+                    if (a.nchunks >= 32 && q8_0_ks_takes<16, 16>(a, pairs))
+                        return dbg ? launch_q8_0_ks<16, 16, true>(a, s, pairs) : launch_q8_0_ks<16, 16, false>(a, s, pairs);
+                    if (a.nchunks >= 12 && q8_0_ks_takes<16, 8>(a, pairs))
+                        return dbg ? launch_q8_0_ks<16, 8, true>(a, s, pairs) : launch_q8_0_ks<16, 8, false>(a, s, pairs);
                     if (q8_0_ks_takes<8, 4>(a, pairs))
                         return dbg ? launch_q8_0_ks<8, 4, true>(a, s, pairs) : launch_q8_0_ks<8, 4, false>(a, s, pairs);
                     // ten chunks in flight per wave (151936x896 + argmax: 30.3 us
