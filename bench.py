@@ -713,6 +713,9 @@ def main():
             "q3k_14336x4096_b8": (DT.Q3_K, 14336, 4096, 8, ROTATE),
             "q2k_14336x4096_b1": (DT.Q2_K, 14336, 4096, 1, ROTATE),
             "q2k_14336x4096_b8": (DT.Q2_K, 14336, 4096, 8, ROTATE),
+            # the Q6_K matrices of a Q4_K_M file below the output head: ffn_down, attn_v
+            "q6k_4096x14336_b1": (DT.Q6_K, 4096, 14336, 1, ROTATE),
+            "q6k_1024x4096_b1": (DT.Q6_K, 1024, 4096, 1, 9 * ROTATE),  # 3.4 MB: 310 MB over the copies
         }.items():
             o, hs, _, _ = run_config(rlq, ctx, t, r, c, b, 0x51A7E000 + len(extra), max(200, args.steps // 4),
                                      args.warmup, copies)

@@ -1785,19 +1785,84 @@ __global__ __launch_bounds__(W * 64) void q6k_mv_kernel(MvArgs a) {
 // off = 0, 1, 4, 5 for the four weight operands; the lanes kq and kq ^ 2
 // hold the other eight groups of the same classes.  A wave takes whole tiles
 // and walks their blocks in order, so the accumulators stay in registers.
+// Loads of one Q6_K chunk (rlq_layout.hpp): the ql pieces of lane `ln` and
+// the high bits, scales and super-scale of row `r` (a lane's own: ln = lane,
+// r = n; a half tile's lane pairs load row r of the pair, ln = 16 kq + r).
+__device__ __forceinline__ void q6_issue(Q6Step& st, const uint8_t* base, uint32_t ln, uint32_t r, uint32_t kq) {
+    st.l0 = load_stream16(base + ln * 16);
+    st.l1 = load_stream16(base + 1024 + ln * 16);
+    st.h0 = load_stream16(base + 2048 + r * 64 + 32 * (kq >> 1));
+    st.h1 = load_stream16(base + 2048 + r * 64 + 32 * (kq >> 1) + 16);
+    st.sc = load_stream16(base + 3072 + r * 16);
+    st.d = __builtin_nontemporal_load((const uint16_t*)(base + 3328 + r * 2));
+}
+
+// The one-column class operands of lane (n, kq): A row n stands for class
+// n % 8 of K quarter n / 8 (first MFMA of a pair) or 2 + n / 8 (second); the
+// lane's activations (K quarter kq of the block's image, a_step bytes per
+// block, or the zero bytes where neither MFMA is live) masked by m0 / m1 to
+// the class's bytes.
+struct Q6OneOps {
+    const uint8_t* a_ptr;
+    uint32_t a_step, lsh, rsh, g2;
+    uint32_t m0[4], m1[4];
+};
+__device__ __forceinline__ Q6OneOps q6_one_ops(const uint8_t* lds, const LdsMap& L, uint32_t n, uint32_t kq) {
+    Q6OneOps o;
+    const uint32_t s1 = kq & 1;
+    o.lsh = 4 - 2 * s1, o.rsh = 2 * s1;
+    const uint32_t cls = n & 7, qsel = n >> 3;
+    const bool live0 = kq == qsel, live1 = kq == 2 + qsel;
+    o.a_ptr = live0 || live1 ? lds + 16 * (8 * (kq >> 1) + 2 * (kq & 1)) : lds + L.zero_off;
+    o.a_step = live0 || live1 ? 256 : 0;
+    const uint32_t byte = 0xffu << (8 * (cls & 3));
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+        const uint32_t mk = (uint32_t)(w & 1) == (cls >> 2) ? byte : 0u;
+        o.m0[w] = live0 ? mk : 0u;
+        o.m1[w] = live1 ? mk : 0u;
+    }
+    o.g2 = 16 * (kq >> 1);  // bit offset of scale bytes 2 (kq / 2), + 1 in each scale word
+    return o;
+}
+// Block integers of one chunk in lane (n, kq): I[i] = the exact dot of row n
+// over class 4 (kq % 2) + i (elements j with j % 8 == class), scale groups
+// included, summed over the lane's K half (lanes kq and kq ^ 2 hold the
+// other half until the caller's sum_xor32).  p = the block's activations.
+__device__ __forceinline__ void q6_one_ints(const Q6Step& cur, const Q6OneOps& o, const uint8_t* p, int32_t (&I)[4]) {
+    const i32x4 w00 = {(int)q6_lo(cur.l0.x, cur.h0.x, o.lsh), (int)q6_lo(cur.l0.y, cur.h0.y, o.lsh),
+                       (int)q6_lo(cur.l0.z, cur.h0.z, o.lsh), (int)q6_lo(cur.l0.w, cur.h0.w, o.lsh)};
+    const i32x4 w01 = {(int)q6_lo(cur.l1.x, cur.h1.x, o.lsh), (int)q6_lo(cur.l1.y, cur.h1.y, o.lsh),
+                       (int)q6_lo(cur.l1.z, cur.h1.z, o.lsh), (int)q6_lo(cur.l1.w, cur.h1.w, o.lsh)};
+    const i32x4 w10 = {(int)q6_hi(cur.l0.x, cur.h0.x, o.rsh), (int)q6_hi(cur.l0.y, cur.h0.y, o.rsh),
+                       (int)q6_hi(cur.l0.z, cur.h0.z, o.rsh), (int)q6_hi(cur.l0.w, cur.h0.w, o.rsh)};
+    const i32x4 w11 = {(int)q6_hi(cur.l1.x, cur.h1.x, o.rsh), (int)q6_hi(cur.l1.y, cur.h1.y, o.rsh),
+                       (int)q6_hi(cur.l1.z, cur.h1.z, o.rsh), (int)q6_hi(cur.l1.w, cur.h1.w, o.rsh)};
+    // one weight operand: its scale groups' signed scales sa (first MFMA)
+    // and sb (second); |dot| <= 2 * 32 * 128 and |scale| <= 128 fit the
+    // 24-bit multiplies
+    auto pair = [&](const i32x4& wop, uint32_t aoff, int32_t sa, int32_t sb) {
+        const uint4 x = *(const uint4*)(p + aoff);
+        const i32x4 A0 = {(int)(x.x & o.m0[0]), (int)(x.y & o.m0[1]), (int)(x.z & o.m0[2]), (int)(x.w & o.m0[3])};
+        const i32x4 A1 = {(int)(x.x & o.m1[0]), (int)(x.y & o.m1[1]), (int)(x.z & o.m1[2]), (int)(x.w & o.m1[3])};
+        const i32x4 d0 = mfma_i8(A0, wop), d1 = mfma_i8(A1, wop);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) I[i] = mad24(sa, d0[i], mad24(sb, d1[i], I[i]));
+    };
+    const uint32_t g2 = o.g2;
+    pair(w00, 0, __builtin_amdgcn_sbfe((int)cur.sc.x, g2, 8), __builtin_amdgcn_sbfe((int)cur.sc.z, g2, 8));
+    pair(w01, 16, __builtin_amdgcn_sbfe((int)cur.sc.x, g2 + 8, 8), __builtin_amdgcn_sbfe((int)cur.sc.z, g2 + 8, 8));
+    pair(w10, 64, __builtin_amdgcn_sbfe((int)cur.sc.y, g2, 8), __builtin_amdgcn_sbfe((int)cur.sc.w, g2, 8));
+    pair(w11, 80, __builtin_amdgcn_sbfe((int)cur.sc.y, g2 + 8, 8), __builtin_amdgcn_sbfe((int)cur.sc.w, g2 + 8, 8));
+}
+
 template <int W, int D, bool DBG>
 __global__ __launch_bounds__(W * 64) void q6k_mv_one_kernel(MvArgs a) {
     RLQ_MV_PROLOGUE(kQ6_K, a.nb)
     const uint32_t nb = a.nb;
     Q6Step buf[D];
     auto issue = [&](Q6Step& st) {
-        const uint8_t* base = a.w + ((uint64_t)ld_tile * nb + ld_chunk) * kQ6KChunk;
-        st.l0 = load_stream16(base + lane * 16);
-        st.l1 = load_stream16(base + 1024 + lane * 16);
-        st.h0 = load_stream16(base + 2048 + n * 64 + 32 * (kq >> 1));
-        st.h1 = load_stream16(base + 2048 + n * 64 + 32 * (kq >> 1) + 16);
-        st.sc = load_stream16(base + 3072 + n * 16);
-        st.d = __builtin_nontemporal_load((const uint16_t*)(base + 3328 + n * 2));
+        q6_issue(st, a.w + ((uint64_t)ld_tile * nb + ld_chunk) * kQ6KChunk, lane, n, kq);
         next_load();
     };
 #pragma unroll
@@ -1807,53 +1872,14 @@ __global__ __launch_bounds__(W * 64) void q6k_mv_one_kernel(MvArgs a) {
     if (!ok) return finish_argmax(a, lds, L);
     if (a.zero_pair) return zero_wave_tiles(a, gw, tw, n, kq);
 
-    const uint32_t s1 = kq & 1, lsh = 4 - 2 * s1, rsh = 2 * s1;
-    // this lane's A operand: K quarter kq of A row n, i.e. scale group
-    // {0, 2, 8, 10}[kq] of the operand, masked to class n % 8; live in the
-    // first MFMA of a pair when kq == n / 8, in the second when kq == 2 + n / 8
-    const uint32_t cls = n & 7, qsel = n >> 3;
-    const bool live0 = kq == qsel, live1 = kq == 2 + qsel;
-    const uint8_t* a_ptr = live0 || live1 ? lds + 16 * (8 * (kq >> 1) + 2 * (kq & 1)) : lds + L.zero_off;
-    const uint32_t a_step = live0 || live1 ? 256 : 0;
-    const uint32_t byte = 0xffu << (8 * (cls & 3));
-    uint32_t m0[4], m1[4];  // the masks of the two MFMAs (zero where not live)
-#pragma unroll
-    for (int w = 0; w < 4; ++w) {
-        const uint32_t mk = (uint32_t)(w & 1) == (cls >> 2) ? byte : 0u;
-        m0[w] = live0 ? mk : 0u;
-        m1[w] = live1 ? mk : 0u;
-    }
-    const uint32_t g2 = 16 * (kq >> 1);  // bit offset of scale bytes 2 (kq / 2), + 1 in each scale word
+    const Q6OneOps ops = q6_one_ops(lds, L, n, kq);
 
     float lanes[4] = {0.0f, 0.0f, 0.0f, 0.0f};  // classes 4 (kq % 2) + i
     unsigned long long best = 0;
     uint32_t tile = gw, blk = 0;
     auto compute = [&](const Q6Step& cur) {
-        const i32x4 w00 = {(int)q6_lo(cur.l0.x, cur.h0.x, lsh), (int)q6_lo(cur.l0.y, cur.h0.y, lsh),
-                           (int)q6_lo(cur.l0.z, cur.h0.z, lsh), (int)q6_lo(cur.l0.w, cur.h0.w, lsh)};
-        const i32x4 w01 = {(int)q6_lo(cur.l1.x, cur.h1.x, lsh), (int)q6_lo(cur.l1.y, cur.h1.y, lsh),
-                           (int)q6_lo(cur.l1.z, cur.h1.z, lsh), (int)q6_lo(cur.l1.w, cur.h1.w, lsh)};
-        const i32x4 w10 = {(int)q6_hi(cur.l0.x, cur.h0.x, rsh), (int)q6_hi(cur.l0.y, cur.h0.y, rsh),
-                           (int)q6_hi(cur.l0.z, cur.h0.z, rsh), (int)q6_hi(cur.l0.w, cur.h0.w, rsh)};
-        const i32x4 w11 = {(int)q6_hi(cur.l1.x, cur.h1.x, rsh), (int)q6_hi(cur.l1.y, cur.h1.y, rsh),
-                           (int)q6_hi(cur.l1.z, cur.h1.z, rsh), (int)q6_hi(cur.l1.w, cur.h1.w, rsh)};
-        const uint8_t* p = a_ptr + blk * a_step;
         int32_t I[4] = {0, 0, 0, 0};
-        // one weight operand: its scale groups' signed scales sa (first MFMA)
-        // and sb (second); |dot| <= 2 * 32 * 128 and |scale| <= 128 fit the
-        // 24-bit multiplies
-        auto pair = [&](const i32x4& wop, uint32_t aoff, int32_t sa, int32_t sb) {
-            const uint4 x = *(const uint4*)(p + aoff);
-            const i32x4 A0 = {(int)(x.x & m0[0]), (int)(x.y & m0[1]), (int)(x.z & m0[2]), (int)(x.w & m0[3])};
-            const i32x4 A1 = {(int)(x.x & m1[0]), (int)(x.y & m1[1]), (int)(x.z & m1[2]), (int)(x.w & m1[3])};
-            const i32x4 d0 = mfma_i8(A0, wop), d1 = mfma_i8(A1, wop);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) I[i] = mad24(sa, d0[i], mad24(sb, d1[i], I[i]));
-        };
-        pair(w00, 0, __builtin_amdgcn_sbfe((int)cur.sc.x, g2, 8), __builtin_amdgcn_sbfe((int)cur.sc.z, g2, 8));
-        pair(w01, 16, __builtin_amdgcn_sbfe((int)cur.sc.x, g2 + 8, 8), __builtin_amdgcn_sbfe((int)cur.sc.z, g2 + 8, 8));
-        pair(w10, 64, __builtin_amdgcn_sbfe((int)cur.sc.y, g2, 8), __builtin_amdgcn_sbfe((int)cur.sc.w, g2, 8));
-        pair(w11, 80, __builtin_amdgcn_sbfe((int)cur.sc.y, g2 + 8, 8), __builtin_amdgcn_sbfe((int)cur.sc.w, g2 + 8, 8));
+        q6_one_ints(cur, ops, ops.a_ptr + blk * ops.a_step, I);
         const float d = half_to_float(cur.d) * *(const float*)(lds + L.d_off + blk * 32);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -2539,27 +2565,76 @@ __global__ __launch_bounds__(W * 64) void q3k_mv_one_kernel(MvArgs a) {
     finish_argmax(a, lds, L);
 }
 
-// Q3_K, one column, the blocks of each tile split over KS waves: the class
-// dots of q3k_mv_one_kernel, each block's four class terms d * integers[l]
-// (rounded to f32, matvec_extra.rs:287-289) parked in LDS per lane (classes
-// 0..3 in lane kq = 0 of row n, 4..7 in lane kq = 1), and after the last
-// step one wave per tile slot forms each row's sum in the reference's order:
-// lanes[l] over the blocks in order, then sum = 0 + lanes[0] + ... + lanes[7].
-// LDS after the Q8_K image: [tmax][TS][nb][32] float4.  BAL: the balanced
-// deal over a.deal_cus CUs (balanced_deal; one tile per slot, a half tile
-// read by lane pairs and stored by its own half).
-__host__ __device__ inline uint32_t q3_part_off(uint32_t cols) { return (lds_map(kQ3_K, cols, 1).total + 15u) & ~15u; }
-__host__ __device__ inline uint32_t q3_split_lds(uint32_t cols, uint32_t tmax, uint32_t ts) {
-    return q3_part_off(cols) + tmax * ts * (cols / 256) * 512u;
+// Q3_K and Q6_K, one column, the blocks of each tile split over KS waves:
+// the class dots of q3k_mv_one_kernel / q6k_mv_one_kernel, each block's four
+// class terms d * integers[l] (rounded to f32, matvec_extra.rs:287-289)
+// parked in LDS per lane (classes 0..3 in lane kq = 0 of row n, 4..7 in lane
+// kq = 1), and after the last step one wave per tile slot forms each row's
+// sum in the reference's order: lanes[l] over the blocks in order, then
+// sum = 0 + lanes[0] + ... + lanes[7].  LDS after the Q8_K image:
+// [tmax][TS][nb][32] float4.  BAL: the balanced deal over a.deal_cus CUs
+// (balanced_deal; one tile per slot, a half tile read by lane pairs and
+// stored by its own half).
+__host__ __device__ inline uint32_t split_part_off(uint32_t t, uint32_t cols) {
+    return (lds_map(t, cols, 1).total + 15u) & ~15u;
+}
+__host__ __device__ inline uint32_t split_lds(uint32_t t, uint32_t cols, uint32_t tmax, uint32_t ts) {
+    return split_part_off(t, cols) + tmax * ts * (cols / 256) * 512u;
 }
 
-template <int W, int KS, int D, bool DBG, bool BAL = false>
-__global__ __launch_bounds__(W * 64) void q3k_mv_split_kernel(MvArgs a) {
+// The Q3_K class operands of lane (n, kq), as q3k_mv_one_kernel's: the
+// lane's activations (a_step bytes per block; the zero bytes where neither
+// MFMA of a pair is live) masked by m0 / m1 to class n % 8.
+struct Q3OneOps {
+    const uint8_t* a_ptr;
+    uint32_t a_step, hsh, sb0;
+    uint32_t m0[4], m1[4];
+};
+__device__ __forceinline__ Q3OneOps q3_one_ops(const uint8_t* lds, const LdsMap& L, uint32_t n, uint32_t kq) {
+    Q3OneOps o;
+    o.hsh = 4 * (kq >> 1), o.sb0 = kq >> 1;
+    const uint32_t cls = n & 7, qsel = n >> 3;
+    const bool live0 = kq == qsel, live1 = kq == 2 + qsel;
+    o.a_ptr = live0 || live1 ? lds + 128 * (kq >> 1) + 16 * (kq & 1) : lds + L.zero_off;
+    o.a_step = live0 || live1 ? 256 : 0;
+    const uint32_t byte = 0xffu << (8 * (cls & 3));
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+        const uint32_t mk = (uint32_t)(w & 1) == (cls >> 2) ? byte : 0u;
+        o.m0[w] = live0 ? mk : 0u;
+        o.m1[w] = live1 ? mk : 0u;
+    }
+    return o;
+}
+__device__ __forceinline__ void q3_one_ints(const K16Step<kQ3_K>& cur, const Q3OneOps& ops, const uint8_t* p,
+                                            int32_t (&I)[4]) {
+    const K16Ops<kQ3_K> o = k16_ops<kQ3_K>(cur, ops.hsh);
+#pragma unroll
+    for (int sft = 0; sft < 4; ++sft) {
+        const uint4 x = *(const uint4*)(p + 32 * sft);
+        const i32x4 A0 = {(int)(x.x & ops.m0[0]), (int)(x.y & ops.m0[1]), (int)(x.z & ops.m0[2]), (int)(x.w & ops.m0[3])};
+        const i32x4 A1 = {(int)(x.x & ops.m1[0]), (int)(x.y & ops.m1[1]), (int)(x.z & ops.m1[2]), (int)(x.w & ops.m1[3])};
+        const i32x4 d0 = mfma_i8(A0, o.wv[sft]), d1 = mfma_i8(A1, o.wv[sft]);
+        const int32_t sa = sbyte(o.c[sft >> 1], 2 * (sft & 1) + ops.sb0);
+        const int32_t sb = sbyte(o.c[2 + (sft >> 1)], 2 * (sft & 1) + ops.sb0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) I[i] = mad24(sa, d0[i], mad24(sb, d1[i], I[i]));
+    }
+}
+
+template <uint32_t T>
+using SplitStep = std::conditional_t<T == kQ6_K, Q6Step, K16Step<kQ3_K>>;
+template <uint32_t T>
+using SplitOps = std::conditional_t<T == kQ6_K, Q6OneOps, Q3OneOps>;
+
+template <uint32_t T, int W, int KS, int D, bool DBG, bool BAL = false>
+__global__ __launch_bounds__(W * 64) void split_one_kernel(MvArgs a) {
+    static_assert(T == kQ3_K || T == kQ6_K, "the one-column split kernel takes Q3_K and Q6_K");
     constexpr int TS = W / KS;
     static_assert(!BAL || TS == 2 || TS == 4, "the balanced deal takes two or four tile slots");
     if (!mv_enter(a)) return;
     extern __shared__ __align__(16) uint8_t lds[];
-    const LdsMap L = lds_map(kQ3_K, a.cols, a.batch);
+    const LdsMap L = lds_map(T, a.cols, a.batch);
     const uint32_t lane = threadIdx.x & 63, n = lane & 15, kq = lane >> 4;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t ts = wave / KS, kp = wave % KS;
@@ -2576,7 +2651,7 @@ __global__ __launch_bounds__(W * 64) void q3k_mv_split_kernel(MvArgs a) {
     const uint32_t nh = (n & 7) | (hsel << 3);  // the row a lane loads in a half tile
     const uint32_t bpt = kp < nb ? (nb - 1 - kp) / KS + 1 : 0;  // blocks of each tile this wave takes
     const uint32_t steps = my_tiles * bpt;
-    float4* park = (float4*)(lds + q3_part_off(a.cols));
+    float4* park = (float4*)(lds + split_part_off(T, a.cols));
 
     if (threadIdx.x < 16) *(uint4*)(lds + L.zero_off + threadIdx.x * 16) = make_uint4(0, 0, 0, 0);
     if (threadIdx.x < 8) ((unsigned long long*)(lds + L.am_off))[threadIdx.x] = 0ull;
@@ -2587,11 +2662,12 @@ __global__ __launch_bounds__(W * 64) void q3k_mv_split_kernel(MvArgs a) {
     const uint32_t kp0 = kp < nb ? kp : nb - 1;
     uint32_t ld_tile = t0 < ntiles ? t0 : ntiles - 1, ld_blk = kp0;
     if constexpr (BAL) ld_tile = my_tiles ? bt : 0;
-    K16Step<kQ3_K> buf[D];
-    auto issue = [&](K16Step<kQ3_K>& st) {
-        const uint8_t* base = a.w + ((uint64_t)ld_tile * nb + ld_blk) * kQ3KChunk;
-        if (BAL && half) k16_issue<kQ3_K>(st, base, kq * 16 + nh, nh, kq);  // the half tile
-        else k16_issue<kQ3_K>(st, base, lane, n, kq);
+    SplitStep<T> buf[D];
+    auto issue = [&](SplitStep<T>& st) {
+        const uint8_t* base = a.w + ((uint64_t)ld_tile * nb + ld_blk) * (T == kQ6_K ? kQ6KChunk : kQ3KChunk);
+        const uint32_t ln = BAL && half ? kq * 16 + nh : lane, r = BAL && half ? nh : n;  // (a half tile)
+        if constexpr (T == kQ6_K) q6_issue(st, base, ln, r, kq);
+        else k16_issue<kQ3_K>(st, base, ln, r, kq);
         ld_blk += KS;
         if (ld_blk >= nb) {
             ld_blk = kp0;
@@ -2601,41 +2677,19 @@ __global__ __launch_bounds__(W * 64) void q3k_mv_split_kernel(MvArgs a) {
 #pragma unroll
     for (int i = 0; i < D; ++i) issue(buf[i]);
 
-    const bool ok = a.x ? stage_q8k<W, kBsNone>(a, lds, L, wave, xv) : stage_planes<W>(a, lds, L, kQ3_K);
+    const bool ok = a.x ? stage_q8k<W, kBsNone>(a, lds, L, wave, xv) : stage_planes<W>(a, lds, L, T);
     if (!ok) return finish_argmax(a, lds, L);
     if (a.zero_pair) return zero_slot_tiles<W, TS>(a, tmax, tstride);
 
-    // the operands of q3k_mv_one_kernel
-    const uint32_t hsh = 4 * (kq >> 1), sb0 = kq >> 1;
-    const uint32_t cls = n & 7, qsel = n >> 3;
-    const bool live0 = kq == qsel, live1 = kq == 2 + qsel;
-    const uint8_t* a_ptr = live0 || live1 ? lds + 128 * (kq >> 1) + 16 * (kq & 1) : lds + L.zero_off;
-    const uint32_t a_step = live0 || live1 ? 256 : 0;
-    const uint32_t byte = 0xffu << (8 * (cls & 3));
-    uint32_t m0[4], m1[4];
-#pragma unroll
-    for (int w = 0; w < 4; ++w) {
-        const uint32_t mk = (uint32_t)(w & 1) == (cls >> 2) ? byte : 0u;
-        m0[w] = live0 ? mk : 0u;
-        m1[w] = live1 ? mk : 0u;
-    }
+    SplitOps<T> ops;
+    if constexpr (T == kQ6_K) ops = q6_one_ops(lds, L, n, kq);
+    else ops = q3_one_ops(lds, L, n, kq);
 
     uint32_t ti = 0, tile = BAL ? bt : t0, blk = kp, j = 0;
-    auto compute = [&](const K16Step<kQ3_K>& cur) {
-        const K16Ops<kQ3_K> o = k16_ops<kQ3_K>(cur, hsh);
-        const uint8_t* p = a_ptr + blk * a_step;
+    auto compute = [&](const SplitStep<T>& cur) {
         int32_t I[4] = {0, 0, 0, 0};
-#pragma unroll
-        for (int sft = 0; sft < 4; ++sft) {
-            const uint4 x = *(const uint4*)(p + 32 * sft);
-            const i32x4 A0 = {(int)(x.x & m0[0]), (int)(x.y & m0[1]), (int)(x.z & m0[2]), (int)(x.w & m0[3])};
-            const i32x4 A1 = {(int)(x.x & m1[0]), (int)(x.y & m1[1]), (int)(x.z & m1[2]), (int)(x.w & m1[3])};
-            const i32x4 d0 = mfma_i8(A0, o.wv[sft]), d1 = mfma_i8(A1, o.wv[sft]);
-            const int32_t sa = sbyte(o.c[sft >> 1], 2 * (sft & 1) + sb0);
-            const int32_t sb = sbyte(o.c[2 + (sft >> 1)], 2 * (sft & 1) + sb0);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) I[i] = mad24(sa, d0[i], mad24(sb, d1[i], I[i]));
-        }
+        if constexpr (T == kQ6_K) q6_one_ints(cur, ops, ops.a_ptr + blk * ops.a_step, I);
+        else q3_one_ints(cur, ops, ops.a_ptr + blk * ops.a_step, I);
         const float d = half_to_float(cur.d) * *(const float*)(lds + L.d_off + blk * 32);  // :246
 #pragma unroll
         for (int i = 0; i < 4; ++i) I[i] = sum_xor32(I[i]);
@@ -3018,25 +3072,26 @@ static hipError_t launch_q45(const MvArgs& a, uint32_t nbat, bool dbg, uint32_t 
     return dbg ? launch_ks<T, 8, 4, 2, true>(a, s, pairs) : launch_ks<T, 8, 4, 2, false>(a, s, pairs);
 }
 
-// The split Q3_K kernel: 8 waves, two tile slots of a K split of 4, or, at
-// no more tiles than CUs, 16 waves, one slot of a K split of 16 (4096x14336:
-// 13.2 us against 19.8 with two slots, 13.6 with 8 waves of a split of 8);
-// about kSmallWgPerCu workgroups per CU and enough that the parked terms fit
-// LDS (one workgroup's slots at least: q3_split_fits).
-static bool q3_split_fits(const MvArgs& a, uint32_t ts = 2) {
-    const size_t off = q3_part_off(a.cols), per_tile = (size_t)ts * a.nb * 512u;
+// The one-column split kernels (Q3_K, Q6_K): 8 waves, two tile slots of a
+// K split of 4, or, at no more tiles than CUs, 16 waves, one slot of a K
+// split of 16 (Q3_K 4096x14336: 13.2 us against 19.8 with two slots, 13.6
+// with 8 waves of a split of 8); about kSmallWgPerCu workgroups per CU and
+// enough that the parked terms fit LDS (one workgroup's slots at least:
+// split_fits).
+static bool split_fits(uint32_t t, const MvArgs& a, uint32_t ts = 2) {
+    const size_t off = split_part_off(t, a.cols), per_tile = (size_t)ts * a.nb * 512u;
     return off < kMaxLds && (kMaxLds - off) / per_tile > 0;
 }
 // The balanced deal (one matrix of 6144-16384 rows on 256 CUs): one
 // workgroup of 16 waves per CU, four slots of a K split of 4.
-template <bool DBG>
-static hipError_t launch_q3_bal(const MvArgs& a, hipStream_t s) {
+template <uint32_t T, bool DBG>
+static hipError_t launch_split_bal(const MvArgs& a, hipStream_t s) {
     constexpr int W = 16, KS = 4, TS = W / KS;
     static LdsLimit lds_limit;
-    auto kernel = q3k_mv_split_kernel<W, KS, 1, DBG, true>;
+    auto kernel = split_one_kernel<T, W, KS, 1, DBG, true>;
     uint32_t grid, tmax;
     b1_bal_grid<TS>(a, grid, tmax);
-    const size_t lds = q3_split_lds(a.cols, tmax, TS);
+    const size_t lds = split_lds(T, a.cols, tmax, TS);
     if (grid == 0 || a.ids || lds > kMaxLds || (a.am_out && grid > kArgmaxMaxGrid)) return hipErrorInvalidValue;
     if (const hipError_t e = lds_limit.raise((const void*)kernel, lds); e != hipSuccess) return e;
     MvArgs b = a;
@@ -3044,23 +3099,56 @@ static hipError_t launch_q3_bal(const MvArgs& a, hipStream_t s) {
     hipLaunchKernelGGL(kernel, dim3(grid), dim3(W * 64), lds, s, b);
     return hipGetLastError();
 }
-template <int W, int KS, bool DBG>
-static hipError_t launch_q3_split(const MvArgs& a, hipStream_t s, uint32_t pairs) {
+// The grid of a split launch: about kSmallWgPerCu workgroups per CU, more
+// when the tiles of a slot would not fit LDS; false when no grid fits (LDS,
+// or the argmax's workgroup limit).
+template <uint32_t T, int W, int KS>
+static bool split_grid(const MvArgs& a, uint32_t pairs, uint32_t& grid, uint32_t& tmax) {
+    constexpr int TS = W / KS;
+    if (!split_fits(T, a, TS)) return false;
+    const uint32_t gy = grid_rows(a, pairs);
+    grid = grid_cols((a.ntiles + TS - 1) / TS, (uint32_t)kSmallWgPerCu * (uint32_t)device_cus(), gy);
+    const size_t off = split_part_off(T, a.cols), per_tile = (size_t)TS * a.nb * 512u;
+    const uint64_t room = (kMaxLds - off) / per_tile, need = (a.ntiles + room * TS - 1) / (room * TS);
+    if (need > 65535) return false;
+    if (grid < need) grid = (uint32_t)need;
+    const uint32_t tstride = grid * TS;
+    tmax = (a.ntiles + tstride - 1) / tstride;
+    return split_lds(T, a.cols, tmax, TS) <= kMaxLds && !(a.am_out && grid > kArgmaxMaxGrid);
+}
+template <uint32_t T, int W, int KS, bool DBG>
+static hipError_t launch_split(const MvArgs& a, hipStream_t s, uint32_t pairs) {
     constexpr int TS = W / KS;
     static LdsLimit lds_limit;
-    auto kernel = q3k_mv_split_kernel<W, KS, 2, DBG>;
-    const uint32_t gy = grid_rows(a, pairs);
-    uint32_t grid = grid_cols((a.ntiles + TS - 1) / TS, (uint32_t)kSmallWgPerCu * (uint32_t)device_cus(), gy);
-    const size_t off = q3_part_off(a.cols), per_tile = (size_t)TS * a.nb * 512u;
-    if (!q3_split_fits(a, TS)) return hipErrorInvalidValue;
-    const uint64_t room = (kMaxLds - off) / per_tile, need = (a.ntiles + room * TS - 1) / (room * TS);
-    if (grid < need) grid = (uint32_t)need;
-    const uint32_t tstride = grid * TS, tmax = (a.ntiles + tstride - 1) / tstride;
-    const size_t lds = q3_split_lds(a.cols, tmax, TS);
-    if (lds > kMaxLds || (a.am_out && grid > kArgmaxMaxGrid)) return hipErrorInvalidValue;
+    // two steps in flight, one for Q6_K with 16 waves (its 21-register steps
+    // would spill beside the operands within 128 registers)
+    auto kernel = split_one_kernel<T, W, KS, T == kQ6_K && W >= 16 ? 1 : 2, DBG>;
+    uint32_t grid, tmax;
+    if (!split_grid<T, W, KS>(a, pairs, grid, tmax)) return hipErrorInvalidValue;
+    const size_t lds = split_lds(T, a.cols, tmax, TS);
     if (const hipError_t e = lds_limit.raise((const void*)kernel, lds); e != hipSuccess) return e;
-    hipLaunchKernelGGL(kernel, dim3(grid, gy), dim3(W * 64), lds, s, a);
+    hipLaunchKernelGGL(kernel, dim3(grid, grid_rows(a, pairs)), dim3(W * 64), lds, s, a);
     return hipGetLastError();
+}
+// Q6_K with one column takes the split kernels up to 1024 tiles (16384
+// rows; us against the whole-tile kernel: 1024x4096 6.3 / 19.1, 4096x4096
+// 6.9 / 19.4, 4096x14336 15.2 / 56.2, 14336x4096 13.4 / 19.9) and the
+// whole-tile kernel above (28672x4096 25.5 / 22.7, 128256x4096 about 94
+// both; the output head).
+constexpr uint64_t kQ6SplitMaxTiles = 1024;
+
+template <uint32_t T>
+static hipError_t launch_split_one(const MvArgs& a, bool dbg, hipStream_t s, uint32_t pairs, bool& taken) {
+    taken = true;
+    uint32_t grid, tmax;
+    if (!a.ids && grid_rows(a, pairs) == 1 && b1_bal_units(a) >= 5 && split_lds(T, a.cols, 1, 4) <= kMaxLds)
+        return dbg ? launch_split_bal<T, true>(a, s) : launch_split_bal<T, false>(a, s);
+    if (a.ntiles * grid_rows(a, pairs) > (uint32_t)device_cus() && split_grid<T, 8, 4>(a, pairs, grid, tmax))
+        return dbg ? launch_split<T, 8, 4, true>(a, s, pairs) : launch_split<T, 8, 4, false>(a, s, pairs);
+    if (split_grid<T, 16, 16>(a, pairs, grid, tmax))
+        return dbg ? launch_split<T, 16, 16, true>(a, s, pairs) : launch_split<T, 16, 16, false>(a, s, pairs);
+    taken = false;
+    return hipSuccess;
 }
 
 // Q2_K / Q3_K: up to four columns the K-split kernel, while its parked terms
@@ -3107,12 +3195,9 @@ static hipError_t launch_k16(const MvArgs& a, bool dbg, size_t lds_plain, hipStr
     // per tile (14336x4096: balanced 12.0 us, split 13.0, one wave per tile
     // 15.3; the kernels in their own order took 10.2)
     if (T == kQ3_K && a.batch == 1) {
-        if (!a.ids && grid_rows(a, pairs) == 1 && b1_bal_units(a) >= 5 && q3_split_lds(a.cols, 1, 4) <= kMaxLds)
-            return dbg ? launch_q3_bal<true>(a, s) : launch_q3_bal<false>(a, s);
-        if (q3_split_fits(a) && a.ntiles * grid_rows(a, pairs) > (uint32_t)device_cus())
-            return dbg ? launch_q3_split<8, 4, true>(a, s, pairs) : launch_q3_split<8, 4, false>(a, s, pairs);
-        if (q3_split_fits(a, 1))
-            return dbg ? launch_q3_split<16, 16, true>(a, s, pairs) : launch_q3_split<16, 16, false>(a, s, pairs);
+        bool taken;
+        const hipError_t e = launch_split_one<kQ3_K>(a, dbg, s, pairs, taken);
+        if (taken) return e;
         return dbg ? launch_one<kMvWaves, q3k_mv_one_kernel<kMvWaves, 3, true>>(a, lds_plain, s, pairs)
                    : launch_one<kMvWaves, q3k_mv_one_kernel<kMvWaves, 3, false>>(a, lds_plain, s, pairs);
     }
@@ -3225,9 +3310,15 @@ hipError_t launch_matvec_ex(uint32_t wtype, const uint8_t* w, uint64_t rows, uin
                     // wave (128256x4096 + argmax, batch 8: 78.5 us against 79.6
                     // with four and 80.3 with five; batch 1 71.1 with three or four);
                     // one column in the reference's f32 order
-                    if (nbat == 1)
+                    if (nbat == 1) {
+                        if ((uint64_t)a.ntiles * grid_rows(a, pairs) <= kQ6SplitMaxTiles) {
+                            bool taken;
+                            const hipError_t e = launch_split_one<kQ6_K>(a, dbg, s, pairs, taken);
+                            if (taken) return e;
+                        }
                         return dbg ? launch_one<2 * W, q6k_mv_one_kernel<2 * W, 3, true>>(a, lds, s, pairs, 1)
                                    : launch_one<2 * W, q6k_mv_one_kernel<2 * W, 3, false>>(a, lds, s, pairs, 1);
+                    }
                     return dbg ? launch_one<2 * W, q6k_mv_kernel<2 * W, 3, true>>(a, lds, s, pairs, 1)
                                : launch_one<2 * W, q6k_mv_kernel<2 * W, 3, false>>(a, lds, s, pairs, 1);
                 default:

@@ -1,5 +1,6 @@
 """GPU parity of the Q2_K, Q3_K and Q5_K weight formats (matvec.hip kernels,
-quantize.hip decoders) against the golden records and the CPU oracle.
+quantize.hip decoders) against the golden records and the CPU oracle, and of
+the one-column split kernels Q3_K and Q6_K share, on every launch shape.
 
 Bars, as for Q4_K / Q6_K:
   - decoders and per-block integer dot sums: bit-exact;
@@ -33,7 +34,7 @@ DT = rlq.DType
 REL_L2 = 1e-5
 K_OTHER = (DT.Q2_K, DT.Q3_K, DT.Q5_K)
 # byte offsets of the f16 super-block scales (d, and dmin where present)
-HALVES = {DT.Q2_K: (80, 82), DT.Q3_K: (108,), DT.Q5_K: (0, 2)}
+HALVES = {DT.Q2_K: (80, 82), DT.Q3_K: (108,), DT.Q5_K: (0, 2), DT.Q6_K: (208,)}
 
 
 def say(*a):
@@ -249,18 +250,20 @@ def test_block_sums_balanced_deal(ctx, t, rows, batch):
         assert np.array_equal(bits(got), bits(want))
 
 
+@pytest.mark.parametrize("t", [DT.Q3_K, DT.Q6_K])
 @pytest.mark.parametrize("rows,cols", [(300, 4096), (7, 768), (6144, 4096), (8200, 2048), (14336, 4096),
-                                       (33, 49152), (20, 65536)])
-def test_q3k_one_column_every_launch_bitwise(ctx, rows, cols):
-    """Q3_K with one column, each of its launch shapes: one 16-wave tile slot
-    of a K split of 16 (no more tiles than CUs; 3 blocks a row leave most
-    waves without a block, 192 blocks a row fill most of LDS), two 8-wave
-    slots of a split of 4 (more tiles, not the balanced deal), the balanced
-    deal, and one wave per tile where the parked terms of one tile no longer
-    fit LDS (256 blocks a row).  Column 0's integers and every output
-    against the oracle bitwise, and the fused argmax against the oracle's."""
-    t = DT.Q3_K
-    say("Q3_K one column", rows, cols)
+                                       (33, 49152), (20, 65536), (16384, 1024), (16400, 1024)])
+def test_one_column_split_every_launch_bitwise(ctx, t, rows, cols):
+    """Q3_K and Q6_K with one column, each launch shape of the split kernels:
+    one 16-wave tile slot of a K split of 16 (no more tiles than CUs; 3
+    blocks a row leave most waves without a block, 192 blocks a row fill
+    most of LDS), two 8-wave slots of a split of 4 (more tiles, not the
+    balanced deal), the balanced deal, and one wave per tile where the parked
+    terms of one tile no longer fit LDS (256 blocks a row); Q6_K above 1024
+    tiles (16400 rows) walks whole tiles as for the output head.  Column 0's
+    integers and every output against the oracle bitwise, and the fused
+    argmax against the oracle's."""
+    say(t.name, "one column", rows, cols)
     w = random_blocks(t, rows, cols, 500 + rows)
     x = randn(600 + rows, cols).reshape(1, cols)
     W = rlq.Weights(ctx, t, w, rows, cols)
