@@ -2355,8 +2355,10 @@ __global__ __launch_bounds__(W * 64) void q8_0_mv_kernel(MvArgs a) {
 // tiles still spreads over every CU.  Every block's f32 term
 // isum * (dx * dy) is parked in LDS [tmax][TS][nb][16][8] and the wave that
 // completes a tile's count adds them in block order, the reference's order
-// (matvec.rs:124-128): the outputs stay bit-exact.
-template <int W, int KS, int D, bool DBG>
+// (matvec.rs:124-128): the outputs stay bit-exact.  COMPACT parks only the
+// batch's columns ([..][16][batch]: long rows whose eight-column records
+// would not fit LDS; slower where both fit, 4096x4096 10.0 against 8.8 us).
+template <int W, int KS, int D, bool DBG, bool COMPACT = false>
 __global__ __launch_bounds__(W * 64) void q8_0_mv_ks_kernel(MvArgs a) {
     constexpr int TS = W / KS;
     if (!mv_enter(a)) return;
@@ -2373,7 +2375,8 @@ __global__ __launch_bounds__(W * 64) void q8_0_mv_ks_kernel(MvArgs a) {
     const uint32_t cpt = kp < np ? (np - 1 - kp) / KS + 1 : 0;  // chunks of each tile this wave takes
     const uint32_t steps = my_tiles * cpt;
     const uint32_t nk = (uint32_t)KS < np ? (uint32_t)KS : np;  // waves of a tile that take chunks
-    uint32_t* cnt = (uint32_t*)(part + tmax * TS * nb * 16 * 8);
+    const uint32_t pc = COMPACT ? a.batch : 8u;  // columns parked per row
+    uint32_t* cnt = (uint32_t*)(part + tmax * TS * nb * 16 * pc);
     for (uint32_t i = threadIdx.x; i < tmax * TS; i += W * 64) cnt[i] = 0;
     if (threadIdx.x < 16) *(uint4*)(lds + L.zero_off + threadIdx.x * 16) = make_uint4(0, 0, 0, 0);
     if (threadIdx.x < 8) ((unsigned long long*)(lds + L.am_off))[threadIdx.x] = 0ull;
@@ -2418,11 +2421,21 @@ __global__ __launch_bounds__(W * 64) void q8_0_mv_ks_kernel(MvArgs a) {
         // (matvec.rs:124-128), parked for the in-order sum
         const float dx0 = half_to_float(cur.d), dx1 = half_to_float(cur.d >> 16);
         const float2 dy0 = *(const float2*)(lds + L.d_off + (2 * p * 8 + b0) * 4);
-        float* pt = part + (((ti * TS + ts) * nb + 2 * p) * 16 + n) * 8 + b0;
-        *(float2*)pt = make_float2((float)dot[0] * (dx0 * dy0.x), (float)dot[2] * (dx0 * dy0.y));
+        float* pt = part + (((ti * TS + ts) * nb + 2 * p) * 16 + n) * pc + b0;
+        if constexpr (COMPACT) {
+            if (b0 < pc) pt[0] = (float)dot[0] * (dx0 * dy0.x);
+            if (b0 + 1 < pc) pt[1] = (float)dot[2] * (dx0 * dy0.y);
+        } else {
+            *(float2*)pt = make_float2((float)dot[0] * (dx0 * dy0.x), (float)dot[2] * (dx0 * dy0.y));
+        }
         if (second) {
             const float2 dy1 = *(const float2*)(lds + L.d_off + ((2 * p + 1) * 8 + b0) * 4);
-            *(float2*)(pt + 16 * 8) = make_float2((float)dot[1] * (dx1 * dy1.x), (float)dot[3] * (dx1 * dy1.y));
+            if constexpr (COMPACT) {
+                if (b0 < pc) pt[16 * pc] = (float)dot[1] * (dx1 * dy1.x);
+                if (b0 + 1 < pc) pt[16 * pc + 1] = (float)dot[3] * (dx1 * dy1.y);
+            } else {
+                *(float2*)(pt + 16 * 8) = make_float2((float)dot[1] * (dx1 * dy1.x), (float)dot[3] * (dx1 * dy1.y));
+            }
         }
         if (DBG && kq == 0) {
             const uint32_t row = tile * kTileRows + n;
@@ -2458,10 +2471,20 @@ __global__ __launch_bounds__(W * 64) void q8_0_mv_ks_kernel(MvArgs a) {
         const uint32_t slot = i * TS + ts, row = (t0 + i * tstride) * kTileRows + n;
         if (cnt[slot] != nk + 1 + wave) continue;  // (the mark is wave-uniform)
         float s0 = 0.0f, s1 = 0.0f;
-        for (uint32_t blk = 0; blk < nb; ++blk) {
-            const float2 v = *(const float2*)(part + ((slot * nb + blk) * 16 + n) * 8 + b0);
-            s0 += v.x;
-            s1 += v.y;
+        if constexpr (COMPACT) {
+            // (a lane's columns past the batch read column pc - 1 and are not stored)
+            const uint32_t c0 = b0 < pc ? b0 : pc - 1, c1 = b0 + 1 < pc ? b0 + 1 : pc - 1;
+            for (uint32_t blk = 0; blk < nb; ++blk) {
+                const float* v = part + ((slot * nb + blk) * 16 + n) * pc;
+                s0 += v[c0];
+                s1 += v[c1];
+            }
+        } else {
+            for (uint32_t blk = 0; blk < nb; ++blk) {
+                const float2 v = *(const float2*)(part + ((slot * nb + blk) * 16 + n) * 8 + b0);
+                s0 += v.x;
+                s1 += v.y;
+            }
         }
         store_out(a, row, b0, s0, best0);
         store_out(a, row, b0 + 1, s1, best1);
@@ -2960,23 +2983,25 @@ static hipError_t launch_ks_pl(const MvArgs& a, hipStream_t s, uint32_t pairs) {
 
 // The K-split Q8_0 kernel: taken when one workgroup's tile slots hold one
 // tile each (a few hundred tiles) and their parked block terms fit LDS.
-template <int W, int KS>
+template <int W, int KS, bool COMPACT = false>
 static bool q8_0_ks_takes(const MvArgs& a, uint32_t pairs) {
     constexpr int TS = W / KS;
     const uint32_t gy = grid_rows(a, pairs);
     const uint32_t grid = grid_cols((a.ntiles + TS - 1) / TS, (uint32_t)kSmallWgPerCu * (uint32_t)device_cus(), gy);
     const uint64_t tmax = (a.ntiles + (uint64_t)grid * TS - 1) / ((uint64_t)grid * TS);
-    return tmax == 1 && ks_part_off(kQ8_0, a.cols, a.batch) + (uint64_t)TS * a.nb * 16 * 8 * 4 + TS * 4 <= kMaxLds;
+    const uint64_t pc = COMPACT ? a.batch : 8;
+    return tmax == 1 && ks_part_off(kQ8_0, a.cols, a.batch) + (uint64_t)TS * a.nb * 16 * pc * 4 + TS * 4 <= kMaxLds;
 }
 
-template <int W, int KS, bool DBG>
+template <int W, int KS, bool DBG, bool COMPACT = false>
 static hipError_t launch_q8_0_ks(const MvArgs& a, hipStream_t s, uint32_t pairs) {
     constexpr int TS = W / KS;
     static LdsLimit lds_limit;
-    auto kernel = q8_0_mv_ks_kernel<W, KS, 2, DBG>;
+    auto kernel = q8_0_mv_ks_kernel<W, KS, 2, DBG, COMPACT>;
     const uint32_t gy = grid_rows(a, pairs);
     const uint32_t grid = grid_cols((a.ntiles + TS - 1) / TS, (uint32_t)kSmallWgPerCu * (uint32_t)device_cus(), gy);
-    const size_t lds = ks_part_off(kQ8_0, a.cols, a.batch) + (size_t)TS * a.nb * 16 * 8 * 4 + TS * 4;
+    const size_t pc = COMPACT ? a.batch : 8;
+    const size_t lds = ks_part_off(kQ8_0, a.cols, a.batch) + (size_t)TS * a.nb * 16 * pc * 4 + TS * 4;
     if ((a.ntiles + (uint64_t)grid * TS - 1) / ((uint64_t)grid * TS) != 1 || lds > kMaxLds ||
         (a.am_out && grid > kArgmaxMaxGrid))
         return hipErrorInvalidValue;
@@ -3335,6 +3360,11 @@ hipError_t launch_matvec_ex(uint32_t wtype, const uint8_t* w, uint64_t rows, uin
                         return dbg ? launch_q8_0_ks<16, 8, true>(a, s, pairs) : launch_q8_0_ks<16, 8, false>(a, s, pairs);
                     if (q8_0_ks_takes<8, 4>(a, pairs))
                         return dbg ? launch_q8_0_ks<8, 4, true>(a, s, pairs) : launch_q8_0_ks<8, 4, false>(a, s, pairs);
+                    // rows too long for eight parked columns: the batch's only
+                    // (4096x14336 batch 1: 23.9 us against 61.3 walking whole tiles)
+                    if (a.nchunks >= 32 && q8_0_ks_takes<16, 16, true>(a, pairs))
+                        return dbg ? launch_q8_0_ks<16, 16, true, true>(a, s, pairs)
+                                   : launch_q8_0_ks<16, 16, false, true>(a, s, pairs);
                     // ten chunks in flight per wave (151936x896 + argmax: 30.3 us
                     // against 30.9 with eight, 31.8 with six)
                     return dbg ? launch_one<W, q8_0_mv_kernel<W, 10, true>>(a, lds, s, pairs, 3)

@@ -402,6 +402,24 @@ def test_q8_0_qwen_ffn_up_4864x896(ctx):
         assert np.array_equal(bits(y.cpu().numpy()[0]), bits(want)), k
 
 
+@pytest.mark.parametrize("rows,cols,batch", [(4096, 14336, 1), (33, 14336, 2), (70, 16384, 1)])
+def test_q8_0_long_rows_compact_parking(ctx, rows, cols, batch):
+    """Q8_0 rows of 448-512 blocks, too long for the K-split kernels' eight
+    parked columns: 16 waves of a 16-way split park only the batch's
+    columns.  Every output bitwise the oracle's (block order), and the fused
+    argmax of column 0 the oracle's."""
+    say("Q8_0 long rows", rows, cols, "batch", batch)
+    w = rlq.quantize(DT.Q8_0, randn(0x51A7E201 + rows, rows * cols, 0.02))
+    W = rlq.Weights(ctx, DT.Q8_0, w, rows, cols)
+    x = randn(0x51A7E301 + batch, batch * cols).reshape(batch, cols)
+    y, am = ctx.matmul_argmax(W, torch.from_numpy(x).cuda())
+    ctx.sync()
+    want = O.matmul(O.Q8_0, w, rows, cols, x, threads=16)
+    assert np.array_equal(bits(y.cpu().numpy().reshape(batch, rows)), bits(want))
+    for b in range(batch):
+        assert int(am[b]) == O.argmax(want[b]), b
+
+
 def test_q8_0_qwen_lm_head_151936x896(ctx):
     rows, cols = 151936, 896
     say("Q8_0 lm_head", rows, cols)
