@@ -3354,7 +3354,10 @@ hipError_t launch_matvec_ex(uint32_t wtype, const uint8_t* w, uint64_t rows, uin
                     // 8-way split of 16 waves from 12 (14336x4096 20.5 / 24.2 against
                     // 24.5 / 29.2 where the 16-way split would need two tiles per slot;
                     // 4864x896 6.53 against 6.62, 10.5 with the 16-way split)
-                    if (a.nchunks >= 32 && q8_0_ks_takes<16, 16>(a, pairs))
+                    // (the 16-way split while its tiles fit one workgroup per CU:
+                    // 6144x4096 10.8 us against 15.3 with 384 workgroups on 256 CUs)
+                    if (a.nchunks >= 32 && a.ntiles * grid_rows(a, pairs) <= (uint32_t)device_cus() &&
+                        q8_0_ks_takes<16, 16>(a, pairs))
                         return dbg ? launch_q8_0_ks<16, 16, true>(a, s, pairs) : launch_q8_0_ks<16, 16, false>(a, s, pairs);
                     if (a.nchunks >= 12 && q8_0_ks_takes<16, 8>(a, pairs))
                         return dbg ? launch_q8_0_ks<16, 8, true>(a, s, pairs) : launch_q8_0_ks<16, 8, false>(a, s, pairs);
