@@ -3107,13 +3107,15 @@ static bool split_fits(uint32_t t, const MvArgs& a, uint32_t ts = 2) {
     const size_t off = split_part_off(t, a.cols), per_tile = (size_t)ts * a.nb * 512u;
     return off < kMaxLds && (kMaxLds - off) / per_tile > 0;
 }
-// The balanced deal (one matrix of 6144-16384 rows on 256 CUs): one
-// workgroup of 16 waves per CU, four slots of a K split of 4.
-template <uint32_t T, bool DBG>
+// The balanced deal (one matrix of 10240-16384 rows on 256 CUs): one
+// workgroup of 16 waves per CU, four slots of a K split of 4 (two 8-wave
+// slots at 6144 and 8192 rows measured no faster: Q3_K 8.9 against 8.7 us,
+// Q6_K 9.4 against 9.2 at 6144 rows).
+template <uint32_t T, int W, int KS, bool DBG>
 static hipError_t launch_split_bal(const MvArgs& a, hipStream_t s) {
-    constexpr int W = 16, KS = 4, TS = W / KS;
+    constexpr int TS = W / KS;
     static LdsLimit lds_limit;
-    auto kernel = split_one_kernel<T, W, KS, 1, DBG, true>;
+    auto kernel = split_one_kernel<T, W, KS, W >= 16 ? 1 : 2, DBG, true>;
     uint32_t grid, tmax;
     b1_bal_grid<TS>(a, grid, tmax);
     const size_t lds = split_lds(T, a.cols, tmax, TS);
@@ -3166,8 +3168,9 @@ template <uint32_t T>
 static hipError_t launch_split_one(const MvArgs& a, bool dbg, hipStream_t s, uint32_t pairs, bool& taken) {
     taken = true;
     uint32_t grid, tmax;
-    if (!a.ids && grid_rows(a, pairs) == 1 && b1_bal_units(a) >= 5 && split_lds(T, a.cols, 1, 4) <= kMaxLds)
-        return dbg ? launch_split_bal<T, true>(a, s) : launch_split_bal<T, false>(a, s);
+    const uint32_t u = !a.ids && grid_rows(a, pairs) == 1 ? b1_bal_units(a) : 0;
+    if (u >= 5 && split_lds(T, a.cols, 1, 4) <= kMaxLds)
+        return dbg ? launch_split_bal<T, 16, 4, true>(a, s) : launch_split_bal<T, 16, 4, false>(a, s);
     if (a.ntiles * grid_rows(a, pairs) > (uint32_t)device_cus() && split_grid<T, 8, 4>(a, pairs, grid, tmax))
         return dbg ? launch_split<T, 8, 4, true>(a, s, pairs) : launch_split<T, 8, 4, false>(a, s, pairs);
     if (split_grid<T, 16, 16>(a, pairs, grid, tmax))
@@ -3234,6 +3237,11 @@ static hipError_t launch_k16(const MvArgs& a, bool dbg, size_t lds_plain, hipStr
     if (!a.ids && grid_rows(a, pairs) == 1 && b1_bal_units(a) >= 5 &&
         k16_part_off(T, a.cols, a.batch) + 4ull * a.nb * 16ull * a.batch * 4ull <= kMaxLds)
         return dbg ? launch_k16_bal<T, 16, 4, true>(a, s) : launch_k16_bal<T, 16, 4, false>(a, s);
+    // 6144..8192 rows: the balanced deal in 8-wave workgroups of two slots
+    // (Q2_K 6144x4096 batch 1 / 4: 6.9 / 9.4 us against 7.8 / 12.9)
+    if (!a.ids && grid_rows(a, pairs) == 1 && b1_bal_units(a) >= 3 && b1_bal_units(a) <= 4 &&
+        k16_part_off(T, a.cols, a.batch) + 2ull * a.nb * 16ull * a.batch * 4ull <= kMaxLds)
+        return dbg ? launch_k16_bal<T, 8, 4, true>(a, s) : launch_k16_bal<T, 8, 4, false>(a, s);
     constexpr int TS = kK16W / kK16KS;
     const uint32_t want = (a.ntiles + TS - 1) / TS;
     const uint32_t gy = grid_rows(a, pairs);

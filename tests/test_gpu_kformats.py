@@ -285,6 +285,24 @@ def test_one_column_split_every_launch_bitwise(ctx, t, rows, cols):
     assert int(am[0]) == O.argmax(want[0])
 
 
+@pytest.mark.parametrize("rows,cols", [(6144, 4096), (8192, 2048)])
+@pytest.mark.parametrize("batch", [1, 4])
+def test_q2k_balanced_deal_two_slots(ctx, rows, cols, batch):
+    """Q2_K at 1.5 and 2 tiles per CU (6144 and 8192 rows on 256 CUs): the
+    balanced deal in 8-wave workgroups of two tile slots.  Every output
+    bitwise the oracle's (Q2_K keeps the reference's block order at every
+    batch)."""
+    t = DT.Q2_K
+    say("Q2_K balanced deal, two slots", rows, cols, "batch", batch)
+    w = random_blocks(t, rows, cols, 900 + rows + batch)
+    x = randn(910 + rows + batch, batch * cols).reshape(batch, cols)
+    W = rlq.Weights(ctx, t, w, rows, cols)
+    y = ctx.matmul(W, torch.from_numpy(x).cuda())
+    ctx.sync()
+    want = O.matmul(int(t), w, rows, cols, x, threads=16)
+    assert np.array_equal(bits(y.cpu().numpy().reshape(batch, rows)), bits(want))
+
+
 # ------------------------------------------------------------ batched device API
 
 @pytest.mark.parametrize("t", K_OTHER)
