@@ -3094,6 +3094,11 @@ static hipError_t launch_q45(const MvArgs& a, uint32_t nbat, bool dbg, uint32_t 
         if (u >= 3 && ks_bal_takes<T, 8, 4>(a))
             return dbg ? launch_ks<T, 8, 4, 2, true, true>(a, s, pairs) : launch_ks<T, 8, 4, 2, false, true>(a, s, pairs);
     }
+    // no more tiles than CUs and long rows: one 16-wave slot of a K split of
+    // 16 per workgroup (4096x14336 Q4_K batch 2 / 4 / 8: 12.3 / 15.3 / 16.6 us
+    // against 15.7 / 19.6 / 21.3 with two 8-wave slots on half the CUs)
+    if (a.ntiles * grid_rows(a, pairs) <= (uint32_t)device_cus() && a.nb >= 32)
+        return dbg ? launch_ks<T, 16, 16, 1, true>(a, s, pairs) : launch_ks<T, 16, 16, 1, false>(a, s, pairs);
     return dbg ? launch_ks<T, 8, 4, 2, true>(a, s, pairs) : launch_ks<T, 8, 4, 2, false>(a, s, pairs);
 }
 
