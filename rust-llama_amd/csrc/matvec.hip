@@ -3190,13 +3190,13 @@ static hipError_t launch_split_one(const MvArgs& a, bool dbg, hipStream_t s, uin
 // 9.4 us split vs 11.3 us, batch 8 22.8 us vs 20.7 us).
 constexpr int kK16W = 8, kK16KS = 8, kK16D = 2;
 
-template <uint32_t T, bool DBG>
+template <uint32_t T, bool DBG, int W = kK16W, int KS = kK16KS>
 static hipError_t launch_k16_split(const MvArgs& a, size_t lds, uint32_t grid, uint32_t gy, hipStream_t s) {
     static LdsLimit lds_limit;
-    auto kernel = k16_mv_split_kernel<T, kK16W, kK16KS, kK16D, DBG>;
+    auto kernel = k16_mv_split_kernel<T, W, KS, W >= 16 ? 1 : kK16D, DBG>;
     if (a.am_out && grid > kArgmaxMaxGrid) return hipErrorInvalidValue;
     if (const hipError_t e = lds_limit.raise((const void*)kernel, lds); e != hipSuccess) return e;
-    hipLaunchKernelGGL(kernel, dim3(grid, gy), dim3(kK16W * 64), lds, s, a);
+    hipLaunchKernelGGL(kernel, dim3(grid, gy), dim3(W * 64), lds, s, a);
     return hipGetLastError();
 }
 
@@ -3253,6 +3253,12 @@ static hipError_t launch_k16(const MvArgs& a, bool dbg, size_t lds_plain, hipStr
     const uint32_t grid = grid_cols(want, (uint32_t)kSmallWgPerCu * (uint32_t)device_cus(), gy);
     const uint64_t tstride = (uint64_t)grid * TS, tmax = (a.ntiles + tstride - 1) / tstride;
     const uint64_t lds = k16_part_off(T, a.cols, a.batch) + tmax * TS * a.nb * 16ull * a.batch * 4ull;
+    // no more tiles than CUs and long rows: 16 waves of a K split of 16 in the
+    // one tile slot (4096x14336 Q2_K batch 1 / 2 / 4: 10.8 / 13.5 / 20.4 us
+    // against 12.3 / 15.8 / 24.5 with 8 waves; Q3_K batch 4 21.4 against 24.0)
+    if (a.batch <= 4 && lds <= kMaxLds && TS == 1 && a.ntiles * gy <= (uint32_t)device_cus() && a.nb >= 32)
+        return dbg ? launch_k16_split<T, true, 16, 16>(a, lds, grid, gy, s)
+                   : launch_k16_split<T, false, 16, 16>(a, lds, grid, gy, s);
     if (a.batch <= 4 && lds <= kMaxLds)
         return dbg ? launch_k16_split<T, true>(a, lds, grid, gy, s) : launch_k16_split<T, false>(a, lds, grid, gy, s);
     return dbg ? launch_one<kMvWaves, k16_mv_kernel<T, kMvWaves, 4, true>>(a, lds_plain, s, pairs)
