@@ -488,9 +488,16 @@ LLAMA = dict(vocabulary=128256, width=4096, feed_forward=14336, heads=32, kv_hea
              n_layers=32, rms_epsilon=1e-5, rope_base=500000.0)
 
 
-def llama_tensors(rlq, ctx, cfg, seed):
+def q4km_more(i, n):
+    """The layers whose attn_v and ffn_down a Q4_K_M file stores in Q6_K: the first and last eighth
+    and every third layer between (crates/model-quant/src/planner.rs:221-223, 346, 391-402)."""
+    return i < n // 8 or i >= 7 * n // 8 or (i - n // 8) % 3 == 2
+
+
+def llama_tensors(rlq, ctx, cfg, seed, q4km=False):
     """Random-init weights on the GPU: matrices N(0, 0.02) and the embedding N(0, 1) in f32, encoded
-    by the library's own Q4_K / Q6_K encoders; norm weights N(1, 0.05)."""
+    by the library's own Q4_K / Q6_K encoders; norm weights N(1, 0.05).  q4km: the value and down
+    matrices of the q4km_more layers in Q6_K (the layer's `types`), as in a Q4_K_M file."""
     torch = rlq.torch
     g = torch.Generator(device="cuda")
     g.manual_seed(seed)
@@ -507,18 +514,22 @@ def llama_tensors(rlq, ctx, cfg, seed):
 
     W, F, kvw = cfg.width, cfg.feed_forward, cfg.kv_width
     layers = []
-    for _ in range(cfg.n_layers):
-        layers.append({"attention_norm": norm(W), "query": mat(DT.Q4_K, W, W), "key": mat(DT.Q4_K, kvw, W),
-                       "value": mat(DT.Q4_K, kvw, W), "attention_output": mat(DT.Q4_K, W, W),
-                       "feed_forward_norm": norm(W), "gate": mat(DT.Q4_K, F, W), "up": mat(DT.Q4_K, F, W),
-                       "down": mat(DT.Q4_K, W, F)})
+    for i in range(cfg.n_layers):
+        vd = DT.Q6_K if q4km and q4km_more(i, cfg.n_layers) else DT.Q4_K
+        layer = {"attention_norm": norm(W), "query": mat(DT.Q4_K, W, W), "key": mat(DT.Q4_K, kvw, W),
+                 "value": mat(vd, kvw, W), "attention_output": mat(DT.Q4_K, W, W),
+                 "feed_forward_norm": norm(W), "gate": mat(DT.Q4_K, F, W), "up": mat(DT.Q4_K, F, W),
+                 "down": mat(vd, W, F)}
+        if vd != DT.Q4_K:
+            layer["types"] = {"value": int(vd), "down": int(vd)}
+        layers.append(layer)
     emb = torch.cat([mat(DT.Q4_K, 8016, W, 1.0) for _ in range(cfg.vocabulary // 8016)])
     t = {"embedding": emb, "output_norm": norm(W), "output": mat(DT.Q6_K, cfg.vocabulary, W), "layers": layers}
     ctx.sync()
     return t
 
 
-def decode_step(rlq, ctx, steps, warmup, cpu=False):
+def decode_step(rlq, ctx, steps, warmup, cpu=False, q4km=False):
     """Config 5: one decode step of the Llama-3-8B-shape model per token (embedding row, 32 layers,
     final norm, Q6_K output matvec, greedy argmax), with synthetic tokens.  The random-init model is
     written as a GGUF file by the library's GGUF writer and loaded by its llama GGUF loader
@@ -534,12 +545,14 @@ def decode_step(rlq, ctx, steps, warmup, cpu=False):
                           L["max_context"], L["n_layers"], L["rms_epsilon"], L["rope_base"], 0.0, DT.Q4_K, DT.Q6_K,
                           DT.Q4_K)
     t0 = time.perf_counter()
-    tensors = llama_tensors(rlq, ctx, cfg, 0x51A7E005)
+    tensors = llama_tensors(rlq, ctx, cfg, 0x51A7E005, q4km=q4km)
     gen_s = time.perf_counter() - t0
     host_tensors = {"embedding": tensors["embedding"].cpu().numpy(),
                     "output_norm": tensors["output_norm"].cpu().numpy(),
                     "output": tensors["output"].cpu().numpy(),
-                    "layers": [{k: v.cpu().numpy() for k, v in l.items()} for l in tensors["layers"]]}
+                    "layers": [{k: (v if k == "types" else v.cpu().numpy()) for k, v in l.items()}
+                               for l in tensors["layers"]]}
+    n_q6 = sum(1 for l in host_tensors["layers"] if "types" in l)
     del tensors
     torch.cuda.empty_cache()
     tmp = tempfile.mkdtemp(prefix="rlq-llama-")
@@ -582,16 +595,20 @@ def decode_step(rlq, ctx, steps, warmup, cpu=False):
     ctx.sync()
     ms = start.elapsed_time(end) / steps
     kvw = cfg.kv_heads * (cfg.width // cfg.heads)
-    weights = cfg.n_layers * (rlq.row_bytes(DT.Q4_K, cfg.width) * (2 * cfg.width + 2 * kvw + 2 * cfg.feed_forward)
-                              + rlq.row_bytes(DT.Q4_K, cfg.feed_forward) * cfg.width) \
+    def layer_bytes(vd):
+        return rlq.row_bytes(DT.Q4_K, cfg.width) * (2 * cfg.width + kvw + 2 * cfg.feed_forward) \
+            + rlq.row_bytes(vd, cfg.width) * kvw + rlq.row_bytes(vd, cfg.feed_forward) * cfg.width
+
+    weights = (cfg.n_layers - n_q6) * layer_bytes(DT.Q4_K) + n_q6 * layer_bytes(DT.Q6_K) \
         + rlq.row_bytes(DT.Q6_K, cfg.width) * cfg.vocabulary
     mean_ctx = fill + warmup + (steps + 1) / 2.0
     kv = 2 * cfg.n_layers * mean_ctx * kvw * 4
     nbytes = weights + kv
     gbs = nbytes / (ms * 1e-3) / 1e9
     out = {"workload": "Llama-3-8B-shape decode step: 32 layers, d 4096, 32/8 heads of 128, FFN 14336, vocab 128256, "
-                       "Q4_K layers + Q6_K output, f32 KV cache; embedding row + 32 layers + final norm + output "
-                       "matvec + greedy argmax per token",
+                       + ("Q4_K_M layout (attn_v and ffn_down of %d layers in Q6_K, the rest Q4_K)" % n_q6
+                          if q4km else "Q4_K layers") + " + Q6_K output, f32 KV cache; embedding row + 32 layers + "
+                       "final norm + output matvec + greedy argmax per token",
            "steps": steps, "context_rows": [fill + warmup + 1, fill + warmup + steps],
            "ms_per_token": round(ms, 4), "tok_s": round(1e3 / ms, 2),
            "bytes_per_token": int(nbytes), "weight_bytes": int(weights), "kv_bytes_mean": int(kv),
@@ -725,6 +742,7 @@ def main():
             torch.cuda.empty_cache()
         extra["moe_q4k_8x14336x4096_top2"] = moe_decode(rlq, ctx, max(200, args.steps // 4), args.warmup)
         torch.cuda.empty_cache()
+        extra["decode_step_q4km"] = decode_step(rlq, ctx, args.llama_steps, 8, cpu=False, q4km=True)
         result["extra"] = extra
     ctx.close()
     print(json.dumps(result), flush=True)
