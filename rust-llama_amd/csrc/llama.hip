@@ -766,13 +766,16 @@ hipError_t LlamaModel::step(float* hidden, uint64_t position, float* embedding_o
         if (L.fused_qkv()) {
             e = launch_matvec_ex(L.tq, L.wqkv, W + 2 * kvw, W, hidden, nullptr, 1, qkv, W + 2 * kvw, nullptr, err_word,
                                  nullptr, nullptr, norm1, s);
-        } else {  // one launch per type (each quantizes the same normalized input)
-            e = launch_matvec_ex(L.tq, L.wqkv, W, W, hidden, nullptr, 1, qkv, W, nullptr, err_word, nullptr, nullptr,
-                                 norm1, s);
-            if (e == hipSuccess)
-                e = launch_matvec_ex(L.tk, L.wqkv + L.off_k, kvw, W, hidden, nullptr, 1, qkv + W, kvw, nullptr,
-                                     err_word, nullptr, nullptr, norm1, s);
-            if (e == hipSuccess)
+        } else {  // one launch per type (each quantizes the same normalized input); two
+                  // neighbours of one type are one matrix (a Q4_K_M layer's Q and K:
+                  // 1.951 ms per token against 2.030 with three launches)
+            const bool qk = L.tq == L.tk, kv = !qk && L.tk == L.tv;
+            e = launch_matvec_ex(L.tq, L.wqkv, qk ? W + kvw : W, W, hidden, nullptr, 1, qkv, qk ? W + kvw : W, nullptr,
+                                 err_word, nullptr, nullptr, norm1, s);
+            if (e == hipSuccess && !qk)
+                e = launch_matvec_ex(L.tk, L.wqkv + L.off_k, kv ? 2 * kvw : kvw, W, hidden, nullptr, 1, qkv + W,
+                                     kv ? 2 * kvw : kvw, nullptr, err_word, nullptr, nullptr, norm1, s);
+            if (e == hipSuccess && !kv)
                 e = launch_matvec_ex(L.tv, L.wqkv + L.off_v, kvw, W, hidden, nullptr, 1, qkv + W + kvw, kvw, nullptr,
                                      err_word, nullptr, nullptr, norm1, s);
         }
