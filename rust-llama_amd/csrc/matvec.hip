@@ -3296,9 +3296,16 @@ hipError_t launch_matvec_ex(uint32_t wtype, const uint8_t* w, uint64_t rows, uin
                    ex.id_cols == 0 || (ex.id_inline ? (!x || pre || ex.id_cols != 1 || ex.gate)
                                                      : (x || !pre))))
         return hipErrorInvalidValue;
+    // two Q6_K columns of a matrix of no more tiles than CUs: one column per
+    // pass, each on the split kernels (4096x14336: 30.0 us against 49.1 for
+    // both columns walking whole tiles; 4096x4096 13.6 against 17.9; three
+    // columns measure no faster)
+    const bool q6_columns = wtype == kQ6_K && batch == 2 && !ex.ids &&
+                            (rows + kTileRows - 1) / kTileRows <= (uint64_t)device_cus();
     uint64_t b0 = 0;
     while (b0 < batch) {
         uint32_t nbat = (uint32_t)(batch - b0 < 8 ? batch - b0 : 8);
+        if (q6_columns) nbat = 1;
         while (nbat > 1 && lds_map(wtype, (uint32_t)cols, nbat).total > kMaxLds) --nbat;
         const size_t lds = lds_map(wtype, (uint32_t)cols, nbat).total;
         if (lds > kMaxLds) return hipErrorInvalidValue;
